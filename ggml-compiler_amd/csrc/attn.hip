@@ -1,0 +1,284 @@
+// attn.hip - ggml_flash_attn_ext over an f16 KV cache (runtime/src/ops.cpp:217-243 ->
+// runtime/include/ggml_compiler_ops.h:133-136, GGML_PREC_F32), split-K for decode.
+//
+// Semantics (ggml-cpu flash_attn_ext_f16): Q is rounded to f16 (K's vec_dot type); a key's score
+// is (K.Q)*scale + mask; keys whose f16 mask is -inf are skipped; softmax in f32; out = V-sum / S,
+// and 0 when no key is visible. Query head h reads KV head h / (H / Hkv) (GQA).
+//
+// Layout: q[h][s][d] f32 (strides q_h, q_s); k, v [hk][j][d] f16 (strides k_h, k_j / v_h, v_j: a
+// view of the first n_kv rows of a [Hkv][max_context][D] cache); mask [s][j] f16 (row stride
+// m_s); out [s][h][Dv] f32, ggml's ne = [Dv, H, Sq].
+//
+// Decode is HBM-bound by the K/V stream. Grid = (split, KV head, query row): each workgroup
+// streams one contiguous slice of its KV head's rows once and serves all G = H/Hkv query heads
+// that share it. D/8 lanes cover one 2*D-byte row (16 B per lane, 8 f16), so a wavefront reads
+// 64*16 B of consecutive rows per instruction. Pass 1 forms the scores (v_dot2_f32_f16 on f16 Q
+// and K) into LDS; pass 2 is the slice's max and exp-sum; pass 3 accumulates P.V. A merge
+// kernel combines the splits' (max, sum, partial output) exactly as one online softmax would.
+#include "gcq_common.h"
+
+namespace gcq {
+
+constexpr int kChunkMax = 1024;  // keys per workgroup slice
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ half2_t as_h2(uint32_t u) {
+    half2_t h;
+    __builtin_memcpy(&h, &u, 4);
+    return h;
+}
+
+template <int D, int G>
+__global__ __launch_bounds__(256) void k_attn_split(const float * __restrict__ q, int64_t q_h, int64_t q_s,
+                                                    const uint16_t * __restrict__ k, int64_t k_h, int64_t k_j,
+                                                    const uint16_t * __restrict__ v, int64_t v_h, int64_t v_j,
+                                                    const uint16_t * __restrict__ mask, int64_t m_s, float scale,
+                                                    int n_kv, int chunk, const int * __restrict__ n_kv_dev,
+                                                    float * __restrict__ part_o, float2 * __restrict__ part_ml, int H,
+                                                    int nsplit) {
+    constexpr int LPK = D / 8;         // lanes per key row
+    constexpr int KPW = 64 / LPK;      // keys per wavefront step
+    constexpr int KPB = 4 * KPW;       // keys per workgroup step
+    __shared__ float sc[G][kChunkMax];
+    __shared__ float red[4][G];
+    __shared__ float accs[4][G][D];
+
+    if (n_kv_dev) {  // KV length read on the device (a captured decode step): same splits, new chunk
+        n_kv = *n_kv_dev;
+        chunk = (n_kv + nsplit - 1) / nsplit;
+    }
+    chunk = min(chunk, kChunkMax);  // the host sizes nsplit so that this never drops a key
+    const int split = blockIdx.x, hk = blockIdx.y, s = blockIdx.z;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int sub = lane % LPK, slot = lane / LPK;
+    const int j0 = split * chunk;
+    const int j1 = min(n_kv, j0 + chunk);
+    const int len = max(0, j1 - j0);
+
+    // This lane's 8 dims of each of the G query heads, rounded to f16.
+    half2_t qh[G][4];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        const float * qp = q + (int64_t) (hk * G + g) * q_h + (int64_t) s * q_s + 8 * sub;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            half2_t t;
+            t.x = (_Float16) qp[2 * c];
+            t.y = (_Float16) qp[2 * c + 1];
+            qh[g][c] = t;
+        }
+    }
+
+    // Pass 1: scores.
+    const uint16_t * kb = k + (int64_t) hk * k_h;
+    const uint16_t * mrow = mask ? mask + (int64_t) s * m_s : nullptr;
+    for (int base = 0; base < len; base += KPB) {
+        const int jj = base + wave * KPW + slot;
+        float part[G];
+        const bool ok = jj < len;
+        uint4 kr = make_uint4(0, 0, 0, 0);
+        if (ok) kr = *reinterpret_cast<const uint4 *>(kb + (int64_t) (j0 + jj) * k_j + 8 * sub);
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            float a = 0.0f;
+            a = __builtin_amdgcn_fdot2(as_h2(kr.x), qh[g][0], a, false);
+            a = __builtin_amdgcn_fdot2(as_h2(kr.y), qh[g][1], a, false);
+            a = __builtin_amdgcn_fdot2(as_h2(kr.z), qh[g][2], a, false);
+            a = __builtin_amdgcn_fdot2(as_h2(kr.w), qh[g][3], a, false);
+            part[g] = a;
+        }
+#pragma unroll
+        for (int g = 0; g < G; g++)
+#pragma unroll
+            for (int o = LPK / 2; o > 0; o >>= 1) part[g] += __shfl_xor(part[g], o, 64);
+        if (ok && sub == 0) {
+            const float mv = mrow ? h2f(mrow[j0 + jj]) : 0.0f;
+#pragma unroll
+            for (int g = 0; g < G; g++) sc[g][jj] = mv == -INFINITY ? -INFINITY : part[g] * scale + mv;
+        }
+    }
+    __syncthreads();
+
+    // Pass 2: max and sum of exp per head over the slice; scores become weights.
+    float mx[G], sum[G];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        float m = -INFINITY;
+        for (int i = threadIdx.x; i < len; i += 256) m = fmaxf(m, sc[g][i]);
+        m = wave_max(m);
+        if (lane == 0) red[wave][g] = m;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < G; g++) mx[g] = fmaxf(fmaxf(red[0][g], red[1][g]), fmaxf(red[2][g], red[3][g]));
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        float l = 0.0f;
+        for (int i = threadIdx.x; i < len; i += 256) {
+            const float p = mx[g] == -INFINITY ? 0.0f : __expf(sc[g][i] - mx[g]);
+            sc[g][i] = p;
+            l += p;
+        }
+        l = wave_sum(l);
+        if (lane == 0) red[wave][g] = l;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < G; g++) sum[g] = red[0][g] + red[1][g] + red[2][g] + red[3][g];
+
+    // Pass 3: P.V, this lane's 8 dims of one key per step.
+    float acc[G][8];
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int c = 0; c < 8; c++) acc[g][c] = 0.0f;
+    const uint16_t * vb = v + (int64_t) hk * v_h;
+    for (int base = 0; base < len; base += KPB) {
+        const int jj = base + wave * KPW + slot;
+        if (jj < len) {
+            const uint4 vr = *reinterpret_cast<const uint4 *>(vb + (int64_t) (j0 + jj) * v_j + 8 * sub);
+            const uint32_t vw[4] = {vr.x, vr.y, vr.z, vr.w};
+            float vf[8];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                vf[2 * c] = h2f((uint16_t) (vw[c] & 0xffff));
+                vf[2 * c + 1] = h2f((uint16_t) (vw[c] >> 16));
+            }
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                const float p = sc[g][jj];
+#pragma unroll
+                for (int c = 0; c < 8; c++) acc[g][c] += p * vf[c];
+            }
+        }
+    }
+    // Reduce over the key slots of a wavefront, then over the 4 wavefronts.
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int c = 0; c < 8; c++)
+#pragma unroll
+            for (int o = LPK; o < 64; o <<= 1) acc[g][c] += __shfl_xor(acc[g][c], o, 64);
+    if (slot == 0) {
+#pragma unroll
+        for (int g = 0; g < G; g++)
+#pragma unroll
+            for (int c = 0; c < 8; c++) accs[wave][g][8 * sub + c] = acc[g][c];
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < G * D; i += 256) {
+        const int g = i / D, d = i % D;
+        const float o = accs[0][g][d] + accs[1][g][d] + accs[2][g][d] + accs[3][g][d];
+        const int h = hk * G + g;
+        part_o[(((int64_t) s * H + h) * nsplit + split) * D + d] = o;
+    }
+    if (threadIdx.x < G) {
+        const int g = threadIdx.x;
+        const int h = hk * G + g;
+        part_ml[((int64_t) s * H + h) * nsplit + split] = make_float2(mx[g], sum[g]);
+    }
+}
+
+// Combine the splits of one (query row, head): out = sum_i e^(m_i - M) o_i / sum_i e^(m_i - M) l_i.
+template <int D>
+__global__ __launch_bounds__(D) void k_attn_merge(const float * __restrict__ part_o, const float2 * __restrict__ part_ml,
+                                                  float * __restrict__ out, int nsplit) {
+    const int64_t sh = blockIdx.x;  // s * H + h
+    const int d = threadIdx.x;
+    const float2 * ml = part_ml + sh * nsplit;
+    float M = -INFINITY;
+    for (int i = 0; i < nsplit; i++) M = fmaxf(M, ml[i].x);
+    float L = 0.0f, o = 0.0f;
+    if (M != -INFINITY) {
+        for (int i = 0; i < nsplit; i++) {
+            if (ml[i].x == -INFINITY) continue;
+            const float w = __expf(ml[i].x - M);
+            L += w * ml[i].y;
+            o += w * part_o[(sh * nsplit + i) * D + d];
+        }
+    }
+    out[sh * D + d] = L == 0.0f ? 0.0f : o / L;
+}
+
+// ------------------------------------------------------------------------------- dispatch
+
+AttnPlan attn_plan(int Sq, int Hkv, int n_kv) {
+    int nsplit = (n_kv + 63) / 64;
+    const int target = 1024 / max(1, Hkv * Sq);  // about 4 workgroups per CU in all
+    nsplit = max(1, min(nsplit, max(1, target)));
+    int chunk = (n_kv + nsplit - 1) / nsplit;
+    if (chunk > kChunkMax) {
+        nsplit = (n_kv + kChunkMax - 1) / kChunkMax;
+        chunk = (n_kv + nsplit - 1) / nsplit;
+    }
+    return {nsplit, max(chunk, 1)};
+}
+
+size_t attn_workspace(int Sq, int H, int Hkv, int Dv, int n_kv) {
+    const AttnPlan p = attn_plan(Sq, Hkv, n_kv);
+    return align256((size_t) Sq * H * p.nsplit * Dv * sizeof(float)) +
+           align256((size_t) Sq * H * p.nsplit * sizeof(float2));
+}
+
+template <int D>
+static void run_split(int G, const float * q, int64_t q_h, int64_t q_s, const uint16_t * k, int64_t k_h, int64_t k_j,
+                      const uint16_t * v, int64_t v_h, int64_t v_j, const uint16_t * mask, int64_t m_s, int Sq, int H,
+                      int Hkv, int n_kv, float scale, float * po, float2 * pml, const AttnPlan & p,
+                      const int * n_kv_dev, hipStream_t s) {
+    const dim3 grid((unsigned) p.nsplit, (unsigned) Hkv, (unsigned) Sq);
+#define GCQ_A(GG)                                                                                                  \
+    k_attn_split<D, GG><<<grid, 256, 0, s>>>(q, q_h, q_s, k, k_h, k_j, v, v_h, v_j, mask, m_s, scale, n_kv, p.chunk, \
+                                             n_kv_dev, po, pml, H, p.nsplit)
+    switch (G) {
+        case 1: GCQ_A(1); break;
+        case 2: GCQ_A(2); break;
+        case 3: GCQ_A(3); break;
+        case 4: GCQ_A(4); break;
+        case 5: GCQ_A(5); break;
+        case 6: GCQ_A(6); break;
+        case 7: GCQ_A(7); break;
+        case 8: GCQ_A(8); break;
+        default: fail("flash_attn: at most 8 query heads per KV head are supported");
+    }
+#undef GCQ_A
+    check_launch("flash_attn split");
+}
+
+// Split pass only: partials into (po, pml) sized for plan p. With n_kv_dev, the KV length is read
+// on the device (n_kv is then the largest it may be, which p was planned for).
+void launch_attn_split(const float * q, int64_t q_h, int64_t q_s, const void * k, int64_t k_h, int64_t k_j,
+                       const void * v, int64_t v_h, int64_t v_j, const void * mask, int64_t m_s, int D, int Sq, int H,
+                       int Hkv, int n_kv, float scale, float * po, float2 * pml, const AttnPlan & p,
+                       const int * n_kv_dev, hipStream_t s) {
+    require(D == 64 || D == 128 || D == 256, "flash_attn: head size must be 64, 128 or 256");
+    require(H % Hkv == 0, "flash_attn: query heads must be a multiple of KV heads");
+    require((int64_t) p.nsplit * kChunkMax >= n_kv, "flash_attn: too few splits for the KV length");
+    const int G = H / Hkv;
+    const uint16_t * kk = (const uint16_t *) k;
+    const uint16_t * vv = (const uint16_t *) v;
+    const uint16_t * mm = (const uint16_t *) mask;
+    if (D == 64) run_split<64>(G, q, q_h, q_s, kk, k_h, k_j, vv, v_h, v_j, mm, m_s, Sq, H, Hkv, n_kv, scale, po, pml, p, n_kv_dev, s);
+    else if (D == 128) run_split<128>(G, q, q_h, q_s, kk, k_h, k_j, vv, v_h, v_j, mm, m_s, Sq, H, Hkv, n_kv, scale, po, pml, p, n_kv_dev, s);
+    else run_split<256>(G, q, q_h, q_s, kk, k_h, k_j, vv, v_h, v_j, mm, m_s, Sq, H, Hkv, n_kv, scale, po, pml, p, n_kv_dev, s);
+}
+
+void launch_flash_attn(const float * q, int64_t q_h, int64_t q_s, const void * k, int64_t k_h, int64_t k_j,
+                       const void * v, int64_t v_h, int64_t v_j, const void * mask, int64_t m_s, float * out, int D,
+                       int Dv, int Sq, int H, int Hkv, int n_kv, float scale, void * ws, size_t ws_size,
+                       hipStream_t s) {
+    require(D == Dv, "flash_attn: K and V head sizes must match");
+    const AttnPlan p = attn_plan(Sq, Hkv, n_kv);
+    require(ws_size >= attn_workspace(Sq, H, Hkv, Dv, n_kv), "flash_attn: workspace too small");
+    float * po = (float *) ws;
+    float2 * pml = (float2 *) ((uint8_t *) ws + align256((size_t) Sq * H * p.nsplit * Dv * sizeof(float)));
+    launch_attn_split(q, q_h, q_s, k, k_h, k_j, v, v_h, v_j, mask, m_s, D, Sq, H, Hkv, n_kv, scale, po, pml, p,
+                      nullptr, s);
+    if (D == 64) k_attn_merge<64><<<(unsigned) (Sq * H), 64, 0, s>>>(po, pml, out, p.nsplit);
+    else if (D == 128) k_attn_merge<128><<<(unsigned) (Sq * H), 128, 0, s>>>(po, pml, out, p.nsplit);
+    else k_attn_merge<256><<<(unsigned) (Sq * H), 256, 0, s>>>(po, pml, out, p.nsplit);
+    check_launch("flash_attn merge");
+}
+
+}  // namespace gcq

@@ -1,0 +1,271 @@
+// elementwise.hip - the decode step's row-wise and glue ops, and synthetic-data fills.
+//
+//  rms_norm  ggml_rms_norm (runtime/src/ops.cpp:144-148), optionally fused with the ggml_mul by a
+//            norm weight that the graph applies next (passes/fold.py:93-114 emits the pair)
+//  rope      ggml_rope_ext, NEOX mode (runtime/src/ops.cpp:277-291, mode 2 from
+//            emit/gguf_runtime.py:76-78)
+//  set_rows  ggml_set_rows f32 -> f16 KV-cache write (runtime/src/ops.cpp:260-275)
+//  get_rows  ggml_get_rows from a Q4_0 / Q8_0 / F16 / F32 table (runtime/src/ops.cpp:302-309)
+//  swiglu    ggml_swiglu_split (runtime/src/ops.cpp:251-258)
+//  add, mul  ggml_add / ggml_mul with a broadcast second operand
+//  argmax    ggml_argmax (runtime/src/ops.cpp:293-300)
+// All are HBM- or launch-bound and move whole rows with 16-byte accesses where the shapes allow.
+#include "gcq_common.h"
+
+namespace gcq {
+
+// ------------------------------------------------------------------------------ rms_norm
+
+// One 256-thread block per row: y = x * (1/sqrt(mean(x^2) + eps)) [* w]. As ggml-cpu, each x*x
+// is rounded to f32 and summed in double, and the mean rounded to f32: a Q4_0 embedding row (exact
+// multiples of its scale) normalized and quantized to Q8_0 hits exact rounding ties, so the scale
+// must come out bit-identical for the codes to.
+__global__ __launch_bounds__(256) void k_rms_norm(const float * __restrict__ x, int64_t ldx, float * __restrict__ y,
+                                                  int64_t ldy, const float * __restrict__ w, int n, float eps) {
+    const float * xr = x + blockIdx.x * ldx;
+    float * yr = y + blockIdx.x * ldy;
+    const float scale = rms_scale(xr, n, eps);
+    for (int i = threadIdx.x; i < n; i += 256) yr[i] = w ? (xr[i] * scale) * w[i] : xr[i] * scale;
+}
+
+// ---------------------------------------------------------------------------------- rope
+
+// One thread per (s, h, pair i < n_dims/2). theta follows ggml's rope cache: it starts at the
+// position and is multiplied by theta_scale once per pair (theta_scale = powf(base, -2/n_dims),
+// computed on the host in f32 as ggml does).
+__global__ void k_rope_neox(const float * __restrict__ x, int64_t sx_s, int64_t sx_h, float * __restrict__ out,
+                            int64_t so_s, int64_t so_h, const int32_t * __restrict__ pos, int D, int H, int S,
+                            int n_dims, float theta_scale, float freq_scale, float attn_factor,
+                            const float * __restrict__ ff) {
+    const int half = n_dims / 2;
+    const int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t per_row = D - half;  // pairs, then the pass-through dims
+    if (t >= (int64_t) S * H * per_row) return;
+    const int i = (int) (t % per_row);
+    const int h = (int) ((t / per_row) % H);
+    const int s = (int) (t / ((int64_t) per_row * H));
+    const float * xr = x + s * sx_s + h * sx_h;
+    float * o = out + s * so_s + h * so_h;
+    if (i >= half) {  // dims n_dims .. D-1 pass through
+        const int d = i - half + n_dims;
+        if (d < D) o[d] = xr[d];
+        return;
+    }
+    float theta = (float) pos[s];
+    for (int k = 0; k < i; k++) theta *= theta_scale;
+    const float f = ff ? ff[i] : 1.0f;
+    const float th = freq_scale * (theta / f);
+    const float c = cosf(th) * attn_factor, sn = sinf(th) * attn_factor;
+    const float x0 = xr[i], x1 = xr[i + half];
+    o[i] = x0 * c - x1 * sn;
+    o[i + half] = x0 * sn + x1 * c;
+}
+
+// ------------------------------------------------------------------------------ set_rows
+
+// dst[h][idx[j]][d] = f16(src[h][j][d]) for j < n, h < Hrows; 8 values per thread. Rows whose
+// index falls outside [0, dst_rows) are not written.
+__global__ void k_set_rows_f16(uint16_t * __restrict__ dst, int64_t dst_h, int64_t dst_j,
+                               const float * __restrict__ src, int64_t src_h, int64_t src_j,
+                               const int32_t * __restrict__ idx, int n, int D, int Hrows, int64_t dst_rows) {
+    const int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    const int per = D / 8;
+    if (t >= (int64_t) n * Hrows * per) return;
+    const int c = (int) (t % per);
+    const int h = (int) ((t / per) % Hrows);
+    const int j = (int) (t / ((int64_t) per * Hrows));
+    const int64_t r = idx[j];
+    if (r < 0 || r >= dst_rows) return;
+    const float * sp = src + h * src_h + j * src_j + 8 * c;
+    uint16_t * dp = dst + h * dst_h + r * dst_j + 8 * c;
+    uint32_t w[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) w[k] = f2h(sp[2 * k]) | ((uint32_t) f2h(sp[2 * k + 1]) << 16);
+    *reinterpret_cast<uint4 *>(dp) = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// ------------------------------------------------------------------------------ get_rows
+
+__global__ void k_get_rows(int type, const uint8_t * __restrict__ tab, int64_t nrows_tab, int D,
+                           const int32_t * __restrict__ idx, float * __restrict__ out, int n) {
+    const int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= (int64_t) n * D) return;
+    const int j = (int) (t / D), c = (int) (t % D);
+    const int64_t r = idx[j];
+    if (r < 0 || r >= nrows_tab) {  // an index outside the table reads as NaN
+        out[t] = __builtin_nanf("");
+        return;
+    }
+    float v;
+    if (type == T_F32) {
+        v = reinterpret_cast<const float *>(tab)[r * D + c];
+    } else if (type == T_F16) {
+        v = h2f(reinterpret_cast<const uint16_t *>(tab)[r * D + c]);
+    } else {
+        const int nb = D / QK;
+        const int64_t blk = r * nb + c / QK;
+        const int e = c % QK;
+        const size_t qbytes = (size_t) nrows_tab * nb * (type == T_Q4_0 ? 16 : 32);
+        const uint16_t * d = reinterpret_cast<const uint16_t *>(tab + align256(qbytes));
+        if (type == T_Q4_0) {
+            const uint8_t b = tab[blk * 16 + (e & 15)];
+            v = (float) ((e < 16 ? (b & 0xF) : (b >> 4)) - 8) * h2f(d[blk]);
+        } else {
+            v = (float) reinterpret_cast<const int8_t *>(tab)[blk * 32 + e] * h2f(d[blk]);
+        }
+    }
+    out[t] = v;
+}
+
+// ---------------------------------------------------------------------- swiglu, add, mul
+
+__global__ void k_swiglu(const float * __restrict__ g, const float * __restrict__ u, float * __restrict__ y, int64_t n) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float a = g[i];
+    y[i] = a / (1.0f + expf(-a)) * u[i];
+}
+
+__global__ void k_binary(int op, const float * __restrict__ a, const float * __restrict__ b, float * __restrict__ y,
+                         int64_t n, int64_t nb) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float bv = b[i % nb];
+    y[i] = op == 0 ? a[i] + bv : a[i] * bv;
+}
+
+// -------------------------------------------------------------------------------- argmax
+
+// One 256-thread block per row; the first index of the maximum (NaN never wins; a row of -inf /
+// NaN gives 0, as ggml's forward_argmax).
+__global__ __launch_bounds__(256) void k_argmax(const float * __restrict__ x, int64_t ldx, int n, int32_t * __restrict__ out) {
+    __shared__ float bv[4];
+    __shared__ int bi[4];
+    const float * xr = x + blockIdx.x * ldx;
+    float v = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int i = threadIdx.x; i < n; i += 256) {
+        const float a = xr[i];
+        if (a > v) {
+            v = a;
+            idx = i;
+        }
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        const float v2 = __shfl_xor(v, o, 64);
+        const int i2 = __shfl_xor(idx, o, 64);
+        if (v2 > v || (v2 == v && i2 < idx)) {
+            v = v2;
+            idx = i2;
+        }
+    }
+    if ((threadIdx.x & 63) == 0) {
+        bv[threadIdx.x >> 6] = v;
+        bi[threadIdx.x >> 6] = idx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; w++) {
+            if (bv[w] > v || (bv[w] == v && bi[w] < idx)) {
+                v = bv[w];
+                idx = bi[w];
+            }
+        }
+        out[blockIdx.x] = (v == -INFINITY || idx == 0x7fffffff) ? 0 : idx;
+    }
+}
+
+// --------------------------------------------------------------------------- synthetic data
+
+// Same stream as the oracle's: twelve 24-bit uniforms summed (Irwin-Hall), centred, scaled by
+// 2^-24 and by stddev. Integer work, an exact scaling and one rounded multiply: bit-identical.
+__global__ void k_fill_normal(float * __restrict__ dst, int64_t n, uint64_t seed, uint64_t offset, float stddev) {
+#pragma clang fp contract(off)
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const uint64_t e = offset + (uint64_t) i;
+    int64_t s = 0;
+#pragma unroll
+    for (int j = 0; j < 6; j++) {
+        const uint64_t r = rnd64(seed, 6 * e + (uint64_t) j);
+        s += (int64_t) (r & 0xffffffu) + (int64_t) ((r >> 32) & 0xffffffu);
+    }
+    const int32_t c = (int32_t) (s - 6 * (int64_t) 0xffffff);
+    dst[i] = ((float) c * (1.0f / 16777216.0f)) * stddev;
+}
+
+__global__ void k_fill_ids(int32_t * __restrict__ dst, int64_t n, uint64_t seed, uint64_t offset, int32_t vocab) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    dst[i] = (int32_t) (rnd64(seed, offset + (uint64_t) i) % (uint64_t) vocab);
+}
+
+// ------------------------------------------------------------------------- host launchers
+
+static inline unsigned nblk(int64_t n, int t) { return (unsigned) ((n + t - 1) / t); }
+
+void launch_rms_norm(const float * x, int64_t ldx, float * y, int64_t ldy, const float * w, int64_t rows, int64_t n,
+                     float eps, hipStream_t s) {
+    if (rows == 0) return;
+    k_rms_norm<<<(unsigned) rows, 256, 0, s>>>(x, ldx, y, ldy, w, (int) n, eps);
+    check_launch("rms_norm");
+}
+
+void launch_rope_neox(const float * x, int64_t sx_s, int64_t sx_h, float * out, int64_t so_s, int64_t so_h,
+                      const int32_t * pos, int64_t D, int64_t H, int64_t S, int n_dims, float freq_base,
+                      float freq_scale, float attn_factor, const float * ff, hipStream_t s) {
+    const float theta_scale = powf(freq_base, -2.0f / (float) n_dims);
+    const int64_t n = S * H * (D - n_dims / 2);
+    if (n == 0) return;
+    k_rope_neox<<<nblk(n, 256), 256, 0, s>>>(x, sx_s, sx_h, out, so_s, so_h, pos, (int) D, (int) H, (int) S, n_dims,
+                                             theta_scale, freq_scale, attn_factor, ff);
+    check_launch("rope");
+}
+
+void launch_set_rows_f16(void * dst, int64_t dst_h, int64_t dst_j, const float * src, int64_t src_h, int64_t src_j,
+                         const int32_t * idx, int64_t n, int64_t D, int64_t Hrows, int64_t dst_rows, hipStream_t s) {
+    const int64_t t = n * Hrows * (D / 8);
+    if (t == 0) return;
+    k_set_rows_f16<<<nblk(t, 256), 256, 0, s>>>((uint16_t *) dst, dst_h, dst_j, src, src_h, src_j, idx, (int) n,
+                                                (int) D, (int) Hrows, dst_rows);
+    check_launch("set_rows");
+}
+
+void launch_get_rows(int type, const void * tab, int64_t nrows_tab, int64_t D, const int32_t * idx, int64_t n,
+                     float * out, hipStream_t s) {
+    if (n * D == 0) return;
+    k_get_rows<<<nblk(n * D, 256), 256, 0, s>>>(type, (const uint8_t *) tab, nrows_tab, (int) D, idx, out, (int) n);
+    check_launch("get_rows");
+}
+
+void launch_swiglu(const float * g, const float * u, float * y, int64_t n, hipStream_t s) {
+    if (n == 0) return;
+    k_swiglu<<<nblk(n, 256), 256, 0, s>>>(g, u, y, n);
+    check_launch("swiglu");
+}
+
+void launch_binary(int op, const float * a, const float * b, float * y, int64_t n, int64_t nb, hipStream_t s) {
+    if (n == 0) return;
+    k_binary<<<nblk(n, 256), 256, 0, s>>>(op, a, b, y, n, nb);
+    check_launch(op == 0 ? "add" : "mul");
+}
+
+void launch_argmax(const float * x, int64_t ldx, int64_t rows, int64_t n, int32_t * out, hipStream_t s) {
+    if (rows == 0) return;
+    k_argmax<<<(unsigned) rows, 256, 0, s>>>(x, ldx, (int) n, out);
+    check_launch("argmax");
+}
+
+void launch_fill_normal(float * dst, int64_t n, uint64_t seed, uint64_t offset, float stddev, hipStream_t s) {
+    if (n == 0) return;
+    k_fill_normal<<<nblk(n, 256), 256, 0, s>>>(dst, n, seed, offset, stddev);
+    check_launch("fill_normal");
+}
+
+void launch_fill_ids(int32_t * dst, int64_t n, uint64_t seed, uint64_t offset, int32_t vocab, hipStream_t s) {
+    if (n == 0) return;
+    k_fill_ids<<<nblk(n, 256), 256, 0, s>>>(dst, n, seed, offset, vocab);
+    check_launch("fill_ids");
+}
+
+}  // namespace gcq

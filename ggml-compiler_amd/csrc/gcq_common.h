@@ -1,0 +1,172 @@
+// gcq_common.h - shared definitions of libgcq's HIP kernels and C ABI (gfx950 only).
+//
+// Type ids are GGUF's (ggml_type): F32=0, F16=1, Q4_0=2, Q8_0=8, Q4_K=12, Q8_K=15, I32=26.
+//
+// Device layouts (all offsets 256-byte aligned, see gcq_layout below):
+//  * Weights ("packed"): what gcq_pack_weights makes from ggml's block rows.
+//      Q4_0: nibbles [N][K/32][16 B], then fp16 scales [N][K/32]. Byte j of a block's 16 holds
+//            element j (low nibble) and j+16 (high nibble), stored code = q + 8, as in ggml.
+//      Q8_0: codes [N][K/32][32 B], then fp16 scales [N][K/32].
+//      Q4_K: ggml's 144-byte super-blocks unchanged (already 16-byte aligned rows).
+//  * Quantized activations ("act"), rows of the batch b < B:
+//      Q8_0 (for Q4_0 / Q8_0 weights): codes [B][K] int8, then per 32-block {float d, int sum}
+//            [B][K/32]: d is the fp16 scale ggml stores (as its exact f32 value) and sum the
+//            block's code sum (used to fold Q4_0's -8 offset into one integer term).
+//      Q8_K (for Q4_K weights): codes [B][K] int8, then bsums int16 [B][K/16] (ggml's sums of 16
+//            codes), then d float [B][K/256].
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+namespace gcq {
+
+enum : int { T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q8_0 = 8, T_Q4_K = 12, T_Q8_K = 15, T_I32 = 26 };
+
+constexpr int QK = 32;    // Q4_0 / Q8_0 block
+constexpr int QKK = 256;  // K-quant super-block
+
+// ------------------------------------------------------------------------------ host helpers
+
+void set_error(const std::string & msg);
+const char * last_error();
+
+struct Fail {
+    std::string msg;
+};
+[[noreturn]] inline void fail(const std::string & msg) { throw Fail{msg}; }
+inline void require(bool ok, const std::string & msg) {
+    if (!ok) fail(msg);
+}
+void check_hip(hipError_t e, const char * what);
+void check_launch(const char * what);
+
+inline hipStream_t as_stream(void * s) { return reinterpret_cast<hipStream_t>(s); }
+__host__ __device__ inline size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
+inline bool aligned(const void * p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+size_t block_elems(int type);   // elements per block, 0 if unknown
+size_t block_bytes(int type);   // bytes per block in ggml's layout
+size_t row_bytes(int type, int64_t n);
+
+// Byte offsets inside a packed weight and a quantized activation buffer.
+struct WeightLayout {
+    size_t qs = 0, d = 0, total = 0;
+};
+WeightLayout weight_layout(int type, int64_t nrows, int64_t k);
+struct ActLayout {
+    size_t codes = 0, meta = 0, d = 0, total = 0;
+};
+ActLayout act_layout(int wtype, int64_t B, int64_t k);
+
+// Split-K plan of the decode attention (attn.hip).
+struct AttnPlan {
+    int nsplit, chunk;
+};
+AttnPlan attn_plan(int Sq, int Hkv, int n_kv);
+
+// Wraps a C-ABI body: 0 on success, -1 with last_error set on failure.
+template <class F>
+int guarded(F && f) {
+    try {
+        f();
+        return 0;
+    } catch (const Fail & e) {
+        set_error(e.msg);
+    } catch (const std::exception & e) {
+        set_error(e.what());
+    } catch (...) {
+        set_error("unknown error");
+    }
+    return -1;
+}
+
+// ---------------------------------------------------------------------------- device helpers
+
+__device__ __forceinline__ float h2f(uint16_t h) {
+    _Float16 v;
+    __builtin_memcpy(&v, &h, 2);
+    return (float) v;
+}
+// fp32 -> fp16, round to nearest even (v_cvt_f16_f32 in the default rounding mode).
+__device__ __forceinline__ uint16_t f2h(float f) {
+    _Float16 v = (_Float16) f;
+    uint16_t h;
+    __builtin_memcpy(&h, &v, 2);
+    return h;
+}
+
+// fp32 -> fp16 bits, round to nearest even, in integer arithmetic. Used for every stored quant
+// scale: it keeps -0 and fp16 subnormals exact, whatever the compiler folds around a conversion
+// instruction (a multiply feeding v_cvt_f16_f32 may become v_fma_mix with a +0 addend, which
+// turns -0 into +0).
+__device__ __forceinline__ uint16_t f2h_exact(float f) {
+    const uint32_t x = __float_as_uint(f);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const uint32_t ax = x & 0x7fffffffu;
+    if (ax > 0x7f800000u) return (uint16_t) (sign | 0x7e00u);
+    if (ax >= 0x47800000u) return (uint16_t) (sign | 0x7c00u);
+    if (ax < 0x38800000u) {
+        const uint32_t e = ax >> 23;
+        if (e < 102) return (uint16_t) sign;
+        const uint32_t m = (ax & 0x7fffffu) | 0x800000u;
+        const uint32_t shift = 126 - e;
+        uint32_t h = m >> shift;
+        const uint32_t rem = m & ((1u << shift) - 1);
+        const uint32_t half = 1u << (shift - 1);
+        if (rem > half || (rem == half && (h & 1u))) h++;
+        return (uint16_t) (sign | h);
+    }
+    uint32_t h = (((ax >> 23) - 112) << 10) | ((ax >> 13) & 0x3ffu);
+    const uint32_t rem = ax & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;
+    return (uint16_t) (sign | h);
+}
+
+__device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+template <int W = 64>
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+template <int W = 64>
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = W / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+template <int W = 64>
+__device__ __forceinline__ int wave_isum(int v) {
+#pragma unroll
+    for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// 1/sqrt(mean(x^2) + eps) of one row, for a 256-thread block (all threads call it): squares
+// rounded to f32, summed in double, mean rounded to f32, as ggml-cpu's rms_norm.
+__device__ __forceinline__ float rms_scale(const float * xr, int n, float eps) {
+    __shared__ double red[4];
+    double s = 0.0;
+    for (int i = threadIdx.x; i < n; i += 256) s += (double) (xr[i] * xr[i]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+    __syncthreads();
+    const float mean = (float) ((red[0] + red[1] + red[2] + red[3]) / (double) n);
+    return 1.0f / sqrtf(mean + eps);
+}
+
+// Counter-based splitmix64 (output i of a generator whose state starts at seed).
+__device__ __forceinline__ uint64_t rnd64(uint64_t seed, uint64_t i) {
+    uint64_t z = seed + (i + 1) * 0x9e3779b97f4a7c15ull;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+
+}  // namespace gcq

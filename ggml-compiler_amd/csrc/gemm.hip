@@ -1,0 +1,203 @@
+// gemm.hip - quantized mat-mul for prefill (M > 8 activation rows) on int8 MFMA.
+//
+// Replaces ggml_mul_mat of a Q8_0 / Q4_0 weight with an f32 src1 of many rows
+// (runtime/src/ops.cpp:107-119). As ggml, src1 is quantized to Q8_0 per 32 values (quant.hip);
+// then out[m, n] = sum_blk d_x[m, blk] * d_w[n, blk] * isum(m, n, blk) with isum the exact int32
+// dot of one 32-value block.
+//
+// gfx950's v_mfma_i32_32x32x32_i8 has a depth of exactly one quant block, so every MFMA yields
+// the 32x32 tile of block sums isum(., ., blk) exactly; the fp16-scale epilogue folds it into fp32
+// accumulators (d_w and d_x from LDS). Workgroup tile 128 (m) x 128 (n), 4 wavefronts of 64x64
+// (2x2 MFMA tiles); each stage stages 4 K-blocks of A (activation codes) and B (weight codes,
+// Q4_0 nibbles expanded to signed int8 q-8) in LDS with a 16-byte row pad against bank
+// conflicts. Tiles are numbered so that the workgroups sharing one weight tile land on the same
+// XCD (and L2).
+#include "gcq_common.h"
+
+namespace gcq {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+constexpr int GBM = 128, GBN = 128, GKB = 4;
+constexpr int GPITCH = GKB * 32 + 16;
+
+__device__ __forceinline__ uint32_t q4_to_s8(uint32_t w) {  // 4 nibbles (0..15) -> 4 int8 (q - 8)
+    return (((w & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
+}
+
+// RAW: write the int32 block sums of block `raw_blk` instead of the scaled result.
+template <int TYPE, bool RAW>
+__global__ __launch_bounds__(256) void k_gemm(const uint8_t * __restrict__ wqs, const uint16_t * __restrict__ wd,
+                                              const int8_t * __restrict__ xc, const float2 * __restrict__ xm,
+                                              float * y, const float * res, int32_t * __restrict__ yraw, int M, int N,
+                                              int nb, int ldy, int raw_blk) {
+    __shared__ __attribute__((aligned(16))) int8_t sA[GBM * GPITCH];
+    __shared__ __attribute__((aligned(16))) int8_t sB[GBN * GPITCH];
+    __shared__ float sdx[GKB][GBM];
+    __shared__ float sdw[GKB][GBN];
+
+    // Tile numbering: ids id, id+8, ... run on one XCD; give each XCD a contiguous run of tiles,
+    // m-tiles fastest, so the workgroups that read one weight tile share an L2.
+    const int mt = (M + GBM - 1) / GBM, nt = (N + GBN - 1) / GBN;
+    const int total = mt * nt;
+    int id = blockIdx.x;
+    if (total % 8 == 0) id = (id % 8) * (total / 8) + id / 8;
+    const int m0 = (id % mt) * GBM, n0 = (id / mt) * GBN;
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int K = nb * 32;
+    float acc[2][2][16];
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int b = 0; b < 2; b++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[a][b][r] = 0.0f;
+
+    const int kb_begin = RAW ? raw_blk : 0;
+    const int kb_end = RAW ? raw_blk + 1 : nb;
+    for (int kb0 = kb_begin; kb0 < kb_end; kb0 += GKB) {
+        const int nblk = min(GKB, kb_end - kb0);
+        // A: activation codes, 16 B chunks.
+        for (int c = tid; c < GBM * GKB * 2; c += 256) {
+            const int row = c / (GKB * 2), part = c % (GKB * 2);
+            if (part < nblk * 2) {
+                const int gm = min(m0 + row, M - 1);
+                *reinterpret_cast<int4 *>(sA + row * GPITCH + part * 16) =
+                    *reinterpret_cast<const int4 *>(xc + (size_t) gm * K + (size_t) kb0 * 32 + part * 16);
+            }
+        }
+        // B: weight codes.
+        if constexpr (TYPE == T_Q8_0) {
+            for (int c = tid; c < GBN * GKB * 2; c += 256) {
+                const int row = c / (GKB * 2), part = c % (GKB * 2);
+                if (part < nblk * 2) {
+                    const int gn = min(n0 + row, N - 1);
+                    *reinterpret_cast<int4 *>(sB + row * GPITCH + part * 16) =
+                        *reinterpret_cast<const int4 *>(wqs + (size_t) gn * K + (size_t) kb0 * 32 + part * 16);
+                }
+            }
+        } else {
+            for (int c = tid; c < GBN * GKB; c += 256) {
+                const int row = c / GKB, j = c % GKB;
+                if (j < nblk) {
+                    const int gn = min(n0 + row, N - 1);
+                    const uint4 w = *reinterpret_cast<const uint4 *>(wqs + ((size_t) gn * nb + kb0 + j) * 16);
+                    int4 lo, hi;
+                    lo.x = (int) q4_to_s8(w.x);
+                    lo.y = (int) q4_to_s8(w.y);
+                    lo.z = (int) q4_to_s8(w.z);
+                    lo.w = (int) q4_to_s8(w.w);
+                    hi.x = (int) q4_to_s8(w.x >> 4);
+                    hi.y = (int) q4_to_s8(w.y >> 4);
+                    hi.z = (int) q4_to_s8(w.z >> 4);
+                    hi.w = (int) q4_to_s8(w.w >> 4);
+                    *reinterpret_cast<int4 *>(sB + row * GPITCH + j * 32) = lo;
+                    *reinterpret_cast<int4 *>(sB + row * GPITCH + j * 32 + 16) = hi;
+                }
+            }
+        }
+        for (int c = tid; c < GBM * GKB; c += 256) {
+            const int row = c / GKB, j = c % GKB;
+            if (j < nblk) sdx[j][row] = xm[(size_t) min(m0 + row, M - 1) * nb + kb0 + j].x;
+        }
+        for (int c = tid; c < GBN * GKB; c += 256) {
+            const int row = c / GKB, j = c % GKB;
+            if (j < nblk) sdw[j][row] = h2f(wd[(size_t) min(n0 + row, N - 1) * nb + kb0 + j]);
+        }
+        __syncthreads();
+
+        for (int j = 0; j < nblk; j++) {
+            v4i af[2], bf[2];
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                af[t] = *reinterpret_cast<const v4i *>(sA + (wm * 64 + t * 32 + (lane & 31)) * GPITCH + j * 32 + 16 * (lane >> 5));
+                bf[t] = *reinterpret_cast<const v4i *>(sB + (wn * 64 + t * 32 + (lane & 31)) * GPITCH + j * 32 + 16 * (lane >> 5));
+            }
+#pragma unroll
+            for (int tm = 0; tm < 2; tm++) {
+#pragma unroll
+                for (int tn = 0; tn < 2; tn++) {
+                    v16i c = {};
+                    c = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[tm], bf[tn], c, 0, 0, 0);
+                    if constexpr (RAW) {
+#pragma unroll
+                        for (int r = 0; r < 16; r++) acc[tm][tn][r] = __int_as_float(c[r]);
+                    } else {
+                        const float dw = sdw[j][wn * 64 + tn * 32 + (lane & 31)];
+#pragma unroll
+                        for (int r = 0; r < 16; r++) {
+                            const int mi = wm * 64 + tm * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+                            acc[tm][tn][r] += ((float) c[r] * dw) * sdx[j][mi];
+                        }
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int tm = 0; tm < 2; tm++)
+#pragma unroll
+        for (int tn = 0; tn < 2; tn++) {
+            const int n = n0 + wn * 64 + tn * 32 + (lane & 31);
+            if (n >= N) continue;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int m = m0 + wm * 64 + tm * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+                if (m >= M) continue;
+                if constexpr (RAW) yraw[(size_t) m * N + n] = __float_as_int(acc[tm][tn][r]);
+                else {
+                    const size_t o = (size_t) m * ldy + n;
+                    y[o] = res ? acc[tm][tn][r] + res[o] : acc[tm][tn][r];
+                }
+            }
+        }
+}
+
+void launch_gemm(int type, const void * wv, int64_t N, int64_t K, const void * act, int64_t M, float * y, int64_t ldy,
+                 hipStream_t s, const float * res) {
+    const WeightLayout L = weight_layout(type, N, K);
+    const ActLayout A = act_layout(type, M, K);
+    const uint8_t * w = (const uint8_t *) wv;
+    const uint8_t * a = (const uint8_t *) act;
+    const unsigned grid = (unsigned) (((M + GBM - 1) / GBM) * ((N + GBN - 1) / GBN));
+    const int nb = (int) (K / 32);
+    if (type == T_Q8_0)
+        k_gemm<T_Q8_0, false><<<grid, 256, 0, s>>>(w + L.qs, (const uint16_t *) (w + L.d), (const int8_t *) (a + A.codes),
+                                                    (const float2 *) (a + A.meta), y, res, nullptr, (int) M, (int) N, nb,
+                                                    (int) ldy, 0);
+    else if (type == T_Q4_0)
+        k_gemm<T_Q4_0, false><<<grid, 256, 0, s>>>(w + L.qs, (const uint16_t *) (w + L.d), (const int8_t *) (a + A.codes),
+                                                    (const float2 *) (a + A.meta), y, res, nullptr, (int) M, (int) N, nb,
+                                                    (int) ldy, 0);
+    else
+        fail("gemm: unsupported weight type " + std::to_string(type));
+    check_launch("gemm");
+}
+
+void launch_gemm_block_isums(int type, const void * wv, int64_t N, int64_t K, const void * act, int64_t M, int blk,
+                             int32_t * out, hipStream_t s) {
+    const WeightLayout L = weight_layout(type, N, K);
+    const ActLayout A = act_layout(type, M, K);
+    const uint8_t * w = (const uint8_t *) wv;
+    const uint8_t * a = (const uint8_t *) act;
+    const unsigned grid = (unsigned) (((M + GBM - 1) / GBM) * ((N + GBN - 1) / GBN));
+    const int nb = (int) (K / 32);
+    if (type == T_Q8_0)
+        k_gemm<T_Q8_0, true><<<grid, 256, 0, s>>>(w + L.qs, (const uint16_t *) (w + L.d), (const int8_t *) (a + A.codes),
+                                                   (const float2 *) (a + A.meta), nullptr, nullptr, out, (int) M, (int) N, nb, 0,
+                                                   blk);
+    else if (type == T_Q4_0)
+        k_gemm<T_Q4_0, true><<<grid, 256, 0, s>>>(w + L.qs, (const uint16_t *) (w + L.d), (const int8_t *) (a + A.codes),
+                                                   (const float2 *) (a + A.meta), nullptr, nullptr, out, (int) M, (int) N, nb, 0,
+                                                   blk);
+    else
+        fail("gemm: unsupported weight type " + std::to_string(type));
+    check_launch("gemm isums");
+}
+
+}  // namespace gcq

@@ -1,0 +1,529 @@
+// gemv.hip - quantized mat-vec for decode (batch 1..8): y[b, n] = sum_k W[n, k] x[b, k].
+//
+// Replaces ggml_mul_mat on a Q4_0 / Q8_0 / Q4_K weight with an f32 src1 of 1..8 rows
+// (runtime/src/ops.cpp:107-119 -> runtime/include/ggml_compiler_ops.h:116-122). As ggml-cpu
+// does, the activation is first quantized to the weight's vec_dot_type (quant.hip); each
+// weight block then contributes an exact int32 dot sum times its fp16 scale(s), accumulated in
+// fp32 (ggml vec_dot_q4_0_q8_0 / vec_dot_q8_0_q8_0 / vec_dot_q4_K_q8_K).
+//
+// HBM-bound by the weight stream. One wavefront owns R rows; lane l takes blocks l, l+64, ...
+// so each weight load instruction moves 64 x 16 B of one row contiguously. All of a lane's
+// weight loads for a pass of 64*NBL blocks are issued before any math (NBL*R*16 B in flight
+// per lane); the small activation (x codes + scales) is re-read from L1/L2 per block and
+// reused across the R rows; integer dots use v_dot4_i32_i8; a butterfly over the wavefront
+// finishes each output.
+#include "gcq_common.h"
+
+#include <algorithm>
+
+namespace gcq {
+
+// Integer dot of one Q4_0 block (16 B of nibbles) with one Q8_0 activation block (32 codes):
+// sum_j (q_j - 8) * x_j, computed as sum q_j x_j - 8 sum x_j (xsum from the quantizer).
+__device__ __forceinline__ int dot_q4_0(const uint4 w, const int4 xa, const int4 xb, int xsum) {
+    int s = 0;
+    s = sdot4((int) (w.x & 0x0F0F0F0Fu), xa.x, s);
+    s = sdot4((int) (w.y & 0x0F0F0F0Fu), xa.y, s);
+    s = sdot4((int) (w.z & 0x0F0F0F0Fu), xa.z, s);
+    s = sdot4((int) (w.w & 0x0F0F0F0Fu), xa.w, s);
+    s = sdot4((int) ((w.x >> 4) & 0x0F0F0F0Fu), xb.x, s);
+    s = sdot4((int) ((w.y >> 4) & 0x0F0F0F0Fu), xb.y, s);
+    s = sdot4((int) ((w.z >> 4) & 0x0F0F0F0Fu), xb.z, s);
+    s = sdot4((int) ((w.w >> 4) & 0x0F0F0F0Fu), xb.w, s);
+    return s - 8 * xsum;
+}
+
+__device__ __forceinline__ int dot_q8_0(const uint4 wa, const uint4 wb, const int4 xa, const int4 xb) {
+    int s = 0;
+    s = sdot4((int) wa.x, xa.x, s);
+    s = sdot4((int) wa.y, xa.y, s);
+    s = sdot4((int) wa.z, xa.z, s);
+    s = sdot4((int) wa.w, xa.w, s);
+    s = sdot4((int) wb.x, xb.x, s);
+    s = sdot4((int) wb.y, xb.y, s);
+    s = sdot4((int) wb.z, xb.z, s);
+    s = sdot4((int) wb.w, xb.w, s);
+    return s;
+}
+
+// One 64-value chunk c of a Q4_K super-block (32 bytes of nibbles: low = sub-block 2c, high =
+// sub-block 2c+1) against 64 Q8_K codes: the two sub-block dots.
+__device__ __forceinline__ void dot_q4_K_chunk(const uint4 wa, const uint4 wb, const int4 x0, const int4 x1,
+                                               const int4 x2, const int4 x3, int & lo, int & hi) {
+    const uint32_t w[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+    const int xl[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    const int xh[8] = {x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
+    int a = 0, b = 0;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        a = sdot4((int) (w[j] & 0x0F0F0F0Fu), xl[j], a);
+        b = sdot4((int) ((w[j] >> 4) & 0x0F0F0F0Fu), xh[j], b);
+    }
+    lo = a;
+    hi = b;
+}
+
+__device__ __forceinline__ void scale_min_k4_w(int j, const uint32_t s[3], int & sc, int & m) {
+    auto byte = [&](int i) { return (int) ((s[i >> 2] >> (8 * (i & 3))) & 0xff); };
+    if (j < 4) {
+        sc = byte(j) & 63;
+        m = byte(j + 4) & 63;
+    } else {
+        sc = (byte(j + 4) & 0xF) | ((byte(j - 4) >> 6) << 4);
+        m = (byte(j + 4) >> 4) | ((byte(j) >> 6) << 4);
+    }
+}
+
+// ------------------------------------------------------------------ Q4_0 / Q8_0 kernel
+
+template <int TYPE, int B, int R, int NBL>
+__global__ __launch_bounds__(256) void k_gemv_q0(const uint8_t * __restrict__ wqs, const uint16_t * __restrict__ wd,
+                                                 const int8_t * __restrict__ xc, const float2 * __restrict__ xm,
+                                                 float * y, const float * res, int N, int nb, int ldy) {
+    constexpr int CV = TYPE == T_Q4_0 ? 1 : 2;  // uint4 per block
+    const int lane = threadIdx.x & 63;
+    const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
+    if (row0 >= N) return;
+    const int K = nb * QK;
+    const uint4 * qs = reinterpret_cast<const uint4 *>(wqs);
+    float acc[R][B];
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int b = 0; b < B; b++) acc[r][b] = 0.0f;
+
+    for (int base = 0; base < nb; base += 64 * NBL) {
+        uint4 w[NBL][R][CV];
+        float d[NBL][R];
+#pragma unroll
+        for (int i = 0; i < NBL; i++) {
+            const int blk = base + lane + 64 * i;
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const int row = min(row0 + r, N - 1);  // rows past N recompute N-1; never stored
+                if (blk < nb) {
+                    const size_t o = (size_t) row * nb + blk;
+#pragma unroll
+                    for (int c = 0; c < CV; c++) w[i][r][c] = qs[o * CV + c];
+                    d[i][r] = h2f(wd[o]);
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NBL; i++) {
+            const int blk = base + lane + 64 * i;
+            if (blk >= nb) break;
+#pragma unroll
+            for (int b = 0; b < B; b++) {
+                const int4 * xp = reinterpret_cast<const int4 *>(xc + (size_t) b * K + (size_t) blk * QK);
+                const int4 xa = xp[0], xb = xp[1];
+                const float2 m = xm[(size_t) b * nb + blk];
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    int s;
+                    if constexpr (TYPE == T_Q4_0) s = dot_q4_0(w[i][r][0], xa, xb, __float_as_int(m.y));
+                    else s = dot_q8_0(w[i][r][0], w[i][r][CV - 1], xa, xb);
+                    acc[r][b] += ((float) s * d[i][r]) * m.x;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int b = 0; b < B; b++) {
+            const float v = wave_sum(acc[r][b]);
+            if (lane == r * B + b && row0 + r < N) {
+                const size_t o = (size_t) b * ldy + row0 + r;
+                y[o] = res ? v + res[o] : v;
+            }
+        }
+}
+
+// Persistent variant for rows that fit one pass (nb <= 64*NBL): each wavefront keeps its lanes'
+// activation blocks in registers for the whole launch and walks row groups g, g + waves, ...,
+// loading the next group's weights before it reduces the current one, so a wavefront always has
+// R*NBL*(16 or 32) bytes per lane of HBM reads in flight.
+template <int TYPE, int B, int R, int NBL>
+__global__ __launch_bounds__(256) void k_gemv_p(const uint8_t * __restrict__ wqs, const uint16_t * __restrict__ wd,
+                                                const int8_t * __restrict__ xc, const float2 * __restrict__ xm,
+                                                float * y, const float * res, int N, int nb, int ldy) {
+    constexpr int CV = TYPE == T_Q4_0 ? 1 : 2;
+    const int lane = threadIdx.x & 63;
+    const int nw = gridDim.x * 4;
+    const int ng = (N + R - 1) / R;
+    const int K = nb * QK;
+    const uint4 * qs = reinterpret_cast<const uint4 *>(wqs);
+
+    uint4 w[NBL][R][CV];
+    float d[NBL][R];
+    auto load = [&](int g, uint4 (&wv)[NBL][R][CV], float (&dv)[NBL][R]) {
+#pragma unroll
+        for (int i = 0; i < NBL; i++) {
+            const int blk = lane + 64 * i;
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const int row = min(g * R + r, N - 1);
+                if (blk < nb) {
+                    const size_t o = (size_t) row * nb + blk;
+#pragma unroll
+                    for (int c = 0; c < CV; c++) wv[i][r][c] = qs[o * CV + c];
+                    dv[i][r] = h2f(wd[o]);
+                }
+            }
+        }
+    };
+
+    int g = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (g < ng) load(g, w, d);  // first weights in flight before the activation loads
+
+    int4 xa[NBL][B], xb[NBL][B];
+    float2 xmv[NBL][B];
+#pragma unroll
+    for (int i = 0; i < NBL; i++) {
+        const int blk = lane + 64 * i;
+#pragma unroll
+        for (int b = 0; b < B; b++) {
+            if (blk < nb) {
+                const int4 * xp = reinterpret_cast<const int4 *>(xc + (size_t) b * K + (size_t) blk * QK);
+                xa[i][b] = xp[0];
+                xb[i][b] = xp[1];
+                xmv[i][b] = xm[(size_t) b * nb + blk];
+            }
+        }
+    }
+
+    while (g < ng) {
+        const int gn = g + nw;
+        uint4 wn[NBL][R][CV];
+        float dn[NBL][R];
+        if (gn < ng) load(gn, wn, dn);
+        float acc[R][B];
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int b = 0; b < B; b++) acc[r][b] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NBL; i++) {
+            if (lane + 64 * i >= nb) break;
+#pragma unroll
+            for (int b = 0; b < B; b++) {
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    int s;
+                    if constexpr (TYPE == T_Q4_0) s = dot_q4_0(w[i][r][0], xa[i][b], xb[i][b], __float_as_int(xmv[i][b].y));
+                    else s = dot_q8_0(w[i][r][0], w[i][r][CV - 1], xa[i][b], xb[i][b]);
+                    acc[r][b] += ((float) s * d[i][r]) * xmv[i][b].x;
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int b = 0; b < B; b++) {
+                const float v = wave_sum(acc[r][b]);
+                if (lane == r * B + b && g * R + r < N) {
+                    const size_t o = (size_t) b * ldy + g * R + r;
+                    y[o] = res ? v + res[o] : v;
+                }
+            }
+#pragma unroll
+        for (int i = 0; i < NBL; i++)
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+#pragma unroll
+                for (int c = 0; c < CV; c++) w[i][r][c] = wn[i][r][c];
+                d[i][r] = dn[i][r];
+            }
+        g = gn;
+    }
+}
+
+// ----------------------------------------------------------------------------- Q4_K kernel
+
+// Lane task = (super-block, 64-value chunk): 4 tasks per super-block, NBL tasks per lane per
+// pass. Per task: the 16-byte header (d, dmin, packed scales), 32 bytes of nibbles.
+template <int B, int R, int NBL>
+__global__ __launch_bounds__(256) void k_gemv_q4_K(const uint8_t * __restrict__ w, const int8_t * __restrict__ xc,
+                                                   const int16_t * __restrict__ xbs, const float * __restrict__ xd,
+                                                   float * y, const float * res, int N, int nsb, int ldy) {
+    const int lane = threadIdx.x & 63;
+    const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
+    if (row0 >= N) return;
+    const int K = nsb * QKK;
+    const int ntask = nsb * 4;
+    const size_t rowb = (size_t) nsb * 144;
+    float acc[R][B];
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int b = 0; b < B; b++) acc[r][b] = 0.0f;
+
+    for (int base = 0; base < ntask; base += 64 * NBL) {
+        uint4 hdr[NBL][R], qa[NBL][R], qb[NBL][R];
+#pragma unroll
+        for (int i = 0; i < NBL; i++) {
+            const int t = base + lane + 64 * i;
+            if (t < ntask) {
+                const int sb = t >> 2, c = t & 3;
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    const int row = min(row0 + r, N - 1);
+                    const uint4 * p = reinterpret_cast<const uint4 *>(w + row * rowb + (size_t) sb * 144);
+                    hdr[i][r] = p[0];
+                    qa[i][r] = p[1 + 2 * c];
+                    qb[i][r] = p[2 + 2 * c];
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NBL; i++) {
+            const int t = base + lane + 64 * i;
+            if (t >= ntask) break;
+            const int sb = t >> 2, c = t & 3;
+#pragma unroll
+            for (int b = 0; b < B; b++) {
+                const int4 * xp = reinterpret_cast<const int4 *>(xc + (size_t) b * K + (size_t) sb * QKK + 64 * c);
+                const int4 x0 = xp[0], x1 = xp[1], x2 = xp[2], x3 = xp[3];
+                const int2 bs = *reinterpret_cast<const int2 *>(xbs + (size_t) b * (K / 16) + sb * 16 + 4 * c);
+                const int bs01 = (int) (int16_t) (bs.x & 0xffff) + (int) (int16_t) (bs.x >> 16);
+                const int bs23 = (int) (int16_t) (bs.y & 0xffff) + (int) (int16_t) (bs.y >> 16);
+                const float dx = xd[(size_t) b * nsb + sb];
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    const uint32_t sc3[3] = {hdr[i][r].y, hdr[i][r].z, hdr[i][r].w};
+                    int sc0, m0, sc1, m1, lo, hi;
+                    scale_min_k4_w(2 * c, sc3, sc0, m0);
+                    scale_min_k4_w(2 * c + 1, sc3, sc1, m1);
+                    dot_q4_K_chunk(qa[i][r], qb[i][r], x0, x1, x2, x3, lo, hi);
+                    const int isc = sc0 * lo + sc1 * hi;
+                    const int imin = m0 * bs01 + m1 * bs23;
+                    const float dw = h2f((uint16_t) (hdr[i][r].x & 0xffff)) * dx;
+                    const float dm = h2f((uint16_t) (hdr[i][r].x >> 16)) * dx;
+                    acc[r][b] += dw * (float) isc - dm * (float) imin;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int b = 0; b < B; b++) {
+            const float v = wave_sum(acc[r][b]);
+            if (lane == r * B + b && row0 + r < N) {
+                const size_t o = (size_t) b * ldy + row0 + r;
+                y[o] = res ? v + res[o] : v;
+            }
+        }
+}
+
+// -------------------------------------------------------------------- integer-sum dumps
+
+// The int32 block sums the GEMV kernels form, written out for bit-exact comparison:
+// Q4_0 / Q8_0: out[b][n][blk]; Q4_K: out[b][n][sb][10] = 8 sub-block dots, isc, imin.
+__global__ void k_isums_q0(int type, const uint8_t * wqs, const uint16_t *, const int8_t * xc, const float2 * xm,
+                           int32_t * out, int N, int nb, int B) {
+    const int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= (int64_t) B * N * nb) return;
+    const int blk = (int) (t % nb);
+    const int n = (int) ((t / nb) % N);
+    const int b = (int) (t / ((int64_t) nb * N));
+    const int K = nb * QK;
+    const int4 * xp = reinterpret_cast<const int4 *>(xc + (size_t) b * K + (size_t) blk * QK);
+    const size_t o = (size_t) n * nb + blk;
+    int s;
+    if (type == T_Q4_0) {
+        s = dot_q4_0(reinterpret_cast<const uint4 *>(wqs)[o], xp[0], xp[1], __float_as_int(xm[(size_t) b * nb + blk].y));
+    } else {
+        const uint4 * q = reinterpret_cast<const uint4 *>(wqs) + 2 * o;
+        s = dot_q8_0(q[0], q[1], xp[0], xp[1]);
+    }
+    out[t] = s;
+}
+
+__global__ void k_isums_q4_K(const uint8_t * w, const int8_t * xc, const int16_t * xbs, int32_t * out, int N, int nsb,
+                             int B) {
+    const int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= (int64_t) B * N * nsb) return;
+    const int sb = (int) (t % nsb);
+    const int n = (int) ((t / nsb) % N);
+    const int b = (int) (t / ((int64_t) nsb * N));
+    const int K = nsb * QKK;
+    const uint4 * p = reinterpret_cast<const uint4 *>(w + (size_t) n * nsb * 144 + (size_t) sb * 144);
+    const uint4 hdr = p[0];
+    const uint32_t sc3[3] = {hdr.y, hdr.z, hdr.w};
+    int32_t * o = out + t * 10;
+    int isc = 0, imin = 0;
+    for (int c = 0; c < 4; c++) {
+        const int4 * xp = reinterpret_cast<const int4 *>(xc + (size_t) b * K + (size_t) sb * QKK + 64 * c);
+        int lo, hi, sc0, m0, sc1, m1;
+        dot_q4_K_chunk(p[1 + 2 * c], p[2 + 2 * c], xp[0], xp[1], xp[2], xp[3], lo, hi);
+        scale_min_k4_w(2 * c, sc3, sc0, m0);
+        scale_min_k4_w(2 * c + 1, sc3, sc1, m1);
+        const int16_t * bs = xbs + (size_t) b * (K / 16) + sb * 16 + 4 * c;
+        o[2 * c] = lo;
+        o[2 * c + 1] = hi;
+        isc += sc0 * lo + sc1 * hi;
+        imin += m0 * (bs[0] + bs[1]) + m1 * (bs[2] + bs[3]);
+    }
+    o[8] = isc;
+    o[9] = imin;
+}
+
+// -------------------------------------------------------------------------------- dispatch
+
+// Compute units of the current device (cached per thread and device).
+int cu_count() {
+    static thread_local int dev = -1, cus = 0;
+    int d = 0;
+    check_hip(hipGetDevice(&d), "hipGetDevice");
+    if (d != dev) {
+        check_hip(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, d), "CU count");
+        dev = d;
+    }
+    return cus;
+}
+
+namespace {
+
+// Rows per wavefront and blocks-per-lane per pass, by batch size and row length.
+constexpr int kR = 2;
+constexpr int kRp = 2;        // rows per wavefront step of the persistent kernel
+constexpr int kWgPerCu = 4;   // persistent grid: workgroups per CU
+
+template <int TYPE, int B, int NBL>
+void run_p(const uint8_t * w, const WeightLayout & L, const int8_t * xc, const float2 * xm, float * y, const float * res, int N, int nb,
+           int ldy, hipStream_t s) {
+    const int groups = (N + kRp - 1) / kRp;
+    const unsigned grid = (unsigned) std::max(1, std::min((groups + 3) / 4, cu_count() * kWgPerCu));
+    k_gemv_p<TYPE, B, kRp, NBL><<<grid, 256, 0, s>>>(w + L.qs, (const uint16_t *) (w + L.d), xc, xm, y, res, N, nb, ldy);
+}
+
+int pick_nbl(int tasks) {  // tasks per row (blocks, or Q4_K chunks)
+    const int per_lane = (tasks + 63) / 64;
+    if (per_lane <= 1) return 1;
+    if (per_lane <= 2) return 2;
+    if (per_lane <= 4) return 4;
+    return 8;
+}
+
+template <int TYPE, int B, int NBL>
+void run_q0(const uint8_t * w, const WeightLayout & L, const int8_t * xc, const float2 * xm, float * y, const float * res,
+            int N, int nb, int ldy, hipStream_t s) {
+    const unsigned grid = (unsigned) ((N + 4 * kR - 1) / (4 * kR));
+    k_gemv_q0<TYPE, B, kR, NBL><<<grid, 256, 0, s>>>(w + L.qs, (const uint16_t *) (w + L.d), xc, xm, y, res, N, nb, ldy);
+}
+
+template <int TYPE, int B>
+void run_q0_nbl(int nbl, const uint8_t * w, const WeightLayout & L, const int8_t * xc, const float2 * xm, float * y,
+                const float * res, int N, int nb, int ldy, hipStream_t s) {
+    if constexpr (B <= 4) {  // rows of up to 128 blocks: the persistent kernel
+        if (nbl == 1) return run_p<TYPE, B, 1>(w, L, xc, xm, y, res, N, nb, ldy, s);
+        if (nbl == 2) return run_p<TYPE, B, 2>(w, L, xc, xm, y, res, N, nb, ldy, s);
+    }
+    if (nbl == 8) nbl = 4;  // long rows: two passes of 256 blocks measured faster than one of 512
+    switch (nbl) {
+        case 1: run_q0<TYPE, B, 1>(w, L, xc, xm, y, res, N, nb, ldy, s); break;
+        case 2: run_q0<TYPE, B, 2>(w, L, xc, xm, y, res, N, nb, ldy, s); break;
+        case 4: run_q0<TYPE, B, 4>(w, L, xc, xm, y, res, N, nb, ldy, s); break;
+        default: run_q0<TYPE, B, 8>(w, L, xc, xm, y, res, N, nb, ldy, s); break;
+    }
+}
+
+template <int B, int NBL>
+void run_q4k(const uint8_t * w, const int8_t * xc, const int16_t * xbs, const float * xd, float * y, const float * res,
+             int N, int nsb, int ldy, hipStream_t s) {
+    const unsigned grid = (unsigned) ((N + 4 * kR - 1) / (4 * kR));
+    k_gemv_q4_K<B, kR, NBL><<<grid, 256, 0, s>>>(w, xc, xbs, xd, y, res, N, nsb, ldy);
+}
+
+template <int B>
+void run_q4k_nbl(int nbl, const uint8_t * w, const int8_t * xc, const int16_t * xbs, const float * xd, float * y,
+                 const float * res, int N, int nsb, int ldy, hipStream_t s) {
+    switch (nbl) {
+        case 1: run_q4k<B, 1>(w, xc, xbs, xd, y, res, N, nsb, ldy, s); break;
+        case 2: run_q4k<B, 2>(w, xc, xbs, xd, y, res, N, nsb, ldy, s); break;
+        case 4: run_q4k<B, 4>(w, xc, xbs, xd, y, res, N, nsb, ldy, s); break;
+        default: run_q4k<B, 8>(w, xc, xbs, xd, y, res, N, nsb, ldy, s); break;
+    }
+}
+
+}  // namespace
+
+// y [B][ldy] (first N columns written) from packed weights and a quantized activation; with res,
+// y = res + W x (res has y's layout and may be y itself).
+void launch_gemv(int type, const void * wv, int64_t N, int64_t K, const void * act, int64_t B, float * y, int64_t ldy,
+                 hipStream_t s, const float * res) {
+    const uint8_t * w = (const uint8_t *) wv;
+    const ActLayout A = act_layout(type, B, K);
+    const uint8_t * a = (const uint8_t *) act;
+    if (type == T_Q4_0 || type == T_Q8_0) {
+        const WeightLayout L = weight_layout(type, N, K);
+        const int nb = (int) (K / QK);
+        const int nbl = pick_nbl(nb);
+        const int8_t * xc = (const int8_t *) (a + A.codes);
+        const float2 * xm = (const float2 *) (a + A.meta);
+#define GCQ_Q0(TY)                                                                                     \
+    switch (B) {                                                                                       \
+        case 1: run_q0_nbl<TY, 1>(nbl, w, L, xc, xm, y, res, (int) N, nb, (int) ldy, s); break;             \
+        case 2: run_q0_nbl<TY, 2>(nbl, w, L, xc, xm, y, res, (int) N, nb, (int) ldy, s); break;             \
+        case 3: run_q0_nbl<TY, 3>(nbl, w, L, xc, xm, y, res, (int) N, nb, (int) ldy, s); break;             \
+        case 4: run_q0_nbl<TY, 4>(nbl, w, L, xc, xm, y, res, (int) N, nb, (int) ldy, s); break;             \
+        case 5: run_q0_nbl<TY, 5>(nbl, w, L, xc, xm, y, res, (int) N, nb, (int) ldy, s); break;             \
+        case 6: run_q0_nbl<TY, 6>(nbl, w, L, xc, xm, y, res, (int) N, nb, (int) ldy, s); break;             \
+        case 7: run_q0_nbl<TY, 7>(nbl, w, L, xc, xm, y, res, (int) N, nb, (int) ldy, s); break;             \
+        default: run_q0_nbl<TY, 8>(nbl, w, L, xc, xm, y, res, (int) N, nb, (int) ldy, s); break;            \
+    }
+        if (type == T_Q4_0) {
+            GCQ_Q0(T_Q4_0)
+        } else {
+            GCQ_Q0(T_Q8_0)
+        }
+#undef GCQ_Q0
+    } else if (type == T_Q4_K) {
+        const int nsb = (int) (K / QKK);
+        const int nbl = pick_nbl(nsb * 4);
+        const int8_t * xc = (const int8_t *) (a + A.codes);
+        const int16_t * xbs = (const int16_t *) (a + A.meta);
+        const float * xd = (const float *) (a + A.d);
+        switch (B) {
+            case 1: run_q4k_nbl<1>(nbl, w, xc, xbs, xd, y, res, (int) N, nsb, (int) ldy, s); break;
+            case 2: run_q4k_nbl<2>(nbl, w, xc, xbs, xd, y, res, (int) N, nsb, (int) ldy, s); break;
+            case 3: run_q4k_nbl<3>(nbl, w, xc, xbs, xd, y, res, (int) N, nsb, (int) ldy, s); break;
+            case 4: run_q4k_nbl<4>(nbl, w, xc, xbs, xd, y, res, (int) N, nsb, (int) ldy, s); break;
+            case 5: run_q4k_nbl<5>(nbl, w, xc, xbs, xd, y, res, (int) N, nsb, (int) ldy, s); break;
+            case 6: run_q4k_nbl<6>(nbl, w, xc, xbs, xd, y, res, (int) N, nsb, (int) ldy, s); break;
+            case 7: run_q4k_nbl<7>(nbl, w, xc, xbs, xd, y, res, (int) N, nsb, (int) ldy, s); break;
+            default: run_q4k_nbl<8>(nbl, w, xc, xbs, xd, y, res, (int) N, nsb, (int) ldy, s); break;
+        }
+    } else {
+        fail("mul_mat: unsupported weight type " + std::to_string(type));
+    }
+    check_launch("gemv");
+}
+
+void launch_isums(int type, const void * wv, int64_t N, int64_t K, const void * act, int64_t B, int32_t * out,
+                  hipStream_t s) {
+    const uint8_t * w = (const uint8_t *) wv;
+    const ActLayout A = act_layout(type, B, K);
+    const uint8_t * a = (const uint8_t *) act;
+    if (type == T_Q4_0 || type == T_Q8_0) {
+        const WeightLayout L = weight_layout(type, N, K);
+        const int nb = (int) (K / QK);
+        const int64_t n = B * N * nb;
+        k_isums_q0<<<(unsigned) ((n + 255) / 256), 256, 0, s>>>(type, w + L.qs, (const uint16_t *) (w + L.d),
+                                                             (const int8_t *) (a + A.codes),
+                                                             (const float2 *) (a + A.meta), out, (int) N, nb, (int) B);
+    } else if (type == T_Q4_K) {
+        const int nsb = (int) (K / QKK);
+        const int64_t n = B * N * nsb;
+        k_isums_q4_K<<<(unsigned) ((n + 255) / 256), 256, 0, s>>>(w, (const int8_t *) (a + A.codes),
+                                                               (const int16_t *) (a + A.meta), out, (int) N, nsb,
+                                                               (int) B);
+    } else {
+        fail("isums: unsupported type " + std::to_string(type));
+    }
+    check_launch("isums");
+}
+
+}  // namespace gcq

@@ -1,0 +1,456 @@
+// llama.hip - a Llama-style causal LM (GQA attention, SwiGLU FFN, RMSNorm, NEOX RoPE, f16 KV cache,
+// Q4_0 or Q8_0 weights) executed with libgcq's kernels: the program ggml-compiler's causal_lm
+// builds (ggml_compiler/llm.py:361-444) with its three entry points:
+//   prefill(tokens, positions, mask) -> logits of the last token       (llm.py:12-13)
+//   decode(token, position, mask1)   -> logits                          (llm.py:14)
+//   generate(first, start)           -> greedy tokens, on the device    (llm.py:421-436)
+// The KV cache is state, zeroed at creation and by reset (runtime/src/ggml_compiler_rt.cpp:528,
+// :1020-1031). Per layer the graph is the one causal_lm emits at O3 (rms_norm, mul, mul_mat q/k/v,
+// rope, set_rows, flash_attn, mul_mat o, add, rms_norm, mul, mul_mat gate/up, swiglu, mul_mat
+// down, add; tests/unit/test_llm.py:130-134), with q/k/v and gate/up each one row-stacked weight
+// (rows are independent, so the results equal separate mul_mats) and ten launches per layer.
+//
+// The decode step is captured once in a HIP graph (the counterpart of the reference's CUDA
+// graphs, runtime/CMakeLists.txt:29-31). Its kernels read the token, position and KV length
+// from a small device state that the step's last kernel advances, so a greedy generate is a run
+// of graph launches with no host round trip.
+#include "gcq_common.h"
+
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "../../include/gcq.h"
+
+namespace gcq {
+
+void launch_encode(int type, const float * src, int64_t nrows, int64_t k, void * dst, hipStream_t s);
+void launch_pack(int type, const void * src, int64_t nrows, int64_t k, void * dst, hipStream_t s);
+void launch_unpack(int type, const void * src, int64_t nrows, int64_t k, void * dst, hipStream_t s);
+void launch_gemv(int type, const void * w, int64_t N, int64_t K, const void * act, int64_t B, float * y, int64_t ldy,
+                 hipStream_t s, const float * res);
+void launch_gemm(int type, const void * w, int64_t N, int64_t K, const void * act, int64_t M, float * y, int64_t ldy,
+                 hipStream_t s, const float * res);
+void launch_get_rows(int type, const void * tab, int64_t nrows_tab, int64_t D, const int32_t * idx, int64_t n,
+                     float * out, hipStream_t s);
+void launch_fill_normal(float * dst, int64_t n, uint64_t seed, uint64_t offset, float stddev, hipStream_t s);
+void launch_attn_split(const float * q, int64_t q_h, int64_t q_s, const void * k, int64_t k_h, int64_t k_j,
+                       const void * v, int64_t v_h, int64_t v_j, const void * mask, int64_t m_s, int D, int Sq, int H,
+                       int Hkv, int n_kv, float scale, float * po, float2 * pml, const AttnPlan & p,
+                       const int * n_kv_dev, hipStream_t s);
+void launch_rmsnorm_q8(const float * x, int64_t ldx, const float * w, float eps, int64_t rows, int64_t n, void * act,
+                       hipStream_t s);
+void launch_swiglu_q8(const float * g, const float * u, int64_t ld, int64_t n, int64_t rows, void * act,
+                      hipStream_t s);
+void launch_rope_kv(float * qkv, int64_t ld, const int32_t * pos, int S, int H, int Hkv, int D, float base,
+                    void * cache, int64_t ctx, hipStream_t s);
+void launch_merge_q8(const float * part_o, const float2 * part_ml, int nsplit, int Sq, int H, int D, float * out,
+                     void * act, hipStream_t s);
+void launch_causal_mask(void * mask, int S, int n_kv, int pos0, hipStream_t s);
+void launch_step_end(const float * logits, int n, void * state, int32_t * out_tokens, int max_out, hipStream_t s);
+
+int cu_count();
+
+struct StepStateHost {
+    int pos, n_kv, token, step;
+};
+
+namespace {
+
+struct DevBuf {
+    void * p = nullptr;
+    size_t n = 0;
+    DevBuf() = default;
+    explicit DevBuf(size_t bytes) : n(bytes) { check_hip(hipMalloc(&p, std::max<size_t>(bytes, 256)), "hipMalloc"); }
+    DevBuf(const DevBuf &) = delete;
+    DevBuf & operator=(const DevBuf &) = delete;
+    DevBuf(DevBuf && o) noexcept : p(o.p), n(o.n) { o.p = nullptr; }
+    DevBuf & operator=(DevBuf && o) noexcept {
+        std::swap(p, o.p);
+        std::swap(n, o.n);
+        return *this;
+    }
+    ~DevBuf() {
+        if (p) (void) hipFree(p);
+    }
+    template <class T> T * as() const { return reinterpret_cast<T *>(p); }
+};
+
+struct Tensor {
+    std::string name;
+    int type;           // T_F32 (norm weights) or the model's weight type
+    int64_t rows, cols;
+    bool random;        // drawn by init_random
+    DevBuf buf;         // packed (quantized) or f32
+};
+
+}  // namespace
+
+struct Llama {
+    gcq_llama_config c{};
+    int max_prompt = 0;
+    hipStream_t stream = nullptr;
+    std::vector<Tensor> tensors;
+    // indices into tensors
+    int t_embd = -1, t_out_norm = -1, t_out = -1;
+    struct Layer {
+        int attn_norm, qkv, wo, ffn_norm, gate_up, down;
+    };
+    std::vector<Layer> layers;
+
+    int64_t qkv_dim = 0, attn_dim = 0;
+    DevBuf kv, x, qkv, gu, act_a, act_b, part_o, part_ml, mask, positions, logits, state, out_tokens, tok_in;
+    AttnPlan plan_decode{};
+    int pos = 0;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t graph_exec = nullptr;
+
+    ~Llama() {
+        if (graph_exec) (void) hipGraphExecDestroy(graph_exec);
+        if (graph) (void) hipGraphDestroy(graph);
+        if (stream) (void) hipStreamDestroy(stream);
+    }
+
+    int add(const std::string & name, int type, int64_t rows, int64_t cols, bool random) {
+        Tensor t;
+        t.name = name;
+        t.type = type;
+        t.rows = rows;
+        t.cols = cols;
+        t.random = random;
+        t.buf = DevBuf(type == T_F32 ? (size_t) rows * cols * 4 : weight_layout(type, rows, cols).total);
+        tensors.push_back(std::move(t));
+        return (int) tensors.size() - 1;
+    }
+
+    const Tensor & T(int i) const { return tensors[i]; }
+    uint16_t * kv_layer(int l) const {
+        return kv.as<uint16_t>() + (size_t) l * 2 * c.n_head_kv * c.max_ctx * c.head_dim;
+    }
+
+    void init(const gcq_llama_config & cfg, int max_prompt_) {
+        c = cfg;
+        max_prompt = max_prompt_;
+        require(c.n_layer > 0 && c.n_embd > 0 && c.n_head > 0 && c.n_head_kv > 0 && c.head_dim > 0 && c.n_ff > 0 &&
+                    c.n_vocab > 0 && c.max_ctx > 0,
+                "llama: every size must be positive");
+        require(c.wtype == T_Q4_0 || c.wtype == T_Q8_0, "llama: weight type must be Q4_0 or Q8_0");
+        require(c.n_head % c.n_head_kv == 0 && c.n_head / c.n_head_kv <= 8, "llama: 1..8 query heads per KV head");
+        require(c.head_dim == 64 || c.head_dim == 128, "llama: head_dim must be 64 or 128");
+        require(c.n_embd % 256 == 0 && c.n_ff % 32 == 0 && ((int64_t) c.n_head * c.head_dim) % 32 == 0,
+                "llama: n_embd must be a multiple of 256 and n_ff of 32");
+        require(max_prompt >= 1 && max_prompt <= c.max_ctx, "llama: 1 <= max_prompt <= max_ctx");
+        check_hip(hipStreamCreate(&stream), "hipStreamCreate");
+        qkv_dim = (int64_t) (c.n_head + 2 * c.n_head_kv) * c.head_dim;
+        attn_dim = (int64_t) c.n_head * c.head_dim;
+        // Tensor order = seed order of init_random (tensor i draws from seed + i).
+        t_embd = add("token_embd", c.wtype, c.n_vocab, c.n_embd, true);
+        for (int l = 0; l < c.n_layer; l++) {
+            const std::string b = "blk." + std::to_string(l) + ".";
+            Layer L;
+            L.attn_norm = add(b + "attn_norm", T_F32, 1, c.n_embd, false);
+            L.qkv = add(b + "attn_qkv", c.wtype, qkv_dim, c.n_embd, true);
+            L.wo = add(b + "attn_output", c.wtype, c.n_embd, attn_dim, true);
+            L.ffn_norm = add(b + "ffn_norm", T_F32, 1, c.n_embd, false);
+            L.gate_up = add(b + "ffn_gate_up", c.wtype, 2 * (int64_t) c.n_ff, c.n_embd, true);
+            L.down = add(b + "ffn_down", c.wtype, c.n_embd, c.n_ff, true);
+            layers.push_back(L);
+        }
+        t_out_norm = add("output_norm", T_F32, 1, c.n_embd, false);
+        t_out = add("output", c.wtype, c.n_vocab, c.n_embd, true);
+
+        const size_t kv_bytes = (size_t) c.n_layer * 2 * c.n_head_kv * c.max_ctx * c.head_dim * 2;
+        kv = DevBuf(kv_bytes);
+        x = DevBuf((size_t) max_prompt * c.n_embd * 4);
+        qkv = DevBuf((size_t) max_prompt * qkv_dim * 4);
+        gu = DevBuf((size_t) max_prompt * 2 * c.n_ff * 4);
+        const int64_t widest = std::max<int64_t>({(int64_t) c.n_embd, (int64_t) c.n_ff, attn_dim});
+        act_a = DevBuf(act_layout(c.wtype, max_prompt, widest).total);
+        act_b = DevBuf(act_layout(c.wtype, max_prompt, widest).total);
+        size_t po = 0, pml = 0;
+        for (int S = 1; S <= max_prompt; S++) {
+            const AttnPlan p = attn_plan(S, c.n_head_kv, c.max_ctx);
+            po = std::max(po, (size_t) S * c.n_head * p.nsplit * c.head_dim * 4);
+            pml = std::max(pml, (size_t) S * c.n_head * p.nsplit * 8);
+        }
+        part_o = DevBuf(po);
+        part_ml = DevBuf(pml);
+        plan_decode = attn_plan(1, c.n_head_kv, c.max_ctx);
+        mask = DevBuf((size_t) max_prompt * c.max_ctx * 2);
+        positions = DevBuf((size_t) max_prompt * 4);
+        tok_in = DevBuf((size_t) max_prompt * 4);
+        logits = DevBuf((size_t) c.n_vocab * 4);
+        state = DevBuf(sizeof(StepStateHost));
+        out_tokens = DevBuf((size_t) c.max_ctx * 4);
+        std::vector<float> ones(c.n_embd, 1.0f);
+        for (auto & t : tensors)
+            if (t.type == T_F32)
+                check_hip(hipMemcpy(t.buf.p, ones.data(), (size_t) t.cols * 4, hipMemcpyHostToDevice), "norm init");
+        reset();
+    }
+
+    void reset() {
+        check_hip(hipMemsetAsync(kv.p, 0, kv.n, stream), "KV reset");
+        check_hip(hipStreamSynchronize(stream), "sync");
+        pos = 0;
+    }
+
+    // Weights: N(0, stddev^2) from the counter-based stream (tensor i: seed + i), encoded on the GPU.
+    void init_random(uint64_t seed, float stddev) {
+        size_t biggest = 0;
+        for (auto & t : tensors)
+            if (t.random) biggest = std::max(biggest, (size_t) (t.rows * t.cols));
+        DevBuf f32(biggest * 4), raw(biggest / 32 * 34 + 256);
+        for (size_t i = 0; i < tensors.size(); i++) {
+            Tensor & t = tensors[i];
+            if (!t.random) continue;
+            launch_fill_normal(f32.as<float>(), t.rows * t.cols, seed + i, 0, stddev, stream);
+            launch_encode(t.type, f32.as<float>(), t.rows, t.cols, raw.p, stream);
+            launch_pack(t.type, raw.p, t.rows, t.cols, t.buf.p, stream);
+        }
+        check_hip(hipStreamSynchronize(stream), "init_random");
+    }
+
+    int find(const char * name) const {
+        require(name != nullptr, "weight name is NULL");
+        for (size_t i = 0; i < tensors.size(); i++)
+            if (tensors[i].name == name) return (int) i;
+        fail(std::string("no weight named '") + name + "'");
+    }
+
+    void set_weight(const char * name, const void * host, size_t nbytes) {
+        Tensor & t = tensors[find(name)];
+        const size_t want = t.type == T_F32 ? (size_t) t.cols * 4 : row_bytes(t.type, t.cols) * t.rows;
+        require(nbytes == want, std::string(name) + ": " + std::to_string(nbytes) + " bytes given, " +
+                                    std::to_string(want) + " expected (ggml block bytes)");
+        require(host != nullptr, "data is NULL");
+        if (t.type == T_F32) {
+            check_hip(hipMemcpy(t.buf.p, host, nbytes, hipMemcpyHostToDevice), "set_weight");
+            return;
+        }
+        DevBuf raw(nbytes);
+        check_hip(hipMemcpy(raw.p, host, nbytes, hipMemcpyHostToDevice), "set_weight");
+        launch_pack(t.type, raw.p, t.rows, t.cols, t.buf.p, stream);
+        check_hip(hipStreamSynchronize(stream), "set_weight");
+    }
+
+    void get_weight(const char * name, void * host, size_t nbytes) const {
+        const Tensor & t = tensors[find(name)];
+        const size_t want = t.type == T_F32 ? (size_t) t.cols * 4 : row_bytes(t.type, t.cols) * t.rows;
+        require(nbytes == want, std::string(name) + ": buffer of " + std::to_string(nbytes) + " bytes, need " +
+                                    std::to_string(want));
+        require(host != nullptr, "data is NULL");
+        if (t.type == T_F32) {
+            check_hip(hipMemcpy(host, t.buf.p, nbytes, hipMemcpyDeviceToHost), "get_weight");
+            return;
+        }
+        DevBuf raw(nbytes);
+        launch_unpack(t.type, t.buf.p, t.rows, t.cols, raw.p, stream);
+        check_hip(hipStreamSynchronize(stream), "get_weight");
+        check_hip(hipMemcpy(host, raw.p, nbytes, hipMemcpyDeviceToHost), "get_weight");
+    }
+
+    void mul_mat(int ti, const void * act, int64_t S, float * y, int64_t ldy, const float * res) {
+        const Tensor & t = tensors[ti];
+        if (S <= 8) launch_gemv(t.type, t.buf.p, t.rows, t.cols, act, S, y, ldy, stream, res);
+        else launch_gemm(t.type, t.buf.p, t.rows, t.cols, act, S, y, ldy, stream, res);
+    }
+
+    // S tokens at positions pos_dev[0..S) (device), the last of which sees n_kv keys. Decode (the
+    // captured step) passes the state's position / KV length pointers and no mask.
+    void forward(int S, const int32_t * tok_dev, const int32_t * pos_dev, int n_kv, const int * n_kv_dev,
+                 const void * mask_dev, const AttnPlan & plan) {
+        const float * embd = nullptr;
+        (void) embd;
+        float * xs = x.as<float>();
+        const Tensor & E = tensors[t_embd];
+        launch_get_rows(E.type, E.buf.p, E.rows, E.cols, tok_dev, S, xs, stream);
+        const float scale = 1.0f / std::sqrt((float) c.head_dim);
+        const int64_t kv_h = (int64_t) c.max_ctx * c.head_dim;
+        for (int l = 0; l < c.n_layer; l++) {
+            const Layer & L = layers[l];
+            uint16_t * kvl = kv_layer(l);
+            launch_rmsnorm_q8(xs, c.n_embd, tensors[L.attn_norm].buf.as<float>(), c.rms_eps, S, c.n_embd, act_a.p,
+                              stream);
+            mul_mat(L.qkv, act_a.p, S, qkv.as<float>(), qkv_dim, nullptr);
+            launch_rope_kv(qkv.as<float>(), qkv_dim, pos_dev, S, c.n_head, c.n_head_kv, c.head_dim, c.rope_base, kvl,
+                           c.max_ctx, stream);
+            launch_attn_split(qkv.as<float>(), c.head_dim, qkv_dim, kvl, kv_h, c.head_dim,
+                              kvl + (size_t) c.n_head_kv * kv_h, kv_h, c.head_dim, mask_dev, n_kv, c.head_dim, S,
+                              c.n_head, c.n_head_kv, n_kv, scale, part_o.as<float>(), part_ml.as<float2>(), plan,
+                              n_kv_dev, stream);
+            launch_merge_q8(part_o.as<float>(), part_ml.as<float2>(), plan.nsplit, S, c.n_head, c.head_dim, nullptr,
+                            act_b.p, stream);
+            mul_mat(L.wo, act_b.p, S, xs, c.n_embd, xs);
+            launch_rmsnorm_q8(xs, c.n_embd, tensors[L.ffn_norm].buf.as<float>(), c.rms_eps, S, c.n_embd, act_a.p,
+                              stream);
+            mul_mat(L.gate_up, act_a.p, S, gu.as<float>(), 2 * (int64_t) c.n_ff, nullptr);
+            launch_swiglu_q8(gu.as<float>(), gu.as<float>() + c.n_ff, 2 * (int64_t) c.n_ff, c.n_ff, S, act_b.p,
+                             stream);
+            mul_mat(L.down, act_b.p, S, xs, c.n_embd, xs);
+        }
+        launch_rmsnorm_q8(xs + (size_t) (S - 1) * c.n_embd, c.n_embd, tensors[t_out_norm].buf.as<float>(), c.rms_eps,
+                          1, c.n_embd, act_a.p, stream);
+        mul_mat(t_out, act_a.p, 1, logits.as<float>(), c.n_vocab, nullptr);
+    }
+
+    void prefill(const int32_t * tokens, int n, float * logits_host) {
+        require(n >= 1, "prefill: at least one token");
+        require(pos + n <= c.max_ctx, "context full: " + std::to_string(pos) + " + " + std::to_string(n) +
+                                          " tokens > max_ctx " + std::to_string(c.max_ctx));
+        for (int i = 0; i < n; i += max_prompt) {
+            const int S = std::min(max_prompt, n - i);
+            std::vector<int32_t> p(S);
+            for (int j = 0; j < S; j++) p[j] = pos + j;
+            check_hip(hipMemcpyAsync(positions.p, p.data(), S * 4, hipMemcpyHostToDevice, stream), "positions");
+            check_hip(hipMemcpyAsync(tok_in.p, tokens + i, S * 4, hipMemcpyHostToDevice, stream), "tokens");
+            const int n_kv = pos + S;
+            launch_causal_mask(mask.p, S, n_kv, pos, stream);
+            forward(S, tok_in.as<int32_t>(), positions.as<int32_t>(), n_kv, nullptr, mask.p,
+                    attn_plan(S, c.n_head_kv, n_kv));
+            check_hip(hipStreamSynchronize(stream), "prefill");
+            pos += S;
+        }
+        if (logits_host)
+            check_hip(hipMemcpy(logits_host, logits.p, (size_t) c.n_vocab * 4, hipMemcpyDeviceToHost), "logits");
+    }
+
+    void ensure_graph() {
+        if (graph_exec) return;
+        (void) cu_count();  // device queries happen before capture
+        // Capture: token from state.token, position / KV length from the state, no mask (every
+        // key up to the position is visible), step_end advances the state.
+        StepStateHost * st = state.as<StepStateHost>();
+        check_hip(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "capture");
+        forward(1, &st->token, &st->pos, c.max_ctx, &st->n_kv, nullptr, plan_decode);
+        launch_step_end(logits.as<float>(), c.n_vocab, state.p, out_tokens.as<int32_t>(), c.max_ctx, stream);
+        check_hip(hipStreamEndCapture(stream, &graph), "capture end");
+        check_hip(hipGraphInstantiate(&graph_exec, graph, nullptr, nullptr, 0), "graph instantiate");
+    }
+
+    void set_state(int token) {
+        const StepStateHost st{pos, pos + 1, token, 0};
+        check_hip(hipMemcpyAsync(state.p, &st, sizeof st, hipMemcpyHostToDevice, stream), "state");
+    }
+
+    void decode(int32_t token, float * logits_host, int32_t * next) {
+        require(token >= 0 && token < c.n_vocab, "token id out of range");
+        require(pos + 1 <= c.max_ctx, "context full");
+        ensure_graph();
+        set_state(token);
+        check_hip(hipGraphLaunch(graph_exec, stream), "graph launch");
+        check_hip(hipStreamSynchronize(stream), "decode");
+        pos += 1;
+        if (logits_host)
+            check_hip(hipMemcpy(logits_host, logits.p, (size_t) c.n_vocab * 4, hipMemcpyDeviceToHost), "logits");
+        if (next) {
+            StepStateHost st;
+            check_hip(hipMemcpy(&st, state.p, sizeof st, hipMemcpyDeviceToHost), "state");
+            *next = st.token;
+        }
+    }
+
+    void generate(int32_t first, int n_new, int32_t * out) {
+        require(first >= 0 && first < c.n_vocab, "token id out of range");
+        require(n_new >= 0 && pos + n_new <= c.max_ctx, "context full: generate would pass max_ctx");
+        if (n_new == 0) return;
+        ensure_graph();
+        set_state(first);
+        for (int i = 0; i < n_new; i++) check_hip(hipGraphLaunch(graph_exec, stream), "graph launch");
+        check_hip(hipStreamSynchronize(stream), "generate");
+        pos += n_new;
+        if (out) check_hip(hipMemcpy(out, out_tokens.p, (size_t) n_new * 4, hipMemcpyDeviceToHost), "tokens");
+    }
+};
+
+}  // namespace gcq
+
+using namespace gcq;
+
+struct gcq_llama : Llama {};
+
+extern "C" {
+
+gcq_llama * gcq_llama_create(const gcq_llama_config * cfg, int max_prompt) {
+    gcq_llama * m = nullptr;
+    const int rc = guarded([&] {
+        require(cfg != nullptr, "config is NULL");
+        require(gcq_device_count() > 0, "no HIP device");
+        std::unique_ptr<gcq_llama> p(new gcq_llama());
+        p->init(*cfg, max_prompt);
+        m = p.release();
+    });
+    return rc == 0 ? m : nullptr;
+}
+
+void gcq_llama_free(gcq_llama * m) { delete m; }
+
+int gcq_llama_init_random(gcq_llama * m, uint64_t seed, float stddev) {
+    return guarded([&] {
+        require(m != nullptr, "model is NULL");
+        m->init_random(seed, stddev);
+    });
+}
+
+int gcq_llama_n_weights(const gcq_llama * m) { return m ? (int) m->tensors.size() : -1; }
+
+int gcq_llama_weight_info(const gcq_llama * m, int i, const char ** name, int * type, int64_t * rows, int64_t * cols) {
+    return guarded([&] {
+        require(m != nullptr, "model is NULL");
+        require(i >= 0 && i < (int) m->tensors.size(), "weight index out of range");
+        const auto & t = m->tensors[i];
+        if (name) *name = t.name.c_str();
+        if (type) *type = t.type;
+        if (rows) *rows = t.rows;
+        if (cols) *cols = t.cols;
+    });
+}
+
+int gcq_llama_set_weight(gcq_llama * m, const char * name, const void * data, size_t nbytes) {
+    return guarded([&] {
+        require(m != nullptr, "model is NULL");
+        m->set_weight(name, data, nbytes);
+    });
+}
+
+int gcq_llama_get_weight(const gcq_llama * m, const char * name, void * data, size_t nbytes) {
+    return guarded([&] {
+        require(m != nullptr, "model is NULL");
+        m->get_weight(name, data, nbytes);
+    });
+}
+
+int gcq_llama_reset(gcq_llama * m) {
+    return guarded([&] {
+        require(m != nullptr, "model is NULL");
+        m->reset();
+    });
+}
+
+int gcq_llama_position(const gcq_llama * m) { return m ? m->pos : -1; }
+
+int gcq_llama_prefill(gcq_llama * m, const int32_t * tokens, int n, float * logits) {
+    return guarded([&] {
+        require(m != nullptr && tokens != nullptr, "model or tokens is NULL");
+        for (int i = 0; i < n; i++) require(tokens[i] >= 0 && tokens[i] < m->c.n_vocab, "token id out of range");
+        m->prefill(tokens, n, logits);
+    });
+}
+
+int gcq_llama_decode(gcq_llama * m, int32_t token, float * logits, int32_t * next) {
+    return guarded([&] {
+        require(m != nullptr, "model is NULL");
+        m->decode(token, logits, next);
+    });
+}
+
+int gcq_llama_generate(gcq_llama * m, int32_t first, int n_new, int32_t * out_tokens) {
+    return guarded([&] {
+        require(m != nullptr, "model is NULL");
+        m->generate(first, n_new, out_tokens);
+    });
+}
+
+}  // extern "C"

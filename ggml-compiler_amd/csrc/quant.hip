@@ -1,0 +1,496 @@
+// quant.hip - weight encoders, weight repacking, dequantization and activation quantizers.
+//
+// Weight encoders produce ggml's block bytes exactly (the ggml_compiler_quantize contract,
+// runtime/include/ggml_compiler_rt.h:83-87, whose CPU implementation is ggml_quantize_chunk with
+// no importance matrix, runtime/src/ggml_compiler_rt.cpp:859-876). They run one thread per block
+// (one per 256-super-block for Q4_K) in ggml's sequential order with contraction off, so every
+// float operation rounds as the C reference does. Activation quantizers produce the vec_dot_type
+// that ggml-cpu converts src1 into before a quantized mul_mat (Q8_0 for Q4_0/Q8_0 weights, Q8_K
+// for Q4_K), in the device "act" layout described in gcq_common.h.
+#include "gcq_common.h"
+
+namespace gcq {
+
+// ----------------------------------------------------------------------- weight encoders
+
+// ggml quantize_row_q8_0_ref: d = amax/127, q = roundf(x * (1/d)).
+__global__ void k_enc_q8_0(const float * __restrict__ x, uint8_t * __restrict__ out, int64_t nblocks) {
+#pragma clang fp contract(off)
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblocks) return;
+    const float * xb = x + i * QK;
+    float amax = 0.0f;
+    for (int j = 0; j < QK; j++) amax = fmaxf(amax, fabsf(xb[j]));
+    const float d = __fdiv_rn(amax, 127.0f);
+    const float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+    uint8_t * o = out + i * 34;
+    const uint16_t dh = f2h_exact(d);
+    o[0] = (uint8_t) dh;
+    o[1] = (uint8_t) (dh >> 8);
+    for (int j = 0; j < QK; j++) o[2 + j] = (uint8_t) (int8_t) roundf(xb[j] * id);
+}
+
+// ggml quantize_row_q4_0_ref: d = (first largest-|x| value)/-8, q = min(15, trunc(x/d + 8.5)).
+__global__ void k_enc_q4_0(const float * __restrict__ x, uint8_t * __restrict__ out, int64_t nblocks) {
+#pragma clang fp contract(off)
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblocks) return;
+    const float * xb = x + i * QK;
+    float amax = 0.0f, max = 0.0f;
+    for (int j = 0; j < QK; j++) {
+        const float a = fabsf(xb[j]);
+        if (amax < a) {
+            amax = a;
+            max = xb[j];
+        }
+    }
+    const float d = __fdiv_rn(max, -8.0f);
+    const float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+    uint8_t * o = out + i * 18;
+    const uint16_t dh = f2h_exact(d);
+    o[0] = (uint8_t) dh;
+    o[1] = (uint8_t) (dh >> 8);
+    for (int j = 0; j < QK / 2; j++) {
+        int lo = (int) (xb[j] * id + 8.5f);
+        int hi = (int) (xb[j + 16] * id + 8.5f);
+        lo = lo < 15 ? lo : 15;
+        hi = hi < 15 ? hi : 15;
+        o[2 + j] = (uint8_t) (lo | (hi << 4));
+    }
+}
+
+__device__ __forceinline__ int near_int(float v) { return __float2int_rn(v); }
+
+// ggml make_qkx2_quants(32, 15, x, w, L, &min, Laux, -1, 0.1, 20, false): weighted least-squares
+// (scale, min) over 21 candidate inverse scales. Sequential, as the C reference.
+__device__ float qkx2_fit(const float * x, const float * w, uint8_t * L, float * the_min) {
+#pragma clang fp contract(off)
+    uint8_t Laux[32];
+    float min = x[0], max = x[0];
+    float sum_w = w[0];
+    float sum_x = sum_w * x[0];
+    for (int i = 1; i < 32; i++) {
+        if (x[i] < min) min = x[i];
+        if (x[i] > max) max = x[i];
+        const float wi = w[i];
+        sum_w += wi;
+        sum_x += wi * x[i];
+    }
+    if (min > 0) min = 0;
+    if (max == min) {
+        for (int i = 0; i < 32; i++) L[i] = 0;
+        *the_min = -min;
+        return 0.0f;
+    }
+    float iscale = __fdiv_rn(15.0f, max - min);
+    float scale = __fdiv_rn(1.0f, iscale);
+    float best = 0;
+    for (int i = 0; i < 32; i++) {
+        int l = near_int(iscale * (x[i] - min));
+        l = l < 0 ? 0 : (l > 15 ? 15 : l);
+        L[i] = (uint8_t) l;
+        const float diff = scale * (float) L[i] + min - x[i];
+        best += w[i] * (diff * diff);
+    }
+    for (int is = 0; is <= 20; is++) {
+        iscale = __fdiv_rn(-1.0f + 0.1f * (float) is + 15.0f, max - min);
+        float sum_l = 0, sum_l2 = 0, sum_xl = 0;
+        for (int i = 0; i < 32; i++) {
+            int l = near_int(iscale * (x[i] - min));
+            l = l < 0 ? 0 : (l > 15 ? 15 : l);
+            Laux[i] = (uint8_t) l;
+            const float wi = w[i];
+            const float lf = (float) l;
+            sum_l += wi * lf;
+            sum_l2 += wi * lf * lf;
+            sum_xl += wi * lf * x[i];
+        }
+        const float D = sum_w * sum_l2 - sum_l * sum_l;
+        if (D > 0) {
+            float this_scale = __fdiv_rn(sum_w * sum_xl - sum_x * sum_l, D);
+            float this_min = __fdiv_rn(sum_l2 * sum_x - sum_l * sum_xl, D);
+            if (this_min > 0) {
+                this_min = 0;
+                this_scale = __fdiv_rn(sum_xl, sum_l2);
+            }
+            float mad = 0;
+            for (int i = 0; i < 32; i++) {
+                const float diff = this_scale * (float) Laux[i] + this_min - x[i];
+                mad += w[i] * (diff * diff);
+            }
+            if (mad < best) {
+                for (int i = 0; i < 32; i++) L[i] = Laux[i];
+                best = mad;
+                scale = this_scale;
+                min = this_min;
+            }
+        }
+    }
+    *the_min = -min;
+    return scale;
+}
+
+__device__ __forceinline__ void scale_min_k4(int j, const uint8_t * q, int & sc, int & m) {
+    if (j < 4) {
+        sc = q[j] & 63;
+        m = q[j + 4] & 63;
+    } else {
+        sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+        m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+}
+
+// ggml quantize_row_q4_K_ref, one thread per 256-value super-block.
+__global__ void k_enc_q4_K(const float * __restrict__ xall, uint8_t * __restrict__ out, int64_t nblocks) {
+#pragma clang fp contract(off)
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblocks) return;
+    const float * x = xall + i * QKK;
+    uint8_t L[QKK];
+    float w[32], mins[8], scales[8];
+    float max_scale = 0, max_min = 0;
+    for (int j = 0; j < 8; j++) {
+        float sum_x2 = 0;
+        for (int l = 0; l < 32; l++) sum_x2 += x[32 * j + l] * x[32 * j + l];
+        const float av_x = __fsqrt_rn(__fdiv_rn(sum_x2, 32.0f));
+        for (int l = 0; l < 32; l++) w[l] = av_x + fabsf(x[32 * j + l]);
+        scales[j] = qkx2_fit(x + 32 * j, w, L + 32 * j, &mins[j]);
+        if (scales[j] > max_scale) max_scale = scales[j];
+        if (mins[j] > max_min) max_min = mins[j];
+    }
+    const float inv_scale = max_scale > 0 ? __fdiv_rn(63.f, max_scale) : 0.f;
+    const float inv_min = max_min > 0 ? __fdiv_rn(63.f, max_min) : 0.f;
+    uint8_t sb[12];
+    for (int j = 0; j < 12; j++) sb[j] = 0;
+    for (int j = 0; j < 8; j++) {
+        int ls = near_int(inv_scale * scales[j]);
+        int lm = near_int(inv_min * mins[j]);
+        ls = ls > 63 ? 63 : ls;
+        lm = lm > 63 ? 63 : lm;
+        if (j < 4) {
+            sb[j] = (uint8_t) ls;
+            sb[j + 4] = (uint8_t) lm;
+        } else {
+            sb[j + 4] = (uint8_t) ((ls & 0xF) | ((lm & 0xF) << 4));
+            sb[j - 4] |= (uint8_t) ((ls >> 4) << 6);
+            sb[j] |= (uint8_t) ((lm >> 4) << 6);
+        }
+    }
+    const uint16_t dh = f2h_exact(__fdiv_rn(max_scale, 63.f));
+    const uint16_t mh = f2h_exact(__fdiv_rn(max_min, 63.f));
+    for (int j = 0; j < 8; j++) {
+        int sc, m;
+        scale_min_k4(j, sb, sc, m);
+        const float d = h2f(dh) * (float) sc;
+        if (d == 0.0f) continue;  // the fit's codes stay, as in ggml
+        const float dm = h2f(mh) * (float) m;
+        for (int l = 0; l < 32; l++) {
+            int q = near_int(__fdiv_rn(x[32 * j + l] + dm, d));
+            L[32 * j + l] = (uint8_t) (q < 0 ? 0 : (q > 15 ? 15 : q));
+        }
+    }
+    uint8_t * o = out + i * 144;
+    o[0] = (uint8_t) dh;
+    o[1] = (uint8_t) (dh >> 8);
+    o[2] = (uint8_t) mh;
+    o[3] = (uint8_t) (mh >> 8);
+    for (int j = 0; j < 12; j++) o[4 + j] = sb[j];
+    for (int c = 0; c < 4; c++)
+        for (int l = 0; l < 32; l++) o[16 + 32 * c + l] = (uint8_t) (L[64 * c + l] | (L[64 * c + 32 + l] << 4));
+}
+
+// f32 -> f16 rows (ggml_quantize_chunk for F16: round to nearest even).
+__global__ void k_enc_f16(const float * __restrict__ x, uint16_t * __restrict__ out, int64_t n) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = f2h_exact(x[i]);
+}
+
+// ------------------------------------------------------------------------------ repacking
+
+// ggml block rows -> packed: Q4_0 / Q8_0 split into 16/32-byte code blocks and an fp16 scale
+// array; one thread per block.
+template <int CB>  // code bytes per block: 16 (Q4_0) or 32 (Q8_0)
+__global__ void k_pack(const uint8_t * __restrict__ src, uint8_t * __restrict__ qs, uint16_t * __restrict__ d,
+                       int64_t nblocks) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblocks) return;
+    const uint8_t * b = src + i * (2 + CB);
+    d[i] = (uint16_t) (b[0] | (b[1] << 8));
+    uint32_t w[CB / 4];
+#pragma unroll
+    for (int j = 0; j < CB / 4; j++)
+        w[j] = b[2 + 4 * j] | (b[3 + 4 * j] << 8) | (b[4 + 4 * j] << 16) | ((uint32_t) b[5 + 4 * j] << 24);
+    uint4 * o = reinterpret_cast<uint4 *>(qs + i * CB);
+#pragma unroll
+    for (int j = 0; j < CB / 16; j++) o[j] = make_uint4(w[4 * j], w[4 * j + 1], w[4 * j + 2], w[4 * j + 3]);
+}
+
+// packed -> ggml block rows (the inverse of k_pack).
+template <int CB>
+__global__ void k_unpack(const uint8_t * __restrict__ qs, const uint16_t * __restrict__ d, uint8_t * __restrict__ dst,
+                         int64_t nblocks) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblocks) return;
+    uint8_t * b = dst + i * (2 + CB);
+    b[0] = (uint8_t) d[i];
+    b[1] = (uint8_t) (d[i] >> 8);
+    for (int j = 0; j < CB; j++) b[2 + j] = qs[i * CB + j];
+}
+
+// ------------------------------------------------------------------------------ dequant
+
+// Packed weight rows -> f32 (ggml dequantize_row_*). Exact: every product is representable.
+__global__ void k_dequant_q4_0(const uint8_t * __restrict__ qs, const uint16_t * __restrict__ d, float * __restrict__ y,
+                               int64_t nblocks) {
+    const int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;  // one thread per byte
+    if (t >= nblocks * 16) return;
+    const int64_t i = t / 16;
+    const int j = (int) (t % 16);
+    const float dd = h2f(d[i]);
+    const uint8_t b = qs[t];
+    y[i * 32 + j] = (float) ((b & 0xF) - 8) * dd;
+    y[i * 32 + j + 16] = (float) ((b >> 4) - 8) * dd;
+}
+
+__global__ void k_dequant_q8_0(const int8_t * __restrict__ qs, const uint16_t * __restrict__ d, float * __restrict__ y,
+                               int64_t nblocks) {
+    const int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= nblocks * 32) return;
+    y[t] = (float) qs[t] * h2f(d[t / 32]);
+}
+
+__global__ void k_dequant_q4_K(const uint8_t * __restrict__ w, float * __restrict__ y, int64_t nblocks) {
+#pragma clang fp contract(off)
+    const int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;  // one thread per qs byte
+    if (t >= nblocks * 128) return;
+    const int64_t i = t / 128;
+    const int k = (int) (t % 128);
+    const int c = k / 32, l = k % 32;
+    const uint8_t * b = w + i * 144;
+    const float d = h2f((uint16_t) (b[0] | (b[1] << 8)));
+    const float dmin = h2f((uint16_t) (b[2] | (b[3] << 8)));
+    int sc, m;
+    scale_min_k4(2 * c, b + 4, sc, m);
+    const float d1 = d * (float) sc, m1 = dmin * (float) m;
+    scale_min_k4(2 * c + 1, b + 4, sc, m);
+    const float d2 = d * (float) sc, m2 = dmin * (float) m;
+    const uint8_t q = b[16 + k];
+    y[i * 256 + 64 * c + l] = d1 * (float) (q & 0xF) - m1;
+    y[i * 256 + 64 * c + 32 + l] = d2 * (float) (q >> 4) - m2;
+}
+
+// ------------------------------------------------------------------ activation quantizers
+
+// Q8_0 vec_dot_type, canonical variant (ggml-cpu x86 AVX2 quantize_row_q8_0): d = amax/127 kept
+// as fp16, id = 127/amax, q = rint(x*id) (ties to even). 8 lanes per 32-block, 4 values each.
+__global__ void k_act_q8_0(const float * __restrict__ x, int64_t ldx, int8_t * __restrict__ codes,
+                           float2 * __restrict__ meta, int64_t B, int64_t K) {
+#pragma clang fp contract(off)
+    const int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t per_row = K / 4;
+    if (t >= B * per_row) return;  // B*K/4 is a multiple of 8: whole 8-lane groups stay together
+    const int64_t b = t / per_row;
+    const int64_t e = (t % per_row) * 4;
+    const float4 v = *reinterpret_cast<const float4 *>(x + b * ldx + e);
+    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+    const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+    const int q0 = (int) __builtin_rintf(v.x * id);
+    const int q1 = (int) __builtin_rintf(v.y * id);
+    const int q2 = (int) __builtin_rintf(v.z * id);
+    const int q3 = (int) __builtin_rintf(v.w * id);
+    *reinterpret_cast<int *>(codes + b * K + e) =
+        (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | ((q3 & 0xff) << 24);
+    int s = q0 + q1 + q2 + q3;
+    s += __shfl_xor(s, 1, 64);
+    s += __shfl_xor(s, 2, 64);
+    s += __shfl_xor(s, 4, 64);
+    if ((threadIdx.x & 7) == 0) {
+        const float d = h2f(f2h_exact(__fdiv_rn(amax, 127.0f)));
+        meta[b * (K / QK) + e / QK] = make_float2(d, __int_as_float(s));
+    }
+}
+
+// Q8_K vec_dot_type (ggml quantize_row_q8_K_ref): max = signed value of the first largest |x|,
+// iscale = -127/max, q = min(127, rint(iscale*x)), d = 1/iscale, bsums of 16. One wave per
+// super-block, 4 values per lane; an all-zero block stores zeros.
+__global__ void k_act_q8_K(const float * __restrict__ x, int64_t ldx, int8_t * __restrict__ codes,
+                           int16_t * __restrict__ bsums, float * __restrict__ dout, int64_t B, int64_t K) {
+#pragma clang fp contract(off)
+    const int64_t wave = ((int64_t) blockIdx.x * blockDim.x + threadIdx.x) / 64;
+    const int lane = threadIdx.x & 63;
+    const int64_t nsb = K / QKK;
+    if (wave >= B * nsb) return;
+    const int64_t b = wave / nsb, sbi = wave % nsb;
+    const int64_t e = sbi * QKK + lane * 4;
+    const float4 v = *reinterpret_cast<const float4 *>(x + b * ldx + e);
+    const float vv[4] = {v.x, v.y, v.z, v.w};
+    float ax = 0.0f, mx = 0.0f;
+    int idx = 1 << 30;
+    for (int j = 0; j < 4; j++) {
+        if (fabsf(vv[j]) > ax) {
+            ax = fabsf(vv[j]);
+            mx = vv[j];
+            idx = lane * 4 + j;
+        }
+    }
+    for (int o = 32; o > 0; o >>= 1) {  // largest |x|, ties to the lowest index
+        const float ax2 = __shfl_xor(ax, o, 64);
+        const float mx2 = __shfl_xor(mx, o, 64);
+        const int idx2 = __shfl_xor(idx, o, 64);
+        if (ax2 > ax || (ax2 == ax && idx2 < idx)) {
+            ax = ax2;
+            mx = mx2;
+            idx = idx2;
+        }
+    }
+    int q[4] = {0, 0, 0, 0};
+    float d = 0.0f;
+    if (ax != 0.0f) {
+        const float iscale = __fdiv_rn(-127.0f, mx);
+        for (int j = 0; j < 4; j++) {
+            const int r = (int) __builtin_rintf((iscale * vv[j]));
+            q[j] = r < 127 ? r : 127;
+        }
+        d = __fdiv_rn(1.0f, iscale);
+    }
+    *reinterpret_cast<int *>(codes + b * K + e) =
+        (q[0] & 0xff) | ((q[1] & 0xff) << 8) | ((q[2] & 0xff) << 16) | ((q[3] & 0xff) << 24);
+    int s = q[0] + q[1] + q[2] + q[3];
+    s += __shfl_xor(s, 1, 64);
+    s += __shfl_xor(s, 2, 64);
+    if ((lane & 3) == 0) bsums[b * (K / 16) + sbi * 16 + lane / 4] = (int16_t) s;
+    if (lane == 0) dout[b * nsb + sbi] = d;
+}
+
+// Device act layout -> ggml block bytes (block_q8_0 / block_q8_K), for byte comparisons.
+__global__ void k_act_to_ggml_q8_0(const int8_t * codes, const float2 * meta, uint8_t * out, int64_t nblocks) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblocks) return;
+    const uint16_t h = f2h_exact(meta[i].x);
+    uint8_t * o = out + i * 34;
+    o[0] = (uint8_t) h;
+    o[1] = (uint8_t) (h >> 8);
+    for (int j = 0; j < 32; j++) o[2 + j] = (uint8_t) codes[i * 32 + j];
+}
+
+__global__ void k_act_to_ggml_q8_K(const int8_t * codes, const int16_t * bsums, const float * d, uint8_t * out,
+                                   int64_t nblocks) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblocks) return;
+    uint8_t * o = out + i * 292;
+    const float dv = d[i];
+    __builtin_memcpy(o, &dv, 4);
+    for (int j = 0; j < 256; j++) o[4 + j] = (uint8_t) codes[i * 256 + j];
+    for (int j = 0; j < 16; j++) {
+        const int16_t s = bsums[i * 16 + j];
+        o[260 + 2 * j] = (uint8_t) s;
+        o[261 + 2 * j] = (uint8_t) ((uint16_t) s >> 8);
+    }
+}
+
+// ------------------------------------------------------------------------- host launchers
+
+static inline unsigned nblk(int64_t n, int t) { return (unsigned) ((n + t - 1) / t); }
+
+void launch_encode(int type, const float * src, int64_t nrows, int64_t k, void * dst, hipStream_t s) {
+    const int64_t nb = nrows * (k / (int64_t) block_elems(type));
+    if (nb == 0) return;
+    switch (type) {
+        case T_Q8_0: k_enc_q8_0<<<nblk(nb, 128), 128, 0, s>>>(src, (uint8_t *) dst, nb); break;
+        case T_Q4_0: k_enc_q4_0<<<nblk(nb, 128), 128, 0, s>>>(src, (uint8_t *) dst, nb); break;
+        case T_Q4_K: k_enc_q4_K<<<nblk(nb, 64), 64, 0, s>>>(src, (uint8_t *) dst, nb); break;
+        case T_F16: k_enc_f16<<<nblk(nb, 256), 256, 0, s>>>(src, (uint16_t *) dst, nb); break;
+        default: fail("encode: unsupported type " + std::to_string(type));
+    }
+    check_launch("encode");
+}
+
+void launch_pack(int type, const void * src, int64_t nrows, int64_t k, void * dst, hipStream_t s) {
+    const WeightLayout L = weight_layout(type, nrows, k);
+    uint8_t * o = (uint8_t *) dst;
+    if (type == T_Q4_K) {
+        check_hip(hipMemcpyAsync(dst, src, row_bytes(type, k) * nrows, hipMemcpyDeviceToDevice, s), "pack copy");
+        return;
+    }
+    const int64_t nb = nrows * (k / QK);
+    if (nb == 0) return;
+    if (type == T_Q4_0)
+        k_pack<16><<<nblk(nb, 256), 256, 0, s>>>((const uint8_t *) src, o + L.qs, (uint16_t *) (o + L.d), nb);
+    else if (type == T_Q8_0)
+        k_pack<32><<<nblk(nb, 256), 256, 0, s>>>((const uint8_t *) src, o + L.qs, (uint16_t *) (o + L.d), nb);
+    else
+        fail("pack: unsupported type " + std::to_string(type));
+    check_launch("pack");
+}
+
+void launch_unpack(int type, const void * src, int64_t nrows, int64_t k, void * dst, hipStream_t s) {
+    const WeightLayout L = weight_layout(type, nrows, k);
+    const uint8_t * p = (const uint8_t *) src;
+    if (type == T_Q4_K) {
+        check_hip(hipMemcpyAsync(dst, src, row_bytes(type, k) * nrows, hipMemcpyDeviceToDevice, s), "unpack copy");
+        return;
+    }
+    const int64_t nb = nrows * (k / QK);
+    if (nb == 0) return;
+    if (type == T_Q4_0)
+        k_unpack<16><<<nblk(nb, 256), 256, 0, s>>>(p + L.qs, (const uint16_t *) (p + L.d), (uint8_t *) dst, nb);
+    else if (type == T_Q8_0)
+        k_unpack<32><<<nblk(nb, 256), 256, 0, s>>>(p + L.qs, (const uint16_t *) (p + L.d), (uint8_t *) dst, nb);
+    else
+        fail("unpack: unsupported type " + std::to_string(type));
+    check_launch("unpack");
+}
+
+void launch_dequant(int type, const void * w, int64_t nrows, int64_t k, float * y, hipStream_t s) {
+    const WeightLayout L = weight_layout(type, nrows, k);
+    const uint8_t * p = (const uint8_t *) w;
+    if (type == T_Q4_0) {
+        const int64_t nb = nrows * (k / QK);
+        if (nb) k_dequant_q4_0<<<nblk(nb * 16, 256), 256, 0, s>>>(p + L.qs, (const uint16_t *) (p + L.d), y, nb);
+    } else if (type == T_Q8_0) {
+        const int64_t nb = nrows * (k / QK);
+        if (nb) k_dequant_q8_0<<<nblk(nb * 32, 256), 256, 0, s>>>((const int8_t *) (p + L.qs), (const uint16_t *) (p + L.d), y, nb);
+    } else if (type == T_Q4_K) {
+        const int64_t nb = nrows * (k / QKK);
+        if (nb) k_dequant_q4_K<<<nblk(nb * 128, 256), 256, 0, s>>>(p, y, nb);
+    } else {
+        fail("dequantize: unsupported type " + std::to_string(type));
+    }
+    check_launch("dequantize");
+}
+
+void launch_act_quant(int wtype, const float * x, int64_t ldx, int64_t B, int64_t k, void * act, hipStream_t s) {
+    const ActLayout L = act_layout(wtype, B, k);
+    uint8_t * a = (uint8_t *) act;
+    if (wtype == T_Q4_0 || wtype == T_Q8_0) {
+        const int64_t n = B * k / 4;
+        k_act_q8_0<<<nblk(n, 256), 256, 0, s>>>(x, ldx, (int8_t *) (a + L.codes), (float2 *) (a + L.meta), B, k);
+    } else if (wtype == T_Q4_K) {
+        const int64_t waves = B * (k / QKK);
+        k_act_q8_K<<<nblk(waves * 64, 256), 256, 0, s>>>(x, ldx, (int8_t *) (a + L.codes), (int16_t *) (a + L.meta),
+                                                        (float *) (a + L.d), B, k);
+    } else {
+        fail("activation quantize: unsupported weight type " + std::to_string(wtype));
+    }
+    check_launch("activation quantize");
+}
+
+void launch_act_to_ggml(int wtype, const void * act, int64_t B, int64_t k, void * out, hipStream_t s) {
+    const ActLayout L = act_layout(wtype, B, k);
+    const uint8_t * a = (const uint8_t *) act;
+    if (wtype == T_Q4_0 || wtype == T_Q8_0) {
+        const int64_t nb = B * k / QK;
+        k_act_to_ggml_q8_0<<<nblk(nb, 128), 128, 0, s>>>((const int8_t *) (a + L.codes), (const float2 *) (a + L.meta),
+                                                         (uint8_t *) out, nb);
+    } else {
+        const int64_t nb = B * k / QKK;
+        k_act_to_ggml_q8_K<<<nblk(nb, 64), 64, 0, s>>>((const int8_t *) (a + L.codes), (const int16_t *) (a + L.meta),
+                                                       (const float *) (a + L.d), (uint8_t *) out, nb);
+    }
+    check_launch("act_to_ggml");
+}
+
+}  // namespace gcq

@@ -1,0 +1,82 @@
+"""CPU reference of the Llama-style decoder, composed from the oracle's ggml restatements.
+
+TEST INFRASTRUCTURE ONLY (tests/, __graft_entry__.smoke(), bench.py's cpu_baseline leg). It runs
+the graph ggml-compiler's causal_lm emits per layer at O3 (ggml_compiler/llm.py:361-444;
+tests/unit/test_llm.py:130-134): get_rows, then rms_norm, mul, mul_mat q/k/v, rope (NEOX),
+set_rows into an f16 KV cache [kv_heads, max_ctx, head_dim] (llm.py:386), flash_attn_ext with the
+causal mask of llm.py:355-358, mul_mat o, add, rms_norm, mul, mul_mat gate/up, swiglu, mul_mat
+down, add; final rms_norm, mul and the lm_head mul_mat. Weights are ggml block bytes, q/k/v and
+gate/up row-stacked as the HIP model stores them.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+import oracle as orc
+
+
+class OracleLlama:
+    def __init__(self, cfg, weights: dict[str, np.ndarray], threads: int = 0) -> None:
+        self.cfg = cfg
+        self.w = weights
+        self.threads = threads
+        self.t = cfg.wtype
+        L, Hkv, ctx, D = cfg.n_layer, cfg.n_head_kv, cfg.max_ctx, cfg.head_dim
+        self.k = np.zeros((L, Hkv, ctx, D), np.uint16)
+        self.v = np.zeros((L, Hkv, ctx, D), np.uint16)
+        self.pos = 0
+
+    def reset(self) -> None:
+        self.k[:] = 0
+        self.v[:] = 0
+        self.pos = 0
+
+    def _mm(self, name: str, x: np.ndarray) -> np.ndarray:
+        return orc.mul_mat(self.w[name], self.t, x, x.shape[1], threads=self.threads)
+
+    def _norm(self, name: str, x: np.ndarray) -> np.ndarray:
+        return orc.rms_norm(x, self.cfg.rms_eps, threads=self.threads) * self.w[name][None, :]
+
+    def forward(self, tokens) -> np.ndarray:
+        """Append tokens at the next positions; logits of the last one."""
+        c = self.cfg
+        S = len(tokens)
+        H, Hkv, D = c.n_head, c.n_head_kv, c.head_dim
+        pos = np.arange(self.pos, self.pos + S, dtype=np.int32)
+        n_kv = self.pos + S
+        emb = self.w["token_embd"]
+        x = orc.dequantize(emb[np.asarray(tokens)], self.t, c.n_embd)
+        mask = np.where(np.arange(n_kv)[None, :] <= pos[:, None], 0.0, -np.inf).astype(np.float32)
+        m16 = orc.fp32_to_fp16(mask)
+        for l in range(c.n_layer):
+            b = f"blk.{l}."
+            qkv = self._mm(b + "attn_qkv", self._norm(b + "attn_norm", x))
+            q = orc.rope_neox(qkv[:, :H * D].reshape(S, H, D), pos, D, c.rope_base)
+            k = orc.rope_neox(qkv[:, H * D:(H + Hkv) * D].reshape(S, Hkv, D), pos, D, c.rope_base)
+            v = qkv[:, (H + Hkv) * D:].reshape(S, Hkv, D)
+            self.k[l][:, pos] = orc.fp32_to_fp16(k.transpose(1, 0, 2))
+            self.v[l][:, pos] = orc.fp32_to_fp16(v.transpose(1, 0, 2))
+            att = orc.flash_attn_ext(q.transpose(1, 0, 2), self.k[l][:, :n_kv], self.v[l][:, :n_kv], m16,
+                                     1.0 / np.sqrt(D), threads=self.threads)
+            x = x + self._mm(b + "attn_output", att.reshape(S, H * D))
+            gu = self._mm(b + "ffn_gate_up", self._norm(b + "ffn_norm", x))
+            a = orc.swiglu(gu[:, :c.n_ff], gu[:, c.n_ff:])
+            x = x + self._mm(b + "ffn_down", a)
+        self.pos += S
+        h = self._norm("output_norm", x[-1:])
+        return self._mm("output", h)[0]
+
+
+def random_weights(model_weights, seed: int, std: float = 0.02, names=None) -> dict[str, np.ndarray]:
+    """The weights gcq_llama_init_random draws (tensor i: the normal stream of seed + i, encoded by
+    the reference encoder), regenerated on the CPU. model_weights: (name, type, rows, cols) in order."""
+    out = {}
+    for i, (name, t, rows, cols) in enumerate(model_weights):
+        if names is not None and name not in names:
+            continue
+        if t == orc.F32:
+            out[name] = np.ones(cols, np.float32)
+        else:
+            out[name] = orc.quantize(orc.normal((rows, cols), seed=seed + i, std=std), t)
+    return out

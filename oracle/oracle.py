@@ -233,3 +233,17 @@ def parity(out: np.ndarray, ref: np.ndarray) -> float:
     if not np.isfinite(out[np.isfinite(ref)]).all():
         return float("inf")
     return float(np.max(np.abs(out - ref))) / max(1.0, float(np.max(np.abs(ref))))
+
+
+def logit_kl(out: np.ndarray, ref: np.ndarray) -> float:
+    """KL(ref || out) of the next-token distributions of one row of logits, as
+    ggml_compiler/verify/parity.py:55-71 (token_stats) computes it; inf if out is not finite."""
+    r = np.asarray(ref, np.float64)
+    o = np.asarray(out, np.float64)
+    if not np.isfinite(o).all():
+        return float("inf")
+    lr = r - r.max()
+    lr -= np.log(np.exp(lr).sum())
+    lo = o - o.max()
+    lo -= np.log(np.exp(lo).sum())
+    return float((np.exp(lr) * (lr - lo)).sum())

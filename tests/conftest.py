@@ -22,3 +22,18 @@ def orc():
 
     oracle.lib()
     return oracle
+
+
+@pytest.fixture(scope="session")
+def gops():
+    """libgcq's ops on cuda:0. No skip: on a GPU run a missing library or device is a failure."""
+    import torch  # noqa: F401
+
+    from ggml_compiler_amd import ops
+
+    ops.require_device()
+    return ops
+
+
+def to_np(t):
+    return t.detach().cpu().numpy()

@@ -1,0 +1,49 @@
+"""Fused decode-step nodes equal their unfused ggml op sequence, byte for byte."""
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import to_np
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("rows,n", [(1, 256), (3, 4096), (12, 14336)])
+def test_rms_norm_q8_equals_norm_then_quantize(gops, orc, rows, n):
+    x = torch.from_numpy(orc.normal((rows, n), seed=70) * 2).cuda()
+    w = torch.from_numpy(orc.normal((n,), seed=71)).cuda()
+    fused = gops.rms_norm_q8(x, w, 1e-5)
+    unfused = gops.quantize_act("q4_0", gops.rms_norm(x, 1e-5, w))
+    assert torch.equal(gops.act_to_ggml("q4_0", fused, rows, n), gops.act_to_ggml("q4_0", unfused, rows, n))
+
+
+@pytest.mark.parametrize("rows,n", [(1, 512), (5, 14336)])
+def test_swiglu_q8_equals_swiglu_then_quantize(gops, orc, rows, n):
+    gu = torch.from_numpy(orc.normal((rows, 2 * n), seed=72)).cuda()
+    g, u = gu[:, :n], gu[:, n:]
+    fused = gops.swiglu_q8(g, u)
+    unfused = gops.quantize_act("q4_0", gops.swiglu(g.contiguous(), u.contiguous()))
+    assert torch.equal(gops.act_to_ggml("q4_0", fused, rows, n), gops.act_to_ggml("q4_0", unfused, rows, n))
+
+
+@pytest.mark.parametrize("t", ["q4_0", "q8_0", "q4_K"])
+@pytest.mark.parametrize("B,N,K", [(1, 512, 256), (1, 1000, 256), (2, 300, 512), (1, 40000, 4096), (3, 4096, 4096),
+                                   (12, 256, 512)])
+def test_mul_mat_q_with_residual(gops, orc, t, B, N, K):
+    """y = res + W x in one launch equals W x then ggml_add; also in place (y is res). N=40000 runs
+    the persistent GEMV's multi-group loop; 12 rows run the GEMM (Q4_0, Q8_0)."""
+    if t == "q4_K" and B > 8:
+        pytest.skip("Q4_K runs more than 8 rows through gcq_mul_mat")
+    raw = orc.quantize(orc.normal((N, K), seed=73, std=0.02), t)
+    qw = gops.QuantWeight.from_ggml(torch.from_numpy(raw), t, K)
+    x = orc.normal((B, K), seed=74)
+    act = gops.quantize_act(t, torch.from_numpy(x).cuda())
+    r = torch.from_numpy(orc.normal((B, N), seed=75)).cuda()
+    plain = gops.mul_mat_q(qw, act, B)
+    fused = gops.mul_mat_q(qw, act, B, res=r)
+    assert torch.equal(fused, plain + r)
+    inplace = r.clone()
+    gops.mul_mat_q(qw, act, B, res=inplace, out=inplace)
+    assert torch.equal(inplace, plain + r)
+    assert orc.parity(to_np(plain), orc.mul_mat(raw, t, x, K)) < 1e-3
