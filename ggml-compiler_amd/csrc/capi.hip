@@ -20,6 +20,8 @@ void launch_act_quant(int wtype, const float * x, int64_t ldx, int64_t B, int64_
 void launch_act_to_ggml(int wtype, const void * act, int64_t B, int64_t k, void * out, hipStream_t s);
 void launch_gemv(int type, const void * w, int64_t N, int64_t K, const void * act, int64_t B, float * y, int64_t ldy,
                  hipStream_t s, const float * res = nullptr);
+bool launch_gemv_f32(int type, const void * w, int64_t N, int64_t K, const float * x, const float * norm_w, float eps,
+                     float * y, const float * res, hipStream_t s);
 void launch_isums(int type, const void * w, int64_t N, int64_t K, const void * act, int64_t B, int32_t * out,
                   hipStream_t s);
 void launch_gemm(int type, const void * w, int64_t N, int64_t K, const void * act, int64_t M, float * y, int64_t ldy,
@@ -295,6 +297,7 @@ int gcq_mul_mat(int wtype, const void * w, int64_t N, int64_t K, const float * x
         const size_t need = gcq_mul_mat_workspace(wtype, M, K);
         require(ws_size >= need, "workspace of " + std::to_string(ws_size) + " bytes, need " + std::to_string(need));
         hipStream_t s = as_stream(stream);
+        if (M == 1 && launch_gemv_f32(wtype, w, N, K, x, nullptr, 0.0f, y, nullptr, s)) return;
         if (M <= 8) {
             launch_act_quant(wtype, x, ldx, M, K, ws, s);
             launch_gemv(wtype, w, N, K, ws, M, y, ldy, s);
@@ -308,6 +311,28 @@ int gcq_mul_mat(int wtype, const void * w, int64_t N, int64_t K, const float * x
                 launch_gemv(wtype, w, N, K, ws, b, y + m * ldy, ldy, s);
             }
         }
+    });
+}
+
+int gcq_rms_norm_mul_mat(int wtype, const void * w, int64_t N, int64_t K, const float * x, const float * norm_w,
+                         float eps, float * y, const float * res, void * ws, size_t ws_size, void * stream) {
+    return guarded([&] {
+        require(wtype == T_Q4_0 || wtype == T_Q8_0, "rms_norm_mul_mat: weight type must be Q4_0 or Q8_0");
+        need_k(wtype, K);
+        need_dims(N, "N");
+        need_ptr(w, "w", 16);
+        need_ptr(x, "x", 16);
+        if (norm_w) need_ptr(norm_w, "norm_w", 16);
+        need_ptr(y, "y", 4);
+        if (res) need_ptr(res, "res", 4);
+        hipStream_t s = as_stream(stream);
+        if (launch_gemv_f32(wtype, w, N, K, x, norm_w, eps, y, res, s)) return;
+        need_ptr(ws, "workspace", 256);
+        const size_t need = gcq_mul_mat_workspace(wtype, 1, K);
+        require(ws_size >= need, "workspace of " + std::to_string(ws_size) + " bytes, need " + std::to_string(need));
+        if (norm_w) launch_rmsnorm_q8(x, K, norm_w, eps, 1, K, ws, s);
+        else launch_act_quant(wtype, x, K, 1, K, ws, s);
+        launch_gemv(wtype, w, N, K, ws, 1, y, N, s, res);
     });
 }
 

@@ -17,6 +17,8 @@
 
 namespace gcq {
 
+constexpr int kStepEndBlocks = 256;
+
 // Decoder-step state on the device, read by the captured decode graph.
 struct StepState {
     int pos;    // position of the token being decoded
@@ -25,45 +27,12 @@ struct StepState {
     int step;   // tokens generated so far
 };
 
-// Shared Q8_0 quantization of one 32-value block held 4 per lane by 8 consecutive lanes (the
-// canonical variant of quant.hip's k_act_q8_0, same operations in the same order).
-__device__ __forceinline__ void q8_block_store(float4 v, int8_t * codes, float2 * meta, int lane8) {
-#pragma clang fp contract(off)
-    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
-    const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
-    const int q0 = (int) __builtin_rintf(v.x * id);
-    const int q1 = (int) __builtin_rintf(v.y * id);
-    const int q2 = (int) __builtin_rintf(v.z * id);
-    const int q3 = (int) __builtin_rintf(v.w * id);
-    *reinterpret_cast<int *>(codes + 4 * lane8) =
-        (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | ((q3 & 0xff) << 24);
-    int s = q0 + q1 + q2 + q3;
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);
-    s += __shfl_xor(s, 4, 64);
-    if (lane8 == 0) *meta = make_float2(h2f(f2h_exact(__fdiv_rn(amax, 127.0f))), __int_as_float(s));
-}
-
 // One 256-thread block per row; n a multiple of 32.
 __global__ __launch_bounds__(256) void k_rmsnorm_q8(const float * __restrict__ x, int64_t ldx,
                                                     const float * __restrict__ w, float eps, int n,
                                                     int8_t * __restrict__ codes, float2 * __restrict__ meta) {
     const int row = blockIdx.x;
-    const float * xr = x + row * ldx;
-    const float scale = rms_scale(xr, n, eps);
-    for (int e = threadIdx.x * 4; e < n; e += 1024) {  // 8 lanes per 32-block
-        float4 v = *reinterpret_cast<const float4 *>(xr + e);
-        const float4 wv = *reinterpret_cast<const float4 *>(w + e);
-        v.x = (v.x * scale) * wv.x;
-        v.y = (v.y * scale) * wv.y;
-        v.z = (v.z * scale) * wv.z;
-        v.w = (v.w * scale) * wv.w;
-        q8_block_store(v, codes + (int64_t) row * n + (e & ~31), meta + (int64_t) row * (n / 32) + e / 32,
-                       (e / 4) & 7);
-    }
+    rmsnorm_q8_row(x + row * ldx, n, w, eps, codes + (int64_t) row * n, meta + (int64_t) row * (n / 32));
 }
 
 // silu(g) * u over rows of n (g, u at row strides), quantized to Q8_0.
@@ -171,46 +140,64 @@ __global__ void k_causal_mask(uint16_t * __restrict__ mask, int S, int n_kv, int
 }
 
 // argmax of the logits (first index of the maximum) and the generate loop's step: record the
-// token, advance position and KV length. One 256-thread block.
-__global__ __launch_bounds__(256) void k_step_end(const float * __restrict__ logits, int n, StepState * st,
-                                                  int32_t * __restrict__ out_tokens, int max_out) {
+// token, advance position and KV length. Every workgroup reduces a slice to (max, first index)
+// and the last one to finish (a device counter, reset by that workgroup for the next launch)
+// reduces the partials and advances the state: one launch, no wait on other workgroups.
+__device__ __forceinline__ void argmax_combine(float & v, int & i, float v2, int i2) {
+    if (v2 > v || (v2 == v && i2 < i)) {
+        v = v2;
+        i = i2;
+    }
+}
+
+__device__ __forceinline__ void block_argmax(float & v, int & idx) {
     __shared__ float bv[4];
     __shared__ int bi[4];
-    float v = -INFINITY;
-    int idx = 0x7fffffff;
-    for (int i = threadIdx.x; i < n; i += 256) {
-        const float a = logits[i];
-        if (a > v) {
-            v = a;
-            idx = i;
-        }
-    }
-    for (int o = 32; o > 0; o >>= 1) {
-        const float v2 = __shfl_xor(v, o, 64);
-        const int i2 = __shfl_xor(idx, o, 64);
-        if (v2 > v || (v2 == v && i2 < idx)) {
-            v = v2;
-            idx = i2;
-        }
-    }
+    for (int o = 32; o > 0; o >>= 1) argmax_combine(v, idx, __shfl_xor(v, o, 64), __shfl_xor(idx, o, 64));
     if ((threadIdx.x & 63) == 0) {
         bv[threadIdx.x >> 6] = v;
         bi[threadIdx.x >> 6] = idx;
     }
     __syncthreads();
+    v = bv[0];
+    idx = bi[0];
+    for (int w = 1; w < 4; w++) argmax_combine(v, idx, bv[w], bi[w]);
+    __syncthreads();
+}
+
+__global__ __launch_bounds__(256) void k_step_end(const float * __restrict__ logits, int n, StepState * st,
+                                                  int32_t * __restrict__ out_tokens, int max_out,
+                                                  float2 * __restrict__ part, unsigned int * __restrict__ counter) {
+    __shared__ bool last;
+    float v = -INFINITY;
+    int idx = 0x7fffffff;
+    const int per = (n + gridDim.x - 1) / gridDim.x;
+    const int lo = blockIdx.x * per, hi = min(n, lo + per);
+    for (int i = lo + threadIdx.x; i < hi; i += 256) argmax_combine(v, idx, logits[i], i);
+    block_argmax(v, idx);
     if (threadIdx.x == 0) {
-        for (int w = 1; w < 4; w++) {
-            if (bv[w] > v || (bv[w] == v && bi[w] < idx)) {
-                v = bv[w];
-                idx = bi[w];
-            }
-        }
+        part[blockIdx.x] = make_float2(v, __int_as_float(idx));
+        __threadfence();
+        last = atomicAdd(counter, 1u) == gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    v = -INFINITY;
+    idx = 0x7fffffff;
+    for (int b = threadIdx.x; b < (int) gridDim.x; b += 256) {
+        const float2 p = part[b];
+        argmax_combine(v, idx, p.x, __float_as_int(p.y));
+    }
+    block_argmax(v, idx);
+    if (threadIdx.x == 0) {
         const int tok = (v == -INFINITY || idx == 0x7fffffff) ? 0 : idx;
         if (out_tokens && st->step < max_out) out_tokens[st->step] = tok;
         st->step += 1;
         st->token = tok;
         st->pos += 1;
         st->n_kv = st->pos + 1;
+        *counter = 0u;
     }
 }
 
@@ -258,8 +245,11 @@ void launch_causal_mask(void * mask, int S, int n_kv, int pos0, hipStream_t s) {
     check_launch("causal_mask");
 }
 
-void launch_step_end(const float * logits, int n, void * state, int32_t * out_tokens, int max_out, hipStream_t s) {
-    k_step_end<<<1, 256, 0, s>>>(logits, n, (StepState *) state, out_tokens, max_out);
+// part: kStepEndBlocks float2, counter: one zeroed unsigned int (left zeroed after each launch).
+void launch_step_end(const float * logits, int n, void * state, int32_t * out_tokens, int max_out, void * part,
+                     void * counter, hipStream_t s) {
+    k_step_end<<<kStepEndBlocks, 256, 0, s>>>(logits, n, (StepState *) state, out_tokens, max_out, (float2 *) part,
+                                              (unsigned int *) counter);
     check_launch("step_end");
 }
 

@@ -91,30 +91,7 @@ __global__ void k_get_rows(int type, const uint8_t * __restrict__ tab, int64_t n
     const int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= (int64_t) n * D) return;
     const int j = (int) (t / D), c = (int) (t % D);
-    const int64_t r = idx[j];
-    if (r < 0 || r >= nrows_tab) {  // an index outside the table reads as NaN
-        out[t] = __builtin_nanf("");
-        return;
-    }
-    float v;
-    if (type == T_F32) {
-        v = reinterpret_cast<const float *>(tab)[r * D + c];
-    } else if (type == T_F16) {
-        v = h2f(reinterpret_cast<const uint16_t *>(tab)[r * D + c]);
-    } else {
-        const int nb = D / QK;
-        const int64_t blk = r * nb + c / QK;
-        const int e = c % QK;
-        const size_t qbytes = (size_t) nrows_tab * nb * (type == T_Q4_0 ? 16 : 32);
-        const uint16_t * d = reinterpret_cast<const uint16_t *>(tab + align256(qbytes));
-        if (type == T_Q4_0) {
-            const uint8_t b = tab[blk * 16 + (e & 15)];
-            v = (float) ((e < 16 ? (b & 0xF) : (b >> 4)) - 8) * h2f(d[blk]);
-        } else {
-            v = (float) reinterpret_cast<const int8_t *>(tab)[blk * 32 + e] * h2f(d[blk]);
-        }
-    }
-    out[t] = v;
+    out[t] = table_value(type, tab, nrows_tab, D, idx[j], c);
 }
 
 // ---------------------------------------------------------------------- swiglu, add, mul

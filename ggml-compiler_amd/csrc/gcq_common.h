@@ -161,6 +161,62 @@ __device__ __forceinline__ float rms_scale(const float * xr, int n, float eps) {
     return 1.0f / sqrtf(mean + eps);
 }
 
+// Q8_0 conversion (canonical variant, as quant.hip's k_act_q8_0) of one 32-value block held 4 per
+// lane by 8 consecutive lanes; lane8 = the lane's index in its group of 8.
+__device__ __forceinline__ void q8_block_store(float4 v, int8_t * codes, float2 * meta, int lane8) {
+#pragma clang fp contract(off)
+    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+    const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+    const int q0 = (int) __builtin_rintf(v.x * id);
+    const int q1 = (int) __builtin_rintf(v.y * id);
+    const int q2 = (int) __builtin_rintf(v.z * id);
+    const int q3 = (int) __builtin_rintf(v.w * id);
+    *reinterpret_cast<int *>(codes + 4 * lane8) =
+        (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | ((q3 & 0xff) << 24);
+    int s = q0 + q1 + q2 + q3;
+    s += __shfl_xor(s, 1, 64);
+    s += __shfl_xor(s, 2, 64);
+    s += __shfl_xor(s, 4, 64);
+    if (lane8 == 0) *meta = make_float2(h2f(f2h_exact(__fdiv_rn(amax, 127.0f))), __int_as_float(s));
+}
+
+// rms_norm of one row of n (a multiple of 32) times w, quantized to Q8_0: codes [n], meta [n/32].
+// Called by all 256 threads of a block.
+__device__ __forceinline__ void rmsnorm_q8_row(const float * xr, int n, const float * w, float eps, int8_t * codes,
+                                               float2 * meta) {
+    const float scale = rms_scale(xr, n, eps);
+    for (int e = threadIdx.x * 4; e < n; e += 1024) {  // 8 lanes per 32-block
+        float4 v = *reinterpret_cast<const float4 *>(xr + e);
+        const float4 wv = *reinterpret_cast<const float4 *>(w + e);
+        v.x = (v.x * scale) * wv.x;
+        v.y = (v.y * scale) * wv.y;
+        v.z = (v.z * scale) * wv.z;
+        v.w = (v.w * scale) * wv.w;
+        q8_block_store(v, codes + (e & ~31), meta + e / 32, (e / 4) & 7);
+    }
+}
+
+// Element c of row r of a get_rows table (F32, F16, or packed Q4_0 / Q8_0 of nrows x D); NaN
+// for a row outside the table.
+__device__ __forceinline__ float table_value(int type, const uint8_t * tab, int64_t nrows, int D, int64_t r, int c) {
+    if (r < 0 || r >= nrows) return __builtin_nanf("");
+    if (type == T_F32) return reinterpret_cast<const float *>(tab)[r * D + c];
+    if (type == T_F16) return h2f(reinterpret_cast<const uint16_t *>(tab)[r * D + c]);
+    const int nb = D / QK;
+    const int64_t blk = r * nb + c / QK;
+    const int e = c % QK;
+    const size_t qbytes = (size_t) nrows * nb * (type == T_Q4_0 ? 16 : 32);
+    const uint16_t * d = reinterpret_cast<const uint16_t *>(tab + align256(qbytes));
+    if (type == T_Q4_0) {
+        const uint8_t b = tab[blk * 16 + (e & 15)];
+        return (float) ((e < 16 ? (b & 0xF) : (b >> 4)) - 8) * h2f(d[blk]);
+    }
+    return (float) reinterpret_cast<const int8_t *>(tab)[blk * 32 + e] * h2f(d[blk]);
+}
+
 // Counter-based splitmix64 (output i of a generator whose state starts at seed).
 __device__ __forceinline__ uint64_t rnd64(uint64_t seed, uint64_t i) {
     uint64_t z = seed + (i + 1) * 0x9e3779b97f4a7c15ull;

@@ -31,6 +31,8 @@ void launch_pack(int type, const void * src, int64_t nrows, int64_t k, void * ds
 void launch_unpack(int type, const void * src, int64_t nrows, int64_t k, void * dst, hipStream_t s);
 void launch_gemv(int type, const void * w, int64_t N, int64_t K, const void * act, int64_t B, float * y, int64_t ldy,
                  hipStream_t s, const float * res);
+bool launch_gemv_f32(int type, const void * w, int64_t N, int64_t K, const float * x, const float * norm_w, float eps,
+                     float * y, const float * res, hipStream_t s);
 void launch_gemm(int type, const void * w, int64_t N, int64_t K, const void * act, int64_t M, float * y, int64_t ldy,
                  hipStream_t s, const float * res);
 void launch_get_rows(int type, const void * tab, int64_t nrows_tab, int64_t D, const int32_t * idx, int64_t n,
@@ -49,7 +51,8 @@ void launch_rope_kv(float * qkv, int64_t ld, const int32_t * pos, int S, int H, 
 void launch_merge_q8(const float * part_o, const float2 * part_ml, int nsplit, int Sq, int H, int D, float * out,
                      void * act, hipStream_t s);
 void launch_causal_mask(void * mask, int S, int n_kv, int pos0, hipStream_t s);
-void launch_step_end(const float * logits, int n, void * state, int32_t * out_tokens, int max_out, hipStream_t s);
+void launch_step_end(const float * logits, int n, void * state, int32_t * out_tokens, int max_out, void * part,
+                     void * counter, hipStream_t s);
 
 int cu_count();
 
@@ -102,6 +105,7 @@ struct Llama {
 
     int64_t qkv_dim = 0, attn_dim = 0;
     DevBuf kv, x, qkv, gu, act_a, act_b, part_o, part_ml, mask, positions, logits, state, out_tokens, tok_in;
+    DevBuf argmax_part, counters;  // step_end partials; step_end's completion counter (zero between launches)
     AttnPlan plan_decode{};
     int pos = 0;
     hipGraph_t graph = nullptr;
@@ -184,6 +188,9 @@ struct Llama {
         logits = DevBuf((size_t) c.n_vocab * 4);
         state = DevBuf(sizeof(StepStateHost));
         out_tokens = DevBuf((size_t) c.max_ctx * 4);
+        argmax_part = DevBuf(256 * sizeof(float2));
+        counters = DevBuf(4096);
+        check_hip(hipMemset(counters.p, 0, counters.n), "counters");
         std::vector<float> ones(c.n_embd, 1.0f);
         for (auto & t : tensors)
             if (t.type == T_F32)
@@ -258,12 +265,24 @@ struct Llama {
         else launch_gemm(t.type, t.buf.p, t.rows, t.cols, act, S, y, ldy, stream, res);
     }
 
+    // ggml_rms_norm + ggml_mul by norm t_norm of S rows of the residual stream (the last row only
+    // when last_only), then mul_mat by weight ti into y. One row: a single launch, the GEMV
+    // quantizing the normalized row itself where the shape allows; else rmsnorm_q8 into act_a first.
+    void norm_mul_mat(int t_norm, int ti, const float * xs, int S, bool last_only, float * y, int64_t ldy) {
+        const Tensor & t = tensors[ti];
+        const float * nw = tensors[t_norm].buf.as<float>();
+        const int rows = last_only ? 1 : S;
+        const float * xr = xs + (size_t) (S - rows) * c.n_embd;
+        if (rows == 1 && launch_gemv_f32(t.type, t.buf.p, t.rows, t.cols, xr, nw, c.rms_eps, y, nullptr, stream))
+            return;
+        launch_rmsnorm_q8(xr, c.n_embd, nw, c.rms_eps, rows, c.n_embd, act_a.p, stream);
+        mul_mat(ti, act_a.p, rows, y, ldy, nullptr);
+    }
+
     // S tokens at positions pos_dev[0..S) (device), the last of which sees n_kv keys. Decode (the
     // captured step) passes the state's position / KV length pointers and no mask.
     void forward(int S, const int32_t * tok_dev, const int32_t * pos_dev, int n_kv, const int * n_kv_dev,
                  const void * mask_dev, const AttnPlan & plan) {
-        const float * embd = nullptr;
-        (void) embd;
         float * xs = x.as<float>();
         const Tensor & E = tensors[t_embd];
         launch_get_rows(E.type, E.buf.p, E.rows, E.cols, tok_dev, S, xs, stream);
@@ -272,9 +291,7 @@ struct Llama {
         for (int l = 0; l < c.n_layer; l++) {
             const Layer & L = layers[l];
             uint16_t * kvl = kv_layer(l);
-            launch_rmsnorm_q8(xs, c.n_embd, tensors[L.attn_norm].buf.as<float>(), c.rms_eps, S, c.n_embd, act_a.p,
-                              stream);
-            mul_mat(L.qkv, act_a.p, S, qkv.as<float>(), qkv_dim, nullptr);
+            norm_mul_mat(L.attn_norm, L.qkv, xs, S, false, qkv.as<float>(), qkv_dim);
             launch_rope_kv(qkv.as<float>(), qkv_dim, pos_dev, S, c.n_head, c.n_head_kv, c.head_dim, c.rope_base, kvl,
                            c.max_ctx, stream);
             launch_attn_split(qkv.as<float>(), c.head_dim, qkv_dim, kvl, kv_h, c.head_dim,
@@ -284,16 +301,12 @@ struct Llama {
             launch_merge_q8(part_o.as<float>(), part_ml.as<float2>(), plan.nsplit, S, c.n_head, c.head_dim, nullptr,
                             act_b.p, stream);
             mul_mat(L.wo, act_b.p, S, xs, c.n_embd, xs);
-            launch_rmsnorm_q8(xs, c.n_embd, tensors[L.ffn_norm].buf.as<float>(), c.rms_eps, S, c.n_embd, act_a.p,
-                              stream);
-            mul_mat(L.gate_up, act_a.p, S, gu.as<float>(), 2 * (int64_t) c.n_ff, nullptr);
+            norm_mul_mat(L.ffn_norm, L.gate_up, xs, S, false, gu.as<float>(), 2 * (int64_t) c.n_ff);
             launch_swiglu_q8(gu.as<float>(), gu.as<float>() + c.n_ff, 2 * (int64_t) c.n_ff, c.n_ff, S, act_b.p,
                              stream);
             mul_mat(L.down, act_b.p, S, xs, c.n_embd, xs);
         }
-        launch_rmsnorm_q8(xs + (size_t) (S - 1) * c.n_embd, c.n_embd, tensors[t_out_norm].buf.as<float>(), c.rms_eps,
-                          1, c.n_embd, act_a.p, stream);
-        mul_mat(t_out, act_a.p, 1, logits.as<float>(), c.n_vocab, nullptr);
+        norm_mul_mat(t_out_norm, t_out, xs, S, true, logits.as<float>(), c.n_vocab);
     }
 
     void prefill(const int32_t * tokens, int n, float * logits_host) {
@@ -325,7 +338,8 @@ struct Llama {
         StepStateHost * st = state.as<StepStateHost>();
         check_hip(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "capture");
         forward(1, &st->token, &st->pos, c.max_ctx, &st->n_kv, nullptr, plan_decode);
-        launch_step_end(logits.as<float>(), c.n_vocab, state.p, out_tokens.as<int32_t>(), c.max_ctx, stream);
+        launch_step_end(logits.as<float>(), c.n_vocab, state.p, out_tokens.as<int32_t>(), c.max_ctx, argmax_part.p,
+                        counters.as<unsigned int>() + 0, stream);
         check_hip(hipStreamEndCapture(stream, &graph), "capture end");
         check_hip(hipGraphInstantiate(&graph_exec, graph, nullptr, nullptr, 0), "graph instantiate");
     }

@@ -57,6 +57,7 @@ SIGNATURES = {
     "gcq_mul_mat": ([i32, p, i64, i64, p, i64, i64, p, i64, p, sz, p], i32),
     "gcq_mul_mat_q": ([i32, p, i64, i64, p, i64, p, i64, p, p], i32),
     "gcq_rms_norm_q8": ([p, i64, p, i64, i64, f32, p, p], i32),
+    "gcq_rms_norm_mul_mat": ([i32, p, i64, i64, p, p, f32, p, p, p, sz, p], i32),
     "gcq_swiglu_q8": ([p, p, i64, i64, i64, p, p], i32),
     "gcq_block_isums": ([i32, p, i64, i64, p, i64, p, p], i32),
     "gcq_gemm_block_isums": ([i32, p, i64, i64, p, i64, i32, p, p], i32),

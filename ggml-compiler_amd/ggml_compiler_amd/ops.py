@@ -166,6 +166,22 @@ def rms_norm_q8(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
     return act
 
 
+def rms_norm_mul_mat(w: QuantWeight, x: torch.Tensor, norm_w: torch.Tensor | None, eps: float,
+                     res: torch.Tensor | None = None) -> torch.Tensor:
+    """One row: ggml_rms_norm -> mul by norm_w -> ggml_mul_mat(w, .) [+ res], fused (norm_w None:
+    the mul_mat alone). x f32 [K] or [1, K] -> [1, N]."""
+    x = _cuda(x, torch.float32, "x").contiguous().reshape(1, -1)
+    K = x.shape[1]
+    if K != w.K:
+        raise ValueError(f"x has {K} columns, the weight {w.K}")
+    nw = None if norm_w is None else _cuda(norm_w, torch.float32, "norm_w").contiguous()
+    y = torch.empty((1, w.N), dtype=torch.float32, device=x.device)
+    ws = workspace(int(load().gcq_mul_mat_workspace(w.type, 1, K)), x.device)
+    check(load().gcq_rms_norm_mul_mat(w.type, _p(w.data), w.N, K, _p(x), _p(nw), float(eps), _p(y), _p(res), _p(ws),
+                                      ws.numel(), _stream()))
+    return y
+
+
 def swiglu_q8(g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
     """silu(g) * u + Q8_0 conversion, fused -> act buffer. g, u [rows, n] sharing a row stride."""
     rows, n = g.shape

@@ -47,3 +47,28 @@ def test_mul_mat_q_with_residual(gops, orc, t, B, N, K):
     gops.mul_mat_q(qw, act, B, res=inplace, out=inplace)
     assert torch.equal(inplace, plain + r)
     assert orc.parity(to_np(plain), orc.mul_mat(raw, t, x, K)) < 1e-3
+
+
+@pytest.mark.parametrize("t", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("N,K", [(5, 256), (6144, 4096), (40000, 4096), (300, 14336)])
+@pytest.mark.parametrize("norm", [True, False])
+def test_rms_norm_mul_mat_equals_separate_launches(gops, orc, t, N, K, norm):
+    """gcq_rms_norm_mul_mat (one launch for K <= 4096: the GEMV normalizes and quantizes its row)
+    equals gcq_rms_norm_q8 (or gcq_quantize_act) + gcq_mul_mat_q bit for bit, with and without a
+    residual, and is within 1e-3 of the oracle's rms_norm -> mul -> mul_mat. N=5 leaves most
+    wavefronts without rows; N=40000 walks several row groups per wavefront; K=14336 takes the
+    two-launch path."""
+    raw = orc.quantize(orc.normal((N, K), seed=76, std=0.02), t)
+    qw = gops.QuantWeight.from_ggml(torch.from_numpy(raw), t, K)
+    x = orc.normal((1, K), seed=77) * 3
+    nw = orc.normal((K,), seed=78) if norm else None
+    xd = torch.from_numpy(x).cuda()
+    nwd = None if nw is None else torch.from_numpy(nw).cuda()
+    act = gops.rms_norm_q8(xd, nwd, 1e-5) if norm else gops.quantize_act(t, xd)
+    plain = gops.mul_mat_q(qw, act, 1)
+    fused = gops.rms_norm_mul_mat(qw, xd, nwd, 1e-5)
+    assert torch.equal(fused, plain)
+    r = torch.from_numpy(orc.normal((1, N), seed=79)).cuda()
+    assert torch.equal(gops.rms_norm_mul_mat(qw, xd, nwd, 1e-5, res=r), plain + r)
+    xn = orc.rms_norm(x, 1e-5) * nw[None, :] if norm else x
+    assert orc.parity(to_np(fused), orc.mul_mat(raw, t, xn, K)) < 1e-3
