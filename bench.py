@@ -9,9 +9,12 @@ of the captured decode graph, inside the on-device generate loop), and `value` i
 (QKV 4096x6144, O 4096x4096, gate/up 4096x28672, down 14336x4096) over weights rotated past the
 256 MB Infinity Cache; `value` is GB/s.
 
-`roofline` is the Q4_0 batch-1 GEMV kernel (algorithmic bytes N*K/32*18 + 4K + 4N per launch)
-timed with events on its stream; `cpu_baseline` is the repo's CPU oracle (a restatement of ggml's
-CPU semantics, not ggml) on the host cores, on a bounded sample of the same workload.
+`roofline` is the dominant decode kernel, the f32-row Q4_0 GEMV that runs the QKV, gate/up and
+lm-head projections (algorithmic bytes N*K/32*18 + 8K + 4N per launch), its launches of one step
+replayed from a HIP graph between events on their stream; `traffic` comes from the committed
+rocprofv3 --pmc summary. `cpu_baseline` is the repo's CPU oracle (a restatement of ggml's CPU
+semantics, not ggml) on the host cores, on a bounded sample of the same workload. Mode "roofline"
+runs only the roofline leg plus a 1 GiB copy (the counter calibration) for rocprofv3 --pmc.
 """
 
 from __future__ import annotations
@@ -42,38 +45,96 @@ def _weights(ops, K: int, N: int, seed: int, copies: int):
     return [w] + [ops.QuantWeight(w.type, w.N, w.K, w.data.clone()) for _ in range(copies - 1)]
 
 
-def gemv_roofline(ops, torch, iters: int = 40) -> dict:
-    """Average duration of the batch-1 Q4_0 GEMV kernel over the decode layer shapes, each launch
-    bracketed by events on the launch stream, weights rotated past the Infinity Cache."""
-    total_bytes, total_ms, n = 0, 0.0, 0
-    per_shape = {}
-    for K, N in LAYER_SHAPES:
-        wbytes = N * (K // 32) * 18
-        copies = max(2, math.ceil(ROTATE_BYTES / wbytes))
-        ws = _weights(ops, K, N, seed=K + N, copies=copies)
-        act = ops.quantize_act("q4_0", ops.fill_normal((1, K), seed=1))
-        for i in range(copies):
-            ops.mul_mat_q(ws[i], act, 1)
-        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(iters)]
+# The launches of the dominant decode kernel in one 8B decode step, in step order: per layer the
+# QKV and gate/up projections, then the lm head (name, K, N, launches per step).
+ROOF_KERNEL = "k_gemv_p<Q4_0, f32 row: rms_norm + norm weight + Q8_0 in the prologue, 1024 threads>"
+ROOF_LAUNCHES = [("attn_qkv", 4096, 6144, 32), ("ffn_gate_up", 4096, 28672, 32), ("output", 4096, 128256, 1)]
+ROOF_BYTES_NOTE = ("per launch: N*K/32*18 (Q4_0 weight) + 4K (x) + 4K (norm weight) + 4N (y); "
+                   "mean over a step's 65 launches")
+PMC_SUMMARY = ROOT / "profiles" / "k_gemv_p_f32_q4_0_decode_pmc.md"
+
+
+def _f32_launch_bytes(K: int, N: int) -> int:
+    return N * (K // 32) * 18 + 8 * K + 4 * N
+
+
+def _pmc_traffic():
+    """HBM bytes per launch of the roofline kernel from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE, scaled by a plain copy's readings), or None."""
+    if not PMC_SUMMARY.exists():
+        return None
+    for line in PMC_SUMMARY.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":")[1].strip())
+    return None
+
+
+def gemv_roofline(ops, torch, passes: int = 10) -> dict:
+    """The dominant decode kernel: the persistent GEMV that reads its activation as an f32 row and
+    does ggml_rms_norm, the norm-weight mul and the Q8_0 conversion in its prologue. It runs the
+    QKV, gate/up and lm-head projections: 65 of a decode step's launches and 2.5 of its 4.3 GB.
+    Its launches in one step's order, with distinct weights per layer (2.4 GB, far past the 256 MB
+    Infinity Cache), are captured once in a HIP graph, and `passes` replays are bracketed by two
+    events on the stream they run on; avg_us = elapsed / launches. Each shape alone (same launch
+    counts) gives the per-shape figures."""
+    from ggml_compiler_amd._lib import check, load
+
+    lib = load()
+    x = ops.fill_normal((1, 4096), seed=1)
+    nw = ops.fill_normal((4096,), seed=2)
+    ws = {name: [ops.QuantWeight.quantize(ops.fill_normal((N, K), seed=1000 + 7 * i + K + N, std=0.02), "q4_0")
+                 for i in range(n)] for name, K, N, n in ROOF_LAUNCHES}
+    ys = {N: torch.empty(N, dtype=torch.float32, device="cuda") for _, _, N, _ in ROOF_LAUNCHES}
+    step = [w for l in range(32) for w in (ws["attn_qkv"][l], ws["ffn_gate_up"][l])] + ws["output"]
+
+    def launch(seq):
+        s = ops._stream()
+        for w in seq:
+            check(lib.gcq_rms_norm_mul_mat(w.type, ops._p(w.data), w.N, w.K, ops._p(x), ops._p(nw), 1e-5,
+                                           ops._p(ys[w.N]), None, None, 0, s))
+
+    def timed(seq):
+        launch(seq)  # device queries happen before capture
         torch.cuda.synchronize()
-        for i in range(iters):
-            ev[i][0].record()
-            ops.mul_mat_q(ws[i % copies], act, 1)
-            ev[i][1].record()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            launch(seq)
+        g.replay()
         torch.cuda.synchronize()
-        ms = [a.elapsed_time(b) for a, b in ev]
-        avg = sum(ms) / len(ms)
-        b = gemv_bytes(N, K)
-        per_shape[f"{K}x{N}"] = {"us": round(avg * 1e3, 2), "GB/s": round(b / (avg * 1e-3) / 1e9, 1)}
-        total_bytes += b * iters
-        total_ms += sum(ms)
-        n += iters
-        del ws
-    achieved = total_bytes / (total_ms * 1e-3) / 1e9
-    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": "k_gemv_q0<Q4_0, B=1> (decode layer shapes)", "avg_us": round(total_ms / n * 1e3, 2),
-            "shapes": per_shape}
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(passes):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / (passes * len(seq))
+        nbytes = sum(_f32_launch_bytes(w.K, w.N) for w in seq) / len(seq)
+        return us, nbytes
+
+    us, nbytes = timed(step)
+    achieved = nbytes / (us * 1e-6) / 1e9
+    shapes = {}
+    for name, K, N, _ in ROOF_LAUNCHES:
+        s_us, s_b = timed(ws[name])
+        shapes[f"{name} {K}x{N}"] = {"us": round(s_us, 2), "GB/s": round(s_b / (s_us * 1e-6) / 1e9, 1)}
+    traffic = _pmc_traffic()
+    out = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+           "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": ROOF_KERNEL,
+           "avg_us": round(us, 2), "algorithmic_bytes_per_launch": int(nbytes), "bytes_note": ROOF_BYTES_NOTE,
+           "shapes": shapes}
+    if traffic is not None:
+        out["traffic_note"] = f"HBM bytes per launch from {PMC_SUMMARY.relative_to(ROOT)}"
+    del ws
+    return out
+
+
+def copy_calibration(torch, nbytes: int = 1 << 30) -> None:
+    """A plain device copy of nbytes (reads nbytes, writes nbytes) for scaling the FETCH_SIZE /
+    WRITE_SIZE counters of a --pmc run."""
+    a = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    b.copy_(a)
+    torch.cuda.synchronize()
 
 
 def cpu_gemv_baseline(seconds: float = 10.0) -> dict:
@@ -206,14 +267,15 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--mode", choices=["decode", "gemv"], default="decode")
+    ap.add_argument("--mode", choices=["decode", "gemv", "roofline"], default="decode",
+                    help="roofline: only the roofline leg and a 1 GiB copy (for rocprofv3 --pmc runs)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for {args.gpus}); multi-GPU sharding is design-only here.",
               file=sys.stderr)
         return 2
-    args.steps = args.steps or (128 if args.mode == "decode" else 200)
+    args.steps = args.steps or {"decode": 128, "gemv": 200, "roofline": 10}[args.mode]
     args.warmup = args.warmup if args.warmup is not None else 8
 
     import torch
@@ -223,6 +285,12 @@ def main() -> int:
     ops.require_device()
     torch.cuda.set_device(0)
     model = None
+    if args.mode == "roofline":
+        roof = gemv_roofline(ops, torch, passes=args.steps)
+        copy_calibration(torch)
+        print(json.dumps({"metric": "roofline kernel GB/s", "value": roof["achieved"], "unit": "GB/s",
+                          "roofline": roof}), flush=True)
+        return 0
     if args.mode == "decode":
         res, model = bench_decode(args, torch)
     else:
