@@ -40,6 +40,7 @@ __global__ __launch_bounds__(256) void k_attn_split(const float * __restrict__ q
     constexpr int LPK = D / 8;         // lanes per key row
     constexpr int KPW = 64 / LPK;      // keys per wavefront step
     constexpr int KPB = 4 * KPW;       // keys per workgroup step
+    constexpr int NB = 8;              // steps per load batch (8 K rows and 8 V rows per lane)
     __shared__ float sc[G][kChunkMax];
     __shared__ float red[4][G];
     __shared__ float accs[4][G][D];
@@ -70,32 +71,49 @@ __global__ __launch_bounds__(256) void k_attn_split(const float * __restrict__ q
         }
     }
 
-    // Pass 1: scores.
+    // Pass 1: scores. Keys go in batches of NB steps with every load of a batch issued before
+    // any math; the first batch's V rows are loaded with its K rows (they do not depend on the
+    // scores), so a slice of up to NB*KPB keys costs one HBM round trip.
     const uint16_t * kb = k + (int64_t) hk * k_h;
+    const uint16_t * vb = v + (int64_t) hk * v_h;
     const uint16_t * mrow = mask ? mask + (int64_t) s * m_s : nullptr;
-    for (int base = 0; base < len; base += KPB) {
-        const int jj = base + wave * KPW + slot;
-        float part[G];
-        const bool ok = jj < len;
-        uint4 kr = make_uint4(0, 0, 0, 0);
-        if (ok) kr = *reinterpret_cast<const uint4 *>(kb + (int64_t) (j0 + jj) * k_j + 8 * sub);
+    uint4 vpre[NB];
 #pragma unroll
-        for (int g = 0; g < G; g++) {
-            float a = 0.0f;
-            a = __builtin_amdgcn_fdot2(as_h2(kr.x), qh[g][0], a, false);
-            a = __builtin_amdgcn_fdot2(as_h2(kr.y), qh[g][1], a, false);
-            a = __builtin_amdgcn_fdot2(as_h2(kr.z), qh[g][2], a, false);
-            a = __builtin_amdgcn_fdot2(as_h2(kr.w), qh[g][3], a, false);
-            part[g] = a;
+    for (int b = 0; b < NB; b++) {
+        const int jj = b * KPB + wave * KPW + slot;
+        vpre[b] = jj < len ? *reinterpret_cast<const uint4 *>(vb + (int64_t) (j0 + jj) * v_j + 8 * sub)
+                           : make_uint4(0, 0, 0, 0);
+    }
+    for (int base = 0; base < len; base += NB * KPB) {
+        uint4 kr[NB];
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            const int jj = base + b * KPB + wave * KPW + slot;
+            kr[b] = jj < len ? *reinterpret_cast<const uint4 *>(kb + (int64_t) (j0 + jj) * k_j + 8 * sub)
+                             : make_uint4(0, 0, 0, 0);
         }
 #pragma unroll
-        for (int g = 0; g < G; g++)
+        for (int b = 0; b < NB; b++) {
+            const int jj = base + b * KPB + wave * KPW + slot;
+            float part[G];
 #pragma unroll
-            for (int o = LPK / 2; o > 0; o >>= 1) part[g] += __shfl_xor(part[g], o, 64);
-        if (ok && sub == 0) {
-            const float mv = mrow ? h2f(mrow[j0 + jj]) : 0.0f;
+            for (int g = 0; g < G; g++) {
+                float a = 0.0f;
+                a = __builtin_amdgcn_fdot2(as_h2(kr[b].x), qh[g][0], a, false);
+                a = __builtin_amdgcn_fdot2(as_h2(kr[b].y), qh[g][1], a, false);
+                a = __builtin_amdgcn_fdot2(as_h2(kr[b].z), qh[g][2], a, false);
+                a = __builtin_amdgcn_fdot2(as_h2(kr[b].w), qh[g][3], a, false);
+                part[g] = a;
+            }
 #pragma unroll
-            for (int g = 0; g < G; g++) sc[g][jj] = mv == -INFINITY ? -INFINITY : part[g] * scale + mv;
+            for (int g = 0; g < G; g++)
+#pragma unroll
+                for (int o = LPK / 2; o > 0; o >>= 1) part[g] += __shfl_xor(part[g], o, 64);
+            if (jj < len && sub == 0) {
+                const float mv = mrow ? h2f(mrow[j0 + jj]) : 0.0f;
+#pragma unroll
+                for (int g = 0; g < G; g++) sc[g][jj] = mv == -INFINITY ? -INFINITY : part[g] * scale + mv;
+            }
         }
     }
     __syncthreads();
@@ -128,29 +146,38 @@ __global__ __launch_bounds__(256) void k_attn_split(const float * __restrict__ q
 #pragma unroll
     for (int g = 0; g < G; g++) sum[g] = red[0][g] + red[1][g] + red[2][g] + red[3][g];
 
-    // Pass 3: P.V, this lane's 8 dims of one key per step.
+    // Pass 3: P.V, this lane's 8 dims of one key per step, batches as in pass 1.
     float acc[G][8];
 #pragma unroll
     for (int g = 0; g < G; g++)
 #pragma unroll
         for (int c = 0; c < 8; c++) acc[g][c] = 0.0f;
-    const uint16_t * vb = v + (int64_t) hk * v_h;
-    for (int base = 0; base < len; base += KPB) {
-        const int jj = base + wave * KPW + slot;
-        if (jj < len) {
-            const uint4 vr = *reinterpret_cast<const uint4 *>(vb + (int64_t) (j0 + jj) * v_j + 8 * sub);
-            const uint32_t vw[4] = {vr.x, vr.y, vr.z, vr.w};
-            float vf[8];
+    for (int base = 0; base < len; base += NB * KPB) {
+        uint4 vr[NB];
 #pragma unroll
-            for (int c = 0; c < 4; c++) {
-                vf[2 * c] = h2f((uint16_t) (vw[c] & 0xffff));
-                vf[2 * c + 1] = h2f((uint16_t) (vw[c] >> 16));
-            }
+        for (int b = 0; b < NB; b++) {
+            const int jj = base + b * KPB + wave * KPW + slot;
+            if (base == 0) vr[b] = vpre[b];
+            else vr[b] = jj < len ? *reinterpret_cast<const uint4 *>(vb + (int64_t) (j0 + jj) * v_j + 8 * sub)
+                                  : make_uint4(0, 0, 0, 0);
+        }
 #pragma unroll
-            for (int g = 0; g < G; g++) {
-                const float p = sc[g][jj];
+        for (int b = 0; b < NB; b++) {
+            const int jj = base + b * KPB + wave * KPW + slot;
+            if (jj < len) {
+                const uint32_t vw[4] = {vr[b].x, vr[b].y, vr[b].z, vr[b].w};
+                float vf[8];
 #pragma unroll
-                for (int c = 0; c < 8; c++) acc[g][c] += p * vf[c];
+                for (int c = 0; c < 4; c++) {
+                    vf[2 * c] = h2f((uint16_t) (vw[c] & 0xffff));
+                    vf[2 * c + 1] = h2f((uint16_t) (vw[c] >> 16));
+                }
+#pragma unroll
+                for (int g = 0; g < G; g++) {
+                    const float p = sc[g][jj];
+#pragma unroll
+                    for (int c = 0; c < 8; c++) acc[g][c] += p * vf[c];
+                }
             }
         }
     }
@@ -178,6 +205,179 @@ __global__ __launch_bounds__(256) void k_attn_split(const float * __restrict__ q
         const int g = threadIdx.x;
         const int h = hk * G + g;
         part_ml[((int64_t) s * H + h) * nsplit + split] = make_float2(mx[g], sum[g]);
+    }
+}
+
+// Decode attention: one query row, every key below n_kv visible (no mask), grid (split, KV head),
+// NW wavefronts. Each wavefront takes a contiguous run of the split's keys; its lanes work in
+// groups of D/8 (8 dims, 16 B of a K or V row each) and every lane group keeps its own online
+// softmax per query head (running max m, exp-sum l, P.V accumulator) over load batches of NB
+// keys, K and V rows of a batch loaded together, so no reduction crosses lane groups inside the
+// loop. The lane groups and then the NW wavefronts are merged at the end (shuffles, LDS). One
+// split: the normalized output out[h][d]; several: the split's (max, exp-sum, unnormalized output)
+// in k_attn_split's partial layout, for the merge (k_attn_merge, or a GEMV prologue). The host
+// sizes splits so that each wavefront's keys are one load batch (decode_keys).
+//
+// Wavefronts per k_attn_decode workgroup: 16, or 8 for four query heads per KV head (whose
+// registers need two wavefronts' share); keys one workgroup loads in one batch per wavefront.
+__host__ __device__ constexpr int decode_waves(int G) { return G >= 4 ? 8 : 16; }
+__host__ __device__ constexpr int decode_keys(int D, int G) { return decode_waves(G) * (64 / (D / 8)) * 4; }
+
+// f16 value c (0..7) of 8 packed in a uint4, as f32.
+__device__ __forceinline__ float half_at(const uint4 & r, int c) {
+    const uint32_t w = c < 2 ? r.x : c < 4 ? r.y : c < 6 ? r.z : r.w;
+    return h2f((uint16_t) (c & 1 ? w >> 16 : w & 0xffff));
+}
+
+template <int D, int G, int NW>
+__global__ __launch_bounds__(NW * 64) void k_attn_decode(const float * __restrict__ q, int64_t q_h,
+                                                         const uint16_t * __restrict__ k, int64_t k_h, int64_t k_j,
+                                                         const uint16_t * __restrict__ v, int64_t v_h, int64_t v_j,
+                                                         float scale, int n_kv, const int * __restrict__ n_kv_dev,
+                                                         int nsplit, float * __restrict__ out,
+                                                         float * __restrict__ part_o, float2 * __restrict__ part_ml) {
+    constexpr int LPK = D / 8;     // lanes per key row
+    constexpr int KPW = 64 / LPK;  // lane groups (keys per step) per wavefront
+    constexpr int NB = 4;          // steps per load batch
+    static_assert(G * D <= NW * 64, "one output per thread in the merge");
+    static_assert(NW == decode_waves(G) && NW * KPW * NB == decode_keys(D, G), "decode split size");
+    __shared__ float so[NW][G * D];
+    __shared__ float2 sml[NW][G];
+
+    if (n_kv_dev) n_kv = *n_kv_dev;
+    const int split = blockIdx.x, hk = blockIdx.y;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int sub = lane % LPK, slot = lane / LPK;
+    const int chunk = (n_kv + nsplit - 1) / nsplit;
+    const int j0 = split * chunk;
+    const int len = max(0, min(n_kv, j0 + chunk) - j0);
+    const int per_wave = (len + NW - 1) / NW;
+    const int w0 = min(len, wave * per_wave), w1 = min(len, w0 + per_wave);
+
+    half2_t qh[G][4];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        const float * qp = q + (int64_t) (hk * G + g) * q_h + 8 * sub;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            half2_t t;
+            t.x = (_Float16) qp[2 * c];
+            t.y = (_Float16) qp[2 * c + 1];
+            qh[g][c] = t;
+        }
+    }
+    float m[G], l[G], acc[G][8];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        m[g] = -INFINITY;
+        l[g] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 8; c++) acc[g][c] = 0.0f;
+    }
+    const uint16_t * kb = k + (int64_t) hk * k_h + (int64_t) j0 * k_j + 8 * sub;
+    const uint16_t * vb = v + (int64_t) hk * v_h + (int64_t) j0 * v_j + 8 * sub;
+    for (int base = w0; base < w1; base += NB * KPW) {
+        uint4 kr[NB], vr[NB];
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            const int jj = base + b * KPW + slot;
+            const bool ok = jj < w1;
+            kr[b] = ok ? *reinterpret_cast<const uint4 *>(kb + (int64_t) jj * k_j) : make_uint4(0, 0, 0, 0);
+            vr[b] = ok ? *reinterpret_cast<const uint4 *>(vb + (int64_t) jj * v_j) : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            float sc[NB];
+            float bm = -INFINITY;
+#pragma unroll
+            for (int b = 0; b < NB; b++) {
+                float a = 0.0f;
+                a = __builtin_amdgcn_fdot2(as_h2(kr[b].x), qh[g][0], a, false);
+                a = __builtin_amdgcn_fdot2(as_h2(kr[b].y), qh[g][1], a, false);
+                a = __builtin_amdgcn_fdot2(as_h2(kr[b].z), qh[g][2], a, false);
+                a = __builtin_amdgcn_fdot2(as_h2(kr[b].w), qh[g][3], a, false);
+#pragma unroll
+                for (int o = LPK / 2; o > 0; o >>= 1) a += __shfl_xor(a, o, 64);
+                sc[b] = base + b * KPW + slot < w1 ? a * scale : -INFINITY;
+                bm = fmaxf(bm, sc[b]);
+            }
+            const float mn = fmaxf(m[g], bm);
+            if (mn == -INFINITY) continue;  // no key of this lane group yet
+            const float f = m[g] == -INFINITY ? 0.0f : __expf(m[g] - mn);
+            float p[NB];
+            float ps = 0.0f;
+#pragma unroll
+            for (int b = 0; b < NB; b++) {
+                p[b] = sc[b] == -INFINITY ? 0.0f : __expf(sc[b] - mn);
+                ps += p[b];
+            }
+            l[g] = l[g] * f + ps;
+#pragma unroll
+            for (int c = 0; c < 8; c++) {
+                float t = acc[g][c] * f;
+#pragma unroll
+                for (int b = 0; b < NB; b++) t += p[b] * half_at(vr[b], c);
+                acc[g][c] = t;
+            }
+            m[g] = mn;
+        }
+    }
+    // Merge the wavefront's lane groups (same sub, slots 0..KPW-1), then the NW wavefronts.
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        float M = m[g];
+#pragma unroll
+        for (int o = LPK; o < 64; o <<= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+        const float f = m[g] == -INFINITY ? 0.0f : __expf(m[g] - M);
+        float L = l[g] * f;
+#pragma unroll
+        for (int o = LPK; o < 64; o <<= 1) L += __shfl_xor(L, o, 64);
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            float t = acc[g][c] * f;
+#pragma unroll
+            for (int o = LPK; o < 64; o <<= 1) t += __shfl_xor(t, o, 64);
+            acc[g][c] = t;
+        }
+        m[g] = M;
+        l[g] = L;
+    }
+    if (slot == 0) {
+#pragma unroll
+        for (int g = 0; g < G; g++)
+#pragma unroll
+            for (int c = 0; c < 8; c++) so[wave][g * D + 8 * sub + c] = acc[g][c];
+    }
+    if (lane < G) {
+#pragma unroll
+        for (int g = 0; g < G; g++)
+            if (lane == g) sml[wave][g] = make_float2(m[g], l[g]);
+    }
+    __syncthreads();
+    const int i = threadIdx.x;
+    if (i < G * D) {
+        const int g = i / D, d = i % D;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < NW; w++) M = fmaxf(M, sml[w][g].x);
+        float L = 0.0f, o = 0.0f;
+        if (M != -INFINITY) {
+#pragma unroll
+            for (int w = 0; w < NW; w++) {
+                const float2 ml = sml[w][g];
+                if (ml.x == -INFINITY) continue;
+                const float f = __expf(ml.x - M);
+                L += f * ml.y;
+                o += f * so[w][i];
+            }
+        }
+        const int h = hk * G + g;
+        if (nsplit == 1) {
+            out[h * D + d] = L == 0.0f ? 0.0f : o / L;
+        } else {
+            part_o[((int64_t) h * nsplit + split) * D + d] = o;
+            if (d == 0) part_ml[(int64_t) h * nsplit + split] = make_float2(M, L);
+        }
     }
 }
 
@@ -214,6 +414,38 @@ AttnPlan attn_plan(int Sq, int Hkv, int n_kv) {
         chunk = (n_kv + nsplit - 1) / nsplit;
     }
     return {nsplit, max(chunk, 1)};
+}
+
+// k_attn_decode's split count for n_kv keys: one load batch per wavefront, at most max_split
+// splits (the wavefronts then take several batches).
+int decode_splits(int D, int G, int n_kv, int max_split) {
+    return max(1, min(max_split, (n_kv + decode_keys(D, G) - 1) / decode_keys(D, G)));
+}
+
+// Decode (one query row, captured once for every KV length up to max_ctx): the split count for
+// max_ctx keys; the KV length itself is read on the device and each split takes an equal share.
+AttnPlan attn_plan_decode(int D, int G, int max_ctx, int max_split) {
+    const int nsplit = decode_splits(D, G, max_ctx, max_split);
+    return {nsplit, (max_ctx + nsplit - 1) / nsplit};
+}
+
+bool attn_decode_fits(int D, int G) { return (D == 64 || D == 128) && (G == 1 || G == 2 || G == 4); }
+
+// out [H*D] (one split) or part_o / part_ml (several), q [H][D] at head stride q_h.
+void launch_attn_decode(const float * q, int64_t q_h, const void * k, int64_t k_h, int64_t k_j, const void * v,
+                        int64_t v_h, int64_t v_j, int D, int H, int Hkv, int n_kv, const int * n_kv_dev, float scale,
+                        int nsplit, float * out, float * part_o, float2 * part_ml, hipStream_t s) {
+    const int G = H / Hkv;
+    require(attn_decode_fits(D, G) && H % Hkv == 0, "attn decode: D 64 / 128 and 1, 2 or 4 query heads per KV head");
+    const dim3 grid((unsigned) nsplit, (unsigned) Hkv);
+    const uint16_t *kp = (const uint16_t *) k, *vp = (const uint16_t *) v;
+#define GCQ_AD(DD, GG)                                                                                          \
+    if (D == DD && G == GG)                                                                                     \
+        k_attn_decode<DD, GG, decode_waves(GG)><<<grid, decode_waves(GG) * 64, 0, s>>>(                         \
+            q, q_h, kp, k_h, k_j, vp, v_h, v_j, scale, n_kv, n_kv_dev, nsplit, out, part_o, part_ml);
+    GCQ_AD(64, 1) GCQ_AD(64, 2) GCQ_AD(64, 4) GCQ_AD(128, 1) GCQ_AD(128, 2) GCQ_AD(128, 4)
+#undef GCQ_AD
+    check_launch("attn decode");
 }
 
 size_t attn_workspace(int Sq, int H, int Hkv, int Dv, int n_kv) {
@@ -273,6 +505,18 @@ void launch_flash_attn(const float * q, int64_t q_h, int64_t q_s, const void * k
     require(ws_size >= attn_workspace(Sq, H, Hkv, Dv, n_kv), "flash_attn: workspace too small");
     float * po = (float *) ws;
     float2 * pml = (float2 *) ((uint8_t *) ws + align256((size_t) Sq * H * p.nsplit * Dv * sizeof(float)));
+    if (Sq == 1 && mask == nullptr && H % Hkv == 0 && attn_decode_fits(D, H / Hkv)) {
+        // One query row, every key visible: the one-pass decode kernel (fewer splits than p, so the
+        // workspace holds its partials).
+        const int nsplit = decode_splits(D, H / Hkv, n_kv, p.nsplit);
+        launch_attn_decode(q, q_h, k, k_h, k_j, v, v_h, v_j, D, H, Hkv, n_kv, nullptr, scale, nsplit, out, po, pml,
+                           s);
+        if (nsplit == 1) return;
+        if (D == 64) k_attn_merge<64><<<(unsigned) H, 64, 0, s>>>(po, pml, out, nsplit);
+        else k_attn_merge<128><<<(unsigned) H, 128, 0, s>>>(po, pml, out, nsplit);
+        check_launch("flash_attn merge");
+        return;
+    }
     launch_attn_split(q, q_h, q_s, k, k_h, k_j, v, v_h, v_j, mask, m_s, D, Sq, H, Hkv, n_kv, scale, po, pml, p,
                       nullptr, s);
     if (D == 64) k_attn_merge<64><<<(unsigned) (Sq * H), 64, 0, s>>>(po, pml, out, p.nsplit);

@@ -20,8 +20,6 @@ void launch_act_quant(int wtype, const float * x, int64_t ldx, int64_t B, int64_
 void launch_act_to_ggml(int wtype, const void * act, int64_t B, int64_t k, void * out, hipStream_t s);
 void launch_gemv(int type, const void * w, int64_t N, int64_t K, const void * act, int64_t B, float * y, int64_t ldy,
                  hipStream_t s, const float * res = nullptr);
-bool launch_gemv_f32(int type, const void * w, int64_t N, int64_t K, const float * x, const float * norm_w, float eps,
-                     float * y, const float * res, hipStream_t s);
 void launch_isums(int type, const void * w, int64_t N, int64_t K, const void * act, int64_t B, int32_t * out,
                   hipStream_t s);
 void launch_gemm(int type, const void * w, int64_t N, int64_t K, const void * act, int64_t M, float * y, int64_t ldy,
@@ -140,6 +138,18 @@ void need_k(int t, int64_t k) {
 void need_ptr(const void * p, const char * what, size_t align = 1) {
     require(p != nullptr, std::string(what) + " is NULL");
     require(aligned(p, align), std::string(what) + " must be " + std::to_string(align) + "-byte aligned");
+}
+
+// The decode-row GEMV's arguments for a packed weight w [N][K] and an f32 row x.
+RowArgs row_args(int wtype, const void * w, int64_t N, int64_t K, const float * x) {
+    const WeightLayout L = weight_layout(wtype, N, K);
+    RowArgs a{};
+    a.wqs = (const uint8_t *) w + L.qs;
+    a.wd = (const uint16_t *) ((const uint8_t *) w + L.d);
+    a.N = (int) N;
+    a.nb = (int) (K / QK);
+    a.x = x;
+    return a;
 }
 
 void need_dims(int64_t v, const char * what, int64_t lo = 1, int64_t hi = INT32_MAX) {
@@ -297,7 +307,11 @@ int gcq_mul_mat(int wtype, const void * w, int64_t N, int64_t K, const float * x
         const size_t need = gcq_mul_mat_workspace(wtype, M, K);
         require(ws_size >= need, "workspace of " + std::to_string(ws_size) + " bytes, need " + std::to_string(need));
         hipStream_t s = as_stream(stream);
-        if (M == 1 && launch_gemv_f32(wtype, w, N, K, x, nullptr, 0.0f, y, nullptr, s)) return;
+        if (M == 1 && row_gemv_fits(wtype, K)) {  // one row: quantized inside the GEMV
+            RowArgs a = row_args(wtype, w, N, K, x);
+            a.y = y;
+            return launch_row_gemv(wtype, PRO_PLAIN, EPI_STORE, a, s);
+        }
         if (M <= 8) {
             launch_act_quant(wtype, x, ldx, M, K, ws, s);
             launch_gemv(wtype, w, N, K, ws, M, y, ldy, s);
@@ -326,7 +340,14 @@ int gcq_rms_norm_mul_mat(int wtype, const void * w, int64_t N, int64_t K, const 
         need_ptr(y, "y", 4);
         if (res) need_ptr(res, "res", 4);
         hipStream_t s = as_stream(stream);
-        if (launch_gemv_f32(wtype, w, N, K, x, norm_w, eps, y, res, s)) return;
+        if (row_gemv_fits(wtype, K)) {
+            RowArgs a = row_args(wtype, w, N, K, x);
+            a.norm_w = norm_w;
+            a.eps = eps;
+            a.y = y;
+            a.res = res;
+            return launch_row_gemv(wtype, norm_w ? PRO_NORM : PRO_PLAIN, EPI_STORE, a, s);
+        }
         need_ptr(ws, "workspace", 256);
         const size_t need = gcq_mul_mat_workspace(wtype, 1, K);
         require(ws_size >= need, "workspace of " + std::to_string(ws_size) + " bytes, need " + std::to_string(need));

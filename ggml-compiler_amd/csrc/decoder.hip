@@ -131,6 +131,17 @@ __global__ __launch_bounds__(D / 4) void k_merge_q8(const float * __restrict__ p
     q8_block_store(o, codes + s * n + (e & ~31), meta + s * (n / 32) + e / 32, (d0 / 4) & 7);
 }
 
+// dst[r][map[c]] = src[r][c] for S rows of n columns: a mul_mat result whose weight rows were
+// packed in another order, back in the weight's own row order.
+__global__ void k_scatter_cols(const float * __restrict__ src, int64_t lds, float * __restrict__ dst, int64_t ldd,
+                               const int32_t * __restrict__ map, int S, int n) {
+    const int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= (int64_t) S * n) return;
+    const int64_t r = t / n;
+    const int c = (int) (t % n);
+    dst[r * ldd + map[c]] = src[r * lds + c];
+}
+
 // mask[s][j] = 0 for j <= pos0 + s, -inf after (f16), j < n_kv.
 __global__ void k_causal_mask(uint16_t * __restrict__ mask, int S, int n_kv, int pos0) {
     const int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
@@ -238,6 +249,12 @@ void launch_merge_q8(const float * part_o, const float2 * part_ml, int nsplit, i
     else if (D == 64) k_merge_q8<64><<<(unsigned) (Sq * H), 16, 0, s>>>(part_o, part_ml, nsplit, H, out, codes, meta);
     else fail("merge_q8: head size must be 64 or 128");
     check_launch("merge_q8");
+}
+
+void launch_scatter_cols(const float * src, int64_t lds, float * dst, int64_t ldd, const int32_t * map, int S, int n,
+                         hipStream_t s) {
+    k_scatter_cols<<<nblk((int64_t) S * n, 256), 256, 0, s>>>(src, lds, dst, ldd, map, S, n);
+    check_launch("scatter_cols");
 }
 
 void launch_causal_mask(void * mask, int S, int n_kv, int pos0, hipStream_t s) {

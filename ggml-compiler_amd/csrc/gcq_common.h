@@ -68,6 +68,37 @@ struct AttnPlan {
 };
 AttnPlan attn_plan(int Sq, int Hkv, int n_kv);
 
+// Arguments of the decode-row GEMV (rowgemv.hip): one f32 activation row times a packed Q4_0 /
+// Q8_0 weight, with the node before (prologue) and after (epilogue) the mul_mat in one launch.
+enum { PRO_PLAIN = 0, PRO_NORM = 1, PRO_MERGE = 2 };
+enum { EPI_STORE = 0, EPI_ROPE_KV = 1, EPI_SWIGLU = 2 };
+
+struct RowArgs {
+    const uint8_t * wqs;
+    const uint16_t * wd;
+    int N, nb;  // packed weight rows, blocks per row
+    // prologue
+    const float * x;
+    const float * norm_w;
+    float eps;
+    const float * part_o;     // [H][nsplit][D]
+    const float2 * part_ml;   // [H][nsplit] (max, exp-sum)
+    int nsplit;
+    // epilogue
+    float * y;  // EPI_STORE [N], EPI_SWIGLU [N/2], EPI_ROPE_KV: roped q [H*D]
+    const float * res;
+    const int * pos;
+    uint16_t * kc;  // [Hkv][ctx][D] f16
+    uint16_t * vc;
+    int64_t ctx;
+    int H, Hkv, D;
+    float theta_scale;
+};
+
+void launch_row_gemv(int type, int pro, int epi, const RowArgs & a, hipStream_t s);
+bool row_gemv_fits(int type, int64_t K);
+int row_gemv_merge_max();
+
 // Wraps a C-ABI body: 0 on success, -1 with last_error set on failure.
 template <class F>
 int guarded(F && f) {

@@ -144,21 +144,12 @@ __global__ __launch_bounds__(256) void k_gemv_q0(const uint8_t * __restrict__ wq
 // activation blocks in registers for the whole launch and walks row groups g, g + waves, ...,
 // loading the next group's weights before it reduces the current one, so a wavefront always has
 // R*NBL*(16 or 32) bytes per lane of HBM reads in flight.
-//
-// XF (one activation row, K <= 4*NT): the activation arrives as f32 and each workgroup quantizes
-// it into LDS itself, optionally after ggml_rms_norm and the mul by a norm weight (the launches
-// before a mul_mat in ggml's graph): squares rounded to f32 and summed in double, the mean rounded
-// to f32, then (x * scale) * w and the canonical Q8_0 conversion, so the codes equal those of the
-// separate rms_norm + quantize launches. The workgroup's first weights are already in flight
-// while it does this; with one 1024-thread workgroup per CU the row is read once per CU.
-template <int TYPE, int B, int R, int NBL, bool XF, int NT>
-__global__ __launch_bounds__(NT) void k_gemv_p(const uint8_t * __restrict__ wqs, const uint16_t * __restrict__ wd,
-                                               const int8_t * __restrict__ xc, const float2 * __restrict__ xm,
-                                               const float * __restrict__ xf, const float * __restrict__ norm_w,
-                                               float eps, float * y, const float * res, int N, int nb, int ldy) {
+template <int TYPE, int B, int R, int NBL>
+__global__ __launch_bounds__(256) void k_gemv_p(const uint8_t * __restrict__ wqs, const uint16_t * __restrict__ wd,
+                                                const int8_t * __restrict__ xc, const float2 * __restrict__ xm,
+                                                float * y, const float * res, int N, int nb, int ldy) {
     constexpr int CV = TYPE == T_Q4_0 ? 1 : 2;
-    constexpr int NWV = NT / 64;
-    static_assert(!XF || B == 1, "f32 activation: one row");
+    constexpr int NWV = 4;
     const int lane = threadIdx.x & 63;
     const int nw = gridDim.x * NWV;
     const int ng = (N + R - 1) / R;
@@ -185,58 +176,20 @@ __global__ __launch_bounds__(NT) void k_gemv_p(const uint8_t * __restrict__ wqs,
     };
 
     int g = blockIdx.x * NWV + (threadIdx.x >> 6);
-    if (g < ng) load(g, w, d);  // first weights in flight before the activation work
+    if (g < ng) load(g, w, d);  // first weights in flight before the activation loads
 
     int4 xa[NBL][B], xb[NBL][B];
     float2 xmv[NBL][B];
-    if constexpr (XF) {
-        __shared__ int4 lc[NT / 2];  // the row's codes: 4*NT bytes
-        __shared__ float2 lm[NT / 8];
-        __shared__ double red[NWV];
-        const int e = threadIdx.x * 4;  // 8 lanes per 32-value block
-        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (e < K) v = *reinterpret_cast<const float4 *>(xf + e);
-        if (norm_w) {
-            double ss = (double) (v.x * v.x) + (double) (v.y * v.y) + (double) (v.z * v.z) + (double) (v.w * v.w);
 #pragma unroll
-            for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-            if (lane == 0) red[threadIdx.x >> 6] = ss;
-            __syncthreads();
-            double tot = 0.0;
+    for (int i = 0; i < NBL; i++) {
+        const int blk = lane + 64 * i;
 #pragma unroll
-            for (int i = 0; i < NWV; i++) tot += red[i];
-            const float scale = 1.0f / sqrtf((float) (tot / (double) K) + eps);
-            if (e < K) {
-                const float4 wv = *reinterpret_cast<const float4 *>(norm_w + e);
-                v.x = (v.x * scale) * wv.x;
-                v.y = (v.y * scale) * wv.y;
-                v.z = (v.z * scale) * wv.z;
-                v.w = (v.w * scale) * wv.w;
-            }
-        }
-        if (e < K) q8_block_store(v, reinterpret_cast<int8_t *>(lc) + (e & ~31), lm + e / 32, (e / 4) & 7);
-        __syncthreads();
-#pragma unroll
-        for (int i = 0; i < NBL; i++) {
-            const int blk = lane + 64 * i;
+        for (int b = 0; b < B; b++) {
             if (blk < nb) {
-                xa[i][0] = lc[2 * blk];
-                xb[i][0] = lc[2 * blk + 1];
-                xmv[i][0] = lm[blk];
-            }
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < NBL; i++) {
-            const int blk = lane + 64 * i;
-#pragma unroll
-            for (int b = 0; b < B; b++) {
-                if (blk < nb) {
-                    const int4 * xp = reinterpret_cast<const int4 *>(xc + (size_t) b * K + (size_t) blk * QK);
-                    xa[i][b] = xp[0];
-                    xb[i][b] = xp[1];
-                    xmv[i][b] = xm[(size_t) b * nb + blk];
-                }
+                const int4 * xp = reinterpret_cast<const int4 *>(xc + (size_t) b * K + (size_t) blk * QK);
+                xa[i][b] = xp[0];
+                xb[i][b] = xp[1];
+                xmv[i][b] = xm[(size_t) b * nb + blk];
             }
         }
     }
@@ -447,8 +400,8 @@ unsigned persistent_grid(int N, int waves_per_wg, int wg_per_cu) {
 template <int TYPE, int B, int NBL>
 void run_p(const uint8_t * w, const WeightLayout & L, const int8_t * xc, const float2 * xm, float * y, const float * res, int N, int nb,
            int ldy, hipStream_t s) {
-    k_gemv_p<TYPE, B, kRp, NBL, false, 256><<<persistent_grid(N, 4, kWgPerCu), 256, 0, s>>>(
-        w + L.qs, (const uint16_t *) (w + L.d), xc, xm, nullptr, nullptr, 0.0f, y, res, N, nb, ldy);
+    k_gemv_p<TYPE, B, kRp, NBL><<<persistent_grid(N, 4, kWgPerCu), 256, 0, s>>>(
+        w + L.qs, (const uint16_t *) (w + L.d), xc, xm, y, res, N, nb, ldy);
 }
 
 int pick_nbl(int tasks) {  // tasks per row (blocks, or Q4_K chunks)
@@ -552,29 +505,6 @@ void launch_gemv(int type, const void * wv, int64_t N, int64_t K, const void * a
         fail("mul_mat: unsupported weight type " + std::to_string(type));
     }
     check_launch("gemv");
-}
-
-// One f32 activation row x [K] (optionally rms-normalized with norm_w and eps first) times a packed
-// Q4_0 / Q8_0 weight with K <= 4096: the persistent kernel (one 1024-thread workgroup per CU)
-// quantizes x itself. Returns false (nothing launched) for shapes it does not take.
-bool launch_gemv_f32(int type, const void * wv, int64_t N, int64_t K, const float * x, const float * norm_w, float eps,
-                     float * y, const float * res, hipStream_t s) {
-    if ((type != T_Q4_0 && type != T_Q8_0) || K % QK || K > 4 * 1024) return false;
-    const uint8_t * w = (const uint8_t *) wv;
-    const WeightLayout L = weight_layout(type, N, K);
-    const int nb = (int) (K / QK);
-    const unsigned grid = persistent_grid((int) N, 16, 1);
-#define GCQ_XF(TY, NBL)                                                                                        \
-    k_gemv_p<TY, 1, kRp, NBL, true, 1024><<<grid, 1024, 0, s>>>(w + L.qs, (const uint16_t *) (w + L.d), nullptr,       \
-                                                        nullptr, x, norm_w, eps, y, res, (int) N, nb, (int) N)
-    if (type == T_Q4_0) {
-        if (nb <= 64) GCQ_XF(T_Q4_0, 1); else GCQ_XF(T_Q4_0, 2);
-    } else {
-        if (nb <= 64) GCQ_XF(T_Q8_0, 1); else GCQ_XF(T_Q8_0, 2);
-    }
-#undef GCQ_XF
-    check_launch("gemv f32");
-    return true;
 }
 
 void launch_isums(int type, const void * wv, int64_t N, int64_t K, const void * act, int64_t B, int32_t * out,

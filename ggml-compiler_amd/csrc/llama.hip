@@ -31,8 +31,6 @@ void launch_pack(int type, const void * src, int64_t nrows, int64_t k, void * ds
 void launch_unpack(int type, const void * src, int64_t nrows, int64_t k, void * dst, hipStream_t s);
 void launch_gemv(int type, const void * w, int64_t N, int64_t K, const void * act, int64_t B, float * y, int64_t ldy,
                  hipStream_t s, const float * res);
-bool launch_gemv_f32(int type, const void * w, int64_t N, int64_t K, const float * x, const float * norm_w, float eps,
-                     float * y, const float * res, hipStream_t s);
 void launch_gemm(int type, const void * w, int64_t N, int64_t K, const void * act, int64_t M, float * y, int64_t ldy,
                  hipStream_t s, const float * res);
 void launch_get_rows(int type, const void * tab, int64_t nrows_tab, int64_t D, const int32_t * idx, int64_t n,
@@ -51,6 +49,15 @@ void launch_rope_kv(float * qkv, int64_t ld, const int32_t * pos, int S, int H, 
 void launch_merge_q8(const float * part_o, const float2 * part_ml, int nsplit, int Sq, int H, int D, float * out,
                      void * act, hipStream_t s);
 void launch_causal_mask(void * mask, int S, int n_kv, int pos0, hipStream_t s);
+void launch_move_rows(const void * src, void * dst, const int32_t * map, int64_t rows, int64_t row_bytes, bool scatter,
+                      hipStream_t s);
+void launch_scatter_cols(const float * src, int64_t lds, float * dst, int64_t ldd, const int32_t * map, int S, int n,
+                         hipStream_t s);
+AttnPlan attn_plan_decode(int D, int G, int max_ctx, int max_split);
+bool attn_decode_fits(int D, int G);
+void launch_attn_decode(const float * q, int64_t q_h, const void * k, int64_t k_h, int64_t k_j, const void * v,
+                        int64_t v_h, int64_t v_j, int D, int H, int Hkv, int n_kv, const int * n_kv_dev, float scale,
+                        int nsplit, float * out, float * part_o, float2 * part_ml, hipStream_t s);
 void launch_step_end(const float * logits, int n, void * state, int32_t * out_tokens, int max_out, void * part,
                      void * counter, hipStream_t s);
 
@@ -87,6 +94,7 @@ struct Tensor {
     int64_t rows, cols;
     bool random;        // drawn by init_random
     DevBuf buf;         // packed (quantized) or f32
+    DevBuf perm;        // packed row r holds the weight's row perm[r] (int32); empty: same order
 };
 
 }  // namespace
@@ -107,6 +115,10 @@ struct Llama {
     DevBuf kv, x, qkv, gu, act_a, act_b, part_o, part_ml, mask, positions, logits, state, out_tokens, tok_in;
     DevBuf argmax_part, counters;  // step_end partials; step_end's completion counter (zero between launches)
     AttnPlan plan_decode{};
+    bool fused = false;  // one token on the decode-row GEMVs (rowgemv.hip)
+    bool decode_attn = false;  // one token's attention on k_attn_decode
+    DevBuf attn_row;           // its output when it runs unsplit
+    DevBuf ytmp;         // a prompt chunk's mul_mat result in packed row order
     int pos = 0;
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
@@ -179,9 +191,34 @@ struct Llama {
             po = std::max(po, (size_t) S * c.n_head * p.nsplit * c.head_dim * 4);
             pml = std::max(pml, (size_t) S * c.n_head * p.nsplit * 8);
         }
+        // One token runs on the decode-row GEMVs when every projection's K fits them: QKV and
+        // gate/up are then packed in row pairs (rope pairs, gate/up pairs) for their epilogues.
+        decode_attn = attn_decode_fits(c.head_dim, c.n_head / c.n_head_kv);
+        plan_decode = decode_attn ? attn_plan_decode(c.head_dim, c.n_head / c.n_head_kv, c.max_ctx, row_gemv_merge_max())
+                                  : attn_plan(1, c.n_head_kv, c.max_ctx);
+        fused = row_gemv_fits(c.wtype, c.n_embd) && row_gemv_fits(c.wtype, attn_dim) &&
+                row_gemv_fits(c.wtype, c.n_ff) && c.head_dim % 4 == 0 &&
+                plan_decode.nsplit <= row_gemv_merge_max();
+        attn_row = DevBuf((size_t) attn_dim * 4);
+        po = std::max(po, (size_t) c.n_head * plan_decode.nsplit * c.head_dim * 4);
+        pml = std::max(pml, (size_t) c.n_head * plan_decode.nsplit * 8);
+        if (fused) {
+            const int D = c.head_dim, half = D / 2, nqk = (c.n_head + c.n_head_kv) * half;
+            std::vector<int32_t> pq(qkv_dim), pg(2 * (size_t) c.n_ff);
+            for (int64_t r = 0; r < qkv_dim; r++) {
+                const int64_t g = r / 2, b = r % 2;
+                pq[r] = (int32_t) (g < nqk ? (g / half) * D + g % half + b * half
+                                           : (int64_t) (c.n_head + c.n_head_kv) * D + 2 * (g - nqk) + b);
+            }
+            for (int64_t r = 0; r < 2 * (int64_t) c.n_ff; r++) pg[r] = (int32_t) ((r % 2) * c.n_ff + r / 2);
+            for (const Layer & L : layers) {
+                set_perm(L.qkv, pq);
+                set_perm(L.gate_up, pg);
+            }
+            ytmp = DevBuf((size_t) max_prompt * std::max<int64_t>(qkv_dim, 2 * (int64_t) c.n_ff) * 4);
+        }
         part_o = DevBuf(po);
         part_ml = DevBuf(pml);
-        plan_decode = attn_plan(1, c.n_head_kv, c.max_ctx);
         mask = DevBuf((size_t) max_prompt * c.max_ctx * 2);
         positions = DevBuf((size_t) max_prompt * 4);
         tok_in = DevBuf((size_t) max_prompt * 4);
@@ -198,6 +235,22 @@ struct Llama {
         reset();
     }
 
+    void set_perm(int ti, const std::vector<int32_t> & map) {
+        Tensor & t = tensors[ti];
+        t.perm = DevBuf(map.size() * 4);
+        check_hip(hipMemcpy(t.perm.p, map.data(), map.size() * 4, hipMemcpyHostToDevice), "perm");
+    }
+
+    // ggml block rows on the device (raw, natural order) -> the tensor's packed buffer.
+    void pack_into(Tensor & t, const void * raw, void * tmp) {
+        const void * src = raw;
+        if (t.perm.p) {
+            launch_move_rows(raw, tmp, t.perm.as<int32_t>(), t.rows, row_bytes(t.type, t.cols), false, stream);
+            src = tmp;
+        }
+        launch_pack(t.type, src, t.rows, t.cols, t.buf.p, stream);
+    }
+
     void reset() {
         check_hip(hipMemsetAsync(kv.p, 0, kv.n, stream), "KV reset");
         check_hip(hipStreamSynchronize(stream), "sync");
@@ -209,13 +262,13 @@ struct Llama {
         size_t biggest = 0;
         for (auto & t : tensors)
             if (t.random) biggest = std::max(biggest, (size_t) (t.rows * t.cols));
-        DevBuf f32(biggest * 4), raw(biggest / 32 * 34 + 256);
+        DevBuf f32(biggest * 4), raw(biggest / 32 * 34 + 256), tmp(biggest / 32 * 34 + 256);
         for (size_t i = 0; i < tensors.size(); i++) {
             Tensor & t = tensors[i];
             if (!t.random) continue;
             launch_fill_normal(f32.as<float>(), t.rows * t.cols, seed + i, 0, stddev, stream);
             launch_encode(t.type, f32.as<float>(), t.rows, t.cols, raw.p, stream);
-            launch_pack(t.type, raw.p, t.rows, t.cols, t.buf.p, stream);
+            pack_into(t, raw.p, tmp.p);
         }
         check_hip(hipStreamSynchronize(stream), "init_random");
     }
@@ -237,9 +290,9 @@ struct Llama {
             check_hip(hipMemcpy(t.buf.p, host, nbytes, hipMemcpyHostToDevice), "set_weight");
             return;
         }
-        DevBuf raw(nbytes);
+        DevBuf raw(nbytes), tmp(t.perm.p ? nbytes : 0);
         check_hip(hipMemcpy(raw.p, host, nbytes, hipMemcpyHostToDevice), "set_weight");
-        launch_pack(t.type, raw.p, t.rows, t.cols, t.buf.p, stream);
+        pack_into(t, raw.p, tmp.p);
         check_hip(hipStreamSynchronize(stream), "set_weight");
     }
 
@@ -253,16 +306,106 @@ struct Llama {
             check_hip(hipMemcpy(host, t.buf.p, nbytes, hipMemcpyDeviceToHost), "get_weight");
             return;
         }
-        DevBuf raw(nbytes);
+        DevBuf raw(nbytes), tmp(t.perm.p ? nbytes : 0);
         launch_unpack(t.type, t.buf.p, t.rows, t.cols, raw.p, stream);
+        if (t.perm.p) launch_move_rows(raw.p, tmp.p, t.perm.as<int32_t>(), t.rows, nbytes / t.rows, true, stream);
         check_hip(hipStreamSynchronize(stream), "get_weight");
-        check_hip(hipMemcpy(host, raw.p, nbytes, hipMemcpyDeviceToHost), "get_weight");
+        check_hip(hipMemcpy(host, (t.perm.p ? tmp : raw).p, nbytes, hipMemcpyDeviceToHost), "get_weight");
     }
 
     void mul_mat(int ti, const void * act, int64_t S, float * y, int64_t ldy, const float * res) {
         const Tensor & t = tensors[ti];
-        if (S <= 8) launch_gemv(t.type, t.buf.p, t.rows, t.cols, act, S, y, ldy, stream, res);
-        else launch_gemm(t.type, t.buf.p, t.rows, t.cols, act, S, y, ldy, stream, res);
+        float * out = y;
+        int64_t ldo = ldy;
+        if (t.perm.p) {  // rows packed in pairs: compute in packed order, then put columns back
+            require(res == nullptr, "mul_mat: residual on a row-paired weight");
+            out = ytmp.as<float>();
+            ldo = t.rows;
+        }
+        if (S <= 8) launch_gemv(t.type, t.buf.p, t.rows, t.cols, act, S, out, ldo, stream, res);
+        else launch_gemm(t.type, t.buf.p, t.rows, t.cols, act, S, out, ldo, stream, res);
+        if (t.perm.p) launch_scatter_cols(out, ldo, y, ldy, t.perm.as<int32_t>(), (int) S, (int) t.rows, stream);
+    }
+
+    RowArgs row_args(int ti) const {
+        const Tensor & t = tensors[ti];
+        const WeightLayout W = weight_layout(t.type, t.rows, t.cols);
+        RowArgs a{};
+        a.wqs = t.buf.as<uint8_t>() + W.qs;
+        a.wd = reinterpret_cast<const uint16_t *>(t.buf.as<uint8_t>() + W.d);
+        a.N = (int) t.rows;
+        a.nb = (int) (t.cols / QK);
+        return a;
+    }
+
+    // The single-token forward on the decode-row GEMVs: per layer QKV (rms_norm in, rope + K/V
+    // cache out), split-K attention, output projection (merge in, residual out), gate/up
+    // (rms_norm in, swiglu out), down (residual out); then the lm head (rms_norm in).
+    void forward_one(const int32_t * tok_dev, const int32_t * pos_dev, int n_kv, const int * n_kv_dev,
+                     const AttnPlan & plan) {
+        float * xs = x.as<float>();
+        const Tensor & E = tensors[t_embd];
+        launch_get_rows(E.type, E.buf.p, E.rows, E.cols, tok_dev, 1, xs, stream);
+        const float scale = 1.0f / std::sqrt((float) c.head_dim);
+        const float theta_scale = powf(c.rope_base, -2.0f / (float) c.head_dim);
+        const int64_t kv_h = (int64_t) c.max_ctx * c.head_dim;
+        for (int l = 0; l < c.n_layer; l++) {
+            const Layer & L = layers[l];
+            uint16_t * kvl = kv_layer(l);
+            RowArgs a = row_args(L.qkv);
+            a.x = xs;
+            a.norm_w = tensors[L.attn_norm].buf.as<float>();
+            a.eps = c.rms_eps;
+            a.y = qkv.as<float>();
+            a.pos = pos_dev;
+            a.kc = kvl;
+            a.vc = kvl + (size_t) c.n_head_kv * kv_h;
+            a.ctx = c.max_ctx;
+            a.H = c.n_head;
+            a.Hkv = c.n_head_kv;
+            a.D = c.head_dim;
+            a.theta_scale = theta_scale;
+            launch_row_gemv(c.wtype, PRO_NORM, EPI_ROPE_KV, a, stream);
+            if (decode_attn)
+                launch_attn_decode(qkv.as<float>(), c.head_dim, kvl, kv_h, c.head_dim, kvl + (size_t) c.n_head_kv * kv_h,
+                                   kv_h, c.head_dim, c.head_dim, c.n_head, c.n_head_kv, n_kv, n_kv_dev, scale,
+                                   plan.nsplit, attn_row.as<float>(), part_o.as<float>(), part_ml.as<float2>(), stream);
+            else
+                launch_attn_split(qkv.as<float>(), c.head_dim, qkv_dim, kvl, kv_h, c.head_dim,
+                                  kvl + (size_t) c.n_head_kv * kv_h, kv_h, c.head_dim, nullptr, n_kv, c.head_dim, 1,
+                                  c.n_head, c.n_head_kv, n_kv, scale, part_o.as<float>(), part_ml.as<float2>(), plan,
+                                  n_kv_dev, stream);
+            a = row_args(L.wo);
+            a.y = xs;
+            a.res = xs;
+            if (decode_attn && plan.nsplit == 1) {  // the attention row itself
+                a.x = attn_row.as<float>();
+                launch_row_gemv(c.wtype, PRO_PLAIN, EPI_STORE, a, stream);
+            } else {  // its split-K partials, merged in the prologue
+                a.part_o = part_o.as<float>();
+                a.part_ml = part_ml.as<float2>();
+                a.nsplit = plan.nsplit;
+                a.D = c.head_dim;
+                launch_row_gemv(c.wtype, PRO_MERGE, EPI_STORE, a, stream);
+            }
+            a = row_args(L.gate_up);
+            a.x = xs;
+            a.norm_w = tensors[L.ffn_norm].buf.as<float>();
+            a.eps = c.rms_eps;
+            a.y = gu.as<float>();
+            launch_row_gemv(c.wtype, PRO_NORM, EPI_SWIGLU, a, stream);
+            a = row_args(L.down);
+            a.x = gu.as<float>();
+            a.y = xs;
+            a.res = xs;
+            launch_row_gemv(c.wtype, PRO_PLAIN, EPI_STORE, a, stream);
+        }
+        RowArgs a = row_args(t_out);
+        a.x = xs;
+        a.norm_w = tensors[t_out_norm].buf.as<float>();
+        a.eps = c.rms_eps;
+        a.y = logits.as<float>();
+        launch_row_gemv(c.wtype, PRO_NORM, EPI_STORE, a, stream);
     }
 
     // ggml_rms_norm + ggml_mul by norm t_norm of S rows of the residual stream (the last row only
@@ -273,8 +416,14 @@ struct Llama {
         const float * nw = tensors[t_norm].buf.as<float>();
         const int rows = last_only ? 1 : S;
         const float * xr = xs + (size_t) (S - rows) * c.n_embd;
-        if (rows == 1 && launch_gemv_f32(t.type, t.buf.p, t.rows, t.cols, xr, nw, c.rms_eps, y, nullptr, stream))
-            return;
+        if (rows == 1 && !t.perm.p && row_gemv_fits(t.type, t.cols)) {
+            RowArgs a = row_args(ti);
+            a.x = xr;
+            a.norm_w = nw;
+            a.eps = c.rms_eps;
+            a.y = y;
+            return launch_row_gemv(t.type, PRO_NORM, EPI_STORE, a, stream);
+        }
         launch_rmsnorm_q8(xr, c.n_embd, nw, c.rms_eps, rows, c.n_embd, act_a.p, stream);
         mul_mat(ti, act_a.p, rows, y, ldy, nullptr);
     }
@@ -283,6 +432,7 @@ struct Llama {
     // captured step) passes the state's position / KV length pointers and no mask.
     void forward(int S, const int32_t * tok_dev, const int32_t * pos_dev, int n_kv, const int * n_kv_dev,
                  const void * mask_dev, const AttnPlan & plan) {
+        if (S == 1 && fused && mask_dev == nullptr) return forward_one(tok_dev, pos_dev, n_kv, n_kv_dev, plan);
         float * xs = x.as<float>();
         const Tensor & E = tensors[t_embd];
         launch_get_rows(E.type, E.buf.p, E.rows, E.cols, tok_dev, S, xs, stream);

@@ -225,6 +225,19 @@ __global__ void k_pack(const uint8_t * __restrict__ src, uint8_t * __restrict__ 
     for (int j = 0; j < CB / 16; j++) o[j] = make_uint4(w[4 * j], w[4 * j + 1], w[4 * j + 2], w[4 * j + 3]);
 }
 
+// Whole ggml rows moved by a row map, 16 bytes per thread (row_bytes % 16 == 0) or 2 (otherwise):
+// gather dst[r] = src[map[r]], scatter dst[map[r]] = src[r].
+template <class U>
+__global__ void k_move_rows(const U * __restrict__ src, U * __restrict__ dst, const int32_t * __restrict__ map,
+                            int64_t rows, int64_t per_row, bool scatter) {
+    const int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= rows * per_row) return;
+    const int64_t r = t / per_row, c = t % per_row;
+    const int64_t m = map[r];
+    if (scatter) dst[m * per_row + c] = src[r * per_row + c];
+    else dst[r * per_row + c] = src[m * per_row + c];
+}
+
 // packed -> ggml block rows (the inverse of k_pack).
 template <int CB>
 __global__ void k_unpack(const uint8_t * __restrict__ qs, const uint16_t * __restrict__ d, uint8_t * __restrict__ dst,
@@ -424,6 +437,22 @@ void launch_pack(int type, const void * src, int64_t nrows, int64_t k, void * ds
     else
         fail("pack: unsupported type " + std::to_string(type));
     check_launch("pack");
+}
+
+void launch_move_rows(const void * src, void * dst, const int32_t * map, int64_t rows, int64_t row_bytes, bool scatter,
+                      hipStream_t s) {
+    if (rows == 0) return;
+    if (row_bytes % 16 == 0) {
+        const int64_t per = row_bytes / 16;
+        k_move_rows<uint4><<<nblk(rows * per, 256), 256, 0, s>>>((const uint4 *) src, (uint4 *) dst, map, rows, per,
+                                                                 scatter);
+    } else {
+        require(row_bytes % 2 == 0, "move_rows: odd row size");
+        const int64_t per = row_bytes / 2;
+        k_move_rows<uint16_t><<<nblk(rows * per, 256), 256, 0, s>>>((const uint16_t *) src, (uint16_t *) dst, map,
+                                                                    rows, per, scatter);
+    }
+    check_launch("move_rows");
 }
 
 void launch_unpack(int type, const void * src, int64_t nrows, int64_t k, void * dst, hipStream_t s) {

@@ -1,0 +1,360 @@
+// rowgemv.hip - the decode step's projections: one f32 activation row times a packed Q4_0 / Q8_0
+// weight, with the graph node before and after each mul_mat done in the same launch.
+//
+// In ggml-compiler's decoder layer (ggml_compiler/llm.py:361-444 at O3) every mul_mat sits between
+// small nodes: rms_norm + mul before QKV and gate/up, flash_attn before the output projection,
+// rope + set_rows after QKV, swiglu after gate/up, add after the output and down projections. For
+// one token these nodes are latency, not bandwidth, so they move into the GEMV:
+//
+//   prologue (every workgroup, into LDS)        epilogue (per row pair)
+//   PRO_PLAIN  Q8_0 of x                        EPI_STORE    y = W x (+ res)
+//   PRO_NORM   Q8_0 of rms_norm(x) * w          EPI_ROPE_KV  NEOX rope of q and k, q -> f32,
+//   PRO_MERGE  Q8_0 of the merged split-K                    k and v -> f16 KV cache at pos
+//              attention partials               EPI_SWIGLU   y[j] = silu(g_j) * u_j
+//
+// Every value is computed with the same operations, in the same order, as the separate kernels
+// (rmsnorm_q8_row / k_merge_q8 / k_rope_kv / k_swiglu_q8 and the Q8_0 activation quantizer), so
+// the fused step equals the unfused one bit for bit.
+//
+// Layout: one 1024-thread workgroup per CU (persistent). The prologue writes the row's Q8_0 codes
+// and (d, code sum) to LDS once per CU; each wavefront then walks row groups g, g + waves, ...
+// (R rows each) with the next group's weights loaded before the current group is reduced. Lane l
+// takes blocks l, l + 64, ... of its rows, so a load moves 64 x 16 B of one row.
+//
+// Row pairs: EPI_ROPE_KV expects the QKV weight packed so that group g holds the rotation pair
+// (i, i + D/2) of a q or k head, then consecutive v rows; EPI_SWIGLU expects gate row j and up row
+// j in group j (llama.hip packs them so).
+#include "gcq_common.h"
+
+#include <algorithm>
+
+namespace gcq {
+
+constexpr int kRowMaxK = 16384;  // LDS holds the row's codes: K bytes + K/32 float2
+constexpr int kMergeMax = 32;    // split-K partials the merge prologue takes
+
+__device__ __forceinline__ int dot_blk_q4_0(const uint4 w, const int4 xa, const int4 xb, int xsum) {
+    int s = 0;
+    s = sdot4((int) (w.x & 0x0F0F0F0Fu), xa.x, s);
+    s = sdot4((int) (w.y & 0x0F0F0F0Fu), xa.y, s);
+    s = sdot4((int) (w.z & 0x0F0F0F0Fu), xa.z, s);
+    s = sdot4((int) (w.w & 0x0F0F0F0Fu), xa.w, s);
+    s = sdot4((int) ((w.x >> 4) & 0x0F0F0F0Fu), xb.x, s);
+    s = sdot4((int) ((w.y >> 4) & 0x0F0F0F0Fu), xb.y, s);
+    s = sdot4((int) ((w.z >> 4) & 0x0F0F0F0Fu), xb.z, s);
+    s = sdot4((int) ((w.w >> 4) & 0x0F0F0F0Fu), xb.w, s);
+    return s - 8 * xsum;
+}
+
+__device__ __forceinline__ int dot_blk_q8_0(const uint4 wa, const uint4 wb, const int4 xa, const int4 xb) {
+    int s = 0;
+    s = sdot4((int) wa.x, xa.x, s);
+    s = sdot4((int) wa.y, xa.y, s);
+    s = sdot4((int) wa.z, xa.z, s);
+    s = sdot4((int) wa.w, xa.w, s);
+    s = sdot4((int) wb.x, xb.x, s);
+    s = sdot4((int) wb.y, xb.y, s);
+    s = sdot4((int) wb.z, xb.z, s);
+    s = sdot4((int) wb.w, xb.w, s);
+    return s;
+}
+
+// Merged attention output of 4 dims (d0..d0+3) of head h: sum_i e^(m_i - M) o_i / sum_i e^(m_i - M)
+// l_i over the splits, in split order, splits with m_i = -inf contributing nothing, 0 when none is
+// left (k_merge_q8's arithmetic). The partials of 8 splits at a time are loaded before any math.
+__device__ __forceinline__ float4 merge4(const RowArgs & a, int h, int d0) {
+    const float2 * ml = a.part_ml + (int64_t) h * a.nsplit;
+    const float * po = a.part_o + (int64_t) h * a.nsplit * a.D + d0;
+    float M = -INFINITY;
+    for (int i = 0; i < a.nsplit; i++) M = fmaxf(M, ml[i].x);
+    float L = 0.0f;
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int i0 = 0; i0 < a.nsplit; i0 += 8) {
+        float2 mi[8];
+        float4 pi[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const bool ok = i0 + j < a.nsplit;
+            mi[j] = ok ? ml[i0 + j] : make_float2(-INFINITY, 0.0f);
+            pi[j] = ok ? *reinterpret_cast<const float4 *>(po + (int64_t) (i0 + j) * a.D)
+                       : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            if (mi[j].x == -INFINITY) continue;
+            const float w = __expf(mi[j].x - M);
+            L += w * mi[j].y;
+            o.x += w * pi[j].x;
+            o.y += w * pi[j].y;
+            o.z += w * pi[j].z;
+            o.w += w * pi[j].w;
+        }
+    }
+    o.x = L == 0.0f ? 0.0f : o.x / L;
+    o.y = L == 0.0f ? 0.0f : o.y / L;
+    o.z = L == 0.0f ? 0.0f : o.z / L;
+    o.w = L == 0.0f ? 0.0f : o.w / L;
+    return o;
+}
+
+// NEOX rotation of (x0, x1) at rotation index i for position p: theta = p * theta_scale^i by
+// repeated f32 multiplication, as ggml and k_rope_kv.
+__device__ __forceinline__ void rope_pair(float x0, float x1, int p, int i, float ts, float & y0, float & y1) {
+    float theta = (float) p;
+    for (int k = 0; k < i; k++) theta *= ts;
+    const float c = cosf(theta), sn = sinf(theta);
+    y0 = x0 * c - x1 * sn;
+    y1 = x0 * sn + x1 * c;
+}
+
+template <int TYPE, int R, int NBL, int PRO, int EPI>
+__global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
+    constexpr int NT = 1024, NWV = NT / 64;
+    constexpr int CV = TYPE == T_Q4_0 ? 1 : 2;
+    constexpr bool XREG = NBL <= 2;  // activation blocks in registers, else read from LDS per use
+    constexpr bool PF = CV * NBL * R <= 8;  // next group's weights prefetched (else: registers spill)
+    static_assert(EPI == EPI_STORE || R == 2, "row-pair epilogues take two rows per group");
+    __shared__ int4 lc[kRowMaxK / 16];
+    __shared__ float2 lm[kRowMaxK / 32];
+    __shared__ double red[NWV];
+
+    const int lane = threadIdx.x & 63;
+    const int nw = gridDim.x * NWV;
+    const int ng = (a.N + R - 1) / R;
+    const int nb = a.nb;
+    const int K = nb * QK;
+    const uint4 * qs = reinterpret_cast<const uint4 *>(a.wqs);
+
+    uint4 w[NBL][R][CV];
+    float d[NBL][R];
+    auto load = [&](int g, uint4 (&wv)[NBL][R][CV], float (&dv)[NBL][R]) {
+#pragma unroll
+        for (int i = 0; i < NBL; i++) {
+            const int blk = lane + 64 * i;
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const int row = min(g * R + r, a.N - 1);
+                if (blk < nb) {
+                    const size_t o = (size_t) row * nb + blk;
+#pragma unroll
+                    for (int c = 0; c < CV; c++) wv[i][r][c] = qs[o * CV + c];
+                    dv[i][r] = h2f(a.wd[o]);
+                }
+            }
+        }
+    };
+
+    int g = blockIdx.x * NWV + (threadIdx.x >> 6);
+    if (g < ng) load(g, w, d);  // the first weights are in flight during the prologue
+
+    // ---- prologue: the row, 4 values per thread per pass of 4096, into LDS as Q8_0
+    {
+        constexpr int PASSES = kRowMaxK / (4 * NT);
+        float4 v[PASSES], nwv[PASSES];
+#pragma unroll
+        for (int p = 0; p < PASSES; p++) {  // x and the norm weight in one round trip
+            const int e = (p * NT + threadIdx.x) * 4;
+            v[p] = make_float4(0.f, 0.f, 0.f, 0.f);
+            nwv[p] = v[p];
+            if (e < K) {
+                if constexpr (PRO == PRO_MERGE) v[p] = merge4(a, e / a.D, e % a.D);
+                else v[p] = *reinterpret_cast<const float4 *>(a.x + e);
+                if constexpr (PRO == PRO_NORM) nwv[p] = *reinterpret_cast<const float4 *>(a.norm_w + e);
+            }
+        }
+        if constexpr (PRO == PRO_NORM) {
+            double ss = 0.0;
+#pragma unroll
+            for (int p = 0; p < PASSES; p++)
+                ss += (double) (v[p].x * v[p].x) + (double) (v[p].y * v[p].y) + (double) (v[p].z * v[p].z) +
+                      (double) (v[p].w * v[p].w);
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+            if (lane == 0) red[threadIdx.x >> 6] = ss;
+            __syncthreads();
+            double tot = 0.0;
+#pragma unroll
+            for (int i = 0; i < NWV; i++) tot += red[i];
+            const float scale = 1.0f / sqrtf((float) (tot / (double) K) + a.eps);
+#pragma unroll
+            for (int p = 0; p < PASSES; p++) {
+                v[p].x = (v[p].x * scale) * nwv[p].x;
+                v[p].y = (v[p].y * scale) * nwv[p].y;
+                v[p].z = (v[p].z * scale) * nwv[p].z;
+                v[p].w = (v[p].w * scale) * nwv[p].w;
+            }
+        }
+#pragma unroll
+        for (int p = 0; p < PASSES; p++) {
+            const int e = (p * NT + threadIdx.x) * 4;
+            if (e < K) q8_block_store(v[p], reinterpret_cast<int8_t *>(lc) + (e & ~31), lm + e / 32, (e / 4) & 7);
+        }
+        __syncthreads();
+    }
+
+    int4 xa[XREG ? NBL : 1], xb[XREG ? NBL : 1];
+    float2 xm[XREG ? NBL : 1];
+    if constexpr (XREG) {
+#pragma unroll
+        for (int i = 0; i < NBL; i++) {
+            const int blk = lane + 64 * i;
+            if (blk < nb) {
+                xa[i] = lc[2 * blk];
+                xb[i] = lc[2 * blk + 1];
+                xm[i] = lm[blk];
+            }
+        }
+    }
+    const int p_tok = EPI == EPI_ROPE_KV ? *a.pos : 0;
+    const int half = a.D / 2;
+
+    while (g < ng) {
+        const int gn = g + nw;
+        uint4 wn[NBL][R][CV];
+        float dn[NBL][R];
+        if (PF && gn < ng) load(gn, wn, dn);
+        float acc[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) acc[r] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NBL; i++) {
+            const int blk = lane + 64 * i;
+            if (blk >= nb) break;
+            int4 ca, cb;
+            float2 cm;
+            if constexpr (XREG) {
+                ca = xa[i];
+                cb = xb[i];
+                cm = xm[i];
+            } else {
+                ca = lc[2 * blk];
+                cb = lc[2 * blk + 1];
+                cm = lm[blk];
+            }
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                int s;
+                if constexpr (TYPE == T_Q4_0) s = dot_blk_q4_0(w[i][r][0], ca, cb, __float_as_int(cm.y));
+                else s = dot_blk_q8_0(w[i][r][0], w[i][r][CV - 1], ca, cb);
+                acc[r] += ((float) s * d[i][r]) * cm.x;
+            }
+        }
+        float v[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) v[r] = wave_sum(acc[r]);
+        if constexpr (EPI == EPI_STORE) {
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const int row = g * R + r;
+                if (lane == r && row < a.N) a.y[row] = a.res ? v[r] + a.res[row] : v[r];
+            }
+        } else if constexpr (EPI == EPI_SWIGLU) {
+            if (lane == 0) a.y[g] = v[0] / (1.0f + expf(-v[0])) * v[1];
+        } else {  // EPI_ROPE_KV
+            if (lane == 0 && p_tok >= 0 && p_tok < a.ctx) {
+                const int nqk = (a.H + a.Hkv) * half;
+                if (g < nqk) {
+                    const int h = g / half, i = g % half;
+                    float y0, y1;
+                    rope_pair(v[0], v[1], p_tok, i, a.theta_scale, y0, y1);
+                    if (h < a.H) {
+                        a.y[h * a.D + i] = y0;
+                        a.y[h * a.D + i + half] = y1;
+                    } else {
+                        uint16_t * kr = a.kc + ((int64_t) (h - a.H) * a.ctx + p_tok) * a.D;
+                        kr[i] = f2h(y0);
+                        kr[i + half] = f2h(y1);
+                    }
+                } else {
+                    const int e = 2 * (g - nqk);  // v value index over [Hkv][D]
+                    const int hv = e / a.D, dd = e % a.D;
+                    const uint32_t pair = f2h(v[0]) | ((uint32_t) f2h(v[1]) << 16);
+                    *reinterpret_cast<uint32_t *>(a.vc + ((int64_t) hv * a.ctx + p_tok) * a.D + dd) = pair;
+                }
+            }
+        }
+        if constexpr (PF) {
+#pragma unroll
+            for (int i = 0; i < NBL; i++)
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+#pragma unroll
+                    for (int c = 0; c < CV; c++) w[i][r][c] = wn[i][r][c];
+                    d[i][r] = dn[i][r];
+                }
+        } else if (gn < ng) {
+            load(gn, w, d);
+        }
+        g = gn;
+    }
+}
+
+// ------------------------------------------------------------------------------ dispatch
+
+int cu_count();
+
+namespace {
+
+template <int TYPE, int R, int NBL, int PRO, int EPI>
+void go(const RowArgs & a, unsigned grid, hipStream_t s) {
+    k_row_gemv<TYPE, R, NBL, PRO, EPI><<<grid, 1024, 0, s>>>(a);
+}
+
+// Two rows per group when there are enough groups to give every wavefront of the grid one and
+// their weights fit the registers (K <= 4096), else one row per group; the row-pair epilogues
+// always take two. Long rows (K > 4096): lanes hold up to 8 blocks of a row.
+template <int TYPE, int PRO, int EPI>
+void run_row_r(const RowArgs & a, hipStream_t s) {
+    const int nbl = (a.nb + 63) / 64;
+    const int waves = cu_count() * 16;
+    const int R = EPI != EPI_STORE || (nbl <= 2 && a.N / 2 >= waves) ? 2 : 1;
+    const int ng = (a.N + R - 1) / R;
+    const unsigned grid = (unsigned) std::max(1, std::min((ng + 15) / 16, cu_count()));
+    if (R == 2) {
+        if (nbl == 1) return go<TYPE, 2, 1, PRO, EPI>(a, grid, s);
+        if (nbl == 2) return go<TYPE, 2, 2, PRO, EPI>(a, grid, s);
+    } else if constexpr (EPI == EPI_STORE) {
+        switch (nbl) {
+            case 1: return go<TYPE, 1, 1, PRO, EPI>(a, grid, s);
+            case 2: return go<TYPE, 1, 2, PRO, EPI>(a, grid, s);
+            case 3: return go<TYPE, 1, 3, PRO, EPI>(a, grid, s);
+            case 4: return go<TYPE, 1, 4, PRO, EPI>(a, grid, s);
+            case 5: return go<TYPE, 1, 5, PRO, EPI>(a, grid, s);
+            case 6: return go<TYPE, 1, 6, PRO, EPI>(a, grid, s);
+            case 7: return go<TYPE, 1, 7, PRO, EPI>(a, grid, s);
+            case 8: return go<TYPE, 1, 8, PRO, EPI>(a, grid, s);
+            default: break;
+        }
+    }
+    fail("row gemv: K = " + std::to_string(a.nb * QK) + " not supported by this epilogue");
+}
+
+template <int TYPE>
+void run_row_t(int pro, int epi, const RowArgs & a, hipStream_t s) {
+#define GCQ_PE(P, E)                                  \
+    if (pro == P && epi == E) return run_row_r<TYPE, P, E>(a, s);
+    GCQ_PE(PRO_PLAIN, EPI_STORE) GCQ_PE(PRO_NORM, EPI_STORE) GCQ_PE(PRO_MERGE, EPI_STORE)
+    GCQ_PE(PRO_NORM, EPI_ROPE_KV) GCQ_PE(PRO_NORM, EPI_SWIGLU)
+#undef GCQ_PE
+    fail("row gemv: unsupported prologue / epilogue pair");
+}
+
+}  // namespace
+
+bool row_gemv_fits(int type, int64_t K) {
+    return (type == T_Q4_0 || type == T_Q8_0) && K % QK == 0 && K > 0 && K <= kRowMaxK;
+}
+
+int row_gemv_merge_max() { return kMergeMax; }
+
+void launch_row_gemv(int type, int pro, int epi, const RowArgs & a, hipStream_t s) {
+    require(row_gemv_fits(type, (int64_t) a.nb * QK), "row gemv: weight type or K not supported");
+    require(epi == EPI_STORE || a.N % 2 == 0, "row gemv: row-pair epilogue needs an even row count");
+    require(pro != PRO_MERGE || (a.nsplit >= 1 && a.nsplit <= kMergeMax && a.D % 4 == 0),
+            "row gemv: merge of 1.." + std::to_string(kMergeMax) + " splits");
+    if (type == T_Q4_0) run_row_t<T_Q4_0>(pro, epi, a, s);
+    else run_row_t<T_Q8_0>(pro, epi, a, s);
+    check_launch("row gemv");
+}
+
+}  // namespace gcq

@@ -113,9 +113,9 @@ GCQ_API int gcq_rms_norm(const float * x, int64_t ldx, float * y, int64_t ldy, c
 /* One row x [K]: ggml_rms_norm (eps) -> ggml_mul by the norm weight norm_w [K] -> ggml_mul_mat by
  * the packed Q4_0 / Q8_0 weight w [N][K], the three nodes every decoder layer feeds its QKV and
  * gate/up projections with (ggml_compiler/llm.py:369-373, 421-425), into y [N] (y = res + W x' when
- * res is given). For K <= 4096 one launch: the GEMV workgroups normalize and quantize x themselves
- * (ws unused, may be NULL); otherwise gcq_rms_norm_q8 into ws (gcq_mul_mat_workspace(wtype, 1, K)
- * bytes) then the GEMV. y equals gcq_rms_norm_q8 + gcq_mul_mat_q bit for bit; with norm_w NULL
+ * res is given). For K <= 16384 one launch: the GEMV workgroups normalize and quantize x
+ * themselves (ws unused, may be NULL); otherwise gcq_rms_norm_q8 into ws
+ * (gcq_mul_mat_workspace(wtype, 1, K) bytes) then the GEMV. y equals gcq_rms_norm_q8 + gcq_mul_mat_q bit for bit; with norm_w NULL
  * the norm is skipped and y equals gcq_mul_mat's. */
 GCQ_API int gcq_rms_norm_mul_mat(int wtype, const void * w, int64_t N, int64_t K, const float * x, const float * norm_w,
                                  float eps, float * y, const float * res, void * ws, size_t ws_size, void * stream);

@@ -50,13 +50,14 @@ def test_mul_mat_q_with_residual(gops, orc, t, B, N, K):
 
 
 @pytest.mark.parametrize("t", ["q4_0", "q8_0"])
-@pytest.mark.parametrize("N,K", [(5, 256), (6144, 4096), (40000, 4096), (300, 14336)])
+@pytest.mark.parametrize("N,K", [(5, 256), (6144, 4096), (40000, 4096), (4096, 14336), (64, 16384 + 512)])
 @pytest.mark.parametrize("norm", [True, False])
 def test_rms_norm_mul_mat_equals_separate_launches(gops, orc, t, N, K, norm):
-    """gcq_rms_norm_mul_mat (one launch for K <= 4096: the GEMV normalizes and quantizes its row)
+    """gcq_rms_norm_mul_mat (one launch for K <= 16384: the GEMV normalizes and quantizes its row)
     equals gcq_rms_norm_q8 (or gcq_quantize_act) + gcq_mul_mat_q bit for bit, with and without a
     residual, and is within 1e-3 of the oracle's rms_norm -> mul -> mul_mat. N=5 leaves most
-    wavefronts without rows; N=40000 walks several row groups per wavefront; K=14336 takes the
+    wavefronts without rows; N=40000 walks several row groups per wavefront; K=14336 is the down
+    projection's shape (one row per wavefront, activation read from LDS); K=16896 takes the
     two-launch path."""
     raw = orc.quantize(orc.normal((N, K), seed=76, std=0.02), t)
     qw = gops.QuantWeight.from_ggml(torch.from_numpy(raw), t, K)
