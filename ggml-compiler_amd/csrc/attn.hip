@@ -234,7 +234,7 @@ __global__ __launch_bounds__(NW * 64) void k_attn_decode(const float * __restric
                                                          const uint16_t * __restrict__ k, int64_t k_h, int64_t k_j,
                                                          const uint16_t * __restrict__ v, int64_t v_h, int64_t v_j,
                                                          float scale, int n_kv, const int * __restrict__ n_kv_dev,
-                                                         int nsplit, float * __restrict__ out,
+                                                         int chunk, int kv_rows, int nsplit, float * __restrict__ out,
                                                          float * __restrict__ part_o, float2 * __restrict__ part_ml) {
     constexpr int LPK = D / 8;     // lanes per key row
     constexpr int KPW = 64 / LPK;  // lane groups (keys per step) per wavefront
@@ -244,15 +244,17 @@ __global__ __launch_bounds__(NW * 64) void k_attn_decode(const float * __restric
     __shared__ float so[NW][G * D];
     __shared__ float2 sml[NW][G];
 
+    // Split and wavefront ranges come from the host's chunk, so the K/V addresses do not wait for
+    // the KV length read from the device; rows are clamped into the kv_rows that exist and keys
+    // at or past n_kv are masked.
     if (n_kv_dev) n_kv = *n_kv_dev;
     const int split = blockIdx.x, hk = blockIdx.y;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int sub = lane % LPK, slot = lane / LPK;
-    const int chunk = (n_kv + nsplit - 1) / nsplit;
     const int j0 = split * chunk;
-    const int len = max(0, min(n_kv, j0 + chunk) - j0);
-    const int per_wave = (len + NW - 1) / NW;
-    const int w0 = min(len, wave * per_wave), w1 = min(len, w0 + per_wave);
+    const int per_wave = (chunk + NW - 1) / NW;
+    const int w0 = min(chunk, wave * per_wave), w1 = min(chunk, w0 + per_wave);
+    const int len = max(0, min(n_kv - j0, chunk));  // keys of this split below n_kv
 
     half2_t qh[G][4];
 #pragma unroll
@@ -274,16 +276,15 @@ __global__ __launch_bounds__(NW * 64) void k_attn_decode(const float * __restric
 #pragma unroll
         for (int c = 0; c < 8; c++) acc[g][c] = 0.0f;
     }
-    const uint16_t * kb = k + (int64_t) hk * k_h + (int64_t) j0 * k_j + 8 * sub;
-    const uint16_t * vb = v + (int64_t) hk * v_h + (int64_t) j0 * v_j + 8 * sub;
+    const uint16_t * kb = k + (int64_t) hk * k_h + 8 * sub;
+    const uint16_t * vb = v + (int64_t) hk * v_h + 8 * sub;
     for (int base = w0; base < w1; base += NB * KPW) {
         uint4 kr[NB], vr[NB];
 #pragma unroll
         for (int b = 0; b < NB; b++) {
-            const int jj = base + b * KPW + slot;
-            const bool ok = jj < w1;
-            kr[b] = ok ? *reinterpret_cast<const uint4 *>(kb + (int64_t) jj * k_j) : make_uint4(0, 0, 0, 0);
-            vr[b] = ok ? *reinterpret_cast<const uint4 *>(vb + (int64_t) jj * v_j) : make_uint4(0, 0, 0, 0);
+            const int64_t row = min(j0 + base + b * KPW + slot, kv_rows - 1);
+            kr[b] = *reinterpret_cast<const uint4 *>(kb + row * k_j);
+            vr[b] = *reinterpret_cast<const uint4 *>(vb + row * v_j);
         }
 #pragma unroll
         for (int g = 0; g < G; g++) {
@@ -298,7 +299,8 @@ __global__ __launch_bounds__(NW * 64) void k_attn_decode(const float * __restric
                 a = __builtin_amdgcn_fdot2(as_h2(kr[b].w), qh[g][3], a, false);
 #pragma unroll
                 for (int o = LPK / 2; o > 0; o >>= 1) a += __shfl_xor(a, o, 64);
-                sc[b] = base + b * KPW + slot < w1 ? a * scale : -INFINITY;
+                const int jj = base + b * KPW + slot;
+                sc[b] = jj < w1 && jj < len ? a * scale : -INFINITY;
                 bm = fmaxf(bm, sc[b]);
             }
             const float mn = fmaxf(m[g], bm);
@@ -432,17 +434,21 @@ AttnPlan attn_plan_decode(int D, int G, int max_ctx, int max_split) {
 bool attn_decode_fits(int D, int G) { return (D == 64 || D == 128) && (G == 1 || G == 2 || G == 4); }
 
 // out [H*D] (one split) or part_o / part_ml (several), q [H][D] at head stride q_h.
+// chunk: keys per split (nsplit * chunk >= n_kv); kv_rows: rows the K and V buffers hold per head.
 void launch_attn_decode(const float * q, int64_t q_h, const void * k, int64_t k_h, int64_t k_j, const void * v,
                         int64_t v_h, int64_t v_j, int D, int H, int Hkv, int n_kv, const int * n_kv_dev, float scale,
-                        int nsplit, float * out, float * part_o, float2 * part_ml, hipStream_t s) {
+                        int nsplit, int chunk, int kv_rows, float * out, float * part_o, float2 * part_ml,
+                        hipStream_t s) {
     const int G = H / Hkv;
     require(attn_decode_fits(D, G) && H % Hkv == 0, "attn decode: D 64 / 128 and 1, 2 or 4 query heads per KV head");
+    require(kv_rows >= 1 && chunk >= 1 && (int64_t) nsplit * chunk >= (n_kv_dev ? kv_rows : n_kv),
+            "attn decode: the splits must cover the keys");
     const dim3 grid((unsigned) nsplit, (unsigned) Hkv);
     const uint16_t *kp = (const uint16_t *) k, *vp = (const uint16_t *) v;
 #define GCQ_AD(DD, GG)                                                                                          \
     if (D == DD && G == GG)                                                                                     \
         k_attn_decode<DD, GG, decode_waves(GG)><<<grid, decode_waves(GG) * 64, 0, s>>>(                         \
-            q, q_h, kp, k_h, k_j, vp, v_h, v_j, scale, n_kv, n_kv_dev, nsplit, out, part_o, part_ml);
+            q, q_h, kp, k_h, k_j, vp, v_h, v_j, scale, n_kv, n_kv_dev, chunk, kv_rows, nsplit, out, part_o, part_ml);
     GCQ_AD(64, 1) GCQ_AD(64, 2) GCQ_AD(64, 4) GCQ_AD(128, 1) GCQ_AD(128, 2) GCQ_AD(128, 4)
 #undef GCQ_AD
     check_launch("attn decode");
@@ -509,8 +515,8 @@ void launch_flash_attn(const float * q, int64_t q_h, int64_t q_s, const void * k
         // One query row, every key visible: the one-pass decode kernel (fewer splits than p, so the
         // workspace holds its partials).
         const int nsplit = decode_splits(D, H / Hkv, n_kv, p.nsplit);
-        launch_attn_decode(q, q_h, k, k_h, k_j, v, v_h, v_j, D, H, Hkv, n_kv, nullptr, scale, nsplit, out, po, pml,
-                           s);
+        launch_attn_decode(q, q_h, k, k_h, k_j, v, v_h, v_j, D, H, Hkv, n_kv, nullptr, scale, nsplit,
+                           (n_kv + nsplit - 1) / nsplit, n_kv, out, po, pml, s);
         if (nsplit == 1) return;
         if (D == 64) k_attn_merge<64><<<(unsigned) H, 64, 0, s>>>(po, pml, out, nsplit);
         else k_attn_merge<128><<<(unsigned) H, 128, 0, s>>>(po, pml, out, nsplit);

@@ -94,7 +94,7 @@ __global__ __launch_bounds__(256) void k_gemv_q0(const uint8_t * __restrict__ wq
 
     for (int base = 0; base < nb; base += 64 * NBL) {
         uint4 w[NBL][R][CV];
-        float d[NBL][R];
+        uint32_t d[NBL][R];  // raw fp16 scale bits, one per register: converted where used, so no load waits
 #pragma unroll
         for (int i = 0; i < NBL; i++) {
             const int blk = base + lane + 64 * i;
@@ -105,7 +105,7 @@ __global__ __launch_bounds__(256) void k_gemv_q0(const uint8_t * __restrict__ wq
                     const size_t o = (size_t) row * nb + blk;
 #pragma unroll
                     for (int c = 0; c < CV; c++) w[i][r][c] = qs[o * CV + c];
-                    d[i][r] = h2f(wd[o]);
+                    d[i][r] = wd[o];
                 }
             }
         }
@@ -123,7 +123,7 @@ __global__ __launch_bounds__(256) void k_gemv_q0(const uint8_t * __restrict__ wq
                     int s;
                     if constexpr (TYPE == T_Q4_0) s = dot_q4_0(w[i][r][0], xa, xb, __float_as_int(m.y));
                     else s = dot_q8_0(w[i][r][0], w[i][r][CV - 1], xa, xb);
-                    acc[r][b] += ((float) s * d[i][r]) * m.x;
+                    acc[r][b] += ((float) s * h2f((uint16_t) d[i][r])) * m.x;
                 }
             }
         }
@@ -157,20 +157,18 @@ __global__ __launch_bounds__(256) void k_gemv_p(const uint8_t * __restrict__ wqs
     const uint4 * qs = reinterpret_cast<const uint4 *>(wqs);
 
     uint4 w[NBL][R][CV];
-    float d[NBL][R];
-    auto load = [&](int g, uint4 (&wv)[NBL][R][CV], float (&dv)[NBL][R]) {
+    uint32_t d[NBL][R];  // raw fp16 scale bits, one per register: converted where used, so no load waits
+    auto load = [&](int g, uint4 (&wv)[NBL][R][CV], uint32_t (&dv)[NBL][R]) {
 #pragma unroll
         for (int i = 0; i < NBL; i++) {
-            const int blk = lane + 64 * i;
+            const int blk = min(lane + 64 * i, nb - 1);  // lanes past the row reload its last block, unused
 #pragma unroll
             for (int r = 0; r < R; r++) {
                 const int row = min(g * R + r, N - 1);
-                if (blk < nb) {
-                    const size_t o = (size_t) row * nb + blk;
+                const size_t o = (size_t) row * nb + blk;
 #pragma unroll
-                    for (int c = 0; c < CV; c++) wv[i][r][c] = qs[o * CV + c];
-                    dv[i][r] = h2f(wd[o]);
-                }
+                for (int c = 0; c < CV; c++) wv[i][r][c] = qs[o * CV + c];
+                dv[i][r] = wd[o];
             }
         }
     };
@@ -197,7 +195,7 @@ __global__ __launch_bounds__(256) void k_gemv_p(const uint8_t * __restrict__ wqs
     while (g < ng) {
         const int gn = g + nw;
         uint4 wn[NBL][R][CV];
-        float dn[NBL][R];
+        uint32_t dn[NBL][R];
         if (gn < ng) load(gn, wn, dn);
         float acc[R][B];
 #pragma unroll
@@ -214,7 +212,7 @@ __global__ __launch_bounds__(256) void k_gemv_p(const uint8_t * __restrict__ wqs
                     int s;
                     if constexpr (TYPE == T_Q4_0) s = dot_q4_0(w[i][r][0], xa[i][b], xb[i][b], __float_as_int(xmv[i][b].y));
                     else s = dot_q8_0(w[i][r][0], w[i][r][CV - 1], xa[i][b], xb[i][b]);
-                    acc[r][b] += ((float) s * d[i][r]) * xmv[i][b].x;
+                    acc[r][b] += ((float) s * h2f((uint16_t) d[i][r])) * xmv[i][b].x;
                 }
             }
         }

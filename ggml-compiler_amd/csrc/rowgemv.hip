@@ -10,7 +10,7 @@
 //   PRO_PLAIN  Q8_0 of x                        EPI_STORE    y = W x (+ res)
 //   PRO_NORM   Q8_0 of rms_norm(x) * w          EPI_ROPE_KV  NEOX rope of q and k, q -> f32,
 //   PRO_MERGE  Q8_0 of the merged split-K                    k and v -> f16 KV cache at pos
-//              attention partials               EPI_SWIGLU   y[j] = silu(g_j) * u_j
+//              attention partials (<= 8)        EPI_SWIGLU   y[j] = silu(g_j) * u_j
 //
 // Every value is computed with the same operations, in the same order, as the separate kernels
 // (rmsnorm_q8_row / k_merge_q8 / k_rope_kv / k_swiglu_q8 and the Q8_0 activation quantizer), so
@@ -31,7 +31,7 @@
 namespace gcq {
 
 constexpr int kRowMaxK = 16384;  // LDS holds the row's codes: K bytes + K/32 float2
-constexpr int kMergeMax = 32;    // split-K partials the merge prologue takes
+constexpr int kMergeMax = 8;     // split-K partials the merge prologue takes (held in registers)
 
 __device__ __forceinline__ int dot_blk_q4_0(const uint4 w, const int4 xa, const int4 xb, int xsum) {
     int s = 0;
@@ -59,44 +59,6 @@ __device__ __forceinline__ int dot_blk_q8_0(const uint4 wa, const uint4 wb, cons
     return s;
 }
 
-// Merged attention output of 4 dims (d0..d0+3) of head h: sum_i e^(m_i - M) o_i / sum_i e^(m_i - M)
-// l_i over the splits, in split order, splits with m_i = -inf contributing nothing, 0 when none is
-// left (k_merge_q8's arithmetic). The partials of 8 splits at a time are loaded before any math.
-__device__ __forceinline__ float4 merge4(const RowArgs & a, int h, int d0) {
-    const float2 * ml = a.part_ml + (int64_t) h * a.nsplit;
-    const float * po = a.part_o + (int64_t) h * a.nsplit * a.D + d0;
-    float M = -INFINITY;
-    for (int i = 0; i < a.nsplit; i++) M = fmaxf(M, ml[i].x);
-    float L = 0.0f;
-    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int i0 = 0; i0 < a.nsplit; i0 += 8) {
-        float2 mi[8];
-        float4 pi[8];
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const bool ok = i0 + j < a.nsplit;
-            mi[j] = ok ? ml[i0 + j] : make_float2(-INFINITY, 0.0f);
-            pi[j] = ok ? *reinterpret_cast<const float4 *>(po + (int64_t) (i0 + j) * a.D)
-                       : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            if (mi[j].x == -INFINITY) continue;
-            const float w = __expf(mi[j].x - M);
-            L += w * mi[j].y;
-            o.x += w * pi[j].x;
-            o.y += w * pi[j].y;
-            o.z += w * pi[j].z;
-            o.w += w * pi[j].w;
-        }
-    }
-    o.x = L == 0.0f ? 0.0f : o.x / L;
-    o.y = L == 0.0f ? 0.0f : o.y / L;
-    o.z = L == 0.0f ? 0.0f : o.z / L;
-    o.w = L == 0.0f ? 0.0f : o.w / L;
-    return o;
-}
-
 // NEOX rotation of (x0, x1) at rotation index i for position p: theta = p * theta_scale^i by
 // repeated f32 multiplication, as ggml and k_rope_kv.
 __device__ __forceinline__ void rope_pair(float x0, float x1, int p, int i, float ts, float & y0, float & y1) {
@@ -113,6 +75,8 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
     constexpr int CV = TYPE == T_Q4_0 ? 1 : 2;
     constexpr bool XREG = NBL <= 2;  // activation blocks in registers, else read from LDS per use
     constexpr bool PF = CV * NBL * R <= 8;  // next group's weights prefetched (else: registers spill)
+    // ... and issued before the prologue when the registers hold both groups and the prologue's data
+    constexpr bool PF_EARLY = PF && CV * NBL * R <= 4 && PRO != PRO_MERGE;
     static_assert(EPI == EPI_STORE || R == 2, "row-pair epilogues take two rows per group");
     __shared__ int4 lc[kRowMaxK / 16];
     __shared__ float2 lm[kRowMaxK / 32];
@@ -126,42 +90,97 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
     const uint4 * qs = reinterpret_cast<const uint4 *>(a.wqs);
 
     uint4 w[NBL][R][CV];
-    float d[NBL][R];
-    auto load = [&](int g, uint4 (&wv)[NBL][R][CV], float (&dv)[NBL][R]) {
+    uint32_t d[NBL][R];  // raw fp16 scale bits, one per register: converted where used, so no load waits
+    auto load = [&](int g, uint4 (&wv)[NBL][R][CV], uint32_t (&dv)[NBL][R]) {
 #pragma unroll
         for (int i = 0; i < NBL; i++) {
-            const int blk = lane + 64 * i;
+            const int blk = min(lane + 64 * i, nb - 1);  // lanes past the row reload its last block, unused
 #pragma unroll
             for (int r = 0; r < R; r++) {
                 const int row = min(g * R + r, a.N - 1);
-                if (blk < nb) {
-                    const size_t o = (size_t) row * nb + blk;
+                const size_t o = (size_t) row * nb + blk;
 #pragma unroll
-                    for (int c = 0; c < CV; c++) wv[i][r][c] = qs[o * CV + c];
-                    dv[i][r] = h2f(a.wd[o]);
-                }
+                for (int c = 0; c < CV; c++) wv[i][r][c] = qs[o * CV + c];
+                dv[i][r] = a.wd[o];
             }
         }
     };
 
     int g = blockIdx.x * NWV + (threadIdx.x >> 6);
-    if (g < ng) load(g, w, d);  // the first weights are in flight during the prologue
+
+    // Order of issue matters: a wavefront's vector loads complete in order, so the prologue's
+    // loads go first and the weights after them; the prologue then waits for its own data only,
+    // while the first two row groups' weights stream in.
+    constexpr int PASSES = (NBL * 64 * QK + 4 * NT - 1) / (4 * NT);  // K <= 64 * NBL * 32
+    constexpr bool MERGE = PRO == PRO_MERGE;  // one pass (K <= 4096), up to kMergeMax splits
+    float4 v[PASSES], nwv[PASSES];
+    float2 mlv[MERGE ? kMergeMax : 1];
+    float4 pov[MERGE ? kMergeMax : 1];
+    // Every load below is unconditional (addresses clamped into range, values past the end
+    // discarded afterwards), so the compiler knows how many are in flight and waits for the
+    // oldest only.
+#pragma unroll
+    for (int p = 0; p < PASSES; p++) {
+        const int e = min((p * NT + (int) threadIdx.x) * 4, K - 4);
+        if constexpr (PRO != PRO_MERGE) v[p] = *reinterpret_cast<const float4 *>(a.x + e);
+        if constexpr (PRO == PRO_NORM) nwv[p] = *reinterpret_cast<const float4 *>(a.norm_w + e);
+    }
+    if constexpr (MERGE) {
+        const int e = min((int) threadIdx.x * 4, K - 4);
+        const int h = e / a.D;
+        const float2 * ml = a.part_ml + (int64_t) h * a.nsplit;
+        const float * po = a.part_o + (int64_t) h * a.nsplit * a.D + e % a.D;
+#pragma unroll
+        for (int j = 0; j < kMergeMax; j++) {
+            const int jc = min(j, a.nsplit - 1);
+            mlv[j] = ml[jc];
+            pov[j] = *reinterpret_cast<const float4 *>(po + (int64_t) jc * a.D);
+        }
+#pragma unroll
+        for (int j = 0; j < kMergeMax; j++)
+            if (j >= a.nsplit) mlv[j] = make_float2(-INFINITY, 0.0f);  // splits past the last: none
+    }
+    const int p_tok = EPI == EPI_ROPE_KV ? *a.pos : 0;
+    __builtin_amdgcn_sched_barrier(0);  // keep the prologue's loads ahead of the weights'
+
+    uint4 wn[NBL][R][CV];
+    uint32_t dn[NBL][R];
+    load(min(g, ng - 1), w, d);  // waves past the last group load it again and never use it
+    if constexpr (PF_EARLY) load(min(g + nw, ng - 1), wn, dn);
 
     // ---- prologue: the row, 4 values per thread per pass of 4096, into LDS as Q8_0
     {
-        constexpr int PASSES = kRowMaxK / (4 * NT);
-        float4 v[PASSES], nwv[PASSES];
-#pragma unroll
-        for (int p = 0; p < PASSES; p++) {  // x and the norm weight in one round trip
-            const int e = (p * NT + threadIdx.x) * 4;
-            v[p] = make_float4(0.f, 0.f, 0.f, 0.f);
-            nwv[p] = v[p];
+        if constexpr (MERGE) {
+            // The merged attention output (k_merge_q8's arithmetic): sum_i e^(m_i - M) o_i /
+            // sum_i e^(m_i - M) l_i in split order, splits with m_i = -inf left out, 0 if none.
+            const int e = threadIdx.x * 4;
             if (e < K) {
-                if constexpr (PRO == PRO_MERGE) v[p] = merge4(a, e / a.D, e % a.D);
-                else v[p] = *reinterpret_cast<const float4 *>(a.x + e);
-                if constexpr (PRO == PRO_NORM) nwv[p] = *reinterpret_cast<const float4 *>(a.norm_w + e);
+                float M = -INFINITY;
+#pragma unroll
+                for (int j = 0; j < kMergeMax; j++) M = fmaxf(M, mlv[j].x);
+                float L = 0.0f;
+                float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (M != -INFINITY) {
+#pragma unroll
+                    for (int j = 0; j < kMergeMax; j++) {
+                        if (mlv[j].x == -INFINITY) continue;
+                        const float wj = __expf(mlv[j].x - M);
+                        L += wj * mlv[j].y;
+                        o.x += wj * pov[j].x;
+                        o.y += wj * pov[j].y;
+                        o.z += wj * pov[j].z;
+                        o.w += wj * pov[j].w;
+                    }
+                }
+                v[0].x = L == 0.0f ? 0.0f : o.x / L;
+                v[0].y = L == 0.0f ? 0.0f : o.y / L;
+                v[0].z = L == 0.0f ? 0.0f : o.z / L;
+                v[0].w = L == 0.0f ? 0.0f : o.w / L;
             }
         }
+#pragma unroll
+        for (int p = 0; p < PASSES; p++)
+            if ((p * NT + (int) threadIdx.x) * 4 >= K) v[p] = make_float4(0.f, 0.f, 0.f, 0.f);
         if constexpr (PRO == PRO_NORM) {
             double ss = 0.0;
 #pragma unroll
@@ -185,12 +204,13 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
             }
         }
 #pragma unroll
-        for (int p = 0; p < PASSES; p++) {
+        for (int p = 0; p < (MERGE ? 1 : PASSES); p++) {
             const int e = (p * NT + threadIdx.x) * 4;
             if (e < K) q8_block_store(v[p], reinterpret_cast<int8_t *>(lc) + (e & ~31), lm + e / 32, (e / 4) & 7);
         }
         __syncthreads();
     }
+    if constexpr (PF && !PF_EARLY) load(min(g + nw, ng - 1), wn, dn);
 
     int4 xa[XREG ? NBL : 1], xb[XREG ? NBL : 1];
     float2 xm[XREG ? NBL : 1];
@@ -205,14 +225,10 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
             }
         }
     }
-    const int p_tok = EPI == EPI_ROPE_KV ? *a.pos : 0;
     const int half = a.D / 2;
 
-    while (g < ng) {
-        const int gn = g + nw;
-        uint4 wn[NBL][R][CV];
-        float dn[NBL][R];
-        if (PF && gn < ng) load(gn, wn, dn);
+    // One row group: block dots, the row sums, the epilogue.
+    auto group = [&](int gg, const uint4 (&wv)[NBL][R][CV], const uint32_t (&dv)[NBL][R]) {
         float acc[R];
 #pragma unroll
         for (int r = 0; r < R; r++) acc[r] = 0.0f;
@@ -233,10 +249,10 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
             }
 #pragma unroll
             for (int r = 0; r < R; r++) {
-                int s;
-                if constexpr (TYPE == T_Q4_0) s = dot_blk_q4_0(w[i][r][0], ca, cb, __float_as_int(cm.y));
-                else s = dot_blk_q8_0(w[i][r][0], w[i][r][CV - 1], ca, cb);
-                acc[r] += ((float) s * d[i][r]) * cm.x;
+                int sdot;
+                if constexpr (TYPE == T_Q4_0) sdot = dot_blk_q4_0(wv[i][r][0], ca, cb, __float_as_int(cm.y));
+                else sdot = dot_blk_q8_0(wv[i][r][0], wv[i][r][CV - 1], ca, cb);
+                acc[r] += ((float) sdot * h2f((uint16_t) dv[i][r])) * cm.x;
             }
         }
         float v[R];
@@ -245,16 +261,16 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
         if constexpr (EPI == EPI_STORE) {
 #pragma unroll
             for (int r = 0; r < R; r++) {
-                const int row = g * R + r;
+                const int row = gg * R + r;
                 if (lane == r && row < a.N) a.y[row] = a.res ? v[r] + a.res[row] : v[r];
             }
         } else if constexpr (EPI == EPI_SWIGLU) {
-            if (lane == 0) a.y[g] = v[0] / (1.0f + expf(-v[0])) * v[1];
+            if (lane == 0) a.y[gg] = v[0] / (1.0f + expf(-v[0])) * v[1];
         } else {  // EPI_ROPE_KV
             if (lane == 0 && p_tok >= 0 && p_tok < a.ctx) {
                 const int nqk = (a.H + a.Hkv) * half;
-                if (g < nqk) {
-                    const int h = g / half, i = g % half;
+                if (gg < nqk) {
+                    const int h = gg / half, i = gg % half;
                     float y0, y1;
                     rope_pair(v[0], v[1], p_tok, i, a.theta_scale, y0, y1);
                     if (h < a.H) {
@@ -266,26 +282,33 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
                         kr[i + half] = f2h(y1);
                     }
                 } else {
-                    const int e = 2 * (g - nqk);  // v value index over [Hkv][D]
+                    const int e = 2 * (gg - nqk);  // v value index over [Hkv][D]
                     const int hv = e / a.D, dd = e % a.D;
                     const uint32_t pair = f2h(v[0]) | ((uint32_t) f2h(v[1]) << 16);
                     *reinterpret_cast<uint32_t *>(a.vc + ((int64_t) hv * a.ctx + p_tok) * a.D + dd) = pair;
                 }
             }
         }
-        if constexpr (PF) {
-#pragma unroll
-            for (int i = 0; i < NBL; i++)
-#pragma unroll
-                for (int r = 0; r < R; r++) {
-#pragma unroll
-                    for (int c = 0; c < CV; c++) w[i][r][c] = wn[i][r][c];
-                    d[i][r] = dn[i][r];
-                }
-        } else if (gn < ng) {
-            load(gn, w, d);
+    };
+
+    if constexpr (PF) {
+        // Two buffers in turn (w: groups g, g + 2 waves, ...; wn: the ones between), so a group's
+        // weights are loaded two groups ahead and never copied between registers.
+        while (g < ng) {
+            group(g, w, d);
+            load(min(g + 2 * nw, ng - 1), w, d);
+            g += nw;
+            if (g >= ng) break;
+            group(g, wn, dn);
+            load(min(g + 2 * nw, ng - 1), wn, dn);
+            g += nw;
         }
-        g = gn;
+    } else {
+        while (g < ng) {
+            group(g, w, d);
+            g += nw;
+            if (g < ng) load(g, w, d);
+        }
     }
 }
 
@@ -313,6 +336,9 @@ void run_row_r(const RowArgs & a, hipStream_t s) {
     if (R == 2) {
         if (nbl == 1) return go<TYPE, 2, 1, PRO, EPI>(a, grid, s);
         if (nbl == 2) return go<TYPE, 2, 2, PRO, EPI>(a, grid, s);
+    } else if constexpr (EPI == EPI_STORE && PRO == PRO_MERGE) {
+        if (nbl == 1) return go<TYPE, 1, 1, PRO, EPI>(a, grid, s);
+        if (nbl == 2) return go<TYPE, 1, 2, PRO, EPI>(a, grid, s);
     } else if constexpr (EPI == EPI_STORE) {
         switch (nbl) {
             case 1: return go<TYPE, 1, 1, PRO, EPI>(a, grid, s);
@@ -350,8 +376,8 @@ int row_gemv_merge_max() { return kMergeMax; }
 void launch_row_gemv(int type, int pro, int epi, const RowArgs & a, hipStream_t s) {
     require(row_gemv_fits(type, (int64_t) a.nb * QK), "row gemv: weight type or K not supported");
     require(epi == EPI_STORE || a.N % 2 == 0, "row gemv: row-pair epilogue needs an even row count");
-    require(pro != PRO_MERGE || (a.nsplit >= 1 && a.nsplit <= kMergeMax && a.D % 4 == 0),
-            "row gemv: merge of 1.." + std::to_string(kMergeMax) + " splits");
+    require(pro != PRO_MERGE || (a.nsplit >= 1 && a.nsplit <= kMergeMax && a.D % 4 == 0 && a.nb * QK <= 4096),
+            "row gemv: merge of 1.." + std::to_string(kMergeMax) + " splits, K <= 4096");
     if (type == T_Q4_0) run_row_t<T_Q4_0>(pro, epi, a, s);
     else run_row_t<T_Q8_0>(pro, epi, a, s);
     check_launch("row gemv");
