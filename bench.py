@@ -1,6 +1,6 @@
 """Benchmark of the quantized mat-mul / KV-cache attention path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--mode decode|gemv]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--mode decode|gemv|roofline|sweep]
 
 Prints one JSON line. Default workload (mode "decode"): a random-init Llama-3-8B-shaped decoder
 (32 layers, hidden 4096, GQA 32/8 x 128, SwiGLU 14336, vocab 128256, every matmul weight Q4_0,
@@ -32,6 +32,7 @@ sys.path.insert(0, str(ROOT / "ggml-compiler_amd"))
 
 METRIC = "decode tok/s (8B-shape Q4_0, 1 GPU); quant GEMV GB/s and % of HBM peak"
 HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
 LAYER_SHAPES = [(4096, 6144), (4096, 4096), (4096, 28672), (14336, 4096)]  # (K, N)
 ROTATE_BYTES = 768 << 20  # > 256 MB Infinity Cache
 
@@ -262,20 +263,93 @@ def bench_gemv(args, ops, torch) -> dict:
                        "global_batch": 1, "seq_len": 1, "parallelism": "none"}}
 
 
+def _graph_us(torch, calls, passes: int = 5) -> float:
+    """Average µs per call of `calls` (a list of thunks) captured once in a HIP graph and replayed
+    `passes` times between two events on the capture's stream."""
+    for c in calls[:2]:
+        c()  # device queries and allocator warm-up happen before capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for c in calls:
+            c()
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(passes):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (passes * len(calls))
+
+
+def _rotating_weights(ops, t: str, N: int, K: int, seed: int):
+    """Copies of one N x K weight (N(0, 0.02) -> t) covering ROTATE_BYTES, so successive launches
+    read HBM, not the 256 MB Infinity Cache."""
+    w = ops.QuantWeight.quantize(ops.fill_normal((N, K), seed=seed, std=0.02), t)
+    copies = max(2, math.ceil(ROTATE_BYTES / w.data.numel()))
+    return [w] + [ops.QuantWeight(w.type, w.N, w.K, w.data.clone()) for _ in range(copies - 1)]
+
+
+def bench_sweep(ops, torch) -> list[dict]:
+    """The other measured configurations (ggml_mul_mat GEMV / GEMM, decode flash_attn_ext), each
+    op launched back to back from a HIP graph over inputs rotated past the Infinity Cache."""
+    out = []
+
+    def gemv_case(cfg, t, K, N, B):
+        ws = _rotating_weights(ops, t, N, K, seed=K + N)
+        x = ops.fill_normal((B, K), seed=1)
+        us = _graph_us(torch, [lambda w=w: ops.mul_mat(w, x) for w in ws] * max(1, 64 // len(ws)))
+        wbytes = ws[0].data.numel()
+        nbytes = wbytes + B * K * 4 + B * N * 4
+        out.append({"config": cfg, "op": "mul_mat", "type": t, "K": K, "N": N, "B": B, "us": round(us, 2),
+                    "GB/s": round(nbytes / us / 1e3, 1), "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)})
+        del ws
+
+    gemv_case("C1", "q8_0", 4096, 4096, 1)
+    for t in ("q4_0", "q4_K"):
+        for K, N in LAYER_SHAPES:
+            for B in (1, 2, 4, 8):
+                gemv_case("C2", t, K, N, B)
+    # C3: prefill GEMM, Q8_0 K=4096 N=14336, 512 rows (activation quantization included)
+    ws = _rotating_weights(ops, "q8_0", 14336, 4096, seed=3)[:4]
+    x = ops.fill_normal((512, 4096), seed=4)
+    us = _graph_us(torch, [lambda w=w: ops.mul_mat(w, x) for w in ws] * 4, passes=3)
+    flops = 2 * 512 * 14336 * 4096
+    out.append({"config": "C3", "op": "mul_mat", "type": "q8_0", "K": 4096, "N": 14336, "M": 512, "us": round(us, 1),
+                "TOP/s": round(flops / us / 1e6, 1), "frac_int8_mfma": round(flops / us / 1e6 / INT8_PEAK_TOPS, 4)})
+    # C4: decode attention, 32 q heads on 8 KV heads of 128, one query row, every key visible
+    for ctx in (512, 4096, 32768):
+        kv_bytes = 2 * ctx * 8 * 128 * 2
+        copies = max(2, math.ceil(ROTATE_BYTES / kv_bytes))
+        k = ops.fill_normal((copies, 8, ctx, 128), seed=5).half()
+        v = ops.fill_normal((copies, 8, ctx, 128), seed=6).half()
+        q = ops.fill_normal((32, 1, 128), seed=7)
+        calls = [lambda i=i: ops.flash_attn_ext(q, k[i], v[i], None, 1 / math.sqrt(128)) for i in range(copies)]
+        us = _graph_us(torch, calls * max(1, 64 // copies))
+        nbytes = kv_bytes + 2 * 32 * 128 * 4
+        out.append({"config": "C4", "op": "flash_attn_ext", "ctx": ctx, "us": round(us, 2),
+                    "GB/s": round(nbytes / us / 1e3, 1), "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)})
+        del k, v
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--mode", choices=["decode", "gemv", "roofline"], default="decode",
-                    help="roofline: only the roofline leg and a 1 GiB copy (for rocprofv3 --pmc runs)")
+    ap.add_argument("--mode", choices=["decode", "gemv", "roofline", "sweep"], default="decode",
+                    help="roofline: only the roofline leg and a 1 GiB copy (for rocprofv3 --pmc runs); "
+                         "sweep: the GEMV / GEMM / attention configurations, one JSON line each")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for {args.gpus}); multi-GPU sharding is design-only here.",
               file=sys.stderr)
         return 2
-    args.steps = args.steps or {"decode": 128, "gemv": 200, "roofline": 10}[args.mode]
+    args.steps = args.steps or {"decode": 128, "gemv": 200, "roofline": 10, "sweep": 1}[args.mode]
     args.warmup = args.warmup if args.warmup is not None else 8
 
     import torch
@@ -285,6 +359,10 @@ def main() -> int:
     ops.require_device()
     torch.cuda.set_device(0)
     model = None
+    if args.mode == "sweep":
+        for r in bench_sweep(ops, torch):
+            print(json.dumps(r), flush=True)
+        return 0
     if args.mode == "roofline":
         roof = gemv_roofline(ops, torch, passes=args.steps)
         copy_calibration(torch)

@@ -384,21 +384,47 @@ __global__ __launch_bounds__(NW * 64) void k_attn_decode(const float * __restric
 }
 
 // Combine the splits of one (query row, head): out = sum_i e^(m_i - M) o_i / sum_i e^(m_i - M) l_i.
+// D threads; the (max, sum) pairs go through LDS once, and each thread's partials are loaded 8 at a
+// time before any math, so a long context's many splits cost few round trips.
 template <int D>
 __global__ __launch_bounds__(D) void k_attn_merge(const float * __restrict__ part_o, const float2 * __restrict__ part_ml,
                                                   float * __restrict__ out, int nsplit) {
+    constexpr int kMaxSplit = 1024;
+    __shared__ float2 sml[kMaxSplit];
+    __shared__ float red[D / 64 > 0 ? D / 64 : 1];
     const int64_t sh = blockIdx.x;  // s * H + h
     const int d = threadIdx.x;
     const float2 * ml = part_ml + sh * nsplit;
     float M = -INFINITY;
-    for (int i = 0; i < nsplit; i++) M = fmaxf(M, ml[i].x);
+    for (int i = d; i < nsplit; i += D) {
+        const float2 t = ml[i];
+        sml[i] = t;
+        M = fmaxf(M, t.x);
+    }
+    M = wave_max<(D < 64 ? D : 64)>(M);
+    if constexpr (D > 64) {
+        if ((d & 63) == 0) red[d >> 6] = M;
+        __syncthreads();
+#pragma unroll
+        for (int w = 0; w < D / 64; w++) M = fmaxf(M, red[w]);
+    }
+    __syncthreads();
     float L = 0.0f, o = 0.0f;
     if (M != -INFINITY) {
-        for (int i = 0; i < nsplit; i++) {
-            if (ml[i].x == -INFINITY) continue;
-            const float w = __expf(ml[i].x - M);
-            L += w * ml[i].y;
-            o += w * part_o[(sh * nsplit + i) * D + d];
+        const float * po = part_o + sh * nsplit * D + d;
+        for (int i0 = 0; i0 < nsplit; i0 += 8) {
+            float pv[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) pv[j] = po[(int64_t) min(i0 + j, nsplit - 1) * D];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                if (i0 + j >= nsplit) break;
+                const float2 t = sml[i0 + j];
+                if (t.x == -INFINITY) continue;
+                const float w = __expf(t.x - M);
+                L += w * t.y;
+                o += w * pv[j];
+            }
         }
     }
     out[sh * D + d] = L == 0.0f ? 0.0f : o / L;
@@ -508,6 +534,7 @@ void launch_flash_attn(const float * q, int64_t q_h, int64_t q_s, const void * k
                        hipStream_t s) {
     require(D == Dv, "flash_attn: K and V head sizes must match");
     const AttnPlan p = attn_plan(Sq, Hkv, n_kv);
+    require(p.nsplit <= 1024, "flash_attn: n_kv above 1024 * 1024 keys");  // k_attn_merge's LDS
     require(ws_size >= attn_workspace(Sq, H, Hkv, Dv, n_kv), "flash_attn: workspace too small");
     float * po = (float *) ws;
     float2 * pml = (float2 *) ((uint8_t *) ws + align256((size_t) Sq * H * p.nsplit * Dv * sizeof(float)));

@@ -214,6 +214,33 @@ __device__ __forceinline__ void q8_block_store(float4 v, int8_t * codes, float2 
     if (lane8 == 0) *meta = make_float2(h2f(f2h_exact(__fdiv_rn(amax, 127.0f))), __int_as_float(s));
 }
 
+// The same conversion of one 32-value block held 16 per lane by two neighbouring lanes (half = the
+// lane's half of the block): codes of the block at codes[0..32), its (d, code sum) at *meta.
+__device__ __forceinline__ void q8_half_block_store(const float (&v)[16], int8_t * codes, float2 * meta, int half) {
+#pragma clang fp contract(off)
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; j++) amax = fmaxf(amax, fabsf(v[j]));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+    int w[4];
+    int s = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        int packed = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int q = (int) __builtin_rintf(v[4 * k + j] * id);
+            s += q;
+            packed |= (q & 0xff) << (8 * j);
+        }
+        w[k] = packed;
+    }
+    *reinterpret_cast<int4 *>(codes + 16 * half) = make_int4(w[0], w[1], w[2], w[3]);
+    s += __shfl_xor(s, 1, 64);
+    if (half == 0) *meta = make_float2(h2f(f2h_exact(__fdiv_rn(amax, 127.0f))), __int_as_float(s));
+}
+
 // rms_norm of one row of n (a multiple of 32) times w, quantized to Q8_0: codes [n], meta [n/32].
 // Called by all 256 threads of a block.
 __device__ __forceinline__ void rmsnorm_q8_row(const float * xr, int n, const float * w, float eps, int8_t * codes,

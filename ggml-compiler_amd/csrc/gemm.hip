@@ -8,10 +8,13 @@
 // gfx950's v_mfma_i32_32x32x32_i8 has a depth of exactly one quant block, so every MFMA yields
 // the 32x32 tile of block sums isum(., ., blk) exactly; the fp16-scale epilogue folds it into fp32
 // accumulators (d_w and d_x from LDS). Workgroup tile 128 (m) x 128 (n), 4 wavefronts of 64x64
-// (2x2 MFMA tiles); each stage stages 4 K-blocks of A (activation codes) and B (weight codes,
-// Q4_0 nibbles expanded to signed int8 q-8) in LDS with a 16-byte row pad against bank
-// conflicts. Tiles are numbered so that the workgroups sharing one weight tile land on the same
-// XCD (and L2).
+// (2x2 MFMA tiles); two LDS stages of 2 K-blocks each of A (activation codes) and B (weight codes,
+// Q4_0 nibbles expanded to signed int8 q-8), with a 16-byte row pad against bank conflicts. Tiles
+// are numbered so that the workgroups sharing one weight tile land on the same XCD (and L2).
+//
+// The per-block epilogue (3 VALU operations per output element per K-block of 32, against one
+// 32-deep MFMA step) bounds this kernel near 1/6 of the int8 MFMA peak: ggml's semantics put a
+// scale on every block, so the block sums cannot stay in the int32 accumulator.
 #include "gcq_common.h"
 
 namespace gcq {
@@ -19,23 +22,114 @@ namespace gcq {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
-constexpr int GBM = 128, GBN = 128, GKB = 4;
-constexpr int GPITCH = GKB * 32 + 16;
+constexpr int GBM = 128, GBN = 128;  // workgroup tile
+constexpr int GKB = 2;               // K-blocks (of 32) per LDS stage
+constexpr int GPITCH = GKB * 32 + 16;  // LDS row pitch in bytes (16 B pad against bank conflicts)
 
 __device__ __forceinline__ uint32_t q4_to_s8(uint32_t w) {  // 4 nibbles (0..15) -> 4 int8 (q - 8)
     return (((w & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
 }
 
+// One LDS stage's worth of global data held in registers between its load and its LDS store.
+template <int TYPE>
+struct GemmStage {
+    int4 a[2];                         // activation codes: 2 x 16 B per thread
+    uint4 b[TYPE == T_Q8_0 ? 2 : 1];   // weight codes: Q8_0 2 x 16 B, Q4_0 one block's 16 B of nibbles
+    float dx;                          // one activation scale
+    uint32_t dw;                       // one weight scale (fp16 bits)
+};
+
+// Chunk c (K-blocks kb0 .. kb0 + GKB) of this workgroup's tile: thread t's share. Rows past M or
+// N reload the last row; blocks past nb reload the last block (never used).
+template <int TYPE>
+__device__ __forceinline__ void gemm_load(GemmStage<TYPE> & st, const uint8_t * __restrict__ wqs,
+                                          const uint16_t * __restrict__ wd, const int8_t * __restrict__ xc,
+                                          const float2 * __restrict__ xm, int m0, int n0, int M, int N, int nb, int kb0) {
+    const int t = threadIdx.x;
+    const int K = nb * 32;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {  // A: 128 rows x GKB*32 B = 512 chunks of 16 B
+        const int c = t + 256 * i;
+        const int row = c / (GKB * 2), part = c % (GKB * 2);
+        const int gm = min(m0 + row, M - 1);
+        const int kb = min(kb0 + part / 2, nb - 1);
+        st.a[i] = *reinterpret_cast<const int4 *>(xc + (size_t) gm * K + (size_t) kb * 32 + (part & 1) * 16);
+    }
+    if constexpr (TYPE == T_Q8_0) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int c = t + 256 * i;
+            const int row = c / (GKB * 2), part = c % (GKB * 2);
+            const int gn = min(n0 + row, N - 1);
+            const int kb = min(kb0 + part / 2, nb - 1);
+            st.b[i] = *reinterpret_cast<const uint4 *>(wqs + ((size_t) gn * nb + kb) * 32 + (part & 1) * 16);
+        }
+    } else {  // 128 rows x GKB blocks of 16 B
+        const int row = t / GKB, j = t % GKB;
+        const int gn = min(n0 + row, N - 1);
+        const int kb = min(kb0 + j, nb - 1);
+        st.b[0] = *reinterpret_cast<const uint4 *>(wqs + ((size_t) gn * nb + kb) * 16);
+    }
+    {  // scales: 128 rows x GKB blocks each
+        const int row = t / GKB, j = t % GKB;
+        const int kb = min(kb0 + j, nb - 1);
+        st.dx = xm[(size_t) min(m0 + row, M - 1) * nb + kb].x;
+        st.dw = wd[(size_t) min(n0 + row, N - 1) * nb + kb];
+    }
+}
+
+template <int TYPE>
+__device__ __forceinline__ void gemm_store(const GemmStage<TYPE> & st, int8_t * sA, int8_t * sB, float * sdx,
+                                           float * sdw) {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int c = t + 256 * i;
+        const int row = c / (GKB * 2), part = c % (GKB * 2);
+        *reinterpret_cast<int4 *>(sA + row * GPITCH + part * 16) = st.a[i];
+    }
+    if constexpr (TYPE == T_Q8_0) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int c = t + 256 * i;
+            const int row = c / (GKB * 2), part = c % (GKB * 2);
+            *reinterpret_cast<uint4 *>(sB + row * GPITCH + part * 16) = st.b[i];
+        }
+    } else {
+        const int row = t / GKB, j = t % GKB;
+        const uint4 w = st.b[0];
+        int4 lo, hi;
+        lo.x = (int) q4_to_s8(w.x);
+        lo.y = (int) q4_to_s8(w.y);
+        lo.z = (int) q4_to_s8(w.z);
+        lo.w = (int) q4_to_s8(w.w);
+        hi.x = (int) q4_to_s8(w.x >> 4);
+        hi.y = (int) q4_to_s8(w.y >> 4);
+        hi.z = (int) q4_to_s8(w.z >> 4);
+        hi.w = (int) q4_to_s8(w.w >> 4);
+        *reinterpret_cast<int4 *>(sB + row * GPITCH + j * 32) = lo;
+        *reinterpret_cast<int4 *>(sB + row * GPITCH + j * 32 + 16) = hi;
+    }
+    const int row = t / GKB, j = t % GKB;
+    sdx[j * GBM + row] = st.dx;
+    sdw[j * GBN + row] = h2f((uint16_t) st.dw);
+}
+
 // RAW: write the int32 block sums of block `raw_blk` instead of the scaled result.
+//
+// Pipeline: chunk c + 1's global loads are issued into registers before chunk c is computed from
+// LDS, then stored to the other LDS buffer; one barrier per chunk. Per K-block each wavefront
+// issues its four 32x32x32 MFMAs, then folds each int32 result into the fp32 accumulators as
+// (isum * d_w) * d_x, the scales read from LDS once per block as vectors.
 template <int TYPE, bool RAW>
 __global__ __launch_bounds__(256) void k_gemm(const uint8_t * __restrict__ wqs, const uint16_t * __restrict__ wd,
                                               const int8_t * __restrict__ xc, const float2 * __restrict__ xm,
                                               float * y, const float * res, int32_t * __restrict__ yraw, int M, int N,
                                               int nb, int ldy, int raw_blk) {
-    __shared__ __attribute__((aligned(16))) int8_t sA[GBM * GPITCH];
-    __shared__ __attribute__((aligned(16))) int8_t sB[GBN * GPITCH];
-    __shared__ float sdx[GKB][GBM];
-    __shared__ float sdw[GKB][GBN];
+    __shared__ __attribute__((aligned(16))) int8_t sA[2][GBM * GPITCH];
+    __shared__ __attribute__((aligned(16))) int8_t sB[2][GBN * GPITCH];
+    __shared__ __attribute__((aligned(16))) float sdx[2][GKB * GBM];
+    __shared__ __attribute__((aligned(16))) float sdw[2][GKB * GBN];
 
     // Tile numbering: ids id, id+8, ... run on one XCD; give each XCD a contiguous run of tiles,
     // m-tiles fastest, so the workgroups that read one weight tile share an L2.
@@ -47,7 +141,6 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t * __restrict__ wqs, 
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int wm = wave >> 1, wn = wave & 1;
-    const int K = nb * 32;
     float acc[2][2][16];
 #pragma unroll
     for (int a = 0; a < 2; a++)
@@ -58,84 +151,67 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t * __restrict__ wqs, 
 
     const int kb_begin = RAW ? raw_blk : 0;
     const int kb_end = RAW ? raw_blk + 1 : nb;
-    for (int kb0 = kb_begin; kb0 < kb_end; kb0 += GKB) {
-        const int nblk = min(GKB, kb_end - kb0);
-        // A: activation codes, 16 B chunks.
-        for (int c = tid; c < GBM * GKB * 2; c += 256) {
-            const int row = c / (GKB * 2), part = c % (GKB * 2);
-            if (part < nblk * 2) {
-                const int gm = min(m0 + row, M - 1);
-                *reinterpret_cast<int4 *>(sA + row * GPITCH + part * 16) =
-                    *reinterpret_cast<const int4 *>(xc + (size_t) gm * K + (size_t) kb0 * 32 + part * 16);
-            }
-        }
-        // B: weight codes.
-        if constexpr (TYPE == T_Q8_0) {
-            for (int c = tid; c < GBN * GKB * 2; c += 256) {
-                const int row = c / (GKB * 2), part = c % (GKB * 2);
-                if (part < nblk * 2) {
-                    const int gn = min(n0 + row, N - 1);
-                    *reinterpret_cast<int4 *>(sB + row * GPITCH + part * 16) =
-                        *reinterpret_cast<const int4 *>(wqs + (size_t) gn * K + (size_t) kb0 * 32 + part * 16);
-                }
-            }
-        } else {
-            for (int c = tid; c < GBN * GKB; c += 256) {
-                const int row = c / GKB, j = c % GKB;
-                if (j < nblk) {
-                    const int gn = min(n0 + row, N - 1);
-                    const uint4 w = *reinterpret_cast<const uint4 *>(wqs + ((size_t) gn * nb + kb0 + j) * 16);
-                    int4 lo, hi;
-                    lo.x = (int) q4_to_s8(w.x);
-                    lo.y = (int) q4_to_s8(w.y);
-                    lo.z = (int) q4_to_s8(w.z);
-                    lo.w = (int) q4_to_s8(w.w);
-                    hi.x = (int) q4_to_s8(w.x >> 4);
-                    hi.y = (int) q4_to_s8(w.y >> 4);
-                    hi.z = (int) q4_to_s8(w.z >> 4);
-                    hi.w = (int) q4_to_s8(w.w >> 4);
-                    *reinterpret_cast<int4 *>(sB + row * GPITCH + j * 32) = lo;
-                    *reinterpret_cast<int4 *>(sB + row * GPITCH + j * 32 + 16) = hi;
-                }
-            }
-        }
-        for (int c = tid; c < GBM * GKB; c += 256) {
-            const int row = c / GKB, j = c % GKB;
-            if (j < nblk) sdx[j][row] = xm[(size_t) min(m0 + row, M - 1) * nb + kb0 + j].x;
-        }
-        for (int c = tid; c < GBN * GKB; c += 256) {
-            const int row = c / GKB, j = c % GKB;
-            if (j < nblk) sdw[j][row] = h2f(wd[(size_t) min(n0 + row, N - 1) * nb + kb0 + j]);
-        }
-        __syncthreads();
+    const int nchunk = (kb_end - kb_begin + GKB - 1) / GKB;
+    GemmStage<TYPE> st;
+    gemm_load<TYPE>(st, wqs, wd, xc, xm, m0, n0, M, N, nb, kb_begin);
+    gemm_store<TYPE>(st, sA[0], sB[0], sdx[0], sdw[0]);
+    __syncthreads();
 
-        for (int j = 0; j < nblk; j++) {
+    for (int c = 0; c < nchunk; c++) {
+        const int buf = c & 1;
+        const int kb0 = kb_begin + c * GKB;
+        if (c + 1 < nchunk) gemm_load<TYPE>(st, wqs, wd, xc, xm, m0, n0, M, N, nb, kb0 + GKB);
+        const int nblk = min(GKB, kb_end - kb0);
+#pragma unroll
+        for (int j = 0; j < GKB; j++) {
+            if (j >= nblk) break;
             v4i af[2], bf[2];
 #pragma unroll
             for (int t = 0; t < 2; t++) {
-                af[t] = *reinterpret_cast<const v4i *>(sA + (wm * 64 + t * 32 + (lane & 31)) * GPITCH + j * 32 + 16 * (lane >> 5));
-                bf[t] = *reinterpret_cast<const v4i *>(sB + (wn * 64 + t * 32 + (lane & 31)) * GPITCH + j * 32 + 16 * (lane >> 5));
+                af[t] = *reinterpret_cast<const v4i *>(sA[buf] + (wm * 64 + t * 32 + (lane & 31)) * GPITCH + j * 32 +
+                                                       16 * (lane >> 5));
+                bf[t] = *reinterpret_cast<const v4i *>(sB[buf] + (wn * 64 + t * 32 + (lane & 31)) * GPITCH + j * 32 +
+                                                       16 * (lane >> 5));
             }
+            v16i cc[2][2];
 #pragma unroll
-            for (int tm = 0; tm < 2; tm++) {
+            for (int tm = 0; tm < 2; tm++)
 #pragma unroll
-                for (int tn = 0; tn < 2; tn++) {
-                    v16i c = {};
-                    c = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[tm], bf[tn], c, 0, 0, 0);
-                    if constexpr (RAW) {
+                for (int tn = 0; tn < 2; tn++)
+                    cc[tm][tn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[tm], bf[tn], v16i{}, 0, 0, 0);
+            if constexpr (RAW) {
 #pragma unroll
-                        for (int r = 0; r < 16; r++) acc[tm][tn][r] = __int_as_float(c[r]);
-                    } else {
-                        const float dw = sdw[j][wn * 64 + tn * 32 + (lane & 31)];
+                for (int tm = 0; tm < 2; tm++)
 #pragma unroll
-                        for (int r = 0; r < 16; r++) {
-                            const int mi = wm * 64 + tm * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-                            acc[tm][tn][r] += ((float) c[r] * dw) * sdx[j][mi];
+                    for (int tn = 0; tn < 2; tn++)
+#pragma unroll
+                        for (int r = 0; r < 16; r++) acc[tm][tn][r] = __int_as_float(cc[tm][tn][r]);
+            } else {
+                // d_x of this lane's rows: element r of tile tm is row wm*64 + tm*32 + 8*(r/4) + 4*(lane/32) + r%4
+                float4 dx[2][4];
+#pragma unroll
+                for (int tm = 0; tm < 2; tm++)
+#pragma unroll
+                    for (int q = 0; q < 4; q++)
+                        dx[tm][q] = *reinterpret_cast<const float4 *>(sdx[buf] + j * GBM + wm * 64 + tm * 32 + q * 8 +
+                                                                      (lane >> 5) * 4);
+                float dwv[2];
+#pragma unroll
+                for (int tn = 0; tn < 2; tn++) dwv[tn] = sdw[buf][j * GBN + wn * 64 + tn * 32 + (lane & 31)];
+#pragma unroll
+                for (int tm = 0; tm < 2; tm++)
+#pragma unroll
+                    for (int tn = 0; tn < 2; tn++)
+#pragma unroll
+                        for (int q = 0; q < 4; q++) {
+                            acc[tm][tn][4 * q + 0] += ((float) cc[tm][tn][4 * q + 0] * dwv[tn]) * dx[tm][q].x;
+                            acc[tm][tn][4 * q + 1] += ((float) cc[tm][tn][4 * q + 1] * dwv[tn]) * dx[tm][q].y;
+                            acc[tm][tn][4 * q + 2] += ((float) cc[tm][tn][4 * q + 2] * dwv[tn]) * dx[tm][q].z;
+                            acc[tm][tn][4 * q + 3] += ((float) cc[tm][tn][4 * q + 3] * dwv[tn]) * dx[tm][q].w;
                         }
-                    }
-                }
             }
         }
+        if (c + 1 < nchunk) gemm_store<TYPE>(st, sA[buf ^ 1], sB[buf ^ 1], sdx[buf ^ 1], sdw[buf ^ 1]);
         __syncthreads();
     }
 

@@ -110,22 +110,25 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
 
     // Order of issue matters: a wavefront's vector loads complete in order, so the prologue's
     // loads go first and the weights after them; the prologue then waits for its own data only,
-    // while the first two row groups' weights stream in.
-    constexpr int PASSES = (NBL * 64 * QK + 4 * NT - 1) / (4 * NT);  // K <= 64 * NBL * 32
-    constexpr bool MERGE = PRO == PRO_MERGE;  // one pass (K <= 4096), up to kMergeMax splits
-    float4 v[PASSES], nwv[PASSES];
+    // while the first row groups' weights stream in. Every load is unconditional (addresses
+    // clamped into range, values past the end discarded), so the compiler knows how many are in
+    // flight and waits for the oldest only.
+    //
+    // PLAIN / NORM: thread t takes values [16t, 16t + 16), half a Q8_0 block, so the prologue's
+    // arithmetic sits on K/1024 wavefronts (one per SIMD at K = 4096) rather than on all sixteen.
+    // MERGE: 4 values per thread (K <= 4096), the partials of up to kMergeMax splits in registers.
+    constexpr bool MERGE = PRO == PRO_MERGE;
+    float4 xv[MERGE ? 1 : 4], nv[PRO == PRO_NORM ? 4 : 1];
     float2 mlv[MERGE ? kMergeMax : 1];
     float4 pov[MERGE ? kMergeMax : 1];
-    // Every load below is unconditional (addresses clamped into range, values past the end
-    // discarded afterwards), so the compiler knows how many are in flight and waits for the
-    // oldest only.
+    if constexpr (!MERGE) {
+        const int e = min((int) threadIdx.x * 16, K - 16);
 #pragma unroll
-    for (int p = 0; p < PASSES; p++) {
-        const int e = min((p * NT + (int) threadIdx.x) * 4, K - 4);
-        if constexpr (PRO != PRO_MERGE) v[p] = *reinterpret_cast<const float4 *>(a.x + e);
-        if constexpr (PRO == PRO_NORM) nwv[p] = *reinterpret_cast<const float4 *>(a.norm_w + e);
-    }
-    if constexpr (MERGE) {
+        for (int c = 0; c < 4; c++) {
+            xv[c] = *reinterpret_cast<const float4 *>(a.x + e + 4 * c);
+            if constexpr (PRO == PRO_NORM) nv[c] = *reinterpret_cast<const float4 *>(a.norm_w + e + 4 * c);
+        }
+    } else {
         const int e = min((int) threadIdx.x * 4, K - 4);
         const int h = e / a.D;
         const float2 * ml = a.part_ml + (int64_t) h * a.nsplit;
@@ -148,45 +151,23 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
     load(min(g, ng - 1), w, d);  // waves past the last group load it again and never use it
     if constexpr (PF_EARLY) load(min(g + nw, ng - 1), wn, dn);
 
-    // ---- prologue: the row, 4 values per thread per pass of 4096, into LDS as Q8_0
-    {
-        if constexpr (MERGE) {
-            // The merged attention output (k_merge_q8's arithmetic): sum_i e^(m_i - M) o_i /
-            // sum_i e^(m_i - M) l_i in split order, splits with m_i = -inf left out, 0 if none.
-            const int e = threadIdx.x * 4;
-            if (e < K) {
-                float M = -INFINITY;
+    // ---- prologue: the row into LDS as Q8_0
+    if constexpr (!MERGE) {
+        const int t = threadIdx.x;
+        const bool act = t * 16 < K;
+        float v[16];
 #pragma unroll
-                for (int j = 0; j < kMergeMax; j++) M = fmaxf(M, mlv[j].x);
-                float L = 0.0f;
-                float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (M != -INFINITY) {
-#pragma unroll
-                    for (int j = 0; j < kMergeMax; j++) {
-                        if (mlv[j].x == -INFINITY) continue;
-                        const float wj = __expf(mlv[j].x - M);
-                        L += wj * mlv[j].y;
-                        o.x += wj * pov[j].x;
-                        o.y += wj * pov[j].y;
-                        o.z += wj * pov[j].z;
-                        o.w += wj * pov[j].w;
-                    }
-                }
-                v[0].x = L == 0.0f ? 0.0f : o.x / L;
-                v[0].y = L == 0.0f ? 0.0f : o.y / L;
-                v[0].z = L == 0.0f ? 0.0f : o.z / L;
-                v[0].w = L == 0.0f ? 0.0f : o.w / L;
-            }
+        for (int c = 0; c < 4; c++) {
+            v[4 * c] = act ? xv[c].x : 0.0f;
+            v[4 * c + 1] = act ? xv[c].y : 0.0f;
+            v[4 * c + 2] = act ? xv[c].z : 0.0f;
+            v[4 * c + 3] = act ? xv[c].w : 0.0f;
         }
-#pragma unroll
-        for (int p = 0; p < PASSES; p++)
-            if ((p * NT + (int) threadIdx.x) * 4 >= K) v[p] = make_float4(0.f, 0.f, 0.f, 0.f);
         if constexpr (PRO == PRO_NORM) {
+            // ggml_rms_norm: squares rounded to f32, summed in double, the mean rounded to f32
             double ss = 0.0;
 #pragma unroll
-            for (int p = 0; p < PASSES; p++)
-                ss += (double) (v[p].x * v[p].x) + (double) (v[p].y * v[p].y) + (double) (v[p].z * v[p].z) +
-                      (double) (v[p].w * v[p].w);
+            for (int j = 0; j < 16; j++) ss += (double) (v[j] * v[j]);
 #pragma unroll
             for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
             if (lane == 0) red[threadIdx.x >> 6] = ss;
@@ -196,20 +177,44 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
             for (int i = 0; i < NWV; i++) tot += red[i];
             const float scale = 1.0f / sqrtf((float) (tot / (double) K) + a.eps);
 #pragma unroll
-            for (int p = 0; p < PASSES; p++) {
-                v[p].x = (v[p].x * scale) * nwv[p].x;
-                v[p].y = (v[p].y * scale) * nwv[p].y;
-                v[p].z = (v[p].z * scale) * nwv[p].z;
-                v[p].w = (v[p].w * scale) * nwv[p].w;
+            for (int c = 0; c < 4; c++) {
+                v[4 * c] = (v[4 * c] * scale) * nv[c].x;
+                v[4 * c + 1] = (v[4 * c + 1] * scale) * nv[c].y;
+                v[4 * c + 2] = (v[4 * c + 2] * scale) * nv[c].z;
+                v[4 * c + 3] = (v[4 * c + 3] * scale) * nv[c].w;
             }
         }
+        if (act) q8_half_block_store(v, reinterpret_cast<int8_t *>(lc) + (t / 2) * 32, lm + t / 2, t & 1);
+    } else {
+        // The merged attention output (k_merge_q8's arithmetic): sum_i e^(m_i - M) o_i /
+        // sum_i e^(m_i - M) l_i in split order, splits with m_i = -inf left out, 0 if none.
+        const int e = threadIdx.x * 4;
+        if (e < K) {
+            float M = -INFINITY;
 #pragma unroll
-        for (int p = 0; p < (MERGE ? 1 : PASSES); p++) {
-            const int e = (p * NT + threadIdx.x) * 4;
-            if (e < K) q8_block_store(v[p], reinterpret_cast<int8_t *>(lc) + (e & ~31), lm + e / 32, (e / 4) & 7);
+            for (int j = 0; j < kMergeMax; j++) M = fmaxf(M, mlv[j].x);
+            float L = 0.0f;
+            float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (M != -INFINITY) {
+#pragma unroll
+                for (int j = 0; j < kMergeMax; j++) {
+                    if (mlv[j].x == -INFINITY) continue;
+                    const float wj = __expf(mlv[j].x - M);
+                    L += wj * mlv[j].y;
+                    o.x += wj * pov[j].x;
+                    o.y += wj * pov[j].y;
+                    o.z += wj * pov[j].z;
+                    o.w += wj * pov[j].w;
+                }
+            }
+            o.x = L == 0.0f ? 0.0f : o.x / L;
+            o.y = L == 0.0f ? 0.0f : o.y / L;
+            o.z = L == 0.0f ? 0.0f : o.z / L;
+            o.w = L == 0.0f ? 0.0f : o.w / L;
+            q8_block_store(o, reinterpret_cast<int8_t *>(lc) + (e & ~31), lm + e / 32, (e / 4) & 7);
         }
-        __syncthreads();
     }
+    __syncthreads();
     if constexpr (PF && !PF_EARLY) load(min(g + nw, ng - 1), wn, dn);
 
     int4 xa[XREG ? NBL : 1], xb[XREG ? NBL : 1];
