@@ -106,9 +106,10 @@ __global__ __launch_bounds__(256) void k_attn_split(const float * __restrict__ q
                 part[g] = a;
             }
 #pragma unroll
-            for (int g = 0; g < G; g++)
-#pragma unroll
-                for (int o = LPK / 2; o > 0; o >>= 1) part[g] += __shfl_xor(part[g], o, 64);
+            for (int g = 0; g < G; g++) {
+                if constexpr (LPK <= 16) part[g] = group_reduce<LPK, float, op_add<float>>(part[g]);
+                else part[g] = wave_sum<LPK>(part[g]);
+            }
             if (jj < len && sub == 0) {
                 const float mv = mrow ? h2f(mrow[j0 + jj]) : 0.0f;
 #pragma unroll
@@ -297,8 +298,7 @@ __global__ __launch_bounds__(NW * 64) void k_attn_decode(const float * __restric
                 a = __builtin_amdgcn_fdot2(as_h2(kr[b].y), qh[g][1], a, false);
                 a = __builtin_amdgcn_fdot2(as_h2(kr[b].z), qh[g][2], a, false);
                 a = __builtin_amdgcn_fdot2(as_h2(kr[b].w), qh[g][3], a, false);
-#pragma unroll
-                for (int o = LPK / 2; o > 0; o >>= 1) a += __shfl_xor(a, o, 64);
+                a = group_reduce<LPK, float, op_add<float>>(a);
                 const int jj = base + b * KPW + slot;
                 sc[b] = jj < w1 && jj < len ? a * scale : -INFINITY;
                 bm = fmaxf(bm, sc[b]);

@@ -159,18 +159,77 @@ __device__ __forceinline__ uint16_t f2h_exact(float f) {
 
 __device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
+// Cross-lane reductions on DPP (VALU lane moves) instead of LDS permutes. Within a group of 2O
+// lanes, step O pairs each lane with lane ^ O (O = 1, 2: quad permutes) or with its mirror
+// (O = 4, 8: row half-mirror, row mirror); once each half of the group holds one value, both pair
+// the same two halves, so a reduction gives the xor butterfly's result bit for bit. Across the four
+// 16-lane rows of a wavefront the row results are read with readlane and combined as the
+// butterfly's last two steps would: (row0 . row1) . (row2 . row3).
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, true);
+}
+template <int O>
+__device__ __forceinline__ int lane_pair_i(int v) {
+    static_assert(O == 1 || O == 2 || O == 4 || O == 8, "DPP pairs within 16 lanes");
+    return dpp_i<O == 1 ? 0xB1 : O == 2 ? 0x4E : O == 4 ? 0x141 : 0x140>(v);
+}
+template <int O>
+__device__ __forceinline__ float lane_pair(float v) { return __int_as_float(lane_pair_i<O>(__float_as_int(v))); }
+template <int O>
+__device__ __forceinline__ double lane_pair(double v) {
+    const long long b = __double_as_longlong(v);
+    const int lo = lane_pair_i<O>((int) (b & 0xffffffffll)), hi = lane_pair_i<O>((int) (b >> 32));
+    return __longlong_as_double(((long long) hi << 32) | (unsigned int) lo);
+}
+
+template <class T> __device__ __forceinline__ T op_add(T a, T b) { return a + b; }
+__device__ __forceinline__ float fmaxf_op(float a, float b) { return fmaxf(a, b); }
+
+// Reduction over each group of W lanes (W in 1..16, a power of two), every lane getting its
+// group's result.
+template <int W, class T, T (*OP)(T, T)>
+__device__ __forceinline__ T group_reduce(T v) {
+    if constexpr (W >= 2) v = OP(v, lane_pair<1>(v));
+    if constexpr (W >= 4) v = OP(v, lane_pair<2>(v));
+    if constexpr (W >= 8) v = OP(v, lane_pair<4>(v));
+    if constexpr (W >= 16) v = OP(v, lane_pair<8>(v));
+    return v;
+}
+
+__device__ __forceinline__ float readlane_f(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+__device__ __forceinline__ double readlane_d(double v, int l) {
+    const long long b = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_readlane((int) (b & 0xffffffffll), l), hi = __builtin_amdgcn_readlane((int) (b >> 32), l);
+    return __longlong_as_double(((long long) hi << 32) | (unsigned int) lo);
+}
+
+template <class T, T (*OP)(T, T)>
+__device__ __forceinline__ T wave_reduce(T v) {
+    v = group_reduce<16, T, OP>(v);
+    if constexpr (sizeof(T) == 8) {
+        return OP(OP(readlane_d(v, 0), readlane_d(v, 16)), OP(readlane_d(v, 32), readlane_d(v, 48)));
+    } else {
+        return OP(OP(readlane_f(v, 0), readlane_f(v, 16)), OP(readlane_f(v, 32), readlane_f(v, 48)));
+    }
+}
+
+// W = 64: the whole wavefront (wave-uniform result); W <= 16: each W-lane group; W = 32: each half.
 template <int W = 64>
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+    if constexpr (W == 64) return wave_reduce<float, op_add<float>>(v);
+    else if constexpr (W == 32) return group_reduce<16, float, op_add<float>>(v) + __shfl_xor(group_reduce<16, float, op_add<float>>(v), 16, 64);
+    else return group_reduce<W, float, op_add<float>>(v);
 }
 template <int W = 64>
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = W / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
+    if constexpr (W == 64) return wave_reduce<float, fmaxf_op>(v);
+    else if constexpr (W == 32) return fmaxf(group_reduce<16, float, fmaxf_op>(v), __shfl_xor(group_reduce<16, float, fmaxf_op>(v), 16, 64));
+    else return group_reduce<W, float, fmaxf_op>(v);
 }
+__device__ __forceinline__ double wave_sum_d(double v) { return wave_reduce<double, op_add<double>>(v); }
 template <int W = 64>
 __device__ __forceinline__ int wave_isum(int v) {
 #pragma unroll
@@ -184,8 +243,7 @@ __device__ __forceinline__ float rms_scale(const float * xr, int n, float eps) {
     __shared__ double red[4];
     double s = 0.0;
     for (int i = threadIdx.x; i < n; i += 256) s += (double) (xr[i] * xr[i]);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+    s = wave_sum_d(s);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
     __syncthreads();
     const float mean = (float) ((red[0] + red[1] + red[2] + red[3]) / (double) n);
@@ -197,9 +255,7 @@ __device__ __forceinline__ float rms_scale(const float * xr, int n, float eps) {
 __device__ __forceinline__ void q8_block_store(float4 v, int8_t * codes, float2 * meta, int lane8) {
 #pragma clang fp contract(off)
     float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+    amax = group_reduce<8, float, fmaxf_op>(amax);
     const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
     const int q0 = (int) __builtin_rintf(v.x * id);
     const int q1 = (int) __builtin_rintf(v.y * id);
@@ -208,9 +264,9 @@ __device__ __forceinline__ void q8_block_store(float4 v, int8_t * codes, float2 
     *reinterpret_cast<int *>(codes + 4 * lane8) =
         (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | ((q3 & 0xff) << 24);
     int s = q0 + q1 + q2 + q3;
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);
-    s += __shfl_xor(s, 4, 64);
+    s += lane_pair_i<1>(s);
+    s += lane_pair_i<2>(s);
+    s += lane_pair_i<4>(s);
     if (lane8 == 0) *meta = make_float2(h2f(f2h_exact(__fdiv_rn(amax, 127.0f))), __int_as_float(s));
 }
 
@@ -221,7 +277,7 @@ __device__ __forceinline__ void q8_half_block_store(const float (&v)[16], int8_t
     float amax = 0.0f;
 #pragma unroll
     for (int j = 0; j < 16; j++) amax = fmaxf(amax, fabsf(v[j]));
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    amax = fmaxf(amax, lane_pair<1>(amax));
     const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
     int w[4];
     int s = 0;
@@ -237,7 +293,7 @@ __device__ __forceinline__ void q8_half_block_store(const float (&v)[16], int8_t
         w[k] = packed;
     }
     *reinterpret_cast<int4 *>(codes + 16 * half) = make_int4(w[0], w[1], w[2], w[3]);
-    s += __shfl_xor(s, 1, 64);
+    s += lane_pair_i<1>(s);
     if (half == 0) *meta = make_float2(h2f(f2h_exact(__fdiv_rn(amax, 127.0f))), __int_as_float(s));
 }
 

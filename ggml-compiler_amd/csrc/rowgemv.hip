@@ -168,8 +168,7 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
             double ss = 0.0;
 #pragma unroll
             for (int j = 0; j < 16; j++) ss += (double) (v[j] * v[j]);
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+            ss = wave_sum_d(ss);
             if (lane == 0) red[threadIdx.x >> 6] = ss;
             __syncthreads();
             double tot = 0.0;
