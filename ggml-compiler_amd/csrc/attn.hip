@@ -231,7 +231,7 @@ __device__ __forceinline__ float half_at(const uint4 & r, int c) {
 }
 
 template <int D, int G, int NW>
-__global__ __launch_bounds__(NW * 64) void k_attn_decode(const float * __restrict__ q, int64_t q_h,
+__global__ __launch_bounds__(NW * 64) void k_attn_decode(int GT, const float * __restrict__ q, int64_t q_h,
                                                          const uint16_t * __restrict__ k, int64_t k_h, int64_t k_j,
                                                          const uint16_t * __restrict__ v, int64_t v_h, int64_t v_j,
                                                          float scale, int n_kv, const int * __restrict__ n_kv_dev,
@@ -250,6 +250,7 @@ __global__ __launch_bounds__(NW * 64) void k_attn_decode(const float * __restric
     // at or past n_kv are masked.
     if (n_kv_dev) n_kv = *n_kv_dev;
     const int split = blockIdx.x, hk = blockIdx.y;
+    const int h0 = hk * GT + blockIdx.z * G;  // this workgroup's first query head (GT per KV head)
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int sub = lane % LPK, slot = lane / LPK;
     const int j0 = split * chunk;
@@ -260,7 +261,7 @@ __global__ __launch_bounds__(NW * 64) void k_attn_decode(const float * __restric
     half2_t qh[G][4];
 #pragma unroll
     for (int g = 0; g < G; g++) {
-        const float * qp = q + (int64_t) (hk * G + g) * q_h + 8 * sub;
+        const float * qp = q + (int64_t) (h0 + g) * q_h + 8 * sub;
 #pragma unroll
         for (int c = 0; c < 4; c++) {
             half2_t t;
@@ -287,6 +288,11 @@ __global__ __launch_bounds__(NW * 64) void k_attn_decode(const float * __restric
             kr[b] = *reinterpret_cast<const uint4 *>(kb + row * k_j);
             vr[b] = *reinterpret_cast<const uint4 *>(vb + row * v_j);
         }
+        float vf[NB][8];  // this lane's 8 dims of each key's V row, converted once for all G heads
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+#pragma unroll
+            for (int c = 0; c < 8; c++) vf[b][c] = half_at(vr[b], c);
 #pragma unroll
         for (int g = 0; g < G; g++) {
             float sc[NB];
@@ -318,31 +324,30 @@ __global__ __launch_bounds__(NW * 64) void k_attn_decode(const float * __restric
             for (int c = 0; c < 8; c++) {
                 float t = acc[g][c] * f;
 #pragma unroll
-                for (int b = 0; b < NB; b++) t += p[b] * half_at(vr[b], c);
+                for (int b = 0; b < NB; b++) t += p[b] * vf[b][c];
                 acc[g][c] = t;
             }
             m[g] = mn;
         }
     }
     // Merge the wavefront's lane groups (same sub, slots 0..KPW-1), then the NW wavefronts.
+    // Reduction over the slots (lanes sub, sub + LPK, ...): lane ^ 8 for the 8-lane slots of
+    // D = 64, then the row swaps.
+    auto slots = [&](float v, auto f) {
+        if constexpr (LPK == 8) v = f(v, lane_xor8(v));
+        v = row_pair<16>(v, f);
+        return row_pair<32>(v, f);
+    };
+    auto fmax2 = [](float a, float b) { return fmaxf(a, b); };
+    auto add2 = [](float a, float b) { return a + b; };
 #pragma unroll
     for (int g = 0; g < G; g++) {
-        float M = m[g];
-#pragma unroll
-        for (int o = LPK; o < 64; o <<= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+        const float M = slots(m[g], fmax2);
         const float f = m[g] == -INFINITY ? 0.0f : __expf(m[g] - M);
-        float L = l[g] * f;
+        l[g] = slots(l[g] * f, add2);
 #pragma unroll
-        for (int o = LPK; o < 64; o <<= 1) L += __shfl_xor(L, o, 64);
-#pragma unroll
-        for (int c = 0; c < 8; c++) {
-            float t = acc[g][c] * f;
-#pragma unroll
-            for (int o = LPK; o < 64; o <<= 1) t += __shfl_xor(t, o, 64);
-            acc[g][c] = t;
-        }
+        for (int c = 0; c < 8; c++) acc[g][c] = slots(acc[g][c] * f, add2);
         m[g] = M;
-        l[g] = L;
     }
     if (slot == 0) {
 #pragma unroll
@@ -373,7 +378,7 @@ __global__ __launch_bounds__(NW * 64) void k_attn_decode(const float * __restric
                 o += f * so[w][i];
             }
         }
-        const int h = hk * G + g;
+        const int h = h0 + g;
         if (nsplit == 1) {
             out[h * D + d] = L == 0.0f ? 0.0f : o / L;
         } else {
@@ -444,6 +449,11 @@ AttnPlan attn_plan(int Sq, int Hkv, int n_kv) {
     return {nsplit, max(chunk, 1)};
 }
 
+// Query heads one k_attn_decode workgroup takes of its KV head's GT: all of them (each K/V row read
+// once) for long contexts, one (4x the workgroups, a quarter of the arithmetic each, K/V re-read
+// from L2) up to 4096 keys, where the kernel is bound by latency and arithmetic, not HBM.
+int decode_group(int GT, int max_kv) { return max_kv <= 4096 ? 1 : GT; }
+
 // k_attn_decode's split count for n_kv keys: one load batch per wavefront, at most max_split
 // splits (the wavefronts then take several batches).
 int decode_splits(int D, int G, int n_kv, int max_split) {
@@ -453,28 +463,30 @@ int decode_splits(int D, int G, int n_kv, int max_split) {
 // Decode (one query row, captured once for every KV length up to max_ctx): the split count for
 // max_ctx keys; the KV length itself is read on the device and each split takes an equal share.
 AttnPlan attn_plan_decode(int D, int G, int max_ctx, int max_split) {
-    const int nsplit = decode_splits(D, G, max_ctx, max_split);
+    const int nsplit = decode_splits(D, decode_group(G, max_ctx), max_ctx, max_split);
     return {nsplit, (max_ctx + nsplit - 1) / nsplit};
 }
 
 bool attn_decode_fits(int D, int G) { return (D == 64 || D == 128) && (G == 1 || G == 2 || G == 4); }
 
 // out [H*D] (one split) or part_o / part_ml (several), q [H][D] at head stride q_h.
-// chunk: keys per split (nsplit * chunk >= n_kv); kv_rows: rows the K and V buffers hold per head.
+// chunk: keys per split (nsplit * chunk >= n_kv); kv_rows: rows the K and V buffers hold per head;
+// GS: query heads per workgroup (decode_group).
 void launch_attn_decode(const float * q, int64_t q_h, const void * k, int64_t k_h, int64_t k_j, const void * v,
                         int64_t v_h, int64_t v_j, int D, int H, int Hkv, int n_kv, const int * n_kv_dev, float scale,
-                        int nsplit, int chunk, int kv_rows, float * out, float * part_o, float2 * part_ml,
+                        int nsplit, int chunk, int kv_rows, int GS, float * out, float * part_o, float2 * part_ml,
                         hipStream_t s) {
     const int G = H / Hkv;
     require(attn_decode_fits(D, G) && H % Hkv == 0, "attn decode: D 64 / 128 and 1, 2 or 4 query heads per KV head");
+    require(GS >= 1 && G % GS == 0, "attn decode: head group must divide the query heads per KV head");
     require(kv_rows >= 1 && chunk >= 1 && (int64_t) nsplit * chunk >= (n_kv_dev ? kv_rows : n_kv),
             "attn decode: the splits must cover the keys");
-    const dim3 grid((unsigned) nsplit, (unsigned) Hkv);
+    const dim3 grid((unsigned) nsplit, (unsigned) Hkv, (unsigned) (G / GS));
     const uint16_t *kp = (const uint16_t *) k, *vp = (const uint16_t *) v;
 #define GCQ_AD(DD, GG)                                                                                          \
-    if (D == DD && G == GG)                                                                                     \
+    if (D == DD && GS == GG)                                                                                    \
         k_attn_decode<DD, GG, decode_waves(GG)><<<grid, decode_waves(GG) * 64, 0, s>>>(                         \
-            q, q_h, kp, k_h, k_j, vp, v_h, v_j, scale, n_kv, n_kv_dev, chunk, kv_rows, nsplit, out, part_o, part_ml);
+            G, q, q_h, kp, k_h, k_j, vp, v_h, v_j, scale, n_kv, n_kv_dev, chunk, kv_rows, nsplit, out, part_o, part_ml);
     GCQ_AD(64, 1) GCQ_AD(64, 2) GCQ_AD(64, 4) GCQ_AD(128, 1) GCQ_AD(128, 2) GCQ_AD(128, 4)
 #undef GCQ_AD
     check_launch("attn decode");
@@ -541,9 +553,10 @@ void launch_flash_attn(const float * q, int64_t q_h, int64_t q_s, const void * k
     if (Sq == 1 && mask == nullptr && H % Hkv == 0 && attn_decode_fits(D, H / Hkv)) {
         // One query row, every key visible: the one-pass decode kernel (fewer splits than p, so the
         // workspace holds its partials).
-        const int nsplit = decode_splits(D, H / Hkv, n_kv, p.nsplit);
+        const int GS = decode_group(H / Hkv, n_kv);
+        const int nsplit = decode_splits(D, GS, n_kv, p.nsplit);
         launch_attn_decode(q, q_h, k, k_h, k_j, v, v_h, v_j, D, H, Hkv, n_kv, nullptr, scale, nsplit,
-                           (n_kv + nsplit - 1) / nsplit, n_kv, out, po, pml, s);
+                           (n_kv + nsplit - 1) / nsplit, n_kv, GS, out, po, pml, s);
         if (nsplit == 1) return;
         if (D == 64) k_attn_merge<64><<<(unsigned) H, 64, 0, s>>>(po, pml, out, nsplit);
         else k_attn_merge<128><<<(unsigned) H, 128, 0, s>>>(po, pml, out, nsplit);

@@ -183,6 +183,9 @@ __device__ __forceinline__ double lane_pair(double v) {
     return __longlong_as_double(((long long) hi << 32) | (unsigned int) lo);
 }
 
+// Lane l ^ 8 exactly (row rotate by 8), for values that differ within the 8-lane halves.
+__device__ __forceinline__ float lane_xor8(float v) { return __int_as_float(dpp_i<0x128>(__float_as_int(v))); }
+
 template <class T> __device__ __forceinline__ T op_add(T a, T b) { return a + b; }
 __device__ __forceinline__ float fmaxf_op(float a, float b) { return fmaxf(a, b); }
 
@@ -195,6 +198,21 @@ __device__ __forceinline__ T group_reduce(T v) {
     if constexpr (W >= 8) v = OP(v, lane_pair<4>(v));
     if constexpr (W >= 16) v = OP(v, lane_pair<8>(v));
     return v;
+}
+
+// Pair sums across rows with gfx950's row swaps: lane l gets f(v[l & ~16], v[l | 16]) (X16) or
+// f(v[l & ~32], v[l | 32]) (X32), the xor butterfly's pairs, low lane first.
+template <int X, class F>
+__device__ __forceinline__ float row_pair(float v, F f) {
+    static_assert(X == 16 || X == 32, "row pairs");
+    const unsigned u = __float_as_uint(v);
+    if constexpr (X == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        return f(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    } else {
+        const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        return f(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    }
 }
 
 __device__ __forceinline__ float readlane_f(float v, int l) {

@@ -57,8 +57,9 @@ AttnPlan attn_plan_decode(int D, int G, int max_ctx, int max_split);
 bool attn_decode_fits(int D, int G);
 void launch_attn_decode(const float * q, int64_t q_h, const void * k, int64_t k_h, int64_t k_j, const void * v,
                         int64_t v_h, int64_t v_j, int D, int H, int Hkv, int n_kv, const int * n_kv_dev, float scale,
-                        int nsplit, int chunk, int kv_rows, float * out, float * part_o, float2 * part_ml,
+                        int nsplit, int chunk, int kv_rows, int GS, float * out, float * part_o, float2 * part_ml,
                         hipStream_t s);
+int decode_group(int GT, int max_kv);
 void launch_step_end(const float * logits, int n, void * state, int32_t * out_tokens, int max_out, void * part,
                      void * counter, hipStream_t s);
 
@@ -370,8 +371,8 @@ struct Llama {
             if (decode_attn)
                 launch_attn_decode(qkv.as<float>(), c.head_dim, kvl, kv_h, c.head_dim, kvl + (size_t) c.n_head_kv * kv_h,
                                    kv_h, c.head_dim, c.head_dim, c.n_head, c.n_head_kv, n_kv, n_kv_dev, scale,
-                                   plan.nsplit, plan.chunk, c.max_ctx, attn_row.as<float>(), part_o.as<float>(),
-                                   part_ml.as<float2>(), stream);
+                                   plan.nsplit, plan.chunk, c.max_ctx, decode_group(c.n_head / c.n_head_kv, c.max_ctx),
+                                   attn_row.as<float>(), part_o.as<float>(), part_ml.as<float2>(), stream);
             else
                 launch_attn_split(qkv.as<float>(), c.head_dim, qkv_dim, kvl, kv_h, c.head_dim,
                                   kvl + (size_t) c.n_head_kv * kv_h, kv_h, c.head_dim, nullptr, n_kv, c.head_dim, 1,
