@@ -15,6 +15,8 @@
 //               (runtime/src/ggml_compiler_rt.cpp:402-439): the next token, position and KV length.
 #include "gcq_common.h"
 
+#include <algorithm>
+
 namespace gcq {
 
 constexpr int kStepEndBlocks = 256;
@@ -129,6 +131,22 @@ __global__ __launch_bounds__(D / 4) void k_merge_q8(const float * __restrict__ p
     const int n = H * D;
     const int e = h * D + d0;
     q8_block_store(o, codes + s * n + (e & ~31), meta + s * (n / 32) + e / 32, (d0 / 4) & 7);
+}
+
+// The decode step's first launch: ggml_get_rows of the token's embedding row into x, and the NEOX
+// rotation table of the token's position, cs[i] = (cos theta_i, sin theta_i) for i < half with
+// theta_i = pos * theta_scale^i by repeated f32 multiplication (k_rope_kv's arithmetic), which
+// every layer's QKV projection applies in its epilogue.
+__global__ void k_embed_rope(int type, const uint8_t * __restrict__ tab, int64_t nrows, int D,
+                             const int32_t * __restrict__ idx, float * __restrict__ x, const int32_t * __restrict__ pos,
+                             int half, float theta_scale, float2 * __restrict__ cs) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t < D) x[t] = table_value(type, tab, nrows, D, idx[0], t);
+    if (t < half) {
+        float theta = (float) pos[0];
+        for (int k = 0; k < t; k++) theta *= theta_scale;
+        cs[t] = make_float2(cosf(theta), sinf(theta));
+    }
 }
 
 // dst[r][map[c]] = src[r][c] for S rows of n columns: a mul_mat result whose weight rows were
@@ -249,6 +267,16 @@ void launch_merge_q8(const float * part_o, const float2 * part_ml, int nsplit, i
     else if (D == 64) k_merge_q8<64><<<(unsigned) (Sq * H), 16, 0, s>>>(part_o, part_ml, nsplit, H, out, codes, meta);
     else fail("merge_q8: head size must be 64 or 128");
     check_launch("merge_q8");
+}
+
+void launch_embed_rope(int type, const void * tab, int64_t nrows, int64_t D, const int32_t * idx, float * x,
+                       const int32_t * pos, int head_dim, float base, void * cs, hipStream_t s) {
+    const int half = head_dim / 2;
+    const float theta_scale = powf(base, -2.0f / (float) head_dim);
+    const int64_t n = std::max<int64_t>(D, half);
+    k_embed_rope<<<nblk(n, 256), 256, 0, s>>>(type, (const uint8_t *) tab, nrows, (int) D, idx, x, pos, half,
+                                             theta_scale, (float2 *) cs);
+    check_launch("embed_rope");
 }
 
 void launch_scatter_cols(const float * src, int64_t lds, float * dst, int64_t ldd, const int32_t * map, int S, int n,

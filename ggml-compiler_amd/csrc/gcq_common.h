@@ -88,11 +88,11 @@ struct RowArgs {
     float * y;  // EPI_STORE [N], EPI_SWIGLU [N/2], EPI_ROPE_KV: roped q [H*D]
     const float * res;
     const int * pos;
+    const float2 * rope_cs;  // EPI_ROPE_KV: (cos, sin) of rotation index i at pos, i < D/2
     uint16_t * kc;  // [Hkv][ctx][D] f16
     uint16_t * vc;
     int64_t ctx;
     int H, Hkv, D;
-    float theta_scale;
 };
 
 void launch_row_gemv(int type, int pro, int epi, const RowArgs & a, hipStream_t s);

@@ -60,6 +60,8 @@ void launch_attn_decode(const float * q, int64_t q_h, const void * k, int64_t k_
                         int nsplit, int chunk, int kv_rows, int GS, float * out, float * part_o, float2 * part_ml,
                         hipStream_t s);
 int decode_group(int GT, int max_kv);
+void launch_embed_rope(int type, const void * tab, int64_t nrows, int64_t D, const int32_t * idx, float * x,
+                       const int32_t * pos, int head_dim, float base, void * cs, hipStream_t s);
 void launch_step_end(const float * logits, int n, void * state, int32_t * out_tokens, int max_out, void * part,
                      void * counter, hipStream_t s);
 
@@ -120,6 +122,7 @@ struct Llama {
     bool fused = false;  // one token on the decode-row GEMVs (rowgemv.hip)
     bool decode_attn = false;  // one token's attention on k_attn_decode
     DevBuf attn_row;           // its output when it runs unsplit
+    DevBuf rope_cs;            // the decode step's rotation table (cos, sin) per rotation index
     DevBuf ytmp;         // a prompt chunk's mul_mat result in packed row order
     int pos = 0;
     hipGraph_t graph = nullptr;
@@ -202,6 +205,7 @@ struct Llama {
                 row_gemv_fits(c.wtype, c.n_ff) && c.head_dim % 4 == 0 &&
                 plan_decode.nsplit <= row_gemv_merge_max();
         attn_row = DevBuf((size_t) attn_dim * 4);
+        rope_cs = DevBuf((size_t) c.head_dim / 2 * sizeof(float2));
         po = std::max(po, (size_t) c.n_head * plan_decode.nsplit * c.head_dim * 4);
         pml = std::max(pml, (size_t) c.n_head * plan_decode.nsplit * 8);
         if (fused) {
@@ -347,9 +351,9 @@ struct Llama {
                      const AttnPlan & plan) {
         float * xs = x.as<float>();
         const Tensor & E = tensors[t_embd];
-        launch_get_rows(E.type, E.buf.p, E.rows, E.cols, tok_dev, 1, xs, stream);
+        launch_embed_rope(E.type, E.buf.p, E.rows, E.cols, tok_dev, xs, pos_dev, c.head_dim, c.rope_base, rope_cs.p,
+                          stream);
         const float scale = 1.0f / std::sqrt((float) c.head_dim);
-        const float theta_scale = powf(c.rope_base, -2.0f / (float) c.head_dim);
         const int64_t kv_h = (int64_t) c.max_ctx * c.head_dim;
         for (int l = 0; l < c.n_layer; l++) {
             const Layer & L = layers[l];
@@ -366,7 +370,7 @@ struct Llama {
             a.H = c.n_head;
             a.Hkv = c.n_head_kv;
             a.D = c.head_dim;
-            a.theta_scale = theta_scale;
+            a.rope_cs = rope_cs.as<float2>();
             launch_row_gemv(c.wtype, PRO_NORM, EPI_ROPE_KV, a, stream);
             if (decode_attn)
                 launch_attn_decode(qkv.as<float>(), c.head_dim, kvl, kv_h, c.head_dim, kvl + (size_t) c.n_head_kv * kv_h,

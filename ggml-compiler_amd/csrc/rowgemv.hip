@@ -8,7 +8,8 @@
 //
 //   prologue (every workgroup, into LDS)        epilogue (per row pair)
 //   PRO_PLAIN  Q8_0 of x                        EPI_STORE    y = W x (+ res)
-//   PRO_NORM   Q8_0 of rms_norm(x) * w          EPI_ROPE_KV  NEOX rope of q and k, q -> f32,
+//   PRO_NORM   Q8_0 of rms_norm(x) * w          EPI_ROPE_KV  NEOX rope of q and k (the step's
+//                                                            cos/sin table), q -> f32,
 //   PRO_MERGE  Q8_0 of the merged split-K                    k and v -> f16 KV cache at pos
 //              attention partials (<= 8)        EPI_SWIGLU   y[j] = silu(g_j) * u_j
 //
@@ -57,16 +58,6 @@ __device__ __forceinline__ int dot_blk_q8_0(const uint4 wa, const uint4 wb, cons
     s = sdot4((int) wb.z, xb.z, s);
     s = sdot4((int) wb.w, xb.w, s);
     return s;
-}
-
-// NEOX rotation of (x0, x1) at rotation index i for position p: theta = p * theta_scale^i by
-// repeated f32 multiplication, as ggml and k_rope_kv.
-__device__ __forceinline__ void rope_pair(float x0, float x1, int p, int i, float ts, float & y0, float & y1) {
-    float theta = (float) p;
-    for (int k = 0; k < i; k++) theta *= ts;
-    const float c = cosf(theta), sn = sinf(theta);
-    y0 = x0 * c - x1 * sn;
-    y1 = x0 * sn + x1 * c;
 }
 
 template <int TYPE, int R, int NBL, int PRO, int EPI>
@@ -144,6 +135,10 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
             if (j >= a.nsplit) mlv[j] = make_float2(-INFINITY, 0.0f);  // splits past the last: none
     }
     const int p_tok = EPI == EPI_ROPE_KV ? *a.pos : 0;
+    const int half = a.D / 2;
+    const int nqk = (a.H + a.Hkv) * half;  // row-pair groups of q and k (rotated)
+    float2 cs_first = make_float2(0.0f, 0.0f);  // the rotation of this wave's first group
+    if constexpr (EPI == EPI_ROPE_KV) cs_first = a.rope_cs[min(g, nqk - 1) % half];
     __builtin_amdgcn_sched_barrier(0);  // keep the prologue's loads ahead of the weights'
 
     uint4 wn[NBL][R][CV];
@@ -229,7 +224,7 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
             }
         }
     }
-    const int half = a.D / 2;
+    const int g_first = g;
 
     // One row group: block dots, the row sums, the epilogue.
     auto group = [&](int gg, const uint4 (&wv)[NBL][R][CV], const uint32_t (&dv)[NBL][R]) {
@@ -272,11 +267,10 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
             if (lane == 0) a.y[gg] = v[0] / (1.0f + expf(-v[0])) * v[1];
         } else {  // EPI_ROPE_KV
             if (lane == 0 && p_tok >= 0 && p_tok < a.ctx) {
-                const int nqk = (a.H + a.Hkv) * half;
                 if (gg < nqk) {
                     const int h = gg / half, i = gg % half;
-                    float y0, y1;
-                    rope_pair(v[0], v[1], p_tok, i, a.theta_scale, y0, y1);
+                    const float2 cs = gg == g_first ? cs_first : a.rope_cs[i];
+                    const float y0 = v[0] * cs.x - v[1] * cs.y, y1 = v[0] * cs.y + v[1] * cs.x;
                     if (h < a.H) {
                         a.y[h * a.D + i] = y0;
                         a.y[h * a.D + i + half] = y1;
