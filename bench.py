@@ -9,10 +9,10 @@ of the captured decode graph, inside the on-device generate loop), and `value` i
 (QKV 4096x6144, O 4096x4096, gate/up 4096x28672, down 14336x4096) over weights rotated past the
 256 MB Infinity Cache; `value` is GB/s.
 
-`roofline` is the dominant decode kernel, the f32-row Q4_0 GEMV that runs the QKV, gate/up and
-lm-head projections (algorithmic bytes N*K/32*18 + 8K + 4N per launch), its launches of one step
-replayed from a HIP graph between events on their stream; `traffic` comes from the committed
-rocprofv3 --pmc summary. `cpu_baseline` is the repo's CPU oracle (a restatement of ggml's CPU
+`roofline` is the dominant decode kernel, the row GEMV with the rms_norm + Q8_0 prologue, at the
+gate/up projection's shape (algorithmic bytes N*K/32*18 + 8K + 4N per launch), 32 launches over
+32 distinct weights replayed from a HIP graph between events on their stream; `traffic` comes
+from the committed rocprofv3 --pmc summary. `cpu_baseline` is the repo's CPU oracle (a restatement of ggml's CPU
 semantics, not ggml) on the host cores, on a bounded sample of the same workload. Mode "roofline"
 runs only the roofline leg plus a 1 GiB copy (the counter calibration) for rocprofv3 --pmc.
 """
@@ -46,13 +46,14 @@ def _weights(ops, K: int, N: int, seed: int, copies: int):
     return [w] + [ops.QuantWeight(w.type, w.N, w.K, w.data.clone()) for _ in range(copies - 1)]
 
 
-# The launches of the dominant decode kernel in one 8B decode step, in step order: per layer the
-# QKV and gate/up projections, then the lm head (name, K, N, launches per step).
-ROOF_KERNEL = "k_gemv_p<Q4_0, f32 row: rms_norm + norm weight + Q8_0 in the prologue, 1024 threads>"
-ROOF_LAUNCHES = [("attn_qkv", 4096, 6144, 32), ("ffn_gate_up", 4096, 28672, 32), ("output", 4096, 128256, 1)]
-ROOF_BYTES_NOTE = ("per launch: N*K/32*18 (Q4_0 weight) + 4K (x) + 4K (norm weight) + 4N (y); "
-                   "mean over a step's 65 launches")
-PMC_SUMMARY = ROOT / "profiles" / "k_gemv_p_f32_q4_0_decode_pmc.md"
+# The dominant decode kernel: the row GEMV that takes an f32 row, rms-normalizes and quantizes it in
+# its prologue (ggml_rms_norm -> mul -> mul_mat), at the gate/up projection's shape, the step's
+# largest (a third of its time); 32 distinct weights, one per layer as in the 8B model.
+ROOF_KERNEL = "k_row_gemv<Q4_0, R=2, NBL=2, PRO_NORM, EPI_STORE> (rms_norm + Q8_0 prologue, 1024 threads)"
+ROOF_SHAPE = ("ffn_gate_up", 4096, 28672, 32)  # name, K, N, distinct weights
+ROOF_EXTRA = [("attn_qkv", 4096, 6144, 32), ("output", 4096, 128256, 1)]
+ROOF_BYTES_NOTE = "per launch: N*K/32*18 (Q4_0 weight) + 4K (x) + 4K (norm weight) + 4N (y)"
+PMC_SUMMARY = ROOT / "profiles" / "k_row_gemv_norm_q4_0_gate_up_pmc.md"
 
 
 def _f32_launch_bytes(K: int, N: int) -> int:
@@ -70,27 +71,28 @@ def _pmc_traffic():
     return None
 
 
-def gemv_roofline(ops, torch, passes: int = 10) -> dict:
-    """The dominant decode kernel: the persistent GEMV that reads its activation as an f32 row and
-    does ggml_rms_norm, the norm-weight mul and the Q8_0 conversion in its prologue. It runs the
-    QKV, gate/up and lm-head projections: 65 of a decode step's launches and 2.5 of its 4.3 GB.
-    Its launches in one step's order, with distinct weights per layer (2.4 GB, far past the 256 MB
-    Infinity Cache), are captured once in a HIP graph, and `passes` replays are bracketed by two
-    events on the stream they run on; avg_us = elapsed / launches. Each shape alone (same launch
-    counts) gives the per-shape figures."""
+def gemv_roofline(ops, torch, passes: int = 10, extra: bool = True) -> dict:
+    """The roofline kernel (ROOF_KERNEL) at the gate/up shape: 32 launches over 32 distinct weights
+    (2.1 GB, far past the 256 MB Infinity Cache) captured once in a HIP graph, `passes` replays
+    bracketed by two events on the stream they run on; avg_us = elapsed / launches. With extra,
+    the QKV and lm-head shapes are timed the same way (other instantiations: reported, not the
+    roofline)."""
     from ggml_compiler_amd._lib import check, load
 
     lib = load()
     x = ops.fill_normal((1, 4096), seed=1)
     nw = ops.fill_normal((4096,), seed=2)
-    ws = {name: [ops.QuantWeight.quantize(ops.fill_normal((N, K), seed=1000 + 7 * i + K + N, std=0.02), "q4_0")
-                 for i in range(n)] for name, K, N, n in ROOF_LAUNCHES}
-    ys = {N: torch.empty(N, dtype=torch.float32, device="cuda") for _, _, N, _ in ROOF_LAUNCHES}
-    step = [w for l in range(32) for w in (ws["attn_qkv"][l], ws["ffn_gate_up"][l])] + ws["output"]
+    ys = {}
+
+    def weights(K, N, n):
+        return [ops.QuantWeight.quantize(ops.fill_normal((N, K), seed=1000 + 7 * i + K + N, std=0.02), "q4_0")
+                for i in range(n)]
 
     def launch(seq):
         s = ops._stream()
         for w in seq:
+            if w.N not in ys:
+                ys[w.N] = torch.empty(w.N, dtype=torch.float32, device="cuda")
             check(lib.gcq_rms_norm_mul_mat(w.type, ops._p(w.data), w.N, w.K, ops._p(x), ops._p(nw), 1e-5,
                                            ops._p(ys[w.N]), None, None, 0, s))
 
@@ -108,24 +110,30 @@ def gemv_roofline(ops, torch, passes: int = 10) -> dict:
             g.replay()
         e1.record()
         torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / (passes * len(seq))
-        nbytes = sum(_f32_launch_bytes(w.K, w.N) for w in seq) / len(seq)
-        return us, nbytes
+        return e0.elapsed_time(e1) * 1e3 / (passes * len(seq))
 
-    us, nbytes = timed(step)
+    name, K, N, n = ROOF_SHAPE
+    ws = weights(K, N, n)
+    us = timed(ws)
+    del ws
+    nbytes = _f32_launch_bytes(K, N)
     achieved = nbytes / (us * 1e-6) / 1e9
-    shapes = {}
-    for name, K, N, _ in ROOF_LAUNCHES:
-        s_us, s_b = timed(ws[name])
-        shapes[f"{name} {K}x{N}"] = {"us": round(s_us, 2), "GB/s": round(s_b / (s_us * 1e-6) / 1e9, 1)}
     traffic = _pmc_traffic()
     out = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": ROOF_KERNEL,
-           "avg_us": round(us, 2), "algorithmic_bytes_per_launch": int(nbytes), "bytes_note": ROOF_BYTES_NOTE,
-           "shapes": shapes}
+           "shape": f"{name} K={K} N={N}", "avg_us": round(us, 2), "algorithmic_bytes_per_launch": nbytes,
+           "bytes_note": ROOF_BYTES_NOTE}
     if traffic is not None:
         out["traffic_note"] = f"HBM bytes per launch from {PMC_SUMMARY.relative_to(ROOT)}"
-    del ws
+    if extra:
+        shapes = {}
+        for ename, eK, eN, en in ROOF_EXTRA:
+            ews = weights(eK, eN, en)
+            e_us = timed(ews)
+            del ews
+            shapes[f"{ename} {eK}x{eN}"] = {"us": round(e_us, 2),
+                                           "GB/s": round(_f32_launch_bytes(eK, eN) / (e_us * 1e-6) / 1e9, 1)}
+        out["other_shapes"] = shapes
     return out
 
 
@@ -364,7 +372,7 @@ def main() -> int:
             print(json.dumps(r), flush=True)
         return 0
     if args.mode == "roofline":
-        roof = gemv_roofline(ops, torch, passes=args.steps)
+        roof = gemv_roofline(ops, torch, passes=args.steps, extra=False)
         copy_calibration(torch)
         print(json.dumps({"metric": "roofline kernel GB/s", "value": roof["achieved"], "unit": "GB/s",
                           "roofline": roof}), flush=True)
