@@ -17,7 +17,11 @@
 // kernel combines the splits' (max, sum, partial output) exactly as one online softmax would.
 #include "gcq_common.h"
 
+#include <algorithm>
+
 namespace gcq {
+
+int cu_count();
 
 constexpr int kChunkMax = 1024;  // keys per workgroup slice
 
@@ -236,7 +240,8 @@ __global__ __launch_bounds__(NW * 64) void k_attn_decode(int GT, const float * _
                                                          const uint16_t * __restrict__ v, int64_t v_h, int64_t v_j,
                                                          float scale, int n_kv, const int * __restrict__ n_kv_dev,
                                                          int chunk, int kv_rows, int nsplit, float * __restrict__ out,
-                                                         float * __restrict__ part_o, float2 * __restrict__ part_ml) {
+                                                         float * __restrict__ part_o, float2 * __restrict__ part_ml,
+                                                         const Prefetch pf) {
     constexpr int LPK = D / 8;     // lanes per key row
     constexpr int KPW = 64 / LPK;  // lane groups (keys per step) per wavefront
     constexpr int NB = 4;          // steps per load batch
@@ -248,6 +253,11 @@ __global__ __launch_bounds__(NW * 64) void k_attn_decode(int GT, const float * _
     // Split and wavefront ranges come from the host's chunk, so the K/V addresses do not wait for
     // the KV length read from the device; rows are clamped into the kv_rows that exist and keys
     // at or past n_kv are masked.
+    if ((int) blockIdx.x >= nsplit) {  // a spare workgroup: read ahead for the next launches
+        const int w = ((blockIdx.x - nsplit) * gridDim.y + blockIdx.y) * gridDim.z + blockIdx.z;
+        prefetch_share(pf, w, NW * 64);
+        return;
+    }
     if (n_kv_dev) n_kv = *n_kv_dev;
     const int split = blockIdx.x, hk = blockIdx.y;
     const int h0 = hk * GT + blockIdx.z * G;  // this workgroup's first query head (GT per KV head)
@@ -471,22 +481,33 @@ bool attn_decode_fits(int D, int G) { return (D == 64 || D == 128) && (G == 1 ||
 
 // out [H*D] (one split) or part_o / part_ml (several), q [H][D] at head stride q_h.
 // chunk: keys per split (nsplit * chunk >= n_kv); kv_rows: rows the K and V buffers hold per head;
-// GS: query heads per workgroup (decode_group).
+// GS: query heads per workgroup (decode_group). pf (optional): byte ranges that about as many spare
+// workgroups as leave the CUs one each read ahead into the Infinity Cache.
 void launch_attn_decode(const float * q, int64_t q_h, const void * k, int64_t k_h, int64_t k_j, const void * v,
                         int64_t v_h, int64_t v_j, int D, int H, int Hkv, int n_kv, const int * n_kv_dev, float scale,
                         int nsplit, int chunk, int kv_rows, int GS, float * out, float * part_o, float2 * part_ml,
-                        hipStream_t s) {
+                        hipStream_t s, const Prefetch * pf) {
     const int G = H / Hkv;
     require(attn_decode_fits(D, G) && H % Hkv == 0, "attn decode: D 64 / 128 and 1, 2 or 4 query heads per KV head");
     require(GS >= 1 && G % GS == 0, "attn decode: head group must divide the query heads per KV head");
     require(kv_rows >= 1 && chunk >= 1 && (int64_t) nsplit * chunk >= (n_kv_dev ? kv_rows : n_kv),
             "attn decode: the splits must cover the keys");
-    const dim3 grid((unsigned) nsplit, (unsigned) Hkv, (unsigned) (G / GS));
+    Prefetch P{};
+    int extra = 0;  // spare split slots: extra * Hkv * (G / GS) prefetching workgroups
+    if (pf && (pf->n[0] || pf->n[1])) {
+        require(pf->sink && pf->n[0] % 16 == 0 && pf->n[1] % 16 == 0, "attn decode: prefetch ranges of 16 B");
+        const int per_slot = Hkv * (G / GS);
+        const int spare = cu_count() - nsplit * per_slot;
+        extra = std::max(0, spare / per_slot);
+        P = *pf;
+        P.wgs = extra * per_slot;
+    }
+    const dim3 grid((unsigned) (nsplit + extra), (unsigned) Hkv, (unsigned) (G / GS));
     const uint16_t *kp = (const uint16_t *) k, *vp = (const uint16_t *) v;
 #define GCQ_AD(DD, GG)                                                                                          \
     if (D == DD && GS == GG)                                                                                    \
         k_attn_decode<DD, GG, decode_waves(GG)><<<grid, decode_waves(GG) * 64, 0, s>>>(                         \
-            G, q, q_h, kp, k_h, k_j, vp, v_h, v_j, scale, n_kv, n_kv_dev, chunk, kv_rows, nsplit, out, part_o, part_ml);
+            G, q, q_h, kp, k_h, k_j, vp, v_h, v_j, scale, n_kv, n_kv_dev, chunk, kv_rows, nsplit, out, part_o, part_ml, P);
     GCQ_AD(64, 1) GCQ_AD(64, 2) GCQ_AD(64, 4) GCQ_AD(128, 1) GCQ_AD(128, 2) GCQ_AD(128, 4)
 #undef GCQ_AD
     check_launch("attn decode");
@@ -556,7 +577,7 @@ void launch_flash_attn(const float * q, int64_t q_h, int64_t q_s, const void * k
         const int GS = decode_group(H / Hkv, n_kv);
         const int nsplit = decode_splits(D, GS, n_kv, p.nsplit);
         launch_attn_decode(q, q_h, k, k_h, k_j, v, v_h, v_j, D, H, Hkv, n_kv, nullptr, scale, nsplit,
-                           (n_kv + nsplit - 1) / nsplit, n_kv, GS, out, po, pml, s);
+                           (n_kv + nsplit - 1) / nsplit, n_kv, GS, out, po, pml, s, nullptr);
         if (nsplit == 1) return;
         if (D == 64) k_attn_merge<64><<<(unsigned) H, 64, 0, s>>>(po, pml, out, nsplit);
         else k_attn_merge<128><<<(unsigned) H, 128, 0, s>>>(po, pml, out, nsplit);

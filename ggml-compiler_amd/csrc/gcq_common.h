@@ -68,6 +68,36 @@ struct AttnPlan {
 };
 AttnPlan attn_plan(int Sq, int Hkv, int n_kv);
 
+// Byte ranges a kernel's spare workgroups read ahead of their use, so that the next launches find
+// them in the 256 MB Infinity Cache instead of HBM (contents unchanged; nothing is written but a
+// sink word on an impossible value).
+struct Prefetch {
+    const uint8_t * p[2] = {nullptr, nullptr};
+    size_t n[2] = {0, 0};  // bytes, multiples of 16
+    unsigned int * sink = nullptr;
+    int wgs = 0;  // workgroups given to it
+};
+
+// Workgroup w of `wgs` reads its share of the ranges (16 B per thread per step) and folds it into
+// an xor that is stored only if it equals a constant, so the loads are kept.
+__device__ __forceinline__ void prefetch_share(const Prefetch & pf, int w, int nthreads) {
+    unsigned acc = 0u;
+    const size_t stride = (size_t) pf.wgs * nthreads;
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        const uint4 * q = reinterpret_cast<const uint4 *>(pf.p[r]);
+        const size_t n16 = pf.n[r] / 16;
+        for (size_t i = (size_t) w * nthreads + threadIdx.x; i < n16; i += 4 * stride) {
+            uint4 v[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) v[k] = q[min(i + k * stride, n16 - 1)];
+#pragma unroll
+            for (int k = 0; k < 4; k++) acc ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
+        }
+    }
+    if (acc == 0x9e3779b9u) *pf.sink = acc;
+}
+
 // Arguments of the decode-row GEMV (rowgemv.hip): one f32 activation row times a packed Q4_0 /
 // Q8_0 weight, with the node before (prologue) and after (epilogue) the mul_mat in one launch.
 enum { PRO_PLAIN = 0, PRO_NORM = 1, PRO_MERGE = 2 };

@@ -17,6 +17,7 @@
 #include "gcq_common.h"
 
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <string>
@@ -58,7 +59,7 @@ bool attn_decode_fits(int D, int G);
 void launch_attn_decode(const float * q, int64_t q_h, const void * k, int64_t k_h, int64_t k_j, const void * v,
                         int64_t v_h, int64_t v_j, int D, int H, int Hkv, int n_kv, const int * n_kv_dev, float scale,
                         int nsplit, int chunk, int kv_rows, int GS, float * out, float * part_o, float2 * part_ml,
-                        hipStream_t s);
+                        hipStream_t s, const Prefetch * pf);
 int decode_group(int GT, int max_kv);
 void launch_embed_rope(int type, const void * tab, int64_t nrows, int64_t D, const int32_t * idx, float * x,
                        const int32_t * pos, int head_dim, float base, void * cs, hipStream_t s);
@@ -123,6 +124,7 @@ struct Llama {
     bool decode_attn = false;  // one token's attention on k_attn_decode
     DevBuf attn_row;           // its output when it runs unsplit
     DevBuf rope_cs;            // the decode step's rotation table (cos, sin) per rotation index
+    bool prefetch = true;      // attention's spare CUs read the next weights ahead (GCQ_DECODE_PREFETCH=0: off)
     DevBuf ytmp;         // a prompt chunk's mul_mat result in packed row order
     int pos = 0;
     hipGraph_t graph = nullptr;
@@ -199,6 +201,7 @@ struct Llama {
         // One token runs on the decode-row GEMVs when every projection's K fits them: QKV and
         // gate/up are then packed in row pairs (rope pairs, gate/up pairs) for their epilogues.
         decode_attn = attn_decode_fits(c.head_dim, c.n_head / c.n_head_kv);
+        if (const char * e = std::getenv("GCQ_DECODE_PREFETCH")) prefetch = std::string(e) != "0";
         plan_decode = decode_attn ? attn_plan_decode(c.head_dim, c.n_head / c.n_head_kv, c.max_ctx, row_gemv_merge_max())
                                   : attn_plan(1, c.n_head_kv, c.max_ctx);
         fused = row_gemv_fits(c.wtype, c.n_embd) && row_gemv_fits(c.wtype, attn_dim) &&
@@ -372,16 +375,29 @@ struct Llama {
             a.D = c.head_dim;
             a.rope_cs = rope_cs.as<float2>();
             launch_row_gemv(c.wtype, PRO_NORM, EPI_ROPE_KV, a, stream);
-            if (decode_attn)
+            if (decode_attn) {
+                // Spare CUs read this layer's output projection and the next layer's QKV weights
+                // into the Infinity Cache while the attention runs.
+                Prefetch pf;
+                pf.p[0] = tensors[L.wo].buf.as<uint8_t>();
+                pf.n[0] = tensors[L.wo].buf.n & ~(size_t) 15;
+                if (l + 1 < c.n_layer) {
+                    pf.p[1] = tensors[layers[l + 1].qkv].buf.as<uint8_t>();
+                    pf.n[1] = tensors[layers[l + 1].qkv].buf.n & ~(size_t) 15;
+                }
+                pf.sink = counters.as<unsigned int>() + 64;
                 launch_attn_decode(qkv.as<float>(), c.head_dim, kvl, kv_h, c.head_dim, kvl + (size_t) c.n_head_kv * kv_h,
                                    kv_h, c.head_dim, c.head_dim, c.n_head, c.n_head_kv, n_kv, n_kv_dev, scale,
                                    plan.nsplit, plan.chunk, c.max_ctx, decode_group(c.n_head / c.n_head_kv, c.max_ctx),
-                                   attn_row.as<float>(), part_o.as<float>(), part_ml.as<float2>(), stream);
-            else
+                                   attn_row.as<float>(), part_o.as<float>(), part_ml.as<float2>(), stream,
+                                   prefetch ? &pf : nullptr);
+            } else
+            {
                 launch_attn_split(qkv.as<float>(), c.head_dim, qkv_dim, kvl, kv_h, c.head_dim,
                                   kvl + (size_t) c.n_head_kv * kv_h, kv_h, c.head_dim, nullptr, n_kv, c.head_dim, 1,
                                   c.n_head, c.n_head_kv, n_kv, scale, part_o.as<float>(), part_ml.as<float2>(), plan,
                                   n_kv_dev, stream);
+            }
             a = row_args(L.wo);
             a.y = xs;
             a.res = xs;
