@@ -330,7 +330,10 @@ void run_row_r(const RowArgs & a, hipStream_t s) {
     const int waves = cu_count() * 16;
     const int R = EPI != EPI_STORE || (nbl <= 2 && a.N / 2 >= waves) ? 2 : 1;
     const int ng = (a.N + R - 1) / R;
-    const unsigned grid = (unsigned) std::max(1, std::min((ng + 15) / 16, cu_count()));
+    // As many workgroups as give every wavefront the same whole number of groups (no wavefront
+    // left with one more at the end), at most one per CU.
+    const int per_wave = (ng + 16 * cu_count() - 1) / (16 * cu_count());
+    const unsigned grid = (unsigned) std::max(1, (ng + 16 * per_wave - 1) / (16 * per_wave));
     if (R == 2) {
         if (nbl == 1) return go<TYPE, 2, 1, PRO, EPI>(a, grid, s);
         if (nbl == 2) return go<TYPE, 2, 2, PRO, EPI>(a, grid, s);
