@@ -348,16 +348,17 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--mode", choices=["decode", "gemv", "roofline", "sweep"], default="decode",
+    ap.add_argument("--mode", choices=["decode", "gemv", "roofline", "sweep", "gemm"], default="decode",
                     help="roofline: only the roofline leg and a 1 GiB copy (for rocprofv3 --pmc runs); "
-                         "sweep: the GEMV / GEMM / attention configurations, one JSON line each")
+                         "sweep: the GEMV / GEMM / attention configurations, one JSON line each; "
+                         "gemm: the prefill GEMM configuration alone, --steps launches (for counter runs)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for {args.gpus}); multi-GPU sharding is design-only here.",
               file=sys.stderr)
         return 2
-    args.steps = args.steps or {"decode": 128, "gemv": 200, "roofline": 10, "sweep": 1}[args.mode]
+    args.steps = args.steps or {"decode": 128, "gemv": 200, "roofline": 10, "sweep": 1, "gemm": 3}[args.mode]
     args.warmup = args.warmup if args.warmup is not None else 8
 
     import torch
@@ -367,6 +368,21 @@ def main() -> int:
     ops.require_device()
     torch.cuda.set_device(0)
     model = None
+    if args.mode == "gemm":  # Q8_0 K=4096 N=14336, 512 rows: the activation quantized once, K launches
+        w = ops.QuantWeight.quantize(ops.fill_normal((14336, 4096), seed=3, std=0.02), "q8_0")
+        act = ops.quantize_act("q8_0", ops.fill_normal((512, 4096), seed=4))
+        y = torch.empty((512, 14336), dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            ops.mul_mat_q(w, act, 512, out=y)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / args.steps
+        print(json.dumps({"metric": "prefill GEMM TOP/s", "value": round(2 * 512 * 14336 * 4096 / us / 1e6, 1),
+                          "unit": "TOP/s", "us": round(us, 1)}), flush=True)
+        return 0
     if args.mode == "sweep":
         for r in bench_sweep(ops, torch):
             print(json.dumps(r), flush=True)
