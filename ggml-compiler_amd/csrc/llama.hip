@@ -124,7 +124,7 @@ struct Llama {
     bool decode_attn = false;  // one token's attention on k_attn_decode
     DevBuf attn_row;           // its output when it runs unsplit
     DevBuf rope_cs;            // the decode step's rotation table (cos, sin) per rotation index
-    bool prefetch = true;      // attention's spare CUs read the next weights ahead (GCQ_DECODE_PREFETCH=0: off)
+    bool prefetch = false;     // attention's spare CUs read the next weights ahead (GCQ_DECODE_PREFETCH=1: on)
     DevBuf ytmp;         // a prompt chunk's mul_mat result in packed row order
     int pos = 0;
     hipGraph_t graph = nullptr;
@@ -201,7 +201,7 @@ struct Llama {
         // One token runs on the decode-row GEMVs when every projection's K fits them: QKV and
         // gate/up are then packed in row pairs (rope pairs, gate/up pairs) for their epilogues.
         decode_attn = attn_decode_fits(c.head_dim, c.n_head / c.n_head_kv);
-        if (const char * e = std::getenv("GCQ_DECODE_PREFETCH")) prefetch = std::string(e) != "0";
+        if (const char * e = std::getenv("GCQ_DECODE_PREFETCH")) prefetch = std::string(e) == "1";
         plan_decode = decode_attn ? attn_plan_decode(c.head_dim, c.n_head / c.n_head_kv, c.max_ctx, row_gemv_merge_max())
                                   : attn_plan(1, c.n_head_kv, c.max_ctx);
         fused = row_gemv_fits(c.wtype, c.n_embd) && row_gemv_fits(c.wtype, attn_dim) &&

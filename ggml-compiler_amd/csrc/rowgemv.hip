@@ -66,120 +66,183 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
     constexpr int CV = TYPE == T_Q4_0 ? 1 : 2;
     constexpr bool XREG = NBL <= 2;  // activation blocks in registers, else read from LDS per use
     constexpr bool PF = CV * NBL * R <= 8;  // next group's weights prefetched (else: registers spill)
-    // ... and issued before the prologue when the registers hold both groups and the prologue's data
-    constexpr bool PF_EARLY = PF && CV * NBL * R <= 4 && PRO != PRO_MERGE;
     static_assert(EPI == EPI_STORE || R == 2, "row-pair epilogues take two rows per group");
     __shared__ int4 lc[kRowMaxK / 16];
     __shared__ float2 lm[kRowMaxK / 32];
     __shared__ double red[NWV];
 
     const int lane = threadIdx.x & 63;
-    const int nw = gridDim.x * NWV;
     const int ng = (a.N + R - 1) / R;
     const int nb = a.nb;
     const int K = nb * QK;
-    const uint4 * qs = reinterpret_cast<const uint4 *>(a.wqs);
+    // Weights through buffer loads: an offset past the buffer's end reads zeros without a memory
+    // access, so the loads of groups past the last (every wavefront issues the same number of
+    // loads, which lets the compiler count them) cost nothing and leave nothing in flight.
+    // Codes are streamed (non-temporal); the fp16 scales arrive as the aligned 32-bit word holding
+    // them (halves picked where used, so the loads' results need no conversion and no wait until
+    // then; the word of the last scale stays inside the scales' 256-byte-aligned region).
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(a.wqs), 0, (int) ((size_t) a.N * nb * CV * 16), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t *>(a.wd), 0, (int) (((size_t) a.N * nb + 1) / 2 * 4), 0x00020000);
+    constexpr uint32_t kPast = 0x80000000u;  // an offset past every buffer (sizes < 2 GB)
 
     uint4 w[NBL][R][CV];
-    uint32_t d[NBL][R];  // raw fp16 scale bits, one per register: converted where used, so no load waits
+    uint32_t d[NBL][R];
     auto load = [&](int g, uint4 (&wv)[NBL][R][CV], uint32_t (&dv)[NBL][R]) {
+        const bool live = g < ng;
 #pragma unroll
         for (int i = 0; i < NBL; i++) {
-            const int blk = min(lane + 64 * i, nb - 1);  // lanes past the row reload its last block, unused
+            const int blk = lane + 64 * i;  // lanes past the row read zeros, unused
 #pragma unroll
             for (int r = 0; r < R; r++) {
                 const int row = min(g * R + r, a.N - 1);
-                const size_t o = (size_t) row * nb + blk;
+                const uint32_t o = (uint32_t) row * (uint32_t) nb + (uint32_t) blk;
+                const bool in = live && blk < nb;
 #pragma unroll
-                for (int c = 0; c < CV; c++) wv[i][r][c] = qs[o * CV + c];
-                dv[i][r] = a.wd[o];
+                for (int c = 0; c < CV; c++) {
+                    const uint32_t off = in ? (o * CV + c) * 16u : kPast;
+                    const auto t = __builtin_amdgcn_raw_buffer_load_b128(rq, off, 0, 2);  // 2: nt
+                    wv[i][r][c] = make_uint4(t[0], t[1], t[2], t[3]);
+                }
+                dv[i][r] = __builtin_amdgcn_raw_buffer_load_b32(rd, in ? (o >> 1) * 4u : kPast, 0, 0);
             }
         }
     };
 
-    int g = blockIdx.x * NWV + (threadIdx.x >> 6);
-
-    // Order of issue matters: a wavefront's vector loads complete in order, so the prologue's
-    // loads go first and the weights after them; the prologue then waits for its own data only,
-    // while the first row groups' weights stream in. Every load is unconditional (addresses
+    // Wavefronts. PLAIN / NORM: the first XW ("x waves") only turn the activation row into Q8_0
+    // codes in LDS; the other CW = 16 - XW walk the row groups. A CU's vector memory requests
+    // queue in issue order and a wavefront's loads complete in order, so the x waves issue their
+    // loads first and the workgroup meets before any weight load is issued: the activation row
+    // is not queued behind the CU's weight stream, and the compute waves start that stream at
+    // once. The compute waves take the codes through an LDS counter, not a workgroup barrier
+    // (which would also wait for wavefronts stalled on issuing loads into a full memory queue).
+    // MERGE: every wavefront merges 4 values (K <= 4096) and then walks row groups; its weights
+    // are issued before the prologue.
+    //
+    // x thread t (of 64 XW) takes half blocks t, t + 64 XW, ... (16 values each), so the
+    // prologue's arithmetic sits on a few wavefronts. Weight loads are unconditional (addresses
     // clamped into range, values past the end discarded), so the compiler knows how many are in
     // flight and waits for the oldest only.
-    //
-    // PLAIN / NORM: thread t takes values [16t, 16t + 16), half a Q8_0 block, so the prologue's
-    // arithmetic sits on K/1024 wavefronts (one per SIMD at K = 4096) rather than on all sixteen.
-    // MERGE: 4 values per thread (K <= 4096), the partials of up to kMergeMax splits in registers.
     constexpr bool MERGE = PRO == PRO_MERGE;
-    float4 xv[MERGE ? 1 : 4], nv[PRO == PRO_NORM ? 4 : 1];
-    float2 mlv[MERGE ? kMergeMax : 1];
-    float4 pov[MERGE ? kMergeMax : 1];
-    if constexpr (!MERGE) {
-        const int e = min((int) threadIdx.x * 16, K - 16);
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            xv[c] = *reinterpret_cast<const float4 *>(a.x + e + 4 * c);
-            if constexpr (PRO == PRO_NORM) nv[c] = *reinterpret_cast<const float4 *>(a.norm_w + e + 4 * c);
-        }
-    } else {
-        const int e = min((int) threadIdx.x * 4, K - 4);
-        const int h = e / a.D;
-        const float2 * ml = a.part_ml + (int64_t) h * a.nsplit;
-        const float * po = a.part_o + (int64_t) h * a.nsplit * a.D + e % a.D;
-#pragma unroll
-        for (int j = 0; j < kMergeMax; j++) {
-            const int jc = min(j, a.nsplit - 1);
-            mlv[j] = ml[jc];
-            pov[j] = *reinterpret_cast<const float4 *>(po + (int64_t) jc * a.D);
-        }
-#pragma unroll
-        for (int j = 0; j < kMergeMax; j++)
-            if (j >= a.nsplit) mlv[j] = make_float2(-INFINITY, 0.0f);  // splits past the last: none
+    constexpr int XWMAX = (PRO == PRO_NORM && NBL > 4) ? 8 : 4;  // x waves at most
+    constexpr int RMAX = MERGE ? 1 : (2 * NBL + XWMAX - 1) / XWMAX;  // half blocks per x thread at most
+    const int wave = threadIdx.x >> 6;
+    const int XW = MERGE ? NWV : min(XWMAX, (K + 1023) / 1024);
+    const int rounds = MERGE ? 1 : (K + XW * 1024 - 1) / (XW * 1024);
+    const int CW = MERGE ? NWV : NWV - XW;  // compute waves (host: row_gemv_compute_waves)
+    const bool xw = !MERGE && wave < XW;  // an x wave of PLAIN / NORM
+    int g = blockIdx.x * CW + (MERGE ? wave : max(wave - XW, 0));
+    const int nw = gridDim.x * CW;
+
+    __shared__ unsigned int s_flag[2];  // x waves done with: [0] their norm partial, [1] their codes
+    if (threadIdx.x == 0) {
+        s_flag[0] = 0u;
+        s_flag[1] = 0u;
     }
     const int p_tok = EPI == EPI_ROPE_KV ? *a.pos : 0;
     const int half = a.D / 2;
     const int nqk = (a.H + a.Hkv) * half;  // row-pair groups of q and k (rotated)
     float2 cs_first = make_float2(0.0f, 0.0f);  // the rotation of this wave's first group
-    if constexpr (EPI == EPI_ROPE_KV) cs_first = a.rope_cs[min(g, nqk - 1) % half];
-    __builtin_amdgcn_sched_barrier(0);  // keep the prologue's loads ahead of the weights'
-
     uint4 wn[NBL][R][CV];
     uint32_t dn[NBL][R];
-    load(min(g, ng - 1), w, d);  // waves past the last group load it again and never use it
-    if constexpr (PF_EARLY) load(min(g + nw, ng - 1), wn, dn);
 
-    // ---- prologue: the row into LDS as Q8_0
     if constexpr (!MERGE) {
-        const int t = threadIdx.x;
-        const bool act = t * 16 < K;
-        float v[16];
+        // The x waves' path ends in this block (their loads never meet the compute waves' code,
+        // whose waits would otherwise count them).
+        if (xw) {
+            float4 xv[RMAX][4], nv[PRO == PRO_NORM ? RMAX : 1][4];
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
-            v[4 * c] = act ? xv[c].x : 0.0f;
-            v[4 * c + 1] = act ? xv[c].y : 0.0f;
-            v[4 * c + 2] = act ? xv[c].z : 0.0f;
-            v[4 * c + 3] = act ? xv[c].w : 0.0f;
+            for (int r = 0; r < RMAX; r++) {
+                if (r < rounds) {
+                    const int e = min(((int) threadIdx.x + r * XW * 64) * 16, K - 16);
+#pragma unroll
+                    for (int c = 0; c < 4; c++) {
+                        xv[r][c] = *reinterpret_cast<const float4 *>(a.x + e + 4 * c);
+                        if constexpr (PRO == PRO_NORM)
+                            nv[r][c] = *reinterpret_cast<const float4 *>(a.norm_w + e + 4 * c);
+                    }
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_barrier();  // the x waves' loads are issued before any weight load
+            __builtin_amdgcn_sched_barrier(0);
+            const int t = threadIdx.x;
+            float v[RMAX][16];
+#pragma unroll
+            for (int r = 0; r < RMAX; r++) {
+                const bool act = r < rounds && (t + r * XW * 64) * 16 < K;
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    v[r][4 * c] = act ? xv[r][c].x : 0.0f;
+                    v[r][4 * c + 1] = act ? xv[r][c].y : 0.0f;
+                    v[r][4 * c + 2] = act ? xv[r][c].z : 0.0f;
+                    v[r][4 * c + 3] = act ? xv[r][c].w : 0.0f;
+                }
+            }
+            if constexpr (PRO == PRO_NORM) {
+                // ggml_rms_norm: squares rounded to f32, summed in double, the mean rounded to f32
+                double ss = 0.0;
+#pragma unroll
+                for (int r = 0; r < RMAX; r++)
+#pragma unroll
+                    for (int j = 0; j < 16; j++) ss += (double) (v[r][j] * v[r][j]);
+                ss = wave_sum_d(ss);
+                if (lane == 0) {
+                    red[wave] = ss;
+                    lds_signal(&s_flag[0]);
+                }
+                lds_wait(&s_flag[0], XW);
+                double tot = 0.0;
+#pragma unroll
+                for (int i = 0; i < XWMAX; i++)
+                    if (i < XW) tot += red[i];
+                const float scale = 1.0f / sqrtf((float) (tot / (double) K) + a.eps);
+#pragma unroll
+                for (int r = 0; r < RMAX; r++)
+#pragma unroll
+                    for (int c = 0; c < 4; c++) {
+                        v[r][4 * c] = (v[r][4 * c] * scale) * nv[r][c].x;
+                        v[r][4 * c + 1] = (v[r][4 * c + 1] * scale) * nv[r][c].y;
+                        v[r][4 * c + 2] = (v[r][4 * c + 2] * scale) * nv[r][c].z;
+                        v[r][4 * c + 3] = (v[r][4 * c + 3] * scale) * nv[r][c].w;
+                    }
+            }
+#pragma unroll
+            for (int r = 0; r < RMAX; r++) {
+                const int hb = t + r * XW * 64;  // half block; its pair is in the neighbouring lane
+                if (r < rounds && hb * 16 < K)
+                    q8_half_block_store(v[r], reinterpret_cast<int8_t *>(lc) + (hb / 2) * 32, lm + hb / 2, hb & 1);
+            }
+            if (lane == 0) lds_signal(&s_flag[1]);
+            return;
         }
-        if constexpr (PRO == PRO_NORM) {
-            // ggml_rms_norm: squares rounded to f32, summed in double, the mean rounded to f32
-            double ss = 0.0;
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (EPI == EPI_ROPE_KV) cs_first = a.rope_cs[min(g, nqk - 1) % half];
+        load(g, w, d);
+    } else {
+        float2 mlv[kMergeMax];
+        float4 pov[kMergeMax];
+        const int e0 = min((int) threadIdx.x * 4, K - 4);
+        const int h = e0 / a.D;
+        const float2 * ml = a.part_ml + (int64_t) h * a.nsplit;
+        const float * po = a.part_o + (int64_t) h * a.nsplit * a.D + e0 % a.D;
 #pragma unroll
-            for (int j = 0; j < 16; j++) ss += (double) (v[j] * v[j]);
-            ss = wave_sum_d(ss);
-            if (lane == 0) red[threadIdx.x >> 6] = ss;
-            __syncthreads();
-            double tot = 0.0;
-#pragma unroll
-            for (int i = 0; i < NWV; i++) tot += red[i];
-            const float scale = 1.0f / sqrtf((float) (tot / (double) K) + a.eps);
-#pragma unroll
-            for (int c = 0; c < 4; c++) {
-                v[4 * c] = (v[4 * c] * scale) * nv[c].x;
-                v[4 * c + 1] = (v[4 * c + 1] * scale) * nv[c].y;
-                v[4 * c + 2] = (v[4 * c + 2] * scale) * nv[c].z;
-                v[4 * c + 3] = (v[4 * c + 3] * scale) * nv[c].w;
+        for (int j = 0; j < kMergeMax; j++) {
+            if (j < a.nsplit) {
+                mlv[j] = ml[j];
+                pov[j] = *reinterpret_cast<const float4 *>(po + (int64_t) j * a.D);
+            } else {
+                mlv[j] = make_float2(-INFINITY, 0.0f);  // splits past the last: none
             }
         }
-        if (act) q8_half_block_store(v, reinterpret_cast<int8_t *>(lc) + (t / 2) * 32, lm + t / 2, t & 1);
-    } else {
+        if constexpr (EPI == EPI_ROPE_KV) cs_first = a.rope_cs[min(g, nqk - 1) % half];
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();  // the partials' loads are issued before any weight load
+        __builtin_amdgcn_sched_barrier(0);
+        load(g, w, d);
         // The merged attention output (k_merge_q8's arithmetic): sum_i e^(m_i - M) o_i /
         // sum_i e^(m_i - M) l_i in split order, splits with m_i = -inf left out, 0 if none.
         const int e = threadIdx.x * 4;
@@ -207,9 +270,10 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
             o.w = L == 0.0f ? 0.0f : o.w / L;
             q8_block_store(o, reinterpret_cast<int8_t *>(lc) + (e & ~31), lm + e / 32, (e / 4) & 7);
         }
+        if (lane == 0) lds_signal(&s_flag[1]);
     }
-    __syncthreads();
-    if constexpr (PF && !PF_EARLY) load(min(g + nw, ng - 1), wn, dn);
+    lds_wait(&s_flag[1], XW);
+    if constexpr (PF) load(g + nw, wn, dn);
 
     int4 xa[XREG ? NBL : 1], xb[XREG ? NBL : 1];
     float2 xm[XREG ? NBL : 1];
@@ -251,7 +315,10 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
                 int sdot;
                 if constexpr (TYPE == T_Q4_0) sdot = dot_blk_q4_0(wv[i][r][0], ca, cb, __float_as_int(cm.y));
                 else sdot = dot_blk_q8_0(wv[i][r][0], wv[i][r][CV - 1], ca, cb);
-                acc[r] += ((float) sdot * h2f((uint16_t) dv[i][r])) * cm.x;
+                // scale index row * nb + blk: its parity picks the half (blk's parity is the lane's)
+                const int row = min(gg * R + r, a.N - 1);
+                const uint32_t sh = (uint32_t) (((lane ^ (row & nb)) & 1) << 4);
+                acc[r] += ((float) sdot * h2f((uint16_t) (dv[i][r] >> sh))) * cm.x;
             }
         }
         float v[R];
@@ -294,11 +361,11 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
         // weights are loaded two groups ahead and never copied between registers.
         while (g < ng) {
             group(g, w, d);
-            load(min(g + 2 * nw, ng - 1), w, d);
+            load(g + 2 * nw, w, d);
             g += nw;
             if (g >= ng) break;
             group(g, wn, dn);
-            load(min(g + 2 * nw, ng - 1), wn, dn);
+            load(g + 2 * nw, wn, dn);
             g += nw;
         }
     } else {
@@ -324,16 +391,26 @@ void go(const RowArgs & a, unsigned grid, hipStream_t s) {
 // Two rows per group when there are enough groups to give every wavefront of the grid one and
 // their weights fit the registers (K <= 4096), else one row per group; the row-pair epilogues
 // always take two. Long rows (K > 4096): lanes hold up to 8 blocks of a row.
+// Row-group wavefronts of a workgroup (the kernel's CW): all 16 for MERGE, else 16 less the x
+// waves that build the prologue.
+int row_gemv_compute_waves(int pro, int nb) {
+    if (pro == PRO_MERGE) return 16;
+    const int nbl = (nb + 63) / 64, K = nb * QK;
+    const int xwmax = (pro == PRO_NORM && nbl > 4) ? 8 : 4;
+    return 16 - std::min(xwmax, (K + 1023) / 1024);
+}
+
 template <int TYPE, int PRO, int EPI>
 void run_row_r(const RowArgs & a, hipStream_t s) {
     const int nbl = (a.nb + 63) / 64;
-    const int waves = cu_count() * 16;
+    const int cw = row_gemv_compute_waves(PRO, a.nb);
+    const int waves = cu_count() * cw;
     const int R = EPI != EPI_STORE || (nbl <= 2 && a.N / 2 >= waves) ? 2 : 1;
     const int ng = (a.N + R - 1) / R;
-    // As many workgroups as give every wavefront the same whole number of groups (no wavefront
-    // left with one more at the end), at most one per CU.
-    const int per_wave = (ng + 16 * cu_count() - 1) / (16 * cu_count());
-    const unsigned grid = (unsigned) std::max(1, (ng + 16 * per_wave - 1) / (16 * per_wave));
+    // As many workgroups as give every compute wavefront the same whole number of groups (no
+    // wavefront left with one more at the end), at most one per CU.
+    const int per_wave = (ng + waves - 1) / waves;
+    const unsigned grid = (unsigned) std::max(1, (ng + cw * per_wave - 1) / (cw * per_wave));
     if (R == 2) {
         if (nbl == 1) return go<TYPE, 2, 1, PRO, EPI>(a, grid, s);
         if (nbl == 2) return go<TYPE, 2, 2, PRO, EPI>(a, grid, s);
@@ -372,10 +449,16 @@ bool row_gemv_fits(int type, int64_t K) {
     return (type == T_Q4_0 || type == T_Q8_0) && K % QK == 0 && K > 0 && K <= kRowMaxK;
 }
 
+// The weight's codes must stay below 2 GB (32-bit buffer offsets).
+static bool row_gemv_rows_fit(int type, int64_t N, int nb) {
+    return N > 0 && (uint64_t) N * (uint64_t) nb * (type == T_Q4_0 ? 16u : 32u) < 0x80000000ull;
+}
+
 int row_gemv_merge_max() { return kMergeMax; }
 
 void launch_row_gemv(int type, int pro, int epi, const RowArgs & a, hipStream_t s) {
     require(row_gemv_fits(type, (int64_t) a.nb * QK), "row gemv: weight type or K not supported");
+    require(row_gemv_rows_fit(type, a.N, a.nb), "row gemv: weight of 2 GB or more");
     require(epi == EPI_STORE || a.N % 2 == 0, "row gemv: row-pair epilogue needs an even row count");
     require(pro != PRO_MERGE || (a.nsplit >= 1 && a.nsplit <= kMergeMax && a.D % 4 == 0 && a.nb * QK <= 4096),
             "row gemv: merge of 1.." + std::to_string(kMergeMax) + " splits, K <= 4096");
