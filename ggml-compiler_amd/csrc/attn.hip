@@ -268,15 +268,37 @@ __global__ __launch_bounds__(NW * 64) void k_attn_decode(int GT, const float * _
     const int w0 = min(chunk, wave * per_wave), w1 = min(chunk, w0 + per_wave);
     const int len = max(0, min(n_kv - j0, chunk));  // keys of this split below n_kv
 
-    half2_t qh[G][4];
+    // q, then the first batch of K / V rows, are in flight before q is converted (the K / V
+    // loads do not wait for q).
+    float4 qf[G][2];
 #pragma unroll
     for (int g = 0; g < G; g++) {
         const float * qp = q + (int64_t) (h0 + g) * q_h + 8 * sub;
+        qf[g][0] = *reinterpret_cast<const float4 *>(qp);
+        qf[g][1] = *reinterpret_cast<const float4 *>(qp + 4);
+    }
+    const uint16_t * kb = k + (int64_t) hk * k_h + 8 * sub;
+    const uint16_t * vb = v + (int64_t) hk * v_h + 8 * sub;
+    uint4 kr[NB], vr[NB];
+    auto load = [&](int base) {
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            const int64_t row = min(j0 + base + b * KPW + slot, kv_rows - 1);
+            kr[b] = *reinterpret_cast<const uint4 *>(kb + row * k_j);
+            vr[b] = *reinterpret_cast<const uint4 *>(vb + row * v_j);
+        }
+    };
+    if (w0 < w1) load(w0);
+    __builtin_amdgcn_sched_barrier(0);  // all of the batch's loads issued before any wait
+    half2_t qh[G][4];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
 #pragma unroll
         for (int c = 0; c < 4; c++) {
+            const float4 f = qf[g][c / 2];
             half2_t t;
-            t.x = (_Float16) qp[2 * c];
-            t.y = (_Float16) qp[2 * c + 1];
+            t.x = (_Float16) ((c & 1) ? f.z : f.x);
+            t.y = (_Float16) ((c & 1) ? f.w : f.y);
             qh[g][c] = t;
         }
     }
@@ -288,16 +310,9 @@ __global__ __launch_bounds__(NW * 64) void k_attn_decode(int GT, const float * _
 #pragma unroll
         for (int c = 0; c < 8; c++) acc[g][c] = 0.0f;
     }
-    const uint16_t * kb = k + (int64_t) hk * k_h + 8 * sub;
-    const uint16_t * vb = v + (int64_t) hk * v_h + 8 * sub;
     for (int base = w0; base < w1; base += NB * KPW) {
-        uint4 kr[NB], vr[NB];
-#pragma unroll
-        for (int b = 0; b < NB; b++) {
-            const int64_t row = min(j0 + base + b * KPW + slot, kv_rows - 1);
-            kr[b] = *reinterpret_cast<const uint4 *>(kb + row * k_j);
-            vr[b] = *reinterpret_cast<const uint4 *>(vb + row * v_j);
-        }
+        if (base != w0) load(base);
+        __builtin_amdgcn_sched_barrier(0);
         float vf[NB][8];  // this lane's 8 dims of each key's V row, converted once for all G heads
 #pragma unroll
         for (int b = 0; b < NB; b++)
