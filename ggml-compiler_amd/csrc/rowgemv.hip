@@ -118,7 +118,8 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
     // once. The compute waves take the codes through an LDS counter, not a workgroup barrier
     // (which would also wait for wavefronts stalled on issuing loads into a full memory queue).
     // MERGE: every wavefront merges 4 values (K <= 4096) and then walks row groups; its weights
-    // are issued before the prologue.
+    // are issued before the prologue. Long rows (K > 8192, few groups per wavefront): the x waves
+    // take row groups too, the last ones of the workgroup, loaded once their prologue is done.
     //
     // x thread t (of 64 XW) takes half blocks t, t + 64 XW, ... (16 values each), so the
     // prologue's arithmetic sits on a few wavefronts. Weight loads are unconditional (addresses
@@ -130,9 +131,10 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
     const int wave = threadIdx.x >> 6;
     const int XW = MERGE ? NWV : min(XWMAX, (K + 1023) / 1024);
     const int rounds = MERGE ? 1 : (K + XW * 1024 - 1) / (XW * 1024);
-    const int CW = MERGE ? NWV : NWV - XW;  // compute waves (host: row_gemv_compute_waves)
+    constexpr bool XC = !MERGE && NBL > 4;  // x waves compute too
+    const int CW = (MERGE || XC) ? NWV : NWV - XW;  // compute waves (host: row_gemv_compute_waves)
     const bool xw = !MERGE && wave < XW;  // an x wave of PLAIN / NORM
-    int g = blockIdx.x * CW + (MERGE ? wave : max(wave - XW, 0));
+    int g = blockIdx.x * CW + (MERGE ? wave : XC ? (wave + NWV - XW) % NWV : max(wave - XW, 0));
     const int nw = gridDim.x * CW;
 
     __shared__ unsigned int s_flag[2];  // x waves done with: [0] their norm partial, [1] their codes
@@ -215,11 +217,12 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
                     q8_half_block_store(v[r], reinterpret_cast<int8_t *>(lc) + (hb / 2) * 32, lm + hb / 2, hb & 1);
             }
             if (lane == 0) lds_signal(&s_flag[1]);
-            return;
+            if constexpr (!XC) return;
+        } else {
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
         }
-        __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_barrier();
-        __builtin_amdgcn_sched_barrier(0);
         if constexpr (EPI == EPI_ROPE_KV) cs_first = a.rope_cs[min(g, nqk - 1) % half];
         load(g, w, d);
     } else {
@@ -391,11 +394,11 @@ void go(const RowArgs & a, unsigned grid, hipStream_t s) {
 // Two rows per group when there are enough groups to give every wavefront of the grid one and
 // their weights fit the registers (K <= 4096), else one row per group; the row-pair epilogues
 // always take two. Long rows (K > 4096): lanes hold up to 8 blocks of a row.
-// Row-group wavefronts of a workgroup (the kernel's CW): all 16 for MERGE, else 16 less the x
-// waves that build the prologue.
+// Row-group wavefronts of a workgroup (the kernel's CW): all 16 for MERGE and for rows of more
+// than 8192 values, else 16 less the x waves that build the prologue.
 int row_gemv_compute_waves(int pro, int nb) {
-    if (pro == PRO_MERGE) return 16;
     const int nbl = (nb + 63) / 64, K = nb * QK;
+    if (pro == PRO_MERGE || nbl > 4) return 16;
     const int xwmax = (pro == PRO_NORM && nbl > 4) ? 8 : 4;
     return 16 - std::min(xwmax, (K + 1023) / 1024);
 }
