@@ -123,6 +123,7 @@ struct RowArgs {
     uint16_t * vc;
     int64_t ctx;
     int H, Hkv, D;
+    int xc;  // set by launch_row_gemv: the x waves take row groups too (PLAIN / NORM)
 };
 
 void launch_row_gemv(int type, int pro, int epi, const RowArgs & a, hipStream_t s);

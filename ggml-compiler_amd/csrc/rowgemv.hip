@@ -118,8 +118,9 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
     // once. The compute waves take the codes through an LDS counter, not a workgroup barrier
     // (which would also wait for wavefronts stalled on issuing loads into a full memory queue).
     // MERGE: every wavefront merges 4 values (K <= 4096) and then walks row groups; its weights
-    // are issued before the prologue. Long rows (K > 8192, few groups per wavefront): the x waves
-    // take row groups too, the last ones of the workgroup, loaded once their prologue is done.
+    // are issued before the prologue. With few groups per wavefront (long rows, or groups that
+    // all 16 wavefronts of every CU take in one round) the x waves take row groups too, the last
+    // ones of the workgroup, loaded once their prologue is done (a.xc, chosen by the dispatch).
     //
     // x thread t (of 64 XW) takes half blocks t, t + 64 XW, ... (16 values each), so the
     // prologue's arithmetic sits on a few wavefronts. Weight loads are unconditional (addresses
@@ -131,8 +132,8 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
     const int wave = threadIdx.x >> 6;
     const int XW = MERGE ? NWV : min(XWMAX, (K + 1023) / 1024);
     const int rounds = MERGE ? 1 : (K + XW * 1024 - 1) / (XW * 1024);
-    constexpr bool XC = !MERGE && NBL > 4;  // x waves compute too
-    const int CW = (MERGE || XC) ? NWV : NWV - XW;  // compute waves (host: row_gemv_compute_waves)
+    const bool XC = !MERGE && a.xc != 0;  // x waves compute too
+    const int CW = (MERGE || XC) ? NWV : NWV - XW;  // compute waves (host: run_row_r's cw)
     const bool xw = !MERGE && wave < XW;  // an x wave of PLAIN / NORM
     int g = blockIdx.x * CW + (MERGE ? wave : XC ? (wave + NWV - XW) % NWV : max(wave - XW, 0));
     const int nw = gridDim.x * CW;
@@ -217,7 +218,7 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
                     q8_half_block_store(v[r], reinterpret_cast<int8_t *>(lc) + (hb / 2) * 32, lm + hb / 2, hb & 1);
             }
             if (lane == 0) lds_signal(&s_flag[1]);
-            if constexpr (!XC) return;
+            if (!XC) return;
         } else {
             __builtin_amdgcn_sched_barrier(0);
             __builtin_amdgcn_s_barrier();
@@ -391,25 +392,30 @@ void go(const RowArgs & a, unsigned grid, hipStream_t s) {
     k_row_gemv<TYPE, R, NBL, PRO, EPI><<<grid, 1024, 0, s>>>(a);
 }
 
-// Two rows per group when there are enough groups to give every wavefront of the grid one and
-// their weights fit the registers (K <= 4096), else one row per group; the row-pair epilogues
-// always take two. Long rows (K > 4096): lanes hold up to 8 blocks of a row.
-// Row-group wavefronts of a workgroup (the kernel's CW): all 16 for MERGE and for rows of more
-// than 8192 values, else 16 less the x waves that build the prologue.
-int row_gemv_compute_waves(int pro, int nb) {
+// Two rows per group when there are enough groups to give every compute wavefront of the grid
+// one and their weights fit the registers (K <= 4096), else one row per group; the row-pair
+// epilogues always take two. Long rows (K > 4096): lanes hold up to 8 blocks of a row.
+// x waves of a workgroup (the kernel's XW): none for MERGE, else up to 4 (8 for long NORM rows).
+int row_gemv_x_waves(int pro, int nb) {
+    if (pro == PRO_MERGE) return 0;
     const int nbl = (nb + 63) / 64, K = nb * QK;
-    if (pro == PRO_MERGE || nbl > 4) return 16;
     const int xwmax = (pro == PRO_NORM && nbl > 4) ? 8 : 4;
-    return 16 - std::min(xwmax, (K + 1023) / 1024);
+    return std::min(xwmax, (K + 1023) / 1024);
 }
 
 template <int TYPE, int PRO, int EPI>
-void run_row_r(const RowArgs & a, hipStream_t s) {
+void run_row_r(const RowArgs & a0, hipStream_t s) {
+    RowArgs a = a0;
     const int nbl = (a.nb + 63) / 64;
-    const int cw = row_gemv_compute_waves(PRO, a.nb);
-    const int waves = cu_count() * cw;
-    const int R = EPI != EPI_STORE || (nbl <= 2 && a.N / 2 >= waves) ? 2 : 1;
+    const int cus = cu_count();
+    const int xw = row_gemv_x_waves(PRO, a.nb);
+    const int R = EPI != EPI_STORE || (nbl <= 2 && a.N / 2 >= cus * (16 - xw)) ? 2 : 1;
     const int ng = (a.N + R - 1) / R;
+    // The x waves compute too for long rows and when all 16 wavefronts of every CU take the
+    // groups in one round but the compute waves alone would need two.
+    a.xc = PRO != PRO_MERGE && (nbl > 4 || (ng <= 16 * cus && ng > (16 - xw) * cus));
+    const int cw = (PRO == PRO_MERGE || a.xc) ? 16 : 16 - xw;  // the kernel's CW
+    const int waves = cus * cw;
     // As many workgroups as give every compute wavefront the same whole number of groups (no
     // wavefront left with one more at the end), at most one per CU.
     const int per_wave = (ng + waves - 1) / waves;
