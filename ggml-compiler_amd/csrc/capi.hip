@@ -53,9 +53,14 @@ void launch_fill_ids(int32_t * dst, int64_t n, uint64_t seed, uint64_t offset, i
 
 namespace {
 thread_local std::string g_error;
+thread_local uint64_t g_errors = 0;
 }
 
-void set_error(const std::string & msg) { g_error = msg; }
+void set_error(const std::string & msg) {
+    g_error = msg;
+    g_errors++;
+}
+uint64_t error_count() { return g_errors; }
 const char * last_error() { return g_error.c_str(); }
 
 void check_hip(hipError_t e, const char * what) {
@@ -169,6 +174,8 @@ extern "C" {
 const char * gcq_version(void) { return "libgcq 0.1 (gfx950 HIP)"; }
 
 const char * gcq_last_error(void) { return last_error(); }
+
+uint64_t gcq_error_count(void) { return error_count(); }
 
 int gcq_device_count(void) {
     int n = 0;

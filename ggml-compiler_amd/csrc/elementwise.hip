@@ -9,6 +9,9 @@
 //  swiglu    ggml_swiglu_split (runtime/src/ops.cpp:251-258)
 //  add, mul  ggml_add / ggml_mul with a broadcast second operand
 //  argmax    ggml_argmax (runtime/src/ops.cpp:293-300)
+//  cpy       ggml_cpy / ggml_cont / ggml_cast between f32 and f16 at any strides (runtime/src/ops.cpp:101,
+//            :344-348)
+//  scale     ggml_scale / ggml_scale_bias (runtime/src/ops.cpp:121-131)
 // All are HBM- or launch-bound and move whole rows with 16-byte accesses where the shapes allow.
 #include "gcq_common.h"
 
@@ -177,6 +180,38 @@ __global__ void k_fill_ids(int32_t * __restrict__ dst, int64_t n, uint64_t seed,
     dst[i] = (int32_t) (rnd64(seed, offset + (uint64_t) i) % (uint64_t) vocab);
 }
 
+// ----------------------------------------------------------------------------- cpy, scale
+
+// Element i in row-major order of the logical shape: source element (shape sne, byte strides snb)
+// to destination element (dne, dnb); the two shapes have the same element count. f32 / f16 either
+// side, f32 -> f16 rounding to nearest even as ggml's conversion.
+__global__ void k_cpy(const uint8_t * __restrict__ src, int st, uint8_t * __restrict__ dst, int dt, Cpy4 g, int64_t n) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    int64_t r = i, so = 0, dof = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        so += (r % g.sne[k]) * g.snb[k];
+        r /= g.sne[k];
+    }
+    r = i;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        dof += (r % g.dne[k]) * g.dnb[k];
+        r /= g.dne[k];
+    }
+    const float v = st == T_F32 ? *reinterpret_cast<const float *>(src + so)
+                                : h2f(*reinterpret_cast<const uint16_t *>(src + so));
+    if (dt == T_F32) *reinterpret_cast<float *>(dst + dof) = v;
+    else *reinterpret_cast<uint16_t *>(dst + dof) = f2h(v);
+}
+
+__global__ void k_scale(const float * __restrict__ x, float * __restrict__ y, int64_t n, float sc, float b) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    y[i] = x[i] * sc + b;
+}
+
 // ------------------------------------------------------------------------- host launchers
 
 static inline unsigned nblk(int64_t n, int t) { return (unsigned) ((n + t - 1) / t); }
@@ -231,6 +266,18 @@ void launch_argmax(const float * x, int64_t ldx, int64_t rows, int64_t n, int32_
     if (rows == 0) return;
     k_argmax<<<(unsigned) rows, 256, 0, s>>>(x, ldx, (int) n, out);
     check_launch("argmax");
+}
+
+void launch_cpy(const void * src, int st, void * dst, int dt, const Cpy4 & g, int64_t n, hipStream_t s) {
+    if (n == 0) return;
+    k_cpy<<<nblk(n, 256), 256, 0, s>>>((const uint8_t *) src, st, (uint8_t *) dst, dt, g, n);
+    check_launch("cpy");
+}
+
+void launch_scale(const float * x, float * y, int64_t n, float sc, float b, hipStream_t s) {
+    if (n == 0) return;
+    k_scale<<<nblk(n, 256), 256, 0, s>>>(x, y, n, sc, b);
+    check_launch("scale");
 }
 
 void launch_fill_normal(float * dst, int64_t n, uint64_t seed, uint64_t offset, float stddev, hipStream_t s) {

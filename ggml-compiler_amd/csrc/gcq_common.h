@@ -33,6 +33,7 @@ constexpr int QKK = 256;  // K-quant super-block
 
 void set_error(const std::string & msg);
 const char * last_error();
+uint64_t error_count();  // errors recorded by this thread so far
 
 struct Fail {
     std::string msg;
@@ -127,6 +128,13 @@ struct RowArgs {
 };
 
 void launch_row_gemv(int type, int pro, int epi, const RowArgs & a, hipStream_t s);
+
+// Shapes and byte strides of a strided copy / conversion (elementwise.hip).
+struct Cpy4 {
+    int64_t sne[4], snb[4], dne[4], dnb[4];
+};
+void launch_cpy(const void * src, int st, void * dst, int dt, const Cpy4 & g, int64_t n, hipStream_t s);
+void launch_scale(const float * x, float * y, int64_t n, float sc, float b, hipStream_t s);
 bool row_gemv_fits(int type, int64_t K);
 int row_gemv_merge_max();
 

@@ -1,0 +1,1192 @@
+// ggml_backend.hip - the HIP backend of the ggml API subset (include/ggml-backend.h,
+// include/ggml-alloc.h): device buffers, the graph allocator, and graph execution on libgcq's
+// kernels.
+//
+// Execution plans a graph into launch steps (one per node, or one per fusion chain), then runs the
+// steps on the backend's stream. Chains (find_chains) fold the nodes the reference's decoder graph
+// emits around each projection (runtime/src/ops.cpp:107-148, ggml_compiler/llm.py:361-444) into the
+// launches libgcq has for them:
+//   rms_norm -> mul(w)                     one rms_norm launch with the weight
+//   rms_norm -> mul(w) -> mul_mat [-> add]  one decode-row GEMV normalizing x itself (one row), or
+//                                          rms_norm + Q8_0 conversion, then the GEMV / GEMM
+//   swiglu -> mul_mat [-> add]             swiglu + Q8_0 conversion, then the GEMV / GEMM
+//   mul_mat -> add                         the residual added in the GEMV / GEMM epilogue
+// A chain is formed only where each intermediate has exactly one reader and is not flagged as an
+// output, so no node outside the chain sees the difference. The allocator uses the same chains:
+// a chain's inputs stay live until the chain's last node, where its work runs.
+//
+// The steps' launches are captured into a HIP graph per ggml_cgraph and replayed while the plan
+// (every kernel argument) is unchanged; device inputs set with ggml_backend_tensor_set between
+// computes are read by the replay.
+#include "gcq_common.h"
+#include "ggml_impl.h"
+
+#include <algorithm>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <unordered_map>
+
+namespace gcq {
+
+void launch_pack(int type, const void * src, int64_t nrows, int64_t k, void * dst, hipStream_t s);
+void launch_unpack(int type, const void * src, int64_t nrows, int64_t k, void * dst, hipStream_t s);
+void launch_act_quant(int wtype, const float * x, int64_t ldx, int64_t B, int64_t k, void * act, hipStream_t s);
+void launch_gemv(int type, const void * w, int64_t N, int64_t K, const void * act, int64_t B, float * y, int64_t ldy,
+                 hipStream_t s, const float * res);
+void launch_gemm(int type, const void * w, int64_t N, int64_t K, const void * act, int64_t M, float * y, int64_t ldy,
+                 hipStream_t s, const float * res);
+size_t attn_workspace(int Sq, int H, int Hkv, int Dv, int n_kv);
+void launch_flash_attn(const float * q, int64_t q_h, int64_t q_s, const void * k, int64_t k_h, int64_t k_j,
+                       const void * v, int64_t v_h, int64_t v_j, const void * mask, int64_t m_s, float * out, int D,
+                       int Dv, int Sq, int H, int Hkv, int n_kv, float scale, void * ws, size_t ws_size, hipStream_t s);
+void launch_rms_norm(const float * x, int64_t ldx, float * y, int64_t ldy, const float * w, int64_t rows, int64_t n,
+                     float eps, hipStream_t s);
+void launch_rmsnorm_q8(const float * x, int64_t ldx, const float * w, float eps, int64_t rows, int64_t n, void * act,
+                       hipStream_t s);
+void launch_swiglu_q8(const float * g, const float * u, int64_t ld, int64_t n, int64_t rows, void * act,
+                      hipStream_t s);
+void launch_rope_neox(const float * x, int64_t sx_s, int64_t sx_h, float * out, int64_t so_s, int64_t so_h,
+                      const int32_t * pos, int64_t D, int64_t H, int64_t S, int n_dims, float freq_base,
+                      float freq_scale, float attn_factor, const float * ff, hipStream_t s);
+void launch_set_rows_f16(void * dst, int64_t dst_h, int64_t dst_j, const float * src, int64_t src_h, int64_t src_j,
+                         const int32_t * idx, int64_t n, int64_t D, int64_t Hrows, int64_t dst_rows, hipStream_t s);
+void launch_get_rows(int type, const void * tab, int64_t nrows_tab, int64_t D, const int32_t * idx, int64_t n,
+                     float * out, hipStream_t s);
+void launch_swiglu(const float * g, const float * u, float * y, int64_t n, hipStream_t s);
+void launch_binary(int op, const float * a, const float * b, float * y, int64_t n, int64_t nb, hipStream_t s);
+void launch_argmax(const float * x, int64_t ldx, int64_t rows, int64_t n, int32_t * out, hipStream_t s);
+
+namespace {
+
+// ------------------------------------------------------------------------ tensor predicates
+
+std::string tname(const ggml_tensor * t) {
+    std::string s = std::string(ggml_op_name(t->op));
+    if (t->name[0]) s += " '" + std::string(t->name) + "'";
+    s += " [";
+    for (int i = 0; i < 4; i++) s += std::to_string(t->ne[i]) + (i < 3 ? ", " : "]");
+    return s;
+}
+
+bool is_output(const ggml_tensor * t) { return (t->flags & GGML_TENSOR_FLAG_OUTPUT) != 0; }
+
+// Rows of ne[0] elements at one byte stride (dims 1..3 collapse into rows), elements packed.
+bool uniform_rows(const ggml_tensor * t, int64_t & rows, size_t & stride) {
+    if (t->nb[0] != ggml_tsize(t->type) || ggml_blck(t->type) != 1) return false;
+    rows = ggml_nrows(t);
+    stride = t->nb[0] * (size_t) t->ne[0];
+    bool first = true;
+    size_t expect = 0;
+    for (int k = 1; k < 4; k++) {
+        if (t->ne[k] == 1) continue;
+        if (first) {
+            stride = t->nb[k];
+            first = false;
+        } else if (t->nb[k] != expect) {
+            return false;
+        }
+        expect = t->nb[k] * (size_t) t->ne[k];
+    }
+    return stride >= t->nb[0] * (size_t) t->ne[0];
+}
+
+// The tensor starts 16-byte aligned in its buffer (buffers are 256-byte aligned).
+bool aligned16(const ggml_tensor * t) { return t->view_offs % 16 == 0; }
+
+// f32 rows usable as a GEMV / GEMM activation: uniform, 16-byte aligned rows.
+bool act_rows(const ggml_tensor * t, int64_t & rows, int64_t & ld) {
+    size_t stride;
+    if (t->type != GGML_TYPE_F32 || !uniform_rows(t, rows, stride) || !aligned16(t) || stride % 16) return false;
+    ld = (int64_t) (stride / 4);
+    return true;
+}
+
+// A packed weight used whole: the tensor owning the memory (or a full reshape / view of it at
+// offset 0 with the same row length).
+bool whole_packed(const ggml_tensor * a) {
+    if (!is_packed_type(a->type)) return false;
+    const ggml_tensor * b = base_of(a);
+    return a->view_offs == 0 && b->type == a->type && b->ne[0] == a->ne[0] && ggml_nelements(b) == ggml_nelements(a) &&
+           ggml_is_contiguous(a) && ggml_is_contiguous(b);
+}
+
+bool f32_contig(const ggml_tensor * t) { return t->type == GGML_TYPE_F32 && ggml_is_contiguous(t); }
+
+// b repeats over a as y[i] = a[i] op b[i % nelements(b)]: b's shape is a prefix of a's.
+bool prefix_broadcast(const ggml_tensor * b, const ggml_tensor * a) {
+    int j = 0;
+    while (j < 4 && b->ne[j] == a->ne[j]) j++;
+    for (int k = j; k < 4; k++)
+        if (b->ne[k] != 1) return false;
+    return true;
+}
+
+// mul_mat whose weight is a whole packed Q4_0 / Q8_0 (fused activation conversions make Q8_0 codes).
+bool q8_mul_mat(const ggml_tensor * mm) {
+    const ggml_tensor * a = mm->src[0];
+    return (a->type == GGML_TYPE_Q4_0 || a->type == GGML_TYPE_Q8_0) && whole_packed(a) && a->ne[2] == 1 &&
+           a->ne[3] == 1;
+}
+
+bool add_takes(const ggml_tensor * add, const ggml_tensor * mm) {
+    if (add->op != GGML_OP_ADD || add->type != GGML_TYPE_F32) return false;
+    const ggml_tensor * r = add->src[0] == mm ? add->src[1] : add->src[1] == mm ? add->src[0] : nullptr;
+    return r && r != mm && f32_contig(r) && ggml_are_same_shape(r, mm) && aligned16(r);
+}
+
+}  // namespace
+
+// --------------------------------------------------------------------------------- chains
+
+Chains find_chains(const ggml_cgraph * g) {
+    const int n = (int) g->nodes.size();
+    Chains c;
+    c.end.resize(n);
+    c.member.assign(n, false);
+    for (int i = 0; i < n; i++) c.end[i] = i;
+    std::unordered_map<const ggml_tensor *, int> uses, reader, index;
+    for (int i = 0; i < n; i++) {
+        index[g->nodes[i]] = i;
+        for (const ggml_tensor * s : g->nodes[i]->src) {
+            if (!s) continue;
+            uses[s]++;
+            reader[s] = i;
+        }
+    }
+    // The one node reading t, if t may be folded into it.
+    auto sole = [&](const ggml_tensor * t) -> int {
+        if (is_output(t) || t == g->nodes[n - 1] || t->view_src) return -1;
+        auto u = uses.find(t);
+        if (u == uses.end() || u->second != 1) return -1;
+        return reader[t];
+    };
+    auto link = [&](std::initializer_list<int> idx) {
+        const int last = *(idx.end() - 1);
+        for (int i : idx) {
+            c.end[i] = last;
+            if (i != last) c.member[i] = true;
+        }
+    };
+    // mul_mat at k, optionally followed by the add of a residual.
+    auto with_add = [&](int k) -> int {
+        const int a = sole(g->nodes[k]);
+        return a >= 0 && add_takes(g->nodes[a], g->nodes[k]) ? a : -1;
+    };
+    for (int i = 0; i < n; i++) {
+        const ggml_tensor * t = g->nodes[i];
+        if (c.member[i] || c.end[i] != i) continue;
+        int64_t rows, ld;
+        if (t->op == GGML_OP_RMS_NORM && t->type == GGML_TYPE_F32 && act_rows(t->src[0], rows, ld)) {
+            const int j = sole(t);
+            if (j < 0) continue;
+            const ggml_tensor * m = g->nodes[j];
+            const ggml_tensor * w = m->src[1];
+            if (m->op != GGML_OP_MUL || m->src[0] != t || !f32_contig(w) || w->ne[0] != t->ne[0] || !ggml_is_vector(w))
+                continue;
+            const int k = sole(m);
+            if (k >= 0 && g->nodes[k]->op == GGML_OP_MUL_MAT && g->nodes[k]->src[1] == m && q8_mul_mat(g->nodes[k])) {
+                const int a = with_add(k);
+                if (a >= 0) link({i, j, k, a});
+                else link({i, j, k});
+            } else {
+                link({i, j});
+            }
+        } else if (t->op == GGML_OP_GLU && f32_contig(t->src[0]) && f32_contig(t->src[1]) && aligned16(t->src[0]) &&
+                   aligned16(t->src[1]) && t->ne[0] % 32 == 0) {
+            const int k = sole(t);
+            if (k < 0 || g->nodes[k]->op != GGML_OP_MUL_MAT || g->nodes[k]->src[1] != t || !q8_mul_mat(g->nodes[k]))
+                continue;
+            const int a = with_add(k);
+            if (a >= 0) link({i, k, a});
+            else link({i, k});
+        } else if (t->op == GGML_OP_MUL_MAT && whole_packed(t->src[0])) {
+            const int a = with_add(i);
+            if (a >= 0) link({i, a});
+        }
+    }
+    (void) index;
+    return c;
+}
+
+}  // namespace gcq
+
+using namespace gcq;
+
+// ------------------------------------------------------------------------------ structures
+
+struct ggml_backend_buffer_type {
+    ggml_backend * be;
+};
+
+struct ggml_backend_buffer {
+    ggml_backend * be = nullptr;
+    void * base = nullptr;
+    size_t size = 0;
+};
+
+namespace {
+
+enum StepKind {
+    S_MULMAT,         // [rms_norm ->] mul_mat [-> add] (x rows f32)
+    S_SWIGLU_MULMAT,  // swiglu -> mul_mat [-> add]
+    S_RMSNORM,
+    S_BINARY,
+    S_SCALE,
+    S_CPY,
+    S_GETROWS,
+    S_SETROWS,
+    S_ROPE,
+    S_FATTN,
+    S_SWIGLU,
+    S_ARGMAX,
+};
+
+// One launch sequence with every argument it takes; compared byte for byte to decide whether a
+// captured graph can be replayed, so it is always zero-initialized.
+struct Step {
+    int kind, type, op, pad;
+    const void * in[6];
+    void * out;
+    int64_t n[12];
+    float f[6];
+    Cpy4 g;
+};
+
+Step new_step(int kind) {
+    Step s;
+    std::memset(&s, 0, sizeof(s));
+    s.kind = kind;
+    return s;
+}
+
+struct Cached {
+    std::vector<uint8_t> sig;
+    hipGraphExec_t exec = nullptr;
+};
+
+}  // namespace
+
+struct ggml_backend {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    ggml_backend_buffer_type buft{};
+    std::string name;
+    void * ws = nullptr;  // workspace of the mul_mat activations and flash-attention partials
+    size_t ws_size = 0;
+    bool use_graphs = true;
+    std::unordered_map<const ggml_cgraph *, Cached> graphs;
+    std::vector<Step> steps;
+
+    ~ggml_backend() {
+        if (stream) (void) hipStreamSynchronize(stream);
+        for (auto & kv : graphs)
+            if (kv.second.exec) (void) hipGraphExecDestroy(kv.second.exec);
+        if (ws) (void) hipFree(ws);
+        if (stream) (void) hipStreamDestroy(stream);
+    }
+};
+
+struct ggml_gallocr {
+    ggml_backend * be = nullptr;
+    ggml_backend_buffer buf;
+    std::unordered_map<const ggml_tensor *, bool> mine;  // tensors this allocator placed
+};
+
+namespace {
+
+// --------------------------------------------------------------------------------- helpers
+
+size_t alloc_size(const ggml_tensor * t) {
+    if (is_packed_type(t->type) && ggml_is_contiguous(t)) {
+        const WeightLayout L = weight_layout(t->type, ggml_nrows(t), t->ne[0]);
+        return L.total;
+    }
+    return ggml_nbytes(t);
+}
+
+// The packed weight t (whole, contiguous): rows and row length.
+void packed_dims(const ggml_tensor * t, int64_t & rows, int64_t & k) {
+    rows = ggml_nrows(t);
+    k = t->ne[0];
+}
+
+void set_device(const ggml_backend * be) { check_hip(hipSetDevice(be->device), "hipSetDevice"); }
+
+const char * data_of(const ggml_tensor * t) {
+    require(t->data != nullptr, "tensor " + tname(t) + " has no memory (allocate its context or graph)");
+    require(base_of(t)->buffer != nullptr, "tensor " + tname(t) + " is in host memory, not in a HIP buffer");
+    return (const char *) t->data;
+}
+void * mut_data(const ggml_tensor * t) { return (void *) data_of(t); }
+
+void ensure_ws(ggml_backend * be, size_t need) {
+    if (need <= be->ws_size) return;
+    check_hip(hipStreamSynchronize(be->stream), "workspace");
+    if (be->ws) check_hip(hipFree(be->ws), "hipFree");
+    be->ws = nullptr;
+    be->ws_size = 0;
+    const size_t n = (need + (1 << 20) - 1) & ~size_t((1 << 20) - 1);
+    check_hip(hipMalloc(&be->ws, n), "hipMalloc workspace");
+    be->ws_size = n;
+    for (auto & kv : be->graphs) {  // every captured graph points at the old workspace
+        if (kv.second.exec) (void) hipGraphExecDestroy(kv.second.exec);
+    }
+    be->graphs.clear();
+}
+
+// ------------------------------------------------------------------------------- planning
+
+struct Planner {
+    ggml_backend * be;
+    std::vector<Step> & steps;
+    size_t ws_need = 0;
+    bool dry = false;  // supports_op: shapes and types only, no data
+
+    const char * d(const ggml_tensor * t) const { return dry ? nullptr : data_of(t); }
+    void * o(const ggml_tensor * t) const { return dry ? nullptr : mut_data(t); }
+
+    void mulmat(const ggml_tensor * mm, const ggml_tensor * x, const ggml_tensor * norm_w, float eps,
+                const ggml_tensor * res, const ggml_tensor * y) {
+        const ggml_tensor * w = mm->src[0];
+        require(whole_packed(w), "mul_mat " + tname(mm) + ": the weight must be a whole Q4_0 / Q8_0 / Q4_K tensor in "
+                                                          "a HIP buffer (other weight types are not on this path)");
+        require(w->ne[2] == 1 && w->ne[3] == 1, "mul_mat " + tname(mm) + ": batched weights are not supported");
+        int64_t M = 0, ldx = 0;
+        require(act_rows(x, M, ldx), "mul_mat " + tname(mm) + ": the activation must be f32 rows at one stride, "
+                                                              "16-byte aligned (add a cont)");
+        int64_t N, K;
+        packed_dims(w, N, K);
+        Step s = new_step(S_MULMAT);
+        s.type = w->type;
+        s.in[0] = d(w);
+        s.in[1] = d(x);
+        s.in[2] = norm_w ? d(norm_w) : nullptr;
+        s.in[3] = res ? d(res) : nullptr;
+        s.out = o(y);
+        s.n[0] = N;
+        s.n[1] = K;
+        s.n[2] = M;
+        s.n[3] = ldx;
+        s.n[4] = N;  // ldy: results are contiguous
+        s.f[0] = eps;
+        const bool row = M == 1 && (w->type == GGML_TYPE_Q4_0 || w->type == GGML_TYPE_Q8_0) && row_gemv_fits(w->type, K);
+        if (!row) {
+            const int64_t B = w->type == GGML_TYPE_Q4_K ? std::min<int64_t>(M, 8) : M;
+            ws_need = std::max(ws_need, act_layout(w->type, B, K).total);
+        }
+        steps.push_back(s);
+    }
+
+    void swiglu_mulmat(const ggml_tensor * glu, const ggml_tensor * mm, const ggml_tensor * res, const ggml_tensor * y) {
+        const ggml_tensor * w = mm->src[0];
+        int64_t N, K;
+        packed_dims(w, N, K);
+        Step s = new_step(S_SWIGLU_MULMAT);
+        s.type = w->type;
+        s.in[0] = d(w);
+        s.in[1] = d(glu->src[0]);
+        s.in[2] = d(glu->src[1]);
+        s.in[3] = res ? d(res) : nullptr;
+        s.out = o(y);
+        s.n[0] = N;
+        s.n[1] = K;
+        s.n[2] = ggml_nrows(glu);
+        s.n[3] = glu->ne[0];
+        ws_need = std::max(ws_need, act_layout(w->type, s.n[2], K).total);
+        steps.push_back(s);
+    }
+
+    void rmsnorm(const ggml_tensor * nrm, const ggml_tensor * w, const ggml_tensor * y) {
+        const ggml_tensor * x = nrm->src[0];
+        int64_t rows = 0;
+        size_t stride = 0;
+        require(x->type == GGML_TYPE_F32 && uniform_rows(x, rows, stride),
+                "rms_norm " + tname(nrm) + ": needs f32 rows at one stride");
+        Step s = new_step(S_RMSNORM);
+        s.in[0] = d(x);
+        s.in[1] = w ? d(w) : nullptr;
+        s.out = o(y);
+        s.n[0] = (int64_t) (stride / 4);
+        s.n[1] = rows;
+        s.n[2] = x->ne[0];
+        float eps;
+        std::memcpy(&eps, &nrm->op_params[0], 4);
+        s.f[0] = eps;
+        steps.push_back(s);
+    }
+
+    void node(const ggml_tensor * t) {
+        switch (t->op) {
+            case GGML_OP_NONE:
+            case GGML_OP_VIEW:
+            case GGML_OP_RESHAPE:
+            case GGML_OP_PERMUTE:
+            case GGML_OP_TRANSPOSE:
+                return;
+            case GGML_OP_MUL_MAT:
+                require(t->src[1]->ne[2] % std::max<int64_t>(1, t->src[0]->ne[2]) == 0, "mul_mat: batch mismatch");
+                return mulmat(t, t->src[1], nullptr, 0.0f, nullptr, t);
+            case GGML_OP_RMS_NORM:
+                return rmsnorm(t, nullptr, t);
+            case GGML_OP_ADD:
+            case GGML_OP_MUL: {
+                const ggml_tensor *a = t->src[0], *b = t->src[1];
+                require(f32_contig(a) && f32_contig(b) && prefix_broadcast(b, a),
+                        std::string(ggml_op_name(t->op)) + " " + tname(t) +
+                            ": needs contiguous f32 operands, the second of a leading-dims shape of the first");
+                Step s = new_step(S_BINARY);
+                s.op = t->op == GGML_OP_ADD ? 0 : 1;
+                s.in[0] = d(a);
+                s.in[1] = d(b);
+                s.out = o(t);
+                s.n[0] = ggml_nelements(a);
+                s.n[1] = ggml_nelements(b);
+                steps.push_back(s);
+                return;
+            }
+            case GGML_OP_SCALE: {
+                require(f32_contig(t->src[0]), "scale " + tname(t) + ": needs a contiguous f32 input");
+                Step s = new_step(S_SCALE);
+                s.in[0] = d(t->src[0]);
+                s.out = o(t);
+                s.n[0] = ggml_nelements(t);
+                std::memcpy(&s.f[0], &t->op_params[0], 4);
+                std::memcpy(&s.f[1], &t->op_params[1], 4);
+                steps.push_back(s);
+                return;
+            }
+            case GGML_OP_CPY:
+            case GGML_OP_CONT: {
+                const ggml_tensor * a = t->src[0];
+                auto ok = [](const ggml_tensor * x) {
+                    return (x->type == GGML_TYPE_F32 || x->type == GGML_TYPE_F16) && x->nb[0] % ggml_tsize(x->type) == 0;
+                };
+                require(ok(a) && ok(t), "cpy " + tname(t) + ": f32 / f16 only");
+                Step s = new_step(S_CPY);
+                s.type = a->type;
+                s.op = t->type;
+                s.in[0] = d(a);
+                s.out = o(t);
+                for (int k = 0; k < 4; k++) {
+                    s.g.sne[k] = a->ne[k];
+                    s.g.snb[k] = (int64_t) a->nb[k];
+                    s.g.dne[k] = t->ne[k];
+                    s.g.dnb[k] = (int64_t) t->nb[k];
+                }
+                s.n[0] = ggml_nelements(t);
+                steps.push_back(s);
+                return;
+            }
+            case GGML_OP_GET_ROWS: {
+                const ggml_tensor *a = t->src[0], *b = t->src[1];
+                const bool table = ((a->type == GGML_TYPE_F32 || a->type == GGML_TYPE_F16) && ggml_is_contiguous(a)) ||
+                                   ((a->type == GGML_TYPE_Q4_0 || a->type == GGML_TYPE_Q8_0) && whole_packed(a));
+                require(table && a->ne[2] == 1 && a->ne[3] == 1,
+                        "get_rows " + tname(t) + ": the table must be a contiguous F32 / F16 matrix or a whole Q4_0 / "
+                                                 "Q8_0 tensor");
+                require(ggml_is_contiguous(b) && ggml_is_vector(b), "get_rows " + tname(t) + ": one i32 index vector");
+                Step s = new_step(S_GETROWS);
+                s.type = a->type;
+                s.in[0] = d(a);
+                s.in[1] = d(b);
+                s.out = o(t);
+                s.n[0] = a->ne[1];
+                s.n[1] = a->ne[0];
+                s.n[2] = b->ne[0];
+                steps.push_back(s);
+                return;
+            }
+            case GGML_OP_SET_ROWS: {
+                const ggml_tensor *b = t->src[0], *c = t->src[1], *a = t->src[2];
+                require(a->type == GGML_TYPE_F16 && a->nb[0] == 2 && a->ne[0] % 8 == 0 && a->nb[1] % 16 == 0 &&
+                            a->nb[2] % 16 == 0 && a->ne[3] == 1 && aligned16(a),
+                        "set_rows " + tname(t) + ": the destination must be an f16 cache with 16-byte rows");
+                require(b->type == GGML_TYPE_F32 && b->nb[0] == 4 && b->nb[1] % 4 == 0 && b->nb[2] % 4 == 0,
+                        "set_rows " + tname(t) + ": the rows must be f32");
+                require(c->type == GGML_TYPE_I32 && ggml_is_contiguous(c) && ggml_is_vector(c),
+                        "set_rows " + tname(t) + ": one i32 index vector");
+                Step s = new_step(S_SETROWS);
+                s.out = o(a);
+                s.in[0] = d(b);
+                s.in[1] = d(c);
+                s.n[0] = (int64_t) a->nb[2] / 2;
+                s.n[1] = (int64_t) a->nb[1] / 2;
+                s.n[2] = (int64_t) b->nb[2] / 4;
+                s.n[3] = (int64_t) b->nb[1] / 4;
+                s.n[4] = b->ne[1];
+                s.n[5] = b->ne[0];
+                s.n[6] = b->ne[2];
+                s.n[7] = a->ne[1];
+                steps.push_back(s);
+                return;
+            }
+            case GGML_OP_ROPE: {
+                const ggml_tensor *x = t->src[0], *pos = t->src[1], *ff = t->src[2];
+                float fp[6];
+                std::memcpy(fp, &t->op_params[5], sizeof(fp));
+                const int n_dims = t->op_params[1], mode = t->op_params[2];
+                require(mode == GGML_ROPE_TYPE_NEOX, "rope " + tname(t) + ": NEOX mode (2) only");
+                require(fp[2] == 0.0f, "rope " + tname(t) + ": ext_factor must be 0 (no YaRN)");
+                require(x->type == GGML_TYPE_F32 && x->nb[0] == 4 && x->nb[1] % 4 == 0 && x->nb[2] % 4 == 0 &&
+                            x->ne[3] == 1 && t->type == GGML_TYPE_F32,
+                        "rope " + tname(t) + ": f32 [D, H, S] input");
+                require(n_dims > 0 && n_dims % 2 == 0 && n_dims <= x->ne[0], "rope: n_dims must be even and <= D");
+                require(ggml_is_contiguous(pos), "rope: positions must be contiguous");
+                Step s = new_step(S_ROPE);
+                s.in[0] = d(x);
+                s.in[1] = d(pos);
+                s.in[2] = ff ? d(ff) : nullptr;
+                s.out = o(t);
+                s.n[0] = (int64_t) x->nb[2] / 4;
+                s.n[1] = (int64_t) x->nb[1] / 4;
+                s.n[2] = x->ne[0] * x->ne[1];
+                s.n[3] = x->ne[0];
+                s.n[4] = x->ne[0];
+                s.n[5] = x->ne[1];
+                s.n[6] = x->ne[2];
+                s.n[7] = n_dims;
+                s.f[0] = fp[0];
+                s.f[1] = fp[1];
+                s.f[2] = fp[3];
+                steps.push_back(s);
+                return;
+            }
+            case GGML_OP_FLASH_ATTN_EXT: {
+                const ggml_tensor *q = t->src[0], *k = t->src[1], *v = t->src[2], *m = t->src[3];
+                float fp[3];
+                std::memcpy(fp, &t->op_params[0], sizeof(fp));
+                require(fp[1] == 0.0f && fp[2] == 0.0f, "flash_attn_ext " + tname(t) + ": no ALiBi or softcap");
+                require(q->type == GGML_TYPE_F32 && q->nb[0] == 4 && q->nb[1] % 4 == 0 && q->nb[2] % 4 == 0 &&
+                            q->ne[3] == 1,
+                        "flash_attn_ext " + tname(t) + ": q must be f32 [D, Sq, H, 1]");
+                require(k->type == GGML_TYPE_F16 && v->type == GGML_TYPE_F16 && k->nb[0] == 2 && v->nb[0] == 2 &&
+                            k->nb[1] % 16 == 0 && k->nb[2] % 16 == 0 && v->nb[1] % 16 == 0 && v->nb[2] % 16 == 0 &&
+                            aligned16(k) && aligned16(v),
+                        "flash_attn_ext " + tname(t) + ": K and V must be f16 with 16-byte rows");
+                const int64_t D = q->ne[0], H = q->ne[2], Hkv = k->ne[2];
+                require(v->ne[0] == D && (D == 64 || D == 128 || D == 256), "flash_attn_ext: head size 64, 128 or 256");
+                require(H % Hkv == 0 && H / Hkv <= 8, "flash_attn_ext: 1 to 8 query heads per KV head");
+                if (m) require(m->type == GGML_TYPE_F16 && m->nb[0] == 2 && m->nb[1] % 2 == 0 && m->ne[2] == 1,
+                               "flash_attn_ext: the mask must be f16 [n_kv, Sq]");
+                Step s = new_step(S_FATTN);
+                s.in[0] = d(q);
+                s.in[1] = d(k);
+                s.in[2] = d(v);
+                s.in[3] = m ? d(m) : nullptr;
+                s.out = o(t);
+                s.n[0] = (int64_t) q->nb[2] / 4;
+                s.n[1] = (int64_t) q->nb[1] / 4;
+                s.n[2] = (int64_t) k->nb[2] / 2;
+                s.n[3] = (int64_t) k->nb[1] / 2;
+                s.n[4] = (int64_t) v->nb[2] / 2;
+                s.n[5] = (int64_t) v->nb[1] / 2;
+                s.n[6] = m ? (int64_t) m->nb[1] / 2 : 0;
+                s.n[7] = D;
+                s.n[8] = q->ne[1];
+                s.n[9] = H;
+                s.n[10] = Hkv;
+                s.n[11] = k->ne[1];
+                s.f[0] = fp[0];
+                require(s.n[11] >= 1 && s.n[8] >= 1, "flash_attn_ext: empty attention");
+                ws_need = std::max(ws_need, attn_workspace((int) s.n[8], (int) H, (int) Hkv, (int) D, (int) s.n[11]));
+                steps.push_back(s);
+                return;
+            }
+            case GGML_OP_GLU: {
+                require(t->op_params[0] == GGML_GLU_OP_SWIGLU && f32_contig(t->src[0]) && f32_contig(t->src[1]),
+                        "glu " + tname(t) + ": swiglu of contiguous f32 operands only");
+                Step s = new_step(S_SWIGLU);
+                s.in[0] = d(t->src[0]);
+                s.in[1] = d(t->src[1]);
+                s.out = o(t);
+                s.n[0] = ggml_nelements(t);
+                steps.push_back(s);
+                return;
+            }
+            case GGML_OP_ARGMAX: {
+                int64_t rows = 0;
+                size_t stride = 0;
+                require(t->src[0]->type == GGML_TYPE_F32 && uniform_rows(t->src[0], rows, stride),
+                        "argmax " + tname(t) + ": needs f32 rows");
+                Step s = new_step(S_ARGMAX);
+                s.in[0] = d(t->src[0]);
+                s.out = o(t);
+                s.n[0] = (int64_t) stride / 4;
+                s.n[1] = rows;
+                s.n[2] = t->src[0]->ne[0];
+                steps.push_back(s);
+                return;
+            }
+            default:
+                fail(std::string("op ") + ggml_op_name(t->op) + " (" + tname(t) + ") is not on this library's path");
+        }
+    }
+
+    // The chain ending at node f (members before it, in order).
+    void chain(const ggml_cgraph * g, const std::vector<int> & idx) {
+        const ggml_tensor * first = g->nodes[idx.front()];
+        const ggml_tensor * last = g->nodes[idx.back()];
+        if (first->op == GGML_OP_RMS_NORM) {
+            const ggml_tensor * mul = g->nodes[idx[1]];
+            if (idx.size() == 2) return rmsnorm(first, mul->src[1], mul);
+            const ggml_tensor * mm = g->nodes[idx[2]];
+            float eps;
+            std::memcpy(&eps, &first->op_params[0], 4);
+            const ggml_tensor * res = idx.size() == 4 ? (last->src[0] == mm ? last->src[1] : last->src[0]) : nullptr;
+            return mulmat(mm, first->src[0], mul->src[1], eps, res, last);
+        }
+        if (first->op == GGML_OP_GLU) {
+            const ggml_tensor * mm = g->nodes[idx[1]];
+            const ggml_tensor * res = idx.size() == 3 ? (last->src[0] == mm ? last->src[1] : last->src[0]) : nullptr;
+            return swiglu_mulmat(first, mm, res, last);
+        }
+        // mul_mat -> add
+        const ggml_tensor * res = last->src[0] == first ? last->src[1] : last->src[0];
+        return mulmat(first, first->src[1], nullptr, 0.0f, res, last);
+    }
+};
+
+// ------------------------------------------------------------------------------- running
+
+void run_step(const ggml_backend * be, const Step & s) {
+    hipStream_t st = be->stream;
+    switch (s.kind) {
+        case S_MULMAT: {
+            const int wt = s.type;
+            const int64_t N = s.n[0], K = s.n[1], M = s.n[2], ldx = s.n[3], ldy = s.n[4];
+            const float * x = (const float *) s.in[1];
+            const float * nw = (const float *) s.in[2];
+            const float * res = (const float *) s.in[3];
+            float * y = (float *) s.out;
+            if (M == 1 && (wt == T_Q4_0 || wt == T_Q8_0) && row_gemv_fits(wt, K)) {
+                const WeightLayout L = weight_layout(wt, N, K);
+                RowArgs a{};
+                a.wqs = (const uint8_t *) s.in[0] + L.qs;
+                a.wd = (const uint16_t *) ((const uint8_t *) s.in[0] + L.d);
+                a.N = (int) N;
+                a.nb = (int) (K / QK);
+                a.x = x;
+                a.norm_w = nw;
+                a.eps = s.f[0];
+                a.y = y;
+                a.res = res;
+                launch_row_gemv(wt, nw ? PRO_NORM : PRO_PLAIN, EPI_STORE, a, st);
+                return;
+            }
+            if (wt == T_Q4_K && M > 8) {
+                for (int64_t m = 0; m < M; m += 8) {
+                    const int64_t b = std::min<int64_t>(8, M - m);
+                    launch_act_quant(wt, x + m * ldx, ldx, b, K, be->ws, st);
+                    launch_gemv(wt, s.in[0], N, K, be->ws, b, y + m * ldy, ldy, st, res ? res + m * ldy : nullptr);
+                }
+                return;
+            }
+            if (nw) launch_rmsnorm_q8(x, ldx, nw, s.f[0], M, K, be->ws, st);
+            else launch_act_quant(wt, x, ldx, M, K, be->ws, st);
+            if (M <= 8) launch_gemv(wt, s.in[0], N, K, be->ws, M, y, ldy, st, res);
+            else launch_gemm(wt, s.in[0], N, K, be->ws, M, y, ldy, st, res);
+            return;
+        }
+        case S_SWIGLU_MULMAT: {
+            const int64_t N = s.n[0], K = s.n[1], M = s.n[2], n = s.n[3];
+            launch_swiglu_q8((const float *) s.in[1], (const float *) s.in[2], n, n, M, be->ws, st);
+            if (M <= 8) launch_gemv(s.type, s.in[0], N, K, be->ws, M, (float *) s.out, N, st, (const float *) s.in[3]);
+            else launch_gemm(s.type, s.in[0], N, K, be->ws, M, (float *) s.out, N, st, (const float *) s.in[3]);
+            return;
+        }
+        case S_RMSNORM:
+            launch_rms_norm((const float *) s.in[0], s.n[0], (float *) s.out, s.n[2], (const float *) s.in[1], s.n[1],
+                            s.n[2], s.f[0], st);
+            return;
+        case S_BINARY:
+            launch_binary(s.op, (const float *) s.in[0], (const float *) s.in[1], (float *) s.out, s.n[0], s.n[1], st);
+            return;
+        case S_SCALE:
+            launch_scale((const float *) s.in[0], (float *) s.out, s.n[0], s.f[0], s.f[1], st);
+            return;
+        case S_CPY:
+            launch_cpy(s.in[0], s.type, s.out, s.op, s.g, s.n[0], st);
+            return;
+        case S_GETROWS:
+            launch_get_rows(s.type, s.in[0], s.n[0], s.n[1], (const int32_t *) s.in[1], s.n[2], (float *) s.out, st);
+            return;
+        case S_SETROWS:
+            launch_set_rows_f16(s.out, s.n[0], s.n[1], (const float *) s.in[0], s.n[2], s.n[3],
+                                (const int32_t *) s.in[1], s.n[4], s.n[5], s.n[6], s.n[7], st);
+            return;
+        case S_ROPE:
+            launch_rope_neox((const float *) s.in[0], s.n[0], s.n[1], (float *) s.out, s.n[2], s.n[3],
+                             (const int32_t *) s.in[1], s.n[4], s.n[5], s.n[6], (int) s.n[7], s.f[0], s.f[1], s.f[2],
+                             (const float *) s.in[2], st);
+            return;
+        case S_FATTN:
+            launch_flash_attn((const float *) s.in[0], s.n[0], s.n[1], s.in[1], s.n[2], s.n[3], s.in[2], s.n[4], s.n[5],
+                              s.in[3], s.n[6], (float *) s.out, (int) s.n[7], (int) s.n[7], (int) s.n[8], (int) s.n[9],
+                              (int) s.n[10], (int) s.n[11], s.f[0], be->ws, be->ws_size, st);
+            return;
+        case S_SWIGLU:
+            launch_swiglu((const float *) s.in[0], (const float *) s.in[1], (float *) s.out, s.n[0], st);
+            return;
+        case S_ARGMAX:
+            launch_argmax((const float *) s.in[0], s.n[0], s.n[1], s.n[2], (int32_t *) s.out, st);
+            return;
+    }
+}
+
+// Gives every view of g its base's memory (views made before their base was allocated, or whose
+// base has moved since).
+void refresh_views(ggml_cgraph * g) {
+    for (auto * list : {&g->leafs, &g->nodes})
+        for (ggml_tensor * t : *list)
+            if (t->view_src && t->view_src->data) {
+                t->data = (char *) t->view_src->data + t->view_offs;
+                t->buffer = t->view_src->buffer;
+            }
+}
+
+enum ggml_status compute(ggml_backend * be, ggml_cgraph * g) {
+    require(g != nullptr, "graph is NULL");
+    require(g->error.empty(), g->error);
+    if (g->nodes.empty()) return GGML_STATUS_SUCCESS;
+    set_device(be);
+    refresh_views(g);
+    const Chains c = find_chains(g);
+    be->steps.clear();
+    Planner p{be, be->steps};
+    std::vector<int> idx;
+    for (int i = 0; i < (int) g->nodes.size(); i++) {
+        if (c.member[i]) continue;
+        idx.clear();
+        for (int j = 0; j < i; j++)  // members of the chain ending here, in order
+            if (c.member[j] && c.end[j] == i) idx.push_back(j);
+        if (idx.empty()) {
+            p.node(g->nodes[i]);
+        } else {
+            idx.push_back(i);
+            p.chain(g, idx);
+        }
+    }
+    ensure_ws(be, p.ws_need);
+    std::vector<uint8_t> sig((const uint8_t *) be->steps.data(),
+                             (const uint8_t *) (be->steps.data() + be->steps.size()));
+    const uint8_t * wsp = (const uint8_t *) &be->ws;
+    sig.insert(sig.end(), wsp, wsp + sizeof(void *));
+    if (!be->use_graphs) {
+        for (const Step & s : be->steps) run_step(be, s);
+    } else {
+        Cached & cc = be->graphs[g];
+        if (!cc.exec || cc.sig != sig) {
+            if (cc.exec) check_hip(hipGraphExecDestroy(cc.exec), "hipGraphExecDestroy");
+            cc.exec = nullptr;
+            cc.sig.clear();
+            check_hip(hipStreamBeginCapture(be->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+            hipGraph_t graph = nullptr;
+            try {
+                for (const Step & s : be->steps) run_step(be, s);
+            } catch (...) {
+                (void) hipStreamEndCapture(be->stream, &graph);
+                if (graph) (void) hipGraphDestroy(graph);
+                throw;
+            }
+            check_hip(hipStreamEndCapture(be->stream, &graph), "hipStreamEndCapture");
+            const hipError_t e = hipGraphInstantiate(&cc.exec, graph, nullptr, nullptr, 0);
+            (void) hipGraphDestroy(graph);
+            check_hip(e, "hipGraphInstantiate");
+            cc.sig = std::move(sig);
+        }
+        check_hip(hipGraphLaunch(cc.exec, be->stream), "hipGraphLaunch");
+    }
+    check_hip(hipStreamSynchronize(be->stream), "graph compute");
+    return GGML_STATUS_SUCCESS;
+}
+
+// ------------------------------------------------------------------------- graph allocator
+
+// First-fit placement of byte ranges (256-byte granules) with merging of freed neighbours.
+struct Arena {
+    std::map<size_t, size_t> holes;  // offset -> size, below top
+    size_t top = 0, peak = 0;
+    size_t take(size_t n) {
+        n = align256(std::max<size_t>(n, 1));
+        for (auto it = holes.begin(); it != holes.end(); ++it) {
+            if (it->second < n) continue;
+            const size_t off = it->first, left = it->second - n;
+            holes.erase(it);
+            if (left) holes[off + n] = left;
+            return off;
+        }
+        const size_t off = top;
+        top += n;
+        peak = std::max(peak, top);
+        return off;
+    }
+    void give(size_t off, size_t n) {
+        n = align256(std::max<size_t>(n, 1));
+        auto it = holes.emplace(off, n).first;
+        auto nx = std::next(it);
+        if (nx != holes.end() && it->first + it->second == nx->first) {
+            it->second += nx->second;
+            holes.erase(nx);
+        }
+        if (it != holes.begin()) {
+            auto pv = std::prev(it);
+            if (pv->first + pv->second == it->first) {
+                pv->second += it->second;
+                holes.erase(it);
+                it = pv;
+            }
+        }
+        if (it->first + it->second == top) {
+            top = it->first;
+            holes.erase(it);
+        }
+    }
+};
+
+// Offsets for every tensor of g this allocator places; the buffer size they need.
+size_t place(ggml_gallocr * ga, ggml_cgraph * g, std::vector<std::pair<ggml_tensor *, size_t>> & where) {
+    require(g->error.empty(), g->error);
+    const int n = (int) g->nodes.size();
+    const Chains c = find_chains(g);
+    // Needs memory: no data yet (or placed by this allocator before), not a view, not folded.
+    auto needs = [&](const ggml_tensor * t) { return !t->view_src && (!t->data || ga->mine.count(t)); };
+    std::unordered_map<const ggml_tensor *, int> last;
+    std::unordered_map<const ggml_tensor *, bool> keep;
+    for (ggml_tensor * t : g->leafs) keep[t] = true;
+    for (int i = 0; i < n; i++) {
+        const ggml_tensor * t = g->nodes[i];
+        if (t->flags & (GGML_TENSOR_FLAG_OUTPUT | GGML_TENSOR_FLAG_INPUT)) keep[base_of(t)] = true;
+        for (const ggml_tensor * s : t->src) {
+            if (!s) continue;
+            const ggml_tensor * b = base_of(s);
+            last[b] = std::max(last.count(b) ? last[b] : -1, c.end[i]);
+        }
+    }
+    keep[base_of(g->nodes[n - 1])] = true;
+    Arena A;
+    for (ggml_tensor * t : g->leafs)
+        if (needs(t)) where.emplace_back(t, A.take(alloc_size(t)));
+    std::vector<std::vector<const ggml_tensor *>> dies(n);
+    for (auto & kv : last)
+        if (!keep.count(kv.first)) dies[kv.second].push_back(kv.first);
+    std::unordered_map<const ggml_tensor *, size_t> off;
+    for (int i = 0; i < n; i++) {
+        ggml_tensor * t = g->nodes[i];
+        if (!c.member[i] && needs(t)) {
+            const size_t o = A.take(alloc_size(t));
+            off[t] = o;
+            where.emplace_back(t, o);
+        }
+        for (const ggml_tensor * b : dies[i]) {
+            auto it = off.find(b);
+            if (it != off.end()) A.give(it->second, alloc_size(b));
+        }
+    }
+    return A.peak;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------------- C API
+
+extern "C" {
+
+ggml_backend_t ggml_backend_hip_init(int device) {
+    ggml_backend * be = nullptr;
+    const int rc = guarded([&] {
+        int n = 0;
+        check_hip(hipGetDeviceCount(&n), "hipGetDeviceCount");
+        require(device >= 0 && device < n, "HIP device " + std::to_string(device) + " of " + std::to_string(n));
+        hipDeviceProp_t pr;
+        check_hip(hipGetDeviceProperties(&pr, device), "hipGetDeviceProperties");
+        require(std::strncmp(pr.gcnArchName, "gfx950", 6) == 0,
+                std::string("device ") + std::to_string(device) + " is " + pr.gcnArchName + ", not gfx950");
+        auto b = std::make_unique<ggml_backend>();
+        b->device = device;
+        b->name = "HIP" + std::to_string(device);
+        b->buft.be = b.get();
+        check_hip(hipSetDevice(device), "hipSetDevice");
+        check_hip(hipStreamCreate(&b->stream), "hipStreamCreate");
+        be = b.release();
+    });
+    if (rc) (void) hipGetLastError();
+    return be;
+}
+
+bool ggml_backend_is_hip(ggml_backend_t backend) { return backend != nullptr; }
+
+void ggml_backend_free(ggml_backend_t backend) { delete backend; }
+
+const char * ggml_backend_name(ggml_backend_t backend) { return backend ? backend->name.c_str() : "NULL"; }
+
+void ggml_backend_synchronize(ggml_backend_t backend) {
+    if (backend) (void) hipStreamSynchronize(backend->stream);
+}
+
+ggml_backend_buffer_type_t ggml_backend_get_default_buffer_type(ggml_backend_t backend) {
+    return backend ? &backend->buft : nullptr;
+}
+
+const char * ggml_backend_buft_name(ggml_backend_buffer_type_t buft) {
+    return buft ? buft->be->name.c_str() : "NULL";
+}
+
+void ggml_backend_hip_set_use_graphs(ggml_backend_t backend, bool use) {
+    if (backend) backend->use_graphs = use;
+}
+
+bool ggml_backend_supports_op(ggml_backend_t backend, const ggml_tensor * op) {
+    if (!backend || !op) return false;
+    std::vector<Step> steps;
+    Planner p{backend, steps};
+    p.dry = true;
+    return guarded([&] { p.node(op); }) == 0;
+}
+
+enum ggml_status ggml_backend_graph_compute(ggml_backend_t backend, ggml_cgraph * cgraph) {
+    enum ggml_status st = GGML_STATUS_FAILED;
+    if (!backend) {
+        set_error("ggml_backend_graph_compute: backend is NULL");
+        return st;
+    }
+    if (guarded([&] { st = compute(backend, cgraph); })) return GGML_STATUS_FAILED;
+    return st;
+}
+
+size_t ggml_backend_buft_get_alloc_size(ggml_backend_buffer_type_t, const ggml_tensor * tensor) {
+    return tensor ? alloc_size(tensor) : 0;
+}
+
+ggml_backend_buffer_t ggml_backend_alloc_ctx_tensors_from_buft(ggml_context * ctx, ggml_backend_buffer_type_t buft) {
+    ggml_backend_buffer * buf = nullptr;
+    guarded([&] {
+        require(ctx && buft, "alloc_ctx_tensors: NULL context or buffer type");
+        size_t total = 0;
+        for (ggml_tensor * t : ctx->tensors)
+            if (!t->data && !t->view_src) total += align256(alloc_size(t));
+        if (total == 0) {
+            set_error("alloc_ctx_tensors: no tensor without memory");
+            return;
+        }
+        set_device(buft->be);
+        auto b = std::make_unique<ggml_backend_buffer>();
+        b->be = buft->be;
+        check_hip(hipMalloc(&b->base, total), "hipMalloc");
+        b->size = total;
+        size_t off = 0;
+        for (ggml_tensor * t : ctx->tensors) {
+            if (t->data || t->view_src) continue;
+            t->data = (char *) b->base + off;
+            t->buffer = b.get();
+            off += align256(alloc_size(t));
+        }
+        for (ggml_tensor * t : ctx->tensors)
+            if (t->view_src && t->view_src->data) {
+                t->data = (char *) t->view_src->data + t->view_offs;
+                t->buffer = t->view_src->buffer;
+            }
+        buf = b.release();
+    });
+    return buf;
+}
+
+ggml_backend_buffer_t ggml_backend_alloc_ctx_tensors(ggml_context * ctx, ggml_backend_t backend) {
+    return ggml_backend_alloc_ctx_tensors_from_buft(ctx, ggml_backend_get_default_buffer_type(backend));
+}
+
+void ggml_backend_buffer_free(ggml_backend_buffer_t buffer) {
+    if (!buffer) return;
+    if (buffer->base) (void) hipFree(buffer->base);
+    delete buffer;
+}
+
+size_t ggml_backend_buffer_get_size(ggml_backend_buffer_t buffer) { return buffer ? buffer->size : 0; }
+void * ggml_backend_buffer_get_base(ggml_backend_buffer_t buffer) { return buffer ? buffer->base : nullptr; }
+bool ggml_backend_buffer_is_host(ggml_backend_buffer_t) { return false; }
+
+void ggml_backend_buffer_clear(ggml_backend_buffer_t buffer, uint8_t value) {
+    if (!buffer || !buffer->base) return;
+    guarded([&] {
+        set_device(buffer->be);
+        check_hip(hipMemset(buffer->base, value, buffer->size), "buffer_clear");
+    });
+}
+
+void ggml_backend_tensor_set(ggml_tensor * t, const void * data, size_t offset, size_t size) {
+    guarded([&] {
+        require(t && data, "tensor_set: NULL tensor or data");
+        const ggml_tensor * b = base_of(t);
+        require(b->buffer && t->data, "tensor_set: " + tname(t) + " is not in a HIP buffer");
+        const size_t nb = ggml_nbytes(t);
+        require(offset + size <= nb, "tensor_set: " + std::to_string(offset + size) + " bytes into " + tname(t) +
+                                         " of " + std::to_string(nb));
+        ggml_backend * be = b->buffer->be;
+        set_device(be);
+        if (is_packed_type(t->type)) {
+            require(t == b && offset == 0 && size == nb,
+                    "tensor_set: a " + std::string(ggml_type_name(t->type)) +
+                        " tensor is set whole (offset 0, ggml_nbytes bytes), not as a view or a part");
+            void * tmp = nullptr;
+            check_hip(hipMalloc(&tmp, size), "hipMalloc");
+            hipError_t e = hipMemcpy(tmp, data, size, hipMemcpyHostToDevice);
+            if (e == hipSuccess) {
+                try {
+                    launch_pack(t->type, tmp, ggml_nrows(t), t->ne[0], t->data, be->stream);
+                } catch (...) {
+                    (void) hipFree(tmp);
+                    throw;
+                }
+                e = hipStreamSynchronize(be->stream);
+            }
+            (void) hipFree(tmp);
+            check_hip(e, "tensor_set");
+            return;
+        }
+        check_hip(hipMemcpy((char *) t->data + offset, data, size, hipMemcpyHostToDevice), "tensor_set");
+    });
+}
+
+void ggml_backend_tensor_get(const ggml_tensor * t, void * data, size_t offset, size_t size) {
+    guarded([&] {
+        require(t && data, "tensor_get: NULL tensor or data");
+        const ggml_tensor * b = base_of(t);
+        require(b->buffer && t->data, "tensor_get: " + tname(t) + " is not in a HIP buffer");
+        const size_t nb = ggml_nbytes(t);
+        require(offset + size <= nb, "tensor_get: " + std::to_string(offset + size) + " bytes from " + tname(t) +
+                                         " of " + std::to_string(nb));
+        ggml_backend * be = b->buffer->be;
+        set_device(be);
+        check_hip(hipStreamSynchronize(be->stream), "tensor_get");
+        if (is_packed_type(t->type)) {
+            require(t == b && offset == 0 && size == nb,
+                    "tensor_get: a " + std::string(ggml_type_name(t->type)) + " tensor is read whole");
+            void * tmp = nullptr;
+            check_hip(hipMalloc(&tmp, size), "hipMalloc");
+            hipError_t e = hipSuccess;
+            try {
+                launch_unpack(t->type, t->data, ggml_nrows(t), t->ne[0], tmp, be->stream);
+            } catch (...) {
+                (void) hipFree(tmp);
+                throw;
+            }
+            e = hipStreamSynchronize(be->stream);
+            if (e == hipSuccess) e = hipMemcpy(data, tmp, size, hipMemcpyDeviceToHost);
+            (void) hipFree(tmp);
+            check_hip(e, "tensor_get");
+            return;
+        }
+        check_hip(hipMemcpy(data, (const char *) t->data + offset, size, hipMemcpyDeviceToHost), "tensor_get");
+    });
+}
+
+void ggml_backend_tensor_memset(ggml_tensor * t, uint8_t value, size_t offset, size_t size) {
+    guarded([&] {
+        require(t && t->data && base_of(t)->buffer, "tensor_memset: tensor is not in a HIP buffer");
+        require(!is_packed_type(t->type), "tensor_memset: not for quantized tensors");
+        require(offset + size <= ggml_nbytes(t), "tensor_memset: range exceeds the tensor");
+        set_device(base_of(t)->buffer->be);
+        check_hip(hipMemset((char *) t->data + offset, value, size), "tensor_memset");
+    });
+}
+
+void ggml_backend_tensor_copy(ggml_tensor * src, ggml_tensor * dst) {
+    guarded([&] {
+        require(src && dst && src->data && dst->data && base_of(src)->buffer && base_of(dst)->buffer,
+                "tensor_copy: both tensors must be in HIP buffers");
+        require(src->type == dst->type && ggml_are_same_shape(src, dst) && ggml_is_contiguous(src) &&
+                    ggml_is_contiguous(dst),
+                "tensor_copy: same type and shape, both contiguous");
+        const size_t n = is_packed_type(src->type) ? alloc_size(src) : ggml_nbytes(src);
+        if (is_packed_type(src->type)) require(src == base_of(src) && dst == base_of(dst), "tensor_copy: whole tensors");
+        set_device(base_of(dst)->buffer->be);
+        check_hip(hipMemcpy(dst->data, src->data, n, hipMemcpyDeviceToDevice), "tensor_copy");
+    });
+}
+
+enum ggml_status ggml_backend_view_init(ggml_tensor * t) {
+    if (!t || !t->view_src || !t->view_src->data) {
+        set_error("view_init: not a view of a tensor with memory");
+        return GGML_STATUS_FAILED;
+    }
+    t->data = (char *) t->view_src->data + t->view_offs;
+    t->buffer = t->view_src->buffer;
+    return GGML_STATUS_SUCCESS;
+}
+
+const char * ggml_status_to_string(enum ggml_status status) {
+    switch (status) {
+        case GGML_STATUS_ALLOC_FAILED: return "GGML status: error (failed to allocate memory)";
+        case GGML_STATUS_FAILED: return "GGML status: error (operation failed)";
+        case GGML_STATUS_SUCCESS: return "GGML status: success";
+        case GGML_STATUS_ABORTED: return "GGML status: warning (operation aborted)";
+    }
+    return "GGML status: unknown";
+}
+
+// ------------------------------------------------------------------------------ ggml-alloc
+
+ggml_gallocr_t ggml_gallocr_new(ggml_backend_buffer_type_t buft) {
+    if (!buft) {
+        set_error("gallocr_new: buffer type is NULL");
+        return nullptr;
+    }
+    auto * ga = new ggml_gallocr;
+    ga->be = buft->be;
+    ga->buf.be = buft->be;
+    return ga;
+}
+
+void ggml_gallocr_free(ggml_gallocr_t ga) {
+    if (!ga) return;
+    if (ga->buf.base) (void) hipFree(ga->buf.base);
+    delete ga;
+}
+
+bool ggml_gallocr_reserve(ggml_gallocr_t ga, ggml_cgraph * g) {
+    if (!ga || !g) return false;
+    return guarded([&] {
+               std::vector<std::pair<ggml_tensor *, size_t>> where;
+               const size_t need = place(ga, g, where);
+               if (need > ga->buf.size) {
+                   set_device(ga->be);
+                   if (ga->buf.base) check_hip(hipFree(ga->buf.base), "hipFree");
+                   ga->buf.base = nullptr;
+                   ga->buf.size = 0;
+                   check_hip(hipMalloc(&ga->buf.base, need), "hipMalloc compute buffer");
+                   ga->buf.size = need;
+                   for (auto & kv : ga->mine) const_cast<ggml_tensor *>(kv.first)->data = nullptr;
+               }
+           }) == 0;
+}
+
+bool ggml_gallocr_alloc_graph(ggml_gallocr_t ga, ggml_cgraph * g) {
+    if (!ga || !g) return false;
+    return guarded([&] {
+               std::vector<std::pair<ggml_tensor *, size_t>> where;
+               const size_t need = place(ga, g, where);
+               if (need > ga->buf.size) {
+                   set_device(ga->be);
+                   check_hip(hipDeviceSynchronize(), "gallocr");
+                   if (ga->buf.base) check_hip(hipFree(ga->buf.base), "hipFree");
+                   ga->buf.base = nullptr;
+                   ga->buf.size = 0;
+                   check_hip(hipMalloc(&ga->buf.base, need), "hipMalloc compute buffer");
+                   ga->buf.size = need;
+               }
+               for (auto & kv : ga->mine) const_cast<ggml_tensor *>(kv.first)->data = nullptr;
+               ga->mine.clear();
+               for (auto & w : where) {
+                   w.first->data = (char *) ga->buf.base + w.second;
+                   w.first->buffer = &ga->buf;
+                   ga->mine[w.first] = true;
+               }
+               refresh_views(g);
+           }) == 0;
+}
+
+size_t ggml_gallocr_get_buffer_size(ggml_gallocr_t ga, int buffer_id) {
+    return ga && buffer_id == 0 ? ga->buf.size : 0;
+}
+
+}  // extern "C"

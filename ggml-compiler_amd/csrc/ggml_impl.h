@@ -1,0 +1,52 @@
+// ggml_impl.h - libgcq-internal definitions shared by the ggml API's graph construction (ggml.hip)
+// and its HIP backend (ggml_backend.hip).
+#pragma once
+
+#include <string>
+#include <unordered_set>
+#include <vector>
+
+#include "../../include/ggml-alloc.h"
+#include "../../include/ggml-backend.h"
+#include "../../include/ggml.h"
+
+struct ggml_context {
+    bool no_alloc = true;
+    std::vector<ggml_tensor *> tensors;  // owned, in creation order
+    std::vector<void *> host_data;       // owned host memory of no_alloc == false tensors
+    std::vector<ggml_cgraph *> graphs;   // owned
+};
+
+struct ggml_cgraph {
+    size_t size = GGML_DEFAULT_GRAPH_SIZE;
+    std::vector<ggml_tensor *> nodes;  // in execution order
+    std::vector<ggml_tensor *> leafs;
+    std::unordered_set<const ggml_tensor *> visited;
+    std::string error;  // a NULL tensor was expanded: the reason it is NULL
+};
+
+namespace gcq {
+
+// Element counts of a type's block and bytes of one block (0 for a type this library does not
+// know). Shared with the C ABI's size functions.
+int64_t ggml_blck(int type);
+size_t ggml_tsize(int type);
+
+// The tensor owning t's memory (t itself if it is not a view).
+inline const ggml_tensor * base_of(const ggml_tensor * t) { return t->view_src ? t->view_src : t; }
+inline bool is_view_op(int op) {
+    return op == GGML_OP_VIEW || op == GGML_OP_RESHAPE || op == GGML_OP_PERMUTE || op == GGML_OP_TRANSPOSE;
+}
+// A Q4_0 / Q8_0 / Q4_K tensor in this library's device buffers: stored packed (gcq_pack_weights).
+inline bool is_packed_type(int t) { return t == GGML_TYPE_Q4_0 || t == GGML_TYPE_Q8_0 || t == GGML_TYPE_Q4_K; }
+
+// Fusion chains of a graph (ggml_backend.hip): end[i] is the node index at which node i's work
+// runs (i itself, or the last node of the chain it starts or belongs to); member[i] is true for a
+// node whose result is folded into a later node of its chain and never materialized.
+struct Chains {
+    std::vector<int> end;
+    std::vector<bool> member;
+};
+Chains find_chains(const ggml_cgraph * g);
+
+}  // namespace gcq

@@ -14,11 +14,17 @@ from pathlib import Path
 
 _PKG = Path(__file__).resolve().parent
 LIBRARY = _PKG.parent / "lib" / "libgcq.so"
-HEADERS = [_PKG.parents[1] / "include" / "gcq.h", _PKG.parents[1] / "include" / "ggml_compiler_rt.h"]
+HEADERS = [_PKG.parents[1] / "include" / h for h in ("gcq.h", "ggml_compiler_rt.h", "ggml.h", "ggml-backend.h",
+                                                     "ggml-alloc.h")]
 
 
 class GcqError(RuntimeError):
     """An error reported by libgcq (its gcq_last_error / ggml_compiler_last_error text)."""
+
+
+class InitParams(ctypes.Structure):
+    """struct ggml_init_params (include/ggml.h)."""
+    _fields_ = [("mem_size", ctypes.c_size_t), ("mem_buffer", ctypes.c_void_p), ("no_alloc", ctypes.c_bool)]
 
 
 class _Options(ctypes.Structure):
@@ -43,6 +49,7 @@ p, i32, i64, u64, sz, f32 = (ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctyp
 SIGNATURES = {
     "gcq_version": ([], ctypes.c_char_p),
     "gcq_last_error": ([], ctypes.c_char_p),
+    "gcq_error_count": ([], u64),
     "gcq_device_count": ([], i32),
     "gcq_row_size": ([i32, i64], sz),
     "gcq_weight_size": ([i32, i64, i64], sz),
@@ -92,6 +99,110 @@ SIGNATURES = {
     "ggml_compiler_has_backend": ([i32], ctypes.c_bool),
     "ggml_compiler_quantize": ([ctypes.c_char_p, p, i64, i64, p, sz], sz),
     "ggml_compiler_row_size": ([ctypes.c_char_p, i64], sz),
+    # ggml.h (contexts, tensors and graphs are opaque pointers here; ggml.py views tensors)
+    "ggml_last_error": ([], ctypes.c_char_p),
+    "ggml_init": ([InitParams], p),
+    "ggml_free": ([p], None),
+    "ggml_tensor_overhead": ([], sz),
+    "ggml_graph_overhead": ([], sz),
+    "ggml_graph_overhead_custom": ([sz, ctypes.c_bool], sz),
+    "ggml_type_size": ([i32], sz),
+    "ggml_blck_size": ([i32], i64),
+    "ggml_row_size": ([i32, i64], sz),
+    "ggml_type_name": ([i32], ctypes.c_char_p),
+    "ggml_is_quantized": ([i32], ctypes.c_bool),
+    "ggml_op_name": ([i32], ctypes.c_char_p),
+    "ggml_op_desc": ([p], ctypes.c_char_p),
+    "ggml_nelements": ([p], i64),
+    "ggml_nrows": ([p], i64),
+    "ggml_nbytes": ([p], sz),
+    "ggml_is_contiguous": ([p], ctypes.c_bool),
+    "ggml_is_transposed": ([p], ctypes.c_bool),
+    "ggml_is_permuted": ([p], ctypes.c_bool),
+    "ggml_is_vector": ([p], ctypes.c_bool),
+    "ggml_is_matrix": ([p], ctypes.c_bool),
+    "ggml_are_same_shape": ([p, p], ctypes.c_bool),
+    "ggml_can_repeat": ([p, p], ctypes.c_bool),
+    "ggml_new_tensor": ([p, i32, i32, ctypes.POINTER(ctypes.c_int64)], p),
+    "ggml_new_tensor_1d": ([p, i32, i64], p),
+    "ggml_new_tensor_2d": ([p, i32, i64, i64], p),
+    "ggml_new_tensor_3d": ([p, i32, i64, i64, i64], p),
+    "ggml_new_tensor_4d": ([p, i32, i64, i64, i64, i64], p),
+    "ggml_set_name": ([p, ctypes.c_char_p], p),
+    "ggml_get_name": ([p], ctypes.c_char_p),
+    "ggml_get_tensor": ([p, ctypes.c_char_p], p),
+    "ggml_get_first_tensor": ([p], p),
+    "ggml_get_next_tensor": ([p, p], p),
+    "ggml_set_input": ([p], None),
+    "ggml_set_output": ([p], None),
+    "ggml_view_1d": ([p, p, i64, sz], p),
+    "ggml_view_2d": ([p, p, i64, i64, sz, sz], p),
+    "ggml_view_3d": ([p, p, i64, i64, i64, sz, sz, sz], p),
+    "ggml_view_4d": ([p, p, i64, i64, i64, i64, sz, sz, sz, sz], p),
+    "ggml_view_tensor": ([p, p], p),
+    "ggml_reshape": ([p, p, p], p),
+    "ggml_reshape_1d": ([p, p, i64], p),
+    "ggml_reshape_2d": ([p, p, i64, i64], p),
+    "ggml_reshape_3d": ([p, p, i64, i64, i64], p),
+    "ggml_reshape_4d": ([p, p, i64, i64, i64, i64], p),
+    "ggml_permute": ([p, p, i32, i32, i32, i32], p),
+    "ggml_transpose": ([p, p], p),
+    "ggml_cont": ([p, p], p),
+    "ggml_cpy": ([p, p, p], p),
+    "ggml_cast": ([p, p, i32], p),
+    "ggml_add": ([p, p, p], p),
+    "ggml_mul": ([p, p, p], p),
+    "ggml_scale": ([p, p, f32], p),
+    "ggml_scale_bias": ([p, p, f32, f32], p),
+    "ggml_mul_mat": ([p, p, p], p),
+    "ggml_prec_set_acc": ([p, i32], None),
+    "ggml_mul_mat_set_prec": ([p, i32], None),
+    "ggml_flash_attn_ext_set_prec": ([p, i32], None),
+    "ggml_rms_norm": ([p, p, f32], p),
+    "ggml_rope_ext": ([p, p, p, p, i32, i32, i32, f32, f32, f32, f32, f32, f32], p),
+    "ggml_get_rows": ([p, p, p], p),
+    "ggml_set_rows": ([p, p, p, p], p),
+    "ggml_flash_attn_ext": ([p, p, p, p, p, f32, f32, f32], p),
+    "ggml_swiglu_split": ([p, p, p], p),
+    "ggml_argmax": ([p, p], p),
+    "ggml_new_graph": ([p], p),
+    "ggml_new_graph_custom": ([p, sz, ctypes.c_bool], p),
+    "ggml_build_forward_expand": ([p, p], None),
+    "ggml_graph_n_nodes": ([p], i32),
+    "ggml_graph_node": ([p, i32], p),
+    "ggml_graph_add_node": ([p, p], None),
+    "ggml_graph_clear": ([p], None),
+    # ggml-backend.h
+    "ggml_backend_hip_init": ([i32], p),
+    "ggml_backend_is_hip": ([p], ctypes.c_bool),
+    "ggml_backend_free": ([p], None),
+    "ggml_backend_name": ([p], ctypes.c_char_p),
+    "ggml_backend_synchronize": ([p], None),
+    "ggml_backend_get_default_buffer_type": ([p], p),
+    "ggml_backend_buft_name": ([p], ctypes.c_char_p),
+    "ggml_backend_supports_op": ([p, p], ctypes.c_bool),
+    "ggml_backend_graph_compute": ([p, p], i32),
+    "ggml_backend_hip_set_use_graphs": ([p, ctypes.c_bool], None),
+    "ggml_backend_alloc_ctx_tensors": ([p, p], p),
+    "ggml_backend_alloc_ctx_tensors_from_buft": ([p, p], p),
+    "ggml_backend_buffer_free": ([p], None),
+    "ggml_backend_buffer_get_size": ([p], sz),
+    "ggml_backend_buffer_get_base": ([p], p),
+    "ggml_backend_buffer_clear": ([p, ctypes.c_uint8], None),
+    "ggml_backend_buffer_is_host": ([p], ctypes.c_bool),
+    "ggml_backend_buft_get_alloc_size": ([p, p], sz),
+    "ggml_backend_tensor_set": ([p, p, sz, sz], None),
+    "ggml_backend_tensor_get": ([p, p, sz, sz], None),
+    "ggml_backend_tensor_memset": ([p, ctypes.c_uint8, sz, sz], None),
+    "ggml_backend_tensor_copy": ([p, p], None),
+    "ggml_backend_view_init": ([p], i32),
+    "ggml_status_to_string": ([i32], ctypes.c_char_p),
+    # ggml-alloc.h
+    "ggml_gallocr_new": ([p], p),
+    "ggml_gallocr_free": ([p], None),
+    "ggml_gallocr_reserve": ([p, p], ctypes.c_bool),
+    "ggml_gallocr_alloc_graph": ([p, p], ctypes.c_bool),
+    "ggml_gallocr_get_buffer_size": ([p, i32], sz),
 }
 
 

@@ -42,6 +42,9 @@ enum {
 
 GCQ_API const char * gcq_version(void);
 GCQ_API const char * gcq_last_error(void);
+/* Errors recorded by the calling thread so far: lets a caller of a void function (ggml_backend_tensor_set
+ * and the like, whose ggml originals abort) see whether it failed. */
+GCQ_API uint64_t gcq_error_count(void);
 /* Number of gfx950 devices HIP reports (0 when none is present or HIP cannot start). */
 GCQ_API int gcq_device_count(void);
 

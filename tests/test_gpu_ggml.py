@@ -1,0 +1,365 @@
+"""The ggml API subset on the HIP backend: graphs built with ggml calls, allocated by the graph
+allocator and run by ggml_backend_graph_compute, against the oracle (1e-3 by the reference's parity
+metric for float results, bit-exact for integer and byte results) and against libgcq's direct
+entry points, which run the same kernels (bit-exact). Covers every supported node, each fusion
+chain and its unfused twin, HIP-graph replay with changing inputs, the allocator's memory reuse,
+the errors for nodes off the path, and a Llama decoder built node by node as the reference's
+decode stage builds it (ggml_compiler/llm.py:361-444) against the oracle's run of that model."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import to_np
+from ggml_compiler_amd import ggml as G
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+TOL_LM = 1e-2
+NP = {0: np.float32, 1: np.uint16, 26: np.int32}
+
+
+@pytest.fixture(scope="module")
+def be(gops):
+    b = G.Backend(0)
+    yield b
+    b.close()
+
+
+class Graph:
+    """Leaves in one device buffer, nodes built by `build`, allocated and computed."""
+
+    def __init__(self, be, leaves, build, outputs=(), use_graphs=True):
+        g = G.lib()
+        self.g, self.be = g, be
+        self.wctx = G.init()
+        self.L = {}
+        for name, (typ, ne, data) in leaves.items():
+            t = g.ggml_new_tensor(self.wctx, typ, len(ne), (G.ctypes.c_int64 * len(ne))(*ne))
+            G.T(t)
+            g.ggml_set_name(t, name.encode())
+            self.L[name] = t
+        self.buf = g.ggml_backend_alloc_ctx_tensors(self.wctx, be.be)
+        assert self.buf, g.ggml_last_error()
+        for name, (typ, ne, data) in leaves.items():
+            if data is not None:
+                G.set_data(self.L[name], data)
+        self.ctx = G.init()
+        built = build(g, self.ctx, self.L)
+        built = built if isinstance(built, list) else [built]
+        self.out = built[0]
+        for t in outputs:
+            g.ggml_set_output(t(self) if callable(t) else t)
+        self.graph = g.ggml_new_graph(self.ctx)
+        for t in built:
+            G.T(t)
+            g.ggml_build_forward_expand(self.graph, t)
+        self.ga = g.ggml_gallocr_new(g.ggml_backend_get_default_buffer_type(be.be))
+        assert g.ggml_gallocr_alloc_graph(self.ga, self.graph), g.ggml_last_error()
+        g.ggml_backend_hip_set_use_graphs(be.be, use_graphs)
+
+    def run(self, t=None):
+        G.compute(self.be.be, self.graph)
+        t = self.out if t is None else t
+        return G.get_data(t, NP[G.T(t).type])
+
+    def close(self):
+        self.g.ggml_gallocr_free(self.ga)
+        self.g.ggml_free(self.ctx)
+        self.g.ggml_backend_buffer_free(self.buf)
+        self.g.ggml_free(self.wctx)
+        self.g.ggml_backend_hip_set_use_graphs(self.be.be, True)
+
+
+def _weight(orc, t, N, K, seed):
+    return orc.quantize(orc.normal((N, K), seed=seed, std=0.02), t)
+
+
+# ------------------------------------------------------------------------------- mul_mat
+
+@pytest.mark.parametrize("t", ["q4_0", "q8_0", "q4_K"])
+@pytest.mark.parametrize("M", [1, 3, 16])
+def test_mul_mat_node(be, gops, orc, t, M):
+    """The mul_mat node against the oracle, and bit-exact against gcq_mul_mat (the same kernels:
+    decode-row GEMV, GEMV, MFMA GEMM or Q4_K row groups)."""
+    N, K = 300, 1024
+    tid = orc.TYPES[t]
+    raw = _weight(orc, t, N, K, 40 + M)
+    x = orc.normal((M, K), seed=41)
+    gr = Graph(be, {"w": (tid, [K, N], raw), "x": (G.F32, [K, M], x)},
+               lambda g, ctx, L: g.ggml_mul_mat(ctx, L["w"], L["x"]))
+    y = gr.run().reshape(M, N)
+    gr.close()
+    assert orc.parity(y, orc.mul_mat(raw, t, x, K)) < TOL
+    qw = gops.QuantWeight.from_ggml(torch.from_numpy(raw), t, K)
+    assert np.array_equal(y, to_np(gops.mul_mat(qw, torch.from_numpy(x).cuda())))
+
+
+@pytest.mark.parametrize("M", [1, 4, 12])
+@pytest.mark.parametrize("t", ["q4_0", "q8_0"])
+def test_norm_mul_mat_add_chain(be, orc, t, M):
+    """rms_norm -> mul(w) -> mul_mat -> add(residual) folded into one GEMV / GEMM launch sequence,
+    against the oracle and against the same graph with the chain broken (every node launched)."""
+    N, K = 512, 2048
+    tid = orc.TYPES[t]
+    raw = _weight(orc, t, N, K, 50)
+    x = orc.normal((M, K), seed=51)
+    nw = (1.0 + 0.1 * orc.normal((K,), seed=52)).astype(np.float32)
+    r = orc.normal((M, N), seed=53)
+    leaves = {"w": (tid, [K, N], raw), "x": (G.F32, [K, M], x), "nw": (G.F32, [K], nw), "r": (G.F32, [N, M], r)}
+    keep = {}
+
+    def build(g, ctx, L):
+        keep["n"] = g.ggml_rms_norm(ctx, L["x"], 1e-5)
+        keep["m"] = g.ggml_mul(ctx, keep["n"], L["nw"])
+        keep["mm"] = g.ggml_mul_mat(ctx, L["w"], keep["m"])
+        return g.ggml_add(ctx, L["r"], keep["mm"])
+
+    fused = Graph(be, leaves, build)
+    yf = fused.run().reshape(M, N)
+    fused.close()
+    split = Graph(be, leaves, build, outputs=[lambda s: keep["n"], lambda s: keep["mm"]])
+    ys = split.run().reshape(M, N)
+    split.close()
+    ref = orc.mul_mat(raw, t, orc.rms_norm(x, 1e-5) * nw[None, :], K) + r
+    assert orc.parity(yf, ref) < TOL
+    assert orc.parity(ys, ref) < TOL
+    assert orc.parity(yf, ys) < TOL
+
+
+@pytest.mark.parametrize("M", [1, 9])
+def test_swiglu_mul_mat_add_chain(be, orc, M):
+    N, F = 256, 1024
+    raw = _weight(orc, "q4_0", N, F, 60)
+    gt = orc.normal((M, F), seed=61)
+    up = orc.normal((M, F), seed=62)
+    r = orc.normal((M, N), seed=63)
+    gr = Graph(be, {"w": (G.Q4_0, [F, N], raw), "g": (G.F32, [F, M], gt), "u": (G.F32, [F, M], up),
+                    "r": (G.F32, [N, M], r)},
+               lambda g, ctx, L: g.ggml_add(ctx, L["r"], g.ggml_mul_mat(ctx, L["w"],
+                                                                        g.ggml_swiglu_split(ctx, L["g"], L["u"]))))
+    y = gr.run().reshape(M, N)
+    gr.close()
+    assert orc.parity(y, orc.mul_mat(raw, "q4_0", orc.swiglu(gt, up), F) + r) < TOL
+
+
+# ----------------------------------------------------------------------------- attention
+
+@pytest.mark.parametrize("Sq,n_kv,H,Hkv,D", [(1, 300, 8, 2, 128), (5, 130, 4, 4, 64), (1, 1, 32, 8, 128),
+                                             (3, 513, 16, 2, 256)])
+def test_flash_attn_over_cache_views(be, orc, Sq, n_kv, H, Hkv, D):
+    """q as a permuted view [D, Sq, H] of [D, H, Sq]; K and V the first n_kv rows of f16 caches
+    [D, ctx, Hkv]; a causal f16 mask with -inf (every query row sees at least one key)."""
+    ctx_rows = n_kv + 64
+    q = orc.normal((Sq, H, D), seed=70)
+    kc = orc.fp32_to_fp16(orc.normal((Hkv, ctx_rows, D), seed=71))
+    vc = orc.fp32_to_fp16(orc.normal((Hkv, ctx_rows, D), seed=72))
+    pos0 = n_kv - Sq
+    mask = np.where(np.arange(n_kv)[None, :] <= pos0 + np.arange(Sq)[:, None], 0.0, -np.inf).astype(np.float32)
+    m16 = orc.fp32_to_fp16(mask)
+    scale = 1.0 / math.sqrt(D)
+
+    def build(g, ctx, L):
+        qp = g.ggml_permute(ctx, L["q"], 0, 2, 1, 3)
+        kv = g.ggml_view_3d(ctx, L["k"], D, n_kv, Hkv, 2 * D, 2 * D * ctx_rows, 0)
+        vv = g.ggml_view_3d(ctx, L["v"], D, n_kv, Hkv, 2 * D, 2 * D * ctx_rows, 0)
+        o = g.ggml_flash_attn_ext(ctx, qp, kv, vv, L["m"], scale, 0.0, 0.0)
+        g.ggml_prec_set_acc(o, G.PREC_F32)
+        return o
+
+    gr = Graph(be, {"q": (G.F32, [D, H, Sq], q), "k": (G.F16, [D, ctx_rows, Hkv], kc),
+                    "v": (G.F16, [D, ctx_rows, Hkv], vc), "m": (G.F16, [n_kv, Sq], m16)}, build)
+    assert G.lib().ggml_backend_supports_op(be.be, gr.out)
+    y = gr.run().reshape(Sq, H, D)
+    gr.close()
+    ref = orc.flash_attn_ext(q.transpose(1, 0, 2), kc[:, :n_kv], vc[:, :n_kv], m16, scale)
+    assert orc.parity(y, ref) < TOL
+
+
+def test_supports_op_and_off_path_errors(be, orc):
+    g = G.lib()
+    ctx = G.init()
+    q = g.ggml_new_tensor_3d(ctx, G.F32, 96, 1, 4)
+    k = g.ggml_new_tensor_3d(ctx, G.F16, 96, 64, 4)
+    assert not g.ggml_backend_supports_op(be.be, g.ggml_flash_attn_ext(ctx, q, k, k, None, 0.1, 0.0, 0.0))
+    w = g.ggml_new_tensor_2d(ctx, G.F32, 64, 8)
+    x = g.ggml_new_tensor_2d(ctx, G.F32, 64, 1)
+    assert not g.ggml_backend_supports_op(be.be, g.ggml_mul_mat(ctx, w, x))  # f32 weights are off the path
+    assert "weight must be a whole" in g.ggml_last_error().decode()
+    rope = g.ggml_rope_ext(ctx, g.ggml_new_tensor_3d(ctx, G.F32, 64, 2, 1), g.ggml_new_tensor_1d(ctx, G.I32, 1),
+                           None, 64, 0, 0, 1e4, 1, 0, 1, 32, 1)
+    assert not g.ggml_backend_supports_op(be.be, rope)
+    assert "NEOX" in g.ggml_last_error().decode()
+    # a graph whose tensors have no device memory fails to compute, with the reason
+    gr = g.ggml_new_graph(ctx)
+    g.ggml_build_forward_expand(gr, g.ggml_scale(ctx, x, 2.0))
+    assert g.ggml_backend_graph_compute(be.be, gr) == -1
+    assert "no memory" in g.ggml_last_error().decode()
+    g.ggml_free(ctx)
+
+
+# --------------------------------------------------------------------- rope, rows, copies
+
+def test_rope_node_on_a_strided_view(be, orc):
+    """rope of q taken as a view of a fused projection row block ([D, H, S] with a wider head
+    stride), positions per token."""
+    D, H, S, Hx = 128, 6, 4, 8
+    big = orc.normal((S, Hx, D), seed=80)
+    pos = np.array([3, 700, 1, 4095], np.int32)
+
+    def build(g, ctx, L):
+        v = g.ggml_view_3d(ctx, L["x"], D, H, S, 4 * D, 4 * D * Hx, 4 * D)  # heads 1..6
+        return g.ggml_rope_ext(ctx, v, L["p"], None, D, G.ROPE_NEOX, 0, 500000.0, 1.0, 0.0, 1.0, 32.0, 1.0)
+
+    gr = Graph(be, {"x": (G.F32, [D, Hx, S], big), "p": (G.I32, [S], pos)}, build)
+    y = gr.run().reshape(S, H, D)
+    gr.close()
+    assert orc.parity(y, orc.rope_neox(big[:, 1:7], pos, D, 500000.0)) < TOL
+
+
+def test_set_rows_then_get_rows(be, orc):
+    """set_rows of a permuted f32 block into an f16 cache (exact f16 rounding, other rows untouched);
+    get_rows of a Q4_0 table (bit-exact dequantized rows)."""
+    D, Hkv, rows, n = 64, 2, 32, 3
+    k = orc.normal((n, Hkv, D), seed=90)
+    idx = np.array([5, 0, 31], np.int32)
+    init = orc.fp32_to_fp16(orc.normal((Hkv, rows, D), seed=91))
+
+    def build(g, ctx, L):
+        return g.ggml_set_rows(ctx, L["c"], g.ggml_permute(ctx, L["k"], 0, 2, 1, 3), L["i"])
+
+    gr = Graph(be, {"c": (G.F16, [D, rows, Hkv], init), "k": (G.F32, [D, Hkv, n], k), "i": (G.I32, [n], idx)},
+               build)
+    gr.run()
+    got = G.get_data(gr.L["c"], np.uint16).reshape(Hkv, rows, D)
+    gr.close()
+    want = init.copy()
+    want[:, idx] = orc.fp32_to_fp16(k.transpose(1, 0, 2))
+    assert np.array_equal(got, want)
+
+    V, E = 100, 256
+    tab = _weight(orc, "q4_0", V, E, 92)
+    ids = np.array([7, 99, 0, 7], np.int32)
+    gr = Graph(be, {"t": (G.Q4_0, [E, V], tab), "i": (G.I32, [4], ids)},
+               lambda g, ctx, L: g.ggml_get_rows(ctx, L["t"], L["i"]))
+    y = gr.run().reshape(4, E)
+    back = G.get_data(gr.L["t"], np.uint8)  # the packed weight read back as ggml bytes
+    gr.close()
+    assert np.array_equal(y, orc.dequantize(tab[ids], "q4_0", E))
+    assert np.array_equal(back.reshape(V, -1), tab)
+
+
+def test_cont_cast_scale_binary_argmax(be, orc):
+    a = orc.normal((3, 5, 8), seed=100)  # ggml [8, 5, 3]
+    b = orc.normal((8,), seed=101)
+    outs = {}
+
+    def build(g, ctx, L):
+        p = g.ggml_permute(ctx, L["a"], 0, 2, 1, 3)  # [8, 3, 5]
+        outs["cont"] = g.ggml_cont(ctx, p)
+        outs["f16"] = g.ggml_cast(ctx, p, G.F16)
+        outs["back"] = g.ggml_cast(ctx, outs["f16"], G.F32)
+        outs["scale"] = g.ggml_scale_bias(ctx, L["a"], 0.5, 2.0)
+        outs["add"] = g.ggml_add(ctx, L["a"], L["b"])
+        outs["mul"] = g.ggml_mul(ctx, outs["add"], L["b"])
+        outs["amax"] = g.ggml_argmax(ctx, g.ggml_reshape_2d(ctx, outs["mul"], 8, 15))
+        outs["glu"] = g.ggml_swiglu_split(ctx, L["a"], outs["scale"])
+        for t in outs.values():
+            g.ggml_set_output(t)
+        return list(outs.values())
+
+    gr = Graph(be, {"a": (G.F32, [8, 5, 3], a), "b": (G.F32, [8], b)}, build)
+    gr.run()
+    got = {k: G.get_data(t, NP[G.T(t).type]) for k, t in outs.items()}
+    gr.close()
+    pa = a.transpose(1, 0, 2)
+    assert np.array_equal(got["cont"], pa.reshape(-1))
+    assert np.array_equal(got["f16"], orc.fp32_to_fp16(pa).reshape(-1))
+    assert np.array_equal(got["back"], orc.fp16_to_fp32(orc.fp32_to_fp16(pa)).reshape(-1))
+    assert np.allclose(got["scale"], (a * 0.5 + 2.0).reshape(-1), rtol=0, atol=1e-6)
+    s = a + b
+    assert np.array_equal(got["add"], s.reshape(-1))
+    assert np.array_equal(got["mul"], (s * b).reshape(-1))
+    assert np.array_equal(got["amax"], np.argmax((s * b).reshape(15, 8), axis=1).astype(np.int32))
+    assert orc.parity(got["glu"], orc.swiglu(a, a * 0.5 + 2.0).reshape(-1)) < 1e-6
+
+
+# -------------------------------------------------------------------- replay, allocation
+
+def test_graph_replay_with_new_inputs(be, orc):
+    """The captured HIP graph is replayed for each compute; inputs set in between are read; every
+    replay equals the launches run one by one (graphs off)."""
+    N, K = 512, 1024
+    raw = _weight(orc, "q4_0", N, K, 110)
+    nw = np.ones(K, np.float32)
+
+    def build(g, ctx, L):
+        return g.ggml_mul_mat(ctx, L["w"], g.ggml_mul(ctx, g.ggml_rms_norm(ctx, L["x"], 1e-5), L["nw"]))
+
+    leaves = {"w": (G.Q4_0, [K, N], raw), "x": (G.F32, [K, 1], None), "nw": (G.F32, [K], nw)}
+    results = {}
+    for use in (True, False):
+        gr = Graph(be, leaves, build, use_graphs=use)
+        outs = []
+        for seed in (111, 112, 111, 113):
+            G.set_data(gr.L["x"], orc.normal((1, K), seed=seed))
+            outs.append(gr.run().copy())
+        gr.close()
+        results[use] = outs
+    for a, b in zip(results[True], results[False]):
+        assert np.array_equal(a, b)
+    assert np.array_equal(results[True][0], results[True][2])
+    assert not np.array_equal(results[True][0], results[True][1])
+    ref = orc.mul_mat(raw, "q4_0", orc.rms_norm(orc.normal((1, K), seed=113), 1e-5), K)
+    assert orc.parity(results[True][3].reshape(1, N), ref) < TOL
+
+
+def test_allocator_reuses_memory(be, orc):
+    """A chain of 12 elementwise nodes over 1 MiB each needs a few live buffers, not 12."""
+    n = 1 << 18
+    x = orc.normal((n,), seed=120)
+
+    def build(g, ctx, L):
+        t = L["x"]
+        for i in range(12):
+            t = g.ggml_scale_bias(ctx, t, 1.0, 1.0)
+        return t
+
+    gr = Graph(be, {"x": (G.F32, [n], x)}, build)
+    size = G.lib().ggml_gallocr_get_buffer_size(gr.ga, 0)
+    y = gr.run()
+    gr.close()
+    assert size <= 3 * 4 * n
+    assert np.allclose(y, x + 12.0, rtol=0, atol=1e-4)
+
+
+# ------------------------------------------------------------------------ decoder graph
+
+@pytest.mark.parametrize("wtype", [2, 8])
+def test_decode_graph_matches_oracle_and_fused_model(be, orc, wtype):
+    """The decode step built with ggml calls (separate q / k / v and gate / up weights, f16 cache
+    written by set_rows, flash attention over cache views with an f16 mask) for 8 tokens: logits
+    against the oracle's run of the same model and against the hand-fused decoder."""
+    from ggml_compiler_amd.llm import LlamaConfig, Model
+    from llama_ref import OracleLlama
+
+    cfg = LlamaConfig(n_layer=2, n_embd=256, n_head=4, n_head_kv=2, head_dim=64, n_ff=512, n_vocab=1000,
+                      max_ctx=256, wtype=wtype, rms_eps=1e-5, rope_base=10000.0)
+    m = Model(cfg, max_prompt=16)
+    m.init_random(seed=11)
+    w = {name: m.get_weight(name) for name, *_ in m.weights()}
+    o = OracleLlama(cfg, w)
+    dg = G.DecodeGraph(be, cfg, w, n_kv=256)
+    tok = 17
+    for p in range(8):
+        lg = dg.step(tok, p)
+        lo = o.forward([tok])
+        lm, _ = m.decode(tok)
+        assert orc.parity(lg, lo) < TOL_LM, p
+        assert orc.parity(lg, lm) < TOL_LM, p
+        tok = int(np.argmax(lo))
+    dg.reset()
+    assert orc.parity(dg.step(17, 0), OracleLlama(cfg, w).forward([17])) < TOL_LM
+    dg.close()
