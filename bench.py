@@ -1,6 +1,6 @@
 """Benchmark of the quantized mat-mul / KV-cache attention path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--mode decode|gemv|roofline|sweep]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--mode decode|gemv|roofline|sweep|gemm|ggml]
 
 Prints one JSON line. Default workload (mode "decode"): a random-init Llama-3-8B-shaped decoder
 (32 layers, hidden 4096, GQA 32/8 x 128, SwiGLU 14336, vocab 128256, every matmul weight Q4_0,
@@ -222,6 +222,45 @@ def bench_decode(args, torch) -> tuple[dict, object]:
     return res, m
 
 
+def bench_ggml_decode(args) -> dict:
+    """The same 8B-shaped model's decode step built node by node with the ggml API
+    (ggml_compiler_amd.ggml.DecodeGraph: separate q / k / v and gate / up mul_mats, rope, set_rows,
+    flash_attn_ext over cache views with an f16 mask, n_kv = 768 as the reference pads it for
+    positions 512..639) and run by ggml_backend_graph_compute, one host round trip per token
+    (inputs set, graph replayed, logits read back, greedy argmax on the host) as the reference's
+    decode entry runs (llm.py:550-634)."""
+    import numpy as np
+
+    from ggml_compiler_amd import ggml as G
+    from ggml_compiler_amd.llm import LlamaConfig, Model
+
+    cfg = LlamaConfig.llama3_8b(max_ctx=768)
+    m = Model(cfg, max_prompt=16)
+    m.init_random(seed=0, std=0.02)
+    w = {name: m.get_weight(name) for name, *_ in m.weights()}
+    m.close()
+    be = G.Backend(0)
+    dg = G.DecodeGraph(be, cfg, w, n_kv=768)
+    del w
+    prompt = np.random.default_rng(0).integers(0, cfg.n_vocab, PROMPT).tolist()
+    t0 = time.perf_counter()
+    for p, tok in enumerate(prompt):
+        lg = dg.step(tok, p)
+    t_prompt = time.perf_counter() - t0
+    tok = int(np.argmax(lg))
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        tok = int(np.argmax(dg.step(tok, PROMPT + i)))
+    dt = time.perf_counter() - t0
+    dg.close()
+    be.close()
+    return {"metric": "decode tok/s, ggml graph API (host loop)", "value": round(args.steps / dt, 2),
+            "unit": "tok/s", "steps": args.steps, "ms_per_step": round(dt / args.steps * 1e3, 4),
+            "prompt_tok_s_one_token_graphs": round(PROMPT / t_prompt, 1),
+            "config": {"workload": f"Llama-3-8B-shaped Q4_0 decoder (random init), {PROMPT} prompt tokens fed one "
+                                   f"per graph, then {args.steps} greedy tokens; n_kv 768"}}
+
+
 def cpu_decode_baseline(m, seconds: float = 15.0) -> dict:
     """The CPU oracle (repo restatement of ggml-cpu, OpenMP) decoding the same 8B-shaped model on the
     host cores: a 4-token prompt, then greedy tokens until `seconds` have passed."""
@@ -348,17 +387,19 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--mode", choices=["decode", "gemv", "roofline", "sweep", "gemm"], default="decode",
+    ap.add_argument("--mode", choices=["decode", "gemv", "roofline", "sweep", "gemm", "ggml"], default="decode",
                     help="roofline: only the roofline leg and a 1 GiB copy (for rocprofv3 --pmc runs); "
                          "sweep: the GEMV / GEMM / attention configurations, one JSON line each; "
-                         "gemm: the prefill GEMM configuration alone, --steps launches (for counter runs)")
+                         "gemm: the prefill GEMM configuration alone, --steps launches (for counter runs); "
+                         "ggml: the decode step built with the ggml API and run by its graph executor")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for {args.gpus}); multi-GPU sharding is design-only here.",
               file=sys.stderr)
         return 2
-    args.steps = args.steps or {"decode": 128, "gemv": 200, "roofline": 10, "sweep": 1, "gemm": 3}[args.mode]
+    args.steps = args.steps or {"decode": 128, "gemv": 200, "roofline": 10, "sweep": 1, "gemm": 3,
+                                "ggml": 128}[args.mode]
     args.warmup = args.warmup if args.warmup is not None else 8
 
     import torch
@@ -382,6 +423,9 @@ def main() -> int:
         us = e0.elapsed_time(e1) * 1e3 / args.steps
         print(json.dumps({"metric": "prefill GEMM TOP/s", "value": round(2 * 512 * 14336 * 4096 / us / 1e6, 1),
                           "unit": "TOP/s", "us": round(us, 1)}), flush=True)
+        return 0
+    if args.mode == "ggml":
+        print(json.dumps(bench_ggml_decode(args)), flush=True)
         return 0
     if args.mode == "sweep":
         for r in bench_sweep(ops, torch):

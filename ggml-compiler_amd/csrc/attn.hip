@@ -237,14 +237,16 @@ __device__ __forceinline__ float half_at(const uint4 & r, int c) {
     return h2f((uint16_t) (c & 1 ? w >> 16 : w & 0xffff));
 }
 
-template <int D, int G, int NW>
+// MASK: an f16 mask row (n_kv values, ggml's [n_kv, 1] mask of one query row) is added to the
+// scaled scores, -inf dropping a key.
+template <int D, int G, int NW, bool MASK>
 __global__ __launch_bounds__(NW * 64) void k_attn_decode(int GT, const float * __restrict__ q, int64_t q_h,
                                                          const uint16_t * __restrict__ k, int64_t k_h, int64_t k_j,
                                                          const uint16_t * __restrict__ v, int64_t v_h, int64_t v_j,
                                                          float scale, int n_kv, const int * __restrict__ n_kv_dev,
                                                          int chunk, int kv_rows, int nsplit, float * __restrict__ out,
                                                          float * __restrict__ part_o, float2 * __restrict__ part_ml,
-                                                         const Prefetch pf) {
+                                                         const Prefetch pf, const uint16_t * __restrict__ mask) {
     constexpr int LPK = D / 8;     // lanes per key row
     constexpr int KPW = 64 / LPK;  // lane groups (keys per step) per wavefront
     constexpr int NB = decode_nb(G);  // steps per load batch
@@ -283,12 +285,14 @@ __global__ __launch_bounds__(NW * 64) void k_attn_decode(int GT, const float * _
     const uint16_t * kb = k + (int64_t) hk * k_h + 8 * sub;
     const uint16_t * vb = v + (int64_t) hk * v_h + 8 * sub;
     uint4 kr[NB], vr[NB];
+    uint16_t mk[NB];
     auto load = [&](int base) {
 #pragma unroll
         for (int b = 0; b < NB; b++) {
             const int64_t row = min(j0 + base + b * KPW + slot, kv_rows - 1);
             kr[b] = *reinterpret_cast<const uint4 *>(kb + row * k_j);
             vr[b] = *reinterpret_cast<const uint4 *>(vb + row * v_j);
+            if constexpr (MASK) mk[b] = mask[min(j0 + base + b * KPW + slot, n_kv - 1)];
         }
     };
     if (w0 < w1) load(w0);
@@ -334,7 +338,8 @@ __global__ __launch_bounds__(NW * 64) void k_attn_decode(int GT, const float * _
                 a = __builtin_amdgcn_fdot2(as_h2(kr[b].w), qh[g][3], a, false);
                 a = group_reduce<LPK, float, op_add<float>>(a);
                 const int jj = base + b * KPW + slot;
-                sc[b] = jj < w1 && jj < len ? a * scale : -INFINITY;
+                if constexpr (MASK) sc[b] = jj < w1 && jj < len ? a * scale + h2f(mk[b]) : -INFINITY;
+                else sc[b] = jj < w1 && jj < len ? a * scale : -INFINITY;
                 bm = fmaxf(bm, sc[b]);
             }
             const float mn = fmaxf(m[g], bm);
@@ -504,7 +509,8 @@ bool attn_decode_fits(int D, int G) { return (D == 64 || D == 128) && (G == 1 ||
 void launch_attn_decode(const float * q, int64_t q_h, const void * k, int64_t k_h, int64_t k_j, const void * v,
                         int64_t v_h, int64_t v_j, int D, int H, int Hkv, int n_kv, const int * n_kv_dev, float scale,
                         int nsplit, int chunk, int kv_rows, int GS, float * out, float * part_o, float2 * part_ml,
-                        hipStream_t s, const Prefetch * pf) {
+                        hipStream_t s, const Prefetch * pf,
+                        const void * mask) {
     const int G = H / Hkv;
     require(attn_decode_fits(D, G) && H % Hkv == 0, "attn decode: D 64 / 128 and 1, 2 or 4 query heads per KV head");
     require(GS >= 1 && G % GS == 0, "attn decode: head group must divide the query heads per KV head");
@@ -522,10 +528,18 @@ void launch_attn_decode(const float * q, int64_t q_h, const void * k, int64_t k_
     }
     const dim3 grid((unsigned) (nsplit + extra), (unsigned) Hkv, (unsigned) (G / GS));
     const uint16_t *kp = (const uint16_t *) k, *vp = (const uint16_t *) v;
+    const uint16_t * mp = (const uint16_t *) mask;
 #define GCQ_AD(DD, GG)                                                                                          \
-    if (D == DD && GS == GG)                                                                                    \
-        k_attn_decode<DD, GG, decode_waves(GG)><<<grid, decode_waves(GG) * 64, 0, s>>>(                         \
-            G, q, q_h, kp, k_h, k_j, vp, v_h, v_j, scale, n_kv, n_kv_dev, chunk, kv_rows, nsplit, out, part_o, part_ml, P);
+    if (D == DD && GS == GG) {                                                                                  \
+        if (mp)                                                                                                 \
+            k_attn_decode<DD, GG, decode_waves(GG), true><<<grid, decode_waves(GG) * 64, 0, s>>>(               \
+                G, q, q_h, kp, k_h, k_j, vp, v_h, v_j, scale, n_kv, n_kv_dev, chunk, kv_rows, nsplit, out, part_o, \
+                part_ml, P, mp);                                                                                \
+        else                                                                                                    \
+            k_attn_decode<DD, GG, decode_waves(GG), false><<<grid, decode_waves(GG) * 64, 0, s>>>(              \
+                G, q, q_h, kp, k_h, k_j, vp, v_h, v_j, scale, n_kv, n_kv_dev, chunk, kv_rows, nsplit, out, part_o, \
+                part_ml, P, nullptr);                                                                           \
+    }
     GCQ_AD(64, 1) GCQ_AD(64, 2) GCQ_AD(64, 4) GCQ_AD(128, 1) GCQ_AD(128, 2) GCQ_AD(128, 4)
 #undef GCQ_AD
     check_launch("attn decode");
@@ -589,13 +603,13 @@ void launch_flash_attn(const float * q, int64_t q_h, int64_t q_s, const void * k
     require(ws_size >= attn_workspace(Sq, H, Hkv, Dv, n_kv), "flash_attn: workspace too small");
     float * po = (float *) ws;
     float2 * pml = (float2 *) ((uint8_t *) ws + align256((size_t) Sq * H * p.nsplit * Dv * sizeof(float)));
-    if (Sq == 1 && mask == nullptr && H % Hkv == 0 && attn_decode_fits(D, H / Hkv)) {
-        // One query row, every key visible: the one-pass decode kernel (fewer splits than p, so the
-        // workspace holds its partials).
+    if (Sq == 1 && H % Hkv == 0 && attn_decode_fits(D, H / Hkv)) {
+        // One query row (its mask row added to the scores, if any): the one-pass decode kernel
+        // (fewer splits than p, so the workspace holds its partials).
         const int GS = decode_group(H / Hkv, n_kv);
         const int nsplit = decode_splits(D, GS, n_kv, p.nsplit);
         launch_attn_decode(q, q_h, k, k_h, k_j, v, v_h, v_j, D, H, Hkv, n_kv, nullptr, scale, nsplit,
-                           (n_kv + nsplit - 1) / nsplit, n_kv, GS, out, po, pml, s, nullptr);
+                           (n_kv + nsplit - 1) / nsplit, n_kv, GS, out, po, pml, s, nullptr, mask);
         if (nsplit == 1) return;
         if (D == 64) k_attn_merge<64><<<(unsigned) H, 64, 0, s>>>(po, pml, out, nsplit);
         else k_attn_merge<128><<<(unsigned) H, 128, 0, s>>>(po, pml, out, nsplit);

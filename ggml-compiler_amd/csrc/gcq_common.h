@@ -322,7 +322,15 @@ __device__ __forceinline__ int wave_isum(int v) {
 __device__ __forceinline__ float rms_scale(const float * xr, int n, float eps) {
     __shared__ double red[4];
     double s = 0.0;
-    for (int i = threadIdx.x; i < n; i += 256) s += (double) (xr[i] * xr[i]);
+    // Loads of 8 strides issued together, then summed in the same order as one at a time.
+    for (int i0 = threadIdx.x; i0 < n; i0 += 8 * 256) {
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) v[k] = i0 + 256 * k < n ? xr[i0 + 256 * k] : 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+            if (i0 + 256 * k < n) s += (double) (v[k] * v[k]);
+    }
     s = wave_sum_d(s);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
     __syncthreads();

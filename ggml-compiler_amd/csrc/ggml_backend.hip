@@ -261,9 +261,34 @@ Step new_step(int kind) {
 }
 
 struct Cached {
-    std::vector<uint8_t> sig;
+    std::vector<uintptr_t> fp;  // the nodes it was planned from
+    std::vector<uint8_t> sig;   // the steps it holds
     hipGraphExec_t exec = nullptr;
 };
+
+// Everything about g's nodes that planning reads: ops, types, flags, shapes, strides, parameters,
+// sources and every data address. Equal fingerprints plan to equal steps.
+std::vector<uintptr_t> fingerprint(const ggml_cgraph * g) {
+    std::vector<uintptr_t> f;
+    f.reserve(g->nodes.size() * 40);
+    for (const ggml_tensor * t : g->nodes) {
+        f.push_back((uintptr_t) t);
+        f.push_back(((uintptr_t) t->op << 32) | ((uintptr_t) t->type << 16) | (uintptr_t) (t->flags & 0xffff));
+        f.push_back((uintptr_t) t->data);
+        f.push_back((uintptr_t) t->view_offs);
+        for (int i = 0; i < 4; i++) {
+            f.push_back((uintptr_t) t->ne[i]);
+            f.push_back((uintptr_t) t->nb[i]);
+        }
+        for (int i = 0; i < GGML_MAX_OP_PARAMS / 4; i += 2)
+            f.push_back(((uintptr_t) (uint32_t) t->op_params[i] << 32) | (uint32_t) t->op_params[i + 1]);
+        for (const ggml_tensor * s : t->src) {
+            f.push_back((uintptr_t) s);
+            if (s) f.push_back((uintptr_t) s->data);
+        }
+    }
+    return f;
+}
 
 }  // namespace
 
@@ -751,6 +776,15 @@ enum ggml_status compute(ggml_backend * be, ggml_cgraph * g) {
     if (g->nodes.empty()) return GGML_STATUS_SUCCESS;
     set_device(be);
     refresh_views(g);
+    std::vector<uintptr_t> fp = fingerprint(g);
+    if (be->use_graphs) {  // unchanged since the last compute: replay without planning
+        auto it = be->graphs.find(g);
+        if (it != be->graphs.end() && it->second.exec && it->second.fp == fp) {
+            check_hip(hipGraphLaunch(it->second.exec, be->stream), "hipGraphLaunch");
+            check_hip(hipStreamSynchronize(be->stream), "graph compute");
+            return GGML_STATUS_SUCCESS;
+        }
+    }
     const Chains c = find_chains(g);
     be->steps.clear();
     Planner p{be, be->steps};
@@ -780,6 +814,7 @@ enum ggml_status compute(ggml_backend * be, ggml_cgraph * g) {
             if (cc.exec) check_hip(hipGraphExecDestroy(cc.exec), "hipGraphExecDestroy");
             cc.exec = nullptr;
             cc.sig.clear();
+            cc.fp.clear();
             check_hip(hipStreamBeginCapture(be->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
             hipGraph_t graph = nullptr;
             try {
@@ -795,6 +830,7 @@ enum ggml_status compute(ggml_backend * be, ggml_cgraph * g) {
             check_hip(e, "hipGraphInstantiate");
             cc.sig = std::move(sig);
         }
+        cc.fp = std::move(fp);
         check_hip(hipGraphLaunch(cc.exec, be->stream), "hipGraphLaunch");
     }
     check_hip(hipStreamSynchronize(be->stream), "graph compute");

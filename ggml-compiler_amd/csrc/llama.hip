@@ -59,7 +59,7 @@ bool attn_decode_fits(int D, int G);
 void launch_attn_decode(const float * q, int64_t q_h, const void * k, int64_t k_h, int64_t k_j, const void * v,
                         int64_t v_h, int64_t v_j, int D, int H, int Hkv, int n_kv, const int * n_kv_dev, float scale,
                         int nsplit, int chunk, int kv_rows, int GS, float * out, float * part_o, float2 * part_ml,
-                        hipStream_t s, const Prefetch * pf);
+                        hipStream_t s, const Prefetch * pf, const void * mask);
 int decode_group(int GT, int max_kv);
 void launch_embed_rope(int type, const void * tab, int64_t nrows, int64_t D, const int32_t * idx, float * x,
                        const int32_t * pos, int head_dim, float base, void * cs, hipStream_t s);
@@ -390,7 +390,7 @@ struct Llama {
                                    kv_h, c.head_dim, c.head_dim, c.n_head, c.n_head_kv, n_kv, n_kv_dev, scale,
                                    plan.nsplit, plan.chunk, c.max_ctx, decode_group(c.n_head / c.n_head_kv, c.max_ctx),
                                    attn_row.as<float>(), part_o.as<float>(), part_ml.as<float2>(), stream,
-                                   prefetch ? &pf : nullptr);
+                                   prefetch ? &pf : nullptr, nullptr);
             } else
             {
                 launch_attn_split(qkv.as<float>(), c.head_dim, qkv_dim, kvl, kv_h, c.head_dim,
