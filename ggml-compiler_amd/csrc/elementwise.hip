@@ -28,7 +28,20 @@ __global__ __launch_bounds__(256) void k_rms_norm(const float * __restrict__ x, 
     const float * xr = x + blockIdx.x * ldx;
     float * yr = y + blockIdx.x * ldy;
     const float scale = rms_scale(xr, n, eps);
-    for (int i = threadIdx.x; i < n; i += 256) yr[i] = w ? (xr[i] * scale) * w[i] : xr[i] * scale;
+    for (int i0 = threadIdx.x; i0 < n; i0 += 8 * 256) {  // 8 strides of loads in flight at once
+        float xv[8], wv[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int i = i0 + 256 * k;
+            xv[k] = i < n ? xr[i] : 0.0f;
+            wv[k] = i < n && w ? w[i] : 1.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int i = i0 + 256 * k;
+            if (i < n) yr[i] = w ? (xv[k] * scale) * wv[k] : xv[k] * scale;
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------------- rope

@@ -144,14 +144,16 @@ Chains find_chains(const ggml_cgraph * g) {
     Chains c;
     c.end.resize(n);
     c.member.assign(n, false);
+    c.in_fold.assign(n, false);
     for (int i = 0; i < n; i++) c.end[i] = i;
-    std::unordered_map<const ggml_tensor *, int> uses, reader, index;
+    std::unordered_map<const ggml_tensor *, int> uses, reader;
+    std::unordered_map<const ggml_tensor *, std::vector<int>> readers;
     for (int i = 0; i < n; i++) {
-        index[g->nodes[i]] = i;
         for (const ggml_tensor * s : g->nodes[i]->src) {
             if (!s) continue;
             uses[s]++;
             reader[s] = i;
+            readers[s].push_back(i);
         }
     }
     // The one node reading t, if t may be folded into it.
@@ -189,9 +191,31 @@ Chains find_chains(const ggml_cgraph * g) {
                 const int a = with_add(k);
                 if (a >= 0) link({i, j, k, a});
                 else link({i, j, k});
-            } else {
-                link({i, j});
+                continue;
             }
+            // One row read by several GEMVs (q / k / v, gate / up): each normalizes x itself in its
+            // prologue and the normalized row is never written.
+            const std::vector<int> & rd = readers[m];
+            bool rows1 = ggml_nrows(m) == 1 && !is_output(m) && m != g->nodes[n - 1] && rd.size() >= 2;
+            for (int r : rd) {
+                const ggml_tensor * mm = g->nodes[r];
+                rows1 = rows1 && mm->op == GGML_OP_MUL_MAT && mm->src[1] == m && mm->src[0] != m &&
+                        q8_mul_mat(mm) && row_gemv_fits(mm->src[0]->type, m->ne[0]);
+            }
+            if (!rows1) {
+                link({i, j});
+                continue;
+            }
+            c.member[i] = c.member[j] = true;
+            c.in_fold[i] = c.in_fold[j] = true;
+            c.folded.push_back(m);
+            int last = j;
+            for (int r : rd) {
+                const int a = with_add(r);
+                if (a >= 0) link({r, a});
+                last = std::max(last, c.end[r]);
+            }
+            c.end[i] = c.end[j] = last;  // x and w are read until the last reader's work runs
         } else if (t->op == GGML_OP_GLU && f32_contig(t->src[0]) && f32_contig(t->src[1]) && aligned16(t->src[0]) &&
                    aligned16(t->src[1]) && t->ne[0] % 32 == 0) {
             const int k = sole(t);
@@ -205,7 +229,6 @@ Chains find_chains(const ggml_cgraph * g) {
             if (a >= 0) link({i, a});
         }
     }
-    (void) index;
     return c;
 }
 
@@ -371,9 +394,17 @@ struct Planner {
     const char * d(const ggml_tensor * t) const { return dry ? nullptr : data_of(t); }
     void * o(const ggml_tensor * t) const { return dry ? nullptr : mut_data(t); }
 
+    const std::vector<const ggml_tensor *> * folded = nullptr;  // mul(rms_norm(x), w) rows read by GEMVs
+
     void mulmat(const ggml_tensor * mm, const ggml_tensor * x, const ggml_tensor * norm_w, float eps,
                 const ggml_tensor * res, const ggml_tensor * y) {
         const ggml_tensor * w = mm->src[0];
+        if (folded && std::find(folded->begin(), folded->end(), x) != folded->end()) {
+            const ggml_tensor * nrm = x->src[0];
+            norm_w = x->src[1];
+            std::memcpy(&eps, &nrm->op_params[0], 4);
+            x = nrm->src[0];
+        }
         require(whole_packed(w), "mul_mat " + tname(mm) + ": the weight must be a whole Q4_0 / Q8_0 / Q4_K tensor in "
                                                           "a HIP buffer (other weight types are not on this path)");
         require(w->ne[2] == 1 && w->ne[3] == 1, "mul_mat " + tname(mm) + ": batched weights are not supported");
@@ -788,12 +819,13 @@ enum ggml_status compute(ggml_backend * be, ggml_cgraph * g) {
     const Chains c = find_chains(g);
     be->steps.clear();
     Planner p{be, be->steps};
+    p.folded = &c.folded;
     std::vector<int> idx;
     for (int i = 0; i < (int) g->nodes.size(); i++) {
         if (c.member[i]) continue;
         idx.clear();
         for (int j = 0; j < i; j++)  // members of the chain ending here, in order
-            if (c.member[j] && c.end[j] == i) idx.push_back(j);
+            if (c.member[j] && !c.in_fold[j] && c.end[j] == i) idx.push_back(j);
         if (idx.empty()) {
             p.node(g->nodes[i]);
         } else {

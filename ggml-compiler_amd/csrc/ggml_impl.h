@@ -41,11 +41,16 @@ inline bool is_view_op(int op) {
 inline bool is_packed_type(int t) { return t == GGML_TYPE_Q4_0 || t == GGML_TYPE_Q8_0 || t == GGML_TYPE_Q4_K; }
 
 // Fusion chains of a graph (ggml_backend.hip): end[i] is the node index at which node i's work
-// runs (i itself, or the last node of the chain it starts or belongs to); member[i] is true for a
-// node whose result is folded into a later node of its chain and never materialized.
+// runs (i itself, or the last node of the chain it starts or belongs to; for a folded norm, its
+// last reader); member[i] is true for a node whose result is folded into later nodes and never
+// materialized.
 struct Chains {
     std::vector<int> end;
     std::vector<bool> member;
+    // mul(rms_norm(x), w) rows of one row folded into each of their GEMV readers (x and w are
+    // read by every reader; the norm and the mul are members).
+    std::vector<const ggml_tensor *> folded;
+    std::vector<bool> in_fold;  // the norm and mul nodes of a folded row
 };
 Chains find_chains(const ggml_cgraph * g);
 

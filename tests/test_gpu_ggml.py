@@ -49,6 +49,7 @@ class Graph:
         self.ctx = G.init()
         built = build(g, self.ctx, self.L)
         built = built if isinstance(built, list) else [built]
+        self.built = built
         self.out = built[0]
         for t in outputs:
             g.ggml_set_output(t(self) if callable(t) else t)
@@ -127,6 +128,45 @@ def test_norm_mul_mat_add_chain(be, orc, t, M):
     assert orc.parity(yf, ref) < TOL
     assert orc.parity(ys, ref) < TOL
     assert orc.parity(yf, ys) < TOL
+
+
+@pytest.mark.parametrize("t", ["q4_0", "q8_0"])
+def test_norm_row_folded_into_several_gemvs(be, orc, t):
+    """One normalized row read by three mul_mats (q / k / v of a decode step), one of them followed
+    by an add: each GEMV normalizes x in its prologue; against the oracle and the unfolded graph."""
+    K = 2048
+    tid = orc.TYPES[t]
+    Ns = (512, 256, 256)
+    raws = [_weight(orc, t, N, K, 130 + i) for i, N in enumerate(Ns)]
+    x = orc.normal((1, K), seed=134)
+    nw = (1.0 + 0.1 * orc.normal((K,), seed=135)).astype(np.float32)
+    r = orc.normal((1, Ns[2]), seed=136)
+    leaves = {"x": (G.F32, [K, 1], x), "nw": (G.F32, [K], nw), "r": (G.F32, [Ns[2], 1], r)}
+    for i, (N, raw) in enumerate(zip(Ns, raws)):
+        leaves[f"w{i}"] = (tid, [K, N], raw)
+    keep = {}
+
+    def build(g, ctx, L):
+        keep["m"] = g.ggml_mul(ctx, g.ggml_rms_norm(ctx, L["x"], 1e-5), L["nw"])
+        a = g.ggml_mul_mat(ctx, L["w0"], keep["m"])
+        b = g.ggml_mul_mat(ctx, L["w1"], keep["m"])
+        c = g.ggml_add(ctx, g.ggml_mul_mat(ctx, L["w2"], keep["m"]), L["r"])
+        for u in (a, b, c):
+            g.ggml_set_output(u)
+        return [a, b, c]
+
+    got = {}
+    for name, outs in (("fold", ()), ("split", [lambda s: keep["m"]])):
+        gr = Graph(be, leaves, build, outputs=outs)
+        gr.run()
+        got[name] = [G.get_data(gr.built[i], np.float32) for i in range(3)]
+        gr.close()
+    xn = orc.rms_norm(x, 1e-5) * nw[None, :]
+    refs = [orc.mul_mat(raws[0], t, xn, K)[0], orc.mul_mat(raws[1], t, xn, K)[0],
+            orc.mul_mat(raws[2], t, xn, K)[0] + r[0]]
+    for i in range(3):
+        assert orc.parity(got["fold"][i], refs[i]) < TOL, i
+        assert orc.parity(got["split"][i], refs[i]) < TOL, i
 
 
 @pytest.mark.parametrize("M", [1, 9])
