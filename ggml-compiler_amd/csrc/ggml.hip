@@ -40,7 +40,8 @@ const TypeTraits * traits(int type) {
 const char * kOpNames[GGML_OP_COUNT] = {"NONE",    "ADD",      "MUL",      "SCALE",    "CPY",
                                         "CONT",    "RESHAPE",  "VIEW",     "PERMUTE",  "TRANSPOSE",
                                         "GET_ROWS", "SET_ROWS", "RMS_NORM", "MUL_MAT",  "ROPE",
-                                        "FLASH_ATTN_EXT", "ARGMAX", "GLU"};
+                                        "FLASH_ATTN_EXT", "ARGMAX", "GLU", "UNARY", "SOFT_MAX",
+                                        "IM2COL", "CONV_2D_DIRECT"};
 
 // NULL with the reason recorded.
 ggml_tensor * none(const std::string & why) {
@@ -570,6 +571,61 @@ ggml_tensor * ggml_argmax(ggml_context * ctx, ggml_tensor * a) {
     ggml_tensor * t = new_tensor(ctx, GGML_TYPE_I32, 1, &a->ne[1], nullptr, 0, "ggml_argmax");
     if (!t) return nullptr;
     set_src(t, GGML_OP_ARGMAX, {a});
+    return t;
+}
+
+// ------------------------------------------------------------------ off-path constructors
+
+namespace {
+ggml_tensor * unary(ggml_context * ctx, ggml_tensor * a, int uop, const char * what) {
+    if (!a) return nullptr;
+    ggml_tensor * t = dup_shape(ctx, a, a->type, what);
+    if (!t) return nullptr;
+    set_src(t, GGML_OP_UNARY, {a});
+    t->op_params[0] = uop;
+    return t;
+}
+int64_t conv_out(int64_t in, int64_t k, int s, int p, int d) { return (in + 2 * p - d * (k - 1) - 1) / s + 1; }
+}  // namespace
+
+ggml_tensor * ggml_gelu(ggml_context * ctx, ggml_tensor * a) { return unary(ctx, a, GGML_UNARY_OP_GELU, "ggml_gelu"); }
+ggml_tensor * ggml_tanh(ggml_context * ctx, ggml_tensor * a) { return unary(ctx, a, GGML_UNARY_OP_TANH, "ggml_tanh"); }
+ggml_tensor * ggml_sqr(ggml_context * ctx, ggml_tensor * a) { return unary(ctx, a, GGML_UNARY_OP_SQR, "ggml_sqr"); }
+
+ggml_tensor * ggml_soft_max_ext(ggml_context * ctx, ggml_tensor * a, ggml_tensor * mask, float scale,
+                                float max_bias) {
+    if (!a) return nullptr;
+    ggml_tensor * t = dup_shape(ctx, a, a->type, "ggml_soft_max_ext");
+    if (!t) return nullptr;
+    set_src(t, GGML_OP_SOFT_MAX, {a, mask});
+    set_param(t, 0, scale);
+    set_param(t, 1, max_bias);
+    return t;
+}
+
+ggml_tensor * ggml_im2col(ggml_context * ctx, ggml_tensor * a, ggml_tensor * b, int s0, int s1, int p0, int p1,
+                          int d0, int d1, bool is_2D, ggml_type dst_type) {
+    if (!a || !b) return nullptr;
+    if (!is_2D) return none("ggml_im2col: only the 2-D form is declared here");
+    if (s0 <= 0 || s1 <= 0 || d0 <= 0 || d1 <= 0 || a->ne[2] != b->ne[2]) return none("ggml_im2col: bad operands");
+    const int64_t ne[4] = {a->ne[0] * a->ne[1] * a->ne[2], conv_out(b->ne[0], a->ne[0], s0, p0, d0),
+                           conv_out(b->ne[1], a->ne[1], s1, p1, d1), b->ne[3]};
+    ggml_tensor * t = new_tensor(ctx, dst_type, 4, ne, nullptr, 0, "ggml_im2col");
+    if (!t) return nullptr;
+    set_src(t, GGML_OP_IM2COL, {a, b});
+    return t;
+}
+
+ggml_tensor * ggml_conv_2d_direct(ggml_context * ctx, ggml_tensor * a, ggml_tensor * b, int s0, int s1, int p0,
+                                  int p1, int d0, int d1) {
+    if (!a || !b) return nullptr;
+    if (s0 <= 0 || s1 <= 0 || d0 <= 0 || d1 <= 0 || a->ne[2] != b->ne[2])
+        return none("ggml_conv_2d_direct: bad operands");
+    const int64_t ne[4] = {conv_out(b->ne[0], a->ne[0], s0, p0, d0), conv_out(b->ne[1], a->ne[1], s1, p1, d1),
+                           a->ne[3], b->ne[3]};
+    ggml_tensor * t = new_tensor(ctx, b->type, 4, ne, nullptr, 0, "ggml_conv_2d_direct");
+    if (!t) return nullptr;
+    set_src(t, GGML_OP_CONV_2D_DIRECT, {a, b});
     return t;
 }
 

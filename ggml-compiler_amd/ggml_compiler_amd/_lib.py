@@ -165,6 +165,12 @@ SIGNATURES = {
     "ggml_flash_attn_ext": ([p, p, p, p, p, f32, f32, f32], p),
     "ggml_swiglu_split": ([p, p, p], p),
     "ggml_argmax": ([p, p], p),
+    "ggml_gelu": ([p, p], p),
+    "ggml_tanh": ([p, p], p),
+    "ggml_sqr": ([p, p], p),
+    "ggml_soft_max_ext": ([p, p, p, f32, f32], p),
+    "ggml_im2col": ([p, p, p, i32, i32, i32, i32, i32, i32, ctypes.c_bool, i32], p),
+    "ggml_conv_2d_direct": ([p, p, p, i32, i32, i32, i32, i32, i32], p),
     "ggml_new_graph": ([p], p),
     "ggml_new_graph_custom": ([p, sz, ctypes.c_bool], p),
     "ggml_build_forward_expand": ([p, p], None),

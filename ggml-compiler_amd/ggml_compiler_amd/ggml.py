@@ -22,7 +22,8 @@ PREC_F32 = 10
 FLAG_INPUT, FLAG_OUTPUT = 1, 2
 OP = {name: i for i, name in enumerate(
     ["NONE", "ADD", "MUL", "SCALE", "CPY", "CONT", "RESHAPE", "VIEW", "PERMUTE", "TRANSPOSE", "GET_ROWS",
-     "SET_ROWS", "RMS_NORM", "MUL_MAT", "ROPE", "FLASH_ATTN_EXT", "ARGMAX", "GLU"])}
+     "SET_ROWS", "RMS_NORM", "MUL_MAT", "ROPE", "FLASH_ATTN_EXT", "ARGMAX", "GLU", "UNARY", "SOFT_MAX", "IM2COL",
+     "CONV_2D_DIRECT"])}
 
 
 class Tensor(ctypes.Structure):

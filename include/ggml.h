@@ -93,7 +93,17 @@ enum ggml_op {
     GGML_OP_FLASH_ATTN_EXT,
     GGML_OP_ARGMAX,
     GGML_OP_GLU,
+    GGML_OP_UNARY,
+    GGML_OP_SOFT_MAX,
+    GGML_OP_IM2COL,
+    GGML_OP_CONV_2D_DIRECT,
     GGML_OP_COUNT,
+};
+
+enum ggml_unary_op {
+    GGML_UNARY_OP_TANH = 2,
+    GGML_UNARY_OP_GELU = 7,
+    GGML_UNARY_OP_SQR  = 100, /* ggml has sqr as its own op; kept under UNARY here */
 };
 
 enum ggml_glu_op {
@@ -247,6 +257,23 @@ GGML_API struct ggml_tensor * ggml_swiglu_split(struct ggml_context * ctx, struc
                                                 struct ggml_tensor * b);
 /* index of the maximum of each row -> i32 [rows] (ops.cpp:293-300) */
 GGML_API struct ggml_tensor * ggml_argmax(struct ggml_context * ctx, struct ggml_tensor * a);
+
+/* Off the path: declared so that code written against ggml (runtime/include/ggml_compiler_ops.h's
+   conv_2d, gelu_tanh and flash-attention fallback) compiles; they build nodes with ggml's result
+   shapes, which ggml_backend_supports_op rejects and graph_compute reports as unsupported. */
+GGML_API struct ggml_tensor * ggml_gelu(struct ggml_context * ctx, struct ggml_tensor * a);
+GGML_API struct ggml_tensor * ggml_tanh(struct ggml_context * ctx, struct ggml_tensor * a);
+GGML_API struct ggml_tensor * ggml_sqr(struct ggml_context * ctx, struct ggml_tensor * a);
+GGML_API struct ggml_tensor * ggml_soft_max_ext(struct ggml_context * ctx, struct ggml_tensor * a,
+                                                struct ggml_tensor * mask, float scale, float max_bias);
+/* a kernel [KW, KH, IC, OC], b input [W, H, IC, N] -> [IC*KH*KW, OW, OH, N] (is_2D) */
+GGML_API struct ggml_tensor * ggml_im2col(struct ggml_context * ctx, struct ggml_tensor * a, struct ggml_tensor * b,
+                                          int s0, int s1, int p0, int p1, int d0, int d1, bool is_2D,
+                                          enum ggml_type dst_type);
+/* a kernel [KW, KH, IC, OC], b input [W, H, IC, N] -> [OW, OH, OC, N] */
+GGML_API struct ggml_tensor * ggml_conv_2d_direct(struct ggml_context * ctx, struct ggml_tensor * a,
+                                                  struct ggml_tensor * b, int s0, int s1, int p0, int p1, int d0,
+                                                  int d1);
 
 /* ---- graphs --------------------------------------------------------------------------------- */
 GGML_API struct ggml_cgraph * ggml_new_graph(struct ggml_context * ctx);
