@@ -31,12 +31,20 @@ __device__ __forceinline__ uint32_t q4_to_s8(uint32_t w) {  // 4 nibbles (0..15)
 }
 
 // One LDS stage's worth of global data held in registers between its load and its LDS store.
+// A stage is GKB K-blocks of the workgroup's 128 activation rows and 128 weight rows.
+constexpr int GA = GBM * GKB * 2 / 256;  // 16-byte activation chunks per thread (two per row-block)
+constexpr int GS = GBM * GKB / 256;      // row-blocks per thread for the scales and Q4_0 nibbles
+static_assert(GA >= 1 && GS >= 1, "stage size");
+
+// Native vector types, not HIP's int4 / uint4 structs: struct copies become memcpys through a
+// stack object that is not promoted to registers, which puts the staged loads in scratch memory
+// and makes every chunk wait for its global loads before computing.
 template <int TYPE>
 struct GemmStage {
-    int4 a[2];                         // activation codes: 2 x 16 B per thread
-    uint4 b[TYPE == T_Q8_0 ? 2 : 1];   // weight codes: Q8_0 2 x 16 B, Q4_0 one block's 16 B of nibbles
-    float dx;                          // one activation scale
-    uint32_t dw;                       // one weight scale (fp16 bits)
+    v4i a[GA];                                // activation codes
+    v4i b[TYPE == T_Q8_0 ? GA : GS];          // weight codes: Q8_0 like a, Q4_0 one block's 16 B of nibbles
+    float dx[GS];                             // activation scales
+    uint32_t dw[GS];                          // weight scales (fp16 bits)
 };
 
 // Chunk c (K-blocks kb0 .. kb0 + GKB) of this workgroup's tile: thread t's share. Rows past M or
@@ -48,33 +56,39 @@ __device__ __forceinline__ void gemm_load(GemmStage<TYPE> & st, const uint8_t * 
     const int t = threadIdx.x;
     const int K = nb * 32;
 #pragma unroll
-    for (int i = 0; i < 2; i++) {  // A: 128 rows x GKB*32 B = 512 chunks of 16 B
+    for (int i = 0; i < GA; i++) {  // A: 128 rows x GKB*32 B in chunks of 16 B
         const int c = t + 256 * i;
         const int row = c / (GKB * 2), part = c % (GKB * 2);
         const int gm = min(m0 + row, M - 1);
         const int kb = min(kb0 + part / 2, nb - 1);
-        st.a[i] = *reinterpret_cast<const int4 *>(xc + (size_t) gm * K + (size_t) kb * 32 + (part & 1) * 16);
+        st.a[i] = *reinterpret_cast<const v4i *>(xc + (size_t) gm * K + (size_t) kb * 32 + (part & 1) * 16);
     }
     if constexpr (TYPE == T_Q8_0) {
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
+        for (int i = 0; i < GA; i++) {
             const int c = t + 256 * i;
             const int row = c / (GKB * 2), part = c % (GKB * 2);
             const int gn = min(n0 + row, N - 1);
             const int kb = min(kb0 + part / 2, nb - 1);
-            st.b[i] = *reinterpret_cast<const uint4 *>(wqs + ((size_t) gn * nb + kb) * 32 + (part & 1) * 16);
+            st.b[i] = *reinterpret_cast<const v4i *>(wqs + ((size_t) gn * nb + kb) * 32 + (part & 1) * 16);
         }
     } else {  // 128 rows x GKB blocks of 16 B
-        const int row = t / GKB, j = t % GKB;
-        const int gn = min(n0 + row, N - 1);
-        const int kb = min(kb0 + j, nb - 1);
-        st.b[0] = *reinterpret_cast<const uint4 *>(wqs + ((size_t) gn * nb + kb) * 16);
+#pragma unroll
+        for (int i = 0; i < GS; i++) {
+            const int c = t + 256 * i;
+            const int row = c / GKB, j = c % GKB;
+            const int gn = min(n0 + row, N - 1);
+            const int kb = min(kb0 + j, nb - 1);
+            st.b[i] = *reinterpret_cast<const v4i *>(wqs + ((size_t) gn * nb + kb) * 16);
+        }
     }
-    {  // scales: 128 rows x GKB blocks each
-        const int row = t / GKB, j = t % GKB;
+#pragma unroll
+    for (int i = 0; i < GS; i++) {  // scales: 128 rows x GKB blocks each
+        const int c = t + 256 * i;
+        const int row = c / GKB, j = c % GKB;
         const int kb = min(kb0 + j, nb - 1);
-        st.dx = xm[(size_t) min(m0 + row, M - 1) * nb + kb].x;
-        st.dw = wd[(size_t) min(n0 + row, N - 1) * nb + kb];
+        st.dx[i] = xm[(size_t) min(m0 + row, M - 1) * nb + kb].x;
+        st.dw[i] = wd[(size_t) min(n0 + row, N - 1) * nb + kb];
     }
 }
 
@@ -83,36 +97,41 @@ __device__ __forceinline__ void gemm_store(const GemmStage<TYPE> & st, int8_t * 
                                            float * sdw) {
     const int t = threadIdx.x;
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
+    for (int i = 0; i < GA; i++) {
         const int c = t + 256 * i;
         const int row = c / (GKB * 2), part = c % (GKB * 2);
-        *reinterpret_cast<int4 *>(sA + row * GPITCH + part * 16) = st.a[i];
+        *reinterpret_cast<v4i *>(sA + row * GPITCH + part * 16) = st.a[i];
     }
     if constexpr (TYPE == T_Q8_0) {
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
+        for (int i = 0; i < GA; i++) {
             const int c = t + 256 * i;
             const int row = c / (GKB * 2), part = c % (GKB * 2);
-            *reinterpret_cast<uint4 *>(sB + row * GPITCH + part * 16) = st.b[i];
+            *reinterpret_cast<v4i *>(sB + row * GPITCH + part * 16) = st.b[i];
         }
     } else {
-        const int row = t / GKB, j = t % GKB;
-        const uint4 w = st.b[0];
-        int4 lo, hi;
-        lo.x = (int) q4_to_s8(w.x);
-        lo.y = (int) q4_to_s8(w.y);
-        lo.z = (int) q4_to_s8(w.z);
-        lo.w = (int) q4_to_s8(w.w);
-        hi.x = (int) q4_to_s8(w.x >> 4);
-        hi.y = (int) q4_to_s8(w.y >> 4);
-        hi.z = (int) q4_to_s8(w.z >> 4);
-        hi.w = (int) q4_to_s8(w.w >> 4);
-        *reinterpret_cast<int4 *>(sB + row * GPITCH + j * 32) = lo;
-        *reinterpret_cast<int4 *>(sB + row * GPITCH + j * 32 + 16) = hi;
+#pragma unroll
+        for (int i = 0; i < GS; i++) {
+            const int c = t + 256 * i;
+            const int row = c / GKB, j = c % GKB;
+            const v4i w = st.b[i];
+            v4i lo, hi;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                lo[e] = (int) q4_to_s8((uint32_t) w[e]);
+                hi[e] = (int) q4_to_s8((uint32_t) w[e] >> 4);
+            }
+            *reinterpret_cast<v4i *>(sB + row * GPITCH + j * 32) = lo;
+            *reinterpret_cast<v4i *>(sB + row * GPITCH + j * 32 + 16) = hi;
+        }
     }
-    const int row = t / GKB, j = t % GKB;
-    sdx[j * GBM + row] = st.dx;
-    sdw[j * GBN + row] = h2f((uint16_t) st.dw);
+#pragma unroll
+    for (int i = 0; i < GS; i++) {
+        const int c = t + 256 * i;
+        const int row = c / GKB, j = c % GKB;
+        sdx[j * GBM + row] = st.dx[i];
+        sdw[j * GBN + row] = h2f((uint16_t) st.dw[i]);
+    }
 }
 
 // RAW: write the int32 block sums of block `raw_blk` instead of the scaled result.
