@@ -72,6 +72,18 @@ class Model:
             raise GcqError(self._lib.gcq_last_error().decode())
         self.max_prompt = max_prompt
 
+    @classmethod
+    def from_gguf(cls, path, max_ctx: int | None = None, max_prompt: int = 512) -> "Model":
+        """A model loaded from a ggml-compiler GGUF of a Llama-style causal LM (gguf.read_causal_lm:
+        Q4_0 or Q8_0 weights, shape from the tensors, eps and RoPE base from the program)."""
+        from .gguf import read_causal_lm
+
+        lm = read_causal_lm(path)
+        m = cls(lm.config(max_ctx), max_prompt=max_prompt)
+        for name, data in lm.stacked().items():
+            m.set_weight(name, data)
+        return m
+
     def close(self) -> None:
         if getattr(self, "_m", None):
             self._lib.gcq_llama_free(self._m)

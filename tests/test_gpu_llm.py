@@ -180,3 +180,29 @@ def test_llama3_8b_shape_matches_oracle(gops, orc):
         assert orc.logit_kl(lg, lo) < 1e-2
         assert np.corrcoef(lg, lo)[0, 1] > 0.99
         assert orc.parity(lg, lo) < 0.2
+
+
+@pytest.mark.parametrize("wtype", [2, 8])
+def test_model_from_reference_layout_gguf(gops, orc, tmp_path, wtype):
+    """A model written in ggml-compiler's GGUF layout (module paths, w.N tensors, eps and RoPE base in
+    the program) loads into the decoder and matches the oracle's run of the same tensors."""
+    from ggml_compiler_amd import gguf
+    from ggml_compiler_amd.llm import Model
+    from llama_ref import OracleLlama
+    from test_gguf import tiny_lm
+
+    p = tmp_path / "lm.gguf"
+    gguf.write_causal_lm(p, tiny_lm(orc, wtype=wtype, seed=40))
+    m = Model.from_gguf(p, max_prompt=16)
+    assert (m.cfg.n_layer, m.cfg.n_head, m.cfg.n_head_kv, m.cfg.wtype) == (2, 4, 2, wtype)
+    o = OracleLlama(m.cfg, gguf.read_causal_lm(p).stacked())
+    prompt = orc.ids(9, seed=41, vocab=m.cfg.n_vocab).tolist()
+    lg, lo = m.prefill(prompt), o.forward(prompt)
+    assert orc.parity(lg, lo) < TOL_LM
+    tok = int(np.argmax(lo))
+    for step in range(4):
+        lg, _ = m.decode(tok)
+        lo = o.forward([tok])
+        assert orc.parity(lg, lo) < TOL_LM, step
+        tok = int(np.argmax(lo))
+    m.close()
