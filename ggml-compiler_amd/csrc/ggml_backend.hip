@@ -56,6 +56,13 @@ void launch_get_rows(int type, const void * tab, int64_t nrows_tab, int64_t D, c
 void launch_swiglu(const float * g, const float * u, float * y, int64_t n, hipStream_t s);
 void launch_binary(int op, const float * a, const float * b, float * y, int64_t n, int64_t nb, hipStream_t s);
 void launch_argmax(const float * x, int64_t ldx, int64_t rows, int64_t n, int32_t * out, hipStream_t s);
+int decode_group(int GT, int max_kv);
+int decode_splits(int D, int G, int n_kv, int max_split);
+bool attn_decode_fits(int D, int G);
+void launch_attn_decode(const float * q, int64_t q_h, const void * k, int64_t k_h, int64_t k_j, const void * v,
+                        int64_t v_h, int64_t v_j, int D, int H, int Hkv, int n_kv, const int * n_kv_dev, float scale,
+                        int nsplit, int chunk, int kv_rows, int GS, float * out, float * part_o, float2 * part_ml,
+                        hipStream_t s, const Prefetch * pf, const void * mask);
 
 namespace {
 
@@ -127,6 +134,24 @@ bool q8_mul_mat(const ggml_tensor * mm) {
     const ggml_tensor * a = mm->src[0];
     return (a->type == GGML_TYPE_Q4_0 || a->type == GGML_TYPE_Q8_0) && whole_packed(a) && a->ne[2] == 1 &&
            a->ne[3] == 1;
+}
+
+// flash_attn_ext of one query row that the one-pass decode kernel runs (f16 K/V with 16-byte rows,
+// f16 mask or none, no ALiBi / softcap) and whose output the decode-row GEMV can merge from
+// split partials (H * D <= 4096).
+bool decode_attn_node(const ggml_tensor * t) {
+    if (t->op != GGML_OP_FLASH_ATTN_EXT) return false;
+    const ggml_tensor *q = t->src[0], *k = t->src[1], *v = t->src[2], *m = t->src[3];
+    float fp[3];
+    std::memcpy(fp, &t->op_params[0], sizeof(fp));
+    const int64_t D = q->ne[0], H = q->ne[2], Hkv = k->ne[2];
+    return fp[1] == 0.0f && fp[2] == 0.0f && q->type == GGML_TYPE_F32 && q->nb[0] == 4 && q->nb[1] % 4 == 0 &&
+           q->nb[2] % 4 == 0 && q->ne[1] == 1 && q->ne[3] == 1 && aligned16(q) && (q->nb[2] / 4) % 4 == 0 &&
+           k->type == GGML_TYPE_F16 && v->type == GGML_TYPE_F16 &&
+           k->nb[0] == 2 && v->nb[0] == 2 && k->nb[1] % 16 == 0 && k->nb[2] % 16 == 0 && v->nb[1] % 16 == 0 &&
+           v->nb[2] % 16 == 0 && aligned16(k) && aligned16(v) && v->ne[0] == D && H % Hkv == 0 &&
+           attn_decode_fits((int) D, (int) (H / Hkv)) && H * D <= 4096 &&
+           (!m || (m->type == GGML_TYPE_F16 && m->nb[0] == 2));
 }
 
 bool add_takes(const ggml_tensor * add, const ggml_tensor * mm) {
@@ -224,6 +249,23 @@ Chains find_chains(const ggml_cgraph * g) {
             const int a = with_add(k);
             if (a >= 0) link({i, k, a});
             else link({i, k});
+        } else if (decode_attn_node(t)) {
+            // attention row -> reshape to [H*D, 1] -> output projection: the GEMV merges the
+            // attention's split partials in its prologue; the row is never written.
+            const int j = sole(t);
+            if (j < 0) continue;
+            const ggml_tensor * rs = g->nodes[j];
+            if (rs->op != GGML_OP_RESHAPE || rs->src[0] != t || is_output(rs) || rs == g->nodes[n - 1]) continue;
+            auto u = uses.find(rs);
+            if (u == uses.end() || u->second != 1) continue;
+            const int k = reader[rs];
+            const ggml_tensor * mm = g->nodes[k];
+            if (mm->op != GGML_OP_MUL_MAT || mm->src[1] != rs || !q8_mul_mat(mm) || ggml_nrows(rs) != 1 ||
+                !row_gemv_fits(mm->src[0]->type, rs->ne[0]))
+                continue;
+            const int a = with_add(k);
+            if (a >= 0) link({i, j, k, a});
+            else link({i, j, k});
         } else if (t->op == GGML_OP_MUL_MAT && whole_packed(t->src[0])) {
             const int a = with_add(i);
             if (a >= 0) link({i, a});
@@ -263,6 +305,7 @@ enum StepKind {
     S_FATTN,
     S_SWIGLU,
     S_ARGMAX,
+    S_ATTN_MULMAT,  // decode attention (split partials) -> mul_mat merging them [-> add]
 };
 
 // One launch sequence with every argument it takes; compared byte for byte to decide whether a
@@ -679,10 +722,52 @@ struct Planner {
         }
     }
 
+    void attn_mulmat(const ggml_tensor * fa, const ggml_tensor * mm, const ggml_tensor * res, const ggml_tensor * y) {
+        const ggml_tensor *q = fa->src[0], *k = fa->src[1], *v = fa->src[2], *m = fa->src[3];
+        const ggml_tensor * w = mm->src[0];
+        const int64_t D = q->ne[0], H = q->ne[2], Hkv = k->ne[2], n_kv = k->ne[1];
+        require(n_kv >= 1, "flash_attn_ext: empty attention");
+        Step s = new_step(S_ATTN_MULMAT);
+        s.type = w->type;
+        s.in[0] = d(q);
+        s.in[1] = d(k);
+        s.in[2] = d(v);
+        s.in[3] = m ? d(m) : nullptr;
+        s.in[4] = d(w);
+        s.in[5] = res ? d(res) : nullptr;
+        s.out = o(y);
+        s.n[0] = (int64_t) q->nb[2] / 4;
+        s.n[1] = (int64_t) k->nb[2] / 2;
+        s.n[2] = (int64_t) k->nb[1] / 2;
+        s.n[3] = (int64_t) v->nb[2] / 2;
+        s.n[4] = (int64_t) v->nb[1] / 2;
+        s.n[5] = D;
+        s.n[6] = H;
+        s.n[7] = Hkv;
+        s.n[8] = n_kv;
+        s.n[9] = w->ne[1];  // N
+        s.n[10] = w->ne[0];  // K = H * D
+        std::memcpy(&s.f[0], &fa->op_params[0], 4);
+        // split plan: as many splits as the merge prologue holds at most
+        const int GS = decode_group((int) (H / Hkv), (int) n_kv);
+        const int nsplit = decode_splits((int) D, GS, (int) n_kv, row_gemv_merge_max());
+        s.g.sne[0] = GS;
+        s.g.sne[1] = nsplit;
+        s.g.sne[2] = (n_kv + nsplit - 1) / nsplit;
+        ws_need = std::max(ws_need, align256((size_t) H * nsplit * D * 4) + align256((size_t) H * nsplit * 8) +
+                                        align256((size_t) H * D * 4));
+        steps.push_back(s);
+    }
+
     // The chain ending at node f (members before it, in order).
     void chain(const ggml_cgraph * g, const std::vector<int> & idx) {
         const ggml_tensor * first = g->nodes[idx.front()];
         const ggml_tensor * last = g->nodes[idx.back()];
+        if (first->op == GGML_OP_FLASH_ATTN_EXT) {  // [attention, reshape, mul_mat (, add)]
+            const ggml_tensor * mm = g->nodes[idx[2]];
+            const ggml_tensor * res = idx.size() == 4 ? (last->src[0] == mm ? last->src[1] : last->src[0]) : nullptr;
+            return attn_mulmat(first, mm, res, last);
+        }
         if (first->op == GGML_OP_RMS_NORM) {
             const ggml_tensor * mul = g->nodes[idx[1]];
             if (idx.size() == 2) return rmsnorm(first, mul->src[1], mul);
@@ -787,6 +872,35 @@ void run_step(const ggml_backend * be, const Step & s) {
         case S_ARGMAX:
             launch_argmax((const float *) s.in[0], s.n[0], s.n[1], s.n[2], (int32_t *) s.out, st);
             return;
+        case S_ATTN_MULMAT: {
+            const int64_t D = s.n[5], H = s.n[6], Hkv = s.n[7], n_kv = s.n[8], N = s.n[9], K = s.n[10];
+            const int GS = (int) s.g.sne[0], nsplit = (int) s.g.sne[1], chunk = (int) s.g.sne[2];
+            float * po = (float *) be->ws;
+            float2 * pml = (float2 *) ((uint8_t *) be->ws + align256((size_t) H * nsplit * D * 4));
+            float * row = (float *) ((uint8_t *) pml + align256((size_t) H * nsplit * 8));
+            launch_attn_decode((const float *) s.in[0], s.n[0], s.in[1], s.n[1], s.n[2], s.in[2], s.n[3], s.n[4],
+                               (int) D, (int) H, (int) Hkv, (int) n_kv, nullptr, s.f[0], nsplit, chunk, (int) n_kv, GS,
+                               row, po, pml, st, nullptr, s.in[3]);
+            const WeightLayout L = weight_layout(s.type, N, K);
+            RowArgs a{};
+            a.wqs = (const uint8_t *) s.in[4] + L.qs;
+            a.wd = (const uint16_t *) ((const uint8_t *) s.in[4] + L.d);
+            a.N = (int) N;
+            a.nb = (int) (K / QK);
+            a.y = (float *) s.out;
+            a.res = (const float *) s.in[5];
+            if (nsplit == 1) {  // the kernel wrote the normalized row
+                a.x = row;
+                launch_row_gemv(s.type, PRO_PLAIN, EPI_STORE, a, st);
+            } else {
+                a.part_o = po;
+                a.part_ml = pml;
+                a.nsplit = nsplit;
+                a.D = (int) D;
+                launch_row_gemv(s.type, PRO_MERGE, EPI_STORE, a, st);
+            }
+            return;
+        }
     }
 }
 
