@@ -46,35 +46,44 @@ __global__ __launch_bounds__(256) void k_rms_norm(const float * __restrict__ x, 
 
 // ---------------------------------------------------------------------------------- rope
 
-// One thread per (s, h, pair i < n_dims/2). theta follows ggml's rope cache: it starts at the
-// position and is multiplied by theta_scale once per pair (theta_scale = powf(base, -2/n_dims),
-// computed on the host in f32 as ggml does).
-__global__ void k_rope_neox(const float * __restrict__ x, int64_t sx_s, int64_t sx_h, float * __restrict__ out,
-                            int64_t so_s, int64_t so_h, const int32_t * __restrict__ pos, int D, int H, int S,
-                            int n_dims, float theta_scale, float freq_scale, float attn_factor,
-                            const float * __restrict__ ff) {
+// One workgroup per (token s, block of RH heads): its first n_dims/2 threads build the rotation of
+// every pair i of the token (theta as ggml's rope cache: the position multiplied by theta_scale
+// once per pair, theta_scale = powf(base, -2/n_dims) computed on the host in f32 as ggml does),
+// then all threads rotate the block's heads with it; dims n_dims .. D-1 pass through.
+constexpr int RH = 8;
+__global__ __launch_bounds__(256) void k_rope_neox(const float * __restrict__ x, int64_t sx_s, int64_t sx_h,
+                                                   float * __restrict__ out, int64_t so_s, int64_t so_h,
+                                                   const int32_t * __restrict__ pos, int D, int H, int S, int n_dims,
+                                                   float theta_scale, float freq_scale, float attn_factor,
+                                                   const float * __restrict__ ff) {
+    __shared__ float2 cs[128];  // n_dims / 2 <= 128
     const int half = n_dims / 2;
-    const int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
-    const int64_t per_row = D - half;  // pairs, then the pass-through dims
-    if (t >= (int64_t) S * H * per_row) return;
-    const int i = (int) (t % per_row);
-    const int h = (int) ((t / per_row) % H);
-    const int s = (int) (t / ((int64_t) per_row * H));
-    const float * xr = x + s * sx_s + h * sx_h;
-    float * o = out + s * so_s + h * so_h;
-    if (i >= half) {  // dims n_dims .. D-1 pass through
-        const int d = i - half + n_dims;
-        if (d < D) o[d] = xr[d];
-        return;
+    const int s = blockIdx.x, h0 = blockIdx.y * RH;
+    const int nh = min(RH, H - h0);
+    if ((int) threadIdx.x < half) {
+        const int i = threadIdx.x;
+        float theta = (float) pos[s];
+        for (int k = 0; k < i; k++) theta *= theta_scale;
+        const float f = ff ? ff[i] : 1.0f;
+        const float th = freq_scale * (theta / f);
+        cs[i] = make_float2(cosf(th) * attn_factor, sinf(th) * attn_factor);
     }
-    float theta = (float) pos[s];
-    for (int k = 0; k < i; k++) theta *= theta_scale;
-    const float f = ff ? ff[i] : 1.0f;
-    const float th = freq_scale * (theta / f);
-    const float c = cosf(th) * attn_factor, sn = sinf(th) * attn_factor;
-    const float x0 = xr[i], x1 = xr[i + half];
-    o[i] = x0 * c - x1 * sn;
-    o[i + half] = x0 * sn + x1 * c;
+    __syncthreads();
+    const int per_row = D - half;  // pairs, then the pass-through dims
+    for (int p = threadIdx.x; p < nh * per_row; p += 256) {
+        const int h = h0 + p / per_row, i = p % per_row;
+        const float * xr = x + s * sx_s + h * sx_h;
+        float * o = out + s * so_s + h * so_h;
+        if (i >= half) {
+            const int d = i - half + n_dims;
+            if (d < D) o[d] = xr[d];
+            continue;
+        }
+        const float c = cs[i].x, sn = cs[i].y;
+        const float x0 = xr[i], x1 = xr[i + half];
+        o[i] = x0 * c - x1 * sn;
+        o[i + half] = x0 * sn + x1 * c;
+    }
 }
 
 // ------------------------------------------------------------------------------ set_rows
@@ -240,10 +249,11 @@ void launch_rope_neox(const float * x, int64_t sx_s, int64_t sx_h, float * out, 
                       const int32_t * pos, int64_t D, int64_t H, int64_t S, int n_dims, float freq_base,
                       float freq_scale, float attn_factor, const float * ff, hipStream_t s) {
     const float theta_scale = powf(freq_base, -2.0f / (float) n_dims);
-    const int64_t n = S * H * (D - n_dims / 2);
-    if (n == 0) return;
-    k_rope_neox<<<nblk(n, 256), 256, 0, s>>>(x, sx_s, sx_h, out, so_s, so_h, pos, (int) D, (int) H, (int) S, n_dims,
-                                             theta_scale, freq_scale, attn_factor, ff);
+    if (S * H * D == 0) return;
+    require(n_dims <= 256, "rope: n_dims above 256");
+    const dim3 grid((unsigned) S, (unsigned) ((H + RH - 1) / RH));
+    k_rope_neox<<<grid, 256, 0, s>>>(x, sx_s, sx_h, out, so_s, so_h, pos, (int) D, (int) H, (int) S, n_dims,
+                                     theta_scale, freq_scale, attn_factor, ff);
     check_launch("rope");
 }
 
