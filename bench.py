@@ -359,6 +359,11 @@ def bench_sweep(ops, torch) -> list[dict]:
         for K, N in LAYER_SHAPES:
             for B in (1, 2, 4, 8):
                 gemv_case("C2", t, K, N, B)
+    # the other K-quant storage types at the same layer shapes (Q4_K_M files mix Q4_K with Q6_K)
+    for t in ("q5_K", "q6_K"):
+        for K, N in LAYER_SHAPES:
+            for B in (1, 8):
+                gemv_case("K56", t, K, N, B)
     # C3: prefill GEMM, Q8_0 K=4096 N=14336, 512 rows (activation quantization included)
     ws = _rotating_weights(ops, "q8_0", 14336, 4096, seed=3)[:4]
     x = ops.fill_normal((512, 4096), seed=4)

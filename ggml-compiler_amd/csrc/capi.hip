@@ -73,7 +73,7 @@ size_t block_elems(int type) {
     switch (type) {
         case T_F32: case T_F16: case T_I32: return 1;
         case T_Q4_0: case T_Q8_0: return QK;
-        case T_Q4_K: case T_Q8_K: return QKK;
+        case T_Q4_K: case T_Q5_K: case T_Q6_K: case T_Q8_K: return QKK;
         default: return 0;
     }
 }
@@ -85,6 +85,8 @@ size_t block_bytes(int type) {
         case T_Q4_0: return 18;
         case T_Q8_0: return 34;
         case T_Q4_K: return 144;
+        case T_Q5_K: return 176;
+        case T_Q6_K: return 210;
         case T_Q8_K: return 292;
         default: return 0;
     }
@@ -103,6 +105,11 @@ WeightLayout weight_layout(int type, int64_t nrows, int64_t k) {
         L.qs = 0;
         L.d = align256(nb * (type == T_Q4_0 ? 16 : 32));
         L.total = L.d + align256(nb * 2);
+    } else if (type == T_Q6_K) {
+        const size_t nb = (size_t) nrows * (size_t) (k / QKK);
+        L.qs = 0;
+        L.d = align256(nb * 208);
+        L.total = L.d + align256(nb * 2);
     } else {
         L.total = align256(row_bytes(type, k) * (size_t) nrows);
     }
@@ -113,7 +120,7 @@ ActLayout act_layout(int wtype, int64_t B, int64_t k) {
     ActLayout L;
     L.codes = 0;
     L.meta = align256((size_t) B * (size_t) k);
-    if (wtype == T_Q4_K) {
+    if (is_kquant(wtype)) {
         L.d = L.meta + align256((size_t) B * (size_t) (k / 16) * 2);
         L.total = L.d + align256((size_t) B * (size_t) (k / QKK) * 4);
     } else {
@@ -127,10 +134,11 @@ ActLayout act_layout(int wtype, int64_t B, int64_t k) {
 
 namespace {
 
-bool is_weight_type(int t) { return t == T_Q4_0 || t == T_Q8_0 || t == T_Q4_K; }
+bool is_weight_type(int t) { return t == T_Q4_0 || t == T_Q8_0 || is_kquant(t); }
 
 void need_weight_type(int t) {
-    require(is_weight_type(t), "unsupported weight type " + std::to_string(t) + " (Q4_0=2, Q8_0=8, Q4_K=12)");
+    require(is_weight_type(t),
+            "unsupported weight type " + std::to_string(t) + " (Q4_0=2, Q8_0=8, Q4_K=12, Q5_K=13, Q6_K=14)");
 }
 
 void need_k(int t, int64_t k) {
@@ -209,7 +217,7 @@ size_t gcq_act_size(int wtype, int64_t B, int64_t K) {
 }
 
 size_t gcq_mul_mat_workspace(int wtype, int64_t M, int64_t K) {
-    return gcq_act_size(wtype, (wtype == T_Q4_K && M > 8) ? 8 : M, K);
+    return gcq_act_size(wtype, (is_kquant(wtype) && M > 8) ? 8 : M, K);
 }
 
 size_t gcq_flash_attn_workspace(int Sq, int H, int Hkv, int Dv, int n_kv) {
@@ -292,7 +300,7 @@ int gcq_mul_mat_q(int wtype, const void * w, int64_t N, int64_t K, const void * 
         if (M <= 8) {
             launch_gemv(wtype, w, N, K, act, M, y, ldy, as_stream(stream), res);
         } else {
-            require(wtype != T_Q4_K, "mul_mat_q: Q4_K with more than 8 rows needs gcq_mul_mat");
+            require(!is_kquant(wtype), "mul_mat_q: a K-quant weight with more than 8 rows needs gcq_mul_mat");
             launch_gemm(wtype, w, N, K, act, M, y, ldy, as_stream(stream), res);
         }
     });
@@ -322,7 +330,7 @@ int gcq_mul_mat(int wtype, const void * w, int64_t N, int64_t K, const float * x
         if (M <= 8) {
             launch_act_quant(wtype, x, ldx, M, K, ws, s);
             launch_gemv(wtype, w, N, K, ws, M, y, ldy, s);
-        } else if (wtype != T_Q4_K) {
+        } else if (!is_kquant(wtype)) {
             launch_act_quant(wtype, x, ldx, M, K, ws, s);
             launch_gemm(wtype, w, N, K, ws, M, y, ldy, s);
         } else {
@@ -590,7 +598,9 @@ static int parse_type(const char * type) {
     if (t == "q4_0") return T_Q4_0;
     if (t == "q8_0") return T_Q8_0;
     if (t == "q4_K" || t == "q4_k") return T_Q4_K;
-    fail("unknown or unsupported type '" + t + "' (f32, f16, q4_0, q8_0, q4_K)");
+    if (t == "q5_K" || t == "q5_k") return T_Q5_K;
+    if (t == "q6_K" || t == "q6_k") return T_Q6_K;
+    fail("unknown or unsupported type '" + t + "' (f32, f16, q4_0, q8_0, q4_K, q5_K, q6_K)");
 }
 
 size_t ggml_compiler_row_size(const char * type, int64_t n) {

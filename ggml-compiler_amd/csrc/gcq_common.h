@@ -1,18 +1,21 @@
 // gcq_common.h - shared definitions of libgcq's HIP kernels and C ABI (gfx950 only).
 //
-// Type ids are GGUF's (ggml_type): F32=0, F16=1, Q4_0=2, Q8_0=8, Q4_K=12, Q8_K=15, I32=26.
+// Type ids are GGUF's (ggml_type): F32=0, F16=1, Q4_0=2, Q8_0=8, Q4_K=12, Q5_K=13, Q6_K=14,
+// Q8_K=15, I32=26.
 //
 // Device layouts (all offsets 256-byte aligned, see gcq_layout below):
 //  * Weights ("packed"): what gcq_pack_weights makes from ggml's block rows.
 //      Q4_0: nibbles [N][K/32][16 B], then fp16 scales [N][K/32]. Byte j of a block's 16 holds
 //            element j (low nibble) and j+16 (high nibble), stored code = q + 8, as in ggml.
 //      Q8_0: codes [N][K/32][32 B], then fp16 scales [N][K/32].
-//      Q4_K: ggml's 144-byte super-blocks unchanged (already 16-byte aligned rows).
+//      Q4_K, Q5_K: ggml's 144- / 176-byte super-blocks unchanged (16-byte aligned rows).
+//      Q6_K: ggml's 210-byte super-block split: {ql[128], qh[64], scales[16]} [N][K/256][208 B],
+//            then fp16 d [N][K/256] (the 208 bytes in ggml's order, so loads stay 16-byte aligned).
 //  * Quantized activations ("act"), rows of the batch b < B:
 //      Q8_0 (for Q4_0 / Q8_0 weights): codes [B][K] int8, then per 32-block {float d, int sum}
 //            [B][K/32]: d is the fp16 scale ggml stores (as its exact f32 value) and sum the
 //            block's code sum (used to fold Q4_0's -8 offset into one integer term).
-//      Q8_K (for Q4_K weights): codes [B][K] int8, then bsums int16 [B][K/16] (ggml's sums of 16
+//      Q8_K (for Q4_K / Q5_K / Q6_K weights): codes [B][K] int8, then bsums int16 [B][K/16] (ggml's sums of 16
 //            codes), then d float [B][K/256].
 #pragma once
 
@@ -24,7 +27,10 @@
 
 namespace gcq {
 
-enum : int { T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q8_0 = 8, T_Q4_K = 12, T_Q8_K = 15, T_I32 = 26 };
+enum : int { T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_Q8_K = 15, T_I32 = 26 };
+
+// K-quant weights: 256-value super-blocks, Q8_K activations.
+__host__ __device__ inline bool is_kquant(int t) { return t == T_Q4_K || t == T_Q5_K || t == T_Q6_K; }
 
 constexpr int QK = 32;    // Q4_0 / Q8_0 block
 constexpr int QKK = 256;  // K-quant super-block

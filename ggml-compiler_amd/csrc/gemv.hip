@@ -1,10 +1,10 @@
 // gemv.hip - quantized mat-vec for decode (batch 1..8): y[b, n] = sum_k W[n, k] x[b, k].
 //
-// Replaces ggml_mul_mat on a Q4_0 / Q8_0 / Q4_K weight with an f32 src1 of 1..8 rows
+// Replaces ggml_mul_mat on a Q4_0 / Q8_0 / Q4_K / Q5_K / Q6_K weight with an f32 src1 of 1..8 rows
 // (runtime/src/ops.cpp:107-119 -> runtime/include/ggml_compiler_ops.h:116-122). As ggml-cpu
 // does, the activation is first quantized to the weight's vec_dot_type (quant.hip); each
 // weight block then contributes an exact int32 dot sum times its fp16 scale(s), accumulated in
-// fp32 (ggml vec_dot_q4_0_q8_0 / vec_dot_q8_0_q8_0 / vec_dot_q4_K_q8_K).
+// fp32 (ggml vec_dot_q4_0_q8_0 / vec_dot_q8_0_q8_0 / vec_dot_q{4,5,6}_K_q8_K).
 //
 // HBM-bound by the weight stream. One wavefront owns R rows; lane l takes blocks l, l+64, ...
 // so each weight load instruction moves 64 x 16 B of one row contiguously. All of a lane's
@@ -72,6 +72,59 @@ __device__ __forceinline__ void scale_min_k4_w(int j, const uint32_t s[3], int &
         sc = (byte(j + 4) & 0xF) | ((byte(j - 4) >> 6) << 4);
         m = (byte(j + 4) >> 4) | ((byte(j) >> 6) << 4);
     }
+}
+
+// Chunk c of a Q5_K super-block: the Q4_K nibbles plus the fifth bit of value l (l < 32) of
+// sub-block 2c in bit 2c of qh[l], of sub-block 2c + 1 in bit 2c + 1.
+__device__ __forceinline__ void dot_q5_K_chunk(const uint4 wa, const uint4 wb, const uint4 ha, const uint4 hb, int c,
+                                               const int4 x0, const int4 x1, const int4 x2, const int4 x3, int & lo,
+                                               int & hi) {
+    const uint32_t w[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+    const uint32_t h[8] = {ha.x, ha.y, ha.z, ha.w, hb.x, hb.y, hb.z, hb.w};
+    const int xl[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    const int xh[8] = {x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
+    int a = 0, b = 0;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const uint32_t ql = (w[j] & 0x0F0F0F0Fu) | (((h[j] >> (2 * c)) & 0x01010101u) << 4);
+        const uint32_t qh = ((w[j] >> 4) & 0x0F0F0F0Fu) | (((h[j] >> (2 * c + 1)) & 0x01010101u) << 4);
+        a = sdot4((int) ql, xl[j], a);
+        b = sdot4((int) qh, xh[j], b);
+    }
+    lo = a;
+    hi = b;
+}
+
+// Task (hh, jj) of a packed Q6_K super-block: 32 ql bytes at 64 hh + 32 jj (low nibbles: values
+// 128 hh + 32 jj + l, high: + 64), the 32 qh bytes of half hh (2 bits per value at shift 2 jj and
+// 2 jj + 4). d[k] = sum over the k-th of the task's four 16-value sub-blocks of q * x, q in 0..63
+// (the stored code; the -32 offset is folded in with the bsums).
+__device__ __forceinline__ void dot_q6_K_task(const uint4 la, const uint4 lb, const uint4 ha, const uint4 hb, int jj,
+                                              const int4 x0, const int4 x1, const int4 x2, const int4 x3, int (&d)[4]) {
+    const uint32_t w[8] = {la.x, la.y, la.z, la.w, lb.x, lb.y, lb.z, lb.w};
+    const uint32_t h[8] = {ha.x, ha.y, ha.z, ha.w, hb.x, hb.y, hb.z, hb.w};
+    const int xl[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    const int xh[8] = {x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
+    int s[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const uint32_t ql = (w[j] & 0x0F0F0F0Fu) | (((h[j] >> (2 * jj)) & 0x03030303u) << 4);
+        const uint32_t qh = ((w[j] >> 4) & 0x0F0F0F0Fu) | (((h[j] >> (2 * jj + 4)) & 0x03030303u) << 4);
+        s[j >> 2] = sdot4((int) ql, xl[j], s[j >> 2]);
+        s[2 + (j >> 2)] = sdot4((int) qh, xh[j], s[2 + (j >> 2)]);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++) d[k] = s[k];
+}
+
+// The task's int32 sum: sum_k sc_k * (d_k - 32 * bsum_k). sc8: the 8 scale bytes of half hh;
+// bs01 / bs23: the two int16 bsums pairs of the task's low / high sub-blocks.
+__device__ __forceinline__ int isum_q6_K_task(const int (&d)[4], const uint2 sc8, int jj, uint32_t bs01, uint32_t bs23) {
+    const int s0 = (int) (int8_t) (sc8.x >> (16 * jj)), s1 = (int) (int8_t) (sc8.x >> (16 * jj + 8));
+    const int s2 = (int) (int8_t) (sc8.y >> (16 * jj)), s3 = (int) (int8_t) (sc8.y >> (16 * jj + 8));
+    const int b0 = (int) (int16_t) (bs01 & 0xffff), b1 = (int) (int16_t) (bs01 >> 16);
+    const int b2 = (int) (int16_t) (bs23 & 0xffff), b3 = (int) (int16_t) (bs23 >> 16);
+    return s0 * (d[0] - 32 * b0) + s1 * (d[1] - 32 * b1) + s2 * (d[2] - 32 * b2) + s3 * (d[3] - 32 * b3);
 }
 
 // ------------------------------------------------------------------ Q4_0 / Q8_0 kernel
@@ -316,6 +369,162 @@ __global__ __launch_bounds__(256) void k_gemv_q4_K(const uint8_t * __restrict__ 
         }
 }
 
+// ------------------------------------------------------------------- Q5_K / Q6_K kernels
+
+// Q5_K: the Q4_K task walk (super-block, 64-value chunk) with the 32 qh bytes loaded per task.
+template <int B, int R, int NBL>
+__global__ __launch_bounds__(256) void k_gemv_q5_K(const uint8_t * __restrict__ w, const int8_t * __restrict__ xc,
+                                                   const int16_t * __restrict__ xbs, const float * __restrict__ xd,
+                                                   float * y, const float * res, int N, int nsb, int ldy) {
+    const int lane = threadIdx.x & 63;
+    const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
+    if (row0 >= N) return;
+    const int K = nsb * QKK;
+    const int ntask = nsb * 4;
+    const size_t rowb = (size_t) nsb * 176;
+    float acc[R][B];
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int b = 0; b < B; b++) acc[r][b] = 0.0f;
+
+    for (int base = 0; base < ntask; base += 64 * NBL) {
+        uint4 hdr[NBL][R], ha[NBL][R], hb[NBL][R], qa[NBL][R], qb[NBL][R];
+#pragma unroll
+        for (int i = 0; i < NBL; i++) {
+            const int t = base + lane + 64 * i;
+            if (t < ntask) {
+                const int sb = t >> 2, c = t & 3;
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    const int row = min(row0 + r, N - 1);
+                    const uint4 * p = reinterpret_cast<const uint4 *>(w + row * rowb + (size_t) sb * 176);
+                    hdr[i][r] = p[0];
+                    ha[i][r] = p[1];
+                    hb[i][r] = p[2];
+                    qa[i][r] = p[3 + 2 * c];
+                    qb[i][r] = p[4 + 2 * c];
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NBL; i++) {
+            const int t = base + lane + 64 * i;
+            if (t >= ntask) break;
+            const int sb = t >> 2, c = t & 3;
+#pragma unroll
+            for (int b = 0; b < B; b++) {
+                const int4 * xp = reinterpret_cast<const int4 *>(xc + (size_t) b * K + (size_t) sb * QKK + 64 * c);
+                const int4 x0 = xp[0], x1 = xp[1], x2 = xp[2], x3 = xp[3];
+                const int2 bs = *reinterpret_cast<const int2 *>(xbs + (size_t) b * (K / 16) + sb * 16 + 4 * c);
+                const int bs01 = (int) (int16_t) (bs.x & 0xffff) + (int) (int16_t) (bs.x >> 16);
+                const int bs23 = (int) (int16_t) (bs.y & 0xffff) + (int) (int16_t) (bs.y >> 16);
+                const float dx = xd[(size_t) b * nsb + sb];
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    const uint32_t sc3[3] = {hdr[i][r].y, hdr[i][r].z, hdr[i][r].w};
+                    int sc0, m0, sc1, m1, lo, hi;
+                    scale_min_k4_w(2 * c, sc3, sc0, m0);
+                    scale_min_k4_w(2 * c + 1, sc3, sc1, m1);
+                    dot_q5_K_chunk(qa[i][r], qb[i][r], ha[i][r], hb[i][r], c, x0, x1, x2, x3, lo, hi);
+                    const int isc = sc0 * lo + sc1 * hi;
+                    const int imin = m0 * bs01 + m1 * bs23;
+                    const float dw = h2f((uint16_t) (hdr[i][r].x & 0xffff)) * dx;
+                    const float dm = h2f((uint16_t) (hdr[i][r].x >> 16)) * dx;
+                    acc[r][b] += dw * (float) isc - dm * (float) imin;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int b = 0; b < B; b++) {
+            const float v = wave_sum(acc[r][b]);
+            if (lane == r * B + b && row0 + r < N) {
+                const size_t o = (size_t) b * ldy + row0 + r;
+                y[o] = res ? v + res[o] : v;
+            }
+        }
+}
+
+// Q6_K (packed: 208-byte super-blocks, fp16 d apart): lane task = (super-block, half hh, ql
+// part jj), 4 tasks per super-block: 32 ql + 32 qh bytes, the half's 8 scale bytes and d.
+template <int B, int R, int NBL>
+__global__ __launch_bounds__(256) void k_gemv_q6_K(const uint8_t * __restrict__ wqs, const uint16_t * __restrict__ wd,
+                                                   const int8_t * __restrict__ xc, const int16_t * __restrict__ xbs,
+                                                   const float * __restrict__ xd, float * y, const float * res, int N,
+                                                   int nsb, int ldy) {
+    const int lane = threadIdx.x & 63;
+    const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
+    if (row0 >= N) return;
+    const int K = nsb * QKK;
+    const int ntask = nsb * 4;
+    float acc[R][B];
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int b = 0; b < B; b++) acc[r][b] = 0.0f;
+
+    for (int base = 0; base < ntask; base += 64 * NBL) {
+        uint4 la[NBL][R], lb[NBL][R], ha[NBL][R], hb[NBL][R];
+        uint2 sc[NBL][R];
+        uint32_t dw[NBL][R];
+#pragma unroll
+        for (int i = 0; i < NBL; i++) {
+            const int t = base + lane + 64 * i;
+            if (t < ntask) {
+                const int sb = t >> 2, hh = (t >> 1) & 1, jj = t & 1;
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    const int row = min(row0 + r, N - 1);
+                    const size_t blk = (size_t) row * nsb + sb;
+                    const uint4 * p = reinterpret_cast<const uint4 *>(wqs + blk * 208);
+                    la[i][r] = p[4 * hh + 2 * jj];
+                    lb[i][r] = p[4 * hh + 2 * jj + 1];
+                    ha[i][r] = p[8 + 2 * hh];
+                    hb[i][r] = p[9 + 2 * hh];
+                    sc[i][r] = *reinterpret_cast<const uint2 *>(wqs + blk * 208 + 192 + 8 * hh);
+                    dw[i][r] = wd[blk];
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NBL; i++) {
+            const int t = base + lane + 64 * i;
+            if (t >= ntask) break;
+            const int sb = t >> 2, hh = (t >> 1) & 1, jj = t & 1;
+#pragma unroll
+            for (int b = 0; b < B; b++) {
+                const int8_t * xb = xc + (size_t) b * K + (size_t) sb * QKK + 128 * hh + 32 * jj;
+                const int4 * xp = reinterpret_cast<const int4 *>(xb);
+                const int4 * xq = reinterpret_cast<const int4 *>(xb + 64);
+                const int4 x0 = xp[0], x1 = xp[1], x2 = xq[0], x3 = xq[1];
+                const uint32_t * bsw = reinterpret_cast<const uint32_t *>(xbs + (size_t) b * (K / 16) + sb * 16 + 8 * hh + 2 * jj);
+                const uint32_t bs01 = bsw[0], bs23 = bsw[2];
+                const float dx = xd[(size_t) b * nsb + sb];
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    int dd[4];
+                    dot_q6_K_task(la[i][r], lb[i][r], ha[i][r], hb[i][r], jj, x0, x1, x2, x3, dd);
+                    const int is = isum_q6_K_task(dd, sc[i][r], jj, bs01, bs23);
+                    acc[r][b] += (h2f((uint16_t) dw[i][r]) * dx) * (float) is;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int b = 0; b < B; b++) {
+            const float v = wave_sum(acc[r][b]);
+            if (lane == r * B + b && row0 + r < N) {
+                const size_t o = (size_t) b * ldy + row0 + r;
+                y[o] = res ? v + res[o] : v;
+            }
+        }
+}
+
 // -------------------------------------------------------------------- integer-sum dumps
 
 // The int32 block sums the GEMV kernels form, written out for bit-exact comparison:
@@ -367,6 +576,68 @@ __global__ void k_isums_q4_K(const uint8_t * w, const int8_t * xc, const int16_t
     }
     o[8] = isc;
     o[9] = imin;
+}
+
+// Q5_K: out[b][n][sb][10] as Q4_K (q = the 5-bit code).
+__global__ void k_isums_q5_K(const uint8_t * w, const int8_t * xc, const int16_t * xbs, int32_t * out, int N, int nsb,
+                             int B) {
+    const int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= (int64_t) B * N * nsb) return;
+    const int sb = (int) (t % nsb);
+    const int n = (int) ((t / nsb) % N);
+    const int b = (int) (t / ((int64_t) nsb * N));
+    const int K = nsb * QKK;
+    const uint4 * p = reinterpret_cast<const uint4 *>(w + (size_t) n * nsb * 176 + (size_t) sb * 176);
+    const uint4 hdr = p[0];
+    const uint32_t sc3[3] = {hdr.y, hdr.z, hdr.w};
+    int32_t * o = out + t * 10;
+    int isc = 0, imin = 0;
+    for (int c = 0; c < 4; c++) {
+        const int4 * xp = reinterpret_cast<const int4 *>(xc + (size_t) b * K + (size_t) sb * QKK + 64 * c);
+        int lo, hi, sc0, m0, sc1, m1;
+        dot_q5_K_chunk(p[3 + 2 * c], p[4 + 2 * c], p[1], p[2], c, xp[0], xp[1], xp[2], xp[3], lo, hi);
+        scale_min_k4_w(2 * c, sc3, sc0, m0);
+        scale_min_k4_w(2 * c + 1, sc3, sc1, m1);
+        const int16_t * bs = xbs + (size_t) b * (K / 16) + sb * 16 + 4 * c;
+        o[2 * c] = lo;
+        o[2 * c + 1] = hi;
+        isc += sc0 * lo + sc1 * hi;
+        imin += m0 * (bs[0] + bs[1]) + m1 * (bs[2] + bs[3]);
+    }
+    o[8] = isc;
+    o[9] = imin;
+}
+
+// Q6_K: out[b][n][sb][17] = the 16 sub-block sums of (q - 32) * x, then sum_j sc_j * those.
+__global__ void k_isums_q6_K(const uint8_t * wqs, const int8_t * xc, const int16_t * xbs, int32_t * out, int N,
+                             int nsb, int B) {
+    const int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= (int64_t) B * N * nsb) return;
+    const int sb = (int) (t % nsb);
+    const int n = (int) ((t / nsb) % N);
+    const int b = (int) (t / ((int64_t) nsb * N));
+    const int K = nsb * QKK;
+    const size_t blk = (size_t) n * nsb + sb;
+    const uint4 * p = reinterpret_cast<const uint4 *>(wqs + blk * 208);
+    int32_t * o = out + t * 17;
+    int total = 0;
+    for (int task = 0; task < 4; task++) {
+        const int hh = task >> 1, jj = task & 1;
+        const int8_t * xb = xc + (size_t) b * K + (size_t) sb * QKK + 128 * hh + 32 * jj;
+        const int4 * xp = reinterpret_cast<const int4 *>(xb);
+        const int4 * xq = reinterpret_cast<const int4 *>(xb + 64);
+        int dd[4];
+        dot_q6_K_task(p[4 * hh + 2 * jj], p[4 * hh + 2 * jj + 1], p[8 + 2 * hh], p[9 + 2 * hh], jj, xp[0], xp[1], xq[0],
+                      xq[1], dd);
+        const int16_t * bs = xbs + (size_t) b * (K / 16) + sb * 16;
+        const int s0 = 8 * hh + 2 * jj;
+        const int sub[4] = {s0, s0 + 1, s0 + 4, s0 + 5};
+        for (int k = 0; k < 4; k++) o[sub[k]] = dd[k] - 32 * bs[sub[k]];
+        const uint2 sc8 = *reinterpret_cast<const uint2 *>(wqs + blk * 208 + 192 + 8 * hh);
+        const uint32_t * bsw = reinterpret_cast<const uint32_t *>(bs + s0);
+        total += isum_q6_K_task(dd, sc8, jj, bsw[0], bsw[2]);
+    }
+    o[16] = total;
 }
 
 // -------------------------------------------------------------------------------- dispatch
@@ -440,6 +711,34 @@ void run_q4k(const uint8_t * w, const int8_t * xc, const int16_t * xbs, const fl
     k_gemv_q4_K<B, kR, NBL><<<grid, 256, 0, s>>>(w, xc, xbs, xd, y, res, N, nsb, ldy);
 }
 
+template <int B, int NBL>
+void run_q5k(const uint8_t * w, const int8_t * xc, const int16_t * xbs, const float * xd, float * y, const float * res,
+             int N, int nsb, int ldy, hipStream_t s) {
+    const unsigned grid = (unsigned) ((N + 4 * kR - 1) / (4 * kR));
+    k_gemv_q5_K<B, kR, NBL><<<grid, 256, 0, s>>>(w, xc, xbs, xd, y, res, N, nsb, ldy);
+}
+
+template <int B, int NBL>
+void run_q6k(const uint8_t * w, const WeightLayout & L, const int8_t * xc, const int16_t * xbs, const float * xd,
+             float * y, const float * res, int N, int nsb, int ldy, hipStream_t s) {
+    const unsigned grid = (unsigned) ((N + 4 * kR - 1) / (4 * kR));
+    k_gemv_q6_K<B, kR, NBL><<<grid, 256, 0, s>>>(w + L.qs, (const uint16_t *) (w + L.d), xc, xbs, xd, y, res, N, nsb,
+                                                 ldy);
+}
+
+// Q5_K / Q6_K hold 5 x 16 B of loads per (task, row): at most 2 tasks per lane per pass.
+template <int B>
+void run_k56_nbl(int type, int nbl, const uint8_t * w, const WeightLayout & L, const int8_t * xc, const int16_t * xbs,
+                 const float * xd, float * y, const float * res, int N, int nsb, int ldy, hipStream_t s) {
+    if (type == T_Q5_K) {
+        if (nbl == 1) run_q5k<B, 1>(w, xc, xbs, xd, y, res, N, nsb, ldy, s);
+        else run_q5k<B, 2>(w, xc, xbs, xd, y, res, N, nsb, ldy, s);
+    } else {
+        if (nbl == 1) run_q6k<B, 1>(w, L, xc, xbs, xd, y, res, N, nsb, ldy, s);
+        else run_q6k<B, 2>(w, L, xc, xbs, xd, y, res, N, nsb, ldy, s);
+    }
+}
+
 template <int B>
 void run_q4k_nbl(int nbl, const uint8_t * w, const int8_t * xc, const int16_t * xbs, const float * xd, float * y,
                  const float * res, int N, int nsb, int ldy, hipStream_t s) {
@@ -499,6 +798,23 @@ void launch_gemv(int type, const void * wv, int64_t N, int64_t K, const void * a
             case 7: run_q4k_nbl<7>(nbl, w, xc, xbs, xd, y, res, (int) N, nsb, (int) ldy, s); break;
             default: run_q4k_nbl<8>(nbl, w, xc, xbs, xd, y, res, (int) N, nsb, (int) ldy, s); break;
         }
+    } else if (type == T_Q5_K || type == T_Q6_K) {
+        const WeightLayout L = weight_layout(type, N, K);
+        const int nsb = (int) (K / QKK);
+        const int nbl = std::min(pick_nbl(nsb * 4), 2);
+        const int8_t * xc = (const int8_t *) (a + A.codes);
+        const int16_t * xbs = (const int16_t *) (a + A.meta);
+        const float * xd = (const float *) (a + A.d);
+        switch (B) {
+            case 1: run_k56_nbl<1>(type, nbl, w, L, xc, xbs, xd, y, res, (int) N, nsb, (int) ldy, s); break;
+            case 2: run_k56_nbl<2>(type, nbl, w, L, xc, xbs, xd, y, res, (int) N, nsb, (int) ldy, s); break;
+            case 3: run_k56_nbl<3>(type, nbl, w, L, xc, xbs, xd, y, res, (int) N, nsb, (int) ldy, s); break;
+            case 4: run_k56_nbl<4>(type, nbl, w, L, xc, xbs, xd, y, res, (int) N, nsb, (int) ldy, s); break;
+            case 5: run_k56_nbl<5>(type, nbl, w, L, xc, xbs, xd, y, res, (int) N, nsb, (int) ldy, s); break;
+            case 6: run_k56_nbl<6>(type, nbl, w, L, xc, xbs, xd, y, res, (int) N, nsb, (int) ldy, s); break;
+            case 7: run_k56_nbl<7>(type, nbl, w, L, xc, xbs, xd, y, res, (int) N, nsb, (int) ldy, s); break;
+            default: run_k56_nbl<8>(type, nbl, w, L, xc, xbs, xd, y, res, (int) N, nsb, (int) ldy, s); break;
+        }
     } else {
         fail("mul_mat: unsupported weight type " + std::to_string(type));
     }
@@ -521,6 +837,19 @@ void launch_isums(int type, const void * wv, int64_t N, int64_t K, const void * 
         const int nsb = (int) (K / QKK);
         const int64_t n = B * N * nsb;
         k_isums_q4_K<<<(unsigned) ((n + 255) / 256), 256, 0, s>>>(w, (const int8_t *) (a + A.codes),
+                                                               (const int16_t *) (a + A.meta), out, (int) N, nsb,
+                                                               (int) B);
+    } else if (type == T_Q5_K) {
+        const int nsb = (int) (K / QKK);
+        const int64_t n = B * N * nsb;
+        k_isums_q5_K<<<(unsigned) ((n + 255) / 256), 256, 0, s>>>(w, (const int8_t *) (a + A.codes),
+                                                               (const int16_t *) (a + A.meta), out, (int) N, nsb,
+                                                               (int) B);
+    } else if (type == T_Q6_K) {
+        const WeightLayout L = weight_layout(type, N, K);
+        const int nsb = (int) (K / QKK);
+        const int64_t n = B * N * nsb;
+        k_isums_q6_K<<<(unsigned) ((n + 255) / 256), 256, 0, s>>>(w + L.qs, (const int8_t *) (a + A.codes),
                                                                (const int16_t *) (a + A.meta), out, (int) N, nsb,
                                                                (int) B);
     } else {

@@ -448,7 +448,7 @@ struct Planner {
             std::memcpy(&eps, &nrm->op_params[0], 4);
             x = nrm->src[0];
         }
-        require(whole_packed(w), "mul_mat " + tname(mm) + ": the weight must be a whole Q4_0 / Q8_0 / Q4_K tensor in "
+        require(whole_packed(w), "mul_mat " + tname(mm) + ": the weight must be a whole Q4_0 / Q8_0 / Q4_K / Q5_K / Q6_K tensor in "
                                                           "a HIP buffer (other weight types are not on this path)");
         require(w->ne[2] == 1 && w->ne[3] == 1, "mul_mat " + tname(mm) + ": batched weights are not supported");
         int64_t M = 0, ldx = 0;
@@ -471,7 +471,7 @@ struct Planner {
         s.f[0] = eps;
         const bool row = M == 1 && (w->type == GGML_TYPE_Q4_0 || w->type == GGML_TYPE_Q8_0) && row_gemv_fits(w->type, K);
         if (!row) {
-            const int64_t B = w->type == GGML_TYPE_Q4_K ? std::min<int64_t>(M, 8) : M;
+            const int64_t B = is_kquant(w->type) ? std::min<int64_t>(M, 8) : M;
             ws_need = std::max(ws_need, act_layout(w->type, B, K).total);
         }
         steps.push_back(s);
@@ -815,7 +815,7 @@ void run_step(const ggml_backend * be, const Step & s) {
                 launch_row_gemv(wt, nw ? PRO_NORM : PRO_PLAIN, EPI_STORE, a, st);
                 return;
             }
-            if (wt == T_Q4_K && M > 8) {
+            if (is_kquant(wt) && M > 8) {
                 for (int64_t m = 0; m < M; m += 8) {
                     const int64_t b = std::min<int64_t>(8, M - m);
                     launch_act_quant(wt, x + m * ldx, ldx, b, K, be->ws, st);

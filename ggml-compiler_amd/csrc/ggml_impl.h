@@ -37,8 +37,10 @@ inline const ggml_tensor * base_of(const ggml_tensor * t) { return t->view_src ?
 inline bool is_view_op(int op) {
     return op == GGML_OP_VIEW || op == GGML_OP_RESHAPE || op == GGML_OP_PERMUTE || op == GGML_OP_TRANSPOSE;
 }
-// A Q4_0 / Q8_0 / Q4_K tensor in this library's device buffers: stored packed (gcq_pack_weights).
-inline bool is_packed_type(int t) { return t == GGML_TYPE_Q4_0 || t == GGML_TYPE_Q8_0 || t == GGML_TYPE_Q4_K; }
+// A Q4_0 / Q8_0 / Q4_K / Q5_K / Q6_K tensor in this library's device buffers: stored packed (gcq_pack_weights).
+inline bool is_packed_type(int t) {
+    return t == GGML_TYPE_Q4_0 || t == GGML_TYPE_Q8_0 || t == GGML_TYPE_Q4_K || t == GGML_TYPE_Q5_K || t == GGML_TYPE_Q6_K;
+}
 
 // Fusion chains of a graph (ggml_backend.hip): end[i] is the node index at which node i's work
 // runs (i itself, or the last node of the chain it starts or belongs to; for a folded norm, its

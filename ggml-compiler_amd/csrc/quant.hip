@@ -3,10 +3,10 @@
 // Weight encoders produce ggml's block bytes exactly (the ggml_compiler_quantize contract,
 // runtime/include/ggml_compiler_rt.h:83-87, whose CPU implementation is ggml_quantize_chunk with
 // no importance matrix, runtime/src/ggml_compiler_rt.cpp:859-876). They run one thread per block
-// (one per 256-super-block for Q4_K) in ggml's sequential order with contraction off, so every
+// (one per 256-super-block for the K-quants) in ggml's sequential order with contraction off, so every
 // float operation rounds as the C reference does. Activation quantizers produce the vec_dot_type
 // that ggml-cpu converts src1 into before a quantized mul_mat (Q8_0 for Q4_0/Q8_0 weights, Q8_K
-// for Q4_K), in the device "act" layout described in gcq_common.h.
+// for Q4_K / Q5_K / Q6_K), in the device "act" layout described in gcq_common.h.
 #include "gcq_common.h"
 
 namespace gcq {
@@ -61,9 +61,11 @@ __global__ void k_enc_q4_0(const float * __restrict__ x, uint8_t * __restrict__ 
 
 __device__ __forceinline__ int near_int(float v) { return __float2int_rn(v); }
 
-// ggml make_qkx2_quants(32, 15, x, w, L, &min, Laux, -1, 0.1, 20, false): weighted least-squares
-// (scale, min) over 21 candidate inverse scales. Sequential, as the C reference.
-__device__ float qkx2_fit(const float * x, const float * w, uint8_t * L, float * the_min) {
+// ggml make_qkx2_quants(32, NMAX, x, w, L, &min, Laux, rmin, 0.1, NSTEP, false): weighted
+// least-squares (scale, min) over NSTEP + 1 candidate inverse scales. Sequential, as the C
+// reference. Q4_K: NMAX 15, rmin -1, NSTEP 20; Q5_K: NMAX 31, rmin -0.5, NSTEP 15.
+template <int NMAX, int NSTEP>
+__device__ float qkx2_fit(const float * x, const float * w, uint8_t * L, float * the_min, float rmin) {
 #pragma clang fp contract(off)
     uint8_t Laux[32];
     float min = x[0], max = x[0];
@@ -82,22 +84,22 @@ __device__ float qkx2_fit(const float * x, const float * w, uint8_t * L, float *
         *the_min = -min;
         return 0.0f;
     }
-    float iscale = __fdiv_rn(15.0f, max - min);
+    float iscale = __fdiv_rn((float) NMAX, max - min);
     float scale = __fdiv_rn(1.0f, iscale);
     float best = 0;
     for (int i = 0; i < 32; i++) {
         int l = near_int(iscale * (x[i] - min));
-        l = l < 0 ? 0 : (l > 15 ? 15 : l);
+        l = l < 0 ? 0 : (l > NMAX ? NMAX : l);
         L[i] = (uint8_t) l;
         const float diff = scale * (float) L[i] + min - x[i];
         best += w[i] * (diff * diff);
     }
-    for (int is = 0; is <= 20; is++) {
-        iscale = __fdiv_rn(-1.0f + 0.1f * (float) is + 15.0f, max - min);
+    for (int is = 0; is <= NSTEP; is++) {
+        iscale = __fdiv_rn(rmin + 0.1f * (float) is + (float) NMAX, max - min);
         float sum_l = 0, sum_l2 = 0, sum_xl = 0;
         for (int i = 0; i < 32; i++) {
             int l = near_int(iscale * (x[i] - min));
-            l = l < 0 ? 0 : (l > 15 ? 15 : l);
+            l = l < 0 ? 0 : (l > NMAX ? NMAX : l);
             Laux[i] = (uint8_t) l;
             const float wi = w[i];
             const float lf = (float) l;
@@ -140,27 +142,13 @@ __device__ __forceinline__ void scale_min_k4(int j, const uint8_t * q, int & sc,
     }
 }
 
-// ggml quantize_row_q4_K_ref, one thread per 256-value super-block.
-__global__ void k_enc_q4_K(const float * __restrict__ xall, uint8_t * __restrict__ out, int64_t nblocks) {
+// The 6-bit (scale, min) pairs of a Q4_K / Q5_K super-block, relative to its largest scale and
+// min (ggml quantize_row_q4_K_ref / q5_K_ref): writes scales[12], returns fp16 (d, dmin).
+__device__ void pack_scale_min_k4(const float * scales, const float * mins, float max_scale, float max_min,
+                                  uint8_t * sb, uint16_t & dh, uint16_t & mh) {
 #pragma clang fp contract(off)
-    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= nblocks) return;
-    const float * x = xall + i * QKK;
-    uint8_t L[QKK];
-    float w[32], mins[8], scales[8];
-    float max_scale = 0, max_min = 0;
-    for (int j = 0; j < 8; j++) {
-        float sum_x2 = 0;
-        for (int l = 0; l < 32; l++) sum_x2 += x[32 * j + l] * x[32 * j + l];
-        const float av_x = __fsqrt_rn(__fdiv_rn(sum_x2, 32.0f));
-        for (int l = 0; l < 32; l++) w[l] = av_x + fabsf(x[32 * j + l]);
-        scales[j] = qkx2_fit(x + 32 * j, w, L + 32 * j, &mins[j]);
-        if (scales[j] > max_scale) max_scale = scales[j];
-        if (mins[j] > max_min) max_min = mins[j];
-    }
     const float inv_scale = max_scale > 0 ? __fdiv_rn(63.f, max_scale) : 0.f;
     const float inv_min = max_min > 0 ? __fdiv_rn(63.f, max_min) : 0.f;
-    uint8_t sb[12];
     for (int j = 0; j < 12; j++) sb[j] = 0;
     for (int j = 0; j < 8; j++) {
         int ls = near_int(inv_scale * scales[j]);
@@ -176,8 +164,31 @@ __global__ void k_enc_q4_K(const float * __restrict__ xall, uint8_t * __restrict
             sb[j] |= (uint8_t) ((lm >> 4) << 6);
         }
     }
-    const uint16_t dh = f2h_exact(__fdiv_rn(max_scale, 63.f));
-    const uint16_t mh = f2h_exact(__fdiv_rn(max_min, 63.f));
+    dh = f2h_exact(__fdiv_rn(max_scale, 63.f));
+    mh = f2h_exact(__fdiv_rn(max_min, 63.f));
+}
+
+// ggml quantize_row_q4_K_ref, one thread per 256-value super-block.
+__global__ void k_enc_q4_K(const float * __restrict__ xall, uint8_t * __restrict__ out, int64_t nblocks) {
+#pragma clang fp contract(off)
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblocks) return;
+    const float * x = xall + i * QKK;
+    uint8_t L[QKK];
+    float w[32], mins[8], scales[8];
+    float max_scale = 0, max_min = 0;
+    for (int j = 0; j < 8; j++) {
+        float sum_x2 = 0;
+        for (int l = 0; l < 32; l++) sum_x2 += x[32 * j + l] * x[32 * j + l];
+        const float av_x = __fsqrt_rn(__fdiv_rn(sum_x2, 32.0f));
+        for (int l = 0; l < 32; l++) w[l] = av_x + fabsf(x[32 * j + l]);
+        scales[j] = qkx2_fit<15, 20>(x + 32 * j, w, L + 32 * j, &mins[j], -1.0f);
+        if (scales[j] > max_scale) max_scale = scales[j];
+        if (mins[j] > max_min) max_min = mins[j];
+    }
+    uint8_t sb[12];
+    uint16_t dh, mh;
+    pack_scale_min_k4(scales, mins, max_scale, max_min, sb, dh, mh);
     for (int j = 0; j < 8; j++) {
         int sc, m;
         scale_min_k4(j, sb, sc, m);
@@ -197,6 +208,174 @@ __global__ void k_enc_q4_K(const float * __restrict__ xall, uint8_t * __restrict
     for (int j = 0; j < 12; j++) o[4 + j] = sb[j];
     for (int c = 0; c < 4; c++)
         for (int l = 0; l < 32; l++) o[16 + 32 * c + l] = (uint8_t) (L[64 * c + l] | (L[64 * c + 32 + l] << 4));
+}
+
+// ggml quantize_row_q5_K_ref, one thread per 256-value super-block: the Q4_K fit with 5-bit codes
+// (make_qkx2_quants(32, 31, ..., -0.5, 0.1, 15)), the fifth bit of value 64c + l (c < 4, l < 64)
+// in bit 2c + (l >= 32) of qh[l % 32].
+__global__ void k_enc_q5_K(const float * __restrict__ xall, uint8_t * __restrict__ out, int64_t nblocks) {
+#pragma clang fp contract(off)
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblocks) return;
+    const float * x = xall + i * QKK;
+    uint8_t L[QKK];
+    float w[32], mins[8], scales[8];
+    float max_scale = 0, max_min = 0;
+    for (int j = 0; j < 8; j++) {
+        float sum_x2 = 0;
+        for (int l = 0; l < 32; l++) sum_x2 += x[32 * j + l] * x[32 * j + l];
+        const float av_x = __fsqrt_rn(__fdiv_rn(sum_x2, 32.0f));
+        for (int l = 0; l < 32; l++) w[l] = av_x + fabsf(x[32 * j + l]);
+        scales[j] = qkx2_fit<31, 15>(x + 32 * j, w, L + 32 * j, &mins[j], -0.5f);
+        if (scales[j] > max_scale) max_scale = scales[j];
+        if (mins[j] > max_min) max_min = mins[j];
+    }
+    uint8_t sb[12];
+    uint16_t dh, mh;
+    pack_scale_min_k4(scales, mins, max_scale, max_min, sb, dh, mh);
+    for (int j = 0; j < 8; j++) {
+        int sc, m;
+        scale_min_k4(j, sb, sc, m);
+        const float d = h2f(dh) * (float) sc;
+        if (d == 0.0f) continue;  // the fit's codes stay, as in ggml
+        const float dm = h2f(mh) * (float) m;
+        for (int l = 0; l < 32; l++) {
+            int q = near_int(__fdiv_rn(x[32 * j + l] + dm, d));
+            L[32 * j + l] = (uint8_t) (q < 0 ? 0 : (q > 31 ? 31 : q));
+        }
+    }
+    uint8_t * o = out + i * 176;
+    o[0] = (uint8_t) dh;
+    o[1] = (uint8_t) (dh >> 8);
+    o[2] = (uint8_t) mh;
+    o[3] = (uint8_t) (mh >> 8);
+    for (int j = 0; j < 12; j++) o[4 + j] = sb[j];
+    uint8_t * qh = o + 16;
+    uint8_t * ql = o + 48;
+    for (int l = 0; l < 32; l++) qh[l] = 0;
+    for (int c = 0; c < 4; c++) {
+        for (int l = 0; l < 32; l++) {
+            int l1 = L[64 * c + l], l2 = L[64 * c + 32 + l];
+            if (l1 > 15) {
+                l1 -= 16;
+                qh[l] |= (uint8_t) (1u << (2 * c));
+            }
+            if (l2 > 15) {
+                l2 -= 16;
+                qh[l] |= (uint8_t) (2u << (2 * c));
+            }
+            ql[32 * c + l] = (uint8_t) (l1 | (l2 << 4));
+        }
+    }
+}
+
+// ggml make_qx_quants(16, 32, x, L, rmse_type = 1, no weights): the symmetric scale of 16 values
+// with codes l + 32, l in [-32, 31], refined over 18 candidate inverse scales by the x^2-weighted
+// least-squares fit. L receives the codes (0..63).
+__device__ float qx_fit16(const float * x, uint8_t * L) {
+#pragma clang fp contract(off)
+    constexpr int nmax = 32;
+    float max = 0, amax = 0;
+    for (int i = 0; i < 16; i++) {
+        const float ax = fabsf(x[i]);
+        if (ax > amax) {
+            amax = ax;
+            max = x[i];
+        }
+    }
+    if (amax < 1e-15f) {  // GROUP_MAX_EPS
+        for (int i = 0; i < 16; i++) L[i] = 0;
+        return 0.0f;
+    }
+    float iscale = __fdiv_rn((float) -nmax, max);
+    float sumlx = 0, suml2 = 0;
+    for (int i = 0; i < 16; i++) {
+        int l = near_int(iscale * x[i]);
+        l = l < -nmax ? -nmax : (l > nmax - 1 ? nmax - 1 : l);
+        L[i] = (uint8_t) (l + nmax);
+        const float w = x[i] * x[i];
+        sumlx += w * x[i] * (float) l;
+        suml2 += w * (float) l * (float) l;
+    }
+    float scale = suml2 != 0.0f ? __fdiv_rn(sumlx, suml2) : 0.0f;
+    float best = scale * sumlx;
+    for (int is = -9; is <= 9; is++) {
+        if (is == 0) continue;
+        iscale = __fdiv_rn(-((float) nmax + 0.1f * (float) is), max);
+        sumlx = suml2 = 0;
+        for (int i = 0; i < 16; i++) {
+            int l = near_int(iscale * x[i]);
+            l = l < -nmax ? -nmax : (l > nmax - 1 ? nmax - 1 : l);
+            const float w = x[i] * x[i];
+            sumlx += w * x[i] * (float) l;
+            suml2 += w * (float) l * (float) l;
+        }
+        if (suml2 > 0 && sumlx * sumlx > best * suml2) {
+            for (int i = 0; i < 16; i++) {
+                int l = near_int(iscale * x[i]);
+                L[i] = (uint8_t) (nmax + (l < -nmax ? -nmax : (l > nmax - 1 ? nmax - 1 : l)));
+            }
+            scale = __fdiv_rn(sumlx, suml2);
+            best = scale * sumlx;
+        }
+    }
+    return scale;
+}
+
+// ggml quantize_row_q6_K_ref, one thread per 256-value super-block, written in ggml's 210-byte
+// block_q6_K {ql[128], qh[64], scales[16] int8, fp16 d}: 16 sub-block fits, int8 scales against
+// the largest-magnitude one (iscale = -128 / max), codes recomputed against the rounded scales.
+__global__ void k_enc_q6_K(const float * __restrict__ xall, uint8_t * __restrict__ out, int64_t nblocks) {
+#pragma clang fp contract(off)
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblocks) return;
+    const float * x = xall + i * QKK;
+    uint8_t * o = out + i * 210;
+    uint8_t L[QKK];
+    float scales[16];
+    float max_scale = 0, max_abs_scale = 0;
+    for (int ib = 0; ib < 16; ib++) {
+        const float sc = qx_fit16(x + 16 * ib, L + 16 * ib);
+        scales[ib] = sc;
+        if (fabsf(sc) > max_abs_scale) {
+            max_abs_scale = fabsf(sc);
+            max_scale = sc;
+        }
+    }
+    if (max_abs_scale < 1e-15f) {  // an all-zero block
+        for (int j = 0; j < 210; j++) o[j] = 0;
+        return;
+    }
+    const float iscale = __fdiv_rn(-128.0f, max_scale);
+    const uint16_t dh = f2h_exact(__fdiv_rn(1.0f, iscale));
+    int8_t sc8[16];
+    for (int ib = 0; ib < 16; ib++) {
+        const int v = near_int(iscale * scales[ib]);
+        sc8[ib] = (int8_t) (v < 127 ? v : 127);
+    }
+    for (int j = 0; j < 16; j++) {
+        const float d = h2f(dh) * (float) sc8[j];
+        if (d == 0.0f) continue;
+        for (int ii = 0; ii < 16; ii++) {
+            int l = near_int(__fdiv_rn(x[16 * j + ii], d));
+            l = l < -32 ? -32 : (l > 31 ? 31 : l);
+            L[16 * j + ii] = (uint8_t) (l + 32);
+        }
+    }
+    uint8_t * ql = o;
+    uint8_t * qh = o + 128;
+    for (int h = 0; h < 2; h++) {
+        const uint8_t * Lh = L + 128 * h;
+        for (int l = 0; l < 32; l++) {
+            ql[64 * h + l] = (uint8_t) ((Lh[l] & 0xF) | ((Lh[l + 64] & 0xF) << 4));
+            ql[64 * h + 32 + l] = (uint8_t) ((Lh[l + 32] & 0xF) | ((Lh[l + 96] & 0xF) << 4));
+            qh[32 * h + l] = (uint8_t) ((Lh[l] >> 4) | ((Lh[l + 32] >> 4) << 2) | ((Lh[l + 64] >> 4) << 4) |
+                                        ((Lh[l + 96] >> 4) << 6));
+        }
+    }
+    for (int j = 0; j < 16; j++) o[192 + j] = (uint8_t) sc8[j];
+    o[208] = (uint8_t) dh;
+    o[209] = (uint8_t) (dh >> 8);
 }
 
 // f32 -> f16 rows (ggml_quantize_chunk for F16: round to nearest even).
@@ -223,6 +402,33 @@ __global__ void k_pack(const uint8_t * __restrict__ src, uint8_t * __restrict__ 
     uint4 * o = reinterpret_cast<uint4 *>(qs + i * CB);
 #pragma unroll
     for (int j = 0; j < CB / 16; j++) o[j] = make_uint4(w[4 * j], w[4 * j + 1], w[4 * j + 2], w[4 * j + 3]);
+}
+
+// ggml block_q6_K rows -> packed: the first 208 bytes (ql, qh, scales) of each 210-byte block as
+// 13 aligned 16-byte words, the fp16 d into its own array; one thread per word.
+__global__ void k_pack_q6_K(const uint8_t * __restrict__ src, uint8_t * __restrict__ qs, uint16_t * __restrict__ d,
+                            int64_t nblocks) {
+    const int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= nblocks * 13) return;
+    const int64_t i = t / 13;
+    const int c = (int) (t % 13);
+    const uint8_t * b = src + i * 210 + 16 * c;
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+        w[j] = b[4 * j] | (b[4 * j + 1] << 8) | (b[4 * j + 2] << 16) | ((uint32_t) b[4 * j + 3] << 24);
+    reinterpret_cast<uint4 *>(qs)[t] = make_uint4(w[0], w[1], w[2], w[3]);
+    if (c == 0) d[i] = (uint16_t) (src[i * 210 + 208] | (src[i * 210 + 209] << 8));
+}
+
+// packed Q6_K -> ggml block rows; one thread per output byte.
+__global__ void k_unpack_q6_K(const uint8_t * __restrict__ qs, const uint16_t * __restrict__ d, uint8_t * __restrict__ dst,
+                              int64_t nblocks) {
+    const int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= nblocks * 210) return;
+    const int64_t i = t / 210;
+    const int j = (int) (t % 210);
+    dst[t] = j < 208 ? qs[i * 208 + j] : (uint8_t) (d[i] >> (8 * (j - 208)));
 }
 
 // Whole ggml rows moved by a row map, 16 bytes per thread (row_bytes % 16 == 0) or 2 (otherwise):
@@ -290,6 +496,52 @@ __global__ void k_dequant_q4_K(const uint8_t * __restrict__ w, float * __restric
     const uint8_t q = b[16 + k];
     y[i * 256 + 64 * c + l] = d1 * (float) (q & 0xF) - m1;
     y[i * 256 + 64 * c + 32 + l] = d2 * (float) (q >> 4) - m2;
+}
+
+// ggml dequantize_row_q5_K: y = d * sc * (nibble + 16 * high bit) - dmin * m; one thread per qs byte.
+__global__ void k_dequant_q5_K(const uint8_t * __restrict__ w, float * __restrict__ y, int64_t nblocks) {
+#pragma clang fp contract(off)
+    const int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= nblocks * 128) return;
+    const int64_t i = t / 128;
+    const int k = (int) (t % 128);
+    const int c = k / 32, l = k % 32;
+    const uint8_t * b = w + i * 176;
+    const float d = h2f((uint16_t) (b[0] | (b[1] << 8)));
+    const float dmin = h2f((uint16_t) (b[2] | (b[3] << 8)));
+    int sc, m;
+    scale_min_k4(2 * c, b + 4, sc, m);
+    const float d1 = d * (float) sc, m1 = dmin * (float) m;
+    scale_min_k4(2 * c + 1, b + 4, sc, m);
+    const float d2 = d * (float) sc, m2 = dmin * (float) m;
+    const uint8_t q = b[48 + k], h = b[16 + l];
+    y[i * 256 + 64 * c + l] = d1 * (float) ((q & 0xF) + ((h >> (2 * c)) & 1 ? 16 : 0)) - m1;
+    y[i * 256 + 64 * c + 32 + l] = d2 * (float) ((q >> 4) + ((h >> (2 * c + 1)) & 1 ? 16 : 0)) - m2;
+}
+
+// ggml dequantize_row_q6_K on the packed layout: y = d * sc * (q - 32); one thread per (block,
+// half h, l < 32), four values each.
+__global__ void k_dequant_q6_K(const uint8_t * __restrict__ qs, const uint16_t * __restrict__ dv,
+                               float * __restrict__ y, int64_t nblocks) {
+#pragma clang fp contract(off)
+    const int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= nblocks * 64) return;
+    const int64_t i = t / 64;
+    const int h = (int) (t % 64) / 32, l = (int) (t % 32);
+    const uint8_t * b = qs + i * 208;
+    const float d = h2f(dv[i]);
+    const uint8_t a0 = b[64 * h + l], a1 = b[64 * h + 32 + l], qh = b[128 + 32 * h + l];
+    const int8_t * sc = reinterpret_cast<const int8_t *>(b + 192 + 8 * h);
+    const int is = l / 16;
+    const int q1 = (int) ((a0 & 0xF) | (((qh >> 0) & 3) << 4)) - 32;
+    const int q2 = (int) ((a1 & 0xF) | (((qh >> 2) & 3) << 4)) - 32;
+    const int q3 = (int) ((a0 >> 4) | (((qh >> 4) & 3) << 4)) - 32;
+    const int q4 = (int) ((a1 >> 4) | (((qh >> 6) & 3) << 4)) - 32;
+    float * o = y + i * 256 + 128 * h + l;
+    o[0] = d * (float) sc[is + 0] * (float) q1;
+    o[32] = d * (float) sc[is + 2] * (float) q2;
+    o[64] = d * (float) sc[is + 4] * (float) q3;
+    o[96] = d * (float) sc[is + 6] * (float) q4;
 }
 
 // ------------------------------------------------------------------ activation quantizers
@@ -415,6 +667,8 @@ void launch_encode(int type, const float * src, int64_t nrows, int64_t k, void *
         case T_Q8_0: k_enc_q8_0<<<nblk(nb, 128), 128, 0, s>>>(src, (uint8_t *) dst, nb); break;
         case T_Q4_0: k_enc_q4_0<<<nblk(nb, 128), 128, 0, s>>>(src, (uint8_t *) dst, nb); break;
         case T_Q4_K: k_enc_q4_K<<<nblk(nb, 64), 64, 0, s>>>(src, (uint8_t *) dst, nb); break;
+        case T_Q5_K: k_enc_q5_K<<<nblk(nb, 64), 64, 0, s>>>(src, (uint8_t *) dst, nb); break;
+        case T_Q6_K: k_enc_q6_K<<<nblk(nb, 64), 64, 0, s>>>(src, (uint8_t *) dst, nb); break;
         case T_F16: k_enc_f16<<<nblk(nb, 256), 256, 0, s>>>(src, (uint16_t *) dst, nb); break;
         default: fail("encode: unsupported type " + std::to_string(type));
     }
@@ -424,8 +678,14 @@ void launch_encode(int type, const float * src, int64_t nrows, int64_t k, void *
 void launch_pack(int type, const void * src, int64_t nrows, int64_t k, void * dst, hipStream_t s) {
     const WeightLayout L = weight_layout(type, nrows, k);
     uint8_t * o = (uint8_t *) dst;
-    if (type == T_Q4_K) {
+    if (type == T_Q4_K || type == T_Q5_K) {
         check_hip(hipMemcpyAsync(dst, src, row_bytes(type, k) * nrows, hipMemcpyDeviceToDevice, s), "pack copy");
+        return;
+    }
+    if (type == T_Q6_K) {
+        const int64_t nb = nrows * (k / QKK);
+        if (nb) k_pack_q6_K<<<nblk(nb * 13, 256), 256, 0, s>>>((const uint8_t *) src, o + L.qs, (uint16_t *) (o + L.d), nb);
+        check_launch("pack");
         return;
     }
     const int64_t nb = nrows * (k / QK);
@@ -458,8 +718,14 @@ void launch_move_rows(const void * src, void * dst, const int32_t * map, int64_t
 void launch_unpack(int type, const void * src, int64_t nrows, int64_t k, void * dst, hipStream_t s) {
     const WeightLayout L = weight_layout(type, nrows, k);
     const uint8_t * p = (const uint8_t *) src;
-    if (type == T_Q4_K) {
+    if (type == T_Q4_K || type == T_Q5_K) {
         check_hip(hipMemcpyAsync(dst, src, row_bytes(type, k) * nrows, hipMemcpyDeviceToDevice, s), "unpack copy");
+        return;
+    }
+    if (type == T_Q6_K) {
+        const int64_t nb = nrows * (k / QKK);
+        if (nb) k_unpack_q6_K<<<nblk(nb * 210, 256), 256, 0, s>>>(p + L.qs, (const uint16_t *) (p + L.d), (uint8_t *) dst, nb);
+        check_launch("unpack");
         return;
     }
     const int64_t nb = nrows * (k / QK);
@@ -485,6 +751,12 @@ void launch_dequant(int type, const void * w, int64_t nrows, int64_t k, float * 
     } else if (type == T_Q4_K) {
         const int64_t nb = nrows * (k / QKK);
         if (nb) k_dequant_q4_K<<<nblk(nb * 128, 256), 256, 0, s>>>(p, y, nb);
+    } else if (type == T_Q5_K) {
+        const int64_t nb = nrows * (k / QKK);
+        if (nb) k_dequant_q5_K<<<nblk(nb * 128, 256), 256, 0, s>>>(p, y, nb);
+    } else if (type == T_Q6_K) {
+        const int64_t nb = nrows * (k / QKK);
+        if (nb) k_dequant_q6_K<<<nblk(nb * 64, 256), 256, 0, s>>>(p + L.qs, (const uint16_t *) (p + L.d), y, nb);
     } else {
         fail("dequantize: unsupported type " + std::to_string(type));
     }
@@ -497,7 +769,7 @@ void launch_act_quant(int wtype, const float * x, int64_t ldx, int64_t B, int64_
     if (wtype == T_Q4_0 || wtype == T_Q8_0) {
         const int64_t n = B * k / 4;
         k_act_q8_0<<<nblk(n, 256), 256, 0, s>>>(x, ldx, (int8_t *) (a + L.codes), (float2 *) (a + L.meta), B, k);
-    } else if (wtype == T_Q4_K) {
+    } else if (is_kquant(wtype)) {
         const int64_t waves = B * (k / QKK);
         k_act_q8_K<<<nblk(waves * 64, 256), 256, 0, s>>>(x, ldx, (int8_t *) (a + L.codes), (int16_t *) (a + L.meta),
                                                         (float *) (a + L.d), B, k);

@@ -14,8 +14,10 @@ import torch
 
 from ._lib import GcqError, check, load
 
-F32, F16, Q4_0, Q8_0, Q4_K, Q8_K = 0, 1, 2, 8, 12, 15
-TYPES = {"f32": F32, "f16": F16, "q4_0": Q4_0, "q8_0": Q8_0, "q4_K": Q4_K, "q4_k": Q4_K}
+F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, Q8_K = 0, 1, 2, 8, 12, 13, 14, 15
+TYPES = {"f32": F32, "f16": F16, "q4_0": Q4_0, "q8_0": Q8_0, "q4_K": Q4_K, "q4_k": Q4_K, "q5_K": Q5_K, "q5_k": Q5_K,
+         "q6_K": Q6_K, "q6_k": Q6_K}
+KQUANTS = (Q4_K, Q5_K, Q6_K)
 
 
 def type_id(t: int | str) -> int:
@@ -130,7 +132,7 @@ def quantize_act(wtype: int | str, x: torch.Tensor) -> torch.Tensor:
 
 def act_to_ggml(wtype: int | str, act: torch.Tensor, B: int, K: int) -> torch.Tensor:
     wtype = type_id(wtype)
-    xt = Q8_K if wtype == Q4_K else Q8_0
+    xt = Q8_K if wtype in KQUANTS else Q8_0
     out = torch.empty((B, row_size(xt, K)), dtype=torch.uint8, device=act.device)
     check(load().gcq_act_to_ggml(wtype, _p(act), B, K, _p(out), _stream()))
     return out
@@ -191,7 +193,7 @@ def swiglu_q8(g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
 
 
 def block_isums(w: QuantWeight, act: torch.Tensor, B: int) -> torch.Tensor:
-    per = w.K // 32 if w.type in (Q4_0, Q8_0) else 10 * (w.K // 256)
+    per = w.K // 32 if w.type in (Q4_0, Q8_0) else (17 if w.type == Q6_K else 10) * (w.K // 256)
     out = torch.empty((B, w.N, per), dtype=torch.int32, device=act.device)
     check(load().gcq_block_isums(w.type, _p(w.data), w.N, w.K, _p(act), B, _p(out), _stream()))
     return out

@@ -1,6 +1,6 @@
 /*
  * gcq.h - C ABI of libgcq: gfx950 HIP kernels for the quantized mat-mul and KV-cache attention
- * path of ggml-compiler's programs (ggml_mul_mat on GGUF Q8_0 / Q4_0 / Q4_K blocks,
+ * path of ggml-compiler's programs (ggml_mul_mat on GGUF Q8_0 / Q4_0 / Q4_K (and Q5_K / Q6_K) blocks,
  * ggml_flash_attn_ext over an f16 cache, ggml_rms_norm, ggml_rope_ext and the decode step's glue).
  *
  * Plain C: device pointers, sizes and a hipStream_t passed as void* (NULL = the default stream).
@@ -36,6 +36,8 @@ enum {
     GCQ_TYPE_Q4_0 = 2,
     GCQ_TYPE_Q8_0 = 8,
     GCQ_TYPE_Q4_K = 12,
+    GCQ_TYPE_Q5_K = 13,
+    GCQ_TYPE_Q6_K = 14,
     GCQ_TYPE_Q8_K = 15,
     GCQ_TYPE_I32 = 26,
 };
@@ -64,14 +66,15 @@ GCQ_API size_t gcq_flash_attn_workspace(int Sq, int H, int Hkv, int Dv, int n_kv
 /* Encode f32 rows (device) in ggml's block bytes (device), exactly as ggml's reference encoders
  * (ggml_quantize_chunk without an importance matrix). Replaces the arithmetic behind
  * ggml_compiler_quantize (runtime/include/ggml_compiler_rt.h:83-87,
- * runtime/src/ggml_compiler_rt.cpp:859-876). Types: Q8_0, Q4_0, Q4_K. */
+ * runtime/src/ggml_compiler_rt.cpp:859-876). Types: Q8_0, Q4_0, Q4_K, Q5_K, Q6_K (the storage types of
+ * ggml_compiler/quant/types.py:6-19 this library computes with). */
 GCQ_API int gcq_quantize(int type, const float * src, int64_t nrows, int64_t n_per_row, void * dst, void * stream);
 /* ggml block rows (device) -> packed device weight. dst must hold gcq_weight_size bytes, 16-byte
  * aligned. Replaces the weight upload of runtime/src/ggml_compiler_rt.cpp:445-479 (:476). */
 GCQ_API int gcq_pack_weights(int type, const void * src, int64_t nrows, int64_t n_per_row, void * dst, void * stream);
 /* Packed weight -> f32 rows (ggml dequantize_row_*; bit-exact). */
 GCQ_API int gcq_dequantize(int type, const void * w, int64_t nrows, int64_t n_per_row, float * dst, void * stream);
-/* f32 rows x [B][ldx] -> the weight type's vec_dot_type (Q8_0 for Q4_0/Q8_0, Q8_K for Q4_K): the
+/* f32 rows x [B][ldx] -> the weight type's vec_dot_type (Q8_0 for Q4_0/Q8_0, Q8_K for the K-quants): the
  * src1 conversion ggml-cpu's mul_mat performs (canonical Q8_0 variant: x86 AVX2). */
 GCQ_API int gcq_quantize_act(int wtype, const float * x, int64_t ldx, int64_t B, int64_t K, void * act, void * stream);
 /* A quantized activation in ggml's block bytes (block_q8_0 / block_q8_K), for comparisons. */
@@ -79,9 +82,9 @@ GCQ_API int gcq_act_to_ggml(int wtype, const void * act, int64_t B, int64_t K, v
 
 /* ---- mul_mat -------------------------------------------------------------------------------- */
 /* y[m][n] (row stride ldy) = sum_k W[n][k] x[m][k], x f32 [M][ldx]: ggml_mul_mat(W, x) with W a
- * packed Q4_0 / Q8_0 / Q4_K weight (runtime/src/ops.cpp:107-119 ->
+ * packed Q4_0 / Q8_0 / Q4_K / Q5_K / Q6_K weight (runtime/src/ops.cpp:107-119 ->
  * runtime/include/ggml_compiler_ops.h:116-122). M <= 8: GEMV; M > 8: int8-MFMA GEMM (Q4_0, Q8_0)
- * or GEMV in groups of 8 rows (Q4_K). ws: gcq_mul_mat_workspace bytes, 256-byte aligned. */
+ * or GEMV in groups of 8 rows (K-quants). ws: gcq_mul_mat_workspace bytes, 256-byte aligned. */
 GCQ_API int gcq_mul_mat(int wtype, const void * w, int64_t N, int64_t K, const float * x, int64_t ldx, int64_t M,
                         float * y, int64_t ldy, void * ws, size_t ws_size, void * stream);
 /* The same with the activation already quantized (gcq_quantize_act, gcq_rms_norm_q8,
@@ -89,8 +92,9 @@ GCQ_API int gcq_mul_mat(int wtype, const void * w, int64_t N, int64_t K, const f
  * a residual that follows the mul_mat, fused. */
 GCQ_API int gcq_mul_mat_q(int wtype, const void * w, int64_t N, int64_t K, const void * act, int64_t M, float * y,
                           int64_t ldy, const float * res, void * stream);
-/* The GEMV kernels' exact int32 block dot sums: out[b][n][blk] (Q4_0/Q8_0) or
- * out[b][n][superblock][10] (Q4_K: 8 sub-block dots, sum sc*dot, sum m*bsums). B <= 8. */
+/* The GEMV kernels' exact int32 block dot sums: out[b][n][blk] (Q4_0/Q8_0),
+ * out[b][n][superblock][10] (Q4_K, Q5_K: 8 sub-block dots, sum sc*dot, sum m*bsums) or
+ * out[b][n][superblock][17] (Q6_K: 16 sub-block sums of (q - 32) * x, sum sc * those). B <= 8. */
 GCQ_API int gcq_block_isums(int wtype, const void * w, int64_t N, int64_t K, const void * act, int64_t B,
                             int32_t * out, void * stream);
 /* The GEMM's (MFMA) int32 sums of K-block blk: out[m][n]. */

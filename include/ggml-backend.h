@@ -9,7 +9,7 @@
  * site's graph with ggml_backend_graph_compute (:356-374), asking ggml_backend_supports_op before
  * choosing flash attention (runtime/src/ops.cpp:228-240). Same names, arguments and status values.
  *
- * Quantized weights: a Q4_0 / Q8_0 / Q4_K tensor allocated here holds the layout the kernels read
+ * Quantized weights: a Q4_0 / Q8_0 / Q4_K / Q5_K / Q6_K tensor allocated here holds the layout the kernels read
  * (gcq_pack_weights), which takes a few bytes more than ggml_nbytes. ggml_backend_tensor_set and
  * _get convert whole tensors to and from ggml's block bytes (offset 0, size ggml_nbytes); a partial
  * range of a quantized tensor is an error.

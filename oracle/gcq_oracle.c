@@ -14,9 +14,9 @@
  * Parity pins (tests/test_oracle.py): fp16 against numpy's IEEE conversion; encoders against
  * hand-worked blocks, on-grid round trips (the tests/unit/test_modelopt.py:60-72 pattern) and
  * error invariants; integer block sums against int64 brute force; mul_mat / rms_norm / rope /
- * flash_attn against float64 closed forms. The Q4_K encoder's exact bytes (make_qkx2_quants
- * search) and ggml's float summation order are parity unpinned: no ggml build exists to compare
- * against.
+ * flash_attn against float64 closed forms. The K-quant encoders' exact bytes (the
+ * make_qkx2_quants / make_qx_quants searches) and ggml's float summation order are parity
+ * unpinned: no ggml build exists to compare against.
  */
 #include "gcq_oracle.h"
 
@@ -34,11 +34,15 @@
 typedef struct { uint16_t d; int8_t qs[QK32]; } blk_q8_0;                       /* 34 B */
 typedef struct { uint16_t d; uint8_t qs[QK32 / 2]; } blk_q4_0;                  /* 18 B */
 typedef struct { uint16_t d, dmin; uint8_t scales[12]; uint8_t qs[QKK / 2]; } blk_q4_K;  /* 144 B */
+typedef struct { uint16_t d, dmin; uint8_t scales[12]; uint8_t qh[QKK / 8]; uint8_t qs[QKK / 2]; } blk_q5_K; /* 176 B */
+typedef struct { uint8_t ql[QKK / 2]; uint8_t qh[QKK / 4]; int8_t scales[QKK / 16]; uint16_t d; } blk_q6_K; /* 210 B */
 typedef struct { float d; int8_t qs[QKK]; int16_t bsums[QKK / 16]; } blk_q8_K; /* 292 B */
 
 _Static_assert(sizeof(blk_q8_0) == 34, "q8_0 block");
 _Static_assert(sizeof(blk_q4_0) == 18, "q4_0 block");
 _Static_assert(sizeof(blk_q4_K) == 144, "q4_K block");
+_Static_assert(sizeof(blk_q5_K) == 176, "q5_K block");
+_Static_assert(sizeof(blk_q6_K) == 210, "q6_K block");
 _Static_assert(sizeof(blk_q8_K) == 292, "q8_K block");
 
 static int nthreads_of(int n) {
@@ -146,7 +150,7 @@ size_t orc_block_size(int type) {
     switch (type) {
         case ORC_F32: case ORC_F16: return 1;
         case ORC_Q4_0: case ORC_Q8_0: return QK32;
-        case ORC_Q4_K: case ORC_Q8_K: return QKK;
+        case ORC_Q4_K: case ORC_Q5_K: case ORC_Q6_K: case ORC_Q8_K: return QKK;
         default: return 0;
     }
 }
@@ -158,6 +162,8 @@ size_t orc_type_size(int type) {
         case ORC_Q4_0: return sizeof(blk_q4_0);
         case ORC_Q8_0: return sizeof(blk_q8_0);
         case ORC_Q4_K: return sizeof(blk_q4_K);
+        case ORC_Q5_K: return sizeof(blk_q5_K);
+        case ORC_Q6_K: return sizeof(blk_q6_K);
         case ORC_Q8_K: return sizeof(blk_q8_K);
         default: return 0;
     }
@@ -208,11 +214,12 @@ static void enc_q4_0(const float * x, blk_q4_0 * y, int64_t nb) {
 /* ggml nearest_int: round to nearest, ties to even, for |v| < 2^22. */
 static inline int nearest_int(float v) { return (int) lrintf(v); }
 
-/* ggml make_qkx2_quants(n=32, nmax=15, rmin=-1, rdelta=0.1, nstep=20, use_mad=false): an
- * asymmetric (scale, min) fit by weighted least squares over 21 candidate scales. */
-static float make_qkx2(const float * x, const float * w, uint8_t * L, float * the_min) {
-    const int n = 32, nmax = 15, nstep = 20;
-    const float rmin = -1.0f, rdelta = 0.1f;
+/* ggml make_qkx2_quants(n=32, nmax, rmin, rdelta=0.1, nstep, use_mad=false): an asymmetric
+ * (scale, min) fit by weighted least squares over nstep + 1 candidate scales. Q4_K calls it with
+ * (nmax 15, rmin -1, nstep 20), Q5_K with (31, -0.5, 15). */
+static float make_qkx2(const float * x, const float * w, uint8_t * L, float * the_min, int nmax, float rmin, int nstep) {
+    const int n = 32;
+    const float rdelta = 0.1f;
     uint8_t Laux[32];
     float min = x[0], max = x[0];
     float sum_w = w[0];
@@ -288,6 +295,31 @@ static inline void scale_min_k4(int j, const uint8_t * q, uint8_t * sc, uint8_t 
     }
 }
 
+/* The 6-bit (scale, min) pairs of a Q4_K / Q5_K super-block against its largest scale and min,
+ * and the fp16 (d, dmin) they are relative to (quantize_row_q4_K_ref / q5_K_ref). */
+static void pack_scale_min_k4(const float * scales, const float * mins, float max_scale, float max_min,
+                              uint8_t sb[12], uint16_t * d, uint16_t * dmin) {
+    const float inv_scale = max_scale > 0 ? 63.f / max_scale : 0.f;
+    const float inv_min = max_min > 0 ? 63.f / max_min : 0.f;
+    memset(sb, 0, 12);
+    for (int j = 0; j < 8; j++) {
+        int ls = nearest_int(inv_scale * scales[j]);
+        int lm = nearest_int(inv_min * mins[j]);
+        ls = ls > 63 ? 63 : ls;
+        lm = lm > 63 ? 63 : lm;
+        if (j < 4) {
+            sb[j] = (uint8_t) ls;
+            sb[j + 4] = (uint8_t) lm;
+        } else {
+            sb[j + 4] = (uint8_t) ((ls & 0xF) | ((lm & 0xF) << 4));
+            sb[j - 4] |= (uint8_t) ((ls >> 4) << 6);
+            sb[j] |= (uint8_t) ((lm >> 4) << 6);
+        }
+    }
+    *d = orc_fp32_to_fp16(max_scale / 63.f);
+    *dmin = orc_fp32_to_fp16(max_min / 63.f);
+}
+
 /* ggml quantize_row_q4_K_ref: per 32-sub-block make_qkx2 fit with weights sqrt(mean x^2) + |x|,
  * then 6-bit scales/mins relative to the super-block's max scale and max min, then codes
  * recomputed against the rounded scales. */
@@ -301,29 +333,11 @@ static void enc_q4_K(const float * x, blk_q4_K * y, int64_t nb) {
             for (int l = 0; l < 32; l++) sum_x2 += x[32 * j + l] * x[32 * j + l];
             const float av_x = sqrtf(sum_x2 / 32);
             for (int l = 0; l < 32; l++) weights[l] = av_x + fabsf(x[32 * j + l]);
-            scales[j] = make_qkx2(x + 32 * j, weights, L + 32 * j, &mins[j]);
+            scales[j] = make_qkx2(x + 32 * j, weights, L + 32 * j, &mins[j], 15, -1.0f, 20);
             if (scales[j] > max_scale) max_scale = scales[j];
             if (mins[j] > max_min) max_min = mins[j];
         }
-        const float inv_scale = max_scale > 0 ? 63.f / max_scale : 0.f;
-        const float inv_min = max_min > 0 ? 63.f / max_min : 0.f;
-        memset(y[i].scales, 0, 12);
-        for (int j = 0; j < 8; j++) {
-            int ls = nearest_int(inv_scale * scales[j]);
-            int lm = nearest_int(inv_min * mins[j]);
-            ls = ls > 63 ? 63 : ls;
-            lm = lm > 63 ? 63 : lm;
-            if (j < 4) {
-                y[i].scales[j] = (uint8_t) ls;
-                y[i].scales[j + 4] = (uint8_t) lm;
-            } else {
-                y[i].scales[j + 4] = (uint8_t) ((ls & 0xF) | ((lm & 0xF) << 4));
-                y[i].scales[j - 4] |= (uint8_t) ((ls >> 4) << 6);
-                y[i].scales[j] |= (uint8_t) ((lm >> 4) << 6);
-            }
-        }
-        y[i].d = orc_fp32_to_fp16(max_scale / 63.f);
-        y[i].dmin = orc_fp32_to_fp16(max_min / 63.f);
+        pack_scale_min_k4(scales, mins, max_scale, max_min, y[i].scales, &y[i].d, &y[i].dmin);
         for (int j = 0; j < 8; j++) {
             uint8_t sc, m;
             scale_min_k4(j, y[i].scales, &sc, &m);
@@ -341,6 +355,154 @@ static void enc_q4_K(const float * x, blk_q4_K * y, int64_t nb) {
     }
 }
 
+/* ggml quantize_row_q5_K_ref: the Q4_K scheme with 5-bit codes (make_qkx2 with nmax 31, rmin
+ * -0.5, 15 steps); the fifth bit of value 64c + l (l < 32) goes to bit 2c of qh[l], that of value
+ * 64c + 32 + l to bit 2c + 1. */
+static void enc_q5_K(const float * x, blk_q5_K * y, int64_t nb) {
+    uint8_t L[QKK];
+    float weights[32], mins[8], scales[8];
+    for (int64_t i = 0; i < nb; i++, x += QKK) {
+        float max_scale = 0, max_min = 0;
+        for (int j = 0; j < 8; j++) {
+            float sum_x2 = 0;
+            for (int l = 0; l < 32; l++) sum_x2 += x[32 * j + l] * x[32 * j + l];
+            const float av_x = sqrtf(sum_x2 / 32);
+            for (int l = 0; l < 32; l++) weights[l] = av_x + fabsf(x[32 * j + l]);
+            scales[j] = make_qkx2(x + 32 * j, weights, L + 32 * j, &mins[j], 31, -0.5f, 15);
+            if (scales[j] > max_scale) max_scale = scales[j];
+            if (mins[j] > max_min) max_min = mins[j];
+        }
+        pack_scale_min_k4(scales, mins, max_scale, max_min, y[i].scales, &y[i].d, &y[i].dmin);
+        for (int j = 0; j < 8; j++) {
+            uint8_t sc, m;
+            scale_min_k4(j, y[i].scales, &sc, &m);
+            const float d = orc_fp16_to_fp32(y[i].d) * sc;
+            if (d == 0.0f) continue;
+            const float dm = orc_fp16_to_fp32(y[i].dmin) * m;
+            for (int l = 0; l < 32; l++) {
+                int q = nearest_int((x[32 * j + l] + dm) / d);
+                L[32 * j + l] = (uint8_t) (q < 0 ? 0 : (q > 31 ? 31 : q));
+            }
+        }
+        memset(y[i].qh, 0, sizeof(y[i].qh));
+        for (int c = 0; c < 4; c++) {
+            for (int l = 0; l < 32; l++) {
+                int l1 = L[64 * c + l], l2 = L[64 * c + 32 + l];
+                if (l1 > 15) {
+                    l1 -= 16;
+                    y[i].qh[l] |= (uint8_t) (1u << (2 * c));
+                }
+                if (l2 > 15) {
+                    l2 -= 16;
+                    y[i].qh[l] |= (uint8_t) (2u << (2 * c));
+                }
+                y[i].qs[32 * c + l] = (uint8_t) (l1 | (l2 << 4));
+            }
+        }
+    }
+}
+
+/* ggml make_qx_quants(n = 16, nmax = 32, rmse_type = 1, no importance weights): the symmetric scale
+ * of a 16-value sub-block, codes L = l + 32 with l in [-32, 31], the first scale -32/max refined
+ * over 18 candidates -(32 + 0.1 is)/max (is = -9..9, not 0) by the x^2-weighted fit. */
+static float make_qx16(const float * x, uint8_t * L) {
+    const int n = 16, nmax = 32;
+    float max = 0, amax = 0;
+    for (int i = 0; i < n; i++) {
+        const float ax = fabsf(x[i]);
+        if (ax > amax) {
+            amax = ax;
+            max = x[i];
+        }
+    }
+    if (amax < 1e-15f) { /* GROUP_MAX_EPS */
+        memset(L, 0, (size_t) n);
+        return 0.f;
+    }
+    float iscale = -nmax / max;
+    float sumlx = 0, suml2 = 0;
+    for (int i = 0; i < n; i++) {
+        int l = nearest_int(iscale * x[i]);
+        l = l < -nmax ? -nmax : (l > nmax - 1 ? nmax - 1 : l);
+        L[i] = (uint8_t) (l + nmax);
+        const float w = x[i] * x[i];
+        sumlx += w * x[i] * l;
+        suml2 += w * l * l;
+    }
+    float scale = suml2 != 0.0f ? sumlx / suml2 : 0.0f;
+    float best = scale * sumlx;
+    for (int is = -9; is <= 9; is++) {
+        if (is == 0) continue;
+        iscale = -(nmax + 0.1f * is) / max;
+        sumlx = suml2 = 0;
+        for (int i = 0; i < n; i++) {
+            int l = nearest_int(iscale * x[i]);
+            l = l < -nmax ? -nmax : (l > nmax - 1 ? nmax - 1 : l);
+            const float w = x[i] * x[i];
+            sumlx += w * x[i] * l;
+            suml2 += w * l * l;
+        }
+        if (suml2 > 0 && sumlx * sumlx > best * suml2) {
+            for (int i = 0; i < n; i++) {
+                int l = nearest_int(iscale * x[i]);
+                L[i] = (uint8_t) (nmax + (l < -nmax ? -nmax : (l > nmax - 1 ? nmax - 1 : l)));
+            }
+            scale = sumlx / suml2;
+            best = scale * sumlx;
+        }
+    }
+    return scale;
+}
+
+/* ggml quantize_row_q6_K_ref: 16 sub-block fits (make_qx16), int8 scales against the scale of
+ * largest magnitude (iscale = -128/max, d = 1/iscale), codes recomputed against the rounded
+ * scales, then 4 low bits to ql and 2 high bits to qh in ggml's interleaved order. */
+static void enc_q6_K(const float * x, blk_q6_K * y, int64_t nb) {
+    uint8_t L[QKK];
+    float scales[16];
+    for (int64_t i = 0; i < nb; i++, x += QKK) {
+        float max_scale = 0, max_abs_scale = 0;
+        for (int ib = 0; ib < 16; ib++) {
+            const float sc = make_qx16(x + 16 * ib, L + 16 * ib);
+            scales[ib] = sc;
+            if (fabsf(sc) > max_abs_scale) {
+                max_abs_scale = fabsf(sc);
+                max_scale = sc;
+            }
+        }
+        if (max_abs_scale < 1e-15f) {
+            memset(&y[i], 0, sizeof(blk_q6_K));
+            continue;
+        }
+        const float iscale = -128.f / max_scale;
+        y[i].d = orc_fp32_to_fp16(1 / iscale);
+        for (int ib = 0; ib < 16; ib++) {
+            const int v = nearest_int(iscale * scales[ib]);
+            y[i].scales[ib] = (int8_t) (v < 127 ? v : 127);
+        }
+        for (int j = 0; j < 16; j++) {
+            const float d = orc_fp16_to_fp32(y[i].d) * y[i].scales[j];
+            if (d == 0.0f) continue;
+            for (int ii = 0; ii < 16; ii++) {
+                int l = nearest_int(x[16 * j + ii] / d);
+                l = l < -32 ? -32 : (l > 31 ? 31 : l);
+                L[16 * j + ii] = (uint8_t) (l + 32);
+            }
+        }
+        for (int h = 0; h < 2; h++) {
+            const uint8_t * Lh = L + 128 * h;
+            uint8_t * ql = y[i].ql + 64 * h;
+            uint8_t * qh = y[i].qh + 32 * h;
+            for (int l = 0; l < 32; l++) {
+                ql[l] = (uint8_t) ((Lh[l] & 0xF) | ((Lh[l + 64] & 0xF) << 4));
+                ql[l + 32] = (uint8_t) ((Lh[l + 32] & 0xF) | ((Lh[l + 96] & 0xF) << 4));
+                qh[l] = (uint8_t) ((Lh[l] >> 4) | ((Lh[l + 32] >> 4) << 2) | ((Lh[l + 64] >> 4) << 4) |
+                                   ((Lh[l + 96] >> 4) << 6));
+            }
+        }
+    }
+}
+
 size_t orc_quantize(int type, const float * src, int64_t nrows, int64_t n_per_row, void * dst) {
     const size_t rs = orc_row_size(type, n_per_row);
     if (!rs || nrows < 0) return 0;
@@ -353,6 +515,8 @@ size_t orc_quantize(int type, const float * src, int64_t nrows, int64_t n_per_ro
             case ORC_Q8_0: enc_q8_0(x, (blk_q8_0 *) y, nb); break;
             case ORC_Q4_0: enc_q4_0(x, (blk_q4_0 *) y, nb); break;
             case ORC_Q4_K: enc_q4_K(x, (blk_q4_K *) y, nb); break;
+            case ORC_Q5_K: enc_q5_K(x, (blk_q5_K *) y, nb); break;
+            case ORC_Q6_K: enc_q6_K(x, (blk_q6_K *) y, nb); break;
             case ORC_F16: orc_fp32_to_fp16_n(x, (uint16_t *) y, n_per_row); break;
             case ORC_F32: memcpy(y, x, rs); break;
             default: break;
@@ -418,7 +582,7 @@ void orc_quantize_act_q8_K(const float * x, void * yv, int64_t k) {
 
 /* ------------------------------------------------------------------------------ dequant */
 
-/* ggml dequantize_row_q8_0 / q4_0 / q4_K. */
+/* ggml dequantize_row_q8_0 / q4_0 / q4_K / q5_K / q6_K. */
 int orc_dequantize(int type, const void * src, float * dst, int64_t nrows, int64_t n_per_row) {
     const size_t rs = orc_row_size(type, n_per_row);
     if (!rs) return -1;
@@ -454,6 +618,46 @@ int orc_dequantize(int type, const void * src, float * dst, int64_t nrows, int64
                     const float d2 = d * sc, m2 = dmin * m;
                     for (int l = 0; l < 32; l++) o[64 * c + l] = d1 * (q[32 * c + l] & 0xF) - m1;
                     for (int l = 0; l < 32; l++) o[64 * c + 32 + l] = d2 * (q[32 * c + l] >> 4) - m2;
+                }
+            }
+        } else if (type == ORC_Q5_K) {
+            const blk_q5_K * b = (const blk_q5_K *) row;
+            for (int64_t i = 0; i < n_per_row / QKK; i++) {
+                const float d = orc_fp16_to_fp32(b[i].d), dmin = orc_fp16_to_fp32(b[i].dmin);
+                float * o = y + i * QKK;
+                for (int c = 0; c < 4; c++) {
+                    uint8_t sc, m;
+                    scale_min_k4(2 * c, b[i].scales, &sc, &m);
+                    const float d1 = d * sc, m1 = dmin * m;
+                    scale_min_k4(2 * c + 1, b[i].scales, &sc, &m);
+                    const float d2 = d * sc, m2 = dmin * m;
+                    const uint8_t * q = b[i].qs + 32 * c;
+                    for (int l = 0; l < 32; l++)
+                        o[64 * c + l] = d1 * ((q[l] & 0xF) + (b[i].qh[l] & (1u << (2 * c)) ? 16 : 0)) - m1;
+                    for (int l = 0; l < 32; l++)
+                        o[64 * c + 32 + l] = d2 * ((q[l] >> 4) + (b[i].qh[l] & (2u << (2 * c)) ? 16 : 0)) - m2;
+                }
+            }
+        } else if (type == ORC_Q6_K) {
+            const blk_q6_K * b = (const blk_q6_K *) row;
+            for (int64_t i = 0; i < n_per_row / QKK; i++) {
+                const float d = orc_fp16_to_fp32(b[i].d);
+                for (int h = 0; h < 2; h++) {
+                    const uint8_t * ql = b[i].ql + 64 * h;
+                    const uint8_t * qh = b[i].qh + 32 * h;
+                    const int8_t * sc = b[i].scales + 8 * h;
+                    float * o = y + i * QKK + 128 * h;
+                    for (int l = 0; l < 32; l++) {
+                        const int is = l / 16;
+                        const int q1 = (int) ((ql[l] & 0xF) | (((qh[l] >> 0) & 3) << 4)) - 32;
+                        const int q2 = (int) ((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32;
+                        const int q3 = (int) ((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+                        const int q4 = (int) ((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+                        o[l] = d * sc[is + 0] * q1;
+                        o[l + 32] = d * sc[is + 2] * q2;
+                        o[l + 64] = d * sc[is + 4] * q3;
+                        o[l + 96] = d * sc[is + 6] * q4;
+                    }
                 }
             }
         } else if (type == ORC_F16) {
@@ -505,6 +709,46 @@ static inline void isum_q4_K(const blk_q4_K * w, const blk_q8_K * x, int32_t dot
     }
 }
 
+/* ggml vec_dot_q5_K_q8_K integer parts: as Q4_K with q = nibble + 16 * (its qh bit). */
+static inline void isum_q5_K(const blk_q5_K * w, const blk_q8_K * x, int32_t dot[8], int32_t * isc, int32_t * imin) {
+    *isc = 0;
+    *imin = 0;
+    for (int j = 0; j < 8; j++) {
+        const int c = j / 2, hi = j & 1;
+        int32_t s = 0;
+        for (int l = 0; l < 32; l++) {
+            const int nib = hi ? (w->qs[32 * c + l] >> 4) : (w->qs[32 * c + l] & 0xF);
+            const int q = nib + ((w->qh[l] >> j) & 1) * 16;
+            s += q * x->qs[32 * j + l];
+        }
+        uint8_t sc, m;
+        scale_min_k4(j, w->scales, &sc, &m);
+        dot[j] = s;
+        *isc += sc * s;
+        *imin += m * (x->bsums[2 * j] + x->bsums[2 * j + 1]);
+    }
+}
+
+/* ggml vec_dot_q6_K_q8_K integer parts: sub[j] = sum over 16-value sub-block j of (q - 32) * q8,
+ * total = sum_j scales[j] * sub[j]. The 6-bit code of value v (half h = v / 128, r = v % 128,
+ * l = r % 32, part p = r / 32) is ql[64h + 32(p & 1) + l] (low nibble for p < 2, high for
+ * p >= 2) | ((qh[32h + l] >> 2p) & 3) << 4. */
+static inline void isum_q6_K(const blk_q6_K * w, const blk_q8_K * x, int32_t sub[16], int32_t * total) {
+    *total = 0;
+    for (int j = 0; j < 16; j++) {
+        int32_t s = 0;
+        for (int t = 0; t < 16; t++) {
+            const int v = 16 * j + t, h = v / 128, r = v % 128, p = r / 32, l = r % 32;
+            const uint8_t b = w->ql[64 * h + 32 * (p & 1) + l];
+            const int lo4 = p < 2 ? (b & 0xF) : (b >> 4);
+            const int q = lo4 | (((w->qh[32 * h + l] >> (2 * p)) & 3) << 4);
+            s += (q - 32) * x->qs[v];
+        }
+        sub[j] = s;
+        *total += w->scales[j] * s;
+    }
+}
+
 int64_t orc_block_isums(int type, const void * w_row, const void * xq_row, int64_t k, int32_t * out) {
     if (type == ORC_Q4_0 || type == ORC_Q8_0) {
         const int64_t nb = k / QK32;
@@ -515,13 +759,23 @@ int64_t orc_block_isums(int type, const void * w_row, const void * xq_row, int64
         }
         return nb;
     }
-    if (type == ORC_Q4_K) {
+    if (type == ORC_Q4_K || type == ORC_Q5_K) {
         const int64_t nb = k / QKK;
         for (int64_t i = 0; i < nb; i++) {
-            isum_q4_K((const blk_q4_K *) w_row + i, (const blk_q8_K *) xq_row + i, out + 10 * i, out + 10 * i + 8,
-                      out + 10 * i + 9);
+            if (type == ORC_Q4_K)
+                isum_q4_K((const blk_q4_K *) w_row + i, (const blk_q8_K *) xq_row + i, out + 10 * i, out + 10 * i + 8,
+                          out + 10 * i + 9);
+            else
+                isum_q5_K((const blk_q5_K *) w_row + i, (const blk_q8_K *) xq_row + i, out + 10 * i, out + 10 * i + 8,
+                          out + 10 * i + 9);
         }
         return 10 * nb;
+    }
+    if (type == ORC_Q6_K) {
+        const int64_t nb = k / QKK;
+        for (int64_t i = 0; i < nb; i++)
+            isum_q6_K((const blk_q6_K *) w_row + i, (const blk_q8_K *) xq_row + i, out + 17 * i, out + 17 * i + 16);
+        return 17 * nb;
     }
     return 0;
 }
@@ -530,13 +784,14 @@ int64_t orc_block_isums(int type, const void * w_row, const void * xq_row, int64
 
 /* ggml_compute_forward_mul_mat for a quantized src0 and f32 src1 (runtime/src/ops.cpp:107-119):
  * src1 rows converted to the vec_dot_type, then per output the block dot with the fp32
- * epilogue sumf += isum * d_w * d_x (Q4_K: d*isc - dmin*imin with d = fp16(d_w)*d_x). */
+ * epilogue sumf += isum * d_w * d_x (Q4_K, Q5_K: d*isc - dmin*imin with d = fp16(d_w)*d_x; Q6_K:
+ * (fp16(d_w)*d_x) * sum_j sc_j*sub_j). */
 int orc_mul_mat(int type, const void * w, int64_t N, int64_t K, const float * x, int64_t M, float * y,
                 int n_threads) {
     const size_t wrs = orc_row_size(type, K);
-    if (!wrs || (type != ORC_Q4_0 && type != ORC_Q8_0 && type != ORC_Q4_K && type != ORC_F16 && type != ORC_F32))
-        return -1;
-    const int xtype = type == ORC_Q4_K ? ORC_Q8_K : (type == ORC_F16 || type == ORC_F32 ? ORC_F32 : ORC_Q8_0);
+    const int kq = type == ORC_Q4_K || type == ORC_Q5_K || type == ORC_Q6_K;
+    if (!wrs || (type != ORC_Q4_0 && type != ORC_Q8_0 && !kq && type != ORC_F16 && type != ORC_F32)) return -1;
+    const int xtype = kq ? ORC_Q8_K : (type == ORC_F16 || type == ORC_F32 ? ORC_F32 : ORC_Q8_0);
     const size_t xrs = orc_row_size(xtype, K);
     uint8_t * xq = (uint8_t *) malloc(xrs * (size_t) M);
     if (!xq) return -1;
@@ -571,6 +826,24 @@ int orc_mul_mat(int type, const void * w, int64_t N, int64_t K, const float * x,
                     const float d = orc_fp16_to_fp32(wb[i].d) * xb[i].d;
                     const float dmin = orc_fp16_to_fp32(wb[i].dmin) * xb[i].d;
                     sumf += d * (float) isc - dmin * (float) imin;
+                }
+            } else if (type == ORC_Q5_K) {
+                const blk_q5_K * wb = (const blk_q5_K *) wr;
+                const blk_q8_K * xb = (const blk_q8_K *) xr;
+                for (int64_t i = 0; i < K / QKK; i++) {
+                    int32_t dot[8], isc, imin;
+                    isum_q5_K(wb + i, xb + i, dot, &isc, &imin);
+                    const float d = orc_fp16_to_fp32(wb[i].d) * xb[i].d;
+                    const float dmin = orc_fp16_to_fp32(wb[i].dmin) * xb[i].d;
+                    sumf += d * (float) isc - dmin * (float) imin;
+                }
+            } else if (type == ORC_Q6_K) {
+                const blk_q6_K * wb = (const blk_q6_K *) wr;
+                const blk_q8_K * xb = (const blk_q8_K *) xr;
+                for (int64_t i = 0; i < K / QKK; i++) {
+                    int32_t sub[16], tot;
+                    isum_q6_K(wb + i, xb + i, sub, &tot);
+                    sumf += (orc_fp16_to_fp32(wb[i].d) * xb[i].d) * (float) tot;
                 }
             } else {
                 const float * xf = (const float *) xr;

@@ -13,7 +13,7 @@
  * algorithms follow ggml's published ggml-quants.c / ggml-cpu semantics as restated per function
  * in gcq_oracle.c.
  *
- * Type ids are GGUF's: F32=0, F16=1, Q4_0=2, Q8_0=8, Q4_K=12, Q8_K=15.
+ * Type ids are GGUF's: F32=0, F16=1, Q4_0=2, Q8_0=8, Q4_K=12, Q5_K=13, Q6_K=14, Q8_K=15.
  */
 #ifndef GCQ_ORACLE_H
 #define GCQ_ORACLE_H
@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-enum { ORC_F32 = 0, ORC_F16 = 1, ORC_Q4_0 = 2, ORC_Q8_0 = 8, ORC_Q4_K = 12, ORC_Q8_K = 15 };
+enum { ORC_F32 = 0, ORC_F16 = 1, ORC_Q4_0 = 2, ORC_Q8_0 = 8, ORC_Q4_K = 12, ORC_Q5_K = 13, ORC_Q6_K = 14, ORC_Q8_K = 15 };
 
 /* Activation (vec_dot_type) Q8_0 quantizer variants. */
 enum { ORC_ACT_Q8_0_AVX2 = 0, ORC_ACT_Q8_0_SCALAR = 1 };
@@ -49,17 +49,19 @@ size_t orc_quantize(int type, const float * src, int64_t nrows, int64_t n_per_ro
 /* Activation quantizers: Q8_0 (variant ORC_ACT_*) or Q8_K, k values. */
 void   orc_quantize_act_q8_0(const float * x, void * y, int64_t k, int variant);
 void   orc_quantize_act_q8_K(const float * x, void * y, int64_t k);
-/* Dequantize whole rows of a weight type (Q8_0, Q4_0, Q4_K, F16, F32) to f32. */
+/* Dequantize whole rows of a weight type (Q8_0, Q4_0, Q4_K, Q5_K, Q6_K, F16, F32) to f32. */
 int    orc_dequantize(int type, const void * src, float * dst, int64_t nrows, int64_t n_per_row);
 
 /* Integer block dot sums of one weight row against one quantized activation row.
  * Q4_0, Q8_0 (activation Q8_0): one int32 per 32-block.
- * Q4_K (activation Q8_K): per 256-superblock 10 int32: the 8 sub-block sums sum_l q4*q8,
- * then sum_j sc_j*dot_j, then sum_j m_j*(bsums[2j]+bsums[2j+1]). Returns the count written. */
+ * Q4_K, Q5_K (activation Q8_K): per 256-superblock 10 int32: the 8 sub-block sums sum_l q*q8,
+ * then sum_j sc_j*dot_j, then sum_j m_j*(bsums[2j]+bsums[2j+1]).
+ * Q6_K (activation Q8_K): per 256-superblock 17 int32: the 16 sub-block sums sum_l (q-32)*q8,
+ * then sum_j sc_j*those. Returns the count written. */
 int64_t orc_block_isums(int type, const void * w_row, const void * xq_row, int64_t k, int32_t * out);
 
 /* y[m, n] = sum_k w[n, k] * x[m, k]: w is N rows of a weight type in ggml layout, x f32 [M, K]
- * quantized to the weight's vec_dot type first (Q8_0 canonical variant, or Q8_K). */
+ * quantized to the weight's vec_dot type first (Q8_0 canonical variant, or Q8_K for the K-quants). */
 int orc_mul_mat(int type, const void * w, int64_t N, int64_t K, const float * x, int64_t M, float * y,
                 int n_threads);
 

@@ -17,8 +17,10 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 LIB = HERE / "lib" / "libgcq_oracle.so"
 
-F32, F16, Q4_0, Q8_0, Q4_K, Q8_K = 0, 1, 2, 8, 12, 15
-TYPES = {"f32": F32, "f16": F16, "q4_0": Q4_0, "q8_0": Q8_0, "q4_K": Q4_K, "q4_k": Q4_K, "q8_K": Q8_K}
+F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, Q8_K = 0, 1, 2, 8, 12, 13, 14, 15
+TYPES = {"f32": F32, "f16": F16, "q4_0": Q4_0, "q8_0": Q8_0, "q4_K": Q4_K, "q4_k": Q4_K, "q5_K": Q5_K,
+         "q5_k": Q5_K, "q6_K": Q6_K, "q6_k": Q6_K, "q8_K": Q8_K}
+KQUANTS = (Q4_K, Q5_K, Q6_K)
 ACT_AVX2, ACT_SCALAR = 0, 1
 
 _lib: ctypes.CDLL | None = None
@@ -153,7 +155,7 @@ def dequantize(q: np.ndarray, t: int | str, n: int) -> np.ndarray:
 
 def block_isums(t: int | str, w_row: np.ndarray, xq_row: np.ndarray, k: int) -> np.ndarray:
     t = _tid(t)
-    n = k // 32 if t in (Q4_0, Q8_0) else 10 * (k // 256)
+    n = k // 32 if t in (Q4_0, Q8_0) else (17 if t == Q6_K else 10) * (k // 256)
     out = np.empty(n, np.int32)
     w_row, xq_row = _c(w_row, np.uint8), _c(xq_row, np.uint8)
     lib().orc_block_isums(t, w_row.ctypes.data, xq_row.ctypes.data, k, out.ctypes.data)

@@ -80,11 +80,11 @@ def _weight(orc, t, N, K, seed):
 
 # ------------------------------------------------------------------------------- mul_mat
 
-@pytest.mark.parametrize("t", ["q4_0", "q8_0", "q4_K"])
+@pytest.mark.parametrize("t", ["q4_0", "q8_0", "q4_K", "q5_K", "q6_K"])
 @pytest.mark.parametrize("M", [1, 3, 16])
 def test_mul_mat_node(be, gops, orc, t, M):
     """The mul_mat node against the oracle, and bit-exact against gcq_mul_mat (the same kernels:
-    decode-row GEMV, GEMV, MFMA GEMM or Q4_K row groups)."""
+    decode-row GEMV, GEMV, MFMA GEMM or K-quant row groups); the weight's ggml bytes read back."""
     N, K = 300, 1024
     tid = orc.TYPES[t]
     raw = _weight(orc, t, N, K, 40 + M)
@@ -92,7 +92,9 @@ def test_mul_mat_node(be, gops, orc, t, M):
     gr = Graph(be, {"w": (tid, [K, N], raw), "x": (G.F32, [K, M], x)},
                lambda g, ctx, L: g.ggml_mul_mat(ctx, L["w"], L["x"]))
     y = gr.run().reshape(M, N)
+    back = G.get_data(gr.L["w"], np.uint8)
     gr.close()
+    assert np.array_equal(back.reshape(-1), raw.reshape(-1))  # packed on set, unpacked on get
     assert orc.parity(y, orc.mul_mat(raw, t, x, K)) < TOL
     qw = gops.QuantWeight.from_ggml(torch.from_numpy(raw), t, K)
     assert np.array_equal(y, to_np(gops.mul_mat(qw, torch.from_numpy(x).cuda())))

@@ -17,7 +17,7 @@ def _weight(gops, orc, t, N, K, seed):
     return raw, gops.QuantWeight.from_ggml(torch.from_numpy(raw), t, K)
 
 
-@pytest.mark.parametrize("t", ["q4_0", "q8_0", "q4_K"])
+@pytest.mark.parametrize("t", ["q4_0", "q8_0", "q4_K", "q5_K", "q6_K"])
 @pytest.mark.parametrize("B", [1, 3, 8])
 def test_gemv_block_isums_bit_exact(gops, orc, t, B):
     N, K = 37, 1024
@@ -25,13 +25,13 @@ def test_gemv_block_isums_bit_exact(gops, orc, t, B):
     x = orc.normal((B, K), seed=22)
     act = gops.quantize_act(t, torch.from_numpy(x).cuda())
     got = to_np(gops.block_isums(qw, act, B))
-    xq = orc.quantize_act_q8_K(x) if t == "q4_K" else orc.quantize_act_q8_0(x)
+    xq = orc.quantize_act_q8_K(x) if t in ("q4_K", "q5_K", "q6_K") else orc.quantize_act_q8_0(x)
     for b in range(B):
         for n in range(N):
             assert np.array_equal(got[b, n], orc.block_isums(t, raw[n], xq[b], K)), (b, n)
 
 
-@pytest.mark.parametrize("t", ["q4_0", "q8_0", "q4_K"])
+@pytest.mark.parametrize("t", ["q4_0", "q8_0", "q4_K", "q5_K", "q6_K"])
 @pytest.mark.parametrize("B", list(range(1, 9)))
 def test_gemv_matches_oracle(gops, orc, t, B):
     N, K = 1001, 4096
@@ -41,7 +41,7 @@ def test_gemv_matches_oracle(gops, orc, t, B):
     assert orc.parity(y, orc.mul_mat(raw, t, x, K)) < TOL
 
 
-@pytest.mark.parametrize("t", ["q4_0", "q4_K"])
+@pytest.mark.parametrize("t", ["q4_0", "q4_K", "q5_K", "q6_K"])
 @pytest.mark.parametrize("N,K", [(6144, 4096), (512, 14336), (300, 256), (64, 16384 + 512)])
 def test_gemv_llama_shapes(gops, orc, t, N, K):
     """The decode shapes (fused QKV 4096x6144, down 14336x4096 on a row slice) and K past one pass."""
@@ -88,11 +88,12 @@ def test_gemm_prefill_shape_row_slices(gops, orc):
     assert orc.parity(y[np.ix_(rows, cols)], ref) < TOL
 
 
-def test_q4_K_many_rows_in_groups_of_8(gops, orc):
-    raw, qw = _weight(gops, orc, "q4_K", 100, 512, 33)
+@pytest.mark.parametrize("t", ["q4_K", "q5_K", "q6_K"])
+def test_kquant_many_rows_in_groups_of_8(gops, orc, t):
+    raw, qw = _weight(gops, orc, t, 100, 512, 33)
     x = orc.normal((21, 512), seed=34)
     y = to_np(gops.mul_mat(qw, torch.from_numpy(x).cuda()))
-    assert orc.parity(y, orc.mul_mat(raw, "q4_K", x, 512)) < TOL
+    assert orc.parity(y, orc.mul_mat(raw, t, x, 512)) < TOL
 
 
 def test_gemv_is_linear_at_full_size(gops):

@@ -23,7 +23,7 @@ def test_fill_normal_matches_oracle_stream(gops, orc):
     assert np.array_equal(ids, orc.ids(1000, seed=3, vocab=128256))
 
 
-@pytest.mark.parametrize("t", ["q8_0", "q4_0", "q4_K"])
+@pytest.mark.parametrize("t", ["q8_0", "q4_0", "q4_K", "q5_K", "q6_K"])
 def test_weight_encoders_bit_exact(gops, orc, t):
     w = orc.normal((64, 1024), seed=11, std=0.02)
     w[3] = 0.0                      # zero row
@@ -47,12 +47,12 @@ def test_runtime_quantize_host_api(orc):
     from ggml_compiler_amd import runtime
 
     w = orc.normal((8, 512), seed=5, std=0.02)
-    for t in ("q8_0", "q4_0", "q4_K", "f16"):
+    for t in ("q8_0", "q4_0", "q4_K", "q5_K", "q6_K", "f16"):
         assert np.array_equal(runtime.quantize(w, t), orc.quantize(w, t)), t
     assert runtime.has_backend("hip") and runtime.has_backend("auto") and not runtime.has_backend("cpu")
 
 
-@pytest.mark.parametrize("t", ["q8_0", "q4_0", "q4_K"])
+@pytest.mark.parametrize("t", ["q8_0", "q4_0", "q4_K", "q5_K", "q6_K"])
 def test_pack_dequantize_bit_exact(gops, orc, t):
     w = orc.normal((37, 2048), seed=12, std=0.02)
     raw = orc.quantize(w, t)
@@ -62,7 +62,7 @@ def test_pack_dequantize_bit_exact(gops, orc, t):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
-@pytest.mark.parametrize("wt", ["q4_0", "q4_K"])
+@pytest.mark.parametrize("wt", ["q4_0", "q4_K", "q6_K"])
 @pytest.mark.parametrize("B", [1, 5, 8])
 def test_activation_quantizers_bit_exact(gops, orc, wt, B):
     K = 4096
@@ -72,7 +72,7 @@ def test_activation_quantizers_bit_exact(gops, orc, wt, B):
         x[1, :256] = 0.0  # all-zero blocks
     act = gops.quantize_act(wt, torch.from_numpy(x).cuda())
     got = to_np(gops.act_to_ggml(wt, act, B, K))
-    want = orc.quantize_act_q8_K(x) if wt == "q4_K" else orc.quantize_act_q8_0(x, orc.ACT_AVX2)
+    want = orc.quantize_act_q8_K(x) if wt != "q4_0" else orc.quantize_act_q8_0(x, orc.ACT_AVX2)
     assert np.array_equal(got, want)
 
 
@@ -87,3 +87,4 @@ def test_activation_kats(gops):
         else:
             continue
         assert to_np(got)[0].tobytes().hex() == k["hex"], name
+

@@ -116,7 +116,7 @@ def test_q4_0_on_grid_round_trip(orc):
 # ---------------------------------------------------------------------- encoder invariants
 
 
-@pytest.mark.parametrize("t,bound", [("q8_0", 1e-2), ("q4_0", 0.2), ("q4_K", 0.15)])
+@pytest.mark.parametrize("t,bound", [("q8_0", 1e-2), ("q4_0", 0.2), ("q4_K", 0.15), ("q5_K", 0.08), ("q6_K", 0.04)])
 def test_encoder_error_bounds(orc, t, bound):
     """Random weights decode within the type's error (tests/unit/test_frontend.py:299-304 bounds
     4-bit at 0.15 of max |w|; :311-318 orders q8_0 < 1e-2 < q4_0 < 0.2)."""
@@ -174,6 +174,108 @@ def test_q4_K_encoder_special_blocks(orc):
     assert np.abs(back - pos).max() < 0.1 * pos.max()
 
 
+def test_kquant_row_sizes(orc):
+    """Bytes per 256 values: 144 / 176 / 210 (ggml_compiler/compiler.py:82)."""
+    assert [orc.row_size(t, 512) for t in ("q4_K", "q5_K", "q6_K")] == [288, 352, 420]
+
+
+def test_kquant_error_order(orc):
+    """More bits, less error: q6_K < q5_K < q4_K on the same weights (a misplaced high bit in q5_K
+    or q6_K would break the order)."""
+    w = orc.normal((32, 1024), seed=30, std=0.02)
+    err = [np.abs(orc.dequantize(orc.quantize(w, t), t, 1024) - w).mean() for t in ("q4_K", "q5_K", "q6_K")]
+    assert err[0] > 1.6 * err[1] > 0 and err[1] > 1.6 * err[2] > 0
+
+
+def _pack_scale_min(sc, m):
+    packed = np.zeros(12, np.uint8)
+    for j in range(8):
+        if j < 4:
+            packed[j] = sc[j] | ((sc[j + 4] >> 4) << 6)
+            packed[j + 4] = m[j] | ((m[j + 4] >> 4) << 6)
+        else:
+            packed[j + 4] = (sc[j] & 15) | ((m[j] & 15) << 4)
+    return packed
+
+
+def test_q5_K_layout_closed_form(orc):
+    """A hand-built Q5_K block ({d, dmin, scales[12], qh[32], qs[128]}) decodes as
+    d*sc_j*q - dmin*m_j, q = nibble + 16 * bit: value 64c + l (l < 32) takes the low nibble of
+    qs[32c + l] and bit 2c of qh[l]; value 64c + 32 + l the high nibble and bit 2c + 1."""
+    rng = np.random.default_rng(31)
+    sc, m = rng.integers(0, 64, 8), rng.integers(0, 64, 8)
+    q = rng.integers(0, 32, 256)
+    qs = np.zeros(128, np.uint8)
+    qh = np.zeros(32, np.uint8)
+    for v in range(256):
+        c, r = divmod(v, 64)
+        hi, l = divmod(r, 32)
+        qs[32 * c + l] |= (q[v] & 15) << (4 * hi)
+        qh[l] |= (q[v] >> 4) << (2 * c + hi)
+    d, dmin = np.float16(0.0123), np.float16(0.0456)
+    blk = np.concatenate([np.array([d, dmin], np.float16).view(np.uint8), _pack_scale_min(sc, m), qh, qs])
+    assert blk.size == 176
+    got = orc.dequantize(blk[None], "q5_K", 256)[0].astype(np.float64)
+    sub = np.repeat(np.arange(8), 32)
+    want = np.float32(d) * sc[sub].astype(np.float32) * q - np.float32(dmin) * m[sub].astype(np.float32)
+    np.testing.assert_allclose(got, want, rtol=0, atol=1e-6)
+
+
+def _q6_K_block(q, sc, d):
+    """ggml block_q6_K bytes from 256 codes q in [0, 63] (value = q - 32), 16 int8 scales, fp16 d.
+    Value 128h + 32p + l (h < 2, p < 4, l < 32): low 4 bits in ql[64h + 32(p % 2) + l] (low nibble
+    for p < 2, high for p >= 2), high 2 bits at bit 2p of qh[32h + l]."""
+    ql = np.zeros(128, np.uint8)
+    qh = np.zeros(64, np.uint8)
+    for v in range(256):
+        h, r = divmod(v, 128)
+        p, l = divmod(r, 32)
+        ql[64 * h + 32 * (p % 2) + l] |= (q[v] & 15) << (4 * (p // 2))
+        qh[32 * h + l] |= (q[v] >> 4) << (2 * p)
+    return np.concatenate([ql, qh, np.asarray(sc, np.int8).view(np.uint8), np.array([d], np.float16).view(np.uint8)])
+
+
+def test_q6_K_layout_closed_form(orc):
+    rng = np.random.default_rng(32)
+    q = rng.integers(0, 64, 256)
+    sc = rng.integers(-128, 128, 16)
+    d = np.float16(0.00731)
+    blk = _q6_K_block(q, sc, d)
+    assert blk.size == 210
+    got = orc.dequantize(blk[None], "q6_K", 256)[0]
+    want = (np.float32(d) * sc[np.arange(256) // 16].astype(np.float32)) * (q - 32).astype(np.float32)
+    assert np.array_equal(got, want.astype(np.float32))
+
+
+def test_q6_K_on_grid_round_trip(orc):
+    """Weights d*sc_j*l with d a power of two, one sub-block scale -128 (the largest magnitude),
+    l in [-31, 31] and one l = -32 per sub-block (its largest |x|): the encoder recovers d, every
+    scale and every code, so the block round-trips exactly and its bytes are the hand-packed ones."""
+    rng = np.random.default_rng(33)
+    d = 2.0 ** -12
+    sc = rng.integers(-127, 128, 16)
+    sc[sc == 0] = 5
+    sc[rng.integers(0, 16)] = -128
+    l = rng.integers(-31, 32, (16, 16))
+    l[np.arange(16), rng.integers(0, 16, 16)] = -32
+    w = (d * sc[:, None] * l).astype(np.float32).reshape(1, 256)
+    qb = orc.quantize(w, "q6_K")
+    assert np.array_equal(qb[0], _q6_K_block((l + 32).reshape(-1), sc, np.float16(d)))
+    assert np.array_equal(orc.dequantize(qb, "q6_K", 256), w)
+
+
+@pytest.mark.parametrize("t", ["q5_K", "q6_K"])
+def test_kquant_encoder_special_blocks(orc, t):
+    z = np.zeros((1, 256), np.float32)
+    assert not orc.quantize(z, t).any()  # an all-zero super-block is all zero bytes
+    x = orc.normal((1, 256), seed=34)
+    x[0, :16] = 0.0  # a zero sub-block inside a live super-block decodes to zeros
+    back = orc.dequantize(orc.quantize(x, t), t, 256)
+    if t == "q6_K":
+        assert not back[0, :16].any()
+    assert np.abs(back - x).max() < 0.1 * np.abs(x).max()
+
+
 def test_act_q8_K_bsums_and_sign(orc):
     x = orc.normal((2, 512), seed=7)
     q = orc.quantize_act_q8_K(x).reshape(-1, 292)
@@ -196,17 +298,28 @@ def _codes(t, wrow, k):
     if t == "q4_0":
         b = wrow.reshape(-1, 18)[:, 2:].astype(np.int64)
         return np.concatenate([(b & 15) - 8, (b >> 4) - 8], axis=1).reshape(-1)
-    b = wrow.reshape(-1, 144)[:, 16:].astype(np.int64).reshape(-1, 4, 32)
-    return np.stack([b & 15, b >> 4], axis=2).reshape(-1)  # chunk c: low 32 then high 32
+    if t == "q4_K":
+        b = wrow.reshape(-1, 144)[:, 16:].astype(np.int64).reshape(-1, 4, 32)
+        return np.stack([b & 15, b >> 4], axis=2).reshape(-1)  # chunk c: low 32 then high 32
+    if t == "q5_K":
+        blk = wrow.reshape(-1, 176).astype(np.int64)
+        qh, b = blk[:, 16:48], blk[:, 48:].reshape(-1, 4, 32)
+        bit = (qh[:, None, None, :] >> (2 * np.arange(4)[None, :, None, None] + np.arange(2)[None, None, :, None])) & 1
+        return (np.stack([b & 15, b >> 4], axis=2) + 16 * bit).reshape(-1)
+    blk = wrow.reshape(-1, 210).astype(np.int64)  # q6_K: codes minus 32
+    ql, qh = blk[:, :128].reshape(-1, 2, 2, 32), blk[:, 128:192].reshape(-1, 2, 32)
+    low = np.stack([ql[:, :, 0] & 15, ql[:, :, 1] & 15, ql[:, :, 0] >> 4, ql[:, :, 1] >> 4], axis=2)  # [sb, h, p, l]
+    high = (qh[:, :, None, :] >> (2 * np.arange(4))[None, None, :, None]) & 3
+    return (low | (high << 4)).reshape(-1) - 32
 
 
-@pytest.mark.parametrize("t", ["q8_0", "q4_0", "q4_K"])
+@pytest.mark.parametrize("t", ["q8_0", "q4_0", "q4_K", "q5_K", "q6_K"])
 def test_block_isums_brute_force(orc, t):
     k = 1024
     w = orc.normal((3, k), seed=8, std=0.02)
     x = orc.normal((k,), seed=9)
     wq = orc.quantize(w, t)
-    if t == "q4_K":
+    if t in ("q4_K", "q5_K", "q6_K"):
         xq = orc.quantize_act_q8_K(x)
         xc = xq.reshape(-1, 292)[:, 4:260].view(np.int8).astype(np.int64).reshape(-1)
         bs = xq.reshape(-1, 292)[:, 260:].copy().view(np.int16).astype(np.int64)
@@ -216,13 +329,20 @@ def test_block_isums_brute_force(orc, t):
     for r in range(3):
         got = orc.block_isums(t, wq[r], xq, k)
         prod = _codes(t, wq[r], k) * xc
-        if t != "q4_K":
+        if t in ("q8_0", "q4_0"):
             assert np.array_equal(got, prod.reshape(-1, 32).sum(1))
+            continue
+        if t == "q6_K":
+            got = got.reshape(-1, 17)
+            subs = prod.reshape(-1, 16, 16).sum(2)
+            sc = wq[r].reshape(-1, 210)[:, 192:208].view(np.int8).astype(np.int64)
+            assert np.array_equal(got[:, :16], subs)
+            assert np.array_equal(got[:, 16], (sc * subs).sum(1))
             continue
         got = got.reshape(-1, 10)
         dots = prod.reshape(-1, 8, 32).sum(2)
         assert np.array_equal(got[:, :8], dots)
-        hdr = wq[r].reshape(-1, 144)[:, 4:16]
+        hdr = wq[r].reshape(-1, 144 if t == "q4_K" else 176)[:, 4:16]
         for b in range(k // 256):
             scm = [_scale_min(hdr[b], j) for j in range(8)]
             assert got[b, 8] == sum(s * dots[b, j] for j, (s, _) in enumerate(scm))
@@ -239,7 +359,7 @@ def _scale_min(p, j):
 # ---------------------------------------------------------------------------- float ops
 
 
-@pytest.mark.parametrize("t", ["q8_0", "q4_0", "q4_K"])
+@pytest.mark.parametrize("t", ["q8_0", "q4_0", "q4_K", "q5_K", "q6_K"])
 def test_mul_mat_closed_form(orc, t):
     """y = x_q . w_q^T in float64 from both dequantized operands; oracle (f32 accumulation)
     within 1e-5 of it, and within quantization error of the unquantized product."""
@@ -249,7 +369,7 @@ def test_mul_mat_closed_form(orc, t):
     wq = orc.quantize(w, t)
     y = orc.mul_mat(wq, t, x, K)
     wd = orc.dequantize(wq, t, K).astype(np.float64)
-    if t == "q4_K":
+    if t in ("q4_K", "q5_K", "q6_K"):
         xq = orc.quantize_act_q8_K(x).reshape(M, -1, 292)
         xd = (xq[:, :, :4].copy().view(np.float32) * xq[:, :, 4:260].view(np.int8)).reshape(M, K)
     else:
