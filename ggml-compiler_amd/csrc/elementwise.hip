@@ -222,6 +222,10 @@ __global__ void k_cpy(const uint8_t * __restrict__ src, int st, uint8_t * __rest
         dof += (r % g.dne[k]) * g.dnb[k];
         r /= g.dne[k];
     }
+    if (st == T_I32) {  // i32 -> i32: the bits
+        *reinterpret_cast<int32_t *>(dst + dof) = *reinterpret_cast<const int32_t *>(src + so);
+        return;
+    }
     const float v = st == T_F32 ? *reinterpret_cast<const float *>(src + so)
                                 : h2f(*reinterpret_cast<const uint16_t *>(src + so));
     if (dt == T_F32) *reinterpret_cast<float *>(dst + dof) = v;

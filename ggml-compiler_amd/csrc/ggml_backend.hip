@@ -380,8 +380,7 @@ struct ggml_backend {
 
 struct ggml_gallocr {
     ggml_backend * be = nullptr;
-    ggml_backend_buffer buf;
-    std::unordered_map<const ggml_tensor *, bool> mine;  // tensors this allocator placed
+    ggml_backend_buffer buf;  // a tensor placed here has buffer == &buf
 };
 
 namespace {
@@ -561,7 +560,9 @@ struct Planner {
                 auto ok = [](const ggml_tensor * x) {
                     return (x->type == GGML_TYPE_F32 || x->type == GGML_TYPE_F16) && x->nb[0] % ggml_tsize(x->type) == 0;
                 };
-                require(ok(a) && ok(t), "cpy " + tname(t) + ": f32 / f16 only");
+                const bool ints = a->type == GGML_TYPE_I32 && t->type == GGML_TYPE_I32 && a->nb[0] % 4 == 0 &&
+                                  t->nb[0] % 4 == 0;
+                require(ints || (ok(a) && ok(t)), "cpy " + tname(t) + ": f32 / f16, or i32 to i32");
                 Step s = new_step(S_CPY);
                 s.type = a->type;
                 s.op = t->type;
@@ -1032,7 +1033,8 @@ size_t place(ggml_gallocr * ga, ggml_cgraph * g, std::vector<std::pair<ggml_tens
     const int n = (int) g->nodes.size();
     const Chains c = find_chains(g);
     // Needs memory: no data yet (or placed by this allocator before), not a view, not folded.
-    auto needs = [&](const ggml_tensor * t) { return !t->view_src && (!t->data || ga->mine.count(t)); };
+    // Tensors of graphs placed earlier are never touched: their contexts may be gone.
+    auto needs = [&](const ggml_tensor * t) { return !t->view_src && (!t->data || t->buffer == &ga->buf); };
     std::unordered_map<const ggml_tensor *, int> last;
     std::unordered_map<const ggml_tensor *, bool> keep;
     for (ggml_tensor * t : g->leafs) keep[t] = true;
@@ -1337,7 +1339,6 @@ bool ggml_gallocr_reserve(ggml_gallocr_t ga, ggml_cgraph * g) {
                    ga->buf.size = 0;
                    check_hip(hipMalloc(&ga->buf.base, need), "hipMalloc compute buffer");
                    ga->buf.size = need;
-                   for (auto & kv : ga->mine) const_cast<ggml_tensor *>(kv.first)->data = nullptr;
                }
            }) == 0;
 }
@@ -1356,12 +1357,9 @@ bool ggml_gallocr_alloc_graph(ggml_gallocr_t ga, ggml_cgraph * g) {
                    check_hip(hipMalloc(&ga->buf.base, need), "hipMalloc compute buffer");
                    ga->buf.size = need;
                }
-               for (auto & kv : ga->mine) const_cast<ggml_tensor *>(kv.first)->data = nullptr;
-               ga->mine.clear();
                for (auto & w : where) {
                    w.first->data = (char *) ga->buf.base + w.second;
                    w.first->buffer = &ga->buf;
-                   ga->mine[w.first] = true;
                }
                refresh_views(g);
            }) == 0;

@@ -32,6 +32,22 @@ class _Options(ctypes.Structure):
                 ("allow_cpu_fallback", ctypes.c_bool)]
 
 
+class TensorInfo(ctypes.Structure):
+    """ggml_compiler_tensor_info (include/ggml_compiler_rt.h)."""
+    _fields_ = [("name", ctypes.c_char_p), ("dtype", ctypes.c_int), ("ndim", ctypes.c_int),
+                ("shape", ctypes.c_int64 * 8), ("nbytes", ctypes.c_size_t)]
+
+
+class Stats(ctypes.Structure):
+    """ggml_compiler_stats (include/ggml_compiler_rt.h)."""
+    _fields_ = [("ms_total", ctypes.c_double), ("n_calls", ctypes.c_int)]
+
+
+class Builder(ctypes.Structure):
+    """ggml_compiler_builder (include/ggml_compiler_rt.h)."""
+    _fields_ = [("stage", ctypes.c_char_p), ("build", ctypes.c_void_p)]
+
+
 def library_path() -> Path:
     env = os.environ.get("GCQ_LIB")
     if env:
@@ -99,6 +115,40 @@ SIGNATURES = {
     "ggml_compiler_has_backend": ([i32], ctypes.c_bool),
     "ggml_compiler_quantize": ([ctypes.c_char_p, p, i64, i64, p, sz], sz),
     "ggml_compiler_row_size": ([ctypes.c_char_p, i64], sz),
+    "ggml_compiler_load": ([ctypes.c_char_p, p], p),
+    "ggml_compiler_load_with": ([ctypes.c_char_p, p, p, i32], p),
+    "ggml_compiler_metadata": ([p, ctypes.c_char_p], ctypes.c_char_p),
+    "ggml_compiler_free": ([p], None),
+    "ggml_compiler_backend_name": ([p], ctypes.c_char_p),
+    "ggml_compiler_n_entries": ([p], i32),
+    "ggml_compiler_entry_name": ([p, i32], ctypes.c_char_p),
+    "ggml_compiler_entry_n_inputs": ([p, i32], i32),
+    "ggml_compiler_entry_n_outputs": ([p, i32], i32),
+    "ggml_compiler_entry_input_info": ([p, i32, i32, p], i32),
+    "ggml_compiler_entry_output_info": ([p, i32, i32, p], i32),
+    "ggml_compiler_run_entry": ([p, ctypes.c_char_p], i32),
+    "ggml_compiler_reset": ([p], i32),
+    "ggml_compiler_n_inputs": ([p], i32),
+    "ggml_compiler_n_outputs": ([p], i32),
+    "ggml_compiler_input_info": ([p, i32, p], i32),
+    "ggml_compiler_output_info": ([p, i32, p], i32),
+    "ggml_compiler_n_symbols": ([p], i32),
+    "ggml_compiler_symbol_info": ([p, i32, p, p, p, p], i32),
+    "ggml_compiler_set_symbol": ([p, ctypes.c_char_p, i64], i32),
+    "ggml_compiler_set_input_shape": ([p, ctypes.c_char_p, i32, p], i32),
+    "ggml_compiler_set_input": ([p, ctypes.c_char_p, p, sz], i32),
+    "ggml_compiler_run": ([p], i32),
+    "ggml_compiler_get_output": ([p, ctypes.c_char_p, p, sz], i32),
+    "ggml_compiler_last_stats": ([p, p], i32),
+    "ggml_compiler_n_stages": ([p], i32),
+    "ggml_compiler_stage_stats": ([p, i32, p, p, p], i32),
+    "ggml_compiler_build_ctx": ([p], p),
+    "ggml_compiler_build_gpu": ([p], ctypes.c_bool),
+    "ggml_compiler_build_supports": ([p, p], ctypes.c_bool),
+    "ggml_compiler_build_param": ([p, i32], p),
+    "ggml_compiler_build_weight": ([p, ctypes.c_char_p], p),
+    "ggml_compiler_build_symbol": ([p, i32], i64),
+    "ggml_compiler_build_output": ([p, i32, p], None),
     # ggml.h (contexts, tensors and graphs are opaque pointers here; ggml.py views tensors)
     "ggml_last_error": ([], ctypes.c_char_p),
     "ggml_init": ([InitParams], p),

@@ -1,0 +1,154 @@
+"""GGUF programs loaded and run by libgcq's loader (include/ggml_compiler_rt.h, runtime.Session):
+a one-call stage against the oracle, the loop driver's carries / scalars / slices / counters /
+causal masks / collected rows / until test, and a Llama decoder program (ggml_compiler_amd.program,
+the format the reference's compiler writes for llm.py's decode stage) against the oracle's run of
+the same model, by its decode entry (symbolic n_kv bound from the mask's shape) and its generate
+entry (n_kv bound per step from the position, greedy tokens, stop at an end-of-sequence id)."""
+
+import json
+import math
+
+import numpy as np
+import pytest
+
+from ggml_compiler_amd import gguf, runtime
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+TOL_LM = 1e-2
+
+
+def _write(path, program, tensors=()):
+    w = gguf.GGUFWriter()
+    w.add("general.architecture", "ggml_compiler")
+    w.add("ggml_compiler.program", json.dumps(program))
+    w.add("ggml_compiler.meta", json.dumps({"note": "test"}))
+    for name, data, typ, ne in tensors:
+        w.add_tensor(name, data, typ, ne)
+    w.write(path)
+    return str(path)
+
+
+def _v(name, typ, ne, shape):
+    return {"name": name, "type": typ, "ne": list(ne) + [1] * (4 - len(ne)), "shape": shape}
+
+
+def _n(i, op, src, typ, ne, **p):
+    return {"id": f"%{i}", "op": op, "src": src, "type": typ, "ne": list(ne) + [1] * (4 - len(ne)), "p": p, "loc": ""}
+
+
+def test_one_call_program(tmp_path, orc):
+    """y = W x + b: a Q8_0 weight and an f32 bias from the GGUF, one stage, one call."""
+    N, K = 300, 512
+    raw = orc.quantize(orc.normal((N, K), seed=50, std=0.02), "q8_0")
+    bias = orc.normal((N,), seed=51)
+    st = {"name": "lin", "params": [_v("a.0", "f32", [K, 1], [1, K])], "outputs": ["%1"],
+          "nodes": [_n(0, "mul_mat", ["w.0", "a.0"], "f32", [N, 1]), _n(1, "add", ["%0", "c.0"], "f32", [N, 1])]}
+    prog = {"format_version": 3, "symbols": [], "values": [_v("x", "f32", [K, 1], [1, K]), _v("y", "f32", [N, 1], [1, N])],
+            "stages": [st], "entries": [{"name": "main", "inputs": ["x"], "outputs": ["y"],
+                                         "driver": [{"op": "call", "stage": "lin", "args": ["x"], "out": ["y"]}]}],
+            "state": []}
+    path = _write(tmp_path / "lin.gguf", prog, [("w.0", raw, 8, (K, N)), ("c.0", bias, 0, (N,))])
+    with runtime.Session(path) as s:
+        assert s.backend_name and [t.name for t in s.inputs] == ["x"] and s.outputs[0].shape == (1, N)
+        assert s.metadata == {"note": "test"}
+        for seed in (52, 53):
+            x = orc.normal((1, K), seed=seed)
+            y = s.run(x)["y"]
+            assert orc.parity(y, orc.mul_mat(raw, "q8_0", x, K) + bias) < TOL
+        assert s.stats["n_calls"] == 1 and s.stats["stages"]["lin"]["calls"] == 1
+        with pytest.raises(ValueError, match="shape"):
+            s.run(np.zeros((2, K), np.float32))
+
+
+def test_loop_driver(tmp_path):
+    """h_{k+1} = h_k * s_k + R[k] (carry from h0, per-iteration scalars, slices of R); the causal
+    mask row of position start + k; both collected per iteration; stop once argmax(h) is 7."""
+    n, E = 4, 8
+    step = {"name": "step", "params": [_v("a.0", "f32", [E], [E]), _v("a.1", "f32", [1], [1]),
+                                       _v("a.2", "f32", [E], [E])],
+            "outputs": ["%1"], "nodes": [_n(0, "mul", ["a.0", "a.1"], "f32", [E]), _n(1, "add", ["%0", "a.2"], "f32", [E])]}
+    cpm = {"name": "cpm", "params": [_v("a.0", "f32", [E], [E])], "outputs": ["%0"],
+           "nodes": [_n(0, "cont", ["a.0"], "f32", [E])]}
+    am = {"name": "am", "params": [_v("a.0", "f32", [E], [E])], "outputs": ["%0"],
+          "nodes": [_n(0, "argmax", ["a.0"], "i32", [1])]}
+    values = [_v("h0", "f32", [E], [E]), _v("h", "f32", [E], [E]), _v("s", "f32", [1], [1]), _v("R", "f32", [E, n], [n, E]),
+              _v("r", "f32", [E], [E]), _v("i0", "i32", [1], [1]), _v("i", "i32", [1], [1]), _v("m", "f32", [E], [E]),
+              _v("mo", "f32", [E], [E]), _v("t", "i32", [1], [1]), _v("hs", "f32", [E, n], [n, E]),
+              _v("ms", "f32", [E, n], [n, E])]
+    svals = [2.0, 3.0, 0.5, 1.0]
+    loop = {"op": "loop", "n": n, "carry": [["h", "h0"]], "scalars": [{"value": "s", "values": svals}],
+            "slices": [["r", "R"]], "counters": [["i", "i0"]], "masks": [["m", "i"]],
+            "collect": [["hs", "h"], ["ms", "mo"]], "until": [["t", [7]]],
+            "body": [{"op": "call", "stage": "step", "args": ["h", "s", "r"], "out": ["h"]},
+                     {"op": "call", "stage": "cpm", "args": ["m"], "out": ["mo"]},
+                     {"op": "call", "stage": "am", "args": ["h"], "out": ["t"]}]}
+    prog = {"format_version": 3, "symbols": [], "values": values, "stages": [step, cpm, am],
+            "entries": [{"name": "main", "inputs": ["h0", "R", "i0"], "outputs": ["hs", "ms", "t"], "driver": [loop]}],
+            "state": []}
+    h0 = np.array([1, 0, 0, 0, 0, 0, 0, 0], np.float32)
+    R = np.zeros((n, E), np.float32)
+    R[0, 2] = 5.0   # argmax 2 after step 0
+    R[1, 4] = 50.0  # 4 after step 1
+    R[2, 7] = 90.0  # 7 after step 2: the loop stops there
+    R[3, 0] = 1.0
+    with runtime.Session(_write(tmp_path / "loop.gguf", prog)) as s:
+        out = s.run(h0, R, np.array([3], np.int32))
+        h, want = h0.copy(), np.zeros((n, E), np.float32)
+        for k in range(3):
+            h = h * svals[k] + R[k]
+            want[k] = h
+        np.testing.assert_array_equal(out["hs"], want)  # row 3 stays zero: stopped
+        assert int(out["t"][0]) == 7
+        masks = np.zeros((n, E), np.float32)
+        for k in range(3):
+            masks[k] = np.where(np.arange(E) <= 3 + k, 0.0, -np.inf)
+        np.testing.assert_array_equal(out["ms"], masks)
+        assert s.stats["n_calls"] == 9
+
+
+def _llama(orc, wtype):
+    from ggml_compiler_amd.llm import LlamaConfig, Model
+
+    cfg = LlamaConfig(n_layer=2, n_embd=256, n_head=4, n_head_kv=2, head_dim=64, n_ff=512, n_vocab=1000,
+                      max_ctx=64, wtype=wtype, rms_eps=1e-5, rope_base=10000.0)
+    m = Model(cfg, max_prompt=16)
+    m.init_random(seed=12)
+    w = {name: m.get_weight(name) for name, *_ in m.weights()}
+    m.close()
+    return cfg, w
+
+
+@pytest.mark.parametrize("wtype", [2, 8])
+def test_llama_program_decode_and_generate(tmp_path, orc, wtype):
+    from ggml_compiler_amd.program import write_llama_program
+    from llama_ref import OracleLlama
+
+    cfg, w = _llama(orc, wtype)
+    path = str(tmp_path / "llama.gguf")
+    write_llama_program(path, cfg, w, kv_step=16, n_gen=24, eos=(999,))
+    with runtime.Session(path) as s:
+        assert list(s.entries) == ["decode", "generate"] and s.symbols == {"n_kv": (16, 64)}
+        o = OracleLlama(cfg, w)
+        tok, toks = 17, []
+        for p in range(20):  # n_kv 16 then 32: the decode stage is rebuilt for the new binding
+            n_kv = max(16, (p + 16) // 16 * 16)
+            mask = np.where(np.arange(n_kv) <= p, 0.0, -np.inf).astype(np.float32).reshape(1, 1, 1, n_kv)
+            lg = s.run(np.array([[tok]], np.int32), np.array([p], np.int32), mask, entry="decode")["logits"]
+            assert s.bound() == {"n_kv": n_kv}
+            lo = o.forward([tok])
+            assert orc.parity(lg.reshape(-1), lo) < TOL_LM, p
+            tok = int(np.argmax(lg))
+            toks.append(tok)
+        # generate: the same greedy tokens from a fresh cache, n_kv bound per step by the loop
+        s.reset()
+        gen = s.run(np.array([[17]], np.int32), np.array([0], np.int32), entry="generate")["tokens"]
+        assert list(gen[:20]) == toks
+        assert s.stats["stages"]["decode"]["calls"] == 24 and s.stats["stages"]["pick"]["calls"] == 24
+        # stop at an end-of-sequence id: the first generated token
+        path2 = str(tmp_path / "llama_eos.gguf")
+        write_llama_program(path2, cfg, w, kv_step=16, n_gen=24, eos=(toks[2],))
+    with runtime.Session(path2) as s2:
+        gen = s2.run(np.array([[17]], np.int32), np.array([0], np.int32), entry="generate")["tokens"]
+        assert list(gen[:3]) == toks[:3] and not gen[3:].any()
+        assert s2.stats["n_calls"] == 6
