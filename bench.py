@@ -261,6 +261,64 @@ def bench_ggml_decode(args) -> dict:
                                    f"per graph, then {args.steps} greedy tokens; n_kv 768"}}
 
 
+def bench_program_decode(args) -> dict:
+    """The same 8B-shaped model as a ggml-compiler program GGUF (ggml_compiler_amd.program: the
+    decode stage node for node, symbolic n_kv bound per step like llm.py:527-529), loaded by
+    libgcq's loader and run as the reference's runtime runs it: the prompt through the `decode`
+    entry one token per call, then the `generate` entry's loop (per step: counter, bound n_kv,
+    causal mask set from the host, the decode and argmax stages, the token read back for the
+    until test and collected)."""
+    import tempfile
+
+    import numpy as np
+
+    from ggml_compiler_amd import runtime
+    from ggml_compiler_amd.llm import LlamaConfig, Model
+    from ggml_compiler_amd.program import write_llama_program
+
+    cfg = LlamaConfig.llama3_8b(max_ctx=1024)
+    m = Model(cfg, max_prompt=16)
+    m.init_random(seed=0, std=0.02)
+    w = {name: m.get_weight(name) for name, *_ in m.weights()}
+    m.close()
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "llama3_8b_q4_0.gguf")
+        t0 = time.perf_counter()
+        write_llama_program(path, cfg, w, kv_step=256, n_gen=args.steps)
+        del w
+        t_write = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        s = runtime.Session(path)
+        t_load = time.perf_counter() - t0
+    prompt = np.random.default_rng(0).integers(0, cfg.n_vocab, PROMPT).tolist()
+    t0 = time.perf_counter()
+    for p, tok in enumerate(prompt):
+        n_kv = max(512, (p + 256) // 256 * 256)
+        mask = np.where(np.arange(n_kv) <= p, 0.0, -np.inf).astype(np.float32).reshape(1, 1, 1, n_kv)
+        lg = s.run(np.array([[tok]], np.int32), np.array([p], np.int32), mask, entry="decode")["logits"]
+    t_prompt = time.perf_counter() - t0
+    tok = int(np.argmax(lg))
+    s.run(np.array([[tok]], np.int32), np.array([PROMPT], np.int32), entry="generate")  # warm: builds n_kv 768
+    s.reset()
+    for p, t in enumerate(prompt):  # the same cache state again
+        n_kv = max(512, (p + 256) // 256 * 256)
+        mask = np.where(np.arange(n_kv) <= p, 0.0, -np.inf).astype(np.float32).reshape(1, 1, 1, n_kv)
+        s.run(np.array([[t]], np.int32), np.array([p], np.int32), mask, entry="decode")
+    t0 = time.perf_counter()
+    out = s.run(np.array([[tok]], np.int32), np.array([PROMPT], np.int32), entry="generate")["tokens"]
+    dt = time.perf_counter() - t0
+    st = s.stats
+    s.close()
+    return {"metric": "decode tok/s, ggml-compiler program GGUF through libgcq's loader", "value": round(args.steps / dt, 2),
+            "unit": "tok/s", "steps": args.steps, "ms_per_step": round(dt / args.steps * 1e3, 4),
+            "stage_calls": st["n_calls"], "first_tokens": [int(t) for t in out[:4]],
+            "prompt_tok_s_decode_entry": round(PROMPT / t_prompt, 1), "write_s": round(t_write, 1),
+            "load_s": round(t_load, 1),
+            "config": {"workload": f"Llama-3-8B-shaped Q4_0 decoder (random init) as a program GGUF, {PROMPT} prompt "
+                                   f"tokens by the decode entry, then the generate entry's {args.steps} greedy steps "
+                                   f"(n_kv 768)"}}
+
+
 def cpu_decode_baseline(m, seconds: float = 15.0) -> dict:
     """The CPU oracle (repo restatement of ggml-cpu, OpenMP) decoding the same 8B-shaped model on the
     host cores: a 4-token prompt, then greedy tokens until `seconds` have passed."""
@@ -392,11 +450,12 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--mode", choices=["decode", "gemv", "roofline", "sweep", "gemm", "ggml"], default="decode",
+    ap.add_argument("--mode", choices=["decode", "gemv", "roofline", "sweep", "gemm", "ggml", "program"], default="decode",
                     help="roofline: only the roofline leg and a 1 GiB copy (for rocprofv3 --pmc runs); "
                          "sweep: the GEMV / GEMM / attention configurations, one JSON line each; "
                          "gemm: the prefill GEMM configuration alone, --steps launches (for counter runs); "
-                         "ggml: the decode step built with the ggml API and run by its graph executor")
+                         "ggml: the decode step built with the ggml API and run by its graph executor; "
+                         "program: the same model as a ggml-compiler program GGUF run by the loader")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -404,7 +463,7 @@ def main() -> int:
               file=sys.stderr)
         return 2
     args.steps = args.steps or {"decode": 128, "gemv": 200, "roofline": 10, "sweep": 1, "gemm": 3,
-                                "ggml": 128}[args.mode]
+                                "ggml": 128, "program": 128}[args.mode]
     args.warmup = args.warmup if args.warmup is not None else 8
 
     import torch
@@ -431,6 +490,9 @@ def main() -> int:
         return 0
     if args.mode == "ggml":
         print(json.dumps(bench_ggml_decode(args)), flush=True)
+        return 0
+    if args.mode == "program":
+        print(json.dumps(bench_program_decode(args)), flush=True)
         return 0
     if args.mode == "sweep":
         for r in bench_sweep(ops, torch):

@@ -107,7 +107,7 @@ __device__ __forceinline__ void prefetch_share(const Prefetch & pf, int w, int n
 
 // Arguments of the decode-row GEMV (rowgemv.hip): one f32 activation row times a packed Q4_0 /
 // Q8_0 weight, with the node before (prologue) and after (epilogue) the mul_mat in one launch.
-enum { PRO_PLAIN = 0, PRO_NORM = 1, PRO_MERGE = 2 };
+enum { PRO_PLAIN = 0, PRO_NORM = 1, PRO_MERGE = 2, PRO_SWIGLU = 3 };
 enum { EPI_STORE = 0, EPI_ROPE_KV = 1, EPI_SWIGLU = 2 };
 
 struct RowArgs {
@@ -115,8 +115,9 @@ struct RowArgs {
     const uint16_t * wd;
     int N, nb;  // packed weight rows, blocks per row
     // prologue
-    const float * x;
+    const float * x;          // PRO_SWIGLU: the gate row
     const float * norm_w;
+    const float * up;         // PRO_SWIGLU: the up row
     float eps;
     const float * part_o;     // [H][nsplit][D]
     const float2 * part_ml;   // [H][nsplit] (max, exp-sum)

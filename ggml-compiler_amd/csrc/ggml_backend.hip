@@ -832,6 +832,21 @@ void run_step(const ggml_backend * be, const Step & s) {
         }
         case S_SWIGLU_MULMAT: {
             const int64_t N = s.n[0], K = s.n[1], M = s.n[2], n = s.n[3];
+            if (M == 1 && (s.type == T_Q4_0 || s.type == T_Q8_0) && row_gemv_fits(s.type, K) &&
+                aligned(s.in[1], 16) && aligned(s.in[2], 16)) {  // one launch: silu(g) * u quantized in the GEMV
+                const WeightLayout L = weight_layout(s.type, N, K);
+                RowArgs a{};
+                a.wqs = (const uint8_t *) s.in[0] + L.qs;
+                a.wd = (const uint16_t *) ((const uint8_t *) s.in[0] + L.d);
+                a.N = (int) N;
+                a.nb = (int) (K / QK);
+                a.x = (const float *) s.in[1];
+                a.up = (const float *) s.in[2];
+                a.y = (float *) s.out;
+                a.res = (const float *) s.in[3];
+                launch_row_gemv(s.type, PRO_SWIGLU, EPI_STORE, a, st);
+                return;
+            }
             launch_swiglu_q8((const float *) s.in[1], (const float *) s.in[2], n, n, M, be->ws, st);
             if (M <= 8) launch_gemv(s.type, s.in[0], N, K, be->ws, M, (float *) s.out, N, st, (const float *) s.in[3]);
             else launch_gemm(s.type, s.in[0], N, K, be->ws, M, (float *) s.out, N, st, (const float *) s.in[3]);

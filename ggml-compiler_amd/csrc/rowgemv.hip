@@ -12,6 +12,7 @@
 //                                                            cos/sin table), q -> f32,
 //   PRO_MERGE  Q8_0 of the merged split-K                    k and v -> f16 KV cache at pos
 //              attention partials (<= 8)        EPI_SWIGLU   y[j] = silu(g_j) * u_j
+//   PRO_SWIGLU Q8_0 of silu(g) * u (two f32 rows)
 //
 // Every value is computed with the same operations, in the same order, as the separate kernels
 // (rmsnorm_q8_row / k_merge_q8 / k_rope_kv / k_swiglu_q8 and the Q8_0 activation quantizer), so
@@ -127,7 +128,8 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
     // clamped into range, values past the end discarded), so the compiler knows how many are in
     // flight and waits for the oldest only.
     constexpr bool MERGE = PRO == PRO_MERGE;
-    constexpr int XWMAX = (PRO == PRO_NORM && NBL > 4) ? 8 : 4;  // x waves at most
+    constexpr bool TWO = PRO == PRO_NORM || PRO == PRO_SWIGLU;  // the x waves read two rows
+    constexpr int XWMAX = (TWO && NBL > 4) ? 8 : 4;  // x waves at most
     constexpr int RMAX = MERGE ? 1 : (2 * NBL + XWMAX - 1) / XWMAX;  // half blocks per x thread at most
     const int wave = threadIdx.x >> 6;
     const int XW = MERGE ? NWV : min(XWMAX, (K + 1023) / 1024);
@@ -154,7 +156,7 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
         // The x waves' path ends in this block (their loads never meet the compute waves' code,
         // whose waits would otherwise count them).
         if (xw) {
-            float4 xv[RMAX][4], nv[PRO == PRO_NORM ? RMAX : 1][4];
+            float4 xv[RMAX][4], nv[TWO ? RMAX : 1][4];
 #pragma unroll
             for (int r = 0; r < RMAX; r++) {
                 if (r < rounds) {
@@ -164,6 +166,8 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
                         xv[r][c] = *reinterpret_cast<const float4 *>(a.x + e + 4 * c);
                         if constexpr (PRO == PRO_NORM)
                             nv[r][c] = *reinterpret_cast<const float4 *>(a.norm_w + e + 4 * c);
+                        if constexpr (PRO == PRO_SWIGLU)
+                            nv[r][c] = *reinterpret_cast<const float4 *>(a.up + e + 4 * c);
                     }
                 }
             }
@@ -209,6 +213,18 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
                         v[r][4 * c + 1] = (v[r][4 * c + 1] * scale) * nv[r][c].y;
                         v[r][4 * c + 2] = (v[r][4 * c + 2] * scale) * nv[r][c].z;
                         v[r][4 * c + 3] = (v[r][4 * c + 3] * scale) * nv[r][c].w;
+                    }
+            }
+            if constexpr (PRO == PRO_SWIGLU) {
+                // k_swiglu_q8's arithmetic: g / (1 + e^-g) * u
+#pragma unroll
+                for (int r = 0; r < RMAX; r++)
+#pragma unroll
+                    for (int c = 0; c < 4; c++) {
+                        v[r][4 * c] = v[r][4 * c] / (1.0f + expf(-v[r][4 * c])) * nv[r][c].x;
+                        v[r][4 * c + 1] = v[r][4 * c + 1] / (1.0f + expf(-v[r][4 * c + 1])) * nv[r][c].y;
+                        v[r][4 * c + 2] = v[r][4 * c + 2] / (1.0f + expf(-v[r][4 * c + 2])) * nv[r][c].z;
+                        v[r][4 * c + 3] = v[r][4 * c + 3] / (1.0f + expf(-v[r][4 * c + 3])) * nv[r][c].w;
                     }
             }
 #pragma unroll
@@ -399,7 +415,7 @@ void go(const RowArgs & a, unsigned grid, hipStream_t s) {
 int row_gemv_x_waves(int pro, int nb) {
     if (pro == PRO_MERGE) return 0;
     const int nbl = (nb + 63) / 64, K = nb * QK;
-    const int xwmax = (pro == PRO_NORM && nbl > 4) ? 8 : 4;
+    const int xwmax = ((pro == PRO_NORM || pro == PRO_SWIGLU) && nbl > 4) ? 8 : 4;
     return std::min(xwmax, (K + 1023) / 1024);
 }
 
@@ -447,7 +463,7 @@ void run_row_t(int pro, int epi, const RowArgs & a, hipStream_t s) {
 #define GCQ_PE(P, E)                                  \
     if (pro == P && epi == E) return run_row_r<TYPE, P, E>(a, s);
     GCQ_PE(PRO_PLAIN, EPI_STORE) GCQ_PE(PRO_NORM, EPI_STORE) GCQ_PE(PRO_MERGE, EPI_STORE)
-    GCQ_PE(PRO_NORM, EPI_ROPE_KV) GCQ_PE(PRO_NORM, EPI_SWIGLU)
+    GCQ_PE(PRO_NORM, EPI_ROPE_KV) GCQ_PE(PRO_NORM, EPI_SWIGLU) GCQ_PE(PRO_SWIGLU, EPI_STORE)
 #undef GCQ_PE
     fail("row gemv: unsupported prologue / epilogue pair");
 }

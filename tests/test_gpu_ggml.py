@@ -187,6 +187,28 @@ def test_swiglu_mul_mat_add_chain(be, orc, M):
     assert orc.parity(y, orc.mul_mat(raw, "q4_0", orc.swiglu(gt, up), F) + r) < TOL
 
 
+@pytest.mark.parametrize("t", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("F", [1024, 14336])
+def test_swiglu_prologue_equals_separate_launches(be, gops, orc, t, F):
+    """One token: swiglu -> mul_mat -> add runs as one decode-row GEMV whose prologue computes
+    silu(g) * u and its Q8_0 codes; equal bit for bit to gcq_swiglu_q8 + gcq_mul_mat_q (+ add)."""
+    N = 512
+    raw = _weight(orc, t, N, F, 64)
+    gt, up, r = orc.normal((1, F), seed=65), orc.normal((1, F), seed=66), orc.normal((1, N), seed=67)
+    tid = orc.TYPES[t]
+    gr = Graph(be, {"w": (tid, [F, N], raw), "g": (G.F32, [F, 1], gt), "u": (G.F32, [F, 1], up),
+                    "r": (G.F32, [N, 1], r)},
+               lambda g, ctx, L: g.ggml_add(ctx, L["r"], g.ggml_mul_mat(ctx, L["w"],
+                                                                        g.ggml_swiglu_split(ctx, L["g"], L["u"]))))
+    y = gr.run().reshape(1, N)
+    gr.close()
+    qw = gops.QuantWeight.from_ggml(torch.from_numpy(raw), t, F)
+    act = gops.swiglu_q8(torch.from_numpy(gt).cuda(), torch.from_numpy(up).cuda())
+    want = to_np(gops.mul_mat_q(qw, act, 1, res=torch.from_numpy(r).cuda()))
+    assert np.array_equal(y, want)
+    assert orc.parity(y, orc.mul_mat(raw, t, orc.swiglu(gt, up), F) + r) < TOL
+
+
 # ----------------------------------------------------------------------------- attention
 
 @pytest.mark.parametrize("Sq,n_kv,H,Hkv,D", [(1, 300, 8, 2, 128), (5, 130, 4, 4, 64), (1, 1, 32, 8, 128),

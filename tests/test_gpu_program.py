@@ -152,3 +152,65 @@ def test_llama_program_decode_and_generate(tmp_path, orc, wtype):
         gen = s2.run(np.array([[17]], np.int32), np.array([0], np.int32), entry="generate")["tokens"]
         assert list(gen[:3]) == toks[:3] and not gen[3:].any()
         assert s2.stats["n_calls"] == 6
+
+
+def test_compiled_builder_replaces_a_stage(tmp_path, orc):
+    """ggml_compiler_load_with: a builder (here a ctypes callback, as generated C++ would be)
+    builds stage `lin` from its parameter and the GGUF weight by name; the program's own nodes for
+    the stage are not used (they compute something else) and the result is the builder's."""
+    import ctypes
+
+    from ggml_compiler_amd import _lib
+
+    lib = _lib.load()
+    N, K = 64, 256
+    raw = orc.quantize(orc.normal((N, K), seed=60, std=0.02), "q4_0")
+    st = {"name": "lin", "params": [_v("a.0", "f32", [K, 1], [1, K])], "outputs": ["%0"],
+          "nodes": [_n(0, "mul_mat", ["w.0", "a.0"], "f32", [N, 1])]}
+    prog = {"format_version": 3, "symbols": [], "values": [_v("x", "f32", [K, 1], [1, K]), _v("y", "f32", [N, 1], [1, N])],
+            "stages": [st], "entries": [{"name": "main", "inputs": ["x"], "outputs": ["y"],
+                                         "driver": [{"op": "call", "stage": "lin", "args": ["x"], "out": ["y"]}]}],
+            "state": []}
+    path = _write(tmp_path / "b.gguf", prog, [("w.0", raw, 2, (K, N))])
+    calls = []
+
+    @ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p)
+    def build(b):
+        calls.append(1)
+        ctx = lib.ggml_compiler_build_ctx(b)
+        x = lib.ggml_compiler_build_param(b, 0)
+        w = lib.ggml_compiler_build_weight(b, b"w.0")
+        assert lib.ggml_compiler_build_gpu(b) and lib.ggml_compiler_build_weight(b, b"nope") is None
+        y = lib.ggml_scale(ctx, lib.ggml_mul_mat(ctx, w, x), ctypes.c_float(2.0))
+        lib.ggml_compiler_build_output(b, 0, y)
+        return 0
+
+    builders = (_lib.Builder * 1)(_lib.Builder(b"lin", ctypes.cast(build, ctypes.c_void_p)))
+    m = lib.ggml_compiler_load_with(path.encode(), None, builders, 1)
+    assert not m and "no tensor 'nope'" in lib.ggml_compiler_last_error().decode()  # the builder's error fails the load
+
+    @ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p)
+    def build_ok(b):
+        ctx = lib.ggml_compiler_build_ctx(b)
+        y = lib.ggml_scale(ctx, lib.ggml_mul_mat(ctx, lib.ggml_compiler_build_weight(b, b"w.0"),
+                                                  lib.ggml_compiler_build_param(b, 0)), ctypes.c_float(2.0))
+        lib.ggml_compiler_build_output(b, 0, y)
+        return 0
+
+    builders = (_lib.Builder * 1)(_lib.Builder(b"lin", ctypes.cast(build_ok, ctypes.c_void_p)))
+    m = lib.ggml_compiler_load_with(path.encode(), None, builders, 1)
+    assert m, lib.ggml_compiler_last_error().decode()
+    try:
+        x = orc.normal((1, K), seed=61)
+        assert lib.ggml_compiler_set_input(m, b"x", x.ctypes.data, x.nbytes) == 0
+        assert lib.ggml_compiler_run(m) == 0, lib.ggml_compiler_last_error().decode()
+        y = np.empty((1, N), np.float32)
+        assert lib.ggml_compiler_get_output(m, b"y", y.ctypes.data, y.nbytes) == 0
+        assert orc.parity(y, 2 * orc.mul_mat(raw, "q4_0", x, K)) < TOL
+        assert lib.ggml_compiler_get_output(m, b"y", y.ctypes.data, 4) == -1
+        assert "has 256 bytes" in lib.ggml_compiler_last_error().decode()
+    finally:
+        lib.ggml_compiler_free(m)
+    bad = (_lib.Builder * 1)(_lib.Builder(b"other", ctypes.cast(build_ok, ctypes.c_void_p)))
+    assert not lib.ggml_compiler_load_with(path.encode(), None, bad, 1)
+    assert "builder for stage 'other'" in lib.ggml_compiler_last_error().decode()
