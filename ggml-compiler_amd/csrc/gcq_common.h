@@ -132,9 +132,19 @@ struct RowArgs {
     int64_t ctx;
     int H, Hkv, D;
     int xc;  // set by launch_row_gemv: the x waves take row groups too (PLAIN / NORM)
+    // Several weights of one row length read by the same row (q / k / v, gate / up), EPI_STORE:
+    // rows [r_end[k-1], r_end[k]) are weight k's, its codes and scales at byte offsets r_qs[k] /
+    // r_d[k] from wqs / wd (spans qs_span / d_span bytes, < 2 GB), its results to r_y[k].
+    int nr;  // 0: one weight
+    int r_end[3];
+    uint32_t r_qs[3], r_d[3], qs_span, d_span;
+    float * r_y[3];
 };
 
 void launch_row_gemv(int type, int pro, int epi, const RowArgs & a, hipStream_t s);
+// Byte offsets and spans of up to 3 packed weights (qs[k], d[k], N[k] rows of K) for RowArgs'
+// ranges; false when they span 2 GB or more.
+bool row_gemv_ranges(int type, int n, const uint8_t * const * w, const int64_t * N, int64_t K, RowArgs & a);
 
 // Shapes and byte strides of a strided copy / conversion (elementwise.hip).
 struct Cpy4 {

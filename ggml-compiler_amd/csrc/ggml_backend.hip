@@ -171,6 +171,7 @@ Chains find_chains(const ggml_cgraph * g) {
     c.member.assign(n, false);
     c.in_fold.assign(n, false);
     for (int i = 0; i < n; i++) c.end[i] = i;
+    c.sib.assign(n, -1);
     std::unordered_map<const ggml_tensor *, int> uses, reader;
     std::unordered_map<const ggml_tensor *, std::vector<int>> readers;
     for (int i = 0; i < n; i++) {
@@ -235,12 +236,21 @@ Chains find_chains(const ggml_cgraph * g) {
             c.in_fold[i] = c.in_fold[j] = true;
             c.folded.push_back(m);
             int last = j;
+            bool adds = false, same = true;
             for (int r : rd) {
                 const int a = with_add(r);
                 if (a >= 0) link({r, a});
+                adds = adds || a >= 0;
+                same = same && g->nodes[r]->src[0]->type == g->nodes[rd[0]]->src[0]->type;
                 last = std::max(last, c.end[r]);
             }
             c.end[i] = c.end[j] = last;  // x and w are read until the last reader's work runs
+            if (!adds && same && rd.size() <= 3) {
+                std::vector<int> grp(rd.begin(), rd.end());
+                std::sort(grp.begin(), grp.end());
+                for (int r : grp) c.sib[r] = (int) c.groups.size();
+                c.groups.push_back(std::move(grp));
+            }
         } else if (t->op == GGML_OP_GLU && f32_contig(t->src[0]) && f32_contig(t->src[1]) && aligned16(t->src[0]) &&
                    aligned16(t->src[1]) && t->ne[0] % 32 == 0) {
             const int k = sole(t);
@@ -306,6 +316,7 @@ enum StepKind {
     S_SWIGLU,
     S_ARGMAX,
     S_ATTN_MULMAT,  // decode attention (split partials) -> mul_mat merging them [-> add]
+    S_MULMAT3,      // rms_norm -> mul -> 2 or 3 mul_mats of the one row: one decode-row GEMV
 };
 
 // One launch sequence with every argument it takes; compared byte for byte to decide whether a
@@ -314,6 +325,7 @@ struct Step {
     int kind, type, op, pad;
     const void * in[6];
     void * out;
+    void * out2[2];  // S_MULMAT3: the second and third results
     int64_t n[12];
     float f[6];
     Cpy4 g;
@@ -473,6 +485,49 @@ struct Planner {
             const int64_t B = is_kquant(w->type) ? std::min<int64_t>(M, 8) : M;
             ws_need = std::max(ws_need, act_layout(w->type, B, K).total);
         }
+        steps.push_back(s);
+    }
+
+    // GEMVs of one folded row (nodes grp of g): one decode-row launch over the weights' rows when
+    // they fit one (same type, spans under 2 GB), else one step each, all at this place.
+    void mulmat_group(const ggml_cgraph * g, const std::vector<int> & grp) {
+        const ggml_tensor * m0 = g->nodes[grp[0]];
+        const ggml_tensor * x = m0->src[1];
+        const ggml_tensor * nrm = x->src[0];
+        const int type = m0->src[0]->type;
+        const uint8_t * w[3];
+        int64_t N[3], K = 0;
+        bool ok = grp.size() >= 2 && grp.size() <= 3 && (type == GGML_TYPE_Q4_0 || type == GGML_TYPE_Q8_0);
+        for (size_t k = 0; ok && k < grp.size(); k++) {
+            const ggml_tensor * mm = g->nodes[grp[k]];
+            const ggml_tensor * wt = mm->src[0];
+            ok = whole_packed(wt) && wt->type == type && wt->ne[2] == 1 && wt->ne[3] == 1 && ggml_is_contiguous(mm) &&
+                 !dry;
+            if (!ok) break;
+            packed_dims(wt, N[k], K);
+            w[k] = (const uint8_t *) d(wt);
+        }
+        RowArgs ra{};
+        if (ok) ok = row_gemv_ranges(type, (int) grp.size(), w, N, K, ra);
+        if (!ok) {
+            for (int r : grp) mulmat(g->nodes[r], g->nodes[r]->src[1], nullptr, 0.0f, nullptr, g->nodes[r]);
+            return;
+        }
+        Step s = new_step(S_MULMAT3);
+        s.type = type;
+        s.in[0] = w[0];
+        s.in[1] = d(nrm->src[0]);
+        s.in[2] = d(x->src[1]);
+        s.in[3] = w[1];
+        s.in[4] = grp.size() > 2 ? w[2] : nullptr;
+        s.out = o(m0);
+        s.out2[0] = o(g->nodes[grp[1]]);
+        s.out2[1] = grp.size() > 2 ? o(g->nodes[grp[2]]) : nullptr;
+        s.n[0] = N[0];
+        s.n[1] = N[1];
+        s.n[2] = grp.size() > 2 ? N[2] : 0;
+        s.n[3] = K;
+        std::memcpy(&s.f[0], &nrm->op_params[0], 4);
         steps.push_back(s);
     }
 
@@ -830,6 +885,20 @@ void run_step(const ggml_backend * be, const Step & s) {
             else launch_gemm(wt, s.in[0], N, K, be->ws, M, y, ldy, st, res);
             return;
         }
+        case S_MULMAT3: {
+            const int n = s.in[4] ? 3 : 2;
+            const uint8_t * w[3] = {(const uint8_t *) s.in[0], (const uint8_t *) s.in[3], (const uint8_t *) s.in[4]};
+            RowArgs a{};
+            require(row_gemv_ranges(s.type, n, w, s.n, s.n[3], a), "mul_mat group: weights do not fit one launch");
+            a.x = (const float *) s.in[1];
+            a.norm_w = (const float *) s.in[2];
+            a.eps = s.f[0];
+            a.r_y[0] = (float *) s.out;
+            a.r_y[1] = (float *) s.out2[0];
+            a.r_y[2] = (float *) s.out2[1];
+            launch_row_gemv(s.type, PRO_NORM, EPI_STORE, a, st);
+            return;
+        }
         case S_SWIGLU_MULMAT: {
             const int64_t N = s.n[0], K = s.n[1], M = s.n[2], n = s.n[3];
             if (M == 1 && (s.type == T_Q4_0 || s.type == T_Q8_0) && row_gemv_fits(s.type, K) &&
@@ -953,6 +1022,11 @@ enum ggml_status compute(ggml_backend * be, ggml_cgraph * g) {
     std::vector<int> idx;
     for (int i = 0; i < (int) g->nodes.size(); i++) {
         if (c.member[i]) continue;
+        if (c.sib[i] >= 0) {
+            const std::vector<int> & grp = c.groups[(size_t) c.sib[i]];
+            if (i == grp[0]) p.mulmat_group(g, grp);
+            continue;
+        }
         idx.clear();
         for (int j = 0; j < i; j++)  // members of the chain ending here, in order
             if (c.member[j] && !c.in_fold[j] && c.end[j] == i) idx.push_back(j);
@@ -1072,7 +1146,17 @@ size_t place(ggml_gallocr * ga, ggml_cgraph * g, std::vector<std::pair<ggml_tens
     std::unordered_map<const ggml_tensor *, size_t> off;
     for (int i = 0; i < n; i++) {
         ggml_tensor * t = g->nodes[i];
-        if (!c.member[i] && needs(t)) {
+        if (c.sib[i] >= 0) {  // one launch at the group's first node writes every result
+            const std::vector<int> & grp = c.groups[(size_t) c.sib[i]];
+            if (i == grp[0])
+                for (int r : grp) {
+                    ggml_tensor * u = g->nodes[r];
+                    if (!needs(u)) continue;
+                    const size_t o = A.take(alloc_size(u));
+                    off[u] = o;
+                    where.emplace_back(u, o);
+                }
+        } else if (!c.member[i] && needs(t)) {
             const size_t o = A.take(alloc_size(t));
             off[t] = o;
             where.emplace_back(t, o);

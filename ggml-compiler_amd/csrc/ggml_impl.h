@@ -53,6 +53,10 @@ struct Chains {
     // read by every reader; the norm and the mul are members).
     std::vector<const ggml_tensor *> folded;
     std::vector<bool> in_fold;  // the norm and mul nodes of a folded row
+    // GEMVs of one folded row with no residual add (q / k / v, gate / up): run as one launch at
+    // the first one's place, their results all placed there (sib[i]: group of node i, or -1).
+    std::vector<std::vector<int>> groups;
+    std::vector<int> sib;
 };
 Chains find_chains(const ggml_cgraph * g);
 

@@ -61,13 +61,14 @@ __device__ __forceinline__ int dot_blk_q8_0(const uint4 wa, const uint4 wb, cons
     return s;
 }
 
-template <int TYPE, int R, int NBL, int PRO, int EPI>
+template <int TYPE, int R, int NBL, int PRO, int EPI, int MR>
 __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
     constexpr int NT = 1024, NWV = NT / 64;
     constexpr int CV = TYPE == T_Q4_0 ? 1 : 2;
     constexpr bool XREG = NBL <= 2;  // activation blocks in registers, else read from LDS per use
     constexpr bool PF = CV * NBL * R <= 8;  // next group's weights prefetched (else: registers spill)
     static_assert(EPI == EPI_STORE || R == 2, "row-pair epilogues take two rows per group");
+    static_assert(MR == 1 || EPI == EPI_STORE, "several weights: plain stores only");
     __shared__ int4 lc[kRowMaxK / 16];
     __shared__ float2 lm[kRowMaxK / 32];
     __shared__ double red[NWV];
@@ -83,9 +84,20 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
     // them (halves picked where used, so the loads' results need no conversion and no wait until
     // then; the word of the last scale stays inside the scales' 256-byte-aligned region).
     const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint8_t *>(a.wqs), 0, (int) ((size_t) a.N * nb * CV * 16), 0x00020000);
+        const_cast<uint8_t *>(a.wqs), 0, MR > 1 ? (int) a.qs_span : (int) ((size_t) a.N * nb * CV * 16), 0x00020000);
     const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t *>(a.wd), 0, (int) (((size_t) a.N * nb + 1) / 2 * 4), 0x00020000);
+        const_cast<uint16_t *>(a.wd), 0, MR > 1 ? (int) a.d_span : (int) (((size_t) a.N * nb + 1) / 2 * 4),
+        0x00020000);
+    // Weight k of row `row` (wave-uniform, kept in scalar registers) and the row's index in it; the
+    // per-weight values are picked with constant indices (a dynamic index into the kernel
+    // arguments becomes a vector memory load in front of every weight load).
+    auto range_of = [&](int row, int & local) -> int {
+        row = __builtin_amdgcn_readfirstlane(row);
+        const bool k1 = a.nr > 1 && row >= a.r_end[0], k2 = a.nr > 2 && row >= a.r_end[1];
+        local = k2 ? row - a.r_end[1] : k1 ? row - a.r_end[0] : row;
+        return k2 ? 2 : k1 ? 1 : 0;
+    };
+    auto pick_u = [](int k, const uint32_t (&v)[3]) { return k == 2 ? v[2] : k == 1 ? v[1] : v[0]; };
     constexpr uint32_t kPast = 0x80000000u;  // an offset past every buffer (sizes < 2 GB)
 
     uint4 w[NBL][R][CV];
@@ -97,16 +109,22 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
             const int blk = lane + 64 * i;  // lanes past the row read zeros, unused
 #pragma unroll
             for (int r = 0; r < R; r++) {
-                const int row = min(g * R + r, a.N - 1);
+                int row = min(g * R + r, a.N - 1);
+                uint32_t qb = 0, db = 0;
+                if constexpr (MR > 1) {
+                    const int k = range_of(row, row);
+                    qb = pick_u(k, a.r_qs);
+                    db = pick_u(k, a.r_d);
+                }
                 const uint32_t o = (uint32_t) row * (uint32_t) nb + (uint32_t) blk;
                 const bool in = live && blk < nb;
 #pragma unroll
                 for (int c = 0; c < CV; c++) {
-                    const uint32_t off = in ? (o * CV + c) * 16u : kPast;
+                    const uint32_t off = in ? qb + (o * CV + c) * 16u : kPast;
                     const auto t = __builtin_amdgcn_raw_buffer_load_b128(rq, off, 0, 2);  // 2: nt
                     wv[i][r][c] = make_uint4(t[0], t[1], t[2], t[3]);
                 }
-                dv[i][r] = __builtin_amdgcn_raw_buffer_load_b32(rd, in ? (o >> 1) * 4u : kPast, 0, 0);
+                dv[i][r] = __builtin_amdgcn_raw_buffer_load_b32(rd, in ? db + (o >> 1) * 4u : kPast, 0, 0);
             }
         }
     };
@@ -336,7 +354,8 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
                 if constexpr (TYPE == T_Q4_0) sdot = dot_blk_q4_0(wv[i][r][0], ca, cb, __float_as_int(cm.y));
                 else sdot = dot_blk_q8_0(wv[i][r][0], wv[i][r][CV - 1], ca, cb);
                 // scale index row * nb + blk: its parity picks the half (blk's parity is the lane's)
-                const int row = min(gg * R + r, a.N - 1);
+                int row = min(gg * R + r, a.N - 1);
+                if constexpr (MR > 1) (void) range_of(row, row);  // the index within its weight
                 const uint32_t sh = (uint32_t) (((lane ^ (row & nb)) & 1) << 4);
                 acc[r] += ((float) sdot * h2f((uint16_t) (dv[i][r] >> sh))) * cm.x;
             }
@@ -344,7 +363,17 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
         float v[R];
 #pragma unroll
         for (int r = 0; r < R; r++) v[r] = wave_sum(acc[r]);
-        if constexpr (EPI == EPI_STORE) {
+        if constexpr (EPI == EPI_STORE && MR > 1) {
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                int row = gg * R + r;
+                if (lane == r && row < a.N) {
+                    const int k = range_of(row, row);
+                    float * y = k == 2 ? a.r_y[2] : k == 1 ? a.r_y[1] : a.r_y[0];
+                    y[row] = v[r];
+                }
+            }
+        } else if constexpr (EPI == EPI_STORE) {
 #pragma unroll
             for (int r = 0; r < R; r++) {
                 const int row = gg * R + r;
@@ -405,7 +434,13 @@ namespace {
 
 template <int TYPE, int R, int NBL, int PRO, int EPI>
 void go(const RowArgs & a, unsigned grid, hipStream_t s) {
-    k_row_gemv<TYPE, R, NBL, PRO, EPI><<<grid, 1024, 0, s>>>(a);
+    if constexpr (EPI == EPI_STORE && PRO == PRO_NORM) {
+        if (a.nr > 1) {
+            k_row_gemv<TYPE, R, NBL, PRO, EPI, 3><<<grid, 1024, 0, s>>>(a);
+            return;
+        }
+    }
+    k_row_gemv<TYPE, R, NBL, PRO, EPI, 1><<<grid, 1024, 0, s>>>(a);
 }
 
 // Two rows per group when there are enough groups to give every compute wavefront of the grid
@@ -480,6 +515,39 @@ static bool row_gemv_rows_fit(int type, int64_t N, int nb) {
 }
 
 int row_gemv_merge_max() { return kMergeMax; }
+
+bool row_gemv_ranges(int type, int n, const uint8_t * const * w, const int64_t * N, int64_t K, RowArgs & a) {
+    if (n < 1 || n > 3 || !row_gemv_fits(type, K)) return false;
+    const uint8_t *qs[3], *d[3];
+    uintptr_t qlo = UINTPTR_MAX, dlo = UINTPTR_MAX;
+    int64_t total = 0;
+    for (int k = 0; k < n; k++) {
+        const WeightLayout L = weight_layout(type, N[k], K);
+        qs[k] = w[k] + L.qs;
+        d[k] = w[k] + L.d;
+        qlo = std::min(qlo, (uintptr_t) qs[k]);
+        dlo = std::min(dlo, (uintptr_t) d[k]);
+        total += N[k];
+    }
+    const uint64_t cb = type == T_Q4_0 ? 16u : 32u, nb = (uint64_t) (K / QK);
+    uint64_t qspan = 0, dspan = 0;
+    for (int k = 0; k < n; k++) {
+        a.r_qs[k] = (uint32_t) ((uintptr_t) qs[k] - qlo);
+        a.r_d[k] = (uint32_t) ((uintptr_t) d[k] - dlo);
+        qspan = std::max(qspan, (uint64_t) ((uintptr_t) qs[k] - qlo) + (uint64_t) N[k] * nb * cb);
+        dspan = std::max(dspan, (uint64_t) ((uintptr_t) d[k] - dlo) + ((uint64_t) N[k] * nb + 1) / 2 * 4);
+        a.r_end[k] = (int) ((k ? a.r_end[k - 1] : 0) + N[k]);
+    }
+    if (qspan >= 0x80000000ull || dspan >= 0x80000000ull || total > INT32_MAX) return false;
+    a.nr = n;
+    a.wqs = (const uint8_t *) qlo;
+    a.wd = (const uint16_t *) dlo;
+    a.N = (int) total;
+    a.nb = (int) nb;
+    a.qs_span = (uint32_t) qspan;
+    a.d_span = (uint32_t) dspan;
+    return true;
+}
 
 void launch_row_gemv(int type, int pro, int epi, const RowArgs & a, hipStream_t s) {
     require(row_gemv_fits(type, (int64_t) a.nb * QK), "row gemv: weight type or K not supported");

@@ -171,6 +171,39 @@ def test_norm_row_folded_into_several_gemvs(be, orc, t):
         assert orc.parity(got["split"][i], refs[i]) < TOL, i
 
 
+@pytest.mark.parametrize("t", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("Ns,K", [((512, 128, 128), 4096), ((1024, 1024), 2048), ((640, 64, 192), 14336)])
+def test_sibling_gemvs_in_one_launch(be, gops, orc, t, Ns, K):
+    """Two or three mul_mats of one normalized row with no add (q / k / v, gate / up) run as one
+    decode-row launch over the weights' rows; each result equals gcq_rms_norm_mul_mat on its weight
+    alone bit for bit, and the oracle within 1e-3."""
+    tid = orc.TYPES[t]
+    raws = [_weight(orc, t, N, K, 140 + i) for i, N in enumerate(Ns)]
+    x = orc.normal((1, K), seed=144)
+    nw = (1.0 + 0.1 * orc.normal((K,), seed=145)).astype(np.float32)
+    leaves = {"x": (G.F32, [K, 1], x), "nw": (G.F32, [K], nw)}
+    for i, (N, raw) in enumerate(zip(Ns, raws)):
+        leaves[f"w{i}"] = (tid, [K, N], raw)
+
+    def build(g, ctx, L):
+        m = g.ggml_mul(ctx, g.ggml_rms_norm(ctx, L["x"], 1e-5), L["nw"])
+        outs = [g.ggml_mul_mat(ctx, L[f"w{i}"], m) for i in range(len(Ns))]
+        for u in outs:
+            g.ggml_set_output(u)
+        return outs
+
+    gr = Graph(be, leaves, build)
+    gr.run()
+    got = [G.get_data(gr.built[i], np.float32) for i in range(len(Ns))]
+    gr.close()
+    xd, nwd = torch.from_numpy(x).cuda(), torch.from_numpy(nw).cuda()
+    xn = orc.rms_norm(x, 1e-5) * nw[None, :]
+    for i, raw in enumerate(raws):
+        qw = gops.QuantWeight.from_ggml(torch.from_numpy(raw), t, K)
+        assert np.array_equal(got[i], to_np(gops.rms_norm_mul_mat(qw, xd, nwd, 1e-5)).reshape(-1)), i
+        assert orc.parity(got[i], orc.mul_mat(raw, t, xn, K)[0]) < TOL, i
+
+
 @pytest.mark.parametrize("M", [1, 9])
 def test_swiglu_mul_mat_add_chain(be, orc, M):
     N, F = 256, 1024
