@@ -36,11 +36,6 @@ void launch_rmsnorm_q8(const float * x, int64_t ldx, const float * w, float eps,
                        hipStream_t s);
 void launch_swiglu_q8(const float * g, const float * u, int64_t ld, int64_t n, int64_t rows, void * act,
                       hipStream_t s);
-void launch_rope_neox(const float * x, int64_t sx_s, int64_t sx_h, float * out, int64_t so_s, int64_t so_h,
-                      const int32_t * pos, int64_t D, int64_t H, int64_t S, int n_dims, float freq_base,
-                      float freq_scale, float attn_factor, const float * ff, hipStream_t s);
-void launch_set_rows_f16(void * dst, int64_t dst_h, int64_t dst_j, const float * src, int64_t src_h, int64_t src_j,
-                         const int32_t * idx, int64_t n, int64_t D, int64_t Hrows, int64_t dst_rows, hipStream_t s);
 void launch_get_rows(int type, const void * tab, int64_t nrows_tab, int64_t D, const int32_t * idx, int64_t n,
                      float * out, hipStream_t s);
 void launch_swiglu(const float * g, const float * u, float * y, int64_t n, hipStream_t s);

@@ -51,14 +51,28 @@ __global__ __launch_bounds__(256) void k_rms_norm(const float * __restrict__ x, 
 // once per pair, theta_scale = powf(base, -2/n_dims) computed on the host in f32 as ggml does),
 // then all threads rotate the block's heads with it; dims n_dims .. D-1 pass through.
 constexpr int RH = 8;
+// A second tensor (x2 / out2, H2 heads, the same positions and parameters: q and k of a layer)
+// takes the grid rows past the first's.
 __global__ __launch_bounds__(256) void k_rope_neox(const float * __restrict__ x, int64_t sx_s, int64_t sx_h,
                                                    float * __restrict__ out, int64_t so_s, int64_t so_h,
                                                    const int32_t * __restrict__ pos, int D, int H, int S, int n_dims,
                                                    float theta_scale, float freq_scale, float attn_factor,
-                                                   const float * __restrict__ ff) {
+                                                   const float * __restrict__ ff, const float * __restrict__ x2,
+                                                   int64_t sx2_s, int64_t sx2_h, float * __restrict__ out2,
+                                                   int64_t so2_s, int64_t so2_h, int H2) {
     __shared__ float2 cs[128];  // n_dims / 2 <= 128
     const int half = n_dims / 2;
-    const int s = blockIdx.x, h0 = blockIdx.y * RH;
+    const int s = blockIdx.x, yb1 = (H + RH - 1) / RH;
+    if ((int) blockIdx.y >= yb1) {  // the second tensor's heads
+        x = x2;
+        sx_s = sx2_s;
+        sx_h = sx2_h;
+        out = out2;
+        so_s = so2_s;
+        so_h = so2_h;
+        H = H2;
+    }
+    const int h0 = ((int) blockIdx.y < yb1 ? (int) blockIdx.y : (int) blockIdx.y - yb1) * RH;
     const int nh = min(RH, H - h0);
     if ((int) threadIdx.x < half) {
         const int i = threadIdx.x;
@@ -92,9 +106,24 @@ __global__ __launch_bounds__(256) void k_rope_neox(const float * __restrict__ x,
 // index falls outside [0, dst_rows) are not written.
 __global__ void k_set_rows_f16(uint16_t * __restrict__ dst, int64_t dst_h, int64_t dst_j,
                                const float * __restrict__ src, int64_t src_h, int64_t src_j,
-                               const int32_t * __restrict__ idx, int n, int D, int Hrows, int64_t dst_rows) {
-    const int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
-    const int per = D / 8;
+                               const int32_t * __restrict__ idx, int n, int D, int Hrows, int64_t dst_rows,
+                               SetRowsSecond r2) {
+    int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    int per = D / 8;
+    const int64_t n1 = (int64_t) n * Hrows * per;
+    if (t >= n1) {  // a second write of the same rows (k and v of a layer)
+        t -= n1;
+        dst = r2.dst;
+        dst_h = r2.dst_h;
+        dst_j = r2.dst_j;
+        src = r2.src;
+        src_h = r2.src_h;
+        src_j = r2.src_j;
+        D = r2.D;
+        Hrows = r2.Hrows;
+        dst_rows = r2.dst_rows;
+        per = D / 8;
+    }
     if (t >= (int64_t) n * Hrows * per) return;
     const int c = (int) (t % per);
     const int h = (int) ((t / per) % Hrows);
@@ -251,22 +280,28 @@ void launch_rms_norm(const float * x, int64_t ldx, float * y, int64_t ldy, const
 
 void launch_rope_neox(const float * x, int64_t sx_s, int64_t sx_h, float * out, int64_t so_s, int64_t so_h,
                       const int32_t * pos, int64_t D, int64_t H, int64_t S, int n_dims, float freq_base,
-                      float freq_scale, float attn_factor, const float * ff, hipStream_t s) {
+                      float freq_scale, float attn_factor, const float * ff, hipStream_t s, const RopeSecond * r2) {
     const float theta_scale = powf(freq_base, -2.0f / (float) n_dims);
-    if (S * H * D == 0) return;
+    const int64_t H2 = r2 ? r2->H : 0;
+    if (S * (H + H2) * D == 0) return;
     require(n_dims <= 256, "rope: n_dims above 256");
-    const dim3 grid((unsigned) S, (unsigned) ((H + RH - 1) / RH));
+    require(H > 0 || H2 == 0, "rope: the second tensor needs a first");
+    const dim3 grid((unsigned) S, (unsigned) ((H + RH - 1) / RH + (H2 + RH - 1) / RH));
     k_rope_neox<<<grid, 256, 0, s>>>(x, sx_s, sx_h, out, so_s, so_h, pos, (int) D, (int) H, (int) S, n_dims,
-                                     theta_scale, freq_scale, attn_factor, ff);
+                                     theta_scale, freq_scale, attn_factor, ff, r2 ? r2->x : nullptr,
+                                     r2 ? r2->sx_s : 0, r2 ? r2->sx_h : 0, r2 ? r2->out : nullptr,
+                                     r2 ? r2->so_s : 0, r2 ? r2->so_h : 0, (int) H2);
     check_launch("rope");
 }
 
 void launch_set_rows_f16(void * dst, int64_t dst_h, int64_t dst_j, const float * src, int64_t src_h, int64_t src_j,
-                         const int32_t * idx, int64_t n, int64_t D, int64_t Hrows, int64_t dst_rows, hipStream_t s) {
-    const int64_t t = n * Hrows * (D / 8);
+                         const int32_t * idx, int64_t n, int64_t D, int64_t Hrows, int64_t dst_rows, hipStream_t s,
+                         const SetRowsSecond * r2) {
+    const int64_t t = n * Hrows * (D / 8) + (r2 ? n * r2->Hrows * (r2->D / 8) : 0);
     if (t == 0) return;
+    SetRowsSecond z{};
     k_set_rows_f16<<<nblk(t, 256), 256, 0, s>>>((uint16_t *) dst, dst_h, dst_j, src, src_h, src_j, idx, (int) n,
-                                                (int) D, (int) Hrows, dst_rows);
+                                                (int) D, (int) Hrows, dst_rows, r2 ? *r2 : z);
     check_launch("set_rows");
 }
 

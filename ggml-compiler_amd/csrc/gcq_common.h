@@ -151,6 +151,29 @@ struct Cpy4 {
     int64_t sne[4], snb[4], dne[4], dnb[4];
 };
 void launch_cpy(const void * src, int st, void * dst, int dt, const Cpy4 & g, int64_t n, hipStream_t s);
+
+// A second tensor for one launch of rope / set_rows (q and k; k and v of a layer), same positions.
+struct RopeSecond {
+    const float * x;
+    int64_t sx_s, sx_h;
+    float * out;
+    int64_t so_s, so_h, H;
+};
+struct SetRowsSecond {
+    uint16_t * dst;
+    int64_t dst_h, dst_j;
+    const float * src;
+    int64_t src_h, src_j;
+    int D, Hrows;
+    int64_t dst_rows;
+};
+void launch_rope_neox(const float * x, int64_t sx_s, int64_t sx_h, float * out, int64_t so_s, int64_t so_h,
+                      const int32_t * pos, int64_t D, int64_t H, int64_t S, int n_dims, float freq_base,
+                      float freq_scale, float attn_factor, const float * ff, hipStream_t s,
+                      const RopeSecond * r2 = nullptr);
+void launch_set_rows_f16(void * dst, int64_t dst_h, int64_t dst_j, const float * src, int64_t src_h, int64_t src_j,
+                         const int32_t * idx, int64_t n, int64_t D, int64_t Hrows, int64_t dst_rows, hipStream_t s,
+                         const SetRowsSecond * r2 = nullptr);
 void launch_scale(const float * x, float * y, int64_t n, float sc, float b, hipStream_t s);
 bool row_gemv_fits(int type, int64_t K);
 int row_gemv_merge_max();

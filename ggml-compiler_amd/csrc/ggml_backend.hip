@@ -46,11 +46,6 @@ void launch_rmsnorm_q8(const float * x, int64_t ldx, const float * w, float eps,
                        hipStream_t s);
 void launch_swiglu_q8(const float * g, const float * u, int64_t ld, int64_t n, int64_t rows, void * act,
                       hipStream_t s);
-void launch_rope_neox(const float * x, int64_t sx_s, int64_t sx_h, float * out, int64_t so_s, int64_t so_h,
-                      const int32_t * pos, int64_t D, int64_t H, int64_t S, int n_dims, float freq_base,
-                      float freq_scale, float attn_factor, const float * ff, hipStream_t s);
-void launch_set_rows_f16(void * dst, int64_t dst_h, int64_t dst_j, const float * src, int64_t src_h, int64_t src_j,
-                         const int32_t * idx, int64_t n, int64_t D, int64_t Hrows, int64_t dst_rows, hipStream_t s);
 void launch_get_rows(int type, const void * tab, int64_t nrows_tab, int64_t D, const int32_t * idx, int64_t n,
                      float * out, hipStream_t s);
 void launch_swiglu(const float * g, const float * u, float * y, int64_t n, hipStream_t s);
@@ -250,6 +245,7 @@ Chains find_chains(const ggml_cgraph * g) {
                 std::sort(grp.begin(), grp.end());
                 for (int r : grp) c.sib[r] = (int) c.groups.size();
                 c.groups.push_back(std::move(grp));
+                c.kind.push_back(0);
             }
         } else if (t->op == GGML_OP_GLU && f32_contig(t->src[0]) && f32_contig(t->src[1]) && aligned16(t->src[0]) &&
                    aligned16(t->src[1]) && t->ne[0] % 32 == 0) {
@@ -279,6 +275,43 @@ Chains find_chains(const ggml_cgraph * g) {
         } else if (t->op == GGML_OP_MUL_MAT && whole_packed(t->src[0])) {
             const int a = with_add(i);
             if (a >= 0) link({i, a});
+        }
+    }
+    // Pairs of ropes / set_rows (kinds 1, 2). at(t): the node whose launch computes t's memory
+    // (a chain's end, a group's first), -1 for what exists before the graph.
+    std::unordered_map<const ggml_tensor *, int> prod;
+    for (int i = 0; i < n; i++) prod[g->nodes[i]] = i;
+    auto at = [&](const ggml_tensor * t) -> int {
+        while (t->view_src) t = t->view_src;
+        auto it = prod.find(t);
+        if (it == prod.end()) return -1;
+        int k = it->second;
+        if (c.member[k]) k = c.end[k];
+        if (c.sib[k] >= 0) k = c.groups[(size_t) c.sib[k]][0];
+        return k;
+    };
+    auto free_node = [&](int i) { return !c.member[i] && c.sib[i] < 0 && c.end[i] == i; };
+    for (int i = 0; i < n; i++) {
+        const ggml_tensor * a = g->nodes[i];
+        if ((a->op != GGML_OP_ROPE && a->op != GGML_OP_SET_ROWS) || !free_node(i)) continue;
+        for (int j = i + 1; j < n; j++) {
+            const ggml_tensor * b = g->nodes[j];
+            if (b->op != a->op || !free_node(j) || b->src[1] != a->src[1] || at(b->src[0]) >= i) continue;
+            if (a->op == GGML_OP_ROPE) {
+                if (b->src[2] != a->src[2] || std::memcmp(a->op_params, b->op_params, sizeof(a->op_params)) != 0 ||
+                    a->src[0]->ne[0] != b->src[0]->ne[0] || a->src[0]->ne[2] != b->src[0]->ne[2])
+                    continue;
+            } else {
+                const ggml_tensor * dst = base_of(b->src[2]);
+                bool read = false;  // nothing between the two may read the second's destination
+                for (int k = i + 1; k < j && !read; k++)
+                    for (const ggml_tensor * q : g->nodes[k]->src) read = read || (q && base_of(q) == dst);
+                if (read || base_of(a->src[2]) == dst) continue;
+            }
+            c.sib[i] = c.sib[j] = (int) c.groups.size();
+            c.groups.push_back({i, j});
+            c.kind.push_back(a->op == GGML_OP_ROPE ? 1 : 2);
+            break;
         }
     }
     return c;
@@ -317,6 +350,8 @@ enum StepKind {
     S_ARGMAX,
     S_ATTN_MULMAT,  // decode attention (split partials) -> mul_mat merging them [-> add]
     S_MULMAT3,      // rms_norm -> mul -> 2 or 3 mul_mats of the one row: one decode-row GEMV
+    S_ROPE2,        // two ropes of the same positions
+    S_SETROWS2,     // two set_rows of the same indices
 };
 
 // One launch sequence with every argument it takes; compared byte for byte to decide whether a
@@ -325,7 +360,8 @@ struct Step {
     int kind, type, op, pad;
     const void * in[6];
     void * out;
-    void * out2[2];  // S_MULMAT3: the second and third results
+    void * out2[2];  // S_MULMAT3: the second and third results; S_ROPE2 / S_SETROWS2: the second's
+    int64_t m[8];    // S_ROPE2 / S_SETROWS2: the second tensor's strides and sizes
     int64_t n[12];
     float f[6];
     Cpy4 g;
@@ -486,6 +522,42 @@ struct Planner {
             ws_need = std::max(ws_need, act_layout(w->type, B, K).total);
         }
         steps.push_back(s);
+    }
+
+    // Two ropes / set_rows planned as one step when each plans to one step of that kind with the
+    // same positions; else their two steps, here.
+    void pair(const ggml_tensor * a, const ggml_tensor * b) {
+        const size_t n0 = steps.size();
+        node(a);
+        const size_t n1 = steps.size();
+        node(b);
+        if (n1 != n0 + 1 || steps.size() != n0 + 2) return;
+        Step & s = steps[n0];
+        const Step & t = steps[n0 + 1];
+        if (s.kind == S_ROPE && t.kind == S_ROPE && s.in[1] == t.in[1] && s.in[2] == t.in[2] && s.n[4] == t.n[4] &&
+            s.n[6] == t.n[6] && s.n[7] == t.n[7] && s.f[0] == t.f[0] && s.f[1] == t.f[1] && s.f[2] == t.f[2]) {
+            s.kind = S_ROPE2;
+            s.in[3] = t.in[0];
+            s.out2[0] = t.out;
+            s.m[0] = t.n[0];
+            s.m[1] = t.n[1];
+            s.m[2] = t.n[2];
+            s.m[3] = t.n[3];
+            s.m[4] = t.n[5];
+            steps.pop_back();
+        } else if (s.kind == S_SETROWS && t.kind == S_SETROWS && s.in[1] == t.in[1] && s.n[4] == t.n[4]) {
+            s.kind = S_SETROWS2;
+            s.in[3] = t.in[0];
+            s.out2[0] = t.out;
+            s.m[0] = t.n[0];
+            s.m[1] = t.n[1];
+            s.m[2] = t.n[2];
+            s.m[3] = t.n[3];
+            s.m[4] = t.n[5];
+            s.m[5] = t.n[6];
+            s.m[6] = t.n[7];
+            steps.pop_back();
+        }
     }
 
     // GEMVs of one folded row (nodes grp of g): one decode-row launch over the weights' rows when
@@ -941,6 +1013,20 @@ void run_step(const ggml_backend * be, const Step & s) {
             launch_set_rows_f16(s.out, s.n[0], s.n[1], (const float *) s.in[0], s.n[2], s.n[3],
                                 (const int32_t *) s.in[1], s.n[4], s.n[5], s.n[6], s.n[7], st);
             return;
+        case S_SETROWS2: {
+            const SetRowsSecond r2{(uint16_t *) s.out2[0], s.m[0], s.m[1], (const float *) s.in[3], s.m[2], s.m[3],
+                                   (int) s.m[4], (int) s.m[5], s.m[6]};
+            launch_set_rows_f16(s.out, s.n[0], s.n[1], (const float *) s.in[0], s.n[2], s.n[3],
+                                (const int32_t *) s.in[1], s.n[4], s.n[5], s.n[6], s.n[7], st, &r2);
+            return;
+        }
+        case S_ROPE2: {
+            const RopeSecond r2{(const float *) s.in[3], s.m[0], s.m[1], (float *) s.out2[0], s.m[2], s.m[3], s.m[4]};
+            launch_rope_neox((const float *) s.in[0], s.n[0], s.n[1], (float *) s.out, s.n[2], s.n[3],
+                             (const int32_t *) s.in[1], s.n[4], s.n[5], s.n[6], (int) s.n[7], s.f[0], s.f[1], s.f[2],
+                             (const float *) s.in[2], st, &r2);
+            return;
+        }
         case S_ROPE:
             launch_rope_neox((const float *) s.in[0], s.n[0], s.n[1], (float *) s.out, s.n[2], s.n[3],
                              (const int32_t *) s.in[1], s.n[4], s.n[5], s.n[6], (int) s.n[7], s.f[0], s.f[1], s.f[2],
@@ -1024,7 +1110,10 @@ enum ggml_status compute(ggml_backend * be, ggml_cgraph * g) {
         if (c.member[i]) continue;
         if (c.sib[i] >= 0) {
             const std::vector<int> & grp = c.groups[(size_t) c.sib[i]];
-            if (i == grp[0]) p.mulmat_group(g, grp);
+            if (i == grp[0]) {
+                if (c.kind[(size_t) c.sib[i]] == 0) p.mulmat_group(g, grp);
+                else p.pair(g->nodes[grp[0]], g->nodes[grp[1]]);
+            }
             continue;
         }
         idx.clear();

@@ -57,6 +57,9 @@ struct Chains {
     // the first one's place, their results all placed there (sib[i]: group of node i, or -1).
     std::vector<std::vector<int>> groups;
     std::vector<int> sib;
+    // group kinds: 0 the GEMVs above; 1 two ropes (q, k) and 2 two set_rows (k, v) of the same
+    // positions, the second's input computed before the first: one launch at the first's place.
+    std::vector<int> kind;
 };
 Chains find_chains(const ggml_cgraph * g);
 
