@@ -100,6 +100,19 @@ __global__ __launch_bounds__(256) void k_rope_neox(const float * __restrict__ x,
     }
 }
 
+// The (cos, sin) pairs k_rope_neox builds for position pos[0], written out: the table the
+// decode-row GEMV's rope epilogue reads (same arithmetic, so the same rotations).
+__global__ void k_rope_table(const int32_t * __restrict__ pos, int n_dims, float theta_scale, float freq_scale,
+                             float attn_factor, const float * __restrict__ ff, float2 * __restrict__ cs) {
+    const int i = threadIdx.x;
+    if (i >= n_dims / 2) return;
+    float theta = (float) pos[0];
+    for (int k = 0; k < i; k++) theta *= theta_scale;
+    const float f = ff ? ff[i] : 1.0f;
+    const float th = freq_scale * (theta / f);
+    cs[i] = make_float2(cosf(th) * attn_factor, sinf(th) * attn_factor);
+}
+
 // ------------------------------------------------------------------------------ set_rows
 
 // dst[h][idx[j]][d] = f16(src[h][j][d]) for j < n, h < Hrows; 8 values per thread. Rows whose
@@ -302,6 +315,14 @@ void launch_rope_neox(const float * x, int64_t sx_s, int64_t sx_h, float * out, 
                                      r2 ? r2->sx_s : 0, r2 ? r2->sx_h : 0, r2 ? r2->out : nullptr,
                                      r2 ? r2->so_s : 0, r2 ? r2->so_h : 0, (int) H2);
     check_launch("rope");
+}
+
+void launch_rope_table(const int32_t * pos, int n_dims, float freq_base, float freq_scale, float attn_factor,
+                       const float * ff, float2 * cs, hipStream_t s) {
+    require(n_dims > 0 && n_dims % 2 == 0 && n_dims <= 256, "rope table: n_dims must be even, <= 256");
+    const float theta_scale = powf(freq_base, -2.0f / (float) n_dims);
+    k_rope_table<<<1, 128, 0, s>>>(pos, n_dims, theta_scale, freq_scale, attn_factor, ff, cs);
+    check_launch("rope table");
 }
 
 void launch_set_rows_f16(void * dst, int64_t dst_h, int64_t dst_j, const float * src, int64_t src_h, int64_t src_j,

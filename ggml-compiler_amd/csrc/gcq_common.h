@@ -174,6 +174,8 @@ void launch_rope_neox(const float * x, int64_t sx_s, int64_t sx_h, float * out, 
 void launch_set_rows_f16(void * dst, int64_t dst_h, int64_t dst_j, const float * src, int64_t src_h, int64_t src_j,
                          const int32_t * idx, int64_t n, int64_t D, int64_t Hrows, int64_t dst_rows, hipStream_t s,
                          const SetRowsSecond * r2 = nullptr);
+void launch_rope_table(const int32_t * pos, int n_dims, float freq_base, float freq_scale, float attn_factor,
+                       const float * ff, float2 * cs, hipStream_t s);
 void launch_scale(const float * x, float * y, int64_t n, float sc, float b, hipStream_t s);
 bool row_gemv_fits(int type, int64_t K);
 int row_gemv_merge_max();

@@ -159,6 +159,87 @@ bool add_takes(const ggml_tensor * add, const ggml_tensor * mm) {
 
 // --------------------------------------------------------------------------------- chains
 
+// The decode step's attention inputs built the reference's way from three GEMVs of one row
+// (llm.py:361-444): q -> reshape [D, H, 1] -> rope; k -> reshape -> rope (same positions and
+// parameters) -> permute [D, 1, Hkv] -> set_rows into an f16 cache [D, ctx, Hkv]; v -> reshape ->
+// permute -> set_rows (same positions) into another. Each intermediate read by the next node only,
+// one position, NEOX over all D, no frequency factors, and nothing between the first GEMV and the
+// last set_rows reading either cache. Returns {mm_q, mm_k, mm_v, rope_q, members...} or {}.
+std::vector<int> qkv_rope_group(const ggml_cgraph * g, const std::vector<int> & mms,
+                                const std::unordered_map<const ggml_tensor *, int> & uses,
+                                const std::unordered_map<const ggml_tensor *, int> & reader) {
+    const int n = (int) g->nodes.size();
+    auto next = [&](const ggml_tensor * t) -> int {  // the node reading t, if t has exactly one
+        if (is_output(t) || t == g->nodes[n - 1]) return -1;
+        auto u = uses.find(t);
+        if (u == uses.end() || u->second != 1) return -1;
+        return reader.at(t);
+    };
+    auto is = [&](int i, ggml_op op) { return i >= 0 && g->nodes[i]->op == op; };
+    int q = -1, k = -1, v = -1, rq = -1, rk = -1;
+    std::vector<int> mem;
+    const ggml_tensor *pos = nullptr, *ck = nullptr, *cv = nullptr;
+    for (int m : mms) {
+        const ggml_tensor * mm = g->nodes[m];
+        const int rs = next(mm);
+        if (!is(rs, GGML_OP_RESHAPE)) return {};
+        const int nx = next(g->nodes[rs]);
+        if (is(nx, GGML_OP_ROPE)) {
+            const int pm = next(g->nodes[nx]);
+            const int sr = is(pm, GGML_OP_PERMUTE) ? next(g->nodes[pm]) : -1;
+            if (is(sr, GGML_OP_SET_ROWS) && g->nodes[sr]->src[0] == g->nodes[pm]) {
+                if (k >= 0) return {};
+                k = m;
+                rk = nx;
+                ck = base_of(g->nodes[sr]->src[2]);
+                mem.insert(mem.end(), {rs, nx, pm, sr});
+            } else {
+                if (q >= 0) return {};
+                q = m;
+                rq = nx;
+                mem.push_back(rs);
+            }
+        } else if (is(nx, GGML_OP_PERMUTE)) {
+            const int sr = next(g->nodes[nx]);
+            if (!is(sr, GGML_OP_SET_ROWS) || g->nodes[sr]->src[0] != g->nodes[nx] || v >= 0) return {};
+            v = m;
+            cv = base_of(g->nodes[sr]->src[2]);
+            pos = g->nodes[sr]->src[1];
+            mem.insert(mem.end(), {rs, nx, sr});
+        } else {
+            return {};
+        }
+    }
+    if (q < 0 || k < 0 || v < 0) return {};
+    const ggml_tensor *ropq = g->nodes[rq], *ropk = g->nodes[rk];
+    const ggml_tensor * xq = ropq->src[0];
+    const int64_t D = xq->ne[0], H = xq->ne[1], Hkv = ropk->src[0]->ne[1];
+    float fp[6];
+    std::memcpy(fp, &ropq->op_params[5], sizeof(fp));
+    const bool ok =
+        ropq->src[1] == pos && ropk->src[1] == pos && !ropq->src[2] && !ropk->src[2] &&
+        std::memcmp(ropq->op_params, ropk->op_params, sizeof(ropq->op_params)) == 0 &&
+        ropq->op_params[1] == D && ropq->op_params[2] == GGML_ROPE_TYPE_NEOX && fp[2] == 0.0f && D % 2 == 0 &&
+        D <= 256 && xq->ne[2] == 1 && xq->ne[3] == 1 && ropk->src[0]->ne[0] == D && ropk->src[0]->ne[2] == 1 &&
+        pos->type == GGML_TYPE_I32 && ggml_nelements(pos) == 1 && ropq->type == GGML_TYPE_F32 &&
+        ggml_is_contiguous(ropq) && ck != cv && ck->type == GGML_TYPE_F16 && cv->type == GGML_TYPE_F16 &&
+        ggml_is_contiguous(ck) && ggml_is_contiguous(cv) && ck->ne[0] == D && cv->ne[0] == D &&
+        ck->ne[2] == Hkv && cv->ne[2] == Hkv && ck->ne[1] == cv->ne[1] && ck->ne[3] == 1 && cv->ne[3] == 1 &&
+        g->nodes[q]->ne[0] == H * D && g->nodes[k]->ne[0] == Hkv * D && g->nodes[v]->ne[0] == Hkv * D;
+    if (!ok) return {};
+    std::vector<int> grp = {q, k, v, rq};
+    grp.insert(grp.end(), mem.begin(), mem.end());
+    const int lo = *std::min_element(grp.begin(), grp.end()), hi = *std::max_element(grp.begin(), grp.end());
+    for (int i = lo + 1; i < hi; i++) {  // the caches are written at lo: nothing else may read them before hi
+        if (std::find(grp.begin(), grp.end(), i) != grp.end()) continue;
+        const ggml_op op = g->nodes[i]->op;  // views read nothing (their readers are checked in turn)
+        if (op == GGML_OP_VIEW || op == GGML_OP_RESHAPE || op == GGML_OP_PERMUTE || op == GGML_OP_TRANSPOSE) continue;
+        for (const ggml_tensor * src : g->nodes[i]->src)
+            if (src && (base_of(src) == ck || base_of(src) == cv)) return {};
+    }
+    return grp;
+}
+
 Chains find_chains(const ggml_cgraph * g) {
     const int n = (int) g->nodes.size();
     Chains c;
@@ -243,9 +324,17 @@ Chains find_chains(const ggml_cgraph * g) {
             if (!adds && same && rd.size() <= 3) {
                 std::vector<int> grp(rd.begin(), rd.end());
                 std::sort(grp.begin(), grp.end());
-                for (int r : grp) c.sib[r] = (int) c.groups.size();
+                std::vector<int> qkv = grp.size() == 3 ? qkv_rope_group(g, grp, uses, reader) : std::vector<int>{};
+                const int kind = qkv.empty() ? 0 : 3;
+                if (kind == 3) grp = qkv;
+                int lo = n;
+                for (int r : grp) {
+                    c.sib[r] = (int) c.groups.size();
+                    lo = std::min(lo, r);
+                }
                 c.groups.push_back(std::move(grp));
-                c.kind.push_back(0);
+                c.kind.push_back(kind);
+                c.first.push_back(lo);
             }
         } else if (t->op == GGML_OP_GLU && f32_contig(t->src[0]) && f32_contig(t->src[1]) && aligned16(t->src[0]) &&
                    aligned16(t->src[1]) && t->ne[0] % 32 == 0) {
@@ -287,7 +376,7 @@ Chains find_chains(const ggml_cgraph * g) {
         if (it == prod.end()) return -1;
         int k = it->second;
         if (c.member[k]) k = c.end[k];
-        if (c.sib[k] >= 0) k = c.groups[(size_t) c.sib[k]][0];
+        if (c.sib[k] >= 0) k = c.first[(size_t) c.sib[k]];
         return k;
     };
     auto free_node = [&](int i) { return !c.member[i] && c.sib[i] < 0 && c.end[i] == i; };
@@ -311,6 +400,7 @@ Chains find_chains(const ggml_cgraph * g) {
             c.sib[i] = c.sib[j] = (int) c.groups.size();
             c.groups.push_back({i, j});
             c.kind.push_back(a->op == GGML_OP_ROPE ? 1 : 2);
+            c.first.push_back(i);
             break;
         }
     }
@@ -352,6 +442,8 @@ enum StepKind {
     S_MULMAT3,      // rms_norm -> mul -> 2 or 3 mul_mats of the one row: one decode-row GEMV
     S_ROPE2,        // two ropes of the same positions
     S_SETROWS2,     // two set_rows of the same indices
+    S_ROPE_TABLE,   // the (cos, sin) table of one position for S_QKV_ROPE
+    S_QKV_ROPE,     // q / k / v GEMVs with q / k rope and k / v cache writes in the epilogue
 };
 
 // One launch sequence with every argument it takes; compared byte for byte to decide whether a
@@ -413,6 +505,7 @@ struct ggml_backend {
     std::string name;
     void * ws = nullptr;  // workspace of the mul_mat activations and flash-attention partials
     size_t ws_size = 0;
+    float2 * rope_cs = nullptr;  // (cos, sin) table of the fused q / k / v rope step (<= 128 pairs)
     bool use_graphs = true;
     std::unordered_map<const ggml_cgraph *, Cached> graphs;
     std::vector<Step> steps;
@@ -422,6 +515,7 @@ struct ggml_backend {
         for (auto & kv : graphs)
             if (kv.second.exec) (void) hipGraphExecDestroy(kv.second.exec);
         if (ws) (void) hipFree(ws);
+        if (rope_cs) (void) hipFree(rope_cs);
         if (stream) (void) hipStreamDestroy(stream);
     }
 };
@@ -521,6 +615,75 @@ struct Planner {
             const int64_t B = is_kquant(w->type) ? std::min<int64_t>(M, 8) : M;
             ws_need = std::max(ws_need, act_layout(w->type, B, K).total);
         }
+        steps.push_back(s);
+    }
+
+    const ggml_tensor * table_pos = nullptr;  // the position and parameters of the last table step
+    int32_t table_params[16] = {};
+
+    // Group kind 3 (qkv_rope_group's order): the rotation table of the step's position (once for
+    // every layer that shares it), then one decode-row launch over the three weights whose
+    // epilogue ropes q into rope_q's result and writes roped k and v into the caches at pos.
+    void qkv_rope(const ggml_cgraph * g, const std::vector<int> & grp) {
+        const ggml_tensor *mq = g->nodes[grp[0]], *mk = g->nodes[grp[1]], *mv = g->nodes[grp[2]];
+        const ggml_tensor * rq = g->nodes[grp[3]];
+        const ggml_tensor * x = mq->src[1];
+        const ggml_tensor * nrm = x->src[0];
+        const ggml_tensor * srk = nullptr;
+        const ggml_tensor * srv = nullptr;
+        for (size_t q = 4; q < grp.size(); q++) {
+            const ggml_tensor * t = g->nodes[grp[q]];
+            if (t->op != GGML_OP_SET_ROWS) continue;
+            if (t->src[0]->src[0] && t->src[0]->src[0]->op == GGML_OP_ROPE) srk = t;
+            else srv = t;
+        }
+        require(srk && srv, "q / k / v rope group: set_rows nodes not found");
+        const int type = mq->src[0]->type;
+        const uint8_t * w[3] = {(const uint8_t *) d(mq->src[0]), (const uint8_t *) d(mk->src[0]),
+                                (const uint8_t *) d(mv->src[0])};
+        int64_t N[3], K = 0;
+        packed_dims(mq->src[0], N[0], K);
+        packed_dims(mk->src[0], N[1], K);
+        packed_dims(mv->src[0], N[2], K);
+        const ggml_tensor * pos = srv->src[1];
+        const ggml_tensor * ck = base_of(srk->src[2]);
+        const ggml_tensor * cv = base_of(srv->src[2]);
+        if (table_pos != pos || std::memcmp(table_params, rq->op_params, sizeof(table_params)) != 0) {
+            if (!be->rope_cs) check_hip(hipMalloc((void **) &be->rope_cs, 128 * sizeof(float2)), "hipMalloc rope table");
+            float fp[6];
+            std::memcpy(fp, &rq->op_params[5], sizeof(fp));
+            Step t = new_step(S_ROPE_TABLE);
+            t.in[0] = d(pos);
+            t.n[0] = rq->op_params[1];
+            t.f[0] = fp[0];
+            t.f[1] = fp[1];
+            t.f[2] = fp[3];
+            steps.push_back(t);
+            table_pos = pos;
+            std::memcpy(table_params, rq->op_params, sizeof(table_params));
+        }
+        Step s = new_step(S_QKV_ROPE);
+        s.type = type;
+        s.in[0] = w[0];
+        s.in[1] = d(nrm->src[0]);
+        s.in[2] = d(x->src[1]);
+        s.in[3] = w[1];
+        s.in[4] = w[2];
+        s.in[5] = d(pos);
+        s.out = o(rq);
+        s.out2[0] = o(ck);
+        s.out2[1] = o(cv);
+        s.n[0] = N[0];
+        s.n[1] = N[1];
+        s.n[2] = N[2];
+        s.n[3] = K;
+        s.n[4] = rq->ne[1];   // H
+        s.n[5] = ck->ne[2];   // Hkv
+        s.n[6] = rq->ne[0];   // D
+        s.n[7] = ck->ne[1];   // ctx
+        std::memcpy(&s.f[0], &nrm->op_params[0], 4);
+        RowArgs ra{};
+        require(row_gemv_ranges(type, 3, w, N, K, ra), "q / k / v rope group: the weights do not fit one launch");
         steps.push_back(s);
     }
 
@@ -957,6 +1120,29 @@ void run_step(const ggml_backend * be, const Step & s) {
             else launch_gemm(wt, s.in[0], N, K, be->ws, M, y, ldy, st, res);
             return;
         }
+        case S_ROPE_TABLE:
+            launch_rope_table((const int32_t *) s.in[0], (int) s.n[0], s.f[0], s.f[1], s.f[2], nullptr, be->rope_cs,
+                              st);
+            return;
+        case S_QKV_ROPE: {
+            const uint8_t * w[3] = {(const uint8_t *) s.in[0], (const uint8_t *) s.in[3], (const uint8_t *) s.in[4]};
+            RowArgs a{};
+            require(row_gemv_ranges(s.type, 3, w, s.n, s.n[3], a), "q / k / v rope: weights do not fit one launch");
+            a.x = (const float *) s.in[1];
+            a.norm_w = (const float *) s.in[2];
+            a.eps = s.f[0];
+            a.y = (float *) s.out;
+            a.pos = (const int *) s.in[5];
+            a.rope_cs = be->rope_cs;
+            a.kc = (uint16_t *) s.out2[0];
+            a.vc = (uint16_t *) s.out2[1];
+            a.H = (int) s.n[4];
+            a.Hkv = (int) s.n[5];
+            a.D = (int) s.n[6];
+            a.ctx = s.n[7];
+            launch_row_gemv(s.type, PRO_NORM, EPI_ROPE_KV, a, st);
+            return;
+        }
         case S_MULMAT3: {
             const int n = s.in[4] ? 3 : 2;
             const uint8_t * w[3] = {(const uint8_t *) s.in[0], (const uint8_t *) s.in[3], (const uint8_t *) s.in[4]};
@@ -1109,9 +1295,11 @@ enum ggml_status compute(ggml_backend * be, ggml_cgraph * g) {
     for (int i = 0; i < (int) g->nodes.size(); i++) {
         if (c.member[i]) continue;
         if (c.sib[i] >= 0) {
-            const std::vector<int> & grp = c.groups[(size_t) c.sib[i]];
-            if (i == grp[0]) {
-                if (c.kind[(size_t) c.sib[i]] == 0) p.mulmat_group(g, grp);
+            const size_t gi = (size_t) c.sib[i];
+            const std::vector<int> & grp = c.groups[gi];
+            if (i == c.first[gi]) {
+                if (c.kind[gi] == 0) p.mulmat_group(g, grp);
+                else if (c.kind[gi] == 3) p.qkv_rope(g, grp);
                 else p.pair(g->nodes[grp[0]], g->nodes[grp[1]]);
             }
             continue;
@@ -1236,15 +1424,19 @@ size_t place(ggml_gallocr * ga, ggml_cgraph * g, std::vector<std::pair<ggml_tens
     for (int i = 0; i < n; i++) {
         ggml_tensor * t = g->nodes[i];
         if (c.sib[i] >= 0) {  // one launch at the group's first node writes every result
-            const std::vector<int> & grp = c.groups[(size_t) c.sib[i]];
-            if (i == grp[0])
-                for (int r : grp) {
-                    ggml_tensor * u = g->nodes[r];
+            const size_t gi = (size_t) c.sib[i];
+            const std::vector<int> & grp = c.groups[gi];
+            if (i == c.first[gi]) {
+                // kind 3 writes rope_q's result only (and the caches in place)
+                const size_t nres = c.kind[gi] == 3 ? 1 : grp.size();
+                for (size_t q = 0; q < nres; q++) {
+                    ggml_tensor * u = g->nodes[grp[c.kind[gi] == 3 ? 3 : q]];
                     if (!needs(u)) continue;
                     const size_t o = A.take(alloc_size(u));
                     off[u] = o;
                     where.emplace_back(u, o);
                 }
+            }
         } else if (!c.member[i] && needs(t)) {
             const size_t o = A.take(alloc_size(t));
             off[t] = o;

@@ -60,6 +60,10 @@ struct Chains {
     // group kinds: 0 the GEMVs above; 1 two ropes (q, k) and 2 two set_rows (k, v) of the same
     // positions, the second's input computed before the first: one launch at the first's place.
     std::vector<int> kind;
+    // kind 3: q / k / v GEMVs of one row with the decode step's rope of q and k and the set_rows of
+    // k and v into f16 caches, as one launch: {mm_q, mm_k, mm_v, rope_q, then the reshape / rope /
+    // permute / set_rows members}; only rope_q's result is written to memory of its own.
+    std::vector<int> first;  // each group's earliest node: where its launch runs
 };
 Chains find_chains(const ggml_cgraph * g);
 

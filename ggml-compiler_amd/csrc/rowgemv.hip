@@ -68,7 +68,7 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
     constexpr bool XREG = NBL <= 2;  // activation blocks in registers, else read from LDS per use
     constexpr bool PF = CV * NBL * R <= 8;  // next group's weights prefetched (else: registers spill)
     static_assert(EPI == EPI_STORE || R == 2, "row-pair epilogues take two rows per group");
-    static_assert(MR == 1 || EPI == EPI_STORE, "several weights: plain stores only");
+    static_assert(MR == 1 || EPI != EPI_SWIGLU, "several weights: plain stores or q / k / v rope");
     __shared__ int4 lc[kRowMaxK / 16];
     __shared__ float2 lm[kRowMaxK / 32];
     __shared__ double red[NWV];
@@ -98,6 +98,25 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
         return k2 ? 2 : k1 ? 1 : 0;
     };
     auto pick_u = [](int k, const uint32_t (&v)[3]) { return k == 2 ? v[2] : k == 1 ? v[1] : v[0]; };
+    // Row r of group g with several weights: EPI_STORE takes the rows in order; EPI_ROPE_KV takes
+    // separate q, k, v weights (ranges 0, 1, 2) in the packed QKV order: group g < (H + Hkv) D/2
+    // is the rotation pair (i, i + D/2) of q head h (h < H) or k head h - H, then pairs of v rows.
+    auto map_row = [&](int g, int r, int & local) -> int {
+        if constexpr (EPI == EPI_ROPE_KV) {
+            g = __builtin_amdgcn_readfirstlane(g);
+            const int hd = a.D >> 1, nq = (a.H + a.Hkv) * hd;
+            if (g < nq) {
+                const int h = g / hd, i = g - h * hd;
+                const bool qh = h < a.H;
+                local = (qh ? h : h - a.H) * a.D + i + r * hd;
+                return qh ? 0 : 1;
+            }
+            local = min(2 * (g - nq) + r, a.Hkv * a.D - 1);
+            return 2;
+        } else {
+            return range_of(min(g * R + r, a.N - 1), local);
+        }
+    };
     constexpr uint32_t kPast = 0x80000000u;  // an offset past every buffer (sizes < 2 GB)
 
     uint4 w[NBL][R][CV];
@@ -112,7 +131,7 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
                 int row = min(g * R + r, a.N - 1);
                 uint32_t qb = 0, db = 0;
                 if constexpr (MR > 1) {
-                    const int k = range_of(row, row);
+                    const int k = map_row(g, r, row);
                     qb = pick_u(k, a.r_qs);
                     db = pick_u(k, a.r_d);
                 }
@@ -355,7 +374,7 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
                 else sdot = dot_blk_q8_0(wv[i][r][0], wv[i][r][CV - 1], ca, cb);
                 // scale index row * nb + blk: its parity picks the half (blk's parity is the lane's)
                 int row = min(gg * R + r, a.N - 1);
-                if constexpr (MR > 1) (void) range_of(row, row);  // the index within its weight
+                if constexpr (MR > 1) (void) map_row(gg, r, row);  // the index within its weight
                 const uint32_t sh = (uint32_t) (((lane ^ (row & nb)) & 1) << 4);
                 acc[r] += ((float) sdot * h2f((uint16_t) (dv[i][r] >> sh))) * cm.x;
             }
@@ -434,7 +453,7 @@ namespace {
 
 template <int TYPE, int R, int NBL, int PRO, int EPI>
 void go(const RowArgs & a, unsigned grid, hipStream_t s) {
-    if constexpr (EPI == EPI_STORE && PRO == PRO_NORM) {
+    if constexpr ((EPI == EPI_STORE || (EPI == EPI_ROPE_KV && R == 2)) && PRO == PRO_NORM) {
         if (a.nr > 1) {
             k_row_gemv<TYPE, R, NBL, PRO, EPI, 3><<<grid, 1024, 0, s>>>(a);
             return;
@@ -553,6 +572,10 @@ void launch_row_gemv(int type, int pro, int epi, const RowArgs & a, hipStream_t 
     require(row_gemv_fits(type, (int64_t) a.nb * QK), "row gemv: weight type or K not supported");
     require(row_gemv_rows_fit(type, a.N, a.nb), "row gemv: weight of 2 GB or more");
     require(epi == EPI_STORE || a.N % 2 == 0, "row gemv: row-pair epilogue needs an even row count");
+    require(a.nr <= 1 || epi == EPI_STORE ||
+                (epi == EPI_ROPE_KV && a.nr == 3 && a.D % 2 == 0 && a.r_end[0] == a.H * a.D &&
+                 a.r_end[1] == (a.H + a.Hkv) * a.D && a.r_end[2] == (a.H + 2 * a.Hkv) * a.D),
+            "row gemv: separate q / k / v weights of H*D, Hkv*D, Hkv*D rows");
     require(pro != PRO_MERGE || (a.nsplit >= 1 && a.nsplit <= kMergeMax && a.D % 4 == 0 && a.nb * QK <= 4096),
             "row gemv: merge of 1.." + std::to_string(kMergeMax) + " splits, K <= 4096");
     if (type == T_Q4_0) run_row_t<T_Q4_0>(pro, epi, a, s);

@@ -204,6 +204,53 @@ def test_sibling_gemvs_in_one_launch(be, gops, orc, t, Ns, K):
         assert orc.parity(got[i], orc.mul_mat(raw, t, xn, K)[0]) < TOL, i
 
 
+@pytest.mark.parametrize("t", ["q4_0", "q8_0"])
+def test_qkv_rope_cache_writes_in_one_launch(be, orc, t):
+    """The decode step's q / k / v GEMVs of one normalized row, the q and k ropes and the k / v
+    set_rows into f16 caches (built as the reference builds them) run as one launch whose epilogue
+    ropes and writes the caches; the roped q and both caches equal the unfused graph's (each
+    intermediate marked as an output, which keeps them apart) to 1e-6."""
+    K, H, Hkv, D, ctx, p = 2048, 8, 2, 128, 64, 13
+    tid = orc.TYPES[t]
+    raws = [_weight(orc, t, N, K, 150 + i) for i, N in enumerate((H * D, Hkv * D, Hkv * D))]
+    x = orc.normal((1, K), seed=154)
+    nw = (1.0 + 0.1 * orc.normal((K,), seed=155)).astype(np.float32)
+    leaves = {"x": (G.F32, [K, 1], x), "nw": (G.F32, [K], nw), "pos": (G.I32, [1], np.array([p], np.int32)),
+              "ck": (G.F16, [D, ctx, Hkv], None), "cv": (G.F16, [D, ctx, Hkv], None)}
+    for i, raw in enumerate(raws):
+        leaves[f"w{i}"] = (tid, [K, raw.shape[0]], raw)
+    res = {}
+    for split in (False, True):
+        keep = {}
+
+        def build(g, ctx_, L):
+            n = g.ggml_mul(ctx_, g.ggml_rms_norm(ctx_, L["x"], 1e-5), L["nw"])
+            q, k, v = (g.ggml_mul_mat(ctx_, L[f"w{i}"], n) for i in range(3))
+            rp = (D, 2, 0, 500000.0, 1.0, 0.0, 1.0, 32.0, 1.0)
+            q = g.ggml_rope_ext(ctx_, g.ggml_reshape_3d(ctx_, q, D, H, 1), L["pos"], None, *rp)
+            k = g.ggml_rope_ext(ctx_, g.ggml_reshape_3d(ctx_, k, D, Hkv, 1), L["pos"], None, *rp)
+            v = g.ggml_reshape_3d(ctx_, v, D, Hkv, 1)
+            kw = g.ggml_set_rows(ctx_, L["ck"], g.ggml_permute(ctx_, k, 0, 2, 1, 3), L["pos"])
+            vw = g.ggml_set_rows(ctx_, L["cv"], g.ggml_permute(ctx_, v, 0, 2, 1, 3), L["pos"])
+            keep["k"] = k
+            out = g.ggml_cont(ctx_, g.ggml_permute(ctx_, q, 0, 2, 1, 3))
+            return [out, kw, vw]
+
+        gr = Graph(be, leaves, build, outputs=[lambda s: keep["k"]] if split else ())
+        for name in ("ck", "cv"):
+            G.checked(G.lib().ggml_backend_tensor_memset, gr.L[name], 0, 0, G.nbytes(gr.L[name]))
+        gr.run()
+        res[split] = [G.get_data(gr.built[0], np.float32), G.get_data(gr.L["ck"], np.uint16),
+                      G.get_data(gr.L["cv"], np.uint16)]
+        gr.close()
+    assert orc.parity(res[False][0], res[True][0]) < 1e-6
+    for i in (1, 2):
+        a = res[False][i].view(np.float16).astype(np.float32).reshape(Hkv, ctx, D)
+        b = res[True][i].view(np.float16).astype(np.float32).reshape(Hkv, ctx, D)
+        assert not a[:, np.arange(ctx) != p].any() and not b[:, np.arange(ctx) != p].any()
+        assert orc.parity(a[:, p], b[:, p]) < 1e-3  # f16 rows: one f16 ulp where a last f32 bit differs
+
+
 @pytest.mark.parametrize("M", [1, 9])
 def test_swiglu_mul_mat_add_chain(be, orc, M):
     N, F = 256, 1024
