@@ -123,18 +123,24 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
     uint32_t d[NBL][R];
     auto load = [&](int g, uint4 (&wv)[NBL][R][CV], uint32_t (&dv)[NBL][R]) {
         const bool live = g < ng;
+        int rows[R];
+        uint32_t qbs[R], dbs[R];  // several weights: each row's index and offsets, once per group
+        if constexpr (MR > 1) {
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                rows[r] = min(g * R + r, a.N - 1);
+                const int k = map_row(g, r, rows[r]);
+                qbs[r] = pick_u(k, a.r_qs);
+                dbs[r] = pick_u(k, a.r_d);
+            }
+        }
 #pragma unroll
         for (int i = 0; i < NBL; i++) {
             const int blk = lane + 64 * i;  // lanes past the row read zeros, unused
 #pragma unroll
             for (int r = 0; r < R; r++) {
-                int row = min(g * R + r, a.N - 1);
-                uint32_t qb = 0, db = 0;
-                if constexpr (MR > 1) {
-                    const int k = map_row(g, r, row);
-                    qb = pick_u(k, a.r_qs);
-                    db = pick_u(k, a.r_d);
-                }
+                const int row = MR > 1 ? rows[r] : min(g * R + r, a.N - 1);
+                const uint32_t qb = MR > 1 ? qbs[r] : 0u, db = MR > 1 ? dbs[r] : 0u;
                 const uint32_t o = (uint32_t) row * (uint32_t) nb + (uint32_t) blk;
                 const bool in = live && blk < nb;
 #pragma unroll
@@ -352,6 +358,14 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
         float acc[R];
 #pragma unroll
         for (int r = 0; r < R; r++) acc[r] = 0.0f;
+        int prow[R];  // several weights: each row's index within its weight, once per group
+        if constexpr (MR > 1) {
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                prow[r] = min(gg * R + r, a.N - 1);
+                (void) map_row(gg, r, prow[r]);
+            }
+        }
 #pragma unroll
         for (int i = 0; i < NBL; i++) {
             const int blk = lane + 64 * i;
@@ -373,8 +387,7 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
                 if constexpr (TYPE == T_Q4_0) sdot = dot_blk_q4_0(wv[i][r][0], ca, cb, __float_as_int(cm.y));
                 else sdot = dot_blk_q8_0(wv[i][r][0], wv[i][r][CV - 1], ca, cb);
                 // scale index row * nb + blk: its parity picks the half (blk's parity is the lane's)
-                int row = min(gg * R + r, a.N - 1);
-                if constexpr (MR > 1) (void) map_row(gg, r, row);  // the index within its weight
+                const int row = MR > 1 ? prow[r] : min(gg * R + r, a.N - 1);
                 const uint32_t sh = (uint32_t) (((lane ^ (row & nb)) & 1) << 4);
                 acc[r] += ((float) sdot * h2f((uint16_t) (dv[i][r] >> sh))) * cm.x;
             }
