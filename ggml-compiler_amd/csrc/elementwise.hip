@@ -15,6 +15,8 @@
 // All are HBM- or launch-bound and move whole rows with 16-byte accesses where the shapes allow.
 #include "gcq_common.h"
 
+#include <stdexcept>
+
 namespace gcq {
 
 // ------------------------------------------------------------------------------ rms_norm
@@ -174,8 +176,85 @@ __global__ void k_binary(int op, const float * __restrict__ a, const float * __r
                          int64_t n, int64_t nb) {
     const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
-    const float bv = b[i % nb];
-    y[i] = op == 0 ? a[i] + bv : a[i] * bv;
+    const float av = a[i], bv = b[i % nb];
+    y[i] = op == 0 ? av + bv : op == 1 ? av * bv : op == 2 ? av - bv : av / bv;
+}
+
+// ----------------------------------------------------------------------- unary, softmax
+
+bool unary_known(int op) {
+    switch (op) {
+        case UN_ABS: case UN_NEG: case UN_TANH: case UN_RELU: case UN_SIGMOID: case UN_GELU: case UN_SILU:
+        case UN_EXP: case UN_GELU_ERF: case UN_SOFTPLUS: case UN_SQR: case UN_SQRT: case UN_LOG: case UN_SIN:
+        case UN_COS:
+            return true;
+        default:
+            return false;
+    }
+}
+
+// y = f(x); the op is uniform over the launch, so the switch is one scalar branch per wave.
+__global__ void k_unary(int op, const float * __restrict__ x, float * __restrict__ y, int64_t n) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float v = x[i];
+    float r;
+    switch (op) {
+        case UN_ABS: r = fabsf(v); break;
+        case UN_NEG: r = -v; break;
+        case UN_TANH: r = tanhf(v); break;
+        case UN_RELU: r = v > 0.0f ? v : 0.0f; break;
+        case UN_SIGMOID: r = 1.0f / (1.0f + expf(-v)); break;
+        case UN_GELU: r = 0.5f * v * (1.0f + tanhf(0.7978845608f * v * (1.0f + 0.044715f * v * v))); break;
+        case UN_SILU: r = v / (1.0f + expf(-v)); break;
+        case UN_EXP: r = expf(v); break;
+        case UN_GELU_ERF: r = 0.5f * v * (1.0f + erff(v * 0.70710678118f)); break;
+        case UN_SOFTPLUS: r = v > 20.0f ? v : log1pf(expf(v)); break;
+        case UN_SQR: r = v * v; break;
+        case UN_SQRT: r = sqrtf(v); break;
+        case UN_LOG: r = logf(v); break;
+        case UN_SIN: r = sinf(v); break;
+        default: r = cosf(v); break;
+    }
+    y[i] = r;
+}
+
+// One 256-thread block per row: the row maximum of x * scale + mask, then e^(v - max) written
+// with its sum, then scaled by 1 / sum. Each thread reads an element before it writes the same
+// element, and all reads of the first pass end at a barrier, so y may alias x. A row masked to
+// -inf everywhere comes out NaN, as ggml's.
+__global__ __launch_bounds__(256) void k_soft_max(const float * x, float * y, int n, int r1, int r2,
+                                                  const void * __restrict__ mask, int mask_f16, int64_t mld,
+                                                  int64_t ms2, int64_t ms3, int m2, int m3, float scale) {
+    __shared__ float red[2][4];
+    const int64_t row = blockIdx.x;
+    const int64_t i1 = row % r1, i23 = row / r1, i2 = i23 % r2, i3 = i23 / r2;
+    const float * xr = x + row * n;
+    float * yr = y + row * n;
+    const int64_t mo = i1 * mld + (i2 % m2) * ms2 + (i3 % m3) * ms3;
+    auto val = [&](int i) {
+        float v = xr[i] * scale;
+        if (mask) v += mask_f16 ? h2f(static_cast<const uint16_t *>(mask)[mo + i]) : static_cast<const float *>(mask)[mo + i];
+        return v;
+    };
+    const int w = threadIdx.x >> 6;
+    float mx = -INFINITY;
+    for (int i = threadIdx.x; i < n; i += 256) mx = fmaxf(mx, val(i));
+    mx = wave_max(mx);
+    if ((threadIdx.x & 63) == 0) red[0][w] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+    float sum = 0.0f;
+    for (int i = threadIdx.x; i < n; i += 256) {
+        const float e = expf(val(i) - mx);
+        yr[i] = e;
+        sum += e;
+    }
+    sum = wave_sum(sum);
+    if ((threadIdx.x & 63) == 0) red[1][w] = sum;
+    __syncthreads();
+    const float inv = 1.0f / (red[1][0] + red[1][1] + red[1][2] + red[1][3]);
+    for (int i = threadIdx.x; i < n; i += 256) yr[i] *= inv;
 }
 
 // -------------------------------------------------------------------------------- argmax
@@ -352,7 +431,27 @@ void launch_swiglu(const float * g, const float * u, float * y, int64_t n, hipSt
 void launch_binary(int op, const float * a, const float * b, float * y, int64_t n, int64_t nb, hipStream_t s) {
     if (n == 0) return;
     k_binary<<<nblk(n, 256), 256, 0, s>>>(op, a, b, y, n, nb);
-    check_launch(op == 0 ? "add" : "mul");
+    check_launch(op == 0 ? "add" : op == 1 ? "mul" : op == 2 ? "sub" : "div");
+}
+
+void launch_unary(int op, const float * x, float * y, int64_t n, hipStream_t s) {
+    if (!unary_known(op)) throw std::runtime_error("unary: unknown op " + std::to_string(op));
+    if (n == 0) return;
+    k_unary<<<nblk(n, 256), 256, 0, s>>>(op, x, y, n);
+    check_launch("unary");
+}
+
+void launch_soft_max(const float * x, float * y, int64_t n, int64_t r1, int64_t r2, int64_t r3, const void * mask,
+                     bool mask_f16, int64_t mld, int64_t ms2, int64_t ms3, int64_t m2, int64_t m3, float scale,
+                     hipStream_t s) {
+    const int64_t rows = r1 * r2 * r3;
+    if (rows == 0 || n == 0) return;
+    if (n > INT32_MAX || r1 > INT32_MAX || r2 > INT32_MAX || rows > INT32_MAX || m2 < 1 || m3 < 1 || m2 > INT32_MAX ||
+        m3 > INT32_MAX)
+        throw std::runtime_error("soft_max: sizes out of range");
+    k_soft_max<<<(unsigned) rows, 256, 0, s>>>(x, y, (int) n, (int) r1, (int) r2, mask, mask_f16 ? 1 : 0, mld, ms2,
+                                                 ms3, (int) m2, (int) m3, scale);
+    check_launch("soft_max");
 }
 
 void launch_argmax(const float * x, int64_t ldx, int64_t rows, int64_t n, int32_t * out, hipStream_t s) {

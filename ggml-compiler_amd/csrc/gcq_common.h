@@ -177,6 +177,18 @@ void launch_set_rows_f16(void * dst, int64_t dst_h, int64_t dst_j, const float *
 void launch_rope_table(const int32_t * pos, int n_dims, float freq_base, float freq_scale, float attn_factor,
                        const float * ff, float2 * cs, hipStream_t s);
 void launch_scale(const float * x, float * y, int64_t n, float sc, float b, hipStream_t s);
+// Elementwise functions of k_unary (the numbering is ggml_unary_op's in include/ggml.h).
+enum UnaryOp : int {
+    UN_ABS = 0, UN_NEG = 1, UN_TANH = 2, UN_RELU = 3, UN_SIGMOID = 4, UN_GELU = 7, UN_SILU = 10, UN_EXP = 11,
+    UN_GELU_ERF = 12, UN_SOFTPLUS = 13, UN_SQR = 100, UN_SQRT = 101, UN_LOG = 102, UN_SIN = 103, UN_COS = 104,
+};
+bool unary_known(int op);
+void launch_unary(int op, const float * x, float * y, int64_t n, hipStream_t s);
+// softmax(x * scale + mask) over rows of n; rows = r1 * r2 * r3 (x and y contiguous); mask row
+// (i1, i2 % m2, i3 % m3) at element strides mld, ms2, ms3, f16 when mask_f16, or no mask.
+void launch_soft_max(const float * x, float * y, int64_t n, int64_t r1, int64_t r2, int64_t r3, const void * mask,
+                     bool mask_f16, int64_t mld, int64_t ms2, int64_t ms3, int64_t m2, int64_t m3, float scale,
+                     hipStream_t s);
 bool row_gemv_fits(int type, int64_t K);
 int row_gemv_merge_max();
 

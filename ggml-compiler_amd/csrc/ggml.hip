@@ -41,7 +41,7 @@ const char * kOpNames[GGML_OP_COUNT] = {"NONE",    "ADD",      "MUL",      "SCAL
                                         "CONT",    "RESHAPE",  "VIEW",     "PERMUTE",  "TRANSPOSE",
                                         "GET_ROWS", "SET_ROWS", "RMS_NORM", "MUL_MAT",  "ROPE",
                                         "FLASH_ATTN_EXT", "ARGMAX", "GLU", "UNARY", "SOFT_MAX",
-                                        "IM2COL", "CONV_2D_DIRECT"};
+                                        "IM2COL", "CONV_2D_DIRECT", "SUB", "DIV"};
 
 // NULL with the reason recorded.
 ggml_tensor * none(const std::string & why) {
@@ -439,6 +439,12 @@ ggml_tensor * ggml_add(ggml_context * ctx, ggml_tensor * a, ggml_tensor * b) {
 ggml_tensor * ggml_mul(ggml_context * ctx, ggml_tensor * a, ggml_tensor * b) {
     return binary(ctx, a, b, GGML_OP_MUL, "ggml_mul");
 }
+ggml_tensor * ggml_sub(ggml_context * ctx, ggml_tensor * a, ggml_tensor * b) {
+    return binary(ctx, a, b, GGML_OP_SUB, "ggml_sub");
+}
+ggml_tensor * ggml_div(ggml_context * ctx, ggml_tensor * a, ggml_tensor * b) {
+    return binary(ctx, a, b, GGML_OP_DIV, "ggml_div");
+}
 
 ggml_tensor * ggml_scale_bias(ggml_context * ctx, ggml_tensor * a, float s, float b) {
     if (!a) return nullptr;
@@ -574,7 +580,7 @@ ggml_tensor * ggml_argmax(ggml_context * ctx, ggml_tensor * a) {
     return t;
 }
 
-// ------------------------------------------------------------------ off-path constructors
+// ------------------------------------------------ elementwise, softmax and off-path constructors
 
 namespace {
 ggml_tensor * unary(ggml_context * ctx, ggml_tensor * a, int uop, const char * what) {
@@ -591,6 +597,42 @@ int64_t conv_out(int64_t in, int64_t k, int s, int p, int d) { return (in + 2 * 
 ggml_tensor * ggml_gelu(ggml_context * ctx, ggml_tensor * a) { return unary(ctx, a, GGML_UNARY_OP_GELU, "ggml_gelu"); }
 ggml_tensor * ggml_tanh(ggml_context * ctx, ggml_tensor * a) { return unary(ctx, a, GGML_UNARY_OP_TANH, "ggml_tanh"); }
 ggml_tensor * ggml_sqr(ggml_context * ctx, ggml_tensor * a) { return unary(ctx, a, GGML_UNARY_OP_SQR, "ggml_sqr"); }
+ggml_tensor * ggml_gelu_erf(ggml_context * ctx, ggml_tensor * a) {
+    return unary(ctx, a, GGML_UNARY_OP_GELU_ERF, "ggml_gelu_erf");
+}
+ggml_tensor * ggml_silu(ggml_context * ctx, ggml_tensor * a) {
+    return unary(ctx, a, GGML_UNARY_OP_SILU, "ggml_silu");
+}
+ggml_tensor * ggml_relu(ggml_context * ctx, ggml_tensor * a) {
+    return unary(ctx, a, GGML_UNARY_OP_RELU, "ggml_relu");
+}
+ggml_tensor * ggml_sigmoid(ggml_context * ctx, ggml_tensor * a) {
+    return unary(ctx, a, GGML_UNARY_OP_SIGMOID, "ggml_sigmoid");
+}
+ggml_tensor * ggml_exp(ggml_context * ctx, ggml_tensor * a) {
+    return unary(ctx, a, GGML_UNARY_OP_EXP, "ggml_exp");
+}
+ggml_tensor * ggml_log(ggml_context * ctx, ggml_tensor * a) {
+    return unary(ctx, a, GGML_UNARY_OP_LOG, "ggml_log");
+}
+ggml_tensor * ggml_neg(ggml_context * ctx, ggml_tensor * a) {
+    return unary(ctx, a, GGML_UNARY_OP_NEG, "ggml_neg");
+}
+ggml_tensor * ggml_abs(ggml_context * ctx, ggml_tensor * a) {
+    return unary(ctx, a, GGML_UNARY_OP_ABS, "ggml_abs");
+}
+ggml_tensor * ggml_sqrt(ggml_context * ctx, ggml_tensor * a) {
+    return unary(ctx, a, GGML_UNARY_OP_SQRT, "ggml_sqrt");
+}
+ggml_tensor * ggml_sin(ggml_context * ctx, ggml_tensor * a) {
+    return unary(ctx, a, GGML_UNARY_OP_SIN, "ggml_sin");
+}
+ggml_tensor * ggml_cos(ggml_context * ctx, ggml_tensor * a) {
+    return unary(ctx, a, GGML_UNARY_OP_COS, "ggml_cos");
+}
+ggml_tensor * ggml_softplus(ggml_context * ctx, ggml_tensor * a) {
+    return unary(ctx, a, GGML_UNARY_OP_SOFTPLUS, "ggml_softplus");
+}
 
 ggml_tensor * ggml_soft_max_ext(ggml_context * ctx, ggml_tensor * a, ggml_tensor * mask, float scale,
                                 float max_bias) {

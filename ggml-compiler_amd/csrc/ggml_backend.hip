@@ -113,6 +113,14 @@ bool whole_packed(const ggml_tensor * a) {
            ggml_is_contiguous(a) && ggml_is_contiguous(b);
 }
 
+static_assert(UN_ABS == GGML_UNARY_OP_ABS && UN_NEG == GGML_UNARY_OP_NEG && UN_TANH == GGML_UNARY_OP_TANH &&
+                  UN_RELU == GGML_UNARY_OP_RELU && UN_SIGMOID == GGML_UNARY_OP_SIGMOID && UN_GELU == GGML_UNARY_OP_GELU &&
+                  UN_SILU == GGML_UNARY_OP_SILU && UN_EXP == GGML_UNARY_OP_EXP &&
+                  UN_GELU_ERF == GGML_UNARY_OP_GELU_ERF && UN_SOFTPLUS == GGML_UNARY_OP_SOFTPLUS &&
+                  UN_SQR == GGML_UNARY_OP_SQR && UN_SQRT == GGML_UNARY_OP_SQRT && UN_LOG == GGML_UNARY_OP_LOG &&
+                  UN_SIN == GGML_UNARY_OP_SIN && UN_COS == GGML_UNARY_OP_COS,
+              "k_unary's numbering is ggml_unary_op's");
+
 bool f32_contig(const ggml_tensor * t) { return t->type == GGML_TYPE_F32 && ggml_is_contiguous(t); }
 
 // b repeats over a as y[i] = a[i] op b[i % nelements(b)]: b's shape is a prefix of a's.
@@ -437,6 +445,8 @@ enum StepKind {
     S_ROPE,
     S_FATTN,
     S_SWIGLU,
+    S_UNARY,
+    S_SOFTMAX,
     S_ARGMAX,
     S_ATTN_MULMAT,  // decode attention (split partials) -> mul_mat merging them [-> add]
     S_MULMAT3,      // rms_norm -> mul -> 2 or 3 mul_mats of the one row: one decode-row GEMV
@@ -818,13 +828,15 @@ struct Planner {
             case GGML_OP_RMS_NORM:
                 return rmsnorm(t, nullptr, t);
             case GGML_OP_ADD:
+            case GGML_OP_SUB:
+            case GGML_OP_DIV:
             case GGML_OP_MUL: {
                 const ggml_tensor *a = t->src[0], *b = t->src[1];
                 require(f32_contig(a) && f32_contig(b) && prefix_broadcast(b, a),
                         std::string(ggml_op_name(t->op)) + " " + tname(t) +
                             ": needs contiguous f32 operands, the second of a leading-dims shape of the first");
                 Step s = new_step(S_BINARY);
-                s.op = t->op == GGML_OP_ADD ? 0 : 1;
+                s.op = t->op == GGML_OP_ADD ? 0 : t->op == GGML_OP_MUL ? 1 : t->op == GGML_OP_SUB ? 2 : 3;
                 s.in[0] = d(a);
                 s.in[1] = d(b);
                 s.out = o(t);
@@ -991,6 +1003,47 @@ struct Planner {
                 s.in[1] = d(t->src[1]);
                 s.out = o(t);
                 s.n[0] = ggml_nelements(t);
+                steps.push_back(s);
+                return;
+            }
+            case GGML_OP_UNARY: {
+                require(f32_contig(t->src[0]) && unary_known(t->op_params[0]),
+                        "unary " + tname(t) + ": a known function of a contiguous f32 tensor");
+                Step s = new_step(S_UNARY);
+                s.op = t->op_params[0];
+                s.in[0] = d(t->src[0]);
+                s.out = o(t);
+                s.n[0] = ggml_nelements(t);
+                steps.push_back(s);
+                return;
+            }
+            case GGML_OP_SOFT_MAX: {
+                const ggml_tensor *a = t->src[0], *m = t->src[1];
+                float fp[2];
+                std::memcpy(fp, &t->op_params[0], sizeof(fp));
+                require(f32_contig(a) && fp[1] == 0.0f,
+                        "soft_max " + tname(t) + ": a contiguous f32 input and no ALiBi (max_bias 0)");
+                Step s = new_step(S_SOFTMAX);
+                s.in[0] = d(a);
+                s.out = o(t);
+                for (int k = 0; k < 4; k++) s.n[k] = a->ne[k];
+                s.n[7] = s.n[8] = 1;
+                if (m) {
+                    const size_t es = ggml_tsize(m->type);
+                    require((m->type == GGML_TYPE_F32 || m->type == GGML_TYPE_F16) && m->nb[0] == es &&
+                                m->nb[1] % es == 0 && m->nb[2] % es == 0 && m->nb[3] % es == 0 &&
+                                m->ne[0] == a->ne[0] && m->ne[1] >= a->ne[1] && a->ne[2] % m->ne[2] == 0 &&
+                                a->ne[3] % m->ne[3] == 0,
+                            "soft_max " + tname(t) + ": the mask must be f32 / f16 [n, >= rows, a divisor of each batch dim]");
+                    s.in[1] = d(m);
+                    s.type = m->type;
+                    s.n[4] = (int64_t) (m->nb[1] / es);
+                    s.n[5] = (int64_t) (m->nb[2] / es);
+                    s.n[6] = (int64_t) (m->nb[3] / es);
+                    s.n[7] = m->ne[2];
+                    s.n[8] = m->ne[3];
+                }
+                s.f[0] = fp[0];
                 steps.push_back(s);
                 return;
             }
@@ -1225,6 +1278,13 @@ void run_step(const ggml_backend * be, const Step & s) {
             return;
         case S_SWIGLU:
             launch_swiglu((const float *) s.in[0], (const float *) s.in[1], (float *) s.out, s.n[0], st);
+            return;
+        case S_UNARY:
+            launch_unary(s.op, (const float *) s.in[0], (float *) s.out, s.n[0], st);
+            return;
+        case S_SOFTMAX:
+            launch_soft_max((const float *) s.in[0], (float *) s.out, s.n[0], s.n[1], s.n[2], s.n[3], s.in[1],
+                            s.type == GGML_TYPE_F16, s.n[4], s.n[5], s.n[6], s.n[7], s.n[8], s.f[0], st);
             return;
         case S_ARGMAX:
             launch_argmax((const float *) s.in[0], s.n[0], s.n[1], s.n[2], (int32_t *) s.out, st);

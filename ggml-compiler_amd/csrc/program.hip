@@ -779,7 +779,8 @@ ggml_tensor * reshape_of(ggml_context * ctx, ggml_tensor * x, const int64_t * ne
 }
 
 // One program node as ggml calls (the op surface of runtime/src/ops.cpp:56-309 that this library
-// runs; the others fail here with the node's name).
+// runs: binaries and unaries as ops.cpp:76-100, and the rest below; the others fail here with the
+// node's name).
 ggml_tensor * emit(ggml_context * ctx, const NodeSpec & n, const std::vector<ggml_tensor *> & s) {
     auto need = [&](size_t lo, size_t hi) {
         if (s.size() < lo || s.size() > hi)
@@ -788,13 +789,23 @@ ggml_tensor * emit(ggml_context * ctx, const NodeSpec & n, const std::vector<ggm
     };
     const std::string & op = n.op;
     ggml_tensor * t = nullptr;
-    if (op == "add" || op == "mul") {
+    using Binary = ggml_tensor * (*)(ggml_context *, ggml_tensor *, ggml_tensor *);
+    using Unary = ggml_tensor * (*)(ggml_context *, ggml_tensor *);
+    static const std::map<std::string, Binary> binaries = {
+        {"add", ggml_add}, {"sub", ggml_sub}, {"mul", ggml_mul}, {"div", ggml_div}};
+    // gelu_tanh is the tanh form, which is what ggml_gelu computes here.
+    static const std::map<std::string, Unary> unaries = {
+        {"relu", ggml_relu}, {"gelu", ggml_gelu},       {"gelu_tanh", ggml_gelu}, {"gelu_erf", ggml_gelu_erf},
+        {"silu", ggml_silu}, {"tanh", ggml_tanh},       {"sigmoid", ggml_sigmoid}, {"exp", ggml_exp},
+        {"log", ggml_log},   {"neg", ggml_neg},         {"abs", ggml_abs},         {"sqr", ggml_sqr},
+        {"sqrt", ggml_sqrt}, {"sin", ggml_sin},         {"cos", ggml_cos},         {"softplus", ggml_softplus}};
+    if (const auto b = binaries.find(op); b != binaries.end()) {
         need(2, 2);
         if (!ggml_can_repeat(s[1], s[0])) node_fail(n, "cannot broadcast " + ne_str(s[1]->ne) + " into " + ne_str(s[0]->ne));
-        t = op == "add" ? ggml_add(ctx, s[0], s[1]) : ggml_mul(ctx, s[0], s[1]);
-    } else if (op == "gelu" || op == "tanh" || op == "sqr") {
+        t = b->second(ctx, s[0], s[1]);
+    } else if (const auto u = unaries.find(op); u != unaries.end()) {
         need(1, 1);
-        t = op == "gelu" ? ggml_gelu(ctx, s[0]) : op == "tanh" ? ggml_tanh(ctx, s[0]) : ggml_sqr(ctx, s[0]);
+        t = u->second(ctx, s[0]);
     } else if (op == "cont") {
         need(1, 1);
         t = ggml_cont(ctx, s[0]);

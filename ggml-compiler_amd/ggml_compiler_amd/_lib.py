@@ -218,6 +218,20 @@ SIGNATURES = {
     "ggml_gelu": ([p, p], p),
     "ggml_tanh": ([p, p], p),
     "ggml_sqr": ([p, p], p),
+    "ggml_gelu_erf": ([p, p], p),
+    "ggml_silu": ([p, p], p),
+    "ggml_relu": ([p, p], p),
+    "ggml_sigmoid": ([p, p], p),
+    "ggml_exp": ([p, p], p),
+    "ggml_log": ([p, p], p),
+    "ggml_neg": ([p, p], p),
+    "ggml_abs": ([p, p], p),
+    "ggml_sqrt": ([p, p], p),
+    "ggml_sin": ([p, p], p),
+    "ggml_cos": ([p, p], p),
+    "ggml_softplus": ([p, p], p),
+    "ggml_sub": ([p, p, p], p),
+    "ggml_div": ([p, p, p], p),
     "ggml_soft_max_ext": ([p, p, p, f32, f32], p),
     "ggml_im2col": ([p, p, p, i32, i32, i32, i32, i32, i32, ctypes.c_bool, i32], p),
     "ggml_conv_2d_direct": ([p, p, p, i32, i32, i32, i32, i32, i32], p),

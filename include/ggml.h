@@ -97,13 +97,28 @@ enum ggml_op {
     GGML_OP_SOFT_MAX,
     GGML_OP_IM2COL,
     GGML_OP_CONV_2D_DIRECT,
+    GGML_OP_SUB,
+    GGML_OP_DIV,
     GGML_OP_COUNT,
 };
 
 enum ggml_unary_op {
-    GGML_UNARY_OP_TANH = 2,
-    GGML_UNARY_OP_GELU = 7,
-    GGML_UNARY_OP_SQR  = 100, /* ggml has sqr as its own op; kept under UNARY here */
+    GGML_UNARY_OP_ABS      = 0,
+    GGML_UNARY_OP_NEG      = 1,
+    GGML_UNARY_OP_TANH     = 2,
+    GGML_UNARY_OP_RELU     = 3,
+    GGML_UNARY_OP_SIGMOID  = 4,
+    GGML_UNARY_OP_GELU     = 7,
+    GGML_UNARY_OP_SILU     = 10,
+    GGML_UNARY_OP_EXP      = 11,
+    GGML_UNARY_OP_GELU_ERF = 12,
+    GGML_UNARY_OP_SOFTPLUS = 13,
+    /* ggml has these as ops of their own; kept under UNARY here */
+    GGML_UNARY_OP_SQR  = 100,
+    GGML_UNARY_OP_SQRT = 101,
+    GGML_UNARY_OP_LOG  = 102,
+    GGML_UNARY_OP_SIN  = 103,
+    GGML_UNARY_OP_COS  = 104,
 };
 
 enum ggml_glu_op {
@@ -221,9 +236,34 @@ GGML_API struct ggml_tensor * ggml_transpose(struct ggml_context * ctx, struct g
 GGML_API struct ggml_tensor * ggml_cont(struct ggml_context * ctx, struct ggml_tensor * a);
 GGML_API struct ggml_tensor * ggml_cpy(struct ggml_context * ctx, struct ggml_tensor * a, struct ggml_tensor * b);
 GGML_API struct ggml_tensor * ggml_cast(struct ggml_context * ctx, struct ggml_tensor * a, enum ggml_type type);
-/* a + b, a * b, b repeated over a (ggml_can_repeat; ops.cpp:56-64,76-78) */
+/* a + b, a - b, a * b, a / b, b repeated over a (ggml_can_repeat; ops.cpp:56-64,76-79) */
 GGML_API struct ggml_tensor * ggml_add(struct ggml_context * ctx, struct ggml_tensor * a, struct ggml_tensor * b);
+GGML_API struct ggml_tensor * ggml_sub(struct ggml_context * ctx, struct ggml_tensor * a, struct ggml_tensor * b);
 GGML_API struct ggml_tensor * ggml_mul(struct ggml_context * ctx, struct ggml_tensor * a, struct ggml_tensor * b);
+GGML_API struct ggml_tensor * ggml_div(struct ggml_context * ctx, struct ggml_tensor * a, struct ggml_tensor * b);
+/* Elementwise f(a) of a contiguous f32 tensor (ops.cpp:81-100): gelu is the tanh form
+   0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), gelu_erf 0.5 x (1 + erf(x / sqrt 2)), silu
+   x / (1 + e^-x), softplus log(1 + e^x) (x itself above 20). */
+GGML_API struct ggml_tensor * ggml_gelu(struct ggml_context * ctx, struct ggml_tensor * a);
+GGML_API struct ggml_tensor * ggml_gelu_erf(struct ggml_context * ctx, struct ggml_tensor * a);
+GGML_API struct ggml_tensor * ggml_silu(struct ggml_context * ctx, struct ggml_tensor * a);
+GGML_API struct ggml_tensor * ggml_relu(struct ggml_context * ctx, struct ggml_tensor * a);
+GGML_API struct ggml_tensor * ggml_tanh(struct ggml_context * ctx, struct ggml_tensor * a);
+GGML_API struct ggml_tensor * ggml_sigmoid(struct ggml_context * ctx, struct ggml_tensor * a);
+GGML_API struct ggml_tensor * ggml_exp(struct ggml_context * ctx, struct ggml_tensor * a);
+GGML_API struct ggml_tensor * ggml_log(struct ggml_context * ctx, struct ggml_tensor * a);
+GGML_API struct ggml_tensor * ggml_neg(struct ggml_context * ctx, struct ggml_tensor * a);
+GGML_API struct ggml_tensor * ggml_abs(struct ggml_context * ctx, struct ggml_tensor * a);
+GGML_API struct ggml_tensor * ggml_sqr(struct ggml_context * ctx, struct ggml_tensor * a);
+GGML_API struct ggml_tensor * ggml_sqrt(struct ggml_context * ctx, struct ggml_tensor * a);
+GGML_API struct ggml_tensor * ggml_sin(struct ggml_context * ctx, struct ggml_tensor * a);
+GGML_API struct ggml_tensor * ggml_cos(struct ggml_context * ctx, struct ggml_tensor * a);
+GGML_API struct ggml_tensor * ggml_softplus(struct ggml_context * ctx, struct ggml_tensor * a);
+/* softmax(a * scale + mask) over each row of a contiguous f32 a [n, r1, r2, r3]; mask f32 or
+   f16 [n, >= r1, m2, m3] (contiguous, r2 % m2 == 0, r3 % m3 == 0) or NULL; max_bias 0 (no ALiBi)
+   (ops.cpp:150-155) */
+GGML_API struct ggml_tensor * ggml_soft_max_ext(struct ggml_context * ctx, struct ggml_tensor * a,
+                                                struct ggml_tensor * mask, float scale, float max_bias);
 /* a * s + b (ops.cpp:121-131, runtime/include/ggml_compiler_ops.h:110-113) */
 GGML_API struct ggml_tensor * ggml_scale(struct ggml_context * ctx, struct ggml_tensor * a, float s);
 GGML_API struct ggml_tensor * ggml_scale_bias(struct ggml_context * ctx, struct ggml_tensor * a, float s, float b);
@@ -259,13 +299,8 @@ GGML_API struct ggml_tensor * ggml_swiglu_split(struct ggml_context * ctx, struc
 GGML_API struct ggml_tensor * ggml_argmax(struct ggml_context * ctx, struct ggml_tensor * a);
 
 /* Off the path: declared so that code written against ggml (runtime/include/ggml_compiler_ops.h's
-   conv_2d, gelu_tanh and flash-attention fallback) compiles; they build nodes with ggml's result
-   shapes, which ggml_backend_supports_op rejects and graph_compute reports as unsupported. */
-GGML_API struct ggml_tensor * ggml_gelu(struct ggml_context * ctx, struct ggml_tensor * a);
-GGML_API struct ggml_tensor * ggml_tanh(struct ggml_context * ctx, struct ggml_tensor * a);
-GGML_API struct ggml_tensor * ggml_sqr(struct ggml_context * ctx, struct ggml_tensor * a);
-GGML_API struct ggml_tensor * ggml_soft_max_ext(struct ggml_context * ctx, struct ggml_tensor * a,
-                                                struct ggml_tensor * mask, float scale, float max_bias);
+   conv_2d) compiles; they build nodes with ggml's result shapes, which ggml_backend_supports_op
+   rejects and graph_compute reports as unsupported. */
 /* a kernel [KW, KH, IC, OC], b input [W, H, IC, N] -> [IC*KH*KW, OW, OH, N] (is_2D) */
 GGML_API struct ggml_tensor * ggml_im2col(struct ggml_context * ctx, struct ggml_tensor * a, struct ggml_tensor * b,
                                           int s0, int s1, int p0, int p1, int d0, int d1, bool is_2D,

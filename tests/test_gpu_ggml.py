@@ -464,6 +464,76 @@ def test_cont_cast_scale_binary_argmax(be, orc):
     assert orc.parity(got["glu"], orc.swiglu(a, a * 0.5 + 2.0).reshape(-1)) < 1e-6
 
 
+UNARY_REF = {  # torch's fp32 functions on the CPU (softplus: ggml's threshold of 20)
+    "relu": torch.relu, "gelu": lambda x: torch.nn.functional.gelu(x, approximate="tanh"),
+    "gelu_erf": torch.nn.functional.gelu, "silu": torch.nn.functional.silu, "tanh": torch.tanh,
+    "sigmoid": torch.sigmoid, "exp": torch.exp, "log": torch.log, "neg": torch.neg, "abs": torch.abs,
+    "sqr": torch.square, "sqrt": torch.sqrt, "sin": torch.sin, "cos": torch.cos,
+    "softplus": lambda x: torch.nn.functional.softplus(x, threshold=20.0)}
+
+
+def test_unary_sub_div(be, orc):
+    """Each elementwise function against torch's, on values that cover both signs (log and sqrt
+    on |x| + 0.1); sub and div with a broadcast row, bit-exact."""
+    a = orc.normal((3, 7, 40), seed=110) * 3.0
+    pos = np.abs(a) + 0.1
+    b = orc.normal((40,), seed=111) + 2.0
+    outs = {}
+
+    def build(g, ctx, L):
+        for name in UNARY_REF:
+            src = L["p"] if name in ("log", "sqrt") else L["a"]
+            outs[name] = getattr(g, "ggml_" + name)(ctx, src)
+        outs["sub"] = g.ggml_sub(ctx, L["a"], L["b"])
+        outs["div"] = g.ggml_div(ctx, L["a"], L["b"])
+        for t in outs.values():
+            g.ggml_set_output(t)
+        return list(outs.values())
+
+    gr = Graph(be, {"a": (G.F32, [40, 7, 3], a), "p": (G.F32, [40, 7, 3], pos), "b": (G.F32, [40], b)}, build)
+    gr.run()
+    got = {k: G.get_data(t, np.float32) for k, t in outs.items()}
+    gr.close()
+    for name, f in UNARY_REF.items():
+        x = torch.from_numpy(pos if name in ("log", "sqrt") else a)
+        want = f(x).numpy().reshape(-1)
+        assert np.allclose(got[name], want, rtol=2e-6, atol=2e-6), name
+    assert np.array_equal(got["sub"], (a - b).reshape(-1))
+    assert np.array_equal(got["div"], (a / b).reshape(-1))
+
+
+@pytest.mark.parametrize("mask_type", [None, G.F16, G.F32])
+@pytest.mark.parametrize("n", [7, 300, 4097])
+def test_soft_max(be, orc, n, mask_type):
+    """softmax(x * scale + mask) over rows [n, 5, 4, 2], the mask [n, 6, 2, 1] broadcast over the
+    batch dims (rows 0..4 of it), against torch's; rows sum to 1."""
+    x = orc.normal((2, 4, 5, n), seed=120 + n) * 4.0
+    m = orc.normal((1, 2, 6, n), seed=121 + n) * 2.0
+    m[..., : n // 3] = -np.inf
+    mdata = orc.fp32_to_fp16(m) if mask_type == G.F16 else m
+    mval = orc.fp16_to_fp32(mdata) if mask_type == G.F16 else m
+    out = {}
+
+    def build(g, ctx, L):
+        out["y"] = g.ggml_soft_max_ext(ctx, L["x"], L["m"] if mask_type is not None else None, 0.7, 0.0)
+        g.ggml_set_output(out["y"])
+        return [out["y"]]
+
+    leaves = {"x": (G.F32, [n, 5, 4, 2], x)}
+    if mask_type is not None:
+        leaves["m"] = (mask_type, [n, 6, 2, 1], mdata)
+    gr = Graph(be, leaves, build)
+    y = gr.run().reshape(2, 4, 5, n)
+    gr.close()
+    logits = torch.from_numpy(x) * 0.7
+    if mask_type is not None:
+        mb = np.broadcast_to(mval[:, :, :5], (1, 2, 5, n))
+        logits = logits + torch.from_numpy(np.concatenate([mb, mb], axis=1).repeat(2, axis=0))
+    want = torch.softmax(logits, dim=-1).numpy()
+    assert np.allclose(y, want, rtol=1e-5, atol=1e-7)
+    assert np.allclose(y.sum(-1), 1.0, atol=1e-5)
+
+
 # -------------------------------------------------------------------- replay, allocation
 
 def test_graph_replay_with_new_inputs(be, orc):

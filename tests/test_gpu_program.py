@@ -10,6 +10,7 @@ import math
 
 import numpy as np
 import pytest
+import torch
 
 from ggml_compiler_amd import gguf, runtime
 
@@ -59,6 +60,34 @@ def test_one_call_program(tmp_path, orc):
         assert s.stats["n_calls"] == 1 and s.stats["stages"]["lin"]["calls"] == 1
         with pytest.raises(ValueError, match="shape"):
             s.run(np.zeros((2, K), np.float32))
+
+
+def test_unfused_glu_and_eager_attention_ops(tmp_path, orc):
+    """A program left unfused (silu then mul rather than swiglu; soft_max over scores with an f16
+    mask rather than flash_attn), with sub, div and gelu_erf: ops.cpp's binary and unary tables."""
+    E, S = 64, 5
+    st = {"name": "f", "params": [_v("a.0", "f32", [E, S], [S, E]), _v("a.1", "f32", [E, S], [S, E]),
+                                  _v("a.2", "f16", [E, S], [S, E])],
+          "outputs": ["%5"],
+          "nodes": [_n(0, "silu", ["a.0"], "f32", [E, S]), _n(1, "mul", ["%0", "a.1"], "f32", [E, S]),
+                    _n(2, "sub", ["%1", "a.0"], "f32", [E, S]), _n(3, "div", ["%2", "c.0"], "f32", [E, S]),
+                    _n(4, "gelu_erf", ["%3"], "f32", [E, S]),
+                    _n(5, "soft_max", ["%4", "a.2"], "f32", [E, S], scale=0.5)]}
+    c = orc.normal((E,), seed=60) + 3.0
+    prog = {"format_version": 3, "symbols": [],
+            "values": [_v("g", "f32", [E, S], [S, E]), _v("u", "f32", [E, S], [S, E]), _v("m", "f16", [E, S], [S, E]),
+                       _v("y", "f32", [E, S], [S, E])],
+            "stages": [st], "entries": [{"name": "main", "inputs": ["g", "u", "m"], "outputs": ["y"],
+                                         "driver": [{"op": "call", "stage": "f", "args": ["g", "u", "m"], "out": ["y"]}]}],
+            "state": []}
+    g, u = orc.normal((S, E), seed=61), orc.normal((S, E), seed=62)
+    m = np.triu(np.full((S, E), -np.inf, np.float32), k=E - S + 1)  # causal-style -inf tail per row
+    with runtime.Session(_write(tmp_path / "f.gguf", prog, [("c.0", c, 0, (E,))])) as s:
+        y = s.run(g, u, m)["y"]  # Session converts values to the input type (f16 here)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a))
+    h = (torch.nn.functional.silu(t(g)) * t(u) - t(g)) / t(c)
+    want = torch.softmax(torch.nn.functional.gelu(h) * 0.5 + t(m), dim=-1).numpy()
+    assert np.allclose(y, want, rtol=1e-5, atol=1e-7)
 
 
 def test_loop_driver(tmp_path):
