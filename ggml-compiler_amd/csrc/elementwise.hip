@@ -186,7 +186,7 @@ bool unary_known(int op) {
     switch (op) {
         case UN_ABS: case UN_NEG: case UN_TANH: case UN_RELU: case UN_SIGMOID: case UN_GELU: case UN_SILU:
         case UN_EXP: case UN_GELU_ERF: case UN_SOFTPLUS: case UN_SQR: case UN_SQRT: case UN_LOG: case UN_SIN:
-        case UN_COS:
+        case UN_COS: case UN_CLAMP:
             return true;
         default:
             return false;
@@ -194,7 +194,7 @@ bool unary_known(int op) {
 }
 
 // y = f(x); the op is uniform over the launch, so the switch is one scalar branch per wave.
-__global__ void k_unary(int op, const float * __restrict__ x, float * __restrict__ y, int64_t n) {
+__global__ void k_unary(int op, const float * __restrict__ x, float * __restrict__ y, int64_t n, float lo, float hi) {
     const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
     const float v = x[i];
@@ -214,9 +214,51 @@ __global__ void k_unary(int op, const float * __restrict__ x, float * __restrict
         case UN_SQRT: r = sqrtf(v); break;
         case UN_LOG: r = logf(v); break;
         case UN_SIN: r = sinf(v); break;
+        case UN_CLAMP: r = fmaxf(fminf(v, hi), lo); break;
         default: r = cosf(v); break;
     }
     y[i] = r;
+}
+
+// One 256-thread block per contiguous row: the mean and then the variance of the row about it, both
+// summed in double and rounded to f32 as ggml-cpu's norm, then (x - mean) / sqrt(var + eps). The
+// last pass reads each element before the same thread writes it, after barriers that end the
+// earlier passes, so y may alias x.
+__global__ __launch_bounds__(256) void k_norm(const float * x, float * y, int n, float eps) {
+    __shared__ double red[2][4];
+    const float * xr = x + (int64_t) blockIdx.x * n;
+    float * yr = y + (int64_t) blockIdx.x * n;
+    const int w = threadIdx.x >> 6;
+    double s = 0.0;
+    for (int i = threadIdx.x; i < n; i += 256) s += (double) xr[i];
+    s = wave_sum_d(s);
+    if ((threadIdx.x & 63) == 0) red[0][w] = s;
+    __syncthreads();
+    const float mean = (float) ((red[0][0] + red[0][1] + red[0][2] + red[0][3]) / (double) n);
+    double s2 = 0.0;
+    for (int i = threadIdx.x; i < n; i += 256) {
+        const float dv = xr[i] - mean;
+        s2 += (double) (dv * dv);
+    }
+    s2 = wave_sum_d(s2);
+    if ((threadIdx.x & 63) == 0) red[1][w] = s2;
+    __syncthreads();
+    const float var = (float) ((red[1][0] + red[1][1] + red[1][2] + red[1][3]) / (double) n);
+    const float sc = 1.0f / sqrtf(var + eps);
+    for (int i = threadIdx.x; i < n; i += 256) yr[i] = (xr[i] - mean) * sc;
+}
+
+// Sum of each contiguous row (in double, rounded to f32) times scale: sum_rows (1) or mean (1 / n).
+__global__ __launch_bounds__(256) void k_row_sum(const float * __restrict__ x, float * __restrict__ y, int n,
+                                                 float scale) {
+    __shared__ double red[4];
+    const float * xr = x + (int64_t) blockIdx.x * n;
+    double s = 0.0;
+    for (int i = threadIdx.x; i < n; i += 256) s += (double) xr[i];
+    s = wave_sum_d(s);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) y[blockIdx.x] = (float) (red[0] + red[1] + red[2] + red[3]) * scale;
 }
 
 // One 256-thread block per row: the row maximum of x * scale + mask, then e^(v - max) written
@@ -434,11 +476,25 @@ void launch_binary(int op, const float * a, const float * b, float * y, int64_t 
     check_launch(op == 0 ? "add" : op == 1 ? "mul" : op == 2 ? "sub" : "div");
 }
 
-void launch_unary(int op, const float * x, float * y, int64_t n, hipStream_t s) {
+void launch_unary(int op, const float * x, float * y, int64_t n, float lo, float hi, hipStream_t s) {
     if (!unary_known(op)) throw std::runtime_error("unary: unknown op " + std::to_string(op));
     if (n == 0) return;
-    k_unary<<<nblk(n, 256), 256, 0, s>>>(op, x, y, n);
+    k_unary<<<nblk(n, 256), 256, 0, s>>>(op, x, y, n, lo, hi);
     check_launch("unary");
+}
+
+void launch_norm(const float * x, float * y, int64_t rows, int64_t n, float eps, hipStream_t s) {
+    if (rows == 0 || n == 0) return;
+    if (rows > INT32_MAX || n > INT32_MAX) throw std::runtime_error("norm: sizes out of range");
+    k_norm<<<(unsigned) rows, 256, 0, s>>>(x, y, (int) n, eps);
+    check_launch("norm");
+}
+
+void launch_row_sum(const float * x, float * y, int64_t rows, int64_t n, float scale, hipStream_t s) {
+    if (rows == 0) return;
+    if (rows > INT32_MAX || n > INT32_MAX) throw std::runtime_error("sum_rows: sizes out of range");
+    k_row_sum<<<(unsigned) rows, 256, 0, s>>>(x, y, (int) n, scale);
+    check_launch("sum_rows");
 }
 
 void launch_soft_max(const float * x, float * y, int64_t n, int64_t r1, int64_t r2, int64_t r3, const void * mask,

@@ -181,9 +181,14 @@ void launch_scale(const float * x, float * y, int64_t n, float sc, float b, hipS
 enum UnaryOp : int {
     UN_ABS = 0, UN_NEG = 1, UN_TANH = 2, UN_RELU = 3, UN_SIGMOID = 4, UN_GELU = 7, UN_SILU = 10, UN_EXP = 11,
     UN_GELU_ERF = 12, UN_SOFTPLUS = 13, UN_SQR = 100, UN_SQRT = 101, UN_LOG = 102, UN_SIN = 103, UN_COS = 104,
+    UN_CLAMP = 105,
 };
 bool unary_known(int op);
-void launch_unary(int op, const float * x, float * y, int64_t n, hipStream_t s);
+// lo / hi: clamp's bounds (unused by the other functions).
+void launch_unary(int op, const float * x, float * y, int64_t n, float lo, float hi, hipStream_t s);
+// Per contiguous row of n: (x - mean) / sqrt(var + eps) (norm), or the sum times scale.
+void launch_norm(const float * x, float * y, int64_t rows, int64_t n, float eps, hipStream_t s);
+void launch_row_sum(const float * x, float * y, int64_t rows, int64_t n, float scale, hipStream_t s);
 // softmax(x * scale + mask) over rows of n; rows = r1 * r2 * r3 (x and y contiguous); mask row
 // (i1, i2 % m2, i3 % m3) at element strides mld, ms2, ms3, f16 when mask_f16, or no mask.
 void launch_soft_max(const float * x, float * y, int64_t n, int64_t r1, int64_t r2, int64_t r3, const void * mask,

@@ -41,7 +41,7 @@ const char * kOpNames[GGML_OP_COUNT] = {"NONE",    "ADD",      "MUL",      "SCAL
                                         "CONT",    "RESHAPE",  "VIEW",     "PERMUTE",  "TRANSPOSE",
                                         "GET_ROWS", "SET_ROWS", "RMS_NORM", "MUL_MAT",  "ROPE",
                                         "FLASH_ATTN_EXT", "ARGMAX", "GLU", "UNARY", "SOFT_MAX",
-                                        "IM2COL", "CONV_2D_DIRECT", "SUB", "DIV"};
+                                        "IM2COL", "CONV_2D_DIRECT", "SUB", "DIV", "NORM", "SUM_ROWS", "MEAN"};
 
 // NULL with the reason recorded.
 ggml_tensor * none(const std::string & why) {
@@ -633,6 +633,38 @@ ggml_tensor * ggml_cos(ggml_context * ctx, ggml_tensor * a) {
 ggml_tensor * ggml_softplus(ggml_context * ctx, ggml_tensor * a) {
     return unary(ctx, a, GGML_UNARY_OP_SOFTPLUS, "ggml_softplus");
 }
+
+ggml_tensor * ggml_clamp(ggml_context * ctx, ggml_tensor * a, float min, float max) {
+    ggml_tensor * t = unary(ctx, a, GGML_UNARY_OP_CLAMP, "ggml_clamp");
+    if (!t) return nullptr;
+    set_param(t, 1, min);
+    set_param(t, 2, max);
+    return t;
+}
+
+ggml_tensor * ggml_norm(ggml_context * ctx, ggml_tensor * a, float eps) {
+    if (!a) return nullptr;
+    ggml_tensor * t = dup_shape(ctx, a, a->type, "ggml_norm");
+    if (!t) return nullptr;
+    set_src(t, GGML_OP_NORM, {a});
+    set_param(t, 0, eps);
+    return t;
+}
+
+namespace {
+ggml_tensor * row_reduce(ggml_context * ctx, ggml_tensor * a, ggml_op op, const char * what) {
+    if (!a) return nullptr;
+    if (a->type != GGML_TYPE_F32) return none(std::string(what) + ": needs an f32 tensor");
+    const int64_t ne[4] = {1, a->ne[1], a->ne[2], a->ne[3]};
+    ggml_tensor * t = new_tensor(ctx, GGML_TYPE_F32, 4, ne, nullptr, 0, what);
+    if (!t) return nullptr;
+    set_src(t, op, {a});
+    return t;
+}
+}  // namespace
+
+ggml_tensor * ggml_sum_rows(ggml_context * ctx, ggml_tensor * a) { return row_reduce(ctx, a, GGML_OP_SUM_ROWS, "ggml_sum_rows"); }
+ggml_tensor * ggml_mean(ggml_context * ctx, ggml_tensor * a) { return row_reduce(ctx, a, GGML_OP_MEAN, "ggml_mean"); }
 
 ggml_tensor * ggml_soft_max_ext(ggml_context * ctx, ggml_tensor * a, ggml_tensor * mask, float scale,
                                 float max_bias) {

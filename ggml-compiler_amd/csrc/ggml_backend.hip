@@ -118,7 +118,7 @@ static_assert(UN_ABS == GGML_UNARY_OP_ABS && UN_NEG == GGML_UNARY_OP_NEG && UN_T
                   UN_SILU == GGML_UNARY_OP_SILU && UN_EXP == GGML_UNARY_OP_EXP &&
                   UN_GELU_ERF == GGML_UNARY_OP_GELU_ERF && UN_SOFTPLUS == GGML_UNARY_OP_SOFTPLUS &&
                   UN_SQR == GGML_UNARY_OP_SQR && UN_SQRT == GGML_UNARY_OP_SQRT && UN_LOG == GGML_UNARY_OP_LOG &&
-                  UN_SIN == GGML_UNARY_OP_SIN && UN_COS == GGML_UNARY_OP_COS,
+                  UN_SIN == GGML_UNARY_OP_SIN && UN_COS == GGML_UNARY_OP_COS && UN_CLAMP == GGML_UNARY_OP_CLAMP,
               "k_unary's numbering is ggml_unary_op's");
 
 bool f32_contig(const ggml_tensor * t) { return t->type == GGML_TYPE_F32 && ggml_is_contiguous(t); }
@@ -447,6 +447,8 @@ enum StepKind {
     S_SWIGLU,
     S_UNARY,
     S_SOFTMAX,
+    S_NORM,
+    S_ROWSUM,
     S_ARGMAX,
     S_ATTN_MULMAT,  // decode attention (split partials) -> mul_mat merging them [-> add]
     S_MULMAT3,      // rms_norm -> mul -> 2 or 3 mul_mats of the one row: one decode-row GEMV
@@ -1014,6 +1016,23 @@ struct Planner {
                 s.in[0] = d(t->src[0]);
                 s.out = o(t);
                 s.n[0] = ggml_nelements(t);
+                std::memcpy(&s.f[0], &t->op_params[1], 4);
+                std::memcpy(&s.f[1], &t->op_params[2], 4);
+                steps.push_back(s);
+                return;
+            }
+            case GGML_OP_NORM:
+            case GGML_OP_SUM_ROWS:
+            case GGML_OP_MEAN: {
+                const ggml_tensor * a = t->src[0];
+                require(f32_contig(a), std::string(ggml_op_name(t->op)) + " " + tname(t) + ": needs a contiguous f32 input");
+                Step s = new_step(t->op == GGML_OP_NORM ? S_NORM : S_ROWSUM);
+                s.in[0] = d(a);
+                s.out = o(t);
+                s.n[0] = ggml_nrows(a);
+                s.n[1] = a->ne[0];
+                if (t->op == GGML_OP_NORM) std::memcpy(&s.f[0], &t->op_params[0], 4);
+                else s.f[0] = t->op == GGML_OP_MEAN ? 1.0f / (float) a->ne[0] : 1.0f;
                 steps.push_back(s);
                 return;
             }
@@ -1280,7 +1299,13 @@ void run_step(const ggml_backend * be, const Step & s) {
             launch_swiglu((const float *) s.in[0], (const float *) s.in[1], (float *) s.out, s.n[0], st);
             return;
         case S_UNARY:
-            launch_unary(s.op, (const float *) s.in[0], (float *) s.out, s.n[0], st);
+            launch_unary(s.op, (const float *) s.in[0], (float *) s.out, s.n[0], s.f[0], s.f[1], st);
+            return;
+        case S_NORM:
+            launch_norm((const float *) s.in[0], (float *) s.out, s.n[0], s.n[1], s.f[0], st);
+            return;
+        case S_ROWSUM:
+            launch_row_sum((const float *) s.in[0], (float *) s.out, s.n[0], s.n[1], s.f[0], st);
             return;
         case S_SOFTMAX:
             launch_soft_max((const float *) s.in[0], (float *) s.out, s.n[0], s.n[1], s.n[2], s.n[3], s.in[1],

@@ -806,6 +806,15 @@ ggml_tensor * emit(ggml_context * ctx, const NodeSpec & n, const std::vector<ggm
     } else if (const auto u = unaries.find(op); u != unaries.end()) {
         need(1, 1);
         t = u->second(ctx, s[0]);
+    } else if (op == "mean" || op == "sum_rows") {
+        need(1, 1);
+        t = op == "mean" ? ggml_mean(ctx, s[0]) : ggml_sum_rows(ctx, s[0]);
+    } else if (op == "clamp") {
+        need(1, 1);
+        t = ggml_clamp(ctx, s[0], (float) n.num("min"), (float) n.num("max"));
+    } else if (op == "norm") {
+        need(1, 1);
+        t = ggml_norm(ctx, s[0], (float) n.num("eps"));
     } else if (op == "cont") {
         need(1, 1);
         t = ggml_cont(ctx, s[0]);

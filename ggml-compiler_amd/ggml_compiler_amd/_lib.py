@@ -231,6 +231,10 @@ SIGNATURES = {
     "ggml_cos": ([p, p], p),
     "ggml_softplus": ([p, p], p),
     "ggml_sub": ([p, p, p], p),
+    "ggml_clamp": ([p, p, f32, f32], p),
+    "ggml_norm": ([p, p, f32], p),
+    "ggml_sum_rows": ([p, p], p),
+    "ggml_mean": ([p, p], p),
     "ggml_div": ([p, p, p], p),
     "ggml_soft_max_ext": ([p, p, p, f32, f32], p),
     "ggml_im2col": ([p, p, p, i32, i32, i32, i32, i32, i32, ctypes.c_bool, i32], p),

@@ -99,6 +99,9 @@ enum ggml_op {
     GGML_OP_CONV_2D_DIRECT,
     GGML_OP_SUB,
     GGML_OP_DIV,
+    GGML_OP_NORM,
+    GGML_OP_SUM_ROWS,
+    GGML_OP_MEAN,
     GGML_OP_COUNT,
 };
 
@@ -119,6 +122,7 @@ enum ggml_unary_op {
     GGML_UNARY_OP_LOG  = 102,
     GGML_UNARY_OP_SIN  = 103,
     GGML_UNARY_OP_COS  = 104,
+    GGML_UNARY_OP_CLAMP = 105, /* ggml's clamp op: op_params[1] min, [2] max */
 };
 
 enum ggml_glu_op {
@@ -259,6 +263,14 @@ GGML_API struct ggml_tensor * ggml_sqrt(struct ggml_context * ctx, struct ggml_t
 GGML_API struct ggml_tensor * ggml_sin(struct ggml_context * ctx, struct ggml_tensor * a);
 GGML_API struct ggml_tensor * ggml_cos(struct ggml_context * ctx, struct ggml_tensor * a);
 GGML_API struct ggml_tensor * ggml_softplus(struct ggml_context * ctx, struct ggml_tensor * a);
+/* min(max(a, min), max) elementwise (ops.cpp clamp) */
+GGML_API struct ggml_tensor * ggml_clamp(struct ggml_context * ctx, struct ggml_tensor * a, float min, float max);
+/* (x - mean) / sqrt(var + eps) per row of a contiguous f32 tensor, no affine (ops.cpp norm) */
+GGML_API struct ggml_tensor * ggml_norm(struct ggml_context * ctx, struct ggml_tensor * a, float eps);
+/* sum / mean of each row of a contiguous f32 tensor -> [1, ne1, ne2, ne3] (ops.cpp:81-100's
+   mean and sum_rows) */
+GGML_API struct ggml_tensor * ggml_sum_rows(struct ggml_context * ctx, struct ggml_tensor * a);
+GGML_API struct ggml_tensor * ggml_mean(struct ggml_context * ctx, struct ggml_tensor * a);
 /* softmax(a * scale + mask) over each row of a contiguous f32 a [n, r1, r2, r3]; mask f32 or
    f16 [n, >= r1, m2, m3] (contiguous, r2 % m2 == 0, r3 % m3 == 0) or NULL; max_bias 0 (no ALiBi)
    (ops.cpp:150-155) */

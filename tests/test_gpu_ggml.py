@@ -502,6 +502,35 @@ def test_unary_sub_div(be, orc):
     assert np.array_equal(got["div"], (a / b).reshape(-1))
 
 
+@pytest.mark.parametrize("n", [1, 96, 5000])
+def test_norm_clamp_row_sums(be, orc, n):
+    """norm (layer norm without affine) against torch's layer_norm, clamp against torch's, sum_rows
+    and mean against float64 sums, over rows [n, 3, 2]."""
+    a = orc.normal((2, 3, n), seed=130 + n) * 2.0 + 0.5
+    outs = {}
+
+    def build(g, ctx, L):
+        outs["norm"] = g.ggml_norm(ctx, L["a"], 1e-5)
+        outs["clamp"] = g.ggml_clamp(ctx, L["a"], -1.0, 0.75)
+        outs["sum"] = g.ggml_sum_rows(ctx, L["a"])
+        outs["mean"] = g.ggml_mean(ctx, L["a"])
+        for t in outs.values():
+            g.ggml_set_output(t)
+        return list(outs.values())
+
+    gr = Graph(be, {"a": (G.F32, [n, 3, 2], a)}, build)
+    gr.run()
+    got = {k: G.get_data(t, np.float32) for k, t in outs.items()}
+    gr.close()
+    x = torch.from_numpy(a)
+    want = torch.nn.functional.layer_norm(x, (n,), eps=1e-5).numpy().reshape(-1)
+    assert np.allclose(got["norm"], want, rtol=1e-5, atol=2e-5)
+    assert np.array_equal(got["clamp"], np.clip(a, -1.0, 0.75).reshape(-1))
+    s64 = a.astype(np.float64).sum(-1).reshape(-1)
+    assert np.allclose(got["sum"], s64, rtol=1e-6, atol=1e-5)
+    assert np.allclose(got["mean"], s64 / n, rtol=1e-6, atol=1e-6)
+
+
 @pytest.mark.parametrize("mask_type", [None, G.F16, G.F32])
 @pytest.mark.parametrize("n", [7, 300, 4097])
 def test_soft_max(be, orc, n, mask_type):

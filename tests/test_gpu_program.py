@@ -90,6 +90,28 @@ def test_unfused_glu_and_eager_attention_ops(tmp_path, orc):
     assert np.allclose(y, want, rtol=1e-5, atol=1e-7)
 
 
+def test_layer_norm_gelu_mean_program(tmp_path, orc):
+    """A GPT-2-style piece: norm, then * weight + bias from the GGUF, gelu (tanh form), clamp, and
+    the mean of each row."""
+    E, S = 96, 3
+    st = {"name": "ln", "params": [_v("a.0", "f32", [E, S], [S, E])], "outputs": ["%5"],
+          "nodes": [_n(0, "norm", ["a.0"], "f32", [E, S], eps=1e-5), _n(1, "mul", ["%0", "c.0"], "f32", [E, S]),
+                    _n(2, "add", ["%1", "c.1"], "f32", [E, S]), _n(3, "gelu_tanh", ["%2"], "f32", [E, S]),
+                    _n(4, "clamp", ["%3"], "f32", [E, S], min=-0.1, max=2.0), _n(5, "mean", ["%4"], "f32", [1, S])]}
+    w, b = orc.normal((E,), seed=70) + 1.0, orc.normal((E,), seed=71)
+    prog = {"format_version": 3, "symbols": [],
+            "values": [_v("x", "f32", [E, S], [S, E]), _v("y", "f32", [1, S], [S, 1])],
+            "stages": [st], "entries": [{"name": "main", "inputs": ["x"], "outputs": ["y"],
+                                         "driver": [{"op": "call", "stage": "ln", "args": ["x"], "out": ["y"]}]}],
+            "state": []}
+    x = orc.normal((S, E), seed=72) * 3.0
+    with runtime.Session(_write(tmp_path / "ln.gguf", prog, [("c.0", w, 0, (E,)), ("c.1", b, 0, (E,))])) as s:
+        y = s.run(x)["y"]
+    h = torch.nn.functional.layer_norm(torch.from_numpy(x), (E,), torch.from_numpy(w), torch.from_numpy(b), eps=1e-5)
+    want = torch.clamp(torch.nn.functional.gelu(h, approximate="tanh"), -0.1, 2.0).mean(-1, keepdim=True).numpy()
+    assert np.allclose(y, want, rtol=1e-5, atol=1e-6)
+
+
 def test_loop_driver(tmp_path):
     """h_{k+1} = h_k * s_k + R[k] (carry from h0, per-iteration scalars, slices of R); the causal
     mask row of position start + k; both collected per iteration; stop once argmax(h) is 7."""
