@@ -405,6 +405,18 @@ __global__ void k_cpy(const uint8_t * __restrict__ src, int st, uint8_t * __rest
     else *reinterpret_cast<uint16_t *>(dst + dof) = f2h(v);
 }
 
+__global__ void k_repeat(const uint8_t * __restrict__ src, float * __restrict__ dst, Cpy4 g, int64_t n) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    int64_t r = i, so = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        so += ((r % g.dne[k]) % g.sne[k]) * g.snb[k];
+        r /= g.dne[k];
+    }
+    dst[i] = *reinterpret_cast<const float *>(src + so);
+}
+
 __global__ void k_scale(const float * __restrict__ x, float * __restrict__ y, int64_t n, float sc, float b) {
     const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
@@ -481,6 +493,12 @@ void launch_unary(int op, const float * x, float * y, int64_t n, float lo, float
     if (n == 0) return;
     k_unary<<<nblk(n, 256), 256, 0, s>>>(op, x, y, n, lo, hi);
     check_launch("unary");
+}
+
+void launch_repeat(const float * src, float * dst, const Cpy4 & g, int64_t n, hipStream_t s) {
+    if (n == 0) return;
+    k_repeat<<<nblk(n, 256), 256, 0, s>>>((const uint8_t *) src, dst, g, n);
+    check_launch("repeat");
 }
 
 void launch_norm(const float * x, float * y, int64_t rows, int64_t n, float eps, hipStream_t s) {

@@ -41,7 +41,7 @@ const char * kOpNames[GGML_OP_COUNT] = {"NONE",    "ADD",      "MUL",      "SCAL
                                         "CONT",    "RESHAPE",  "VIEW",     "PERMUTE",  "TRANSPOSE",
                                         "GET_ROWS", "SET_ROWS", "RMS_NORM", "MUL_MAT",  "ROPE",
                                         "FLASH_ATTN_EXT", "ARGMAX", "GLU", "UNARY", "SOFT_MAX",
-                                        "IM2COL", "CONV_2D_DIRECT", "SUB", "DIV", "NORM", "SUM_ROWS", "MEAN"};
+                                        "IM2COL", "CONV_2D_DIRECT", "SUB", "DIV", "NORM", "SUM_ROWS", "MEAN", "REPEAT", "CONCAT"};
 
 // NULL with the reason recorded.
 ggml_tensor * none(const std::string & why) {
@@ -662,6 +662,34 @@ ggml_tensor * row_reduce(ggml_context * ctx, ggml_tensor * a, ggml_op op, const 
     return t;
 }
 }  // namespace
+
+ggml_tensor * ggml_repeat_4d(ggml_context * ctx, ggml_tensor * a, int64_t ne0, int64_t ne1, int64_t ne2, int64_t ne3) {
+    if (!a) return nullptr;
+    const int64_t ne[4] = {ne0, ne1, ne2, ne3};
+    for (int k = 0; k < 4; k++)
+        if (ne[k] <= 0 || a->ne[k] <= 0 || ne[k] % a->ne[k] != 0)
+            return none("ggml_repeat_4d: cannot tile " + shape(a) + " to a shape that is not a multiple of it");
+    ggml_tensor * t = new_tensor(ctx, a->type, 4, ne, nullptr, 0, "ggml_repeat_4d");
+    if (!t) return nullptr;
+    set_src(t, GGML_OP_REPEAT, {a});
+    return t;
+}
+
+ggml_tensor * ggml_concat(ggml_context * ctx, ggml_tensor * a, ggml_tensor * b, int dim) {
+    if (!a || !b) return nullptr;
+    if (dim < 0 || dim > 3 || a->type != b->type) return none("ggml_concat: dim 0-3 and one type");
+    int64_t ne[4];
+    for (int k = 0; k < 4; k++) {
+        if (k != dim && a->ne[k] != b->ne[k])
+            return none("ggml_concat: " + shape(a) + " and " + shape(b) + " differ outside dim " + std::to_string(dim));
+        ne[k] = k == dim ? a->ne[k] + b->ne[k] : a->ne[k];
+    }
+    ggml_tensor * t = new_tensor(ctx, a->type, 4, ne, nullptr, 0, "ggml_concat");
+    if (!t) return nullptr;
+    set_src(t, GGML_OP_CONCAT, {a, b});
+    t->op_params[0] = dim;
+    return t;
+}
 
 ggml_tensor * ggml_sum_rows(ggml_context * ctx, ggml_tensor * a) { return row_reduce(ctx, a, GGML_OP_SUM_ROWS, "ggml_sum_rows"); }
 ggml_tensor * ggml_mean(ggml_context * ctx, ggml_tensor * a) { return row_reduce(ctx, a, GGML_OP_MEAN, "ggml_mean"); }

@@ -449,6 +449,7 @@ enum StepKind {
     S_SOFTMAX,
     S_NORM,
     S_ROWSUM,
+    S_REPEAT,
     S_ARGMAX,
     S_ATTN_MULMAT,  // decode attention (split partials) -> mul_mat merging them [-> add]
     S_MULMAT3,      // rms_norm -> mul -> 2 or 3 mul_mats of the one row: one decode-row GEMV
@@ -1021,6 +1022,49 @@ struct Planner {
                 steps.push_back(s);
                 return;
             }
+            case GGML_OP_REPEAT: {
+                const ggml_tensor * a = t->src[0];
+                require(a->type == GGML_TYPE_F32 && a->nb[0] == 4 && f32_contig(t),
+                        "repeat " + tname(t) + ": an f32 source with unit element stride");
+                Step s = new_step(S_REPEAT);
+                s.in[0] = d(a);
+                s.out = o(t);
+                for (int k = 0; k < 4; k++) {
+                    s.g.sne[k] = a->ne[k];
+                    s.g.snb[k] = (int64_t) a->nb[k];
+                    s.g.dne[k] = t->ne[k];
+                    s.g.dnb[k] = (int64_t) t->nb[k];
+                }
+                s.n[0] = ggml_nelements(t);
+                steps.push_back(s);
+                return;
+            }
+            case GGML_OP_CONCAT: {
+                // Two copies into the halves of the result: a at offset 0, b after a along dim.
+                const int dim = t->op_params[0];
+                const ggml_tensor * src[2] = {t->src[0], t->src[1]};
+                require((t->type == GGML_TYPE_F32 || t->type == GGML_TYPE_F16) && ggml_is_contiguous(t) &&
+                            src[0]->nb[0] % ggml_tsize(t->type) == 0 && src[1]->nb[0] % ggml_tsize(t->type) == 0,
+                        "concat " + tname(t) + ": f32 / f16 operands");
+                for (int h = 0; h < 2; h++) {
+                    const ggml_tensor * a = src[h];
+                    Step s = new_step(S_CPY);
+                    s.type = a->type;
+                    s.op = t->type;
+                    s.in[0] = d(a);
+                    char * base = static_cast<char *>(o(t));
+                    s.out = base && h == 1 ? base + src[0]->ne[dim] * t->nb[dim] : base;
+                    for (int k = 0; k < 4; k++) {
+                        s.g.sne[k] = a->ne[k];
+                        s.g.snb[k] = (int64_t) a->nb[k];
+                        s.g.dne[k] = a->ne[k];
+                        s.g.dnb[k] = (int64_t) t->nb[k];
+                    }
+                    s.n[0] = ggml_nelements(a);
+                    steps.push_back(s);
+                }
+                return;
+            }
             case GGML_OP_NORM:
             case GGML_OP_SUM_ROWS:
             case GGML_OP_MEAN: {
@@ -1300,6 +1344,9 @@ void run_step(const ggml_backend * be, const Step & s) {
             return;
         case S_UNARY:
             launch_unary(s.op, (const float *) s.in[0], (float *) s.out, s.n[0], s.f[0], s.f[1], st);
+            return;
+        case S_REPEAT:
+            launch_repeat((const float *) s.in[0], (float *) s.out, s.g, s.n[0], st);
             return;
         case S_NORM:
             launch_norm((const float *) s.in[0], (float *) s.out, s.n[0], s.n[1], s.f[0], st);

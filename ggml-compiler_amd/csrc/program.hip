@@ -812,6 +812,14 @@ ggml_tensor * emit(ggml_context * ctx, const NodeSpec & n, const std::vector<ggm
     } else if (op == "clamp") {
         need(1, 1);
         t = ggml_clamp(ctx, s[0], (float) n.num("min"), (float) n.num("max"));
+    } else if (op == "repeat") {
+        need(1, 1);
+        for (int k = 0; k < 4; k++)
+            if (s[0]->ne[k] <= 0 || n.ne[k] % s[0]->ne[k] != 0) node_fail(n, "cannot tile " + ne_str(s[0]->ne) + " to " + ne_str(n.ne));
+        t = ggml_repeat_4d(ctx, s[0], n.ne[0], n.ne[1], n.ne[2], n.ne[3]);
+    } else if (op == "concat") {
+        need(2, 2);
+        t = ggml_concat(ctx, s[0], s[1], (int) n.integer("dim"));
     } else if (op == "norm") {
         need(1, 1);
         t = ggml_norm(ctx, s[0], (float) n.num("eps"));

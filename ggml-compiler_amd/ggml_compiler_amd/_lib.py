@@ -235,6 +235,8 @@ SIGNATURES = {
     "ggml_norm": ([p, p, f32], p),
     "ggml_sum_rows": ([p, p], p),
     "ggml_mean": ([p, p], p),
+    "ggml_repeat_4d": ([p, p, i64, i64, i64, i64], p),
+    "ggml_concat": ([p, p, p, i32], p),
     "ggml_div": ([p, p, p], p),
     "ggml_soft_max_ext": ([p, p, p, f32, f32], p),
     "ggml_im2col": ([p, p, p, i32, i32, i32, i32, i32, i32, ctypes.c_bool, i32], p),

@@ -102,6 +102,8 @@ enum ggml_op {
     GGML_OP_NORM,
     GGML_OP_SUM_ROWS,
     GGML_OP_MEAN,
+    GGML_OP_REPEAT,
+    GGML_OP_CONCAT,
     GGML_OP_COUNT,
 };
 
@@ -271,6 +273,12 @@ GGML_API struct ggml_tensor * ggml_norm(struct ggml_context * ctx, struct ggml_t
    mean and sum_rows) */
 GGML_API struct ggml_tensor * ggml_sum_rows(struct ggml_context * ctx, struct ggml_tensor * a);
 GGML_API struct ggml_tensor * ggml_mean(struct ggml_context * ctx, struct ggml_tensor * a);
+/* a tiled to [ne0, ne1, ne2, ne3] (each a multiple of a's; ops.cpp repeat) */
+GGML_API struct ggml_tensor * ggml_repeat_4d(struct ggml_context * ctx, struct ggml_tensor * a, int64_t ne0, int64_t ne1,
+                                             int64_t ne2, int64_t ne3);
+/* a then b along dim (0-3), the other dims equal, one type (ops.cpp concat) */
+GGML_API struct ggml_tensor * ggml_concat(struct ggml_context * ctx, struct ggml_tensor * a, struct ggml_tensor * b,
+                                          int dim);
 /* softmax(a * scale + mask) over each row of a contiguous f32 a [n, r1, r2, r3]; mask f32 or
    f16 [n, >= r1, m2, m3] (contiguous, r2 % m2 == 0, r3 % m3 == 0) or NULL; max_bias 0 (no ALiBi)
    (ops.cpp:150-155) */

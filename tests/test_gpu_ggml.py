@@ -531,6 +531,35 @@ def test_norm_clamp_row_sums(be, orc, n):
     assert np.allclose(got["mean"], s64 / n, rtol=1e-6, atol=1e-6)
 
 
+def test_repeat_and_concat(be, orc):
+    """repeat_4d tiles a [5, 2, 1] tensor to [10, 6, 3]; concat along each dim, one operand a
+    permuted (strided) view; both bit-exact against numpy."""
+    a = orc.normal((1, 2, 5), seed=140)
+    x = orc.normal((3, 4, 6), seed=141)   # ggml [6, 4, 3]
+    y = orc.normal((3, 4, 6), seed=142)
+    outs = {}
+
+    def build(g, ctx, L):
+        outs["rep"] = g.ggml_repeat_4d(ctx, L["a"], 10, 6, 3, 1)
+        for dim in range(3):
+            outs[f"cat{dim}"] = g.ggml_concat(ctx, L["x"], L["y"], dim)
+        yp = g.ggml_permute(ctx, L["y"], 1, 0, 2, 3)  # [4, 6, 3], strided
+        outs["catp"] = g.ggml_concat(ctx, g.ggml_cont(ctx, g.ggml_permute(ctx, L["x"], 1, 0, 2, 3)), yp, 2)
+        for t in outs.values():
+            g.ggml_set_output(t)
+        return list(outs.values())
+
+    gr = Graph(be, {"a": (G.F32, [5, 2, 1], a), "x": (G.F32, [6, 4, 3], x), "y": (G.F32, [6, 4, 3], y)}, build)
+    gr.run()
+    got = {k: G.get_data(t, np.float32) for k, t in outs.items()}
+    gr.close()
+    assert np.array_equal(got["rep"], np.tile(a, (3, 3, 2)).reshape(-1))
+    for dim in range(3):  # ggml dim d is numpy axis 2 - d
+        assert np.array_equal(got[f"cat{dim}"], np.concatenate([x, y], axis=2 - dim).reshape(-1)), dim
+    xt, yt = x.transpose(0, 2, 1), y.transpose(0, 2, 1)
+    assert np.array_equal(got["catp"], np.concatenate([xt, yt], axis=0).reshape(-1))
+
+
 @pytest.mark.parametrize("mask_type", [None, G.F16, G.F32])
 @pytest.mark.parametrize("n", [7, 300, 4097])
 def test_soft_max(be, orc, n, mask_type):
