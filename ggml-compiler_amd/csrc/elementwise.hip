@@ -180,6 +180,27 @@ __global__ void k_binary(int op, const float * __restrict__ a, const float * __r
     y[i] = op == 0 ? av + bv : op == 1 ? av * bv : op == 2 ? av - bv : av / bv;
 }
 
+// b repeated over a along every dim (ggml_can_repeat(b, a)): element (i0, i1, i2, i3) of a meets
+// element (i0 % bne0, i1 % bne1, i2 % bne2, i3 % bne3) of b. Both contiguous.
+struct Bcast4 {
+    int64_t ane[4], bne[4];
+};
+
+__global__ void k_binary_bcast(int op, const float * __restrict__ a, const float * __restrict__ b,
+                               float * __restrict__ y, int64_t n, Bcast4 g) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    int64_t r = i, bi = 0, bstride = 1;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        bi += (r % g.ane[k]) % g.bne[k] * bstride;
+        r /= g.ane[k];
+        bstride *= g.bne[k];
+    }
+    const float av = a[i], bv = b[bi];
+    y[i] = op == 0 ? av + bv : op == 1 ? av * bv : op == 2 ? av - bv : av / bv;
+}
+
 // ----------------------------------------------------------------------- unary, softmax
 
 bool unary_known(int op) {
@@ -248,9 +269,10 @@ __global__ __launch_bounds__(256) void k_norm(const float * x, float * y, int n,
     for (int i = threadIdx.x; i < n; i += 256) yr[i] = (xr[i] - mean) * sc;
 }
 
-// Sum of each contiguous row (in double, rounded to f32) times scale: sum_rows (1) or mean (1 / n).
+// Sum of each contiguous row in double, rounded to f32 (ggml_sum_rows); mean: that f32 sum divided
+// by (float) n (ggml_mean: the rounded sum, then one f32 division).
 __global__ __launch_bounds__(256) void k_row_sum(const float * __restrict__ x, float * __restrict__ y, int n,
-                                                 float scale) {
+                                                 int mean) {
     __shared__ double red[4];
     const float * xr = x + (int64_t) blockIdx.x * n;
     double s = 0.0;
@@ -258,7 +280,10 @@ __global__ __launch_bounds__(256) void k_row_sum(const float * __restrict__ x, f
     s = wave_sum_d(s);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
     __syncthreads();
-    if (threadIdx.x == 0) y[blockIdx.x] = (float) (red[0] + red[1] + red[2] + red[3]) * scale;
+    if (threadIdx.x == 0) {
+        const float sum = (float) (red[0] + red[1] + red[2] + red[3]);
+        y[blockIdx.x] = mean ? sum / (float) n : sum;
+    }
 }
 
 // One 256-thread block per row: the row maximum of x * scale + mask, then e^(v - max) written
@@ -488,6 +513,21 @@ void launch_binary(int op, const float * a, const float * b, float * y, int64_t 
     check_launch(op == 0 ? "add" : op == 1 ? "mul" : op == 2 ? "sub" : "div");
 }
 
+void launch_binary_bcast(int op, const float * a, const float * b, float * y, const int64_t * ane, const int64_t * bne,
+                         hipStream_t s) {
+    Bcast4 g;
+    int64_t n = 1;
+    for (int k = 0; k < 4; k++) {
+        if (bne[k] <= 0 || ane[k] % bne[k] != 0) throw std::runtime_error("binary: the second operand does not repeat over the first");
+        g.ane[k] = ane[k];
+        g.bne[k] = bne[k];
+        n *= ane[k];
+    }
+    if (n == 0) return;
+    k_binary_bcast<<<nblk(n, 256), 256, 0, s>>>(op, a, b, y, n, g);
+    check_launch(op == 0 ? "add" : op == 1 ? "mul" : op == 2 ? "sub" : "div");
+}
+
 void launch_unary(int op, const float * x, float * y, int64_t n, float lo, float hi, hipStream_t s) {
     if (!unary_known(op)) throw std::runtime_error("unary: unknown op " + std::to_string(op));
     if (n == 0) return;
@@ -508,10 +548,10 @@ void launch_norm(const float * x, float * y, int64_t rows, int64_t n, float eps,
     check_launch("norm");
 }
 
-void launch_row_sum(const float * x, float * y, int64_t rows, int64_t n, float scale, hipStream_t s) {
+void launch_row_sum(const float * x, float * y, int64_t rows, int64_t n, bool mean, hipStream_t s) {
     if (rows == 0) return;
     if (rows > INT32_MAX || n > INT32_MAX) throw std::runtime_error("sum_rows: sizes out of range");
-    k_row_sum<<<(unsigned) rows, 256, 0, s>>>(x, y, (int) n, scale);
+    k_row_sum<<<(unsigned) rows, 256, 0, s>>>(x, y, (int) n, mean ? 1 : 0);
     check_launch("sum_rows");
 }
 

@@ -186,11 +186,11 @@ enum UnaryOp : int {
 bool unary_known(int op);
 // lo / hi: clamp's bounds (unused by the other functions).
 void launch_unary(int op, const float * x, float * y, int64_t n, float lo, float hi, hipStream_t s);
-// Per contiguous row of n: (x - mean) / sqrt(var + eps) (norm), or the sum times scale.
+// Per contiguous row of n: (x - mean) / sqrt(var + eps) (norm); the sum, or the mean (sum / n).
 void launch_norm(const float * x, float * y, int64_t rows, int64_t n, float eps, hipStream_t s);
 // dst (contiguous f32, shape g.dne) = src tiled: element c of dst reads src at c % g.sne (byte strides g.snb).
 void launch_repeat(const float * src, float * dst, const Cpy4 & g, int64_t n, hipStream_t s);
-void launch_row_sum(const float * x, float * y, int64_t rows, int64_t n, float scale, hipStream_t s);
+void launch_row_sum(const float * x, float * y, int64_t rows, int64_t n, bool mean, hipStream_t s);
 // softmax(x * scale + mask) over rows of n; rows = r1 * r2 * r3 (x and y contiguous); mask row
 // (i1, i2 % m2, i3 % m3) at element strides mld, ms2, ms3, f16 when mask_f16, or no mask.
 void launch_soft_max(const float * x, float * y, int64_t n, int64_t r1, int64_t r2, int64_t r3, const void * mask,

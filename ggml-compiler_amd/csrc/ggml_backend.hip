@@ -50,6 +50,10 @@ void launch_get_rows(int type, const void * tab, int64_t nrows_tab, int64_t D, c
                      float * out, hipStream_t s);
 void launch_swiglu(const float * g, const float * u, float * y, int64_t n, hipStream_t s);
 void launch_binary(int op, const float * a, const float * b, float * y, int64_t n, int64_t nb, hipStream_t s);
+void launch_mul_mat_f(bool a_f16, const void * a, const int64_t * ane, const int64_t * anb_el, const float * b,
+                      const int64_t * bne, const int64_t * bnb_el, float * out, hipStream_t s);
+void launch_binary_bcast(int op, const float * a, const float * b, float * y, const int64_t * ane, const int64_t * bne,
+                         hipStream_t s);
 void launch_argmax(const float * x, int64_t ldx, int64_t rows, int64_t n, int32_t * out, hipStream_t s);
 int decode_group(int GT, int max_kv);
 int decode_splits(int D, int G, int n_kv, int max_split);
@@ -457,6 +461,7 @@ enum StepKind {
     S_SETROWS2,     // two set_rows of the same indices
     S_ROPE_TABLE,   // the (cos, sin) table of one position for S_QKV_ROPE
     S_QKV_ROPE,     // q / k / v GEMVs with q / k rope and k / v cache writes in the epilogue
+    S_MULMAT_F,     // mul_mat of an f32 / f16 first operand (activations, KV-cache views)
 };
 
 // One launch sequence with every argument it takes; compared byte for byte to decide whether a
@@ -627,6 +632,34 @@ struct Planner {
         if (!row) {
             const int64_t B = is_kquant(w->type) ? std::min<int64_t>(M, 8) : M;
             ws_need = std::max(ws_need, act_layout(w->type, B, K).total);
+        }
+        steps.push_back(s);
+    }
+
+    // mul_mat(a, b) with a f32 / f16 (any strides, innermost contiguous) and b f32 rows (any
+    // strides, innermost contiguous): a's batch repeat-interleaved over b's (grouped-query heads).
+    void mulmat_float(const ggml_tensor * mm) {
+        const ggml_tensor *a = mm->src[0], *b = mm->src[1];
+        const size_t ea = ggml_type_size(a->type);
+        require(b->type == GGML_TYPE_F32, "mul_mat " + tname(mm) + ": an f32 / f16 first operand needs f32 rows as the second");
+        require(a->nb[0] == ea && b->nb[0] == 4, "mul_mat " + tname(mm) + ": both operands need contiguous rows (add a cont)");
+        for (int k = 1; k < 4; k++)
+            require(a->nb[k] % ea == 0 && b->nb[k] % 4 == 0, "mul_mat " + tname(mm) + ": strides are not whole elements");
+        require(a->ne[0] == b->ne[0] && b->ne[2] % a->ne[2] == 0 && b->ne[3] % a->ne[3] == 0,
+                "mul_mat " + tname(mm) + ": cannot multiply " + tname(a) + " by " + tname(b));
+        require(ggml_is_contiguous(mm), "mul_mat " + tname(mm) + ": the result must be contiguous");
+        Step s = new_step(S_MULMAT_F);
+        s.type = a->type;
+        s.in[0] = d(a);
+        s.in[1] = d(b);
+        s.out = o(mm);
+        for (int k = 0; k < 4; k++) {
+            s.m[k] = a->ne[k];
+            s.n[k] = b->ne[k];
+        }
+        for (int k = 1; k < 4; k++) {
+            s.m[3 + k] = (int64_t) (a->nb[k] / ea);
+            s.n[3 + k] = (int64_t) (b->nb[k] / 4);
         }
         steps.push_back(s);
     }
@@ -827,6 +860,7 @@ struct Planner {
                 return;
             case GGML_OP_MUL_MAT:
                 require(t->src[1]->ne[2] % std::max<int64_t>(1, t->src[0]->ne[2]) == 0, "mul_mat: batch mismatch");
+                if (t->src[0]->type == GGML_TYPE_F32 || t->src[0]->type == GGML_TYPE_F16) return mulmat_float(t);
                 return mulmat(t, t->src[1], nullptr, 0.0f, nullptr, t);
             case GGML_OP_RMS_NORM:
                 return rmsnorm(t, nullptr, t);
@@ -835,9 +869,9 @@ struct Planner {
             case GGML_OP_DIV:
             case GGML_OP_MUL: {
                 const ggml_tensor *a = t->src[0], *b = t->src[1];
-                require(f32_contig(a) && f32_contig(b) && prefix_broadcast(b, a),
+                require(f32_contig(a) && f32_contig(b) && ggml_can_repeat(b, a),
                         std::string(ggml_op_name(t->op)) + " " + tname(t) +
-                            ": needs contiguous f32 operands, the second of a leading-dims shape of the first");
+                            ": needs contiguous f32 operands, the second repeating over the first");
                 Step s = new_step(S_BINARY);
                 s.op = t->op == GGML_OP_ADD ? 0 : t->op == GGML_OP_MUL ? 1 : t->op == GGML_OP_SUB ? 2 : 3;
                 s.in[0] = d(a);
@@ -845,6 +879,11 @@ struct Planner {
                 s.out = o(t);
                 s.n[0] = ggml_nelements(a);
                 s.n[1] = ggml_nelements(b);
+                s.n[2] = prefix_broadcast(b, a) ? 0 : 1;  // 1: per-dim broadcast
+                for (int k = 0; k < 4; k++) {
+                    s.m[k] = a->ne[k];
+                    s.m[4 + k] = b->ne[k];
+                }
                 steps.push_back(s);
                 return;
             }
@@ -1076,7 +1115,7 @@ struct Planner {
                 s.n[0] = ggml_nrows(a);
                 s.n[1] = a->ne[0];
                 if (t->op == GGML_OP_NORM) std::memcpy(&s.f[0], &t->op_params[0], 4);
-                else s.f[0] = t->op == GGML_OP_MEAN ? 1.0f / (float) a->ne[0] : 1.0f;
+                else s.op = t->op == GGML_OP_MEAN;
                 steps.push_back(s);
                 return;
             }
@@ -1300,7 +1339,8 @@ void run_step(const ggml_backend * be, const Step & s) {
                             s.n[2], s.f[0], st);
             return;
         case S_BINARY:
-            launch_binary(s.op, (const float *) s.in[0], (const float *) s.in[1], (float *) s.out, s.n[0], s.n[1], st);
+            if (s.n[2]) launch_binary_bcast(s.op, (const float *) s.in[0], (const float *) s.in[1], (float *) s.out, &s.m[0], &s.m[4], st);
+            else launch_binary(s.op, (const float *) s.in[0], (const float *) s.in[1], (float *) s.out, s.n[0], s.n[1], st);
             return;
         case S_SCALE:
             launch_scale((const float *) s.in[0], (float *) s.out, s.n[0], s.f[0], s.f[1], st);
@@ -1351,8 +1391,14 @@ void run_step(const ggml_backend * be, const Step & s) {
         case S_NORM:
             launch_norm((const float *) s.in[0], (float *) s.out, s.n[0], s.n[1], s.f[0], st);
             return;
+        case S_MULMAT_F: {
+            const int64_t anb[4] = {1, s.m[4], s.m[5], s.m[6]}, bnb[4] = {1, s.n[4], s.n[5], s.n[6]};
+            launch_mul_mat_f(s.type == GGML_TYPE_F16, s.in[0], &s.m[0], anb, (const float *) s.in[1], &s.n[0], bnb,
+                             (float *) s.out, st);
+            return;
+        }
         case S_ROWSUM:
-            launch_row_sum((const float *) s.in[0], (float *) s.out, s.n[0], s.n[1], s.f[0], st);
+            launch_row_sum((const float *) s.in[0], (float *) s.out, s.n[0], s.n[1], s.op != 0, st);
             return;
         case S_SOFTMAX:
             launch_soft_max((const float *) s.in[0], (float *) s.out, s.n[0], s.n[1], s.n[2], s.n[3], s.in[1],

@@ -364,8 +364,10 @@ def test_supports_op_and_off_path_errors(be, orc):
     assert not g.ggml_backend_supports_op(be.be, g.ggml_flash_attn_ext(ctx, q, k, k, None, 0.1, 0.0, 0.0))
     w = g.ggml_new_tensor_2d(ctx, G.F32, 64, 8)
     x = g.ggml_new_tensor_2d(ctx, G.F32, 64, 1)
-    assert not g.ggml_backend_supports_op(be.be, g.ggml_mul_mat(ctx, w, x))  # f32 weights are off the path
-    assert "weight must be a whole" in g.ggml_last_error().decode()
+    assert g.ggml_backend_supports_op(be.be, g.ggml_mul_mat(ctx, w, x))  # activation x activation
+    xh = g.ggml_new_tensor_2d(ctx, G.F16, 64, 1)
+    assert not g.ggml_backend_supports_op(be.be, g.ggml_mul_mat(ctx, w, xh))  # f16 rows as the second operand
+    assert "needs f32 rows" in g.ggml_last_error().decode()
     rope = g.ggml_rope_ext(ctx, g.ggml_new_tensor_3d(ctx, G.F32, 64, 2, 1), g.ggml_new_tensor_1d(ctx, G.I32, 1),
                            None, 64, 0, 0, 1e4, 1, 0, 1, 32, 1)
     assert not g.ggml_backend_supports_op(be.be, rope)
@@ -376,6 +378,100 @@ def test_supports_op_and_off_path_errors(be, orc):
     assert g.ggml_backend_graph_compute(be.be, gr) == -1
     assert "no memory" in g.ggml_last_error().decode()
     g.ggml_free(ctx)
+
+
+# ------------------------------------------------------------ activation x activation mul_mat
+
+def _mul_mat_ref(a, b, a_f16):
+    """ggml_mul_mat's closed form (ggml_compiler/ir/ops.py:201-211) in float64 over numpy arrays in
+    PyTorch order: a [..., N, K], b [..., M, K] -> [..., M, N], a's batch dims repeat-interleaved
+    over b's. With an f16 a, b is rounded to f16 first (ggml-cpu's vec_dot_type conversion)."""
+    rank = max(a.ndim, b.ndim)
+    a = a.reshape((1,) * (rank - a.ndim) + a.shape).astype(np.float64)
+    b = b.reshape((1,) * (rank - b.ndim) + b.shape)
+    if a_f16:
+        b = b.astype(np.float16)
+    b = b.astype(np.float64)
+    for d in range(rank - 2):
+        if a.shape[d] != b.shape[d]:
+            a = np.repeat(a, b.shape[d] // a.shape[d], axis=d)
+    return b @ np.swapaxes(a, -1, -2)
+
+
+@pytest.mark.parametrize("ashape,bshape", [
+    ((8, 16), (5, 16)),              # the reference's cases (tests/unit/test_runtime_ops.py:86-95)
+    ((8, 16), (3, 5, 16)),
+    ((3, 8, 16), (3, 5, 16)),
+    ((2, 8, 16), (4, 5, 16)),        # grouped-query: a's batch repeat-interleaved
+    ((2, 3, 8, 16), (2, 3, 5, 16)),
+    ((8, 100, 128), (32, 1, 128)),   # decode Q·Kᵀ: 8 KV heads, 32 query heads, one query row
+    ((2, 70, 33), (6, 130, 33)),     # ragged tiles in every direction
+])
+@pytest.mark.parametrize("a_type", [G.F32, G.F16])
+def test_mul_mat_activations(be, orc, ashape, bshape, a_type):
+    """mul_mat of an f32 / f16 first operand (an activation, a KV-cache view) by f32 rows against
+    the float64 closed form: 1e-5 by the parity metric (the reference's f32 bar)."""
+    a = orc.normal(ashape, seed=160)
+    b = orc.normal(bshape, seed=161)
+    a_dev = a.astype(np.float16).view(np.uint16) if a_type == G.F16 else a
+    gr = Graph(be, {"a": (a_type, list(reversed(ashape)), a_dev), "b": (G.F32, list(reversed(bshape)), b)},
+               lambda g, ctx, L: g.ggml_mul_mat(ctx, L["a"], L["b"]))
+    got = gr.run()
+    gr.close()
+    a_used = a.astype(np.float16).astype(np.float32) if a_type == G.F16 else a
+    want = _mul_mat_ref(a_used, b, a_type == G.F16)
+    assert orc.parity(got.reshape(want.shape), want) < 1e-5
+
+
+def test_mul_mat_strided_operands(be, orc):
+    """Both operands as permuted views (q stored [Sq, H, D] read as [H, Sq, D]; k stored [n, Hkv, D]
+    read as [Hkv, n, D]): no copy, same result as the contiguous product."""
+    Sq, H, Hkv, n, D = 5, 8, 2, 37, 64
+    q = orc.normal((Sq, H, D), seed=162)
+    k = orc.normal((n, Hkv, D), seed=163)
+
+    def build(g, ctx, L):
+        qv = g.ggml_permute(ctx, L["q"], 0, 2, 1, 3)   # ggml [D, Sq, H]
+        kv = g.ggml_permute(ctx, L["k"], 0, 2, 1, 3)   # ggml [D, n, Hkv]
+        return g.ggml_mul_mat(ctx, kv, qv)             # [n, Sq, H]
+
+    gr = Graph(be, {"q": (G.F32, [D, H, Sq], q), "k": (G.F32, [D, Hkv, n], k)}, build)
+    got = gr.run()
+    gr.close()
+    want = _mul_mat_ref(k.transpose(1, 0, 2), q.transpose(1, 0, 2), False)
+    assert orc.parity(got.reshape(want.shape), want) < 1e-5
+
+
+@pytest.mark.parametrize("Sq,n_kv", [(1, 300), (6, 64)])
+def test_eager_attention_matches_flash(be, orc, Sq, n_kv):
+    """The flash-attention fallback of runtime/include/ggml_compiler_ops.h:140-148 (the attention an
+    unfused program computes): mul_mat(k, q) -> soft_max_ext(mask, scale) -> mul_mat(cont(vᵀ), kq) ->
+    cont(permute), with f16 K/V and grouped-query heads, against the oracle's flash_attn_ext at 1e-3."""
+    D, H, Hkv = 128, 8, 2
+    scale = D ** -0.5
+    q = orc.normal((H, Sq, D), seed=164)
+    k16 = orc.fp32_to_fp16(orc.normal((Hkv, n_kv, D), seed=165))
+    v16 = orc.fp32_to_fp16(orc.normal((Hkv, n_kv, D), seed=166))
+    mask = np.zeros((Sq, n_kv), np.float32)
+    for s_ in range(Sq):
+        mask[s_, n_kv - Sq + s_ + 1:] = -np.inf
+    m16 = orc.fp32_to_fp16(mask)
+
+    def build(g, ctx, L):
+        kq = g.ggml_mul_mat(ctx, L["k"], L["q"])                       # [n_kv, Sq, H]
+        g.ggml_mul_mat_set_prec(kq, 10)
+        kq = g.ggml_soft_max_ext(ctx, kq, L["m"], scale, 0.0)
+        vt = g.ggml_cont(ctx, g.ggml_transpose(ctx, L["v"]))          # [n_kv, D, Hkv]
+        kqv = g.ggml_mul_mat(ctx, vt, kq)                              # [D, Sq, H]
+        g.ggml_mul_mat_set_prec(kqv, 10)
+        return g.ggml_cont(ctx, g.ggml_permute(ctx, kqv, 0, 2, 1, 3))  # [D, H, Sq]
+
+    gr = Graph(be, {"q": (G.F32, [D, Sq, H], q), "k": (G.F16, [D, n_kv, Hkv], k16),
+                    "v": (G.F16, [D, n_kv, Hkv], v16), "m": (G.F16, [n_kv, Sq], m16)}, build)
+    got = gr.run().reshape(Sq, H, D)
+    gr.close()
+    want = orc.flash_attn_ext(q, k16, v16, m16, scale)
+    assert orc.parity(got, want.reshape(Sq, H, D)) < TOL
 
 
 # --------------------------------------------------------------------- rope, rows, copies
@@ -528,7 +624,32 @@ def test_norm_clamp_row_sums(be, orc, n):
     assert np.array_equal(got["clamp"], np.clip(a, -1.0, 0.75).reshape(-1))
     s64 = a.astype(np.float64).sum(-1).reshape(-1)
     assert np.allclose(got["sum"], s64, rtol=1e-6, atol=1e-5)
-    assert np.allclose(got["mean"], s64 / n, rtol=1e-6, atol=1e-6)
+    # ggml's forward_mean: the row sum rounded to f32, then one f32 division by (float) n
+    assert np.array_equal(got["mean"], s64.astype(np.float32) / np.float32(n))
+
+
+@pytest.mark.parametrize("bshape", [[40, 1, 3], [1, 7, 3], [1, 1, 3], [1, 7, 1], [40, 7, 1], [1, 1, 1]])
+def test_binary_broadcast_every_dim(be, orc, bshape):
+    """add / sub / mul / div with the second operand repeated along any dims (ggml_can_repeat), as
+    lowered programs emit them: x - mean over a leading dim, x * rsqrt(var + eps), rope's cos / sin
+    products broadcast over heads. Bit-exact against numpy's broadcasting of the same f32 values."""
+    a = orc.normal((3, 7, 40), seed=150)                  # ggml ne [40, 7, 3]
+    b = orc.normal(tuple(reversed(bshape)), seed=151) + 3.0
+    outs = {}
+
+    def build(g, ctx, L):
+        for name in ("add", "sub", "mul", "div"):
+            outs[name] = getattr(g, "ggml_" + name)(ctx, L["a"], L["b"])
+        for t in outs.values():
+            g.ggml_set_output(t)
+        return list(outs.values())
+
+    gr = Graph(be, {"a": (G.F32, [40, 7, 3], a), "b": (G.F32, bshape, b)}, build)
+    gr.run()
+    got = {k: G.get_data(t, np.float32) for k, t in outs.items()}
+    gr.close()
+    for name, f in (("add", np.add), ("sub", np.subtract), ("mul", np.multiply), ("div", np.divide)):
+        assert np.array_equal(got[name], f(a, b).reshape(-1)), name
 
 
 def test_repeat_and_concat(be, orc):
