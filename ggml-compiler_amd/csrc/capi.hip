@@ -166,6 +166,52 @@ void need_dims(int64_t v, const char * what, int64_t lo = 1, int64_t hi = INT32_
 }
 
 }  // namespace
+
+// ggml_mul_mat(W, x) with the caller's workspace for the quantized activation (gcq_mul_mat and
+// gcq_mul_mat_noalloc): checks every argument, then launches on s. One row is quantized inside the
+// decode-row GEMV; up to 8 rows go through the workspace into the multi-row GEMV; more rows into
+// the int8 MFMA GEMM (Q4_0 / Q8_0) or, for the K-quants, the GEMV in groups of 8 rows.
+void mul_mat_with_workspace(int wtype, const void * w, int64_t N, int64_t K, const float * x, int64_t ldx, int64_t M,
+                            float * y, int64_t ldy, void * ws, size_t ws_size, hipStream_t s) {
+    need_weight_type(wtype);
+    need_k(wtype, K);
+    need_dims(N, "N");
+    need_dims(M, "M");
+    require(ldy >= N, "ldy must be >= N");
+    require(ldx >= K && ldx % 4 == 0, "ldx must be >= K and a multiple of 4");
+    need_ptr(w, "w", 16);
+    need_ptr(x, "x", 16);
+    need_ptr(y, "y", 4);
+    need_ptr(ws, "workspace", 256);
+    const size_t need = mul_mat_workspace_bytes(wtype, M, K);
+    require(ws_size >= need, "workspace of " + std::to_string(ws_size) + " bytes, need " + std::to_string(need));
+    if (M == 1 && row_gemv_fits(wtype, K)) {
+        RowArgs a = row_args(wtype, w, N, K, x);
+        a.y = y;
+        launch_row_gemv(wtype, PRO_PLAIN, EPI_STORE, a, s);
+        return;
+    }
+    if (M <= 8) {
+        launch_act_quant(wtype, x, ldx, M, K, ws, s);
+        launch_gemv(wtype, w, N, K, ws, M, y, ldy, s);
+    } else if (!is_kquant(wtype)) {
+        launch_act_quant(wtype, x, ldx, M, K, ws, s);
+        launch_gemm(wtype, w, N, K, ws, M, y, ldy, s);
+    } else {
+        for (int64_t m = 0; m < M; m += 8) {
+            const int64_t b = std::min<int64_t>(8, M - m);
+            launch_act_quant(wtype, x + m * ldx, ldx, b, K, ws, s);
+            launch_gemv(wtype, w, N, K, ws, b, y + m * ldy, ldy, s);
+        }
+    }
+}
+
+// Workspace bytes of mul_mat_with_workspace (0 for arguments gcq_act_size rejects).
+size_t mul_mat_workspace_bytes(int wtype, int64_t M, int64_t K) {
+    if (!is_weight_type(wtype) || M <= 0 || !row_bytes(wtype, K)) return 0;
+    return act_layout(wtype, (is_kquant(wtype) && M > 8) ? 8 : M, K).total;
+}
+
 }  // namespace gcq
 
 using namespace gcq;
@@ -303,39 +349,7 @@ int gcq_mul_mat_q(int wtype, const void * w, int64_t N, int64_t K, const void * 
 
 int gcq_mul_mat(int wtype, const void * w, int64_t N, int64_t K, const float * x, int64_t ldx, int64_t M, float * y,
                 int64_t ldy, void * ws, size_t ws_size, void * stream) {
-    return guarded([&] {
-        need_weight_type(wtype);
-        need_k(wtype, K);
-        need_dims(N, "N");
-        need_dims(M, "M");
-        require(ldy >= N, "ldy must be >= N");
-        require(ldx >= K && ldx % 4 == 0, "ldx must be >= K and a multiple of 4");
-        need_ptr(w, "w", 16);
-        need_ptr(x, "x", 16);
-        need_ptr(y, "y", 4);
-        need_ptr(ws, "workspace", 256);
-        const size_t need = gcq_mul_mat_workspace(wtype, M, K);
-        require(ws_size >= need, "workspace of " + std::to_string(ws_size) + " bytes, need " + std::to_string(need));
-        hipStream_t s = as_stream(stream);
-        if (M == 1 && row_gemv_fits(wtype, K)) {  // one row: quantized inside the GEMV
-            RowArgs a = row_args(wtype, w, N, K, x);
-            a.y = y;
-            return launch_row_gemv(wtype, PRO_PLAIN, EPI_STORE, a, s);
-        }
-        if (M <= 8) {
-            launch_act_quant(wtype, x, ldx, M, K, ws, s);
-            launch_gemv(wtype, w, N, K, ws, M, y, ldy, s);
-        } else if (!is_kquant(wtype)) {
-            launch_act_quant(wtype, x, ldx, M, K, ws, s);
-            launch_gemm(wtype, w, N, K, ws, M, y, ldy, s);
-        } else {
-            for (int64_t m = 0; m < M; m += 8) {
-                const int64_t b = std::min<int64_t>(8, M - m);
-                launch_act_quant(wtype, x + m * ldx, ldx, b, K, ws, s);
-                launch_gemv(wtype, w, N, K, ws, b, y + m * ldy, ldy, s);
-            }
-        }
-    });
+    return guarded([&] { mul_mat_with_workspace(wtype, w, N, K, x, ldx, M, y, ldy, ws, ws_size, as_stream(stream)); });
 }
 
 int gcq_rms_norm_mul_mat(int wtype, const void * w, int64_t N, int64_t K, const float * x, const float * norm_w,

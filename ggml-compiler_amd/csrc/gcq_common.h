@@ -198,6 +198,11 @@ void launch_soft_max(const float * x, float * y, int64_t n, int64_t r1, int64_t 
                      hipStream_t s);
 bool row_gemv_fits(int type, int64_t K);
 int row_gemv_merge_max();
+// ggml_mul_mat(W, x) of f32 rows with the caller's workspace (the body of gcq_mul_mat and
+// gcq_mul_mat_noalloc); throws on a bad argument. mul_mat_workspace_bytes: the workspace it needs.
+void mul_mat_with_workspace(int wtype, const void * w, int64_t N, int64_t K, const float * x, int64_t ldx, int64_t M,
+                            float * y, int64_t ldy, void * ws, size_t ws_size, hipStream_t s);
+size_t mul_mat_workspace_bytes(int wtype, int64_t M, int64_t K);
 
 // Wraps a C-ABI body: 0 on success, -1 with last_error set on failure.
 template <class F>

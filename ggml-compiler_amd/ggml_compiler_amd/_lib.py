@@ -78,6 +78,7 @@ SIGNATURES = {
     "gcq_quantize_act": ([i32, p, i64, i64, i64, p, p], i32),
     "gcq_act_to_ggml": ([i32, p, i64, i64, p, p], i32),
     "gcq_mul_mat": ([i32, p, i64, i64, p, i64, i64, p, i64, p, sz, p], i32),
+    "gcq_mul_mat_noalloc": ([i32, p, i64, i64, p, i64, i64, p, i64, p], i32),
     "gcq_mul_mat_q": ([i32, p, i64, i64, p, i64, p, i64, p, p], i32),
     "gcq_rms_norm_q8": ([p, i64, p, i64, i64, f32, p, p], i32),
     "gcq_rms_norm_mul_mat": ([i32, p, i64, i64, p, p, f32, p, p, p, sz, p], i32),

@@ -87,6 +87,16 @@ GCQ_API int gcq_act_to_ggml(int wtype, const void * act, int64_t B, int64_t K, v
  * or GEMV in groups of 8 rows (K-quants). ws: gcq_mul_mat_workspace bytes, 256-byte aligned. */
 GCQ_API int gcq_mul_mat(int wtype, const void * w, int64_t N, int64_t K, const float * x, int64_t ldx, int64_t M,
                         float * y, int64_t ldy, void * ws, size_t ws_size, void * stream);
+/* gcq_mul_mat without a workspace argument and without any device allocation. No counterpart in
+ * the reference: it is for callers that cannot allocate (code under HIP graph capture, serving
+ * loops, harnesses that forbid hipMalloc). The quantized activation lives in a static device
+ * array of GCQ_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; a call whose
+ * gcq_mul_mat_workspace(wtype, M, K) exceeds it fails with an error. Runs on the current device
+ * (the stream must belong to it). Calls that overlap on one GPU share the array and race.
+ * Results equal gcq_mul_mat's bit for bit. */
+#define GCQ_NOALLOC_SCRATCH_BYTES (16u << 20)
+GCQ_API int gcq_mul_mat_noalloc(int wtype, const void * w, int64_t N, int64_t K, const float * x, int64_t ldx,
+                                int64_t M, float * y, int64_t ldy, void * stream);
 /* The same with the activation already quantized (gcq_quantize_act, gcq_rms_norm_q8,
  * gcq_swiglu_q8); with res (M x N at row stride ldy, may be y itself) y = res + W x: the ggml_add of
  * a residual that follows the mul_mat, fused. */
