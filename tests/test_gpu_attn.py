@@ -75,12 +75,28 @@ def test_prefill_rows(gops, orc):
 
 
 @pytest.mark.parametrize("n_kv", [1, 17, 700, 1024, 1500, 4096, 32768])
-@pytest.mark.parametrize("H,Hkv,D", [(32, 8, 128), (8, 8, 128), (8, 4, 64), (16, 4, 64)])
+@pytest.mark.parametrize("H,Hkv,D", [(32, 8, 128), (8, 8, 128), (8, 4, 64), (16, 4, 64), (64, 8, 128), (16, 2, 64)])
 def test_decode_kernel_no_mask(gops, orc, n_kv, H, Hkv, D):
-    """One query row without a mask takes the one-pass decode kernel (per-lane-group online
-    softmax, wavefronts merged in LDS; one workgroup per 1024 keys and a merge above that): against
-    the oracle within 1e-3. 17 keys leave most wavefronts without a key."""
+    """One query row takes the matrix-core decode kernel (16-key blocks per wavefront, Q·Kᵀ and
+    Vᵀ·P on MFMA, online softmax per head, wavefronts merged in LDS, splits merged by
+    k_attn_merge): against the oracle within 1e-3, 1 to 8 query heads per KV head. 17 keys leave
+    most wavefronts without a key; 1500 ends inside a 16-key block."""
     q, kc, vc, _ = _case(orc, H, Hkv, 1, n_kv, D, n_kv, seed=45)
     out = _run(gops, q, kc, vc, None, n_kv, 1 / np.sqrt(D))
     ref = orc.flash_attn_ext(q, kc, vc, None, 1 / np.sqrt(D))
     assert orc.parity(out, ref) < TOL
+
+
+@pytest.mark.parametrize("H,Hkv", [(32, 8), (16, 2)])
+def test_decode_row_with_holes_in_the_mask(gops, orc, H, Hkv):
+    """One query row with an f16 mask that drops keys inside blocks and whole blocks, and adds
+    finite biases to others: the decode kernel's mask path against the oracle."""
+    D, n_kv = 128, 1000
+    q, kc, vc, _ = _case(orc, H, Hkv, 1, n_kv, D, n_kv, seed=46)
+    mask = (orc.normal((1, n_kv), seed=47) * 0.5).astype(np.float32)
+    mask[0, 3:9] = -np.inf
+    mask[0, 64:160] = -np.inf
+    mask[0, 997] = -np.inf
+    m16 = orc.fp32_to_fp16(mask)
+    out = _run(gops, q, kc, vc, m16, n_kv, 1 / np.sqrt(D))
+    assert orc.parity(out, orc.flash_attn_ext(q, kc, vc, m16, 1 / np.sqrt(D))) < TOL
