@@ -252,7 +252,7 @@ std::vector<int> qkv_rope_group(const ggml_cgraph * g, const std::vector<int> & 
     return grp;
 }
 
-Chains find_chains(const ggml_cgraph * g) {
+Chains find_chains(const ggml_cgraph * g, bool fuse) {
     const int n = (int) g->nodes.size();
     Chains c;
     c.end.resize(n);
@@ -260,6 +260,7 @@ Chains find_chains(const ggml_cgraph * g) {
     c.in_fold.assign(n, false);
     for (int i = 0; i < n; i++) c.end[i] = i;
     c.sib.assign(n, -1);
+    if (!fuse) return c;  // every node its own launch and its own memory
     std::unordered_map<const ggml_tensor *, int> uses, reader;
     std::unordered_map<const ggml_tensor *, std::vector<int>> readers;
     for (int i = 0; i < n; i++) {
@@ -525,6 +526,7 @@ struct ggml_backend {
     size_t ws_size = 0;
     float2 * rope_cs = nullptr;  // (cos, sin) table of the fused q / k / v rope step (<= 128 pairs)
     bool use_graphs = true;
+    bool fuse = true;  // fusion chains and launch groups (off: every node alone, materialized)
     std::unordered_map<const ggml_cgraph *, Cached> graphs;
     std::vector<Step> steps;
 
@@ -1450,7 +1452,8 @@ void refresh_views(ggml_cgraph * g) {
             }
 }
 
-enum ggml_status compute(ggml_backend * be, ggml_cgraph * g) {
+// Plans (or replays) g on the backend's stream; waits for it unless `async`.
+enum ggml_status compute(ggml_backend * be, ggml_cgraph * g, bool async = false) {
     require(g != nullptr, "graph is NULL");
     require(g->error.empty(), g->error);
     if (g->nodes.empty()) return GGML_STATUS_SUCCESS;
@@ -1461,11 +1464,11 @@ enum ggml_status compute(ggml_backend * be, ggml_cgraph * g) {
         auto it = be->graphs.find(g);
         if (it != be->graphs.end() && it->second.exec && it->second.fp == fp) {
             check_hip(hipGraphLaunch(it->second.exec, be->stream), "hipGraphLaunch");
-            check_hip(hipStreamSynchronize(be->stream), "graph compute");
+            if (!async) check_hip(hipStreamSynchronize(be->stream), "graph compute");
             return GGML_STATUS_SUCCESS;
         }
     }
-    const Chains c = find_chains(g);
+    const Chains c = find_chains(g, be->fuse);
     be->steps.clear();
     Planner p{be, be->steps};
     p.folded = &c.folded;
@@ -1524,7 +1527,7 @@ enum ggml_status compute(ggml_backend * be, ggml_cgraph * g) {
         cc.fp = std::move(fp);
         check_hip(hipGraphLaunch(cc.exec, be->stream), "hipGraphLaunch");
     }
-    check_hip(hipStreamSynchronize(be->stream), "graph compute");
+    if (!async) check_hip(hipStreamSynchronize(be->stream), "graph compute");
     return GGML_STATUS_SUCCESS;
 }
 
@@ -1575,7 +1578,7 @@ struct Arena {
 size_t place(ggml_gallocr * ga, ggml_cgraph * g, std::vector<std::pair<ggml_tensor *, size_t>> & where) {
     require(g->error.empty(), g->error);
     const int n = (int) g->nodes.size();
-    const Chains c = find_chains(g);
+    const Chains c = find_chains(g, ga->be->fuse);
     // Needs memory: no data yet (or placed by this allocator before), not a view, not folded.
     // Tensors of graphs placed earlier are never touched: their contexts may be gone.
     auto needs = [&](const ggml_tensor * t) { return !t->view_src && (!t->data || t->buffer == &ga->buf); };
@@ -1685,6 +1688,32 @@ bool ggml_backend_supports_op(ggml_backend_t backend, const ggml_tensor * op) {
     p.dry = true;
     return guarded([&] { p.node(op); }) == 0;
 }
+
+}  // extern "C"
+
+namespace gcq {
+
+enum ggml_status graph_compute_async(ggml_backend_t backend, ggml_cgraph * cgraph) {
+    enum ggml_status st = GGML_STATUS_FAILED;
+    require(backend != nullptr, "graph compute: backend is NULL");
+    st = compute(backend, cgraph, true);
+    return st;
+}
+
+hipStream_t backend_stream(ggml_backend_t backend) { return backend ? backend->stream : nullptr; }
+
+void backend_activate(ggml_backend_t backend) {
+    require(backend != nullptr, "backend is NULL");
+    set_device(backend);
+}
+
+void backend_set_fusion(ggml_backend_t backend, bool on) {
+    if (backend) backend->fuse = on;
+}
+
+}  // namespace gcq
+
+extern "C" {
 
 enum ggml_status ggml_backend_graph_compute(ggml_backend_t backend, ggml_cgraph * cgraph) {
     enum ggml_status st = GGML_STATUS_FAILED;

@@ -2,6 +2,8 @@
 // and its HIP backend (ggml_backend.hip).
 #pragma once
 
+#include <hip/hip_runtime.h>
+
 #include <string>
 #include <unordered_set>
 #include <vector>
@@ -65,6 +67,14 @@ struct Chains {
     // permute / set_rows members}; only rope_q's result is written to memory of its own.
     std::vector<int> first;  // each group's earliest node: where its launch runs
 };
-Chains find_chains(const ggml_cgraph * g);
+Chains find_chains(const ggml_cgraph * g, bool fuse = true);
+
+// The HIP backend's stream for work a driver orders around its graphs, and graph computes that
+// do not wait for the graph (ggml_backend_graph_compute does). backend_set_fusion(false): every
+// node planned alone and given memory of its own (node-by-node profiling).
+enum ggml_status graph_compute_async(ggml_backend_t backend, ggml_cgraph * cgraph);
+hipStream_t backend_stream(ggml_backend_t backend);
+void backend_activate(ggml_backend_t backend);
+void backend_set_fusion(ggml_backend_t backend, bool on);
 
 }  // namespace gcq

@@ -4,22 +4,25 @@
 // A GGUF written by ggml-compiler holds weights and constants (tensors "w.N" / "c.N") and a program
 // (JSON under "ggml_compiler.program", written by ggml_compiler/emit/gguf_runtime.py:104-207):
 // symbols with ranges, driver values, stages whose nodes are already in ggml terms (innermost-first
-// `ne`, ggml axes), entry points whose drivers call stages and run loops, and state values. Loading
-// uploads every tensor into one HIP buffer (quantized ones in this library's packed layout),
-// allocates every driver value in a second buffer (zeroed, so state starts at zero) and builds one
-// graph per driver call site with the ggml API, placed by the graph allocator. A run walks the
-// entry's driver; each call computes its site's graph with ggml_backend_graph_compute, which
-// replays a captured HIP graph after the first run. Results reach their driver values through
-// ggml_cpy nodes appended after every other node, except a result that already is its value's
-// memory (set_rows into a KV cache the stage read).
+// `ne`, ggml axes), entry points whose drivers call stages and run loops, and state values.
 //
-// Semantics kept from the reference: the program schema and its checks (runtime/src/program.cpp:
-// 61-300), symbolic dims as expression trees evaluated per binding, driver values of symbolic size
-// held at their largest size with per-binding views (runtime/src/ggml_compiler_rt.cpp:481-548), the
-// per-site graph build and its result copies (:566-700), the loop's order of carries, scalars,
-// slices, counters, bound symbols, causal masks, body, collected rows and the until test (:376-441),
-// and the C API's argument checks and messages (:812-1170). The JSON reader, GGUF reader, op
-// dispatch and data structures are this file's own.
+// Loading uploads every tensor into one HIP buffer (quantized ones in this library's packed
+// layout), allocates every driver value in a second buffer (zeroed, so state starts at zero; a
+// symbolic value at its largest size, viewed per binding), and builds one graph per driver call
+// with the ggml API, placed by the graph allocator; each node is one ggml call, and the ggml layer
+// and the backend's supports_op refuse, with the reason, what cannot run. Each entry's driver is
+// compiled to flat code (calls; loops as enter / top / bottom with jumps) and run by a small
+// interpreter. Everything a run does between graphs - loop carries, counters, per-iteration scalars
+// and slices, causal mask rows, collected rows - is device work ordered on the backend's stream
+// with the graphs, so an iteration waits for the host only to read a counter's start or an until
+// token. Stage times are GPU times from events around each call.
+//
+// Semantics kept from the reference (runtime/src/ggml_compiler_rt.cpp, runtime/src/program.cpp,
+// runtime/src/ops.cpp): the program schema and its checks, symbolic dims with Python's integer
+// semantics, the per-iteration order of a loop (carries and counter starts at entry; then per
+// iteration scalars, slices, counters, bound symbols, masks, the body, collected rows, the until
+// test), results reaching driver values after every other node, the C API's argument checks and
+// messages, and the GGML_COMPILER_PROFILE / GGML_COMPILER_LOG environment switches.
 #include "gcq_common.h"
 #include "ggml_impl.h"
 
@@ -32,9 +35,11 @@
 #include <climits>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <functional>
 #include <map>
+#include <set>
 #include <memory>
 #include <unordered_map>
 #include <vector>
@@ -357,6 +362,7 @@ struct GgufFile {
     }
 };
 
+
 // ---------------------------------------------------------------------------------- program
 
 struct Symbol {
@@ -364,76 +370,98 @@ struct Symbol {
     int64_t min = 1, max = 1;
 };
 
-// An integer dim: a constant, symbol `v`, or an operation folded left over its arguments.
-struct Expr {
-    enum Kind { Const, Sym, Add, Mul, FloorDiv, Mod, Max, Min } kind = Const;
-    int64_t v = 0;
-    std::vector<Expr> args;
+// A symbolic integer dim compiled to postfix code: a literal or a symbol read pushes a value, an
+// operator pops the right operand and replaces the left one. The program's n-ary form
+// ["op", a, b, c] is a left fold, compiled as a b op c op. Operators follow Python on ints
+// (ggml_compiler/ir/sym.py): // rounds toward minus infinity and % takes the divisor's sign.
+class Dim {
+  public:
+    enum Op : uint8_t { Lit, Sym, Add, Mul, FloorDiv, Mod, Max, Min };
+    static constexpr int kMaxDepth = 64;
 
-    bool constant() const { return kind == Const; }
-    int64_t eval(const std::vector<int64_t> & b) const {
-        if (kind == Const) return v;
-        if (kind == Sym) return b.at((size_t) v);
-        int64_t acc = args.at(0).eval(b);
-        for (size_t k = 1; k < args.size(); k++) {
-            const int64_t x = args[k].eval(b);
-            switch (kind) {
-                case Add: acc += x; break;
-                case Mul: acc *= x; break;
-                case FloorDiv: {  // Python's //: rounds toward minus infinity
-                    if (x == 0) fail("division by zero in a symbolic dim");
-                    const int64_t q = acc / x;
-                    acc = (q * x != acc && ((acc < 0) != (x < 0))) ? q - 1 : q;
-                    break;
-                }
-                case Mod: {  // Python's %: the sign of the divisor
-                    if (x == 0) fail("modulo by zero in a symbolic dim");
-                    int64_t r = acc % x;
-                    if (r != 0 && ((r < 0) != (x < 0))) r += x;
-                    acc = r;
-                    break;
-                }
-                case Max: acc = std::max(acc, x); break;
-                case Min: acc = std::min(acc, x); break;
-                default: break;
+    static Dim literal(int64_t v) {
+        Dim d;
+        d.code_.push_back({Lit, v});
+        return d;
+    }
+    static Dim symbol(int k) {
+        Dim d;
+        d.code_.push_back({Sym, k});
+        return d;
+    }
+    // this op rhs, as the next step of a left fold
+    void fold(Op op, const Dim & rhs) {
+        depth_ = std::max(depth_, rhs.depth_ + 1);
+        if (depth_ > kMaxDepth) fail("symbolic dim nested too deeply");
+        code_.insert(code_.end(), rhs.code_.begin(), rhs.code_.end());
+        code_.push_back({op, 0});
+    }
+    bool fixed() const { return code_.size() == 1 && code_[0].op == Lit; }
+    void mark(std::vector<bool> & used) const {
+        for (const Insn & in : code_)
+            if (in.op == Sym) used.at((size_t) in.arg) = true;
+    }
+    int64_t operator()(const std::vector<int64_t> & sym) const {
+        int64_t st[kMaxDepth];
+        int sp = 0;
+        for (const Insn & in : code_) {
+            if (in.op == Lit) {
+                st[sp++] = in.arg;
+            } else if (in.op == Sym) {
+                st[sp++] = sym.at((size_t) in.arg);
+            } else {
+                sp--;
+                st[sp - 1] = apply(in.op, st[sp - 1], st[sp]);
             }
         }
-        return acc;
+        return st[0];
     }
-    void uses(std::vector<bool> & used) const {
-        if (kind == Sym) used.at((size_t) v) = true;
-        for (const auto & a : args) a.uses(used);
+
+  private:
+    struct Insn {
+        Op op;
+        int64_t arg;
+    };
+    std::vector<Insn> code_;
+    int depth_ = 1;
+
+    static int64_t apply(Op op, int64_t a, int64_t b) {
+        switch (op) {
+            case Add: return a + b;
+            case Mul: return a * b;
+            case Max: return a < b ? b : a;
+            case Min: return b < a ? b : a;
+            case FloorDiv:
+            case Mod: {
+                if (b == 0) fail(op == FloorDiv ? "division by zero in a symbolic dim" : "modulo by zero in a symbolic dim");
+                lldiv_t qr = std::lldiv(a, b);  // truncating; move to the floor when the signs differ
+                if (qr.rem != 0 && ((qr.rem > 0) != (b > 0))) {
+                    qr.quot -= 1;
+                    qr.rem += b;
+                }
+                return op == FloorDiv ? qr.quot : qr.rem;
+            }
+            default: return 0;
+        }
     }
 };
 
-Expr parse_dim(const Json & j, const std::vector<Symbol> & syms) {
-    Expr e;
-    if (j.kind == Json::Num) {
-        e.v = j.as_int();
-        return e;
-    }
+// A dim in the JSON: an integer, a symbol name, or [op, operand...] (ggml_compiler/ir/sym.py).
+Dim parse_dim(const Json & j, const std::vector<Symbol> & syms) {
+    if (j.kind == Json::Num) return Dim::literal(j.as_int());
     if (j.kind == Json::Str) {
         for (size_t k = 0; k < syms.size(); k++)
-            if (syms[k].name == j.s) {
-                e.kind = Expr::Sym;
-                e.v = (int64_t) k;
-                return e;
-            }
+            if (syms[k].name == j.s) return Dim::symbol((int) k);
         fail("dim refers to unknown symbol '" + j.s + "'");
     }
     if (j.kind != Json::Arr || j.arr.size() < 2 || j.arr[0].kind != Json::Str) fail("malformed dim");
-    static const std::pair<const char *, Expr::Kind> ops[] = {{"+", Expr::Add},       {"*", Expr::Mul},
-                                                               {"//", Expr::FloorDiv}, {"%", Expr::Mod},
-                                                               {"max", Expr::Max},     {"min", Expr::Min}};
-    bool known = false;
-    for (const auto & o : ops)
-        if (j.arr[0].s == o.first) {
-            e.kind = o.second;
-            known = true;
-        }
-    if (!known) fail("unknown dim operator '" + j.arr[0].s + "'");
-    for (size_t k = 1; k < j.arr.size(); k++) e.args.push_back(parse_dim(j.arr[k], syms));
-    return e;
+    static const std::map<std::string, Dim::Op> ops = {{"+", Dim::Add},  {"*", Dim::Mul},   {"//", Dim::FloorDiv},
+                                                        {"%", Dim::Mod},  {"max", Dim::Max}, {"min", Dim::Min}};
+    const auto op = ops.find(j.arr[0].s);
+    if (op == ops.end()) fail("unknown dim operator '" + j.arr[0].s + "'");
+    Dim d = parse_dim(j.arr[1], syms);
+    for (size_t k = 2; k < j.arr.size(); k++) d.fold(op->second, parse_dim(j.arr[k], syms));
+    return d;
 }
 
 int parse_type_name(const std::string & name) {
@@ -447,32 +475,32 @@ int parse_type_name(const std::string & name) {
 struct TensorSpec {
     std::string name;
     int type = GGML_TYPE_F32;
-    Expr ne_x[4];
-    std::vector<Expr> shape_x;
+    Dim ne_x[4];
+    std::vector<Dim> shape_x;
     int64_t ne[4] = {1, 1, 1, 1};  // for the current binding
-    std::vector<int64_t> shape;
 
     bool symbolic() const {
         for (const auto & d : ne_x)
-            if (!d.constant()) return true;
+            if (!d.fixed()) return true;
         return false;
     }
     void bind(const std::vector<int64_t> & b) {
         for (int k = 0; k < 4; k++) {
-            ne[k] = ne_x[k].eval(b);
+            ne[k] = ne_x[k](b);
             if (ne[k] < 1) fail("value '" + name + "' gets a dim of " + std::to_string(ne[k]));
         }
-        shape.clear();
-        for (const auto & d : shape_x) shape.push_back(d.eval(b));
+    }
+    std::vector<int64_t> shape(const std::vector<int64_t> & b) const {
+        std::vector<int64_t> s;
+        for (const auto & d : shape_x) s.push_back(d(b));
+        return s;
     }
     size_t nbytes(const std::vector<int64_t> & b) const {
-        int64_t n[4];
-        for (int k = 0; k < 4; k++) n[k] = ne_x[k].eval(b);
-        return ggml_row_size((ggml_type) type, n[0]) * (size_t) (n[1] * n[2] * n[3]);
+        return ggml_row_size((ggml_type) type, ne_x[0](b)) * (size_t) (ne_x[1](b) * ne_x[2](b) * ne_x[3](b));
     }
 };
 
-void parse_ne(const Json & j, const std::vector<Symbol> & syms, Expr (&ne)[4]) {
+void parse_ne(const Json & j, const std::vector<Symbol> & syms, Dim (&ne)[4]) {
     if (j.kind != Json::Arr || j.arr.size() != 4) fail("'ne' must be an array of 4 dims");
     for (int k = 0; k < 4; k++) ne[k] = parse_dim(j.arr[k], syms);
 }
@@ -490,11 +518,11 @@ struct NodeSpec {
     std::string id, op, loc;
     std::vector<std::string> src;
     int type = GGML_TYPE_F32;
-    Expr ne_x[4];
+    Dim ne_x[4];
     int64_t ne[4] = {1, 1, 1, 1};
-    Json p;                                    // op parameters
-    std::vector<std::pair<std::string, Expr>> p_x;  // symbolic ones (a view's start)
-    std::map<std::string, int64_t> p_bound;         // their values for the binding
+    Json p;                                        // op parameters
+    std::vector<std::pair<std::string, Dim>> p_x;  // symbolic ones (a view's start)
+    std::map<std::string, int64_t> p_bound;        // their values for the binding
 
     bool has(const char * key) const { return p_bound.count(key) || p.find(key); }
     double num(const char * key) const {
@@ -527,16 +555,14 @@ struct DriverOp {
     // call
     std::string stage;
     std::vector<std::string> args, out;
-    int site = -1;
     // loop
     int n = 0, n_symbol = -1;
     std::vector<std::pair<std::string, std::string>> counters, collect, carry, slices;
-    std::vector<std::pair<int, Expr>> bind;
+    std::vector<std::pair<int, Dim>> bind;
     std::vector<std::pair<std::string, int>> masks;
     std::vector<std::pair<std::string, std::vector<int>>> until;
     std::vector<std::pair<std::string, std::vector<float>>> scalars;
     std::vector<DriverOp> body;
-    std::vector<std::vector<ggml_tensor *>> slice_rows;  // per slice, n row views (made at bind)
 };
 
 struct EntrySpec {
@@ -558,18 +584,22 @@ struct Program {
             if (symbols[k].name == name) return (int) k;
         return -1;
     }
+    // "symbol 'n' = 9 is outside [1, 8]" unless v lies in symbol k's range
+    void check_range(int k, int64_t v) const {
+        const Symbol & sy = symbols[(size_t) k];
+        if (v < sy.min || v > sy.max)
+            fail("symbol '" + sy.name + "' = " + std::to_string(v) + " is outside [" + std::to_string(sy.min) + ", " +
+                 std::to_string(sy.max) + "]");
+    }
     void bind(const std::vector<int64_t> & b) {
         if (b.size() != symbols.size()) fail("binding has the wrong number of symbols");
-        for (size_t k = 0; k < symbols.size(); k++)
-            if (b[k] < symbols[k].min || b[k] > symbols[k].max)
-                fail("symbol '" + symbols[k].name + "' = " + std::to_string(b[k]) + " is outside [" +
-                     std::to_string(symbols[k].min) + ", " + std::to_string(symbols[k].max) + "]");
+        for (size_t k = 0; k < symbols.size(); k++) check_range((int) k, b[k]);
         for (auto & v : values) v.bind(b);
         for (auto & s : stages) {
             for (auto & p : s.params) p.bind(b);
             for (auto & n : s.nodes) {
-                for (int k = 0; k < 4; k++) n.ne[k] = n.ne_x[k].eval(b);
-                for (const auto & kv : n.p_x) n.p_bound[kv.first] = kv.second.eval(b);
+                for (int k = 0; k < 4; k++) n.ne[k] = n.ne_x[k](b);
+                for (const auto & kv : n.p_x) n.p_bound[kv.first] = kv.second(b);
             }
         }
     }
@@ -664,7 +694,7 @@ Program parse_program(const std::string & text) {
         std::vector<bool> used(prog.symbols.size(), false);
         for (const auto & p : js.at("params").items()) {
             s.params.push_back(parse_tensor(p, prog.symbols));
-            for (const auto & d : s.params.back().ne_x) d.uses(used);
+            for (const auto & d : s.params.back().ne_x) d.mark(used);
         }
         s.outputs = js.at("outputs").strings();
         for (const auto & jn : js.at("nodes").items()) {
@@ -676,11 +706,11 @@ Program parse_program(const std::string & text) {
             parse_ne(jn.at("ne"), prog.symbols, n.ne_x);
             if (const Json * p = jn.find("p")) n.p = *p;
             if (const Json * l = jn.find("loc"); l && l->kind == Json::Str) n.loc = l->s;
-            for (const auto & d : n.ne_x) d.uses(used);
+            for (const auto & d : n.ne_x) d.mark(used);
             for (const char * key : {"start", "stop"})
                 if (const Json * v = n.p.find(key); v && v->kind != Json::Num) {
                     n.p_x.emplace_back(key, parse_dim(*v, prog.symbols));
-                    n.p_x.back().second.uses(used);
+                    n.p_x.back().second.mark(used);
                 }
             s.nodes.push_back(std::move(n));
         }
@@ -710,33 +740,10 @@ Program parse_program(const std::string & text) {
 }  // namespace
 }  // namespace gcq
 
-// ------------------------------------------------------------------------------------ model
+// ------------------------------------------------------------------------------- node -> ggml
 
 namespace gcq {
 namespace {
-
-struct Site {
-    const StageSpec * stage = nullptr;
-    int stage_index = -1;
-    ggml_context * ctx = nullptr;
-    ggml_cgraph * gf = nullptr;
-    ggml_gallocr_t ga = nullptr;
-    bool stale = false;
-};
-
-struct StageStat {
-    double ms = 0.0;
-    int calls = 0;
-};
-
-// A ggml API call that reports failure through the library's error record (the void tensor
-// functions), turned into an exception.
-template <class F>
-void must(const std::string & what, F && f) {
-    const uint64_t before = error_count();
-    f();
-    if (error_count() != before) fail(what + ": " + last_error());
-}
 
 std::string ne_str(const int64_t * ne) {
     return "[" + std::to_string(ne[0]) + ", " + std::to_string(ne[1]) + ", " + std::to_string(ne[2]) + ", " +
@@ -778,160 +785,277 @@ ggml_tensor * reshape_of(ggml_context * ctx, ggml_tensor * x, const int64_t * ne
     return ggml_view_4d(ctx, x, ne[0], ne[1], ne[2], ne[3], nb[1], nb[2], nb[3], 0);
 }
 
-// One program node as ggml calls (the op surface of runtime/src/ops.cpp:56-309 that this library
-// runs: binaries and unaries as ops.cpp:76-100, and the rest below; the others fail here with the
-// node's name).
-ggml_tensor * emit(ggml_context * ctx, const NodeSpec & n, const std::vector<ggml_tensor *> & s) {
-    auto need = [&](size_t lo, size_t hi) {
-        if (s.size() < lo || s.size() > hi)
-            node_fail(n, "expected " + std::to_string(lo) + (lo == hi ? "" : "-" + std::to_string(hi)) +
-                             " inputs, got " + std::to_string(s.size()));
-    };
-    const std::string & op = n.op;
+// The program ops this runtime turns into ggml calls (the op surface of runtime/src/ops.cpp:56-309
+// that runs on this library). Shape rules are enforced by the ggml layer, whose constructors refuse
+// what ggml would abort on and say why; what the HIP executor cannot run fails supports_op when the
+// stage's graph is checked. The loader itself only picks parameters and arities.
+enum class NodeOp {
+    Add, Sub, Mul, Div, Unary, Mean, SumRows, Clamp, Repeat, Concat, Norm, Cont, MulMat, Scale, RmsNorm, SoftMax,
+    Reshape, Permute, View, FlashAttn, Swiglu, SetRows, Rope, Argmax, GetRows, Cast,
+};
+
+using UnaryFn = ggml_tensor * (*)(ggml_context *, ggml_tensor *);
+
+struct NodeKind {
+    NodeOp op;
+    int lo, hi;             // inputs
+    UnaryFn fn = nullptr;  // NodeOp::Unary
+};
+
+const std::unordered_map<std::string, NodeKind> & node_kinds() {
+    static const std::unordered_map<std::string, NodeKind> kinds = [] {
+        std::unordered_map<std::string, NodeKind> k = {
+            {"add", {NodeOp::Add, 2, 2}},        {"sub", {NodeOp::Sub, 2, 2}},
+            {"mul", {NodeOp::Mul, 2, 2}},        {"div", {NodeOp::Div, 2, 2}},
+            {"mean", {NodeOp::Mean, 1, 1}},      {"sum_rows", {NodeOp::SumRows, 1, 1}},
+            {"clamp", {NodeOp::Clamp, 1, 1}},    {"repeat", {NodeOp::Repeat, 1, 1}},
+            {"concat", {NodeOp::Concat, 2, 2}},  {"norm", {NodeOp::Norm, 1, 1}},
+            {"cont", {NodeOp::Cont, 1, 1}},      {"mul_mat", {NodeOp::MulMat, 2, 2}},
+            {"scale", {NodeOp::Scale, 1, 1}},    {"rms_norm", {NodeOp::RmsNorm, 1, 1}},
+            {"soft_max", {NodeOp::SoftMax, 1, 2}}, {"reshape", {NodeOp::Reshape, 1, 1}},
+            {"permute", {NodeOp::Permute, 1, 1}}, {"view", {NodeOp::View, 1, 1}},
+            {"flash_attn", {NodeOp::FlashAttn, 3, 4}}, {"swiglu", {NodeOp::Swiglu, 2, 2}},
+            {"set_rows", {NodeOp::SetRows, 3, 3}}, {"rope", {NodeOp::Rope, 2, 3}},
+            {"argmax", {NodeOp::Argmax, 1, 1}},  {"get_rows", {NodeOp::GetRows, 2, 2}},
+            {"cast", {NodeOp::Cast, 1, 1}},
+        };
+        // elementwise functions; gelu_tanh is the tanh form, which is what ggml_gelu computes here
+        const std::pair<const char *, UnaryFn> unaries[] = {
+            {"relu", ggml_relu}, {"gelu", ggml_gelu},       {"gelu_tanh", ggml_gelu}, {"gelu_erf", ggml_gelu_erf},
+            {"silu", ggml_silu}, {"tanh", ggml_tanh},       {"sigmoid", ggml_sigmoid}, {"exp", ggml_exp},
+            {"log", ggml_log},   {"neg", ggml_neg},         {"abs", ggml_abs},         {"sqr", ggml_sqr},
+            {"sqrt", ggml_sqrt}, {"sin", ggml_sin},         {"cos", ggml_cos},         {"softplus", ggml_softplus},
+        };
+        for (const auto & u : unaries) k[u.first] = {NodeOp::Unary, 1, 1, u.second};
+        return k;
+    }();
+    return kinds;
+}
+
+ggml_tensor * emit_node(ggml_context * ctx, const NodeSpec & n, const std::vector<ggml_tensor *> & s) {
+    const auto & kinds = node_kinds();
+    const auto it = kinds.find(n.op);
+    if (it == kinds.end()) node_fail(n, "op is not supported by this runtime");
+    const NodeKind & k = it->second;
+    if ((int) s.size() < k.lo || (int) s.size() > k.hi)
+        node_fail(n, "expected " + std::to_string(k.lo) + (k.lo == k.hi ? "" : "-" + std::to_string(k.hi)) +
+                         " inputs, got " + std::to_string(s.size()));
+    auto f = [&](const char * key) { return (float) n.num(key); };
     ggml_tensor * t = nullptr;
-    using Binary = ggml_tensor * (*)(ggml_context *, ggml_tensor *, ggml_tensor *);
-    using Unary = ggml_tensor * (*)(ggml_context *, ggml_tensor *);
-    static const std::map<std::string, Binary> binaries = {
-        {"add", ggml_add}, {"sub", ggml_sub}, {"mul", ggml_mul}, {"div", ggml_div}};
-    // gelu_tanh is the tanh form, which is what ggml_gelu computes here.
-    static const std::map<std::string, Unary> unaries = {
-        {"relu", ggml_relu}, {"gelu", ggml_gelu},       {"gelu_tanh", ggml_gelu}, {"gelu_erf", ggml_gelu_erf},
-        {"silu", ggml_silu}, {"tanh", ggml_tanh},       {"sigmoid", ggml_sigmoid}, {"exp", ggml_exp},
-        {"log", ggml_log},   {"neg", ggml_neg},         {"abs", ggml_abs},         {"sqr", ggml_sqr},
-        {"sqrt", ggml_sqrt}, {"sin", ggml_sin},         {"cos", ggml_cos},         {"softplus", ggml_softplus}};
-    if (const auto b = binaries.find(op); b != binaries.end()) {
-        need(2, 2);
-        if (!ggml_can_repeat(s[1], s[0])) node_fail(n, "cannot broadcast " + ne_str(s[1]->ne) + " into " + ne_str(s[0]->ne));
-        t = b->second(ctx, s[0], s[1]);
-    } else if (const auto u = unaries.find(op); u != unaries.end()) {
-        need(1, 1);
-        t = u->second(ctx, s[0]);
-    } else if (op == "mean" || op == "sum_rows") {
-        need(1, 1);
-        t = op == "mean" ? ggml_mean(ctx, s[0]) : ggml_sum_rows(ctx, s[0]);
-    } else if (op == "clamp") {
-        need(1, 1);
-        t = ggml_clamp(ctx, s[0], (float) n.num("min"), (float) n.num("max"));
-    } else if (op == "repeat") {
-        need(1, 1);
-        for (int k = 0; k < 4; k++)
-            if (s[0]->ne[k] <= 0 || n.ne[k] % s[0]->ne[k] != 0) node_fail(n, "cannot tile " + ne_str(s[0]->ne) + " to " + ne_str(n.ne));
-        t = ggml_repeat_4d(ctx, s[0], n.ne[0], n.ne[1], n.ne[2], n.ne[3]);
-    } else if (op == "concat") {
-        need(2, 2);
-        t = ggml_concat(ctx, s[0], s[1], (int) n.integer("dim"));
-    } else if (op == "norm") {
-        need(1, 1);
-        t = ggml_norm(ctx, s[0], (float) n.num("eps"));
-    } else if (op == "cont") {
-        need(1, 1);
-        t = ggml_cont(ctx, s[0]);
-    } else if (op == "mul_mat") {
-        need(2, 2);
-        ggml_tensor *a = s[0], *b = s[1];
-        if (a->ne[0] != b->ne[0] || b->ne[2] % a->ne[2] != 0 || b->ne[3] % a->ne[3] != 0)
-            node_fail(n, "cannot multiply " + ne_str(a->ne) + " by " + ne_str(b->ne));
-        if (ggml_is_transposed(a)) node_fail(n, "weight operand is transposed; it needs a cont first");
-        t = ggml_mul_mat(ctx, a, b);
-        if (t && n.has("acc") && n.integer("acc") != 0) ggml_prec_set_acc(t, GGML_PREC_F32);
-    } else if (op == "scale") {
-        need(1, 1);
-        const ggml_tensor * x = s[0];
-        if (x->nb[0] != ggml_type_size(x->type) || x->nb[2] != x->nb[1] * x->ne[1] || x->nb[3] != x->nb[2] * x->ne[2])
-            node_fail(n, "input " + ne_str(x->ne) + " is a strided view; it needs a cont first");
-        const float sc = (float) n.num("s"), b = (float) n.num_or("b", 0.0);
-        t = b == 0.0f ? ggml_scale(ctx, s[0], sc) : ggml_scale_bias(ctx, s[0], sc, b);
-    } else if (op == "rms_norm") {
-        need(1, 1);
-        t = ggml_rms_norm(ctx, s[0], (float) n.num("eps"));
-    } else if (op == "soft_max") {
-        need(1, 2);
-        t = ggml_soft_max_ext(ctx, s[0], s.size() > 1 ? s[1] : nullptr, (float) n.num_or("scale", 1.0),
-                              (float) n.num_or("max_bias", 0.0));
-    } else if (op == "reshape") {
-        need(1, 1);
-        if (ggml_nelements(s[0]) != n.ne[0] * n.ne[1] * n.ne[2] * n.ne[3])
-            node_fail(n, "cannot reshape " + ne_str(s[0]->ne) + " to " + ne_str(n.ne));
-        t = reshape_of(ctx, s[0], n.ne);
-        if (!t)
-            node_fail(n, "input is a strided view and the reshape does more than add or drop size-1 dims; it needs a "
-                         "cont first");
-    } else if (op == "permute") {
-        need(1, 1);
-        const Json * ax = n.p.find("axes");
-        if (!ax || ax->items().size() != 4) node_fail(n, "'axes' must have 4 entries");
-        t = ggml_permute(ctx, s[0], (int) ax->arr[0].as_int(), (int) ax->arr[1].as_int(), (int) ax->arr[2].as_int(),
-                         (int) ax->arr[3].as_int());
-    } else if (op == "view") {
-        need(1, 1);
-        const int64_t dim = n.integer("dim"), start = n.integer("start");
-        if (dim < 0 || dim > 3 || start < 0 || start + n.ne[dim] > s[0]->ne[dim])
-            node_fail(n, "slice out of range of " + ne_str(s[0]->ne));
-        t = slice_of(ctx, s[0], (int) dim, start, n.ne);
-    } else if (op == "flash_attn") {
-        need(3, 4);
-        ggml_tensor *q = s[0], *k = s[1], *v = s[2];
-        ggml_tensor * mask = s.size() > 3 ? s[3] : nullptr;
-        if (k->ne[0] != q->ne[0] || k->ne[1] != v->ne[1] || q->ne[3] != k->ne[3] || q->ne[3] != v->ne[3] ||
-            q->ne[2] % k->ne[2] != 0)
-            node_fail(n, "q " + ne_str(q->ne) + ", k " + ne_str(k->ne) + ", v " + ne_str(v->ne) + " do not line up");
-        if (mask && (mask->type != GGML_TYPE_F16 || !ggml_is_contiguous(mask) || q->ne[2] % mask->ne[2] != 0))
-            node_fail(n, "mask must be a contiguous f16 tensor broadcastable over heads");
-        t = ggml_flash_attn_ext(ctx, q, k, v, mask, (float) n.num("scale"), 0.0f, 0.0f);
-        if (t) ggml_prec_set_acc(t, GGML_PREC_F32);
-    } else if (op == "swiglu") {
-        need(2, 2);
-        if (!ggml_are_same_shape(s[0], s[1]) || !ggml_is_contiguous(s[0]) || !ggml_is_contiguous(s[1]))
-            node_fail(n, "swiglu needs a gate and an up of one shape, both contiguous");
-        t = ggml_swiglu_split(ctx, s[0], s[1]);
-    } else if (op == "set_rows") {
-        need(3, 3);
-        ggml_tensor *dst = s[0], *src = s[1], *idx = s[2];
-        if (dst->ne[0] != src->ne[0] || dst->ne[2] != src->ne[2] || dst->ne[3] != src->ne[3] ||
-            src->ne[1] != idx->ne[0] || idx->ne[1] != 1 || idx->type != GGML_TYPE_I32 ||
-            (src->type != GGML_TYPE_F32 && src->type != GGML_TYPE_F16))
-            node_fail(n, "cannot write rows " + ne_str(src->ne) + " at indices " + ne_str(idx->ne) + " into " +
-                             ne_str(dst->ne));
-        if (dst->nb[0] != ggml_type_size(dst->type) || src->nb[0] != ggml_type_size(src->type))
-            node_fail(n, "set_rows needs rows that are contiguous");
-        t = ggml_set_rows(ctx, dst, src, idx);
-    } else if (op == "rope") {
-        need(2, 3);
-        ggml_tensor *x = s[0], *pos = s[1];
-        ggml_tensor * ff = s.size() > 2 ? s[2] : nullptr;
-        const int n_dims = (int) n.integer("n_dims");
-        if (x->type != GGML_TYPE_F32 || x->nb[0] != ggml_type_size(x->type) || pos->type != GGML_TYPE_I32 ||
-            !ggml_is_vector(pos) || pos->ne[0] != x->ne[2] || n_dims % 2 || n_dims > x->ne[0] ||
-            (ff && (ff->type != GGML_TYPE_F32 || ff->ne[0] < n_dims / 2)))
-            node_fail(n, "cannot rotate " + ne_str(x->ne) + " at positions " + ne_str(pos->ne));
-        t = ggml_rope_ext(ctx, x, pos, ff, n_dims, (int) n.integer("mode"), 0, (float) n.num("freq_base"),
-                          (float) n.num("freq_scale"), 0.0f, (float) n.num("attn_factor"), 32.0f, 1.0f);
-    } else if (op == "argmax") {
-        need(1, 1);
-        if (!ggml_is_matrix(s[0])) node_fail(n, "argmax needs a matrix, got " + ne_str(s[0]->ne));
-        t = ggml_argmax(ctx, s[0]);
-    } else if (op == "get_rows") {
-        need(2, 2);
-        if (s[1]->type != GGML_TYPE_I32) node_fail(n, "row indices must be i32");
-        t = ggml_get_rows(ctx, s[0], s[1]);
-    } else if (op == "cast") {
-        need(1, 1);
-        t = ggml_cast(ctx, s[0], (ggml_type) n.type);
-    } else {
-        node_fail(n, "op is not supported by this runtime");
+    switch (k.op) {
+        case NodeOp::Add: t = ggml_add(ctx, s[0], s[1]); break;
+        case NodeOp::Sub: t = ggml_sub(ctx, s[0], s[1]); break;
+        case NodeOp::Mul: t = ggml_mul(ctx, s[0], s[1]); break;
+        case NodeOp::Div: t = ggml_div(ctx, s[0], s[1]); break;
+        case NodeOp::Unary: t = k.fn(ctx, s[0]); break;
+        case NodeOp::Mean: t = ggml_mean(ctx, s[0]); break;
+        case NodeOp::SumRows: t = ggml_sum_rows(ctx, s[0]); break;
+        case NodeOp::Clamp: t = ggml_clamp(ctx, s[0], f("min"), f("max")); break;
+        case NodeOp::Repeat: t = ggml_repeat_4d(ctx, s[0], n.ne[0], n.ne[1], n.ne[2], n.ne[3]); break;
+        case NodeOp::Concat: t = ggml_concat(ctx, s[0], s[1], (int) n.integer("dim")); break;
+        case NodeOp::Norm: t = ggml_norm(ctx, s[0], f("eps")); break;
+        case NodeOp::Cont: t = ggml_cont(ctx, s[0]); break;
+        case NodeOp::MulMat:
+            t = ggml_mul_mat(ctx, s[0], s[1]);
+            if (t && n.has("acc") && n.integer("acc") != 0) ggml_prec_set_acc(t, GGML_PREC_F32);
+            break;
+        case NodeOp::Scale: {
+            const float b = (float) n.num_or("b", 0.0);
+            t = b == 0.0f ? ggml_scale(ctx, s[0], f("s")) : ggml_scale_bias(ctx, s[0], f("s"), b);
+            break;
+        }
+        case NodeOp::RmsNorm: t = ggml_rms_norm(ctx, s[0], f("eps")); break;
+        case NodeOp::SoftMax:
+            t = ggml_soft_max_ext(ctx, s[0], s.size() > 1 ? s[1] : nullptr, (float) n.num_or("scale", 1.0),
+                                  (float) n.num_or("max_bias", 0.0));
+            break;
+        case NodeOp::Reshape:
+            if (ggml_nelements(s[0]) != n.ne[0] * n.ne[1] * n.ne[2] * n.ne[3])
+                node_fail(n, "cannot reshape " + ne_str(s[0]->ne) + " to " + ne_str(n.ne));
+            t = reshape_of(ctx, s[0], n.ne);
+            if (!t)
+                node_fail(n, "input is a strided view and the reshape does more than add or drop size-1 dims; it "
+                             "needs a cont first");
+            break;
+        case NodeOp::Permute: {
+            const Json * ax = n.p.find("axes");
+            if (!ax || ax->items().size() != 4) node_fail(n, "'axes' must have 4 entries");
+            t = ggml_permute(ctx, s[0], (int) ax->arr[0].as_int(), (int) ax->arr[1].as_int(),
+                             (int) ax->arr[2].as_int(), (int) ax->arr[3].as_int());
+            break;
+        }
+        case NodeOp::View: {
+            const int64_t dim = n.integer("dim"), start = n.integer("start");
+            if (dim < 0 || dim > 3 || start < 0 || start + n.ne[dim] > s[0]->ne[dim])
+                node_fail(n, "slice out of range of " + ne_str(s[0]->ne));
+            t = slice_of(ctx, s[0], (int) dim, start, n.ne);
+            break;
+        }
+        case NodeOp::FlashAttn:
+            t = ggml_flash_attn_ext(ctx, s[0], s[1], s[2], s.size() > 3 ? s[3] : nullptr, f("scale"), 0.0f, 0.0f);
+            if (t) ggml_prec_set_acc(t, GGML_PREC_F32);
+            break;
+        case NodeOp::Swiglu: t = ggml_swiglu_split(ctx, s[0], s[1]); break;
+        case NodeOp::SetRows: t = ggml_set_rows(ctx, s[0], s[1], s[2]); break;
+        case NodeOp::Rope:
+            t = ggml_rope_ext(ctx, s[0], s[1], s.size() > 2 ? s[2] : nullptr, (int) n.integer("n_dims"),
+                              (int) n.integer("mode"), 0, f("freq_base"), f("freq_scale"), 0.0f, f("attn_factor"),
+                              32.0f, 1.0f);
+            break;
+        case NodeOp::Argmax: t = ggml_argmax(ctx, s[0]); break;
+        case NodeOp::GetRows: t = ggml_get_rows(ctx, s[0], s[1]); break;
+        case NodeOp::Cast: t = ggml_cast(ctx, s[0], (ggml_type) n.type); break;
     }
     if (!t) node_fail(n, std::string("ggml could not build it: ") + ggml_last_error());
     if (t->type != n.type)
         node_fail(n, std::string("produced type ") + ggml_type_name(t->type) + ", program expects " +
                          ggml_type_name((ggml_type) n.type));
-    for (int k = 0; k < 4; k++)
-        if (t->ne[k] != n.ne[k]) node_fail(n, "produced shape " + ne_str(t->ne) + ", program expects " + ne_str(n.ne));
+    for (int q = 0; q < 4; q++)
+        if (t->ne[q] != n.ne[q]) node_fail(n, "produced shape " + ne_str(t->ne) + ", program expects " + ne_str(n.ne));
     ggml_set_name(t, n.id.c_str());
     return t;
 }
 
 }  // namespace
 }  // namespace gcq
+
+// ------------------------------------------------------------------------ device-side driver work
+
+namespace gcq {
+namespace {
+
+__global__ void k_fill_words(uint32_t * __restrict__ p, int64_t n, uint32_t bits) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = bits;
+}
+
+// Rows of a causal mask for position pos: 0 where the key index (element % len) is <= pos, else -inf.
+__global__ void k_causal_rows(float * __restrict__ p, int64_t n, int64_t len, int64_t pos) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = i % len <= pos ? 0.0f : -INFINITY;
+}
+
+unsigned blocks_for(int64_t n) { return (unsigned) ((n + 255) / 256); }
+
+// The work a driver does between its graphs, ordered on the backend's stream with them, so a loop
+// iteration waits for the host only where the host must see a value (a counter's start, an until
+// token).
+class StreamOps {
+  public:
+    void attach(ggml_backend_t be) {
+        s_ = backend_stream(be);
+        check_hip(hipHostMalloc(&pinned_, 64, hipHostMallocDefault), "hipHostMalloc");
+    }
+    ~StreamOps() {
+        if (pinned_) (void) hipHostFree(pinned_);
+    }
+    void fill32(void * p, int64_t n, uint32_t bits) {
+        if (n <= 0) return;
+        k_fill_words<<<blocks_for(n), 256, 0, s_>>>((uint32_t *) p, n, bits);
+        check_launch("driver fill");
+    }
+    void causal(float * p, int64_t n, int64_t len, int64_t pos) {
+        if (n <= 0) return;
+        k_causal_rows<<<blocks_for(n), 256, 0, s_>>>(p, n, len, pos);
+        check_launch("driver mask");
+    }
+    void copy(void * dst, const void * src, size_t n) {
+        if (n) check_hip(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToDevice, s_), "driver copy");
+    }
+    void clear(void * dst, size_t n) {
+        if (n) check_hip(hipMemsetAsync(dst, 0, n, s_), "driver clear");
+    }
+    int32_t read_i32(const void * src) {
+        check_hip(hipMemcpyAsync(pinned_, src, 4, hipMemcpyDeviceToHost, s_), "driver read");
+        check_hip(hipStreamSynchronize(s_), "driver read");
+        int32_t v;
+        std::memcpy(&v, pinned_, 4);
+        return v;
+    }
+    void finish() { check_hip(hipStreamSynchronize(s_), "driver"); }
+    hipStream_t stream() const { return s_; }
+
+  private:
+    hipStream_t s_ = nullptr;
+    void * pinned_ = nullptr;
+};
+
+// GPU time per stage: an event pair around each call, read after the run's final wait.
+class StageClock {
+  public:
+    ~StageClock() {
+        for (hipEvent_t e : events_) (void) hipEventDestroy(e);
+    }
+    void begin_run() {
+        marks_.clear();
+        used_ = 0;
+    }
+    // events before / after one call of stage `stage`
+    void mark(int stage, hipStream_t s, bool after) {
+        if (used_ == events_.size()) {
+            hipEvent_t e;
+            check_hip(hipEventCreate(&e), "hipEventCreate");
+            events_.push_back(e);
+        }
+        check_hip(hipEventRecord(events_[used_], s), "hipEventRecord");
+        if (!after) marks_.push_back({stage, used_, 0});
+        else marks_.back().stop = used_;
+        used_++;
+    }
+    // ms of each call, accumulated into per-stage totals
+    template <class F>
+    void collect(F && add) {
+        for (const Mark & m : marks_) {
+            float ms = 0.0f;
+            check_hip(hipEventElapsedTime(&ms, events_[m.start], events_[m.stop]), "hipEventElapsedTime");
+            add(m.stage, (double) ms);
+        }
+    }
+
+  private:
+    struct Mark {
+        int stage;
+        size_t start, stop;
+    };
+    std::vector<hipEvent_t> events_;
+    std::vector<Mark> marks_;
+    size_t used_ = 0;
+};
+
+// GGML_COMPILER_PROFILE=<file>: every graph runs one node at a time, waited for, and after each
+// run "stage<TAB>node<TAB>op<TAB>ms" lines are appended to <file> (the reference runtime's
+// profile, runtime/src/ggml_compiler_rt.cpp:83-88, 219-240, 343-354). Fusion is off in this mode,
+// so every node is one launch of its own.
+const char * profile_file() {
+    static const char * p = [] {
+        const char * e = std::getenv("GGML_COMPILER_PROFILE");
+        return e && *e ? e : nullptr;
+    }();
+    return p;
+}
+
+// GGML_COMPILER_LOG=debug: the runtime's informational messages on stderr (warnings always).
+bool log_debug() {
+    static const bool on = [] {
+        const char * e = std::getenv("GGML_COMPILER_LOG");
+        return e && std::strcmp(e, "debug") == 0;
+    }();
+    return on;
+}
+
+// Runs f, which calls the ggml API's void functions (errors recorded, not thrown); throws with
+// `what` if any of them recorded one.
+template <class F>
+void ggml_checked(const std::string & what, F && f) {
+    const uint64_t before = error_count();
+    f();
+    if (error_count() != before) fail(what + ": " + last_error());
+}
+
+}  // namespace
+}  // namespace gcq
+
+// ------------------------------------------------------------------------------------ model
 
 using namespace gcq;
 
@@ -944,39 +1068,86 @@ struct ggml_compiler_stage_build {
     std::string error;
 };
 
+namespace gcq {
+namespace {
+
+// One driver call of a stage: the stage's graph built over the driver values it reads and writes.
+struct CallGraph {
+    int stage = -1;
+    const DriverOp * op = nullptr;
+    ggml_context * ctx = nullptr;
+    ggml_cgraph * graph = nullptr;
+    ggml_gallocr_t alloc = nullptr;
+    bool stale = false;  // the binding changed a shape it reads: rebuilt before its next run
+
+    void drop_graph() {
+        if (ctx) ggml_free(ctx);
+        ctx = nullptr;
+        graph = nullptr;
+    }
+};
+
+// A driver compiled to flat code: calls, and loops as enter / top / bottom with jumps.
+struct VmCode {
+    enum Kind : uint8_t { Call, Enter, Top, Bottom };
+    Kind kind;
+    const DriverOp * op;
+    int jump;  // Top: the instruction after its Bottom; Bottom: its Top
+    int call;  // Call: index into the model's call graphs
+};
+
+struct LoopFrame {
+    const DriverOp * op;
+    int trips, i;
+    std::vector<int32_t> start;  // counters' values at loop entry
+};
+
+}  // namespace
+}  // namespace gcq
+
 struct ggml_compiler_model {
+    // ---- what was loaded
     Program prog;
-    std::map<std::string, ggml_compiler_build_fn> builders;
     GgufFile file;
+    std::map<std::string, ggml_compiler_build_fn> builders;
     ggml_backend_t backend = nullptr;
-    ggml_context * wctx = nullptr;  // weights and constants
+    ggml_context * wctx = nullptr;  // weights and constants, one HIP buffer
     ggml_backend_buffer_t wbuf = nullptr;
-    ggml_context * vctx = nullptr;  // driver values
+    // ---- driver values: storage sized for the largest binding, views for the current one
+    ggml_context * vctx = nullptr;
     ggml_backend_buffer_t vbuf = nullptr;
-    ggml_context * bctx = nullptr;  // per binding: views of symbolic values
-    std::vector<ggml_context *> slice_ctxs;  // per binding: row views of loop slice sources
-    std::vector<int64_t> binding;   // the next run's
-    std::vector<int64_t> built;     // the views' and graphs'
-    std::unordered_map<std::string, ggml_tensor *> store;  // each value's memory
-    std::unordered_map<std::string, ggml_tensor *> view;   // each value as the bound graphs see it
+    ggml_context * view_ctx = nullptr;
     std::unordered_map<std::string, const TensorSpec *> spec;
+    std::unordered_map<std::string, ggml_tensor *> storage, bound;
+    std::set<std::string> inputs_set;  // inputs given since load
+    // ---- symbols: the binding the next run uses, the one the views and graphs were made for
+    std::vector<int64_t> binding, built;
+    // ---- compiled drivers and their call graphs
     struct Entry {
         const EntrySpec * spec = nullptr;
-        std::vector<const TensorSpec *> inputs, outputs;
+        std::vector<const TensorSpec *> in, out;
+        std::vector<VmCode> code;
     };
     std::vector<Entry> entries;
-    std::map<std::string, bool> input_set;
-    std::vector<Site> sites;
-    std::vector<StageStat> stage_stats;
+    std::vector<CallGraph> calls;
+    // ---- running
+    StreamOps ops;
+    StageClock clock;
+    std::vector<ggml_compiler_stats> stage_totals;  // ms_total, n_calls per stage
     ggml_compiler_stats last{};
+    struct ProfileLine {
+        std::string stage, node, op;
+        double ms;
+    };
+    std::vector<ProfileLine> profile;
 
     ~ggml_compiler_model() {
-        for (auto & c : sites) {
-            if (c.ga) ggml_gallocr_free(c.ga);
-            if (c.ctx) ggml_free(c.ctx);
+        if (backend) (void) hipStreamSynchronize(backend_stream(backend));
+        for (auto & c : calls) {
+            if (c.alloc) ggml_gallocr_free(c.alloc);
+            c.drop_graph();
         }
-        for (auto * c : slice_ctxs) ggml_free(c);
-        if (bctx) ggml_free(bctx);
+        if (view_ctx) ggml_free(view_ctx);
         if (vbuf) ggml_backend_buffer_free(vbuf);
         if (vctx) ggml_free(vctx);
         if (wbuf) ggml_backend_buffer_free(wbuf);
@@ -984,40 +1155,45 @@ struct ggml_compiler_model {
         if (backend) ggml_backend_free(backend);
     }
 
-    ggml_tensor * value(const std::string & name) const {
-        auto it = view.find(name);
-        if (it == view.end()) fail("driver value '" + name + "' is not declared");
-        return it->second;
-    }
+    // ------------------------------------------------------------------------------ loading
 
-    void load(const char * path, const ggml_compiler_options & o) {
+    void open(const char * path, const ggml_compiler_options & o) {
         if (o.allow_cpu_fallback) fail("allow_cpu_fallback is not available: this runtime runs on HIP devices only");
         if (o.backend != GGML_COMPILER_BACKEND_HIP && o.backend != GGML_COMPILER_BACKEND_AUTO)
             fail("backend " + std::to_string((int) o.backend) + " is not available: this runtime has the HIP backend "
                  "(GGML_COMPILER_BACKEND_HIP or _AUTO)");
         file.open(path);
-        auto it = file.strings.find("ggml_compiler.program");
-        if (it == file.strings.end())
+        const auto text = file.strings.find("ggml_compiler.program");
+        if (text == file.strings.end())
             fail(std::string("'") + path + "' has no ggml_compiler.program; it was not written by ggml-compiler compile");
-        prog = parse_program(it->second);
-        const int n_dev = gcq_device_count();
-        if (n_dev == 0) fail("no HIP device");
-        if (o.device < 0 || o.device >= n_dev)
-            fail("device index " + std::to_string(o.device) + " out of range; " + std::to_string(n_dev) +
+        prog = parse_program(text->second);
+        const int devices = gcq_device_count();
+        if (devices == 0) fail("no HIP device");
+        if (o.device < 0 || o.device >= devices)
+            fail("device index " + std::to_string(o.device) + " out of range; " + std::to_string(devices) +
                  " HIP device(s) found");
         backend = ggml_backend_hip_init(o.device);
         if (!backend) fail(std::string("cannot start the HIP backend: ") + last_error());
-        load_weights();
+        if (profile_file()) {  // nodes one by one: unfused, and no graph capture of single nodes
+            backend_set_fusion(backend, false);
+            ggml_backend_hip_set_use_graphs(backend, false);
+        }
+        ops.attach(backend);
+        if (log_debug())
+            std::fprintf(stderr, "ggml_compiler: %s on %s, %zu tensors, %zu stages, %zu entries\n", path,
+                         ggml_backend_name(backend), file.tensors.size(), prog.stages.size(), prog.entries.size());
+        upload_tensors();
         for (const auto & sy : prog.symbols) binding.push_back(sy.max);
         prog.bind(binding);
-        alloc_values();
-        stage_stats.assign(prog.stages.size(), StageStat{});
-        bind_values();
-        for (auto & e : prog.entries) build_ops(e.driver);
+        create_values();
+        link_entries();
+        stage_totals.assign(prog.stages.size(), ggml_compiler_stats{});
+        make_views();
+        for (auto & e : entries) compile(e);
         built = binding;
     }
 
-    void load_weights() {
+    void upload_tensors() {
         if (file.tensors.empty()) return;
         ggml_init_params ip{};
         ip.mem_size = ggml_tensor_overhead() * (file.tensors.size() + 1);
@@ -1043,433 +1219,562 @@ struct ggml_compiler_model {
             ggml_tensor * t = ggml_get_tensor(wctx, in.name.c_str());
             const size_t n = ggml_nbytes(t);
             staging.resize(n);
-            size_t got = 0;
-            while (got < n) {
+            for (size_t got = 0; got < n;) {
                 const ssize_t r = ::pread(fd, staging.data() + got, n - got, (off_t) (file.data_offset + in.offset + got));
                 if (r <= 0) fail("short read for tensor " + in.name);
                 got += (size_t) r;
             }
-            must("upload of tensor " + in.name, [&] { ggml_backend_tensor_set(t, staging.data(), 0, n); });
+            ggml_checked("upload of tensor " + in.name, [&] { ggml_backend_tensor_set(t, staging.data(), 0, n); });
         }
     }
 
-    void alloc_values() {
+    // Largest element count of a value over its symbols' ranges. Dims grow with each symbol, so
+    // one of the corners of the box of ranges holds it.
+    int64_t largest_count(const TensorSpec & v) const {
+        std::vector<bool> used(prog.symbols.size(), false);
+        for (const auto & d : v.ne_x) d.mark(used);
+        std::vector<size_t> free_syms;
+        for (size_t k = 0; k < used.size(); k++)
+            if (used[k]) free_syms.push_back(k);
+        if (free_syms.size() > 20) fail("value '" + v.name + "' depends on too many symbols");
+        std::vector<int64_t> b = binding;
+        int64_t best = 0;
+        for (uint32_t corner = 0; corner < (1u << free_syms.size()); corner++) {
+            for (size_t q = 0; q < free_syms.size(); q++) {
+                const Symbol & sy = prog.symbols[free_syms[q]];
+                b[free_syms[q]] = (corner >> q) & 1u ? sy.max : sy.min;
+            }
+            int64_t count = 1;
+            for (const auto & d : v.ne_x) count *= d(b);
+            best = std::max(best, count);
+        }
+        return best;
+    }
+
+    void create_values() {
         ggml_init_params ip{};
         ip.mem_size = ggml_tensor_overhead() * (prog.values.size() + 1);
         ip.no_alloc = true;
         vctx = ggml_init(ip);
         for (const auto & v : prog.values) {
-            ggml_tensor * t = nullptr;
-            if (!v.symbolic()) {
-                t = ggml_new_tensor_4d(vctx, (ggml_type) v.type, v.ne[0], v.ne[1], v.ne[2], v.ne[3]);
-            } else {
-                // Room for the largest size over the corners of its symbols' ranges (dims are
-                // monotone in each symbol, so a corner holds the maximum).
-                std::vector<bool> used(prog.symbols.size(), false);
-                for (const auto & d : v.ne_x) d.uses(used);
-                std::vector<size_t> idx;
-                for (size_t k = 0; k < used.size(); k++)
-                    if (used[k]) idx.push_back(k);
-                if (idx.size() > 20) fail("value '" + v.name + "' depends on too many symbols");
-                int64_t most = 0;
-                std::vector<int64_t> b = binding;
-                for (size_t mask = 0; mask < ((size_t) 1 << idx.size()); mask++) {
-                    for (size_t k = 0; k < idx.size(); k++)
-                        b[idx[k]] = (mask >> k) & 1 ? prog.symbols[idx[k]].max : prog.symbols[idx[k]].min;
-                    int64_t n = 1;
-                    for (const auto & d : v.ne_x) n *= d.eval(b);
-                    most = std::max(most, n);
-                }
-                t = ggml_new_tensor_1d(vctx, (ggml_type) v.type, most);
-            }
+            ggml_tensor * t = v.symbolic() ? ggml_new_tensor_1d(vctx, (ggml_type) v.type, largest_count(v))
+                                           : ggml_new_tensor_4d(vctx, (ggml_type) v.type, v.ne[0], v.ne[1], v.ne[2], v.ne[3]);
             if (!t) fail("driver value '" + v.name + "': " + last_error());
             ggml_set_name(t, v.name.c_str());
-            store[v.name] = t;
-            view[v.name] = t;
+            storage[v.name] = bound[v.name] = t;
             spec[v.name] = &v;
         }
-        if (!prog.values.empty()) {
-            vbuf = ggml_backend_alloc_ctx_tensors(vctx, backend);
-            if (!vbuf) fail(std::string("cannot allocate driver value buffer: ") + last_error());
-            must("clearing the driver values", [&] { ggml_backend_buffer_clear(vbuf, 0); });
-        }
+        if (prog.values.empty()) return;
+        vbuf = ggml_backend_alloc_ctx_tensors(vctx, backend);
+        if (!vbuf) fail(std::string("cannot allocate driver value buffer: ") + last_error());
+        ggml_checked("clearing the driver values", [&] { ggml_backend_buffer_clear(vbuf, 0); });  // state starts at 0
+    }
+
+    const TensorSpec & declared(const std::string & name, const char * role) const {
+        const auto it = spec.find(name);
+        if (it == spec.end()) fail(std::string(role) + " '" + name + "' is not a declared value");
+        return *it->second;
+    }
+
+    void link_entries() {
         for (const auto & e : prog.entries) {
             Entry en;
             en.spec = &e;
-            for (const auto & name : e.inputs) {
-                if (!spec.count(name)) fail("input '" + name + "' is not a declared value");
-                en.inputs.push_back(spec[name]);
-                input_set[name] = false;
-            }
-            for (const auto & name : e.outputs) {
-                if (!spec.count(name)) fail("output '" + name + "' is not a declared value");
-                en.outputs.push_back(spec[name]);
-            }
+            for (const auto & name : e.inputs) en.in.push_back(&declared(name, "input"));
+            for (const auto & name : e.outputs) en.out.push_back(&declared(name, "output"));
             entries.push_back(std::move(en));
         }
-        for (const auto & name : prog.state)
-            if (!spec.count(name)) fail("state '" + name + "' is not a declared value");
+        for (const auto & name : prog.state) (void) declared(name, "state");
     }
 
-    // Views with the binding's shape over the storage of every symbolic value.
-    void bind_values() {
-        if (bctx) {
-            ggml_free(bctx);
-            bctx = nullptr;
-        }
+    // The current binding's view of every symbolic value (same storage, the binding's shape).
+    void make_views() {
+        if (view_ctx) ggml_free(view_ctx);
+        view_ctx = nullptr;
         size_t n = 0;
         for (const auto & v : prog.values) n += v.symbolic();
         if (n == 0) return;
         ggml_init_params ip{};
         ip.mem_size = ggml_tensor_overhead() * (n + 1);
         ip.no_alloc = true;
-        bctx = ggml_init(ip);
+        view_ctx = ggml_init(ip);
         for (const auto & v : prog.values) {
             if (!v.symbolic()) continue;
-            const size_t nb1 = ggml_row_size((ggml_type) v.type, v.ne[0]), nb2 = nb1 * (size_t) v.ne[1],
-                         nb3 = nb2 * (size_t) v.ne[2];
-            ggml_tensor * t = ggml_view_4d(bctx, store.at(v.name), v.ne[0], v.ne[1], v.ne[2], v.ne[3], nb1, nb2, nb3, 0);
+            const size_t nb1 = ggml_row_size((ggml_type) v.type, v.ne[0]), nb2 = nb1 * (size_t) v.ne[1];
+            ggml_tensor * t = ggml_view_4d(view_ctx, storage.at(v.name), v.ne[0], v.ne[1], v.ne[2], v.ne[3], nb1, nb2,
+                                           nb2 * (size_t) v.ne[2], 0);
             if (!t || ggml_backend_view_init(t) != GGML_STATUS_SUCCESS) fail("cannot view driver value '" + v.name + "'");
             ggml_set_name(t, v.name.c_str());
-            view[v.name] = t;
+            bound[v.name] = t;
         }
     }
 
-    void rebind() {
-        if (binding == built) return;
-        prog.bind(binding);
-        for (auto * c : slice_ctxs) ggml_free(c);
-        slice_ctxs.clear();
-        bind_values();
-        for (auto & e : prog.entries) build_ops(e.driver);
-        built = binding;
+    ggml_tensor * value(const std::string & name) const {
+        const auto it = bound.find(name);
+        if (it == bound.end()) fail("driver value '" + name + "' is not declared");
+        return it->second;
     }
 
-    void build_ops(std::vector<DriverOp> & ops) {
-        for (auto & d : ops) {
+    // ------------------------------------------------------------------------ compiling drivers
+
+    void compile(Entry & e) {
+        e.code.clear();
+        emit_code(e.code, e.spec->driver);
+    }
+
+    void emit_code(std::vector<VmCode> & code, const std::vector<DriverOp> & ops_) {
+        for (const DriverOp & d : ops_) {
             if (!d.loop) {
-                build_call(d);
+                code.push_back({VmCode::Call, &d, -1, call_for(d)});
                 continue;
             }
-            for (const auto & c : d.carry) {
-                ggml_tensor *a = value(c.first), *b = value(c.second);
-                if (a->type != b->type || !ggml_are_same_shape(a, b))
-                    fail("loop carry '" + c.first + "' does not match its initial value '" + c.second + "'");
-            }
-            for (const auto & sc : d.scalars)
-                if (value(sc.first)->type != GGML_TYPE_F32) fail("loop scalar '" + sc.first + "' must be f32");
-            d.slice_rows.clear();
-            if (!d.slices.empty()) {
-                ggml_init_params ip{};
-                ip.mem_size = ggml_tensor_overhead() * (d.slices.size() * (size_t) d.n + 1);
-                ip.no_alloc = true;
-                ggml_context * vc = ggml_init(ip);
-                slice_ctxs.push_back(vc);
-                for (const auto & sl : d.slices) {
-                    ggml_tensor *a = value(sl.first), *b = value(sl.second);
-                    // the source is [n, ...a] in PyTorch order: a's elements n times, outermost
-                    if (a->type != b->type || ggml_nelements(b) != ggml_nelements(a) * d.n || !ggml_is_contiguous(b))
-                        fail("loop slice '" + sl.first + "' does not match its source '" + sl.second + "'");
-                    std::vector<ggml_tensor *> rows;
-                    for (int i = 0; i < d.n; i++) {
-                        ggml_tensor * r = ggml_view_4d(vc, b, a->ne[0], a->ne[1], a->ne[2], a->ne[3], a->nb[1], a->nb[2],
-                                                       a->nb[3], (size_t) i * ggml_nbytes(a));
-                        if (!r || ggml_backend_view_init(r) != GGML_STATUS_SUCCESS)
-                            fail("cannot view loop slice source '" + sl.second + "'");
-                        rows.push_back(r);
-                    }
-                    d.slice_rows.push_back(std::move(rows));
-                }
-            }
-            build_ops(d.body);
+            check_loop(d);
+            code.push_back({VmCode::Enter, &d, -1, -1});
+            const int top = (int) code.size();
+            code.push_back({VmCode::Top, &d, -1, -1});
+            emit_code(code, d.body);
+            code.push_back({VmCode::Bottom, &d, top, -1});
+            code[(size_t) top].jump = (int) code.size();
         }
     }
 
-    void build_call(DriverOp & d) {
-        if (d.site >= 0) {
-            // Rebinding: a stage with static shapes keeps its graph; any other is rebuilt when its
-            // site next runs (so one entry never rebuilds another's stages).
-            Site & c = sites[d.site];
-            if (!c.stage->symbolic) return;
-            if (c.ctx) ggml_free(c.ctx);
-            c.ctx = nullptr;
-            c.gf = nullptr;
-            c.stale = true;
-            return;
+    void check_loop(const DriverOp & d) const {
+        for (const auto & c : d.carry) {
+            const ggml_tensor *a = value(c.first), *b = value(c.second);
+            if (a->type != b->type || !ggml_are_same_shape(a, b))
+                fail("loop carry '" + c.first + "' does not match its initial value '" + c.second + "'");
         }
-        Site c;
+        for (const auto & sc : d.scalars)
+            if (value(sc.first)->type != GGML_TYPE_F32) fail("loop scalar '" + sc.first + "' must be f32");
+        for (const auto & sl : d.slices) {
+            // the source is [n, ...row] in PyTorch order: the row's elements n times, outermost
+            const ggml_tensor *row = value(sl.first), *src = value(sl.second);
+            if (row->type != src->type || ggml_nelements(src) != ggml_nelements(row) * d.n || !ggml_is_contiguous(src) ||
+                !ggml_is_contiguous(row))
+                fail("loop slice '" + sl.first + "' does not match its source '" + sl.second + "'");
+        }
+        for (const auto & m : d.masks)
+            if (spec.at(m.first)->type != GGML_TYPE_F32) fail("loop mask '" + m.first + "' must be f32");
+    }
+
+    // The call graph of driver call d, made the first time the call is compiled.
+    int call_for(const DriverOp & d) {
+        for (size_t k = 0; k < calls.size(); k++)
+            if (calls[k].op == &d) return (int) k;
+        CallGraph c;
+        c.op = &d;
         for (size_t k = 0; k < prog.stages.size(); k++)
-            if (prog.stages[k].name == d.stage) {
-                c.stage = &prog.stages[k];
-                c.stage_index = (int) k;
-            }
-        if (!c.stage) fail("driver calls unknown stage '" + d.stage + "'");
-        d.site = (int) sites.size();
-        sites.push_back(c);
-        build_site(d);
+            if (prog.stages[k].name == d.stage) c.stage = (int) k;
+        if (c.stage < 0) fail("driver calls unknown stage '" + d.stage + "'");
+        calls.push_back(c);
+        build_graph(calls.back());
+        return (int) calls.size() - 1;
     }
 
-    void build_site(const DriverOp & d) {
-        Site & cs = sites[d.site];
-        const StageSpec & st = *cs.stage;
-        cs.stale = false;
-        if (d.args.size() != st.params.size() || d.out.size() != st.outputs.size())
-            fail("call to stage '" + st.name + "' has the wrong number of arguments or results");
-        const size_t n_tensors = 8 * st.nodes.size() + 2 * st.outputs.size() + 16;
-        const size_t graph_size = n_tensors + st.params.size() + file.tensors.size() + 64;
-        ggml_init_params ip{};
-        ip.mem_size = ggml_tensor_overhead() * n_tensors + ggml_graph_overhead_custom(graph_size, false);
-        ip.no_alloc = true;
-        cs.ctx = ggml_init(ip);
-        std::unordered_map<std::string, ggml_tensor *> env;
-        for (size_t k = 0; k < st.params.size(); k++) {
-            ggml_tensor * arg = value(d.args[k]);
-            const TensorSpec & p = st.params[k];
-            for (int q = 0; q < 4; q++)
-                if (arg->ne[q] != p.ne[q] || arg->type != p.type)
-                    fail("stage '" + st.name + "' parameter " + p.name + " does not match value '" + d.args[k] + "'");
-            env[p.name] = arg;
-        }
+    // ------------------------------------------------------------------------- stage graphs
+
+    // The stage's results as tensors of c.ctx: from a compiled builder, or node by node.
+    std::vector<ggml_tensor *> stage_results(CallGraph & c, const StageSpec & st,
+                                             std::unordered_map<std::string, ggml_tensor *> & env) {
         std::vector<ggml_tensor *> results;
-        auto bf = builders.find(st.name);
-        if (bf != builders.end()) {
+        const auto custom = builders.find(st.name);
+        if (custom != builders.end()) {
             ggml_compiler_stage_build b;
-            b.ctx = cs.ctx;
+            b.ctx = c.ctx;
             b.backend = backend;
             b.wctx = wctx;
             b.binding = &binding;
             for (const auto & p : st.params) b.params.push_back(env.at(p.name));
             b.outputs.assign(st.outputs.size(), nullptr);
-            if (bf->second(&b) != 0 || !b.error.empty())
+            if (custom->second(&b) != 0 || !b.error.empty())
                 fail("builder for stage '" + st.name + "' failed: " + b.error);
-            std::unordered_map<std::string, const NodeSpec *> nodes;
-            for (const auto & n : st.nodes) nodes[n.id] = &n;
             for (size_t k = 0; k < st.outputs.size(); k++) {
                 ggml_tensor * t = b.outputs[k];
                 if (!t) fail("builder for stage '" + st.name + "' left output " + std::to_string(k) + " unset");
-                auto it = nodes.find(st.outputs[k]);
-                if (it != nodes.end()) {
-                    bool same = t->type == it->second->type;
-                    for (int q = 0; q < 4; q++) same = same && t->ne[q] == it->second->ne[q];
+                for (const auto & nd : st.nodes) {
+                    if (nd.id != st.outputs[k]) continue;
+                    bool same = t->type == nd.type;
+                    for (int q = 0; q < 4; q++) same = same && t->ne[q] == nd.ne[q];
                     if (!same)
                         fail("builder for stage '" + st.name + "' output " + std::to_string(k) +
                              " does not match the program");
                 }
                 results.push_back(t);
             }
-        } else {
-            std::vector<ggml_tensor *> src;
-            for (const auto & n : st.nodes) {
-                src.clear();
-                for (const auto & name : n.src) {
-                    auto it = env.find(name);
-                    if (it != env.end()) {
-                        src.push_back(it->second);
-                        continue;
-                    }
-                    ggml_tensor * w = wctx ? ggml_get_tensor(wctx, name.c_str()) : nullptr;
-                    if (!w) fail("stage '" + st.name + "' node " + n.id + " reads unknown tensor '" + name + "'");
-                    src.push_back(w);
-                }
-                env[n.id] = emit(cs.ctx, n, src);
-            }
-            for (const auto & id : st.outputs) {
-                auto it = env.find(id);
-                if (it == env.end()) fail("stage '" + st.name + "' returns unknown value '" + id + "'");
-                results.push_back(it->second);
-            }
+            return results;
         }
-        cs.gf = ggml_new_graph_custom(cs.ctx, graph_size, false);
-        for (ggml_tensor * t : results) ggml_build_forward_expand(cs.gf, t);
-        // Copies into the driver values go last, after every read of the stage's arguments.
+        std::vector<ggml_tensor *> srcs;
+        for (const auto & nd : st.nodes) {
+            srcs.clear();
+            for (const auto & name : nd.src) {
+                const auto it = env.find(name);
+                ggml_tensor * t = it != env.end() ? it->second : (wctx ? ggml_get_tensor(wctx, name.c_str()) : nullptr);
+                if (!t) fail("stage '" + st.name + "' node " + nd.id + " reads unknown tensor '" + name + "'");
+                srcs.push_back(t);
+            }
+            env[nd.id] = emit_node(c.ctx, nd, srcs);
+        }
+        for (const auto & id : st.outputs) {
+            const auto it = env.find(id);
+            if (it == env.end()) fail("stage '" + st.name + "' returns unknown value '" + id + "'");
+            results.push_back(it->second);
+        }
+        return results;
+    }
+
+    void build_graph(CallGraph & c) {
+        const StageSpec & st = prog.stages[(size_t) c.stage];
+        const DriverOp & d = *c.op;
+        c.stale = false;
+        if (d.args.size() != st.params.size() || d.out.size() != st.outputs.size())
+            fail("call to stage '" + st.name + "' has the wrong number of arguments or results");
+        const size_t tensors = 8 * st.nodes.size() + 2 * st.outputs.size() + 16;
+        const size_t graph_nodes = tensors + st.params.size() + file.tensors.size() + 64;
+        ggml_init_params ip{};
+        ip.mem_size = ggml_tensor_overhead() * tensors + ggml_graph_overhead_custom(graph_nodes, false);
+        ip.no_alloc = true;
+        c.ctx = ggml_init(ip);
+        std::unordered_map<std::string, ggml_tensor *> env;
+        for (size_t k = 0; k < st.params.size(); k++) {
+            ggml_tensor * arg = value(d.args[k]);
+            const TensorSpec & p = st.params[k];
+            bool fits = arg->type == p.type;
+            for (int q = 0; q < 4; q++) fits = fits && arg->ne[q] == p.ne[q];
+            if (!fits) fail("stage '" + st.name + "' parameter " + p.name + " does not match value '" + d.args[k] + "'");
+            env[p.name] = arg;
+        }
+        const std::vector<ggml_tensor *> results = stage_results(c, st, env);
+        c.graph = ggml_new_graph_custom(c.ctx, graph_nodes, false);
+        for (ggml_tensor * t : results) ggml_build_forward_expand(c.graph, t);
+        // Results reach their driver values through copies after every other node (so after
+        // every read of the stage's arguments); a result that already is its value's memory (a
+        // set_rows into the cache the stage read) needs none.
         for (size_t k = 0; k < results.size(); k++) {
             ggml_tensor *dst = value(d.out[k]), *res = results[k];
-            if (res == dst) continue;
-            // A result that is its value's memory already (set_rows into the state it read).
-            if (res->data && res->data == dst->data && res->type == dst->type && ggml_are_same_shape(res, dst) &&
-                ggml_is_contiguous(res))
-                continue;
+            const bool in_place = res == dst || (res->data && res->data == dst->data && res->type == dst->type &&
+                                                 ggml_are_same_shape(res, dst) && ggml_is_contiguous(res));
+            if (in_place) continue;
             if (ggml_nelements(res) != ggml_nelements(dst) || res->type != dst->type)
                 fail("stage '" + st.name + "' result " + std::to_string(k) + " does not match value '" + d.out[k] + "'");
-            ggml_build_forward_expand(cs.gf, ggml_cpy(cs.ctx, res, dst));
+            ggml_build_forward_expand(c.graph, ggml_cpy(c.ctx, res, dst));
         }
-        std::string unsupported;
-        for (int k = 0; k < ggml_graph_n_nodes(cs.gf); k++) {
-            ggml_tensor * t = ggml_graph_node(cs.gf, k);
+        std::string refused;
+        for (int k = 0; k < ggml_graph_n_nodes(c.graph); k++) {
+            ggml_tensor * t = ggml_graph_node(c.graph, k);
             if (!ggml_backend_supports_op(backend, t))
-                unsupported += std::string("\n  ") + t->name + " (" + ggml_op_desc(t) + "): " + last_error();
+                refused += std::string("\n  ") + t->name + " (" + ggml_op_desc(t) + "): " + last_error();
         }
-        if (!unsupported.empty())
+        if (!refused.empty())
             fail(std::string("backend ") + ggml_backend_name(backend) + " cannot run these nodes of stage '" + st.name +
-                 "':" + unsupported);
-        if (!cs.ga) cs.ga = ggml_gallocr_new(ggml_backend_get_default_buffer_type(backend));
-        if (!ggml_gallocr_alloc_graph(cs.ga, cs.gf))
+                 "':" + refused);
+        if (!c.alloc) c.alloc = ggml_gallocr_new(ggml_backend_get_default_buffer_type(backend));
+        if (!ggml_gallocr_alloc_graph(c.alloc, c.graph))
             fail("cannot allocate compute buffer for stage '" + st.name + "': " + last_error());
     }
 
-    void run_ops(const std::vector<DriverOp> & ops) {
-        using clock = std::chrono::steady_clock;
-        for (const auto & d : ops) {
-            if (!d.loop) {
-                if (sites[d.site].stale) build_site(d);
-                Site & c = sites[d.site];
-                const auto t0 = clock::now();
-                const ggml_status status = ggml_backend_graph_compute(backend, c.gf);
-                if (status != GGML_STATUS_SUCCESS)
-                    fail("stage '" + c.stage->name + "' failed: " + ggml_status_to_string(status) + ": " + last_error());
-                auto & st = stage_stats[c.stage_index];
-                st.ms += std::chrono::duration<double, std::milli>(clock::now() - t0).count();
-                st.calls++;
-                last.n_calls++;
-                continue;
+    // A new binding: values viewed at their new shapes; graphs of stages whose shapes read a symbol
+    // are rebuilt when next run (so an entry never rebuilds another entry's stages).
+    void apply_binding() {
+        if (binding == built) return;
+        prog.bind(binding);
+        make_views();
+        for (auto & c : calls) {
+            if (!prog.stages[(size_t) c.stage].symbolic) continue;
+            c.drop_graph();
+            c.stale = true;
+        }
+        for (auto & e : entries)
+            for (const VmCode & vc : e.code)
+                if (vc.kind == VmCode::Enter) check_loop(*vc.op);
+        built = binding;
+    }
+
+    // ------------------------------------------------------------------------------- running
+
+    void run_call(CallGraph & c) {
+        if (c.stale) build_graph(c);
+        const StageSpec & st = prog.stages[(size_t) c.stage];
+        last.n_calls++;
+        if (profile_file()) {
+            run_nodes(c, st);
+            return;
+        }
+        clock.mark(c.stage, ops.stream(), false);
+        if (graph_compute_async(backend, c.graph) != GGML_STATUS_SUCCESS)
+            fail("stage '" + st.name + "' failed: " + last_error());
+        clock.mark(c.stage, ops.stream(), true);
+    }
+
+    // Profiling: each node of the graph alone, waited for and timed.
+    void run_nodes(CallGraph & c, const StageSpec & st) {
+        using wall = std::chrono::steady_clock;
+        const auto t_call = wall::now();
+        ggml_cgraph one;
+        for (int k = 0; k < ggml_graph_n_nodes(c.graph); k++) {
+            ggml_tensor * t = ggml_graph_node(c.graph, k);
+            one.nodes.assign(1, t);
+            const auto t0 = wall::now();
+            if (ggml_backend_graph_compute(backend, &one) != GGML_STATUS_SUCCESS)
+                fail("profiling: node " + std::string(t->name) + " of stage '" + st.name + "' failed: " + last_error());
+            profile.push_back({st.name, t->name, ggml_op_desc(t),
+                               std::chrono::duration<double, std::milli>(wall::now() - t0).count()});
+        }
+        auto & tot = stage_totals[(size_t) c.stage];
+        tot.ms_total += std::chrono::duration<double, std::milli>(wall::now() - t_call).count();
+        tot.n_calls++;
+    }
+
+    void loop_enter(LoopFrame & f) {
+        const DriverOp & d = *f.op;
+        for (const auto & c : d.carry) ops.copy(value(c.first)->data, value(c.second)->data, ggml_nbytes(value(c.first)));
+        f.trips = d.n_symbol >= 0 ? (int) binding[(size_t) d.n_symbol] : d.n;
+        f.i = 0;
+        f.start.clear();
+        for (const auto & c : d.counters) f.start.push_back(ops.read_i32(value(c.second)->data));
+        for (const auto & c : d.collect) {
+            ggml_tensor * t = storage.at(c.first);
+            ops.clear(t->data, ggml_nbytes(t));
+        }
+    }
+
+    // Before the body of iteration f.i: scalars, slices, counters, bound symbols, causal masks.
+    void loop_top(LoopFrame & f) {
+        const DriverOp & d = *f.op;
+        const int i = f.i;
+        for (const auto & sc : d.scalars) {
+            ggml_tensor * t = value(sc.first);
+            uint32_t bits;
+            std::memcpy(&bits, &sc.second[(size_t) i], 4);
+            ops.fill32(t->data, ggml_nelements(t), bits);
+        }
+        for (const auto & sl : d.slices) {
+            ggml_tensor *row = value(sl.first), *src = value(sl.second);
+            const size_t nb = ggml_nbytes(row);
+            ops.copy(row->data, (const char *) src->data + (size_t) i * nb, nb);
+        }
+        for (size_t k = 0; k < d.counters.size(); k++)
+            ops.fill32(value(d.counters[k].first)->data, 1, (uint32_t) (f.start[k] + i));
+        if (!d.bind.empty()) {
+            std::vector<int64_t> with_counters = binding;
+            for (int32_t v : f.start) with_counters.push_back(v + i);
+            for (const auto & bnd : d.bind) {
+                const int64_t v = bnd.second(with_counters);
+                const Symbol & sy = prog.symbols[(size_t) bnd.first];
+                if (v < sy.min || v > sy.max)
+                    fail("loop binds " + sy.name + " = " + std::to_string(v) + ", outside its range");
+                binding[(size_t) bnd.first] = v;
             }
-            for (const auto & c : d.carry)
-                must("loop carry '" + c.first + "'", [&] { ggml_backend_tensor_copy(value(c.second), value(c.first)); });
-            const int n = d.n_symbol >= 0 ? (int) binding[d.n_symbol] : d.n;
-            std::vector<int32_t> starts;
-            for (const auto & c : d.counters) {
-                int32_t v = 0;
-                must("loop counter '" + c.first + "'", [&] { ggml_backend_tensor_get(value(c.second), &v, 0, sizeof v); });
-                starts.push_back(v);
-            }
-            for (const auto & c : d.collect) {
-                ggml_tensor * t = store.at(c.first);
-                must("loop collect '" + c.first + "'", [&] { ggml_backend_tensor_memset(t, 0, 0, ggml_nbytes(t)); });
-            }
-            std::vector<float> fill;
-            std::vector<int64_t> ext;
-            std::vector<char> row;
-            for (int i = 0; i < n; i++) {
-                for (const auto & sc : d.scalars) {
-                    ggml_tensor * t = value(sc.first);
-                    fill.assign((size_t) ggml_nelements(t), sc.second[(size_t) i]);
-                    must("loop scalar '" + sc.first + "'", [&] { ggml_backend_tensor_set(t, fill.data(), 0, ggml_nbytes(t)); });
-                }
-                for (size_t k = 0; k < d.slices.size(); k++)
-                    must("loop slice '" + d.slices[k].first + "'",
-                         [&] { ggml_backend_tensor_copy(d.slice_rows[k][(size_t) i], value(d.slices[k].first)); });
-                for (size_t k = 0; k < d.counters.size(); k++) {
-                    const int32_t v = starts[k] + i;
-                    must("loop counter '" + d.counters[k].first + "'",
-                         [&] { ggml_backend_tensor_set(value(d.counters[k].first), &v, 0, sizeof v); });
-                }
-                if (!d.bind.empty()) {
-                    ext = binding;
-                    for (int32_t v : starts) ext.push_back(v + i);
-                    for (const auto & bnd : d.bind) {
-                        const int64_t v = bnd.second.eval(ext);
-                        const Symbol & sy = prog.symbols[(size_t) bnd.first];
-                        if (v < sy.min || v > sy.max)
-                            fail("loop binds " + sy.name + " = " + std::to_string(v) + ", outside its range");
-                        binding[(size_t) bnd.first] = v;
+            apply_binding();
+        }
+        for (const auto & m : d.masks) {
+            const TensorSpec & v = *spec.at(m.first);
+            ops.causal((float *) storage.at(m.first)->data, v.ne[0] * v.ne[1] * v.ne[2] * v.ne[3], v.ne[0],
+                       f.start[(size_t) m.second] + i);
+        }
+    }
+
+    // After the body: collected rows; true when an until value holds a stop id.
+    bool loop_bottom(LoopFrame & f) {
+        const DriverOp & d = *f.op;
+        for (const auto & c : d.collect) {
+            const size_t nb = spec.at(c.second)->nbytes(binding);
+            ops.copy((char *) storage.at(c.first)->data + (size_t) f.i * nb, storage.at(c.second)->data, nb);
+        }
+        for (const auto & u : d.until) {
+            const int32_t tok = ops.read_i32(storage.at(u.first)->data);
+            if (std::find(u.second.begin(), u.second.end(), tok) != u.second.end()) return true;
+        }
+        return false;
+    }
+
+    void execute(const Entry & e) {
+        std::vector<LoopFrame> frames;
+        const std::vector<VmCode> & code = e.code;
+        size_t pc = 0;
+        while (pc < code.size()) {
+            const VmCode & in = code[pc];
+            switch (in.kind) {
+                case VmCode::Call:
+                    run_call(calls[(size_t) in.call]);
+                    pc++;
+                    break;
+                case VmCode::Enter:
+                    frames.push_back({in.op, 0, 0, {}});
+                    loop_enter(frames.back());
+                    pc++;
+                    break;
+                case VmCode::Top:
+                    if (frames.back().i >= frames.back().trips) {
+                        frames.pop_back();
+                        pc = (size_t) in.jump;
+                    } else {
+                        loop_top(frames.back());
+                        pc++;
                     }
-                    rebind();  // a no-op unless a symbol changed
-                }
-                for (const auto & m : d.masks) {
-                    // the causal mask row(s) of position pos: 0 up to pos, -inf after
-                    const TensorSpec & v = *spec.at(m.first);
-                    const int64_t pos = starts[(size_t) m.second] + i, len = v.ne[0];
-                    fill.resize((size_t) (v.ne[0] * v.ne[1] * v.ne[2] * v.ne[3]));
-                    for (size_t j = 0; j < fill.size(); j++) fill[j] = (int64_t) (j % (size_t) len) <= pos ? 0.0f : -INFINITY;
-                    if (v.type != GGML_TYPE_F32) fail("loop mask '" + m.first + "' must be f32");
-                    must("loop mask '" + m.first + "'",
-                         [&] { ggml_backend_tensor_set(store.at(m.first), fill.data(), 0, fill.size() * sizeof(float)); });
-                }
-                run_ops(d.body);
-                for (const auto & c : d.collect) {
-                    const size_t nb = spec.at(c.second)->nbytes(binding);
-                    row.resize(nb);
-                    must("loop collect '" + c.first + "'", [&] {
-                        ggml_backend_tensor_get(store.at(c.second), row.data(), 0, nb);
-                        ggml_backend_tensor_set(store.at(c.first), row.data(), (size_t) i * nb, nb);
-                    });
-                }
-                bool stop = false;
-                for (const auto & u : d.until) {
-                    int32_t v = 0;
-                    must("loop until '" + u.first + "'", [&] { ggml_backend_tensor_get(store.at(u.first), &v, 0, sizeof v); });
-                    stop = stop || std::find(u.second.begin(), u.second.end(), v) != u.second.end();
-                }
-                if (stop) break;
+                    break;
+                case VmCode::Bottom:
+                    if (loop_bottom(frames.back())) {
+                        frames.pop_back();
+                        pc = (size_t) code[(size_t) in.jump].jump;
+                    } else {
+                        frames.back().i++;
+                        pc = (size_t) in.jump;
+                    }
+                    break;
             }
         }
     }
+
+    void run(const char * entry_name) {
+        const Entry * e = nullptr;
+        for (const auto & en : entries)
+            if (en.spec->name == entry_name) e = &en;
+        require(e != nullptr, "no entry point named '" + std::string(entry_name) + "'");
+        for (const TensorSpec * v : e->in) require(inputs_set.count(v->name) != 0, "input '" + v->name + "' was never set");
+        apply_binding();
+        for (auto & t : stage_totals) t = ggml_compiler_stats{};
+        last = ggml_compiler_stats{};
+        clock.begin_run();
+        const auto t0 = std::chrono::steady_clock::now();
+        execute(*e);
+        ops.finish();
+        last.ms_total = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+        clock.collect([&](int stage, double ms) {
+            stage_totals[(size_t) stage].ms_total += ms;
+            stage_totals[(size_t) stage].n_calls++;
+        });
+        write_profile();
+    }
+
+    void write_profile() {
+        if (!profile_file() || profile.empty()) return;
+        if (FILE * f = std::fopen(profile_file(), "a")) {
+            for (const auto & p : profile)
+                std::fprintf(f, "%s\t%s\t%s\t%.6f\n", p.stage.c_str(), p.node.c_str(), p.op.c_str(), p.ms);
+            std::fclose(f);
+        }
+        profile.clear();
+    }
+
+    // ------------------------------------------------------------------------- inputs, outputs
+
+    const TensorSpec & input(const char * name) const {
+        for (const auto & e : entries)
+            for (const TensorSpec * v : e.in)
+                if (v->name == name) return *v;
+        fail("no input named '" + std::string(name) + "'");
+    }
+
+    // The symbols an input's shape fixes: a dim with one unknown symbol is solved by bisection over
+    // the symbol's range (dims are monotone in each symbol); then every dim must match.
+    void bind_shape(const TensorSpec & v, const std::vector<int64_t> & shape) {
+        if (shape.size() != v.shape_x.size())
+            fail("input '" + v.name + "' has rank " + std::to_string(v.shape_x.size()) + ", got " +
+                 std::to_string(shape.size()));
+        std::vector<int64_t> b = binding;
+        std::vector<bool> known(b.size(), false);
+        for (int pass = 0; pass < 2; pass++) {
+            for (size_t i = 0; i < shape.size(); i++) {
+                std::vector<bool> used(b.size(), false);
+                v.shape_x[i].mark(used);
+                int unknown = -1, n_unknown = 0;
+                for (size_t k = 0; k < used.size(); k++)
+                    if (used[k] && !known[k]) {
+                        unknown = (int) k;
+                        n_unknown++;
+                    }
+                if (n_unknown != 1) continue;
+                const Symbol & sy = prog.symbols[(size_t) unknown];
+                int64_t lo = sy.min, hi = sy.max;
+                while (lo < hi) {  // the smallest value whose dim reaches shape[i]
+                    const int64_t mid = lo + (hi - lo) / 2;
+                    b[(size_t) unknown] = mid;
+                    if (v.shape_x[i](b) < shape[i]) lo = mid + 1;
+                    else hi = mid;
+                }
+                b[(size_t) unknown] = lo;
+                if (v.shape_x[i](b) != shape[i])
+                    fail("input '" + v.name + "': no " + sy.name + " in [" + std::to_string(sy.min) + ", " +
+                         std::to_string(sy.max) + "] gives dim " + std::to_string(i) + " = " + std::to_string(shape[i]));
+                known[(size_t) unknown] = true;
+            }
+        }
+        const std::vector<int64_t> got = v.shape(b);
+        if (got != shape) {
+            std::string want, have;
+            for (auto dv : shape) want += (want.empty() ? "" : ", ") + std::to_string(dv);
+            for (auto dv : got) have += (have.empty() ? "" : ", ") + std::to_string(dv);
+            fail("input '" + v.name + "' cannot have shape [" + want + "] (with the other symbols as bound, it is [" +
+                 have + "])");
+        }
+        binding = b;
+    }
+
+    void write_input(const char * name, const void * data, size_t nbytes) {
+        const TensorSpec & v = input(name);
+        const size_t want = v.nbytes(binding);
+        require(nbytes == want, "input '" + std::string(name) + "' needs " + std::to_string(want) + " bytes, got " +
+                                    std::to_string(nbytes));
+        ggml_checked("input '" + std::string(name) + "'",
+                     [&] { ggml_backend_tensor_set(storage.at(v.name), data, 0, nbytes); });
+        inputs_set.insert(v.name);
+    }
+
+    void read_output(const char * name, void * dst, size_t nbytes) const {
+        for (const auto & e : entries)
+            for (const TensorSpec * v : e.out) {
+                if (v->name != name) continue;
+                const size_t have = v->nbytes(built);
+                require(nbytes == have, "output '" + std::string(name) + "' has " + std::to_string(have) +
+                                            " bytes, buffer has " + std::to_string(nbytes));
+                ggml_checked("output '" + std::string(name) + "'",
+                             [&] { ggml_backend_tensor_get(storage.at(name), dst, 0, nbytes); });
+                return;
+            }
+        fail("no output named '" + std::string(name) + "'");
+    }
+
+    void clear_state() {
+        for (const auto & name : prog.state) {
+            ggml_tensor * t = storage.at(name);
+            ops.clear(t->data, ggml_nbytes(t));
+        }
+        ops.finish();
+    }
+
+    void describe(const TensorSpec & v, const std::vector<int64_t> & b, ggml_compiler_tensor_info * info) const {
+        require(info != nullptr, "info is NULL");
+        static const std::map<int, ggml_compiler_dtype> dtypes = {
+            {GGML_TYPE_F32, GGML_COMPILER_DTYPE_F32}, {GGML_TYPE_F16, GGML_COMPILER_DTYPE_F16},
+            {GGML_TYPE_I32, GGML_COMPILER_DTYPE_I32}};
+        const auto dt = dtypes.find(v.type);
+        if (dt == dtypes.end()) fail("value '" + v.name + "' has a type the C API cannot describe");
+        const std::vector<int64_t> shape = v.shape(b);
+        require(shape.size() <= GGML_COMPILER_MAX_RANK, "value '" + v.name + "' has rank above GGML_COMPILER_MAX_RANK");
+        info->name = v.name.c_str();
+        info->dtype = dt->second;
+        info->ndim = (int) shape.size();
+        std::copy(shape.begin(), shape.end(), info->shape);
+        info->nbytes = v.nbytes(b);
+    }
+
+    const Entry * entry_at(int e) const { return e >= 0 && e < (int) entries.size() ? &entries[(size_t) e] : nullptr; }
 };
 
 // ------------------------------------------------------------------------------------ C API
 
 namespace {
 
-int fill_info(const TensorSpec & v, const std::vector<int64_t> & b, ggml_compiler_tensor_info * info) {
-    require(info != nullptr, "info is NULL");
-    std::vector<int64_t> shape;
-    for (const auto & d : v.shape_x) shape.push_back(d.eval(b));
-    switch (v.type) {
-        case GGML_TYPE_F32: info->dtype = GGML_COMPILER_DTYPE_F32; break;
-        case GGML_TYPE_F16: info->dtype = GGML_COMPILER_DTYPE_F16; break;
-        case GGML_TYPE_I32: info->dtype = GGML_COMPILER_DTYPE_I32; break;
-        default: fail("value '" + v.name + "' has a type the C API cannot describe");
-    }
-    require(shape.size() <= GGML_COMPILER_MAX_RANK, "value '" + v.name + "' has rank above GGML_COMPILER_MAX_RANK");
-    info->name = v.name.c_str();
-    info->ndim = (int) shape.size();
-    for (size_t k = 0; k < shape.size(); k++) info->shape[k] = shape[k];
-    info->nbytes = v.nbytes(b);
-    return 0;
+// A C entry point's body: 0, or -1 with the message recorded; pointer / value variants return
+// `bad` on an error.
+template <class F>
+int api(F && f) {
+    return guarded(std::forward<F>(f));
 }
-
-// The symbols an input's shape fixes: a dim with one unknown symbol is solved by bisection over
-// the symbol's range (dims are monotone in each symbol); then every dim must match.
-void solve_shape(ggml_compiler_model * m, const TensorSpec & v, const std::vector<int64_t> & shape) {
-    if (shape.size() != v.shape_x.size())
-        fail("input '" + v.name + "' has rank " + std::to_string(v.shape_x.size()) + ", got " +
-             std::to_string(shape.size()));
-    std::vector<int64_t> b = m->binding;
-    std::vector<bool> known(b.size(), false);
-    for (int pass = 0; pass < 2; pass++) {
-        for (size_t i = 0; i < shape.size(); i++) {
-            std::vector<bool> used(b.size(), false);
-            v.shape_x[i].uses(used);
-            int unknown = -1, n_unknown = 0;
-            for (size_t k = 0; k < used.size(); k++)
-                if (used[k] && !known[k]) {
-                    unknown = (int) k;
-                    n_unknown++;
-                }
-            if (n_unknown != 1) continue;
-            const Symbol & sy = m->prog.symbols[(size_t) unknown];
-            int64_t lo = sy.min, hi = sy.max;
-            while (lo < hi) {  // the smallest value whose dim reaches shape[i]
-                const int64_t mid = lo + (hi - lo) / 2;
-                b[(size_t) unknown] = mid;
-                if (v.shape_x[i].eval(b) < shape[i]) lo = mid + 1;
-                else hi = mid;
-            }
-            b[(size_t) unknown] = lo;
-            if (v.shape_x[i].eval(b) != shape[i])
-                fail("input '" + v.name + "': no " + sy.name + " in [" + std::to_string(sy.min) + ", " +
-                     std::to_string(sy.max) + "] gives dim " + std::to_string(i) + " = " + std::to_string(shape[i]));
-            known[(size_t) unknown] = true;
-        }
-    }
-    std::vector<int64_t> got;
-    for (const auto & d : v.shape_x) got.push_back(d.eval(b));
-    if (got != shape) {
-        std::string want, have;
-        for (auto d : shape) want += (want.empty() ? "" : ", ") + std::to_string(d);
-        for (auto d : got) have += (have.empty() ? "" : ", ") + std::to_string(d);
-        fail("input '" + v.name + "' cannot have shape [" + want + "] (with the other symbols as bound, it is [" + have +
-             "])");
-    }
-    m->binding = b;
-}
-
-// Run f; on an error record the message and return `bad`.
 template <class T, class F>
-T guarded_value(T bad, F && f) {
+T api_or(T bad, F && f) {
     T out = bad;
-    if (guarded([&] { out = f(); }) != 0) return bad;
-    return out;
+    return guarded([&] { out = f(); }) == 0 ? out : bad;
 }
 
 }  // namespace
@@ -1482,8 +1787,7 @@ ggml_compiler_model * ggml_compiler_load(const char * path, const ggml_compiler_
 
 ggml_compiler_model * ggml_compiler_load_with(const char * path, const ggml_compiler_options * opt,
                                               const ggml_compiler_builder * builders, int n_builders) {
-    const ggml_compiler_options o = opt ? *opt : ggml_compiler_default_options();
-    return guarded_value<ggml_compiler_model *>(nullptr, [&]() -> ggml_compiler_model * {
+    return api_or<ggml_compiler_model *>(nullptr, [&] {
         require(path != nullptr, "path is NULL");
         require(n_builders == 0 || builders != nullptr, "builders is NULL");
         auto m = std::make_unique<ggml_compiler_model>();
@@ -1491,11 +1795,11 @@ ggml_compiler_model * ggml_compiler_load_with(const char * path, const ggml_comp
             require(builders[k].stage && builders[k].build, "builder " + std::to_string(k) + " is incomplete");
             m->builders[builders[k].stage] = builders[k].build;
         }
-        m->load(path, o);
-        for (const auto & b : m->builders) {
-            bool found = false;
-            for (const auto & st : m->prog.stages) found = found || st.name == b.first;
-            if (!found) fail("builder for stage '" + b.first + "', which the program does not have");
+        m->open(path, opt ? *opt : ggml_compiler_default_options());
+        for (const auto & kv : m->builders) {
+            const bool known = std::any_of(m->prog.stages.begin(), m->prog.stages.end(),
+                                           [&](const StageSpec & st) { return st.name == kv.first; });
+            if (!known) fail("builder for stage '" + kv.first + "', which the program does not have");
         }
         return m.release();
     });
@@ -1511,41 +1815,34 @@ bool ggml_compiler_build_supports(ggml_compiler_stage_build * b, const ggml_tens
 
 ggml_tensor * ggml_compiler_build_param(ggml_compiler_stage_build * b, int i) {
     if (!b) return nullptr;
-    if (i < 0 || i >= (int) b->params.size()) {
-        b->error = "parameter index " + std::to_string(i) + " out of range";
-        return nullptr;
-    }
-    return b->params[(size_t) i];
+    if (i >= 0 && i < (int) b->params.size()) return b->params[(size_t) i];
+    b->error = "parameter index " + std::to_string(i) + " out of range";
+    return nullptr;
 }
 
 ggml_tensor * ggml_compiler_build_weight(ggml_compiler_stage_build * b, const char * name) {
     if (!b) return nullptr;
-    ggml_tensor * t = b->wctx && name ? ggml_get_tensor(b->wctx, name) : nullptr;
+    ggml_tensor * t = (b->wctx && name) ? ggml_get_tensor(b->wctx, name) : nullptr;
     if (!t) b->error = std::string("no tensor '") + (name ? name : "(null)") + "' in the GGUF";
     return t;
 }
 
 int64_t ggml_compiler_build_symbol(ggml_compiler_stage_build * b, int i) {
     if (!b) return 1;
-    if (!b->binding || i < 0 || i >= (int) b->binding->size()) {
-        b->error = "symbol index " + std::to_string(i) + " out of range";
-        return 1;
-    }
-    return (*b->binding)[(size_t) i];
+    if (b->binding && i >= 0 && i < (int) b->binding->size()) return (*b->binding)[(size_t) i];
+    b->error = "symbol index " + std::to_string(i) + " out of range";
+    return 1;
 }
 
 void ggml_compiler_build_output(ggml_compiler_stage_build * b, int i, ggml_tensor * t) {
     if (!b) return;
-    if (i < 0 || i >= (int) b->outputs.size()) {
-        b->error = "output index " + std::to_string(i) + " out of range";
-        return;
-    }
-    b->outputs[(size_t) i] = t;
+    if (i >= 0 && i < (int) b->outputs.size()) b->outputs[(size_t) i] = t;
+    else b->error = "output index " + std::to_string(i) + " out of range";
 }
 
 const char * ggml_compiler_metadata(const ggml_compiler_model * m, const char * key) {
     if (!m || !key) return nullptr;
-    auto it = m->file.strings.find(key);
+    const auto it = m->file.strings.find(key);
     return it == m->file.strings.end() ? nullptr : it->second.c_str();
 }
 
@@ -1558,34 +1855,35 @@ const char * ggml_compiler_backend_name(const ggml_compiler_model * m) {
 int ggml_compiler_n_entries(const ggml_compiler_model * m) { return m ? (int) m->entries.size() : -1; }
 
 const char * ggml_compiler_entry_name(const ggml_compiler_model * m, int e) {
-    if (!m || e < 0 || e >= (int) m->entries.size()) {
-        set_error("entry index out of range");
-        return nullptr;
-    }
-    return m->entries[(size_t) e].spec->name.c_str();
+    const auto * en = m ? m->entry_at(e) : nullptr;
+    if (en) return en->spec->name.c_str();
+    set_error("entry index out of range");
+    return nullptr;
 }
 
 int ggml_compiler_entry_n_inputs(const ggml_compiler_model * m, int e) {
-    return m && e >= 0 && e < (int) m->entries.size() ? (int) m->entries[(size_t) e].inputs.size() : -1;
+    const auto * en = m ? m->entry_at(e) : nullptr;
+    return en ? (int) en->in.size() : -1;
 }
 
 int ggml_compiler_entry_n_outputs(const ggml_compiler_model * m, int e) {
-    return m && e >= 0 && e < (int) m->entries.size() ? (int) m->entries[(size_t) e].outputs.size() : -1;
+    const auto * en = m ? m->entry_at(e) : nullptr;
+    return en ? (int) en->out.size() : -1;
 }
 
 int ggml_compiler_entry_input_info(const ggml_compiler_model * m, int e, int i, ggml_compiler_tensor_info * info) {
-    return guarded_value<int>(-1, [&] {
-        require(m && e >= 0 && e < (int) m->entries.size() && i >= 0 && i < (int) m->entries[(size_t) e].inputs.size(),
-                "input index out of range");
-        return fill_info(*m->entries[(size_t) e].inputs[(size_t) i], m->binding, info);
+    return api([&] {
+        const auto * en = m ? m->entry_at(e) : nullptr;
+        require(en && i >= 0 && i < (int) en->in.size(), "input index out of range");
+        m->describe(*en->in[(size_t) i], m->binding, info);
     });
 }
 
 int ggml_compiler_entry_output_info(const ggml_compiler_model * m, int e, int i, ggml_compiler_tensor_info * info) {
-    return guarded_value<int>(-1, [&] {
-        require(m && e >= 0 && e < (int) m->entries.size() && i >= 0 && i < (int) m->entries[(size_t) e].outputs.size(),
-                "output index out of range");
-        return fill_info(*m->entries[(size_t) e].outputs[(size_t) i], m->binding, info);
+    return api([&] {
+        const auto * en = m ? m->entry_at(e) : nullptr;
+        require(en && i >= 0 && i < (int) en->out.size(), "output index out of range");
+        m->describe(*en->out[(size_t) i], m->binding, info);
     });
 }
 
@@ -1599,12 +1897,9 @@ int ggml_compiler_output_info(const ggml_compiler_model * m, int i, ggml_compile
 }
 
 int ggml_compiler_reset(ggml_compiler_model * m) {
-    return guarded([&] {
+    return api([&] {
         require(m != nullptr, "model is NULL");
-        for (const auto & name : m->prog.state) {
-            ggml_tensor * t = m->store.at(name);
-            must("reset of '" + name + "'", [&] { ggml_backend_tensor_memset(t, 0, 0, ggml_nbytes(t)); });
-        }
+        m->clear_state();
     });
 }
 
@@ -1612,48 +1907,37 @@ int ggml_compiler_n_symbols(const ggml_compiler_model * m) { return m ? (int) m-
 
 int ggml_compiler_symbol_info(const ggml_compiler_model * m, int i, const char ** name, int64_t * min, int64_t * max,
                               int64_t * value) {
-    if (!m || i < 0 || i >= (int) m->prog.symbols.size()) {
-        set_error("symbol index out of range");
-        return -1;
-    }
-    const Symbol & sy = m->prog.symbols[(size_t) i];
-    if (name) *name = sy.name.c_str();
-    if (min) *min = sy.min;
-    if (max) *max = sy.max;
-    if (value) *value = m->binding[(size_t) i];
-    return 0;
+    return api([&] {
+        require(m && i >= 0 && i < (int) m->prog.symbols.size(), "symbol index out of range");
+        const Symbol & sy = m->prog.symbols[(size_t) i];
+        if (name) *name = sy.name.c_str();
+        if (min) *min = sy.min;
+        if (max) *max = sy.max;
+        if (value) *value = m->binding[(size_t) i];
+    });
 }
 
 int ggml_compiler_set_symbol(ggml_compiler_model * m, const char * name, int64_t value) {
-    return guarded([&] {
+    return api([&] {
         require(m && name, "NULL argument");
-        const int i = m->prog.symbol(name);
-        require(i >= 0, "no symbol named '" + std::string(name) + "'");
-        const Symbol & sy = m->prog.symbols[(size_t) i];
-        require(value >= sy.min && value <= sy.max, "symbol '" + sy.name + "' = " + std::to_string(value) +
-                                                        " is outside [" + std::to_string(sy.min) + ", " +
-                                                        std::to_string(sy.max) + "]");
-        m->binding[(size_t) i] = value;
+        const int k = m->prog.symbol(name);
+        require(k >= 0, "no symbol named '" + std::string(name) + "'");
+        m->prog.check_range(k, value);
+        m->binding[(size_t) k] = value;
     });
 }
 
 int ggml_compiler_set_input_shape(ggml_compiler_model * m, const char * name, int ndim, const int64_t * shape) {
-    return guarded([&] {
+    return api([&] {
         require(m && name && (ndim <= 0 || shape), "NULL argument");
-        require(m->input_set.count(name) != 0, "no input named '" + std::string(name) + "'");
-        solve_shape(m, *m->spec.at(name), std::vector<int64_t>(shape, shape + std::max(ndim, 0)));
+        m->bind_shape(m->input(name), std::vector<int64_t>(shape, shape + std::max(ndim, 0)));
     });
 }
 
 int ggml_compiler_set_input(ggml_compiler_model * m, const char * name, const void * data, size_t nbytes) {
-    return guarded([&] {
+    return api([&] {
         require(m && name && data, "NULL argument");
-        require(m->input_set.count(name) != 0, "no input named '" + std::string(name) + "'");
-        const size_t want = m->spec.at(name)->nbytes(m->binding);
-        require(nbytes == want, "input '" + std::string(name) + "' needs " + std::to_string(want) + " bytes, got " +
-                                    std::to_string(nbytes));
-        must("input '" + std::string(name) + "'", [&] { ggml_backend_tensor_set(m->store.at(name), data, 0, nbytes); });
-        m->input_set[name] = true;
+        m->write_input(name, data, nbytes);
     });
 }
 
@@ -1666,60 +1950,35 @@ int ggml_compiler_run(ggml_compiler_model * m) {
 }
 
 int ggml_compiler_run_entry(ggml_compiler_model * m, const char * entry) {
-    return guarded([&] {
+    return api([&] {
         require(m && entry, "NULL argument");
-        const ggml_compiler_model::Entry * e = nullptr;
-        for (const auto & en : m->entries)
-            if (en.spec->name == entry) e = &en;
-        require(e != nullptr, "no entry point named '" + std::string(entry) + "'");
-        for (const TensorSpec * v : e->inputs)
-            require(m->input_set.at(v->name), "input '" + v->name + "' was never set");
-        m->rebind();
-        for (auto & st : m->stage_stats) st = StageStat{};
-        m->last.n_calls = 0;
-        const auto t0 = std::chrono::steady_clock::now();
-        m->run_ops(e->spec->driver);
-        ggml_backend_synchronize(m->backend);
-        m->last.ms_total = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+        m->run(entry);
     });
 }
 
 int ggml_compiler_get_output(ggml_compiler_model * m, const char * name, void * dst, size_t nbytes) {
-    return guarded([&] {
+    return api([&] {
         require(m && name && dst, "NULL argument");
-        for (const auto & e : m->entries)
-            for (const TensorSpec * v : e.outputs) {
-                if (v->name != name) continue;
-                const size_t have = v->nbytes(m->built);
-                require(nbytes == have, "output '" + std::string(name) + "' has " + std::to_string(have) +
-                                            " bytes, buffer has " + std::to_string(nbytes));
-                must("output '" + std::string(name) + "'", [&] { ggml_backend_tensor_get(m->store.at(name), dst, 0, nbytes); });
-                return;
-            }
-        fail("no output named '" + std::string(name) + "'");
+        m->read_output(name, dst, nbytes);
     });
 }
 
 int ggml_compiler_last_stats(const ggml_compiler_model * m, ggml_compiler_stats * st) {
-    if (!m || !st) {
-        set_error("NULL argument");
-        return -1;
-    }
-    *st = m->last;
-    return 0;
+    return api([&] {
+        require(m && st, "NULL argument");
+        *st = m->last;
+    });
 }
 
 int ggml_compiler_n_stages(const ggml_compiler_model * m) { return m ? (int) m->prog.stages.size() : -1; }
 
 int ggml_compiler_stage_stats(const ggml_compiler_model * m, int i, const char ** name, double * ms, int * n_calls) {
-    if (!m || i < 0 || i >= (int) m->prog.stages.size()) {
-        set_error("stage index out of range");
-        return -1;
-    }
-    if (name) *name = m->prog.stages[(size_t) i].name.c_str();
-    if (ms) *ms = m->stage_stats[(size_t) i].ms;
-    if (n_calls) *n_calls = m->stage_stats[(size_t) i].calls;
-    return 0;
+    return api([&] {
+        require(m && i >= 0 && i < (int) m->prog.stages.size(), "stage index out of range");
+        if (name) *name = m->prog.stages[(size_t) i].name.c_str();
+        if (ms) *ms = m->stage_totals[(size_t) i].ms_total;
+        if (n_calls) *n_calls = m->stage_totals[(size_t) i].n_calls;
+    });
 }
 
 }  // extern "C"
