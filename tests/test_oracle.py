@@ -174,6 +174,84 @@ def test_q4_K_encoder_special_blocks(orc):
     assert np.abs(back - pos).max() < 0.1 * pos.max()
 
 
+# ----------------------------------------------------- K-quant encoders: the search, pinned
+
+def _kr():
+    import sys
+
+    sys.path.insert(0, str(GOLDEN))
+    import kquant_ref
+
+    return kquant_ref
+
+
+def _kquant_kats():
+    return {k: v for k, v in _kats().items() if v["kind"] == "weight" and v["type"] in ("q4_K", "q5_K", "q6_K")}
+
+
+def test_kquant_restatement_reproduces_kats():
+    """tests/golden/kquant_ref.py (a Python restatement of ggml's make_qkx2_quants /
+    make_qx_quants encoders, written apart from the C oracle) gives every K-quant fixture's bytes,
+    the hand-worked exact-grid block included; test_encoder_known_answers holds the oracle to the
+    same bytes."""
+    kr = _kr()
+    for name, k in _kquant_kats().items():
+        assert kr.ENCODERS[k["type"]](k["x"]).hex() == k["hex"], name
+
+
+def test_kquant_kats_expose_every_wrong_search_parameter():
+    """Each wrong parameter of the encoders' searches (make_qkx2_quants' rmin / rdelta / nstep and
+    sub-block weighting, make_qx_quants' candidate range and weighting) changes the bytes of at
+    least one fixture, so an oracle with that mistake fails test_encoder_known_answers."""
+    kr = _kr()
+    rec = json.loads((GOLDEN / "kquant_mutations.json").read_text())
+    kats = _kquant_kats()
+    for t, muts in rec["mutations"].items():
+        for mname, kw in muts.items():
+            kw = {k: (range(v[0], v[-1] + 1) if isinstance(v, list) and v else range(0) if isinstance(v, list) else v)
+                  for k, v in kw.items()}
+            caught = [n for n, c in rec["caught_by"].items() if mname in c["catches"] and kats[n]["type"] == t]
+            assert caught, (t, mname)
+            x = kats[caught[0]]["x"]
+            assert kr.ENCODERS[t](x, **kw).hex() != kats[caught[0]]["hex"], (t, mname, caught[0])
+
+
+def test_kquant_kats_cover_the_search_branches():
+    """The fixtures exercise the branches the reference's error bounds leave open: a candidate of the
+    search beating the min/max fit (the exact-grid Q4_K block; the last candidate winning in Q4_K and
+    Q5_K), the least-squares min clamped to 0, an fp16-subnormal dmin, and Q6_K's search moving the
+    scale away from -nmax / max."""
+    kr = _kr()
+    seen = {t: set() for t in ("q4_K", "q5_K", "q6_K")}
+    for name, k in _kquant_kats().items():
+        t, tr = k["type"], []
+        h = kr.ENCODERS[t](k["x"], trace=tr)
+        if t == "q6_K":
+            if any(w != 0 for w in tr):
+                seen[t].add("search moves the scale")
+            continue
+        if any(w >= 0 for w, _ in tr):
+            seen[t].add("a candidate beats min/max")
+        if any(c for _, c in tr):
+            seen[t].add("clamped min wins")
+        if any(w == (20 if t == "q4_K" else 15) for w, _ in tr):
+            seen[t].add("last candidate wins")
+        if 0 < int.from_bytes(h[2:4], "little") < 0x400:
+            seen[t].add("subnormal dmin")
+    full = {"a candidate beats min/max", "clamped min wins", "last candidate wins", "subnormal dmin"}
+    assert seen == {"q4_K": full, "q5_K": full, "q6_K": {"search moves the scale"}}
+
+
+@pytest.mark.parametrize("t", ["q4_K", "q5_K", "q6_K"])
+def test_kquant_oracle_equals_restatement_on_random_blocks(orc, t):
+    """The C oracle and the Python restatement agree byte for byte beyond the fixtures."""
+    kr = _kr()
+    rng = np.random.default_rng(11)
+    for trial in range(6):
+        x = (rng.normal(0, 0.02, 256) if trial % 2 else rng.standard_t(3, 256) * 0.01).astype(np.float32)
+        assert orc.quantize(x[None], t).tobytes() == kr.ENCODERS[t](x.tolist()), (t, trial)
+
+
 def test_kquant_row_sizes(orc):
     """Bytes per 256 values: 144 / 176 / 210 (ggml_compiler/compiler.py:82)."""
     assert [orc.row_size(t, 512) for t in ("q4_K", "q5_K", "q6_K")] == [288, 352, 420]
