@@ -356,79 +356,85 @@ struct Llama {
         const Tensor & E = tensors[t_embd];
         launch_embed_rope(E.type, E.buf.p, E.rows, E.cols, tok_dev, xs, pos_dev, c.head_dim, c.rope_base, rope_cs.p,
                           stream);
-        const float scale = 1.0f / std::sqrt((float) c.head_dim);
-        const int64_t kv_h = (int64_t) c.max_ctx * c.head_dim;
-        for (int l = 0; l < c.n_layer; l++) {
-            const Layer & L = layers[l];
-            uint16_t * kvl = kv_layer(l);
-            RowArgs a = row_args(L.qkv);
-            a.x = xs;
-            a.norm_w = tensors[L.attn_norm].buf.as<float>();
-            a.eps = c.rms_eps;
-            a.y = qkv.as<float>();
-            a.pos = pos_dev;
-            a.kc = kvl;
-            a.vc = kvl + (size_t) c.n_head_kv * kv_h;
-            a.ctx = c.max_ctx;
-            a.H = c.n_head;
-            a.Hkv = c.n_head_kv;
-            a.D = c.head_dim;
-            a.rope_cs = rope_cs.as<float2>();
-            launch_row_gemv(c.wtype, PRO_NORM, EPI_ROPE_KV, a, stream);
-            if (decode_attn) {
-                // Spare CUs read this layer's output projection and the next layer's QKV weights
-                // into the Infinity Cache while the attention runs.
-                Prefetch pf;
-                pf.p[0] = tensors[L.wo].buf.as<uint8_t>();
-                pf.n[0] = tensors[L.wo].buf.n & ~(size_t) 15;
-                if (l + 1 < c.n_layer) {
-                    pf.p[1] = tensors[layers[l + 1].qkv].buf.as<uint8_t>();
-                    pf.n[1] = tensors[layers[l + 1].qkv].buf.n & ~(size_t) 15;
-                }
-                pf.sink = counters.as<unsigned int>() + 64;
-                launch_attn_decode(qkv.as<float>(), c.head_dim, kvl, kv_h, c.head_dim, kvl + (size_t) c.n_head_kv * kv_h,
-                                   kv_h, c.head_dim, c.head_dim, c.n_head, c.n_head_kv, n_kv, n_kv_dev, scale,
-                                   plan.nsplit, plan.chunk, c.max_ctx, decode_group(c.n_head / c.n_head_kv, c.max_ctx),
-                                   attn_row.as<float>(), part_o.as<float>(), part_ml.as<float2>(), stream,
-                                   prefetch ? &pf : nullptr, nullptr);
-            } else
-            {
-                launch_attn_split(qkv.as<float>(), c.head_dim, qkv_dim, kvl, kv_h, c.head_dim,
-                                  kvl + (size_t) c.n_head_kv * kv_h, kv_h, c.head_dim, nullptr, n_kv, c.head_dim, 1,
-                                  c.n_head, c.n_head_kv, n_kv, scale, part_o.as<float>(), part_ml.as<float2>(), plan,
-                                  n_kv_dev, stream);
-            }
-            a = row_args(L.wo);
-            a.y = xs;
-            a.res = xs;
-            if (decode_attn && plan.nsplit == 1) {  // the attention row itself
-                a.x = attn_row.as<float>();
-                launch_row_gemv(c.wtype, PRO_PLAIN, EPI_STORE, a, stream);
-            } else {  // its split-K partials, merged in the prologue
-                a.part_o = part_o.as<float>();
-                a.part_ml = part_ml.as<float2>();
-                a.nsplit = plan.nsplit;
-                a.D = c.head_dim;
-                launch_row_gemv(c.wtype, PRO_MERGE, EPI_STORE, a, stream);
-            }
-            a = row_args(L.gate_up);
-            a.x = xs;
-            a.norm_w = tensors[L.ffn_norm].buf.as<float>();
-            a.eps = c.rms_eps;
-            a.y = gu.as<float>();
-            launch_row_gemv(c.wtype, PRO_NORM, EPI_SWIGLU, a, stream);
-            a = row_args(L.down);
-            a.x = gu.as<float>();
-            a.y = xs;
-            a.res = xs;
-            launch_row_gemv(c.wtype, PRO_PLAIN, EPI_STORE, a, stream);
-        }
+        for (int l = 0; l < c.n_layer; l++) decode_layer(l, pos_dev, n_kv, n_kv_dev, plan, nullptr);
         RowArgs a = row_args(t_out);
         a.x = xs;
         a.norm_w = tensors[t_out_norm].buf.as<float>();
         a.eps = c.rms_eps;
         a.y = logits.as<float>();
         launch_row_gemv(c.wtype, PRO_NORM, EPI_STORE, a, stream);
+    }
+
+    // Layer l of the single-token forward on the residual row x (the rotation table of the
+    // position already in rope_cs). mid (device, optional): the residual after attention.
+    void decode_layer(int l, const int32_t * pos_dev, int n_kv, const int * n_kv_dev, const AttnPlan & plan,
+                      float * mid) {
+        float * xs = x.as<float>();
+        const float scale = 1.0f / std::sqrt((float) c.head_dim);
+        const int64_t kv_h = (int64_t) c.max_ctx * c.head_dim;
+        const Layer & L = layers[l];
+        uint16_t * kvl = kv_layer(l);
+        RowArgs a = row_args(L.qkv);
+        a.x = xs;
+        a.norm_w = tensors[L.attn_norm].buf.as<float>();
+        a.eps = c.rms_eps;
+        a.y = qkv.as<float>();
+        a.pos = pos_dev;
+        a.kc = kvl;
+        a.vc = kvl + (size_t) c.n_head_kv * kv_h;
+        a.ctx = c.max_ctx;
+        a.H = c.n_head;
+        a.Hkv = c.n_head_kv;
+        a.D = c.head_dim;
+        a.rope_cs = rope_cs.as<float2>();
+        launch_row_gemv(c.wtype, PRO_NORM, EPI_ROPE_KV, a, stream);
+        if (decode_attn) {
+            // Spare CUs read this layer's output projection and the next layer's QKV weights
+            // into the Infinity Cache while the attention runs.
+            Prefetch pf;
+            pf.p[0] = tensors[L.wo].buf.as<uint8_t>();
+            pf.n[0] = tensors[L.wo].buf.n & ~(size_t) 15;
+            if (l + 1 < c.n_layer) {
+                pf.p[1] = tensors[layers[l + 1].qkv].buf.as<uint8_t>();
+                pf.n[1] = tensors[layers[l + 1].qkv].buf.n & ~(size_t) 15;
+            }
+            pf.sink = counters.as<unsigned int>() + 64;
+            launch_attn_decode(qkv.as<float>(), c.head_dim, kvl, kv_h, c.head_dim, kvl + (size_t) c.n_head_kv * kv_h,
+                               kv_h, c.head_dim, c.head_dim, c.n_head, c.n_head_kv, n_kv, n_kv_dev, scale,
+                               plan.nsplit, plan.chunk, c.max_ctx, decode_group(c.n_head / c.n_head_kv, c.max_ctx),
+                               attn_row.as<float>(), part_o.as<float>(), part_ml.as<float2>(), stream,
+                               prefetch ? &pf : nullptr, nullptr);
+        } else {
+            launch_attn_split(qkv.as<float>(), c.head_dim, qkv_dim, kvl, kv_h, c.head_dim,
+                              kvl + (size_t) c.n_head_kv * kv_h, kv_h, c.head_dim, nullptr, n_kv, c.head_dim, 1,
+                              c.n_head, c.n_head_kv, n_kv, scale, part_o.as<float>(), part_ml.as<float2>(), plan,
+                              n_kv_dev, stream);
+        }
+        a = row_args(L.wo);
+        a.y = xs;
+        a.res = xs;
+        if (decode_attn && plan.nsplit == 1) {  // the attention row itself
+            a.x = attn_row.as<float>();
+            launch_row_gemv(c.wtype, PRO_PLAIN, EPI_STORE, a, stream);
+        } else {  // its split-K partials, merged in the prologue
+            a.part_o = part_o.as<float>();
+            a.part_ml = part_ml.as<float2>();
+            a.nsplit = plan.nsplit;
+            a.D = c.head_dim;
+            launch_row_gemv(c.wtype, PRO_MERGE, EPI_STORE, a, stream);
+        }
+        if (mid) check_hip(hipMemcpyAsync(mid, xs, (size_t) c.n_embd * 4, hipMemcpyDeviceToDevice, stream), "mid");
+        a = row_args(L.gate_up);
+        a.x = xs;
+        a.norm_w = tensors[L.ffn_norm].buf.as<float>();
+        a.eps = c.rms_eps;
+        a.y = gu.as<float>();
+        launch_row_gemv(c.wtype, PRO_NORM, EPI_SWIGLU, a, stream);
+        a = row_args(L.down);
+        a.x = gu.as<float>();
+        a.y = xs;
+        a.res = xs;
+        launch_row_gemv(c.wtype, PRO_PLAIN, EPI_STORE, a, stream);
     }
 
     // ggml_rms_norm + ggml_mul by norm t_norm of S rows of the residual stream (the last row only
@@ -459,27 +465,74 @@ struct Llama {
         float * xs = x.as<float>();
         const Tensor & E = tensors[t_embd];
         launch_get_rows(E.type, E.buf.p, E.rows, E.cols, tok_dev, S, xs, stream);
+        for (int l = 0; l < c.n_layer; l++) prompt_layer(l, S, pos_dev, n_kv, n_kv_dev, mask_dev, plan, nullptr);
+        norm_mul_mat(t_out_norm, t_out, xs, S, true, logits.as<float>(), c.n_vocab);
+    }
+
+    // Layer l of a prompt chunk of S rows of the residual stream x. mid (device, optional): the
+    // rows after attention.
+    void prompt_layer(int l, int S, const int32_t * pos_dev, int n_kv, const int * n_kv_dev, const void * mask_dev,
+                      const AttnPlan & plan, float * mid) {
+        float * xs = x.as<float>();
         const float scale = 1.0f / std::sqrt((float) c.head_dim);
         const int64_t kv_h = (int64_t) c.max_ctx * c.head_dim;
-        for (int l = 0; l < c.n_layer; l++) {
-            const Layer & L = layers[l];
-            uint16_t * kvl = kv_layer(l);
-            norm_mul_mat(L.attn_norm, L.qkv, xs, S, false, qkv.as<float>(), qkv_dim);
-            launch_rope_kv(qkv.as<float>(), qkv_dim, pos_dev, S, c.n_head, c.n_head_kv, c.head_dim, c.rope_base, kvl,
-                           c.max_ctx, stream);
-            launch_attn_split(qkv.as<float>(), c.head_dim, qkv_dim, kvl, kv_h, c.head_dim,
-                              kvl + (size_t) c.n_head_kv * kv_h, kv_h, c.head_dim, mask_dev, n_kv, c.head_dim, S,
-                              c.n_head, c.n_head_kv, n_kv, scale, part_o.as<float>(), part_ml.as<float2>(), plan,
-                              n_kv_dev, stream);
-            launch_merge_q8(part_o.as<float>(), part_ml.as<float2>(), plan.nsplit, S, c.n_head, c.head_dim, nullptr,
-                            act_b.p, stream);
-            mul_mat(L.wo, act_b.p, S, xs, c.n_embd, xs);
-            norm_mul_mat(L.ffn_norm, L.gate_up, xs, S, false, gu.as<float>(), 2 * (int64_t) c.n_ff);
-            launch_swiglu_q8(gu.as<float>(), gu.as<float>() + c.n_ff, 2 * (int64_t) c.n_ff, c.n_ff, S, act_b.p,
-                             stream);
-            mul_mat(L.down, act_b.p, S, xs, c.n_embd, xs);
+        const Layer & L = layers[l];
+        uint16_t * kvl = kv_layer(l);
+        norm_mul_mat(L.attn_norm, L.qkv, xs, S, false, qkv.as<float>(), qkv_dim);
+        launch_rope_kv(qkv.as<float>(), qkv_dim, pos_dev, S, c.n_head, c.n_head_kv, c.head_dim, c.rope_base, kvl,
+                       c.max_ctx, stream);
+        launch_attn_split(qkv.as<float>(), c.head_dim, qkv_dim, kvl, kv_h, c.head_dim, kvl + (size_t) c.n_head_kv * kv_h,
+                          kv_h, c.head_dim, mask_dev, n_kv, c.head_dim, S, c.n_head, c.n_head_kv, n_kv, scale,
+                          part_o.as<float>(), part_ml.as<float2>(), plan, n_kv_dev, stream);
+        launch_merge_q8(part_o.as<float>(), part_ml.as<float2>(), plan.nsplit, S, c.n_head, c.head_dim, nullptr,
+                        act_b.p, stream);
+        mul_mat(L.wo, act_b.p, S, xs, c.n_embd, xs);
+        if (mid) check_hip(hipMemcpyAsync(mid, xs, (size_t) S * c.n_embd * 4, hipMemcpyDeviceToDevice, stream), "mid");
+        norm_mul_mat(L.ffn_norm, L.gate_up, xs, S, false, gu.as<float>(), 2 * (int64_t) c.n_ff);
+        launch_swiglu_q8(gu.as<float>(), gu.as<float>() + c.n_ff, 2 * (int64_t) c.n_ff, c.n_ff, S, act_b.p, stream);
+        mul_mat(L.down, act_b.p, S, xs, c.n_embd, xs);
+    }
+
+    // Layers [first, first + count) on n given residual rows (host, n x n_embd) at positions
+    // pos0 .. pos0 + n - 1, with the kernels a prompt chunk (n > 1) or the decode step (n == 1)
+    // runs, their K / V written into the cache at those positions. x_out (host, n x n_embd): the
+    // last layer's output; mid (host, count x n x n_embd, optional): each layer's rows after
+    // attention. The model's position is left as it is.
+    void forward_layers(const float * x_in, int n, int pos0, int first, int count, float * x_out, float * mid) {
+        require(n >= 1 && n <= max_prompt, "forward_layers: 1 <= n <= max_prompt");
+        require(pos0 >= 0 && pos0 + n <= c.max_ctx, "forward_layers: positions past max_ctx");
+        require(first >= 0 && count >= 1 && first + count <= c.n_layer, "forward_layers: layer range out of range");
+        const size_t row_bytes = (size_t) n * c.n_embd * 4;
+        DevBuf mid_dev(mid ? row_bytes * count : 0);
+        float * xs = x.as<float>();
+        if (n == 1 && fused) {
+            // the decode step's state: position, KV length and a token whose embedding row and the
+            // position's rotation table the step's first launch makes (the row is replaced below)
+            const StepStateHost st{pos0, pos0 + 1, 0, 0};
+            check_hip(hipMemcpyAsync(state.p, &st, sizeof st, hipMemcpyHostToDevice, stream), "state");
+            StepStateHost * sd = state.as<StepStateHost>();
+            const Tensor & E = tensors[t_embd];
+            launch_embed_rope(E.type, E.buf.p, E.rows, E.cols, &sd->token, xs, &sd->pos, c.head_dim, c.rope_base,
+                              rope_cs.p, stream);
+            check_hip(hipMemcpyAsync(xs, x_in, row_bytes, hipMemcpyHostToDevice, stream), "x");
+            for (int l = first; l < first + count; l++)
+                decode_layer(l, &sd->pos, c.max_ctx, &sd->n_kv, plan_decode,
+                             mid ? mid_dev.as<float>() + (size_t) (l - first) * n * c.n_embd : nullptr);
+        } else {
+            std::vector<int32_t> p(n);
+            for (int j = 0; j < n; j++) p[j] = pos0 + j;
+            check_hip(hipMemcpyAsync(positions.p, p.data(), n * 4, hipMemcpyHostToDevice, stream), "positions");
+            check_hip(hipMemcpyAsync(xs, x_in, row_bytes, hipMemcpyHostToDevice, stream), "x");
+            const int n_kv = pos0 + n;
+            launch_causal_mask(mask.p, n, n_kv, pos0, stream);
+            const AttnPlan plan = attn_plan(n, c.n_head_kv, n_kv);
+            for (int l = first; l < first + count; l++)
+                prompt_layer(l, n, positions.as<int32_t>(), n_kv, nullptr, mask.p, plan,
+                             mid ? mid_dev.as<float>() + (size_t) (l - first) * n * c.n_embd : nullptr);
         }
-        norm_mul_mat(t_out_norm, t_out, xs, S, true, logits.as<float>(), c.n_vocab);
+        check_hip(hipStreamSynchronize(stream), "forward_layers");
+        check_hip(hipMemcpy(x_out, xs, row_bytes, hipMemcpyDeviceToHost), "x_out");
+        if (mid) check_hip(hipMemcpy(mid, mid_dev.p, row_bytes * count, hipMemcpyDeviceToHost), "mid");
     }
 
     void prefill(const int32_t * tokens, int n, float * logits_host) {
@@ -630,6 +683,14 @@ int gcq_llama_decode(gcq_llama * m, int32_t token, float * logits, int32_t * nex
     return guarded([&] {
         require(m != nullptr, "model is NULL");
         m->decode(token, logits, next);
+    });
+}
+
+int gcq_llama_forward_layers(gcq_llama * m, const float * x, int n, int pos, int first_layer, int n_layers, float * x_out,
+                             float * x_mid) {
+    return guarded([&] {
+        require(m != nullptr && x != nullptr && x_out != nullptr, "model, x or x_out is NULL");
+        m->forward_layers(x, n, pos, first_layer, n_layers, x_out, x_mid);
     });
 }
 

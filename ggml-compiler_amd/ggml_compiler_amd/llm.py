@@ -145,6 +145,18 @@ class Model:
         check(self._lib.gcq_llama_generate(self._m, int(first), int(n_new), out.ctypes.data))
         return out[:n_new].tolist()
 
+    def forward_layers(self, x: np.ndarray, pos: int, first: int, count: int = 1) -> tuple[np.ndarray, np.ndarray]:
+        """Layers [first, first + count) on given residual rows x [n, n_embd] at positions pos .. pos +
+        n - 1 (the prompt kernels for n > 1, the decode step's for n == 1), their K / V cached:
+        (output rows [n, n_embd], rows after each layer's attention [count, n, n_embd])."""
+        x = np.ascontiguousarray(x, np.float32)
+        n = x.shape[0]
+        out = np.empty_like(x)
+        mid = np.empty((count, n, self.cfg.n_embd), np.float32)
+        check(self._lib.gcq_llama_forward_layers(self._m, x.ctypes.data, n, int(pos), int(first), int(count),
+                                                 out.ctypes.data, mid.ctypes.data))
+        return out, mid
+
 
 class Generator:
     """Greedy decoding on the host or on the device (ggml_compiler/llm.py:473-634, text only)."""

@@ -215,6 +215,15 @@ GCQ_API int gcq_llama_decode(gcq_llama * m, int32_t token, float * logits, int32
 /* Feed `first`, then each greedy token back, n_new steps on the device; out_tokens (host) gets the
  * n_new tokens produced (no end-of-sequence stop). */
 GCQ_API int gcq_llama_generate(gcq_llama * m, int32_t first, int n_new, int32_t * out_tokens);
+/* Layers [first_layer, first_layer + n_layers) on n given residual-stream rows x (host, n x n_embd
+ * f32) at positions pos .. pos + n - 1: the kernels a prompt chunk (n > 1, n <= max_prompt) or the
+ * decode step (n == 1) runs, K / V of those layers written into the cache at those positions.
+ * x_out (host, n x n_embd) gets the last layer's output; x_mid (host, n_layers x n x n_embd, or
+ * NULL) each layer's rows after attention (x + attention, before the FFN). The position that
+ * prefill / decode continue from is not changed. For layer-by-layer comparisons of the decoder
+ * (the per-layer graph of ggml_compiler/llm.py:361-444) against a reference fed the same rows. */
+GCQ_API int gcq_llama_forward_layers(gcq_llama * m, const float * x, int n, int pos, int first_layer, int n_layers,
+                                     float * x_out, float * x_mid);
 
 #ifdef __cplusplus
 }

@@ -38,31 +38,48 @@ class OracleLlama:
     def _norm(self, name: str, x: np.ndarray) -> np.ndarray:
         return orc.rms_norm(x, self.cfg.rms_eps, threads=self.threads) * self.w[name][None, :]
 
+    def layer(self, l: int, x: np.ndarray, pos: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+        """Layer l on residual rows x [S, n_embd] at positions pos (every key up to a row's position
+        visible), K / V written into this model's cache: (rows after attention, output rows)."""
+        mid = self.attention(l, x, pos)
+        return mid, self.ffn(l, mid)
+
+    def ffn(self, l: int, mid: np.ndarray) -> np.ndarray:
+        """Layer l's feed-forward half on the rows after attention: mid + down(swiglu(gate, up))."""
+        c = self.cfg
+        b = f"blk.{l}."
+        gu = self._mm(b + "ffn_gate_up", self._norm(b + "ffn_norm", mid))
+        return mid + self._mm(b + "ffn_down", orc.swiglu(gu[:, :c.n_ff], gu[:, c.n_ff:]))
+
+    def attention(self, l: int, x: np.ndarray, pos: np.ndarray) -> np.ndarray:
+        """Layer l's attention half: x + attn_output(flash_attn(rope(q), cache k, cache v))."""
+        c = self.cfg
+        S = x.shape[0]
+        H, Hkv, D = c.n_head, c.n_head_kv, c.head_dim
+        n_kv = int(pos[-1]) + 1
+        mask = np.where(np.arange(n_kv)[None, :] <= pos[:, None], 0.0, -np.inf).astype(np.float32)
+        b = f"blk.{l}."
+        qkv = self._mm(b + "attn_qkv", self._norm(b + "attn_norm", x))
+        q = orc.rope_neox(qkv[:, :H * D].reshape(S, H, D), pos, D, c.rope_base)
+        k = orc.rope_neox(qkv[:, H * D:(H + Hkv) * D].reshape(S, Hkv, D), pos, D, c.rope_base)
+        v = qkv[:, (H + Hkv) * D:].reshape(S, Hkv, D)
+        self.k[l][:, pos] = orc.fp32_to_fp16(k.transpose(1, 0, 2))
+        self.v[l][:, pos] = orc.fp32_to_fp16(v.transpose(1, 0, 2))
+        att = orc.flash_attn_ext(q.transpose(1, 0, 2), self.k[l][:, :n_kv], self.v[l][:, :n_kv],
+                                 orc.fp32_to_fp16(mask), 1.0 / np.sqrt(D), threads=self.threads)
+        return x + self._mm(b + "attn_output", att.reshape(S, H * D))
+
+    def embed(self, tokens) -> np.ndarray:
+        return orc.dequantize(self.w["token_embd"][np.asarray(tokens)], self.t, self.cfg.n_embd)
+
     def forward(self, tokens) -> np.ndarray:
         """Append tokens at the next positions; logits of the last one."""
         c = self.cfg
         S = len(tokens)
-        H, Hkv, D = c.n_head, c.n_head_kv, c.head_dim
         pos = np.arange(self.pos, self.pos + S, dtype=np.int32)
-        n_kv = self.pos + S
-        emb = self.w["token_embd"]
-        x = orc.dequantize(emb[np.asarray(tokens)], self.t, c.n_embd)
-        mask = np.where(np.arange(n_kv)[None, :] <= pos[:, None], 0.0, -np.inf).astype(np.float32)
-        m16 = orc.fp32_to_fp16(mask)
+        x = self.embed(tokens)
         for l in range(c.n_layer):
-            b = f"blk.{l}."
-            qkv = self._mm(b + "attn_qkv", self._norm(b + "attn_norm", x))
-            q = orc.rope_neox(qkv[:, :H * D].reshape(S, H, D), pos, D, c.rope_base)
-            k = orc.rope_neox(qkv[:, H * D:(H + Hkv) * D].reshape(S, Hkv, D), pos, D, c.rope_base)
-            v = qkv[:, (H + Hkv) * D:].reshape(S, Hkv, D)
-            self.k[l][:, pos] = orc.fp32_to_fp16(k.transpose(1, 0, 2))
-            self.v[l][:, pos] = orc.fp32_to_fp16(v.transpose(1, 0, 2))
-            att = orc.flash_attn_ext(q.transpose(1, 0, 2), self.k[l][:, :n_kv], self.v[l][:, :n_kv], m16,
-                                     1.0 / np.sqrt(D), threads=self.threads)
-            x = x + self._mm(b + "attn_output", att.reshape(S, H * D))
-            gu = self._mm(b + "ffn_gate_up", self._norm(b + "ffn_norm", x))
-            a = orc.swiglu(gu[:, :c.n_ff], gu[:, c.n_ff:])
-            x = x + self._mm(b + "ffn_down", a)
+            x = self.layer(l, x, pos)[1]
         self.pos += S
         h = self._norm("output_norm", x[-1:])
         return self._mm("output", h)[0]

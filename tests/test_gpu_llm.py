@@ -206,3 +206,135 @@ def test_model_from_reference_layout_gguf(gops, orc, tmp_path, wtype):
         assert orc.parity(lg, lo) < TOL_LM, step
         tok = int(np.argmax(lo))
     m.close()
+
+
+# ------------------------------------------------------------- C5: the benchmark configuration
+
+GOLDEN = __import__("pathlib").Path(__file__).resolve().parent / "golden"
+C5_LAYERS = (0, 1, 15, 30, 31)
+TOL_OP = 1e-3
+# Each half of a layer is fed the same rows on both sides: the attention half the rows entering
+# the layer, the FFN half the HIP model's rows after attention. (Fed the oracle's own rows after
+# attention instead, the FFN would see inputs that differ in the last bits, and its rms_norm ->
+# Q8_0 codes would flip at rounding boundaries: ~6e-3 relative at the FFN output for a 2.6e-4
+# difference at its input, the amplification of ggml's own arithmetic, not of a kernel.) The whole
+# layer's output is compared too, and printed, with that amplification allowed for.
+LAYER_MAX = 5e-2
+
+
+def _c5_config():
+    from ggml_compiler_amd.llm import LlamaConfig
+
+    return LlamaConfig(n_layer=32, n_embd=4096, n_head=32, n_head_kv=8, head_dim=128, n_ff=14336, n_vocab=128256,
+                       max_ctx=640, wtype=2, rms_eps=1e-5, rope_base=500000.0)
+
+
+@pytest.mark.timeout(1200)
+def test_c5_layers_teacher_forced(gops, orc):
+    """C5 layer by layer, at 1e-3: the 8B-shaped Q4_0 decoder's layers 0, 1, 15, 30 and 31 for the
+    512-token prompt (prompt kernels) and then decode positions 512..520 (the decode step's fused
+    kernels), each fed the same rows as the oracle's restatement of that layer (the rows entering
+    it on the HIP model's stream; the FFN half fed the HIP rows after attention). Attention output,
+    post-attention residual and FFN output within 1e-3 of the oracle by the parity metric (the op
+    bar); the whole layer within LAYER_MAX; KV rows cached by both sides carry over to the decode
+    positions."""
+    from ggml_compiler_amd.llm import Model
+    from llama_ref import OracleLlama
+
+    cfg = _c5_config()
+    m = Model(cfg, max_prompt=512)
+    m.init_random(seed=0)
+    names = {"token_embd"} | {f"blk.{l}.{t}" for l in C5_LAYERS for t in
+                              ("attn_norm", "attn_qkv", "attn_output", "ffn_norm", "ffn_gate_up", "ffn_down")}
+    o = OracleLlama(cfg, {n: m.get_weight(n) for n in names})
+    worst = {}
+
+    def rel_rms(a, b):
+        a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+        return float(np.sqrt(np.mean((a - b) ** 2) / np.mean(b ** 2)))
+
+    def check(where, l, x, mid, out, omid, oout):
+        offn = o.ffn(l, mid) - mid  # the oracle's FFN half on the HIP rows after attention
+        errs = {"attn": orc.parity(mid - x, omid - x), "mid": orc.parity(mid, omid),
+                "ffn": orc.parity(out - mid, offn), "ffn_rms": rel_rms(out - mid, offn),
+                "layer": orc.parity(out, oout)}
+        print(where, {k: f"{v:.2e}" for k, v in errs.items()}, flush=True)
+        for k, v in errs.items():
+            worst[k] = max(worst.get(k, 0.0), v)
+        assert max(errs["attn"], errs["mid"], errs["ffn"], errs["ffn_rms"]) < TOL_OP, (where, errs)
+        assert errs["layer"] < LAYER_MAX, (where, errs)
+
+    prompt = orc.ids(512, seed=5, vocab=cfg.n_vocab)
+    x = o.embed(prompt)
+    pos = np.arange(512, dtype=np.int32)
+    for l in range(cfg.n_layer):
+        out, mid = m.forward_layers(x, 0, l)
+        if l in C5_LAYERS:
+            omid, oout = o.layer(l, x, pos)
+            check(f"prompt layer {l}", l, x, mid[0], out, omid, oout)
+        x = out
+    for p, tok in zip(range(512, 521), orc.ids(9, seed=6, vocab=cfg.n_vocab)):
+        x = o.embed([tok])
+        for l in range(cfg.n_layer):
+            out, mid = m.forward_layers(x, p, l)
+            if l in C5_LAYERS:
+                omid, oout = o.layer(l, x, np.array([p], np.int32))
+                check(f"decode pos {p} layer {l}", l, x, mid[0], out, omid, oout)
+            x = out
+    print("C5 per-layer worst parity:", {k: f"{v:.2e}" for k, v in worst.items()})
+    m.close()
+
+
+@pytest.mark.timeout(900)
+def test_c5_full_run_matches_oracle(gops, orc):
+    """C5 at its stated configuration: the 32-layer 8B-shaped Q4_0 decoder, a 512-token prompt, then
+    128 greedy tokens (the reference's LM checks, tests/unit/test_llm.py:81-106), against the
+    oracle's run of the same model (tests/golden/c5_oracle.npz, written by make_c5_oracle.py).
+    Teacher-forced with the oracle's tokens, every step's greedy token equals the oracle's unless
+    its top two logits are closer than the logits' difference (_same_greedy); the 64 largest
+    logits of every step are within 2e-2 of the oracle's by the parity metric and the first and
+    last rows' next-token KL below 1e-3. The device's own generate loop makes the oracle's tokens
+    up to the first near-tie."""
+    import sys
+
+    from ggml_compiler_amd.llm import Model
+
+    sys.path.insert(0, str(GOLDEN))
+    from make_c5_oracle import N_GEN, PROMPT_SEED, Cfg, weight_list
+
+    fx = np.load(GOLDEN / "c5_oracle.npz")
+    cfg = _c5_config()
+    m = Model(cfg, max_prompt=512)
+    m.init_random(seed=0)
+    assert [tuple(w) for w in m.weights()] == [tuple(w) for w in weight_list(Cfg)]
+    prompt = fx["prompt"]
+    assert np.array_equal(prompt, orc.ids(512, seed=PROMPT_SEED, vocab=cfg.n_vocab))
+    rows = [m.prefill(prompt.tolist())]
+    for i in range(N_GEN):
+        rows.append(m.decode(int(fx["tokens"][i]))[0])
+    tops, greedy_ok = [], 0
+    for i, lg in enumerate(rows):
+        assert np.isfinite(lg).all(), i
+        ids = fx["top_ids"][i]
+        tops.append(orc.parity(lg[ids], fx["top_logits"][i]))
+        if i < N_GEN:
+            got = int(np.argmax(lg))
+            same = got == int(fx["tokens"][i])
+            greedy_ok += same
+            assert same or fx["margin"][i] <= 2 * np.abs(lg[ids] - fx["top_logits"][i]).max(), (i, got)
+    kl = [orc.logit_kl(rows[0], fx["first"]), orc.logit_kl(rows[-1], fx["last"])]
+    full = [orc.parity(rows[0], fx["first"]), orc.parity(rows[-1], fx["last"])]
+    print(f"C5 teacher-forced: greedy {greedy_ok}/{N_GEN}, top-64 parity max {max(tops):.2e} "
+          f"mean {np.mean(tops):.2e}, first/last row parity {full[0]:.2e}/{full[1]:.2e}, KL {kl[0]:.2e}/{kl[1]:.2e}")
+    assert max(tops) < 2e-2
+    assert max(kl) < 1e-3
+    # free-running: the device's generate loop from the prompt
+    m.reset()
+    m.prefill(prompt.tolist(), logits=False)
+    gen = m.generate(int(fx["tokens"][0]), N_GEN - 1)
+    want = fx["tokens"][1:].tolist()
+    first_diff = next((i for i, (a, b) in enumerate(zip(gen, want)) if a != b), None)
+    print(f"C5 free-running: {len(gen) if first_diff is None else first_diff}/{N_GEN - 1} tokens equal the oracle's")
+    if first_diff is not None:  # allowed only at a near-tie of the oracle's logits
+        assert fx["margin"][first_diff + 1] < 0.05, (first_diff, fx["margin"][first_diff + 1])
+    m.close()
