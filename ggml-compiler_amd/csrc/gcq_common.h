@@ -146,6 +146,52 @@ void launch_row_gemv(int type, int pro, int epi, const RowArgs & a, hipStream_t 
 // ranges; false when they span 2 GB or more.
 bool row_gemv_ranges(int type, int n, const uint8_t * const * w, const int64_t * N, int64_t K, RowArgs & a);
 
+// One decode step's layers in a single persistent launch (decode_step.hip): per layer its packed
+// weights (QKV and gate/up in the row-pair order of the rope and swiglu epilogues) and K / V cache.
+struct StepLayer {
+    const uint8_t *qkv_qs, *o_qs, *gu_qs, *dn_qs;
+    const uint16_t *qkv_d, *o_d, *gu_d, *dn_d;
+    const float *attn_norm, *ffn_norm;
+    uint16_t *kc, *vc;  // [Hkv][ctx][D] f16
+};
+
+struct StepArgs {
+    const StepLayer * layers;
+    int n_layer, n_embd, n_ff, H, Hkv;
+    int64_t ctx;
+    float eps, scale;
+    const int * pos;   // the token's position (its K / V row; rope_cs holds its rotation)
+    const int * n_kv;  // keys visible
+    const float2 * rope_cs;
+    float * x;         // residual row [n_embd]: the embedding in, the last layer's output out
+    // Rings, one slot per layer (x: per layer and write, 2 n_layer - 1 slots), slots
+    // step_ring_stride(floats of a slot) apart: every value the step passes between its phases is
+    // written to an address of its own.
+    float * x_ring;    // [2 n_layer - 1][n_embd]
+    float * q;         // roped q [n_layer][H D]
+    float * part_o;    // [n_layer][H][nsplit][D]
+    float2 * part_ml;  // [n_layer][H][nsplit]
+    float * h;         // silu(gate) * up [n_layer][n_ff]
+    int nsplit, chunk;
+    unsigned * bar;    // decode_step_bar_bytes() of barrier words, zero between launches
+    unsigned * err;    // raised when a barrier wait gave up
+    // Phase timing, when *trace_on: per workgroup w, trace[w * step_trace_events(n_layer) + e] =
+    // the 100 MHz real-time clock at the kernel's start (e = 0), then per layer l and phase p
+    // (QKV, attention, O, gate/up, down): when its first wavefront is done with the phase
+    // (e = 1 + 15 l + 3 p), when the whole workgroup has arrived at the phase's barrier, its
+    // stores complete (e + 1), and when it passes the barrier (e + 2); then at its end.
+    unsigned long long * trace;
+    const unsigned * trace_on;
+};
+__host__ __device__ inline int step_trace_events(int n_layer) { return 2 + 15 * n_layer; }
+
+// Floats from one ring slot to the next: n rounded up to 64 (256 bytes), so that no cache line
+// holds parts of two slots.
+__host__ __device__ inline size_t step_ring_stride(size_t n) { return (n + 63) & ~(size_t) 63; }
+size_t decode_step_bar_bytes();
+bool decode_step_fits(int type, int n_embd, int n_ff, int H, int Hkv, int D, int nsplit);
+void launch_decode_step(int type, int D, const StepArgs & a, hipStream_t s);
+
 // Shapes and byte strides of a strided copy / conversion (elementwise.hip).
 struct Cpy4 {
     int64_t sne[4], snb[4], dne[4], dnb[4];

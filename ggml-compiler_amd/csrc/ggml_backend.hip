@@ -117,12 +117,22 @@ bool whole_packed(const ggml_tensor * a) {
            ggml_is_contiguous(a) && ggml_is_contiguous(b);
 }
 
-static_assert(UN_ABS == GGML_UNARY_OP_ABS && UN_NEG == GGML_UNARY_OP_NEG && UN_TANH == GGML_UNARY_OP_TANH &&
-                  UN_RELU == GGML_UNARY_OP_RELU && UN_SIGMOID == GGML_UNARY_OP_SIGMOID && UN_GELU == GGML_UNARY_OP_GELU &&
-                  UN_SILU == GGML_UNARY_OP_SILU && UN_EXP == GGML_UNARY_OP_EXP &&
-                  UN_GELU_ERF == GGML_UNARY_OP_GELU_ERF && UN_SOFTPLUS == GGML_UNARY_OP_SOFTPLUS &&
-                  UN_SQR == GGML_UNARY_OP_SQR && UN_SQRT == GGML_UNARY_OP_SQRT && UN_LOG == GGML_UNARY_OP_LOG &&
-                  UN_SIN == GGML_UNARY_OP_SIN && UN_COS == GGML_UNARY_OP_COS && UN_CLAMP == GGML_UNARY_OP_CLAMP,
+static_assert((int) UN_ABS == (int) GGML_UNARY_OP_ABS &&
+                  (int) UN_NEG == (int) GGML_UNARY_OP_NEG &&
+                  (int) UN_TANH == (int) GGML_UNARY_OP_TANH &&
+                  (int) UN_RELU == (int) GGML_UNARY_OP_RELU &&
+                  (int) UN_SIGMOID == (int) GGML_UNARY_OP_SIGMOID &&
+                  (int) UN_GELU == (int) GGML_UNARY_OP_GELU &&
+                  (int) UN_SILU == (int) GGML_UNARY_OP_SILU &&
+                  (int) UN_EXP == (int) GGML_UNARY_OP_EXP &&
+                  (int) UN_GELU_ERF == (int) GGML_UNARY_OP_GELU_ERF &&
+                  (int) UN_SOFTPLUS == (int) GGML_UNARY_OP_SOFTPLUS &&
+                  (int) UN_SQR == (int) GGML_UNARY_OP_SQR &&
+                  (int) UN_SQRT == (int) GGML_UNARY_OP_SQRT &&
+                  (int) UN_LOG == (int) GGML_UNARY_OP_LOG &&
+                  (int) UN_SIN == (int) GGML_UNARY_OP_SIN &&
+                  (int) UN_COS == (int) GGML_UNARY_OP_COS &&
+                  (int) UN_CLAMP == (int) GGML_UNARY_OP_CLAMP,
               "k_unary's numbering is ggml_unary_op's");
 
 bool f32_contig(const ggml_tensor * t) { return t->type == GGML_TYPE_F32 && ggml_is_contiguous(t); }

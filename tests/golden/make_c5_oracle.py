@@ -13,7 +13,15 @@ token): the greedy token, the margin between the two largest logits, the log-sum
 largest logits with their ids; the whole first and last rows as float32. The oracle is the repo's
 C restatement of ggml-cpu (oracle/), run on this machine's cores.
 
-Run: python tests/golden/make_c5_oracle.py   (about 10 minutes on 8 cores)
+The noise floor: the same oracle run again, teacher-forced with the first run's tokens, with every
+element of every embedding row moved one float32 ulp up or down (a seeded coin per element), the
+smallest change any difference in rounding can make. How far that run's logits land from the first
+run's (floor_top: its logits at the stored top-64 ids; floor_kl: the first and last rows'
+next-token KL) is how much 32 layers of this random-weight model amplify rounding-level noise, so
+an implementation that rounds differently anywhere cannot be expected to land closer.
+
+Run: python tests/golden/make_c5_oracle.py [--floor-only]   (about 7 minutes per run on 8 cores;
+--floor-only adds the noise floor to an existing c5_oracle.npz)
 """
 
 from __future__ import annotations
@@ -34,6 +42,8 @@ PROMPT_SEED = 5
 N_PROMPT = 512
 N_GEN = 128
 TOP = 64
+FLOOR_SEED = 11
+OUT = Path(__file__).with_name("c5_oracle.npz")
 
 
 class Cfg:
@@ -64,26 +74,46 @@ def summarize(logits: np.ndarray):
     return int(top[0]), float(two[1] - two[0]), float(lse), top.astype(np.int32), logits[top].astype(np.float32)
 
 
+class UlpPerturbed(OracleLlama):
+    """The oracle with every embedding element moved one ulp, up or down by a seeded coin."""
+
+    def embed(self, tokens) -> np.ndarray:
+        x = super().embed(tokens)
+        up = np.random.default_rng(FLOOR_SEED + self.pos).random(x.shape) < 0.5
+        return np.where(up, np.nextafter(x, np.float32(np.inf)), np.nextafter(x, np.float32(-np.inf)))
+
+
+def run(o: OracleLlama, prompt: np.ndarray, tokens, t0: float) -> list[np.ndarray]:
+    """Logit rows of the prompt, then of each fed token; tokens=None feeds the greedy ones."""
+    rows = [o.forward(prompt.tolist())]
+    print(f"prompt {time.time() - t0:.0f} s", flush=True)
+    for i in range(N_GEN):
+        tok = int(np.argmax(rows[-1])) if tokens is None else int(tokens[i])
+        rows.append(o.forward([tok]))
+        if i % 16 == 15:
+            print(f"step {i + 1} {time.time() - t0:.0f} s", flush=True)
+    return rows
+
+
 def main() -> None:
     t0 = time.time()
     c = Cfg()
     w = random_weights(weight_list(c), seed=0)
     print(f"weights {time.time() - t0:.0f} s", flush=True)
-    o = OracleLlama(c, w)
     prompt = orc.ids(N_PROMPT, seed=PROMPT_SEED, vocab=c.n_vocab)
-    rows = [o.forward(prompt.tolist())]
-    print(f"prompt {time.time() - t0:.0f} s", flush=True)
-    for i in range(N_GEN):
-        tok = int(np.argmax(rows[-1]))
-        rows.append(o.forward([tok]))
-        if i % 16 == 15:
-            print(f"step {i + 1} {time.time() - t0:.0f} s", flush=True)
-    s = [summarize(r) for r in rows]
-    np.savez_compressed(Path(__file__).with_name("c5_oracle.npz"), prompt=prompt,
-                        tokens=np.array([x[0] for x in s[:N_GEN]], np.int32),
-                        margin=np.array([x[1] for x in s], np.float32), lse=np.array([x[2] for x in s]),
-                        top_ids=np.stack([x[3] for x in s]), top_logits=np.stack([x[4] for x in s]),
-                        first=rows[0].astype(np.float32), last=rows[-1].astype(np.float32))
+    if "--floor-only" in sys.argv:
+        fx = dict(np.load(OUT))
+    else:
+        rows = run(OracleLlama(c, w), prompt, None, t0)
+        s = [summarize(r) for r in rows]
+        fx = dict(prompt=prompt, tokens=np.array([x[0] for x in s[:N_GEN]], np.int32),
+                  margin=np.array([x[1] for x in s], np.float32), lse=np.array([x[2] for x in s]),
+                  top_ids=np.stack([x[3] for x in s]), top_logits=np.stack([x[4] for x in s]),
+                  first=rows[0].astype(np.float32), last=rows[-1].astype(np.float32))
+    rows = run(UlpPerturbed(c, w), prompt, fx["tokens"], t0)
+    fx["floor_top"] = np.stack([r[ids] for r, ids in zip(rows, fx["top_ids"])]).astype(np.float32)
+    fx["floor_kl"] = np.array([orc.logit_kl(rows[0], fx["first"]), orc.logit_kl(rows[-1], fx["last"])])
+    np.savez_compressed(OUT, **fx)
     print(f"done {time.time() - t0:.0f} s", flush=True)
 
 
