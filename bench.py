@@ -207,6 +207,13 @@ def bench_decode(args, torch) -> tuple[dict, object]:
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     assert len(toks) == args.steps
+    # tg128: 128 tokens from an empty context (the reference's decode protocol, llm.py:671-682)
+    m.reset()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    m.generate(first, 128)
+    torch.cuda.synchronize()
+    tg128 = 128 / (time.perf_counter() - t1)
     gb = sum(decode_bytes(cfg, PROMPT + i) for i in range(args.steps)) / args.steps
     res = {"value": round(args.steps / dt, 2), "unit": "tok/s", "ms_per_step": dt / args.steps * 1e3,
            "dtype": "q4_0 weights x q8_0 activations (int32 dots, fp32 acc), f16 KV",
@@ -215,7 +222,8 @@ def bench_decode(args, torch) -> tuple[dict, object]:
                                   f"{PROMPT}-token uniform-random prompt, then greedy decode (one step = one token, "
                                   "on-device generate loop of graph launches)",
                       "global_batch": 1, "seq_len": PROMPT, "parallelism": "none"},
-           "extra": {"pp512_tok_s": round(PROMPT / t_pp, 1), "decode_bytes_per_token": int(gb),
+           "extra": {"pp512_tok_s": round(PROMPT / t_pp, 1), "tg128_empty_context_tok_s": round(tg128, 2),
+                     "decode_bytes_per_token": int(gb),
                      "decode_GB_s": round(gb * args.steps / dt / 1e9, 1),
                      "decode_frac_hbm_peak": round(gb * args.steps / dt / 1e9 / HBM_PEAK_GBS, 4),
                      "decode_bytes_note": BYTES_PER_TOKEN_NOTE}}
@@ -261,7 +269,7 @@ def bench_ggml_decode(args) -> dict:
                                    f"per graph, then {args.steps} greedy tokens; n_kv 768"}}
 
 
-def bench_program_decode(args) -> dict:
+def bench_program_decode(args, w: dict | None = None) -> dict:
     """The same 8B-shaped model as a ggml-compiler program GGUF (ggml_compiler_amd.program: the
     decode stage node for node, symbolic n_kv bound per step like llm.py:527-529), loaded by
     libgcq's loader and run as the reference's runtime runs it: the prompt through the `decode`
@@ -277,15 +285,15 @@ def bench_program_decode(args) -> dict:
     from ggml_compiler_amd.program import write_llama_program
 
     cfg = LlamaConfig.llama3_8b(max_ctx=1024)
-    m = Model(cfg, max_prompt=16)
-    m.init_random(seed=0, std=0.02)
-    w = {name: m.get_weight(name) for name, *_ in m.weights()}
-    m.close()
+    if w is None:  # the decode benchmark's weights (random init, seed 0)
+        m = Model(cfg, max_prompt=16)
+        m.init_random(seed=0, std=0.02)
+        w = {name: m.get_weight(name) for name, *_ in m.weights()}
+        m.close()
     with tempfile.TemporaryDirectory() as d:
         path = os.path.join(d, "llama3_8b_q4_0.gguf")
         t0 = time.perf_counter()
         write_llama_program(path, cfg, w, kv_step=256, n_gen=args.steps)
-        del w
         t_write = time.perf_counter() - t0
         t0 = time.perf_counter()
         s = runtime.Session(path)
@@ -319,24 +327,105 @@ def bench_program_decode(args) -> dict:
                                    f"(n_kv 768)"}}
 
 
-def cpu_decode_baseline(m, seconds: float = 15.0) -> dict:
-    """The CPU oracle (repo restatement of ggml-cpu, OpenMP) decoding the same 8B-shaped model on the
-    host cores: a 4-token prompt, then greedy tokens until `seconds` have passed."""
+def cpu_info() -> dict:
+    """The host CPU: model name, logical CPUs, and the CPUs this process may run on."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), model)
+    except OSError:
+        pass
+    return {"cpu_model": model, "nproc": os.cpu_count(), "cpus_available": len(os.sched_getaffinity(0))}
+
+
+def cpu_decode_sample(m, w, threads: int, seconds: float) -> dict:
+    """The CPU oracle (repo restatement of ggml-cpu, OpenMP) decoding the same 8B-shaped model at
+    positions PROMPT, PROMPT + 1, ...: the prompt's K / V rows are filled with N(0, 1) f16 values
+    instead of being computed (5 minutes of CPU prefill), so each step does the work of a decode step
+    after a PROMPT-token prompt; greedy tokens until `seconds` have passed."""
     sys.path.insert(0, str(ROOT / "oracle"))
     import numpy as np
+
+    import oracle as orc
     from llama_ref import OracleLlama
 
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    w = {name: m.get_weight(name) for name, *_ in m.weights()}
     o = OracleLlama(m.cfg, w, threads=threads)
-    tok = int(np.argmax(o.forward([1, 2, 3, 4])))
-    n, t0 = 0, time.perf_counter()
+    c = m.cfg
+    o.k[:, :, :PROMPT] = orc.fp32_to_fp16(orc.normal((c.n_layer, c.n_head_kv, PROMPT, c.head_dim), seed=9))
+    o.v[:, :, :PROMPT] = orc.fp32_to_fp16(orc.normal((c.n_layer, c.n_head_kv, PROMPT, c.head_dim), seed=10))
+    o.pos = PROMPT
+    tok, n, t0 = 1, 0, time.perf_counter()
     while time.perf_counter() - t0 < seconds:
         tok = int(np.argmax(o.forward([tok])))
         n += 1
     dt = time.perf_counter() - t0
-    return {"value": round(n / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"{n} greedy decode steps of the same 8B-shaped Q4_0 model after a 4-token prompt, {dt:.1f} s"}
+    return {"value": round(n / dt, 3), "unit": "tok/s", "cores": threads, "steps": n, "seconds": round(dt, 1)}
+
+
+def cpu_config_rates(ops, m, w, threads: int, seconds: float = 0.4) -> dict:
+    """The CPU oracle on C1-C4 at their shapes (one call repeated for ~`seconds`): GEMV GB/s of the
+    algorithmic bytes (weight + f32 activations in and out), prefill GEMM GOP/s on a 64-row sample
+    of its 512 rows, decode attention GB/s of the K/V bytes. Q4_0 weights are the model's layer-0
+    matrices; Q8_0 / Q4_K ones are encoded on the GPU (bit-exact to the oracle's encoders)."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle as orc
+
+    def timed(f):
+        f()
+        n, t0 = 0, time.perf_counter()
+        while True:
+            f()
+            n += 1
+            dt = time.perf_counter() - t0
+            if dt >= seconds:
+                return dt / n
+
+    out = {}
+    layer = {(4096, 6144): "blk.0.attn_qkv", (4096, 4096): "blk.0.attn_output", (4096, 28672): "blk.0.ffn_gate_up",
+             (14336, 4096): "blk.0.ffn_down"}
+
+    def gpu_encoded(t, N, K, seed):
+        return ops.quantize(ops.fill_normal((N, K), seed=seed, std=0.02), t).cpu().numpy()
+
+    raw = gpu_encoded("q8_0", 4096, 4096, 1)
+    x = orc.normal((1, 4096), seed=2)
+    out["C1 q8_0 K4096 N4096 B1 GB/s"] = round(gemv_bytes(4096, 4096, 1) * 34 / 18 / timed(
+        lambda: orc.mul_mat(raw, "q8_0", x, 4096, threads=threads)) / 1e9, 2)
+    for t in ("q4_0", "q4_K"):
+        for K, N in LAYER_SHAPES:
+            raw = w[layer[(K, N)]] if t == "q4_0" else gpu_encoded(t, N, K, K + N)
+            wb = raw.size
+            for B in (1, 8):
+                x = orc.normal((B, K), seed=3)
+                sec = timed(lambda: orc.mul_mat(raw, t, x, K, threads=threads))
+                out[f"C2 {t} K{K} N{N} B{B} GB/s"] = round((wb + B * K * 4 + B * N * 4) / sec / 1e9, 2)
+    raw = gpu_encoded("q8_0", 14336, 4096, 4)
+    x = orc.normal((64, 4096), seed=5)
+    sec = timed(lambda: orc.mul_mat(raw, "q8_0", x, 4096, threads=threads))
+    out["C3 q8_0 K4096 N14336 (64 of 512 rows) GOP/s"] = round(2 * 64 * 14336 * 4096 / sec / 1e9, 1)
+    for ctx in (512, 4096, 32768):
+        q = orc.normal((32, 1, 128), seed=6)
+        k16 = orc.fp32_to_fp16(orc.normal((8, ctx, 128), seed=7))
+        v16 = orc.fp32_to_fp16(orc.normal((8, ctx, 128), seed=8))
+        sec = timed(lambda: orc.flash_attn_ext(q, k16, v16, None, 1 / math.sqrt(128), threads=threads))
+        out[f"C4 attn ctx{ctx} GB/s"] = round(2 * ctx * 8 * 128 * 2 / sec / 1e9, 2)
+    return out
+
+
+def cpu_baseline(ops, m, w: dict, seconds: float = 10.0) -> dict:
+    """The CPU side of the line (the reference measures its CPU backend with 6 threads and with all
+    cores): decode tok/s after a PROMPT-token prompt with all available cores (value) and with 6
+    threads, the host CPU, and the oracle's C1-C4 rates with all cores."""
+    info = cpu_info()
+    cores = info["cpus_available"]
+    allc = cpu_decode_sample(m, w, cores, seconds)
+    six = cpu_decode_sample(m, w, min(6, cores), seconds)
+    res = {"value": allc["value"], "unit": "tok/s", "cores": cores, "kind": "port",
+           "sample": f"{allc['steps']} greedy decode steps of the same 8B-shaped Q4_0 model at positions "
+                     f"{PROMPT}+ (prompt K/V synthetic), {allc['seconds']} s; the repo's C restatement of ggml-cpu",
+           "threads_6": six, **info}
+    res["configs_all_cores"] = cpu_config_rates(ops, m, w, cores)
+    return res
 
 
 def bench_gemv(args, ops, torch) -> dict:
@@ -457,6 +546,7 @@ def main() -> int:
                          "ggml: the decode step built with the ggml API and run by its graph executor; "
                          "program: the same model as a ggml-compiler program GGUF run by the loader")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-program", action="store_true", help="skip the program-GGUF decode figure")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for {args.gpus}); multi-GPU sharding is design-only here.",
@@ -515,8 +605,17 @@ def main() -> int:
     if "extra" in res:
         line["extra"] = res["extra"]
     line["roofline"] = gemv_roofline(ops, torch)
+    w = None
+    if args.mode == "decode" and not (args.no_program and args.no_cpu):
+        w = {name: model.get_weight(name) for name, *_ in model.weights()}
+    if args.mode == "decode" and not args.no_program:
+        # the same model as a ggml-compiler program GGUF run by libgcq's loader (the reference's
+        # boundary: ggml_compiler_load + the generate entry), same step count
+        prog = bench_program_decode(args, w)
+        line["extra"]["program_gguf_decode_tok_s"] = prog["value"]
+        line["extra"]["program_gguf_ms_per_step"] = prog["ms_per_step"]
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_decode_baseline(model) if model is not None else cpu_gemv_baseline()
+        line["cpu_baseline"] = cpu_baseline(ops, model, w) if model is not None else cpu_gemv_baseline()
     print(json.dumps(line), flush=True)
     return 0
 

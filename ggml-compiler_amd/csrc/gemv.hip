@@ -15,6 +15,8 @@
 #include "gcq_common.h"
 
 #include <algorithm>
+#include <cstdlib>
+#include <string>
 
 namespace gcq {
 
@@ -754,11 +756,32 @@ void run_q4k_nbl(int nbl, const uint8_t * w, const int8_t * xc, const int16_t * 
 
 // y [B][ldy] (first N columns written) from packed weights and a quantized activation; with res,
 // y = res + W x (res has y's layout and may be y itself).
+bool gemv_mfma_fits(int type, int64_t K, int64_t B);
+void launch_gemv_mfma(int type, const uint8_t * wqs, const uint16_t * wd, const int8_t * xc, const float2 * xm,
+                      float * y, int N, int nb, int B, int ldy, hipStream_t s);
+
+// Batches of 2..16 rows on the int8 matrix cores (gemv_mfma.hip) with GCQ_GEMV_MFMA=1 (measured
+// slower than the row kernels so far: its loads touch 16 rows each and its per-block epilogue
+// waits on every matrix instruction).
+static bool use_gemv_mfma() {
+    static const bool on = [] {
+        const char * e = std::getenv("GCQ_GEMV_MFMA");
+        return e && std::string(e) == "1";
+    }();
+    return on;
+}
+
 void launch_gemv(int type, const void * wv, int64_t N, int64_t K, const void * act, int64_t B, float * y, int64_t ldy,
                  hipStream_t s, const float * res) {
     const uint8_t * w = (const uint8_t *) wv;
     const ActLayout A = act_layout(type, B, K);
     const uint8_t * a = (const uint8_t *) act;
+    if ((type == T_Q4_0 || type == T_Q8_0) && res == nullptr && gemv_mfma_fits(type, K, B) && use_gemv_mfma()) {
+        const WeightLayout L = weight_layout(type, N, K);
+        launch_gemv_mfma(type, w + L.qs, (const uint16_t *) (w + L.d), (const int8_t *) (a + A.codes),
+                         (const float2 *) (a + A.meta), y, (int) N, (int) (K / QK), (int) B, (int) ldy, s);
+        return;
+    }
     if (type == T_Q4_0 || type == T_Q8_0) {
         const WeightLayout L = weight_layout(type, N, K);
         const int nb = (int) (K / QK);

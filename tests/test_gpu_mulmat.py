@@ -104,3 +104,51 @@ def test_gemv_is_linear_at_full_size(gops):
     y1 = gops.mul_mat(qw, x)
     y2 = gops.mul_mat(qw, 2 * x)
     assert torch.equal(2 * y1, y2)
+
+
+_FULL = {}
+
+
+def _full_weight(gops, t, N, K):
+    """The weight once per (type, shape): N(0, 0.02) from the synthetic stream, encoded on the GPU
+    (the encoder equals the oracle's byte for byte, test_gpu_quant.py), as ggml block bytes."""
+    key = (t, N, K)
+    if key not in _FULL:
+        _FULL.clear()
+        raw = gops.quantize(gops.fill_normal((N, K), seed=41, std=0.02), t)
+        _FULL[key] = (raw.cpu().numpy(), gops.QuantWeight.from_ggml(raw, t, K))
+    return _FULL[key]
+
+
+@pytest.mark.parametrize("t", ["q4_0", "q4_K"])
+@pytest.mark.parametrize("N,K", [(28672, 4096), (4096, 14336)])
+@pytest.mark.parametrize("B", [1, 4, 8])
+def test_gemv_full_decode_shapes(gops, orc, t, N, K, B):
+    """The decode batch shapes at full size (fused gate/up 4096 x 28672, down 14336 x 4096) for 1,
+    4 and 8 rows, every output against the oracle."""
+    raw, qw = _full_weight(gops, t, N, K)
+    x = orc.normal((B, K), seed=42 + B)
+    y = to_np(gops.mul_mat(qw, torch.from_numpy(x).cuda()))
+    assert orc.parity(y, orc.mul_mat(raw, t, x, K)) < TOL
+
+
+def test_gemv_c1_q8_0_4096(gops, orc):
+    """C1 at its shape: Q8_0, 4096 x 4096, one row."""
+    raw, qw = _full_weight(gops, "q8_0", 4096, 4096)
+    x = orc.normal((1, 4096), seed=43)
+    y = to_np(gops.mul_mat(qw, torch.from_numpy(x).cuda()))
+    assert orc.parity(y, orc.mul_mat(raw, "q8_0", x, 4096)) < TOL
+
+
+@pytest.mark.parametrize("t", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("B", [2, 5, 16])
+def test_gemv_mfma_batches(gops, orc, t, B):
+    """The matrix-core GEMV (2..16 rows): a row count that is not a multiple of its 16-row tile,
+    a residual, and K of 64 blocks (16 wavefronts, one block pair each)."""
+    N, K = 1000, 2048
+    raw, qw = _weight(gops, orc, t, N, K, 44)
+    x = orc.normal((B, K), seed=45)
+    r = orc.normal((B, N), seed=46)
+    act = gops.quantize_act(t, torch.from_numpy(x).cuda())
+    y = to_np(gops.mul_mat_q(qw, act, B, res=torch.from_numpy(r).cuda()))
+    assert orc.parity(y, orc.mul_mat(raw, t, x, K) + r) < TOL
