@@ -9,6 +9,8 @@
 //   rms_norm -> mul(w)                     one rms_norm launch with the weight
 //   rms_norm -> mul(w) -> mul_mat [-> add]  one decode-row GEMV normalizing x itself (one row), or
 //                                          rms_norm + Q8_0 conversion, then the GEMV / GEMM
+//   rms_norm -> mul -> {gate, up} mul_mats -> swiglu   one decode-row GEMV over the two weights'
+//                                          row pairs, silu(gate) * up in its epilogue
 //   swiglu -> mul_mat [-> add]             swiglu + Q8_0 conversion, then the GEMV / GEMM
 //   mul_mat -> add                         the residual added in the GEMV / GEMM epilogue
 // A chain is formed only where each intermediate has exactly one reader and is not flagged as an
@@ -262,6 +264,35 @@ std::vector<int> qkv_rope_group(const ggml_cgraph * g, const std::vector<int> & 
     return grp;
 }
 
+// The gate and up GEMVs of one folded row whose results only a swiglu reads (ggml_swiglu_split of
+// the two, llm.py's FFN): one launch writing silu(gate) * up, the row pairs (gate row j, up row j)
+// read from the two weights (kind 4: {mm_gate, mm_up, glu}; only the glu's result has memory of
+// its own). Same weight type and shape, one row. Returns the group or {}.
+std::vector<int> gate_up_group(const ggml_cgraph * g, const std::vector<int> & mms,
+                               const std::unordered_map<const ggml_tensor *, int> & uses,
+                               const std::unordered_map<const ggml_tensor *, int> & reader) {
+    if (mms.size() != 2) return {};
+    const int n = (int) g->nodes.size();
+    auto next = [&](const ggml_tensor * t) -> int {
+        if (is_output(t) || t == g->nodes[n - 1]) return -1;
+        auto u = uses.find(t);
+        if (u == uses.end() || u->second != 1) return -1;
+        return reader.at(t);
+    };
+    const ggml_tensor *a = g->nodes[mms[0]], *b = g->nodes[mms[1]];
+    const int r = next(a);
+    if (r < 0 || next(b) != r) return {};
+    const ggml_tensor * glu = g->nodes[r];
+    if (glu->op != GGML_OP_GLU || glu->op_params[0] != GGML_GLU_OP_SWIGLU || glu->op_params[1] != 0) return {};
+    const ggml_tensor *gate = glu->src[0], *up = glu->src[1];
+    if (!((gate == a && up == b) || (gate == b && up == a))) return {};
+    const ggml_tensor *wg = gate->src[0], *wu = up->src[0];
+    if (wg->type != wu->type || wg->ne[0] != wu->ne[0] || wg->ne[1] != wu->ne[1] || glu->type != GGML_TYPE_F32 ||
+        !ggml_is_contiguous(glu) || ggml_nrows(glu) != 1 || glu->ne[0] != wg->ne[1] || glu->view_src)
+        return {};
+    return {gate == a ? mms[0] : mms[1], gate == a ? mms[1] : mms[0], r};
+}
+
 Chains find_chains(const ggml_cgraph * g, bool fuse) {
     const int n = (int) g->nodes.size();
     Chains c;
@@ -348,8 +379,10 @@ Chains find_chains(const ggml_cgraph * g, bool fuse) {
                 std::vector<int> grp(rd.begin(), rd.end());
                 std::sort(grp.begin(), grp.end());
                 std::vector<int> qkv = grp.size() == 3 ? qkv_rope_group(g, grp, uses, reader) : std::vector<int>{};
-                const int kind = qkv.empty() ? 0 : 3;
+                std::vector<int> gu = grp.size() == 2 ? gate_up_group(g, grp, uses, reader) : std::vector<int>{};
+                const int kind = !qkv.empty() ? 3 : !gu.empty() ? 4 : 0;
                 if (kind == 3) grp = qkv;
+                if (kind == 4) grp = gu;
                 int lo = n;
                 for (int r : grp) {
                     c.sib[r] = (int) c.groups.size();
@@ -359,7 +392,7 @@ Chains find_chains(const ggml_cgraph * g, bool fuse) {
                 c.kind.push_back(kind);
                 c.first.push_back(lo);
             }
-        } else if (t->op == GGML_OP_GLU && f32_contig(t->src[0]) && f32_contig(t->src[1]) && aligned16(t->src[0]) &&
+        } else if (t->op == GGML_OP_GLU && c.sib[i] < 0 && f32_contig(t->src[0]) && f32_contig(t->src[1]) && aligned16(t->src[0]) &&
                    aligned16(t->src[1]) && t->ne[0] % 32 == 0) {
             const int k = sole(t);
             if (k < 0 || g->nodes[k]->op != GGML_OP_MUL_MAT || g->nodes[k]->src[1] != t || !q8_mul_mat(g->nodes[k]))
@@ -472,6 +505,7 @@ enum StepKind {
     S_SETROWS2,     // two set_rows of the same indices
     S_ROPE_TABLE,   // the (cos, sin) table of one position for S_QKV_ROPE
     S_QKV_ROPE,     // q / k / v GEMVs with q / k rope and k / v cache writes in the epilogue
+    S_GATE_UP,      // gate / up GEMVs of one normalized row with swiglu in the epilogue
     S_MULMAT_F,     // mul_mat of an f32 / f16 first operand (activations, KV-cache views)
 };
 
@@ -819,6 +853,28 @@ struct Planner {
         s.n[0] = N[0];
         s.n[1] = N[1];
         s.n[2] = grp.size() > 2 ? N[2] : 0;
+        s.n[3] = K;
+        std::memcpy(&s.f[0], &nrm->op_params[0], 4);
+        steps.push_back(s);
+    }
+
+    // Group kind 4: rms_norm -> mul -> {mul_mat gate, mul_mat up} -> swiglu, one decode-row launch.
+    void gate_up(const ggml_cgraph * g, const std::vector<int> & grp) {
+        const ggml_tensor *mg = g->nodes[grp[0]], *mu = g->nodes[grp[1]], *glu = g->nodes[grp[2]];
+        const ggml_tensor * x = mg->src[1];
+        const ggml_tensor * nrm = x->src[0];
+        int64_t N[2], K = 0;
+        packed_dims(mg->src[0], N[0], K);
+        packed_dims(mu->src[0], N[1], K);
+        Step s = new_step(S_GATE_UP);
+        s.type = mg->src[0]->type;
+        s.in[0] = d(mg->src[0]);
+        s.in[1] = d(nrm->src[0]);
+        s.in[2] = d(x->src[1]);
+        s.in[3] = d(mu->src[0]);
+        s.out = o(glu);
+        s.n[0] = N[0];
+        s.n[1] = N[1];
         s.n[3] = K;
         std::memcpy(&s.f[0], &nrm->op_params[0], 4);
         steps.push_back(s);
@@ -1310,6 +1366,17 @@ void run_step(const ggml_backend * be, const Step & s) {
             launch_row_gemv(s.type, PRO_NORM, EPI_ROPE_KV, a, st);
             return;
         }
+        case S_GATE_UP: {
+            const uint8_t * w[2] = {(const uint8_t *) s.in[0], (const uint8_t *) s.in[3]};
+            RowArgs a{};
+            require(row_gemv_ranges(s.type, 2, w, s.n, s.n[3], a), "gate / up: weights do not fit one launch");
+            a.x = (const float *) s.in[1];
+            a.norm_w = (const float *) s.in[2];
+            a.eps = s.f[0];
+            a.y = (float *) s.out;
+            launch_row_gemv(s.type, PRO_NORM, EPI_SWIGLU, a, st);
+            return;
+        }
         case S_MULMAT3: {
             const int n = s.in[4] ? 3 : 2;
             const uint8_t * w[3] = {(const uint8_t *) s.in[0], (const uint8_t *) s.in[3], (const uint8_t *) s.in[4]};
@@ -1491,6 +1558,7 @@ enum ggml_status compute(ggml_backend * be, ggml_cgraph * g, bool async = false)
             if (i == c.first[gi]) {
                 if (c.kind[gi] == 0) p.mulmat_group(g, grp);
                 else if (c.kind[gi] == 3) p.qkv_rope(g, grp);
+                else if (c.kind[gi] == 4) p.gate_up(g, grp);
                 else p.pair(g->nodes[grp[0]], g->nodes[grp[1]]);
             }
             continue;
@@ -1618,10 +1686,11 @@ size_t place(ggml_gallocr * ga, ggml_cgraph * g, std::vector<std::pair<ggml_tens
             const size_t gi = (size_t) c.sib[i];
             const std::vector<int> & grp = c.groups[gi];
             if (i == c.first[gi]) {
-                // kind 3 writes rope_q's result only (and the caches in place)
-                const size_t nres = c.kind[gi] == 3 ? 1 : grp.size();
+                // kind 3 writes rope_q's result only (and the caches in place), kind 4 the glu's
+                const int only = c.kind[gi] == 3 ? 3 : c.kind[gi] == 4 ? 2 : -1;
+                const size_t nres = only >= 0 ? 1 : grp.size();
                 for (size_t q = 0; q < nres; q++) {
-                    ggml_tensor * u = g->nodes[grp[c.kind[gi] == 3 ? 3 : q]];
+                    ggml_tensor * u = g->nodes[grp[only >= 0 ? (size_t) only : q]];
                     if (!needs(u)) continue;
                     const size_t o = A.take(alloc_size(u));
                     off[u] = o;

@@ -65,6 +65,8 @@ struct Chains {
     // kind 3: q / k / v GEMVs of one row with the decode step's rope of q and k and the set_rows of
     // k and v into f16 caches, as one launch: {mm_q, mm_k, mm_v, rope_q, then the reshape / rope /
     // permute / set_rows members}; only rope_q's result is written to memory of its own.
+    // kind 4: gate / up GEMVs of one row read only by a swiglu, as one launch writing the swiglu's
+    // result: {mm_gate, mm_up, glu}; only the glu's result has memory of its own.
     std::vector<int> first;  // each group's earliest node: where its launch runs
 };
 Chains find_chains(const ggml_cgraph * g, bool fuse = true);

@@ -25,7 +25,7 @@
 //
 // Row pairs: EPI_ROPE_KV expects the QKV weight packed so that group g holds the rotation pair
 // (i, i + D/2) of a q or k head, then consecutive v rows; EPI_SWIGLU expects gate row j and up row
-// j in group j (llama.hip packs them so).
+// j in group j (llama.hip packs them so; with two weights, group j reads row j of each).
 #include "gcq_common.h"
 
 #include <algorithm>
@@ -68,7 +68,6 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
     constexpr bool XREG = NBL <= 2;  // activation blocks in registers, else read from LDS per use
     constexpr bool PF = CV * NBL * R <= 8;  // next group's weights prefetched (else: registers spill)
     static_assert(EPI == EPI_STORE || R == 2, "row-pair epilogues take two rows per group");
-    static_assert(MR == 1 || EPI != EPI_SWIGLU, "several weights: plain stores or q / k / v rope");
     __shared__ int4 lc[kRowMaxK / 16];
     __shared__ float2 lm[kRowMaxK / 32];
     __shared__ double red[NWV];
@@ -100,9 +99,14 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
     auto pick_u = [](int k, const uint32_t (&v)[3]) { return k == 2 ? v[2] : k == 1 ? v[1] : v[0]; };
     // Row r of group g with several weights: EPI_STORE takes the rows in order; EPI_ROPE_KV takes
     // separate q, k, v weights (ranges 0, 1, 2) in the packed QKV order: group g < (H + Hkv) D/2
-    // is the rotation pair (i, i + D/2) of q head h (h < H) or k head h - H, then pairs of v rows.
+    // is the rotation pair (i, i + D/2) of q head h (h < H) or k head h - H, then pairs of v rows;
+    // EPI_SWIGLU takes separate gate and up weights (ranges 0, 1): group g is gate row g and up
+    // row g, the pair the packed gate/up weight holds in group g.
     auto map_row = [&](int g, int r, int & local) -> int {
-        if constexpr (EPI == EPI_ROPE_KV) {
+        if constexpr (EPI == EPI_SWIGLU) {
+            local = min(__builtin_amdgcn_readfirstlane(g), a.r_end[0] - 1);
+            return r;
+        } else if constexpr (EPI == EPI_ROPE_KV) {
             g = __builtin_amdgcn_readfirstlane(g);
             const int hd = a.D >> 1, nq = (a.H + a.Hkv) * hd;
             if (g < nq) {
@@ -466,7 +470,7 @@ namespace {
 
 template <int TYPE, int R, int NBL, int PRO, int EPI>
 void go(const RowArgs & a, unsigned grid, hipStream_t s) {
-    if constexpr ((EPI == EPI_STORE || (EPI == EPI_ROPE_KV && R == 2)) && PRO == PRO_NORM) {
+    if constexpr ((EPI == EPI_STORE || ((EPI == EPI_ROPE_KV || EPI == EPI_SWIGLU) && R == 2)) && PRO == PRO_NORM) {
         if (a.nr > 1) {
             k_row_gemv<TYPE, R, NBL, PRO, EPI, 3><<<grid, 1024, 0, s>>>(a);
             return;
@@ -587,8 +591,10 @@ void launch_row_gemv(int type, int pro, int epi, const RowArgs & a, hipStream_t 
     require(epi == EPI_STORE || a.N % 2 == 0, "row gemv: row-pair epilogue needs an even row count");
     require(a.nr <= 1 || epi == EPI_STORE ||
                 (epi == EPI_ROPE_KV && a.nr == 3 && a.D % 2 == 0 && a.r_end[0] == a.H * a.D &&
-                 a.r_end[1] == (a.H + a.Hkv) * a.D && a.r_end[2] == (a.H + 2 * a.Hkv) * a.D),
-            "row gemv: separate q / k / v weights of H*D, Hkv*D, Hkv*D rows");
+                 a.r_end[1] == (a.H + a.Hkv) * a.D && a.r_end[2] == (a.H + 2 * a.Hkv) * a.D) ||
+                (epi == EPI_SWIGLU && a.nr == 2 && a.r_end[1] == 2 * a.r_end[0]),
+            "row gemv: separate q / k / v weights of H*D, Hkv*D, Hkv*D rows, or gate / up weights of equal rows");
+    require(a.nr <= 1 || pro == PRO_NORM, "row gemv: several weights take the rms_norm prologue");
     require(pro != PRO_MERGE || (a.nsplit >= 1 && a.nsplit <= kMergeMax && a.D % 4 == 0 && a.nb * QK <= 4096),
             "row gemv: merge of 1.." + std::to_string(kMergeMax) + " splits, K <= 4096");
     if (type == T_Q4_0) run_row_t<T_Q4_0>(pro, epi, a, s);

@@ -289,6 +289,40 @@ def test_swiglu_prologue_equals_separate_launches(be, gops, orc, t, F):
     assert orc.parity(y, orc.mul_mat(raw, t, orc.swiglu(gt, up), F) + r) < TOL
 
 
+@pytest.mark.parametrize("t", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("F,K", [(512, 2048), (14336, 4096)])
+def test_gate_up_swiglu_in_one_launch(be, orc, t, F, K):
+    """The FFN of one token as the reference builds it: rms_norm -> mul -> gate and up mul_mats ->
+    swiglu_split -> down mul_mat -> add. The gate / up GEMVs run as one launch writing silu(gate) *
+    up (the row pairs read from the two weights); equal bit for bit to the graph with the
+    normalized row kept as an output (gate and up then launched as a pair with separate results,
+    the swiglu in the down GEMV's prologue), and the oracle within 1e-3."""
+    tid = orc.TYPES[t]
+    N = 256
+    wg, wu, wd = _weight(orc, t, F, K, 150), _weight(orc, t, F, K, 151), _weight(orc, t, N, F, 152)
+    x = orc.normal((1, K), seed=153)
+    nw = (1.0 + 0.1 * orc.normal((K,), seed=154)).astype(np.float32)
+    r = orc.normal((1, N), seed=155)
+    leaves = {"x": (G.F32, [K, 1], x), "nw": (G.F32, [K], nw), "wg": (tid, [K, F], wg), "wu": (tid, [K, F], wu),
+              "wd": (tid, [F, N], wd), "r": (G.F32, [N, 1], r)}
+    keep = {}
+
+    def build(g, ctx, L):
+        keep["m"] = g.ggml_mul(ctx, g.ggml_rms_norm(ctx, L["x"], 1e-5), L["nw"])
+        h = g.ggml_swiglu_split(ctx, g.ggml_mul_mat(ctx, L["wg"], keep["m"]), g.ggml_mul_mat(ctx, L["wu"], keep["m"]))
+        return g.ggml_add(ctx, g.ggml_mul_mat(ctx, L["wd"], h), L["r"])
+
+    got = {}
+    for name, outs in (("fused", ()), ("split", [lambda s: keep["m"]])):
+        gr = Graph(be, leaves, build, outputs=outs)
+        got[name] = gr.run().reshape(1, N)
+        gr.close()
+    assert np.array_equal(got["fused"], got["split"])
+    xn = orc.rms_norm(x, 1e-5) * nw[None, :]
+    h = orc.swiglu(orc.mul_mat(wg, t, xn, K), orc.mul_mat(wu, t, xn, K))
+    assert orc.parity(got["fused"], orc.mul_mat(wd, t, h, F) + r) < TOL
+
+
 # ----------------------------------------------------------------------------- attention
 
 @pytest.mark.parametrize("Sq,n_kv,H,Hkv,D", [(1, 300, 8, 2, 128), (5, 130, 4, 4, 64), (1, 1, 32, 8, 128),
