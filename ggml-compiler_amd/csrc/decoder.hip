@@ -169,41 +169,20 @@ __global__ void k_causal_mask(uint16_t * __restrict__ mask, int S, int n_kv, int
 }
 
 // argmax of the logits (first index of the maximum) and the generate loop's step: record the
-// token, advance position and KV length. Every workgroup reduces a slice to (max, first index)
-// and the last one to finish (a device counter, reset by that workgroup for the next launch)
-// reduces the partials and advances the state: one launch, no wait on other workgroups.
-__device__ __forceinline__ void argmax_combine(float & v, int & i, float v2, int i2) {
-    if (v2 > v || (v2 == v && i2 < i)) {
-        v = v2;
-        i = i2;
-    }
-}
-
-__device__ __forceinline__ void block_argmax(float & v, int & idx) {
-    __shared__ float bv[4];
-    __shared__ int bi[4];
-    for (int o = 32; o > 0; o >>= 1) argmax_combine(v, idx, __shfl_xor(v, o, 64), __shfl_xor(idx, o, 64));
-    if ((threadIdx.x & 63) == 0) {
-        bv[threadIdx.x >> 6] = v;
-        bi[threadIdx.x >> 6] = idx;
-    }
-    __syncthreads();
-    v = bv[0];
-    idx = bi[0];
-    for (int w = 1; w < 4; w++) argmax_combine(v, idx, bv[w], bi[w]);
-    __syncthreads();
-}
-
+// token, advance position and KV length. Every workgroup reduces a kArgmaxSlice-value slice to
+// (max, first index) and the last one to finish (a device counter, reset by that workgroup for
+// the next launch) reduces the partials and advances the state: one launch, no wait on other
+// workgroups.
 __global__ __launch_bounds__(256) void k_step_end(const float * __restrict__ logits, int n, StepState * st,
                                                   int32_t * __restrict__ out_tokens, int max_out,
                                                   float2 * __restrict__ part, unsigned int * __restrict__ counter) {
     __shared__ bool last;
-    float v = -INFINITY;
-    int idx = 0x7fffffff;
-    const int per = (n + gridDim.x - 1) / gridDim.x;
-    const int lo = blockIdx.x * per, hi = min(n, lo + per);
-    for (int i = lo + threadIdx.x; i < hi; i += 256) argmax_combine(v, idx, logits[i], i);
-    block_argmax(v, idx);
+    __shared__ float pv[4];
+    __shared__ int pi[4];
+    float v;
+    int idx;
+    const int lo = blockIdx.x * kArgmaxSlice;
+    slice_argmax(logits, lo, min(n, lo + kArgmaxSlice), (reinterpret_cast<uintptr_t>(logits) & 15) == 0, v, idx);
     if (threadIdx.x == 0) {
         part[blockIdx.x] = make_float2(v, __int_as_float(idx));
         __threadfence();
@@ -216,10 +195,16 @@ __global__ __launch_bounds__(256) void k_step_end(const float * __restrict__ log
     idx = 0x7fffffff;
     for (int b = threadIdx.x; b < (int) gridDim.x; b += 256) {
         const float2 p = part[b];
-        argmax_combine(v, idx, p.x, __float_as_int(p.y));
+        argmax_take(v, idx, p.x, __float_as_int(p.y));
     }
-    block_argmax(v, idx);
+    for (int o = 32; o > 0; o >>= 1) argmax_take(v, idx, __shfl_xor(v, o, 64), __shfl_xor(idx, o, 64));
+    if ((threadIdx.x & 63) == 0) {
+        pv[threadIdx.x >> 6] = v;
+        pi[threadIdx.x >> 6] = idx;
+    }
+    __syncthreads();
     if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; w++) argmax_take(v, idx, pv[w], pi[w]);
         const int tok = (v == -INFINITY || idx == 0x7fffffff) ? 0 : idx;
         if (out_tokens && st->step < max_out) out_tokens[st->step] = tok;
         st->step += 1;
@@ -290,10 +275,12 @@ void launch_causal_mask(void * mask, int S, int n_kv, int pos0, hipStream_t s) {
     check_launch("causal_mask");
 }
 
-// part: kStepEndBlocks float2, counter: one zeroed unsigned int (left zeroed after each launch).
+// part: kStepEndBlocks float2, counter: one zeroed unsigned int (left zeroed after each launch);
+// n <= kStepEndBlocks * kArgmaxSlice.
 void launch_step_end(const float * logits, int n, void * state, int32_t * out_tokens, int max_out, void * part,
                      void * counter, hipStream_t s) {
-    k_step_end<<<kStepEndBlocks, 256, 0, s>>>(logits, n, (StepState *) state, out_tokens, max_out, (float2 *) part,
+    require(n >= 1 && n <= kStepEndBlocks * kArgmaxSlice, "step end: vocabulary of 1 to 524288 logits");
+    k_step_end<<<nblk(n, kArgmaxSlice), 256, 0, s>>>(logits, n, (StepState *) state, out_tokens, max_out, (float2 *) part,
                                               (unsigned int *) counter);
     check_launch("step_end");
 }

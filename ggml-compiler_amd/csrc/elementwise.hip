@@ -330,12 +330,6 @@ __global__ __launch_bounds__(256) void k_soft_max(const float * x, float * y, in
 // 128256 logits is 500 KB: a 256-thread block walking it with one 4-byte load at a time spent
 // 130 us waiting); the first index of the maximum (NaN never wins; a row of -inf / NaN gives 0,
 // as ggml's forward_argmax).
-__device__ __forceinline__ void argmax_take(float & v, int & idx, float a, int i) {
-    if (a > v || (a == v && i < idx)) {
-        v = a;
-        idx = i;
-    }
-}
 
 __global__ __launch_bounds__(1024) void k_argmax(const float * __restrict__ x, int64_t ldx, int n,
                                                  int32_t * __restrict__ out) {
@@ -372,6 +366,51 @@ __global__ __launch_bounds__(1024) void k_argmax(const float * __restrict__ x, i
     if (threadIdx.x == 0) {
         for (int w = 1; w < 16; w++) argmax_take(v, idx, bv[w], bi[w]);
         out[blockIdx.x] = (v == -INFINITY || idx == 0x7fffffff) ? 0 : idx;
+    }
+}
+
+// Long rows, few of them: workgroup (slice, row) reduces kArgmaxSlice values of the row to (max,
+// first index) and the last of the row's workgroups to finish (a per-row device counter, which
+// that workgroup resets for the next launch) picks among the row's partials - one launch whose
+// workgroups all load at once (a single block per 128256-value row measured 15 us, bound by one
+// CU's loads). Same result as k_argmax: the selection does not depend on the order.
+__global__ __launch_bounds__(256) void k_argmax_split(const float * __restrict__ x, int64_t ldx, int n,
+                                                      int32_t * __restrict__ out, float2 * __restrict__ part,
+                                                      unsigned int * __restrict__ counter) {
+    __shared__ bool last;
+    __shared__ float pv[4];
+    __shared__ int pi[4];
+    const int row = blockIdx.y, slices = gridDim.x;
+    const float * xr = x + row * ldx;
+    const int lo = blockIdx.x * kArgmaxSlice;
+    float v;
+    int idx;
+    slice_argmax(xr, lo, min(n, lo + kArgmaxSlice), (reinterpret_cast<uintptr_t>(xr) & 15) == 0, v, idx);
+    float2 * pr = part + (int64_t) row * slices;
+    if (threadIdx.x == 0) {
+        pr[blockIdx.x] = make_float2(v, __int_as_float(idx));
+        __threadfence();
+        last = atomicAdd(counter + row, 1u) == (unsigned) slices - 1;
+    }
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    v = -INFINITY;
+    idx = 0x7fffffff;
+    for (int b = threadIdx.x; b < slices; b += 256) {
+        const float2 p = pr[b];
+        argmax_take(v, idx, p.x, __float_as_int(p.y));
+    }
+    for (int o = 32; o > 0; o >>= 1) argmax_take(v, idx, __shfl_xor(v, o, 64), __shfl_xor(idx, o, 64));
+    if ((threadIdx.x & 63) == 0) {
+        pv[threadIdx.x >> 6] = v;
+        pi[threadIdx.x >> 6] = idx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; w++) argmax_take(v, idx, pv[w], pi[w]);
+        out[row] = (v == -INFINITY || idx == 0x7fffffff) ? 0 : idx;
+        counter[row] = 0u;
     }
 }
 
@@ -572,6 +611,26 @@ void launch_argmax(const float * x, int64_t ldx, int64_t rows, int64_t n, int32_
     if (rows == 0) return;
     k_argmax<<<(unsigned) rows, 1024, 0, s>>>(x, ldx, (int) n, out);
     check_launch("argmax");
+}
+
+// The sliced argmax's scratch: 64 row counters, then up to 16384 partials.
+size_t argmax_split_scratch() { return 256 + 16384 * sizeof(float2); }
+
+bool argmax_split_fits(int64_t rows, int64_t n) {
+    return rows >= 1 && rows <= 64 && n >= 4 * kArgmaxSlice && n <= INT32_MAX &&
+           rows * ((n + kArgmaxSlice - 1) / kArgmaxSlice) <= 16384;
+}
+
+// scratch: argmax_split_scratch() bytes whose first 256 are zero before the first launch (each
+// launch leaves them zero).
+void launch_argmax_split(const float * x, int64_t ldx, int64_t rows, int64_t n, int32_t * out, void * scratch,
+                         hipStream_t s) {
+    require(argmax_split_fits(rows, n), "argmax: the sliced kernel takes 1 to 64 rows of 8192 or more values");
+    const unsigned slices = (unsigned) ((n + kArgmaxSlice - 1) / kArgmaxSlice);
+    unsigned int * counter = (unsigned int *) scratch;
+    float2 * part = (float2 *) ((uint8_t *) scratch + 256);
+    k_argmax_split<<<dim3(slices, (unsigned) rows), 256, 0, s>>>(x, ldx, (int) n, out, part, counter);
+    check_launch("argmax split");
 }
 
 void launch_cpy(const void * src, int st, void * dst, int dt, const Cpy4 & g, int64_t n, hipStream_t s) {

@@ -429,6 +429,62 @@ __device__ __forceinline__ int wave_isum(int v) {
     return v;
 }
 
+// (max, first index) selection: a value wins if greater, or equal at a lower index; NaN never
+// wins. The choice does not depend on the order values are offered in.
+__device__ __forceinline__ void argmax_take(float & v, int & idx, float a, int i) {
+    if (a > v || (a == v && i < idx)) {
+        v = a;
+        idx = i;
+    }
+}
+
+// Values per workgroup of the sliced argmax: 256 threads x two 16-byte loads.
+constexpr int kArgmaxSlice = 2048;
+
+// (max, first index) of x[lo, hi) (hi - lo <= kArgmaxSlice) over a 256-thread workgroup, every
+// thread calling it: both loads of a thread in flight together (16-byte when vec: x + lo 16-byte
+// aligned), then the waves' results through LDS. (v, idx) = (-inf, INT_MAX) for an empty slice.
+__device__ __forceinline__ void slice_argmax(const float * __restrict__ x, int lo, int hi, bool vec, float & v,
+                                             int & idx) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    const int t = threadIdx.x;
+    float q[2][4];
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        const int e = lo + 4 * (t + 256 * u);
+        if (vec && e + 3 < hi) {
+            const float4 f = *reinterpret_cast<const float4 *>(x + e);
+            q[u][0] = f.x;
+            q[u][1] = f.y;
+            q[u][2] = f.z;
+            q[u][3] = f.w;
+        } else {
+#pragma unroll
+            for (int c = 0; c < 4; c++) q[u][c] = e + c < hi ? x[e + c] : -INFINITY;
+        }
+    }
+    v = -INFINITY;
+    idx = 0x7fffffff;
+#pragma unroll
+    for (int u = 0; u < 2; u++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const int e = lo + 4 * (t + 256 * u) + c;
+            if (e < hi) argmax_take(v, idx, q[u][c], e);
+        }
+    for (int o = 32; o > 0; o >>= 1) argmax_take(v, idx, __shfl_xor(v, o, 64), __shfl_xor(idx, o, 64));
+    if ((t & 63) == 0) {
+        sv[t >> 6] = v;
+        si[t >> 6] = idx;
+    }
+    __syncthreads();
+    v = sv[0];
+    idx = si[0];
+    for (int w = 1; w < 4; w++) argmax_take(v, idx, sv[w], si[w]);
+    __syncthreads();
+}
+
 // 1/sqrt(mean(x^2) + eps) of one row, for a 256-thread block (all threads call it): squares
 // rounded to f32, summed in double, mean rounded to f32, as ggml-cpu's rms_norm.
 __device__ __forceinline__ float rms_scale(const float * xr, int n, float eps) {

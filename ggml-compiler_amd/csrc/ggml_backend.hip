@@ -57,6 +57,10 @@ void launch_mul_mat_f(bool a_f16, const void * a, const int64_t * ane, const int
 void launch_binary_bcast(int op, const float * a, const float * b, float * y, const int64_t * ane, const int64_t * bne,
                          hipStream_t s);
 void launch_argmax(const float * x, int64_t ldx, int64_t rows, int64_t n, int32_t * out, hipStream_t s);
+size_t argmax_split_scratch();
+bool argmax_split_fits(int64_t rows, int64_t n);
+void launch_argmax_split(const float * x, int64_t ldx, int64_t rows, int64_t n, int32_t * out, void * scratch,
+                         hipStream_t s);
 int decode_group(int GT, int max_kv);
 int decode_splits(int D, int G, int n_kv, int max_split);
 bool attn_decode_fits(int D, int G);
@@ -569,6 +573,7 @@ struct ggml_backend {
     void * ws = nullptr;  // workspace of the mul_mat activations and flash-attention partials
     size_t ws_size = 0;
     float2 * rope_cs = nullptr;  // (cos, sin) table of the fused q / k / v rope step (<= 128 pairs)
+    void * argmax_scratch = nullptr;  // the sliced argmax's row counters (left zero) and partials
     bool use_graphs = true;
     bool fuse = true;  // fusion chains and launch groups (off: every node alone, materialized)
     std::unordered_map<const ggml_cgraph *, Cached> graphs;
@@ -580,6 +585,7 @@ struct ggml_backend {
             if (kv.second.exec) (void) hipGraphExecDestroy(kv.second.exec);
         if (ws) (void) hipFree(ws);
         if (rope_cs) (void) hipFree(rope_cs);
+        if (argmax_scratch) (void) hipFree(argmax_scratch);
         if (stream) (void) hipStreamDestroy(stream);
     }
 };
@@ -1228,6 +1234,13 @@ struct Planner {
                 s.n[0] = (int64_t) stride / 4;
                 s.n[1] = rows;
                 s.n[2] = t->src[0]->ne[0];
+                if (!dry && argmax_split_fits(rows, s.n[2])) {  // long rows: the sliced kernel
+                    if (!be->argmax_scratch) {
+                        check_hip(hipMalloc(&be->argmax_scratch, argmax_split_scratch()), "hipMalloc argmax scratch");
+                        check_hip(hipMemset(be->argmax_scratch, 0, argmax_split_scratch()), "hipMemset argmax scratch");
+                    }
+                    s.in[1] = be->argmax_scratch;
+                }
                 steps.push_back(s);
                 return;
             }
@@ -1271,6 +1284,58 @@ struct Planner {
         ws_need = std::max(ws_need, align256((size_t) H * nsplit * D * 4) + align256((size_t) H * nsplit * 8) +
                                         align256((size_t) H * D * 4));
         steps.push_back(s);
+    }
+
+    // cpy(a, b) where a is one step's whole result, read by nothing else, and b is memory that no
+    // other node of g reads or writes (a stage result copied into its value, ...): the step writes
+    // b itself and the copy is dropped. Same values, one launch and one pass over a fewer.
+    void fold_result_copies(const ggml_cgraph * g) {
+        if (dry) return;
+        auto range = [](const ggml_tensor * t) {
+            const uintptr_t p = (uintptr_t) t->data;
+            return std::make_pair(p, p + ggml_nbytes(t));
+        };
+        auto overlap = [](std::pair<uintptr_t, uintptr_t> x, std::pair<uintptr_t, uintptr_t> y) {
+            return x.first < y.second && y.first < x.second;
+        };
+        for (const ggml_tensor * t : g->nodes) {
+            if (t->op != GGML_OP_CPY) continue;
+            const ggml_tensor *a = t->src[0], *b = t->src[1];
+            if (!a || !b || !a->data || !b->data || a->type != b->type || is_output(a) || a->view_src ||
+                !ggml_is_contiguous(a) || !ggml_is_contiguous(b) || !ggml_is_contiguous(t) ||
+                ggml_nelements(a) != ggml_nelements(b) || t->data != b->data)
+                continue;
+            int readers = 0;
+            bool shared = false;
+            const auto rb = range(b);
+            for (const ggml_tensor * n : g->nodes) {
+                if (n->view_src == a) readers++;
+                for (const ggml_tensor * s : n->src) {
+                    if (s == a) readers++;
+                    if (n != t && s && s->data && overlap(range(s), rb)) shared = true;
+                }
+                if (n != t && n->data && overlap(range(n), rb)) shared = true;
+            }
+            if (readers != 1 || shared) continue;
+            // a's producer: the last step before the copy that writes a's memory (steps before it
+            // may have written other tensors the allocator placed there earlier)
+            int prod = -1, cpy = -1;
+            for (int i = 0; i < (int) steps.size(); i++) {
+                const Step & s = steps[i];
+                if (s.kind == S_CPY && s.in[0] == a->data && s.out == t->data) {
+                    cpy = i;
+                    break;
+                }
+                if (s.out == a->data || s.out2[0] == a->data || s.out2[1] == a->data) prod = i;
+            }
+            if (cpy < 0 || prod < 0) continue;
+            Step & p = steps[(size_t) prod];
+            const bool whole = p.out == a->data && (p.kind == S_MULMAT || p.kind == S_ARGMAX ||
+                                                    p.kind == S_ATTN_MULMAT || p.kind == S_GATE_UP);
+            if (!whole) continue;
+            p.out = mut_data(b);
+            steps.erase(steps.begin() + cpy);
+        }
     }
 
     // The chain ending at node f (members before it, in order).
@@ -1484,7 +1549,9 @@ void run_step(const ggml_backend * be, const Step & s) {
                             s.type == GGML_TYPE_F16, s.n[4], s.n[5], s.n[6], s.n[7], s.n[8], s.f[0], st);
             return;
         case S_ARGMAX:
-            launch_argmax((const float *) s.in[0], s.n[0], s.n[1], s.n[2], (int32_t *) s.out, st);
+            if (s.in[1]) launch_argmax_split((const float *) s.in[0], s.n[0], s.n[1], s.n[2], (int32_t *) s.out,
+                                             (void *) s.in[1], st);
+            else launch_argmax((const float *) s.in[0], s.n[0], s.n[1], s.n[2], (int32_t *) s.out, st);
             return;
         case S_ATTN_MULMAT: {
             const int64_t D = s.n[5], H = s.n[6], Hkv = s.n[7], n_kv = s.n[8], N = s.n[9], K = s.n[10];
@@ -1573,6 +1640,7 @@ enum ggml_status compute(ggml_backend * be, ggml_cgraph * g, bool async = false)
             p.chain(g, idx);
         }
     }
+    p.fold_result_copies(g);
     ensure_ws(be, p.ws_need);
     std::vector<uint8_t> sig((const uint8_t *) be->steps.data(),
                              (const uint8_t *) (be->steps.data() + be->steps.size()));

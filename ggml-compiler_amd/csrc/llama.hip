@@ -167,6 +167,7 @@ struct Llama {
         require(c.n_layer > 0 && c.n_embd > 0 && c.n_head > 0 && c.n_head_kv > 0 && c.head_dim > 0 && c.n_ff > 0 &&
                     c.n_vocab > 0 && c.max_ctx > 0,
                 "llama: every size must be positive");
+        require(c.n_vocab <= 524288, "llama: at most 524288 vocabulary entries (the greedy step's argmax)");
         require(c.wtype == T_Q4_0 || c.wtype == T_Q8_0, "llama: weight type must be Q4_0 or Q8_0");
         require(c.n_head % c.n_head_kv == 0 && c.n_head / c.n_head_kv <= 8, "llama: 1..8 query heads per KV head");
         require(c.head_dim == 64 || c.head_dim == 128, "llama: head_dim must be 64 or 128");

@@ -924,22 +924,41 @@ ggml_tensor * emit_node(ggml_context * ctx, const NodeSpec & n, const std::vecto
 namespace gcq {
 namespace {
 
-__global__ void k_fill_words(uint32_t * __restrict__ p, int64_t n, uint32_t bits) {
-    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) p[i] = bits;
-}
+// The small work a driver does between its graphs (scalar and counter fills, causal mask rows,
+// slice and collect copies), several of them in one launch: op blockIdx.y, element i.
+enum { D_FILL32, D_CAUSAL, D_COPY4, D_COPY1 };
+constexpr int kDriverBatch = 8;
+constexpr size_t kDriverCopyMax = 1 << 20;  // larger copies: hipMemcpyAsync
+struct DriverKOp {
+    int kind;
+    uint32_t bits;
+    int64_t n, len, pos;  // elements; D_CAUSAL: row length and position
+    uint8_t * dst;
+    const uint8_t * src;
+};
+struct DriverBatch {
+    DriverKOp op[kDriverBatch];
+};
 
-// Rows of a causal mask for position pos: 0 where the key index (element % len) is <= pos, else -inf.
-__global__ void k_causal_rows(float * __restrict__ p, int64_t n, int64_t len, int64_t pos) {
+__global__ void k_driver_ops(const DriverBatch b) {
+    const DriverKOp & o = b.op[blockIdx.y];
     const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) p[i] = i % len <= pos ? 0.0f : -INFINITY;
+    if (i >= o.n) return;
+    switch (o.kind) {
+        case D_FILL32: reinterpret_cast<uint32_t *>(o.dst)[i] = o.bits; break;
+        // rows of a causal mask for position pos: 0 where the key index (element % len) is <= pos
+        case D_CAUSAL: reinterpret_cast<float *>(o.dst)[i] = i % o.len <= o.pos ? 0.0f : -INFINITY; break;
+        case D_COPY4: reinterpret_cast<uint32_t *>(o.dst)[i] = reinterpret_cast<const uint32_t *>(o.src)[i]; break;
+        default: o.dst[i] = o.src[i]; break;
+    }
 }
-
-unsigned blocks_for(int64_t n) { return (unsigned) ((n + 255) / 256); }
 
 // The work a driver does between its graphs, ordered on the backend's stream with them, so a loop
 // iteration waits for the host only where the host must see a value (a counter's start, an until
-// token).
+// token). Fills, mask rows and small copies wait in a batch that one launch runs before the next
+// graph, copy, read or wait (a loop iteration's counter, mask and the previous iteration's
+// collected row: one launch); an op touching memory a waiting one writes, or writing memory one
+// reads, runs the batch first, so the ops keep their order's effect.
 class StreamOps {
   public:
     void attach(ggml_backend_t be) {
@@ -951,36 +970,84 @@ class StreamOps {
     }
     void fill32(void * p, int64_t n, uint32_t bits) {
         if (n <= 0) return;
-        k_fill_words<<<blocks_for(n), 256, 0, s_>>>((uint32_t *) p, n, bits);
-        check_launch("driver fill");
+        add({D_FILL32, bits, n, 0, 0, (uint8_t *) p, nullptr}, (size_t) n * 4);
     }
     void causal(float * p, int64_t n, int64_t len, int64_t pos) {
         if (n <= 0) return;
-        k_causal_rows<<<blocks_for(n), 256, 0, s_>>>(p, n, len, pos);
-        check_launch("driver mask");
+        add({D_CAUSAL, 0, n, len, pos, (uint8_t *) p, nullptr}, (size_t) n * 4);
     }
     void copy(void * dst, const void * src, size_t n) {
-        if (n) check_hip(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToDevice, s_), "driver copy");
+        if (!n) return;
+        if (n > kDriverCopyMax) {
+            flush();
+            check_hip(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToDevice, s_), "driver copy");
+            return;
+        }
+        const bool words = ((uintptr_t) dst & 3) == 0 && ((uintptr_t) src & 3) == 0 && n % 4 == 0;
+        add({words ? D_COPY4 : D_COPY1, 0, (int64_t) (words ? n / 4 : n), 0, 0, (uint8_t *) dst,
+             (const uint8_t *) src},
+            n);
     }
     void clear(void * dst, size_t n) {
+        flush();
         if (n) check_hip(hipMemsetAsync(dst, 0, n, s_), "driver clear");
     }
     int32_t read_i32(const void * src) {
+        flush();
         check_hip(hipMemcpyAsync(pinned_, src, 4, hipMemcpyDeviceToHost, s_), "driver read");
         check_hip(hipStreamSynchronize(s_), "driver read");
         int32_t v;
         std::memcpy(&v, pinned_, 4);
         return v;
     }
-    void finish() { check_hip(hipStreamSynchronize(s_), "driver"); }
-    hipStream_t stream() const { return s_; }
+    void finish() {
+        flush();
+        check_hip(hipStreamSynchronize(s_), "driver");
+    }
+    // the stream, with every waiting op launched on it
+    hipStream_t stream() {
+        flush();
+        return s_;
+    }
+    // ops left waiting by a run that failed: never launched
+    void discard() { n_ = 0; }
+    void flush() {
+        if (n_ == 0) return;
+        int64_t most = 0;
+        for (int k = 0; k < n_; k++) most = std::max(most, b_.op[k].n);
+        k_driver_ops<<<dim3((unsigned) ((most + 255) / 256), (unsigned) n_), 256, 0, s_>>>(b_);
+        n_ = 0;
+        check_launch("driver ops");
+    }
 
   private:
+    void add(const DriverKOp & o, size_t bytes) {
+        const uintptr_t w0 = (uintptr_t) o.dst, w1 = w0 + bytes;
+        const uintptr_t r0 = (uintptr_t) o.src, r1 = o.src ? r0 + bytes : r0;
+        bool clash = n_ == kDriverBatch;
+        for (int k = 0; k < n_ && !clash; k++) {
+            const uintptr_t pw0 = wr_[k][0], pw1 = wr_[k][1], pr0 = rd_[k][0], pr1 = rd_[k][1];
+            clash = (w0 < pw1 && pw0 < w1) || (r0 < pw1 && pw0 < r1) || (w0 < pr1 && pr0 < w1);
+        }
+        if (clash) flush();
+        wr_[n_][0] = w0;
+        wr_[n_][1] = w1;
+        rd_[n_][0] = r0;
+        rd_[n_][1] = r1;
+        b_.op[n_++] = o;
+    }
     hipStream_t s_ = nullptr;
     void * pinned_ = nullptr;
+    DriverBatch b_{};
+    int n_ = 0;
+    uintptr_t wr_[kDriverBatch][2], rd_[kDriverBatch][2];  // byte ranges each waiting op writes / reads
 };
 
-// GPU time per stage: an event pair around each call, read after the run's final wait.
+// GPU time per stage: one event after each call (and one before a run's first), read after the
+// run's final wait. A call's time runs from the event before it (the previous call's, or the
+// run's first) to its own, so driver work between two calls counts with the call after it; one
+// event per call instead of a pair, and events without a system-scope release (the host reads
+// results only after the stream's final wait), since every event costs the stream a few us.
 class StageClock {
   public:
     ~StageClock() {
@@ -990,17 +1057,14 @@ class StageClock {
         marks_.clear();
         used_ = 0;
     }
-    // events before / after one call of stage `stage`
-    void mark(int stage, hipStream_t s, bool after) {
-        if (used_ == events_.size()) {
-            hipEvent_t e;
-            check_hip(hipEventCreate(&e), "hipEventCreate");
-            events_.push_back(e);
-        }
-        check_hip(hipEventRecord(events_[used_], s), "hipEventRecord");
-        if (!after) marks_.push_back({stage, used_, 0});
-        else marks_.back().stop = used_;
-        used_++;
+    // before a call: the run's first event, if this is its first call
+    void before(hipStream_t s) {
+        if (used_ == 0) record(s);
+    }
+    // after a call of stage `stage`
+    void after(int stage, hipStream_t s) {
+        marks_.push_back({stage, used_ - 1, used_});
+        record(s);
     }
     // ms of each call, accumulated into per-stage totals
     template <class F>
@@ -1013,6 +1077,15 @@ class StageClock {
     }
 
   private:
+    void record(hipStream_t s) {
+        if (used_ == events_.size()) {
+            hipEvent_t e;
+            check_hip(hipEventCreateWithFlags(&e, hipEventDisableSystemFence), "hipEventCreate");
+            events_.push_back(e);
+        }
+        check_hip(hipEventRecord(events_[used_], s), "hipEventRecord");
+        used_++;
+    }
     struct Mark {
         int stage;
         size_t start, stop;
@@ -1492,6 +1565,7 @@ struct ggml_compiler_model {
     // ------------------------------------------------------------------------------- running
 
     void run_call(CallGraph & c) {
+        ops.flush();  // the driver's waiting ops before the stage's graph
         if (c.stale) build_graph(c);
         const StageSpec & st = prog.stages[(size_t) c.stage];
         last.n_calls++;
@@ -1499,10 +1573,10 @@ struct ggml_compiler_model {
             run_nodes(c, st);
             return;
         }
-        clock.mark(c.stage, ops.stream(), false);
+        clock.before(ops.stream());
         if (graph_compute_async(backend, c.graph) != GGML_STATUS_SUCCESS)
             fail("stage '" + st.name + "' failed: " + last_error());
-        clock.mark(c.stage, ops.stream(), true);
+        clock.after(c.stage, ops.stream());
     }
 
     // Profiling: each node of the graph alone, waited for and timed.
@@ -1634,6 +1708,7 @@ struct ggml_compiler_model {
         apply_binding();
         for (auto & t : stage_totals) t = ggml_compiler_stats{};
         last = ggml_compiler_stats{};
+        ops.discard();
         clock.begin_run();
         const auto t0 = std::chrono::steady_clock::now();
         execute(*e);
