@@ -102,15 +102,24 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
     // is the rotation pair (i, i + D/2) of q head h (h < H) or k head h - H, then pairs of v rows;
     // EPI_SWIGLU takes separate gate and up weights (ranges 0, 1): group g is gate row g and up
     // row g, the pair the packed gate/up weight holds in group g.
+    // x / (D/2) for the rope epilogue's group indices: a shift for the power-of-two head sizes (a
+    // division by a value known only at run time is a chain of some 30 dependent instructions,
+    // which in front of a group's weight loads delays them).
+    const int hd = a.D >> 1;
+    const int hsh = hd > 0 && (hd & (hd - 1)) == 0 ? __builtin_ctz(hd) : -1;
+    auto div_hd = [&](int x) -> int {
+        if (hsh >= 0) return x >> hsh;
+        return x / hd;
+    };
     auto map_row = [&](int g, int r, int & local) -> int {
         if constexpr (EPI == EPI_SWIGLU) {
             local = min(__builtin_amdgcn_readfirstlane(g), a.r_end[0] - 1);
             return r;
         } else if constexpr (EPI == EPI_ROPE_KV) {
             g = __builtin_amdgcn_readfirstlane(g);
-            const int hd = a.D >> 1, nq = (a.H + a.Hkv) * hd;
+            const int nq = (a.H + a.Hkv) * hd;
             if (g < nq) {
-                const int h = g / hd, i = g - h * hd;
+                const int h = div_hd(g), i = g - h * hd;
                 const bool qh = h < a.H;
                 local = (qh ? h : h - a.H) * a.D + i + r * hd;
                 return qh ? 0 : 1;
@@ -287,7 +296,10 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
             __builtin_amdgcn_s_barrier();
             __builtin_amdgcn_sched_barrier(0);
         }
-        if constexpr (EPI == EPI_ROPE_KV) cs_first = a.rope_cs[min(g, nqk - 1) % half];
+        if constexpr (EPI == EPI_ROPE_KV) {
+            const int gq = min(g, nqk - 1);
+            cs_first = a.rope_cs[gq - div_hd(gq) * half];
+        }
         load(g, w, d);
     } else {
         float2 mlv[kMergeMax];
@@ -305,7 +317,10 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
                 mlv[j] = make_float2(-INFINITY, 0.0f);  // splits past the last: none
             }
         }
-        if constexpr (EPI == EPI_ROPE_KV) cs_first = a.rope_cs[min(g, nqk - 1) % half];
+        if constexpr (EPI == EPI_ROPE_KV) {
+            const int gq = min(g, nqk - 1);
+            cs_first = a.rope_cs[gq - div_hd(gq) * half];
+        }
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_barrier();  // the partials' loads are issued before any weight load
         __builtin_amdgcn_sched_barrier(0);
@@ -420,7 +435,7 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
         } else {  // EPI_ROPE_KV
             if (lane == 0 && p_tok >= 0 && p_tok < a.ctx) {
                 if (gg < nqk) {
-                    const int h = gg / half, i = gg % half;
+                    const int h = div_hd(gg), i = gg - h * half;
                     const float2 cs = gg == g_first ? cs_first : a.rope_cs[i];
                     const float y0 = v[0] * cs.x - v[1] * cs.y, y1 = v[0] * cs.y + v[1] * cs.x;
                     if (h < a.H) {
@@ -433,7 +448,7 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
                     }
                 } else {
                     const int e = 2 * (gg - nqk);  // v value index over [Hkv][D]
-                    const int hv = e / a.D, dd = e % a.D;
+                    const int hv = div_hd(e) >> 1, dd = e - hv * a.D;
                     const uint32_t pair = f2h(v[0]) | ((uint32_t) f2h(v[1]) << 16);
                     *reinterpret_cast<uint32_t *>(a.vc + ((int64_t) hv * a.ctx + p_tok) * a.D + dd) = pair;
                 }

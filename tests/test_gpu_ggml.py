@@ -594,6 +594,74 @@ def test_cont_cast_scale_binary_argmax(be, orc):
     assert orc.parity(got["glu"], orc.swiglu(a, a * 0.5 + 2.0).reshape(-1)) < 1e-6
 
 
+def _argmax_rows(x):
+    """ggml-cpu's forward_argmax per row: the first index of the maximum, NaN never winning, 0 for
+    a row with no value above -inf."""
+    v = np.where(np.isnan(x), -np.inf, x)
+    return np.where(np.isneginf(v).all(axis=1), 0, np.argmax(v, axis=1)).astype(np.int32)
+
+
+@pytest.mark.parametrize("rows,n", [(1, 128256), (3, 8192), (2, 50001), (65, 8192), (4, 1000)])
+def test_argmax_long_rows(be, rows, n):
+    """Up to 64 rows of 8192 values or more take the sliced argmax (each workgroup a 2048-value
+    slice, the last of a row's to finish picks among their results); others the one-workgroup
+    kernel. Ties at the maximum (lower index wins, across slices), NaN, a row of -inf; the graph
+    replayed three times (the sliced kernel's row counters must be left at zero)."""
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((rows, n)).astype(np.float32)
+    x[0, sorted({n // 3, n - 1, min(2049, n - 2)})] = 50.0  # ties (in different slices for long rows)
+    x[0, 5] = np.nan
+    x[-1, :] = -np.inf
+    x[-1, 3] = np.nan
+    if rows > 2:
+        x[1, ::7] = np.nan
+        x[1, 2047:2049] = 60.0  # a tie across a slice boundary
+    want = _argmax_rows(x)
+
+    def build(g, ctx, L):
+        return g.ggml_argmax(ctx, L["x"])
+
+    gr = Graph(be, {"x": (G.F32, [n, rows], x)}, build)
+    for _ in range(3):
+        got = gr.run()
+        assert np.array_equal(got, want), (got[:8], want[:8])
+    gr.close()
+
+
+@pytest.mark.parametrize("kind", ["mul_mat", "argmax"])
+def test_result_copied_into_its_own_tensor(be, orc, kind):
+    """cpy(result, y) into a tensor y that no other node reads or writes (a program stage's result
+    reaching its value): the producing launch writes y itself and the copy is dropped. y equals the
+    graph where the result is also kept as an output (so it is written and copied) bit for bit,
+    and the oracle."""
+    N, K = 2048, 4096
+    w = _weight(orc, "q4_0", N, K, 160)
+    x = orc.normal((1, K), seed=161)
+    res = {}
+
+    def build(g, ctx, L):
+        m = g.ggml_mul_mat(ctx, L["w"], L["x"])
+        res["m"] = g.ggml_argmax(ctx, m) if kind == "argmax" else m
+        return g.ggml_cpy(ctx, res["m"], L["y"])
+
+    ytype = G.I32 if kind == "argmax" else G.F32
+    leaves = {"w": (orc.TYPES["q4_0"], [K, N], w), "x": (G.F32, [K, 1], x),
+              "y": (ytype, [1] if kind == "argmax" else [N, 1], None)}
+    got = {}
+    for name, outs in (("folded", ()), ("copied", [lambda s: res["m"]])):
+        gr = Graph(be, leaves, build, outputs=outs)
+        gr.run()
+        gr.run()
+        got[name] = G.get_data(gr.L["y"], NP[G.T(gr.L["y"]).type])
+        gr.close()
+    assert np.array_equal(got["folded"], got["copied"])
+    ref = orc.mul_mat(w, "q4_0", x, K).reshape(-1)
+    if kind == "argmax":  # the oracle's value at the chosen index is its maximum, to the tolerance
+        assert abs(ref[got["folded"][0]] - ref.max()) <= TOL * np.abs(ref).max()
+    else:
+        assert orc.parity(got["folded"], ref) < TOL
+
+
 UNARY_REF = {  # torch's fp32 functions on the CPU (softplus: ggml's threshold of 20)
     "relu": torch.relu, "gelu": lambda x: torch.nn.functional.gelu(x, approximate="tanh"),
     "gelu_erf": torch.nn.functional.gelu, "silu": torch.nn.functional.silu, "tanh": torch.tanh,
