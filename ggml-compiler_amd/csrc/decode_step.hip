@@ -44,6 +44,7 @@
 // so a barrier that cannot complete ends the kernel instead of hanging it; the counters return to
 // zero at the end of each launch (the last workgroup to leave clears them).
 #include "gcq_common.h"
+#include "grid_sync.h"
 
 #include <algorithm>
 
@@ -56,23 +57,8 @@ namespace {
 constexpr int kThreads = 1024, kWaves = 16;
 constexpr int kMaxK = 16384;       // LDS holds one activation row: K codes + K/32 (d, sum)
 constexpr int kMaxSplit = 8;       // attention splits the O prologue merges
-constexpr unsigned kSpinLimit = 1u << 22;  // barrier polls before giving up (about a second)
 constexpr uint32_t kPast = 0x80000000u;    // a buffer offset past every buffer: reads zeros
 constexpr int kCohere = 16;                // buffer cache policy: sc1 (device-coherent)
-
-// Barrier words (unsigned, 64 apart = one 256-byte line each): [64 (1 + g)] arrivals of group g,
-// [64 * 9] groups arrived, [64 (10 + g)] flag of group g, [64 * 18] workgroups done.
-constexpr int kBarWords = 64 * 19;
-
-__device__ __forceinline__ unsigned ld_co(const unsigned * p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_co(unsigned * p, unsigned v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ unsigned add_co(unsigned * p, unsigned v) {
-    return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 // Workgroup barrier for LDS data only: waits for this wavefront's LDS operations, not for its
 // global loads (a __syncthreads may wait for every outstanding load, prefetched weights included).
@@ -83,43 +69,6 @@ __device__ __forceinline__ void wg_sync() {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-// Barrier number k (1, 2, ... within a launch), in two halves (arrive, wait). Every thread calls
-// both; lane 0 of the sync wavefront (the last) arrives and polls.
-constexpr int kSync = kWaves - 1;
-__device__ __forceinline__ void bar_arrive(unsigned * bar, unsigned k, unsigned long long * stamp_at) {
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0);  // this wavefront's stores are complete
-    __builtin_amdgcn_s_barrier();   // ... and every wavefront's
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    if (threadIdx.x == kSync * 64) {
-        if (stamp_at) *stamp_at = __builtin_amdgcn_s_memrealtime();
-        const unsigned n = gridDim.x, grp = blockIdx.x & 7u;
-        const unsigned in_grp = (n - grp + 7u) / 8u;  // workgroups b with b % 8 == grp
-        if (add_co(&bar[64 * (1 + grp)], 1u) == k * in_grp - 1u) {
-            const unsigned groups = n < 8u ? n : 8u;
-            if (add_co(&bar[64 * 9], 1u) == k * groups - 1u)
-                for (unsigned g = 0; g < groups; g++) st_co(&bar[64 * (10 + g)], k);
-        }
-    }
-}
-__device__ __forceinline__ void bar_wait(unsigned * bar, unsigned * err, unsigned k) {
-    if (threadIdx.x == kSync * 64) {
-        const unsigned grp = blockIdx.x & 7u;
-        unsigned spins = 0;
-        while (ld_co(&bar[64 * (10 + grp)]) < k) {
-            __builtin_amdgcn_s_sleep(1);
-            if (++spins > kSpinLimit || ld_co(err) != 0u) {
-                st_co(err, 1u);
-                break;
-            }
-        }
-    }
-    // The other wavefronts pass once thread 0 has seen the flag; their reads of the phase's data
-    // are device-coherent loads issued after that.
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_barrier();
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void * p, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, (int) bytes, 0x00020000);
@@ -147,31 +96,6 @@ __device__ __forceinline__ void st_u32_co(__amdgpu_buffer_rsrc_t r, uint32_t off
 }
 __device__ __forceinline__ void st_u16_co(__amdgpu_buffer_rsrc_t r, uint32_t off, uint16_t v) {
     __builtin_amdgcn_raw_buffer_store_b16(v, r, off, 0, kCohere);
-}
-
-__device__ __forceinline__ int dot_q4_0(const uint4 w, const int4 xa, const int4 xb, int xsum) {
-    int s = 0;
-    s = sdot4((int) (w.x & 0x0F0F0F0Fu), xa.x, s);
-    s = sdot4((int) (w.y & 0x0F0F0F0Fu), xa.y, s);
-    s = sdot4((int) (w.z & 0x0F0F0F0Fu), xa.z, s);
-    s = sdot4((int) (w.w & 0x0F0F0F0Fu), xa.w, s);
-    s = sdot4((int) ((w.x >> 4) & 0x0F0F0F0Fu), xb.x, s);
-    s = sdot4((int) ((w.y >> 4) & 0x0F0F0F0Fu), xb.y, s);
-    s = sdot4((int) ((w.z >> 4) & 0x0F0F0F0Fu), xb.z, s);
-    s = sdot4((int) ((w.w >> 4) & 0x0F0F0F0Fu), xb.w, s);
-    return s - 8 * xsum;
-}
-__device__ __forceinline__ int dot_q8_0(const uint4 wa, const uint4 wb, const int4 xa, const int4 xb) {
-    int s = 0;
-    s = sdot4((int) wa.x, xa.x, s);
-    s = sdot4((int) wa.y, xa.y, s);
-    s = sdot4((int) wa.z, xa.z, s);
-    s = sdot4((int) wa.w, xa.w, s);
-    s = sdot4((int) wb.x, xb.x, s);
-    s = sdot4((int) wb.y, xb.y, s);
-    s = sdot4((int) wb.z, xb.z, s);
-    s = sdot4((int) wb.w, xb.w, s);
-    return s;
 }
 
 // ------------------------------------------------------------------- weight stream
@@ -254,8 +178,8 @@ __device__ __forceinline__ void dot_step(const WSrc & s, int g, int c, const WSt
 #pragma unroll
         for (int r = 0; r < R; r++) {
             int sdot;
-            if constexpr (TYPE == T_Q4_0) sdot = dot_q4_0(b.w[i][r][0], ca, cb, __float_as_int(cm.y));
-            else sdot = dot_q8_0(b.w[i][r][0], b.w[i][r][CV - 1], ca, cb);
+            if constexpr (TYPE == T_Q4_0) sdot = dot_blk_q4_0(b.w[i][r][0], ca, cb, __float_as_int(cm.y));
+            else sdot = dot_blk_q8_0(b.w[i][r][0], b.w[i][r][CV - 1], ca, cb);
             const int row = min(g * R + r, s.N - 1);
             const uint32_t sh = (uint32_t) (((lane ^ (row & s.nb)) & 1) << 4);
             acc[r] += ((float) sdot * h2f((uint16_t) (b.d[i][r] >> sh))) * cm.x;
@@ -813,9 +737,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_decode_step(const StepArgs a) {
     stamp(n_ev - 1);
     // The last workgroup to leave clears the barrier words for the next launch (every other
     // workgroup has passed its last wait).
-    if (threadIdx.x == 0 && add_co(&a.bar[64 * 18], 1u) == gridDim.x - 1u) {
-        for (int i = 0; i < kBarWords; i += 64) st_co(&a.bar[i], 0u);
-    }
+    bar_leave(a.bar);
 }
 
 }  // namespace

@@ -20,6 +20,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <type_traits>
 
 #include <cstddef>
 #include <cstdint>
@@ -142,6 +143,32 @@ struct RowArgs {
 };
 
 void launch_row_gemv(int type, int pro, int epi, const RowArgs & a, hipStream_t s);
+
+// Arguments of one decode layer's attention + output projection in a single launch
+// (attn_oproj.hip): the lane-group attention of the query row q over the layer's f16 caches, its
+// split partials in part_o / part_ml, a grid barrier, then x += W_o attn.
+struct AttnOArgs {
+    const float * q;            // [H][D] roped query row
+    const uint16_t * kc;        // [Hkv][kv_rows][D] f16 K cache of the layer
+    const uint16_t * vc;        // the same for V
+    int64_t kv_h;               // elements from one KV head to the next (kv_rows D)
+    int kv_rows;
+    const int * n_kv_dev;       // visible keys (device)
+    float scale;
+    int nsplit, chunk, H, Hkv;  // the lane-group split plan
+    float * part_o;             // [H][nsplit][D]
+    float2 * part_ml;           // [H][nsplit]
+    const uint8_t * wqs;        // packed Q4_0 / Q8_0 output weight: N rows of nb blocks
+    const uint16_t * wd;
+    int N, nb;
+    float * x;                  // the residual row: x += W_o attn
+    unsigned * bar;             // attn_oproj_bar_bytes() of zeros (they are zero again after a launch)
+    unsigned * err;             // set to nonzero when a barrier wait gave up (results invalid)
+    int xcd;                    // set by the launcher: XCD-grouped task order
+};
+void launch_attn_oproj(int type, int D, const AttnOArgs & a, hipStream_t s);
+bool attn_oproj_fits(int type, int H, int Hkv, int D, int nsplit);
+size_t attn_oproj_bar_bytes();
 // Byte offsets and spans of up to 3 packed weights (qs[k], d[k], N[k] rows of K) for RowArgs'
 // ranges; false when they span 2 GB or more.
 bool row_gemv_ranges(int type, int n, const uint8_t * const * w, const int64_t * N, int64_t K, RowArgs & a);
@@ -310,6 +337,35 @@ __device__ __forceinline__ uint16_t f2h_exact(float f) {
 
 __device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
+// int32 dot of one Q4_0 weight block (16 nibble bytes, stored code = q + 8) with a Q8_0 activation
+// block (codes xa: elements 0-15, xb: 16-31; xsum = their code sum): sum (q - 8) x.
+__device__ __forceinline__ int dot_blk_q4_0(const uint4 w, const int4 xa, const int4 xb, int xsum) {
+    int s = 0;
+    s = sdot4((int) (w.x & 0x0F0F0F0Fu), xa.x, s);
+    s = sdot4((int) (w.y & 0x0F0F0F0Fu), xa.y, s);
+    s = sdot4((int) (w.z & 0x0F0F0F0Fu), xa.z, s);
+    s = sdot4((int) (w.w & 0x0F0F0F0Fu), xa.w, s);
+    s = sdot4((int) ((w.x >> 4) & 0x0F0F0F0Fu), xb.x, s);
+    s = sdot4((int) ((w.y >> 4) & 0x0F0F0F0Fu), xb.y, s);
+    s = sdot4((int) ((w.z >> 4) & 0x0F0F0F0Fu), xb.z, s);
+    s = sdot4((int) ((w.w >> 4) & 0x0F0F0F0Fu), xb.w, s);
+    return s - 8 * xsum;
+}
+
+// int32 dot of one Q8_0 weight block (codes wa: elements 0-15, wb: 16-31) with a Q8_0 activation block.
+__device__ __forceinline__ int dot_blk_q8_0(const uint4 wa, const uint4 wb, const int4 xa, const int4 xb) {
+    int s = 0;
+    s = sdot4((int) wa.x, xa.x, s);
+    s = sdot4((int) wa.y, xa.y, s);
+    s = sdot4((int) wa.z, xa.z, s);
+    s = sdot4((int) wa.w, xa.w, s);
+    s = sdot4((int) wb.x, xb.x, s);
+    s = sdot4((int) wb.y, xb.y, s);
+    s = sdot4((int) wb.z, xb.z, s);
+    s = sdot4((int) wb.w, xb.w, s);
+    return s;
+}
+
 // Counters in LDS through which the wavefronts of one workgroup hand LDS data to each other
 // without a workgroup barrier (a barrier would also wait for wavefronts stalled on issuing memory
 // loads). A wavefront's LDS operations complete in order, so the writer waits for its LDS writes
@@ -387,6 +443,53 @@ __device__ __forceinline__ float row_pair(float v, F f) {
         const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
         return f(__uint_as_float(r[0]), __uint_as_float(r[1]));
     }
+}
+
+// Sums of V values (V = 1..64, a power of two) over the wavefront's 64 lanes, scattered: at each
+// of the six pair levels (lane ^ 32, ^ 16 with gfx950's row swaps, ^ 8 by a row rotate, the 8-lane
+// mirror, ^ 2, ^ 1) a lane keeps the half of its values that its lane bit selects and adds its
+// partner's copy of that half, until one value is left; later levels add it up plainly. Afterwards
+// v[0] of lane l is the total of value l >> (6 - log2 V) (every total on 64 / V lanes). About two
+// VALU operations per value, against some ten for a separate butterfly per value.
+template <int V>
+__device__ __forceinline__ void wave_reduce_scatter(float (&v)[V]) {
+    static_assert(V >= 1 && V <= 64 && (V & (V - 1)) == 0, "a power of two up to 64 values");
+    const int lane = threadIdx.x & 63;
+    auto lvl_swap = [&](auto X, auto n_c) {
+        constexpr int n = decltype(n_c)::value;
+        if constexpr (n > 1) {
+#pragma unroll
+            for (int j = 0; j < n / 2; j++) {
+                const unsigned a = __float_as_uint(v[j]), b = __float_as_uint(v[j + n / 2]);
+                const auto r = decltype(X)::value == 32 ? __builtin_amdgcn_permlane32_swap(a, b, false, false)
+                                                        : __builtin_amdgcn_permlane16_swap(a, b, false, false);
+                v[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+            }
+        } else {
+            v[0] = row_pair<decltype(X)::value>(v[0], [](float a, float b) { return a + b; });
+        }
+    };
+    auto lvl_dpp = [&](auto O, auto n_c) {
+        constexpr int n = decltype(n_c)::value, o = decltype(O)::value;
+        auto partner = [](float x) { return o == 8 ? lane_xor8(x) : lane_pair<o>(x); };
+        if constexpr (n > 1) {
+            const bool hi = (lane & o) != 0;
+#pragma unroll
+            for (int j = 0; j < n / 2; j++) {
+                const float keep = hi ? v[j + n / 2] : v[j], send = hi ? v[j] : v[j + n / 2];
+                v[j] = keep + partner(send);
+            }
+        } else {
+            v[0] = v[0] + partner(v[0]);
+        }
+    };
+    using I = int;
+    lvl_swap(std::integral_constant<I, 32>{}, std::integral_constant<I, V>{});
+    lvl_swap(std::integral_constant<I, 16>{}, std::integral_constant<I, (V > 1 ? V / 2 : 1)>{});
+    lvl_dpp(std::integral_constant<I, 8>{}, std::integral_constant<I, (V > 4 ? V / 4 : 1)>{});
+    lvl_dpp(std::integral_constant<I, 4>{}, std::integral_constant<I, (V > 8 ? V / 8 : 1)>{});
+    lvl_dpp(std::integral_constant<I, 2>{}, std::integral_constant<I, (V > 16 ? V / 16 : 1)>{});
+    lvl_dpp(std::integral_constant<I, 1>{}, std::integral_constant<I, (V > 32 ? V / 32 : 1)>{});
 }
 
 __device__ __forceinline__ float readlane_f(float v, int l) {

@@ -293,6 +293,167 @@ __global__ __launch_bounds__(256) void k_gemv_p(const uint8_t * __restrict__ wqs
     }
 }
 
+// Batched rows (B = 2..8) on Q4_0 / Q8_0, any row length up to 512 blocks: K-sliced. A workgroup
+// of KW = ceil(nb / 64) wavefronts covers a whole row, wavefront w owning blocks 64 w + lane, and
+// every lane keeps the activation blocks of its block (all B rows: codes, d, and for Q4_0 -8 times
+// the code sum as the dot's starting value) in registers for the whole launch, so the activation
+// is read once per wavefront rather than once per weight row. The workgroup walks batches of R
+// weight rows (the next batch's weights loaded before the current one is reduced); per row a lane
+// forms its block's B products, the wavefront reduce-scatters them (wave_reduce_scatter: the B
+// sums land on lanes b * 64 / BP), and the KW slices' sums meet in LDS, added in slice order by the
+// first wavefront, which stores the batch. Rows past N read zeros and are not stored.
+template <int TYPE, int B, int R>
+__global__ __launch_bounds__(512) void k_gemv_ks(const uint8_t * __restrict__ wqs, const uint16_t * __restrict__ wd,
+                                                 const int8_t * __restrict__ xc, const float2 * __restrict__ xm,
+                                                 float * y, const float * res, int N, int nb, int ldy) {
+    constexpr int CV = TYPE == T_Q4_0 ? 1 : 2;  // 16-byte loads per block
+    constexpr int BP = B <= 1 ? 1 : B <= 2 ? 2 : B <= 4 ? 4 : 8;  // B padded to a power of two
+    constexpr int LG = BP == 1 ? 0 : BP == 2 ? 1 : BP == 4 ? 2 : 3;
+    static_assert(R * BP <= 64, "one stored value per lane of the first wavefront");
+    __shared__ float part[2][8][R][BP];  // [batch parity][slice][row][b]
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, KW = blockDim.x >> 6;
+    const int K = nb * QK;
+    const int blk = wave * 64 + lane;
+    const bool live = blk < nb;
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(wqs), 0, (int) ((size_t) N * nb * CV * 16), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t *>(wd), 0, (int) (((size_t) N * nb + 1) / 2 * 4), 0x00020000);
+
+    const int nbatch = (N + R - 1) / R;
+    const int G = gridDim.x;
+
+    // The activation first, then the first two batches' weights: the loads complete in issue
+    // order, so at every batch the wait is for the older batch only (with the activation last
+    // the first batch would wait for everything, and the compiler's wait at the loop head with
+    // it).
+    int4 xa[B], xb[B];
+    float xd[B];  // activation block scale
+    float xo[B];  // Q4_0: the -8 offset's term (-8 x code sum) x d, 0 for Q8_0
+    float2 xmv[B];
+#pragma unroll
+    for (int b = 0; b < B; b++) {
+        const int bb = live ? blk : 0;
+        const int4 * xp = reinterpret_cast<const int4 *>(xc + (size_t) b * K + (size_t) bb * QK);
+        xa[b] = xp[0];
+        xb[b] = xp[1];
+        xmv[b] = xm[(size_t) b * nb + bb];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // A row's block at o = row * nb + blk: codes at 16 CV o, its scale in the 32-bit word at
+    // (o / 2) * 4. Rows past N lie past the buffers' ends and read zeros; lanes past the row (blk
+    // >= nb) read the next row's block, finite values that their zero activation scale cancels.
+    uint4 w[R][CV], wn[R][CV];
+    uint32_t d[R], dn[R];
+    auto load = [&](int tb, uint4 (&wv)[R][CV], uint32_t (&dv)[R]) {
+        const uint32_t o0 = (uint32_t) tb * (uint32_t) R * (uint32_t) nb + (uint32_t) blk;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t o = o0 + (uint32_t) (r * nb);
+#pragma unroll
+            for (int c = 0; c < CV; c++) {
+                const auto q = __builtin_amdgcn_raw_buffer_load_b128(rq, (o * CV + c) * 16u, 0, 2);
+                wv[r][c] = make_uint4(q[0], q[1], q[2], q[3]);
+            }
+            dv[r] = __builtin_amdgcn_raw_buffer_load_b32(rd, (o >> 1) * 4u, 0, 0);
+        }
+    };
+    int t = blockIdx.x;
+    load(t, w, d);
+    __builtin_amdgcn_sched_barrier(0);
+    load(t + G, wn, dn);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int b = 0; b < B; b++) {
+        xd[b] = live ? xmv[b].x : 0.0f;
+        xo[b] = TYPE == T_Q4_0 ? (float) (-8 * __float_as_int(xmv[b].y)) * xd[b] : 0.0f;
+    }
+
+    // One batch: per row the lane's block products ((sum q x) d_x + offset term) d_w; the R * BP
+    // products reduce-scattered over the wavefront at once into the slice's LDS rows; then the
+    // first wavefront adds the KW slices in order and stores.
+    constexpr int V = R * BP, LV = LG + (R == 1 ? 0 : R == 2 ? 1 : R == 4 ? 2 : R == 8 ? 3 : 4);
+    static_assert(V <= 64 && (1 << LV) == V, "R and B padded: a power of two up to 64 products");
+    auto batch = [&](int tb, const uint4 (&wv)[R][CV], const uint32_t (&dv)[R], int par) {
+        float v[V];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            // scale index row * nb + blk: its parity picks the half (blk's parity is the lane's)
+            const int row = min(tb * R + r, N - 1);
+            const uint32_t sh = (uint32_t) (((lane ^ (row & nb)) & 1) << 4);
+            const float dw = h2f((uint16_t) (dv[r] >> sh));
+            int lo[4], hi[4];
+            if constexpr (TYPE == T_Q4_0) {
+                lo[0] = (int) (wv[r][0].x & 0x0F0F0F0Fu);
+                lo[1] = (int) (wv[r][0].y & 0x0F0F0F0Fu);
+                lo[2] = (int) (wv[r][0].z & 0x0F0F0F0Fu);
+                lo[3] = (int) (wv[r][0].w & 0x0F0F0F0Fu);
+                hi[0] = (int) ((wv[r][0].x >> 4) & 0x0F0F0F0Fu);
+                hi[1] = (int) ((wv[r][0].y >> 4) & 0x0F0F0F0Fu);
+                hi[2] = (int) ((wv[r][0].z >> 4) & 0x0F0F0F0Fu);
+                hi[3] = (int) ((wv[r][0].w >> 4) & 0x0F0F0F0Fu);
+            } else {
+                lo[0] = (int) wv[r][0].x;
+                lo[1] = (int) wv[r][0].y;
+                lo[2] = (int) wv[r][0].z;
+                lo[3] = (int) wv[r][0].w;
+                hi[0] = (int) wv[r][CV - 1].x;
+                hi[1] = (int) wv[r][CV - 1].y;
+                hi[2] = (int) wv[r][CV - 1].z;
+                hi[3] = (int) wv[r][CV - 1].w;
+            }
+#pragma unroll
+            for (int b = 0; b < BP; b++) {
+                if (b < B) {
+                    // clamp: the three-operand form with a zero start (no register set to zero first);
+                    // the sums never come near the int32 limits
+                    int sdot = __builtin_amdgcn_sdot4(lo[0], xa[b].x, 0, true);
+                    sdot = sdot4(lo[1], xa[b].y, sdot);
+                    sdot = sdot4(lo[2], xa[b].z, sdot);
+                    sdot = sdot4(lo[3], xa[b].w, sdot);
+                    sdot = sdot4(hi[0], xb[b].x, sdot);
+                    sdot = sdot4(hi[1], xb[b].y, sdot);
+                    sdot = sdot4(hi[2], xb[b].z, sdot);
+                    sdot = sdot4(hi[3], xb[b].w, sdot);
+                    v[r * BP + b] = __builtin_fmaf((float) sdot, xd[b], xo[b]) * dw;
+                } else {
+                    v[r * BP + b] = 0.0f;
+                }
+            }
+        }
+        wave_reduce_scatter<V>(v);
+        if ((lane & ((64 >> LV) - 1)) == 0) {
+            const int idx = lane >> (6 - LV);
+            part[par][wave][idx / BP][idx % BP] = v[0];
+        }
+        // LDS writes complete and every slice's written (the weight loads in flight are not waited for)
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        if (wave == 0 && lane < R * BP) {
+            const int r = lane / BP, b = lane % BP, row = tb * R + r;
+            float sum = part[par][0][r][b];
+            for (int k = 1; k < KW; k++) sum += part[par][k][r][b];
+            if (b < B && row < N) {
+                const size_t o = (size_t) b * ldy + row;
+                y[o] = res ? sum + res[o] : sum;
+            }
+        }
+    };
+    while (t < nbatch) {
+        batch(t, w, d, 0);
+        load(t + 2 * G, w, d);
+        t += G;
+        if (t >= nbatch) break;
+        batch(t, wn, dn, 1);
+        load(t + 2 * G, wn, dn);
+        t += G;
+    }
+}
+
 // ----------------------------------------------------------------------------- Q4_K kernel
 
 // Lane task = (super-block, 64-value chunk): 4 tasks per super-block, NBL tasks per lane per
@@ -690,9 +851,32 @@ void run_q0(const uint8_t * w, const WeightLayout & L, const int8_t * xc, const 
     k_gemv_q0<TYPE, B, kR, NBL><<<grid, 256, 0, s>>>(w + L.qs, (const uint16_t *) (w + L.d), xc, xm, y, res, N, nb, ldy);
 }
 
+// The K-sliced kernel (k_gemv_ks) for batches of 2..8 rows: ceil(nb / 64) wavefronts per
+// workgroup, as many workgroups as are resident at once (at most), each with the same number of
+// row batches.
+template <int TYPE, int B, int R>
+void run_ks(const uint8_t * w, const WeightLayout & L, const int8_t * xc, const float2 * xm, float * y,
+            const float * res, int N, int nb, int ldy, hipStream_t s) {
+    const int kw = (nb + 63) / 64;
+    static thread_local int occ[9] = {0};  // resident workgroups per CU, by wavefronts per workgroup
+    if (occ[kw] == 0) {
+        check_hip(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ[kw], reinterpret_cast<const void *>(&k_gemv_ks<TYPE, B, R>),
+                                                               kw * 64, 0),
+                  "gemv occupancy");
+        occ[kw] = std::max(occ[kw], 1);
+    }
+    const int nbatch = (N + R - 1) / R, maxg = cu_count() * occ[kw];
+    const int per = (nbatch + maxg - 1) / maxg;
+    const unsigned grid = (unsigned) ((nbatch + per - 1) / per);
+    k_gemv_ks<TYPE, B, R><<<grid, kw * 64, 0, s>>>(w + L.qs, (const uint16_t *) (w + L.d), xc, xm, y, res, N, nb, ldy);
+}
+
 template <int TYPE, int B>
 void run_q0_nbl(int nbl, const uint8_t * w, const WeightLayout & L, const int8_t * xc, const float2 * xm, float * y,
                 const float * res, int N, int nb, int ldy, hipStream_t s) {
+    if constexpr (B >= 2) {
+        if (nb <= 512) return run_ks<TYPE, B, (B <= 2 ? 8 : 4)>(w, L, xc, xm, y, res, N, nb, ldy, s);
+    }
     if constexpr (B <= 4) {  // rows of up to 128 blocks: the persistent kernel
         if (nbl == 1) return run_p<TYPE, B, 1>(w, L, xc, xm, y, res, N, nb, ldy, s);
         if (nbl == 2) return run_p<TYPE, B, 2>(w, L, xc, xm, y, res, N, nb, ldy, s);
@@ -756,32 +940,11 @@ void run_q4k_nbl(int nbl, const uint8_t * w, const int8_t * xc, const int16_t * 
 
 // y [B][ldy] (first N columns written) from packed weights and a quantized activation; with res,
 // y = res + W x (res has y's layout and may be y itself).
-bool gemv_mfma_fits(int type, int64_t K, int64_t B);
-void launch_gemv_mfma(int type, const uint8_t * wqs, const uint16_t * wd, const int8_t * xc, const float2 * xm,
-                      float * y, int N, int nb, int B, int ldy, hipStream_t s);
-
-// Batches of 2..16 rows on the int8 matrix cores (gemv_mfma.hip) with GCQ_GEMV_MFMA=1 (measured
-// slower than the row kernels so far: its loads touch 16 rows each and its per-block epilogue
-// waits on every matrix instruction).
-static bool use_gemv_mfma() {
-    static const bool on = [] {
-        const char * e = std::getenv("GCQ_GEMV_MFMA");
-        return e && std::string(e) == "1";
-    }();
-    return on;
-}
-
 void launch_gemv(int type, const void * wv, int64_t N, int64_t K, const void * act, int64_t B, float * y, int64_t ldy,
                  hipStream_t s, const float * res) {
     const uint8_t * w = (const uint8_t *) wv;
     const ActLayout A = act_layout(type, B, K);
     const uint8_t * a = (const uint8_t *) act;
-    if ((type == T_Q4_0 || type == T_Q8_0) && res == nullptr && gemv_mfma_fits(type, K, B) && use_gemv_mfma()) {
-        const WeightLayout L = weight_layout(type, N, K);
-        launch_gemv_mfma(type, w + L.qs, (const uint16_t *) (w + L.d), (const int8_t *) (a + A.codes),
-                         (const float2 *) (a + A.meta), y, (int) N, (int) (K / QK), (int) B, (int) ldy, s);
-        return;
-    }
     if (type == T_Q4_0 || type == T_Q8_0) {
         const WeightLayout L = weight_layout(type, N, K);
         const int nb = (int) (K / QK);

@@ -132,6 +132,10 @@ struct Llama {
     // raises when a barrier wait gave up.
     bool step_fits = false, step_on = false;
     DevBuf step_layers, step_bar, step_err, step_trace, step_trace_on;
+    // Decode path 2: each layer's attention and output projection in one launch (attn_oproj.hip),
+    // when the configuration fits it (ao_fits); ao_bar / ao_err: its barrier words and error word.
+    bool ao_fits = false, ao_on = false;
+    DevBuf ao_bar, ao_err;
     DevBuf step_x, step_q, step_h, step_po, step_pml;  // the persistent step's rings
     DevBuf ytmp;         // a prompt chunk's mul_mat result in packed row order
     int pos = 0;
@@ -276,6 +280,15 @@ struct Llama {
             check_hip(hipMemset(step_trace_on.p, 0, 4), "step trace");
             const char * e = std::getenv("GCQ_DECODE_STEP");
             step_on = e && std::string(e) == "1";
+        }
+        ao_fits = fused && decode_attn && decode_group(c.n_head / c.n_head_kv, c.max_ctx) == 1 &&
+                  attn_oproj_fits(c.wtype, c.n_head, c.n_head_kv, c.head_dim, plan_decode.nsplit);
+        if (ao_fits) {
+            ao_bar = DevBuf(attn_oproj_bar_bytes());
+            ao_err = DevBuf(4);
+            check_hip(hipMemset(ao_bar.p, 0, ao_bar.n), "attn + output projection barrier");
+            check_hip(hipMemset(ao_err.p, 0, ao_err.n), "attn + output projection error");
+            if (const char * e = std::getenv("GCQ_DECODE_PATH"); e && std::string(e) == "2" && !step_on) ao_on = true;
         }
         mask = DevBuf((size_t) max_prompt * c.max_ctx * 2);
         positions = DevBuf((size_t) max_prompt * 4);
@@ -466,6 +479,33 @@ struct Llama {
         a.D = c.head_dim;
         a.rope_cs = rope_cs.as<float2>();
         launch_row_gemv(c.wtype, PRO_NORM, EPI_ROPE_KV, a, stream);
+        if (ao_on && n_kv_dev) {  // attention and output projection in one launch
+            const RowArgs o = row_args(L.wo);
+            AttnOArgs ao{};
+            ao.q = qkv.as<float>();
+            ao.kc = kvl;
+            ao.vc = kvl + (size_t) c.n_head_kv * kv_h;
+            ao.kv_h = kv_h;
+            ao.kv_rows = c.max_ctx;
+            ao.n_kv_dev = n_kv_dev;
+            ao.scale = scale;
+            ao.nsplit = plan.nsplit;
+            ao.chunk = plan.chunk;
+            ao.H = c.n_head;
+            ao.Hkv = c.n_head_kv;
+            ao.part_o = part_o.as<float>();
+            ao.part_ml = part_ml.as<float2>();
+            ao.wqs = o.wqs;
+            ao.wd = o.wd;
+            ao.N = o.N;
+            ao.nb = o.nb;
+            ao.x = xs;
+            ao.bar = ao_bar.as<unsigned>();
+            ao.err = ao_err.as<unsigned>();
+            launch_attn_oproj(c.wtype, c.head_dim, ao, stream);
+            if (mid) check_hip(hipMemcpyAsync(mid, xs, (size_t) c.n_embd * 4, hipMemcpyDeviceToDevice, stream), "mid");
+            return ffn_decode(L, xs);
+        }
         if (decode_attn) {
             // Spare CUs read this layer's output projection and the next layer's QKV weights
             // into the Infinity Cache while the attention runs.
@@ -502,7 +542,13 @@ struct Llama {
             launch_row_gemv(c.wtype, PRO_MERGE, EPI_STORE, a, stream);
         }
         if (mid) check_hip(hipMemcpyAsync(mid, xs, (size_t) c.n_embd * 4, hipMemcpyDeviceToDevice, stream), "mid");
-        a = row_args(L.gate_up);
+        ffn_decode(L, xs);
+    }
+
+    // The feed-forward half of a decode layer on the residual row xs: rms_norm -> gate/up ->
+    // SwiGLU in one launch, then down + residual.
+    void ffn_decode(const Layer & L, float * xs) {
+        RowArgs a = row_args(L.gate_up);
         a.x = xs;
         a.norm_w = tensors[L.ffn_norm].buf.as<float>();
         a.eps = c.rms_eps;
@@ -651,6 +697,16 @@ struct Llama {
     // The persistent step raises step_err when a barrier wait gave up (a workgroup that never
     // arrived): the step's results are then invalid, and the layer-by-layer path takes over.
     void check_step() {
+        if (ao_on) {
+            unsigned e = 0;
+            check_hip(hipMemcpy(&e, ao_err.p, 4, hipMemcpyDeviceToHost), "attn + output projection error");
+            if (e == 0) return;
+            check_hip(hipMemset(ao_err.p, 0, 4), "attn + output projection error");
+            check_hip(hipMemset(ao_bar.p, 0, ao_bar.n), "attn + output projection barrier");
+            set_decode_path(0);
+            fail("decode path 2: a grid barrier wait gave up, the step's results are invalid; decoding continues on "
+                 "the layer-by-layer path");
+        }
         if (!step_on) return;
         unsigned e = 0;
         check_hip(hipMemcpy(&e, step_err.p, 4, hipMemcpyDeviceToHost), "step error");
@@ -682,11 +738,17 @@ struct Llama {
         return wgs;
     }
 
+    int decode_path() const { return step_on ? 1 : ao_on ? 2 : 0; }
+
     void set_decode_path(int path) {
-        require(path == 0 || path == 1, "decode path must be 0 (per-layer launches) or 1 (one persistent launch)");
-        require(path == 0 || step_fits, "decode path 1: this configuration does not fit the persistent step");
-        if ((path == 1) == step_on) return;
+        require(path >= 0 && path <= 2,
+                "decode path must be 0 (per-layer launches), 1 (one persistent launch) or 2 (attention and output "
+                "projection in one launch)");
+        require(path != 1 || step_fits, "decode path 1: this configuration does not fit the persistent step");
+        require(path != 2 || ao_fits, "decode path 2: this configuration does not fit the fused attention launch");
+        if (path == decode_path()) return;
         step_on = path == 1;
+        ao_on = path == 2;
         if (graph_exec) check_hip(hipGraphExecDestroy(graph_exec), "graph");
         if (graph) check_hip(hipGraphDestroy(graph), "graph");
         graph_exec = nullptr;
@@ -826,7 +888,7 @@ int gcq_llama_set_decode_path(gcq_llama * m, int path) {
     });
 }
 
-int gcq_llama_decode_path(const gcq_llama * m) { return m ? (m->step_on ? 1 : 0) : -1; }
+int gcq_llama_decode_path(const gcq_llama * m) { return m ? m->decode_path() : -1; }
 
 int gcq_llama_step_trace(gcq_llama * m, int32_t token, uint64_t * out, int64_t n) {
     int wgs = -1;

@@ -35,32 +35,6 @@ namespace gcq {
 constexpr int kRowMaxK = 16384;  // LDS holds the row's codes: K bytes + K/32 float2
 constexpr int kMergeMax = 8;     // split-K partials the merge prologue takes (held in registers)
 
-__device__ __forceinline__ int dot_blk_q4_0(const uint4 w, const int4 xa, const int4 xb, int xsum) {
-    int s = 0;
-    s = sdot4((int) (w.x & 0x0F0F0F0Fu), xa.x, s);
-    s = sdot4((int) (w.y & 0x0F0F0F0Fu), xa.y, s);
-    s = sdot4((int) (w.z & 0x0F0F0F0Fu), xa.z, s);
-    s = sdot4((int) (w.w & 0x0F0F0F0Fu), xa.w, s);
-    s = sdot4((int) ((w.x >> 4) & 0x0F0F0F0Fu), xb.x, s);
-    s = sdot4((int) ((w.y >> 4) & 0x0F0F0F0Fu), xb.y, s);
-    s = sdot4((int) ((w.z >> 4) & 0x0F0F0F0Fu), xb.z, s);
-    s = sdot4((int) ((w.w >> 4) & 0x0F0F0F0Fu), xb.w, s);
-    return s - 8 * xsum;
-}
-
-__device__ __forceinline__ int dot_blk_q8_0(const uint4 wa, const uint4 wb, const int4 xa, const int4 xb) {
-    int s = 0;
-    s = sdot4((int) wa.x, xa.x, s);
-    s = sdot4((int) wa.y, xa.y, s);
-    s = sdot4((int) wa.z, xa.z, s);
-    s = sdot4((int) wa.w, xa.w, s);
-    s = sdot4((int) wb.x, xb.x, s);
-    s = sdot4((int) wb.y, xb.y, s);
-    s = sdot4((int) wb.z, xb.z, s);
-    s = sdot4((int) wb.w, xb.w, s);
-    return s;
-}
-
 template <int TYPE, int R, int NBL, int PRO, int EPI, int MR>
 __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
     constexpr int NT = 1024, NWV = NT / 64;

@@ -218,11 +218,14 @@ GCQ_API int gcq_llama_generate(gcq_llama * m, int32_t first, int n_new, int32_t 
 /* How the decode step runs (gcq_llama_decode / gcq_llama_generate): 0 = five launches per layer
  * (row GEMVs with the graph nodes around each mul_mat fused in, split-K attention), the default;
  * 1 = all layers in one persistent launch, one workgroup per CU, grid barriers between a layer's
- * five phases (slower on MI355X: 570 against 736 tok/s for the 8B-shaped Q4_0 decoder). Both
- * compute the same operations in the same order: the logits are equal bit for bit. Path 1 needs
- * Q4_0 / Q8_0, head_dim 64 / 128, n_embd <= 8192, n_ff <= 16384, an attention row of at most
- * 4096 and max_ctx <= 2048; set returns -1 when it does not fit. The environment variable
- * GCQ_DECODE_STEP=1 makes it the initial path. No counterpart in the reference, whose decode is
+ * five phases (slower on MI355X: 570 against 736 tok/s for the 8B-shaped Q4_0 decoder);
+ * 2 = as 0, but each layer's attention and output projection in one launch (one workgroup per CU,
+ * the output weight loaded while the attention runs, one grid barrier). All paths compute the
+ * same operations in the same order: the logits are equal bit for bit. Paths 1 and 2 need
+ * Q4_0 / Q8_0, head_dim 64 / 128, an attention row of at most 4096 and max_ctx <= 2048 (path 1
+ * also n_embd <= 8192, n_ff <= 16384; path 2 at most one split-head task per CU); set returns -1
+ * when it does not fit. The environment variable GCQ_DECODE_STEP=1 makes path 1 the initial path,
+ * GCQ_DECODE_PATH=2 path 2. No counterpart in the reference, whose decode is
  * one ggml graph per token (runtime/src/ggml_compiler_rt.cpp:356-441). */
 GCQ_API int gcq_llama_set_decode_path(gcq_llama * m, int path);
 GCQ_API int gcq_llama_decode_path(const gcq_llama * m);

@@ -1,8 +1,10 @@
-"""The decode step in one persistent launch (decode_step.hip) against the five-launches-per-layer
-decode (decode path 0): the same operations in the same order, so every logit is equal bit for bit.
+"""The decode step in one persistent launch (decode_step.hip, decode path 1) and with each layer's
+attention and output projection in one launch (attn_oproj.hip, path 2) against the
+five-launches-per-layer decode (decode path 0): the same operations in the same order, so every
+logit is equal bit for bit.
 
 Path 0 is the one compared with the oracle op by op and layer by layer (test_gpu_llm.py); equality
-with it carries those checks over to path 1. A missed barrier or a stale read between workgroups
+with it carries those checks over to paths 1 and 2. A missed barrier or a stale read between workgroups
 (the hazards of a persistent kernel) would change values by far less than a tolerance could be
 trusted to catch, which is why the comparison is exact.
 """
@@ -51,21 +53,23 @@ def test_decode_paths_equal(gops, orc, name):
     print(f"decode paths: {name} {cfg}", flush=True)
     m = Model(cfg, max_prompt=min(512, cfg.max_ctx))
     m.init_random(seed=3)
-    m.decode_path = 1  # fits every case above
+    m.decode_path = 1  # paths 1 and 2 fit every case above
+    m.decode_path = 2
     prompt = orc.ids(n_prompt, seed=4, vocab=cfg.n_vocab).tolist()
     feed = orc.ids(n_feed, seed=5, vocab=cfg.n_vocab)
     r0, n0, g0 = _run(m, 0, prompt, feed, n_gen)
-    r1, n1, g1 = _run(m, 1, prompt, feed, n_gen)
     assert np.isfinite(r0).all()
-    assert np.array_equal(r0, r1), (name, float(np.abs(r0 - r1).max()))
-    assert n0 == n1
-    assert g0 == g1
+    for path in (1, 2):
+        r1, n1, g1 = _run(m, path, prompt, feed, n_gen)
+        assert np.array_equal(r0, r1), (name, path, float(np.abs(r0 - r1).max()))
+        assert n0 == n1
+        assert g0 == g1
     m.close()
 
 
 def test_decode_step_8b_shape(gops, orc):
     """The 32-layer 8B-shaped Q4_0 decoder of the decode benchmark (max_ctx 640) after a 512-token
-    prompt: four fed tokens and 32 generated, both paths."""
+    prompt: four fed tokens and 32 generated, every path."""
     from ggml_compiler_amd.llm import LlamaConfig, Model
 
     cfg = LlamaConfig(n_layer=32, n_embd=4096, n_head=32, n_head_kv=8, head_dim=128, n_ff=14336, n_vocab=128256,
@@ -76,14 +80,15 @@ def test_decode_step_8b_shape(gops, orc):
     prompt = orc.ids(512, seed=5, vocab=cfg.n_vocab).tolist()
     feed = orc.ids(4, seed=6, vocab=cfg.n_vocab)
     r0, n0, g0 = _run(m, 0, prompt, feed, 32)
-    r1, n1, g1 = _run(m, 1, prompt, feed, 32)
-    assert np.array_equal(r0, r1), float(np.abs(r0 - r1).max())
-    assert n0 == n1 and g0 == g1
+    for path in (1, 2):
+        r1, n1, g1 = _run(m, path, prompt, feed, 32)
+        assert np.array_equal(r0, r1), (path, float(np.abs(r0 - r1).max()))
+        assert n0 == n1 and g0 == g1
     m.close()
 
 
 def test_decode_path_switch_errors(gops):
-    """Path 1 is refused where the configuration does not fit it (max_ctx past 2048 keys)."""
+    """Paths 1 and 2 are refused where the configuration does not fit them (max_ctx past 2048 keys)."""
     from ggml_compiler_amd._lib import GcqError
     from ggml_compiler_amd.llm import Model
 
@@ -91,6 +96,8 @@ def test_decode_path_switch_errors(gops):
     assert m.decode_path == 0
     with pytest.raises(GcqError, match="does not fit"):
         m.decode_path = 1
-    with pytest.raises(GcqError, match="decode path must be"):
+    with pytest.raises(GcqError, match="does not fit"):
         m.decode_path = 2
+    with pytest.raises(GcqError, match="decode path must be"):
+        m.decode_path = 3
     m.close()

@@ -141,11 +141,14 @@ def test_gemv_c1_q8_0_4096(gops, orc):
 
 
 @pytest.mark.parametrize("t", ["q4_0", "q8_0"])
-@pytest.mark.parametrize("B", [2, 5, 16])
-def test_gemv_mfma_batches(gops, orc, t, B):
-    """The matrix-core GEMV (2..16 rows): a row count that is not a multiple of its 16-row tile,
-    a residual, and K of 64 blocks (16 wavefronts, one block pair each)."""
-    N, K = 1000, 2048
+@pytest.mark.parametrize("B", [2, 3, 5, 8, 16])
+@pytest.mark.parametrize("K", [2048, 3104, 14336])
+def test_gemv_batches_residual(gops, orc, t, B, K):
+    """Batches of 2..8 rows (the K-sliced kernel: one wavefront per 64 blocks of K, the
+    activation in registers, R-row batches) and 16 (the GEMM): a row count that is not a multiple
+    of the row batch, a residual, K of one wavefront (2048), of a partly filled second one (3104 =
+    97 blocks: lanes past the row) and of seven (14336), B padded to a power of two (3, 5)."""
+    N = 1000
     raw, qw = _weight(gops, orc, t, N, K, 44)
     x = orc.normal((B, K), seed=45)
     r = orc.normal((B, N), seed=46)
