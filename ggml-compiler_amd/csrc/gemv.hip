@@ -293,133 +293,223 @@ __global__ __launch_bounds__(256) void k_gemv_p(const uint8_t * __restrict__ wqs
     }
 }
 
-// Batched rows (B = 2..8) on Q4_0 / Q8_0, any row length up to 512 blocks: K-sliced. A workgroup
-// of KW = ceil(nb / 64) wavefronts covers a whole row, wavefront w owning blocks 64 w + lane, and
-// every lane keeps the activation blocks of its block (all B rows: codes, d, and for Q4_0 -8 times
-// the code sum as the dot's starting value) in registers for the whole launch, so the activation
-// is read once per wavefront rather than once per weight row. The workgroup walks batches of R
-// weight rows (the next batch's weights loaded before the current one is reduced); per row a lane
-// forms its block's B products, the wavefront reduce-scatters them (wave_reduce_scatter: the B
-// sums land on lanes b * 64 / BP), and the KW slices' sums meet in LDS, added in slice order by the
-// first wavefront, which stores the batch. Rows past N read zeros and are not stored.
+// Batched rows (B = 2..8), K-sliced, for Q4_0 / Q8_0 / Q4_K / Q5_K weights. A lane's task is 32
+// values of every weight row: a Q4_0 / Q8_0 block, or for the K-quants a half chunk of a 256-value
+// super-block (16 bytes of nibbles: values 16 h .. 16 h + 15 of the chunk's two 32-value
+// sub-blocks 2c and 2c + 1). A workgroup of KW = ceil(tasks / 64) wavefronts covers a whole row,
+// wavefront w owning tasks 64 w + lane, and every lane keeps its task's activation (all B rows:
+// codes and scales, and the terms that do not depend on the weight row) in registers for the whole
+// launch, so the activation is read once per wavefront rather than once per weight row. The
+// workgroup walks batches of R weight rows, the next two batches' weights in flight; per row a
+// lane forms its task's B products (the int32 dot sums exact, as ggml's, then fp32 scaling), the
+// wavefront reduce-scatters the batch's R x B products (wave_reduce_scatter), and the KW slices'
+// sums meet in LDS, added in slice order by the first wavefront, which stores the batch. Rows
+// past N read zeros (past the buffer's end) and are not stored; lanes past the row read the next
+// row's weights, which their zero activation scale cancels.
+//
+// Per task and batch row b (x: Q8_0 / Q8_K codes of the task's values, d_x their scale):
+//   Q4_0: ((sum q x) d_x - 8 (sum x) d_x) d_w (q the stored 0..15 code);  Q8_0: (sum q x) d_x d_w
+//   Q4_K / Q5_K: (sc0 s0 + sc1 s1) d d_x - dmin (m0 bs0 + m1 bs1) d_x, s0 / s1 the task's two
+//     16-value dots with sub-blocks 2c / 2c + 1 and bs0 / bs1 the matching Q8_K bsums.
+template <int TYPE>
+struct KsFmt {
+    static constexpr bool KQ = TYPE == T_Q4_K || TYPE == T_Q5_K;
+    static constexpr int WV = TYPE == T_Q8_0 ? 2 : TYPE == T_Q5_K ? 3 : KQ ? 2 : 1;  // 16-byte loads per row
+    static constexpr uint32_t SB = TYPE == T_Q5_K ? 176u : 144u;                   // K-quant super-block bytes
+};
+
+struct KsArgs {
+    const uint8_t * w;      // Q4_0 / Q8_0: packed codes; K-quants: ggml's super-blocks
+    const uint16_t * wd;    // Q4_0 / Q8_0: packed fp16 scales
+    const int8_t * xc;      // activation codes [B][K]
+    const float2 * xm;      // Q8_0 activation: (d, code sum) [B][K / 32]
+    const int16_t * xbs;    // Q8_K activation: bsums [B][K / 16]
+    const float * xd;       // Q8_K activation: d [B][K / 256]
+    float * y;
+    const float * res;
+    int N, ntask, ldy;      // ntask: tasks per row (K / 32)
+};
+
 template <int TYPE, int B, int R>
-__global__ __launch_bounds__(512) void k_gemv_ks(const uint8_t * __restrict__ wqs, const uint16_t * __restrict__ wd,
-                                                 const int8_t * __restrict__ xc, const float2 * __restrict__ xm,
-                                                 float * y, const float * res, int N, int nb, int ldy) {
-    constexpr int CV = TYPE == T_Q4_0 ? 1 : 2;  // 16-byte loads per block
+__global__ __launch_bounds__(512) void k_gemv_ks(const KsArgs a) {
+    using F = KsFmt<TYPE>;
+    constexpr int WV = F::WV;
     constexpr int BP = B <= 1 ? 1 : B <= 2 ? 2 : B <= 4 ? 4 : 8;  // B padded to a power of two
     constexpr int LG = BP == 1 ? 0 : BP == 2 ? 1 : BP == 4 ? 2 : 3;
-    static_assert(R * BP <= 64, "one stored value per lane of the first wavefront");
     __shared__ float part[2][8][R][BP];  // [batch parity][slice][row][b]
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, KW = blockDim.x >> 6;
-    const int K = nb * QK;
-    const int blk = wave * 64 + lane;
-    const bool live = blk < nb;
+    const int K = a.ntask * QK;
+    const int t = wave * 64 + lane;  // this lane's task
+    const bool live = t < a.ntask;
+    const int tt = live ? t : 0;
+    const int nb = a.ntask;                       // Q4_0 / Q8_0: blocks per row
+    const int sb = tt >> 3, c = (tt >> 1) & 3, h = tt & 1;  // K-quants: super-block, chunk, half
+    const uint32_t csh = 16u * (uint32_t) (c & 1);         // the chunk's scale bytes within their words
+    const bool chi = c >= 2;
+    const uint32_t row_bytes = F::KQ ? (uint32_t) (a.ntask / 8) * F::SB : 0u;
     const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint8_t *>(wqs), 0, (int) ((size_t) N * nb * CV * 16), 0x00020000);
+        const_cast<uint8_t *>(a.w), 0,
+        (int) (F::KQ ? (size_t) a.N * row_bytes : (size_t) a.N * nb * (TYPE == T_Q4_0 ? 16 : 32)), 0x00020000);
     const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t *>(wd), 0, (int) (((size_t) N * nb + 1) / 2 * 4), 0x00020000);
-
-    const int nbatch = (N + R - 1) / R;
+        const_cast<uint16_t *>(a.wd), 0, F::KQ ? 0 : (int) (((size_t) a.N * nb + 1) / 2 * 4), 0x00020000);
+    const int nbatch = (a.N + R - 1) / R;
     const int G = gridDim.x;
 
     // The activation first, then the first two batches' weights: the loads complete in issue
-    // order, so at every batch the wait is for the older batch only (with the activation last
-    // the first batch would wait for everything, and the compiler's wait at the loop head with
-    // it).
-    int4 xa[B], xb[B];
-    float xd[B];  // activation block scale
-    float xo[B];  // Q4_0: the -8 offset's term (-8 x code sum) x d, 0 for Q8_0
+    // order, so at every batch the wait is for the older batch only.
+    int4 xa[B], xb[B];  // the task's 32 codes (K-quants: xa = sub-block 2c's 16, xb = 2c + 1's)
+    float xs[B];        // d_x (Q4_0 / Q8_0) or d_x of the super-block (K-quants)
+    float xo[B], xo2[B];  // Q4_0: -8 (sum x) d_x; K-quants: bs0 d_x, bs1 d_x
     float2 xmv[B];
+    int bsv[B][2];
 #pragma unroll
     for (int b = 0; b < B; b++) {
-        const int bb = live ? blk : 0;
-        const int4 * xp = reinterpret_cast<const int4 *>(xc + (size_t) b * K + (size_t) bb * QK);
-        xa[b] = xp[0];
-        xb[b] = xp[1];
-        xmv[b] = xm[(size_t) b * nb + bb];
+        const int8_t * xr = a.xc + (size_t) b * K;
+        if constexpr (F::KQ) {
+            const int e = sb * QKK + 64 * c + 16 * h;
+            xa[b] = *reinterpret_cast<const int4 *>(xr + e);
+            xb[b] = *reinterpret_cast<const int4 *>(xr + e + 32);
+            const int16_t * bs = a.xbs + (size_t) b * (K / 16) + sb * 16 + 4 * c + h;
+            bsv[b][0] = bs[0];
+            bsv[b][1] = bs[2];
+            xmv[b].x = a.xd[(size_t) b * (K / QKK) + sb];
+        } else {
+            const int4 * xp = reinterpret_cast<const int4 *>(xr + (size_t) tt * QK);
+            xa[b] = xp[0];
+            xb[b] = xp[1];
+            xmv[b] = a.xm[(size_t) b * nb + tt];
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    // A row's block at o = row * nb + blk: codes at 16 CV o, its scale in the 32-bit word at
-    // (o / 2) * 4. Rows past N lie past the buffers' ends and read zeros; lanes past the row (blk
-    // >= nb) read the next row's block, finite values that their zero activation scale cancels.
-    uint4 w[R][CV], wn[R][CV];
+    uint4 w[R][WV], wn[R][WV];
     uint32_t d[R], dn[R];
-    auto load = [&](int tb, uint4 (&wv)[R][CV], uint32_t (&dv)[R]) {
-        const uint32_t o0 = (uint32_t) tb * (uint32_t) R * (uint32_t) nb + (uint32_t) blk;
+    auto load = [&](int tb, uint4 (&wv)[R][WV], uint32_t (&dv)[R]) {
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            const uint32_t o = o0 + (uint32_t) (r * nb);
+            if constexpr (F::KQ) {
+                // header (d, dmin, scales), [Q5_K: the half's 16 qh bytes,] the half chunk's 16 code bytes
+                const uint32_t o = (uint32_t) (tb * R + r) * row_bytes + (uint32_t) sb * F::SB;
+                const uint32_t qo = (TYPE == T_Q5_K ? 48u : 16u) + 32u * (uint32_t) c + 16u * (uint32_t) h;
+                const uint32_t offs[3] = {o, o + qo, o + 16u + 16u * (uint32_t) h};
+                const auto hq = __builtin_amdgcn_raw_buffer_load_b128(rq, offs[0], 0, 0);  // shared by 8 lanes
+                wv[r][0] = make_uint4(hq[0], hq[1], hq[2], hq[3]);
 #pragma unroll
-            for (int c = 0; c < CV; c++) {
-                const auto q = __builtin_amdgcn_raw_buffer_load_b128(rq, (o * CV + c) * 16u, 0, 2);
-                wv[r][c] = make_uint4(q[0], q[1], q[2], q[3]);
+                for (int v = 1; v < WV; v++) {
+                    const auto q = __builtin_amdgcn_raw_buffer_load_b128(rq, offs[v], 0, 2);
+                    wv[r][v] = make_uint4(q[0], q[1], q[2], q[3]);
+                }
+                dv[r] = 0u;
+            } else {
+                const uint32_t o = (uint32_t) (tb * R + r) * (uint32_t) nb + (uint32_t) t;
+#pragma unroll
+                for (int v = 0; v < WV; v++) {
+                    const auto q = __builtin_amdgcn_raw_buffer_load_b128(rq, (o * WV + v) * 16u, 0, 2);
+                    wv[r][v] = make_uint4(q[0], q[1], q[2], q[3]);
+                }
+                dv[r] = __builtin_amdgcn_raw_buffer_load_b32(rd, (o >> 1) * 4u, 0, 0);
             }
-            dv[r] = __builtin_amdgcn_raw_buffer_load_b32(rd, (o >> 1) * 4u, 0, 0);
         }
     };
-    int t = blockIdx.x;
-    load(t, w, d);
+    int tb = blockIdx.x;
+    load(tb, w, d);
     __builtin_amdgcn_sched_barrier(0);
-    load(t + G, wn, dn);
+    load(tb + G, wn, dn);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int b = 0; b < B; b++) {
-        xd[b] = live ? xmv[b].x : 0.0f;
-        xo[b] = TYPE == T_Q4_0 ? (float) (-8 * __float_as_int(xmv[b].y)) * xd[b] : 0.0f;
+        xs[b] = live ? xmv[b].x : 0.0f;
+        if constexpr (F::KQ) {
+            xo[b] = (float) bsv[b][0] * xs[b];
+            xo2[b] = (float) bsv[b][1] * xs[b];
+        } else {
+            xo[b] = TYPE == T_Q4_0 ? (float) (-8 * __float_as_int(xmv[b].y)) * xs[b] : 0.0f;
+            xo2[b] = 0.0f;
+        }
     }
 
-    // One batch: per row the lane's block products ((sum q x) d_x + offset term) d_w; the R * BP
-    // products reduce-scattered over the wavefront at once into the slice's LDS rows; then the
-    // first wavefront adds the KW slices in order and stores.
     constexpr int V = R * BP, LV = LG + (R == 1 ? 0 : R == 2 ? 1 : R == 4 ? 2 : R == 8 ? 3 : 4);
     static_assert(V <= 64 && (1 << LV) == V, "R and B padded: a power of two up to 64 products");
-    auto batch = [&](int tb, const uint4 (&wv)[R][CV], const uint32_t (&dv)[R], int par) {
+    // clamp on the first dot of a chain: the three-operand form with a zero start (no register
+    // set to zero first); the sums never come near the int32 limits
+    auto dot16 = [](const int (&q)[4], const int4 x) {
+        int s = __builtin_amdgcn_sdot4(q[0], x.x, 0, true);
+        s = sdot4(q[1], x.y, s);
+        s = sdot4(q[2], x.z, s);
+        return sdot4(q[3], x.w, s);
+    };
+    auto batch = [&](int tbi, const uint4 (&wv)[R][WV], const uint32_t (&dv)[R], int par) {
         float v[V];
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            // scale index row * nb + blk: its parity picks the half (blk's parity is the lane's)
-            const int row = min(tb * R + r, N - 1);
-            const uint32_t sh = (uint32_t) (((lane ^ (row & nb)) & 1) << 4);
-            const float dw = h2f((uint16_t) (dv[r] >> sh));
             int lo[4], hi[4];
-            if constexpr (TYPE == T_Q4_0) {
-                lo[0] = (int) (wv[r][0].x & 0x0F0F0F0Fu);
-                lo[1] = (int) (wv[r][0].y & 0x0F0F0F0Fu);
-                lo[2] = (int) (wv[r][0].z & 0x0F0F0F0Fu);
-                lo[3] = (int) (wv[r][0].w & 0x0F0F0F0Fu);
-                hi[0] = (int) ((wv[r][0].x >> 4) & 0x0F0F0F0Fu);
-                hi[1] = (int) ((wv[r][0].y >> 4) & 0x0F0F0F0Fu);
-                hi[2] = (int) ((wv[r][0].z >> 4) & 0x0F0F0F0Fu);
-                hi[3] = (int) ((wv[r][0].w >> 4) & 0x0F0F0F0Fu);
-            } else {
+            const uint32_t q[4] = {wv[r][F::KQ ? 1 : 0].x, wv[r][F::KQ ? 1 : 0].y, wv[r][F::KQ ? 1 : 0].z,
+                                   wv[r][F::KQ ? 1 : 0].w};
+            if constexpr (TYPE == T_Q8_0) {
                 lo[0] = (int) wv[r][0].x;
                 lo[1] = (int) wv[r][0].y;
                 lo[2] = (int) wv[r][0].z;
                 lo[3] = (int) wv[r][0].w;
-                hi[0] = (int) wv[r][CV - 1].x;
-                hi[1] = (int) wv[r][CV - 1].y;
-                hi[2] = (int) wv[r][CV - 1].z;
-                hi[3] = (int) wv[r][CV - 1].w;
-            }
+                hi[0] = (int) wv[r][1].x;
+                hi[1] = (int) wv[r][1].y;
+                hi[2] = (int) wv[r][1].z;
+                hi[3] = (int) wv[r][1].w;
+            } else {
 #pragma unroll
-            for (int b = 0; b < BP; b++) {
-                if (b < B) {
-                    // clamp: the three-operand form with a zero start (no register set to zero first);
-                    // the sums never come near the int32 limits
-                    int sdot = __builtin_amdgcn_sdot4(lo[0], xa[b].x, 0, true);
-                    sdot = sdot4(lo[1], xa[b].y, sdot);
-                    sdot = sdot4(lo[2], xa[b].z, sdot);
-                    sdot = sdot4(lo[3], xa[b].w, sdot);
-                    sdot = sdot4(hi[0], xb[b].x, sdot);
-                    sdot = sdot4(hi[1], xb[b].y, sdot);
-                    sdot = sdot4(hi[2], xb[b].z, sdot);
-                    sdot = sdot4(hi[3], xb[b].w, sdot);
-                    v[r * BP + b] = __builtin_fmaf((float) sdot, xd[b], xo[b]) * dw;
-                } else {
-                    v[r * BP + b] = 0.0f;
+                for (int j = 0; j < 4; j++) {
+                    lo[j] = (int) (q[j] & 0x0F0F0F0Fu);
+                    hi[j] = (int) ((q[j] >> 4) & 0x0F0F0F0Fu);
+                }
+            }
+            if constexpr (TYPE == T_Q5_K) {  // the fifth bits: bit 2c of qh[l] (sub-block 2c), 2c + 1
+                const uint32_t qh[4] = {wv[r][2].x, wv[r][2].y, wv[r][2].z, wv[r][2].w};
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    lo[j] |= (int) (((qh[j] >> (2 * c)) & 0x01010101u) << 4);
+                    hi[j] |= (int) (((qh[j] >> (2 * c + 1)) & 0x01010101u) << 4);
+                }
+            }
+            if constexpr (F::KQ) {
+                // The 6-bit scales and mins of sub-blocks 2c and 2c + 1 (ggml's get_scale_min_k4),
+                // both at once: header bytes 4-15 hold scales[12]; c < 2: sc = scales[2c..2c+1] & 63,
+                // m = scales[2c+4..2c+5] & 63; c >= 2: sc = (scales[2c+4..] & 15) | (scales[2c-4..] >> 6) << 4,
+                // m = (scales[2c+4..] >> 4) | (scales[2c..] >> 6) << 4.
+                const uint4 hd = wv[r][0];
+                const uint32_t A = hd.y >> csh, M = hd.z >> csh, H = hd.w >> csh;
+                const uint32_t scp = chi ? ((H & 0x0F0Fu) | ((A >> 2) & 0x3030u)) : (A & 0x3F3Fu);
+                const uint32_t mp = chi ? (((H >> 4) & 0x0F0Fu) | ((M >> 2) & 0x3030u)) : (M & 0x3F3Fu);
+                const int sc0 = (int) (scp & 0xFFu), sc1 = (int) ((scp >> 8) & 0xFFu);
+                const int m0 = (int) (mp & 0xFFu), m1 = (int) ((mp >> 8) & 0xFFu);
+                const float dd = h2f((uint16_t) (hd.x & 0xffff)), dmin = h2f((uint16_t) (hd.x >> 16));
+                const float fm0 = (float) m0 * dmin, fm1 = (float) m1 * dmin;
+#pragma unroll
+                for (int b = 0; b < BP; b++) {
+                    if (b < B) {
+                        const int isc = sc0 * dot16(lo, xa[b]) + sc1 * dot16(hi, xb[b]);
+                        const float fmin = __builtin_fmaf(fm0, xo[b], fm1 * xo2[b]);
+                        v[r * BP + b] = __builtin_fmaf((float) isc * dd, xs[b], -fmin);
+                    } else {
+                        v[r * BP + b] = 0.0f;
+                    }
+                }
+            } else {
+                // scale index row * nb + t: its parity picks the half (t's parity is the lane's)
+                const int row = min(tbi * R + r, a.N - 1);
+                const uint32_t sh = (uint32_t) (((lane ^ (row & nb)) & 1) << 4);
+                const float dw = h2f((uint16_t) (dv[r] >> sh));
+#pragma unroll
+                for (int b = 0; b < BP; b++) {
+                    if (b < B) {
+                        int s = dot16(lo, xa[b]);
+                        s = sdot4(hi[0], xb[b].x, s);
+                        s = sdot4(hi[1], xb[b].y, s);
+                        s = sdot4(hi[2], xb[b].z, s);
+                        s = sdot4(hi[3], xb[b].w, s);
+                        v[r * BP + b] = __builtin_fmaf((float) s, xs[b], xo[b]) * dw;
+                    } else {
+                        v[r * BP + b] = 0.0f;
+                    }
                 }
             }
         }
@@ -434,23 +524,23 @@ __global__ __launch_bounds__(512) void k_gemv_ks(const uint8_t * __restrict__ wq
         __builtin_amdgcn_s_barrier();
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         if (wave == 0 && lane < R * BP) {
-            const int r = lane / BP, b = lane % BP, row = tb * R + r;
+            const int r = lane / BP, b = lane % BP, row = tbi * R + r;
             float sum = part[par][0][r][b];
             for (int k = 1; k < KW; k++) sum += part[par][k][r][b];
-            if (b < B && row < N) {
-                const size_t o = (size_t) b * ldy + row;
-                y[o] = res ? sum + res[o] : sum;
+            if (b < B && row < a.N) {
+                const size_t o = (size_t) b * a.ldy + row;
+                a.y[o] = a.res ? sum + a.res[o] : sum;
             }
         }
     };
-    while (t < nbatch) {
-        batch(t, w, d, 0);
-        load(t + 2 * G, w, d);
-        t += G;
-        if (t >= nbatch) break;
-        batch(t, wn, dn, 1);
-        load(t + 2 * G, wn, dn);
-        t += G;
+    while (tb < nbatch) {
+        batch(tb, w, d, 0);
+        load(tb + 2 * G, w, d);
+        tb += G;
+        if (tb >= nbatch) break;
+        batch(tb, wn, dn, 1);
+        load(tb + 2 * G, wn, dn);
+        tb += G;
     }
 }
 
@@ -851,13 +941,12 @@ void run_q0(const uint8_t * w, const WeightLayout & L, const int8_t * xc, const 
     k_gemv_q0<TYPE, B, kR, NBL><<<grid, 256, 0, s>>>(w + L.qs, (const uint16_t *) (w + L.d), xc, xm, y, res, N, nb, ldy);
 }
 
-// The K-sliced kernel (k_gemv_ks) for batches of 2..8 rows: ceil(nb / 64) wavefronts per
+// The K-sliced kernel (k_gemv_ks) for batches of 2..8 rows: ceil(tasks / 64) wavefronts per
 // workgroup, as many workgroups as are resident at once (at most), each with the same number of
 // row batches.
 template <int TYPE, int B, int R>
-void run_ks(const uint8_t * w, const WeightLayout & L, const int8_t * xc, const float2 * xm, float * y,
-            const float * res, int N, int nb, int ldy, hipStream_t s) {
-    const int kw = (nb + 63) / 64;
+void run_ks(const KsArgs & a, hipStream_t s) {
+    const int kw = (a.ntask + 63) / 64;
     static thread_local int occ[9] = {0};  // resident workgroups per CU, by wavefronts per workgroup
     if (occ[kw] == 0) {
         check_hip(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ[kw], reinterpret_cast<const void *>(&k_gemv_ks<TYPE, B, R>),
@@ -865,18 +954,41 @@ void run_ks(const uint8_t * w, const WeightLayout & L, const int8_t * xc, const 
                   "gemv occupancy");
         occ[kw] = std::max(occ[kw], 1);
     }
-    const int nbatch = (N + R - 1) / R, maxg = cu_count() * occ[kw];
+    const int nbatch = (a.N + R - 1) / R, maxg = cu_count() * occ[kw];
     const int per = (nbatch + maxg - 1) / maxg;
     const unsigned grid = (unsigned) ((nbatch + per - 1) / per);
-    k_gemv_ks<TYPE, B, R><<<grid, kw * 64, 0, s>>>(w + L.qs, (const uint16_t *) (w + L.d), xc, xm, y, res, N, nb, ldy);
+    k_gemv_ks<TYPE, B, R><<<grid, kw * 64, 0, s>>>(a);
+}
+
+// Rows per batch of the K-sliced kernel: R B products reduce-scattered at once (measured: Q4_0 /
+// Q8_0 at B <= 2 best with 8, the rest with 4).
+template <int TYPE, int B>
+void run_ks_b(const KsArgs & a, hipStream_t s) {
+    run_ks<TYPE, B, (B <= 2 && !KsFmt<TYPE>::KQ ? 8 : 4)>(a, s);
+}
+
+template <int TYPE>
+void run_ks_t(int B, const KsArgs & a, hipStream_t s) {
+    switch (B) {
+        case 2: return run_ks_b<TYPE, 2>(a, s);
+        case 3: return run_ks_b<TYPE, 3>(a, s);
+        case 4: return run_ks_b<TYPE, 4>(a, s);
+        case 5: return run_ks_b<TYPE, 5>(a, s);
+        case 6: return run_ks_b<TYPE, 6>(a, s);
+        case 7: return run_ks_b<TYPE, 7>(a, s);
+        default: return run_ks_b<TYPE, 8>(a, s);
+    }
+}
+
+// The K-sliced kernel takes rows of up to 512 tasks (K <= 16384) in B = 2..8 batches.
+bool ks_fits(int type, int64_t K, int64_t B) {
+    return B >= 2 && B <= 8 && K % QK == 0 && K / QK <= 512 &&
+           (type == T_Q4_0 || type == T_Q8_0 || ((type == T_Q4_K || type == T_Q5_K) && K % QKK == 0));
 }
 
 template <int TYPE, int B>
 void run_q0_nbl(int nbl, const uint8_t * w, const WeightLayout & L, const int8_t * xc, const float2 * xm, float * y,
                 const float * res, int N, int nb, int ldy, hipStream_t s) {
-    if constexpr (B >= 2) {
-        if (nb <= 512) return run_ks<TYPE, B, (B <= 2 ? 8 : 4)>(w, L, xc, xm, y, res, N, nb, ldy, s);
-    }
     if constexpr (B <= 4) {  // rows of up to 128 blocks: the persistent kernel
         if (nbl == 1) return run_p<TYPE, B, 1>(w, L, xc, xm, y, res, N, nb, ldy, s);
         if (nbl == 2) return run_p<TYPE, B, 2>(w, L, xc, xm, y, res, N, nb, ldy, s);
@@ -945,6 +1057,30 @@ void launch_gemv(int type, const void * wv, int64_t N, int64_t K, const void * a
     const uint8_t * w = (const uint8_t *) wv;
     const ActLayout A = act_layout(type, B, K);
     const uint8_t * a = (const uint8_t *) act;
+    const uint64_t ks_bytes = is_kquant(type) ? (uint64_t) N * row_bytes(type, K)
+                                              : (uint64_t) N * (uint64_t) (K / QK) * (type == T_Q4_0 ? 16u : 32u);
+    if (ks_fits(type, K, B) && ks_bytes < 0x80000000ull) {
+        const bool kq = is_kquant(type);
+        const WeightLayout L = weight_layout(type, N, K);
+        KsArgs k{};
+        k.w = kq ? w : w + L.qs;
+        k.wd = kq ? nullptr : (const uint16_t *) (w + L.d);
+        k.xc = (const int8_t *) (a + A.codes);
+        k.xm = kq ? nullptr : (const float2 *) (a + A.meta);
+        k.xbs = kq ? (const int16_t *) (a + A.meta) : nullptr;
+        k.xd = kq ? (const float *) (a + A.d) : nullptr;
+        k.y = y;
+        k.res = res;
+        k.N = (int) N;
+        k.ntask = (int) (K / QK);
+        k.ldy = (int) ldy;
+        if (type == T_Q4_0) run_ks_t<T_Q4_0>((int) B, k, s);
+        else if (type == T_Q8_0) run_ks_t<T_Q8_0>((int) B, k, s);
+        else if (type == T_Q4_K) run_ks_t<T_Q4_K>((int) B, k, s);
+        else run_ks_t<T_Q5_K>((int) B, k, s);
+        check_launch("gemv");
+        return;
+    }
     if (type == T_Q4_0 || type == T_Q8_0) {
         const WeightLayout L = weight_layout(type, N, K);
         const int nb = (int) (K / QK);

@@ -140,14 +140,19 @@ def test_gemv_c1_q8_0_4096(gops, orc):
     assert orc.parity(y, orc.mul_mat(raw, "q8_0", x, 4096)) < TOL
 
 
-@pytest.mark.parametrize("t", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("t", ["q4_0", "q8_0", "q4_K", "q5_K"])
 @pytest.mark.parametrize("B", [2, 3, 5, 8, 16])
 @pytest.mark.parametrize("K", [2048, 3104, 14336])
 def test_gemv_batches_residual(gops, orc, t, B, K):
-    """Batches of 2..8 rows (the K-sliced kernel: one wavefront per 64 blocks of K, the
-    activation in registers, R-row batches) and 16 (the GEMM): a row count that is not a multiple
-    of the row batch, a residual, K of one wavefront (2048), of a partly filled second one (3104 =
-    97 blocks: lanes past the row) and of seven (14336), B padded to a power of two (3, 5)."""
+    """Batches of 2..8 rows (the K-sliced kernel: one wavefront per 64 tasks of 32 values of K,
+    the activation in registers, R-row batches) and 16 (the GEMM / K-quant kernel): a row count
+    that is not a multiple of the row batch, a residual, K of one wavefront (2048), of a partly
+    filled second one (3104 = 97 blocks: lanes past the row; Q4_0 / Q8_0 only, K-quant rows are
+    whole 256-value super-blocks) and of seven (14336), B padded to a power of two (3, 5)."""
+    if t in ("q4_K", "q5_K") and K % 256:
+        pytest.skip("K-quant rows are whole 256-value super-blocks")
+    if t in ("q4_K", "q5_K") and B > 8:
+        pytest.skip("mul_mat_q takes a pre-quantized K-quant activation of at most 8 rows")
     N = 1000
     raw, qw = _weight(gops, orc, t, N, K, 44)
     x = orc.normal((B, K), seed=45)
