@@ -325,14 +325,16 @@ struct KsArgs {
     const float2 * xm;      // Q8_0 activation: (d, code sum) [B][K / 32]
     const int16_t * xbs;    // Q8_K activation: bsums [B][K / 16]
     const float * xd;       // Q8_K activation: d [B][K / 256]
+    const float * x;        // FQ: the f32 activation row itself (one row, quantized in the kernel)
     float * y;
     const float * res;
     int N, ntask, ldy;      // ntask: tasks per row (K / 32)
 };
 
-template <int TYPE, int B, int R>
+template <int TYPE, int B, int R, bool FQ = false>
 __global__ __launch_bounds__(512) void k_gemv_ks(const KsArgs a) {
     using F = KsFmt<TYPE>;
+    static_assert(!FQ || (B == 1 && F::KQ), "the activation is quantized in the kernel for one K-quant row");
     constexpr int WV = F::WV;
     constexpr int BP = B <= 1 ? 1 : B <= 2 ? 2 : B <= 4 ? 4 : 8;  // B padded to a power of two
     constexpr int LG = BP == 1 ? 0 : BP == 2 ? 1 : BP == 4 ? 2 : 3;
@@ -366,7 +368,86 @@ __global__ __launch_bounds__(512) void k_gemv_ks(const KsArgs a) {
 #pragma unroll
     for (int b = 0; b < B; b++) {
         const int8_t * xr = a.xc + (size_t) b * K;
-        if constexpr (F::KQ) {
+        if constexpr (FQ) {
+            // ggml's quantize_row_q8_K (as k_act_q8_K) of the super-block, whose 256 values are
+            // the 32 of each of its 8 lanes (consecutive, aligned): max = the signed value of the
+            // first largest |x|, iscale = -127 / max, q = min(127, rint(iscale x)), d = 1 / iscale,
+            // zeros for an all-zero block; this lane's two bsums are the sums of its two 16s.
+#pragma clang fp contract(off)
+            const int il = 64 * c + 16 * h;
+            const float * xf = a.x + sb * QKK + il;
+            float vv[32];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const float4 lo4 = *reinterpret_cast<const float4 *>(xf + 4 * k);
+                const float4 hi4 = *reinterpret_cast<const float4 *>(xf + 32 + 4 * k);
+                vv[4 * k] = lo4.x;
+                vv[4 * k + 1] = lo4.y;
+                vv[4 * k + 2] = lo4.z;
+                vv[4 * k + 3] = lo4.w;
+                vv[16 + 4 * k] = hi4.x;
+                vv[16 + 4 * k + 1] = hi4.y;
+                vv[16 + 4 * k + 2] = hi4.z;
+                vv[16 + 4 * k + 3] = hi4.w;
+            }
+            float ax = 0.0f, mx = 0.0f;
+            int idx = 1 << 30;
+#pragma unroll
+            for (int j = 0; j < 32; j++) {  // in index order: the 16 of sub-block 2c, then of 2c + 1
+                if (fabsf(vv[j]) > ax) {
+                    ax = fabsf(vv[j]);
+                    mx = vv[j];
+                    idx = il + (j < 16 ? j : 16 + j);
+                }
+            }
+            auto take = [&](float ax2, float mx2, int idx2) {
+                if (ax2 > ax || (ax2 == ax && idx2 < idx)) {
+                    ax = ax2;
+                    mx = mx2;
+                    idx = idx2;
+                }
+            };
+            {
+                const float a1 = lane_pair<1>(ax), m1 = lane_pair<1>(mx);
+                const int i1 = lane_pair_i<1>(idx);
+                take(a1, m1, i1);
+                const float a2 = lane_pair<2>(ax), m2 = lane_pair<2>(mx);
+                const int i2 = lane_pair_i<2>(idx);
+                take(a2, m2, i2);
+                const float a4 = lane_pair<4>(ax), m4 = lane_pair<4>(mx);
+                const int i4 = lane_pair_i<4>(idx);
+                take(a4, m4, i4);
+            }
+            int qv[32];
+            float dq = 0.0f;
+            if (ax != 0.0f) {
+                const float iscale = __fdiv_rn(-127.0f, mx);
+#pragma unroll
+                for (int j = 0; j < 32; j++) {
+                    const int r = (int) __builtin_rintf(iscale * vv[j]);
+                    qv[j] = r < 127 ? r : 127;
+                }
+                dq = __fdiv_rn(1.0f, iscale);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 32; j++) qv[j] = 0;
+            }
+            int pk[8], s0 = 0, s1 = 0;
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+                pk[k] = (qv[4 * k] & 0xff) | ((qv[4 * k + 1] & 0xff) << 8) | ((qv[4 * k + 2] & 0xff) << 16) |
+                        ((qv[4 * k + 3] & 0xff) << 24);
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                s0 += qv[j];
+                s1 += qv[16 + j];
+            }
+            xa[b] = make_int4(pk[0], pk[1], pk[2], pk[3]);
+            xb[b] = make_int4(pk[4], pk[5], pk[6], pk[7]);
+            bsv[b][0] = s0;
+            bsv[b][1] = s1;
+            xmv[b].x = dq;
+        } else if constexpr (F::KQ) {
             const int e = sb * QKK + 64 * c + 16 * h;
             xa[b] = *reinterpret_cast<const int4 *>(xr + e);
             xb[b] = *reinterpret_cast<const int4 *>(xr + e + 32);
@@ -944,12 +1025,12 @@ void run_q0(const uint8_t * w, const WeightLayout & L, const int8_t * xc, const 
 // The K-sliced kernel (k_gemv_ks) for batches of 2..8 rows: ceil(tasks / 64) wavefronts per
 // workgroup, as many workgroups as are resident at once (at most), each with the same number of
 // row batches.
-template <int TYPE, int B, int R>
+template <int TYPE, int B, int R, bool FQ = false>
 void run_ks(const KsArgs & a, hipStream_t s) {
     const int kw = (a.ntask + 63) / 64;
     static thread_local int occ[9] = {0};  // resident workgroups per CU, by wavefronts per workgroup
     if (occ[kw] == 0) {
-        check_hip(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ[kw], reinterpret_cast<const void *>(&k_gemv_ks<TYPE, B, R>),
+        check_hip(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ[kw], reinterpret_cast<const void *>(&k_gemv_ks<TYPE, B, R, FQ>),
                                                                kw * 64, 0),
                   "gemv occupancy");
         occ[kw] = std::max(occ[kw], 1);
@@ -957,7 +1038,7 @@ void run_ks(const KsArgs & a, hipStream_t s) {
     const int nbatch = (a.N + R - 1) / R, maxg = cu_count() * occ[kw];
     const int per = (nbatch + maxg - 1) / maxg;
     const unsigned grid = (unsigned) ((nbatch + per - 1) / per);
-    k_gemv_ks<TYPE, B, R><<<grid, kw * 64, 0, s>>>(a);
+    k_gemv_ks<TYPE, B, R, FQ><<<grid, kw * 64, 0, s>>>(a);
 }
 
 // Rows per batch of the K-sliced kernel: R B products reduce-scattered at once (measured: Q4_0 /
@@ -970,6 +1051,7 @@ void run_ks_b(const KsArgs & a, hipStream_t s) {
 template <int TYPE>
 void run_ks_t(int B, const KsArgs & a, hipStream_t s) {
     switch (B) {
+        case 1: return run_ks<TYPE, 1, 4>(a, s);
         case 2: return run_ks_b<TYPE, 2>(a, s);
         case 3: return run_ks_b<TYPE, 3>(a, s);
         case 4: return run_ks_b<TYPE, 4>(a, s);
@@ -980,9 +1062,10 @@ void run_ks_t(int B, const KsArgs & a, hipStream_t s) {
     }
 }
 
-// The K-sliced kernel takes rows of up to 512 tasks (K <= 16384) in B = 2..8 batches.
+// The K-sliced kernel takes rows of up to 512 tasks (K <= 16384) in batches of 2..8 rows (K-quants:
+// 1..8, the one-row case as the kernel that quantizes the row itself).
 bool ks_fits(int type, int64_t K, int64_t B) {
-    return B >= 2 && B <= 8 && K % QK == 0 && K / QK <= 512 &&
+    return B >= (is_kquant(type) ? 1 : 2) && B <= 8 && K % QK == 0 && K / QK <= 512 &&
            (type == T_Q4_0 || type == T_Q8_0 || ((type == T_Q4_K || type == T_Q5_K) && K % QKK == 0));
 }
 
@@ -1050,6 +1133,31 @@ void run_q4k_nbl(int nbl, const uint8_t * w, const int8_t * xc, const int16_t * 
 
 }  // namespace
 
+// One f32 row times a Q4_K / Q5_K weight in one launch, the row quantized to Q8_K in the kernel
+// (k_gemv_ks<..., FQ>): K a multiple of 256 up to 16384, up to kKsRowMaxN rows (measured: beyond,
+// the separate quantization plus the one-row K-quant kernels is faster: 4096 x 28672 Q4_K 15.8 us
+// against 16.9 fused, Q5_K 19.6 against 24.3), the weight below 2 GB.
+constexpr int64_t kKsRowMaxN = 8192;
+
+bool gemv_row_kq_fits(int type, int64_t N, int64_t K) {
+    return (type == T_Q4_K || type == T_Q5_K) && K % QKK == 0 && K > 0 && K / QK <= 512 && N <= kKsRowMaxN &&
+           (uint64_t) N * row_bytes(type, K) < 0x80000000ull;
+}
+
+void launch_gemv_row_kq(int type, const void * w, int64_t N, int64_t K, const float * x, float * y, hipStream_t s) {
+    require(gemv_row_kq_fits(type, N, K), "gemv row: Q4_K / Q5_K, K a multiple of 256 up to 16384");
+    KsArgs k{};
+    k.w = (const uint8_t *) w;
+    k.x = x;
+    k.y = y;
+    k.N = (int) N;
+    k.ntask = (int) (K / QK);
+    k.ldy = (int) N;
+    if (type == T_Q4_K) run_ks<T_Q4_K, 1, 4, true>(k, s);
+    else run_ks<T_Q5_K, 1, 4, true>(k, s);
+    check_launch("gemv row");
+}
+
 // y [B][ldy] (first N columns written) from packed weights and a quantized activation; with res,
 // y = res + W x (res has y's layout and may be y itself).
 void launch_gemv(int type, const void * wv, int64_t N, int64_t K, const void * act, int64_t B, float * y, int64_t ldy,
@@ -1059,7 +1167,7 @@ void launch_gemv(int type, const void * wv, int64_t N, int64_t K, const void * a
     const uint8_t * a = (const uint8_t *) act;
     const uint64_t ks_bytes = is_kquant(type) ? (uint64_t) N * row_bytes(type, K)
                                               : (uint64_t) N * (uint64_t) (K / QK) * (type == T_Q4_0 ? 16u : 32u);
-    if (ks_fits(type, K, B) && ks_bytes < 0x80000000ull) {
+    if (ks_fits(type, K, B) && (B > 1 || N <= kKsRowMaxN) && ks_bytes < 0x80000000ull) {
         const bool kq = is_kquant(type);
         const WeightLayout L = weight_layout(type, N, K);
         KsArgs k{};

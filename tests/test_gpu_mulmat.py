@@ -160,3 +160,25 @@ def test_gemv_batches_residual(gops, orc, t, B, K):
     act = gops.quantize_act(t, torch.from_numpy(x).cuda())
     y = to_np(gops.mul_mat_q(qw, act, B, res=torch.from_numpy(r).cuda()))
     assert orc.parity(y, orc.mul_mat(raw, t, x, K) + r) < TOL
+
+
+@pytest.mark.parametrize("t", ["q4_K", "q5_K"])
+@pytest.mark.parametrize("K", [4096, 14336])
+def test_gemv_row_kquant_fused_quantizer(gops, orc, t, K):
+    """One f32 row times a Q4_K / Q5_K weight: the kernel quantizes the row to Q8_K itself. It must
+    produce what the same kernel gives on the separately quantized row (k_act_q8_K, bit-exact with
+    the oracle's quantize_row_q8_K) bit for bit, so every code, bsum and d is ggml's. The row has
+    an all-zero super-block and, in another, a tie of |max| between lanes (+3 before -3: the first
+    one sets the scale, so -3 maps to +127 by the clamp)."""
+    N = 1000
+    raw, qw = _weight(gops, orc, t, N, K, 47)
+    x = orc.normal((1, K), seed=48)
+    x[0, 256:512] = 0.0
+    x[0, 512 + 40] = 3.0
+    x[0, 512 + 200] = -3.0
+    xt = torch.from_numpy(x).cuda()
+    y = to_np(gops.mul_mat(qw, xt))
+    act = gops.quantize_act(t, xt)
+    y_sep = to_np(gops.mul_mat_q(qw, act, 1))
+    assert np.array_equal(y, y_sep), float(np.abs(y - y_sep).max())
+    assert orc.parity(y, orc.mul_mat(raw, t, x, K)) < TOL
