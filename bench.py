@@ -230,6 +230,27 @@ def bench_decode(args, torch) -> tuple[dict, object]:
     return res, m
 
 
+def bench_steps(args, torch) -> dict:
+    """The decode benchmark's model, its 512-token prefill and --steps greedy decode steps, and
+    nothing else: a short run whose every decode-step kernel a profiler pass can count."""
+    import numpy as np
+
+    from ggml_compiler_amd.llm import LlamaConfig, Model
+
+    cfg = LlamaConfig.llama3_8b(max_ctx=PROMPT + max(args.steps, args.warmup) + 64)
+    m = Model(cfg, max_prompt=PROMPT)
+    m.init_random(seed=0, std=0.02)
+    prompt = np.random.default_rng(0).integers(0, cfg.n_vocab, PROMPT).tolist()
+    first = int(np.argmax(m.prefill(prompt)))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    m.generate(first, args.steps)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    m.close()
+    return {"metric": "decode steps (profiling run)", "steps": args.steps, "ms_per_step": round(dt / args.steps * 1e3, 4)}
+
+
 def bench_ggml_decode(args) -> dict:
     """The same 8B-shaped model's decode step built node by node with the ggml API
     (ggml_compiler_amd.ggml.DecodeGraph: separate q / k / v and gate / up mul_mats, rope, set_rows,
@@ -539,8 +560,11 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--mode", choices=["decode", "gemv", "roofline", "sweep", "gemm", "ggml", "program"], default="decode",
+    ap.add_argument("--mode", choices=["decode", "gemv", "roofline", "sweep", "gemm", "ggml", "program", "steps"],
+                    default="decode",
                     help="roofline: only the roofline leg and a 1 GiB copy (for rocprofv3 --pmc runs); "
+                         "steps: the decode model's 512-token prefill and --steps decode steps only (for counter "
+                         "and kernel-trace runs of the decode kernels); "
                          "sweep: the GEMV / GEMM / attention configurations, one JSON line each; "
                          "gemm: the prefill GEMM configuration alone, --steps launches (for counter runs); "
                          "ggml: the decode step built with the ggml API and run by its graph executor; "
@@ -553,7 +577,7 @@ def main() -> int:
               file=sys.stderr)
         return 2
     args.steps = args.steps or {"decode": 128, "gemv": 200, "roofline": 10, "sweep": 1, "gemm": 3,
-                                "ggml": 128, "program": 128}[args.mode]
+                                "ggml": 128, "program": 128, "steps": 4}[args.mode]
     args.warmup = args.warmup if args.warmup is not None else 8
 
     import torch
@@ -577,6 +601,9 @@ def main() -> int:
         us = e0.elapsed_time(e1) * 1e3 / args.steps
         print(json.dumps({"metric": "prefill GEMM TOP/s", "value": round(2 * 512 * 14336 * 4096 / us / 1e6, 1),
                           "unit": "TOP/s", "us": round(us, 1)}), flush=True)
+        return 0
+    if args.mode == "steps":
+        print(json.dumps(bench_steps(args, torch)), flush=True)
         return 0
     if args.mode == "ggml":
         print(json.dumps(bench_ggml_decode(args)), flush=True)
