@@ -507,10 +507,14 @@ def _rotating_weights(ops, t: str, N: int, K: int, seed: int):
     return [w] + [ops.QuantWeight(w.type, w.N, w.K, w.data.clone()) for _ in range(copies - 1)]
 
 
-def bench_sweep(ops, torch) -> list[dict]:
+def bench_sweep(ops, torch, only: set[str] | None = None) -> list[dict]:
     """The other measured configurations (ggml_mul_mat GEMV / GEMM, decode flash_attn_ext), each
-    op launched back to back from a HIP graph over inputs rotated past the Infinity Cache."""
+    op launched back to back from a HIP graph over inputs rotated past the Infinity Cache. only: the
+    configuration names to run (C1, C2, K56, C3, C4), or all."""
     out = []
+
+    def want(cfg):
+        return only is None or cfg in only
 
     def gemv_case(cfg, t, K, N, B):
         ws = _rotating_weights(ops, t, N, K, seed=K + N)
@@ -522,25 +526,29 @@ def bench_sweep(ops, torch) -> list[dict]:
                     "GB/s": round(nbytes / us / 1e3, 1), "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)})
         del ws
 
-    gemv_case("C1", "q8_0", 4096, 4096, 1)
-    for t in ("q4_0", "q4_K"):
+    if want("C1"):
+        gemv_case("C1", "q8_0", 4096, 4096, 1)
+    for t in ("q4_0", "q4_K") if want("C2") else ():
         for K, N in LAYER_SHAPES:
             for B in (1, 2, 4, 8):
                 gemv_case("C2", t, K, N, B)
     # the other K-quant storage types at the same layer shapes (Q4_K_M files mix Q4_K with Q6_K)
-    for t in ("q5_K", "q6_K"):
+    for t in ("q5_K", "q6_K") if want("K56") else ():
         for K, N in LAYER_SHAPES:
             for B in (1, 8):
                 gemv_case("K56", t, K, N, B)
     # C3: prefill GEMM, Q8_0 K=4096 N=14336, 512 rows (activation quantization included)
-    ws = _rotating_weights(ops, "q8_0", 14336, 4096, seed=3)[:4]
-    x = ops.fill_normal((512, 4096), seed=4)
-    us = _graph_us(torch, [lambda w=w: ops.mul_mat(w, x) for w in ws] * 4, passes=3)
-    flops = 2 * 512 * 14336 * 4096
-    out.append({"config": "C3", "op": "mul_mat", "type": "q8_0", "K": 4096, "N": 14336, "M": 512, "us": round(us, 1),
-                "TOP/s": round(flops / us / 1e6, 1), "frac_int8_mfma": round(flops / us / 1e6 / INT8_PEAK_TOPS, 4)})
+    if want("C3"):
+        ws = _rotating_weights(ops, "q8_0", 14336, 4096, seed=3)[:4]
+        x = ops.fill_normal((512, 4096), seed=4)
+        us = _graph_us(torch, [lambda w=w: ops.mul_mat(w, x) for w in ws] * 4, passes=3)
+        flops = 2 * 512 * 14336 * 4096
+        out.append({"config": "C3", "op": "mul_mat", "type": "q8_0", "K": 4096, "N": 14336, "M": 512,
+                    "us": round(us, 1), "TOP/s": round(flops / us / 1e6, 1),
+                    "frac_int8_mfma": round(flops / us / 1e6 / INT8_PEAK_TOPS, 4)})
+        del ws
     # C4: decode attention, 32 q heads on 8 KV heads of 128, one query row, every key visible
-    for ctx in (512, 4096, 32768):
+    for ctx in (512, 4096, 32768) if want("C4") else ():
         kv_bytes = 2 * ctx * 8 * 128 * 2
         copies = max(2, math.ceil(ROTATE_BYTES / kv_bytes))
         k = ops.fill_normal((copies, 8, ctx, 128), seed=5).half()
@@ -569,6 +577,8 @@ def main() -> int:
                          "gemm: the prefill GEMM configuration alone, --steps launches (for counter runs); "
                          "ggml: the decode step built with the ggml API and run by its graph executor; "
                          "program: the same model as a ggml-compiler program GGUF run by the loader")
+    ap.add_argument("--only", default=None,
+                    help="sweep: comma-separated configurations to run (C1, C2, K56, C3, C4); default all")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-program", action="store_true", help="skip the program-GGUF decode figure")
     args = ap.parse_args()
@@ -612,7 +622,7 @@ def main() -> int:
         print(json.dumps(bench_program_decode(args)), flush=True)
         return 0
     if args.mode == "sweep":
-        for r in bench_sweep(ops, torch):
+        for r in bench_sweep(ops, torch, set(args.only.split(",")) if args.only else None):
             print(json.dumps(r), flush=True)
         return 0
     if args.mode == "roofline":

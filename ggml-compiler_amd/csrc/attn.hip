@@ -542,18 +542,33 @@ bool decode_lanes(int max_kv) { return max_kv <= kLanesMaxKv; }
 // Query heads one decode workgroup takes of its KV head's GT.
 int decode_group(int GT, int max_kv) { return decode_lanes(max_kv) ? 1 : GT; }
 
-// The decode split count for n_kv keys: one load batch (lanes) or one 16-key block (matrix cores)
-// per wavefront, at most max_split splits (the wavefronts then take several).
-int decode_splits(int D, int G, int n_kv, int max_split) {
-    const int per = decode_lanes(n_kv) ? lanes_keys(D, G) : decode_keys(D, G);
+// The decode split count for n_kv keys and H query heads, at most max_split splits:
+//   - lane groups, wide (the decode step's plan: its output projection merges the splits in its
+//     prologue, which every workgroup repeats, so fewer splits): one 16-wavefront load batch per
+//     split, 16 wavefronts each;
+//   - lane groups, not wide (a merge kernel follows): a split per four wavefronts' load batches
+//     (64 keys at D = 128), at most 512 / H splits, 4-16 wavefronts each (lanes_nw). Measured on
+//     MI355X (32 query heads on 8 KV heads of 128): 512-2048 wavefronts in all end soonest, the
+//     first loads of more queue behind the others';
+//   - matrix cores: one 16-key block per wavefront of a 4-wavefront workgroup (the wavefronts then
+//     take several).
+int decode_splits(int D, int H, int G, int n_kv, int max_split, bool wide) {
+    int per = decode_keys(D, G);
+    if (decode_lanes(n_kv)) {
+        if (!wide) {
+            per = 4 * lanes_batch(D, 1);
+            max_split = std::min(max_split, std::max(1, 512 / std::max(1, H)));
+        } else {
+            per = lanes_keys(D, 1);
+        }
+    }
     return std::max(1, std::min(max_split, (n_kv + per - 1) / per));
 }
 
-// Decode (one query row, captured once for every KV length up to max_ctx): the split count for
-// max_ctx keys; the KV length itself is read on the device and each split takes an equal share.
-AttnPlan attn_plan_decode(int D, int G, int max_ctx, int max_split) {
-    const int nsplit = decode_lanes(max_ctx) ? std::max(1, std::min(max_split, (max_ctx + lanes_keys(D, 1) - 1) / lanes_keys(D, 1)))
-                                             : decode_splits(D, G, max_ctx, max_split);
+// Decode (one query row, captured once for every KV length up to max_ctx): the wide split count
+// for max_ctx keys; the KV length itself is read on the device and each split takes an equal share.
+AttnPlan attn_plan_decode(int D, int H, int G, int max_ctx, int max_split) {
+    const int nsplit = decode_splits(D, H, decode_group(G, max_ctx), max_ctx, max_split, true);
     return {nsplit, (max_ctx + nsplit - 1) / nsplit};
 }
 
@@ -563,11 +578,13 @@ bool attn_decode_fits(int D, int G) { return (D == 64 || D == 128) && (G == 1 ||
 // chunk: keys per split (nsplit * chunk >= n_kv); kv_rows: rows the K and V buffers hold per head;
 // GS: query heads per workgroup (decode_group). pf (optional): byte ranges that about as many spare
 // workgroups as leave the CUs one each read ahead into the Infinity Cache.
+// nw_lanes: wavefronts per lane-group split (4, 8 or 16; 16 for a wide plan), or 0 for lanes_nw's
+// choice.
 void launch_attn_decode(const float * q, int64_t q_h, const void * k, int64_t k_h, int64_t k_j, const void * v,
                         int64_t v_h, int64_t v_j, int D, int H, int Hkv, int n_kv, const int * n_kv_dev, float scale,
                         int nsplit, int chunk, int kv_rows, int GS, float * out, float * part_o, float2 * part_ml,
                         hipStream_t s, const Prefetch * pf,
-                        const void * mask) {
+                        const void * mask, int nw_lanes) {
     const int G = H / Hkv;
     require(attn_decode_fits(D, G) && H % Hkv == 0, "attn decode: D 64 / 128 and 1, 2, 4 or 8 query heads per KV head");
     const bool lanes = decode_lanes(n_kv_dev ? kv_rows : n_kv);
@@ -591,18 +608,20 @@ void launch_attn_decode(const float * q, int64_t q_h, const void * k, int64_t k_
     const uint16_t * mp = (const uint16_t *) mask;
     if (lanes) {
         const dim3 grid((unsigned) (nsplit + extra), (unsigned) Hkv, (unsigned) (G / GS));
-#define GCQ_AL(DD)                                                                                              \
-    if (D == DD) {                                                                                              \
+        const int nw = nw_lanes ? nw_lanes : lanes_nw(D, 1, chunk);
+        require(nw == 4 || nw == 8 || nw == 16, "attn decode: 4, 8 or 16 wavefronts per split");
+#define GCQ_AL(DD, NW)                                                                                          \
+    if (D == DD && nw == NW) {                                                                                  \
         if (mp)                                                                                                 \
-            k_attn_lanes<DD, 1, lanes_waves(1), true><<<grid, lanes_waves(1) * 64, 0, s>>>(                     \
-                G, q, q_h, kp, k_h, k_j, vp, v_h, v_j, scale, n_kv, n_kv_dev, chunk, kv_rows, nsplit, out, part_o, \
-                part_ml, P, mp);                                                                                \
+            k_attn_lanes<DD, 1, NW, true><<<grid, NW * 64, 0, s>>>(G, q, q_h, kp, k_h, k_j, vp, v_h, v_j, scale,   \
+                                                               n_kv, n_kv_dev, chunk, kv_rows, nsplit, out,     \
+                                                               part_o, part_ml, P, mp);                         \
         else                                                                                                    \
-            k_attn_lanes<DD, 1, lanes_waves(1), false><<<grid, lanes_waves(1) * 64, 0, s>>>(                    \
-                G, q, q_h, kp, k_h, k_j, vp, v_h, v_j, scale, n_kv, n_kv_dev, chunk, kv_rows, nsplit, out, part_o, \
-                part_ml, P, nullptr);                                                                           \
+            k_attn_lanes<DD, 1, NW, false><<<grid, NW * 64, 0, s>>>(G, q, q_h, kp, k_h, k_j, vp, v_h, v_j, scale,  \
+                                                                n_kv, n_kv_dev, chunk, kv_rows, nsplit, out,    \
+                                                                part_o, part_ml, P, nullptr);                   \
     }
-        GCQ_AL(64) GCQ_AL(128)
+        GCQ_AL(64, 4) GCQ_AL(64, 8) GCQ_AL(64, 16) GCQ_AL(128, 4) GCQ_AL(128, 8) GCQ_AL(128, 16)
 #undef GCQ_AL
         check_launch("attn decode");
         return;
@@ -691,9 +710,9 @@ void launch_flash_attn(const float * q, int64_t q_h, int64_t q_s, const void * k
         const int GS = decode_group(H / Hkv, n_kv);
         // one 16-key block per wavefront, at most about one workgroup per CU (longer contexts take
         // more blocks per wavefront: fewer partials to merge)
-        const int nsplit = decode_splits(D, GS, n_kv, std::min(p.nsplit, std::max(1, cu_count() / Hkv)));
+        const int nsplit = decode_splits(D, H, GS, n_kv, std::min(p.nsplit, std::max(1, cu_count() / Hkv)), false);
         launch_attn_decode(q, q_h, k, k_h, k_j, v, v_h, v_j, D, H, Hkv, n_kv, nullptr, scale, nsplit,
-                           (n_kv + nsplit - 1) / nsplit, n_kv, GS, out, po, pml, s, nullptr, mask);
+                           (n_kv + nsplit - 1) / nsplit, n_kv, GS, out, po, pml, s, nullptr, mask, 0);
         if (nsplit == 1) return;
         if (D == 64) k_attn_merge<64><<<(unsigned) H, 256, 0, s>>>(po, pml, out, nsplit);
         else k_attn_merge<128><<<(unsigned) H, 256, 0, s>>>(po, pml, out, nsplit);

@@ -11,7 +11,7 @@
 // then the NW wavefronts are merged at the end (shuffles, LDS). One split with an output row: the
 // normalized output out[h][d]; else the split's (max, exp-sum, unnormalized output) in
 // k_attn_split's partial layout, for the merge (k_attn_merge, or a GEMV prologue). The host sizes
-// splits so that each wavefront's keys are one load batch (lanes_keys).
+// splits and NW so that each wavefront's keys are about one load batch (lanes_nw).
 #pragma once
 
 #include "gcq_common.h"
@@ -27,13 +27,24 @@ __device__ __forceinline__ half2_t as_h2(uint32_t u) {
     return h;
 }
 
-// Wavefronts per workgroup: 16, or 8 for four query heads per KV head (whose registers need two
-// wavefronts' share); steps per load batch: 4, or 2 for four query heads (with four heads'
-// accumulators per lane the two-step batch measures about 11% faster at 32768 keys and the same
-// at 4096 and below); keys one workgroup loads in one batch per wavefront.
-__host__ __device__ constexpr int lanes_waves(int G) { return G >= 4 ? 8 : 16; }
+// Steps per load batch: 4, or 2 for four query heads per workgroup (with four heads'
+// accumulators per lane the two-step batch measured about 11% faster at 32768 keys and the same at
+// 4096 and below); keys one wavefront loads per batch; the legacy workgroup size (16 wavefronts, 8
+// for four query heads) and the keys such a workgroup loads in one batch.
 __host__ __device__ constexpr int lanes_nb(int G) { return G >= 4 ? 2 : 4; }
-__host__ __device__ constexpr int lanes_keys(int D, int G) { return lanes_waves(G) * (64 / (D / 8)) * lanes_nb(G); }
+__host__ __device__ constexpr int lanes_batch(int D, int G) { return (64 / (D / 8)) * lanes_nb(G); }
+__host__ __device__ constexpr int lanes_waves(int G) { return G >= 4 ? 8 : 16; }
+__host__ __device__ constexpr int lanes_keys(int D, int G) { return lanes_waves(G) * lanes_batch(D, G); }
+
+// Wavefronts per workgroup for a split of `chunk` keys: about one load batch each, 4, 8 or 16.
+// Measured on MI355X (32 query heads on 8 KV heads of 128, one query row): a workgroup's
+// wavefronts wait at the merge for the slowest of them, and 16 per workgroup left each of them a
+// few keys, so 4-8 wavefronts and more splits end 1.5-2.4 us sooner at 512-1024 keys.
+__host__ __device__ constexpr int lanes_nw(int D, int G, int chunk) {
+    return (chunk + lanes_batch(D, G) - 1) / lanes_batch(D, G) <= 4   ? 4
+           : (chunk + lanes_batch(D, G) - 1) / lanes_batch(D, G) <= 8 ? 8
+                                                                       : 16;
+}
 
 // f16 value c (0..7) of 8 packed in a uint4, as f32.
 __device__ __forceinline__ float half_at(const uint4 & r, int c) {
@@ -61,7 +72,6 @@ __device__ __forceinline__ void attn_lanes_task(const float * __restrict__ q, in
     constexpr int KPW = 64 / LPK;  // lane groups (keys per step) per wavefront
     constexpr int NB = lanes_nb(G);  // steps per load batch
     static_assert(G * D <= NW * 64, "one output per thread in the merge");
-    static_assert(NW == lanes_waves(G) && NW * KPW * NB == lanes_keys(D, G), "decode split size");
 
     // Split and wavefront ranges come from the host's chunk, so the K/V addresses do not wait for
     // the KV length read from device state; rows are clamped into the kv_rows that exist and keys

@@ -62,12 +62,12 @@ bool argmax_split_fits(int64_t rows, int64_t n);
 void launch_argmax_split(const float * x, int64_t ldx, int64_t rows, int64_t n, int32_t * out, void * scratch,
                          hipStream_t s);
 int decode_group(int GT, int max_kv);
-int decode_splits(int D, int G, int n_kv, int max_split);
+int decode_splits(int D, int H, int G, int n_kv, int max_split, bool wide);
 bool attn_decode_fits(int D, int G);
 void launch_attn_decode(const float * q, int64_t q_h, const void * k, int64_t k_h, int64_t k_j, const void * v,
                         int64_t v_h, int64_t v_j, int D, int H, int Hkv, int n_kv, const int * n_kv_dev, float scale,
                         int nsplit, int chunk, int kv_rows, int GS, float * out, float * part_o, float2 * part_ml,
-                        hipStream_t s, const Prefetch * pf, const void * mask);
+                        hipStream_t s, const Prefetch * pf, const void * mask, int nw_lanes);
 
 namespace {
 
@@ -1277,7 +1277,7 @@ struct Planner {
         std::memcpy(&s.f[0], &fa->op_params[0], 4);
         // split plan: as many splits as the merge prologue holds at most
         const int GS = decode_group((int) (H / Hkv), (int) n_kv);
-        const int nsplit = decode_splits((int) D, GS, (int) n_kv, row_gemv_merge_max());
+        const int nsplit = decode_splits((int) D, (int) H, GS, (int) n_kv, row_gemv_merge_max(), true);
         s.g.sne[0] = GS;
         s.g.sne[1] = nsplit;
         s.g.sne[2] = (n_kv + nsplit - 1) / nsplit;
@@ -1561,7 +1561,7 @@ void run_step(const ggml_backend * be, const Step & s) {
             float * row = (float *) ((uint8_t *) pml + align256((size_t) H * nsplit * 8));
             launch_attn_decode((const float *) s.in[0], s.n[0], s.in[1], s.n[1], s.n[2], s.in[2], s.n[3], s.n[4],
                                (int) D, (int) H, (int) Hkv, (int) n_kv, nullptr, s.f[0], nsplit, chunk, (int) n_kv, GS,
-                               row, po, pml, st, nullptr, s.in[3]);
+                               row, po, pml, st, nullptr, s.in[3], 16);
             const WeightLayout L = weight_layout(s.type, N, K);
             RowArgs a{};
             a.wqs = (const uint8_t *) s.in[4] + L.qs;

@@ -54,12 +54,12 @@ void launch_move_rows(const void * src, void * dst, const int32_t * map, int64_t
                       hipStream_t s);
 void launch_scatter_cols(const float * src, int64_t lds, float * dst, int64_t ldd, const int32_t * map, int S, int n,
                          hipStream_t s);
-AttnPlan attn_plan_decode(int D, int G, int max_ctx, int max_split);
+AttnPlan attn_plan_decode(int D, int H, int G, int max_ctx, int max_split);
 bool attn_decode_fits(int D, int G);
 void launch_attn_decode(const float * q, int64_t q_h, const void * k, int64_t k_h, int64_t k_j, const void * v,
                         int64_t v_h, int64_t v_j, int D, int H, int Hkv, int n_kv, const int * n_kv_dev, float scale,
                         int nsplit, int chunk, int kv_rows, int GS, float * out, float * part_o, float2 * part_ml,
-                        hipStream_t s, const Prefetch * pf, const void * mask);
+                        hipStream_t s, const Prefetch * pf, const void * mask, int nw_lanes);
 int decode_group(int GT, int max_kv);
 void launch_embed_rope(int type, const void * tab, int64_t nrows, int64_t D, const int32_t * idx, float * x,
                        const int32_t * pos, int head_dim, float base, void * cs, hipStream_t s);
@@ -215,7 +215,8 @@ struct Llama {
         // gate/up are then packed in row pairs (rope pairs, gate/up pairs) for their epilogues.
         decode_attn = attn_decode_fits(c.head_dim, c.n_head / c.n_head_kv);
         if (const char * e = std::getenv("GCQ_DECODE_PREFETCH")) prefetch = std::string(e) == "1";
-        plan_decode = decode_attn ? attn_plan_decode(c.head_dim, c.n_head / c.n_head_kv, c.max_ctx, row_gemv_merge_max())
+        plan_decode = decode_attn ? attn_plan_decode(c.head_dim, c.n_head, c.n_head / c.n_head_kv, c.max_ctx,
+                                                     row_gemv_merge_max())
                                   : attn_plan(1, c.n_head_kv, c.max_ctx);
         fused = row_gemv_fits(c.wtype, c.n_embd) && row_gemv_fits(c.wtype, attn_dim) &&
                 row_gemv_fits(c.wtype, c.n_ff) && c.head_dim % 4 == 0 &&
@@ -521,7 +522,7 @@ struct Llama {
                                kv_h, c.head_dim, c.head_dim, c.n_head, c.n_head_kv, n_kv, n_kv_dev, scale,
                                plan.nsplit, plan.chunk, c.max_ctx, decode_group(c.n_head / c.n_head_kv, c.max_ctx),
                                attn_row.as<float>(), part_o.as<float>(), part_ml.as<float2>(), stream,
-                               prefetch ? &pf : nullptr, nullptr);
+                               prefetch ? &pf : nullptr, nullptr, 16);
         } else {
             launch_attn_split(qkv.as<float>(), c.head_dim, qkv_dim, kvl, kv_h, c.head_dim,
                               kvl + (size_t) c.n_head_kv * kv_h, kv_h, c.head_dim, nullptr, n_kv, c.head_dim, 1,

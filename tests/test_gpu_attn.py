@@ -74,13 +74,16 @@ def test_prefill_rows(gops, orc):
     assert orc.parity(out, orc.flash_attn_ext(q, kc, vc, m16, 1 / np.sqrt(D))) < TOL
 
 
-@pytest.mark.parametrize("n_kv", [1, 17, 700, 1024, 1500, 4096, 32768])
+@pytest.mark.parametrize("n_kv", [1, 17, 129, 700, 1024, 1500, 2048, 2049, 4096, 32768])
 @pytest.mark.parametrize("H,Hkv,D", [(32, 8, 128), (8, 8, 128), (8, 4, 64), (16, 4, 64), (64, 8, 128), (16, 2, 64)])
 def test_decode_kernel_no_mask(gops, orc, n_kv, H, Hkv, D):
-    """One query row takes the matrix-core decode kernel (16-key blocks per wavefront, Q·Kᵀ and
-    Vᵀ·P on MFMA, online softmax per head, wavefronts merged in LDS, splits merged by
-    k_attn_merge): against the oracle within 1e-3, 1 to 8 query heads per KV head. 17 keys leave
-    most wavefronts without a key; 1500 ends inside a 16-key block."""
+    """One query row: up to 2048 keys the lane-group kernel (splits of 64 keys at D = 128, 128 at
+    D = 64, at most 512 / H of them, 4, 8 or 16 wavefronts each), beyond it the matrix-core kernel
+    (16-key blocks per wavefront, Q·Kᵀ and Vᵀ·P on MFMA, online softmax per head, wavefronts merged
+    in LDS); splits merged by k_attn_merge. Against the oracle within 1e-3, 1 to 8 query heads per
+    KV head. 17 keys leave most wavefronts without a key; 129 gives three splits of 43 keys; 1500
+    ends inside a 16-key block; 2048 / 2049 are the last lane-group and first matrix-core
+    lengths."""
     q, kc, vc, _ = _case(orc, H, Hkv, 1, n_kv, D, n_kv, seed=45)
     out = _run(gops, q, kc, vc, None, n_kv, 1 / np.sqrt(D))
     ref = orc.flash_attn_ext(q, kc, vc, None, 1 / np.sqrt(D))
