@@ -104,15 +104,21 @@ __global__ __launch_bounds__(256) void k_rope_neox(const float * __restrict__ x,
 
 // The (cos, sin) pairs k_rope_neox builds for position pos[0], written out: the table the
 // decode-row GEMV's rope epilogue reads (same arithmetic, so the same rotations).
-__global__ void k_rope_table(const int32_t * __restrict__ pos, int n_dims, float theta_scale, float freq_scale,
-                             float attn_factor, const float * __restrict__ ff, float2 * __restrict__ cs) {
-    const int i = threadIdx.x;
-    if (i >= n_dims / 2) return;
+__device__ __forceinline__ void rope_table_at(int i, const int32_t * __restrict__ pos, float theta_scale,
+                                              float freq_scale, float attn_factor, const float * __restrict__ ff,
+                                              float2 * __restrict__ cs) {
     float theta = (float) pos[0];
     for (int k = 0; k < i; k++) theta *= theta_scale;
     const float f = ff ? ff[i] : 1.0f;
     const float th = freq_scale * (theta / f);
     cs[i] = make_float2(cosf(th) * attn_factor, sinf(th) * attn_factor);
+}
+
+__global__ void k_rope_table(const int32_t * __restrict__ pos, int n_dims, float theta_scale, float freq_scale,
+                             float attn_factor, const float * __restrict__ ff, float2 * __restrict__ cs) {
+    const int i = threadIdx.x;
+    if (i >= n_dims / 2) return;
+    rope_table_at(i, pos, theta_scale, freq_scale, attn_factor, ff, cs);
 }
 
 // ------------------------------------------------------------------------------ set_rows
@@ -155,12 +161,17 @@ __global__ void k_set_rows_f16(uint16_t * __restrict__ dst, int64_t dst_h, int64
 
 // ------------------------------------------------------------------------------ get_rows
 
+__device__ __forceinline__ void get_rows_at(int64_t t, int type, const uint8_t * __restrict__ tab, int64_t nrows_tab,
+                                            int D, const int32_t * __restrict__ idx, float * __restrict__ out) {
+    const int j = (int) (t / D), c = (int) (t % D);
+    out[t] = table_value(type, tab, nrows_tab, D, idx[j], c);
+}
+
 __global__ void k_get_rows(int type, const uint8_t * __restrict__ tab, int64_t nrows_tab, int D,
                            const int32_t * __restrict__ idx, float * __restrict__ out, int n) {
     const int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= (int64_t) n * D) return;
-    const int j = (int) (t / D), c = (int) (t % D);
-    out[t] = table_value(type, tab, nrows_tab, D, idx[j], c);
+    get_rows_at(t, type, tab, nrows_tab, D, idx, out);
 }
 
 // ---------------------------------------------------------------------- swiglu, add, mul
@@ -444,9 +455,8 @@ __global__ void k_fill_ids(int32_t * __restrict__ dst, int64_t n, uint64_t seed,
 // Element i in row-major order of the logical shape: source element (shape sne, byte strides snb)
 // to destination element (dne, dnb); the two shapes have the same element count. f32 / f16 either
 // side, f32 -> f16 rounding to nearest even as ggml's conversion.
-__global__ void k_cpy(const uint8_t * __restrict__ src, int st, uint8_t * __restrict__ dst, int dt, Cpy4 g, int64_t n) {
-    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
+__device__ __forceinline__ void cpy_at(int64_t i, const uint8_t * __restrict__ src, int st, uint8_t * __restrict__ dst,
+                                       int dt, const Cpy4 & g) {
     int64_t r = i, so = 0, dof = 0;
 #pragma unroll
     for (int k = 0; k < 4; k++) {
@@ -467,6 +477,36 @@ __global__ void k_cpy(const uint8_t * __restrict__ src, int st, uint8_t * __rest
                                 : h2f(*reinterpret_cast<const uint16_t *>(src + so));
     if (dt == T_F32) *reinterpret_cast<float *>(dst + dof) = v;
     else *reinterpret_cast<uint16_t *>(dst + dof) = f2h(v);
+}
+
+__global__ void k_cpy(const uint8_t * __restrict__ src, int st, uint8_t * __restrict__ dst, int dt, Cpy4 g, int64_t n) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    cpy_at(i, src, st, dst, dt, g);
+}
+
+// ------------------------------------------------------------------------------ small jobs
+
+// Up to three independent get_rows / cpy / rope-table jobs in one launch (a graph's first steps:
+// the embedding row, the mask's cast, the rotation table). Job k takes blocks first[k] ..
+// first[k + 1] - 1 and runs the same per-element code as its own kernel, so its values are the
+// same. Independent: no job reads or writes what another writes (the caller checks).
+__device__ __forceinline__ void small_job_at(const SmallJob & j, int64_t t) {
+    if (t >= j.n) return;
+    if (j.kind == SJ_GETROWS)
+        get_rows_at(t, j.type, (const uint8_t *) j.src, j.rows, j.D, (const int32_t *) j.aux, (float *) j.dst);
+    else if (j.kind == SJ_CPY)
+        cpy_at(t, (const uint8_t *) j.src, j.type, (uint8_t *) j.dst, j.type2, j.g);
+    else
+        rope_table_at((int) t, (const int32_t *) j.src, j.f[0], j.f[1], j.f[2], (const float *) j.aux,
+                      (float2 *) j.dst);
+}
+
+__global__ __launch_bounds__(256) void k_small_jobs(SmallJobs js) {
+    const unsigned b = blockIdx.x;
+    if (js.nj > 2 && b >= js.first[2]) small_job_at(js.j[2], (int64_t) (b - js.first[2]) * 256 + threadIdx.x);
+    else if (js.nj > 1 && b >= js.first[1]) small_job_at(js.j[1], (int64_t) (b - js.first[1]) * 256 + threadIdx.x);
+    else small_job_at(js.j[0], (int64_t) b * 256 + threadIdx.x);
 }
 
 __global__ void k_repeat(const uint8_t * __restrict__ src, float * __restrict__ dst, Cpy4 g, int64_t n) {
@@ -631,6 +671,65 @@ void launch_argmax_split(const float * x, int64_t ldx, int64_t rows, int64_t n, 
     float2 * part = (float2 *) ((uint8_t *) scratch + 256);
     k_argmax_split<<<dim3(slices, (unsigned) rows), 256, 0, s>>>(x, ldx, (int) n, out, part, counter);
     check_launch("argmax split");
+}
+
+SmallJob small_job_get_rows(int type, const void * tab, int64_t nrows_tab, int64_t D, const int32_t * idx, int64_t n,
+                            float * out) {
+    SmallJob j{};
+    j.kind = SJ_GETROWS;
+    j.type = type;
+    j.D = (int) D;
+    j.n = n * D;
+    j.src = tab;
+    j.aux = idx;
+    j.dst = out;
+    j.rows = nrows_tab;
+    return j;
+}
+
+SmallJob small_job_cpy(const void * src, int st, void * dst, int dt, const Cpy4 & g, int64_t n) {
+    SmallJob j{};
+    j.kind = SJ_CPY;
+    j.type = st;
+    j.type2 = dt;
+    j.n = n;
+    j.src = src;
+    j.dst = dst;
+    j.g = g;
+    return j;
+}
+
+SmallJob small_job_rope_table(const int32_t * pos, int n_dims, float freq_base, float freq_scale, float attn_factor,
+                              const float * ff, float2 * cs) {
+    require(n_dims > 0 && n_dims % 2 == 0 && n_dims <= 256, "rope table: n_dims must be even, <= 256");
+    SmallJob j{};
+    j.kind = SJ_ROPE_TABLE;
+    j.D = n_dims;
+    j.n = n_dims / 2;
+    j.src = pos;
+    j.aux = ff;
+    j.dst = cs;
+    j.f[0] = powf(freq_base, -2.0f / (float) n_dims);  // theta_scale, as launch_rope_table
+    j.f[1] = freq_scale;
+    j.f[2] = attn_factor;
+    return j;
+}
+
+void launch_small_jobs(const SmallJob * jobs, int n, hipStream_t s) {
+    require(n >= 1 && n <= 3, "small jobs: 1 to 3 per launch");
+    SmallJobs js{};
+    js.nj = n;
+    unsigned blocks = 0;
+    for (int k = 0; k < n; k++) {
+        js.j[k] = jobs[k];
+        js.first[k] = blocks;
+        const int64_t nb = (jobs[k].n + 255) / 256;
+        require(jobs[k].n >= 0 && blocks + nb < (1u << 30), "small jobs: too many threads");
+        blocks += (unsigned) nb;
+    }
+    if (blocks == 0) return;
+    k_small_jobs<<<blocks, 256, 0, s>>>(js);
+    check_launch("small jobs");
 }
 
 void launch_cpy(const void * src, int st, void * dst, int dt, const Cpy4 & g, int64_t n, hipStream_t s) {

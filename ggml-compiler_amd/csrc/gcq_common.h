@@ -225,6 +225,29 @@ struct Cpy4 {
 };
 void launch_cpy(const void * src, int st, void * dst, int dt, const Cpy4 & g, int64_t n, hipStream_t s);
 
+// One get_rows / cpy / rope-table job of k_small_jobs (n threads, one element each).
+enum { SJ_GETROWS = 0, SJ_CPY = 1, SJ_ROPE_TABLE = 2 };
+struct SmallJob {
+    int kind, type, type2, D;  // get_rows: table type, row length; cpy: source, destination type; rope: n_dims
+    int64_t n, rows;           // threads; get_rows: table rows
+    const void * src;          // table / cpy source / positions
+    const void * aux;          // get_rows: indices; rope: frequency factors (or null)
+    void * dst;
+    float f[3];  // rope: theta_scale, freq_scale, attn_factor
+    Cpy4 g;      // cpy: shapes and strides
+};
+struct SmallJobs {
+    SmallJob j[3];
+    int nj;
+    unsigned first[3];  // job k's first block
+};
+SmallJob small_job_get_rows(int type, const void * tab, int64_t nrows_tab, int64_t D, const int32_t * idx, int64_t n,
+                            float * out);
+SmallJob small_job_cpy(const void * src, int st, void * dst, int dt, const Cpy4 & g, int64_t n);
+SmallJob small_job_rope_table(const int32_t * pos, int n_dims, float freq_base, float freq_scale, float attn_factor,
+                              const float * ff, float2 * cs);
+void launch_small_jobs(const SmallJob * jobs, int n, hipStream_t s);
+
 // A second tensor for one launch of rope / set_rows (q and k; k and v of a layer), same positions.
 struct RopeSecond {
     const float * x;

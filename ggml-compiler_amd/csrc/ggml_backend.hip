@@ -511,6 +511,7 @@ enum StepKind {
     S_QKV_ROPE,     // q / k / v GEMVs with q / k rope and k / v cache writes in the epilogue
     S_GATE_UP,      // gate / up GEMVs of one normalized row with swiglu in the epilogue
     S_MULMAT_F,     // mul_mat of an f32 / f16 first operand (activations, KV-cache views)
+    S_JOBS,         // the next n[0] steps (get_rows / cpy / rope table, independent) as one launch
 };
 
 // One launch sequence with every argument it takes; compared byte for byte to decide whether a
@@ -1338,6 +1339,71 @@ struct Planner {
         }
     }
 
+    // Runs of 2 or 3 consecutive small get_rows / cpy / rope-table steps, none reading or writing
+    // what another of the run writes, become one launch: an S_JOBS marker in front of them (a
+    // decode graph's embedding row, mask cast and rotation table are such a run).
+    void group_small_steps() {
+        if (dry || !be->fuse) return;
+        struct Span {
+            uintptr_t lo, hi;
+        };
+        auto extent = [](const int64_t * ne, const int64_t * nb, int64_t es) {
+            int64_t e = es;
+            for (int k = 0; k < 4; k++) e += (ne[k] - 1) * nb[k];
+            return e;
+        };
+        // the bytes a step reads (up to two spans) and writes; false: not a small job
+        auto spans = [&](const Step & s, Span (&rd)[2], Span & wr) {
+            auto sp = [](const void * p, int64_t n) { return Span{(uintptr_t) p, (uintptr_t) p + (uintptr_t) n}; };
+            if (s.kind == S_GETROWS) {
+                if (s.n[1] * s.n[2] > (1 << 20)) return false;
+                rd[0] = sp(s.in[0], s.n[0] * (int64_t) row_bytes(s.type, s.n[1]));
+                rd[1] = sp(s.in[1], s.n[2] * 4);
+                wr = sp(s.out, s.n[1] * s.n[2] * 4);
+                return true;
+            }
+            if (s.kind == S_CPY) {
+                if (s.n[0] > (1 << 20)) return false;
+                const int64_t ss = s.type == T_F16 ? 2 : 4, ds = s.op == T_F16 ? 2 : 4;
+                rd[0] = sp(s.in[0], extent(s.g.sne, s.g.snb, ss));
+                rd[1] = sp(s.in[0], 0);
+                wr = sp(s.out, extent(s.g.dne, s.g.dnb, ds));
+                return true;
+            }
+            if (s.kind == S_ROPE_TABLE) {
+                rd[0] = sp(s.in[0], 4);
+                rd[1] = rd[0];
+                wr = sp(be->rope_cs, s.n[0] / 2 * (int64_t) sizeof(float2));
+                return true;
+            }
+            return false;
+        };
+        auto meet = [](Span a, Span b) { return a.lo < b.hi && b.lo < a.hi; };
+        std::vector<Step> out;
+        out.reserve(steps.size() + 4);
+        for (size_t i = 0; i < steps.size();) {
+            Span rd[3][2], wr[3];
+            size_t n = 0;
+            while (n < 3 && i + n < steps.size() && spans(steps[i + n], rd[n], wr[n])) {
+                bool free = true;
+                for (size_t k = 0; k < n && free; k++)
+                    free = !meet(wr[k], wr[n]) && !meet(wr[k], rd[n][0]) && !meet(wr[k], rd[n][1]) &&
+                           !meet(wr[n], rd[k][0]) && !meet(wr[n], rd[k][1]);
+                if (!free) break;
+                n++;
+            }
+            if (n >= 2) {
+                Step m = new_step(S_JOBS);
+                m.n[0] = (int64_t) n;
+                out.push_back(m);
+            }
+            const size_t take = std::max<size_t>(n, 1);
+            for (size_t k = 0; k < take; k++) out.push_back(steps[i + k]);
+            i += take;
+        }
+        steps.swap(out);
+    }
+
     // The chain ending at node f (members before it, in order).
     void chain(const ggml_cgraph * g, const std::vector<int> & idx) {
         const ggml_tensor * first = g->nodes[idx.front()];
@@ -1368,6 +1434,15 @@ struct Planner {
 };
 
 // ------------------------------------------------------------------------------- running
+
+// A small step as a job of k_small_jobs (the same arguments as its own launch below).
+SmallJob small_job(const ggml_backend * be, const Step & s) {
+    if (s.kind == S_GETROWS)
+        return small_job_get_rows(s.type, s.in[0], s.n[0], s.n[1], (const int32_t *) s.in[1], s.n[2], (float *) s.out);
+    if (s.kind == S_CPY) return small_job_cpy(s.in[0], s.type, s.out, s.op, s.g, s.n[0]);
+    require(s.kind == S_ROPE_TABLE, "small jobs: get_rows, cpy or rope table steps only");
+    return small_job_rope_table((const int32_t *) s.in[0], (int) s.n[0], s.f[0], s.f[1], s.f[2], nullptr, be->rope_cs);
+}
 
 void run_step(const ggml_backend * be, const Step & s) {
     hipStream_t st = be->stream;
@@ -1585,6 +1660,23 @@ void run_step(const ggml_backend * be, const Step & s) {
     }
 }
 
+// The plan's steps in order; an S_JOBS marker launches the steps it covers as one kernel.
+void run_steps(const ggml_backend * be) {
+    const std::vector<Step> & v = be->steps;
+    for (size_t i = 0; i < v.size(); i++) {
+        if (v[i].kind != S_JOBS) {
+            run_step(be, v[i]);
+            continue;
+        }
+        const int n = (int) v[i].n[0];
+        require(n >= 1 && n <= 3 && i + (size_t) n < v.size(), "small jobs: bad run");
+        SmallJob j[3];
+        for (int k = 0; k < n; k++) j[k] = small_job(be, v[i + 1 + (size_t) k]);
+        launch_small_jobs(j, n, be->stream);
+        i += (size_t) n;
+    }
+}
+
 // Gives every view of g its base's memory (views made before their base was allocated, or whose
 // base has moved since).
 void refresh_views(ggml_cgraph * g) {
@@ -1641,13 +1733,14 @@ enum ggml_status compute(ggml_backend * be, ggml_cgraph * g, bool async = false)
         }
     }
     p.fold_result_copies(g);
+    p.group_small_steps();
     ensure_ws(be, p.ws_need);
     std::vector<uint8_t> sig((const uint8_t *) be->steps.data(),
                              (const uint8_t *) (be->steps.data() + be->steps.size()));
     const uint8_t * wsp = (const uint8_t *) &be->ws;
     sig.insert(sig.end(), wsp, wsp + sizeof(void *));
     if (!be->use_graphs) {
-        for (const Step & s : be->steps) run_step(be, s);
+        run_steps(be);
     } else {
         Cached & cc = be->graphs[g];
         if (!cc.exec || cc.sig != sig) {
@@ -1658,7 +1751,7 @@ enum ggml_status compute(ggml_backend * be, ggml_cgraph * g, bool async = false)
             check_hip(hipStreamBeginCapture(be->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
             hipGraph_t graph = nullptr;
             try {
-                for (const Step & s : be->steps) run_step(be, s);
+                run_steps(be);
             } catch (...) {
                 (void) hipStreamEndCapture(be->stream, &graph);
                 if (graph) (void) hipGraphDestroy(graph);

@@ -209,14 +209,17 @@ def test_qkv_rope_cache_writes_in_one_launch(be, orc, t):
     """The decode step's q / k / v GEMVs of one normalized row, the q and k ropes and the k / v
     set_rows into f16 caches (built as the reference builds them) run as one launch whose epilogue
     ropes and writes the caches; the roped q and both caches equal the unfused graph's (each
-    intermediate marked as an output, which keeps them apart) to 1e-6."""
+    intermediate marked as an output, which keeps them apart) to 1e-6. The row is an embedding
+    row (get_rows), whose launch also builds the epilogue's rotation table."""
     K, H, Hkv, D, ctx, p = 2048, 8, 2, 128, 64, 13
     tid = orc.TYPES[t]
     raws = [_weight(orc, t, N, K, 150 + i) for i, N in enumerate((H * D, Hkv * D, Hkv * D))]
     x = orc.normal((1, K), seed=154)
     nw = (1.0 + 0.1 * orc.normal((K,), seed=155)).astype(np.float32)
-    leaves = {"x": (G.F32, [K, 1], x), "nw": (G.F32, [K], nw), "pos": (G.I32, [1], np.array([p], np.int32)),
-              "ck": (G.F16, [D, ctx, Hkv], None), "cv": (G.F16, [D, ctx, Hkv], None)}
+    emb = np.concatenate([orc.normal((2, K), seed=156), x])  # x: row 2 of an embedding table
+    leaves = {"emb": (G.F32, [K, 3], emb), "tok": (G.I32, [1], np.array([2], np.int32)), "nw": (G.F32, [K], nw),
+              "pos": (G.I32, [1], np.array([p], np.int32)), "ck": (G.F16, [D, ctx, Hkv], None),
+              "cv": (G.F16, [D, ctx, Hkv], None)}
     for i, raw in enumerate(raws):
         leaves[f"w{i}"] = (tid, [K, raw.shape[0]], raw)
     res = {}
@@ -224,7 +227,8 @@ def test_qkv_rope_cache_writes_in_one_launch(be, orc, t):
         keep = {}
 
         def build(g, ctx_, L):
-            n = g.ggml_mul(ctx_, g.ggml_rms_norm(ctx_, L["x"], 1e-5), L["nw"])
+            xr = g.ggml_get_rows(ctx_, L["emb"], L["tok"])  # with the fused launch: one of the rotation table
+            n = g.ggml_mul(ctx_, g.ggml_rms_norm(ctx_, xr, 1e-5), L["nw"])
             q, k, v = (g.ggml_mul_mat(ctx_, L[f"w{i}"], n) for i in range(3))
             rp = (D, 2, 0, 500000.0, 1.0, 0.0, 1.0, 32.0, 1.0)
             q = g.ggml_rope_ext(ctx_, g.ggml_reshape_3d(ctx_, q, D, H, 1), L["pos"], None, *rp)
@@ -557,6 +561,41 @@ def test_set_rows_then_get_rows(be, orc):
     gr.close()
     assert np.array_equal(y, orc.dequantize(tab[ids], "q4_0", E))
     assert np.array_equal(back.reshape(V, -1), tab)
+
+
+def test_small_steps_in_one_launch(be, orc):
+    """A decode graph's first steps, the embedding row (get_rows of a Q8_0 table), the mask's f16
+    cast (0 and -inf) and a strided f32 -> f16 copy, read nothing another writes and run as one
+    launch of three jobs: each result bit-exact (dequantized rows, f16 rounding); then the same
+    graph replayed with new indices and mask values."""
+    V, E, n_kv = 50, 4096, 768
+    tab = _weight(orc, "q8_0", V, E, 93)
+    a = orc.normal((3, 5, 8), seed=94)
+    outs = {}
+
+    def build(g, ctx, L):
+        outs["rows"] = g.ggml_get_rows(ctx, L["t"], L["i"])
+        outs["mask"] = g.ggml_cast(ctx, L["m"], G.F16)
+        outs["perm"] = g.ggml_cast(ctx, g.ggml_permute(ctx, L["a"], 0, 2, 1, 3), G.F16)
+        for t in outs.values():
+            g.ggml_set_output(t)
+        return list(outs.values())
+
+    ids = np.array([49, 3], np.int32)
+    mask = np.where(np.arange(n_kv) <= 517, 0.0, -np.inf).astype(np.float32)
+    gr = Graph(be, {"t": (G.Q8_0, [E, V], tab), "i": (G.I32, [2], ids), "m": (G.F32, [n_kv, 1], mask),
+                    "a": (G.F32, [8, 5, 3], a)}, build)
+    for step in range(2):
+        gr.run()
+        got = {k: G.get_data(t, NP[G.T(t).type]) for k, t in outs.items()}
+        assert np.array_equal(got["rows"].reshape(2, E), orc.dequantize(tab[ids], "q8_0", E)), step
+        assert np.array_equal(got["mask"], orc.fp32_to_fp16(mask)), step
+        assert np.array_equal(got["perm"], orc.fp32_to_fp16(a.transpose(1, 0, 2)).reshape(-1)), step
+        ids = np.array([0, 17], np.int32)
+        mask = np.where(np.arange(n_kv) % 3 == 0, -np.inf, 0.25 * np.arange(n_kv)).astype(np.float32)
+        G.set_data(gr.L["i"], ids)
+        G.set_data(gr.L["m"], mask)
+    gr.close()
 
 
 def test_cont_cast_scale_binary_argmax(be, orc):
