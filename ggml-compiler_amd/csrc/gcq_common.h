@@ -133,6 +133,9 @@ struct RowArgs {
     int64_t ctx;
     int H, Hkv, D;
     int xc;  // set by launch_row_gemv: the x waves take row groups too (PLAIN / NORM)
+    // set by launch_row_gemv for EPI_ROPE_KV: floor(2^32 / (D/2)) + 1, so that x / (D/2) =
+    // mulhi(x, hd_magic) for every 0 <= x < 2^32 / (D/2) (one scalar multiply, no branch)
+    uint32_t hd_magic;
     // Several weights of one row length read by the same row (q / k / v, gate / up), EPI_STORE:
     // rows [r_end[k-1], r_end[k]) are weight k's, its codes and scales at byte offsets r_qs[k] /
     // r_d[k] from wqs / wd (spans qs_span / d_span bytes, < 2 GB), its results to r_y[k].

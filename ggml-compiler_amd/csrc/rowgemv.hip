@@ -76,30 +76,25 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
     // is the rotation pair (i, i + D/2) of q head h (h < H) or k head h - H, then pairs of v rows;
     // EPI_SWIGLU takes separate gate and up weights (ranges 0, 1): group g is gate row g and up
     // row g, the pair the packed gate/up weight holds in group g.
-    // x / (D/2) for the rope epilogue's group indices: a shift for the power-of-two head sizes (a
+    // x / (D/2) for the rope epilogue's group indices (x >= 0): the high half of x * hd_magic (a
     // division by a value known only at run time is a chain of some 30 dependent instructions,
-    // which in front of a group's weight loads delays them).
+    // and a choice between it and a shift a branch, either of which in front of a group's weight
+    // loads delays them).
     const int hd = a.D >> 1;
-    const int hsh = hd > 0 && (hd & (hd - 1)) == 0 ? __builtin_ctz(hd) : -1;
-    auto div_hd = [&](int x) -> int {
-        if (hsh >= 0) return x >> hsh;
-        return x / hd;
-    };
+    auto div_hd = [&](int x) -> int { return (int) __umulhi((uint32_t) x, a.hd_magic); };
     auto map_row = [&](int g, int r, int & local) -> int {
         if constexpr (EPI == EPI_SWIGLU) {
             local = min(__builtin_amdgcn_readfirstlane(g), a.r_end[0] - 1);
             return r;
         } else if constexpr (EPI == EPI_ROPE_KV) {
+            // both cases computed and one selected: scalar selects, no branch
             g = __builtin_amdgcn_readfirstlane(g);
             const int nq = (a.H + a.Hkv) * hd;
-            if (g < nq) {
-                const int h = div_hd(g), i = g - h * hd;
-                const bool qh = h < a.H;
-                local = (qh ? h : h - a.H) * a.D + i + r * hd;
-                return qh ? 0 : 1;
-            }
-            local = min(2 * (g - nq) + r, a.Hkv * a.D - 1);
-            return 2;
+            const int gq = min(g, nq - 1);
+            const int h = div_hd(gq), i = gq - h * hd;
+            const bool qh = h < a.H, vg = g >= nq;
+            local = vg ? min(2 * (g - nq) + r, a.Hkv * a.D - 1) : (qh ? h : h - a.H) * a.D + i + r * hd;
+            return vg ? 2 : qh ? 0 : 1;
         } else {
             return range_of(min(g * R + r, a.N - 1), local);
         }
@@ -490,6 +485,11 @@ void run_row_r(const RowArgs & a0, hipStream_t s) {
     // The x waves compute too for long rows and when all 16 wavefronts of every CU take the
     // groups in one round but the compute waves alone would need two.
     a.xc = PRO != PRO_MERGE && (nbl > 4 || (ng <= 16 * cus && ng > (16 - xw) * cus));
+    if constexpr (EPI == EPI_ROPE_KV) {
+        const uint64_t hd = (uint64_t) (a.D / 2);
+        require(hd > 0 && (uint64_t) a.N * hd < (1ull << 32), "row gemv: rope epilogue indices past 2^32 / (D/2)");
+        a.hd_magic = (uint32_t) ((1ull << 32) / hd + 1);
+    }
     const int cw = (PRO == PRO_MERGE || a.xc) ? 16 : 16 - xw;  // the kernel's CW
     const int waves = cus * cw;
     // As many workgroups as give every compute wavefront the same whole number of groups (no
