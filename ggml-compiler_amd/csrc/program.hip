@@ -1504,7 +1504,7 @@ struct ggml_compiler_model {
         const size_t tensors = 8 * st.nodes.size() + 2 * st.outputs.size() + 16;
         const size_t graph_nodes = tensors + st.params.size() + file.tensors.size() + 64;
         ggml_init_params ip{};
-        ip.mem_size = ggml_tensor_overhead() * tensors + ggml_graph_overhead_custom(graph_nodes, false);
+        ip.mem_size = ggml_tensor_overhead() * tensors + 2 * ggml_graph_overhead_custom(graph_nodes, false);
         ip.no_alloc = true;
         c.ctx = ggml_init(ip);
         std::unordered_map<std::string, ggml_tensor *> env;
@@ -1518,6 +1518,23 @@ struct ggml_compiler_model {
         }
         const std::vector<ggml_tensor *> results = stage_results(c, st, env);
         c.graph = ggml_new_graph_custom(c.ctx, graph_nodes, false);
+        // get_rows / copies that read only the stage's parameters and weights (an embedding row, a
+        // mask's cast) come first, in their order: any topological order computes the same, and
+        // at the front the executor can run such small steps together in one launch.
+        ggml_cgraph * probe = ggml_new_graph_custom(c.ctx, graph_nodes, false);
+        for (ggml_tensor * t : results) ggml_build_forward_expand(probe, t);
+        for (int k = 0; k < ggml_graph_n_nodes(probe); k++) {
+            ggml_tensor * t = ggml_graph_node(probe, k);
+            if (t->op != GGML_OP_GET_ROWS && t->op != GGML_OP_CPY) continue;
+            bool leaves = true;  // every source a leaf or a view of one (a bound value's view)
+            for (const ggml_tensor * src : t->src) {
+                while (src && (src->op == GGML_OP_VIEW || src->op == GGML_OP_RESHAPE || src->op == GGML_OP_PERMUTE ||
+                               src->op == GGML_OP_TRANSPOSE))
+                    src = src->src[0];
+                leaves = leaves && (!src || src->op == GGML_OP_NONE);
+            }
+            if (leaves) ggml_build_forward_expand(c.graph, t);
+        }
         for (ggml_tensor * t : results) ggml_build_forward_expand(c.graph, t);
         // Results reach their driver values through copies after every other node (so after
         // every read of the stage's arguments); a result that already is its value's memory (a
