@@ -217,7 +217,11 @@ static inline int nearest_int(float v) { return (int) lrintf(v); }
 /* ggml make_qkx2_quants(n=32, nmax, rmin, rdelta=0.1, nstep, use_mad=false): an asymmetric
  * (scale, min) fit by weighted least squares over nstep + 1 candidate scales. Q4_K calls it with
  * (nmax 15, rmin -1, nstep 20), Q5_K with (31, -0.5, 15). */
-static float make_qkx2(const float * x, const float * w, uint8_t * L, float * the_min, int nmax, float rmin, int nstep) {
+/* trace (optional, tests): row 0 the min/max fit, row 1 + s candidate s, QKX2_TRACE floats each:
+ * [iscale, D > 0, scale, min, weighted error, taken, min the codes were made against, 0, codes[32]]. */
+#define QKX2_TRACE 40
+static float make_qkx2(const float * x, const float * w, uint8_t * L, float * the_min, int nmax, float rmin, int nstep,
+                       float * trace) {
     const int n = 32;
     const float rdelta = 0.1f;
     uint8_t Laux[32];
@@ -247,13 +251,22 @@ static float make_qkx2(const float * x, const float * w, uint8_t * L, float * th
         const float diff = scale * L[i] + min - x[i];
         best += w[i] * (diff * diff);
     }
+    if (trace) {
+        float * t = trace;
+        t[0] = iscale, t[1] = 1, t[2] = scale, t[3] = min, t[4] = best, t[5] = 1, t[6] = min, t[7] = 0;
+        for (int i = 0; i < n; i++) t[8 + i] = L[i];
+    }
     for (int is = 0; is <= nstep; is++) {
+        float * t = trace ? trace + QKX2_TRACE * (1 + is) : NULL;
+        if (t) memset(t, 0, QKX2_TRACE * sizeof(float));
         iscale = (rmin + rdelta * is + nmax) / (max - min);
+        if (t) t[0] = iscale, t[6] = min;
         float sum_l = 0, sum_l2 = 0, sum_xl = 0;
         for (int i = 0; i < n; i++) {
             int l = nearest_int(iscale * (x[i] - min));
             l = l < 0 ? 0 : (l > nmax ? nmax : l);
             Laux[i] = (uint8_t) l;
+            if (t) t[8 + i] = (float) l;
             const float wi = w[i];
             sum_l += wi * l;
             sum_l2 += wi * l * l;
@@ -272,6 +285,7 @@ static float make_qkx2(const float * x, const float * w, uint8_t * L, float * th
                 const float diff = this_scale * Laux[i] + this_min - x[i];
                 mad += w[i] * (diff * diff);
             }
+            if (t) t[1] = 1, t[2] = this_scale, t[3] = this_min, t[4] = mad, t[5] = mad < best;
             if (mad < best) {
                 for (int i = 0; i < n; i++) L[i] = Laux[i];
                 best = mad;
@@ -282,6 +296,14 @@ static float make_qkx2(const float * x, const float * w, uint8_t * L, float * th
     }
     *the_min = -min;
     return scale;
+}
+
+/* The search of one 32-value sub-block alone (the fit enc_q4_K / enc_q5_K run per sub-block), for
+ * the tests that check each of its steps against the published definition; trace: NULL or
+ * (nstep + 2) x QKX2_TRACE floats (see make_qkx2). */
+float orc_make_qkx2(const float * x, const float * w, uint8_t * L, float * the_min, int nmax, float rmin, int nstep,
+                    float * trace) {
+    return make_qkx2(x, w, L, the_min, nmax, rmin, nstep, trace);
 }
 
 /* ggml get_scale_min_k4: 6-bit (scale, min) of sub-block j from the 12 packed bytes. */
@@ -333,7 +355,7 @@ static void enc_q4_K(const float * x, blk_q4_K * y, int64_t nb) {
             for (int l = 0; l < 32; l++) sum_x2 += x[32 * j + l] * x[32 * j + l];
             const float av_x = sqrtf(sum_x2 / 32);
             for (int l = 0; l < 32; l++) weights[l] = av_x + fabsf(x[32 * j + l]);
-            scales[j] = make_qkx2(x + 32 * j, weights, L + 32 * j, &mins[j], 15, -1.0f, 20);
+            scales[j] = make_qkx2(x + 32 * j, weights, L + 32 * j, &mins[j], 15, -1.0f, 20, NULL);
             if (scales[j] > max_scale) max_scale = scales[j];
             if (mins[j] > max_min) max_min = mins[j];
         }
@@ -368,7 +390,7 @@ static void enc_q5_K(const float * x, blk_q5_K * y, int64_t nb) {
             for (int l = 0; l < 32; l++) sum_x2 += x[32 * j + l] * x[32 * j + l];
             const float av_x = sqrtf(sum_x2 / 32);
             for (int l = 0; l < 32; l++) weights[l] = av_x + fabsf(x[32 * j + l]);
-            scales[j] = make_qkx2(x + 32 * j, weights, L + 32 * j, &mins[j], 31, -0.5f, 15);
+            scales[j] = make_qkx2(x + 32 * j, weights, L + 32 * j, &mins[j], 31, -0.5f, 15, NULL);
             if (scales[j] > max_scale) max_scale = scales[j];
             if (mins[j] > max_min) max_min = mins[j];
         }
@@ -453,6 +475,9 @@ static float make_qx16(const float * x, uint8_t * L) {
     }
     return scale;
 }
+
+/* The search of one 16-value sub-block alone (enc_q6_K's per-sub-block fit), for the tests. */
+float orc_make_qx16(const float * x, uint8_t * L) { return make_qx16(x, L); }
 
 /* ggml quantize_row_q6_K_ref: 16 sub-block fits (make_qx16), int8 scales against the scale of
  * largest magnitude (iscale = -128/max, d = 1/iscale), codes recomputed against the rounded

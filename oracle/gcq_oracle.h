@@ -46,6 +46,11 @@ size_t orc_row_size(int type, int64_t n);
 
 /* Weight encoders (ggml reference encoders, no importance matrix). Return bytes written or 0. */
 size_t orc_quantize(int type, const float * src, int64_t nrows, int64_t n_per_row, void * dst);
+/* The K-quant searches of one sub-block (make_qkx2_quants for Q4_K / Q5_K, make_qx_quants for Q6_K):
+ * codes L, the returned scale and (qkx2) the negated min; for tests of the search's choice. */
+float orc_make_qkx2(const float * x, const float * w, uint8_t * L, float * the_min, int nmax, float rmin, int nstep,
+                    float * trace);
+float orc_make_qx16(const float * x, uint8_t * L);
 /* Activation quantizers: Q8_0 (variant ORC_ACT_*) or Q8_K, k values. */
 void   orc_quantize_act_q8_0(const float * x, void * y, int64_t k, int variant);
 void   orc_quantize_act_q8_K(const float * x, void * y, int64_t k);

@@ -50,6 +50,8 @@ def lib() -> ctypes.CDLL:
         "orc_type_size": ([i32], ctypes.c_size_t),
         "orc_row_size": ([i32, i64], ctypes.c_size_t),
         "orc_quantize": ([i32, p, i64, i64, p], ctypes.c_size_t),
+        "orc_make_qkx2": ([p, p, p, p, i32, f, i32, p], f),
+        "orc_make_qx16": ([p, p], f),
         "orc_quantize_act_q8_0": ([p, p, i64, i32], None),
         "orc_quantize_act_q8_K": ([p, p, i64], None),
         "orc_dequantize": ([i32, p, p, i64, i64], i32),
@@ -119,6 +121,30 @@ def quantize(x: np.ndarray, t: int | str) -> np.ndarray:
     out = np.empty(x.shape[:-1] + (rs,), np.uint8)
     lib().orc_quantize(_tid(t), x.ctypes.data, rows, n, out.ctypes.data)
     return out
+
+
+def make_qkx2(x: np.ndarray, w: np.ndarray, nmax: int, rmin: float, nstep: int, trace: bool = False):
+    """One 32-value sub-block's (scale, min) search of the Q4_K / Q5_K encoder: (codes, scale, min),
+    and with trace the search's steps, float32 [nstep + 2, 40]: row 0 the min/max fit, row 1 + s
+    candidate s, each [iscale, D > 0, scale, min, weighted error, taken, min used, 0, codes[32]]."""
+    x, w = _c(x, np.float32), _c(w, np.float32)
+    assert x.size == 32 and w.size == 32
+    L = np.zeros(32, np.uint8)
+    neg_min = ctypes.c_float(0.0)
+    tr = np.zeros((nstep + 2, 40), np.float32) if trace else None
+    scale = lib().orc_make_qkx2(x.ctypes.data, w.ctypes.data, L.ctypes.data, ctypes.byref(neg_min), nmax, rmin, nstep,
+                                tr.ctypes.data if trace else None)
+    out = (L, float(scale), -float(neg_min.value))
+    return out + (tr,) if trace else out
+
+
+def make_qx16(x: np.ndarray):
+    """One 16-value sub-block's scale search of the Q6_K encoder: (codes l + 32, scale)."""
+    x = _c(x, np.float32)
+    assert x.size == 16
+    L = np.zeros(16, np.uint8)
+    scale = lib().orc_make_qx16(x.ctypes.data, L.ctypes.data)
+    return L, float(scale)
 
 
 def quantize_act_q8_0(x: np.ndarray, variant: int = ACT_AVX2) -> np.ndarray:
