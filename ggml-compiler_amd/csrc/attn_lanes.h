@@ -1,6 +1,5 @@
 // attn_lanes.h - the lane-group decode attention (one query row over an f16 KV cache), as a
-// device function shared by attn.hip's k_attn_lanes and the fused attention + output-projection
-// launch of attn_oproj.hip.
+// device function of attn.hip's k_attn_lanes.
 //
 // Short contexts (up to kLanesMaxKv keys) are latency-bound, so parallel work beats arithmetic
 // efficiency: one query row, one workgroup per (split, KV head, query-head group), NW wavefronts.
@@ -15,7 +14,6 @@
 #pragma once
 
 #include "gcq_common.h"
-#include "grid_sync.h"
 
 namespace gcq {
 

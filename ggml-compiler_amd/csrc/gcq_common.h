@@ -53,6 +53,20 @@ void check_hip(hipError_t e, const char * what);
 void check_launch(const char * what);
 
 inline hipStream_t as_stream(void * s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Device queries (attributes, occupancy, symbol addresses) that the first call on a device makes,
+// possibly while the calling thread captures a stream into a HIP graph: the thread's capture mode
+// is relaxed for their duration, so that no such query invalidates the capture.
+struct RelaxedCapture {
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    bool ok;
+    RelaxedCapture() { ok = hipThreadExchangeStreamCaptureMode(&mode) == hipSuccess; }
+    ~RelaxedCapture() {
+        if (ok) (void) hipThreadExchangeStreamCaptureMode(&mode);
+    }
+    RelaxedCapture(const RelaxedCapture &) = delete;
+    RelaxedCapture & operator=(const RelaxedCapture &) = delete;
+};
 __host__ __device__ inline size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 inline bool aligned(const void * p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
@@ -147,80 +161,9 @@ struct RowArgs {
 
 void launch_row_gemv(int type, int pro, int epi, const RowArgs & a, hipStream_t s);
 
-// Arguments of one decode layer's attention + output projection in a single launch
-// (attn_oproj.hip): the lane-group attention of the query row q over the layer's f16 caches, its
-// split partials in part_o / part_ml, a grid barrier, then x += W_o attn.
-struct AttnOArgs {
-    const float * q;            // [H][D] roped query row
-    const uint16_t * kc;        // [Hkv][kv_rows][D] f16 K cache of the layer
-    const uint16_t * vc;        // the same for V
-    int64_t kv_h;               // elements from one KV head to the next (kv_rows D)
-    int kv_rows;
-    const int * n_kv_dev;       // visible keys (device)
-    float scale;
-    int nsplit, chunk, H, Hkv;  // the lane-group split plan
-    float * part_o;             // [H][nsplit][D]
-    float2 * part_ml;           // [H][nsplit]
-    const uint8_t * wqs;        // packed Q4_0 / Q8_0 output weight: N rows of nb blocks
-    const uint16_t * wd;
-    int N, nb;
-    float * x;                  // the residual row: x += W_o attn
-    unsigned * bar;             // attn_oproj_bar_bytes() of zeros (they are zero again after a launch)
-    unsigned * err;             // set to nonzero when a barrier wait gave up (results invalid)
-    int xcd;                    // set by the launcher: XCD-grouped task order
-};
-void launch_attn_oproj(int type, int D, const AttnOArgs & a, hipStream_t s);
-bool attn_oproj_fits(int type, int H, int Hkv, int D, int nsplit);
-size_t attn_oproj_bar_bytes();
 // Byte offsets and spans of up to 3 packed weights (qs[k], d[k], N[k] rows of K) for RowArgs'
 // ranges; false when they span 2 GB or more.
 bool row_gemv_ranges(int type, int n, const uint8_t * const * w, const int64_t * N, int64_t K, RowArgs & a);
-
-// One decode step's layers in a single persistent launch (decode_step.hip): per layer its packed
-// weights (QKV and gate/up in the row-pair order of the rope and swiglu epilogues) and K / V cache.
-struct StepLayer {
-    const uint8_t *qkv_qs, *o_qs, *gu_qs, *dn_qs;
-    const uint16_t *qkv_d, *o_d, *gu_d, *dn_d;
-    const float *attn_norm, *ffn_norm;
-    uint16_t *kc, *vc;  // [Hkv][ctx][D] f16
-};
-
-struct StepArgs {
-    const StepLayer * layers;
-    int n_layer, n_embd, n_ff, H, Hkv;
-    int64_t ctx;
-    float eps, scale;
-    const int * pos;   // the token's position (its K / V row; rope_cs holds its rotation)
-    const int * n_kv;  // keys visible
-    const float2 * rope_cs;
-    float * x;         // residual row [n_embd]: the embedding in, the last layer's output out
-    // Rings, one slot per layer (x: per layer and write, 2 n_layer - 1 slots), slots
-    // step_ring_stride(floats of a slot) apart: every value the step passes between its phases is
-    // written to an address of its own.
-    float * x_ring;    // [2 n_layer - 1][n_embd]
-    float * q;         // roped q [n_layer][H D]
-    float * part_o;    // [n_layer][H][nsplit][D]
-    float2 * part_ml;  // [n_layer][H][nsplit]
-    float * h;         // silu(gate) * up [n_layer][n_ff]
-    int nsplit, chunk;
-    unsigned * bar;    // decode_step_bar_bytes() of barrier words, zero between launches
-    unsigned * err;    // raised when a barrier wait gave up
-    // Phase timing, when *trace_on: per workgroup w, trace[w * step_trace_events(n_layer) + e] =
-    // the 100 MHz real-time clock at the kernel's start (e = 0), then per layer l and phase p
-    // (QKV, attention, O, gate/up, down): when its first wavefront is done with the phase
-    // (e = 1 + 15 l + 3 p), when the whole workgroup has arrived at the phase's barrier, its
-    // stores complete (e + 1), and when it passes the barrier (e + 2); then at its end.
-    unsigned long long * trace;
-    const unsigned * trace_on;
-};
-__host__ __device__ inline int step_trace_events(int n_layer) { return 2 + 15 * n_layer; }
-
-// Floats from one ring slot to the next: n rounded up to 64 (256 bytes), so that no cache line
-// holds parts of two slots.
-__host__ __device__ inline size_t step_ring_stride(size_t n) { return (n + 63) & ~(size_t) 63; }
-size_t decode_step_bar_bytes();
-bool decode_step_fits(int type, int n_embd, int n_ff, int H, int Hkv, int D, int nsplit);
-void launch_decode_step(int type, int D, const StepArgs & a, hipStream_t s);
 
 // Shapes and byte strides of a strided copy / conversion (elementwise.hip).
 struct Cpy4 {
@@ -405,6 +348,12 @@ __device__ __forceinline__ void lds_signal(unsigned int * f) {
 __device__ __forceinline__ void lds_wait(unsigned int * f, unsigned int n) {
     while (__hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < n) __builtin_amdgcn_s_sleep(1);
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// A 32-bit store that reaches the device-coherent level (sc1), for partials another kernel's
+// workgroups on other XCDs read.
+__device__ __forceinline__ void st_co_f(float * p, float v) {
+    __hip_atomic_store(reinterpret_cast<unsigned *>(p), __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Streaming (non-temporal) loads for data read once per launch (weights, KV rows): they do not

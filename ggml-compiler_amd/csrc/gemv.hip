@@ -982,6 +982,7 @@ int cu_count() {
     int d = 0;
     check_hip(hipGetDevice(&d), "hipGetDevice");
     if (d != dev) {
+        RelaxedCapture relaxed;
         check_hip(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, d), "CU count");
         dev = d;
     }
@@ -1030,6 +1031,7 @@ void run_ks(const KsArgs & a, hipStream_t s) {
     const int kw = (a.ntask + 63) / 64;
     static thread_local int occ[9] = {0};  // resident workgroups per CU, by wavefronts per workgroup
     if (occ[kw] == 0) {
+        RelaxedCapture relaxed;
         check_hip(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ[kw], reinterpret_cast<const void *>(&k_gemv_ks<TYPE, B, R, FQ>),
                                                                kw * 64, 0),
                   "gemv occupancy");

@@ -125,18 +125,6 @@ struct Llama {
     DevBuf attn_row;           // its output when it runs unsplit
     DevBuf rope_cs;            // the decode step's rotation table (cos, sin) per rotation index
     bool prefetch = false;     // attention's spare CUs read the next weights ahead (GCQ_DECODE_PREFETCH=1: on)
-    // The decode step as one persistent launch (decode_step.hip) instead of five per layer: when
-    // the configuration fits it (step_fits), on with GCQ_DECODE_STEP=1 or set_decode_path(1) (it
-    // measures slower than the per-layer launches on MI355X, so it is not the default).
-    // step_layers: its per-layer table; step_bar / step_err: its barrier words and the word it
-    // raises when a barrier wait gave up.
-    bool step_fits = false, step_on = false;
-    DevBuf step_layers, step_bar, step_err, step_trace, step_trace_on;
-    // Decode path 2: each layer's attention and output projection in one launch (attn_oproj.hip),
-    // when the configuration fits it (ao_fits); ao_bar / ao_err: its barrier words and error word.
-    bool ao_fits = false, ao_on = false;
-    DevBuf ao_bar, ao_err;
-    DevBuf step_x, step_q, step_h, step_po, step_pml;  // the persistent step's rings
     DevBuf ytmp;         // a prompt chunk's mul_mat result in packed row order
     int pos = 0;
     hipGraph_t graph = nullptr;
@@ -242,55 +230,6 @@ struct Llama {
         }
         part_o = DevBuf(po);
         part_ml = DevBuf(pml);
-        step_fits = fused && decode_attn && decode_group(c.n_head / c.n_head_kv, c.max_ctx) == 1 &&
-                    decode_step_fits(c.wtype, c.n_embd, c.n_ff, c.n_head, c.n_head_kv, c.head_dim, plan_decode.nsplit);
-        if (step_fits) {
-            std::vector<StepLayer> tab(c.n_layer);
-            const int64_t kv_h = (int64_t) c.max_ctx * c.head_dim;
-            for (int l = 0; l < c.n_layer; l++) {
-                const Layer & L = layers[l];
-                const RowArgs q = row_args(L.qkv), o = row_args(L.wo), g = row_args(L.gate_up), d = row_args(L.down);
-                StepLayer & e = tab[l];
-                e.qkv_qs = q.wqs;
-                e.qkv_d = q.wd;
-                e.o_qs = o.wqs;
-                e.o_d = o.wd;
-                e.gu_qs = g.wqs;
-                e.gu_d = g.wd;
-                e.dn_qs = d.wqs;
-                e.dn_d = d.wd;
-                e.attn_norm = tensors[L.attn_norm].buf.as<float>();
-                e.ffn_norm = tensors[L.ffn_norm].buf.as<float>();
-                e.kc = kv_layer(l);
-                e.vc = kv_layer(l) + (size_t) c.n_head_kv * kv_h;
-            }
-            step_layers = DevBuf(tab.size() * sizeof(StepLayer));
-            check_hip(hipMemcpy(step_layers.p, tab.data(), step_layers.n, hipMemcpyHostToDevice), "step layers");
-            step_bar = DevBuf(decode_step_bar_bytes());
-            step_err = DevBuf(4);
-            check_hip(hipMemset(step_bar.p, 0, step_bar.n), "step barrier");
-            check_hip(hipMemset(step_err.p, 0, step_err.n), "step error");
-            step_trace = DevBuf((size_t) cu_count() * step_trace_events(c.n_layer) * 8);
-            const size_t L = (size_t) c.n_layer, ns = (size_t) plan_decode.nsplit;
-            step_x = DevBuf(std::max<size_t>(1, 2 * L - 1) * step_ring_stride(c.n_embd) * 4);
-            step_q = DevBuf(L * step_ring_stride(attn_dim) * 4);
-            step_h = DevBuf(L * step_ring_stride(c.n_ff) * 4);
-            step_po = DevBuf(L * step_ring_stride(attn_dim * ns) * 4);
-            step_pml = DevBuf(L * step_ring_stride(2 * c.n_head * ns) * 4);
-            step_trace_on = DevBuf(4);
-            check_hip(hipMemset(step_trace_on.p, 0, 4), "step trace");
-            const char * e = std::getenv("GCQ_DECODE_STEP");
-            step_on = e && std::string(e) == "1";
-        }
-        ao_fits = fused && decode_attn && decode_group(c.n_head / c.n_head_kv, c.max_ctx) == 1 &&
-                  attn_oproj_fits(c.wtype, c.n_head, c.n_head_kv, c.head_dim, plan_decode.nsplit);
-        if (ao_fits) {
-            ao_bar = DevBuf(attn_oproj_bar_bytes());
-            ao_err = DevBuf(4);
-            check_hip(hipMemset(ao_bar.p, 0, ao_bar.n), "attn + output projection barrier");
-            check_hip(hipMemset(ao_err.p, 0, ao_err.n), "attn + output projection error");
-            if (const char * e = std::getenv("GCQ_DECODE_PATH"); e && std::string(e) == "2" && !step_on) ao_on = true;
-        }
         mask = DevBuf((size_t) max_prompt * c.max_ctx * 2);
         positions = DevBuf((size_t) max_prompt * 4);
         tok_in = DevBuf((size_t) max_prompt * 4);
@@ -419,36 +358,7 @@ struct Llama {
         const Tensor & E = tensors[t_embd];
         launch_embed_rope(E.type, E.buf.p, E.rows, E.cols, tok_dev, xs, pos_dev, c.head_dim, c.rope_base, rope_cs.p,
                           stream);
-        if (step_on && n_kv_dev) {
-            StepArgs sa{};
-            sa.layers = step_layers.as<StepLayer>();
-            sa.n_layer = c.n_layer;
-            sa.n_embd = c.n_embd;
-            sa.n_ff = c.n_ff;
-            sa.H = c.n_head;
-            sa.Hkv = c.n_head_kv;
-            sa.ctx = c.max_ctx;
-            sa.eps = c.rms_eps;
-            sa.scale = 1.0f / std::sqrt((float) c.head_dim);
-            sa.pos = pos_dev;
-            sa.n_kv = n_kv_dev;
-            sa.rope_cs = rope_cs.as<float2>();
-            sa.x = xs;
-            sa.x_ring = step_x.as<float>();
-            sa.q = step_q.as<float>();
-            sa.part_o = step_po.as<float>();
-            sa.part_ml = step_pml.as<float2>();
-            sa.h = step_h.as<float>();
-            sa.nsplit = plan.nsplit;
-            sa.chunk = plan.chunk;
-            sa.bar = step_bar.as<unsigned>();
-            sa.err = step_err.as<unsigned>();
-            sa.trace = step_trace.as<unsigned long long>();
-            sa.trace_on = step_trace_on.as<unsigned>();
-            launch_decode_step(c.wtype, c.head_dim, sa, stream);
-        } else {
-            for (int l = 0; l < c.n_layer; l++) decode_layer(l, pos_dev, n_kv, n_kv_dev, plan, nullptr);
-        }
+        for (int l = 0; l < c.n_layer; l++) decode_layer(l, pos_dev, n_kv, n_kv_dev, plan, nullptr);
         RowArgs a = row_args(t_out);
         a.x = xs;
         a.norm_w = tensors[t_out_norm].buf.as<float>();
@@ -480,33 +390,6 @@ struct Llama {
         a.D = c.head_dim;
         a.rope_cs = rope_cs.as<float2>();
         launch_row_gemv(c.wtype, PRO_NORM, EPI_ROPE_KV, a, stream);
-        if (ao_on && n_kv_dev) {  // attention and output projection in one launch
-            const RowArgs o = row_args(L.wo);
-            AttnOArgs ao{};
-            ao.q = qkv.as<float>();
-            ao.kc = kvl;
-            ao.vc = kvl + (size_t) c.n_head_kv * kv_h;
-            ao.kv_h = kv_h;
-            ao.kv_rows = c.max_ctx;
-            ao.n_kv_dev = n_kv_dev;
-            ao.scale = scale;
-            ao.nsplit = plan.nsplit;
-            ao.chunk = plan.chunk;
-            ao.H = c.n_head;
-            ao.Hkv = c.n_head_kv;
-            ao.part_o = part_o.as<float>();
-            ao.part_ml = part_ml.as<float2>();
-            ao.wqs = o.wqs;
-            ao.wd = o.wd;
-            ao.N = o.N;
-            ao.nb = o.nb;
-            ao.x = xs;
-            ao.bar = ao_bar.as<unsigned>();
-            ao.err = ao_err.as<unsigned>();
-            launch_attn_oproj(c.wtype, c.head_dim, ao, stream);
-            if (mid) check_hip(hipMemcpyAsync(mid, xs, (size_t) c.n_embd * 4, hipMemcpyDeviceToDevice, stream), "mid");
-            return ffn_decode(L, xs);
-        }
         if (decode_attn) {
             // Spare CUs read this layer's output projection and the next layer's QKV weights
             // into the Infinity Cache while the attention runs.
@@ -695,67 +578,6 @@ struct Llama {
         check_hip(hipGraphInstantiate(&graph_exec, graph, nullptr, nullptr, 0), "graph instantiate");
     }
 
-    // The persistent step raises step_err when a barrier wait gave up (a workgroup that never
-    // arrived): the step's results are then invalid, and the layer-by-layer path takes over.
-    void check_step() {
-        if (ao_on) {
-            unsigned e = 0;
-            check_hip(hipMemcpy(&e, ao_err.p, 4, hipMemcpyDeviceToHost), "attn + output projection error");
-            if (e == 0) return;
-            check_hip(hipMemset(ao_err.p, 0, 4), "attn + output projection error");
-            check_hip(hipMemset(ao_bar.p, 0, ao_bar.n), "attn + output projection barrier");
-            set_decode_path(0);
-            fail("decode path 2: a grid barrier wait gave up, the step's results are invalid; decoding continues on "
-                 "the layer-by-layer path");
-        }
-        if (!step_on) return;
-        unsigned e = 0;
-        check_hip(hipMemcpy(&e, step_err.p, 4, hipMemcpyDeviceToHost), "step error");
-        if (e == 0) return;
-        check_hip(hipMemset(step_err.p, 0, 4), "step error");
-        check_hip(hipMemset(step_bar.p, 0, step_bar.n), "step barrier");
-        set_decode_path(0);
-        fail("decode step: a grid barrier wait gave up, the step's results are invalid; decoding continues on "
-             "the layer-by-layer path");
-    }
-
-    // One decode step on the persistent path with its phase clock on: the timestamps of every
-    // workgroup (step_trace_events per workgroup) into out; returns the workgroup count.
-    int trace_step(int32_t token, uint64_t * out, int64_t n) {
-        require(step_on, "step trace: the persistent decode step is not in use");
-        const int wgs = cu_count(), ev = step_trace_events(c.n_layer);
-        require(out != nullptr && n >= (int64_t) wgs * ev,
-                "step trace: needs " + std::to_string((int64_t) wgs * ev) + " entries");
-        const unsigned one = 1u, zero = 0u;
-        check_hip(hipMemcpy(step_trace_on.p, &one, 4, hipMemcpyHostToDevice), "step trace");
-        try {
-            decode(token, nullptr, nullptr);
-        } catch (...) {
-            (void) hipMemcpy(step_trace_on.p, &zero, 4, hipMemcpyHostToDevice);
-            throw;
-        }
-        check_hip(hipMemcpy(step_trace_on.p, &zero, 4, hipMemcpyHostToDevice), "step trace");
-        check_hip(hipMemcpy(out, step_trace.p, (size_t) wgs * ev * 8, hipMemcpyDeviceToHost), "step trace");
-        return wgs;
-    }
-
-    int decode_path() const { return step_on ? 1 : ao_on ? 2 : 0; }
-
-    void set_decode_path(int path) {
-        require(path >= 0 && path <= 2,
-                "decode path must be 0 (per-layer launches), 1 (one persistent launch) or 2 (attention and output "
-                "projection in one launch)");
-        require(path != 1 || step_fits, "decode path 1: this configuration does not fit the persistent step");
-        require(path != 2 || ao_fits, "decode path 2: this configuration does not fit the fused attention launch");
-        if (path == decode_path()) return;
-        step_on = path == 1;
-        ao_on = path == 2;
-        if (graph_exec) check_hip(hipGraphExecDestroy(graph_exec), "graph");
-        if (graph) check_hip(hipGraphDestroy(graph), "graph");
-        graph_exec = nullptr;
-        graph = nullptr;
-    }
-
     void set_state(int token) {
         const StepStateHost st{pos, pos + 1, token, 0};
         check_hip(hipMemcpyAsync(state.p, &st, sizeof st, hipMemcpyHostToDevice, stream), "state");
@@ -769,7 +591,6 @@ struct Llama {
         check_hip(hipGraphLaunch(graph_exec, stream), "graph launch");
         check_hip(hipStreamSynchronize(stream), "decode");
         pos += 1;
-        check_step();
         if (logits_host)
             check_hip(hipMemcpy(logits_host, logits.p, (size_t) c.n_vocab * 4, hipMemcpyDeviceToHost), "logits");
         if (next) {
@@ -788,7 +609,6 @@ struct Llama {
         for (int i = 0; i < n_new; i++) check_hip(hipGraphLaunch(graph_exec, stream), "graph launch");
         check_hip(hipStreamSynchronize(stream), "generate");
         pos += n_new;
-        check_step();
         if (out) check_hip(hipMemcpy(out, out_tokens.p, (size_t) n_new * 4, hipMemcpyDeviceToHost), "tokens");
     }
 };
@@ -880,24 +700,6 @@ int gcq_llama_forward_layers(gcq_llama * m, const float * x, int n, int pos, int
         require(m != nullptr && x != nullptr && x_out != nullptr, "model, x or x_out is NULL");
         m->forward_layers(x, n, pos, first_layer, n_layers, x_out, x_mid);
     });
-}
-
-int gcq_llama_set_decode_path(gcq_llama * m, int path) {
-    return guarded([&] {
-        require(m != nullptr, "model is NULL");
-        m->set_decode_path(path);
-    });
-}
-
-int gcq_llama_decode_path(const gcq_llama * m) { return m ? m->decode_path() : -1; }
-
-int gcq_llama_step_trace(gcq_llama * m, int32_t token, uint64_t * out, int64_t n) {
-    int wgs = -1;
-    const int rc = guarded([&] {
-        require(m != nullptr, "model is NULL");
-        wgs = m->trace_step(token, out, n);
-    });
-    return rc == 0 ? wgs : -1;
 }
 
 int gcq_llama_generate(gcq_llama * m, int32_t first, int n_new, int32_t * out_tokens) {

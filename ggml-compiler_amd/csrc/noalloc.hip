@@ -6,7 +6,8 @@
 //
 // Host code never passes `scratch` itself to a kernel: on the host that name is a stand-in, not a
 // device address. The first call on a device (with that device current) looks up the array's
-// address on that device with hipGetSymbolAddress and keeps it per device; every launch takes that
+// address on that device with hipGetSymbolAddress (in the thread's relaxed capture mode, so that a
+// first call made while capturing a graph works) and keeps it per device; every launch takes that
 // pointer. The kernels fully overwrite the part of the array a call uses before reading it, so
 // nothing needs clearing between calls. Calls that overlap on one GPU (two streams, two threads)
 // share the array and race.
@@ -32,6 +33,7 @@ void * device_scratch() {
     require(dev >= 0 && dev < kMaxDevices, "device index " + std::to_string(dev) + " out of range");
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (!g_scratch_ptr[dev]) {
+        RelaxedCapture relaxed;  // the first call on a device may come under graph capture
         void * ptr = nullptr;
         check_hip(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
         require(ptr != nullptr, "hipGetSymbolAddress(scratch) returned NULL");

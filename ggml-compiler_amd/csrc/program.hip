@@ -1519,21 +1519,42 @@ struct ggml_compiler_model {
         const std::vector<ggml_tensor *> results = stage_results(c, st, env);
         c.graph = ggml_new_graph_custom(c.ctx, graph_nodes, false);
         // get_rows / copies that read only the stage's parameters and weights (an embedding row, a
-        // mask's cast) come first, in their order: any topological order computes the same, and
-        // at the front the executor can run such small steps together in one launch.
+        // mask's cast) come first, in their order, so that the executor can run such small steps
+        // together in one launch. Moving a node changes nothing only if no other node writes what
+        // it reads or reads what it writes: a leaf written in place (set_rows' destination, a copy's
+        // destination) keeps its nodes in the expand order, as ggml would run them.
         ggml_cgraph * probe = ggml_new_graph_custom(c.ctx, graph_nodes, false);
         for (ggml_tensor * t : results) ggml_build_forward_expand(probe, t);
+        auto leaf_of = [](const ggml_tensor * t) {
+            while (t && (t->op == GGML_OP_VIEW || t->op == GGML_OP_RESHAPE || t->op == GGML_OP_PERMUTE ||
+                         t->op == GGML_OP_TRANSPOSE))
+                t = t->src[0];
+            return t;
+        };
+        auto dest_of = [&](const ggml_tensor * t) -> const ggml_tensor * {
+            if (t->op == GGML_OP_SET_ROWS) return leaf_of(t->src[2]);
+            if (t->op == GGML_OP_CPY) return leaf_of(t->src[1]);
+            return nullptr;
+        };
+        std::unordered_map<const ggml_tensor *, int> writers, readers;
+        for (int k = 0; k < ggml_graph_n_nodes(probe); k++) {
+            const ggml_tensor * t = ggml_graph_node(probe, k);
+            if (const ggml_tensor * d = dest_of(t)) writers[d]++;
+            for (const ggml_tensor * src : t->src)
+                if (src && src != (t->op == GGML_OP_CPY ? t->src[1] : nullptr)) readers[leaf_of(src)]++;
+        }
         for (int k = 0; k < ggml_graph_n_nodes(probe); k++) {
             ggml_tensor * t = ggml_graph_node(probe, k);
             if (t->op != GGML_OP_GET_ROWS && t->op != GGML_OP_CPY) continue;
-            bool leaves = true;  // every source a leaf or a view of one (a bound value's view)
+            bool movable = true;  // every source a leaf (or a view of one) nothing writes in place
             for (const ggml_tensor * src : t->src) {
-                while (src && (src->op == GGML_OP_VIEW || src->op == GGML_OP_RESHAPE || src->op == GGML_OP_PERMUTE ||
-                               src->op == GGML_OP_TRANSPOSE))
-                    src = src->src[0];
-                leaves = leaves && (!src || src->op == GGML_OP_NONE);
+                if (!src || (t->op == GGML_OP_CPY && src == t->src[1])) continue;
+                const ggml_tensor * l = leaf_of(src);
+                movable = movable && l->op == GGML_OP_NONE && writers.count(l) == 0;
             }
-            if (leaves) ggml_build_forward_expand(c.graph, t);
+            if (const ggml_tensor * d = dest_of(t))  // a copy: its destination written and read by it alone
+                movable = movable && writers[d] == 1 && readers.count(d) == 0;
+            if (movable) ggml_build_forward_expand(c.graph, t);
         }
         for (ggml_tensor * t : results) ggml_build_forward_expand(c.graph, t);
         // Results reach their driver values through copies after every other node (so after

@@ -111,9 +111,6 @@ SIGNATURES = {
     "gcq_llama_decode": ([p, ctypes.c_int32, p, p], i32),
     "gcq_llama_generate": ([p, ctypes.c_int32, i32, p], i32),
     "gcq_llama_forward_layers": ([p, p, i32, i32, i32, i32, p, p], i32),
-    "gcq_llama_set_decode_path": ([p, i32], i32),
-    "gcq_llama_decode_path": ([p], i32),
-    "gcq_llama_step_trace": ([p, i32, p, i64], i32),
     "ggml_compiler_version": ([], ctypes.c_char_p),
     "ggml_compiler_last_error": ([], ctypes.c_char_p),
     "ggml_compiler_default_options": ([], _Options),

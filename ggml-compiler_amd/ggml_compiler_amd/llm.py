@@ -145,26 +145,6 @@ class Model:
         check(self._lib.gcq_llama_generate(self._m, int(first), int(n_new), out.ctypes.data))
         return out[:n_new].tolist()
 
-    @property
-    def decode_path(self) -> int:
-        """0: the decode step as five launches per layer; 1: all layers in one persistent launch."""
-        return int(self._lib.gcq_llama_decode_path(self._m))
-
-    @decode_path.setter
-    def decode_path(self, path: int) -> None:
-        check(self._lib.gcq_llama_set_decode_path(self._m, int(path)))
-
-    def step_trace(self, token: int) -> np.ndarray:
-        """One decode step on path 1 with its phase clock on: uint64 [workgroups, 2 + 15 n_layer] of
-        100 MHz real-time ticks (start; per layer and phase: first wavefront done, workgroup
-        arrived, barrier passed; end)."""
-        ev = 2 + 15 * self.cfg.n_layer
-        out = np.zeros(1024 * ev, np.uint64)
-        wgs = self._lib.gcq_llama_step_trace(self._m, int(token), out.ctypes.data, out.size)
-        if wgs < 0:
-            check(-1)
-        return out[: wgs * ev].reshape(wgs, ev)
-
     def forward_layers(self, x: np.ndarray, pos: int, first: int, count: int = 1) -> tuple[np.ndarray, np.ndarray]:
         """Layers [first, first + count) on given residual rows x [n, n_embd] at positions pos .. pos +
         n - 1 (the prompt kernels for n > 1, the decode step's for n == 1), their K / V cached:

@@ -215,30 +215,6 @@ GCQ_API int gcq_llama_decode(gcq_llama * m, int32_t token, float * logits, int32
 /* Feed `first`, then each greedy token back, n_new steps on the device; out_tokens (host) gets the
  * n_new tokens produced (no end-of-sequence stop). */
 GCQ_API int gcq_llama_generate(gcq_llama * m, int32_t first, int n_new, int32_t * out_tokens);
-/* How the decode step runs (gcq_llama_decode / gcq_llama_generate): 0 = five launches per layer
- * (row GEMVs with the graph nodes around each mul_mat fused in, split-K attention), the default;
- * 1 = all layers in one persistent launch, one workgroup per CU, grid barriers between a layer's
- * five phases (slower on MI355X: 570 against 736 tok/s for the 8B-shaped Q4_0 decoder);
- * 2 = as 0, but each layer's attention and output projection in one launch (one workgroup per CU,
- * the output weight loaded while the attention runs, one grid barrier). All paths compute the
- * same operations in the same order: the logits are equal bit for bit. Paths 1 and 2 need
- * Q4_0 / Q8_0, head_dim 64 / 128, an attention row of at most 4096 and max_ctx <= 2048 (path 1
- * also n_embd <= 8192, n_ff <= 16384; path 2 at most one split-head task per CU); set returns -1
- * when it does not fit. The environment variable GCQ_DECODE_STEP=1 makes path 1 the initial path,
- * GCQ_DECODE_PATH=2 path 2. No counterpart in the reference, whose decode is
- * one ggml graph per token (runtime/src/ggml_compiler_rt.cpp:356-441). */
-GCQ_API int gcq_llama_set_decode_path(gcq_llama * m, int path);
-GCQ_API int gcq_llama_decode_path(const gcq_llama * m);
-/* gcq_llama_decode(token) on decode path 1 with its phase clock on: per workgroup w (one per CU)
- * and event e < 2 + 15 n_layer, out[w (2 + 15 n_layer) + e] = the GPU's 100 MHz real-time clock
- * at the step's start (e = 0); for phase p of layer l (phases QKV, attention, output projection,
- * gate/up, down) when the workgroup's first wavefront is done with it (e = 1 + 15 l + 3 p), when
- * the whole workgroup has arrived at the barrier that ends it, its stores complete (e + 1), and
- * when it passes that barrier (e + 2); at its end (e = 1 + 15 n_layer). n: entries of out. Returns
- * the workgroup count, -1 on failure (path 0, or out too small). The per-phase timing of the
- * persistent step (the reference times each graph node alone: GGML_COMPILER_PROFILE,
- * runtime/src/ggml_compiler_rt.cpp:219-240). */
-GCQ_API int gcq_llama_step_trace(gcq_llama * m, int32_t token, uint64_t * out, int64_t n);
 /* Layers [first_layer, first_layer + n_layers) on n given residual-stream rows x (host, n x n_embd
  * f32) at positions pos .. pos + n - 1: the kernels a prompt chunk (n > 1, n <= max_prompt) or the
  * decode step (n == 1) runs, K / V of those layers written into the cache at those positions.

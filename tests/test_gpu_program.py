@@ -112,6 +112,34 @@ def test_layer_norm_gelu_mean_program(tmp_path, orc):
     assert np.allclose(y, want, rtol=1e-5, atol=1e-6)
 
 
+def test_set_rows_then_get_rows_of_the_same_parameter(tmp_path, orc):
+    """A stage that writes a row of its parameter in place (set_rows into an f16 table, as into a KV
+    cache) and reads rows of it (get_rows): the read sees the write, as in ggml's expand order (the
+    set_rows result is the first output); the loader's move of small get_rows to the front of a
+    stage's graph must not reorder them."""
+    E, R = 64, 6
+    st = {"name": "upd", "params": [_v("a.0", "f16", [E, R], [R, E]), _v("a.1", "f32", [E, 1], [1, E]),
+                                    _v("a.2", "i32", [1], [1]), _v("a.3", "i32", [2], [2])],
+          "outputs": ["%0", "%1"],
+          "nodes": [_n(0, "set_rows", ["a.0", "a.1", "a.2"], "f16", [E, R]),
+                    _n(1, "get_rows", ["a.0", "a.3"], "f32", [E, 2])]}
+    prog = {"format_version": 3, "symbols": [],
+            "values": [_v("tab", "f16", [E, R], [R, E]), _v("row", "f32", [E, 1], [1, E]), _v("i", "i32", [1], [1]),
+                       _v("g", "i32", [2], [2]), _v("y", "f32", [E, 2], [2, E])],
+            "stages": [st], "entries": [{"name": "main", "inputs": ["tab", "row", "i", "g"], "outputs": ["y", "tab"],
+                                         "driver": [{"op": "call", "stage": "upd", "args": ["tab", "row", "i", "g"],
+                                                     "out": ["tab", "y"]}]}],
+            "state": []}
+    tab = orc.normal((R, E), seed=80).astype(np.float16)
+    row = orc.normal((1, E), seed=81)
+    with runtime.Session(_write(tmp_path / "upd.gguf", prog)) as s:
+        out = s.run(tab, row, np.array([3], np.int32), np.array([3, 1], np.int32))
+    want = tab.copy()
+    want[3] = row[0].astype(np.float16)
+    assert np.array_equal(np.asarray(out["tab"]).astype(np.float16), want)
+    assert np.array_equal(out["y"], want[[3, 1]].astype(np.float32)), "get_rows ran before the set_rows of its table"
+
+
 def test_loop_driver(tmp_path):
     """h_{k+1} = h_k * s_k + R[k] (carry from h0, per-iteration scalars, slices of R); the causal
     mask row of position start + k; both collected per iteration; stop once argmax(h) is 7."""
