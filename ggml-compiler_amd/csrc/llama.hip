@@ -127,12 +127,13 @@ struct Llama {
     bool prefetch = false;     // attention's spare CUs read the next weights ahead (GCQ_DECODE_PREFETCH=1: on)
     DevBuf ytmp;         // a prompt chunk's mul_mat result in packed row order
     int pos = 0;
-    hipGraph_t graph = nullptr;
-    hipGraphExec_t graph_exec = nullptr;
+    // The captured decode step, one graph per bucket of kKvBucket KV lengths (step_graph).
+    static constexpr int kKvBucket = 32;
+    std::vector<hipGraphExec_t> execs;
 
     ~Llama() {
-        if (graph_exec) (void) hipGraphExecDestroy(graph_exec);
-        if (graph) (void) hipGraphDestroy(graph);
+        for (hipGraphExec_t e : execs)
+            if (e) (void) hipGraphExecDestroy(e);
         if (stream) (void) hipStreamDestroy(stream);
     }
 
@@ -368,7 +369,9 @@ struct Llama {
     }
 
     // Layer l of the single-token forward on the residual row x (the rotation table of the
-    // position already in rope_cs). mid (device, optional): the residual after attention.
+    // position already in rope_cs). n_kv: the most keys the step may see (the KV length itself is
+    // read from n_kv_dev); the attention's splits cover cache rows [0, n_kv) only. mid (device,
+    // optional): the residual after attention.
     void decode_layer(int l, const int32_t * pos_dev, int n_kv, const int * n_kv_dev, const AttnPlan & plan,
                       float * mid) {
         float * xs = x.as<float>();
@@ -403,7 +406,7 @@ struct Llama {
             pf.sink = counters.as<unsigned int>() + 64;
             launch_attn_decode(qkv.as<float>(), c.head_dim, kvl, kv_h, c.head_dim, kvl + (size_t) c.n_head_kv * kv_h,
                                kv_h, c.head_dim, c.head_dim, c.n_head, c.n_head_kv, n_kv, n_kv_dev, scale,
-                               plan.nsplit, plan.chunk, c.max_ctx, decode_group(c.n_head / c.n_head_kv, c.max_ctx),
+                               plan.nsplit, plan.chunk, n_kv, decode_group(c.n_head / c.n_head_kv, n_kv),
                                attn_row.as<float>(), part_o.as<float>(), part_ml.as<float2>(), stream,
                                prefetch ? &pf : nullptr, nullptr, 16);
         } else {
@@ -564,18 +567,40 @@ struct Llama {
             check_hip(hipMemcpy(logits_host, logits.p, (size_t) c.n_vocab * 4, hipMemcpyDeviceToHost), "logits");
     }
 
-    void ensure_graph() {
-        if (graph_exec) return;
+    // The attention plan of a decode step that sees at most n_kv keys.
+    AttnPlan decode_plan(int n_kv) const {
+        return decode_attn ? attn_plan_decode(c.head_dim, c.n_head, c.n_head / c.n_head_kv, n_kv, row_gemv_merge_max())
+                           : attn_plan(1, c.n_head_kv, n_kv);
+    }
+
+    // The captured decode step for a step that sees n_kv keys: one graph per bucket of kKvBucket
+    // KV lengths, its attention planned and its K / V rows read for the bucket's largest length
+    // (so the step's work follows the position, not max_ctx), instantiated on first use. Token,
+    // position and KV length come from the device state; step_end advances it.
+    hipGraphExec_t step_graph(int n_kv) {
+        require(n_kv >= 1 && n_kv <= c.max_ctx, "decode: KV length out of range");
+        const size_t b = (size_t) (n_kv - 1) / kKvBucket;
+        if (execs.size() <= b) execs.resize(b + 1, nullptr);
+        if (execs[b]) return execs[b];
+        const int bound = std::min(c.max_ctx, (int) (b + 1) * kKvBucket);
         (void) cu_count();  // device queries happen before capture
-        // Capture: token from state.token, position / KV length from the state, no mask (every
-        // key up to the position is visible), step_end advances the state.
         StepStateHost * st = state.as<StepStateHost>();
+        hipGraph_t g = nullptr;
         check_hip(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "capture");
-        forward(1, &st->token, &st->pos, c.max_ctx, &st->n_kv, nullptr, plan_decode);
-        launch_step_end(logits.as<float>(), c.n_vocab, state.p, out_tokens.as<int32_t>(), c.max_ctx, argmax_part.p,
-                        counters.as<unsigned int>() + 0, stream);
-        check_hip(hipStreamEndCapture(stream, &graph), "capture end");
-        check_hip(hipGraphInstantiate(&graph_exec, graph, nullptr, nullptr, 0), "graph instantiate");
+        try {
+            forward(1, &st->token, &st->pos, bound, &st->n_kv, nullptr, decode_plan(bound));
+            launch_step_end(logits.as<float>(), c.n_vocab, state.p, out_tokens.as<int32_t>(), c.max_ctx,
+                            argmax_part.p, counters.as<unsigned int>() + 0, stream);
+        } catch (...) {
+            (void) hipStreamEndCapture(stream, &g);
+            if (g) (void) hipGraphDestroy(g);
+            throw;
+        }
+        check_hip(hipStreamEndCapture(stream, &g), "capture end");
+        const hipError_t e = hipGraphInstantiate(&execs[b], g, nullptr, nullptr, 0);
+        (void) hipGraphDestroy(g);
+        check_hip(e, "graph instantiate");
+        return execs[b];
     }
 
     void set_state(int token) {
@@ -586,9 +611,9 @@ struct Llama {
     void decode(int32_t token, float * logits_host, int32_t * next) {
         require(token >= 0 && token < c.n_vocab, "token id out of range");
         require(pos + 1 <= c.max_ctx, "context full");
-        ensure_graph();
+        hipGraphExec_t step = step_graph(pos + 1);
         set_state(token);
-        check_hip(hipGraphLaunch(graph_exec, stream), "graph launch");
+        check_hip(hipGraphLaunch(step, stream), "graph launch");
         check_hip(hipStreamSynchronize(stream), "decode");
         pos += 1;
         if (logits_host)
@@ -604,9 +629,9 @@ struct Llama {
         require(first >= 0 && first < c.n_vocab, "token id out of range");
         require(n_new >= 0 && pos + n_new <= c.max_ctx, "context full: generate would pass max_ctx");
         if (n_new == 0) return;
-        ensure_graph();
+        for (int i = 0; i < n_new; i++) (void) step_graph(pos + i + 1);  // instantiated before any launch
         set_state(first);
-        for (int i = 0; i < n_new; i++) check_hip(hipGraphLaunch(graph_exec, stream), "graph launch");
+        for (int i = 0; i < n_new; i++) check_hip(hipGraphLaunch(step_graph(pos + i + 1), stream), "graph launch");
         check_hip(hipStreamSynchronize(stream), "generate");
         pos += n_new;
         if (out) check_hip(hipMemcpy(out, out_tokens.p, (size_t) n_new * 4, hipMemcpyDeviceToHost), "tokens");
