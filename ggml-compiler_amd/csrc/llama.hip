@@ -603,6 +603,15 @@ struct Llama {
         return execs[b];
     }
 
+    // Instantiates the step graphs a decode up to KV length n_kv may launch, before any of them is
+    // launched: every bucket up to max_ctx on the first call when there are at most 128 (a few
+    // tenths of a ms each), else the buckets up to n_kv.
+    void prepare_graphs(int n_kv) {
+        const int buckets = (c.max_ctx + kKvBucket - 1) / kKvBucket;
+        const int upto = buckets <= 128 ? c.max_ctx : n_kv;
+        for (int b = 0; b * kKvBucket < upto; b++) (void) step_graph(std::min(upto, (b + 1) * kKvBucket));
+    }
+
     void set_state(int token) {
         const StepStateHost st{pos, pos + 1, token, 0};
         check_hip(hipMemcpyAsync(state.p, &st, sizeof st, hipMemcpyHostToDevice, stream), "state");
@@ -611,6 +620,7 @@ struct Llama {
     void decode(int32_t token, float * logits_host, int32_t * next) {
         require(token >= 0 && token < c.n_vocab, "token id out of range");
         require(pos + 1 <= c.max_ctx, "context full");
+        prepare_graphs(pos + 1);
         hipGraphExec_t step = step_graph(pos + 1);
         set_state(token);
         check_hip(hipGraphLaunch(step, stream), "graph launch");
@@ -629,7 +639,7 @@ struct Llama {
         require(first >= 0 && first < c.n_vocab, "token id out of range");
         require(n_new >= 0 && pos + n_new <= c.max_ctx, "context full: generate would pass max_ctx");
         if (n_new == 0) return;
-        for (int i = 0; i < n_new; i++) (void) step_graph(pos + i + 1);  // instantiated before any launch
+        prepare_graphs(pos + n_new);
         set_state(first);
         for (int i = 0; i < n_new; i++) check_hip(hipGraphLaunch(step_graph(pos + i + 1), stream), "graph launch");
         check_hip(hipStreamSynchronize(stream), "generate");

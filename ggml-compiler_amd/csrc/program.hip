@@ -13,9 +13,11 @@
 // and the backend's supports_op refuse, with the reason, what cannot run. Each entry's driver is
 // compiled to flat code (calls; loops as enter / top / bottom with jumps) and run by a small
 // interpreter. Everything a run does between graphs - loop carries, counters, per-iteration scalars
-// and slices, causal mask rows, collected rows - is device work ordered on the backend's stream
-// with the graphs, so an iteration waits for the host only to read a counter's start or an until
-// token. Stage times are GPU times from events around each call.
+// and slices, causal mask rows, collected rows, the until test - is device work ordered on the
+// backend's stream with the graphs; a loop reads its counters' starts once, and the host learns of
+// an until stop one iteration later from a word the test op writes to host memory, so no
+// iteration waits for the host (loop_bottom_device). Stage times are GPU times from events
+// around each call.
 //
 // Semantics kept from the reference (runtime/src/ggml_compiler_rt.cpp, runtime/src/program.cpp,
 // runtime/src/ops.cpp): the program schema and its checks, symbolic dims with Python's integer
@@ -42,6 +44,7 @@
 #include <set>
 #include <memory>
 #include <unordered_map>
+#include <thread>
 #include <vector>
 
 #include <fcntl.h>
@@ -926,15 +929,17 @@ namespace {
 
 // The small work a driver does between its graphs (scalar and counter fills, causal mask rows,
 // slice and collect copies), several of them in one launch: op blockIdx.y, element i.
-enum { D_FILL32, D_CAUSAL, D_COPY4, D_COPY1 };
+enum { D_FILL32, D_CAUSAL, D_COPY4, D_COPY1, D_COPY4_IF, D_COPY1_IF, D_UNTIL };
 constexpr int kDriverBatch = 8;
 constexpr size_t kDriverCopyMax = 1 << 20;  // larger copies: hipMemcpyAsync
 struct DriverKOp {
     int kind;
     uint32_t bits;
-    int64_t n, len, pos;  // elements; D_CAUSAL: row length and position
+    int64_t n, len, pos;  // elements; D_CAUSAL: row length and position; _IF / D_UNTIL: the iteration
     uint8_t * dst;
     const uint8_t * src;
+    const int32_t * aux;  // _IF: the loop's stop word; D_UNTIL: its len stop ids
+    int32_t * host;       // D_UNTIL: host-visible {stop, iterations done}
 };
 struct DriverBatch {
     DriverKOp op[kDriverBatch];
@@ -949,6 +954,30 @@ __global__ void k_driver_ops(const DriverBatch b) {
         // rows of a causal mask for position pos: 0 where the key index (element % len) is <= pos
         case D_CAUSAL: reinterpret_cast<float *>(o.dst)[i] = i % o.len <= o.pos ? 0.0f : -INFINITY; break;
         case D_COPY4: reinterpret_cast<uint32_t *>(o.dst)[i] = reinterpret_cast<const uint32_t *>(o.src)[i]; break;
+        // a collected row of an iteration at or before the loop's stop (the stop word holds the
+        // iteration whose value met the until ids, or INT32_MAX)
+        case D_COPY4_IF:
+            if (o.pos <= *o.aux) reinterpret_cast<uint32_t *>(o.dst)[i] = reinterpret_cast<const uint32_t *>(o.src)[i];
+            break;
+        case D_COPY1_IF:
+            if (o.pos <= *o.aux) o.dst[i] = o.src[i];
+            break;
+        // the until test of iteration pos: the stop word takes pos if the value is one of the ids;
+        // then the host's copy of the stop word, then the iterations done (its release)
+        case D_UNTIL: {
+            const int32_t v = *reinterpret_cast<const int32_t *>(o.src);
+            bool hit = false;
+            for (int64_t k = 0; k < o.len; k++) hit = hit || o.aux[k] == v;
+            int32_t * stop = reinterpret_cast<int32_t *>(o.dst);
+            int32_t cur = *stop;
+            if (hit && cur > (int32_t) o.pos) {
+                cur = (int32_t) o.pos;
+                *stop = cur;
+            }
+            __hip_atomic_store(&o.host[0], cur, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            __hip_atomic_store(&o.host[1], (int32_t) (o.pos + 1), __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+            break;
+        }
         default: o.dst[i] = o.src[i]; break;
     }
 }
@@ -970,11 +999,11 @@ class StreamOps {
     }
     void fill32(void * p, int64_t n, uint32_t bits) {
         if (n <= 0) return;
-        add({D_FILL32, bits, n, 0, 0, (uint8_t *) p, nullptr}, (size_t) n * 4);
+        add({D_FILL32, bits, n, 0, 0, (uint8_t *) p, nullptr, nullptr, nullptr}, (size_t) n * 4);
     }
     void causal(float * p, int64_t n, int64_t len, int64_t pos) {
         if (n <= 0) return;
-        add({D_CAUSAL, 0, n, len, pos, (uint8_t *) p, nullptr}, (size_t) n * 4);
+        add({D_CAUSAL, 0, n, len, pos, (uint8_t *) p, nullptr, nullptr, nullptr}, (size_t) n * 4);
     }
     void copy(void * dst, const void * src, size_t n) {
         if (!n) return;
@@ -985,8 +1014,20 @@ class StreamOps {
         }
         const bool words = ((uintptr_t) dst & 3) == 0 && ((uintptr_t) src & 3) == 0 && n % 4 == 0;
         add({words ? D_COPY4 : D_COPY1, 0, (int64_t) (words ? n / 4 : n), 0, 0, (uint8_t *) dst,
-             (const uint8_t *) src},
+             (const uint8_t *) src, nullptr, nullptr},
             n);
+    }
+    // copy if iteration `it` is at or before the stop word's iteration
+    void copy_if(void * dst, const void * src, size_t n, const int32_t * stop, int64_t it) {
+        if (!n) return;
+        const bool words = ((uintptr_t) dst & 3) == 0 && ((uintptr_t) src & 3) == 0 && n % 4 == 0;
+        DriverKOp o{words ? D_COPY4_IF : D_COPY1_IF, 0, (int64_t) (words ? n / 4 : n), 0, it, (uint8_t *) dst,
+                    (const uint8_t *) src, stop, nullptr};
+        add(o, n);
+    }
+    void until(const int32_t * value, const int32_t * ids, int64_t n_ids, int32_t * stop, int32_t * host, int64_t it) {
+        DriverKOp o{D_UNTIL, 0, 1, n_ids, it, (uint8_t *) stop, (const uint8_t *) value, ids, host};
+        add(o, 4);
     }
     void clear(void * dst, size_t n) {
         flush();
@@ -1066,10 +1107,16 @@ class StageClock {
         marks_.push_back({stage, used_ - 1, used_});
         record(s);
     }
+    size_t marks() const { return marks_.size(); }
+    // calls from mark k on are not counted (a loop iteration that ran past the loop's end)
+    void forget_since(size_t k) {
+        for (size_t i = k; i < marks_.size(); i++) marks_[i].stage = -1;
+    }
     // ms of each call, accumulated into per-stage totals
     template <class F>
     void collect(F && add) {
         for (const Mark & m : marks_) {
+            if (m.stage < 0) continue;
             float ms = 0.0f;
             check_hip(hipEventElapsedTime(&ms, events_[m.start], events_[m.stop]), "hipEventElapsedTime");
             add(m.stage, (double) ms);
@@ -1148,15 +1195,55 @@ namespace {
 struct CallGraph {
     int stage = -1;
     const DriverOp * op = nullptr;
+    // the graph in use: of the current binding, for a stage whose shapes read a symbol
     ggml_context * ctx = nullptr;
     ggml_cgraph * graph = nullptr;
     ggml_gallocr_t alloc = nullptr;
-    bool stale = false;  // the binding changed a shape it reads: rebuilt before its next run
+    bool stale = false;  // no graph for the current binding yet: built before its next run
+    // A symbolic stage's graphs per binding (the model keeps a few bindings' views), each with its
+    // own allocation, so a binding seen again reuses its graph and the executor's capture of it.
+    struct Build {
+        std::vector<int64_t> binding;
+        ggml_context * ctx = nullptr;
+        ggml_cgraph * graph = nullptr;
+        ggml_gallocr_t alloc = nullptr;
+    };
+    std::vector<Build> builds;
 
     void drop_graph() {
         if (ctx) ggml_free(ctx);
         ctx = nullptr;
         graph = nullptr;
+    }
+    void use(const Build & b) {
+        ctx = b.ctx;
+        graph = b.graph;
+        alloc = b.alloc;
+        stale = false;
+    }
+    void forget(const std::vector<int64_t> & binding) {
+        for (size_t k = 0; k < builds.size();) {
+            if (builds[k].binding != binding) {
+                k++;
+                continue;
+            }
+            if (builds[k].graph == graph) ctx = nullptr, graph = nullptr, alloc = nullptr, stale = true;
+            if (builds[k].ctx) ggml_free(builds[k].ctx);
+            if (builds[k].alloc) ggml_gallocr_free(builds[k].alloc);
+            builds.erase(builds.begin() + (long) k);
+        }
+    }
+    void free_all() {
+        for (Build & b : builds) {
+            if (b.ctx) ggml_free(b.ctx);
+            if (b.alloc) ggml_gallocr_free(b.alloc);
+        }
+        if (builds.empty()) {  // a stage without symbols: its one graph
+            if (alloc) ggml_gallocr_free(alloc);
+            drop_graph();
+        }
+        builds.clear();
+        ctx = nullptr, graph = nullptr, alloc = nullptr;
     }
 };
 
@@ -1169,10 +1256,34 @@ struct VmCode {
     int call;  // Call: index into the model's call graphs
 };
 
+// A loop's until test on the device (one int32 until value): its stop word and ids, the values
+// its body writes (state aside) as of the last two iterations, and a host-visible {stop,
+// iterations done} that the iterations' test ops write.
+struct UntilState {
+    void * dev = nullptr;          // [stop word] [ids] [per kept value: two slots]
+    int32_t * stop = nullptr;
+    int32_t * ids = nullptr;
+    int64_t n_ids = 0;
+    std::vector<std::string> kept;  // the values the body writes, state aside
+    std::vector<uint8_t *> ring;    // per kept value: slot (iteration & 1)
+    std::vector<size_t> slot_bytes;
+    int32_t * host = nullptr;      // pinned
+    UntilState() = default;
+    UntilState(const UntilState &) = delete;
+    UntilState & operator=(const UntilState &) = delete;
+    ~UntilState() {
+        if (dev) (void) hipFree(dev);
+        if (host) (void) hipHostFree(host);
+    }
+};
+
 struct LoopFrame {
     const DriverOp * op;
     int trips, i;
     std::vector<int32_t> start;  // counters' values at loop entry
+    UntilState * until = nullptr;  // the until test on the device, when the loop has one
+    uint64_t calls0 = 0;           // calls made and stage-clock marks before this iteration
+    size_t marks0 = 0;
 };
 
 }  // namespace
@@ -1189,7 +1300,16 @@ struct ggml_compiler_model {
     // ---- driver values: storage sized for the largest binding, views for the current one
     ggml_context * vctx = nullptr;
     ggml_backend_buffer_t vbuf = nullptr;
-    ggml_context * view_ctx = nullptr;
+    // Driver values of symbolic shape viewed per binding, the last kKeepBindings bindings used.
+    static constexpr size_t kKeepBindings = 8;
+    struct ViewSet {
+        std::vector<int64_t> binding;
+        ggml_context * ctx = nullptr;
+        std::unordered_map<std::string, ggml_tensor *> views;
+        uint64_t used = 0;
+    };
+    std::vector<ViewSet> view_sets;
+    uint64_t view_clock = 0;
     std::unordered_map<std::string, const TensorSpec *> spec;
     std::unordered_map<std::string, ggml_tensor *> storage, bound;
     std::set<std::string> inputs_set;  // inputs given since load
@@ -1204,6 +1324,7 @@ struct ggml_compiler_model {
     std::vector<Entry> entries;
     std::vector<CallGraph> calls;
     // ---- running
+    std::map<const DriverOp *, std::unique_ptr<UntilState>> untils;
     StreamOps ops;
     StageClock clock;
     std::vector<ggml_compiler_stats> stage_totals;  // ms_total, n_calls per stage
@@ -1216,11 +1337,9 @@ struct ggml_compiler_model {
 
     ~ggml_compiler_model() {
         if (backend) (void) hipStreamSynchronize(backend_stream(backend));
-        for (auto & c : calls) {
-            if (c.alloc) ggml_gallocr_free(c.alloc);
-            c.drop_graph();
-        }
-        if (view_ctx) ggml_free(view_ctx);
+        for (auto & c : calls) c.free_all();
+        for (auto & v : view_sets)
+            if (v.ctx) ggml_free(v.ctx);
         if (vbuf) ggml_backend_buffer_free(vbuf);
         if (vctx) ggml_free(vctx);
         if (wbuf) ggml_backend_buffer_free(wbuf);
@@ -1361,25 +1480,48 @@ struct ggml_compiler_model {
     }
 
     // The current binding's view of every symbolic value (same storage, the binding's shape).
+    // The driver values of symbolic shape, viewed at the current binding: a binding among the
+    // last kKeepBindings reuses its views (which its stages' graphs read); past that the least
+    // recently used binding's views and graphs are dropped.
     void make_views() {
-        if (view_ctx) ggml_free(view_ctx);
-        view_ctx = nullptr;
         size_t n = 0;
         for (const auto & v : prog.values) n += v.symbolic();
         if (n == 0) return;
+        for (ViewSet & vs : view_sets)
+            if (vs.binding == binding) {
+                vs.used = ++view_clock;
+                for (const auto & kv : vs.views) bound[kv.first] = kv.second;
+                return;
+            }
+        if (view_sets.size() >= kKeepBindings) {
+            size_t old = 0;
+            for (size_t k = 1; k < view_sets.size(); k++)
+                if (view_sets[k].used < view_sets[old].used) old = k;
+            for (auto & c : calls) c.forget(view_sets[old].binding);
+            ggml_free(view_sets[old].ctx);
+            view_sets.erase(view_sets.begin() + (long) old);
+        }
+        ViewSet vs;
+        vs.binding = binding;
+        vs.used = ++view_clock;
         ggml_init_params ip{};
         ip.mem_size = ggml_tensor_overhead() * (n + 1);
         ip.no_alloc = true;
-        view_ctx = ggml_init(ip);
+        vs.ctx = ggml_init(ip);
         for (const auto & v : prog.values) {
             if (!v.symbolic()) continue;
             const size_t nb1 = ggml_row_size((ggml_type) v.type, v.ne[0]), nb2 = nb1 * (size_t) v.ne[1];
-            ggml_tensor * t = ggml_view_4d(view_ctx, storage.at(v.name), v.ne[0], v.ne[1], v.ne[2], v.ne[3], nb1, nb2,
+            ggml_tensor * t = ggml_view_4d(vs.ctx, storage.at(v.name), v.ne[0], v.ne[1], v.ne[2], v.ne[3], nb1, nb2,
                                            nb2 * (size_t) v.ne[2], 0);
-            if (!t || ggml_backend_view_init(t) != GGML_STATUS_SUCCESS) fail("cannot view driver value '" + v.name + "'");
+            if (!t || ggml_backend_view_init(t) != GGML_STATUS_SUCCESS) {
+                ggml_free(vs.ctx);
+                fail("cannot view driver value '" + v.name + "'");
+            }
             ggml_set_name(t, v.name.c_str());
+            vs.views[v.name] = t;
             bound[v.name] = t;
         }
+        view_sets.push_back(std::move(vs));
     }
 
     ggml_tensor * value(const std::string & name) const {
@@ -1498,7 +1640,6 @@ struct ggml_compiler_model {
     void build_graph(CallGraph & c) {
         const StageSpec & st = prog.stages[(size_t) c.stage];
         const DriverOp & d = *c.op;
-        c.stale = false;
         if (d.args.size() != st.params.size() || d.out.size() != st.outputs.size())
             fail("call to stage '" + st.name + "' has the wrong number of arguments or results");
         const size_t tensors = 8 * st.nodes.size() + 2 * st.outputs.size() + 16;
@@ -1578,21 +1719,26 @@ struct ggml_compiler_model {
         if (!refused.empty())
             fail(std::string("backend ") + ggml_backend_name(backend) + " cannot run these nodes of stage '" + st.name +
                  "':" + refused);
-        if (!c.alloc) c.alloc = ggml_gallocr_new(ggml_backend_get_default_buffer_type(backend));
+        const bool symbolic = prog.stages[(size_t) c.stage].symbolic;
+        if (symbolic || !c.alloc) c.alloc = ggml_gallocr_new(ggml_backend_get_default_buffer_type(backend));
         if (!ggml_gallocr_alloc_graph(c.alloc, c.graph))
             fail("cannot allocate compute buffer for stage '" + st.name + "': " + last_error());
+        if (symbolic) c.builds.push_back({binding, c.ctx, c.graph, c.alloc});
+        c.stale = false;
     }
 
-    // A new binding: values viewed at their new shapes; graphs of stages whose shapes read a symbol
-    // are rebuilt when next run (so an entry never rebuilds another entry's stages).
+    // A new binding: values viewed at their new shapes; stages whose shapes read a symbol use their
+    // graph of this binding, or build one when next run (so an entry never builds another entry's
+    // stages).
     void apply_binding() {
         if (binding == built) return;
         prog.bind(binding);
         make_views();
         for (auto & c : calls) {
             if (!prog.stages[(size_t) c.stage].symbolic) continue;
-            c.drop_graph();
-            c.stale = true;
+            c.ctx = nullptr, c.graph = nullptr, c.alloc = nullptr, c.stale = true;
+            for (const CallGraph::Build & b : c.builds)
+                if (b.binding == binding) c.use(b);
         }
         for (auto & e : entries)
             for (const VmCode & vc : e.code)
@@ -1647,6 +1793,79 @@ struct ggml_compiler_model {
             ggml_tensor * t = storage.at(c.first);
             ops.clear(t->data, ggml_nbytes(t));
         }
+        f.until = until_state(d);
+        if (f.until) {
+            ops.fill32(f.until->stop, 1, (uint32_t) INT32_MAX);
+            // the loop's previous run waited for its last test op, so nothing still writes these
+            __atomic_store_n(&f.until->host[0], INT32_MAX, __ATOMIC_RELAXED);
+            __atomic_store_n(&f.until->host[1], 0, __ATOMIC_RELEASE);
+        }
+    }
+
+    // The device until test of loop d: one until value of type i32, a body of calls only, the
+    // values it writes (state aside) at most kUntilKeepMax bytes. Other loops (and every loop when
+    // profiling node by node) read their until values after every iteration. Made on the loop's
+    // first entry.
+    static constexpr size_t kUntilKeepMax = 16u << 20;
+    UntilState * until_state(const DriverOp & d) {
+        if (d.until.size() != 1 || spec.at(d.until[0].first)->type != GGML_TYPE_I32 || profile_file()) return nullptr;
+        auto it = untils.find(&d);
+        if (it != untils.end()) return it->second.get();
+        std::vector<std::string> kept;
+        auto keep = [&](const std::string & v) {
+            if (std::find(prog.state.begin(), prog.state.end(), v) == prog.state.end() &&
+                std::find(kept.begin(), kept.end(), v) == kept.end())
+                kept.push_back(v);
+        };
+        for (const DriverOp & b : d.body) {
+            if (b.loop) return nullptr;
+            for (const auto & v : b.out) keep(v);
+        }
+        for (const auto & c : d.carry) keep(c.first);
+        auto u = std::make_unique<UntilState>();
+        const std::vector<int> & ids = d.until[0].second;
+        size_t keep_bytes = 0;
+        for (const auto & v : kept) {
+            u->slot_bytes.push_back(align256(ggml_nbytes(storage.at(v))));
+            keep_bytes += 2 * u->slot_bytes.back();
+        }
+        if (keep_bytes > kUntilKeepMax) return nullptr;
+        u->kept = kept;
+        const size_t id_bytes = align256(std::max<size_t>(1, ids.size()) * 4);
+        check_hip(hipMalloc(&u->dev, 256 + id_bytes + keep_bytes), "hipMalloc (until)");
+        check_hip(hipHostMalloc((void **) &u->host, 2 * sizeof(int32_t), hipHostMallocCoherent), "hipHostMalloc (until)");
+        uint8_t * p = (uint8_t *) u->dev;
+        u->stop = (int32_t *) p;
+        u->ids = (int32_t *) (p + 256);
+        u->n_ids = (int64_t) ids.size();
+        uint8_t * r = p + 256 + id_bytes;
+        for (size_t k = 0; k < kept.size(); k++) {
+            u->ring.push_back(r);
+            r += 2 * u->slot_bytes[k];
+        }
+        std::vector<int32_t> id32(ids.begin(), ids.end());
+        if (!id32.empty())
+            check_hip(hipMemcpy(u->ids, id32.data(), id32.size() * 4, hipMemcpyHostToDevice), "until ids");
+        UntilState * raw = u.get();
+        untils.emplace(&d, std::move(u));
+        return raw;
+    }
+
+    // Waits until the device's until test has run for `done` iterations of the loop (the test op
+    // writes the host's copy; the GPU keeps the next iteration queued meanwhile).
+    void wait_tested(const UntilState & u, int32_t done) {
+        unsigned spins = 0;
+        while (__atomic_load_n(&u.host[1], __ATOMIC_ACQUIRE) < done) {
+            if ((++spins & 1023u) == 0u) {
+                const hipError_t q = hipStreamQuery(ops.stream());
+                if (q == hipSuccess) {
+                    if (__atomic_load_n(&u.host[1], __ATOMIC_ACQUIRE) >= done) break;
+                    fail("loop: the until test of iteration " + std::to_string(done - 1) + " did not report");
+                }
+                if (q != hipErrorNotReady) check_hip(q, "loop until test");
+            }
+            std::this_thread::yield();
+        }
     }
 
     // Before the body of iteration f.i: scalars, slices, counters, bound symbols, causal masks.
@@ -1688,6 +1907,7 @@ struct ggml_compiler_model {
     // After the body: collected rows; true when an until value holds a stop id.
     bool loop_bottom(LoopFrame & f) {
         const DriverOp & d = *f.op;
+        if (f.until) return loop_bottom_device(f);
         for (const auto & c : d.collect) {
             const size_t nb = spec.at(c.second)->nbytes(binding);
             ops.copy((char *) storage.at(c.first)->data + (size_t) f.i * nb, storage.at(c.second)->data, nb);
@@ -1695,6 +1915,52 @@ struct ggml_compiler_model {
         for (const auto & u : d.until) {
             const int32_t tok = ops.read_i32(storage.at(u.first)->data);
             if (std::find(u.second.begin(), u.second.end(), tok) != u.second.end()) return true;
+        }
+        return false;
+    }
+
+    // loop_bottom with the until test on the device. Iteration i's row is collected only at or
+    // before the stop, its test op sets the stop word and the host's copy, and the values its body
+    // wrote (state aside) go to a ring slot. The host then checks iteration i - 1's test
+    // (iteration i stays queued on the GPU meanwhile, so no iteration waits for the host): when
+    // i - 1 stopped, iteration i ran past the loop's end, and every value the loop leaves
+    // (loop-top values, the body's results, carries) is put back to iteration i - 1's, and the
+    // stats drop iteration i's calls. Its one other effect is on state: what the body writes
+    // there one iteration past the stop (the K / V row of the next position, which a later
+    // decode of that position writes before any read). True when the loop ends.
+    bool loop_bottom_device(LoopFrame & f) {
+        const DriverOp & d = *f.op;
+        UntilState & u = *f.until;
+        const int i = f.i;
+        for (const auto & c : d.collect) {
+            const size_t nb = spec.at(c.second)->nbytes(binding);
+            ops.copy_if((char *) storage.at(c.first)->data + (size_t) i * nb, storage.at(c.second)->data, nb, u.stop, i);
+        }
+        ops.until((const int32_t *) storage.at(d.until[0].first)->data, u.ids, u.n_ids, u.stop, u.host, i);
+        for (size_t k = 0; k < u.kept.size(); k++) {
+            ggml_tensor * v = value(u.kept[k]);
+            ops.copy(u.ring[k] + (size_t) (i & 1) * u.slot_bytes[k], v->data, ggml_nbytes(v));
+        }
+        ops.flush();
+        if (i >= 1) {
+            wait_tested(u, i);
+            const int32_t stop = __atomic_load_n(&u.host[0], __ATOMIC_RELAXED);
+            if (stop <= i - 1) {
+                last.n_calls = f.calls0;  // the stats count the calls of the loop's iterations only
+                clock.forget_since(f.marks0);
+                f.i = stop;
+                loop_top(f);  // iteration `stop`'s scalars, slices, counters, symbols, masks
+                for (size_t k = 0; k < u.kept.size(); k++) {
+                    ggml_tensor * v = value(u.kept[k]);
+                    ops.copy(v->data, u.ring[k] + (size_t) (stop & 1) * u.slot_bytes[k], ggml_nbytes(v));
+                }
+                wait_tested(u, i + 1);  // nothing of the loop writes the host's copy after this
+                return true;
+            }
+        }
+        if (i + 1 >= f.trips) {
+            wait_tested(u, i + 1);
+            return true;
         }
         return false;
     }
@@ -1711,7 +1977,7 @@ struct ggml_compiler_model {
                     pc++;
                     break;
                 case VmCode::Enter:
-                    frames.push_back({in.op, 0, 0, {}});
+                    frames.push_back({in.op, 0, 0, {}, nullptr});
                     loop_enter(frames.back());
                     pc++;
                     break;
@@ -1720,6 +1986,8 @@ struct ggml_compiler_model {
                         frames.pop_back();
                         pc = (size_t) in.jump;
                     } else {
+                        frames.back().calls0 = last.n_calls;
+                        frames.back().marks0 = clock.marks();
                         loop_top(frames.back());
                         pc++;
                     }
