@@ -180,7 +180,7 @@ __global__ void k_enc_q4_K(const float * __restrict__ xall, uint8_t * __restrict
     for (int j = 0; j < 8; j++) {
         float sum_x2 = 0;
         for (int l = 0; l < 32; l++) sum_x2 += x[32 * j + l] * x[32 * j + l];
-        const float av_x = __fsqrt_rn(__fdiv_rn(sum_x2, 32.0f));
+        const float av_x = sqrtf(__fdiv_rn(sum_x2, 32.0f));  // IEEE sqrt: __fsqrt_rn is the native approximation here
         for (int l = 0; l < 32; l++) w[l] = av_x + fabsf(x[32 * j + l]);
         scales[j] = qkx2_fit<15, 20>(x + 32 * j, w, L + 32 * j, &mins[j], -1.0f);
         if (scales[j] > max_scale) max_scale = scales[j];
@@ -224,7 +224,7 @@ __global__ void k_enc_q5_K(const float * __restrict__ xall, uint8_t * __restrict
     for (int j = 0; j < 8; j++) {
         float sum_x2 = 0;
         for (int l = 0; l < 32; l++) sum_x2 += x[32 * j + l] * x[32 * j + l];
-        const float av_x = __fsqrt_rn(__fdiv_rn(sum_x2, 32.0f));
+        const float av_x = sqrtf(__fdiv_rn(sum_x2, 32.0f));  // IEEE sqrt: __fsqrt_rn is the native approximation here
         for (int l = 0; l < 32; l++) w[l] = av_x + fabsf(x[32 * j + l]);
         scales[j] = qkx2_fit<31, 15>(x + 32 * j, w, L + 32 * j, &mins[j], -0.5f);
         if (scales[j] > max_scale) max_scale = scales[j];

@@ -34,6 +34,18 @@ def test_weight_encoders_bit_exact(gops, orc, t):
     assert np.array_equal(got, orc.quantize(w, t))
 
 
+@pytest.mark.parametrize("t", ["q4_K", "q5_K", "q6_K"])
+def test_weight_encoders_bit_exact_many_superblocks(gops, orc, t):
+    """32768 super-blocks (a 2048 x 4096 weight): the K-quant searches are sensitive to the last bit
+    of every step (the sub-block weights sqrt(mean x^2) + |x| included, where a sqrt one ulp off
+    changed about one super-block in 800), so every byte must still equal the oracle's."""
+    w = orc.normal((2048, 4096), seed=31, std=0.02)
+    got = to_np(gops.quantize(torch.from_numpy(w).cuda(), t))
+    want = orc.quantize(w, t)
+    bad = np.nonzero((got != want).any(axis=1))[0]
+    assert bad.size == 0, f"{bad.size} rows differ, first {bad[:8].tolist()}"
+
+
 def test_weight_encoder_kats(gops):
     kats = json.loads((GOLDEN / "quant_kats.json").read_text())
     for name, k in kats.items():
