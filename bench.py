@@ -510,7 +510,7 @@ def _rotating_weights(ops, t: str, N: int, K: int, seed: int):
 def bench_sweep(ops, torch, only: set[str] | None = None) -> list[dict]:
     """The other measured configurations (ggml_mul_mat GEMV / GEMM, decode flash_attn_ext), each
     op launched back to back from a HIP graph over inputs rotated past the Infinity Cache. only: the
-    configuration names to run (C1, C2, K56, C3, C4), or all."""
+    configuration names to run (C1, C2, K56, C3, C3K, C4), or all."""
     out = []
 
     def want(cfg):
@@ -537,16 +537,25 @@ def bench_sweep(ops, torch, only: set[str] | None = None) -> list[dict]:
         for K, N in LAYER_SHAPES:
             for B in (1, 8):
                 gemv_case("K56", t, K, N, B)
-    # C3: prefill GEMM, Q8_0 K=4096 N=14336, 512 rows (activation quantization included)
-    if want("C3"):
-        ws = _rotating_weights(ops, "q8_0", 14336, 4096, seed=3)[:4]
-        x = ops.fill_normal((512, 4096), seed=4)
+    def gemm_case(cfg, t, K, N, M):
+        ws = _rotating_weights(ops, t, N, K, seed=3)[:4]
+        x = ops.fill_normal((M, K), seed=4)
         us = _graph_us(torch, [lambda w=w: ops.mul_mat(w, x) for w in ws] * 4, passes=3)
-        flops = 2 * 512 * 14336 * 4096
-        out.append({"config": "C3", "op": "mul_mat", "type": "q8_0", "K": 4096, "N": 14336, "M": 512,
+        flops = 2 * M * N * K
+        out.append({"config": cfg, "op": "mul_mat", "type": t, "K": K, "N": N, "M": M,
                     "us": round(us, 1), "TOP/s": round(flops / us / 1e6, 1),
                     "frac_int8_mfma": round(flops / us / 1e6 / INT8_PEAK_TOPS, 4)})
         del ws
+
+    # C3: prefill GEMM, Q8_0 K=4096 N=14336, 512 rows (activation quantization included)
+    if want("C3"):
+        gemm_case("C3", "q8_0", 4096, 14336, 512)
+    # the same prefill with K-quant weights: gate/up in Q4_K, Q5_K; the down projection (K 14336)
+    # in Q6_K, as Q4_K_M files store it
+    if want("C3K"):
+        gemm_case("C3K", "q4_K", 4096, 14336, 512)
+        gemm_case("C3K", "q5_K", 4096, 14336, 512)
+        gemm_case("C3K", "q6_K", 14336, 4096, 512)
     # C4: decode attention, 32 q heads on 8 KV heads of 128, one query row, every key visible
     for ctx in (512, 4096, 32768) if want("C4") else ():
         kv_bytes = 2 * ctx * 8 * 128 * 2
@@ -578,7 +587,9 @@ def main() -> int:
                          "ggml: the decode step built with the ggml API and run by its graph executor; "
                          "program: the same model as a ggml-compiler program GGUF run by the loader")
     ap.add_argument("--only", default=None,
-                    help="sweep: comma-separated configurations to run (C1, C2, K56, C3, C4); default all")
+                    help="sweep: comma-separated configurations to run (C1, C2, K56, C3, C3K, C4); default all")
+    ap.add_argument("--type", default="q8_0", choices=["q4_0", "q8_0", "q4_K", "q5_K", "q6_K"],
+                    help="gemm: the weight type")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-program", action="store_true", help="skip the program-GGUF decode figure")
     args = ap.parse_args()
@@ -597,10 +608,11 @@ def main() -> int:
     ops.require_device()
     torch.cuda.set_device(0)
     model = None
-    if args.mode == "gemm":  # Q8_0 K=4096 N=14336, 512 rows: the activation quantized once, K launches
-        w = ops.QuantWeight.quantize(ops.fill_normal((14336, 4096), seed=3, std=0.02), "q8_0")
-        act = ops.quantize_act("q8_0", ops.fill_normal((512, 4096), seed=4))
-        y = torch.empty((512, 14336), dtype=torch.float32, device="cuda")
+    if args.mode == "gemm":  # K=4096 N=14336 (Q6_K: K=14336 N=4096), 512 rows: the activation quantized once
+        N, K = (4096, 14336) if args.type == "q6_K" else (14336, 4096)
+        w = ops.QuantWeight.quantize(ops.fill_normal((N, K), seed=3, std=0.02), args.type)
+        act = ops.quantize_act(args.type, ops.fill_normal((512, K), seed=4))
+        y = torch.empty((512, N), dtype=torch.float32, device="cuda")
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
@@ -609,8 +621,8 @@ def main() -> int:
         e1.record()
         torch.cuda.synchronize()
         us = e0.elapsed_time(e1) * 1e3 / args.steps
-        print(json.dumps({"metric": "prefill GEMM TOP/s", "value": round(2 * 512 * 14336 * 4096 / us / 1e6, 1),
-                          "unit": "TOP/s", "us": round(us, 1)}), flush=True)
+        print(json.dumps({"metric": "prefill GEMM TOP/s", "value": round(2 * 512 * N * K / us / 1e6, 1),
+                          "unit": "TOP/s", "us": round(us, 1), "type": args.type}), flush=True)
         return 0
     if args.mode == "steps":
         print(json.dumps(bench_steps(args, torch)), flush=True)

@@ -28,6 +28,11 @@ void launch_gemm(int type, const void * w, int64_t N, int64_t K, const void * ac
                  hipStream_t s, const float * res = nullptr);
 void launch_gemm_block_isums(int type, const void * w, int64_t N, int64_t K, const void * act, int64_t M, int blk,
                              int32_t * out, hipStream_t s);
+bool gemm_kq_fits(int type, int64_t K);
+void launch_gemm_kq(int type, const void * w, int64_t N, int64_t K, const void * act, int64_t M, float * y, int64_t ldy,
+                    hipStream_t s, const float * res = nullptr);
+void launch_gemm_kq_isums(int type, const void * w, int64_t N, int64_t K, const void * act, int64_t M, int sb,
+                          int32_t * out, hipStream_t s);
 size_t attn_workspace(int Sq, int H, int Hkv, int Dv, int n_kv);
 void launch_flash_attn(const float * q, int64_t q_h, int64_t q_s, const void * k, int64_t k_h, int64_t k_j,
                        const void * v, int64_t v_h, int64_t v_j, const void * mask, int64_t m_s, float * out, int D,
@@ -197,22 +202,17 @@ void mul_mat_with_workspace(int wtype, const void * w, int64_t N, int64_t K, con
     if (M <= 8) {
         launch_act_quant(wtype, x, ldx, M, K, ws, s);
         launch_gemv(wtype, w, N, K, ws, M, y, ldy, s);
-    } else if (!is_kquant(wtype)) {
-        launch_act_quant(wtype, x, ldx, M, K, ws, s);
-        launch_gemm(wtype, w, N, K, ws, M, y, ldy, s);
     } else {
-        for (int64_t m = 0; m < M; m += 8) {
-            const int64_t b = std::min<int64_t>(8, M - m);
-            launch_act_quant(wtype, x + m * ldx, ldx, b, K, ws, s);
-            launch_gemv(wtype, w, N, K, ws, b, y + m * ldy, ldy, s);
-        }
+        launch_act_quant(wtype, x, ldx, M, K, ws, s);
+        if (is_kquant(wtype)) launch_gemm_kq(wtype, w, N, K, ws, M, y, ldy, s);
+        else launch_gemm(wtype, w, N, K, ws, M, y, ldy, s);
     }
 }
 
 // Workspace bytes of mul_mat_with_workspace (0 for arguments gcq_act_size rejects).
 size_t mul_mat_workspace_bytes(int wtype, int64_t M, int64_t K) {
     if (!is_weight_type(wtype) || M <= 0 || !row_bytes(wtype, K)) return 0;
-    return act_layout(wtype, (is_kquant(wtype) && M > 8) ? 8 : M, K).total;
+    return act_layout(wtype, M, K).total;
 }
 
 }  // namespace gcq
@@ -261,7 +261,7 @@ size_t gcq_act_size(int wtype, int64_t B, int64_t K) {
 }
 
 size_t gcq_mul_mat_workspace(int wtype, int64_t M, int64_t K) {
-    return gcq_act_size(wtype, (is_kquant(wtype) && M > 8) ? 8 : M, K);
+    return gcq_act_size(wtype, M, K);
 }
 
 size_t gcq_flash_attn_workspace(int Sq, int H, int Hkv, int Dv, int n_kv) {
@@ -343,8 +343,9 @@ int gcq_mul_mat_q(int wtype, const void * w, int64_t N, int64_t K, const void * 
         if (res) need_ptr(res, "res", 4);
         if (M <= 8) {
             launch_gemv(wtype, w, N, K, act, M, y, ldy, as_stream(stream), res);
+        } else if (is_kquant(wtype)) {
+            launch_gemm_kq(wtype, w, N, K, act, M, y, ldy, as_stream(stream), res);
         } else {
-            require(!is_kquant(wtype), "mul_mat_q: a K-quant weight with more than 8 rows needs gcq_mul_mat");
             launch_gemm(wtype, w, N, K, act, M, y, ldy, as_stream(stream), res);
         }
     });
@@ -401,15 +402,16 @@ int gcq_block_isums(int wtype, const void * w, int64_t N, int64_t K, const void 
 int gcq_gemm_block_isums(int wtype, const void * w, int64_t N, int64_t K, const void * act, int64_t M, int blk,
                          int32_t * out, void * stream) {
     return guarded([&] {
-        require(wtype == T_Q4_0 || wtype == T_Q8_0, "gemm isums: Q4_0 or Q8_0 weights");
+        need_weight_type(wtype);
         need_k(wtype, K);
         need_dims(N, "N");
         need_dims(M, "M");
-        need_dims(blk, "blk", 0, K / 32 - 1);
+        need_dims(blk, "blk", 0, K / block_elems(wtype) - 1);
         need_ptr(w, "w", 16);
         need_ptr(act, "act", 256);
         need_ptr(out, "out", 4);
-        launch_gemm_block_isums(wtype, w, N, K, act, M, blk, out, as_stream(stream));
+        if (is_kquant(wtype)) launch_gemm_kq_isums(wtype, w, N, K, act, M, blk, out, as_stream(stream));
+        else launch_gemm_block_isums(wtype, w, N, K, act, M, blk, out, as_stream(stream));
     });
 }
 

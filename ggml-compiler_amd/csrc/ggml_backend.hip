@@ -38,6 +38,8 @@ void launch_gemv(int type, const void * w, int64_t N, int64_t K, const void * ac
                  hipStream_t s, const float * res);
 void launch_gemm(int type, const void * w, int64_t N, int64_t K, const void * act, int64_t M, float * y, int64_t ldy,
                  hipStream_t s, const float * res);
+void launch_gemm_kq(int type, const void * w, int64_t N, int64_t K, const void * act, int64_t M, float * y, int64_t ldy,
+                    hipStream_t s, const float * res);
 size_t attn_workspace(int Sq, int H, int Hkv, int Dv, int n_kv);
 void launch_flash_attn(const float * q, int64_t q_h, int64_t q_s, const void * k, int64_t k_h, int64_t k_j,
                        const void * v, int64_t v_h, int64_t v_j, const void * mask, int64_t m_s, float * out, int D,
@@ -682,10 +684,7 @@ struct Planner {
         s.n[4] = N;  // ldy: results are contiguous
         s.f[0] = eps;
         const bool row = M == 1 && (w->type == GGML_TYPE_Q4_0 || w->type == GGML_TYPE_Q8_0) && row_gemv_fits(w->type, K);
-        if (!row) {
-            const int64_t B = is_kquant(w->type) ? std::min<int64_t>(M, 8) : M;
-            ws_need = std::max(ws_need, act_layout(w->type, B, K).total);
-        }
+        if (!row) ws_need = std::max(ws_need, act_layout(w->type, M, K).total);
         steps.push_back(s);
     }
 
@@ -1469,17 +1468,10 @@ void run_step(const ggml_backend * be, const Step & s) {
                 launch_row_gemv(wt, nw ? PRO_NORM : PRO_PLAIN, EPI_STORE, a, st);
                 return;
             }
-            if (is_kquant(wt) && M > 8) {
-                for (int64_t m = 0; m < M; m += 8) {
-                    const int64_t b = std::min<int64_t>(8, M - m);
-                    launch_act_quant(wt, x + m * ldx, ldx, b, K, be->ws, st);
-                    launch_gemv(wt, s.in[0], N, K, be->ws, b, y + m * ldy, ldy, st, res ? res + m * ldy : nullptr);
-                }
-                return;
-            }
             if (nw) launch_rmsnorm_q8(x, ldx, nw, s.f[0], M, K, be->ws, st);
             else launch_act_quant(wt, x, ldx, M, K, be->ws, st);
             if (M <= 8) launch_gemv(wt, s.in[0], N, K, be->ws, M, y, ldy, st, res);
+            else if (is_kquant(wt)) launch_gemm_kq(wt, s.in[0], N, K, be->ws, M, y, ldy, st, res);
             else launch_gemm(wt, s.in[0], N, K, be->ws, M, y, ldy, st, res);
             return;
         }

@@ -200,7 +200,10 @@ def block_isums(w: QuantWeight, act: torch.Tensor, B: int) -> torch.Tensor:
 
 
 def gemm_block_isums(w: QuantWeight, act: torch.Tensor, M: int, blk: int) -> torch.Tensor:
-    out = torch.empty((M, w.N), dtype=torch.int32, device=act.device)
+    """The GEMM's int32 sums of K-block blk: [M, N] (Q4_0 / Q8_0: a 32-value block; Q6_K: a
+    super-block's sum sc * dot) or [M, N, 2] (Q4_K / Q5_K: sum sc * dot, sum m * bsums)."""
+    shape = (M, w.N, 2) if w.type in KQUANTS and w.type != Q6_K else (M, w.N)
+    out = torch.empty(shape, dtype=torch.int32, device=act.device)
     check(load().gcq_gemm_block_isums(w.type, _p(w.data), w.N, w.K, _p(act), M, blk, _p(out), _stream()))
     return out
 

@@ -83,8 +83,9 @@ GCQ_API int gcq_act_to_ggml(int wtype, const void * act, int64_t B, int64_t K, v
 /* ---- mul_mat -------------------------------------------------------------------------------- */
 /* y[m][n] (row stride ldy) = sum_k W[n][k] x[m][k], x f32 [M][ldx]: ggml_mul_mat(W, x) with W a
  * packed Q4_0 / Q8_0 / Q4_K / Q5_K / Q6_K weight (runtime/src/ops.cpp:107-119 ->
- * runtime/include/ggml_compiler_ops.h:116-122). M <= 8: GEMV; M > 8: int8-MFMA GEMM (Q4_0, Q8_0)
- * or GEMV in groups of 8 rows (K-quants). ws: gcq_mul_mat_workspace bytes, 256-byte aligned. */
+ * runtime/include/ggml_compiler_ops.h:116-122). M <= 8: GEMV; M > 8: int8-MFMA GEMM (Q4_0 / Q8_0
+ * per 32-value block, the K-quants per 256-value super-block). ws: gcq_mul_mat_workspace bytes,
+ * 256-byte aligned. */
 GCQ_API int gcq_mul_mat(int wtype, const void * w, int64_t N, int64_t K, const float * x, int64_t ldx, int64_t M,
                         float * y, int64_t ldy, void * ws, size_t ws_size, void * stream);
 /* gcq_mul_mat without a workspace argument and without any device allocation. No counterpart in
@@ -107,7 +108,9 @@ GCQ_API int gcq_mul_mat_q(int wtype, const void * w, int64_t N, int64_t K, const
  * out[b][n][superblock][17] (Q6_K: 16 sub-block sums of (q - 32) * x, sum sc * those). B <= 8. */
 GCQ_API int gcq_block_isums(int wtype, const void * w, int64_t N, int64_t K, const void * act, int64_t B,
                             int32_t * out, void * stream);
-/* The GEMM's (MFMA) int32 sums of K-block blk: out[m][n]. */
+/* The GEMM's (MFMA) int32 sums of K-block blk: out[m][n] (Q4_0 / Q8_0, blk a 32-value block);
+ * K-quants, blk a 256-value super-block: out[m][n][2] = {sum sc * dot, sum m * bsums} (Q4_K, Q5_K)
+ * or out[m][n] = sum sc * dot (Q6_K), the same integers as gcq_block_isums' last one or two. */
 GCQ_API int gcq_gemm_block_isums(int wtype, const void * w, int64_t N, int64_t K, const void * act, int64_t M,
                                  int blk, int32_t * out, void * stream);
 

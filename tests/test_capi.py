@@ -53,7 +53,9 @@ def test_packed_and_workspace_sizes():
     assert lib.gcq_weight_size(2, 4096, 4096) == 4096 * 128 * 16 + 4096 * 128 * 2
     assert lib.gcq_weight_size(12, 4096, 4096) == 4096 * 2304
     assert lib.gcq_act_size(2, 1, 4096) == 4096 + 128 * 8
-    assert lib.gcq_mul_mat_workspace(12, 100, 4096) == lib.gcq_act_size(12, 8, 4096)
+    # the whole quantized activation: the K-quant GEMM reads every row's codes, block sums and d
+    assert lib.gcq_mul_mat_workspace(12, 100, 4096) == lib.gcq_act_size(12, 100, 4096)
+    assert lib.gcq_act_size(12, 100, 4096) == 100 * 4096 + 100 * 256 * 2 + 100 * 16 * 4
     assert lib.gcq_weight_size(3, 1, 32) == 0
     assert lib.gcq_flash_attn_workspace(1, 32, 8, 128, 4096) > 0
 

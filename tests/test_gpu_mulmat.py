@@ -88,12 +88,62 @@ def test_gemm_prefill_shape_row_slices(gops, orc):
     assert orc.parity(y[np.ix_(rows, cols)], ref) < TOL
 
 
-@pytest.mark.parametrize("t", ["q4_K", "q5_K", "q6_K"])
-def test_kquant_many_rows_in_groups_of_8(gops, orc, t):
-    raw, qw = _weight(gops, orc, t, 100, 512, 33)
-    x = orc.normal((21, 512), seed=34)
+KQ = ["q4_K", "q5_K", "q6_K"]
+
+
+@pytest.mark.parametrize("t", KQ)
+@pytest.mark.parametrize("M,N,K", [(9, 100, 256), (21, 300, 512), (200, 333, 2816), (256, 512, 1024)])
+def test_gemm_kquant_matches_oracle(gops, orc, t, M, N, K):
+    """The K-quant MFMA GEMM (M > 8 rows): one super-block (K 256), a partial row and column tile
+    (9 x 100, 200 x 333), eleven super-blocks, and a grid of 8 tiles (256 x 512, tiles renumbered
+    per XCD)."""
+    raw, qw = _weight(gops, orc, t, N, K, 33)
+    x = orc.normal((M, K), seed=34)
     y = to_np(gops.mul_mat(qw, torch.from_numpy(x).cuda()))
-    assert orc.parity(y, orc.mul_mat(raw, t, x, 512)) < TOL
+    assert orc.parity(y, orc.mul_mat(raw, t, x, K)) < TOL
+
+
+@pytest.mark.parametrize("t", KQ)
+def test_gemm_kquant_superblock_sums_bit_exact(gops, orc, t):
+    """Per super-block, the GEMM's two integers (sum sc * sub-block dot; sum m * bsums, whose
+    bsums the kernel splits as 64 hi + lo) equal the oracle's at every (m, n), over a partial tile
+    in both dimensions. The activation has rows of extreme codes: all +127, all -127, and -127 /
+    +127 alternating, so the block sums reach +-32 * 127 and the split's hi byte its ends."""
+    M, N, K = 133, 70, 768
+    raw, qw = _weight(gops, orc, t, N, K, 29)
+    x = orc.normal((M, K), seed=30)
+    x[3] = 1.0
+    x[4] = -1.0
+    x[5, 0::2], x[5, 1::2] = -1.0, 1.0
+    act = gops.quantize_act(t, torch.from_numpy(x).cuda())
+    xq = orc.quantize_act_q8_K(x)
+    per = 17 if t == "q6_K" else 10
+    want_all = np.array([[orc.block_isums(t, raw[n], xq[m], K) for n in range(N)] for m in range(M)])
+    for sb in (0, 2):
+        got = to_np(gops.gemm_block_isums(qw, act, M, sb))
+        if t == "q6_K":
+            want = want_all[:, :, sb * per + 16]
+        else:
+            want = want_all[:, :, sb * per + 8:sb * per + 10]
+        assert got.shape == want.shape
+        assert np.array_equal(got, want), sb
+
+
+@pytest.mark.parametrize("t", ["q4_K", "q5_K"])
+def test_gemm_kquant_residual(gops, orc, t):
+    """mul_mat_q on a pre-quantized K-quant activation of 16 rows with a residual (y = res + W x),
+    including res aliased to y."""
+    M, N, K = 16, 1000, 2048
+    raw, qw = _weight(gops, orc, t, N, K, 44)
+    x = orc.normal((M, K), seed=45)
+    r = orc.normal((M, N), seed=46)
+    act = gops.quantize_act(t, torch.from_numpy(x).cuda())
+    want = orc.mul_mat(raw, t, x, K) + r
+    y = to_np(gops.mul_mat_q(qw, act, M, res=torch.from_numpy(r).cuda()))
+    assert orc.parity(y, want) < TOL
+    rr = torch.from_numpy(r).cuda()
+    gops.mul_mat_q(qw, act, M, res=rr, out=rr)
+    assert np.array_equal(to_np(rr), y)
 
 
 def test_gemv_is_linear_at_full_size(gops):
@@ -145,14 +195,12 @@ def test_gemv_c1_q8_0_4096(gops, orc):
 @pytest.mark.parametrize("K", [2048, 3104, 14336])
 def test_gemv_batches_residual(gops, orc, t, B, K):
     """Batches of 2..8 rows (the K-sliced kernel: one wavefront per 64 tasks of 32 values of K,
-    the activation in registers, R-row batches) and 16 (the GEMM / K-quant kernel): a row count
+    the activation in registers, R-row batches) and 16 (the GEMMs): a row count
     that is not a multiple of the row batch, a residual, K of one wavefront (2048), of a partly
     filled second one (3104 = 97 blocks: lanes past the row; Q4_0 / Q8_0 only, K-quant rows are
     whole 256-value super-blocks) and of seven (14336), B padded to a power of two (3, 5)."""
     if t in ("q4_K", "q5_K") and K % 256:
         pytest.skip("K-quant rows are whole 256-value super-blocks")
-    if t in ("q4_K", "q5_K") and B > 8:
-        pytest.skip("mul_mat_q takes a pre-quantized K-quant activation of at most 8 rows")
     N = 1000
     raw, qw = _weight(gops, orc, t, N, K, 44)
     x = orc.normal((B, K), seed=45)
@@ -182,3 +230,18 @@ def test_gemv_row_kquant_fused_quantizer(gops, orc, t, K):
     y_sep = to_np(gops.mul_mat_q(qw, act, 1))
     assert np.array_equal(y, y_sep), float(np.abs(y - y_sep).max())
     assert orc.parity(y, orc.mul_mat(raw, t, x, K)) < TOL
+
+
+@pytest.mark.parametrize("t,N,K", [("q4_K", 14336, 4096), ("q6_K", 4096, 14336)])
+def test_gemm_kquant_prefill_shape_row_slices(gops, orc, t, N, K):
+    """Prefill of 512 rows at the 8B shapes (gate/up 4096 -> 14336 in Q4_K, down 14336 -> 4096 in
+    Q6_K), the whole product on the GPU; the oracle checks a slice of rows and columns (each
+    output depends only on its own activation row and weight row)."""
+    M = 512
+    raw, qw = _full_weight(gops, t, N, K)
+    x = gops.fill_normal((M, K), seed=32)
+    y = to_np(gops.mul_mat(qw, x))
+    rows = np.r_[0:8, 250:258, 504:512]
+    cols = np.r_[0:64, N // 2:N // 2 + 64, N - 64:N]
+    ref = orc.mul_mat(raw[cols], t, orc.normal((M, K), seed=32)[rows], K)
+    assert orc.parity(y[np.ix_(rows, cols)], ref) < TOL
