@@ -136,10 +136,13 @@ def _host_array(x: Any, dtype: np.dtype) -> np.ndarray:
 
 
 class Session:
-    """A loaded ggml-compiler GGUF. `run` takes an entry's inputs positionally or by name (any
-    shape its symbols allow: they are bound from the input shapes) and returns its outputs by name.
-    `entries` maps each entry point to its (inputs, outputs); `inputs` / `outputs` are the first
-    entry's. State (a KV cache) persists across runs until `reset()`."""
+    """A ggml-compiler GGUF loaded onto the GPU.
+
+    `run(*inputs, entry=None, **named)` executes one entry point (default: the first) and returns a
+    dict of its outputs. Inputs may have any shape the program's symbolic dimensions admit; the
+    symbols take their values from those shapes. `entries` gives every entry point's input and
+    output descriptions, `inputs` / `outputs` the first one's. Persistent tensors (the KV cache)
+    keep their contents from one run to the next; `reset()` clears them."""
 
     def __init__(self, path: str | os.PathLike, backend: str = "auto", device: int = 0, n_threads: int = 0,
                  allow_cpu_fallback: bool = False) -> None:
@@ -158,20 +161,22 @@ class Session:
 
     @property
     def metadata(self) -> dict[str, Any]:
-        """The program's own metadata ("ggml_compiler.meta"), or {}."""
+        """The JSON object stored under the GGUF key "ggml_compiler.meta" (empty when absent)."""
         text = self._model.lib.ggml_compiler_metadata(self._model.ptr, b"ggml_compiler.meta")
         return json.loads(text.decode()) if text else {}
 
     def set_symbol(self, name: str, value: int) -> None:
-        """Bind a symbol no input shape carries (a loop's trip count)."""
+        """Set a symbol by hand: for symbols that no input's shape determines, such as how many
+        times a driver loop iterates."""
         _check(self._model.lib.ggml_compiler_set_symbol(self._model.ptr, name.encode(), int(value)))
 
     def bound(self) -> dict[str, int]:
-        """Every symbol's current value."""
+        """Symbol name -> the value it is bound to now."""
         return {name: val for name, _, _, val in (self._model.symbol(k) for k in range(len(self.symbols)))}
 
     def reset(self) -> None:
-        """Zero the program's state (a KV cache)."""
+        """Clear every persistent state tensor to zeros, e.g. empty the KV cache before a new
+        sequence."""
         _check(self._model.lib.ggml_compiler_reset(self._model.ptr))
 
     def run(self, *args: Any, entry: str | None = None, **kwargs: Any) -> dict[str, np.ndarray]:

@@ -171,11 +171,12 @@ def _full_weight(gops, t, N, K):
 
 
 @pytest.mark.parametrize("t", ["q4_0", "q4_K"])
-@pytest.mark.parametrize("N,K", [(28672, 4096), (4096, 14336)])
-@pytest.mark.parametrize("B", [1, 4, 8])
+@pytest.mark.parametrize("N,K", [(4096, 4096), (6144, 4096), (28672, 4096), (4096, 14336)])
+@pytest.mark.parametrize("B", [1, 2, 4, 8])
 def test_gemv_full_decode_shapes(gops, orc, t, N, K, B):
-    """The decode batch shapes at full size (fused gate/up 4096 x 28672, down 14336 x 4096) for 1,
-    4 and 8 rows, every output against the oracle."""
+    """The decode shapes at full size for 1, 2, 4 and 8 rows, every output against the oracle:
+    attention output 4096 x 4096, fused QKV 4096 x 6144, fused gate/up 4096 x 28672, down
+    14336 x 4096 (the row GEMV's dispatch and the batched kernels' plans depend on N)."""
     raw, qw = _full_weight(gops, t, N, K)
     x = orc.normal((B, K), seed=42 + B)
     y = to_np(gops.mul_mat(qw, torch.from_numpy(x).cuda()))
