@@ -15,20 +15,26 @@
 // sub-blocks: the activation's block sums split into bytes (bs = 64 hi + lo, lo in [0, 64)) against
 // the weight's 6-bit mins, two MFMAs of K 32 (8 used) per super-block.
 //
-// Workgroup tile 128 (m) x 128 (n), 4 wavefronts of 64 x 64 (2 x 2 MFMA tiles of 32 x 32). The K
+// Workgroup tile 128 (m) x 128 (n), 8 wavefronts of 64 x 32 (2 MFMA tiles of 32 x 32). The K
 // loop steps half a super-block (128 values) at a time: the next half's global loads are issued
 // into registers before the current half is computed from LDS, then stored (weights expanded to
 // int8 codes, the super-block's scales decoded); activations and weights of a tile are read once
-// per workgroup. Tiles are numbered so that the workgroups sharing a weight tile land on one XCD.
+// per workgroup. A wavefront's 64 outputs per lane (f32 sums and the super-block's int32 sums) keep it
+// within 256 registers, two wavefronts per SIMD. Tiles are numbered
+// so that the workgroups sharing a weight tile land on one XCD.
 #include "gcq_common.h"
 
 namespace gcq {
+
+int cu_count();
+
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
-constexpr int TM = 128, TN = 128;  // workgroup tile
+constexpr int TM = 128;            // workgroup tile rows; its columns TN: 128, or 64 for small grids
+constexpr int NT = 512;            // threads: 8 wavefronts of 64 (m) x 32 (n)
 constexpr int HV = 128;            // values per K step (half a super-block)
 constexpr int KP = HV + 16;        // LDS row pitch of the codes (bytes; 16 B pad against bank conflicts)
 
@@ -37,15 +43,14 @@ struct Kq {
     static constexpr int BB = TYPE == T_Q4_K ? 144 : TYPE == T_Q5_K ? 176 : 208;  // device block bytes
     static constexpr bool MIN = TYPE != T_Q6_K;  // a min term (Q4_K / Q5_K)
     static constexpr int NSUB = TYPE == T_Q6_K ? 16 : 8;  // scales per super-block
-    static constexpr int BI = TYPE == T_Q6_K ? 1 : 2;     // weight-code items (16 B of codes each) per thread
 };
 
 // Registers between one K step's global loads and its LDS store (thread t's share).
 template <int TYPE>
 struct KqStage {
-    v4i a[4];          // activation codes: 128 rows x 128 B, 16 B chunks t, t + 256, ...
-    v4i b[Kq<TYPE>::BI];   // weight bytes: Q4_K / Q5_K 16 B of nibbles; Q6_K ql (first half)
-    v4i b2[TYPE == T_Q4_K ? 1 : Kq<TYPE>::BI];  // Q5_K: 16 B of qh; Q6_K: ql (second half)
+    v4i a[2];          // activation codes: 128 rows x 128 B, 16 B chunks t and t + 512
+    v4i b;             // weight bytes: Q4_K / Q5_K 16 B of nibbles; Q6_K (t < 256) ql, first half
+    v4i b2;            // Q5_K: 16 B of qh; Q6_K: ql, second half
     v4i b3;            // Q6_K: 16 B of qh
     // first half only: t < 128: e0 = the weight row's 16 B of d / dmin / scales (Q6_K: scales),
     // dw = its fp16 d (Q6_K); t >= 128: e0, e1 = the activation row's 16 block sums (int16), dx
@@ -80,46 +85,44 @@ struct KqArgs {
     const float * xd;       // d [M][K / 256]
     float * y;
     const float * res;
-    int32_t * raw;          // RAW: the integer parts of super-block raw_sb, [M][N][2] (Q6_K: [M][N][1])
+    int32_t * raw;          // RAW: the integer parts of super-block raw_sb, [M][N][2] (Q6_K: [M][N][1]), stored
+                            // when its second half is done
     int M, N, nsb, ldy, raw_sb;
 };
 
-template <int TYPE>
+template <int TYPE, int TN>
 __device__ __forceinline__ void kq_load(KqStage<TYPE> & st, const KqArgs<TYPE> & a, int m0, int n0, int step) {
     const int t = threadIdx.x;
     const int sb = step >> 1, h = step & 1;
     const int K = a.nsb * 256;
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-        const int c = t + 256 * q, row = c >> 3, part = c & 7;
+    for (int q = 0; q < 2; q++) {
+        const int c = t + NT * q, row = c >> 3, part = c & 7;
         const int m = min(m0 + row, a.M - 1);
         st.a[q] = *reinterpret_cast<const v4i *>(a.xc + (size_t) m * K + sb * 256 + h * HV + 16 * part);
     }
     if constexpr (TYPE == T_Q6_K) {
-        const int row = t >> 1, l0 = 16 * (t & 1);
-        const uint8_t * blk = a.w + ((size_t) min(n0 + row, a.N - 1) * a.nsb + sb) * Kq<TYPE>::BB;
-        st.b[0] = *reinterpret_cast<const v4i *>(blk + 64 * h + l0);
-        st.b2[0] = *reinterpret_cast<const v4i *>(blk + 64 * h + 32 + l0);
-        st.b3 = *reinterpret_cast<const v4i *>(blk + 128 + 32 * h + l0);
-    } else {
-        // items t and t + 256: rows t / 4 and 64 + t / 4, the same u = t % 4
+        if (t < 2 * TN) {  // row t / 2, bytes l0 .. l0 + 15 of each 32 of the half
+            const int row = t >> 1, l0 = 16 * (t & 1);
+            const uint8_t * blk = a.w + ((size_t) min(n0 + row, a.N - 1) * a.nsb + sb) * Kq<TYPE>::BB;
+            st.b = *reinterpret_cast<const v4i *>(blk + 64 * h + l0);
+            st.b2 = *reinterpret_cast<const v4i *>(blk + 64 * h + 32 + l0);
+            st.b3 = *reinterpret_cast<const v4i *>(blk + 128 + 32 * h + l0);
+        }
+    } else if (t < 4 * TN) {
+        // row t / 4, u = t % 4: 16 B of nibbles (and Q5_K the matching 16 B of qh)
         const int row = t >> 2, u = t & 3;
         const int qs = TYPE == T_Q4_K ? 16 : 48;
         const uint8_t * b0 = a.w + ((size_t) min(n0 + row, a.N - 1) * a.nsb + sb) * Kq<TYPE>::BB;
-        const uint8_t * b1 = a.w + ((size_t) min(n0 + row + 64, a.N - 1) * a.nsb + sb) * Kq<TYPE>::BB;
-        st.b[0] = *reinterpret_cast<const v4i *>(b0 + qs + 64 * h + 16 * u);
-        st.b[1] = *reinterpret_cast<const v4i *>(b1 + qs + 64 * h + 16 * u);
-        if constexpr (TYPE == T_Q5_K) {
-            st.b2[0] = *reinterpret_cast<const v4i *>(b0 + 16 + 16 * (u & 1));
-            st.b2[1] = *reinterpret_cast<const v4i *>(b1 + 16 + 16 * (u & 1));
-        }
+        st.b = *reinterpret_cast<const v4i *>(b0 + qs + 64 * h + 16 * u);
+        if constexpr (TYPE == T_Q5_K) st.b2 = *reinterpret_cast<const v4i *>(b0 + 16 + 16 * (u & 1));
     }
     if (h == 0) {
         if (t < TN) {
             const size_t bi = (size_t) min(n0 + t, a.N - 1) * a.nsb + sb;
             st.e0 = *reinterpret_cast<const v4i *>(a.w + bi * Kq<TYPE>::BB + (TYPE == T_Q6_K ? 192 : 0));
             if constexpr (TYPE == T_Q6_K) st.dw = a.wd[bi];
-        } else {
+        } else if (t < TN + TM) {
             const int m = min(m0 + t - TN, a.M - 1);
             st.dx = a.xd[(size_t) m * a.nsb + sb];
             const v4i * bp = reinterpret_cast<const v4i *>(a.xbs + (size_t) m * (a.nsb * 16) + sb * 16);
@@ -129,68 +132,71 @@ __device__ __forceinline__ void kq_load(KqStage<TYPE> & st, const KqArgs<TYPE> &
     }
 }
 
-// LDS of one K step and of one super-block's scales.
+// LDS of one K step and of one super-block's scales (one copy: the next super-block's are stored
+// after a barrier that follows the last use of these, which keeps a workgroup under 80 KB of LDS,
+// two of them per CU).
+template <int TN>
 struct KqLds {
     int8_t A[TM * KP];
     int8_t B[TN * KP];
 };
+template <int TYPE, int TN>
 struct KqScales {
-    int8_t sc[TN][16];   // Q4_K / Q5_K: sc_j (j < 8); Q6_K: the 16 int8 scales
-    int8_t mn[TN][8];    // Q4_K / Q5_K: m_j
-    int8_t bh[TM][8], bl[TM][8];  // activation block sums per sub-block: 64 bh + bl
-    float dw[TN], dm[TN], dx[TM];
+    int8_t sc[TN][Kq<TYPE>::NSUB];  // Q4_K / Q5_K: the 6-bit sc_j; Q6_K: the 16 int8 scales
+    int8_t mn[Kq<TYPE>::MIN ? TN : 1][8];  // Q4_K / Q5_K: m_j
+    int8_t bh[Kq<TYPE>::MIN ? TM : 1][8], bl[Kq<TYPE>::MIN ? TM : 1][8];  // block sums of sub-block j: 64 bh + bl
+    float dw[TN], dm[Kq<TYPE>::MIN ? TN : 1], dx[TM];
 };
 
 // Byte-wise: codes in [0, 64) minus 32 as int8.
 __device__ __forceinline__ uint32_t minus32(uint32_t v) { return ((v | 0x80808080u) - 0x20202020u) ^ 0x80808080u; }
 
-template <int TYPE>
-__device__ __forceinline__ void kq_store(const KqStage<TYPE> & st, KqLds & L, KqScales & S, int step) {
+template <int TYPE, int TN>
+__device__ __forceinline__ void kq_store(const KqStage<TYPE> & st, KqLds<TN> & L, KqScales<TYPE, TN> & S, int step) {
     const int t = threadIdx.x;
     const int h = step & 1;
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-        const int c = t + 256 * q, row = c >> 3, part = c & 7;
+    for (int q = 0; q < 2; q++) {
+        const int c = t + NT * q, row = c >> 3, part = c & 7;
         *reinterpret_cast<v4i *>(L.A + row * KP + 16 * part) = st.a[q];
     }
     if constexpr (TYPE == T_Q6_K) {
         // value r = 32 p + l of the half: low 4 bits from ql (p even: the first 32 bytes, odd: the
         // second; p < 2 low nibbles, else high), 2 high bits from qh[l] >> 2p
-        const int row = t >> 1, l0 = 16 * (t & 1);
-        v4i o[4];
+        if (t < 2 * TN) {
+            const int row = t >> 1, l0 = 16 * (t & 1);
+            v4i o[4];
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const uint32_t x = u32(st.b[0][e]), y = u32(st.b2[0][e]), hq = u32(st.b3[e]);
-            o[0][e] = (int) minus32((x & 0x0F0F0F0Fu) | ((hq & 0x03030303u) << 4));
-            o[1][e] = (int) minus32((y & 0x0F0F0F0Fu) | (((hq >> 2) & 0x03030303u) << 4));
-            o[2][e] = (int) minus32(((x >> 4) & 0x0F0F0F0Fu) | (((hq >> 4) & 0x03030303u) << 4));
-            o[3][e] = (int) minus32(((y >> 4) & 0x0F0F0F0Fu) | (((hq >> 6) & 0x03030303u) << 4));
+            for (int e = 0; e < 4; e++) {
+                const uint32_t x = u32(st.b[e]), y = u32(st.b2[e]), hq = u32(st.b3[e]);
+                o[0][e] = (int) minus32((x & 0x0F0F0F0Fu) | ((hq & 0x03030303u) << 4));
+                o[1][e] = (int) minus32((y & 0x0F0F0F0Fu) | (((hq >> 2) & 0x03030303u) << 4));
+                o[2][e] = (int) minus32(((x >> 4) & 0x0F0F0F0Fu) | (((hq >> 4) & 0x03030303u) << 4));
+                o[3][e] = (int) minus32(((y >> 4) & 0x0F0F0F0Fu) | (((hq >> 6) & 0x03030303u) << 4));
+            }
+#pragma unroll
+            for (int p = 0; p < 4; p++) *reinterpret_cast<v4i *>(L.B + row * KP + 32 * p + l0) = o[p];
         }
-#pragma unroll
-        for (int p = 0; p < 4; p++) *reinterpret_cast<v4i *>(L.B + row * KP + 32 * p + l0) = o[p];
-    } else {
+    } else if (t < 4 * TN) {
         // 16 B of nibbles of chunk c = 2h + u / 2 at bytes l0 = 16 (u % 2): low nibbles are values
         // 64c + l0 + k, high ones 64c + 32 + l0 + k; Q5_K adds 16 times bit 2c / 2c + 1 of qh[l0 + k]
+        const int row = t >> 2, u = t & 3;
+        const int cc = 2 * h + (u >> 1);
+        v4i lo, hi;
 #pragma unroll
-        for (int q = 0; q < 2; q++) {
-            const int e = t + 256 * q, row = e >> 2, u = e & 3;
-            const int cc = 2 * h + (u >> 1);
-            v4i lo, hi;
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const uint32_t x = u32(st.b[q][k]);
-                uint32_t l = x & 0x0F0F0F0Fu, g = (x >> 4) & 0x0F0F0F0Fu;
-                if constexpr (TYPE == T_Q5_K) {
-                    const uint32_t hq = u32(st.b2[q][k]);
-                    l |= ((hq >> (2 * cc)) & 0x01010101u) << 4;
-                    g |= ((hq >> (2 * cc + 1)) & 0x01010101u) << 4;
-                }
-                lo[k] = (int) l;
-                hi[k] = (int) g;
+        for (int k = 0; k < 4; k++) {
+            const uint32_t x = u32(st.b[k]);
+            uint32_t l = x & 0x0F0F0F0Fu, g = (x >> 4) & 0x0F0F0F0Fu;
+            if constexpr (TYPE == T_Q5_K) {
+                const uint32_t hq = u32(st.b2[k]);
+                l |= ((hq >> (2 * cc)) & 0x01010101u) << 4;
+                g |= ((hq >> (2 * cc + 1)) & 0x01010101u) << 4;
             }
-            *reinterpret_cast<v4i *>(L.B + row * KP + 64 * (u >> 1) + 16 * (u & 1)) = lo;
-            *reinterpret_cast<v4i *>(L.B + row * KP + 64 * (u >> 1) + 32 + 16 * (u & 1)) = hi;
+            lo[k] = (int) l;
+            hi[k] = (int) g;
         }
+        *reinterpret_cast<v4i *>(L.B + row * KP + 64 * (u >> 1) + 16 * (u & 1)) = lo;
+        *reinterpret_cast<v4i *>(L.B + row * KP + 64 * (u >> 1) + 32 + 16 * (u & 1)) = hi;
     }
     if (h == 0) {
         if (t < TN) {
@@ -209,7 +215,7 @@ __device__ __forceinline__ void kq_store(const KqStage<TYPE> & st, KqLds & L, Kq
                     S.mn[t][j] = (int8_t) m;
                 }
             }
-        } else {
+        } else if (t < TN + TM) {
             const int row = t - TN;
             S.dx[row] = st.dx;
             if constexpr (Kq<TYPE>::MIN) {
@@ -228,170 +234,154 @@ __device__ __forceinline__ void kq_store(const KqStage<TYPE> & st, KqLds & L, Kq
     }
 }
 
-template <int TYPE, bool RAW>
-__global__ __launch_bounds__(256) void k_gemm_kq(const KqArgs<TYPE> a) {
-    __shared__ __align__(16) KqLds L[2];
-    __shared__ __align__(16) KqScales S[2];
+template <int TYPE, bool RAW, int TN>
+__global__ __launch_bounds__(NT) void k_gemm_kq(const KqArgs<TYPE> a) {
+    constexpr int WN = TN / 32;         // wavefronts along n, each 32 columns
+    constexpr int XT = TM / 32 / (8 / WN);  // 32-row MFMA tiles per wavefront: 2 (TN 128) or 1 (TN 64)
+    __shared__ __align__(16) KqLds<TN> L[2];
+    __shared__ __align__(16) KqScales<TYPE, TN> S;
     const int mt = (a.M + TM - 1) / TM, nt = (a.N + TN - 1) / TN, total = mt * nt;
     int id = blockIdx.x;
     if (total % 8 == 0) id = (id % 8) * (total / 8) + id / 8;  // XCD x holds a contiguous run of tiles
     const int m0 = (id % mt) * TM, n0 = (id / mt) * TN;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WN, wn = wave % WN;  // this wavefront: rows wm * 32 XT + [0, 32 XT), columns wn * 32 + [0, 32)
     const int lr = lane & 31, lk = lane >> 5;
+    const int nc = wn * 32 + lr;  // the tile column of this lane's outputs
 
-    float acc[2][2][16];
-    int i1[2][2][16];
+    float acc[XT][16];
+    int i1[XT][16];
 #pragma unroll
-    for (int x = 0; x < 2; x++)
+    for (int x = 0; x < XT; x++)
 #pragma unroll
-        for (int y = 0; y < 2; y++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) acc[x][y][r] = 0.0f, i1[x][y][r] = 0;
+        for (int r = 0; r < 16; r++) acc[x][r] = 0.0f, i1[x][r] = 0;
 
     const int s_begin = RAW ? 2 * a.raw_sb : 0, s_end = RAW ? 2 * a.raw_sb + 2 : 2 * a.nsb;
     KqStage<TYPE> st;
-    kq_load<TYPE>(st, a, m0, n0, s_begin);
-    kq_store<TYPE>(st, L[0], S[(s_begin >> 1) & 1], s_begin);
+    kq_load<TYPE, TN>(st, a, m0, n0, s_begin);
+    kq_store<TYPE, TN>(st, L[0], S, s_begin);
     __syncthreads();
 
     for (int step = s_begin; step < s_end; step++) {
-        const int buf = (step - s_begin) & 1, sbuf = (step >> 1) & 1, h = step & 1;
-        if (step + 1 < s_end) kq_load<TYPE>(st, a, m0, n0, step + 1);
-        const KqLds & l = L[buf];
-        const KqScales & s = S[sbuf];
+        const int buf = (step - s_begin) & 1, h = step & 1;
+        if (step + 1 < s_end) kq_load<TYPE, TN>(st, a, m0, n0, step + 1);
+        const KqLds<TN> & l = L[buf];
         if constexpr (TYPE == T_Q6_K) {
 #pragma unroll
             for (int jj = 0; jj < 8; jj++) {  // sub-blocks of 16: v_mfma_i32_32x32x16_i8
-                long af[2], bf[2];
+                long af[XT];
 #pragma unroll
-                for (int x = 0; x < 2; x++) {
-                    af[x] = *reinterpret_cast<const long *>(l.A + (wm * 64 + x * 32 + lr) * KP + 16 * jj + 8 * lk);
-                    bf[x] = *reinterpret_cast<const long *>(l.B + (wn * 64 + x * 32 + lr) * KP + 16 * jj + 8 * lk);
-                }
+                for (int x = 0; x < XT; x++)
+                    af[x] = *reinterpret_cast<const long *>(l.A + (wm * 32 * XT + x * 32 + lr) * KP + 16 * jj + 8 * lk);
+                const long bf = *reinterpret_cast<const long *>(l.B + nc * KP + 16 * jj + 8 * lk);
+                const int sc = S.sc[nc][8 * h + jj];
 #pragma unroll
-                for (int y = 0; y < 2; y++) {
-                    const int sc = s.sc[wn * 64 + y * 32 + lr][8 * h + jj];
+                for (int x = 0; x < XT; x++) {
+                    const v16i c = __builtin_amdgcn_mfma_i32_32x32x16_i8(af[x], bf, v16i{}, 0, 0, 0);
 #pragma unroll
-                    for (int x = 0; x < 2; x++) {
-                        const v16i c = __builtin_amdgcn_mfma_i32_32x32x16_i8(af[x], bf[y], v16i{}, 0, 0, 0);
-#pragma unroll
-                        for (int r = 0; r < 16; r++) i1[x][y][r] += sc * c[r];
-                    }
+                    for (int r = 0; r < 16; r++) i1[x][r] += sc * c[r];
                 }
             }
         } else {
 #pragma unroll
             for (int jj = 0; jj < 4; jj++) {  // sub-blocks of 32: v_mfma_i32_32x32x32_i8
-                v4i af[2], bf[2];
+                v4i af[XT];
 #pragma unroll
-                for (int x = 0; x < 2; x++) {
-                    af[x] = *reinterpret_cast<const v4i *>(l.A + (wm * 64 + x * 32 + lr) * KP + 32 * jj + 16 * lk);
-                    bf[x] = *reinterpret_cast<const v4i *>(l.B + (wn * 64 + x * 32 + lr) * KP + 32 * jj + 16 * lk);
-                }
+                for (int x = 0; x < XT; x++)
+                    af[x] = *reinterpret_cast<const v4i *>(l.A + (wm * 32 * XT + x * 32 + lr) * KP + 32 * jj + 16 * lk);
+                const v4i bf = *reinterpret_cast<const v4i *>(l.B + nc * KP + 32 * jj + 16 * lk);
+                const int sc = S.sc[nc][4 * h + jj];
 #pragma unroll
-                for (int y = 0; y < 2; y++) {
-                    const int sc = s.sc[wn * 64 + y * 32 + lr][4 * h + jj];
+                for (int x = 0; x < XT; x++) {
+                    const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[x], bf, v16i{}, 0, 0, 0);
 #pragma unroll
-                    for (int x = 0; x < 2; x++) {
-                        const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[x], bf[y], v16i{}, 0, 0, 0);
-#pragma unroll
-                        for (int r = 0; r < 16; r++) i1[x][y][r] += sc * c[r];
-                    }
+                    for (int r = 0; r < 16; r++) i1[x][r] += sc * c[r];
                 }
             }
         }
         if (h == 1) {  // the super-block is complete: its integer parts into the f32 sums
-            v16i i2[2][2];
+            v16i i2[XT];
             if constexpr (Kq<TYPE>::MIN) {
                 // I2 = sum_j m_j(n) bs_j(m) = 64 (bh . mn) + (bl . mn), K = 8 of 32 (lanes 32..63 and
                 // bytes 8..15 zero)
-                v4i ah[2], al[2], bm[2];
                 const int keep = lk ? 0 : -1;
+                const int2 m8 = *reinterpret_cast<const int2 *>(&S.mn[nc][0]);
+                const v4i bm = v4i{m8.x & keep, m8.y & keep, 0, 0};
 #pragma unroll
-                for (int x = 0; x < 2; x++) {
-                    const int row = wm * 64 + x * 32 + lr;
-                    const int2 h8 = *reinterpret_cast<const int2 *>(&s.bh[row][0]);
-                    const int2 l8 = *reinterpret_cast<const int2 *>(&s.bl[row][0]);
-                    const int2 m8 = *reinterpret_cast<const int2 *>(&s.mn[wn * 64 + x * 32 + lr][0]);
-                    ah[x] = v4i{h8.x & keep, h8.y & keep, 0, 0};
-                    al[x] = v4i{l8.x & keep, l8.y & keep, 0, 0};
-                    bm[x] = v4i{m8.x & keep, m8.y & keep, 0, 0};
+                for (int x = 0; x < XT; x++) {
+                    const int row = wm * 32 * XT + x * 32 + lr;
+                    const int2 h8 = *reinterpret_cast<const int2 *>(&S.bh[row][0]);
+                    const int2 l8 = *reinterpret_cast<const int2 *>(&S.bl[row][0]);
+                    const v4i ah = v4i{h8.x & keep, h8.y & keep, 0, 0};
+                    const v4i al = v4i{l8.x & keep, l8.y & keep, 0, 0};
+                    const v16i hh = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah, bm, v16i{}, 0, 0, 0);
+                    const v16i ll = __builtin_amdgcn_mfma_i32_32x32x32_i8(al, bm, v16i{}, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 16; r++) i2[x][r] = 64 * hh[r] + ll[r];
                 }
-#pragma unroll
-                for (int x = 0; x < 2; x++)
-#pragma unroll
-                    for (int y = 0; y < 2; y++) {
-                        const v16i hh = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah[x], bm[y], v16i{}, 0, 0, 0);
-                        const v16i ll = __builtin_amdgcn_mfma_i32_32x32x32_i8(al[x], bm[y], v16i{}, 0, 0, 0);
-#pragma unroll
-                        for (int r = 0; r < 16; r++) i2[x][y][r] = 64 * hh[r] + ll[r];
-                    }
             }
-            if constexpr (RAW) {
+            if constexpr (RAW) {  // the one super-block's integers, stored here
+                const int n = n0 + nc;
 #pragma unroll
-                for (int x = 0; x < 2; x++)
+                for (int x = 0; x < XT; x++)
 #pragma unroll
-                    for (int y = 0; y < 2; y++)
-#pragma unroll
-                        for (int r = 0; r < 16; r++) {
-                            acc[x][y][r] = __int_as_float(i1[x][y][r]);
-                            if constexpr (Kq<TYPE>::MIN) i1[x][y][r] = i2[x][y][r];
-                        }
+                    for (int r = 0; r < 16; r++) {
+                        const int m = m0 + wm * 32 * XT + x * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
+                        if (m >= a.M || n >= a.N) continue;
+                        int32_t * o = a.raw + ((size_t) m * a.N + n) * (Kq<TYPE>::MIN ? 2 : 1);
+                        o[0] = i1[x][r];
+                        if constexpr (Kq<TYPE>::MIN) o[1] = i2[x][r];
+                    }
             } else {
+                const float dw = S.dw[nc], dm = Kq<TYPE>::MIN ? S.dm[nc] : 0.0f;
 #pragma unroll
-                for (int x = 0; x < 2; x++) {
+                for (int x = 0; x < XT; x++) {
                     // d_x of this lane's rows: element r is row wm*64 + x*32 + 8 (r / 4) + 4 lk + r % 4
                     float4 dxv[4];
 #pragma unroll
                     for (int q = 0; q < 4; q++)
-                        dxv[q] = *reinterpret_cast<const float4 *>(&s.dx[wm * 64 + x * 32 + 8 * q + 4 * lk]);
+                        dxv[q] = *reinterpret_cast<const float4 *>(&S.dx[wm * 32 * XT + x * 32 + 8 * q + 4 * lk]);
 #pragma unroll
-                    for (int y = 0; y < 2; y++) {
-                        const int n = wn * 64 + y * 32 + lr;
-                        const float dw = s.dw[n], dm = Kq<TYPE>::MIN ? s.dm[n] : 0.0f;
-#pragma unroll
-                        for (int r = 0; r < 16; r++) {
-                            const float4 d4 = dxv[r >> 2];
-                            const float dx = (r & 3) == 0 ? d4.x : (r & 3) == 1 ? d4.y : (r & 3) == 2 ? d4.z : d4.w;
-                            float v = (dw * dx) * (float) i1[x][y][r];
-                            if constexpr (Kq<TYPE>::MIN) v -= (dm * dx) * (float) i2[x][y][r];
-                            acc[x][y][r] += v;
-                            i1[x][y][r] = 0;
-                        }
+                    for (int r = 0; r < 16; r++) {
+                        const float4 d4 = dxv[r >> 2];
+                        const float dx = (r & 3) == 0 ? d4.x : (r & 3) == 1 ? d4.y : (r & 3) == 2 ? d4.z : d4.w;
+                        float v = dw * (float) i1[x][r];
+                        if constexpr (Kq<TYPE>::MIN) v = fmaf(-dm, (float) i2[x][r], v);
+                        acc[x][r] = fmaf(dx, v, acc[x][r]);
+                        i1[x][r] = 0;
                     }
                 }
             }
         }
-        if (step + 1 < s_end) kq_store<TYPE>(st, L[buf ^ 1], S[((step + 1) >> 1) & 1], step + 1);
+        if (step + 1 < s_end) {
+            if (h == 1) __syncthreads();  // every wavefront is done with this super-block's scales
+            kq_store<TYPE, TN>(st, L[buf ^ 1], S, step + 1);
+        }
         __syncthreads();
     }
 
+    if constexpr (!RAW) {
+        const int n = n0 + nc;
+        if (n >= a.N) return;
 #pragma unroll
-    for (int x = 0; x < 2; x++)
-#pragma unroll
-        for (int y = 0; y < 2; y++) {
-            const int n = n0 + wn * 64 + y * 32 + lr;
-            if (n >= a.N) continue;
+        for (int x = 0; x < XT; x++) {
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const int m = m0 + wm * 64 + x * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
+                const int m = m0 + wm * 32 * XT + x * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
                 if (m >= a.M) continue;
-                if constexpr (RAW) {
-                    int32_t * o = a.raw + ((size_t) m * a.N + n) * (Kq<TYPE>::MIN ? 2 : 1);
-                    o[0] = __float_as_int(acc[x][y][r]);
-                    if constexpr (Kq<TYPE>::MIN) o[1] = i1[x][y][r];
-                } else {
-                    const size_t o = (size_t) m * a.ldy + n;
-                    a.y[o] = a.res ? acc[x][y][r] + a.res[o] : acc[x][y][r];
-                }
+                const size_t o = (size_t) m * a.ldy + n;
+                a.y[o] = a.res ? acc[x][r] + a.res[o] : acc[x][r];
             }
         }
+    }
 }
 
 template <int TYPE, bool RAW>
 void run_kq(const void * wv, int64_t N, int64_t K, const void * act, int64_t M, float * y, int64_t ldy,
             const float * res, int32_t * raw, int raw_sb, hipStream_t s) {
+    // 64-column tiles when 128-column ones would leave CUs without a workgroup
+    const bool narrow = ((M + TM - 1) / TM) * ((N + 127) / 128) <= cu_count();
+    const int TN = narrow ? 64 : 128;
     const WeightLayout WL = weight_layout(TYPE, N, K);
     const ActLayout AL = act_layout(TYPE, M, K);
     const uint8_t * w = (const uint8_t *) wv;
@@ -411,7 +401,8 @@ void run_kq(const void * wv, int64_t N, int64_t K, const void * act, int64_t M, 
     a.ldy = (int) ldy;
     a.raw_sb = raw_sb;
     const unsigned grid = (unsigned) (((M + TM - 1) / TM) * ((N + TN - 1) / TN));
-    k_gemm_kq<TYPE, RAW><<<grid, 256, 0, s>>>(a);
+    if (narrow) k_gemm_kq<TYPE, RAW, 64><<<grid, NT, 0, s>>>(a);
+    else k_gemm_kq<TYPE, RAW, 128><<<grid, NT, 0, s>>>(a);
 }
 
 }  // namespace

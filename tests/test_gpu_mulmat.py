@@ -92,11 +92,13 @@ KQ = ["q4_K", "q5_K", "q6_K"]
 
 
 @pytest.mark.parametrize("t", KQ)
-@pytest.mark.parametrize("M,N,K", [(9, 100, 256), (21, 300, 512), (200, 333, 2816), (256, 512, 1024)])
+@pytest.mark.parametrize("M,N,K", [(9, 100, 256), (21, 300, 512), (200, 333, 2816), (256, 512, 1024),
+                                   (300, 10958, 256)])
 def test_gemm_kquant_matches_oracle(gops, orc, t, M, N, K):
     """The K-quant MFMA GEMM (M > 8 rows): one super-block (K 256), a partial row and column tile
-    (9 x 100, 200 x 333), eleven super-blocks, and a grid of 8 tiles (256 x 512, tiles renumbered
-    per XCD)."""
+    (9 x 100, 200 x 333), eleven super-blocks, a grid of 8 tiles (256 x 512, tiles renumbered per
+    XCD), all with 64-column tiles (grids of at most one workgroup per CU); 300 x 10958 takes the
+    128-column tiles (258 of them), partial in both dimensions."""
     raw, qw = _weight(gops, orc, t, N, K, 33)
     x = orc.normal((M, K), seed=34)
     y = to_np(gops.mul_mat(qw, torch.from_numpy(x).cuda()))
@@ -127,6 +129,19 @@ def test_gemm_kquant_superblock_sums_bit_exact(gops, orc, t):
             want = want_all[:, :, sb * per + 8:sb * per + 10]
         assert got.shape == want.shape
         assert np.array_equal(got, want), sb
+    # 128-column tiles: a 300 x 10958 grid (258 tiles), checked on the rows and columns of its
+    # first and last tiles
+    M, N, K = 300, 10958, 512
+    raw, qw = _weight(gops, orc, t, N, K, 31)
+    x = orc.normal((M, K), seed=32)
+    act = gops.quantize_act(t, torch.from_numpy(x).cuda())
+    xq = orc.quantize_act_q8_K(x)
+    got = to_np(gops.gemm_block_isums(qw, act, M, 1))
+    for m in (*range(0, 6), *range(290, 300)):
+        for n in (*range(0, 40), *range(10900, 10958)):
+            v = orc.block_isums(t, raw[n], xq[m], K)[per:]
+            want = v[16] if t == "q6_K" else v[8:10]
+            assert np.array_equal(got[m, n], want), (m, n)
 
 
 @pytest.mark.parametrize("t", ["q4_K", "q5_K"])
