@@ -575,6 +575,7 @@ struct ggml_backend {
     std::string name;
     void * ws = nullptr;  // workspace of the mul_mat activations and flash-attention partials
     size_t ws_size = 0;
+    uint64_t epoch = 0;  // bumped whenever the workspace moves (graphs captured before point at the old one)
     float2 * rope_cs = nullptr;  // (cos, sin) table of the fused q / k / v rope step (<= 128 pairs)
     void * argmax_scratch = nullptr;  // the sliced argmax's row counters (left zero) and partials
     bool use_graphs = true;
@@ -634,6 +635,7 @@ void ensure_ws(ggml_backend * be, size_t need) {
     const size_t n = (need + (1 << 20) - 1) & ~size_t((1 << 20) - 1);
     check_hip(hipMalloc(&be->ws, n), "hipMalloc workspace");
     be->ws_size = n;
+    be->epoch++;
     for (auto & kv : be->graphs) {  // every captured graph points at the old workspace
         if (kv.second.exec) (void) hipGraphExecDestroy(kv.second.exec);
     }
@@ -1933,6 +1935,8 @@ enum ggml_status graph_compute_async(ggml_backend_t backend, ggml_cgraph * cgrap
 }
 
 hipStream_t backend_stream(ggml_backend_t backend) { return backend ? backend->stream : nullptr; }
+
+uint64_t backend_epoch(ggml_backend_t backend) { return backend ? backend->epoch : 0; }
 
 void backend_activate(ggml_backend_t backend) {
     require(backend != nullptr, "backend is NULL");

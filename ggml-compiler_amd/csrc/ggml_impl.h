@@ -76,6 +76,9 @@ Chains find_chains(const ggml_cgraph * g, bool fuse = true);
 // node planned alone and given memory of its own (node-by-node profiling).
 enum ggml_status graph_compute_async(ggml_backend_t backend, ggml_cgraph * cgraph);
 hipStream_t backend_stream(ggml_backend_t backend);
+// Changes whenever the executor's workspace moves: graphs captured over its launches before then
+// read the old workspace.
+uint64_t backend_epoch(ggml_backend_t backend);
 void backend_activate(ggml_backend_t backend);
 void backend_set_fusion(ggml_backend_t backend, bool on);
 

@@ -940,6 +940,16 @@ struct DriverKOp {
     const uint8_t * src;
     const int32_t * aux;  // _IF: the loop's stop word; D_UNTIL: its len stop ids
     int32_t * host;       // D_UNTIL: host-visible {stop, iterations done}
+    // Iteration-relative forms (a loop iteration captured once and replayed): with `it` (the
+    // loop's iteration word on the device) set, the op is for iteration it = *it: dst and src
+    // advance by dstep / sstep bytes per iteration (ring: dst alternates between two slots,
+    // dstep apart), a position or D_FILL32 value adds it to the word at `base` (a counter's
+    // start), a D_FILL32 value comes from the table `tab` at it, and _IF / D_UNTIL take pos = it.
+    const int32_t * it;
+    const int32_t * base;
+    const uint32_t * tab;
+    int64_t dstep, sstep;
+    int ring;
 };
 struct DriverBatch {
     DriverKOp op[kDriverBatch];
@@ -949,37 +959,49 @@ __global__ void k_driver_ops(const DriverBatch b) {
     const DriverKOp & o = b.op[blockIdx.y];
     const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= o.n) return;
+    const int64_t it = o.it ? (int64_t) *o.it : 0;
+    uint8_t * dst = o.dst + (o.ring ? (it & 1) : it) * o.dstep;
+    const uint8_t * src = o.src ? o.src + it * o.sstep : nullptr;
+    const int64_t base = o.base ? (int64_t) *o.base + it : 0;  // a counter's value at iteration it
+    const int64_t pos = o.it ? (o.base ? base : it) : o.pos;
     switch (o.kind) {
-        case D_FILL32: reinterpret_cast<uint32_t *>(o.dst)[i] = o.bits; break;
+        case D_FILL32:
+            reinterpret_cast<uint32_t *>(dst)[i] = o.tab ? o.tab[it] : o.base ? (uint32_t) base : o.bits;
+            break;
         // rows of a causal mask for position pos: 0 where the key index (element % len) is <= pos
-        case D_CAUSAL: reinterpret_cast<float *>(o.dst)[i] = i % o.len <= o.pos ? 0.0f : -INFINITY; break;
-        case D_COPY4: reinterpret_cast<uint32_t *>(o.dst)[i] = reinterpret_cast<const uint32_t *>(o.src)[i]; break;
+        case D_CAUSAL: reinterpret_cast<float *>(dst)[i] = i % o.len <= pos ? 0.0f : -INFINITY; break;
+        case D_COPY4: reinterpret_cast<uint32_t *>(dst)[i] = reinterpret_cast<const uint32_t *>(src)[i]; break;
         // a collected row of an iteration at or before the loop's stop (the stop word holds the
         // iteration whose value met the until ids, or INT32_MAX)
         case D_COPY4_IF:
-            if (o.pos <= *o.aux) reinterpret_cast<uint32_t *>(o.dst)[i] = reinterpret_cast<const uint32_t *>(o.src)[i];
+            if (pos <= *o.aux) reinterpret_cast<uint32_t *>(dst)[i] = reinterpret_cast<const uint32_t *>(src)[i];
             break;
         case D_COPY1_IF:
-            if (o.pos <= *o.aux) o.dst[i] = o.src[i];
+            if (pos <= *o.aux) dst[i] = src[i];
             break;
         // the until test of iteration pos: the stop word takes pos if the value is one of the ids;
         // then the host's copy of the stop word, then the iterations done (its release)
         case D_UNTIL: {
-            const int32_t v = *reinterpret_cast<const int32_t *>(o.src);
+            const int32_t v = *reinterpret_cast<const int32_t *>(src);
             bool hit = false;
             for (int64_t k = 0; k < o.len; k++) hit = hit || o.aux[k] == v;
-            int32_t * stop = reinterpret_cast<int32_t *>(o.dst);
+            int32_t * stop = reinterpret_cast<int32_t *>(dst);
             int32_t cur = *stop;
-            if (hit && cur > (int32_t) o.pos) {
-                cur = (int32_t) o.pos;
+            if (hit && cur > (int32_t) pos) {
+                cur = (int32_t) pos;
                 *stop = cur;
             }
             __hip_atomic_store(&o.host[0], cur, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-            __hip_atomic_store(&o.host[1], (int32_t) (o.pos + 1), __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+            __hip_atomic_store(&o.host[1], (int32_t) (pos + 1), __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
             break;
         }
-        default: o.dst[i] = o.src[i]; break;
+        default: dst[i] = src[i]; break;
     }
+}
+
+// The last launch of a captured loop iteration: the loop's iteration word moves to the next.
+__global__ void k_iter_next(int32_t * it) {
+    if (threadIdx.x == 0) *it += 1;
 }
 
 // The work a driver does between its graphs, ordered on the backend's stream with them, so a loop
@@ -1029,6 +1051,57 @@ class StreamOps {
         DriverKOp o{D_UNTIL, 0, 1, n_ids, it, (uint8_t *) stop, (const uint8_t *) value, ids, host};
         add(o, 4);
     }
+    // Iteration-relative ops (DriverKOp::it): for a loop iteration captured once and replayed.
+    // span: the bytes an op may touch over all iterations (from dst / src), for the batch's
+    // overlap check.
+    void fill32_tab(void * p, int64_t n, const uint32_t * tab, const int32_t * it) {
+        DriverKOp o{D_FILL32, 0, n, 0, 0, (uint8_t *) p, nullptr, nullptr, nullptr};
+        o.it = it, o.tab = tab;
+        add(o, (size_t) n * 4);
+    }
+    void fill32_ctr(void * p, int64_t n, const int32_t * base, const int32_t * it) {
+        DriverKOp o{D_FILL32, 0, n, 0, 0, (uint8_t *) p, nullptr, nullptr, nullptr};
+        o.it = it, o.base = base;
+        add(o, (size_t) n * 4);
+    }
+    void causal_rel(float * p, int64_t n, int64_t len, const int32_t * base, const int32_t * it) {
+        DriverKOp o{D_CAUSAL, 0, n, len, 0, (uint8_t *) p, nullptr, nullptr, nullptr};
+        o.it = it, o.base = base;
+        add(o, (size_t) n * 4);
+    }
+    // dst + step(it) <- src + it * sstep, n bytes (at most kDriverCopyMax); step(it) = it * dstep,
+    // or (it & 1) * dstep for a ring
+    void copy_rel(void * dst, const void * src, size_t n, int64_t dstep, int64_t sstep, bool ring, const int32_t * it,
+                  size_t dspan, size_t sspan) {
+        require(n <= kDriverCopyMax, "driver: iteration copy too large");
+        const bool words = ((uintptr_t) dst & 3) == 0 && ((uintptr_t) src & 3) == 0 && n % 4 == 0 && dstep % 4 == 0 &&
+                           sstep % 4 == 0;
+        DriverKOp o{words ? D_COPY4 : D_COPY1, 0, (int64_t) (words ? n / 4 : n), 0, 0, (uint8_t *) dst,
+                    (const uint8_t *) src, nullptr, nullptr};
+        o.it = it, o.dstep = dstep, o.sstep = sstep, o.ring = ring;
+        add(o, dspan, sspan);
+    }
+    void copy_if_rel(void * dst, const void * src, size_t n, int64_t dstep, const int32_t * stop, const int32_t * it,
+                     size_t dspan) {
+        require(n <= kDriverCopyMax, "driver: iteration copy too large");
+        const bool words = ((uintptr_t) dst & 3) == 0 && ((uintptr_t) src & 3) == 0 && n % 4 == 0 && dstep % 4 == 0;
+        DriverKOp o{words ? D_COPY4_IF : D_COPY1_IF, 0, (int64_t) (words ? n / 4 : n), 0, 0, (uint8_t *) dst,
+                    (const uint8_t *) src, stop, nullptr};
+        o.it = it, o.dstep = dstep;
+        add(o, dspan, n);
+    }
+    void until_rel(const int32_t * value, const int32_t * ids, int64_t n_ids, int32_t * stop, int32_t * host,
+                   const int32_t * it) {
+        DriverKOp o{D_UNTIL, 0, 1, n_ids, 0, (uint8_t *) stop, (const uint8_t *) value, ids, host};
+        o.it = it;
+        add(o, 4);
+    }
+    // the waiting ops, then the loop's iteration word to the next iteration
+    void iter_next(int32_t * it) {
+        flush();
+        k_iter_next<<<1, 64, 0, s_>>>(it);
+        check_launch("driver iteration");
+    }
     void clear(void * dst, size_t n) {
         flush();
         if (n) check_hip(hipMemsetAsync(dst, 0, n, s_), "driver clear");
@@ -1062,9 +1135,10 @@ class StreamOps {
     }
 
   private:
-    void add(const DriverKOp & o, size_t bytes) {
-        const uintptr_t w0 = (uintptr_t) o.dst, w1 = w0 + bytes;
-        const uintptr_t r0 = (uintptr_t) o.src, r1 = o.src ? r0 + bytes : r0;
+    void add(const DriverKOp & o, size_t bytes) { add(o, bytes, bytes); }
+    void add(const DriverKOp & o, size_t wbytes, size_t rbytes) {
+        const uintptr_t w0 = (uintptr_t) o.dst, w1 = w0 + wbytes;
+        const uintptr_t r0 = (uintptr_t) o.src, r1 = o.src ? r0 + rbytes : r0;
         bool clash = n_ == kDriverBatch;
         for (int k = 0; k < n_ && !clash; k++) {
             const uintptr_t pw0 = wr_[k][0], pw1 = wr_[k][1], pr0 = rd_[k][0], pr1 = rd_[k][1];
@@ -1088,7 +1162,9 @@ class StreamOps {
 // run's final wait. A call's time runs from the event before it (the previous call's, or the
 // run's first) to its own, so driver work between two calls counts with the call after it; one
 // event per call instead of a pair, and events without a system-scope release (the host reads
-// results only after the stream's final wait), since every event costs the stream a few us.
+// results only after the stream's final wait), since every event costs the stream a few us. A
+// loop iteration replayed from its captured graph has one event for all of its calls; its time is
+// split over the body's stages as the same loop's uncaptured iterations of the run split theirs.
 class StageClock {
   public:
     ~StageClock() {
@@ -1102,24 +1178,46 @@ class StageClock {
     void before(hipStream_t s) {
         if (used_ == 0) record(s);
     }
-    // after a call of stage `stage`
-    void after(int stage, hipStream_t s) {
-        marks_.push_back({stage, used_ - 1, used_});
+    // after a call of stage `stage`; group: the loop (with captured iterations) it belongs to, or -1
+    void after(int stage, hipStream_t s, int group = -1) {
+        marks_.push_back({stage, used_ - 1, used_, group, nullptr, false});
+        record(s);
+    }
+    // after a captured iteration of loop `group`, whose body calls the stages in `body`
+    void after_iteration(int group, const std::vector<int> * body, hipStream_t s) {
+        marks_.push_back({-1, used_ - 1, used_, group, body, false});
         record(s);
     }
     size_t marks() const { return marks_.size(); }
     // calls from mark k on are not counted (a loop iteration that ran past the loop's end)
     void forget_since(size_t k) {
-        for (size_t i = k; i < marks_.size(); i++) marks_[i].stage = -1;
+        for (size_t i = k; i < marks_.size(); i++) marks_[i].dead = true;
     }
-    // ms of each call, accumulated into per-stage totals
+    // ms and calls of each stage, accumulated into per-stage totals: add(stage, ms, calls)
     template <class F>
     void collect(F && add) {
-        for (const Mark & m : marks_) {
-            if (m.stage < 0) continue;
-            float ms = 0.0f;
-            check_hip(hipEventElapsedTime(&ms, events_[m.start], events_[m.stop]), "hipEventElapsedTime");
-            add(m.stage, (double) ms);
+        std::map<int, std::map<int, double>> share;  // loop -> stage -> ms of its uncaptured calls
+        std::vector<float> ms(marks_.size(), 0.0f);
+        for (size_t k = 0; k < marks_.size(); k++) {
+            const Mark & m = marks_[k];
+            if (m.dead) continue;
+            check_hip(hipEventElapsedTime(&ms[k], events_[m.start], events_[m.stop]), "hipEventElapsedTime");
+            if (m.body) continue;
+            add(m.stage, (double) ms[k], 1);
+            if (m.group >= 0) share[m.group][m.stage] += ms[k];
+        }
+        for (size_t k = 0; k < marks_.size(); k++) {
+            const Mark & m = marks_[k];
+            if (m.dead || !m.body || m.body->empty()) continue;
+            std::map<int, int> calls;
+            for (int st : *m.body) calls[st]++;
+            double total = 0.0;
+            for (const auto & c : calls) total += share[m.group][c.first];
+            for (const auto & c : calls) {
+                const double part = total > 0.0 ? share[m.group][c.first] / total
+                                                : (double) c.second / (double) m.body->size();
+                add(c.first, (double) ms[k] * part, c.second);
+            }
         }
     }
 
@@ -1136,6 +1234,9 @@ class StageClock {
     struct Mark {
         int stage;
         size_t start, stop;
+        int group;
+        const std::vector<int> * body;  // a captured iteration's stages, else nullptr
+        bool dead;
     };
     std::vector<hipEvent_t> events_;
     std::vector<Mark> marks_;
@@ -1259,20 +1360,54 @@ struct VmCode {
 // A loop's until test on the device (one int32 until value): its stop word and ids, the values
 // its body writes (state aside) as of the last two iterations, and a host-visible {stop,
 // iterations done} that the iterations' test ops write.
+//
+// Such a loop's iterations can also be captured once into a HIP graph and replayed: every op of
+// an iteration then has an iteration-relative form (DriverKOp::it) reading the loop's iteration
+// word `it` on the device, the counters' starts from `base` and the scalars from device tables,
+// and the last launch of the iteration moves `it` on. One graph per binding of the symbols (and
+// executor workspace epoch); the stages' graphs run inside it as plain launches.
+constexpr int kUntilCounters = 16;  // counters a captured loop may have
 struct UntilState {
-    void * dev = nullptr;          // [stop word] [ids] [per kept value: two slots]
+    void * dev = nullptr;          // [stop word, iteration word, counter starts] [ids] [per kept value: two slots]
     int32_t * stop = nullptr;
+    int32_t * it = nullptr;
+    int32_t * base = nullptr;      // kUntilCounters words
     int32_t * ids = nullptr;
     int64_t n_ids = 0;
     std::vector<std::string> kept;  // the values the body writes, state aside
     std::vector<uint8_t *> ring;    // per kept value: slot (iteration & 1)
     std::vector<size_t> slot_bytes;
     int32_t * host = nullptr;      // pinned
+    // captured iterations
+    bool has_until = false;        // the until test runs on the device (else the loop has none)
+    int group = -1;                // the loop's tag in the stage clock
+    bool graphable = false;        // every op of an iteration has an iteration-relative form
+    void * tab_mem = nullptr;      // the scalars' per-iteration values
+    std::vector<const uint32_t *> tabs;
+    std::vector<int> body_stages;  // the stage of each body call, in order
+    struct IterGraph {
+        std::vector<int64_t> binding;
+        uint64_t epoch;
+        hipGraphExec_t exec;
+    };
+    std::vector<IterGraph> graphs;
+    void drop_graphs(const std::vector<int64_t> * binding) {
+        for (size_t k = 0; k < graphs.size();) {
+            if (binding && graphs[k].binding != *binding) {
+                k++;
+                continue;
+            }
+            (void) hipGraphExecDestroy(graphs[k].exec);
+            graphs.erase(graphs.begin() + (long) k);
+        }
+    }
     UntilState() = default;
     UntilState(const UntilState &) = delete;
     UntilState & operator=(const UntilState &) = delete;
     ~UntilState() {
+        drop_graphs(nullptr);
         if (dev) (void) hipFree(dev);
+        if (tab_mem) (void) hipFree(tab_mem);
         if (host) (void) hipHostFree(host);
     }
 };
@@ -1282,8 +1417,10 @@ struct LoopFrame {
     int trips, i;
     std::vector<int32_t> start;  // counters' values at loop entry
     UntilState * until = nullptr;  // the until test on the device, when the loop has one
+    UntilState * cap = nullptr;    // the loop's device state for captured iterations (a body of calls)
     uint64_t calls0 = 0;           // calls made and stage-clock marks before this iteration
     size_t marks0 = 0;
+    bool replayed = false;         // this iteration ran as its loop's captured graph
 };
 
 }  // namespace
@@ -1325,6 +1462,7 @@ struct ggml_compiler_model {
     std::vector<CallGraph> calls;
     // ---- running
     std::map<const DriverOp *, std::unique_ptr<UntilState>> untils;
+    int cur_group = -1;  // the stage-clock tag of the loop whose body is running, or -1
     StreamOps ops;
     StageClock clock;
     std::vector<ggml_compiler_stats> stage_totals;  // ms_total, n_calls per stage
@@ -1498,6 +1636,7 @@ struct ggml_compiler_model {
             for (size_t k = 1; k < view_sets.size(); k++)
                 if (view_sets[k].used < view_sets[old].used) old = k;
             for (auto & c : calls) c.forget(view_sets[old].binding);
+            for (auto & u : untils) u.second->drop_graphs(&view_sets[old].binding);
             ggml_free(view_sets[old].ctx);
             view_sets.erase(view_sets.begin() + (long) old);
         }
@@ -1760,7 +1899,7 @@ struct ggml_compiler_model {
         clock.before(ops.stream());
         if (graph_compute_async(backend, c.graph) != GGML_STATUS_SUCCESS)
             fail("stage '" + st.name + "' failed: " + last_error());
-        clock.after(c.stage, ops.stream());
+        clock.after(c.stage, ops.stream(), cur_group);
     }
 
     // Profiling: each node of the graph alone, waited for and timed.
@@ -1793,24 +1932,36 @@ struct ggml_compiler_model {
             ggml_tensor * t = storage.at(c.first);
             ops.clear(t->data, ggml_nbytes(t));
         }
-        f.until = until_state(d);
+        f.cap = loop_state(d);
+        f.until = f.cap && f.cap->has_until ? f.cap : nullptr;
+        if (f.cap) {
+            ops.fill32(f.cap->it, 1, 0u);
+            ops.fill32(f.cap->stop, 1, (uint32_t) INT32_MAX);  // no stop yet (or ever, without an until test)
+            for (size_t k = 0; k < f.start.size() && k < (size_t) kUntilCounters; k++)
+                ops.fill32(f.cap->base + k, 1, (uint32_t) f.start[k]);
+        }
         if (f.until) {
-            ops.fill32(f.until->stop, 1, (uint32_t) INT32_MAX);
             // the loop's previous run waited for its last test op, so nothing still writes these
             __atomic_store_n(&f.until->host[0], INT32_MAX, __ATOMIC_RELAXED);
             __atomic_store_n(&f.until->host[1], 0, __ATOMIC_RELEASE);
         }
     }
 
-    // The device until test of loop d: one until value of type i32, a body of calls only, the
-    // values it writes (state aside) at most kUntilKeepMax bytes. Other loops (and every loop when
-    // profiling node by node) read their until values after every iteration. Made on the loop's
-    // first entry.
+    // The device state of loop d, for a body of calls only: its iterations can be captured and
+    // replayed (UntilState), and its until test, if it has one of one i32 value whose body's values
+    // (state aside) take at most kUntilKeepMax bytes, runs on the device. Other loops (and every
+    // loop when profiling node by node) run uncaptured and read their until values after every
+    // iteration. Made on the loop's first entry.
     static constexpr size_t kUntilKeepMax = 16u << 20;
-    UntilState * until_state(const DriverOp & d) {
-        if (d.until.size() != 1 || spec.at(d.until[0].first)->type != GGML_TYPE_I32 || profile_file()) return nullptr;
+    UntilState * loop_state(const DriverOp & d) {
+        if (profile_file()) return nullptr;
         auto it = untils.find(&d);
         if (it != untils.end()) return it->second.get();
+        const bool dev_until = d.until.size() == 1 && spec.at(d.until[0].first)->type == GGML_TYPE_I32;
+        if (!d.until.empty() && !dev_until) {
+            if (log_debug()) std::fprintf(stderr, "ggml_compiler: loop runs uncaptured: its until test is not one i32 value\n");
+            return nullptr;
+        }
         std::vector<std::string> kept;
         auto keep = [&](const std::string & v) {
             if (std::find(prog.state.begin(), prog.state.end(), v) == prog.state.end() &&
@@ -1818,24 +1969,34 @@ struct ggml_compiler_model {
                 kept.push_back(v);
         };
         for (const DriverOp & b : d.body) {
-            if (b.loop) return nullptr;
+            if (b.loop) {
+                if (log_debug()) std::fprintf(stderr, "ggml_compiler: loop runs uncaptured: its body holds a loop\n");
+                return nullptr;
+            }
             for (const auto & v : b.out) keep(v);
         }
         for (const auto & c : d.carry) keep(c.first);
+        if (!dev_until) kept.clear();  // the ring serves the until test's roll-back only
         auto u = std::make_unique<UntilState>();
-        const std::vector<int> & ids = d.until[0].second;
+        u->has_until = dev_until;
+        const std::vector<int> ids = dev_until ? d.until[0].second : std::vector<int>{};
         size_t keep_bytes = 0;
         for (const auto & v : kept) {
             u->slot_bytes.push_back(align256(ggml_nbytes(storage.at(v))));
             keep_bytes += 2 * u->slot_bytes.back();
         }
-        if (keep_bytes > kUntilKeepMax) return nullptr;
+        if (keep_bytes > kUntilKeepMax) {
+            if (log_debug()) std::fprintf(stderr, "ggml_compiler: loop runs uncaptured: %zu bytes to keep\n", keep_bytes);
+            return nullptr;
+        }
         u->kept = kept;
         const size_t id_bytes = align256(std::max<size_t>(1, ids.size()) * 4);
         check_hip(hipMalloc(&u->dev, 256 + id_bytes + keep_bytes), "hipMalloc (until)");
         check_hip(hipHostMalloc((void **) &u->host, 2 * sizeof(int32_t), hipHostMallocCoherent), "hipHostMalloc (until)");
         uint8_t * p = (uint8_t *) u->dev;
         u->stop = (int32_t *) p;
+        u->it = (int32_t *) p + 1;
+        u->base = (int32_t *) p + 2;
         u->ids = (int32_t *) (p + 256);
         u->n_ids = (int64_t) ids.size();
         uint8_t * r = p + 256 + id_bytes;
@@ -1846,6 +2007,21 @@ struct ggml_compiler_model {
         std::vector<int32_t> id32(ids.begin(), ids.end());
         if (!id32.empty())
             check_hip(hipMemcpy(u->ids, id32.data(), id32.size() * 4, hipMemcpyHostToDevice), "until ids");
+        // captured iterations: the scalars' values per iteration on the device
+        u->group = (int) untils.size();
+        u->graphable = d.counters.size() <= (size_t) kUntilCounters && !d.body.empty();
+        size_t tab_bytes = 0;
+        for (const auto & sc : d.scalars) tab_bytes += align256(std::max<size_t>(1, sc.second.size()) * 4);
+        if (u->graphable && tab_bytes) {
+            check_hip(hipMalloc(&u->tab_mem, tab_bytes), "hipMalloc (loop scalars)");
+            uint8_t * t = (uint8_t *) u->tab_mem;
+            for (const auto & sc : d.scalars) {
+                if (!sc.second.empty())
+                    check_hip(hipMemcpy(t, sc.second.data(), sc.second.size() * 4, hipMemcpyHostToDevice), "loop scalars");
+                u->tabs.push_back((const uint32_t *) t);
+                t += align256(std::max<size_t>(1, sc.second.size()) * 4);
+            }
+        }
         UntilState * raw = u.get();
         untils.emplace(&d, std::move(u));
         return raw;
@@ -1908,10 +2084,15 @@ struct ggml_compiler_model {
     bool loop_bottom(LoopFrame & f) {
         const DriverOp & d = *f.op;
         if (f.until) return loop_bottom_device(f);
+        if (f.replayed) {  // its graph holds the collects; the loop has no until test
+            f.replayed = false;
+            return false;
+        }
         for (const auto & c : d.collect) {
             const size_t nb = spec.at(c.second)->nbytes(binding);
             ops.copy((char *) storage.at(c.first)->data + (size_t) f.i * nb, storage.at(c.second)->data, nb);
         }
+        if (f.cap) ops.fill32(f.cap->it, 1, (uint32_t) (f.i + 1));  // the iteration word, for a replay of the next
         for (const auto & u : d.until) {
             const int32_t tok = ops.read_i32(storage.at(u.first)->data);
             if (std::find(u.second.begin(), u.second.end(), tok) != u.second.end()) return true;
@@ -1932,15 +2113,19 @@ struct ggml_compiler_model {
         const DriverOp & d = *f.op;
         UntilState & u = *f.until;
         const int i = f.i;
-        for (const auto & c : d.collect) {
-            const size_t nb = spec.at(c.second)->nbytes(binding);
-            ops.copy_if((char *) storage.at(c.first)->data + (size_t) i * nb, storage.at(c.second)->data, nb, u.stop, i);
+        if (!f.replayed) {  // a replayed iteration's graph holds these ops
+            for (const auto & c : d.collect) {
+                const size_t nb = spec.at(c.second)->nbytes(binding);
+                ops.copy_if((char *) storage.at(c.first)->data + (size_t) i * nb, storage.at(c.second)->data, nb, u.stop, i);
+            }
+            ops.until((const int32_t *) storage.at(d.until[0].first)->data, u.ids, u.n_ids, u.stop, u.host, i);
+            for (size_t k = 0; k < u.kept.size(); k++) {
+                ggml_tensor * v = value(u.kept[k]);
+                ops.copy(u.ring[k] + (size_t) (i & 1) * u.slot_bytes[k], v->data, ggml_nbytes(v));
+            }
+            ops.fill32(u.it, 1, (uint32_t) (i + 1));  // the iteration word, for a replay of the next
         }
-        ops.until((const int32_t *) storage.at(d.until[0].first)->data, u.ids, u.n_ids, u.stop, u.host, i);
-        for (size_t k = 0; k < u.kept.size(); k++) {
-            ggml_tensor * v = value(u.kept[k]);
-            ops.copy(u.ring[k] + (size_t) (i & 1) * u.slot_bytes[k], v->data, ggml_nbytes(v));
-        }
+        f.replayed = false;
         ops.flush();
         if (i >= 1) {
             wait_tested(u, i);
@@ -1965,6 +2150,157 @@ struct ggml_compiler_model {
         return false;
     }
 
+    // The binding of the symbols that iteration f.i binds (loop_top's rule), without applying it.
+    std::vector<int64_t> bind_for(const LoopFrame & f) const {
+        std::vector<int64_t> b = binding, with = binding;
+        for (int32_t v : f.start) with.push_back(v + f.i);
+        for (const auto & bnd : f.op->bind) b[(size_t) bnd.first] = bnd.second(with);
+        return b;
+    }
+
+    // Iteration f.i of a loop with a device until test, replayed from the loop's captured graph
+    // (captured now if there is none for the current binding): when it is not the loop's first
+    // iteration and binds the symbols as the previous one did (whose uncaptured run planned the
+    // stages' graphs for them), and every iteration copy fits one driver op. False: run it
+    // uncaptured.
+    bool replay_iteration(LoopFrame & f, const std::vector<VmCode> & code, size_t top) {
+        f.replayed = false;
+        UntilState * u = f.cap;
+        if (!u || !u->graphable || f.i < 1 || profile_file()) return false;
+        const DriverOp & d = *f.op;
+        auto no = [&](const char * why) {
+            if (log_debug()) std::fprintf(stderr, "ggml_compiler: loop iteration %d uncaptured: %s\n", f.i, why);
+            return false;
+        };
+        if (!d.bind.empty() && bind_for(f) != binding) return no("binding changed");
+        for (const auto & sl : d.slices)
+            if (ggml_nbytes(value(sl.first)) > kDriverCopyMax) return no("slice too large");
+        for (const auto & c : d.collect)
+            if (spec.at(c.second)->nbytes(binding) > kDriverCopyMax) return no("collect too large");
+        for (const auto & k : u->kept)
+            if (ggml_nbytes(value(k)) > kDriverCopyMax) return no("kept value too large");
+        for (size_t k = top + 1; code[k].kind == VmCode::Call; k++)
+            if (calls[(size_t) code[k].call].stale) return no("stage graph stale");
+        const uint64_t epoch = backend_epoch(backend);
+        UntilState::IterGraph * g = nullptr;
+        for (auto & ig : u->graphs)
+            if (ig.binding == binding) g = &ig;
+        if (g && g->epoch != epoch) {
+            u->drop_graphs(&binding);
+            g = nullptr;
+        }
+        if (!g) {
+            hipGraphExec_t exec = nullptr;
+            try {
+                exec = capture_iteration(f, code, top);
+            } catch (const Fail & e) {  // not capturable: this loop runs uncaptured from now on
+                u->graphable = false;
+                if (log_debug()) std::fprintf(stderr, "ggml_compiler: loop iteration not captured: %s\n", e.msg.c_str());
+                return false;
+            }
+            if (log_debug()) std::fprintf(stderr, "ggml_compiler: loop iteration %d captured\n", f.i);
+            u->graphs.push_back({binding, epoch, exec});
+            g = &u->graphs.back();
+        }
+        const hipStream_t s = ops.stream();
+        clock.before(s);
+        check_hip(hipGraphLaunch(g->exec, s), "hipGraphLaunch (loop iteration)");
+        clock.after_iteration(u->group, &u->body_stages, s);
+        last.n_calls += u->body_stages.size();
+        f.replayed = true;
+        return true;
+    }
+
+    // One iteration of the loop at `top` captured into a graph: its top ops, the body's stage
+    // graphs as plain launches (the executor's own graph capture off meanwhile), its bottom ops and
+    // the step of the iteration word, all in iteration-relative form.
+    hipGraphExec_t capture_iteration(LoopFrame & f, const std::vector<VmCode> & code, size_t top) {
+        UntilState & u = *f.cap;
+        const hipStream_t s = ops.stream();  // every waiting op launched, before the capture
+        std::vector<int> stages;
+        hipGraph_t graph = nullptr;
+        ggml_backend_hip_set_use_graphs(backend, false);
+        const hipError_t b = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+        if (b != hipSuccess) {
+            ggml_backend_hip_set_use_graphs(backend, true);
+            (void) hipGetLastError();
+            fail(std::string("hipStreamBeginCapture: ") + hipGetErrorString(b));
+        }
+        try {
+            loop_top_rel(f);
+            for (size_t k = top + 1; code[k].kind == VmCode::Call; k++) {
+                CallGraph & c = calls[(size_t) code[k].call];
+                ops.flush();
+                if (graph_compute_async(backend, c.graph) != GGML_STATUS_SUCCESS)
+                    fail("stage '" + prog.stages[(size_t) c.stage].name + "' failed: " + last_error());
+                stages.push_back(c.stage);
+            }
+            loop_bottom_rel(f);
+            ops.iter_next(u.it);
+        } catch (...) {
+            ops.discard();
+            (void) hipStreamEndCapture(s, &graph);
+            if (graph) (void) hipGraphDestroy(graph);
+            (void) hipGetLastError();
+            ggml_backend_hip_set_use_graphs(backend, true);
+            throw;
+        }
+        const hipError_t e1 = hipStreamEndCapture(s, &graph);
+        ggml_backend_hip_set_use_graphs(backend, true);
+        if (e1 != hipSuccess) {
+            if (graph) (void) hipGraphDestroy(graph);
+            (void) hipGetLastError();
+            fail(std::string("hipStreamEndCapture: ") + hipGetErrorString(e1));
+        }
+        hipGraphExec_t exec = nullptr;
+        const hipError_t e2 = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        (void) hipGraphDestroy(graph);
+        check_hip(e2, "hipGraphInstantiate (loop iteration)");
+        u.body_stages = std::move(stages);
+        return exec;
+    }
+
+    // loop_top's ops in iteration-relative form (the binding is the current one).
+    void loop_top_rel(LoopFrame & f) {
+        const DriverOp & d = *f.op;
+        const UntilState & u = *f.cap;
+        for (size_t k = 0; k < d.scalars.size(); k++) {
+            ggml_tensor * t = value(d.scalars[k].first);
+            ops.fill32_tab(t->data, ggml_nelements(t), u.tabs[k], u.it);
+        }
+        for (const auto & sl : d.slices) {
+            ggml_tensor *row = value(sl.first), *src = value(sl.second);
+            const size_t nb = ggml_nbytes(row);
+            ops.copy_rel(row->data, src->data, nb, 0, (int64_t) nb, false, u.it, nb, ggml_nbytes(src));
+        }
+        for (size_t k = 0; k < d.counters.size(); k++)
+            ops.fill32_ctr(value(d.counters[k].first)->data, 1, u.base + k, u.it);
+        for (const auto & m : d.masks) {
+            const TensorSpec & v = *spec.at(m.first);
+            ops.causal_rel((float *) storage.at(m.first)->data, v.ne[0] * v.ne[1] * v.ne[2] * v.ne[3], v.ne[0],
+                           u.base + m.second, u.it);
+        }
+    }
+
+    // loop_bottom's ops in iteration-relative form (without an until test the collects are
+    // unconditional: the stop word stays INT32_MAX).
+    void loop_bottom_rel(LoopFrame & f) {
+        const DriverOp & d = *f.op;
+        UntilState & u = *f.cap;
+        for (const auto & c : d.collect) {
+            const size_t nb = spec.at(c.second)->nbytes(binding);
+            ggml_tensor * dst = storage.at(c.first);
+            ops.copy_if_rel(dst->data, storage.at(c.second)->data, nb, (int64_t) nb, u.stop, u.it, ggml_nbytes(dst));
+        }
+        if (u.has_until)
+            ops.until_rel((const int32_t *) storage.at(d.until[0].first)->data, u.ids, u.n_ids, u.stop, u.host, u.it);
+        for (size_t k = 0; k < u.kept.size(); k++) {
+            ggml_tensor * v = value(u.kept[k]);
+            ops.copy_rel(u.ring[k], v->data, ggml_nbytes(v), (int64_t) u.slot_bytes[k], 0, true, u.it,
+                         2 * u.slot_bytes[k], ggml_nbytes(v));
+        }
+    }
+
     void execute(const Entry & e) {
         std::vector<LoopFrame> frames;
         const std::vector<VmCode> & code = e.code;
@@ -1984,17 +2320,25 @@ struct ggml_compiler_model {
                 case VmCode::Top:
                     if (frames.back().i >= frames.back().trips) {
                         frames.pop_back();
+                        cur_group = -1;
                         pc = (size_t) in.jump;
                     } else {
-                        frames.back().calls0 = last.n_calls;
-                        frames.back().marks0 = clock.marks();
-                        loop_top(frames.back());
-                        pc++;
+                        LoopFrame & f = frames.back();
+                        f.calls0 = last.n_calls;
+                        f.marks0 = clock.marks();
+                        cur_group = f.cap ? f.cap->group : -1;
+                        if (replay_iteration(f, code, pc)) {
+                            pc = (size_t) in.jump - 1;  // the loop's Bottom
+                        } else {
+                            loop_top(f);
+                            pc++;
+                        }
                     }
                     break;
                 case VmCode::Bottom:
                     if (loop_bottom(frames.back())) {
                         frames.pop_back();
+                        cur_group = -1;
                         pc = (size_t) code[(size_t) in.jump].jump;
                     } else {
                         frames.back().i++;
@@ -2020,9 +2364,9 @@ struct ggml_compiler_model {
         execute(*e);
         ops.finish();
         last.ms_total = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
-        clock.collect([&](int stage, double ms) {
+        clock.collect([&](int stage, double ms, int n) {
             stage_totals[(size_t) stage].ms_total += ms;
-            stage_totals[(size_t) stage].n_calls++;
+            stage_totals[(size_t) stage].n_calls += n;
         });
         write_profile();
     }

@@ -239,6 +239,22 @@ def test_loop_driver(tmp_path):
             masks[k] = np.where(np.arange(E) <= 3 + k, 0.0, -np.inf)
         np.testing.assert_array_equal(out["ms"], masks)
         assert s.stats["n_calls"] == 9
+    # without an until test every iteration runs; iterations after the first replay one captured
+    # graph, which the second run (other inputs, other start position) replays from its start
+    loop.pop("until")
+    with runtime.Session(_write(tmp_path / "loop_all.gguf", prog)) as s:
+        for start, scale in ((3, 1.0), (1, -2.0)):
+            out = s.run(h0 * scale, R * scale, np.array([start], np.int32))
+            h, want, masks = h0 * scale, np.zeros((n, E), np.float32), np.zeros((n, E), np.float32)
+            for k in range(n):
+                h = h * svals[k] + R[k] * scale
+                want[k] = h
+                masks[k] = np.where(np.arange(E) <= start + k, 0.0, -np.inf)
+            np.testing.assert_array_equal(out["hs"], want)
+            np.testing.assert_array_equal(out["ms"], masks)
+            assert int(out["t"][0]) == int(np.argmax(want[-1]))
+            assert s.stats["n_calls"] == 3 * n
+            assert {k: v["calls"] for k, v in s.stats["stages"].items()} == {"step": n, "cpm": n, "am": n}
 
 
 def _llama(orc, wtype):
