@@ -115,6 +115,7 @@ def gemv_roofline(ops, torch, passes: int = 10, extra: bool = True) -> dict:
     name, K, N, n = ROOF_SHAPE
     ws = weights(K, N, n)
     us = timed(ws)
+    f_us, f_cfg = _read_floor_us(torch, [w.data.data_ptr() for w in ws], ws[0].data.numel())
     del ws
     nbytes = _f32_launch_bytes(K, N)
     achieved = nbytes / (us * 1e-6) / 1e9
@@ -122,7 +123,9 @@ def gemv_roofline(ops, torch, passes: int = 10, extra: bool = True) -> dict:
     out = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": ROOF_KERNEL,
            "shape": f"{name} K={K} N={N}", "avg_us": round(us, 2), "algorithmic_bytes_per_launch": nbytes,
-           "bytes_note": ROOF_BYTES_NOTE}
+           "bytes_note": ROOF_BYTES_NOTE, "read_floor_us": round(f_us, 2), "read_floor_cfg": f_cfg,
+           "read_floor_note": "the fastest one-launch read of the same weight bytes (gcq_stream_read), timed the "
+                              "same way"}
     if traffic is not None:
         out["traffic_note"] = f"HBM bytes per launch from {PMC_SUMMARY.relative_to(ROOT)}"
     if extra:
@@ -130,9 +133,11 @@ def gemv_roofline(ops, torch, passes: int = 10, extra: bool = True) -> dict:
         for ename, eK, eN, en in ROOF_EXTRA:
             ews = weights(eK, eN, en)
             e_us = timed(ews)
+            ef_us, _ = _read_floor_us(torch, [w.data.data_ptr() for w in ews], ews[0].data.numel())
             del ews
             shapes[f"{ename} {eK}x{eN}"] = {"us": round(e_us, 2),
-                                           "GB/s": round(_f32_launch_bytes(eK, eN) / (e_us * 1e-6) / 1e9, 1)}
+                                           "GB/s": round(_f32_launch_bytes(eK, eN) / (e_us * 1e-6) / 1e9, 1),
+                                           "read_floor_us": round(ef_us, 2)}
         out["other_shapes"] = shapes
     return out
 
@@ -499,6 +504,28 @@ def _graph_us(torch, calls, passes: int = 5) -> float:
     return e0.elapsed_time(e1) * 1e3 / (passes * len(calls))
 
 
+FLOOR_CONFIGS = ((16, 4), (32, 4), (16, 2), (32, 1))  # (wavefronts per CU, loads in flight) of the read floor
+
+
+def _read_floor_us(torch, bufs, nbytes: int, passes: int = 5) -> tuple[float, str]:
+    """The fastest one-launch read of nbytes: gcq_stream_read over the rotated buffers `bufs`
+    (device pointers, nbytes readable at each), timed like the kernels (a HIP graph of back-to-back
+    launches, `_graph_us`), the best of FLOOR_CONFIGS; (µs, "waves/CU x loads")."""
+    from ggml_compiler_amd._lib import check, load
+
+    lib = load()
+    sink = torch.zeros(64, dtype=torch.int32, device="cuda")
+    best = None
+    for wpc, unroll in FLOOR_CONFIGS:
+        def call(b):
+            check(lib.gcq_stream_read(b, nbytes, wpc, unroll, sink.data_ptr(), torch.cuda.current_stream().cuda_stream))
+
+        us = _graph_us(torch, [lambda b=b: call(b) for b in bufs] * max(1, 64 // len(bufs)), passes)
+        if best is None or us < best[0]:
+            best = (us, f"{wpc}x{unroll}")
+    return best
+
+
 def _rotating_weights(ops, t: str, N: int, K: int, seed: int):
     """Copies of one N x K weight (N(0, 0.02) -> t) covering ROTATE_BYTES, so successive launches
     read HBM, not the 256 MB Infinity Cache."""
@@ -516,14 +543,20 @@ def bench_sweep(ops, torch, only: set[str] | None = None) -> list[dict]:
     def want(cfg):
         return only is None or cfg in only
 
+    floors = {}  # (type, K, N) -> the read floor of the weight's bytes
+
     def gemv_case(cfg, t, K, N, B):
         ws = _rotating_weights(ops, t, N, K, seed=K + N)
         x = ops.fill_normal((B, K), seed=1)
         us = _graph_us(torch, [lambda w=w: ops.mul_mat(w, x) for w in ws] * max(1, 64 // len(ws)))
         wbytes = ws[0].data.numel()
+        if (t, K, N) not in floors:
+            floors[(t, K, N)] = _read_floor_us(torch, [w.data.data_ptr() for w in ws], wbytes)
+        f_us, f_cfg = floors[(t, K, N)]
         nbytes = wbytes + B * K * 4 + B * N * 4
         out.append({"config": cfg, "op": "mul_mat", "type": t, "K": K, "N": N, "B": B, "us": round(us, 2),
-                    "GB/s": round(nbytes / us / 1e3, 1), "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)})
+                    "GB/s": round(nbytes / us / 1e3, 1), "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+                    "read_floor_us": round(f_us, 2), "read_floor_cfg": f_cfg, "floor_over_us": round(f_us / us, 3)})
         del ws
 
     if want("C1"):
@@ -565,9 +598,12 @@ def bench_sweep(ops, torch, only: set[str] | None = None) -> list[dict]:
         q = ops.fill_normal((32, 1, 128), seed=7)
         calls = [lambda i=i: ops.flash_attn_ext(q, k[i], v[i], None, 1 / math.sqrt(128)) for i in range(copies)]
         us = _graph_us(torch, calls * max(1, 64 // copies))
+        # the floor reads kv_bytes contiguous: K copy i and the next (the same bytes, one range)
+        f_us, f_cfg = _read_floor_us(torch, [k[i].data_ptr() for i in range(copies - 1)], kv_bytes)
         nbytes = kv_bytes + 2 * 32 * 128 * 4
         out.append({"config": "C4", "op": "flash_attn_ext", "ctx": ctx, "us": round(us, 2),
-                    "GB/s": round(nbytes / us / 1e3, 1), "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)})
+                    "GB/s": round(nbytes / us / 1e3, 1), "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+                    "read_floor_us": round(f_us, 2), "read_floor_cfg": f_cfg, "floor_over_us": round(f_us / us, 3)})
         del k, v
     return out
 

@@ -96,6 +96,7 @@ SIGNATURES = {
     "gcq_mul": ([p, p, p, i64, i64, p], i32),
     "gcq_argmax": ([p, i64, i64, i64, p, p], i32),
     "gcq_fill_normal": ([p, i64, u64, u64, f32, p], i32),
+    "gcq_stream_read": ([p, sz, i32, i32, p, p], i32),
     "gcq_fill_ids": ([p, i64, u64, u64, ctypes.c_int32, p], i32),
     "gcq_llama_create": ([p, i32], p),
     "gcq_llama_free": ([p], None),

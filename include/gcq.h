@@ -178,6 +178,15 @@ GCQ_API int gcq_argmax(const float * x, int64_t ldx, int64_t rows, int64_t n, in
 GCQ_API int gcq_fill_normal(float * dst, int64_t n, uint64_t seed, uint64_t offset, float stddev, void * stream);
 GCQ_API int gcq_fill_ids(int32_t * dst, int64_t n, uint64_t seed, uint64_t offset, int32_t vocab, void * stream);
 
+/* ---- measurement ---------------------------------------------------------------------------- */
+/* No counterpart in the reference: for benchmarks that set a kernel's time against the fastest
+ * one-launch read of the same bytes. Reads `bytes` (a multiple of 16) at src (16-byte aligned) once
+ * with waves_per_cu (4, 8, 16 or 32) wavefronts per CU, each reading a contiguous range with
+ * `unroll` (1, 2 or 4) 1 KiB loads in flight; computes nothing (sink, a device word, is written
+ * only in the unlikely case that the XOR of the words equals a constant). */
+GCQ_API int gcq_stream_read(const void * src, size_t bytes, int waves_per_cu, int unroll, uint32_t * sink,
+                            void * stream);
+
 /* ---- Llama-style causal LM ------------------------------------------------------------------ */
 /* The program ggml-compiler's causal_lm compiles (ggml_compiler/llm.py:361-444) on libgcq's
  * kernels: GQA attention over an f16 KV cache, SwiGLU FFN, RMSNorm, NEOX RoPE, every matmul weight

@@ -21,7 +21,7 @@ def _declared():
 def test_every_declared_symbol_is_exported():
     lib = _lib.load()
     names = _declared()
-    assert len(names) == 213
+    assert len(names) == 214
     missing = [n for n in names if not hasattr(lib, n)]
     assert not missing, missing
     assert set(names) <= set(_lib.SIGNATURES), set(names) - set(_lib.SIGNATURES)
@@ -78,6 +78,10 @@ def test_host_side_argument_checks():
     assert "multiples of 8" in lib.gcq_last_error().decode()
     assert lib.gcq_rope_neox(p, 0, 0, p, 0, 0, p, 128, 1, 1, 129, 1e4, 1.0, 1.0, None, None) == -1
     assert lib.gcq_set_rows_f16(p, 0, 12, p, 0, 0, p, 1, 128, 1, 64, None) == -1
+    assert lib.gcq_stream_read(p, 1 << 20, 12, 1, p, None) == -1
+    assert "waves_per_cu" in lib.gcq_last_error().decode()
+    assert lib.gcq_stream_read(p, 100, 16, 1, p, None) == -1
+    assert "16-byte" in lib.gcq_last_error().decode()
 
 
 def test_runtime_api_without_a_device():
