@@ -34,6 +34,9 @@ namespace gcq {
 void launch_pack(int type, const void * src, int64_t nrows, int64_t k, void * dst, hipStream_t s);
 void launch_unpack(int type, const void * src, int64_t nrows, int64_t k, void * dst, hipStream_t s);
 void launch_act_quant(int wtype, const float * x, int64_t ldx, int64_t B, int64_t k, void * act, hipStream_t s);
+bool row_gemv_kq_fits(int type, int64_t N, int64_t K);
+void launch_row_gemv_kq(int type, const void * w, int64_t N, int64_t K, const float * x, float * y, const float * res,
+                        hipStream_t s);
 void launch_gemv(int type, const void * w, int64_t N, int64_t K, const void * act, int64_t B, float * y, int64_t ldy,
                  hipStream_t s, const float * res);
 void launch_gemm(int type, const void * w, int64_t N, int64_t K, const void * act, int64_t M, float * y, int64_t ldy,
@@ -1468,6 +1471,10 @@ void run_step(const ggml_backend * be, const Step & s) {
                 a.y = y;
                 a.res = res;
                 launch_row_gemv(wt, nw ? PRO_NORM : PRO_PLAIN, EPI_STORE, a, st);
+                return;
+            }
+            if (M == 1 && !nw && row_gemv_kq_fits(wt, N, K) && aligned(x, 16)) {  // one launch, row quantized in it
+                launch_row_gemv_kq(wt, s.in[0], N, K, x, y, res, st);
                 return;
             }
             if (nw) launch_rmsnorm_q8(x, ldx, nw, s.f[0], M, K, be->ws, st);

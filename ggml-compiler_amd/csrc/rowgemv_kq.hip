@@ -1,0 +1,396 @@
+// rowgemv_kq.hip - ggml_mul_mat of a Q4_K / Q5_K weight with one f32 activation row, in one
+// launch (runtime/src/ops.cpp:107-119 -> runtime/include/ggml_compiler_ops.h:116-122).
+//
+// ggml-cpu quantizes the row to Q8_K (quantize_row_q8_K) and takes vec_dot_q{4,5}_K_q8_K per
+// super-block. Here one workgroup of 1024 threads per CU:
+//   - its first XW wavefronts ("x waves") turn the row into Q8_K in LDS, a thread per 16 values
+//     (one bsum): the super-block's signed maximum of |x| (first one on ties) over its 16 lanes,
+//     iscale = -127 / max, q = min(127, rint(iscale x)), d = 1 / iscale, the thread's own bsum;
+//   - the other wavefronts meanwhile stream their first weight rows: the x waves issue their row
+//     loads first and the workgroup meets before any weight load is issued (a CU's loads complete
+//     in issue order), and the compute wavefronts take the codes through an LDS counter;
+//   - every wavefront walks groups of R whole weight rows (g, g + waves, ...), lane l taking the
+//     row's 64-value chunks l, l + 64, ... (task t: super-block t / 4, chunk c = t % 4: the 32
+//     nibble bytes of sub-blocks 2c (low nibbles) and 2c + 1 (high)), so the four lanes of a quad
+//     share a super-block and each loads one 32-bit word of its 16-byte header (d / dmin, scales),
+//     passed around the quad by DPP; a wavefront sum finishes each output. With long rows (or one
+//     group too many for the compute wavefronts) the x waves take row groups too, once their
+//     prologue is done.
+// Per task: (sc0 s0 + sc1 s1) d d_x - dmin (m0 bs0 + m1 bs1) d_x, s0 / s1 the exact int32 dots of
+// sub-blocks 2c / 2c + 1 with their Q8_K codes and bs0 / bs1 their Q8_K block sums (ggml's
+// vec_dot_q{4,5}_K_q8_K terms); the weight's bytes are read once, as buffer loads (an offset past
+// the weight reads zeros).
+#include "gcq_common.h"
+
+#include <algorithm>
+#include <type_traits>
+
+namespace gcq {
+
+int cu_count();
+
+namespace {
+
+constexpr int kRowKqMaxK = 16384;  // LDS holds the row's Q8_K codes, bsums and d
+constexpr uint32_t kKqPast = 0x80000000u;  // a buffer offset past every weight (sizes < 2 GB)
+
+struct RowKqArgs {
+    const uint8_t * w;  // ggml super-blocks [N][K / 256]
+    const float * x;    // the activation row [K]
+    float * y;          // [N]
+    const float * res;  // optional, y = res + W x
+    int N, ntask;       // ntask: 64-value chunks per row (K / 64)
+    int xc;             // the x waves take row groups too
+};
+
+template <int TYPE>
+struct RowKqFmt {
+    static constexpr int WV = TYPE == T_Q5_K ? 4 : 2;                // 16-byte loads per task
+    static constexpr uint32_t SB = TYPE == T_Q5_K ? 176u : 144u;    // super-block bytes
+    static constexpr uint32_t QS = TYPE == T_Q5_K ? 48u : 16u;      // offset of the nibbles
+};
+
+template <int TYPE, int R, int NBL>
+__global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
+#pragma clang fp contract(off)
+    using F = RowKqFmt<TYPE>;
+    constexpr int NWV = 16, WV = F::WV;
+    constexpr bool XREG = NBL <= 2;                // the task activations in registers
+    constexpr bool PF = WV * NBL * R <= 4;         // the next group's weights prefetched
+    // x waves: at most 4; rounds of 16 values per x thread: K / 16 groups over 64 XW threads,
+    // NBL at most (a row of NBL * 64 chunks of 64)
+    constexpr int XWMAX = 4, RMAX = NBL;
+    __shared__ int4 lc[kRowKqMaxK / 16];           // codes, 16 per entry
+    __shared__ int16_t lbs[kRowKqMaxK / 16];       // bsums of 16
+    __shared__ float ld[kRowKqMaxK / 256];         // d per super-block
+    __shared__ unsigned int s_flag;
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int ntask = a.ntask;
+    const int K = ntask * 64, ngrp = K / 16;       // 16-value groups of the row
+    const uint32_t row_bytes = (uint32_t) (ntask / 4) * F::SB;
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(a.w), 0, (int) ((size_t) a.N * row_bytes), 0x00020000);
+    const int ng = (a.N + R - 1) / R;
+    const int XW = min(XWMAX, (K + 1023) / 1024);
+    const int rounds = (ngrp + 64 * XW - 1) / (64 * XW);
+    const bool XC = a.xc != 0;
+    const int CW = XC ? NWV : NWV - XW;
+    const bool xw = wave < XW;
+    int g = blockIdx.x * CW + (XC ? (wave + NWV - XW) % NWV : max(wave - XW, 0));
+    const int nw = gridDim.x * CW;
+    // the lane's chunk, the same for all its tasks (64 tasks are 16 super-blocks)
+    const int c = lane & 3;
+    const uint32_t csh = 16u * (uint32_t) (c & 1);
+    const bool chi = c >= 2;
+
+    if (threadIdx.x == 0) {
+        s_flag = 0u;
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the count is zero before the workgroup meets
+    }
+
+    // Per task and row: the 32 nibble bytes (Q5_K: and the super-block's 32 qh bytes) and word c
+    // of the super-block's 16-byte header, the quad's four lanes holding the whole header.
+    uint4 w[NBL][R][WV], wn[NBL][R][WV];
+    uint32_t hw[NBL][R], hwn[NBL][R];
+    auto load = [&](int gg, uint4 (&wv)[NBL][R][WV], uint32_t (&hv)[NBL][R]) {
+        const bool live = gg < ng;
+#pragma unroll
+        for (int i = 0; i < NBL; i++) {
+            const int t = lane + 64 * i;
+            const uint32_t sb = (uint32_t) (t >> 2);
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const int row = min(gg * R + r, a.N - 1);
+                const bool in = live && t < ntask && gg * R + r < a.N;
+                const uint32_t o = (uint32_t) row * row_bytes + sb * F::SB;
+                const uint32_t offs[4] = {o + F::QS + 32u * (uint32_t) c, o + F::QS + 32u * (uint32_t) c + 16u, o + 16u,
+                                          o + 32u};
+                hv[i][r] = __builtin_amdgcn_raw_buffer_load_b32(rq, in ? o + 4u * (uint32_t) c : kKqPast, 0, 0);
+#pragma unroll
+                for (int v = 0; v < WV; v++) {
+                    // the nibbles streamed (nt); the qh bytes, read by the quad's four lanes, cached
+                    const auto q = v < 2 ? __builtin_amdgcn_raw_buffer_load_b128(rq, in ? offs[v] : kKqPast, 0, 2)
+                                         : __builtin_amdgcn_raw_buffer_load_b128(rq, in ? offs[v] : kKqPast, 0, 0);
+                    wv[i][r][v] = make_uint4(q[0], q[1], q[2], q[3]);
+                }
+            }
+        }
+    };
+    // word k of the header from lane k of the quad
+    auto hword = [](uint32_t v, auto K) -> uint32_t {
+        constexpr int k = decltype(K)::value;
+        return (uint32_t) __builtin_amdgcn_mov_dpp((int) v, k | (k << 2) | (k << 4) | (k << 6), 0xF, 0xF, false);
+    };
+
+    if (xw) {
+        // the row's loads first, then the workgroup meets (no weight load is ahead of them)
+        float4 xv[RMAX][4];
+#pragma unroll
+        for (int r = 0; r < RMAX; r++) {
+            const int gi = (int) threadIdx.x + r * XW * 64;
+            if (r < rounds && gi < ngrp) {
+#pragma unroll
+                for (int k = 0; k < 4; k++) xv[r][k] = *reinterpret_cast<const float4 *>(a.x + gi * 16 + 4 * k);
+            } else {
+#pragma unroll
+                for (int k = 0; k < 4; k++) xv[r][k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int r = 0; r < RMAX; r++) {
+            const int gi = (int) threadIdx.x + r * XW * 64;
+            if (r >= rounds) break;
+            const float v[16] = {xv[r][0].x, xv[r][0].y, xv[r][0].z, xv[r][0].w, xv[r][1].x, xv[r][1].y,
+                                 xv[r][1].z, xv[r][1].w, xv[r][2].x, xv[r][2].y, xv[r][2].z, xv[r][2].w,
+                                 xv[r][3].x, xv[r][3].y, xv[r][3].z, xv[r][3].w};
+            // the super-block's first largest |x| (its 16 groups are 16 consecutive lanes)
+            float ax = 0.0f, mx = 0.0f;
+            int idx = 1 << 30;
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                if (fabsf(v[j]) > ax) {
+                    ax = fabsf(v[j]);
+                    mx = v[j];
+                    idx = (lane & 15) * 16 + j;
+                }
+            }
+            auto take = [&](float ax2, float mx2, int idx2) {
+                if (ax2 > ax || (ax2 == ax && idx2 < idx)) {
+                    ax = ax2;
+                    mx = mx2;
+                    idx = idx2;
+                }
+            };
+            take(lane_pair<1>(ax), lane_pair<1>(mx), lane_pair_i<1>(idx));
+            take(lane_pair<2>(ax), lane_pair<2>(mx), lane_pair_i<2>(idx));
+            take(lane_pair<4>(ax), lane_pair<4>(mx), lane_pair_i<4>(idx));
+            take(lane_pair<8>(ax), lane_pair<8>(mx), lane_pair_i<8>(idx));
+            int q[16];
+            float d = 0.0f;
+            if (ax != 0.0f) {
+                const float iscale = __fdiv_rn(-127.0f, mx);
+#pragma unroll
+                for (int j = 0; j < 16; j++) {
+                    const int rr = (int) __builtin_rintf(iscale * v[j]);
+                    q[j] = rr < 127 ? rr : 127;
+                }
+                d = __fdiv_rn(1.0f, iscale);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 16; j++) q[j] = 0;
+            }
+            if (gi < ngrp) {
+                int pk[4], s = 0;
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    pk[k] = (q[4 * k] & 0xff) | ((q[4 * k + 1] & 0xff) << 8) | ((q[4 * k + 2] & 0xff) << 16) |
+                            ((q[4 * k + 3] & 0xff) << 24);
+#pragma unroll
+                for (int j = 0; j < 16; j++) s += q[j];
+                lc[gi] = make_int4(pk[0], pk[1], pk[2], pk[3]);
+                lbs[gi] = (int16_t) s;
+                if ((lane & 15) == 0) ld[gi >> 4] = d;
+            }
+            __builtin_amdgcn_sched_barrier(0);  // one round at a time (its codes are 16 registers)
+        }
+        if (lane == 0) lds_signal(&s_flag);
+        if (!XC) return;
+    } else {
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    load(g, w, hw);
+    lds_wait(&s_flag, XW);
+    if constexpr (PF) load(g + nw, wn, hwn);
+
+    // The lane's task activations: the 32 codes of sub-blocks 2c and 2c + 1, d_x, bs0 d_x, bs1 d_x.
+    int4 xa[XREG ? NBL : 1][2], xb[XREG ? NBL : 1][2];
+    float xs[XREG ? NBL : 1], xo[XREG ? NBL : 1], xo2[XREG ? NBL : 1];
+    auto act = [&](int i, int4 (&ca)[2], int4 (&cb)[2], float & ds, float & o1, float & o2) {
+        const int t = lane + 64 * i;
+        if (t < ntask) {
+            const int sb = t >> 2, e = 16 * sb + 4 * c;  // 16-value groups: e, e + 1 (2c), e + 2, e + 3 (2c + 1)
+            ca[0] = lc[e];
+            ca[1] = lc[e + 1];
+            cb[0] = lc[e + 2];
+            cb[1] = lc[e + 3];
+            ds = ld[sb];
+            o1 = (float) ((int) lbs[e] + (int) lbs[e + 1]) * ds;
+            o2 = (float) ((int) lbs[e + 2] + (int) lbs[e + 3]) * ds;
+        } else {
+            ca[0] = make_int4(0, 0, 0, 0);
+            ca[1] = ca[0];
+            cb[0] = ca[0];
+            cb[1] = ca[0];
+            ds = 0.0f;
+            o1 = 0.0f;
+            o2 = 0.0f;
+        }
+    };
+    if constexpr (XREG) {
+#pragma unroll
+        for (int i = 0; i < NBL; i++) act(i, xa[i], xb[i], xs[i], xo[i], xo2[i]);
+    }
+    auto dot16 = [](const int (&q)[4], const int4 x) {
+        int s = __builtin_amdgcn_sdot4(q[0], x.x, 0, true);
+        s = sdot4(q[1], x.y, s);
+        s = sdot4(q[2], x.z, s);
+        return sdot4(q[3], x.w, s);
+    };
+
+    auto group = [&](int gg, const uint4 (&wv)[NBL][R][WV], const uint32_t (&hv)[NBL][R]) {
+        float acc[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) acc[r] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NBL; i++) {
+            int4 ca[2], cb[2];
+            float ds, o1, o2;
+            if constexpr (XREG) {
+                ca[0] = xa[i][0];
+                ca[1] = xa[i][1];
+                cb[0] = xb[i][0];
+                cb[1] = xb[i][1];
+                ds = xs[i];
+                o1 = xo[i];
+                o2 = xo2[i];
+            } else {
+                act(i, ca, cb, ds, o1, o2);  // zeros past the row, as its weights
+            }
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                // values 0-15 / 16-31 of sub-block 2c (low nibbles), of 2c + 1 (high nibbles)
+                int lo[2][4], hi[2][4];
+#pragma unroll
+                for (int u = 0; u < 2; u++) {
+                    const uint4 q = wv[i][r][u];
+                    const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        lo[u][j] = (int) (qw[j] & 0x0F0F0F0Fu);
+                        hi[u][j] = (int) ((qw[j] >> 4) & 0x0F0F0F0Fu);
+                    }
+                    if constexpr (TYPE == T_Q5_K) {  // the fifth bits: bit 2c of qh[l] (sub-block 2c), 2c + 1
+                        const uint4 qh = wv[i][r][2 + u];
+                        const uint32_t hb[4] = {qh.x, qh.y, qh.z, qh.w};
+#pragma unroll
+                        for (int j = 0; j < 4; j++) {
+                            lo[u][j] |= (int) (((hb[j] >> (2 * c)) & 0x01010101u) << 4);
+                            hi[u][j] |= (int) (((hb[j] >> (2 * c + 1)) & 0x01010101u) << 4);
+                        }
+                    }
+                }
+                // the 6-bit scales and mins of sub-blocks 2c and 2c + 1 (ggml's get_scale_min_k4)
+                using I = int;
+                const uint32_t h0 = hword(hv[i][r], std::integral_constant<I, 0>{});
+                const uint32_t A = hword(hv[i][r], std::integral_constant<I, 1>{}) >> csh;
+                const uint32_t M = hword(hv[i][r], std::integral_constant<I, 2>{}) >> csh;
+                const uint32_t H = hword(hv[i][r], std::integral_constant<I, 3>{}) >> csh;
+                const uint32_t scp = chi ? ((H & 0x0F0Fu) | ((A >> 2) & 0x3030u)) : (A & 0x3F3Fu);
+                const uint32_t mp = chi ? (((H >> 4) & 0x0F0Fu) | ((M >> 2) & 0x3030u)) : (M & 0x3F3Fu);
+                const int sc0 = (int) (scp & 0xFFu), sc1 = (int) ((scp >> 8) & 0xFFu);
+                const int m0 = (int) (mp & 0xFFu), m1 = (int) ((mp >> 8) & 0xFFu);
+                const float dd = h2f((uint16_t) (h0 & 0xffff)), dmin = h2f((uint16_t) (h0 >> 16));
+                const float fm0 = (float) m0 * dmin, fm1 = (float) m1 * dmin;
+                const int s0 = sdot4(lo[1][3], ca[1].w, sdot4(lo[1][2], ca[1].z, sdot4(lo[1][1], ca[1].y,
+                               sdot4(lo[1][0], ca[1].x, dot16(lo[0], ca[0])))));
+                const int s1 = sdot4(hi[1][3], cb[1].w, sdot4(hi[1][2], cb[1].z, sdot4(hi[1][1], cb[1].y,
+                               sdot4(hi[1][0], cb[1].x, dot16(hi[0], cb[0])))));
+                const int isc = sc0 * s0 + sc1 * s1;
+                const float fmin = __builtin_fmaf(fm0, o1, fm1 * o2);
+                acc[r] += __builtin_fmaf((float) isc * dd, ds, -fmin);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const float v = wave_sum(acc[r]);
+            const int row = gg * R + r;
+            if (lane == r && gg < ng && row < a.N) a.y[row] = a.res ? v + a.res[row] : v;
+        }
+    };
+
+    if constexpr (PF) {
+        // two buffers in turn: a group's weights are loaded two groups ahead
+        while (g < ng) {
+            group(g, w, hw);
+            load(g + 2 * nw, w, hw);
+            g += nw;
+            if (g >= ng) break;
+            group(g, wn, hwn);
+            load(g + 2 * nw, wn, hwn);
+            g += nw;
+        }
+    } else {
+        while (g < ng) {
+            group(g, w, hw);
+            g += nw;
+            if (g < ng) load(g, w, hw);
+        }
+    }
+}
+
+template <int TYPE, int R>
+void go_kq(int nbl, const RowKqArgs & a, int grid, hipStream_t s) {
+    switch (nbl) {
+        case 1: k_row_gemv_kq<TYPE, R, 1><<<grid, 1024, 0, s>>>(a); return;
+        case 2: k_row_gemv_kq<TYPE, R, 2><<<grid, 1024, 0, s>>>(a); return;
+        default: break;
+    }
+    if constexpr (R == 1) {
+        if (nbl == 3) k_row_gemv_kq<TYPE, 1, 3><<<grid, 1024, 0, s>>>(a);
+        else k_row_gemv_kq<TYPE, 1, 4><<<grid, 1024, 0, s>>>(a);
+        return;
+    }
+    fail("row gemv kq: two rows per group need rows of at most 128 chunks");
+}
+
+}  // namespace
+
+bool row_gemv_kq_fits(int type, int64_t N, int64_t K) {
+    if (type != T_Q4_K && type != T_Q5_K) return false;
+    // longer rows spill registers; more rows stream faster through the batched kernel after a
+    // separate quantization (measured at 4096 x 28672: 15.8 against 18.5 us)
+    if (K <= 0 || K % QKK != 0 || K > 8192 || N <= 0 || N > 8192) return false;
+    const uint64_t row = (uint64_t) (K / QKK) * (type == T_Q5_K ? 176u : 144u);
+    return (uint64_t) N * row < 0x80000000ull;
+}
+
+// y[n] (+ res[n]) = sum_k W[n, k] x[k] for a Q4_K / Q5_K weight in ggml's super-block layout.
+void launch_row_gemv_kq(int type, const void * w, int64_t N, int64_t K, const float * x, float * y, const float * res,
+                        hipStream_t s) {
+    require(row_gemv_kq_fits(type, N, K), "row gemv kq: Q4_K / Q5_K, K a multiple of 256 up to 16384, weight below 2 GB");
+    RowKqArgs a{};
+    a.w = (const uint8_t *) w;
+    a.x = x;
+    a.y = y;
+    a.res = res;
+    a.N = (int) N;
+    a.ntask = (int) (K / 64);
+    const int nbl = (a.ntask + 63) / 64;
+    const int cus = cu_count();
+    const int xw = std::min(4, (int) ((K + 1023) / 1024));
+    // two rows per group when every compute wavefront of the grid gets one and the rows are short
+    // (Q5_K's tasks hold twice the registers: one row, whose next group's weights are prefetched)
+    const int R = type == T_Q4_K && nbl == 1 && N / 2 >= (int64_t) cus * (16 - xw) ? 2 : 1;
+    const int64_t ng = (N + R - 1) / R;
+    // the x waves take groups too for long rows, or when the compute wavefronts alone would need
+    // one more round
+    a.xc = nbl > 4 || (ng <= 16LL * cus && ng > (int64_t) (16 - xw) * cus);
+    const int cw = a.xc ? 16 : 16 - xw;
+    const int grid = (int) std::max<int64_t>(1, std::min<int64_t>(cus, (ng + cw - 1) / cw));
+    if (type == T_Q4_K) {
+        if (R == 2) go_kq<T_Q4_K, 2>(nbl, a, grid, s);
+        else go_kq<T_Q4_K, 1>(nbl, a, grid, s);
+    } else {
+        if (R == 2) go_kq<T_Q5_K, 2>(nbl, a, grid, s);
+        else go_kq<T_Q5_K, 1>(nbl, a, grid, s);
+    }
+    check_launch("row gemv kq");
+}
+
+}  // namespace gcq

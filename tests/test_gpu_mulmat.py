@@ -226,25 +226,71 @@ def test_gemv_batches_residual(gops, orc, t, B, K):
     assert orc.parity(y, orc.mul_mat(raw, t, x, K) + r) < TOL
 
 
+def _exact_kquant(t, N, K, seed):
+    """A Q4_K / Q5_K weight (ggml bytes) and a row for which every float step of the product is
+    exact, so that any summation order gives the same bits: d = dmin = 1/16, the 6-bit scales and
+    mins 0 or 1, random codes; each 256-value super-block of the row holds +-127/8 once (so
+    iscale = -+8 and d_x = -+1/8 exactly) and otherwise values of |x| < 127/8 whose codes need
+    rounding; one super-block all zero, and one with a tie of |max| (+127/8 before -127/8: the first
+    one sets the scale, so the second maps to +127 by the clamp)."""
+    rng = np.random.default_rng(seed)
+    nsb = K // 256
+    bb = 144 if t == "q4_K" else 176
+    raw = np.zeros((N, nsb, bb), np.uint8)
+    raw[:, :, 0:2] = np.frombuffer(np.float16(1 / 16).tobytes(), np.uint8)  # d
+    raw[:, :, 2:4] = np.frombuffer(np.float16(1 / 16).tobytes(), np.uint8)  # dmin
+    sc = rng.integers(0, 2, (N, nsb, 8), dtype=np.uint8)
+    mn = rng.integers(0, 2, (N, nsb, 8), dtype=np.uint8)
+    raw[:, :, 4:8] = sc[:, :, 0:4]  # get_scale_min_k4's packing for values below 16
+    raw[:, :, 8:12] = mn[:, :, 0:4]
+    raw[:, :, 12:16] = sc[:, :, 4:8] | (mn[:, :, 4:8] << 4)
+    qs = 16 if t == "q4_K" else 48
+    raw[:, :, qs:qs + 128] = rng.integers(0, 256, (N, nsb, 128), dtype=np.uint8)
+    if t == "q5_K":
+        raw[:, :, 16:48] = rng.integers(0, 256, (N, nsb, 32), dtype=np.uint8)
+    top = 127 / 8
+    x = rng.uniform(-0.999 * top, 0.999 * top, (1, K)).astype(np.float32)
+    for sb in range(nsb):
+        x[0, sb * 256 + rng.integers(0, 256)] = top if rng.integers(0, 2) else -top
+    x[0, 256:512] = 0.0
+    x[0, 512:768] = np.clip(x[0, 512:768], -0.9 * top, 0.9 * top)
+    x[0, 512 + 40] = top
+    x[0, 512 + 200] = -top
+    return raw.reshape(N, nsb * bb), x
+
+
 @pytest.mark.parametrize("t", ["q4_K", "q5_K"])
 @pytest.mark.parametrize("K", [4096, 14336])
 def test_gemv_row_kquant_fused_quantizer(gops, orc, t, K):
-    """One f32 row times a Q4_K / Q5_K weight: the kernel quantizes the row to Q8_K itself. It must
-    produce what the same kernel gives on the separately quantized row (k_act_q8_K, bit-exact with
-    the oracle's quantize_row_q8_K) bit for bit, so every code, bsum and d is ggml's. The row has
-    an all-zero super-block and, in another, a tie of |max| between lanes (+3 before -3: the first
-    one sets the scale, so -3 maps to +127 by the clamp)."""
+    """One f32 row times a Q4_K / Q5_K weight: the one-launch kernel quantizes the row to Q8_K
+    itself. On a product whose float steps are all exact (_exact_kquant) it must give the same
+    bits as the separately quantized row (k_act_q8_K, bit-exact with the oracle's
+    quantize_row_q8_K) through the batched kernel, so every code, bsum and d is ggml's (a code off
+    by one moves an output by 1/128 at least); on a random weight, within 1e-3 of the oracle."""
     N = 1000
-    raw, qw = _weight(gops, orc, t, N, K, 47)
-    x = orc.normal((1, K), seed=48)
-    x[0, 256:512] = 0.0
-    x[0, 512 + 40] = 3.0
-    x[0, 512 + 200] = -3.0
+    raw, x = _exact_kquant(t, N, K, 47)
+    qw = gops.QuantWeight.from_ggml(torch.from_numpy(raw), t, K)
     xt = torch.from_numpy(x).cuda()
     y = to_np(gops.mul_mat(qw, xt))
     act = gops.quantize_act(t, xt)
     y_sep = to_np(gops.mul_mat_q(qw, act, 1))
     assert np.array_equal(y, y_sep), float(np.abs(y - y_sep).max())
+    assert np.array_equal(y, orc.mul_mat(raw, t, x, K).astype(np.float32).reshape(y.shape))
+    raw2, qw2 = _weight(gops, orc, t, N, K, 48)
+    x2 = orc.normal((1, K), seed=49)
+    y2 = to_np(gops.mul_mat(qw2, torch.from_numpy(x2).cuda()))
+    assert orc.parity(y2, orc.mul_mat(raw2, t, x2, K)) < TOL
+
+
+@pytest.mark.parametrize("t", ["q4_K", "q5_K"])
+@pytest.mark.parametrize("N,K", [(1, 256), (37, 768), (300, 2304), (4097, 4096), (8192, 8192)])
+def test_gemv_row_kquant_shapes(gops, orc, t, N, K):
+    """The one-launch K-quant row kernel at its edges: a row of one super-block (60 of 64 lanes
+    idle), ragged row counts (one row, 37, a group split by N), two chunks per lane, its largest
+    rows and row count."""
+    raw, qw = _weight(gops, orc, t, N, K, 50)
+    x = orc.normal((1, K), seed=51)
+    y = to_np(gops.mul_mat(qw, torch.from_numpy(x).cuda()))
     assert orc.parity(y, orc.mul_mat(raw, t, x, K)) < TOL
 
 
