@@ -309,8 +309,14 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const float v = wave_sum(acc[r]);
-            const int row = gg * R + r;
-            if (lane == r && gg < ng && row < a.N) a.y[row] = a.res ? v + a.res[row] : v;
+            const int row = __builtin_amdgcn_readfirstlane(gg * R + r);
+            // the residual read through the scalar unit (a constant-space pointer): a vector load
+            // here would wait for every weight load issued before it (the next groups'), as loads
+            // complete in order. Each residual value is read before its own output is written and
+            // never after another output (res may be y itself).
+            typedef const float __attribute__((address_space(4))) cfloat_t;
+            const float rv = a.res && row < a.N ? ((cfloat_t *) a.res)[row] : 0.0f;
+            if (lane == r && row < a.N) a.y[row] = a.res ? v + rv : v;
         }
     };
 

@@ -100,6 +100,26 @@ def test_mul_mat_node(be, gops, orc, t, M):
     assert np.array_equal(y, to_np(gops.mul_mat(qw, torch.from_numpy(x).cuda())))
 
 
+@pytest.mark.parametrize("t", ["q4_K", "q5_K"])
+def test_kquant_row_mul_mat_add(be, gops, orc, t):
+    """One row times a K-quant weight, then add(residual): the residual folds into the one-launch
+    row kernel's store (read through the scalar unit); bit-equal to the product plus the residual
+    added on the host in f32."""
+    N, K = 300, 1024
+    tid = orc.TYPES[t]
+    raw = _weight(orc, t, N, K, 60)
+    x = orc.normal((1, K), seed=61)
+    r = orc.normal((1, N), seed=62)
+    gr = Graph(be, {"w": (tid, [K, N], raw), "x": (G.F32, [K, 1], x), "r": (G.F32, [N, 1], r)},
+               lambda g, ctx, L: g.ggml_add(ctx, L["r"], g.ggml_mul_mat(ctx, L["w"], L["x"])))
+    y = gr.run().reshape(1, N)
+    gr.close()
+    qw = gops.QuantWeight.from_ggml(torch.from_numpy(raw), t, K)
+    y0 = to_np(gops.mul_mat(qw, torch.from_numpy(x).cuda())).reshape(1, N)
+    assert np.array_equal(y, (y0 + r).astype(np.float32))
+    assert orc.parity(y, orc.mul_mat(raw, t, x, K) + r) < TOL
+
+
 @pytest.mark.parametrize("M", [1, 4, 12])
 @pytest.mark.parametrize("t", ["q4_0", "q8_0"])
 def test_norm_mul_mat_add_chain(be, orc, t, M):
