@@ -953,11 +953,10 @@ struct DriverKOp {
 };
 struct DriverBatch {
     DriverKOp op[kDriverBatch];
+    int32_t * advance;  // a launch of one workgroup: this iteration word steps once every op has read it
 };
 
-__global__ void k_driver_ops(const DriverBatch b) {
-    const DriverKOp & o = b.op[blockIdx.y];
-    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+__device__ __forceinline__ void driver_op(const DriverKOp & o, int64_t i) {
     if (i >= o.n) return;
     const int64_t it = o.it ? (int64_t) *o.it : 0;
     uint8_t * dst = o.dst + (o.ring ? (it & 1) : it) * o.dstep;
@@ -999,7 +998,16 @@ __global__ void k_driver_ops(const DriverBatch b) {
     }
 }
 
-// The last launch of a captured loop iteration: the loop's iteration word moves to the next.
+__global__ void k_driver_ops(const DriverBatch b) {
+    driver_op(b.op[blockIdx.y], (int64_t) blockIdx.x * blockDim.x + threadIdx.x);
+    if (b.advance) {  // the launch is one workgroup: every read of the word is before the barrier
+        __syncthreads();
+        if (threadIdx.x == 0) *b.advance += 1;
+    }
+}
+
+// The last launch of a captured loop iteration when its ops take several workgroups: the loop's
+// iteration word moves to the next.
 __global__ void k_iter_next(int32_t * it) {
     if (threadIdx.x == 0) *it += 1;
 }
@@ -1096,8 +1104,16 @@ class StreamOps {
         o.it = it;
         add(o, 4);
     }
-    // the waiting ops, then the loop's iteration word to the next iteration
+    // the waiting ops, then the loop's iteration word to the next iteration: in the same launch
+    // when the ops take one workgroup, else a launch of its own
     void iter_next(int32_t * it) {
+        int64_t most = 0;
+        for (int k = 0; k < n_; k++) most = std::max(most, b_.op[k].n);
+        if (n_ == 1 && most <= 256) {
+            b_.advance = it;
+            flush();
+            return;
+        }
         flush();
         k_iter_next<<<1, 64, 0, s_>>>(it);
         check_launch("driver iteration");
@@ -1124,13 +1140,17 @@ class StreamOps {
         return s_;
     }
     // ops left waiting by a run that failed: never launched
-    void discard() { n_ = 0; }
+    void discard() {
+        n_ = 0;
+        b_.advance = nullptr;
+    }
     void flush() {
         if (n_ == 0) return;
         int64_t most = 0;
         for (int k = 0; k < n_; k++) most = std::max(most, b_.op[k].n);
         k_driver_ops<<<dim3((unsigned) ((most + 255) / 256), (unsigned) n_), 256, 0, s_>>>(b_);
         n_ = 0;
+        b_.advance = nullptr;
         check_launch("driver ops");
     }
 
