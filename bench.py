@@ -310,14 +310,23 @@ def bench_program_decode(args, w: dict | None = None) -> dict:
     from ggml_compiler_amd.llm import LlamaConfig, Model
     from ggml_compiler_amd.program import write_llama_program
 
+    import dataclasses
+
+    from ggml_compiler_amd.ops import type_id
+    from ggml_compiler_amd.program import synthetic_weights
+
     cfg = LlamaConfig.llama3_8b(max_ctx=1024)
+    wtype = getattr(args, "wtype", "q4_0")
+    if wtype != "q4_0":  # a type the fused decoder does not hold: the same stream, quantized on the GPU
+        cfg = dataclasses.replace(cfg, wtype=type_id(wtype))
+        w = synthetic_weights(cfg, seed=0, std=0.02)
     if w is None:  # the decode benchmark's weights (random init, seed 0)
         m = Model(cfg, max_prompt=16)
         m.init_random(seed=0, std=0.02)
         w = {name: m.get_weight(name) for name, *_ in m.weights()}
         m.close()
     with tempfile.TemporaryDirectory() as d:
-        path = os.path.join(d, "llama3_8b_q4_0.gguf")
+        path = os.path.join(d, f"llama3_8b_{wtype}.gguf")
         t0 = time.perf_counter()
         write_llama_program(path, cfg, w, kv_step=256, n_gen=args.steps)
         t_write = time.perf_counter() - t0
@@ -348,7 +357,7 @@ def bench_program_decode(args, w: dict | None = None) -> dict:
             "stage_calls": st["n_calls"], "first_tokens": [int(t) for t in out[:4]],
             "prompt_tok_s_decode_entry": round(PROMPT / t_prompt, 1), "write_s": round(t_write, 1),
             "load_s": round(t_load, 1),
-            "config": {"workload": f"Llama-3-8B-shaped Q4_0 decoder (random init) as a program GGUF, {PROMPT} prompt "
+            "config": {"workload": f"Llama-3-8B-shaped {wtype} decoder (random init) as a program GGUF, {PROMPT} prompt "
                                    f"tokens by the decode entry, then the generate entry's {args.steps} greedy steps "
                                    f"(n_kv 768)"}}
 
@@ -624,6 +633,9 @@ def main() -> int:
                          "program: the same model as a ggml-compiler program GGUF run by the loader")
     ap.add_argument("--only", default=None,
                     help="sweep: comma-separated configurations to run (C1, C2, K56, C3, C3K, C4); default all")
+    ap.add_argument("--wtype", default="q4_0", choices=["q4_0", "q8_0", "q4_K", "q5_K", "q6_K"],
+                    help="program: the weight type of every projection, the embedding and the lm head (q4_0: "
+                         "the decode benchmark's weights; the others: synthetic_weights of that type)")
     ap.add_argument("--type", default="q8_0", choices=["q4_0", "q8_0", "q4_K", "q5_K", "q6_K"],
                     help="gemm: the weight type")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")

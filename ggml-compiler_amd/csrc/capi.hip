@@ -516,8 +516,8 @@ int gcq_set_rows_f16(void * dst, int64_t dst_h, int64_t dst_j, const float * src
 int gcq_get_rows(int type, const void * table, int64_t nrows, int64_t D, const int32_t * idx, int64_t n, float * out,
                  void * stream) {
     return guarded([&] {
-        require(type == T_F32 || type == T_F16 || type == T_Q4_0 || type == T_Q8_0,
-                "get_rows: table type must be F32, F16, Q4_0 or Q8_0");
+        require(type == T_F32 || type == T_F16 || type == T_Q4_0 || type == T_Q8_0 || is_kquant(type),
+                "get_rows: table type must be F32, F16, Q4_0, Q8_0, Q4_K, Q5_K or Q6_K");
         need_k(type, D);
         need_dims(nrows, "nrows");
         need_dims(n, "n");

@@ -647,12 +647,48 @@ __device__ __forceinline__ void rmsnorm_q8_row(const float * xr, int n, const fl
     }
 }
 
-// Element c of row r of a get_rows table (F32, F16, or packed Q4_0 / Q8_0 of nrows x D); NaN
-// for a row outside the table.
+// Element c of a K-quant table row, as ggml's dequantize_row_q{4,5,6}_K computes it (products and
+// the difference rounded one at a time): Q4_K / Q5_K in ggml's super-blocks, d * sc * q - dmin * m;
+// Q6_K in the packed layout (208-byte super-blocks, then their fp16 d), d * sc * (q - 32).
+__device__ __forceinline__ float kquant_table_value(int type, const uint8_t * tab, int64_t nrows, int D, int64_t r,
+                                                    int c) {
+    const int nsb = D / QKK, w = c % QKK;
+    const int64_t bi = r * nsb + c / QKK;
+    auto byte = [](const uint8_t * p, int i) { return (int) p[i]; };
+    if (type == T_Q6_K) {
+        const uint8_t * b = tab + bi * 208;
+        const uint16_t * dv = reinterpret_cast<const uint16_t *>(tab + align256((size_t) nrows * nsb * 208));
+        const int h = w / 128, qq = (w % 128) / 32, l = w % 32;
+        const int a = byte(b, 64 * h + 32 * (qq & 1) + l), qh = byte(b, 128 + 32 * h + l);
+        const int q = ((qq < 2 ? a & 0xF : a >> 4) | (((qh >> (2 * qq)) & 3) << 4)) - 32;
+        const int sc = (int) reinterpret_cast<const int8_t *>(b + 192 + 8 * h)[l / 16 + 2 * qq];
+        return __fmul_rn(__fmul_rn(h2f(dv[bi]), (float) sc), (float) q);
+    }
+    const int bb = type == T_Q4_K ? 144 : 176, qs = type == T_Q4_K ? 16 : 48;
+    const uint8_t * b = tab + bi * bb;
+    const int cc = w / 64, hi = (w % 64) >= 32, l = w % 32, j = 2 * cc + hi;  // sub-block j, value l
+    const int x = byte(b, qs + 32 * cc + l);
+    int q = hi ? x >> 4 : x & 0xF;
+    if (type == T_Q5_K) q += ((byte(b, 16 + l) >> j) & 1) << 4;
+    int sc, m;  // get_scale_min_k4 on the 12 scale bytes at 4
+    if (j < 4) {
+        sc = byte(b, 4 + j) & 63;
+        m = byte(b, 8 + j) & 63;
+    } else {
+        sc = (byte(b, 8 + j) & 0xF) | ((byte(b, j) >> 6) << 4);
+        m = (byte(b, 8 + j) >> 4) | ((byte(b, 4 + j) >> 6) << 4);
+    }
+    const float d = h2f((uint16_t) (byte(b, 0) | (byte(b, 1) << 8))), dmin = h2f((uint16_t) (byte(b, 2) | (byte(b, 3) << 8)));
+    return __fsub_rn(__fmul_rn(__fmul_rn(d, (float) sc), (float) q), __fmul_rn(dmin, (float) m));
+}
+
+// Element c of row r of a get_rows table (F32, F16, packed Q4_0 / Q8_0 / Q6_K or ggml Q4_K / Q5_K
+// of nrows x D); NaN for a row outside the table.
 __device__ __forceinline__ float table_value(int type, const uint8_t * tab, int64_t nrows, int D, int64_t r, int c) {
     if (r < 0 || r >= nrows) return __builtin_nanf("");
     if (type == T_F32) return reinterpret_cast<const float *>(tab)[r * D + c];
     if (type == T_F16) return h2f(reinterpret_cast<const uint16_t *>(tab)[r * D + c]);
+    if (type == T_Q4_K || type == T_Q5_K || type == T_Q6_K) return kquant_table_value(type, tab, nrows, D, r, c);
     const int nb = D / QK;
     const int64_t blk = r * nb + c / QK;
     const int e = c % QK;

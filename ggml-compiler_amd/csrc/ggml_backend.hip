@@ -1004,10 +1004,12 @@ struct Planner {
             case GGML_OP_GET_ROWS: {
                 const ggml_tensor *a = t->src[0], *b = t->src[1];
                 const bool table = ((a->type == GGML_TYPE_F32 || a->type == GGML_TYPE_F16) && ggml_is_contiguous(a)) ||
-                                   ((a->type == GGML_TYPE_Q4_0 || a->type == GGML_TYPE_Q8_0) && whole_packed(a));
+                                   ((a->type == GGML_TYPE_Q4_0 || a->type == GGML_TYPE_Q8_0 || a->type == GGML_TYPE_Q4_K ||
+                                     a->type == GGML_TYPE_Q5_K || a->type == GGML_TYPE_Q6_K) &&
+                                    whole_packed(a));
                 require(table && a->ne[2] == 1 && a->ne[3] == 1,
                         "get_rows " + tname(t) + ": the table must be a contiguous F32 / F16 matrix or a whole Q4_0 / "
-                                                 "Q8_0 tensor");
+                                                 "Q8_0 / Q4_K / Q5_K / Q6_K tensor");
                 require(ggml_is_contiguous(b) && ggml_is_vector(b), "get_rows " + tname(t) + ": one i32 index vector");
                 Step s = new_step(S_GETROWS);
                 s.type = a->type;

@@ -163,6 +163,36 @@ def llama_program(cfg, kv_step: int = 256, n_gen: int = 128, eos: tuple[int, ...
     return program, wname
 
 
+def synthetic_weights(cfg, seed: int = 0, std: float = 0.02) -> dict[str, np.ndarray]:
+    """Random-init weights of cfg's decoder under the HIP model's names (q/k/v and gate/up rows
+    stacked), as llm.Model.get_weight gives them: ggml block bytes of cfg.wtype (any storage type the
+    library encodes: Q4_0, Q8_0, Q4_K, Q5_K, Q6_K; the GPU encoders, bit-exact with ggml's) from the
+    library's N(0, std) stream, tensor i from seed + i; norm weights 1. For models the fused decoder
+    does not hold (K-quant weights)."""
+    import torch
+
+    from . import ops
+
+    E, F, V = cfg.n_embd, cfg.n_ff, cfg.n_vocab
+    H, Hkv, D = cfg.n_head, cfg.n_head_kv, cfg.head_dim
+    shapes = [("token_embd", V, E)]
+    for l in range(cfg.n_layer):
+        b = f"blk.{l}."
+        shapes += [(b + "attn_qkv", (H + 2 * Hkv) * D, E), (b + "attn_output", E, H * D),
+                   (b + "ffn_gate_up", 2 * F, E), (b + "ffn_down", E, F)]
+    shapes.append(("output", V, E))
+    out: dict[str, np.ndarray] = {"output_norm": np.ones(E, np.float32)}
+    for l in range(cfg.n_layer):
+        out[f"blk.{l}.attn_norm"] = np.ones(E, np.float32)
+        out[f"blk.{l}.ffn_norm"] = np.ones(E, np.float32)
+    for i, (name, rows, cols) in enumerate(shapes):
+        x = ops.fill_normal((rows, cols), seed=seed + i, std=std)
+        out[name] = ops.quantize(x, cfg.wtype).cpu().numpy()
+        del x
+    torch.cuda.synchronize()
+    return out
+
+
 def write_llama_program(path: str | Path, cfg, weights: dict[str, np.ndarray], kv_step: int = 256, n_gen: int = 128,
                         eos: tuple[int, ...] = ()) -> None:
     """The GGUF: the program JSON, tensor_names (w.N -> the weight's name), and every weight as

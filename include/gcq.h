@@ -161,7 +161,8 @@ GCQ_API int gcq_set_rows_f16(void * dst, int64_t dst_h, int64_t dst_j, const flo
                              int64_t src_j, const int32_t * idx, int64_t n, int64_t D, int64_t Hrows, int64_t dst_rows,
                              void * stream);
 /* ggml_get_rows (runtime/src/ops.cpp:302-309): out[j][:] = row idx[j] of a table of nrows x D
- * (F32, F16, or a packed Q4_0 / Q8_0 weight), as f32; an index outside the table gives NaNs. */
+ * (F32, F16, a packed Q4_0 / Q8_0 / Q6_K weight or Q4_K / Q5_K super-blocks), as f32, each element as
+ * ggml's dequantize_row_* gives it; an index outside the table gives NaNs. */
 GCQ_API int gcq_get_rows(int type, const void * table, int64_t nrows, int64_t D, const int32_t * idx, int64_t n,
                          float * out, void * stream);
 /* ggml_swiglu_split(g, u) = silu(g) * u (runtime/src/ops.cpp:251-258). */

@@ -54,7 +54,7 @@ def test_set_rows_f16(gops, orc):
     assert np.array_equal(got, want)
 
 
-@pytest.mark.parametrize("t", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("t", ["q4_0", "q8_0", "q4_K", "q5_K", "q6_K"])
 def test_get_rows_quantized_table(gops, orc, t):
     raw = orc.quantize(orc.normal((100, 4096), seed=55, std=0.02), t)
     qw = gops.QuantWeight.from_ggml(torch.from_numpy(raw), t, 4096)

@@ -304,6 +304,35 @@ def test_llama_program_decode_and_generate(tmp_path, orc, wtype):
         assert s2.stats["n_calls"] == 6
 
 
+@pytest.mark.parametrize("wtype", [12, 13, 14])
+def test_llama_program_kquant_weights(tmp_path, orc, wtype):
+    """A Llama decoder program whose weights are all one K-quant type (Q4_K, Q5_K, Q6_K: every
+    projection, the embedding table and the lm head), which the fused decoder does not hold: the
+    decode entry against the oracle decoder on the same bytes, then the generate entry's tokens."""
+    from ggml_compiler_amd.llm import LlamaConfig
+    from ggml_compiler_amd.program import synthetic_weights, write_llama_program
+    from llama_ref import OracleLlama
+
+    cfg = LlamaConfig(n_layer=2, n_embd=256, n_head=4, n_head_kv=2, head_dim=64, n_ff=512, n_vocab=1000,
+                      max_ctx=64, wtype=wtype, rms_eps=1e-5, rope_base=10000.0)
+    w = synthetic_weights(cfg, seed=31)
+    path = str(tmp_path / "llama_kq.gguf")
+    write_llama_program(path, cfg, w, kv_step=16, n_gen=12, eos=(999,))
+    with runtime.Session(path) as s:
+        o = OracleLlama(cfg, w)
+        tok, toks = 17, []
+        for p in range(12):
+            n_kv = max(16, (p + 16) // 16 * 16)
+            mask = np.where(np.arange(n_kv) <= p, 0.0, -np.inf).astype(np.float32).reshape(1, 1, 1, n_kv)
+            lg = s.run(np.array([[tok]], np.int32), np.array([p], np.int32), mask, entry="decode")["logits"]
+            assert orc.parity(lg.reshape(-1), o.forward([tok])) < TOL_LM, p
+            tok = int(np.argmax(lg))
+            toks.append(tok)
+        s.reset()
+        gen = s.run(np.array([[17]], np.int32), np.array([0], np.int32), entry="generate")["tokens"]
+        assert list(gen[:12]) == toks
+
+
 def test_compiled_builder_replaces_a_stage(tmp_path, orc):
     """ggml_compiler_load_with: a builder (here a ctypes callback, as generated C++ would be)
     builds stage `lin` from its parameter and the GGUF weight by name; the program's own nodes for
