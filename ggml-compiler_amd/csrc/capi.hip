@@ -21,8 +21,9 @@ void launch_act_to_ggml(int wtype, const void * act, int64_t B, int64_t k, void 
 bool gemv_row_kq_fits(int type, int64_t N, int64_t K);
 void launch_gemv_row_kq(int type, const void * w, int64_t N, int64_t K, const float * x, float * y, hipStream_t s);
 bool row_gemv_kq_fits(int type, int64_t N, int64_t K);
-void launch_row_gemv_kq(int type, const void * w, int64_t N, int64_t K, const float * x, float * y, const float * res,
-                        hipStream_t s);
+bool row_gemv_kq_norm_fits(int type, int64_t N, int64_t K);
+void launch_row_gemv_kq(int type, const void * w, int64_t N, int64_t K, const float * x, const float * norm_w, float eps,
+                        float * y, const float * res, hipStream_t s);
 void launch_gemv(int type, const void * w, int64_t N, int64_t K, const void * act, int64_t B, float * y, int64_t ldy,
                  hipStream_t s, const float * res = nullptr);
 void launch_isums(int type, const void * w, int64_t N, int64_t K, const void * act, int64_t B, int32_t * out,
@@ -201,7 +202,7 @@ void mul_mat_with_workspace(int wtype, const void * w, int64_t N, int64_t K, con
         launch_row_gemv(wtype, PRO_PLAIN, EPI_STORE, a, s);
         return;
     }
-    if (M == 1 && row_gemv_kq_fits(wtype, N, K)) return launch_row_gemv_kq(wtype, w, N, K, x, y, nullptr, s);
+    if (M == 1 && row_gemv_kq_fits(wtype, N, K)) return launch_row_gemv_kq(wtype, w, N, K, x, nullptr, 0.0f, y, nullptr, s);
     if (M == 1 && gemv_row_kq_fits(wtype, N, K)) return launch_gemv_row_kq(wtype, w, N, K, x, y, s);
     if (M <= 8) {
         launch_act_quant(wtype, x, ldx, M, K, ws, s);

@@ -35,8 +35,9 @@ void launch_pack(int type, const void * src, int64_t nrows, int64_t k, void * ds
 void launch_unpack(int type, const void * src, int64_t nrows, int64_t k, void * dst, hipStream_t s);
 void launch_act_quant(int wtype, const float * x, int64_t ldx, int64_t B, int64_t k, void * act, hipStream_t s);
 bool row_gemv_kq_fits(int type, int64_t N, int64_t K);
-void launch_row_gemv_kq(int type, const void * w, int64_t N, int64_t K, const float * x, float * y, const float * res,
-                        hipStream_t s);
+bool row_gemv_kq_norm_fits(int type, int64_t N, int64_t K);
+void launch_row_gemv_kq(int type, const void * w, int64_t N, int64_t K, const float * x, const float * norm_w, float eps,
+                        float * y, const float * res, hipStream_t s);
 void launch_gemv(int type, const void * w, int64_t N, int64_t K, const void * act, int64_t B, float * y, int64_t ldy,
                  hipStream_t s, const float * res);
 void launch_gemm(int type, const void * w, int64_t N, int64_t K, const void * act, int64_t M, float * y, int64_t ldy,
@@ -162,6 +163,14 @@ bool q8_mul_mat(const ggml_tensor * mm) {
     const ggml_tensor * a = mm->src[0];
     return (a->type == GGML_TYPE_Q4_0 || a->type == GGML_TYPE_Q8_0) && whole_packed(a) && a->ne[2] == 1 &&
            a->ne[3] == 1;
+}
+
+// A mul_mat of one row by a Q4_K / Q5_K weight that the K-quant row GEMV runs with the rms_norm
+// prologue.
+bool kq_norm_mul_mat(const ggml_tensor * mm) {
+    const ggml_tensor * a = mm->src[0];
+    return (a->type == GGML_TYPE_Q4_K || a->type == GGML_TYPE_Q5_K) && whole_packed(a) && a->ne[2] == 1 &&
+           a->ne[3] == 1 && ggml_nrows(mm->src[1]) == 1 && row_gemv_kq_norm_fits(a->type, a->ne[1], a->ne[0]);
 }
 
 // flash_attn_ext of one query row that the one-pass decode kernel runs (f16 K/V with 16-byte rows,
@@ -352,7 +361,8 @@ Chains find_chains(const ggml_cgraph * g, bool fuse) {
             if (m->op != GGML_OP_MUL || m->src[0] != t || !f32_contig(w) || w->ne[0] != t->ne[0] || !ggml_is_vector(w))
                 continue;
             const int k = sole(m);
-            if (k >= 0 && g->nodes[k]->op == GGML_OP_MUL_MAT && g->nodes[k]->src[1] == m && q8_mul_mat(g->nodes[k])) {
+            if (k >= 0 && g->nodes[k]->op == GGML_OP_MUL_MAT && g->nodes[k]->src[1] == m &&
+                (q8_mul_mat(g->nodes[k]) || kq_norm_mul_mat(g->nodes[k]))) {
                 const int a = with_add(k);
                 if (a >= 0) link({i, j, k, a});
                 else link({i, j, k});
@@ -362,10 +372,13 @@ Chains find_chains(const ggml_cgraph * g, bool fuse) {
             // prologue and the normalized row is never written.
             const std::vector<int> & rd = readers[m];
             bool rows1 = ggml_nrows(m) == 1 && !is_output(m) && m != g->nodes[n - 1] && rd.size() >= 2;
+            bool allq8 = true;
             for (int r : rd) {
                 const ggml_tensor * mm = g->nodes[r];
-                rows1 = rows1 && mm->op == GGML_OP_MUL_MAT && mm->src[1] == m && mm->src[0] != m &&
-                        q8_mul_mat(mm) && row_gemv_fits(mm->src[0]->type, m->ne[0]);
+                const bool q8 = mm->op == GGML_OP_MUL_MAT && q8_mul_mat(mm) && row_gemv_fits(mm->src[0]->type, m->ne[0]);
+                const bool kq = mm->op == GGML_OP_MUL_MAT && kq_norm_mul_mat(mm);
+                rows1 = rows1 && mm->op == GGML_OP_MUL_MAT && mm->src[1] == m && mm->src[0] != m && (q8 || kq);
+                allq8 = allq8 && q8;
             }
             if (!rows1) {
                 link({i, j});
@@ -384,7 +397,7 @@ Chains find_chains(const ggml_cgraph * g, bool fuse) {
                 last = std::max(last, c.end[r]);
             }
             c.end[i] = c.end[j] = last;  // x and w are read until the last reader's work runs
-            if (!adds && same && rd.size() <= 3) {
+            if (!adds && same && allq8 && rd.size() <= 3) {  // the multi-weight launches: Q4_0 / Q8_0
                 std::vector<int> grp(rd.begin(), rd.end());
                 std::sort(grp.begin(), grp.end());
                 std::vector<int> qkv = grp.size() == 3 ? qkv_rope_group(g, grp, uses, reader) : std::vector<int>{};
@@ -1475,10 +1488,13 @@ void run_step(const ggml_backend * be, const Step & s) {
                 launch_row_gemv(wt, nw ? PRO_NORM : PRO_PLAIN, EPI_STORE, a, st);
                 return;
             }
-            if (M == 1 && !nw && row_gemv_kq_fits(wt, N, K) && aligned(x, 16)) {  // one launch, row quantized in it
-                launch_row_gemv_kq(wt, s.in[0], N, K, x, y, res, st);
+            // one launch, the row (normalized and) quantized in it
+            if (M == 1 && (nw ? row_gemv_kq_norm_fits(wt, N, K) : row_gemv_kq_fits(wt, N, K)) && aligned(x, 16)) {
+                launch_row_gemv_kq(wt, s.in[0], N, K, x, nw, s.f[0], y, res, st);
                 return;
             }
+            // a folded norm reaches a K-quant weight only through the row kernel above
+            require(!nw || wt == T_Q4_0 || wt == T_Q8_0, "mul_mat: a normalized row for a K-quant weight off its row kernel");
             if (nw) launch_rmsnorm_q8(x, ldx, nw, s.f[0], M, K, be->ws, st);
             else launch_act_quant(wt, x, ldx, M, K, be->ws, st);
             if (M <= 8) launch_gemv(wt, s.in[0], N, K, be->ws, M, y, ldy, st, res);

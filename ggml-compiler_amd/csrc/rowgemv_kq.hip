@@ -39,6 +39,8 @@ struct RowKqArgs {
     const float * x;    // the activation row [K]
     float * y;          // [N]
     const float * res;  // optional, y = res + W x
+    const float * norm_w;  // NORM: y = W (rms_norm(x) * norm_w) (ggml_rms_norm then ggml_mul)
+    float eps;
     int N, ntask;       // ntask: 64-value chunks per row (K / 64)
     int xc;             // the x waves take row groups too
 };
@@ -50,7 +52,7 @@ struct RowKqFmt {
     static constexpr uint32_t QS = TYPE == T_Q5_K ? 48u : 16u;      // offset of the nibbles
 };
 
-template <int TYPE, int R, int NBL>
+template <int TYPE, int R, int NBL, bool NORM>
 __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
 #pragma clang fp contract(off)
     using F = RowKqFmt<TYPE>;
@@ -63,7 +65,8 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
     __shared__ int4 lc[kRowKqMaxK / 16];           // codes, 16 per entry
     __shared__ int16_t lbs[kRowKqMaxK / 16];       // bsums of 16
     __shared__ float ld[kRowKqMaxK / 256];         // d per super-block
-    __shared__ unsigned int s_flag;
+    __shared__ unsigned int s_flag, s_norm;        // x waves done with: their codes; their norm partials
+    __shared__ double red[4];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int ntask = a.ntask;
@@ -86,6 +89,7 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
 
     if (threadIdx.x == 0) {
         s_flag = 0u;
+        s_norm = 0u;
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the count is zero before the workgroup meets
     }
 
@@ -125,28 +129,69 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
 
     if (xw) {
         // the row's loads first, then the workgroup meets (no weight load is ahead of them)
-        float4 xv[RMAX][4];
+        float4 xv[RMAX][4], nv[NORM ? RMAX : 1][4];
 #pragma unroll
         for (int r = 0; r < RMAX; r++) {
             const int gi = (int) threadIdx.x + r * XW * 64;
             if (r < rounds && gi < ngrp) {
 #pragma unroll
-                for (int k = 0; k < 4; k++) xv[r][k] = *reinterpret_cast<const float4 *>(a.x + gi * 16 + 4 * k);
+                for (int k = 0; k < 4; k++) {
+                    xv[r][k] = *reinterpret_cast<const float4 *>(a.x + gi * 16 + 4 * k);
+                    if constexpr (NORM) {  // the norm weight at any 4-byte alignment
+                        const float * wp = a.norm_w + gi * 16 + 4 * k;
+                        nv[r][k] = make_float4(wp[0], wp[1], wp[2], wp[3]);
+                    }
+                }
             } else {
 #pragma unroll
-                for (int k = 0; k < 4; k++) xv[r][k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                for (int k = 0; k < 4; k++) {
+                    xv[r][k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    if constexpr (NORM) nv[r][k] = xv[r][k];
+                }
             }
         }
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
+        float scale = 1.0f;
+        if constexpr (NORM) {
+            // ggml_rms_norm: squares rounded to f32, summed in double, the mean rounded to f32
+            double ss = 0.0;
+#pragma unroll
+            for (int r = 0; r < RMAX; r++)
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    ss += (double) (xv[r][k].x * xv[r][k].x);
+                    ss += (double) (xv[r][k].y * xv[r][k].y);
+                    ss += (double) (xv[r][k].z * xv[r][k].z);
+                    ss += (double) (xv[r][k].w * xv[r][k].w);
+                }
+            ss = wave_sum_d(ss);
+            if (lane == 0) {
+                red[wave] = ss;
+                lds_signal(&s_norm);
+            }
+            lds_wait(&s_norm, XW);
+            double tot = 0.0;
+#pragma unroll
+            for (int i = 0; i < XWMAX; i++)
+                if (i < XW) tot += red[i];
+            scale = 1.0f / sqrtf((float) (tot / (double) K) + a.eps);
+        }
 #pragma unroll
         for (int r = 0; r < RMAX; r++) {
             const int gi = (int) threadIdx.x + r * XW * 64;
             if (r >= rounds) break;
-            const float v[16] = {xv[r][0].x, xv[r][0].y, xv[r][0].z, xv[r][0].w, xv[r][1].x, xv[r][1].y,
-                                 xv[r][1].z, xv[r][1].w, xv[r][2].x, xv[r][2].y, xv[r][2].z, xv[r][2].w,
-                                 xv[r][3].x, xv[r][3].y, xv[r][3].z, xv[r][3].w};
+            float v[16] = {xv[r][0].x, xv[r][0].y, xv[r][0].z, xv[r][0].w, xv[r][1].x, xv[r][1].y,
+                           xv[r][1].z, xv[r][1].w, xv[r][2].x, xv[r][2].y, xv[r][2].z, xv[r][2].w,
+                           xv[r][3].x, xv[r][3].y, xv[r][3].z, xv[r][3].w};
+            if constexpr (NORM) {
+                const float w16[16] = {nv[r][0].x, nv[r][0].y, nv[r][0].z, nv[r][0].w, nv[r][1].x, nv[r][1].y,
+                                       nv[r][1].z, nv[r][1].w, nv[r][2].x, nv[r][2].y, nv[r][2].z, nv[r][2].w,
+                                       nv[r][3].x, nv[r][3].y, nv[r][3].z, nv[r][3].w};
+#pragma unroll
+                for (int j = 0; j < 16; j++) v[j] = (v[j] * scale) * w16[j];
+            }
             // the super-block's first largest |x| (its 16 groups are 16 consecutive lanes)
             float ax = 0.0f, mx = 0.0f;
             int idx = 1 << 30;
@@ -340,19 +385,17 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
     }
 }
 
-template <int TYPE, int R>
+template <int TYPE, int R, bool NORM>
 void go_kq(int nbl, const RowKqArgs & a, int grid, hipStream_t s) {
-    switch (nbl) {
-        case 1: k_row_gemv_kq<TYPE, R, 1><<<grid, 1024, 0, s>>>(a); return;
-        case 2: k_row_gemv_kq<TYPE, R, 2><<<grid, 1024, 0, s>>>(a); return;
-        default: break;
-    }
-    if constexpr (R == 1) {
-        if (nbl == 3) k_row_gemv_kq<TYPE, 1, 3><<<grid, 1024, 0, s>>>(a);
-        else k_row_gemv_kq<TYPE, 1, 4><<<grid, 1024, 0, s>>>(a);
-        return;
-    }
-    fail("row gemv kq: two rows per group need rows of at most 128 chunks");
+    if (nbl == 1) k_row_gemv_kq<TYPE, R, 1, NORM><<<grid, 1024, 0, s>>>(a);
+    else if (R == 1) k_row_gemv_kq<TYPE, 1, 2, NORM><<<grid, 1024, 0, s>>>(a);
+    else fail("row gemv kq: two rows per group need rows of at most 64 chunks");
+}
+
+template <int TYPE, bool NORM>
+void go_kq_r(int R, int nbl, const RowKqArgs & a, int grid, hipStream_t s) {
+    if (R == 2) go_kq<TYPE, 2, NORM>(nbl, a, grid, s);
+    else go_kq<TYPE, 1, NORM>(nbl, a, grid, s);
 }
 
 }  // namespace
@@ -366,15 +409,26 @@ bool row_gemv_kq_fits(int type, int64_t N, int64_t K) {
     return (uint64_t) N * row < 0x80000000ull;
 }
 
-// y[n] (+ res[n]) = sum_k W[n, k] x[k] for a Q4_K / Q5_K weight in ggml's super-block layout.
-void launch_row_gemv_kq(int type, const void * w, int64_t N, int64_t K, const float * x, float * y, const float * res,
-                        hipStream_t s) {
-    require(row_gemv_kq_fits(type, N, K), "row gemv kq: Q4_K / Q5_K, K a multiple of 256 up to 16384, weight below 2 GB");
+// With the rms_norm prologue (a normalized row read by several projections, each normalizing it
+// itself): up to 16384 rows, where it also saves the norm's and the quantization's launches.
+bool row_gemv_kq_norm_fits(int type, int64_t N, int64_t K) {
+    return row_gemv_kq_fits(type, std::min<int64_t>(N, 8192), K) && N <= 16384 &&
+           (uint64_t) N * (uint64_t) (K / QKK) * (type == T_Q5_K ? 176u : 144u) < 0x80000000ull;
+}
+
+// y[n] (+ res[n]) = sum_k W[n, k] x'[k] for a Q4_K / Q5_K weight in ggml's super-block layout, x' = x
+// or, with norm_w, ggml_mul(ggml_rms_norm(x, eps), norm_w).
+void launch_row_gemv_kq(int type, const void * w, int64_t N, int64_t K, const float * x, const float * norm_w, float eps,
+                        float * y, const float * res, hipStream_t s) {
+    require(norm_w ? row_gemv_kq_norm_fits(type, N, K) : row_gemv_kq_fits(type, N, K),
+            "row gemv kq: Q4_K / Q5_K, K a multiple of 256 up to 8192, up to 8192 rows (16384 with the norm)");
     RowKqArgs a{};
     a.w = (const uint8_t *) w;
     a.x = x;
     a.y = y;
     a.res = res;
+    a.norm_w = norm_w;
+    a.eps = eps;
     a.N = (int) N;
     a.ntask = (int) (K / 64);
     const int nbl = (a.ntask + 63) / 64;
@@ -390,11 +444,11 @@ void launch_row_gemv_kq(int type, const void * w, int64_t N, int64_t K, const fl
     const int cw = a.xc ? 16 : 16 - xw;
     const int grid = (int) std::max<int64_t>(1, std::min<int64_t>(cus, (ng + cw - 1) / cw));
     if (type == T_Q4_K) {
-        if (R == 2) go_kq<T_Q4_K, 2>(nbl, a, grid, s);
-        else go_kq<T_Q4_K, 1>(nbl, a, grid, s);
+        if (norm_w) go_kq_r<T_Q4_K, true>(R, nbl, a, grid, s);
+        else go_kq_r<T_Q4_K, false>(R, nbl, a, grid, s);
     } else {
-        if (R == 2) go_kq<T_Q5_K, 2>(nbl, a, grid, s);
-        else go_kq<T_Q5_K, 1>(nbl, a, grid, s);
+        if (norm_w) go_kq_r<T_Q5_K, true>(R, nbl, a, grid, s);
+        else go_kq_r<T_Q5_K, false>(R, nbl, a, grid, s);
     }
     check_launch("row gemv kq");
 }

@@ -121,7 +121,7 @@ def test_kquant_row_mul_mat_add(be, gops, orc, t):
 
 
 @pytest.mark.parametrize("M", [1, 4, 12])
-@pytest.mark.parametrize("t", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("t", ["q4_0", "q8_0", "q4_K", "q5_K", "q6_K"])
 def test_norm_mul_mat_add_chain(be, orc, t, M):
     """rms_norm -> mul(w) -> mul_mat -> add(residual) folded into one GEMV / GEMM launch sequence,
     against the oracle and against the same graph with the chain broken (every node launched)."""
@@ -152,7 +152,7 @@ def test_norm_mul_mat_add_chain(be, orc, t, M):
     assert orc.parity(yf, ys) < TOL
 
 
-@pytest.mark.parametrize("t", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("t", ["q4_0", "q8_0", "q4_K", "q5_K", "q6_K"])
 def test_norm_row_folded_into_several_gemvs(be, orc, t):
     """One normalized row read by three mul_mats (q / k / v of a decode step), one of them followed
     by an add: each GEMV normalizes x in its prologue; against the oracle and the unfolded graph."""
