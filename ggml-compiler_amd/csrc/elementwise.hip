@@ -95,10 +95,9 @@ __global__ __launch_bounds__(256) void k_rope_neox(const float * __restrict__ x,
             if (d < D) o[d] = xr[d];
             continue;
         }
-        const float c = cs[i].x, sn = cs[i].y;
-        const float x0 = xr[i], x1 = xr[i + half];
-        o[i] = x0 * c - x1 * sn;
-        o[i + half] = x0 * sn + x1 * c;
+        const float2 r = rope_pair(xr[i], xr[i + half], cs[i]);
+        o[i] = r.x;
+        o[i + half] = r.y;
     }
 }
 

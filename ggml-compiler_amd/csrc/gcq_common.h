@@ -165,6 +165,42 @@ void launch_row_gemv(int type, int pro, int epi, const RowArgs & a, hipStream_t 
 // ranges; false when they span 2 GB or more.
 bool row_gemv_ranges(int type, int n, const uint8_t * const * w, const int64_t * N, int64_t K, RowArgs & a);
 
+// The K-quant decode-row GEMV (rowgemv_kq.hip): a Q4_K / Q5_K weight in ggml's super-block layout
+// times one f32 row, quantized to Q8_K (optionally rms-normalized first) inside the launch.
+struct RowKqArgs {
+    const uint8_t * w;     // super-blocks [N][K / 256]; several weights: the lowest of them
+    const float * x;       // the activation row [K]
+    float * y;             // EPI_STORE [N], EPI_SWIGLU [N/2], EPI_ROPE_KV: roped q [H*D]
+    const float * res;     // EPI_STORE with one weight, optional: y = res + W x
+    const float * norm_w;  // y = W (rms_norm(x) * norm_w) (ggml_rms_norm then ggml_mul)
+    float eps;
+    int N, ntask;          // rows (of all weights), 64-value chunks per row (K / 64)
+    int xc;                // set by the launch: the x waves take row groups too
+    // Several weights of one row length read by the same row: rows [r_end[k-1], r_end[k]) are
+    // weight k's, at byte offset r_off[k] from w (the weights span `span` bytes, < 2 GB); EPI_STORE
+    // writes weight k's results to r_y[k]. Row pairs as RowArgs' (q / k / v rope, gate / up).
+    int nr;  // 0: one weight
+    int r_end[3];
+    uint32_t r_off[3], span;
+    float * r_y[3];
+    // EPI_ROPE_KV: the position, its (cos, sin) table, the f16 caches [Hkv][ctx][D]
+    const int * pos;
+    const float2 * rope_cs;
+    uint16_t * kc;
+    uint16_t * vc;
+    int64_t ctx;
+    int H, Hkv, D;
+    uint32_t hd_magic;  // set by the launch: x / (D/2) = mulhi(x, hd_magic)
+};
+
+// Offsets and span of up to 3 K-quant weights (N[k] rows of K) for RowKqArgs' ranges; false when
+// they span 2 GB or more.
+bool row_gemv_kq_ranges(int type, int n, const uint8_t * const * w, const int64_t * N, int64_t K, RowKqArgs & a);
+// Whether launch_row_gemv_kq_epi runs this epilogue on rows of K values (the row-pair epilogues
+// take rows of at most 4096 values).
+bool row_gemv_kq_epi_fits(int type, int epi, int64_t K);
+void launch_row_gemv_kq_epi(int type, int epi, const RowKqArgs & a, hipStream_t s);
+
 // Shapes and byte strides of a strided copy / conversion (elementwise.hip).
 struct Cpy4 {
     int64_t sne[4], snb[4], dne[4], dnb[4];
@@ -268,6 +304,12 @@ __device__ __forceinline__ float h2f(uint16_t h) {
     _Float16 v;
     __builtin_memcpy(&v, &h, 2);
     return (float) v;
+}
+// The NEOX rotation of the pair (x0, x1) by (cos, sin). Every rope site (the rope kernel, the
+// GEMV epilogues) calls this one expression, so each compiles to the same operations whatever
+// contraction its caller's scope allows.
+__device__ __forceinline__ float2 rope_pair(float x0, float x1, float2 cs) {
+    return make_float2(x0 * cs.x - x1 * cs.y, x0 * cs.y + x1 * cs.x);
 }
 // fp32 -> fp16, round to nearest even (v_cvt_f16_f32 in the default rounding mode).
 __device__ __forceinline__ uint16_t f2h(float f) {

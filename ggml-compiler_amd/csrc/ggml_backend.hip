@@ -173,6 +173,17 @@ bool kq_norm_mul_mat(const ggml_tensor * mm) {
            a->ne[3] == 1 && ggml_nrows(mm->src[1]) == 1 && row_gemv_kq_norm_fits(a->type, a->ne[1], a->ne[0]);
 }
 
+// Up to 3 weights of one type and row length that one decode-row launch reads (Q4_0 / Q8_0 by
+// the row GEMV's ranges, Q4_K / Q5_K by the K-quant row GEMV's): spans under 2 GB.
+bool weights_fit_one_launch(int type, int n, const uint8_t * const * w, const int64_t * N, int64_t K) {
+    if (is_kquant(type)) {
+        RowKqArgs a{};
+        return row_gemv_kq_ranges(type, n, w, N, K, a);
+    }
+    RowArgs a{};
+    return row_gemv_ranges(type, n, w, N, K, a);
+}
+
 // flash_attn_ext of one query row that the one-pass decode kernel runs (f16 K/V with 16-byte rows,
 // f16 mask or none, no ALiBi / softcap) and whose output the decode-row GEMV can merge from
 // split partials (H * D <= 4096).
@@ -372,13 +383,14 @@ Chains find_chains(const ggml_cgraph * g, bool fuse) {
             // prologue and the normalized row is never written.
             const std::vector<int> & rd = readers[m];
             bool rows1 = ggml_nrows(m) == 1 && !is_output(m) && m != g->nodes[n - 1] && rd.size() >= 2;
-            bool allq8 = true;
+            bool allq8 = true, allkq = true;
             for (int r : rd) {
                 const ggml_tensor * mm = g->nodes[r];
                 const bool q8 = mm->op == GGML_OP_MUL_MAT && q8_mul_mat(mm) && row_gemv_fits(mm->src[0]->type, m->ne[0]);
                 const bool kq = mm->op == GGML_OP_MUL_MAT && kq_norm_mul_mat(mm);
                 rows1 = rows1 && mm->op == GGML_OP_MUL_MAT && mm->src[1] == m && mm->src[0] != m && (q8 || kq);
                 allq8 = allq8 && q8;
+                allkq = allkq && kq;
             }
             if (!rows1) {
                 link({i, j});
@@ -397,11 +409,13 @@ Chains find_chains(const ggml_cgraph * g, bool fuse) {
                 last = std::max(last, c.end[r]);
             }
             c.end[i] = c.end[j] = last;  // x and w are read until the last reader's work runs
-            if (!adds && same && allq8 && rd.size() <= 3) {  // the multi-weight launches: Q4_0 / Q8_0
+            if (!adds && same && (allq8 || allkq) && rd.size() <= 3) {  // the multi-weight launches
                 std::vector<int> grp(rd.begin(), rd.end());
                 std::sort(grp.begin(), grp.end());
-                std::vector<int> qkv = grp.size() == 3 ? qkv_rope_group(g, grp, uses, reader) : std::vector<int>{};
-                std::vector<int> gu = grp.size() == 2 ? gate_up_group(g, grp, uses, reader) : std::vector<int>{};
+                // the row-pair epilogues: any Q4_0 / Q8_0 row, K-quant rows of at most 4096 values
+                const bool pairs = allq8 || row_gemv_kq_epi_fits(g->nodes[grp[0]]->src[0]->type, EPI_ROPE_KV, m->ne[0]);
+                std::vector<int> qkv = grp.size() == 3 && pairs ? qkv_rope_group(g, grp, uses, reader) : std::vector<int>{};
+                std::vector<int> gu = grp.size() == 2 && pairs ? gate_up_group(g, grp, uses, reader) : std::vector<int>{};
                 const int kind = !qkv.empty() ? 3 : !gu.empty() ? 4 : 0;
                 if (kind == 3) grp = qkv;
                 if (kind == 4) grp = gu;
@@ -798,8 +812,7 @@ struct Planner {
         s.n[6] = rq->ne[0];   // D
         s.n[7] = ck->ne[1];   // ctx
         std::memcpy(&s.f[0], &nrm->op_params[0], 4);
-        RowArgs ra{};
-        require(row_gemv_ranges(type, 3, w, N, K, ra), "q / k / v rope group: the weights do not fit one launch");
+        require(weights_fit_one_launch(type, 3, w, N, K), "q / k / v rope group: the weights do not fit one launch");
         steps.push_back(s);
     }
 
@@ -848,7 +861,8 @@ struct Planner {
         const int type = m0->src[0]->type;
         const uint8_t * w[3];
         int64_t N[3], K = 0;
-        bool ok = grp.size() >= 2 && grp.size() <= 3 && (type == GGML_TYPE_Q4_0 || type == GGML_TYPE_Q8_0);
+        bool ok = grp.size() >= 2 && grp.size() <= 3 &&
+                  (type == GGML_TYPE_Q4_0 || type == GGML_TYPE_Q8_0 || type == GGML_TYPE_Q4_K || type == GGML_TYPE_Q5_K);
         for (size_t k = 0; ok && k < grp.size(); k++) {
             const ggml_tensor * mm = g->nodes[grp[k]];
             const ggml_tensor * wt = mm->src[0];
@@ -858,8 +872,7 @@ struct Planner {
             packed_dims(wt, N[k], K);
             w[k] = (const uint8_t *) d(wt);
         }
-        RowArgs ra{};
-        if (ok) ok = row_gemv_ranges(type, (int) grp.size(), w, N, K, ra);
+        if (ok) ok = weights_fit_one_launch(type, (int) grp.size(), w, N, K);
         if (!ok) {
             for (int r : grp) mulmat(g->nodes[r], g->nodes[r]->src[1], nullptr, 0.0f, nullptr, g->nodes[r]);
             return;
@@ -1508,6 +1521,24 @@ void run_step(const ggml_backend * be, const Step & s) {
             return;
         case S_QKV_ROPE: {
             const uint8_t * w[3] = {(const uint8_t *) s.in[0], (const uint8_t *) s.in[3], (const uint8_t *) s.in[4]};
+            if (is_kquant(s.type)) {
+                RowKqArgs a{};
+                require(row_gemv_kq_ranges(s.type, 3, w, s.n, s.n[3], a), "q / k / v rope: weights do not fit one launch");
+                a.x = (const float *) s.in[1];
+                a.norm_w = (const float *) s.in[2];
+                a.eps = s.f[0];
+                a.y = (float *) s.out;
+                a.pos = (const int *) s.in[5];
+                a.rope_cs = be->rope_cs;
+                a.kc = (uint16_t *) s.out2[0];
+                a.vc = (uint16_t *) s.out2[1];
+                a.H = (int) s.n[4];
+                a.Hkv = (int) s.n[5];
+                a.D = (int) s.n[6];
+                a.ctx = s.n[7];
+                launch_row_gemv_kq_epi(s.type, EPI_ROPE_KV, a, st);
+                return;
+            }
             RowArgs a{};
             require(row_gemv_ranges(s.type, 3, w, s.n, s.n[3], a), "q / k / v rope: weights do not fit one launch");
             a.x = (const float *) s.in[1];
@@ -1527,6 +1558,16 @@ void run_step(const ggml_backend * be, const Step & s) {
         }
         case S_GATE_UP: {
             const uint8_t * w[2] = {(const uint8_t *) s.in[0], (const uint8_t *) s.in[3]};
+            if (is_kquant(s.type)) {
+                RowKqArgs a{};
+                require(row_gemv_kq_ranges(s.type, 2, w, s.n, s.n[3], a), "gate / up: weights do not fit one launch");
+                a.x = (const float *) s.in[1];
+                a.norm_w = (const float *) s.in[2];
+                a.eps = s.f[0];
+                a.y = (float *) s.out;
+                launch_row_gemv_kq_epi(s.type, EPI_SWIGLU, a, st);
+                return;
+            }
             RowArgs a{};
             require(row_gemv_ranges(s.type, 2, w, s.n, s.n[3], a), "gate / up: weights do not fit one launch");
             a.x = (const float *) s.in[1];
@@ -1539,6 +1580,18 @@ void run_step(const ggml_backend * be, const Step & s) {
         case S_MULMAT3: {
             const int n = s.in[4] ? 3 : 2;
             const uint8_t * w[3] = {(const uint8_t *) s.in[0], (const uint8_t *) s.in[3], (const uint8_t *) s.in[4]};
+            if (is_kquant(s.type)) {
+                RowKqArgs a{};
+                require(row_gemv_kq_ranges(s.type, n, w, s.n, s.n[3], a), "mul_mat group: weights do not fit one launch");
+                a.x = (const float *) s.in[1];
+                a.norm_w = (const float *) s.in[2];
+                a.eps = s.f[0];
+                a.r_y[0] = (float *) s.out;
+                a.r_y[1] = (float *) s.out2[0];
+                a.r_y[2] = (float *) s.out2[1];
+                launch_row_gemv_kq_epi(s.type, EPI_STORE, a, st);
+                return;
+            }
             RowArgs a{};
             require(row_gemv_ranges(s.type, n, w, s.n, s.n[3], a), "mul_mat group: weights do not fit one launch");
             a.x = (const float *) s.in[1];

@@ -406,7 +406,8 @@ __global__ __launch_bounds__(1024) void k_row_gemv(const RowArgs a) {
                 if (gg < nqk) {
                     const int h = div_hd(gg), i = gg - h * half;
                     const float2 cs = gg == g_first ? cs_first : a.rope_cs[i];
-                    const float y0 = v[0] * cs.x - v[1] * cs.y, y1 = v[0] * cs.y + v[1] * cs.x;
+                    const float2 yr = rope_pair(v[0], v[1], cs);
+                    const float y0 = yr.x, y1 = yr.y;
                     if (h < a.H) {
                         a.y[h * a.D + i] = y0;
                         a.y[h * a.D + i + half] = y1;

@@ -34,17 +34,6 @@ namespace {
 constexpr int kRowKqMaxK = 16384;  // LDS holds the row's Q8_K codes, bsums and d
 constexpr uint32_t kKqPast = 0x80000000u;  // a buffer offset past every weight (sizes < 2 GB)
 
-struct RowKqArgs {
-    const uint8_t * w;  // ggml super-blocks [N][K / 256]
-    const float * x;    // the activation row [K]
-    float * y;          // [N]
-    const float * res;  // optional, y = res + W x
-    const float * norm_w;  // NORM: y = W (rms_norm(x) * norm_w) (ggml_rms_norm then ggml_mul)
-    float eps;
-    int N, ntask;       // ntask: 64-value chunks per row (K / 64)
-    int xc;             // the x waves take row groups too
-};
-
 template <int TYPE>
 struct RowKqFmt {
     static constexpr int WV = TYPE == T_Q5_K ? 4 : 2;                // 16-byte loads per task
@@ -52,9 +41,10 @@ struct RowKqFmt {
     static constexpr uint32_t QS = TYPE == T_Q5_K ? 48u : 16u;      // offset of the nibbles
 };
 
-template <int TYPE, int R, int NBL, bool NORM>
+template <int TYPE, int R, int NBL, bool NORM, int EPI, int MR>
 __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
 #pragma clang fp contract(off)
+    static_assert(EPI == EPI_STORE || R == 2, "row-pair epilogues take two rows per group");
     using F = RowKqFmt<TYPE>;
     constexpr int NWV = 16, WV = F::WV;
     constexpr bool XREG = NBL <= 2;                // the task activations in registers
@@ -73,8 +63,41 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
     const int K = ntask * 64, ngrp = K / 16;       // 16-value groups of the row
     const uint32_t row_bytes = (uint32_t) (ntask / 4) * F::SB;
     const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint8_t *>(a.w), 0, (int) ((size_t) a.N * row_bytes), 0x00020000);
+        const_cast<uint8_t *>(a.w), 0, MR > 1 ? (int) a.span : (int) ((size_t) a.N * row_bytes), 0x00020000);
     const int ng = (a.N + R - 1) / R;
+    // Row r of group gg (wave-uniform, in scalar registers): its weight k (returned) and its index
+    // there. One weight (EPI_STORE): rows in order. Several: EPI_STORE takes them in order over the
+    // ranges; EPI_ROPE_KV takes separate q, k, v weights, group g < (H + Hkv) D/2 being the rotation
+    // pair (i, i + D/2) of q head h (h < H) or k head h - H, then pairs of v rows; EPI_SWIGLU takes
+    // gate row g and up row g. Values per weight are picked with constant indices (a dynamic index
+    // into the kernel arguments becomes a memory load).
+    const int hd = a.D >> 1;
+    auto div_hd = [&](int x) -> int { return (int) __umulhi((uint32_t) x, a.hd_magic); };
+    auto range_of = [&](int row, int & local) -> int {
+        const bool k1 = a.nr > 1 && row >= a.r_end[0], k2 = a.nr > 2 && row >= a.r_end[1];
+        local = k2 ? row - a.r_end[1] : k1 ? row - a.r_end[0] : row;
+        return k2 ? 2 : k1 ? 1 : 0;
+    };
+    auto map_row = [&](int gg, int r, int & local) -> int {
+        gg = __builtin_amdgcn_readfirstlane(gg);
+        if constexpr (EPI == EPI_SWIGLU) {
+            local = min(gg, a.r_end[0] - 1);
+            return r;
+        } else if constexpr (EPI == EPI_ROPE_KV) {
+            const int nq = (a.H + a.Hkv) * hd;
+            const int gq = min(gg, nq - 1);
+            const int h = div_hd(gq), i = gq - h * hd;
+            const bool qh = h < a.H, vg = gg >= nq;
+            local = vg ? min(2 * (gg - nq) + r, a.Hkv * a.D - 1) : (qh ? h : h - a.H) * a.D + i + r * hd;
+            return vg ? 2 : qh ? 0 : 1;
+        } else if constexpr (MR > 1) {
+            return range_of(min(gg * R + r, a.N - 1), local);
+        } else {
+            local = min(gg * R + r, a.N - 1);
+            return 0;
+        }
+    };
+    auto pick_u = [](int k, const uint32_t (&v)[3]) { return k == 2 ? v[2] : k == 1 ? v[1] : v[0]; };
     const int XW = min(XWMAX, (K + 1023) / 1024);
     const int rounds = (ngrp + 64 * XW - 1) / (64 * XW);
     const bool XC = a.xc != 0;
@@ -99,15 +122,23 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
     uint32_t hw[NBL][R], hwn[NBL][R];
     auto load = [&](int gg, uint4 (&wv)[NBL][R][WV], uint32_t (&hv)[NBL][R]) {
         const bool live = gg < ng;
+        uint32_t rb[R];  // each row's byte offset, once per group
+        bool rin[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            int local;
+            const int k = map_row(gg, r, local);
+            rb[r] = (MR > 1 ? pick_u(k, a.r_off) : 0u) + (uint32_t) local * row_bytes;
+            rin[r] = live && (EPI != EPI_STORE || gg * R + r < a.N);
+        }
 #pragma unroll
         for (int i = 0; i < NBL; i++) {
             const int t = lane + 64 * i;
             const uint32_t sb = (uint32_t) (t >> 2);
 #pragma unroll
             for (int r = 0; r < R; r++) {
-                const int row = min(gg * R + r, a.N - 1);
-                const bool in = live && t < ntask && gg * R + r < a.N;
-                const uint32_t o = (uint32_t) row * row_bytes + sb * F::SB;
+                const bool in = rin[r] && t < ntask;
+                const uint32_t o = rb[r] + sb * F::SB;
                 const uint32_t offs[4] = {o + F::QS + 32u * (uint32_t) c, o + F::QS + 32u * (uint32_t) c + 16u, o + 16u,
                                           o + 32u};
                 hv[i][r] = __builtin_amdgcn_raw_buffer_load_b32(rq, in ? o + 4u * (uint32_t) c : kKqPast, 0, 0);
@@ -351,17 +382,62 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
                 acc[r] += __builtin_fmaf((float) isc * dd, ds, -fmin);
             }
         }
+        float v[R];
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            const float v = wave_sum(acc[r]);
-            const int row = __builtin_amdgcn_readfirstlane(gg * R + r);
-            // the residual read through the scalar unit (a constant-space pointer): a vector load
-            // here would wait for every weight load issued before it (the next groups'), as loads
-            // complete in order. Each residual value is read before its own output is written and
-            // never after another output (res may be y itself).
-            typedef const float __attribute__((address_space(4))) cfloat_t;
-            const float rv = a.res && row < a.N ? ((cfloat_t *) a.res)[row] : 0.0f;
-            if (lane == r && row < a.N) a.y[row] = a.res ? v + rv : v;
+        for (int r = 0; r < R; r++) v[r] = wave_sum(acc[r]);
+        // What the epilogues read (residual, position, rotation) comes through the scalar unit
+        // (constant-space pointers): a vector load here would wait for every weight load issued
+        // before it (the next groups'), as loads complete in order.
+        typedef const float __attribute__((address_space(4))) cfloat_t;
+        gg = __builtin_amdgcn_readfirstlane(gg);
+        if constexpr (EPI == EPI_STORE && MR > 1) {
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const int row = gg * R + r;
+                if (lane == r && row < a.N) {
+                    int local;
+                    const int k = range_of(row, local);
+                    float * y = k == 2 ? a.r_y[2] : k == 1 ? a.r_y[1] : a.r_y[0];
+                    y[local] = v[r];
+                }
+            }
+        } else if constexpr (EPI == EPI_STORE) {
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const int row = gg * R + r;
+                // each residual value is read before its own output is written and never after
+                // another output (res may be y itself)
+                const float rv = a.res && row < a.N ? ((cfloat_t *) a.res)[row] : 0.0f;
+                if (lane == r && row < a.N) a.y[row] = a.res ? v[r] + rv : v[r];
+            }
+        } else if constexpr (EPI == EPI_SWIGLU) {  // k_swiglu's arithmetic: g / (1 + e^-g) * u
+            if (lane == 0) a.y[gg] = v[0] / (1.0f + expf(-v[0])) * v[1];
+        } else {  // EPI_ROPE_KV: q roped to y, k roped and v to the f16 caches at the position
+            typedef const int __attribute__((address_space(4))) cint_t;
+            const int p = ((cint_t *) a.pos)[0];
+            const int nqk = (a.H + a.Hkv) * hd;
+            if (p >= 0 && p < a.ctx) {
+                if (gg < nqk) {
+                    const int h = div_hd(gg), i = gg - h * hd;
+                    const cfloat_t * cs = (cfloat_t *) a.rope_cs + 2 * i;
+                    const float2 yr = rope_pair(v[0], v[1], make_float2(cs[0], cs[1]));
+                    if (lane == 0) {
+                        if (h < a.H) {
+                            a.y[h * a.D + i] = yr.x;
+                            a.y[h * a.D + i + hd] = yr.y;
+                        } else {
+                            uint16_t * kr = a.kc + ((int64_t) (h - a.H) * a.ctx + p) * a.D;
+                            kr[i] = f2h(yr.x);
+                            kr[i + hd] = f2h(yr.y);
+                        }
+                    }
+                } else if (lane == 0) {
+                    const int e = 2 * (gg - nqk);  // v value index over [Hkv][D]
+                    const int hv = div_hd(e) >> 1, dd = e - hv * a.D;
+                    const uint32_t pair = f2h(v[0]) | ((uint32_t) f2h(v[1]) << 16);
+                    *reinterpret_cast<uint32_t *>(a.vc + ((int64_t) hv * a.ctx + p) * a.D + dd) = pair;
+                }
+            }
         }
     };
 
@@ -385,35 +461,119 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
     }
 }
 
-template <int TYPE, int R, bool NORM>
-void go_kq(int nbl, const RowKqArgs & a, int grid, hipStream_t s) {
-    if (nbl == 1) k_row_gemv_kq<TYPE, R, 1, NORM><<<grid, 1024, 0, s>>>(a);
-    else if (R == 1) k_row_gemv_kq<TYPE, 1, 2, NORM><<<grid, 1024, 0, s>>>(a);
-    else fail("row gemv kq: two rows per group need rows of at most 64 chunks");
+template <int TYPE, bool NORM, int EPI, int MR>
+void go_kq(int R, int nbl, const RowKqArgs & a, int grid, hipStream_t s) {
+    if (R == 2 && nbl == 1) {
+        k_row_gemv_kq<TYPE, 2, 1, NORM, EPI, MR><<<grid, 1024, 0, s>>>(a);
+        return;
+    }
+    if constexpr (EPI == EPI_STORE) {
+        if (R == 1 && nbl == 1) return (void) k_row_gemv_kq<TYPE, 1, 1, NORM, EPI, MR><<<grid, 1024, 0, s>>>(a);
+        if (R == 1 && nbl == 2) return (void) k_row_gemv_kq<TYPE, 1, 2, NORM, EPI, MR><<<grid, 1024, 0, s>>>(a);
+    }
+    fail("row gemv kq: two rows per group need rows of at most 64 chunks");
 }
 
-template <int TYPE, bool NORM>
-void go_kq_r(int R, int nbl, const RowKqArgs & a, int grid, hipStream_t s) {
-    if (R == 2) go_kq<TYPE, 2, NORM>(nbl, a, grid, s);
-    else go_kq<TYPE, 1, NORM>(nbl, a, grid, s);
+template <int TYPE>
+void go_kq_t(int epi, bool norm, bool multi, int R, int nbl, const RowKqArgs & a, int grid, hipStream_t s) {
+    if (epi == EPI_ROPE_KV) return go_kq<TYPE, true, EPI_ROPE_KV, 3>(R, nbl, a, grid, s);
+    if (epi == EPI_SWIGLU) return go_kq<TYPE, true, EPI_SWIGLU, 3>(R, nbl, a, grid, s);
+    if (multi) return go_kq<TYPE, true, EPI_STORE, 3>(R, nbl, a, grid, s);
+    if (norm) return go_kq<TYPE, true, EPI_STORE, 1>(R, nbl, a, grid, s);
+    go_kq<TYPE, false, EPI_STORE, 1>(R, nbl, a, grid, s);
 }
+
+bool kq_rows_fit(int type, int64_t K) {
+    return (type == T_Q4_K || type == T_Q5_K) && K > 0 && K % QKK == 0 && K <= 8192;
+}
+
+uint32_t kq_row_bytes(int type, int64_t K) { return (uint32_t) (K / QKK) * (type == T_Q5_K ? 176u : 144u); }
 
 }  // namespace
 
 bool row_gemv_kq_fits(int type, int64_t N, int64_t K) {
-    if (type != T_Q4_K && type != T_Q5_K) return false;
     // longer rows spill registers; more rows stream faster through the batched kernel after a
     // separate quantization (measured at 4096 x 28672: 15.8 against 18.5 us)
-    if (K <= 0 || K % QKK != 0 || K > 8192 || N <= 0 || N > 8192) return false;
-    const uint64_t row = (uint64_t) (K / QKK) * (type == T_Q5_K ? 176u : 144u);
-    return (uint64_t) N * row < 0x80000000ull;
+    if (!kq_rows_fit(type, K) || N <= 0 || N > 8192) return false;
+    return (uint64_t) N * kq_row_bytes(type, K) < 0x80000000ull;
 }
 
 // With the rms_norm prologue (a normalized row read by several projections, each normalizing it
 // itself): up to 16384 rows, where it also saves the norm's and the quantization's launches.
 bool row_gemv_kq_norm_fits(int type, int64_t N, int64_t K) {
-    return row_gemv_kq_fits(type, std::min<int64_t>(N, 8192), K) && N <= 16384 &&
-           (uint64_t) N * (uint64_t) (K / QKK) * (type == T_Q5_K ? 176u : 144u) < 0x80000000ull;
+    return kq_rows_fit(type, K) && N > 0 && N <= 16384 && (uint64_t) N * kq_row_bytes(type, K) < 0x80000000ull;
+}
+
+bool row_gemv_kq_epi_fits(int type, int epi, int64_t K) {
+    return kq_rows_fit(type, K) && (epi == EPI_STORE || K <= 4096);
+}
+
+bool row_gemv_kq_ranges(int type, int n, const uint8_t * const * w, const int64_t * N, int64_t K, RowKqArgs & a) {
+    if (n < 1 || n > 3 || !kq_rows_fit(type, K)) return false;
+    uintptr_t lo = UINTPTR_MAX;
+    int64_t total = 0;
+    for (int k = 0; k < n; k++) {
+        if (N[k] <= 0) return false;
+        lo = std::min(lo, (uintptr_t) w[k]);
+        total += N[k];
+    }
+    const uint64_t rb = kq_row_bytes(type, K);
+    uint64_t span = 0;
+    for (int k = 0; k < n; k++) {
+        a.r_off[k] = (uint32_t) ((uintptr_t) w[k] - lo);
+        span = std::max(span, (uint64_t) ((uintptr_t) w[k] - lo) + (uint64_t) N[k] * rb);
+        a.r_end[k] = (int) ((k ? a.r_end[k - 1] : 0) + N[k]);
+    }
+    if (span >= 0x80000000ull || total > INT32_MAX) return false;
+    a.nr = n;
+    a.w = (const uint8_t *) lo;
+    a.N = (int) total;
+    a.ntask = (int) (K / 64);
+    a.span = (uint32_t) span;
+    return true;
+}
+
+// The launch behind every K-quant row GEMV: one weight (EPI_STORE, optional residual, optional
+// norm) or several of one row length read by the one normalized row (EPI_STORE to r_y, or the
+// row-pair epilogues).
+void launch_row_gemv_kq_epi(int type, int epi, const RowKqArgs & a0, hipStream_t s) {
+    RowKqArgs a = a0;
+    const int64_t K = (int64_t) a.ntask * 64;
+    require(row_gemv_kq_epi_fits(type, epi, K),
+            "row gemv kq: Q4_K / Q5_K, K a multiple of 256 up to 8192 (4096 for the row-pair epilogues)");
+    const bool multi = a.nr > 1;
+    require(multi ? (uint64_t) a.span < 0x80000000ull && a.r_end[a.nr - 1] == a.N
+                  : a.N > 0 && (uint64_t) a.N * kq_row_bytes(type, K) < 0x80000000ull,
+            "row gemv kq: weights of 2 GB or more");
+    require(!multi || a.norm_w, "row gemv kq: several weights take the rms_norm prologue");
+    require(epi == EPI_STORE || a.N % 2 == 0, "row gemv kq: row-pair epilogue needs an even row count");
+    require(epi == EPI_STORE ||
+                (epi == EPI_ROPE_KV && a.nr == 3 && a.D % 2 == 0 && a.D > 0 && a.r_end[0] == a.H * a.D &&
+                 a.r_end[1] == (a.H + a.Hkv) * a.D && a.r_end[2] == (a.H + 2 * a.Hkv) * a.D) ||
+                (epi == EPI_SWIGLU && a.nr == 2 && a.r_end[1] == 2 * a.r_end[0]),
+            "row gemv kq: separate q / k / v weights of H*D, Hkv*D, Hkv*D rows, or gate / up weights of equal rows");
+    require(!multi || !a.res, "row gemv kq: several weights take no residual");
+    if (epi == EPI_ROPE_KV) {
+        const uint64_t hd = (uint64_t) (a.D / 2);
+        require((uint64_t) a.N * hd < (1ull << 32), "row gemv kq: rope epilogue indices past 2^32 / (D/2)");
+        a.hd_magic = (uint32_t) ((1ull << 32) / hd + 1);
+    }
+    const int nbl = (a.ntask + 63) / 64;
+    const int cus = cu_count();
+    const int xw = std::min(4, (int) ((K + 1023) / 1024));
+    // two rows per group when every compute wavefront of the grid gets one and the rows are short
+    // (Q5_K's tasks hold twice the registers: one row, whose next group's weights are prefetched);
+    // the row-pair epilogues always take two
+    const int R = epi != EPI_STORE || (type == T_Q4_K && nbl == 1 && a.N / 2 >= (int64_t) cus * (16 - xw)) ? 2 : 1;
+    const int64_t ng = (a.N + R - 1) / R;
+    // the x waves take groups too for long rows, or when the compute wavefronts alone would need
+    // one more round
+    a.xc = nbl > 4 || (ng <= 16LL * cus && ng > (int64_t) (16 - xw) * cus);
+    const int cw = a.xc ? 16 : 16 - xw;
+    const int grid = (int) std::max<int64_t>(1, std::min<int64_t>(cus, (ng + cw - 1) / cw));
+    if (type == T_Q4_K) go_kq_t<T_Q4_K>(epi, a.norm_w != nullptr, multi, R, nbl, a, grid, s);
+    else go_kq_t<T_Q5_K>(epi, a.norm_w != nullptr, multi, R, nbl, a, grid, s);
+    check_launch("row gemv kq");
 }
 
 // y[n] (+ res[n]) = sum_k W[n, k] x'[k] for a Q4_K / Q5_K weight in ggml's super-block layout, x' = x
@@ -431,26 +591,7 @@ void launch_row_gemv_kq(int type, const void * w, int64_t N, int64_t K, const fl
     a.eps = eps;
     a.N = (int) N;
     a.ntask = (int) (K / 64);
-    const int nbl = (a.ntask + 63) / 64;
-    const int cus = cu_count();
-    const int xw = std::min(4, (int) ((K + 1023) / 1024));
-    // two rows per group when every compute wavefront of the grid gets one and the rows are short
-    // (Q5_K's tasks hold twice the registers: one row, whose next group's weights are prefetched)
-    const int R = type == T_Q4_K && nbl == 1 && N / 2 >= (int64_t) cus * (16 - xw) ? 2 : 1;
-    const int64_t ng = (N + R - 1) / R;
-    // the x waves take groups too for long rows, or when the compute wavefronts alone would need
-    // one more round
-    a.xc = nbl > 4 || (ng <= 16LL * cus && ng > (int64_t) (16 - xw) * cus);
-    const int cw = a.xc ? 16 : 16 - xw;
-    const int grid = (int) std::max<int64_t>(1, std::min<int64_t>(cus, (ng + cw - 1) / cw));
-    if (type == T_Q4_K) {
-        if (norm_w) go_kq_r<T_Q4_K, true>(R, nbl, a, grid, s);
-        else go_kq_r<T_Q4_K, false>(R, nbl, a, grid, s);
-    } else {
-        if (norm_w) go_kq_r<T_Q5_K, true>(R, nbl, a, grid, s);
-        else go_kq_r<T_Q5_K, false>(R, nbl, a, grid, s);
-    }
-    check_launch("row gemv kq");
+    launch_row_gemv_kq_epi(type, EPI_STORE, a, s);
 }
 
 }  // namespace gcq
