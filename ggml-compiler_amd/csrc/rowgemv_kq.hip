@@ -49,14 +49,16 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
     constexpr int NWV = 16, WV = F::WV;
     constexpr bool XREG = NBL <= 2;                // the task activations in registers
     constexpr bool PF = WV * NBL * R <= 4;         // the next group's weights prefetched
-    // x waves: at most 4; rounds of 16 values per x thread: K / 16 groups over 64 XW threads,
-    // NBL at most (a row of NBL * 64 chunks of 64)
-    constexpr int XWMAX = 4, RMAX = NBL;
-    __shared__ int4 lc[kRowKqMaxK / 16];           // codes, 16 per entry
-    __shared__ int16_t lbs[kRowKqMaxK / 16];       // bsums of 16
+    // x waves: at most 4 (8 for rows past 8192 values); rounds of 16 values per x thread: K / 16
+    // groups over 64 XW threads, NBL at most (a row of NBL * 64 chunks of 64), half that with 8
+    constexpr int XWMAX = NBL > 2 ? 8 : 4, RMAX = NBL > 2 ? (NBL + 1) / 2 : NBL;
+    // codes, 16 per entry: 16-value group j of task t at j * ntask + t, so that a wavefront's
+    // lanes (consecutive tasks) read consecutive entries (no bank conflicts)
+    __shared__ int4 lc[kRowKqMaxK / 16];
+    __shared__ uint32_t lbp[kRowKqMaxK / 64];      // per task: bsums of groups 0 + 1, 2 + 3 (int16 each)
     __shared__ float ld[kRowKqMaxK / 256];         // d per super-block
     __shared__ unsigned int s_flag, s_norm;        // x waves done with: their codes; their norm partials
-    __shared__ double red[4];
+    __shared__ double red[XWMAX];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int ntask = a.ntask;
@@ -122,6 +124,10 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
     uint32_t hw[NBL][R], hwn[NBL][R];
     auto load = [&](int gg, uint4 (&wv)[NBL][R][WV], uint32_t (&hv)[NBL][R]) {
         const bool live = gg < ng;
+        // long rows: the tasks' offsets recomputed per group from an opaque lane index (held
+        // across the groups they would spill)
+        int ln = lane;
+        if constexpr (!XREG) asm volatile("" : "+v"(ln));
         uint32_t rb[R];  // each row's byte offset, once per group
         bool rin[R];
 #pragma unroll
@@ -133,7 +139,7 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
         }
 #pragma unroll
         for (int i = 0; i < NBL; i++) {
-            const int t = lane + 64 * i;
+            const int t = ln + 64 * i;
             const uint32_t sb = (uint32_t) (t >> 2);
 #pragma unroll
             for (int r = 0; r < R; r++) {
@@ -259,16 +265,18 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
 #pragma unroll
                 for (int j = 0; j < 16; j++) q[j] = 0;
             }
+            int s = 0;
+#pragma unroll
+            for (int j = 0; j < 16; j++) s += q[j];
+            const int sp = s + lane_pair_i<1>(s);  // with the neighbouring group's (gi ^ 1)
             if (gi < ngrp) {
-                int pk[4], s = 0;
+                int pk[4];
 #pragma unroll
                 for (int k = 0; k < 4; k++)
                     pk[k] = (q[4 * k] & 0xff) | ((q[4 * k + 1] & 0xff) << 8) | ((q[4 * k + 2] & 0xff) << 16) |
                             ((q[4 * k + 3] & 0xff) << 24);
-#pragma unroll
-                for (int j = 0; j < 16; j++) s += q[j];
-                lc[gi] = make_int4(pk[0], pk[1], pk[2], pk[3]);
-                lbs[gi] = (int16_t) s;
+                lc[(gi & 3) * ntask + (gi >> 2)] = make_int4(pk[0], pk[1], pk[2], pk[3]);
+                if ((gi & 1) == 0) reinterpret_cast<int16_t *>(lbp)[2 * (gi >> 2) + ((gi >> 1) & 1)] = (int16_t) sp;
                 if ((lane & 15) == 0) ld[gi >> 4] = d;
             }
             __builtin_amdgcn_sched_barrier(0);  // one round at a time (its codes are 16 registers)
@@ -288,16 +296,25 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
     int4 xa[XREG ? NBL : 1][2], xb[XREG ? NBL : 1][2];
     float xs[XREG ? NBL : 1], xo[XREG ? NBL : 1], xo2[XREG ? NBL : 1];
     auto act = [&](int i, int4 (&ca)[2], int4 (&cb)[2], float & ds, float & o1, float & o2) {
-        const int t = lane + 64 * i;
-        if (t < ntask) {
-            const int sb = t >> 2, e = 16 * sb + 4 * c;  // 16-value groups: e, e + 1 (2c), e + 2, e + 3 (2c + 1)
-            ca[0] = lc[e];
-            ca[1] = lc[e + 1];
-            cb[0] = lc[e + 2];
-            cb[1] = lc[e + 3];
-            ds = ld[sb];
-            o1 = (float) ((int) lbs[e] + (int) lbs[e + 1]) * ds;
-            o2 = (float) ((int) lbs[e + 2] + (int) lbs[e + 3]) * ds;
+        int t = lane + 64 * i;
+        // read from LDS once per group: an opaque index keeps the compiler from holding every
+        // task's activations in registers across the groups (they would spill)
+        if constexpr (!XREG) {
+            asm volatile("" : "+v"(t));
+            // past the row: a task of the row read instead, whose products with the zero weights
+            // (and zero header: d = dmin = 0) add exact zeros
+            t = min(t, ntask - 1);
+        }
+        if (!XREG || t < ntask) {
+            // the task's 16-value groups 0, 1 (sub-block 2c) and 2, 3 (2c + 1)
+            ca[0] = lc[t];
+            ca[1] = lc[ntask + t];
+            cb[0] = lc[2 * ntask + t];
+            cb[1] = lc[3 * ntask + t];
+            ds = ld[t >> 2];
+            const uint32_t bp = lbp[t];
+            o1 = (float) (int) (int16_t) (bp & 0xffffu) * ds;
+            o2 = (float) (int) (int16_t) (bp >> 16) * ds;
         } else {
             ca[0] = make_int4(0, 0, 0, 0);
             ca[1] = ca[0];
@@ -381,6 +398,8 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
                 const float fmin = __builtin_fmaf(fm0, o1, fm1 * o2);
                 acc[r] += __builtin_fmaf((float) isc * dd, ds, -fmin);
             }
+            // one task's activations in registers at a time
+            if constexpr (!XREG) __builtin_amdgcn_sched_barrier(0);
         }
         float v[R];
 #pragma unroll
@@ -470,6 +489,10 @@ void go_kq(int R, int nbl, const RowKqArgs & a, int grid, hipStream_t s) {
     if constexpr (EPI == EPI_STORE) {
         if (R == 1 && nbl == 1) return (void) k_row_gemv_kq<TYPE, 1, 1, NORM, EPI, MR><<<grid, 1024, 0, s>>>(a);
         if (R == 1 && nbl == 2) return (void) k_row_gemv_kq<TYPE, 1, 2, NORM, EPI, MR><<<grid, 1024, 0, s>>>(a);
+        if constexpr (MR == 1 && TYPE == T_Q4_K) {  // rows past 8192 values: one Q4_K weight
+            if (R == 1 && nbl == 3) return (void) k_row_gemv_kq<TYPE, 1, 3, NORM, EPI, MR><<<grid, 1024, 0, s>>>(a);
+            if (R == 1 && nbl == 4) return (void) k_row_gemv_kq<TYPE, 1, 4, NORM, EPI, MR><<<grid, 1024, 0, s>>>(a);
+        }
     }
     fail("row gemv kq: two rows per group need rows of at most 64 chunks");
 }
@@ -484,7 +507,9 @@ void go_kq_t(int epi, bool norm, bool multi, int R, int nbl, const RowKqArgs & a
 }
 
 bool kq_rows_fit(int type, int64_t K) {
-    return (type == T_Q4_K || type == T_Q5_K) && K > 0 && K % QKK == 0 && K <= 8192;
+    // Q4_K rows up to 16384 values (the LDS row); Q5_K's tasks hold twice the weight registers,
+    // and rows past 8192 values would spill
+    return (type == T_Q4_K || type == T_Q5_K) && K > 0 && K % QKK == 0 && K <= (type == T_Q4_K ? kRowKqMaxK : 8192);
 }
 
 uint32_t kq_row_bytes(int type, int64_t K) { return (uint32_t) (K / QKK) * (type == T_Q5_K ? 176u : 144u); }
@@ -509,7 +534,7 @@ bool row_gemv_kq_epi_fits(int type, int epi, int64_t K) {
 }
 
 bool row_gemv_kq_ranges(int type, int n, const uint8_t * const * w, const int64_t * N, int64_t K, RowKqArgs & a) {
-    if (n < 1 || n > 3 || !kq_rows_fit(type, K)) return false;
+    if (n < 1 || n > 3 || !kq_rows_fit(type, K) || K > 8192) return false;  // several weights: rows of 8192 at most
     uintptr_t lo = UINTPTR_MAX;
     int64_t total = 0;
     for (int k = 0; k < n; k++) {
@@ -540,12 +565,13 @@ void launch_row_gemv_kq_epi(int type, int epi, const RowKqArgs & a0, hipStream_t
     RowKqArgs a = a0;
     const int64_t K = (int64_t) a.ntask * 64;
     require(row_gemv_kq_epi_fits(type, epi, K),
-            "row gemv kq: Q4_K / Q5_K, K a multiple of 256 up to 8192 (4096 for the row-pair epilogues)");
+            "row gemv kq: Q4_K / Q5_K, K a multiple of 256 up to 8192 (Q4_K 16384; 4096 for the row-pair epilogues)");
     const bool multi = a.nr > 1;
     require(multi ? (uint64_t) a.span < 0x80000000ull && a.r_end[a.nr - 1] == a.N
                   : a.N > 0 && (uint64_t) a.N * kq_row_bytes(type, K) < 0x80000000ull,
             "row gemv kq: weights of 2 GB or more");
     require(!multi || a.norm_w, "row gemv kq: several weights take the rms_norm prologue");
+    require(!multi || K <= 8192, "row gemv kq: several weights take rows of at most 8192 values");
     require(epi == EPI_STORE || a.N % 2 == 0, "row gemv kq: row-pair epilogue needs an even row count");
     require(epi == EPI_STORE ||
                 (epi == EPI_ROPE_KV && a.nr == 3 && a.D % 2 == 0 && a.D > 0 && a.r_end[0] == a.H * a.D &&
@@ -560,7 +586,7 @@ void launch_row_gemv_kq_epi(int type, int epi, const RowKqArgs & a0, hipStream_t
     }
     const int nbl = (a.ntask + 63) / 64;
     const int cus = cu_count();
-    const int xw = std::min(4, (int) ((K + 1023) / 1024));
+    const int xw = std::min(nbl > 2 ? 8 : 4, (int) ((K + 1023) / 1024));  // the kernel's XW
     // two rows per group when every compute wavefront of the grid gets one and the rows are short
     // (Q5_K's tasks hold twice the registers: one row, whose next group's weights are prefetched);
     // the row-pair epilogues always take two
@@ -581,7 +607,7 @@ void launch_row_gemv_kq_epi(int type, int epi, const RowKqArgs & a0, hipStream_t
 void launch_row_gemv_kq(int type, const void * w, int64_t N, int64_t K, const float * x, const float * norm_w, float eps,
                         float * y, const float * res, hipStream_t s) {
     require(norm_w ? row_gemv_kq_norm_fits(type, N, K) : row_gemv_kq_fits(type, N, K),
-            "row gemv kq: Q4_K / Q5_K, K a multiple of 256 up to 8192, up to 8192 rows (16384 with the norm)");
+            "row gemv kq: Q4_K / Q5_K, K a multiple of 256 up to 8192 (Q4_K 16384), up to 8192 rows (16384 with the norm)");
     RowKqArgs a{};
     a.w = (const uint8_t *) w;
     a.x = x;
