@@ -116,6 +116,12 @@ WeightLayout weight_layout(int type, int64_t nrows, int64_t k) {
         L.qs = 0;
         L.d = align256(nb * 208);
         L.total = L.d + align256(nb * 2);
+    } else if (type == T_Q4_K || type == T_Q5_K) {
+        const KqRegions R = kq_regions(type, nrows * (k / QKK));
+        L.qs = R.qs;
+        L.qh = R.qh;
+        L.d = R.hdr;
+        L.total = R.total;
     } else {
         L.total = align256(row_bytes(type, k) * (size_t) nrows);
     }
@@ -294,7 +300,7 @@ int gcq_pack_weights(int type, const void * src, int64_t nrows, int64_t n_per_ro
         need_weight_type(type);
         need_k(type, n_per_row);
         need_dims(nrows, "nrows", 1, INT32_MAX);
-        need_ptr(src, "src");
+        need_ptr(src, "src", type == T_Q4_K || type == T_Q5_K ? 16 : 1);  // K-quants move 16-byte pieces
         need_ptr(dst, "dst", 16);
         launch_pack(type, src, nrows, n_per_row, dst, as_stream(stream));
     });

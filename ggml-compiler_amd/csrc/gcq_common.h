@@ -8,7 +8,10 @@
 //      Q4_0: nibbles [N][K/32][16 B], then fp16 scales [N][K/32]. Byte j of a block's 16 holds
 //            element j (low nibble) and j+16 (high nibble), stored code = q + 8, as in ggml.
 //      Q8_0: codes [N][K/32][32 B], then fp16 scales [N][K/32].
-//      Q4_K, Q5_K: ggml's 144- / 176-byte super-blocks unchanged (16-byte aligned rows).
+//      Q4_K, Q5_K: ggml's 144- / 176-byte super-blocks split by field: nibbles (qs[128])
+//            [N][K/256][128 B], then (Q5_K) the fifth bits (qh[32]) [N][K/256][32 B], then the
+//            headers {d, dmin, scales[12]} [N][K/256][16 B], each field's bytes in ggml's order, so
+//            that consecutive lanes read consecutive 16-byte pieces of the nibbles.
 //      Q6_K: ggml's 210-byte super-block split: {ql[128], qh[64], scales[16]} [N][K/256][208 B],
 //            then fp16 d [N][K/256] (the 208 bytes in ggml's order, so loads stay 16-byte aligned).
 //  * Quantized activations ("act"), rows of the batch b < B:
@@ -77,7 +80,18 @@ size_t row_bytes(int type, int64_t n);
 // Byte offsets inside a packed weight and a quantized activation buffer.
 struct WeightLayout {
     size_t qs = 0, d = 0, total = 0;
+    size_t qh = 0;  // Q5_K: the fifth bits (Q4_K / Q5_K: d is the headers' region)
 };
+// The packed Q4_K / Q5_K regions of nb super-blocks, byte offsets from the weight: nibbles
+// [nb][128], Q5_K's fifth bits [nb][32], headers (d, dmin, scales[12]) [nb][16].
+struct KqRegions {
+    size_t qs, qh, hdr, total;
+};
+__host__ __device__ inline KqRegions kq_regions(int type, int64_t nb) {
+    const size_t q = align256((size_t) nb * 128);
+    const size_t h = type == T_Q5_K ? q + align256((size_t) nb * 32) : q;
+    return {0, q, h, h + align256((size_t) nb * 16)};
+}
 WeightLayout weight_layout(int type, int64_t nrows, int64_t k);
 struct ActLayout {
     size_t codes = 0, meta = 0, d = 0, total = 0;
@@ -168,20 +182,21 @@ bool row_gemv_ranges(int type, int n, const uint8_t * const * w, const int64_t *
 // The K-quant decode-row GEMV (rowgemv_kq.hip): a Q4_K / Q5_K weight in ggml's super-block layout
 // times one f32 row, quantized to Q8_K (optionally rms-normalized first) inside the launch.
 struct RowKqArgs {
-    const uint8_t * w;     // super-blocks [N][K / 256]; several weights: the lowest of them
+    const uint8_t * w;     // the packed weight; several weights: the lowest of them
     const float * x;       // the activation row [K]
     float * y;             // EPI_STORE [N], EPI_SWIGLU [N/2], EPI_ROPE_KV: roped q [H*D]
     const float * res;     // EPI_STORE with one weight, optional: y = res + W x
     const float * norm_w;  // y = W (rms_norm(x) * norm_w) (ggml_rms_norm then ggml_mul)
     float eps;
-    int N, ntask;          // rows (of all weights), 64-value chunks per row (K / 64)
+    int N, ntask;          // rows (of all weights), 32-value tasks per row (K / 32)
     int xc;                // set by the launch: the x waves take row groups too
-    // Several weights of one row length read by the same row: rows [r_end[k-1], r_end[k]) are
-    // weight k's, at byte offset r_off[k] from w (the weights span `span` bytes, < 2 GB); EPI_STORE
-    // writes weight k's results to r_y[k]. Row pairs as RowArgs' (q / k / v rope, gate / up).
-    int nr;  // 0: one weight
+    // Weight k's nibbles, fifth bits (Q5_K) and headers at byte offsets r_qs[k], r_qh[k], r_hdr[k]
+    // from w, the weights spanning `span` bytes (< 2 GB). Several weights of one row length read by
+    // the same row: rows [r_end[k-1], r_end[k]) are weight k's; EPI_STORE writes weight k's results
+    // to r_y[k]. Row pairs as RowArgs' (q / k / v rope, gate / up).
+    int nr;  // 0 or 1: one weight
     int r_end[3];
-    uint32_t r_off[3], span;
+    uint32_t r_qs[3], r_qh[3], r_hdr[3], span;
     float * r_y[3];
     // EPI_ROPE_KV: the position, its (cos, sin) table, the f16 caches [Hkv][ctx][D]
     const int * pos;
@@ -706,12 +721,12 @@ __device__ __forceinline__ float kquant_table_value(int type, const uint8_t * ta
         const int sc = (int) reinterpret_cast<const int8_t *>(b + 192 + 8 * h)[l / 16 + 2 * qq];
         return __fmul_rn(__fmul_rn(h2f(dv[bi]), (float) sc), (float) q);
     }
-    const int bb = type == T_Q4_K ? 144 : 176, qs = type == T_Q4_K ? 16 : 48;
-    const uint8_t * b = tab + bi * bb;
+    const KqRegions R = kq_regions(type, nrows * nsb);
+    const uint8_t * b = tab + R.hdr + bi * 16;  // the header: d, dmin, scales[12]
     const int cc = w / 64, hi = (w % 64) >= 32, l = w % 32, j = 2 * cc + hi;  // sub-block j, value l
-    const int x = byte(b, qs + 32 * cc + l);
+    const int x = byte(tab + R.qs + bi * 128, 32 * cc + l);
     int q = hi ? x >> 4 : x & 0xF;
-    if (type == T_Q5_K) q += ((byte(b, 16 + l) >> j) & 1) << 4;
+    if (type == T_Q5_K) q += ((byte(tab + R.qh + bi * 32, l) >> j) & 1) << 4;
     int sc, m;  // get_scale_min_k4 on the 12 scale bytes at 4
     if (j < 4) {
         sc = byte(b, 4 + j) & 63;
@@ -724,8 +739,8 @@ __device__ __forceinline__ float kquant_table_value(int type, const uint8_t * ta
     return __fsub_rn(__fmul_rn(__fmul_rn(d, (float) sc), (float) q), __fmul_rn(dmin, (float) m));
 }
 
-// Element c of row r of a get_rows table (F32, F16, packed Q4_0 / Q8_0 / Q6_K or ggml Q4_K / Q5_K
-// of nrows x D); NaN for a row outside the table.
+// Element c of row r of a get_rows table (F32, F16, packed Q4_0 / Q8_0 / Q4_K / Q5_K / Q6_K of
+// nrows x D); NaN for a row outside the table.
 __device__ __forceinline__ float table_value(int type, const uint8_t * tab, int64_t nrows, int D, int64_t r, int c) {
     if (r < 0 || r >= nrows) return __builtin_nanf("");
     if (type == T_F32) return reinterpret_cast<const float *>(tab)[r * D + c];

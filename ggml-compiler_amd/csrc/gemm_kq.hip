@@ -40,7 +40,7 @@ constexpr int KP = HV + 16;        // LDS row pitch of the codes (bytes; 16 B pa
 
 template <int TYPE>
 struct Kq {
-    static constexpr int BB = TYPE == T_Q4_K ? 144 : TYPE == T_Q5_K ? 176 : 208;  // device block bytes
+    static constexpr int BB = TYPE == T_Q4_K || TYPE == T_Q5_K ? 128 : 208;  // device block bytes (nibbles / Q6_K's)
     static constexpr bool MIN = TYPE != T_Q6_K;  // a min term (Q4_K / Q5_K)
     static constexpr int NSUB = TYPE == T_Q6_K ? 16 : 8;  // scales per super-block
 };
@@ -78,8 +78,10 @@ __device__ __forceinline__ void scale_min(const uint32_t (&q)[3], int j, int & s
 
 template <int TYPE>
 struct KqArgs {
-    const uint8_t * w;      // packed weight: [N][nsb] blocks of Kq::BB bytes
+    const uint8_t * w;      // packed weight: [N][nsb] blocks of Kq::BB bytes (Q4_K / Q5_K: the nibbles)
     const uint16_t * wd;    // Q6_K: fp16 d [N][nsb]
+    const uint8_t * wqh;    // Q5_K: the fifth bits [N][nsb][32]
+    const uint8_t * whdr;   // Q4_K / Q5_K: the headers (d, dmin, scales[12]) [N][nsb][16]
     const int8_t * xc;      // Q8_K codes [M][K]
     const int16_t * xbs;    // block sums [M][K / 16]
     const float * xd;       // d [M][K / 256]
@@ -112,15 +114,15 @@ __device__ __forceinline__ void kq_load(KqStage<TYPE> & st, const KqArgs<TYPE> &
     } else if (t < 4 * TN) {
         // row t / 4, u = t % 4: 16 B of nibbles (and Q5_K the matching 16 B of qh)
         const int row = t >> 2, u = t & 3;
-        const int qs = TYPE == T_Q4_K ? 16 : 48;
-        const uint8_t * b0 = a.w + ((size_t) min(n0 + row, a.N - 1) * a.nsb + sb) * Kq<TYPE>::BB;
-        st.b = *reinterpret_cast<const v4i *>(b0 + qs + 64 * h + 16 * u);
-        if constexpr (TYPE == T_Q5_K) st.b2 = *reinterpret_cast<const v4i *>(b0 + 16 + 16 * (u & 1));
+        const size_t bi = (size_t) min(n0 + row, a.N - 1) * a.nsb + sb;
+        st.b = *reinterpret_cast<const v4i *>(a.w + bi * 128 + 64 * h + 16 * u);
+        if constexpr (TYPE == T_Q5_K) st.b2 = *reinterpret_cast<const v4i *>(a.wqh + bi * 32 + 16 * (u & 1));
     }
     if (h == 0) {
         if (t < TN) {
             const size_t bi = (size_t) min(n0 + t, a.N - 1) * a.nsb + sb;
-            st.e0 = *reinterpret_cast<const v4i *>(a.w + bi * Kq<TYPE>::BB + (TYPE == T_Q6_K ? 192 : 0));
+            if constexpr (TYPE == T_Q6_K) st.e0 = *reinterpret_cast<const v4i *>(a.w + bi * Kq<TYPE>::BB + 192);
+            else st.e0 = *reinterpret_cast<const v4i *>(a.whdr + bi * 16);
             if constexpr (TYPE == T_Q6_K) st.dw = a.wd[bi];
         } else if (t < TN + TM) {
             const int m = min(m0 + t - TN, a.M - 1);
@@ -389,6 +391,8 @@ void run_kq(const void * wv, int64_t N, int64_t K, const void * act, int64_t M, 
     KqArgs<TYPE> a{};
     a.w = w + WL.qs;
     a.wd = TYPE == T_Q6_K ? (const uint16_t *) (w + WL.d) : nullptr;
+    a.wqh = TYPE == T_Q5_K ? w + WL.qh : nullptr;
+    a.whdr = TYPE == T_Q6_K ? nullptr : w + WL.d;
     a.xc = (const int8_t *) (x + AL.codes);
     a.xbs = (const int16_t *) (x + AL.meta);
     a.xd = (const float *) (x + AL.d);

@@ -315,11 +315,10 @@ template <int TYPE>
 struct KsFmt {
     static constexpr bool KQ = TYPE == T_Q4_K || TYPE == T_Q5_K;
     static constexpr int WV = TYPE == T_Q8_0 ? 2 : TYPE == T_Q5_K ? 3 : KQ ? 2 : 1;  // 16-byte loads per row
-    static constexpr uint32_t SB = TYPE == T_Q5_K ? 176u : 144u;                   // K-quant super-block bytes
 };
 
 struct KsArgs {
-    const uint8_t * w;      // Q4_0 / Q8_0: packed codes; K-quants: ggml's super-blocks
+    const uint8_t * w;      // Q4_0 / Q8_0: packed codes; K-quants: the packed weight (nibbles first)
     const uint16_t * wd;    // Q4_0 / Q8_0: packed fp16 scales
     const int8_t * xc;      // activation codes [B][K]
     const float2 * xm;      // Q8_0 activation: (d, code sum) [B][K / 32]
@@ -329,6 +328,7 @@ struct KsArgs {
     float * y;
     const float * res;
     int N, ntask, ldy;      // ntask: tasks per row (K / 32)
+    uint32_t kq_qh, kq_hdr, kq_bytes;  // K-quants: the fifth bits' and headers' offsets, the weight's size
 };
 
 template <int TYPE, int B, int R, bool FQ = false>
@@ -349,10 +349,9 @@ __global__ __launch_bounds__(512) void k_gemv_ks(const KsArgs a) {
     const int sb = tt >> 3, c = (tt >> 1) & 3, h = tt & 1;  // K-quants: super-block, chunk, half
     const uint32_t csh = 16u * (uint32_t) (c & 1);         // the chunk's scale bytes within their words
     const bool chi = c >= 2;
-    const uint32_t row_bytes = F::KQ ? (uint32_t) (a.ntask / 8) * F::SB : 0u;
     const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t *>(a.w), 0,
-        (int) (F::KQ ? (size_t) a.N * row_bytes : (size_t) a.N * nb * (TYPE == T_Q4_0 ? 16 : 32)), 0x00020000);
+        (int) (F::KQ ? (size_t) a.kq_bytes : (size_t) a.N * nb * (TYPE == T_Q4_0 ? 16 : 32)), 0x00020000);
     const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t *>(a.wd), 0, F::KQ ? 0 : (int) (((size_t) a.N * nb + 1) / 2 * 4), 0x00020000);
     const int nbatch = (a.N + R - 1) / R;
@@ -470,10 +469,15 @@ __global__ __launch_bounds__(512) void k_gemv_ks(const KsArgs a) {
 #pragma unroll
         for (int r = 0; r < R; r++) {
             if constexpr (F::KQ) {
-                // header (d, dmin, scales), [Q5_K: the half's 16 qh bytes,] the half chunk's 16 code bytes
-                const uint32_t o = (uint32_t) (tb * R + r) * row_bytes + (uint32_t) sb * F::SB;
-                const uint32_t qo = (TYPE == T_Q5_K ? 48u : 16u) + 32u * (uint32_t) c + 16u * (uint32_t) h;
-                const uint32_t offs[3] = {o, o + qo, o + 16u + 16u * (uint32_t) h};
+                // header (d, dmin, scales), the half chunk's 16 code bytes (piece tt of the row's
+                // nibbles: consecutive lanes, consecutive pieces), [Q5_K: the half's 16 qh bytes];
+                // rows past N read zeros (an offset past the weight)
+                const int row = tb * R + r;
+                const uint32_t bi = (uint32_t) row * (uint32_t) (a.ntask / 8) + (uint32_t) sb;
+                const bool rin = row < a.N;
+                const uint32_t offs[3] = {rin ? a.kq_hdr + 16u * bi : 0x80000000u,
+                                          rin ? 16u * ((uint32_t) row * (uint32_t) a.ntask + (uint32_t) tt) : 0x80000000u,
+                                          rin ? a.kq_qh + 32u * bi + 16u * (uint32_t) h : 0x80000000u};
                 const auto hq = __builtin_amdgcn_raw_buffer_load_b128(rq, offs[0], 0, 0);  // shared by 8 lanes
                 wv[r][0] = make_uint4(hq[0], hq[1], hq[2], hq[3]);
 #pragma unroll
@@ -558,8 +562,10 @@ __global__ __launch_bounds__(512) void k_gemv_ks(const KsArgs a) {
                 // m = (scales[2c+4..] >> 4) | (scales[2c..] >> 6) << 4.
                 const uint4 hd = wv[r][0];
                 const uint32_t A = hd.y >> csh, M = hd.z >> csh, H = hd.w >> csh;
-                const uint32_t scp = chi ? ((H & 0x0F0Fu) | ((A >> 2) & 0x3030u)) : (A & 0x3F3Fu);
-                const uint32_t mp = chi ? (((H >> 4) & 0x0F0Fu) | ((M >> 2) & 0x3030u)) : (M & 0x3F3Fu);
+                // chunks 2, 3 take the high form; chosen by a mask (a select here became a branch)
+                const uint32_t chim = chi ? 0xFFFFFFFFu : 0u;
+                const uint32_t scp = (chim & ((H & 0x0F0Fu) | ((A >> 2) & 0x3030u))) | (~chim & (A & 0x3F3Fu));
+                const uint32_t mp = (chim & (((H >> 4) & 0x0F0Fu) | ((M >> 2) & 0x3030u))) | (~chim & (M & 0x3F3Fu));
                 const int sc0 = (int) (scp & 0xFFu), sc1 = (int) ((scp >> 8) & 0xFFu);
                 const int m0 = (int) (mp & 0xFFu), m1 = (int) ((mp >> 8) & 0xFFu);
                 const float dd = h2f((uint16_t) (hd.x & 0xffff)), dmin = h2f((uint16_t) (hd.x >> 16));
@@ -638,7 +644,7 @@ __global__ __launch_bounds__(256) void k_gemv_q4_K(const uint8_t * __restrict__ 
     if (row0 >= N) return;
     const int K = nsb * QKK;
     const int ntask = nsb * 4;
-    const size_t rowb = (size_t) nsb * 144;
+    const KqRegions L = kq_regions(T_Q4_K, (int64_t) N * nsb);
     float acc[R][B];
 #pragma unroll
     for (int r = 0; r < R; r++)
@@ -655,10 +661,11 @@ __global__ __launch_bounds__(256) void k_gemv_q4_K(const uint8_t * __restrict__ 
 #pragma unroll
                 for (int r = 0; r < R; r++) {
                     const int row = min(row0 + r, N - 1);
-                    const uint4 * p = reinterpret_cast<const uint4 *>(w + row * rowb + (size_t) sb * 144);
-                    hdr[i][r] = p[0];
-                    qa[i][r] = p[1 + 2 * c];
-                    qb[i][r] = p[2 + 2 * c];
+                    const size_t bi = (size_t) row * nsb + sb;
+                    const uint4 * q = reinterpret_cast<const uint4 *>(w + L.qs + bi * 128);
+                    hdr[i][r] = reinterpret_cast<const uint4 *>(w + L.hdr)[bi];
+                    qa[i][r] = q[2 * c];
+                    qb[i][r] = q[2 * c + 1];
                 }
             }
         }
@@ -715,7 +722,7 @@ __global__ __launch_bounds__(256) void k_gemv_q5_K(const uint8_t * __restrict__ 
     if (row0 >= N) return;
     const int K = nsb * QKK;
     const int ntask = nsb * 4;
-    const size_t rowb = (size_t) nsb * 176;
+    const KqRegions L = kq_regions(T_Q5_K, (int64_t) N * nsb);
     float acc[R][B];
 #pragma unroll
     for (int r = 0; r < R; r++)
@@ -732,12 +739,14 @@ __global__ __launch_bounds__(256) void k_gemv_q5_K(const uint8_t * __restrict__ 
 #pragma unroll
                 for (int r = 0; r < R; r++) {
                     const int row = min(row0 + r, N - 1);
-                    const uint4 * p = reinterpret_cast<const uint4 *>(w + row * rowb + (size_t) sb * 176);
-                    hdr[i][r] = p[0];
-                    ha[i][r] = p[1];
-                    hb[i][r] = p[2];
-                    qa[i][r] = p[3 + 2 * c];
-                    qb[i][r] = p[4 + 2 * c];
+                    const size_t bi = (size_t) row * nsb + sb;
+                    const uint4 * q = reinterpret_cast<const uint4 *>(w + L.qs + bi * 128);
+                    const uint4 * qh = reinterpret_cast<const uint4 *>(w + L.qh + bi * 32);
+                    hdr[i][r] = reinterpret_cast<const uint4 *>(w + L.hdr)[bi];
+                    ha[i][r] = qh[0];
+                    hb[i][r] = qh[1];
+                    qa[i][r] = q[2 * c];
+                    qb[i][r] = q[2 * c + 1];
                 }
             }
         }
@@ -891,15 +900,17 @@ __global__ void k_isums_q4_K(const uint8_t * w, const int8_t * xc, const int16_t
     const int n = (int) ((t / nsb) % N);
     const int b = (int) (t / ((int64_t) nsb * N));
     const int K = nsb * QKK;
-    const uint4 * p = reinterpret_cast<const uint4 *>(w + (size_t) n * nsb * 144 + (size_t) sb * 144);
-    const uint4 hdr = p[0];
+    const KqRegions L = kq_regions(T_Q4_K, (int64_t) N * nsb);
+    const size_t bi = (size_t) n * nsb + sb;
+    const uint4 * p = reinterpret_cast<const uint4 *>(w + L.qs + bi * 128);  // the nibbles, 2 x 16 B per chunk
+    const uint4 hdr = reinterpret_cast<const uint4 *>(w + L.hdr)[bi];
     const uint32_t sc3[3] = {hdr.y, hdr.z, hdr.w};
     int32_t * o = out + t * 10;
     int isc = 0, imin = 0;
     for (int c = 0; c < 4; c++) {
         const int4 * xp = reinterpret_cast<const int4 *>(xc + (size_t) b * K + (size_t) sb * QKK + 64 * c);
         int lo, hi, sc0, m0, sc1, m1;
-        dot_q4_K_chunk(p[1 + 2 * c], p[2 + 2 * c], xp[0], xp[1], xp[2], xp[3], lo, hi);
+        dot_q4_K_chunk(p[2 * c], p[2 * c + 1], xp[0], xp[1], xp[2], xp[3], lo, hi);
         scale_min_k4_w(2 * c, sc3, sc0, m0);
         scale_min_k4_w(2 * c + 1, sc3, sc1, m1);
         const int16_t * bs = xbs + (size_t) b * (K / 16) + sb * 16 + 4 * c;
@@ -921,15 +932,18 @@ __global__ void k_isums_q5_K(const uint8_t * w, const int8_t * xc, const int16_t
     const int n = (int) ((t / nsb) % N);
     const int b = (int) (t / ((int64_t) nsb * N));
     const int K = nsb * QKK;
-    const uint4 * p = reinterpret_cast<const uint4 *>(w + (size_t) n * nsb * 176 + (size_t) sb * 176);
-    const uint4 hdr = p[0];
+    const KqRegions L = kq_regions(T_Q5_K, (int64_t) N * nsb);
+    const size_t bi = (size_t) n * nsb + sb;
+    const uint4 * p = reinterpret_cast<const uint4 *>(w + L.qs + bi * 128);   // the nibbles
+    const uint4 * ph = reinterpret_cast<const uint4 *>(w + L.qh + bi * 32);   // the fifth bits
+    const uint4 hdr = reinterpret_cast<const uint4 *>(w + L.hdr)[bi];
     const uint32_t sc3[3] = {hdr.y, hdr.z, hdr.w};
     int32_t * o = out + t * 10;
     int isc = 0, imin = 0;
     for (int c = 0; c < 4; c++) {
         const int4 * xp = reinterpret_cast<const int4 *>(xc + (size_t) b * K + (size_t) sb * QKK + 64 * c);
         int lo, hi, sc0, m0, sc1, m1;
-        dot_q5_K_chunk(p[3 + 2 * c], p[4 + 2 * c], p[1], p[2], c, xp[0], xp[1], xp[2], xp[3], lo, hi);
+        dot_q5_K_chunk(p[2 * c], p[2 * c + 1], ph[0], ph[1], c, xp[0], xp[1], xp[2], xp[3], lo, hi);
         scale_min_k4_w(2 * c, sc3, sc0, m0);
         scale_min_k4_w(2 * c + 1, sc3, sc1, m1);
         const int16_t * bs = xbs + (size_t) b * (K / 16) + sb * 16 + 4 * c;
@@ -1142,14 +1156,18 @@ void run_q4k_nbl(int nbl, const uint8_t * w, const int8_t * xc, const int16_t * 
 constexpr int64_t kKsRowMaxN = 8192;
 
 bool gemv_row_kq_fits(int type, int64_t N, int64_t K) {
-    return (type == T_Q4_K || type == T_Q5_K) && K % QKK == 0 && K > 0 && K / QK <= 512 && N <= kKsRowMaxN &&
-           (uint64_t) N * row_bytes(type, K) < 0x80000000ull;
+    return (type == T_Q4_K || type == T_Q5_K) && K % QKK == 0 && K > 0 && K / QK <= 512 && N > 0 && N <= kKsRowMaxN &&
+           weight_layout(type, N, K).total < 0x80000000ull;
 }
 
 void launch_gemv_row_kq(int type, const void * w, int64_t N, int64_t K, const float * x, float * y, hipStream_t s) {
     require(gemv_row_kq_fits(type, N, K), "gemv row: Q4_K / Q5_K, K a multiple of 256 up to 16384");
     KsArgs k{};
+    const WeightLayout L = weight_layout(type, N, K);
     k.w = (const uint8_t *) w;
+    k.kq_qh = (uint32_t) L.qh;
+    k.kq_hdr = (uint32_t) L.d;
+    k.kq_bytes = (uint32_t) L.total;
     k.x = x;
     k.y = y;
     k.N = (int) N;
@@ -1167,7 +1185,7 @@ void launch_gemv(int type, const void * wv, int64_t N, int64_t K, const void * a
     const uint8_t * w = (const uint8_t *) wv;
     const ActLayout A = act_layout(type, B, K);
     const uint8_t * a = (const uint8_t *) act;
-    const uint64_t ks_bytes = is_kquant(type) ? (uint64_t) N * row_bytes(type, K)
+    const uint64_t ks_bytes = is_kquant(type) ? (uint64_t) weight_layout(type, N, K).total
                                               : (uint64_t) N * (uint64_t) (K / QK) * (type == T_Q4_0 ? 16u : 32u);
     if (ks_fits(type, K, B) && (B > 1 || N <= kKsRowMaxN) && ks_bytes < 0x80000000ull) {
         const bool kq = is_kquant(type);
@@ -1175,6 +1193,9 @@ void launch_gemv(int type, const void * wv, int64_t N, int64_t K, const void * a
         KsArgs k{};
         k.w = kq ? w : w + L.qs;
         k.wd = kq ? nullptr : (const uint16_t *) (w + L.d);
+        k.kq_qh = kq ? (uint32_t) L.qh : 0u;
+        k.kq_hdr = kq ? (uint32_t) L.d : 0u;
+        k.kq_bytes = kq ? (uint32_t) L.total : 0u;
         k.xc = (const int8_t *) (a + A.codes);
         k.xm = kq ? nullptr : (const float2 *) (a + A.meta);
         k.xbs = kq ? (const int16_t *) (a + A.meta) : nullptr;

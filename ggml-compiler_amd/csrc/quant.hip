@@ -485,7 +485,8 @@ __global__ void k_dequant_q4_K(const uint8_t * __restrict__ w, float * __restric
     const int64_t i = t / 128;
     const int k = (int) (t % 128);
     const int c = k / 32, l = k % 32;
-    const uint8_t * b = w + i * 144;
+    const KqRegions R = kq_regions(T_Q4_K, nblocks);
+    const uint8_t * b = w + R.hdr + i * 16;  // d, dmin, scales[12]
     const float d = h2f((uint16_t) (b[0] | (b[1] << 8)));
     const float dmin = h2f((uint16_t) (b[2] | (b[3] << 8)));
     int sc, m;
@@ -493,7 +494,7 @@ __global__ void k_dequant_q4_K(const uint8_t * __restrict__ w, float * __restric
     const float d1 = d * (float) sc, m1 = dmin * (float) m;
     scale_min_k4(2 * c + 1, b + 4, sc, m);
     const float d2 = d * (float) sc, m2 = dmin * (float) m;
-    const uint8_t q = b[16 + k];
+    const uint8_t q = w[R.qs + i * 128 + k];
     y[i * 256 + 64 * c + l] = d1 * (float) (q & 0xF) - m1;
     y[i * 256 + 64 * c + 32 + l] = d2 * (float) (q >> 4) - m2;
 }
@@ -506,7 +507,8 @@ __global__ void k_dequant_q5_K(const uint8_t * __restrict__ w, float * __restric
     const int64_t i = t / 128;
     const int k = (int) (t % 128);
     const int c = k / 32, l = k % 32;
-    const uint8_t * b = w + i * 176;
+    const KqRegions R = kq_regions(T_Q5_K, nblocks);
+    const uint8_t * b = w + R.hdr + i * 16;  // d, dmin, scales[12]
     const float d = h2f((uint16_t) (b[0] | (b[1] << 8)));
     const float dmin = h2f((uint16_t) (b[2] | (b[3] << 8)));
     int sc, m;
@@ -514,7 +516,7 @@ __global__ void k_dequant_q5_K(const uint8_t * __restrict__ w, float * __restric
     const float d1 = d * (float) sc, m1 = dmin * (float) m;
     scale_min_k4(2 * c + 1, b + 4, sc, m);
     const float d2 = d * (float) sc, m2 = dmin * (float) m;
-    const uint8_t q = b[48 + k], h = b[16 + l];
+    const uint8_t q = w[R.qs + i * 128 + k], h = w[R.qh + i * 32 + l];
     y[i * 256 + 64 * c + l] = d1 * (float) ((q & 0xF) + ((h >> (2 * c)) & 1 ? 16 : 0)) - m1;
     y[i * 256 + 64 * c + 32 + l] = d2 * (float) ((q >> 4) + ((h >> (2 * c + 1)) & 1 ? 16 : 0)) - m2;
 }
@@ -675,11 +677,32 @@ void launch_encode(int type, const float * src, int64_t nrows, int64_t k, void *
     check_launch("encode");
 }
 
+// ggml Q4_K / Q5_K super-blocks <-> the packed fields, one thread per 16-byte piece of a super-block
+// (ggml's order: the header {d, dmin, scales[12]}, Q5_K's qh[32] in two, qs[128] in eight).
+template <bool PACK>
+__global__ void k_pack_kq(int type, const uint4 * __restrict__ src, uint4 * __restrict__ dst, int64_t nb) {
+    const int pp = type == T_Q5_K ? 11 : 9;
+    const int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= nb * pp) return;
+    const int64_t i = t / pp;
+    const int p = (int) (t % pp);
+    const KqRegions R = kq_regions(type, nb);
+    size_t o;  // the piece's byte offset in the packed weight
+    if (p == 0) o = R.hdr + (size_t) i * 16;
+    else if (type == T_Q5_K && p < 3) o = R.qh + (size_t) i * 32 + (size_t) (p - 1) * 16;
+    else o = R.qs + (size_t) i * 128 + (size_t) (p - (type == T_Q5_K ? 3 : 1)) * 16;
+    if (PACK) dst[o / 16] = src[t];
+    else dst[t] = src[o / 16];
+}
+
 void launch_pack(int type, const void * src, int64_t nrows, int64_t k, void * dst, hipStream_t s) {
     const WeightLayout L = weight_layout(type, nrows, k);
     uint8_t * o = (uint8_t *) dst;
     if (type == T_Q4_K || type == T_Q5_K) {
-        check_hip(hipMemcpyAsync(dst, src, row_bytes(type, k) * nrows, hipMemcpyDeviceToDevice, s), "pack copy");
+        require(aligned(src, 16) && aligned(dst, 16), "pack: K-quant rows need 16-byte aligned buffers");
+        const int64_t nb = nrows * (k / QKK);
+        if (nb) k_pack_kq<true><<<nblk(nb * (type == T_Q5_K ? 11 : 9), 256), 256, 0, s>>>(type, (const uint4 *) src, (uint4 *) dst, nb);
+        check_launch("pack");
         return;
     }
     if (type == T_Q6_K) {
@@ -719,7 +742,10 @@ void launch_unpack(int type, const void * src, int64_t nrows, int64_t k, void * 
     const WeightLayout L = weight_layout(type, nrows, k);
     const uint8_t * p = (const uint8_t *) src;
     if (type == T_Q4_K || type == T_Q5_K) {
-        check_hip(hipMemcpyAsync(dst, src, row_bytes(type, k) * nrows, hipMemcpyDeviceToDevice, s), "unpack copy");
+        require(aligned(src, 16) && aligned(dst, 16), "unpack: K-quant rows need 16-byte aligned buffers");
+        const int64_t nb = nrows * (k / QKK);
+        if (nb) k_pack_kq<false><<<nblk(nb * (type == T_Q5_K ? 11 : 9), 256), 256, 0, s>>>(type, (const uint4 *) src, (uint4 *) dst, nb);
+        check_launch("unpack");
         return;
     }
     if (type == T_Q6_K) {

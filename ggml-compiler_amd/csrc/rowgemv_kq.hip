@@ -10,16 +10,17 @@
 //     loads first and the workgroup meets before any weight load is issued (a CU's loads complete
 //     in issue order), and the compute wavefronts take the codes through an LDS counter;
 //   - every wavefront walks groups of R whole weight rows (g, g + waves, ...), lane l taking the
-//     row's 64-value chunks l, l + 64, ... (task t: super-block t / 4, chunk c = t % 4: the 32
-//     nibble bytes of sub-blocks 2c (low nibbles) and 2c + 1 (high)), so the four lanes of a quad
-//     share a super-block and each loads one 32-bit word of its 16-byte header (d / dmin, scales),
-//     passed around the quad by DPP; a wavefront sum finishes each output. With long rows (or one
-//     group too many for the compute wavefronts) the x waves take row groups too, once their
-//     prologue is done.
+//     row's 32-value tasks l, l + 64, ... (task t: super-block t / 8, chunk c = (t / 2) % 4, half
+//     h = t % 2: 16 nibble bytes, whose low nibbles are values 16h.. of sub-block 2c and high
+//     nibbles those of 2c + 1), so that a load moves consecutive 16-byte pieces of the packed
+//     nibbles (1 KiB per instruction); each quad's four lanes load one 32-bit word each of their
+//     super-block's 16-byte header (d / dmin, scales), passed around the quad by DPP; a wavefront
+//     sum finishes each output. With long rows (or one group too many for the compute
+//     wavefronts) the x waves take row groups too, once their prologue is done.
 // Per task: (sc0 s0 + sc1 s1) d d_x - dmin (m0 bs0 + m1 bs1) d_x, s0 / s1 the exact int32 dots of
-// sub-blocks 2c / 2c + 1 with their Q8_K codes and bs0 / bs1 their Q8_K block sums (ggml's
-// vec_dot_q{4,5}_K_q8_K terms); the weight's bytes are read once, as buffer loads (an offset past
-// the weight reads zeros).
+// the task's 16 values of sub-blocks 2c / 2c + 1 with their Q8_K codes and bs0 / bs1 those 16s'
+// Q8_K block sums (ggml's vec_dot_q{4,5}_K_q8_K terms); the weight's bytes are read once, as
+// buffer loads (an offset past the weight reads zeros).
 #include "gcq_common.h"
 
 #include <algorithm>
@@ -34,39 +35,46 @@ namespace {
 constexpr int kRowKqMaxK = 16384;  // LDS holds the row's Q8_K codes, bsums and d
 constexpr uint32_t kKqPast = 0x80000000u;  // a buffer offset past every weight (sizes < 2 GB)
 
-template <int TYPE>
-struct RowKqFmt {
-    static constexpr int WV = TYPE == T_Q5_K ? 4 : 2;                // 16-byte loads per task
-    static constexpr uint32_t SB = TYPE == T_Q5_K ? 176u : 144u;    // super-block bytes
-    static constexpr uint32_t QS = TYPE == T_Q5_K ? 48u : 16u;      // offset of the nibbles
-};
-
 template <int TYPE, int R, int NBL, bool NORM, int EPI, int MR>
 __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
 #pragma clang fp contract(off)
     static_assert(EPI == EPI_STORE || R == 2, "row-pair epilogues take two rows per group");
-    using F = RowKqFmt<TYPE>;
-    constexpr int NWV = 16, WV = F::WV;
+    constexpr int NWV = 16;
+    constexpr int WV = TYPE == T_Q5_K ? 2 : 1;     // 16-byte loads per task: nibbles, Q5_K's fifth bits
     constexpr bool XREG = NBL <= 2;                // the task activations in registers
     constexpr bool PF = WV * NBL * R <= 4;         // the next group's weights prefetched
     // x waves: at most 4 (8 for rows past 8192 values); rounds of 16 values per x thread: K / 16
-    // groups over 64 XW threads, NBL at most (a row of NBL * 64 chunks of 64), half that with 8
-    constexpr int XWMAX = NBL > 2 ? 8 : 4, RMAX = NBL > 2 ? (NBL + 1) / 2 : NBL;
-    // codes, 16 per entry: 16-value group j of task t at j * ntask + t, so that a wavefront's
-    // lanes (consecutive tasks) read consecutive entries (no bank conflicts)
+    // groups over 64 XW threads (a row of NBL * 64 tasks of 32)
+    constexpr int XWMAX = NBL > 4 ? 8 : 4, RMAX = NBL > 4 ? (NBL + 3) / 4 : (NBL + 1) / 2;
+    // codes, 16 per entry: task t's 16 values of sub-block 2c at t, of 2c + 1 at ntask + t, so that
+    // a wavefront's lanes (consecutive tasks) read consecutive entries (no bank conflicts)
     __shared__ int4 lc[kRowKqMaxK / 16];
-    __shared__ uint32_t lbp[kRowKqMaxK / 64];      // per task: bsums of groups 0 + 1, 2 + 3 (int16 each)
+    __shared__ uint32_t lbp[kRowKqMaxK / 32];      // per task: the two 16s' bsums (int16 each)
     __shared__ float ld[kRowKqMaxK / 256];         // d per super-block
     __shared__ unsigned int s_flag, s_norm;        // x waves done with: their codes; their norm partials
     __shared__ double red[XWMAX];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int ntask = a.ntask;
-    const int K = ntask * 64, ngrp = K / 16;       // 16-value groups of the row
-    const uint32_t row_bytes = (uint32_t) (ntask / 4) * F::SB;
-    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint8_t *>(a.w), 0, MR > 1 ? (int) a.span : (int) ((size_t) a.N * row_bytes), 0x00020000);
+    const int K = ntask * 32, ngrp = K / 16;       // 16-value groups of the row
+    const int nsb = ntask / 8;                     // super-blocks per row
+    const __amdgpu_buffer_rsrc_t rq =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(a.w), 0, (int) a.span, 0x00020000);
     const int ng = (a.N + R - 1) / R;
+    const int XW = min(XWMAX, (K + 1023) / 1024);
+    const int rounds = (ngrp + 64 * XW - 1) / (64 * XW);
+    const bool XC = a.xc != 0;
+    const int CW = XC ? NWV : NWV - XW;
+    const bool xw = wave < XW;
+    int g = blockIdx.x * CW + (XC ? (wave + NWV - XW) % NWV : max(wave - XW, 0));
+    const int nw = gridDim.x * CW;
+
+    if (threadIdx.x == 0) {
+        s_flag = 0u;
+        s_norm = 0u;
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the count is zero before the workgroup meets
+    }
+
     // Row r of group gg (wave-uniform, in scalar registers): its weight k (returned) and its index
     // there. One weight (EPI_STORE): rows in order. Several: EPI_STORE takes them in order over the
     // ranges; EPI_ROPE_KV takes separate q, k, v weights, group g < (H + Hkv) D/2 being the rotation
@@ -99,68 +107,58 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
             return 0;
         }
     };
-    auto pick_u = [](int k, const uint32_t (&v)[3]) { return k == 2 ? v[2] : k == 1 ? v[1] : v[0]; };
-    const int XW = min(XWMAX, (K + 1023) / 1024);
-    const int rounds = (ngrp + 64 * XW - 1) / (64 * XW);
-    const bool XC = a.xc != 0;
-    const int CW = XC ? NWV : NWV - XW;
-    const bool xw = wave < XW;
-    int g = blockIdx.x * CW + (XC ? (wave + NWV - XW) % NWV : max(wave - XW, 0));
-    const int nw = gridDim.x * CW;
-    // the lane's chunk, the same for all its tasks (64 tasks are 16 super-blocks)
-    const int c = lane & 3;
-    const uint32_t csh = 16u * (uint32_t) (c & 1);
-    const bool chi = c >= 2;
+    // the weights' offsets as values (a choice between kernel-argument loads would become one
+    // dynamically indexed load from a private copy of the arguments)
+    auto rfl = [](uint32_t v) { return (uint32_t) __builtin_amdgcn_readfirstlane((int) v); };
+    const uint32_t oq0 = rfl(a.r_qs[0]), oq1 = rfl(a.r_qs[1]), oq2 = rfl(a.r_qs[2]);
+    const uint32_t oh0 = rfl(a.r_hdr[0]), oh1 = rfl(a.r_hdr[1]), oh2 = rfl(a.r_hdr[2]);
+    const uint32_t ob0 = rfl(a.r_qh[0]), ob1 = rfl(a.r_qh[1]), ob2 = rfl(a.r_qh[2]);
+    auto pick_u = [](int k, uint32_t v0, uint32_t v1, uint32_t v2) { return k == 2 ? v2 : k == 1 ? v1 : v0; };
 
-    if (threadIdx.x == 0) {
-        s_flag = 0u;
-        s_norm = 0u;
-        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the count is zero before the workgroup meets
-    }
-
-    // Per task and row: the 32 nibble bytes (Q5_K: and the super-block's 32 qh bytes) and word c
-    // of the super-block's 16-byte header, the quad's four lanes holding the whole header.
+    // Per task and row: the 16 nibble bytes (Q5_K: and the half's 16 qh bytes) and word t % 4 of
+    // the super-block's 16-byte header, the quad's four lanes holding the whole header.
     uint4 w[NBL][R][WV], wn[NBL][R][WV];
     uint32_t hw[NBL][R], hwn[NBL][R];
     auto load = [&](int gg, uint4 (&wv)[NBL][R][WV], uint32_t (&hv)[NBL][R]) {
         const bool live = gg < ng;
-        // long rows: the tasks' offsets recomputed per group from an opaque lane index (held
-        // across the groups they would spill)
-        int ln = lane;
-        if constexpr (!XREG) asm volatile("" : "+v"(ln));
-        uint32_t rb[R];  // each row's byte offset, once per group
+        uint32_t rq0[R], rh0[R], rqh0[R];  // each row's nibbles, headers, fifth bits: byte offsets
         bool rin[R];
 #pragma unroll
         for (int r = 0; r < R; r++) {
             int local;
             const int k = map_row(gg, r, local);
-            rb[r] = (MR > 1 ? pick_u(k, a.r_off) : 0u) + (uint32_t) local * row_bytes;
+            rq0[r] = pick_u(k, oq0, oq1, oq2) + (uint32_t) local * (uint32_t) ntask * 16u;
+            rh0[r] = pick_u(k, oh0, oh1, oh2) + (uint32_t) local * (uint32_t) nsb * 16u;
+            rqh0[r] = pick_u(k, ob0, ob1, ob2) + (uint32_t) local * (uint32_t) nsb * 32u;
             rin[r] = live && (EPI != EPI_STORE || gg * R + r < a.N);
         }
+        // long rows: the tasks' offsets recomputed per group from an opaque lane index (held
+        // across the groups they would spill)
+        int ln = lane;
+        if constexpr (!XREG) asm volatile("" : "+v"(ln));
 #pragma unroll
         for (int i = 0; i < NBL; i++) {
             const int t = ln + 64 * i;
-            const uint32_t sb = (uint32_t) (t >> 2);
+            const uint32_t sb = (uint32_t) (t >> 3);
 #pragma unroll
             for (int r = 0; r < R; r++) {
                 const bool in = rin[r] && t < ntask;
-                const uint32_t o = rb[r] + sb * F::SB;
-                const uint32_t offs[4] = {o + F::QS + 32u * (uint32_t) c, o + F::QS + 32u * (uint32_t) c + 16u, o + 16u,
-                                          o + 32u};
-                hv[i][r] = __builtin_amdgcn_raw_buffer_load_b32(rq, in ? o + 4u * (uint32_t) c : kKqPast, 0, 0);
-#pragma unroll
-                for (int v = 0; v < WV; v++) {
-                    // the nibbles streamed (nt); the qh bytes, read by the quad's four lanes, cached
-                    const auto q = v < 2 ? __builtin_amdgcn_raw_buffer_load_b128(rq, in ? offs[v] : kKqPast, 0, 2)
-                                         : __builtin_amdgcn_raw_buffer_load_b128(rq, in ? offs[v] : kKqPast, 0, 0);
-                    wv[i][r][v] = make_uint4(q[0], q[1], q[2], q[3]);
+                hv[i][r] = __builtin_amdgcn_raw_buffer_load_b32(rq, in ? rh0[r] + 16u * sb + 4u * (uint32_t) (t & 3) : kKqPast,
+                                                                0, 0);
+                // the nibbles streamed (nt); the qh bytes, read by four lanes, cached
+                const auto q = __builtin_amdgcn_raw_buffer_load_b128(rq, in ? rq0[r] + 16u * (uint32_t) t : kKqPast, 0, 2);
+                wv[i][r][0] = make_uint4(q[0], q[1], q[2], q[3]);
+                if constexpr (TYPE == T_Q5_K) {
+                    const auto qh = __builtin_amdgcn_raw_buffer_load_b128(
+                        rq, in ? rqh0[r] + 32u * sb + 16u * (uint32_t) (t & 1) : kKqPast, 0, 0);
+                    wv[i][r][1] = make_uint4(qh[0], qh[1], qh[2], qh[3]);
                 }
             }
         }
     };
     // word k of the header from lane k of the quad
-    auto hword = [](uint32_t v, auto K) -> uint32_t {
-        constexpr int k = decltype(K)::value;
+    auto hword = [](uint32_t v, auto KI) -> uint32_t {
+        constexpr int k = decltype(KI)::value;
         return (uint32_t) __builtin_amdgcn_mov_dpp((int) v, k | (k << 2) | (k << 4) | (k << 6), 0xF, 0xF, false);
     };
 
@@ -265,18 +263,20 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
 #pragma unroll
                 for (int j = 0; j < 16; j++) q[j] = 0;
             }
-            int s = 0;
-#pragma unroll
-            for (int j = 0; j < 16; j++) s += q[j];
-            const int sp = s + lane_pair_i<1>(s);  // with the neighbouring group's (gi ^ 1)
             if (gi < ngrp) {
-                int pk[4];
+                int pk[4], s = 0;
 #pragma unroll
                 for (int k = 0; k < 4; k++)
                     pk[k] = (q[4 * k] & 0xff) | ((q[4 * k + 1] & 0xff) << 8) | ((q[4 * k + 2] & 0xff) << 16) |
                             ((q[4 * k + 3] & 0xff) << 24);
-                lc[(gi & 3) * ntask + (gi >> 2)] = make_int4(pk[0], pk[1], pk[2], pk[3]);
-                if ((gi & 1) == 0) reinterpret_cast<int16_t *>(lbp)[2 * (gi >> 2) + ((gi >> 1) & 1)] = (int16_t) sp;
+#pragma unroll
+                for (int j = 0; j < 16; j++) s += q[j];
+                // group gi: super-block gi / 16, sub-block 2c + sel (gi % 16 = 4c + 2 sel + h), the
+                // 16s of task 8 (gi / 16) + 2c + h
+                const int gg = gi & 15, sel = (gg >> 1) & 1;
+                const int t = 8 * (gi >> 4) + 2 * (gg >> 2) + (gg & 1);
+                lc[sel * ntask + t] = make_int4(pk[0], pk[1], pk[2], pk[3]);
+                reinterpret_cast<int16_t *>(lbp)[2 * t + sel] = (int16_t) s;
                 if ((lane & 15) == 0) ld[gi >> 4] = d;
             }
             __builtin_amdgcn_sched_barrier(0);  // one round at a time (its codes are 16 registers)
@@ -292,10 +292,10 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
     lds_wait(&s_flag, XW);
     if constexpr (PF) load(g + nw, wn, hwn);
 
-    // The lane's task activations: the 32 codes of sub-blocks 2c and 2c + 1, d_x, bs0 d_x, bs1 d_x.
-    int4 xa[XREG ? NBL : 1][2], xb[XREG ? NBL : 1][2];
+    // The lane's task activations: the 16 codes of sub-block 2c, of 2c + 1, d_x, bs0 d_x, bs1 d_x.
+    int4 xa[XREG ? NBL : 1], xb[XREG ? NBL : 1];
     float xs[XREG ? NBL : 1], xo[XREG ? NBL : 1], xo2[XREG ? NBL : 1];
-    auto act = [&](int i, int4 (&ca)[2], int4 (&cb)[2], float & ds, float & o1, float & o2) {
+    auto act = [&](int i, int4 & ca, int4 & cb, float & ds, float & o1, float & o2) {
         int t = lane + 64 * i;
         // read from LDS once per group: an opaque index keeps the compiler from holding every
         // task's activations in registers across the groups (they would spill)
@@ -306,20 +306,15 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
             t = min(t, ntask - 1);
         }
         if (!XREG || t < ntask) {
-            // the task's 16-value groups 0, 1 (sub-block 2c) and 2, 3 (2c + 1)
-            ca[0] = lc[t];
-            ca[1] = lc[ntask + t];
-            cb[0] = lc[2 * ntask + t];
-            cb[1] = lc[3 * ntask + t];
-            ds = ld[t >> 2];
+            ca = lc[t];
+            cb = lc[ntask + t];
+            ds = ld[t >> 3];
             const uint32_t bp = lbp[t];
             o1 = (float) (int) (int16_t) (bp & 0xffffu) * ds;
             o2 = (float) (int) (int16_t) (bp >> 16) * ds;
         } else {
-            ca[0] = make_int4(0, 0, 0, 0);
-            ca[1] = ca[0];
-            cb[0] = ca[0];
-            cb[1] = ca[0];
+            ca = make_int4(0, 0, 0, 0);
+            cb = ca;
             ds = 0.0f;
             o1 = 0.0f;
             o2 = 0.0f;
@@ -335,6 +330,10 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
         s = sdot4(q[2], x.z, s);
         return sdot4(q[3], x.w, s);
     };
+    // the lane's chunk within the super-block (the same for all its tasks: 64 tasks are 8 super-blocks)
+    const int c = (lane >> 1) & 3;
+    const uint32_t csh = 16u * (uint32_t) (c & 1);
+    const uint32_t chim = c >= 2 ? 0xFFFFFFFFu : 0u;
 
     auto group = [&](int gg, const uint4 (&wv)[NBL][R][WV], const uint32_t (&hv)[NBL][R]) {
         float acc[R];
@@ -342,13 +341,11 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
         for (int r = 0; r < R; r++) acc[r] = 0.0f;
 #pragma unroll
         for (int i = 0; i < NBL; i++) {
-            int4 ca[2], cb[2];
+            int4 ca, cb;
             float ds, o1, o2;
             if constexpr (XREG) {
-                ca[0] = xa[i][0];
-                ca[1] = xa[i][1];
-                cb[0] = xb[i][0];
-                cb[1] = xb[i][1];
+                ca = xa[i];
+                cb = xb[i];
                 ds = xs[i];
                 o1 = xo[i];
                 o2 = xo2[i];
@@ -357,25 +354,22 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
             }
 #pragma unroll
             for (int r = 0; r < R; r++) {
-                // values 0-15 / 16-31 of sub-block 2c (low nibbles), of 2c + 1 (high nibbles)
-                int lo[2][4], hi[2][4];
+                // the task's 16 values of sub-block 2c (low nibbles) and of 2c + 1 (high nibbles)
+                int lo[4], hi[4];
+                const uint4 q = wv[i][r][0];
+                const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
-                for (int u = 0; u < 2; u++) {
-                    const uint4 q = wv[i][r][u];
-                    const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+                for (int j = 0; j < 4; j++) {
+                    lo[j] = (int) (qw[j] & 0x0F0F0F0Fu);
+                    hi[j] = (int) ((qw[j] >> 4) & 0x0F0F0F0Fu);
+                }
+                if constexpr (TYPE == T_Q5_K) {  // the fifth bits: bit 2c of qh[l] (sub-block 2c), 2c + 1
+                    const uint4 qh = wv[i][r][1];
+                    const uint32_t hb[4] = {qh.x, qh.y, qh.z, qh.w};
 #pragma unroll
                     for (int j = 0; j < 4; j++) {
-                        lo[u][j] = (int) (qw[j] & 0x0F0F0F0Fu);
-                        hi[u][j] = (int) ((qw[j] >> 4) & 0x0F0F0F0Fu);
-                    }
-                    if constexpr (TYPE == T_Q5_K) {  // the fifth bits: bit 2c of qh[l] (sub-block 2c), 2c + 1
-                        const uint4 qh = wv[i][r][2 + u];
-                        const uint32_t hb[4] = {qh.x, qh.y, qh.z, qh.w};
-#pragma unroll
-                        for (int j = 0; j < 4; j++) {
-                            lo[u][j] |= (int) (((hb[j] >> (2 * c)) & 0x01010101u) << 4);
-                            hi[u][j] |= (int) (((hb[j] >> (2 * c + 1)) & 0x01010101u) << 4);
-                        }
+                        lo[j] |= (int) (((hb[j] >> (2 * c)) & 0x01010101u) << 4);
+                        hi[j] |= (int) (((hb[j] >> (2 * c + 1)) & 0x01010101u) << 4);
                     }
                 }
                 // the 6-bit scales and mins of sub-blocks 2c and 2c + 1 (ggml's get_scale_min_k4)
@@ -384,17 +378,14 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
                 const uint32_t A = hword(hv[i][r], std::integral_constant<I, 1>{}) >> csh;
                 const uint32_t M = hword(hv[i][r], std::integral_constant<I, 2>{}) >> csh;
                 const uint32_t H = hword(hv[i][r], std::integral_constant<I, 3>{}) >> csh;
-                const uint32_t scp = chi ? ((H & 0x0F0Fu) | ((A >> 2) & 0x3030u)) : (A & 0x3F3Fu);
-                const uint32_t mp = chi ? (((H >> 4) & 0x0F0Fu) | ((M >> 2) & 0x3030u)) : (M & 0x3F3Fu);
+                // chunks 2, 3 take the high form; chosen by a mask (a select here became a branch)
+                const uint32_t scp = (chim & ((H & 0x0F0Fu) | ((A >> 2) & 0x3030u))) | (~chim & (A & 0x3F3Fu));
+                const uint32_t mp = (chim & (((H >> 4) & 0x0F0Fu) | ((M >> 2) & 0x3030u))) | (~chim & (M & 0x3F3Fu));
                 const int sc0 = (int) (scp & 0xFFu), sc1 = (int) ((scp >> 8) & 0xFFu);
                 const int m0 = (int) (mp & 0xFFu), m1 = (int) ((mp >> 8) & 0xFFu);
                 const float dd = h2f((uint16_t) (h0 & 0xffff)), dmin = h2f((uint16_t) (h0 >> 16));
                 const float fm0 = (float) m0 * dmin, fm1 = (float) m1 * dmin;
-                const int s0 = sdot4(lo[1][3], ca[1].w, sdot4(lo[1][2], ca[1].z, sdot4(lo[1][1], ca[1].y,
-                               sdot4(lo[1][0], ca[1].x, dot16(lo[0], ca[0])))));
-                const int s1 = sdot4(hi[1][3], cb[1].w, sdot4(hi[1][2], cb[1].z, sdot4(hi[1][1], cb[1].y,
-                               sdot4(hi[1][0], cb[1].x, dot16(hi[0], cb[0])))));
-                const int isc = sc0 * s0 + sc1 * s1;
+                const int isc = sc0 * dot16(lo, ca) + sc1 * dot16(hi, cb);
                 const float fmin = __builtin_fmaf(fm0, o1, fm1 * o2);
                 acc[r] += __builtin_fmaf((float) isc * dd, ds, -fmin);
             }
@@ -482,19 +473,27 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
 
 template <int TYPE, bool NORM, int EPI, int MR>
 void go_kq(int R, int nbl, const RowKqArgs & a, int grid, hipStream_t s) {
-    if (R == 2 && nbl == 1) {
-        k_row_gemv_kq<TYPE, 2, 1, NORM, EPI, MR><<<grid, 1024, 0, s>>>(a);
-        return;
+#define GCQ_KQ(RR, NB)                                                          \
+    if (R == RR && nbl == NB) {                                                 \
+        k_row_gemv_kq<TYPE, RR, NB, NORM, EPI, MR><<<grid, 1024, 0, s>>>(a);    \
+        return;                                                                 \
     }
+    GCQ_KQ(2, 1)
+    GCQ_KQ(2, 2)
     if constexpr (EPI == EPI_STORE) {
-        if (R == 1 && nbl == 1) return (void) k_row_gemv_kq<TYPE, 1, 1, NORM, EPI, MR><<<grid, 1024, 0, s>>>(a);
-        if (R == 1 && nbl == 2) return (void) k_row_gemv_kq<TYPE, 1, 2, NORM, EPI, MR><<<grid, 1024, 0, s>>>(a);
+        GCQ_KQ(1, 1)
+        GCQ_KQ(1, 2)
+        GCQ_KQ(1, 3)
+        GCQ_KQ(1, 4)
         if constexpr (MR == 1 && TYPE == T_Q4_K) {  // rows past 8192 values: one Q4_K weight
-            if (R == 1 && nbl == 3) return (void) k_row_gemv_kq<TYPE, 1, 3, NORM, EPI, MR><<<grid, 1024, 0, s>>>(a);
-            if (R == 1 && nbl == 4) return (void) k_row_gemv_kq<TYPE, 1, 4, NORM, EPI, MR><<<grid, 1024, 0, s>>>(a);
+            GCQ_KQ(1, 5)
+            GCQ_KQ(1, 6)
+            GCQ_KQ(1, 7)
+            GCQ_KQ(1, 8)
         }
     }
-    fail("row gemv kq: two rows per group need rows of at most 64 chunks");
+#undef GCQ_KQ
+    fail("row gemv kq: no kernel for " + std::to_string(R) + " rows of " + std::to_string(nbl) + " tasks per lane");
 }
 
 template <int TYPE>
@@ -512,21 +511,17 @@ bool kq_rows_fit(int type, int64_t K) {
     return (type == T_Q4_K || type == T_Q5_K) && K > 0 && K % QKK == 0 && K <= (type == T_Q4_K ? kRowKqMaxK : 8192);
 }
 
-uint32_t kq_row_bytes(int type, int64_t K) { return (uint32_t) (K / QKK) * (type == T_Q5_K ? 176u : 144u); }
-
 }  // namespace
 
 bool row_gemv_kq_fits(int type, int64_t N, int64_t K) {
-    // longer rows spill registers; more rows stream faster through the batched kernel after a
-    // separate quantization (measured at 4096 x 28672: 15.8 against 18.5 us)
-    if (!kq_rows_fit(type, K) || N <= 0 || N > 8192) return false;
-    return (uint64_t) N * kq_row_bytes(type, K) < 0x80000000ull;
+    // more rows stream faster through the batched kernel after a separate quantization
+    return kq_rows_fit(type, K) && N > 0 && N <= 8192 && weight_layout(type, N, K).total < 0x80000000ull;
 }
 
 // With the rms_norm prologue (a normalized row read by several projections, each normalizing it
 // itself): up to 16384 rows, where it also saves the norm's and the quantization's launches.
 bool row_gemv_kq_norm_fits(int type, int64_t N, int64_t K) {
-    return kq_rows_fit(type, K) && N > 0 && N <= 16384 && (uint64_t) N * kq_row_bytes(type, K) < 0x80000000ull;
+    return kq_rows_fit(type, K) && N > 0 && N <= 16384 && weight_layout(type, N, K).total < 0x80000000ull;
 }
 
 bool row_gemv_kq_epi_fits(int type, int epi, int64_t K) {
@@ -542,18 +537,22 @@ bool row_gemv_kq_ranges(int type, int n, const uint8_t * const * w, const int64_
         lo = std::min(lo, (uintptr_t) w[k]);
         total += N[k];
     }
-    const uint64_t rb = kq_row_bytes(type, K);
     uint64_t span = 0;
     for (int k = 0; k < n; k++) {
-        a.r_off[k] = (uint32_t) ((uintptr_t) w[k] - lo);
-        span = std::max(span, (uint64_t) ((uintptr_t) w[k] - lo) + (uint64_t) N[k] * rb);
+        const uint64_t o = (uint64_t) ((uintptr_t) w[k] - lo);
+        const WeightLayout L = weight_layout(type, N[k], K);
+        span = std::max(span, o + L.total);
+        if (span >= 0x80000000ull) return false;
+        a.r_qs[k] = (uint32_t) (o + L.qs);
+        a.r_qh[k] = (uint32_t) (o + L.qh);
+        a.r_hdr[k] = (uint32_t) (o + L.d);
         a.r_end[k] = (int) ((k ? a.r_end[k - 1] : 0) + N[k]);
     }
-    if (span >= 0x80000000ull || total > INT32_MAX) return false;
+    if (total > INT32_MAX) return false;
     a.nr = n;
     a.w = (const uint8_t *) lo;
     a.N = (int) total;
-    a.ntask = (int) (K / 64);
+    a.ntask = (int) (K / 32);
     a.span = (uint32_t) span;
     return true;
 }
@@ -563,12 +562,11 @@ bool row_gemv_kq_ranges(int type, int n, const uint8_t * const * w, const int64_
 // row-pair epilogues).
 void launch_row_gemv_kq_epi(int type, int epi, const RowKqArgs & a0, hipStream_t s) {
     RowKqArgs a = a0;
-    const int64_t K = (int64_t) a.ntask * 64;
+    const int64_t K = (int64_t) a.ntask * 32;
     require(row_gemv_kq_epi_fits(type, epi, K),
             "row gemv kq: Q4_K / Q5_K, K a multiple of 256 up to 8192 (Q4_K 16384; 4096 for the row-pair epilogues)");
     const bool multi = a.nr > 1;
-    require(multi ? (uint64_t) a.span < 0x80000000ull && a.r_end[a.nr - 1] == a.N
-                  : a.N > 0 && (uint64_t) a.N * kq_row_bytes(type, K) < 0x80000000ull,
+    require(a.N > 0 && (uint64_t) a.span < 0x80000000ull && (!multi || a.r_end[a.nr - 1] == a.N),
             "row gemv kq: weights of 2 GB or more");
     require(!multi || a.norm_w, "row gemv kq: several weights take the rms_norm prologue");
     require(!multi || K <= 8192, "row gemv kq: several weights take rows of at most 8192 values");
@@ -586,15 +584,14 @@ void launch_row_gemv_kq_epi(int type, int epi, const RowKqArgs & a0, hipStream_t
     }
     const int nbl = (a.ntask + 63) / 64;
     const int cus = cu_count();
-    const int xw = std::min(nbl > 2 ? 8 : 4, (int) ((K + 1023) / 1024));  // the kernel's XW
+    const int xw = std::min(nbl > 4 ? 8 : 4, (int) ((K + 1023) / 1024));  // the kernel's XW
     // two rows per group when every compute wavefront of the grid gets one and the rows are short
     // (Q5_K's tasks hold twice the registers: one row, whose next group's weights are prefetched);
     // the row-pair epilogues always take two
-    const int R = epi != EPI_STORE || (type == T_Q4_K && nbl == 1 && a.N / 2 >= (int64_t) cus * (16 - xw)) ? 2 : 1;
+    const int R = epi != EPI_STORE || (type == T_Q4_K && nbl <= 2 && a.N / 2 >= (int64_t) cus * (16 - xw)) ? 2 : 1;
     const int64_t ng = (a.N + R - 1) / R;
-    // the x waves take groups too for long rows, or when the compute wavefronts alone would need
-    // one more round
-    a.xc = nbl > 4 || (ng <= 16LL * cus && ng > (int64_t) (16 - xw) * cus);
+    // the x waves take groups too when the compute wavefronts alone would need one more round
+    a.xc = ng <= 16LL * cus && ng > (int64_t) (16 - xw) * cus;
     const int cw = a.xc ? 16 : 16 - xw;
     const int grid = (int) std::max<int64_t>(1, std::min<int64_t>(cus, (ng + cw - 1) / cw));
     if (type == T_Q4_K) go_kq_t<T_Q4_K>(epi, a.norm_w != nullptr, multi, R, nbl, a, grid, s);
@@ -602,21 +599,26 @@ void launch_row_gemv_kq_epi(int type, int epi, const RowKqArgs & a0, hipStream_t
     check_launch("row gemv kq");
 }
 
-// y[n] (+ res[n]) = sum_k W[n, k] x'[k] for a Q4_K / Q5_K weight in ggml's super-block layout, x' = x
-// or, with norm_w, ggml_mul(ggml_rms_norm(x, eps), norm_w).
+// y[n] (+ res[n]) = sum_k W[n, k] x'[k] for a packed Q4_K / Q5_K weight, x' = x or, with norm_w,
+// ggml_mul(ggml_rms_norm(x, eps), norm_w).
 void launch_row_gemv_kq(int type, const void * w, int64_t N, int64_t K, const float * x, const float * norm_w, float eps,
                         float * y, const float * res, hipStream_t s) {
     require(norm_w ? row_gemv_kq_norm_fits(type, N, K) : row_gemv_kq_fits(type, N, K),
             "row gemv kq: Q4_K / Q5_K, K a multiple of 256 up to 8192 (Q4_K 16384), up to 8192 rows (16384 with the norm)");
+    const WeightLayout L = weight_layout(type, N, K);
     RowKqArgs a{};
     a.w = (const uint8_t *) w;
+    a.r_qs[0] = (uint32_t) L.qs;
+    a.r_qh[0] = (uint32_t) L.qh;
+    a.r_hdr[0] = (uint32_t) L.d;
+    a.span = (uint32_t) L.total;
     a.x = x;
     a.y = y;
     a.res = res;
     a.norm_w = norm_w;
     a.eps = eps;
     a.N = (int) N;
-    a.ntask = (int) (K / 64);
+    a.ntask = (int) (K / 32);
     launch_row_gemv_kq_epi(type, EPI_STORE, a, s);
 }
 

@@ -70,7 +70,8 @@ GCQ_API size_t gcq_flash_attn_workspace(int Sq, int H, int Hkv, int Dv, int n_kv
  * ggml_compiler/quant/types.py:6-19 this library computes with). */
 GCQ_API int gcq_quantize(int type, const float * src, int64_t nrows, int64_t n_per_row, void * dst, void * stream);
 /* ggml block rows (device) -> packed device weight. dst must hold gcq_weight_size bytes, 16-byte
- * aligned. Replaces the weight upload of runtime/src/ggml_compiler_rt.cpp:445-479 (:476). */
+ * aligned (src too for Q4_K / Q5_K). Replaces the weight upload of
+ * runtime/src/ggml_compiler_rt.cpp:445-479 (:476). */
 GCQ_API int gcq_pack_weights(int type, const void * src, int64_t nrows, int64_t n_per_row, void * dst, void * stream);
 /* Packed weight -> f32 rows (ggml dequantize_row_*; bit-exact). */
 GCQ_API int gcq_dequantize(int type, const void * w, int64_t nrows, int64_t n_per_row, float * dst, void * stream);
