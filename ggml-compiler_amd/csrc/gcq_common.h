@@ -198,13 +198,17 @@ struct RowKqArgs {
     int r_end[3];
     uint32_t r_qs[3], r_qh[3], r_hdr[3], span;
     float * r_y[3];
+    // PRO_MERGE: the attention row from split partials o [H][nsplit][D], (max, exp-sum) [H][nsplit]
+    const float * part_o;
+    const float2 * part_ml;
+    int nsplit;
     // EPI_ROPE_KV: the position, its (cos, sin) table, the f16 caches [Hkv][ctx][D]
     const int * pos;
     const float2 * rope_cs;
     uint16_t * kc;
     uint16_t * vc;
     int64_t ctx;
-    int H, Hkv, D;
+    int H, Hkv, D;      // D: also PRO_MERGE's head size
     uint32_t hd_magic;  // set by the launch: x / (D/2) = mulhi(x, hd_magic)
 };
 
@@ -214,7 +218,7 @@ bool row_gemv_kq_ranges(int type, int n, const uint8_t * const * w, const int64_
 // Whether launch_row_gemv_kq_epi runs this epilogue on rows of K values (the row-pair epilogues
 // take rows of at most 4096 values).
 bool row_gemv_kq_epi_fits(int type, int epi, int64_t K);
-void launch_row_gemv_kq_epi(int type, int epi, const RowKqArgs & a, hipStream_t s);
+void launch_row_gemv_kq_epi(int type, int pro, int epi, const RowKqArgs & a, hipStream_t s);
 
 // Shapes and byte strides of a strided copy / conversion (elementwise.hip).
 struct Cpy4 {

@@ -184,6 +184,14 @@ bool weights_fit_one_launch(int type, int n, const uint8_t * const * w, const in
     return row_gemv_ranges(type, n, w, N, K, a);
 }
 
+// A mul_mat of one row by a Q4_K / Q5_K weight of rows up to 4096 values that the K-quant row
+// GEMV runs with the attention-merge prologue.
+bool kq_merge_mul_mat(const ggml_tensor * mm) {
+    const ggml_tensor * a = mm->src[0];
+    return (a->type == GGML_TYPE_Q4_K || a->type == GGML_TYPE_Q5_K) && whole_packed(a) && a->ne[2] == 1 &&
+           a->ne[3] == 1 && ggml_nrows(mm->src[1]) == 1 && a->ne[0] <= 4096 && row_gemv_kq_fits(a->type, a->ne[1], a->ne[0]);
+}
+
 // flash_attn_ext of one query row that the one-pass decode kernel runs (f16 K/V with 16-byte rows,
 // f16 mask or none, no ALiBi / softcap) and whose output the decode-row GEMV can merge from
 // split partials (H * D <= 4096).
@@ -447,8 +455,8 @@ Chains find_chains(const ggml_cgraph * g, bool fuse) {
             if (u == uses.end() || u->second != 1) continue;
             const int k = reader[rs];
             const ggml_tensor * mm = g->nodes[k];
-            if (mm->op != GGML_OP_MUL_MAT || mm->src[1] != rs || !q8_mul_mat(mm) || ggml_nrows(rs) != 1 ||
-                !row_gemv_fits(mm->src[0]->type, rs->ne[0]))
+            if (mm->op != GGML_OP_MUL_MAT || mm->src[1] != rs || ggml_nrows(rs) != 1 ||
+                !((q8_mul_mat(mm) && row_gemv_fits(mm->src[0]->type, rs->ne[0])) || kq_merge_mul_mat(mm)))
                 continue;
             const int a = with_add(k);
             if (a >= 0) link({i, j, k, a});
@@ -1536,7 +1544,7 @@ void run_step(const ggml_backend * be, const Step & s) {
                 a.Hkv = (int) s.n[5];
                 a.D = (int) s.n[6];
                 a.ctx = s.n[7];
-                launch_row_gemv_kq_epi(s.type, EPI_ROPE_KV, a, st);
+                launch_row_gemv_kq_epi(s.type, PRO_NORM, EPI_ROPE_KV, a, st);
                 return;
             }
             RowArgs a{};
@@ -1565,7 +1573,7 @@ void run_step(const ggml_backend * be, const Step & s) {
                 a.norm_w = (const float *) s.in[2];
                 a.eps = s.f[0];
                 a.y = (float *) s.out;
-                launch_row_gemv_kq_epi(s.type, EPI_SWIGLU, a, st);
+                launch_row_gemv_kq_epi(s.type, PRO_NORM, EPI_SWIGLU, a, st);
                 return;
             }
             RowArgs a{};
@@ -1589,7 +1597,7 @@ void run_step(const ggml_backend * be, const Step & s) {
                 a.r_y[0] = (float *) s.out;
                 a.r_y[1] = (float *) s.out2[0];
                 a.r_y[2] = (float *) s.out2[1];
-                launch_row_gemv_kq_epi(s.type, EPI_STORE, a, st);
+                launch_row_gemv_kq_epi(s.type, PRO_NORM, EPI_STORE, a, st);
                 return;
             }
             RowArgs a{};
@@ -1709,6 +1717,30 @@ void run_step(const ggml_backend * be, const Step & s) {
             launch_attn_decode((const float *) s.in[0], s.n[0], s.in[1], s.n[1], s.n[2], s.in[2], s.n[3], s.n[4],
                                (int) D, (int) H, (int) Hkv, (int) n_kv, nullptr, s.f[0], nsplit, chunk, (int) n_kv, GS,
                                row, po, pml, st, nullptr, s.in[3], 16);
+            if (is_kquant(s.type)) {  // the K-quant row GEMV, the row merged (or read) in its prologue
+                const WeightLayout L = weight_layout(s.type, N, K);
+                RowKqArgs a{};
+                a.w = (const uint8_t *) s.in[4];
+                a.r_qs[0] = (uint32_t) L.qs;
+                a.r_qh[0] = (uint32_t) L.qh;
+                a.r_hdr[0] = (uint32_t) L.d;
+                a.span = (uint32_t) L.total;
+                a.N = (int) N;
+                a.ntask = (int) (K / 32);
+                a.y = (float *) s.out;
+                a.res = (const float *) s.in[5];
+                if (nsplit == 1) {
+                    a.x = row;
+                    launch_row_gemv_kq_epi(s.type, PRO_PLAIN, EPI_STORE, a, st);
+                } else {
+                    a.part_o = po;
+                    a.part_ml = pml;
+                    a.nsplit = nsplit;
+                    a.D = (int) D;
+                    launch_row_gemv_kq_epi(s.type, PRO_MERGE, EPI_STORE, a, st);
+                }
+                return;
+            }
             const WeightLayout L = weight_layout(s.type, N, K);
             RowArgs a{};
             a.wqs = (const uint8_t *) s.in[4] + L.qs;

@@ -35,10 +35,12 @@ namespace {
 constexpr int kRowKqMaxK = 16384;  // LDS holds the row's Q8_K codes, bsums and d
 constexpr uint32_t kKqPast = 0x80000000u;  // a buffer offset past every weight (sizes < 2 GB)
 
-template <int TYPE, int R, int NBL, bool NORM, int EPI, int MR>
+template <int TYPE, int R, int NBL, int PRO, int EPI, int MR>
 __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
 #pragma clang fp contract(off)
     static_assert(EPI == EPI_STORE || R == 2, "row-pair epilogues take two rows per group");
+    constexpr bool NORM = PRO == PRO_NORM, MERGE = PRO == PRO_MERGE;
+    static_assert(!MERGE || NBL <= 2, "the merge prologue takes rows of at most 4096 values");
     constexpr int NWV = 16;
     constexpr int WV = TYPE == T_Q5_K ? 2 : 1;     // 16-byte loads per task: nibbles, Q5_K's fifth bits
     constexpr bool XREG = NBL <= 2;                // the task activations in registers
@@ -61,9 +63,10 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
     const __amdgpu_buffer_rsrc_t rq =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(a.w), 0, (int) a.span, 0x00020000);
     const int ng = (a.N + R - 1) / R;
-    const int XW = min(XWMAX, (K + 1023) / 1024);
-    const int rounds = (ngrp + 64 * XW - 1) / (64 * XW);
-    const bool XC = a.xc != 0;
+    // MERGE: no x waves; every wavefront merges and quantizes 4 values per lane, then computes
+    const int XW = MERGE ? 0 : min(XWMAX, (K + 1023) / 1024);
+    const int rounds = MERGE ? 0 : (ngrp + 64 * XW - 1) / (64 * XW);
+    const bool XC = MERGE || a.xc != 0;
     const int CW = XC ? NWV : NWV - XW;
     const bool xw = wave < XW;
     int g = blockIdx.x * CW + (XC ? (wave + NWV - XW) % NWV : max(wave - XW, 0));
@@ -162,7 +165,105 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
         return (uint32_t) __builtin_amdgcn_mov_dpp((int) v, k | (k << 2) | (k << 4) | (k << 6), 0xF, 0xF, false);
     };
 
-    if (xw) {
+    if constexpr (MERGE) {
+        // The attention row merged from its split partials (the arithmetic of the decode-row
+        // GEMV's merge prologue: sum_j e^(m_j - M) o_j / sum_j e^(m_j - M) l_j in split order,
+        // splits with m_j = -inf left out, 0 if none), 4 values e = 4 t per thread; the partials'
+        // loads are issued before any weight load.
+        constexpr int KM = 8;  // splits at most (the launch checks)
+        float2 mlv[KM];
+        float4 pov[KM];
+        const int e0 = min((int) threadIdx.x * 4, K - 4);
+        const int hh = e0 / a.D;
+        const float2 * ml = a.part_ml + (int64_t) hh * a.nsplit;
+        const float * po = a.part_o + (int64_t) hh * a.nsplit * a.D + (e0 - hh * a.D);
+#pragma unroll
+        for (int j = 0; j < KM; j++) {
+            if (j < a.nsplit) {
+                mlv[j] = ml[j];
+                pov[j] = *reinterpret_cast<const float4 *>(po + (int64_t) j * a.D);
+            } else {
+                mlv[j] = make_float2(-INFINITY, 0.0f);
+                pov[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        load(g, w, hw);
+        const int e = (int) threadIdx.x * 4;
+        float vv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (e < K) {
+            float M = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < KM; j++) M = fmaxf(M, mlv[j].x);
+            float L = 0.0f;
+            float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (M != -INFINITY) {
+#pragma unroll
+                for (int j = 0; j < KM; j++) {
+                    if (mlv[j].x == -INFINITY) continue;
+                    const float wj = __expf(mlv[j].x - M);
+                    L += wj * mlv[j].y;
+                    o.x += wj * pov[j].x;
+                    o.y += wj * pov[j].y;
+                    o.z += wj * pov[j].z;
+                    o.w += wj * pov[j].w;
+                }
+            }
+            vv[0] = L == 0.0f ? 0.0f : o.x / L;
+            vv[1] = L == 0.0f ? 0.0f : o.y / L;
+            vv[2] = L == 0.0f ? 0.0f : o.z / L;
+            vv[3] = L == 0.0f ? 0.0f : o.w / L;
+        }
+        // Q8_K of the wavefront's super-block (its 64 lanes' 256 values): the first largest |x|
+        float ax = 0.0f, mx = 0.0f;
+        int idx = 1 << 30;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            if (fabsf(vv[j]) > ax) {
+                ax = fabsf(vv[j]);
+                mx = vv[j];
+                idx = e + j;
+            }
+        }
+        auto take = [&](float ax2, float mx2, int idx2) {
+            if (ax2 > ax || (ax2 == ax && idx2 < idx)) {
+                ax = ax2;
+                mx = mx2;
+                idx = idx2;
+            }
+        };
+        take(lane_pair<1>(ax), lane_pair<1>(mx), lane_pair_i<1>(idx));
+        take(lane_pair<2>(ax), lane_pair<2>(mx), lane_pair_i<2>(idx));
+        take(lane_pair<4>(ax), lane_pair<4>(mx), lane_pair_i<4>(idx));
+        take(lane_pair<8>(ax), lane_pair<8>(mx), lane_pair_i<8>(idx));
+        take(__shfl_xor(ax, 16), __shfl_xor(mx, 16), __shfl_xor(idx, 16));
+        take(__shfl_xor(ax, 32), __shfl_xor(mx, 32), __shfl_xor(idx, 32));
+        int q[4] = {0, 0, 0, 0};
+        float d = 0.0f;
+        if (ax != 0.0f) {
+            const float iscale = __fdiv_rn(-127.0f, mx);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int rr = (int) __builtin_rintf(iscale * vv[j]);
+                q[j] = rr < 127 ? rr : 127;
+            }
+            d = __fdiv_rn(1.0f, iscale);
+        }
+        const int word = (q[0] & 0xff) | ((q[1] & 0xff) << 8) | ((q[2] & 0xff) << 16) | ((q[3] & 0xff) << 24);
+        int s4 = q[0] + q[1] + q[2] + q[3];
+        s4 += lane_pair_i<1>(s4);
+        s4 += lane_pair_i<2>(s4);  // the 16-value group's bsum (its 4 lanes)
+        if (e < K) {
+            const int gi = (int) threadIdx.x >> 2, gg = gi & 15, sel = (gg >> 1) & 1;
+            const int t = 8 * (gi >> 4) + 2 * (gg >> 2) + (gg & 1);
+            reinterpret_cast<int *>(lc + sel * ntask + t)[threadIdx.x & 3] = word;
+            if ((threadIdx.x & 3) == 0) reinterpret_cast<int16_t *>(lbp)[2 * t + sel] = (int16_t) s4;
+            if (lane == 0) ld[wave] = d;  // the wavefront's 256 values are super-block `wave`
+        }
+        if (lane == 0) lds_signal(&s_flag);
+    } else if (xw) {
         // the row's loads first, then the workgroup meets (no weight load is ahead of them)
         float4 xv[RMAX][4], nv[NORM ? RMAX : 1][4];
 #pragma unroll
@@ -283,13 +384,14 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
         }
         if (lane == 0) lds_signal(&s_flag);
         if (!XC) return;
+        load(g, w, hw);
     } else {
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
+        load(g, w, hw);
     }
-    load(g, w, hw);
-    lds_wait(&s_flag, XW);
+    lds_wait(&s_flag, MERGE ? NWV : XW);
     if constexpr (PF) load(g + nw, wn, hwn);
 
     // The lane's task activations: the 16 codes of sub-block 2c, of 2c + 1, d_x, bs0 d_x, bs1 d_x.
@@ -471,16 +573,19 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
     }
 }
 
-template <int TYPE, bool NORM, int EPI, int MR>
+template <int TYPE, int PRO, int EPI, int MR>
 void go_kq(int R, int nbl, const RowKqArgs & a, int grid, hipStream_t s) {
 #define GCQ_KQ(RR, NB)                                                          \
     if (R == RR && nbl == NB) {                                                 \
-        k_row_gemv_kq<TYPE, RR, NB, NORM, EPI, MR><<<grid, 1024, 0, s>>>(a);    \
+        k_row_gemv_kq<TYPE, RR, NB, PRO, EPI, MR><<<grid, 1024, 0, s>>>(a);     \
         return;                                                                 \
     }
     GCQ_KQ(2, 1)
     GCQ_KQ(2, 2)
-    if constexpr (EPI == EPI_STORE) {
+    if constexpr (PRO == PRO_MERGE) {
+        GCQ_KQ(1, 1)
+        GCQ_KQ(1, 2)
+    } else if constexpr (EPI == EPI_STORE) {
         GCQ_KQ(1, 1)
         GCQ_KQ(1, 2)
         GCQ_KQ(1, 3)
@@ -497,12 +602,13 @@ void go_kq(int R, int nbl, const RowKqArgs & a, int grid, hipStream_t s) {
 }
 
 template <int TYPE>
-void go_kq_t(int epi, bool norm, bool multi, int R, int nbl, const RowKqArgs & a, int grid, hipStream_t s) {
-    if (epi == EPI_ROPE_KV) return go_kq<TYPE, true, EPI_ROPE_KV, 3>(R, nbl, a, grid, s);
-    if (epi == EPI_SWIGLU) return go_kq<TYPE, true, EPI_SWIGLU, 3>(R, nbl, a, grid, s);
-    if (multi) return go_kq<TYPE, true, EPI_STORE, 3>(R, nbl, a, grid, s);
-    if (norm) return go_kq<TYPE, true, EPI_STORE, 1>(R, nbl, a, grid, s);
-    go_kq<TYPE, false, EPI_STORE, 1>(R, nbl, a, grid, s);
+void go_kq_t(int pro, int epi, bool multi, int R, int nbl, const RowKqArgs & a, int grid, hipStream_t s) {
+    if (epi == EPI_ROPE_KV) return go_kq<TYPE, PRO_NORM, EPI_ROPE_KV, 3>(R, nbl, a, grid, s);
+    if (epi == EPI_SWIGLU) return go_kq<TYPE, PRO_NORM, EPI_SWIGLU, 3>(R, nbl, a, grid, s);
+    if (multi) return go_kq<TYPE, PRO_NORM, EPI_STORE, 3>(R, nbl, a, grid, s);
+    if (pro == PRO_NORM) return go_kq<TYPE, PRO_NORM, EPI_STORE, 1>(R, nbl, a, grid, s);
+    if (pro == PRO_MERGE) return go_kq<TYPE, PRO_MERGE, EPI_STORE, 1>(R, nbl, a, grid, s);
+    go_kq<TYPE, PRO_PLAIN, EPI_STORE, 1>(R, nbl, a, grid, s);
 }
 
 bool kq_rows_fit(int type, int64_t K) {
@@ -560,8 +666,13 @@ bool row_gemv_kq_ranges(int type, int n, const uint8_t * const * w, const int64_
 // The launch behind every K-quant row GEMV: one weight (EPI_STORE, optional residual, optional
 // norm) or several of one row length read by the one normalized row (EPI_STORE to r_y, or the
 // row-pair epilogues).
-void launch_row_gemv_kq_epi(int type, int epi, const RowKqArgs & a0, hipStream_t s) {
+void launch_row_gemv_kq_epi(int type, int pro, int epi, const RowKqArgs & a0, hipStream_t s) {
     RowKqArgs a = a0;
+    require((pro == PRO_PLAIN || pro == PRO_NORM || pro == PRO_MERGE) && (pro == PRO_NORM) == (a.norm_w != nullptr),
+            "row gemv kq: plain, norm (with norm_w) or merge prologue");
+    require(pro != PRO_MERGE || (epi == EPI_STORE && a.nr <= 1 && a.ntask * 32 <= 4096 && a.nsplit >= 1 &&
+                                 a.nsplit <= 8 && a.D > 0 && a.D % 4 == 0 && (a.ntask * 32) % a.D == 0),
+            "row gemv kq: merge of 1..8 splits of D-value heads (D a multiple of 4), K <= 4096, one weight");
     const int64_t K = (int64_t) a.ntask * 32;
     require(row_gemv_kq_epi_fits(type, epi, K),
             "row gemv kq: Q4_K / Q5_K, K a multiple of 256 up to 8192 (Q4_K 16384; 4096 for the row-pair epilogues)");
@@ -584,18 +695,18 @@ void launch_row_gemv_kq_epi(int type, int epi, const RowKqArgs & a0, hipStream_t
     }
     const int nbl = (a.ntask + 63) / 64;
     const int cus = cu_count();
-    const int xw = std::min(nbl > 4 ? 8 : 4, (int) ((K + 1023) / 1024));  // the kernel's XW
+    const int xw = pro == PRO_MERGE ? 0 : std::min(nbl > 4 ? 8 : 4, (int) ((K + 1023) / 1024));  // the kernel's XW
     // two rows per group when every compute wavefront of the grid gets one and the rows are short
     // (Q5_K's tasks hold twice the registers: one row, whose next group's weights are prefetched);
     // the row-pair epilogues always take two
     const int R = epi != EPI_STORE || (type == T_Q4_K && nbl <= 2 && a.N / 2 >= (int64_t) cus * (16 - xw)) ? 2 : 1;
     const int64_t ng = (a.N + R - 1) / R;
     // the x waves take groups too when the compute wavefronts alone would need one more round
-    a.xc = ng <= 16LL * cus && ng > (int64_t) (16 - xw) * cus;
+    a.xc = pro == PRO_MERGE || (ng <= 16LL * cus && ng > (int64_t) (16 - xw) * cus);
     const int cw = a.xc ? 16 : 16 - xw;
     const int grid = (int) std::max<int64_t>(1, std::min<int64_t>(cus, (ng + cw - 1) / cw));
-    if (type == T_Q4_K) go_kq_t<T_Q4_K>(epi, a.norm_w != nullptr, multi, R, nbl, a, grid, s);
-    else go_kq_t<T_Q5_K>(epi, a.norm_w != nullptr, multi, R, nbl, a, grid, s);
+    if (type == T_Q4_K) go_kq_t<T_Q4_K>(pro, epi, multi, R, nbl, a, grid, s);
+    else go_kq_t<T_Q5_K>(pro, epi, multi, R, nbl, a, grid, s);
     check_launch("row gemv kq");
 }
 
@@ -619,7 +730,7 @@ void launch_row_gemv_kq(int type, const void * w, int64_t N, int64_t K, const fl
     a.eps = eps;
     a.N = (int) N;
     a.ntask = (int) (K / 32);
-    launch_row_gemv_kq_epi(type, EPI_STORE, a, s);
+    launch_row_gemv_kq_epi(type, norm_w ? PRO_NORM : PRO_PLAIN, EPI_STORE, a, s);
 }
 
 }  // namespace gcq

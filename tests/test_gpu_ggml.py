@@ -422,17 +422,19 @@ def test_flash_attn_over_cache_views(be, orc, Sq, n_kv, H, Hkv, D):
     assert orc.parity(y, ref) < TOL
 
 
-@pytest.mark.parametrize("n_kv,H,Hkv,D", [(40, 32, 8, 128), (3000, 32, 8, 128), (700, 8, 8, 64)])
-def test_attention_merged_into_output_projection(be, orc, n_kv, H, Hkv, D):
+@pytest.mark.parametrize("t", ["q4_0", "q4_K", "q5_K"])
+@pytest.mark.parametrize("n_kv,H,Hkv,D", [(40, 32, 8, 128), (3000, 32, 8, 128), (700, 8, 8, 64), (5, 8, 2, 128)])
+def test_attention_merged_into_output_projection(be, orc, n_kv, H, Hkv, D, t):
     """flash_attn_ext of one query row -> reshape -> mul_mat -> add: the decode kernel's split
-    partials merged in the GEMV prologue (one split: its row), against the oracle and the unfused
-    graph (the attention output flagged as an output)."""
+    partials merged in the GEMV prologue (one split: its row; Q4_K / Q5_K: merged and quantized to
+    Q8_K by every wavefront, a super-block each), against the oracle and the unfused graph (the
+    attention output flagged as an output)."""
     ctx_rows, E = n_kv + 16, 512
     q = orc.normal((1, H, D), seed=140)
     kc = orc.fp32_to_fp16(orc.normal((Hkv, ctx_rows, D), seed=141))
     vc = orc.fp32_to_fp16(orc.normal((Hkv, ctx_rows, D), seed=142))
     m16 = orc.fp32_to_fp16(np.where(np.arange(n_kv) < n_kv - 3, 0.0, -np.inf).astype(np.float32)[None, :])
-    wo = _weight(orc, "q4_0", E, H * D, 143)
+    wo = _weight(orc, t, E, H * D, 143)
     r = orc.normal((1, E), seed=144)
     scale = 1.0 / math.sqrt(D)
     keep = {}
@@ -444,14 +446,14 @@ def test_attention_merged_into_output_projection(be, orc, n_kv, H, Hkv, D):
         return g.ggml_add(ctx, g.ggml_mul_mat(ctx, L["w"], g.ggml_reshape_2d(ctx, keep["a"], D * H, 1)), L["r"])
 
     leaves = {"q": (G.F32, [D, H, 1], q), "k": (G.F16, [D, ctx_rows, Hkv], kc), "v": (G.F16, [D, ctx_rows, Hkv], vc),
-              "m": (G.F16, [n_kv, 1], m16), "w": (G.Q4_0, [H * D, E], wo), "r": (G.F32, [E, 1], r)}
+              "m": (G.F16, [n_kv, 1], m16), "w": (orc.TYPES[t], [H * D, E], wo), "r": (G.F32, [E, 1], r)}
     got = {}
     for name, outs in (("fused", ()), ("split", [lambda s: keep["a"]])):
         gr = Graph(be, leaves, build, outputs=outs)
         got[name] = gr.run().copy()
         gr.close()
     att = orc.flash_attn_ext(q.transpose(1, 0, 2), kc[:, :n_kv], vc[:, :n_kv], m16, scale).reshape(1, H * D)
-    ref = orc.mul_mat(wo, "q4_0", att, H * D) + r
+    ref = orc.mul_mat(wo, t, att, H * D) + r
     assert orc.parity(got["fused"].reshape(1, E), ref) < TOL
     assert orc.parity(got["split"].reshape(1, E), ref) < TOL
 
