@@ -112,10 +112,12 @@ WeightLayout weight_layout(int type, int64_t nrows, int64_t k) {
         L.d = align256(nb * (type == T_Q4_0 ? 16 : 32));
         L.total = L.d + align256(nb * 2);
     } else if (type == T_Q6_K) {
-        const size_t nb = (size_t) nrows * (size_t) (k / QKK);
-        L.qs = 0;
-        L.d = align256(nb * 208);
-        L.total = L.d + align256(nb * 2);
+        const Q6Regions R = q6_regions(nrows * (k / QKK));
+        L.qs = R.ql;
+        L.qh = R.qh;
+        L.sc = R.sc;
+        L.d = R.d;
+        L.total = R.total;
     } else if (type == T_Q4_K || type == T_Q5_K) {
         const KqRegions R = kq_regions(type, nrows * (k / QKK));
         L.qs = R.qs;

@@ -12,8 +12,10 @@
 //            [N][K/256][128 B], then (Q5_K) the fifth bits (qh[32]) [N][K/256][32 B], then the
 //            headers {d, dmin, scales[12]} [N][K/256][16 B], each field's bytes in ggml's order, so
 //            that consecutive lanes read consecutive 16-byte pieces of the nibbles.
-//      Q6_K: ggml's 210-byte super-block split: {ql[128], qh[64], scales[16]} [N][K/256][208 B],
-//            then fp16 d [N][K/256] (the 208 bytes in ggml's order, so loads stay 16-byte aligned).
+//      Q6_K: ggml's 210-byte super-block split by field: ql[128] [N][K/256][128 B], then qh[64]
+//            [N][K/256][64 B], then scales[16] [N][K/256][16 B], then fp16 d [N][K/256] (each
+//            field's bytes in ggml's order, so loads stay 16-byte aligned and consecutive lanes
+//            read consecutive pieces of the low bits).
 //  * Quantized activations ("act"), rows of the batch b < B:
 //      Q8_0 (for Q4_0 / Q8_0 weights): codes [B][K] int8, then per 32-block {float d, int sum}
 //            [B][K/32]: d is the fp16 scale ggml stores (as its exact f32 value) and sum the
@@ -80,7 +82,8 @@ size_t row_bytes(int type, int64_t n);
 // Byte offsets inside a packed weight and a quantized activation buffer.
 struct WeightLayout {
     size_t qs = 0, d = 0, total = 0;
-    size_t qh = 0;  // Q5_K: the fifth bits (Q4_K / Q5_K: d is the headers' region)
+    size_t qh = 0;  // Q5_K: the fifth bits (Q4_K / Q5_K: d is the headers' region); Q6_K: qh
+    size_t sc = 0;  // Q6_K: the scales
 };
 // The packed Q4_K / Q5_K regions of nb super-blocks, byte offsets from the weight: nibbles
 // [nb][128], Q5_K's fifth bits [nb][32], headers (d, dmin, scales[12]) [nb][16].
@@ -91,6 +94,21 @@ __host__ __device__ inline KqRegions kq_regions(int type, int64_t nb) {
     const size_t q = align256((size_t) nb * 128);
     const size_t h = type == T_Q5_K ? q + align256((size_t) nb * 32) : q;
     return {0, q, h, h + align256((size_t) nb * 16)};
+}
+// The packed Q6_K regions of nb super-blocks: ql [nb][128], qh [nb][64], scales [nb][16], d [nb] fp16.
+struct Q6Regions {
+    size_t ql, qh, sc, d, total;
+};
+__host__ __device__ inline Q6Regions q6_regions(int64_t nb) {
+    const size_t qh = align256((size_t) nb * 128), sc = qh + align256((size_t) nb * 64);
+    const size_t d = sc + align256((size_t) nb * 16);
+    return {0, qh, sc, d, d + align256((size_t) nb * 2)};
+}
+// Byte x of ggml's first 208 bytes of super-block bi (ql[128] at 0, qh[64] at 128, scales[16] at
+// 192) in a packed Q6_K weight: its offset from the weight. 16-byte pieces stay 16-byte aligned.
+__host__ __device__ inline size_t q6_off(const Q6Regions & R, int64_t bi, int x) {
+    return x < 128 ? R.ql + (size_t) bi * 128 + x
+                   : x < 192 ? R.qh + (size_t) bi * 64 + (x - 128) : R.sc + (size_t) bi * 16 + (x - 192);
 }
 WeightLayout weight_layout(int type, int64_t nrows, int64_t k);
 struct ActLayout {
@@ -179,8 +197,9 @@ void launch_row_gemv(int type, int pro, int epi, const RowArgs & a, hipStream_t 
 // ranges; false when they span 2 GB or more.
 bool row_gemv_ranges(int type, int n, const uint8_t * const * w, const int64_t * N, int64_t K, RowArgs & a);
 
-// The K-quant decode-row GEMV (rowgemv_kq.hip): a Q4_K / Q5_K weight in ggml's super-block layout
-// times one f32 row, quantized to Q8_K (optionally rms-normalized first) inside the launch.
+// The K-quant decode-row GEMV (rowgemv_kq.hip): a packed Q4_K / Q5_K / Q6_K weight times one f32
+// row, quantized to Q8_K (optionally rms-normalized or merged from attention partials first)
+// inside the launch.
 struct RowKqArgs {
     const uint8_t * w;     // the packed weight; several weights: the lowest of them
     const float * x;       // the activation row [K]
@@ -197,6 +216,7 @@ struct RowKqArgs {
     int nr;  // 0 or 1: one weight
     int r_end[3];
     uint32_t r_qs[3], r_qh[3], r_hdr[3], span;
+    uint32_t r_d[3];  // Q6_K: weight k's fp16 d (its r_qs / r_qh / r_hdr: ql, qh, scales)
     float * r_y[3];
     // PRO_MERGE: the attention row from split partials o [H][nsplit][D], (max, exp-sum) [H][nsplit]
     const float * part_o;
@@ -219,6 +239,8 @@ bool row_gemv_kq_ranges(int type, int n, const uint8_t * const * w, const int64_
 // take rows of at most 4096 values).
 bool row_gemv_kq_epi_fits(int type, int epi, int64_t K);
 void launch_row_gemv_kq_epi(int type, int pro, int epi, const RowKqArgs & a, hipStream_t s);
+// One packed weight of N rows of K as RowKqArgs' weight fields (w, ranges, span, N, ntask).
+void row_gemv_kq_one(int type, const void * w, int64_t N, int64_t K, RowKqArgs & a);
 
 // Shapes and byte strides of a strided copy / conversion (elementwise.hip).
 struct Cpy4 {
@@ -717,12 +739,13 @@ __device__ __forceinline__ float kquant_table_value(int type, const uint8_t * ta
     const int64_t bi = r * nsb + c / QKK;
     auto byte = [](const uint8_t * p, int i) { return (int) p[i]; };
     if (type == T_Q6_K) {
-        const uint8_t * b = tab + bi * 208;
-        const uint16_t * dv = reinterpret_cast<const uint16_t *>(tab + align256((size_t) nrows * nsb * 208));
+        const Q6Regions R = q6_regions(nrows * nsb);
+        const uint16_t * dv = reinterpret_cast<const uint16_t *>(tab + R.d);
         const int h = w / 128, qq = (w % 128) / 32, l = w % 32;
-        const int a = byte(b, 64 * h + 32 * (qq & 1) + l), qh = byte(b, 128 + 32 * h + l);
+        const int a = (int) tab[q6_off(R, bi, 64 * h + 32 * (qq & 1) + l)];
+        const int qh = (int) tab[q6_off(R, bi, 128 + 32 * h + l)];
         const int q = ((qq < 2 ? a & 0xF : a >> 4) | (((qh >> (2 * qq)) & 3) << 4)) - 32;
-        const int sc = (int) reinterpret_cast<const int8_t *>(b + 192 + 8 * h)[l / 16 + 2 * qq];
+        const int sc = (int) reinterpret_cast<const int8_t *>(tab + q6_off(R, bi, 192 + 8 * h))[l / 16 + 2 * qq];
         return __fmul_rn(__fmul_rn(h2f(dv[bi]), (float) sc), (float) q);
     }
     const KqRegions R = kq_regions(type, nrows * nsb);

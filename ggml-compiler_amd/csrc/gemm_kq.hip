@@ -40,7 +40,7 @@ constexpr int KP = HV + 16;        // LDS row pitch of the codes (bytes; 16 B pa
 
 template <int TYPE>
 struct Kq {
-    static constexpr int BB = TYPE == T_Q4_K || TYPE == T_Q5_K ? 128 : 208;  // device block bytes (nibbles / Q6_K's)
+    static constexpr int BB = 128;  // the low bits' bytes per super-block (nibbles / Q6_K's ql)
     static constexpr bool MIN = TYPE != T_Q6_K;  // a min term (Q4_K / Q5_K)
     static constexpr int NSUB = TYPE == T_Q6_K ? 16 : 8;  // scales per super-block
 };
@@ -78,10 +78,10 @@ __device__ __forceinline__ void scale_min(const uint32_t (&q)[3], int j, int & s
 
 template <int TYPE>
 struct KqArgs {
-    const uint8_t * w;      // packed weight: [N][nsb] blocks of Kq::BB bytes (Q4_K / Q5_K: the nibbles)
+    const uint8_t * w;      // packed weight's low bits: [N][nsb][128] (nibbles / Q6_K's ql)
     const uint16_t * wd;    // Q6_K: fp16 d [N][nsb]
-    const uint8_t * wqh;    // Q5_K: the fifth bits [N][nsb][32]
-    const uint8_t * whdr;   // Q4_K / Q5_K: the headers (d, dmin, scales[12]) [N][nsb][16]
+    const uint8_t * wqh;    // Q5_K: the fifth bits [N][nsb][32]; Q6_K: qh [N][nsb][64]
+    const uint8_t * whdr;   // Q4_K / Q5_K: the headers (d, dmin, scales[12]) [N][nsb][16]; Q6_K: scales[16]
     const int8_t * xc;      // Q8_K codes [M][K]
     const int16_t * xbs;    // block sums [M][K / 16]
     const float * xd;       // d [M][K / 256]
@@ -106,10 +106,11 @@ __device__ __forceinline__ void kq_load(KqStage<TYPE> & st, const KqArgs<TYPE> &
     if constexpr (TYPE == T_Q6_K) {
         if (t < 2 * TN) {  // row t / 2, bytes l0 .. l0 + 15 of each 32 of the half
             const int row = t >> 1, l0 = 16 * (t & 1);
-            const uint8_t * blk = a.w + ((size_t) min(n0 + row, a.N - 1) * a.nsb + sb) * Kq<TYPE>::BB;
-            st.b = *reinterpret_cast<const v4i *>(blk + 64 * h + l0);
-            st.b2 = *reinterpret_cast<const v4i *>(blk + 64 * h + 32 + l0);
-            st.b3 = *reinterpret_cast<const v4i *>(blk + 128 + 32 * h + l0);
+            const size_t bi = (size_t) min(n0 + row, a.N - 1) * a.nsb + sb;
+            const uint8_t * ql = a.w + bi * 128;
+            st.b = *reinterpret_cast<const v4i *>(ql + 64 * h + l0);
+            st.b2 = *reinterpret_cast<const v4i *>(ql + 64 * h + 32 + l0);
+            st.b3 = *reinterpret_cast<const v4i *>(a.wqh + bi * 64 + 32 * h + l0);
         }
     } else if (t < 4 * TN) {
         // row t / 4, u = t % 4: 16 B of nibbles (and Q5_K the matching 16 B of qh)
@@ -121,8 +122,7 @@ __device__ __forceinline__ void kq_load(KqStage<TYPE> & st, const KqArgs<TYPE> &
     if (h == 0) {
         if (t < TN) {
             const size_t bi = (size_t) min(n0 + t, a.N - 1) * a.nsb + sb;
-            if constexpr (TYPE == T_Q6_K) st.e0 = *reinterpret_cast<const v4i *>(a.w + bi * Kq<TYPE>::BB + 192);
-            else st.e0 = *reinterpret_cast<const v4i *>(a.whdr + bi * 16);
+            st.e0 = *reinterpret_cast<const v4i *>(a.whdr + bi * 16);  // header / Q6_K scales
             if constexpr (TYPE == T_Q6_K) st.dw = a.wd[bi];
         } else if (t < TN + TM) {
             const int m = min(m0 + t - TN, a.M - 1);
@@ -391,8 +391,8 @@ void run_kq(const void * wv, int64_t N, int64_t K, const void * act, int64_t M, 
     KqArgs<TYPE> a{};
     a.w = w + WL.qs;
     a.wd = TYPE == T_Q6_K ? (const uint16_t *) (w + WL.d) : nullptr;
-    a.wqh = TYPE == T_Q5_K ? w + WL.qh : nullptr;
-    a.whdr = TYPE == T_Q6_K ? nullptr : w + WL.d;
+    a.wqh = TYPE == T_Q4_K ? nullptr : w + WL.qh;
+    a.whdr = TYPE == T_Q6_K ? w + WL.sc : w + WL.d;
     a.xc = (const int8_t *) (x + AL.codes);
     a.xbs = (const int16_t *) (x + AL.meta);
     a.xd = (const float *) (x + AL.d);

@@ -791,7 +791,7 @@ __global__ __launch_bounds__(256) void k_gemv_q5_K(const uint8_t * __restrict__ 
         }
 }
 
-// Q6_K (packed: 208-byte super-blocks, fp16 d apart): lane task = (super-block, half hh, ql
+// Q6_K (packed: ql / qh / scales / d fields): lane task = (super-block, half hh, ql
 // part jj), 4 tasks per super-block: 32 ql + 32 qh bytes, the half's 8 scale bytes and d.
 template <int B, int R, int NBL>
 __global__ __launch_bounds__(256) void k_gemv_q6_K(const uint8_t * __restrict__ wqs, const uint16_t * __restrict__ wd,
@@ -803,6 +803,7 @@ __global__ __launch_bounds__(256) void k_gemv_q6_K(const uint8_t * __restrict__ 
     if (row0 >= N) return;
     const int K = nsb * QKK;
     const int ntask = nsb * 4;
+    const Q6Regions R6 = q6_regions((int64_t) N * nsb);
     float acc[R][B];
 #pragma unroll
     for (int r = 0; r < R; r++)
@@ -822,12 +823,12 @@ __global__ __launch_bounds__(256) void k_gemv_q6_K(const uint8_t * __restrict__ 
                 for (int r = 0; r < R; r++) {
                     const int row = min(row0 + r, N - 1);
                     const size_t blk = (size_t) row * nsb + sb;
-                    const uint4 * p = reinterpret_cast<const uint4 *>(wqs + blk * 208);
-                    la[i][r] = p[4 * hh + 2 * jj];
-                    lb[i][r] = p[4 * hh + 2 * jj + 1];
-                    ha[i][r] = p[8 + 2 * hh];
-                    hb[i][r] = p[9 + 2 * hh];
-                    sc[i][r] = *reinterpret_cast<const uint2 *>(wqs + blk * 208 + 192 + 8 * hh);
+                    auto piece = [&](int k) { return *reinterpret_cast<const uint4 *>(wqs + q6_off(R6, blk, 16 * k)); };
+                    la[i][r] = piece(4 * hh + 2 * jj);
+                    lb[i][r] = piece(4 * hh + 2 * jj + 1);
+                    ha[i][r] = piece(8 + 2 * hh);
+                    hb[i][r] = piece(9 + 2 * hh);
+                    sc[i][r] = *reinterpret_cast<const uint2 *>(wqs + q6_off(R6, blk, 192 + 8 * hh));
                     dw[i][r] = wd[blk];
                 }
             }
@@ -966,7 +967,9 @@ __global__ void k_isums_q6_K(const uint8_t * wqs, const int8_t * xc, const int16
     const int b = (int) (t / ((int64_t) nsb * N));
     const int K = nsb * QKK;
     const size_t blk = (size_t) n * nsb + sb;
-    const uint4 * p = reinterpret_cast<const uint4 *>(wqs + blk * 208);
+    const Q6Regions R6 = q6_regions((int64_t) N * nsb);
+    uint4 p[13];  // ggml's first 208 bytes of the super-block, from their fields
+    for (int k = 0; k < 13; k++) p[k] = *reinterpret_cast<const uint4 *>(wqs + q6_off(R6, blk, 16 * k));
     int32_t * o = out + t * 17;
     int total = 0;
     for (int task = 0; task < 4; task++) {
@@ -981,7 +984,7 @@ __global__ void k_isums_q6_K(const uint8_t * wqs, const int8_t * xc, const int16
         const int s0 = 8 * hh + 2 * jj;
         const int sub[4] = {s0, s0 + 1, s0 + 4, s0 + 5};
         for (int k = 0; k < 4; k++) o[sub[k]] = dd[k] - 32 * bs[sub[k]];
-        const uint2 sc8 = *reinterpret_cast<const uint2 *>(wqs + blk * 208 + 192 + 8 * hh);
+        const uint2 sc8 = *reinterpret_cast<const uint2 *>(wqs + q6_off(R6, blk, 192 + 8 * hh));
         const uint32_t * bsw = reinterpret_cast<const uint32_t *>(bs + s0);
         total += isum_q6_K_task(dd, sc8, jj, bsw[0], bsw[2]);
     }

@@ -165,11 +165,11 @@ bool q8_mul_mat(const ggml_tensor * mm) {
            a->ne[3] == 1;
 }
 
-// A mul_mat of one row by a Q4_K / Q5_K weight that the K-quant row GEMV runs with the rms_norm
-// prologue.
+// A mul_mat of one row by a Q4_K / Q5_K / Q6_K weight that the K-quant row GEMV runs with the
+// rms_norm prologue.
 bool kq_norm_mul_mat(const ggml_tensor * mm) {
     const ggml_tensor * a = mm->src[0];
-    return (a->type == GGML_TYPE_Q4_K || a->type == GGML_TYPE_Q5_K) && whole_packed(a) && a->ne[2] == 1 &&
+    return is_kquant(a->type) && whole_packed(a) && a->ne[2] == 1 &&
            a->ne[3] == 1 && ggml_nrows(mm->src[1]) == 1 && row_gemv_kq_norm_fits(a->type, a->ne[1], a->ne[0]);
 }
 
@@ -184,11 +184,11 @@ bool weights_fit_one_launch(int type, int n, const uint8_t * const * w, const in
     return row_gemv_ranges(type, n, w, N, K, a);
 }
 
-// A mul_mat of one row by a Q4_K / Q5_K weight of rows up to 4096 values that the K-quant row
-// GEMV runs with the attention-merge prologue.
+// A mul_mat of one row by a Q4_K / Q5_K / Q6_K weight of rows up to 4096 values that the K-quant
+// row GEMV runs with the attention-merge prologue.
 bool kq_merge_mul_mat(const ggml_tensor * mm) {
     const ggml_tensor * a = mm->src[0];
-    return (a->type == GGML_TYPE_Q4_K || a->type == GGML_TYPE_Q5_K) && whole_packed(a) && a->ne[2] == 1 &&
+    return is_kquant(a->type) && whole_packed(a) && a->ne[2] == 1 &&
            a->ne[3] == 1 && ggml_nrows(mm->src[1]) == 1 && a->ne[0] <= 4096 && row_gemv_kq_fits(a->type, a->ne[1], a->ne[0]);
 }
 
@@ -870,7 +870,7 @@ struct Planner {
         const uint8_t * w[3];
         int64_t N[3], K = 0;
         bool ok = grp.size() >= 2 && grp.size() <= 3 &&
-                  (type == GGML_TYPE_Q4_0 || type == GGML_TYPE_Q8_0 || type == GGML_TYPE_Q4_K || type == GGML_TYPE_Q5_K);
+                  (type == GGML_TYPE_Q4_0 || type == GGML_TYPE_Q8_0 || is_kquant(type));
         for (size_t k = 0; ok && k < grp.size(); k++) {
             const ggml_tensor * mm = g->nodes[grp[k]];
             const ggml_tensor * wt = mm->src[0];
@@ -1718,15 +1718,8 @@ void run_step(const ggml_backend * be, const Step & s) {
                                (int) D, (int) H, (int) Hkv, (int) n_kv, nullptr, s.f[0], nsplit, chunk, (int) n_kv, GS,
                                row, po, pml, st, nullptr, s.in[3], 16);
             if (is_kquant(s.type)) {  // the K-quant row GEMV, the row merged (or read) in its prologue
-                const WeightLayout L = weight_layout(s.type, N, K);
                 RowKqArgs a{};
-                a.w = (const uint8_t *) s.in[4];
-                a.r_qs[0] = (uint32_t) L.qs;
-                a.r_qh[0] = (uint32_t) L.qh;
-                a.r_hdr[0] = (uint32_t) L.d;
-                a.span = (uint32_t) L.total;
-                a.N = (int) N;
-                a.ntask = (int) (K / 32);
+                row_gemv_kq_one(s.type, s.in[4], N, K, a);
                 a.y = (float *) s.out;
                 a.res = (const float *) s.in[5];
                 if (nsplit == 1) {

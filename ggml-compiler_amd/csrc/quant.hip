@@ -405,7 +405,7 @@ __global__ void k_pack(const uint8_t * __restrict__ src, uint8_t * __restrict__ 
 }
 
 // ggml block_q6_K rows -> packed: the first 208 bytes (ql, qh, scales) of each 210-byte block as
-// 13 aligned 16-byte words, the fp16 d into its own array; one thread per word.
+// 13 aligned 16-byte pieces into their fields, the fp16 d into its own array; one thread per piece.
 __global__ void k_pack_q6_K(const uint8_t * __restrict__ src, uint8_t * __restrict__ qs, uint16_t * __restrict__ d,
                             int64_t nblocks) {
     const int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
@@ -417,7 +417,7 @@ __global__ void k_pack_q6_K(const uint8_t * __restrict__ src, uint8_t * __restri
 #pragma unroll
     for (int j = 0; j < 4; j++)
         w[j] = b[4 * j] | (b[4 * j + 1] << 8) | (b[4 * j + 2] << 16) | ((uint32_t) b[4 * j + 3] << 24);
-    reinterpret_cast<uint4 *>(qs)[t] = make_uint4(w[0], w[1], w[2], w[3]);
+    *reinterpret_cast<uint4 *>(qs + q6_off(q6_regions(nblocks), i, 16 * c)) = make_uint4(w[0], w[1], w[2], w[3]);
     if (c == 0) d[i] = (uint16_t) (src[i * 210 + 208] | (src[i * 210 + 209] << 8));
 }
 
@@ -428,7 +428,7 @@ __global__ void k_unpack_q6_K(const uint8_t * __restrict__ qs, const uint16_t * 
     if (t >= nblocks * 210) return;
     const int64_t i = t / 210;
     const int j = (int) (t % 210);
-    dst[t] = j < 208 ? qs[i * 208 + j] : (uint8_t) (d[i] >> (8 * (j - 208)));
+    dst[t] = j < 208 ? qs[q6_off(q6_regions(nblocks), i, j)] : (uint8_t) (d[i] >> (8 * (j - 208)));
 }
 
 // Whole ggml rows moved by a row map, 16 bytes per thread (row_bytes % 16 == 0) or 2 (otherwise):
@@ -530,10 +530,11 @@ __global__ void k_dequant_q6_K(const uint8_t * __restrict__ qs, const uint16_t *
     if (t >= nblocks * 64) return;
     const int64_t i = t / 64;
     const int h = (int) (t % 64) / 32, l = (int) (t % 32);
-    const uint8_t * b = qs + i * 208;
+    const Q6Regions R = q6_regions(nblocks);
     const float d = h2f(dv[i]);
-    const uint8_t a0 = b[64 * h + l], a1 = b[64 * h + 32 + l], qh = b[128 + 32 * h + l];
-    const int8_t * sc = reinterpret_cast<const int8_t *>(b + 192 + 8 * h);
+    const uint8_t a0 = qs[q6_off(R, i, 64 * h + l)], a1 = qs[q6_off(R, i, 64 * h + 32 + l)];
+    const uint8_t qh = qs[q6_off(R, i, 128 + 32 * h + l)];
+    const int8_t * sc = reinterpret_cast<const int8_t *>(qs + q6_off(R, i, 192 + 8 * h));
     const int is = l / 16;
     const int q1 = (int) ((a0 & 0xF) | (((qh >> 0) & 3) << 4)) - 32;
     const int q2 = (int) ((a1 & 0xF) | (((qh >> 2) & 3) << 4)) - 32;

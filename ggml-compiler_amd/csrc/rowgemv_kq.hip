@@ -42,7 +42,9 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
     constexpr bool NORM = PRO == PRO_NORM, MERGE = PRO == PRO_MERGE;
     static_assert(!MERGE || NBL <= 2, "the merge prologue takes rows of at most 4096 values");
     constexpr int NWV = 16;
-    constexpr int WV = TYPE == T_Q5_K ? 2 : 1;     // 16-byte loads per task: nibbles, Q5_K's fifth bits
+    constexpr bool Q6 = TYPE == T_Q6_K;
+    // 16-byte loads per task: the low bits (nibbles / Q6_K's ql), Q5_K's fifth bits / Q6_K's qh
+    constexpr int WV = TYPE == T_Q4_K ? 1 : 2;
     constexpr bool XREG = NBL <= 2;                // the task activations in registers
     constexpr bool PF = WV * NBL * R <= 4;         // the next group's weights prefetched
     // x waves: at most 4 (8 for rows past 8192 values); rounds of 16 values per x thread: K / 16
@@ -116,15 +118,23 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
     const uint32_t oq0 = rfl(a.r_qs[0]), oq1 = rfl(a.r_qs[1]), oq2 = rfl(a.r_qs[2]);
     const uint32_t oh0 = rfl(a.r_hdr[0]), oh1 = rfl(a.r_hdr[1]), oh2 = rfl(a.r_hdr[2]);
     const uint32_t ob0 = rfl(a.r_qh[0]), ob1 = rfl(a.r_qh[1]), ob2 = rfl(a.r_qh[2]);
+    const uint32_t od0 = rfl(a.r_d[0]), od1 = rfl(a.r_d[1]), od2 = rfl(a.r_d[2]);
     auto pick_u = [](int k, uint32_t v0, uint32_t v1, uint32_t v2) { return k == 2 ? v2 : k == 1 ? v1 : v0; };
 
-    // Per task and row: the 16 nibble bytes (Q5_K: and the half's 16 qh bytes) and word t % 4 of
-    // the super-block's 16-byte header, the quad's four lanes holding the whole header.
-    uint4 w[NBL][R][WV], wn[NBL][R][WV];
-    uint32_t hw[NBL][R], hwn[NBL][R];
-    auto load = [&](int gg, uint4 (&wv)[NBL][R][WV], uint32_t (&hv)[NBL][R]) {
+    // Per task and row (Q4_K / Q5_K): the 16 nibble bytes (Q5_K: and the half's 16 qh bytes) and
+    // word t % 4 of the super-block's 16-byte header, the quad's four lanes holding the whole
+    // header. Q6_K: the 16 ql bytes, the 16 qh bytes of its half, its 8 scale bytes, the 32-bit
+    // word holding its super-block's fp16 d.
+    struct Buf {
+        uint4 q[NBL][R][WV];
+        uint32_t h[NBL][R];
+        uint2 s[Q6 ? NBL : 1][Q6 ? R : 1];
+    };
+    Buf wa, wb;
+    auto load = [&](int gg, Buf & b) {
         const bool live = gg < ng;
-        uint32_t rq0[R], rh0[R], rqh0[R];  // each row's nibbles, headers, fifth bits: byte offsets
+        // each row's fields: byte offsets (Q6_K: r_hdr holds the scales, r_d the d values)
+        uint32_t rq0[R], rh0[R], rqh0[R], rd0[R];
         bool rin[R];
 #pragma unroll
         for (int r = 0; r < R; r++) {
@@ -132,7 +142,8 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
             const int k = map_row(gg, r, local);
             rq0[r] = pick_u(k, oq0, oq1, oq2) + (uint32_t) local * (uint32_t) ntask * 16u;
             rh0[r] = pick_u(k, oh0, oh1, oh2) + (uint32_t) local * (uint32_t) nsb * 16u;
-            rqh0[r] = pick_u(k, ob0, ob1, ob2) + (uint32_t) local * (uint32_t) nsb * 32u;
+            rqh0[r] = pick_u(k, ob0, ob1, ob2) + (uint32_t) local * (uint32_t) nsb * (Q6 ? 64u : 32u);
+            rd0[r] = pick_u(k, od0, od1, od2) + (uint32_t) local * (uint32_t) nsb * 2u;
             rin[r] = live && (EPI != EPI_STORE || gg * R + r < a.N);
         }
         // long rows: the tasks' offsets recomputed per group from an opaque lane index (held
@@ -146,15 +157,30 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
 #pragma unroll
             for (int r = 0; r < R; r++) {
                 const bool in = rin[r] && t < ntask;
-                hv[i][r] = __builtin_amdgcn_raw_buffer_load_b32(rq, in ? rh0[r] + 16u * sb + 4u * (uint32_t) (t & 3) : kKqPast,
-                                                                0, 0);
-                // the nibbles streamed (nt); the qh bytes, read by four lanes, cached
+                if constexpr (Q6) {
+                    // task t: super-block t / 8, half n = (t / 4) % 2, ql part (t / 2) % 2, l half t % 2
+                    const uint32_t n = (uint32_t) ((t >> 2) & 1);
+                    const uint32_t dof = rd0[r] + 2u * sb;  // the fp16 d: its aligned word
+                    b.h[i][r] = __builtin_amdgcn_raw_buffer_load_b32(rq, in ? dof & ~3u : kKqPast, 0, 0);
+                    const auto sc = __builtin_amdgcn_raw_buffer_load_b64(rq, in ? rh0[r] + 16u * sb + 8u * n : kKqPast, 0, 0);
+                    b.s[i][r] = make_uint2(sc[0], sc[1]);
+                } else {
+                    b.h[i][r] = __builtin_amdgcn_raw_buffer_load_b32(
+                        rq, in ? rh0[r] + 16u * sb + 4u * (uint32_t) (t & 3) : kKqPast, 0, 0);
+                }
+                // the low bits streamed (nt); the high bits, read by two (Q6_K) or four lanes, cached
                 const auto q = __builtin_amdgcn_raw_buffer_load_b128(rq, in ? rq0[r] + 16u * (uint32_t) t : kKqPast, 0, 2);
-                wv[i][r][0] = make_uint4(q[0], q[1], q[2], q[3]);
+                b.q[i][r][0] = make_uint4(q[0], q[1], q[2], q[3]);
                 if constexpr (TYPE == T_Q5_K) {
                     const auto qh = __builtin_amdgcn_raw_buffer_load_b128(
                         rq, in ? rqh0[r] + 32u * sb + 16u * (uint32_t) (t & 1) : kKqPast, 0, 0);
-                    wv[i][r][1] = make_uint4(qh[0], qh[1], qh[2], qh[3]);
+                    b.q[i][r][1] = make_uint4(qh[0], qh[1], qh[2], qh[3]);
+                }
+                if constexpr (Q6) {
+                    const uint32_t n = (uint32_t) ((t >> 2) & 1);
+                    const auto qh = __builtin_amdgcn_raw_buffer_load_b128(
+                        rq, in ? rqh0[r] + 64u * sb + 32u * n + 16u * (uint32_t) (t & 1) : kKqPast, 0, 0);
+                    b.q[i][r][1] = make_uint4(qh[0], qh[1], qh[2], qh[3]);
                 }
             }
         }
@@ -163,6 +189,20 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
     auto hword = [](uint32_t v, auto KI) -> uint32_t {
         constexpr int k = decltype(KI)::value;
         return (uint32_t) __builtin_amdgcn_mov_dpp((int) v, k | (k << 2) | (k << 4) | (k << 6), 0xF, 0xF, false);
+    };
+
+    // The task holding 16-value group gi of the row and which of its two 16s it is (sel). Q4_K /
+    // Q5_K: group 4c + 2 sel + h of a super-block is sub-block 2c + sel, values 16h..; Q6_K: group
+    // 8n + 4 sel + 2jj + h is half n, ql part jj, the low (sel 0) or high (1) nibbles, l half h.
+    auto task_of = [](int gi, int & sel) -> int {
+        const int gg = gi & 15;
+        if constexpr (Q6) {
+            sel = (gg >> 2) & 1;
+            return 8 * (gi >> 4) + 4 * (gg >> 3) + (gg & 3);
+        } else {
+            sel = (gg >> 1) & 1;
+            return 8 * (gi >> 4) + 2 * (gg >> 2) + (gg & 1);
+        }
     };
 
     if constexpr (MERGE) {
@@ -190,7 +230,7 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
-        load(g, w, hw);
+        load(g, wa);
         const int e = (int) threadIdx.x * 4;
         float vv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         if (e < K) {
@@ -256,8 +296,9 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
         s4 += lane_pair_i<1>(s4);
         s4 += lane_pair_i<2>(s4);  // the 16-value group's bsum (its 4 lanes)
         if (e < K) {
-            const int gi = (int) threadIdx.x >> 2, gg = gi & 15, sel = (gg >> 1) & 1;
-            const int t = 8 * (gi >> 4) + 2 * (gg >> 2) + (gg & 1);
+            const int gi = (int) threadIdx.x >> 2;
+            int sel;
+            const int t = task_of(gi, sel);
             reinterpret_cast<int *>(lc + sel * ntask + t)[threadIdx.x & 3] = word;
             if ((threadIdx.x & 3) == 0) reinterpret_cast<int16_t *>(lbp)[2 * t + sel] = (int16_t) s4;
             if (lane == 0) ld[wave] = d;  // the wavefront's 256 values are super-block `wave`
@@ -372,10 +413,8 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
                             ((q[4 * k + 3] & 0xff) << 24);
 #pragma unroll
                 for (int j = 0; j < 16; j++) s += q[j];
-                // group gi: super-block gi / 16, sub-block 2c + sel (gi % 16 = 4c + 2 sel + h), the
-                // 16s of task 8 (gi / 16) + 2c + h
-                const int gg = gi & 15, sel = (gg >> 1) & 1;
-                const int t = 8 * (gi >> 4) + 2 * (gg >> 2) + (gg & 1);
+                int sel;
+                const int t = task_of(gi, sel);
                 lc[sel * ntask + t] = make_int4(pk[0], pk[1], pk[2], pk[3]);
                 reinterpret_cast<int16_t *>(lbp)[2 * t + sel] = (int16_t) s;
                 if ((lane & 15) == 0) ld[gi >> 4] = d;
@@ -384,15 +423,15 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
         }
         if (lane == 0) lds_signal(&s_flag);
         if (!XC) return;
-        load(g, w, hw);
+        load(g, wa);
     } else {
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
-        load(g, w, hw);
+        load(g, wa);
     }
     lds_wait(&s_flag, MERGE ? NWV : XW);
-    if constexpr (PF) load(g + nw, wn, hwn);
+    if constexpr (PF) load(g + nw, wb);
 
     // The lane's task activations: the 16 codes of sub-block 2c, of 2c + 1, d_x, bs0 d_x, bs1 d_x.
     int4 xa[XREG ? NBL : 1], xb[XREG ? NBL : 1];
@@ -412,8 +451,13 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
             cb = lc[ntask + t];
             ds = ld[t >> 3];
             const uint32_t bp = lbp[t];
-            o1 = (float) (int) (int16_t) (bp & 0xffffu) * ds;
-            o2 = (float) (int) (int16_t) (bp >> 16) * ds;
+            if constexpr (Q6) {  // -32 bsum of each 16 (Q6_K's offset), as integers in float registers
+                o1 = __int_as_float(-32 * (int) (int16_t) (bp & 0xffffu));
+                o2 = __int_as_float(-32 * (int) (int16_t) (bp >> 16));
+            } else {
+                o1 = (float) (int) (int16_t) (bp & 0xffffu) * ds;
+                o2 = (float) (int) (int16_t) (bp >> 16) * ds;
+            }
         } else {
             ca = make_int4(0, 0, 0, 0);
             cb = ca;
@@ -437,10 +481,23 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
     const uint32_t csh = 16u * (uint32_t) (c & 1);
     const uint32_t chim = c >= 2 ? 0xFFFFFFFFu : 0u;
 
-    auto group = [&](int gg, const uint4 (&wv)[NBL][R][WV], const uint32_t (&hv)[NBL][R]) {
+    // Q6_K: the task's ql part (t / 2) % 2 picks the qh bit pairs; byte t % 4 of its scale words;
+    // the half of the d word its super-block's parity picks (rows of an odd number of super-blocks
+    // alternate it per row)
+    const uint32_t sh6 = 2u * (uint32_t) ((lane >> 1) & 1);
+    const uint32_t bsel = 8u * (uint32_t) (lane & 3);
+    const int sbp = (lane >> 3) & 1;
+
+    auto group = [&](int gg, const Buf & b) {
         float acc[R];
+        int dsh[R];  // Q6_K: each row's d half
 #pragma unroll
-        for (int r = 0; r < R; r++) acc[r] = 0.0f;
+        for (int r = 0; r < R; r++) {
+            acc[r] = 0.0f;
+            int local = 0;
+            if constexpr (Q6) (void) map_row(gg, r, local);
+            dsh[r] = 16 * ((local & nsb & 1) ^ sbp);
+        }
 #pragma unroll
         for (int i = 0; i < NBL; i++) {
             int4 ca, cb;
@@ -456,9 +513,27 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
             }
 #pragma unroll
             for (int r = 0; r < R; r++) {
+                if constexpr (Q6) {
+                    // the task's 16 values of its first 16-group (low nibbles of ql, qh bits 2jj) and
+                    // of the group 64 values on (high nibbles, qh bits 2jj + 4): 6-bit codes q, the
+                    // products sum sc (q - 32) x
+                    int lo6[4], hi6[4];
+                    const uint4 ql = b.q[i][r][0], qh = b.q[i][r][1];
+                    const uint32_t lw[4] = {ql.x, ql.y, ql.z, ql.w}, hw6[4] = {qh.x, qh.y, qh.z, qh.w};
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        lo6[j] = (int) ((lw[j] & 0x0F0F0F0Fu) | (((hw6[j] >> sh6) & 0x03030303u) << 4));
+                        hi6[j] = (int) (((lw[j] >> 4) & 0x0F0F0F0Fu) | (((hw6[j] >> (sh6 + 4)) & 0x03030303u) << 4));
+                    }
+                    const int sc1 = (int) (int8_t) (b.s[i][r].x >> bsel), sc2 = (int) (int8_t) (b.s[i][r].y >> bsel);
+                    const int isum = sc1 * (dot16(lo6, ca) + __float_as_int(o1)) + sc2 * (dot16(hi6, cb) + __float_as_int(o2));
+                    const float dd = h2f((uint16_t) (b.h[i][r] >> dsh[r]));
+                    acc[r] += ((float) isum * dd) * ds;
+                    continue;
+                }
                 // the task's 16 values of sub-block 2c (low nibbles) and of 2c + 1 (high nibbles)
                 int lo[4], hi[4];
-                const uint4 q = wv[i][r][0];
+                const uint4 q = b.q[i][r][0];
                 const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
@@ -466,7 +541,7 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
                     hi[j] = (int) ((qw[j] >> 4) & 0x0F0F0F0Fu);
                 }
                 if constexpr (TYPE == T_Q5_K) {  // the fifth bits: bit 2c of qh[l] (sub-block 2c), 2c + 1
-                    const uint4 qh = wv[i][r][1];
+                    const uint4 qh = b.q[i][r][1];
                     const uint32_t hb[4] = {qh.x, qh.y, qh.z, qh.w};
 #pragma unroll
                     for (int j = 0; j < 4; j++) {
@@ -476,10 +551,10 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
                 }
                 // the 6-bit scales and mins of sub-blocks 2c and 2c + 1 (ggml's get_scale_min_k4)
                 using I = int;
-                const uint32_t h0 = hword(hv[i][r], std::integral_constant<I, 0>{});
-                const uint32_t A = hword(hv[i][r], std::integral_constant<I, 1>{}) >> csh;
-                const uint32_t M = hword(hv[i][r], std::integral_constant<I, 2>{}) >> csh;
-                const uint32_t H = hword(hv[i][r], std::integral_constant<I, 3>{}) >> csh;
+                const uint32_t h0 = hword(b.h[i][r], std::integral_constant<I, 0>{});
+                const uint32_t A = hword(b.h[i][r], std::integral_constant<I, 1>{}) >> csh;
+                const uint32_t M = hword(b.h[i][r], std::integral_constant<I, 2>{}) >> csh;
+                const uint32_t H = hword(b.h[i][r], std::integral_constant<I, 3>{}) >> csh;
                 // chunks 2, 3 take the high form; chosen by a mask (a select here became a branch)
                 const uint32_t scp = (chim & ((H & 0x0F0Fu) | ((A >> 2) & 0x3030u))) | (~chim & (A & 0x3F3Fu));
                 const uint32_t mp = (chim & (((H >> 4) & 0x0F0Fu) | ((M >> 2) & 0x3030u))) | (~chim & (M & 0x3F3Fu));
@@ -556,19 +631,19 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
     if constexpr (PF) {
         // two buffers in turn: a group's weights are loaded two groups ahead
         while (g < ng) {
-            group(g, w, hw);
-            load(g + 2 * nw, w, hw);
+            group(g, wa);
+            load(g + 2 * nw, wa);
             g += nw;
             if (g >= ng) break;
-            group(g, wn, hwn);
-            load(g + 2 * nw, wn, hwn);
+            group(g, wb);
+            load(g + 2 * nw, wb);
             g += nw;
         }
     } else {
         while (g < ng) {
-            group(g, w, hw);
+            group(g, wa);
             g += nw;
-            if (g < ng) load(g, w, hw);
+            if (g < ng) load(g, wa);
         }
     }
 }
@@ -590,7 +665,7 @@ void go_kq(int R, int nbl, const RowKqArgs & a, int grid, hipStream_t s) {
         GCQ_KQ(1, 2)
         GCQ_KQ(1, 3)
         GCQ_KQ(1, 4)
-        if constexpr (MR == 1 && TYPE == T_Q4_K) {  // rows past 8192 values: one Q4_K weight
+        if constexpr (MR == 1) {  // rows past 8192 values: one weight
             GCQ_KQ(1, 5)
             GCQ_KQ(1, 6)
             GCQ_KQ(1, 7)
@@ -612,9 +687,8 @@ void go_kq_t(int pro, int epi, bool multi, int R, int nbl, const RowKqArgs & a, 
 }
 
 bool kq_rows_fit(int type, int64_t K) {
-    // Q4_K rows up to 16384 values (the LDS row); Q5_K's tasks hold twice the weight registers,
-    // and rows past 8192 values would spill
-    return (type == T_Q4_K || type == T_Q5_K) && K > 0 && K % QKK == 0 && K <= (type == T_Q4_K ? kRowKqMaxK : 8192);
+    // rows up to 16384 values (the LDS row)
+    return (type == T_Q4_K || type == T_Q5_K || type == T_Q6_K) && K > 0 && K % QKK == 0 && K <= kRowKqMaxK;
 }
 
 }  // namespace
@@ -651,7 +725,8 @@ bool row_gemv_kq_ranges(int type, int n, const uint8_t * const * w, const int64_
         if (span >= 0x80000000ull) return false;
         a.r_qs[k] = (uint32_t) (o + L.qs);
         a.r_qh[k] = (uint32_t) (o + L.qh);
-        a.r_hdr[k] = (uint32_t) (o + L.d);
+        a.r_hdr[k] = (uint32_t) (o + (type == T_Q6_K ? L.sc : L.d));
+        a.r_d[k] = (uint32_t) (o + L.d);
         a.r_end[k] = (int) ((k ? a.r_end[k - 1] : 0) + N[k]);
     }
     if (total > INT32_MAX) return false;
@@ -675,7 +750,7 @@ void launch_row_gemv_kq_epi(int type, int pro, int epi, const RowKqArgs & a0, hi
             "row gemv kq: merge of 1..8 splits of D-value heads (D a multiple of 4), K <= 4096, one weight");
     const int64_t K = (int64_t) a.ntask * 32;
     require(row_gemv_kq_epi_fits(type, epi, K),
-            "row gemv kq: Q4_K / Q5_K, K a multiple of 256 up to 8192 (Q4_K 16384; 4096 for the row-pair epilogues)");
+            "row gemv kq: Q4_K / Q5_K / Q6_K, K a multiple of 256 up to 16384 (8192 for several weights, 4096 for the row-pair epilogues)");
     const bool multi = a.nr > 1;
     require(a.N > 0 && (uint64_t) a.span < 0x80000000ull && (!multi || a.r_end[a.nr - 1] == a.N),
             "row gemv kq: weights of 2 GB or more");
@@ -700,36 +775,44 @@ void launch_row_gemv_kq_epi(int type, int pro, int epi, const RowKqArgs & a0, hi
     // (Q5_K's tasks hold twice the registers: one row, whose next group's weights are prefetched);
     // the row-pair epilogues always take two
     const int R = epi != EPI_STORE || (type == T_Q4_K && nbl <= 2 && a.N / 2 >= (int64_t) cus * (16 - xw)) ? 2 : 1;
+    // (Q5_K / Q6_K: one row, as their tasks hold twice the weight registers)
     const int64_t ng = (a.N + R - 1) / R;
     // the x waves take groups too when the compute wavefronts alone would need one more round
     a.xc = pro == PRO_MERGE || (ng <= 16LL * cus && ng > (int64_t) (16 - xw) * cus);
     const int cw = a.xc ? 16 : 16 - xw;
     const int grid = (int) std::max<int64_t>(1, std::min<int64_t>(cus, (ng + cw - 1) / cw));
     if (type == T_Q4_K) go_kq_t<T_Q4_K>(pro, epi, multi, R, nbl, a, grid, s);
-    else go_kq_t<T_Q5_K>(pro, epi, multi, R, nbl, a, grid, s);
+    else if (type == T_Q5_K) go_kq_t<T_Q5_K>(pro, epi, multi, R, nbl, a, grid, s);
+    else go_kq_t<T_Q6_K>(pro, epi, multi, R, nbl, a, grid, s);
     check_launch("row gemv kq");
 }
 
-// y[n] (+ res[n]) = sum_k W[n, k] x'[k] for a packed Q4_K / Q5_K weight, x' = x or, with norm_w,
-// ggml_mul(ggml_rms_norm(x, eps), norm_w).
-void launch_row_gemv_kq(int type, const void * w, int64_t N, int64_t K, const float * x, const float * norm_w, float eps,
-                        float * y, const float * res, hipStream_t s) {
-    require(norm_w ? row_gemv_kq_norm_fits(type, N, K) : row_gemv_kq_fits(type, N, K),
-            "row gemv kq: Q4_K / Q5_K, K a multiple of 256 up to 8192 (Q4_K 16384), up to 8192 rows (16384 with the norm)");
+// One packed weight of N rows of K as RowKqArgs' weight fields.
+void row_gemv_kq_one(int type, const void * w, int64_t N, int64_t K, RowKqArgs & a) {
     const WeightLayout L = weight_layout(type, N, K);
-    RowKqArgs a{};
     a.w = (const uint8_t *) w;
     a.r_qs[0] = (uint32_t) L.qs;
     a.r_qh[0] = (uint32_t) L.qh;
-    a.r_hdr[0] = (uint32_t) L.d;
+    a.r_hdr[0] = (uint32_t) (type == T_Q6_K ? L.sc : L.d);
+    a.r_d[0] = (uint32_t) L.d;
     a.span = (uint32_t) L.total;
+    a.N = (int) N;
+    a.ntask = (int) (K / 32);
+}
+
+// y[n] (+ res[n]) = sum_k W[n, k] x'[k] for a packed Q4_K / Q5_K / Q6_K weight, x' = x or, with
+// norm_w, ggml_mul(ggml_rms_norm(x, eps), norm_w).
+void launch_row_gemv_kq(int type, const void * w, int64_t N, int64_t K, const float * x, const float * norm_w, float eps,
+                        float * y, const float * res, hipStream_t s) {
+    require(norm_w ? row_gemv_kq_norm_fits(type, N, K) : row_gemv_kq_fits(type, N, K),
+            "row gemv kq: Q4_K / Q5_K / Q6_K, K a multiple of 256 up to 16384, up to 8192 rows (16384 with the norm)");
+    RowKqArgs a{};
+    row_gemv_kq_one(type, w, N, K, a);
     a.x = x;
     a.y = y;
     a.res = res;
     a.norm_w = norm_w;
     a.eps = eps;
-    a.N = (int) N;
-    a.ntask = (int) (K / 32);
     launch_row_gemv_kq_epi(type, norm_w ? PRO_NORM : PRO_PLAIN, EPI_STORE, a, s);
 }
 

@@ -100,7 +100,7 @@ def test_mul_mat_node(be, gops, orc, t, M):
     assert np.array_equal(y, to_np(gops.mul_mat(qw, torch.from_numpy(x).cuda())))
 
 
-@pytest.mark.parametrize("t", ["q4_K", "q5_K"])
+@pytest.mark.parametrize("t", ["q4_K", "q5_K", "q6_K"])
 def test_kquant_row_mul_mat_add(be, gops, orc, t):
     """One row times a K-quant weight, then add(residual): the residual folds into the one-launch
     row kernel's store (read through the scalar unit); bit-equal to the product plus the residual
@@ -224,7 +224,7 @@ def test_sibling_gemvs_in_one_launch(be, gops, orc, t, Ns, K):
         assert orc.parity(got[i], orc.mul_mat(raw, t, xn, K)[0]) < TOL, i
 
 
-@pytest.mark.parametrize("t", ["q4_K", "q5_K"])
+@pytest.mark.parametrize("t", ["q4_K", "q5_K", "q6_K"])
 @pytest.mark.parametrize("Ns,K", [((512, 128, 128), 4096), ((1024, 1024), 2048), ((640, 64, 192), 8192)])
 def test_kquant_sibling_gemvs_in_one_launch(be, orc, t, Ns, K):
     """Two or three mul_mats of one normalized row by Q4_K / Q5_K weights run as one K-quant row
@@ -261,7 +261,7 @@ def test_kquant_sibling_gemvs_in_one_launch(be, orc, t, Ns, K):
         assert orc.parity(got[i], orc.mul_mat(raw, t, xn, K)[0]) < TOL, i
 
 
-@pytest.mark.parametrize("t", ["q4_0", "q8_0", "q4_K", "q5_K"])
+@pytest.mark.parametrize("t", ["q4_0", "q8_0", "q4_K", "q5_K", "q6_K"])
 def test_qkv_rope_cache_writes_in_one_launch(be, orc, t):
     """The decode step's q / k / v GEMVs of one normalized row, the q and k ropes and the k / v
     set_rows into f16 caches (built as the reference builds them) run as one launch whose epilogue
@@ -350,7 +350,7 @@ def test_swiglu_prologue_equals_separate_launches(be, gops, orc, t, F):
     assert orc.parity(y, orc.mul_mat(raw, t, orc.swiglu(gt, up), F) + r) < TOL
 
 
-@pytest.mark.parametrize("t", ["q4_0", "q8_0", "q4_K", "q5_K"])
+@pytest.mark.parametrize("t", ["q4_0", "q8_0", "q4_K", "q5_K", "q6_K"])
 @pytest.mark.parametrize("F,K", [(512, 2048), (14336, 4096)])
 def test_gate_up_swiglu_in_one_launch(be, orc, t, F, K):
     """The FFN of one token as the reference builds it: rms_norm -> mul -> gate and up mul_mats ->
@@ -378,7 +378,7 @@ def test_gate_up_swiglu_in_one_launch(be, orc, t, F, K):
         gr = Graph(be, leaves, build, outputs=outs)
         got[name] = gr.run().reshape(1, N)
         gr.close()
-    if t in ("q4_K", "q5_K") and F > 8192:
+    if t in ("q4_K", "q5_K", "q6_K") and F > 8192:
         # the split graph's K-quant GEMVs of more than 8192 rows run batched after a separate
         # quantization: the same int32 dots, summed in another order
         assert orc.parity(got["fused"], got["split"]) < 1e-4
@@ -422,7 +422,7 @@ def test_flash_attn_over_cache_views(be, orc, Sq, n_kv, H, Hkv, D):
     assert orc.parity(y, ref) < TOL
 
 
-@pytest.mark.parametrize("t", ["q4_0", "q4_K", "q5_K"])
+@pytest.mark.parametrize("t", ["q4_0", "q4_K", "q5_K", "q6_K"])
 @pytest.mark.parametrize("n_kv,H,Hkv,D", [(40, 32, 8, 128), (3000, 32, 8, 128), (700, 8, 8, 64), (5, 8, 2, 128)])
 def test_attention_merged_into_output_projection(be, orc, n_kv, H, Hkv, D, t):
     """flash_attn_ext of one query row -> reshape -> mul_mat -> add: the decode kernel's split

@@ -282,14 +282,14 @@ def test_gemv_row_kquant_fused_quantizer(gops, orc, t, K):
     assert orc.parity(y2, orc.mul_mat(raw2, t, x2, K)) < TOL
 
 
-@pytest.mark.parametrize("t", ["q4_K", "q5_K"])
+@pytest.mark.parametrize("t", ["q4_K", "q5_K", "q6_K"])
 @pytest.mark.parametrize("N,K", [(1, 256), (37, 768), (300, 2304), (4097, 4096), (8192, 8192), (3, 8448),
                                  (4096, 14336), (5, 16384)])
 def test_gemv_row_kquant_shapes(gops, orc, t, N, K):
-    """The one-launch K-quant row kernel at its edges: a row of one super-block (60 of 64 lanes
-    idle), ragged row counts (one row, 37, a group split by N), two chunks per lane, its largest
-    rows and row count; for Q4_K also three and four chunks per lane (the 8B down projection, the
-    longest row), which Q5_K runs batched."""
+    """The one-launch K-quant row kernel at its edges: a row of one super-block (56 of 64 lanes
+    idle; Q6_K: an odd super-block count, whose d alternates its half of a word per row), ragged
+    row counts (one row, 37, a group split by N), one to eight tasks per lane (the 8B down
+    projection, the longest row), its largest row count."""
     raw, qw = _weight(gops, orc, t, N, K, 50)
     x = orc.normal((1, K), seed=51)
     y = to_np(gops.mul_mat(qw, torch.from_numpy(x).cuda()))
