@@ -313,11 +313,16 @@ def bench_program_decode(args, w: dict | None = None) -> dict:
     import dataclasses
 
     from ggml_compiler_amd.ops import type_id
-    from ggml_compiler_amd.program import synthetic_weights
+    from ggml_compiler_amd.program import q4_k_m_types, synthetic_weights
 
     cfg = LlamaConfig.llama3_8b(max_ctx=1024)
     wtype = getattr(args, "wtype", "q4_0")
-    if wtype != "q4_0":  # a type the fused decoder does not hold: the same stream, quantized on the GPU
+    types = None
+    if wtype == "q4_K_M":  # llama.cpp's Q4_K_M mix: Q4_K with Q6_K lm head, and attn_v / ffn_down in some layers
+        cfg = dataclasses.replace(cfg, wtype=type_id("q4_K"))
+        types = q4_k_m_types(cfg)
+        w = synthetic_weights(cfg, seed=0, std=0.02, types=types)
+    elif wtype != "q4_0":  # a type the fused decoder does not hold: the same stream, quantized on the GPU
         cfg = dataclasses.replace(cfg, wtype=type_id(wtype))
         w = synthetic_weights(cfg, seed=0, std=0.02)
     if w is None:  # the decode benchmark's weights (random init, seed 0)
@@ -328,7 +333,7 @@ def bench_program_decode(args, w: dict | None = None) -> dict:
     with tempfile.TemporaryDirectory() as d:
         path = os.path.join(d, f"llama3_8b_{wtype}.gguf")
         t0 = time.perf_counter()
-        write_llama_program(path, cfg, w, kv_step=256, n_gen=args.steps)
+        write_llama_program(path, cfg, w, kv_step=256, n_gen=args.steps, types=types)
         t_write = time.perf_counter() - t0
         t0 = time.perf_counter()
         s = runtime.Session(path)
@@ -633,9 +638,10 @@ def main() -> int:
                          "program: the same model as a ggml-compiler program GGUF run by the loader")
     ap.add_argument("--only", default=None,
                     help="sweep: comma-separated configurations to run (C1, C2, K56, C3, C3K, C4); default all")
-    ap.add_argument("--wtype", default="q4_0", choices=["q4_0", "q8_0", "q4_K", "q5_K", "q6_K"],
+    ap.add_argument("--wtype", default="q4_0", choices=["q4_0", "q8_0", "q4_K", "q5_K", "q6_K", "q4_K_M"],
                     help="program: the weight type of every projection, the embedding and the lm head (q4_0: "
-                         "the decode benchmark's weights; the others: synthetic_weights of that type)")
+                         "the decode benchmark's weights; the others: synthetic_weights of that type; q4_K_M: "
+                         "llama.cpp's Q4_K_M mix of Q4_K and Q6_K)")
     ap.add_argument("--type", default="q8_0", choices=["q4_0", "q8_0", "q4_K", "q5_K", "q6_K"],
                     help="gemm: the weight type")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")

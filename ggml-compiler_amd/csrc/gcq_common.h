@@ -155,7 +155,8 @@ __device__ __forceinline__ void prefetch_share(const Prefetch & pf, int w, int n
 // Arguments of the decode-row GEMV (rowgemv.hip): one f32 activation row times a packed Q4_0 /
 // Q8_0 weight, with the node before (prologue) and after (epilogue) the mul_mat in one launch.
 enum { PRO_PLAIN = 0, PRO_NORM = 1, PRO_MERGE = 2, PRO_SWIGLU = 3 };
-enum { EPI_STORE = 0, EPI_ROPE_KV = 1, EPI_SWIGLU = 2 };
+// EPI_V_CACHE (K-quant row GEMV only): the v rows alone, pairs written to the f16 v cache at pos.
+enum { EPI_STORE = 0, EPI_ROPE_KV = 1, EPI_SWIGLU = 2, EPI_V_CACHE = 3 };
 
 struct RowArgs {
     const uint8_t * wqs;

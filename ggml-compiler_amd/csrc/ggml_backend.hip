@@ -417,12 +417,18 @@ Chains find_chains(const ggml_cgraph * g, bool fuse) {
                 last = std::max(last, c.end[r]);
             }
             c.end[i] = c.end[j] = last;  // x and w are read until the last reader's work runs
-            if (!adds && same && (allq8 || allkq) && rd.size() <= 3) {  // the multi-weight launches
+            // K-quant q / k / v whose v has a type of its own (Q4_K_M files): the q / k rope launch
+            // and the v launch writing its cache, one group
+            const bool mixed = !adds && !same && allkq && rd.size() == 3;
+            if ((!adds && same && (allq8 || allkq) && rd.size() <= 3) || mixed) {  // the multi-weight launches
                 std::vector<int> grp(rd.begin(), rd.end());
                 std::sort(grp.begin(), grp.end());
                 // the row-pair epilogues: any Q4_0 / Q8_0 row, K-quant rows of at most 4096 values
-                const bool pairs = allq8 || row_gemv_kq_epi_fits(g->nodes[grp[0]]->src[0]->type, EPI_ROPE_KV, m->ne[0]);
+                bool pairs = allq8 || row_gemv_kq_epi_fits(g->nodes[grp[0]]->src[0]->type, EPI_ROPE_KV, m->ne[0]);
+                for (int r : grp) pairs = pairs && (allq8 || row_gemv_kq_epi_fits(g->nodes[r]->src[0]->type, EPI_ROPE_KV, m->ne[0]));
                 std::vector<int> qkv = grp.size() == 3 && pairs ? qkv_rope_group(g, grp, uses, reader) : std::vector<int>{};
+                // mixed: q and k of one type (qkv_rope_group's order: q, k, v)
+                if (mixed && (qkv.empty() || g->nodes[qkv[0]]->src[0]->type != g->nodes[qkv[1]]->src[0]->type)) continue;
                 std::vector<int> gu = grp.size() == 2 && pairs ? gate_up_group(g, grp, uses, reader) : std::vector<int>{};
                 const int kind = !qkv.empty() ? 3 : !gu.empty() ? 4 : 0;
                 if (kind == 3) grp = qkv;
@@ -820,7 +826,12 @@ struct Planner {
         s.n[6] = rq->ne[0];   // D
         s.n[7] = ck->ne[1];   // ctx
         std::memcpy(&s.f[0], &nrm->op_params[0], 4);
-        require(weights_fit_one_launch(type, 3, w, N, K), "q / k / v rope group: the weights do not fit one launch");
+        // v's type: another K-quant type puts the v rows in a launch of their own (EPI_V_CACHE)
+        const int vtype = mv->src[0]->type;
+        s.m[0] = vtype;
+        require(vtype == type ? weights_fit_one_launch(type, 3, w, N, K)
+                              : weights_fit_one_launch(type, 2, w, N, K) && weights_fit_one_launch(vtype, 1, w + 2, N + 2, K),
+                "q / k / v rope group: the weights do not fit one launch");
         steps.push_back(s);
     }
 
@@ -1530,8 +1541,10 @@ void run_step(const ggml_backend * be, const Step & s) {
         case S_QKV_ROPE: {
             const uint8_t * w[3] = {(const uint8_t *) s.in[0], (const uint8_t *) s.in[3], (const uint8_t *) s.in[4]};
             if (is_kquant(s.type)) {
+                const int vtype = (int) s.m[0];
+                const int nqk = vtype == s.type ? 3 : 2;  // v of another type: a launch of its own
                 RowKqArgs a{};
-                require(row_gemv_kq_ranges(s.type, 3, w, s.n, s.n[3], a), "q / k / v rope: weights do not fit one launch");
+                require(row_gemv_kq_ranges(s.type, nqk, w, s.n, s.n[3], a), "q / k / v rope: weights do not fit one launch");
                 a.x = (const float *) s.in[1];
                 a.norm_w = (const float *) s.in[2];
                 a.eps = s.f[0];
@@ -1545,6 +1558,19 @@ void run_step(const ggml_backend * be, const Step & s) {
                 a.D = (int) s.n[6];
                 a.ctx = s.n[7];
                 launch_row_gemv_kq_epi(s.type, PRO_NORM, EPI_ROPE_KV, a, st);
+                if (nqk == 2) {
+                    RowKqArgs b{};
+                    row_gemv_kq_one(vtype, w[2], s.n[2], s.n[3], b);
+                    b.x = a.x;
+                    b.norm_w = a.norm_w;
+                    b.eps = a.eps;
+                    b.pos = a.pos;
+                    b.vc = a.vc;
+                    b.Hkv = a.Hkv;
+                    b.D = a.D;
+                    b.ctx = a.ctx;
+                    launch_row_gemv_kq_epi(vtype, PRO_NORM, EPI_V_CACHE, b, st);
+                }
                 return;
             }
             RowArgs a{};

@@ -98,6 +98,9 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
         if constexpr (EPI == EPI_SWIGLU) {
             local = min(gg, a.r_end[0] - 1);
             return r;
+        } else if constexpr (EPI == EPI_V_CACHE) {
+            local = min(2 * gg + r, a.N - 1);
+            return 0;
         } else if constexpr (EPI == EPI_ROPE_KV) {
             const int nq = (a.H + a.Hkv) * hd;
             const int gq = min(gg, nq - 1);
@@ -599,6 +602,15 @@ __global__ __launch_bounds__(1024) void k_row_gemv_kq(const RowKqArgs a) {
             }
         } else if constexpr (EPI == EPI_SWIGLU) {  // k_swiglu's arithmetic: g / (1 + e^-g) * u
             if (lane == 0) a.y[gg] = v[0] / (1.0f + expf(-v[0])) * v[1];
+        } else if constexpr (EPI == EPI_V_CACHE) {  // the v pair to the f16 v cache at the position
+            typedef const int __attribute__((address_space(4))) cint_t;
+            const int p = ((cint_t *) a.pos)[0];
+            if (p >= 0 && p < a.ctx && lane == 0) {
+                const int e = 2 * gg;  // v value index over [Hkv][D]
+                const int hv = div_hd(e) >> 1, dd = e - hv * a.D;
+                const uint32_t pair = f2h(v[0]) | ((uint32_t) f2h(v[1]) << 16);
+                *reinterpret_cast<uint32_t *>(a.vc + ((int64_t) hv * a.ctx + p) * a.D + dd) = pair;
+            }
         } else {  // EPI_ROPE_KV: q roped to y, k roped and v to the f16 caches at the position
             typedef const int __attribute__((address_space(4))) cint_t;
             const int p = ((cint_t *) a.pos)[0];
@@ -680,6 +692,7 @@ template <int TYPE>
 void go_kq_t(int pro, int epi, bool multi, int R, int nbl, const RowKqArgs & a, int grid, hipStream_t s) {
     if (epi == EPI_ROPE_KV) return go_kq<TYPE, PRO_NORM, EPI_ROPE_KV, 3>(R, nbl, a, grid, s);
     if (epi == EPI_SWIGLU) return go_kq<TYPE, PRO_NORM, EPI_SWIGLU, 3>(R, nbl, a, grid, s);
+    if (epi == EPI_V_CACHE) return go_kq<TYPE, PRO_NORM, EPI_V_CACHE, 1>(R, nbl, a, grid, s);
     if (multi) return go_kq<TYPE, PRO_NORM, EPI_STORE, 3>(R, nbl, a, grid, s);
     if (pro == PRO_NORM) return go_kq<TYPE, PRO_NORM, EPI_STORE, 1>(R, nbl, a, grid, s);
     if (pro == PRO_MERGE) return go_kq<TYPE, PRO_MERGE, EPI_STORE, 1>(R, nbl, a, grid, s);
@@ -758,12 +771,14 @@ void launch_row_gemv_kq_epi(int type, int pro, int epi, const RowKqArgs & a0, hi
     require(!multi || K <= 8192, "row gemv kq: several weights take rows of at most 8192 values");
     require(epi == EPI_STORE || a.N % 2 == 0, "row gemv kq: row-pair epilogue needs an even row count");
     require(epi == EPI_STORE ||
-                (epi == EPI_ROPE_KV && a.nr == 3 && a.D % 2 == 0 && a.D > 0 && a.r_end[0] == a.H * a.D &&
-                 a.r_end[1] == (a.H + a.Hkv) * a.D && a.r_end[2] == (a.H + 2 * a.Hkv) * a.D) ||
-                (epi == EPI_SWIGLU && a.nr == 2 && a.r_end[1] == 2 * a.r_end[0]),
-            "row gemv kq: separate q / k / v weights of H*D, Hkv*D, Hkv*D rows, or gate / up weights of equal rows");
+                (epi == EPI_ROPE_KV && a.D % 2 == 0 && a.D > 0 && a.r_end[0] == a.H * a.D &&
+                 a.r_end[1] == (a.H + a.Hkv) * a.D && (a.nr == 2 || (a.nr == 3 && a.r_end[2] == (a.H + 2 * a.Hkv) * a.D))) ||
+                (epi == EPI_SWIGLU && a.nr == 2 && a.r_end[1] == 2 * a.r_end[0]) ||
+                (epi == EPI_V_CACHE && a.nr <= 1 && a.D % 2 == 0 && a.D > 0 && a.N == a.Hkv * a.D && a.norm_w),
+            "row gemv kq: separate q / k [/ v] weights of H*D, Hkv*D [, Hkv*D] rows, gate / up weights of equal rows, "
+            "or a v weight of Hkv*D rows");
     require(!multi || !a.res, "row gemv kq: several weights take no residual");
-    if (epi == EPI_ROPE_KV) {
+    if (epi == EPI_ROPE_KV || epi == EPI_V_CACHE) {
         const uint64_t hd = (uint64_t) (a.D / 2);
         require((uint64_t) a.N * hd < (1ull << 32), "row gemv kq: rope epilogue indices past 2^32 / (D/2)");
         a.hd_magic = (uint32_t) ((1ull << 32) / hd + 1);

@@ -38,6 +38,8 @@ def _split_weights(cfg, weights: dict[str, np.ndarray]) -> dict[str, np.ndarray]
     from . import ggml as G
 
     H, Hkv, D, E, F = cfg.n_head, cfg.n_head_kv, cfg.head_dim, cfg.n_embd, cfg.n_ff
+    if "blk.0.attn_q" in weights:  # already the GGUF's separate tensors
+        return weights
     row = int(G.lib().ggml_row_size(cfg.wtype, E))
     out = {"token_embd": weights["token_embd"], "output_norm": weights["output_norm"], "output": weights["output"]}
     for l in range(cfg.n_layer):
@@ -163,12 +165,31 @@ def llama_program(cfg, kv_step: int = 256, n_gen: int = 128, eos: tuple[int, ...
     return program, wname
 
 
-def synthetic_weights(cfg, seed: int = 0, std: float = 0.02) -> dict[str, np.ndarray]:
+def q4_k_m_types(cfg) -> dict[str, int]:
+    """The storage type of each weight in a Q4_K_M file of cfg's shape, as llama.cpp's quantizer
+    assigns them (the mix the reference's Q4_K_M rows run, `llm.llama_cpp_policy`): Q6_K for the lm
+    head, and for attn_v and ffn_down of the layers i with i < n/8, i >= 7n/8 or (i - n/8) % 3 == 2;
+    Q4_K for the rest."""
+    n = cfg.n_layer
+    more = [i < n // 8 or i >= 7 * n // 8 or (i - n // 8) % 3 == 2 for i in range(n)]
+    types = {"token_embd": 12, "output": 14}
+    for l in range(n):
+        b = f"blk.{l}."
+        for k in ("attn_q", "attn_k", "attn_output", "ffn_gate", "ffn_up"):
+            types[b + k] = 12
+        types[b + "attn_v"] = 14 if more[l] else 12
+        types[b + "ffn_down"] = 14 if more[l] else 12
+    return types
+
+
+def synthetic_weights(cfg, seed: int = 0, std: float = 0.02, types: dict[str, int] | None = None) -> dict[str, np.ndarray]:
     """Random-init weights of cfg's decoder under the HIP model's names (q/k/v and gate/up rows
     stacked), as llm.Model.get_weight gives them: ggml block bytes of cfg.wtype (any storage type the
     library encodes: Q4_0, Q8_0, Q4_K, Q5_K, Q6_K; the GPU encoders, bit-exact with ggml's) from the
     library's N(0, std) stream, tensor i from seed + i; norm weights 1. For models the fused decoder
-    does not hold (K-quant weights)."""
+    does not hold (K-quant weights). With types (a type per GGUF tensor name, as q4_k_m_types
+    gives): the separate q / k / v and gate / up tensors under their GGUF names, each of its own
+    type (the stacked rows' streams, split)."""
     import torch
 
     from . import ops
@@ -187,16 +208,28 @@ def synthetic_weights(cfg, seed: int = 0, std: float = 0.02) -> dict[str, np.nda
         out[f"blk.{l}.ffn_norm"] = np.ones(E, np.float32)
     for i, (name, rows, cols) in enumerate(shapes):
         x = ops.fill_normal((rows, cols), seed=seed + i, std=std)
-        out[name] = ops.quantize(x, cfg.wtype).cpu().numpy()
+        if types is None:
+            out[name] = ops.quantize(x, cfg.wtype).cpu().numpy()
+        else:
+            b = name[: name.rfind(".") + 1]
+            if name.endswith("attn_qkv"):
+                parts = [("attn_q", 0, H * D), ("attn_k", H * D, (H + Hkv) * D), ("attn_v", (H + Hkv) * D, rows)]
+            elif name.endswith("ffn_gate_up"):
+                parts = [("ffn_gate", 0, F), ("ffn_up", F, 2 * F)]
+            else:
+                parts = [(name[len(b):], 0, rows)]
+            for part, r0, r1 in parts:
+                out[b + part] = ops.quantize(x[r0:r1].contiguous(), types[b + part]).cpu().numpy()
         del x
     torch.cuda.synchronize()
     return out
 
 
 def write_llama_program(path: str | Path, cfg, weights: dict[str, np.ndarray], kv_step: int = 256, n_gen: int = 128,
-                        eos: tuple[int, ...] = ()) -> None:
+                        eos: tuple[int, ...] = (), types: dict[str, int] | None = None) -> None:
     """The GGUF: the program JSON, tensor_names (w.N -> the weight's name), and every weight as
-    ggml block bytes. weights: the HIP model's names and bytes (llm.Model.get_weight)."""
+    ggml block bytes. weights: the HIP model's names and bytes (llm.Model.get_weight), or the
+    separate tensors of synthetic_weights(..., types) with those types."""
     program, wname = llama_program(cfg, kv_step, n_gen, eos)
     split = _split_weights(cfg, weights)
     E, F, V = cfg.n_embd, cfg.n_ff, cfg.n_vocab
@@ -215,6 +248,6 @@ def write_llama_program(path: str | Path, cfg, weights: dict[str, np.ndarray], k
     wr.add("ggml_compiler.meta", json.dumps({"eos_token_ids": list(eos), "max_context": cfg.max_ctx},
                                             separators=(",", ":")))
     for name, gname in wname.items():
-        typ = 0 if name.endswith("norm") else cfg.wtype
+        typ = 0 if name.endswith("norm") else (types or {}).get(name, cfg.wtype)
         wr.add_tensor(gname, np.ascontiguousarray(split[name]).view(np.uint8), typ, ne[name])
     wr.write(path)

@@ -17,11 +17,14 @@ import oracle as orc
 
 
 class OracleLlama:
-    def __init__(self, cfg, weights: dict[str, np.ndarray], threads: int = 0) -> None:
+    def __init__(self, cfg, weights: dict[str, np.ndarray], threads: int = 0, types: dict[str, int] | None = None) -> None:
+        """weights: the stacked q / k / v and gate / up rows of cfg.wtype, or (with types, a type
+        per tensor) the separate GGUF tensors."""
         self.cfg = cfg
         self.w = weights
         self.threads = threads
         self.t = cfg.wtype
+        self.types = types or {}
         L, Hkv, ctx, D = cfg.n_layer, cfg.n_head_kv, cfg.max_ctx, cfg.head_dim
         self.k = np.zeros((L, Hkv, ctx, D), np.uint16)
         self.v = np.zeros((L, Hkv, ctx, D), np.uint16)
@@ -33,7 +36,13 @@ class OracleLlama:
         self.pos = 0
 
     def _mm(self, name: str, x: np.ndarray) -> np.ndarray:
-        return orc.mul_mat(self.w[name], self.t, x, x.shape[1], threads=self.threads)
+        return orc.mul_mat(self.w[name], self.types.get(name, self.t), x, x.shape[1], threads=self.threads)
+
+    def _mm_stacked(self, b: str, stacked: str, parts: tuple[str, ...], x: np.ndarray) -> np.ndarray:
+        """The stacked rows' product, or the separate tensors' products side by side."""
+        if b + stacked in self.w:
+            return self._mm(b + stacked, x)
+        return np.concatenate([self._mm(b + p, x) for p in parts], axis=1)
 
     def _norm(self, name: str, x: np.ndarray) -> np.ndarray:
         return orc.rms_norm(x, self.cfg.rms_eps, threads=self.threads) * self.w[name][None, :]
@@ -48,7 +57,7 @@ class OracleLlama:
         """Layer l's feed-forward half on the rows after attention: mid + down(swiglu(gate, up))."""
         c = self.cfg
         b = f"blk.{l}."
-        gu = self._mm(b + "ffn_gate_up", self._norm(b + "ffn_norm", mid))
+        gu = self._mm_stacked(b, "ffn_gate_up", ("ffn_gate", "ffn_up"), self._norm(b + "ffn_norm", mid))
         return mid + self._mm(b + "ffn_down", orc.swiglu(gu[:, :c.n_ff], gu[:, c.n_ff:]))
 
     def attention(self, l: int, x: np.ndarray, pos: np.ndarray) -> np.ndarray:
@@ -59,7 +68,7 @@ class OracleLlama:
         n_kv = int(pos[-1]) + 1
         mask = np.where(np.arange(n_kv)[None, :] <= pos[:, None], 0.0, -np.inf).astype(np.float32)
         b = f"blk.{l}."
-        qkv = self._mm(b + "attn_qkv", self._norm(b + "attn_norm", x))
+        qkv = self._mm_stacked(b, "attn_qkv", ("attn_q", "attn_k", "attn_v"), self._norm(b + "attn_norm", x))
         q = orc.rope_neox(qkv[:, :H * D].reshape(S, H, D), pos, D, c.rope_base)
         k = orc.rope_neox(qkv[:, H * D:(H + Hkv) * D].reshape(S, Hkv, D), pos, D, c.rope_base)
         v = qkv[:, (H + Hkv) * D:].reshape(S, Hkv, D)
@@ -70,7 +79,8 @@ class OracleLlama:
         return x + self._mm(b + "attn_output", att.reshape(S, H * D))
 
     def embed(self, tokens) -> np.ndarray:
-        return orc.dequantize(self.w["token_embd"][np.asarray(tokens)], self.t, self.cfg.n_embd)
+        return orc.dequantize(self.w["token_embd"][np.asarray(tokens)], self.types.get("token_embd", self.t),
+                              self.cfg.n_embd)
 
     def forward(self, tokens) -> np.ndarray:
         """Append tokens at the next positions; logits of the last one."""

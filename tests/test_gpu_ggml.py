@@ -261,16 +261,18 @@ def test_kquant_sibling_gemvs_in_one_launch(be, orc, t, Ns, K):
         assert orc.parity(got[i], orc.mul_mat(raw, t, xn, K)[0]) < TOL, i
 
 
-@pytest.mark.parametrize("t", ["q4_0", "q8_0", "q4_K", "q5_K", "q6_K"])
+@pytest.mark.parametrize("t", ["q4_0", "q8_0", "q4_K", "q5_K", "q6_K", "q4_K/q6_K"])
 def test_qkv_rope_cache_writes_in_one_launch(be, orc, t):
     """The decode step's q / k / v GEMVs of one normalized row, the q and k ropes and the k / v
     set_rows into f16 caches (built as the reference builds them) run as one launch whose epilogue
-    ropes and writes the caches; the roped q and both caches equal the unfused graph's (each
-    intermediate marked as an output, which keeps them apart) to 1e-6. The row is an embedding
-    row (get_rows), whose launch also builds the epilogue's rotation table."""
+    ropes and writes the caches (q4_K/q6_K: v in Q6_K, as Q4_K_M files store it in some layers:
+    the q / k launch, then the v launch writing its cache); the roped q and both caches equal the
+    unfused graph's (each intermediate marked as an output, which keeps them apart) to 1e-6. The
+    row is an embedding row (get_rows), whose launch also builds the epilogue's rotation table."""
     K, H, Hkv, D, ctx, p = 2048, 8, 2, 128, 64, 13
-    tid = orc.TYPES[t]
-    raws = [_weight(orc, t, N, K, 150 + i) for i, N in enumerate((H * D, Hkv * D, Hkv * D))]
+    ts = t.split("/") if "/" in t else [t, t]
+    wts = [ts[0], ts[0], ts[1]]
+    raws = [_weight(orc, wt, N, K, 150 + i) for i, (wt, N) in enumerate(zip(wts, (H * D, Hkv * D, Hkv * D)))]
     x = orc.normal((1, K), seed=154)
     nw = (1.0 + 0.1 * orc.normal((K,), seed=155)).astype(np.float32)
     emb = np.concatenate([orc.normal((2, K), seed=156), x])  # x: row 2 of an embedding table
@@ -278,7 +280,7 @@ def test_qkv_rope_cache_writes_in_one_launch(be, orc, t):
               "pos": (G.I32, [1], np.array([p], np.int32)), "ck": (G.F16, [D, ctx, Hkv], None),
               "cv": (G.F16, [D, ctx, Hkv], None)}
     for i, raw in enumerate(raws):
-        leaves[f"w{i}"] = (tid, [K, raw.shape[0]], raw)
+        leaves[f"w{i}"] = (orc.TYPES[wts[i]], [K, raw.shape[0]], raw)
     res = {}
     for split in (False, True):
         keep = {}

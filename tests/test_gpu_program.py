@@ -304,22 +304,28 @@ def test_llama_program_decode_and_generate(tmp_path, orc, wtype):
         assert s2.stats["n_calls"] == 6
 
 
-@pytest.mark.parametrize("wtype", [12, 13, 14])
+@pytest.mark.parametrize("wtype", [12, 13, 14, "q4_K_M"])
 def test_llama_program_kquant_weights(tmp_path, orc, wtype):
     """A Llama decoder program whose weights are all one K-quant type (Q4_K, Q5_K, Q6_K: every
-    projection, the embedding table and the lm head), which the fused decoder does not hold: the
-    decode entry against the oracle decoder on the same bytes, then the generate entry's tokens."""
+    projection, the embedding table and the lm head), which the fused decoder does not hold, or
+    llama.cpp's Q4_K_M mix (Q6_K lm head, and v / down of some layers Q6_K, the rest Q4_K: q / k
+    and v of such a layer of two types): the decode entry against the oracle decoder on the same
+    bytes, then the generate entry's tokens."""
     from ggml_compiler_amd.llm import LlamaConfig
-    from ggml_compiler_amd.program import synthetic_weights, write_llama_program
+    from ggml_compiler_amd.program import q4_k_m_types, synthetic_weights, write_llama_program
     from llama_ref import OracleLlama
 
-    cfg = LlamaConfig(n_layer=2, n_embd=256, n_head=4, n_head_kv=2, head_dim=64, n_ff=512, n_vocab=1000,
-                      max_ctx=64, wtype=wtype, rms_eps=1e-5, rope_base=10000.0)
-    w = synthetic_weights(cfg, seed=31)
+    mixed = wtype == "q4_K_M"
+    cfg = LlamaConfig(n_layer=4 if mixed else 2, n_embd=256, n_head=4, n_head_kv=2, head_dim=64, n_ff=512,
+                      n_vocab=1000, max_ctx=64, wtype=12 if mixed else wtype, rms_eps=1e-5, rope_base=10000.0)
+    types = q4_k_m_types(cfg) if mixed else None
+    if mixed:  # of 4 layers, 2 ((i - 0) % 3 == 2) and 3 (i >= 7n/8) take Q6_K v / down
+        assert [types[f"blk.{l}.attn_v"] for l in range(4)] == [12, 12, 14, 14] and types["output"] == 14
+    w = synthetic_weights(cfg, seed=31, types=types)
     path = str(tmp_path / "llama_kq.gguf")
-    write_llama_program(path, cfg, w, kv_step=16, n_gen=12, eos=(999,))
+    write_llama_program(path, cfg, w, kv_step=16, n_gen=12, eos=(999,), types=types)
     with runtime.Session(path) as s:
-        o = OracleLlama(cfg, w)
+        o = OracleLlama(cfg, w, types=types)
         tok, toks = 17, []
         for p in range(12):
             n_kv = max(16, (p + 16) // 16 * 16)

@@ -78,3 +78,18 @@ def test_model_api_rejects_null_and_bad_indices():
     assert lib.ggml_compiler_metadata(None, b"k") is None
     assert lib.ggml_compiler_build_param(None, 0) is None
     lib.ggml_compiler_free(None)
+
+
+def test_q4_k_m_types_follow_llama_cpp_rule():
+    """llama.cpp's Q4_K_M mix at the 8B shape: the lm head and, in layers 0-3, 28-31 and every
+    third from 6, attn_v and ffn_down in Q6_K; every other weight Q4_K."""
+    from ggml_compiler_amd.llm import LlamaConfig
+    from ggml_compiler_amd.program import q4_k_m_types
+
+    t = q4_k_m_types(LlamaConfig.llama3_8b(max_ctx=64))
+    six = [0, 1, 2, 3, 6, 9, 12, 15, 18, 21, 24, 27, 28, 29, 30, 31]
+    assert [l for l in range(32) if t[f"blk.{l}.attn_v"] == 14] == six
+    assert [l for l in range(32) if t[f"blk.{l}.ffn_down"] == 14] == six
+    assert t["output"] == 14 and t["token_embd"] == 12
+    assert all(t[f"blk.{l}.{k}"] == 12 for l in range(32)
+               for k in ("attn_q", "attn_k", "attn_output", "ffn_gate", "ffn_up"))
