@@ -731,9 +731,8 @@ __device__ __forceinline__ void rmsnorm_q8_row(const float * xr, int n, const fl
     }
 }
 
-// Element c of a K-quant table row, as ggml's dequantize_row_q{4,5,6}_K computes it (products and
-// the difference rounded one at a time): Q4_K / Q5_K in ggml's super-blocks, d * sc * q - dmin * m;
-// Q6_K in the packed layout (208-byte super-blocks, then their fp16 d), d * sc * (q - 32).
+// Element c of a packed K-quant table row, as ggml's dequantize_row_q{4,5,6}_K computes it (products
+// and the difference rounded one at a time): Q4_K / Q5_K d * sc * q - dmin * m, Q6_K d * sc * (q - 32).
 __device__ __forceinline__ float kquant_table_value(int type, const uint8_t * tab, int64_t nrows, int D, int64_t r,
                                                     int c) {
     const int nsb = D / QKK, w = c % QKK;
