@@ -1263,18 +1263,6 @@ class StageClock {
     size_t used_ = 0;
 };
 
-// GGML_COMPILER_PROFILE=<file>: every graph runs one node at a time, waited for, and after each
-// run "stage<TAB>node<TAB>op<TAB>ms" lines are appended to <file> (the reference runtime's
-// profile, runtime/src/ggml_compiler_rt.cpp:83-88, 219-240, 343-354). Fusion is off in this mode,
-// so every node is one launch of its own.
-const char * profile_file() {
-    static const char * p = [] {
-        const char * e = std::getenv("GGML_COMPILER_PROFILE");
-        return e && *e ? e : nullptr;
-    }();
-    return p;
-}
-
 // GGML_COMPILER_LOG=debug: the runtime's informational messages on stderr (warnings always).
 bool log_debug() {
     static const bool on = [] {
@@ -1492,6 +1480,13 @@ struct ggml_compiler_model {
         double ms;
     };
     std::vector<ProfileLine> profile;
+    // GGML_COMPILER_PROFILE=<file>, read when the model loads: every graph runs one node at a time,
+    // waited for, and after each run "stage<TAB>node<TAB>op<TAB>ms" lines are appended to <file>
+    // (the reference runtime's profile, runtime/src/ggml_compiler_rt.cpp:83-88, 219-240, 343-354,
+    // which reads the variable once per process). Fusion is off in this mode, so every node is one
+    // launch of its own.
+    std::string profile_path;
+    const char * profile_file() const { return profile_path.empty() ? nullptr : profile_path.c_str(); }
 
     ~ggml_compiler_model() {
         if (backend) (void) hipStreamSynchronize(backend_stream(backend));
@@ -1512,6 +1507,7 @@ struct ggml_compiler_model {
         if (o.backend != GGML_COMPILER_BACKEND_HIP && o.backend != GGML_COMPILER_BACKEND_AUTO)
             fail("backend " + std::to_string((int) o.backend) + " is not available: this runtime has the HIP backend "
                  "(GGML_COMPILER_BACKEND_HIP or _AUTO)");
+        if (const char * e = std::getenv("GGML_COMPILER_PROFILE")) profile_path = e;
         file.open(path);
         const auto text = file.strings.find("ggml_compiler.program");
         if (text == file.strings.end())
