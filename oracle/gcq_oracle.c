@@ -14,9 +14,12 @@
  * Parity pins (tests/test_oracle.py): fp16 against numpy's IEEE conversion; encoders against
  * hand-worked blocks, on-grid round trips (the tests/unit/test_modelopt.py:60-72 pattern) and
  * error invariants; integer block sums against int64 brute force; mul_mat / rms_norm / rope /
- * flash_attn against float64 closed forms. The K-quant encoders' exact bytes (the
- * make_qkx2_quants / make_qx_quants searches) and ggml's float summation order are parity
- * unpinned: no ggml build exists to compare against.
+ * flash_attn against float64 closed forms. The K-quant encoders' searches (make_qkx2_quants,
+ * make_qx_quants) are pinned by tests/test_kquant_search.py in float64: each candidate step
+ * against the published candidate formula, each fit against the closed-form weighted least-squares
+ * solution for its codes, the result the least weighted error of the fits made (Q6_K: of the
+ * published candidate set, enumerated), and a wrong search parameter rejected. ggml's float summation
+ * order inside mul_mat / flash_attn is parity unpinned: no ggml build exists to compare against.
  */
 #include "gcq_oracle.h"
 
