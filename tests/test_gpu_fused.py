@@ -32,9 +32,8 @@ def test_swiglu_q8_equals_swiglu_then_quantize(gops, orc, rows, n):
                                    (12, 256, 512)])
 def test_mul_mat_q_with_residual(gops, orc, t, B, N, K):
     """y = res + W x in one launch equals W x then ggml_add; also in place (y is res). N=40000 runs
-    the persistent GEMV's multi-group loop; 12 rows run the GEMM (Q4_0, Q8_0)."""
-    if t == "q4_K" and B > 8:
-        pytest.skip("Q4_K runs more than 8 rows through gcq_mul_mat")
+    the persistent GEMV's multi-group loop; 12 rows run the GEMMs (k_gemm for Q4_0 / Q8_0,
+    k_gemm_kq for Q4_K)."""
     raw = orc.quantize(orc.normal((N, K), seed=73, std=0.02), t)
     qw = gops.QuantWeight.from_ggml(torch.from_numpy(raw), t, K)
     x = orc.normal((B, K), seed=74)
