@@ -27,13 +27,13 @@ def test_swiglu_q8_equals_swiglu_then_quantize(gops, orc, rows, n):
     assert torch.equal(gops.act_to_ggml("q4_0", fused, rows, n), gops.act_to_ggml("q4_0", unfused, rows, n))
 
 
-@pytest.mark.parametrize("t", ["q4_0", "q8_0", "q4_K"])
+@pytest.mark.parametrize("t", ["q4_0", "q8_0", "q4_K", "q5_K", "q6_K"])
 @pytest.mark.parametrize("B,N,K", [(1, 512, 256), (1, 1000, 256), (2, 300, 512), (1, 40000, 4096), (3, 4096, 4096),
                                    (12, 256, 512)])
 def test_mul_mat_q_with_residual(gops, orc, t, B, N, K):
     """y = res + W x in one launch equals W x then ggml_add; also in place (y is res). N=40000 runs
     the persistent GEMV's multi-group loop; 12 rows run the GEMMs (k_gemm for Q4_0 / Q8_0,
-    k_gemm_kq for Q4_K)."""
+    k_gemm_kq for the K-quants)."""
     raw = orc.quantize(orc.normal((N, K), seed=73, std=0.02), t)
     qw = gops.QuantWeight.from_ggml(torch.from_numpy(raw), t, K)
     x = orc.normal((B, K), seed=74)
